@@ -1,0 +1,147 @@
+/*
+ * tcc_spmm_cnic.h — C-ABI of the block-sparse (BCSR / BCSC) SpMM behind the
+ * `spmm_cnic` PyTorch extension, for MI355X (gfx950).
+ *
+ * Block formats (8x8 blocks, one u64 bitmap each, bit r*8+c = block row r,
+ * block column c):
+ *   BCSR: row window w covers rows 8w..8w+7; its blocks are
+ *         [rowWindowOffset[w], rowWindowOffset[w+1]); block b lists the 8
+ *         global source columns it covers in sparseA2B[8b..8b+7]
+ *         (padding = 0xFFFFFFFF or any value >= num_cols).
+ *         Y[8w+r] += sum_c bit(r,c) * v * X[sparseA2B[8b+c]].
+ *   BCSC: column window w covers sources 8w..8w+7; its blocks are
+ *         [colWindowOffset[w], colWindowOffset[w+1]); block b lists the 8
+ *         global destination rows in sparseA2C[8b..8b+7] (padding >= num_rows).
+ *         Y[sparseA2C[8b+r]] += sum_c bit(r,c) * v * X[8w+c].
+ * Values: when `data` is NULL every stored entry is 1.0 (what the reference
+ * kernels do, spmm_cnic/src/core/spmm_kernel.cu:96-102).  Otherwise the value
+ * of bit i of block b is data[tcOffset[b] + popcount(bitmap & ((1<<i)-1))]
+ * (the layout of the reference's commented-out value load, :88-101).
+ * Products use TF32-rounded (round-to-nearest, ties away from zero, 10
+ * mantissa bits) X and values with fp32 accumulation, reproducing the
+ * reference's mma.m16n8k8 tf32 numerics.
+ *
+ * Reference interface replaced: spmm_cnic/include/class.h:20-58 (views),
+ * spmm_cnic/src/core/spmm_launcher.cu:30-271 (launch_spmm_kernel) and
+ * spmm_cnic/src/core/spmm_dispatcher.cu:15-301 (tf32_spmm_bcsr/bcsc and the
+ * mixed variants).
+ */
+#ifndef TCC_SPMM_CNIC_H
+#define TCC_SPMM_CNIC_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* BCSR<T> (spmm_cnic/include/class.h:20-37) plus the optional value array. */
+typedef struct tcc_bcsr {
+    uint32_t num_rows;
+    uint32_t num_cols;
+    uint32_t nnz;
+    uint32_t num_TCBlocks;
+    uint32_t num_rowWindows;
+    const uint32_t* rowWindowOffset; /* [num_rowWindows+1] */
+    const uint32_t* tcOffset;        /* [num_TCBlocks+1] value offsets (used only with data) */
+    const uint32_t* sparseA2B;       /* [num_TCBlocks*8] */
+    const uint64_t* tcLocalBit;      /* [num_TCBlocks] */
+    const float* data;               /* [nnz] or NULL */
+} tcc_bcsr;
+
+/* BCSC<T> (spmm_cnic/include/class.h:39-58) plus the optional value array. */
+typedef struct tcc_bcsc {
+    uint32_t num_rows;
+    uint32_t num_cols;
+    uint32_t nnz;
+    uint32_t num_TCBlocks;
+    uint32_t num_colWindows;
+    const uint32_t* colWindowOffset; /* [num_colWindows+1] */
+    const uint32_t* tcOffset;        /* [num_TCBlocks+1] */
+    const uint32_t* sparseA2C;       /* [num_TCBlocks*8] */
+    const uint64_t* tcLocalBit;      /* [num_TCBlocks] */
+    const float* data;               /* [nnz] or NULL */
+} tcc_bcsc;
+
+/* Where the first GCN layer reads feature row j from
+ * (spmm_cnic/src/core/spmm_kernel.cu:129-153): g = cache_search_map[j];
+ * g >= 0: hot row gpu_feature_cache[g / gpu_node_capacity] + (g % cap) * F
+ * (device memory); g < 0: cold row cpu_features + id_map[j] * F, a device
+ * pointer to mapped pinned host memory read zero-copy; id_map[j] < 0 reads
+ * zeros.  Two bounds the reference does not check keep bad map values from
+ * reading outside the tables: a cache index g / cap >= gpu_feature_cache_count
+ * (when nonzero) and a host row past cpu_feature_len floats (when > 0) read
+ * zeros.  On one GPU the pointer table has one entry. */
+typedef struct tcc_feature_source {
+    const int32_t* id_map;           /* device [num_cols] */
+    const int32_t* cache_search_map; /* device [num_cols] */
+    const float* const* gpu_feature_cache; /* device array of device pointers */
+    int32_t gpu_node_capacity;
+    const float* cpu_features;       /* device-visible pointer to pinned host rows */
+    int64_t cpu_feature_len;         /* floats available at cpu_features (<= 0: unchecked) */
+    uint32_t gpu_feature_cache_count; /* entries of gpu_feature_cache (0: unchecked) */
+} tcc_feature_source;
+
+/* Y[row-window rows x F] (=, or += when accumulate != 0) A_bcsr * X.
+ * Row windows own their 8 output rows, so no atomics are used; with
+ * accumulate == 0 every row 0..8*num_rowWindows-1 is written (empty windows
+ * write zeros).  Y must hold 8*num_rowWindows*F floats.
+ * (tf32_spmm_bcsr, spmm_dispatcher.cu:167-232; kernel spmm_kernel.cu:1560-1842.) */
+int tcc_bcsr_spmm(const tcc_bcsr* A, const float* X, float* Y, uint32_t featureDim,
+                  int accumulate, void* stream);
+
+/* Y[num_rows x F] += A_bcsc * X with fp32 atomics (rows >= num_rows skipped).
+ * (tf32_spmm_bcsc, spmm_dispatcher.cu:236-301; kernel spmm_kernel.cu:1844-2166.) */
+int tcc_bcsc_spmm(const tcc_bcsc* A, const float* X, float* Y, uint32_t featureDim,
+                  void* stream);
+
+/* Transposed use of a BCSC for the backward pass: dX = A^T * dY, i.e.
+ * dX[8w+c] (=, or +=) sum_b sum_r bit(r,c) * v * dY[sparseA2C[8b+r]] — a
+ * gather with no atomics.  dX must hold 8*num_colWindows*F floats.  The
+ * reference computes this product with torch.sparse.mm
+ * (train/tcgnn_conv_release.py:152); this is its block-sparse replacement. */
+int tcc_bcsc_transpose_spmm(const tcc_bcsc* A, const float* dY, float* dX,
+                            uint32_t featureDim, int accumulate, void* stream);
+
+/* launch_spmm_kernel, non-first-layer form (spmm_launcher.cu:203-271):
+ * denseC[(num_rowWindows+1)*8*F] = A_bcsr*X + A_bcsc*X.  The BCSR part writes
+ * every row (replacing the reference's memset), the BCSC part then adds with
+ * atomics, both on `stream`. */
+int tcc_spmm_cnic_forward(const tcc_bcsr* bcsr, const tcc_bcsc* bcsc, const float* X,
+                          float* denseC, uint32_t featureDim, void* stream);
+
+/* launch_spmm_kernel, first-layer (mixed memory) form
+ * (spmm_launcher.cu:30-112 with the mixed kernels of spmm_kernel.cu:7-794):
+ * as tcc_spmm_cnic_forward, with feature rows resolved through `src`. */
+int tcc_spmm_cnic_forward_mixed(const tcc_bcsr* bcsr, const tcc_bcsc* bcsc,
+                                const tcc_feature_source* src, float* denseC,
+                                uint32_t featureDim, void* stream);
+
+/* The BCSR part of the mixed form alone (for hot/cold measurements). */
+int tcc_bcsr_spmm_mixed(const tcc_bcsr* A, const tcc_feature_source* src, float* Y,
+                        uint32_t featureDim, int accumulate, void* stream);
+
+/* ---- construction ----
+ * The reference receives these arrays from ipc_service (called at
+ * train/tcgnn_conv_release.py:295-296), which is not part of its tree; these
+ * builders produce the layout its kernels consume from a device COO
+ * (row = destination, col = source, no duplicate pairs; dVal may be NULL).
+ *   BCSR: per 8-row window, its distinct columns ascending, 8 per block.
+ *   BCSC: per 8-source window, its rows by (degree desc, dst asc), 8 per
+ *         block (the SWTCF row order with one window per super-window).
+ * Each synchronises `stream` once (to size the output), places all arrays in
+ * one device allocation returned in *allocation (free it with
+ * tcc_block_release) and fills *out with views into it.  `data` is set only
+ * when dVal != NULL. */
+int tcc_coo_to_bcsr(const uint32_t* dRow, const uint32_t* dCol, const float* dVal, uint32_t nnz,
+                    uint32_t numRows, uint32_t numCols, tcc_bcsr* out, void** allocation, void* stream);
+int tcc_coo_to_bcsc(const uint32_t* dRow, const uint32_t* dCol, const float* dVal, uint32_t nnz,
+                    uint32_t numRows, uint32_t numCols, tcc_bcsc* out, void** allocation, void* stream);
+int tcc_block_release(void* allocation);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TCC_SPMM_CNIC_H */

@@ -1,0 +1,81 @@
+// Shared helpers for the gfx950 kernels of libtcc_swtcf.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+namespace tcc {
+
+// ---------------------------------------------------------------- errors
+void set_last_error(const std::string& msg);
+void clear_last_error();
+
+// Returns TCC_ERR_HIP (2) from the enclosing C-ABI function on failure.
+#define TCC_HIP_CHECK(call)                                                              \
+    do {                                                                                 \
+        const hipError_t tcc_err__ = (call);                                             \
+        if (tcc_err__ != hipSuccess) {                                                   \
+            ::tcc::set_last_error(std::string("HIP error: ") + hipGetErrorString(tcc_err__) + \
+                                  " at " + __FILE__ + ":" + std::to_string(__LINE__));   \
+            return 2;                                                                    \
+        }                                                                                \
+    } while (0)
+
+#define TCC_REQUIRE(cond, code, msg)        \
+    do {                                    \
+        if (!(cond)) {                      \
+            ::tcc::set_last_error(msg);     \
+            return (code);                  \
+        }                                   \
+    } while (0)
+
+#define TCC_LAUNCH_CHECK() TCC_HIP_CHECK(hipGetLastError())
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+constexpr int kWave = 64;
+
+inline unsigned grid_for(std::uint64_t n, unsigned threads) {
+    return static_cast<unsigned>((n + threads - 1) / threads);
+}
+
+// ---------------------------------------------------------------- numerics
+// cvt.rna.tf32.f32 restated from its definition: round to nearest with ties
+// away from zero, keeping 10 explicit mantissa bits; inf and NaN unchanged.
+// (Reference use: include/mma_tf32.cuh:17-22.)
+__device__ __forceinline__ float tf32_rna(float x) {
+    const std::uint32_t b = __float_as_uint(x);
+    const std::uint32_t r = ((b & 0x7F800000u) == 0x7F800000u) ? b : ((b + 0x1000u) & 0xFFFFE000u);
+    return __uint_as_float(r);
+}
+
+// ---------------------------------------------------------------- wave64
+__device__ __forceinline__ unsigned lane_id() { return __lane_id(); }
+
+__device__ __forceinline__ std::uint64_t lanemask_lt() {
+    const unsigned l = __lane_id();
+    return (l == 0) ? 0ull : ((~0ull) >> (64 - l));
+}
+
+// Lanes of the wave (among `active`) whose `key` (nbits wide) equals this
+// lane's key.  Used for stable wave-level multisplit ranks.
+template <int NBITS>
+__device__ __forceinline__ std::uint64_t match_peers(unsigned key, bool active) {
+    std::uint64_t peers = __ballot(active);
+#pragma unroll
+    for (int b = 0; b < NBITS; ++b) {
+        const bool bit = (key >> b) & 1u;
+        const std::uint64_t m = __ballot(bit);
+        peers &= bit ? m : ~m;
+    }
+    return active ? peers : 0ull;
+}
+
+// fp32 atomic add to global memory (hardware global_atomic_add_f32; the
+// library is compiled with -munsafe-fp-atomics for coarse-grained memory).
+__device__ __forceinline__ void atomic_add_f32(float* p, float v) { unsafeAtomicAdd(p, v); }
+
+}  // namespace tcc

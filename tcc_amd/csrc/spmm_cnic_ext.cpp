@@ -1,0 +1,311 @@
+// `spmm_cnic` PyTorch extension for ROCm: the drop-in for the reference's
+// pybind module (spmm_cnic/src/bindings/module.cu:344-365).  A thin C++ layer
+// that turns tensors and capsules into raw pointers and calls the C-ABI of
+// libtcc_swtcf.so on torch's current HIP stream; all compute is in the HIP
+// kernels.
+//
+// Both call forms are exported as pybind11 overloads:
+//  * the compiled form (module.cu:100-108, 192-197): explicit device_id and a
+//    caller-provided denseC capsule (from space_malloc); the result is a
+//    tensor view of denseC with no deleter, like torch::from_blob there;
+//  * the form the training scripts call (train/tcgnn_conv_release.py:116-130):
+//    no device_id/denseC, a `data` tensor after each bitmap tensor, and the
+//    output allocated here and kept until freeMatC() (:324).
+// The reference kernels force every stored value to 1.0
+// (spmm_kernel.cu:96-102); by default the `data` tensors are therefore not
+// read, so results equal the reference's.  set_use_values(True) makes the
+// kernels use them (value of bit i of block b = data[tcOffset[b] + rank]).
+#include <torch/extension.h>
+
+#include <c10/hip/HIPStream.h>
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "tcc_spmm_cnic.h"
+#include "tcc_swtcf.h"
+
+namespace py = pybind11;
+
+namespace {
+
+std::vector<torch::Tensor> g_outputs;  // Python-caller form outputs, released by freeMatC()
+std::vector<void*> g_spaces;           // space_malloc buffers, released by finalize()
+bool g_use_values = false;
+
+void check(int rc) {
+    if (rc != 0) {
+        throw std::runtime_error(std::string("spmm_cnic: ") + tcc_last_error());
+    }
+}
+
+void* stream_of(int device) {
+    return reinterpret_cast<void*>(c10::hip::getCurrentHIPStream(static_cast<c10::DeviceIndex>(device)).stream());
+}
+
+const std::uint32_t* u32_ptr(const torch::Tensor& t, const char* name) {
+    TORCH_CHECK(t.is_cuda() && t.is_contiguous(), name, " must be a contiguous device tensor");
+    TORCH_CHECK(t.scalar_type() == torch::kInt32 || t.scalar_type() == torch::kUInt32, name,
+                " must be int32/uint32");
+    return reinterpret_cast<const std::uint32_t*>(t.data_ptr());
+}
+
+const std::uint64_t* u64_ptr(const torch::Tensor& t, const char* name) {
+    TORCH_CHECK(t.is_cuda() && t.is_contiguous(), name, " must be a contiguous device tensor");
+    TORCH_CHECK(t.element_size() == 8, name, " must hold 64-bit bitmaps");
+    return reinterpret_cast<const std::uint64_t*>(t.data_ptr());
+}
+
+const float* values_ptr(const torch::Tensor* data) {
+    if (!g_use_values || data == nullptr || !data->defined() || data->numel() == 0) return nullptr;
+    TORCH_CHECK(data->is_cuda() && data->is_contiguous() && data->scalar_type() == torch::kFloat32,
+                "data must be a contiguous float32 device tensor");
+    return data->data_ptr<float>();
+}
+
+tcc_bcsr make_bcsr(std::uint32_t rows, std::uint32_t cols, std::uint32_t nnz, std::uint32_t blocks,
+                   std::uint32_t windows, const torch::Tensor& rwo, const torch::Tensor& tco,
+                   const torch::Tensor& a2b, const torch::Tensor& bits, const torch::Tensor* data) {
+    tcc_bcsr b{};
+    b.num_rows = rows;
+    b.num_cols = cols;
+    b.nnz = nnz;
+    b.num_TCBlocks = blocks;
+    b.num_rowWindows = windows;
+    b.rowWindowOffset = u32_ptr(rwo, "bcsr_rowWindowOffset");
+    b.tcOffset = u32_ptr(tco, "bcsr_tcOffset");
+    b.sparseA2B = u32_ptr(a2b, "bcsr_sparseA2B");
+    b.tcLocalBit = u64_ptr(bits, "bcsr_tcLocalBit");
+    b.data = values_ptr(data);
+    return b;
+}
+
+tcc_bcsc make_bcsc(std::uint32_t rows, std::uint32_t cols, std::uint32_t nnz, std::uint32_t blocks,
+                   std::uint32_t windows, const torch::Tensor& cwo, const torch::Tensor& tco,
+                   const torch::Tensor& a2c, const torch::Tensor& bits, const torch::Tensor* data) {
+    tcc_bcsc b{};
+    b.num_rows = rows;
+    b.num_cols = cols;
+    b.nnz = nnz;
+    b.num_TCBlocks = blocks;
+    b.num_colWindows = windows;
+    b.colWindowOffset = u32_ptr(cwo, "bcsc_colWindowOffset");
+    b.tcOffset = u32_ptr(tco, "bcsc_tcOffset");
+    b.sparseA2C = u32_ptr(a2c, "bcsc_sparseA2C");
+    b.tcLocalBit = u64_ptr(bits, "bcsc_tcLocalBit");
+    b.data = values_ptr(data);
+    return b;
+}
+
+// (num_rowWindows + 1) * 8 * F floats: spmm_launcher.cu:241-244
+std::int64_t denseC_elems(std::uint32_t windows, std::int32_t F) {
+    return (static_cast<std::int64_t>(windows) + 1) * 8 * F;
+}
+
+torch::Tensor view_of(float* p, std::uint32_t rows, std::int32_t F, int device) {
+    return torch::from_blob(p, {static_cast<std::int64_t>(rows) * F},
+                            torch::TensorOptions().dtype(torch::kFloat32).device(torch::kCUDA, device));
+}
+
+int current_device() {
+    int d = 0;
+    if (hipGetDevice(&d) != hipSuccess) throw std::runtime_error("spmm_cnic: hipGetDevice failed");
+    return d;
+}
+
+tcc_feature_source feature_source(const torch::Tensor& id_map, py::capsule cpu_ptr,
+                                  const torch::Tensor& cache_search_map, py::capsule gpu_ptr,
+                                  std::int32_t gpu_node_capacity, std::int64_t cpu_len) {
+    TORCH_CHECK(id_map.is_cuda() && id_map.scalar_type() == torch::kInt32 && id_map.is_contiguous(),
+                "id_map must be a contiguous int32 device tensor");
+    TORCH_CHECK(cache_search_map.is_cuda() && cache_search_map.scalar_type() == torch::kInt32 &&
+                    cache_search_map.is_contiguous(),
+                "cache_search_map must be a contiguous int32 device tensor");
+    TORCH_CHECK(gpu_node_capacity > 0, "gpu_node_capacity must be positive");
+    tcc_feature_source s{};
+    s.id_map = id_map.data_ptr<std::int32_t>();
+    s.cache_search_map = cache_search_map.data_ptr<std::int32_t>();
+    s.gpu_feature_cache = static_cast<const float* const*>(gpu_ptr.get_pointer());
+    s.gpu_node_capacity = gpu_node_capacity;
+    // The host feature rows are read zero-copy: translate the pinned host
+    // pointer to its device alias (mapped pinned memory only).
+    void* host = cpu_ptr.get_pointer();
+    void* dev = nullptr;
+    if (host != nullptr && hipHostGetDevicePointer(&dev, host, 0) != hipSuccess) {
+        throw std::runtime_error("spmm_cnic: cpu_feature_cache_ptr is not mapped pinned host memory");
+    }
+    s.cpu_features = static_cast<const float*>(dev);
+    s.cpu_feature_len = cpu_len;
+    s.gpu_feature_cache_count = 1;  // one GPU: the clique's pointer table has a single entry
+    return s;
+}
+
+// ---------------------------------------------------------------- compiled form
+
+torch::Tensor fwd_mixed_bound(std::uint32_t r_rows, std::uint32_t r_cols, std::uint32_t r_nnz, std::uint32_t r_blk,
+                              std::uint32_t r_win, torch::Tensor r_rwo, torch::Tensor r_tco, torch::Tensor r_a2b,
+                              torch::Tensor r_bits, std::uint32_t c_rows, std::uint32_t c_cols, std::uint32_t c_nnz,
+                              std::uint32_t c_blk, std::uint32_t c_win, torch::Tensor c_cwo, torch::Tensor c_tco,
+                              torch::Tensor c_a2c, torch::Tensor c_bits, std::int64_t cpu_len, std::int32_t cap,
+                              std::int32_t F, torch::Tensor id_map, py::capsule cpu_ptr, torch::Tensor csm,
+                              py::capsule gpu_ptr, torch::Tensor x, std::int32_t device_id, py::capsule denseC) {
+    // module.cu:100-190 (the compiled variant computes with x; an empty x
+    // selects the hot/cold feature source instead)
+    const tcc_bcsr A = make_bcsr(r_rows, r_cols, r_nnz, r_blk, r_win, r_rwo, r_tco, r_a2b, r_bits, nullptr);
+    const tcc_bcsc B = make_bcsc(c_rows, c_cols, c_nnz, c_blk, c_win, c_cwo, c_tco, c_a2c, c_bits, nullptr);
+    float* C = static_cast<float*>(denseC.get_pointer());
+    if (x.defined() && x.numel() > 0) {
+        TORCH_CHECK(x.is_cuda() && x.is_contiguous() && x.scalar_type() == torch::kFloat32, "x must be fp32 on device");
+        check(tcc_spmm_cnic_forward(&A, &B, x.data_ptr<float>(), C, F, stream_of(device_id)));
+    } else {
+        const tcc_feature_source s = feature_source(id_map, cpu_ptr, csm, gpu_ptr, cap, cpu_len);
+        check(tcc_spmm_cnic_forward_mixed(&A, &B, &s, C, F, stream_of(device_id)));
+    }
+    return view_of(C, r_rows, F, current_device());
+}
+
+torch::Tensor fwd_mixed_bound_nox(std::uint32_t r_rows, std::uint32_t r_cols, std::uint32_t r_nnz, std::uint32_t r_blk,
+                                  std::uint32_t r_win, torch::Tensor r_rwo, torch::Tensor r_tco, torch::Tensor r_a2b,
+                                  torch::Tensor r_bits, std::uint32_t c_rows, std::uint32_t c_cols,
+                                  std::uint32_t c_nnz, std::uint32_t c_blk, std::uint32_t c_win, torch::Tensor c_cwo,
+                                  torch::Tensor c_tco, torch::Tensor c_a2c, torch::Tensor c_bits, std::int64_t cpu_len,
+                                  std::int32_t cap, std::int32_t F, torch::Tensor id_map, py::capsule cpu_ptr,
+                                  torch::Tensor csm, py::capsule gpu_ptr, std::int32_t device_id,
+                                  py::capsule denseC) {
+    // the use_mixed_memory_access variant (module.cu:21-97)
+    return fwd_mixed_bound(r_rows, r_cols, r_nnz, r_blk, r_win, r_rwo, r_tco, r_a2b, r_bits, c_rows, c_cols, c_nnz,
+                           c_blk, c_win, c_cwo, c_tco, c_a2c, c_bits, cpu_len, cap, F, id_map, cpu_ptr, csm, gpu_ptr,
+                           torch::Tensor(), device_id, denseC);
+}
+
+torch::Tensor fwd_bound(std::uint32_t r_rows, std::uint32_t r_cols, std::uint32_t r_nnz, std::uint32_t r_blk,
+                        std::uint32_t r_win, torch::Tensor r_rwo, torch::Tensor r_tco, torch::Tensor r_a2b,
+                        torch::Tensor r_bits, std::uint32_t c_rows, std::uint32_t c_cols, std::uint32_t c_nnz,
+                        std::uint32_t c_blk, std::uint32_t c_win, torch::Tensor c_cwo, torch::Tensor c_tco,
+                        torch::Tensor c_a2c, torch::Tensor c_bits, std::int32_t F, torch::Tensor x,
+                        std::int32_t device_id, py::capsule denseC) {
+    // module.cu:192-273
+    const tcc_bcsr A = make_bcsr(r_rows, r_cols, r_nnz, r_blk, r_win, r_rwo, r_tco, r_a2b, r_bits, nullptr);
+    const tcc_bcsc B = make_bcsc(c_rows, c_cols, c_nnz, c_blk, c_win, c_cwo, c_tco, c_a2c, c_bits, nullptr);
+    TORCH_CHECK(x.is_cuda() && x.is_contiguous() && x.scalar_type() == torch::kFloat32, "x must be fp32 on device");
+    float* C = static_cast<float*>(denseC.get_pointer());
+    check(tcc_spmm_cnic_forward(&A, &B, x.data_ptr<float>(), C, F, stream_of(device_id)));
+    return view_of(C, r_rows, F, current_device());
+}
+
+// ---------------------------------------------------------------- Python-caller form
+
+torch::Tensor alloc_output(std::uint32_t windows, std::int32_t F) {
+    TORCH_CHECK(F >= 1, "feature_dim must be positive");
+    const int dev = current_device();
+    auto out = torch::empty({denseC_elems(windows, F)},
+                            torch::TensorOptions().dtype(torch::kFloat32).device(torch::kCUDA, dev));
+    g_outputs.push_back(out);
+    return out;
+}
+
+torch::Tensor fwd_mixed_py(std::uint32_t r_rows, std::uint32_t r_cols, std::uint32_t r_nnz, std::uint32_t r_blk,
+                           std::uint32_t r_win, torch::Tensor r_rwo, torch::Tensor r_tco, torch::Tensor r_a2b,
+                           torch::Tensor r_bits, torch::Tensor r_data, std::uint32_t c_rows, std::uint32_t c_cols,
+                           std::uint32_t c_nnz, std::uint32_t c_blk, std::uint32_t c_win, torch::Tensor c_cwo,
+                           torch::Tensor c_tco, torch::Tensor c_a2c, torch::Tensor c_bits, torch::Tensor c_data,
+                           std::int64_t cpu_len, std::int32_t cap, std::int32_t F, torch::Tensor id_map,
+                           py::capsule cpu_ptr, torch::Tensor csm, py::capsule gpu_ptr) {
+    // train/tcgnn_conv_release.py:116-122
+    const tcc_bcsr A = make_bcsr(r_rows, r_cols, r_nnz, r_blk, r_win, r_rwo, r_tco, r_a2b, r_bits, &r_data);
+    const tcc_bcsc B = make_bcsc(c_rows, c_cols, c_nnz, c_blk, c_win, c_cwo, c_tco, c_a2c, c_bits, &c_data);
+    const tcc_feature_source s = feature_source(id_map, cpu_ptr, csm, gpu_ptr, cap, cpu_len);
+    torch::Tensor out = alloc_output(r_win, F);
+    check(tcc_spmm_cnic_forward_mixed(&A, &B, &s, out.data_ptr<float>(), F, stream_of(current_device())));
+    return out.narrow(0, 0, static_cast<std::int64_t>(r_rows) * F);
+}
+
+torch::Tensor fwd_py(std::uint32_t r_rows, std::uint32_t r_cols, std::uint32_t r_nnz, std::uint32_t r_blk,
+                     std::uint32_t r_win, torch::Tensor r_rwo, torch::Tensor r_tco, torch::Tensor r_a2b,
+                     torch::Tensor r_bits, torch::Tensor r_data, std::uint32_t c_rows, std::uint32_t c_cols,
+                     std::uint32_t c_nnz, std::uint32_t c_blk, std::uint32_t c_win, torch::Tensor c_cwo,
+                     torch::Tensor c_tco, torch::Tensor c_a2c, torch::Tensor c_bits, torch::Tensor c_data,
+                     std::int32_t F, torch::Tensor x) {
+    // train/tcgnn_conv_release.py:124-130
+    const tcc_bcsr A = make_bcsr(r_rows, r_cols, r_nnz, r_blk, r_win, r_rwo, r_tco, r_a2b, r_bits, &r_data);
+    const tcc_bcsc B = make_bcsc(c_rows, c_cols, c_nnz, c_blk, c_win, c_cwo, c_tco, c_a2c, c_bits, &c_data);
+    TORCH_CHECK(x.is_cuda() && x.is_contiguous() && x.scalar_type() == torch::kFloat32, "x must be fp32 on device");
+    torch::Tensor out = alloc_output(r_win, F);
+    check(tcc_spmm_cnic_forward(&A, &B, x.data_ptr<float>(), out.data_ptr<float>(), F, stream_of(current_device())));
+    return out.narrow(0, 0, static_cast<std::int64_t>(r_rows) * F);
+}
+
+// ---------------------------------------------------------------- lifecycle
+
+void initialize(int device_id) {
+    // module.cu:299-304; work is ordered on torch's current stream instead of
+    // two private streams, so the returned tensors are safe to use at once.
+    if (hipSetDevice(device_id) != hipSuccess) throw std::runtime_error("spmm_cnic: hipSetDevice failed");
+}
+
+std::vector<py::capsule> space_malloc(int device_id, std::uint32_t denseC_size) {
+    // module.cu:306-327: two zeroed fp32 buffers of denseC_size elements
+    if (hipSetDevice(device_id) != hipSuccess) throw std::runtime_error("spmm_cnic: hipSetDevice failed");
+    std::vector<py::capsule> out;
+    for (const char* name : {"denseC", "denseC_2"}) {
+        void* p = nullptr;
+        const std::size_t bytes = static_cast<std::size_t>(denseC_size) * sizeof(float);
+        if (hipMalloc(&p, bytes) != hipSuccess || hipMemset(p, 0, bytes) != hipSuccess) {
+            throw std::runtime_error("spmm_cnic: space_malloc failed");
+        }
+        g_spaces.push_back(p);
+        out.emplace_back(p, name);
+    }
+    return out;
+}
+
+void finalize(int device_id) {
+    // module.cu:329-341
+    if (hipSetDevice(device_id) != hipSuccess) throw std::runtime_error("spmm_cnic: hipSetDevice failed");
+    if (hipDeviceSynchronize() != hipSuccess) throw std::runtime_error("spmm_cnic: hipDeviceSynchronize failed");
+    for (void* p : g_spaces) (void)hipFree(p);
+    g_spaces.clear();
+    g_outputs.clear();
+}
+
+void freeMatC() { g_outputs.clear(); }
+
+void set_use_values(bool on) { g_use_values = on; }
+
+void read_cpu_feature_cache(py::capsule p, std::int32_t len) {
+    const float* f = static_cast<const float*>(p.get_pointer());
+    std::printf("h_cpu_feature_cache: { ");
+    for (std::int32_t i = 0; i < len; ++i) std::printf("%f, ", f[i]);
+    std::printf("}\n");
+}
+
+void read_gpu0_feature_cache(py::capsule p) {
+    float h[100];
+    if (hipMemcpy(h, p.get_pointer(), sizeof(h), hipMemcpyDeviceToHost) != hipSuccess) {
+        throw std::runtime_error("spmm_cnic: hipMemcpy failed");
+    }
+    std::printf("gpu feature: { ");
+    for (float v : h) std::printf("%f, ", v);
+    std::printf("}\n");
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+    m.doc() = "spmm_cnic for ROCm / MI355X (block-sparse TF32-numerics SpMM over libtcc_swtcf)";
+    m.def("forward_tensorcore_mixed", &fwd_mixed_py, "first-layer SpMM, Python-caller form (allocates the output)");
+    m.def("forward_tensorcore_mixed", &fwd_mixed_bound, "first-layer SpMM, compiled form with x, device_id, denseC");
+    m.def("forward_tensorcore_mixed", &fwd_mixed_bound_nox, "first-layer SpMM, mixed-memory compiled form");
+    m.def("forward_tensorcore", &fwd_py, "SpMM, Python-caller form (allocates the output)");
+    m.def("forward_tensorcore", &fwd_bound, "SpMM, compiled form with device_id and denseC");
+    m.def("read_cpu_feature_cache", &read_cpu_feature_cache, "print host feature rows");
+    m.def("read_gpu0_feature_cache", &read_gpu0_feature_cache, "print the first 100 floats of a device cache");
+    m.def("initialize", &initialize, "select the device");
+    m.def("space_malloc", &space_malloc, "two zeroed denseC buffers (capsules)");
+    m.def("finalize", &finalize, "free space_malloc buffers and outputs");
+    m.def("freeMatC", &freeMatC, "release the outputs of the Python-caller form");
+    m.def("set_use_values", &set_use_values, "read the per-block data values (default: all entries 1.0)");
+}

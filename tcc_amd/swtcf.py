@@ -1,0 +1,338 @@
+"""Python host API over the C-ABI, for tests, the bench and Python callers.
+
+Device memory and streams come from PyTorch-ROCm; all compute runs in
+libtcc_swtcf.so.  Names follow the reference C++ API
+(include/swtcf_convert.cuh:74-78, include/swtcf_spmm.cuh:10-25).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import BCSC, BCSR, FeatureSource, SWTCFMatrix, SWTCFWorkspace, check
+
+INVALID_ROW_SLOT = 0xFFFFFFFF
+INVALID_CACHE_SLOT = 0xFF
+REPEAT_CACHE_SIZE = 32
+DEFAULT_TC_THRESHOLD = 12
+FEATURE_DIM = 128
+
+
+_hip = None
+
+
+def _hip_memcpy_d2h(dst: np.ndarray, src_ptr: int) -> None:
+    """hipMemcpy(device -> host) into a numpy array (synchronous)."""
+    global _hip
+    if _hip is None:
+        _hip = ctypes.CDLL("libamdhip64.so")
+        _hip.hipMemcpy.restype = ctypes.c_int
+        _hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    if dst.nbytes:
+        err = _hip.hipMemcpy(dst.ctypes.data, src_ptr, dst.nbytes, 2)  # hipMemcpyDeviceToHost
+        if err != 0:
+            raise RuntimeError(f"hipMemcpy failed ({err})")
+
+
+def _download(ptr: int, count: int, dtype) -> np.ndarray:
+    out = np.empty(int(count), dtype=dtype)
+    if count:
+        _hip_memcpy_d2h(out, ptr)
+    return out
+
+
+def _stream(stream=None) -> int:
+    s = torch.cuda.current_stream() if stream is None else stream
+    return s.cuda_stream
+
+
+def _ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _u32(t: torch.Tensor) -> torch.Tensor:
+    """int32/uint32 device tensor viewed as u32 storage (contiguous)."""
+    if t.dtype not in (torch.int32, torch.uint32):
+        raise TypeError(f"index tensors must be int32/uint32, got {t.dtype}")
+    if not t.is_cuda or not t.is_contiguous():
+        raise ValueError("index tensors must be contiguous device tensors")
+    return t
+
+
+class DeviceSWTCFMatrix:
+    """Owns one SWTCF matrix in device memory (allocateDeviceSWTCF /
+    freeDeviceSWTCF, src/swtcf_convert.cu:1113-1303)."""
+
+    def __init__(self, rows: int, cols: int, nnz: int, superWindowSize: int = 16):
+        self.m = SWTCFMatrix()
+        check(_lib.lib().tcc_swtcf_alloc_matrix(ctypes.byref(self.m), rows, cols, nnz, superWindowSize))
+
+    def free(self) -> None:
+        if self.m.superWindowRowOffset:
+            check(_lib.lib().tcc_swtcf_free_matrix(ctypes.byref(self.m)))
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    @property
+    def numColWindows(self) -> int:
+        return self.m.numColWindows
+
+    @property
+    def numSuperWindows(self) -> int:
+        return self.m.numSuperWindows
+
+    def to_host(self) -> dict:
+        """All arrays at their valid extents (SWTCF semantics, A.1 step 6),
+        as numpy, with the reference names."""
+        torch.cuda.synchronize()
+        m = self.m
+        cw, sw = m.numColWindows, m.numSuperWindows
+        cwo = _download(m.colWindowOffset, cw + 1, np.uint32)
+        swo = _download(m.superWindowRowOffset, sw + 1, np.uint32)
+        T, U = int(cwo[-1]), int(swo[-1])
+        d = dict(
+            colWindowOffset=cwo, superWindowRowOffset=swo,
+            tileLocalBit=_download(m.tileLocalBit, T, np.uint64),
+            tileRowSlot=_download(m.tileRowSlot, 8 * T, np.uint32),
+            superWindowRows=_download(m.superWindowRows, U, np.uint32),
+            superWindowRowCacheSlot=_download(m.superWindowRowCacheSlot, U, np.uint8),
+            superWindowCachedRowSlot=_download(m.superWindowCachedRowSlot, 32 * sw, np.uint32),
+            superWindowCachedCount=_download(m.superWindowCachedCount, sw, np.uint8),
+        )
+        d.update(numTiles=T, numRows=U, numColWindows=cw, numSuperWindows=sw, superWindowSize=m.superWindowSize,
+                 rows=m.rows, cols=m.cols)
+        return d
+
+
+class SWTCFConvertWorkspace:
+    """allocateSWTCFConvertWorkspace / freeSWTCFConvertWorkspace
+    (src/swtcf_convert.cu:1306-1751)."""
+
+    def __init__(self, edgeCapacity: int, numSrc: int, superWindowSize: int = 16):
+        self.ws = SWTCFWorkspace()
+        check(_lib.lib().tcc_swtcf_alloc_workspace(ctypes.byref(self.ws), edgeCapacity, numSrc, superWindowSize))
+
+    def free(self) -> None:
+        if self.ws.scratch:
+            check(_lib.lib().tcc_swtcf_free_workspace(ctypes.byref(self.ws)))
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def device_error(self) -> int:
+        """workspace.deviceError after the stream is drained (0 = none)."""
+        torch.cuda.synchronize()
+        return int(_download(self.ws.deviceError, 1, np.uint32)[0])
+
+    def num_groups(self) -> int:
+        torch.cuda.synchronize()
+        return int(_download(self.ws.deviceNumGroups, 1, np.uint32)[0])
+
+
+def convertCOOToSWTCF(dst: torch.Tensor, src: torch.Tensor, numEdges: int, output: DeviceSWTCFMatrix,
+                      workspace: SWTCFConvertWorkspace, stream=None) -> None:
+    _u32(dst)
+    _u32(src)
+    check(_lib.lib().tcc_swtcf_convert(dst.data_ptr(), src.data_ptr(), numEdges, ctypes.byref(output.m),
+                                       ctypes.byref(workspace.ws), _stream(stream)))
+
+
+def launchSWTCFSpMM(matrix: DeviceSWTCFMatrix, X: torch.Tensor, Y: torch.Tensor,
+                    tcThreshold: int = DEFAULT_TC_THRESHOLD, stream=None) -> None:
+    """Y += A X with F = 128 (src/swtcf_spmm.cu:437-466)."""
+    check(_lib.lib().tcc_swtcf_spmm(ctypes.byref(matrix.m), X.data_ptr(), Y.data_ptr(), tcThreshold,
+                                    _stream(stream)))
+
+
+def swtcf_spmm(matrix: DeviceSWTCFMatrix, X: torch.Tensor, Y: torch.Tensor,
+               tcThreshold: int = DEFAULT_TC_THRESHOLD, stream=None) -> None:
+    """Y += A X for any feature width (X: [cols x F], Y: [rows x F])."""
+    F = X.shape[1]
+    check(_lib.lib().tcc_swtcf_spmm_f(ctypes.byref(matrix.m), X.data_ptr(), Y.data_ptr(), F, tcThreshold,
+                                      _stream(stream)))
+
+
+def launchSWTCFSpMMQuantized(matrix: DeviceSWTCFMatrix, quantizedX: torch.Tensor, scales: torch.Tensor,
+                             srcGlobal: torch.Tensor, Y: torch.Tensor, tcThreshold: int = DEFAULT_TC_THRESHOLD,
+                             stream=None) -> None:
+    check(_lib.lib().tcc_swtcf_spmm_quantized(ctypes.byref(matrix.m), quantizedX.data_ptr(), scales.data_ptr(),
+                                              srcGlobal.data_ptr(), Y.data_ptr(), tcThreshold, _stream(stream)))
+
+
+# ---------------------------------------------------------------- BCSR / BCSC
+
+
+class BlockMatrix:
+    """A BCSR or BCSC built on the device by tcc_coo_to_bcsr/bcsc (owns one
+    allocation) or wrapping caller tensors (owns nothing)."""
+
+    def __init__(self, kind: str, view, allocation=None, keep=()):
+        self.kind = kind
+        self.view = view
+        self._alloc = allocation
+        self._keep = keep
+
+    def release(self) -> None:
+        if self._alloc:
+            check(_lib.lib().tcc_block_release(self._alloc))
+            self._alloc = None
+
+    def __del__(self):
+        try:
+            self.release()
+        except Exception:
+            pass
+
+    @property
+    def num_windows(self) -> int:
+        return self.view.num_rowWindows if self.kind == "bcsr" else self.view.num_colWindows
+
+    def to_host(self) -> dict:
+        torch.cuda.synchronize()
+        v = self.view
+        B, W = v.num_TCBlocks, self.num_windows
+        woff = "rowWindowOffset" if self.kind == "bcsr" else "colWindowOffset"
+        idx = "sparseA2B" if self.kind == "bcsr" else "sparseA2C"
+        d = {
+            woff: _download(getattr(v, woff), W + 1, np.uint32),
+            "tcOffset": _download(v.tcOffset, B + 1, np.uint32),
+            idx: _download(getattr(v, idx), 8 * B, np.uint32),
+            "tcLocalBit": _download(v.tcLocalBit, B, np.uint64),
+            "data": _download(v.data, v.nnz, np.float32) if v.data else None,
+        }
+        d.update(num_rows=v.num_rows, num_cols=v.num_cols, nnz=v.nnz, num_TCBlocks=B)
+        d["num_rowWindows" if self.kind == "bcsr" else "num_colWindows"] = W
+        return d
+
+
+def coo_to_bcsr(row: torch.Tensor, col: torch.Tensor, val: torch.Tensor | None, num_rows: int, num_cols: int,
+                stream=None) -> BlockMatrix:
+    view = BCSR()
+    alloc = ctypes.c_void_p()
+    check(_lib.lib().tcc_coo_to_bcsr(_u32(row).data_ptr(), _u32(col).data_ptr(), _ptr(val), row.numel(), num_rows,
+                                     num_cols, ctypes.byref(view), ctypes.byref(alloc), _stream(stream)))
+    return BlockMatrix("bcsr", view, alloc.value)
+
+
+def coo_to_bcsc(row: torch.Tensor, col: torch.Tensor, val: torch.Tensor | None, num_rows: int, num_cols: int,
+                stream=None) -> BlockMatrix:
+    view = BCSC()
+    alloc = ctypes.c_void_p()
+    check(_lib.lib().tcc_coo_to_bcsc(_u32(row).data_ptr(), _u32(col).data_ptr(), _ptr(val), row.numel(), num_rows,
+                                     num_cols, ctypes.byref(view), ctypes.byref(alloc), _stream(stream)))
+    return BlockMatrix("bcsc", view, alloc.value)
+
+
+def wrap_bcsr(num_rows, num_cols, nnz, num_TCBlocks, num_rowWindows, rowWindowOffset, tcOffset, sparseA2B,
+              tcLocalBit, data=None) -> BlockMatrix:
+    """View caller-owned device tensors as a BCSR (no copy)."""
+    v = BCSR(num_rows, num_cols, nnz, num_TCBlocks, num_rowWindows, _ptr(rowWindowOffset), _ptr(tcOffset),
+             _ptr(sparseA2B), _ptr(tcLocalBit), _ptr(data))
+    return BlockMatrix("bcsr", v, None, keep=(rowWindowOffset, tcOffset, sparseA2B, tcLocalBit, data))
+
+
+def wrap_bcsc(num_rows, num_cols, nnz, num_TCBlocks, num_colWindows, colWindowOffset, tcOffset, sparseA2C,
+              tcLocalBit, data=None) -> BlockMatrix:
+    v = BCSC(num_rows, num_cols, nnz, num_TCBlocks, num_colWindows, _ptr(colWindowOffset), _ptr(tcOffset),
+             _ptr(sparseA2C), _ptr(tcLocalBit), _ptr(data))
+    return BlockMatrix("bcsc", v, None, keep=(colWindowOffset, tcOffset, sparseA2C, tcLocalBit, data))
+
+
+def host_to_bcsr(d: dict, use_data: bool = False) -> BlockMatrix:
+    """Upload a host BCSR dict (numpy arrays, reference names) and wrap it."""
+    t = {k: torch.from_numpy(np.ascontiguousarray(d[k]).view(np.int32 if d[k].dtype == np.uint32 else
+                                                              (np.int64 if d[k].dtype == np.uint64 else d[k].dtype)))
+         .cuda() for k in ("rowWindowOffset", "tcOffset", "sparseA2B", "tcLocalBit", "data")}
+    return wrap_bcsr(d["num_rows"], d["num_cols"], d["nnz"], d["num_TCBlocks"], d["num_rowWindows"],
+                     t["rowWindowOffset"], t["tcOffset"], t["sparseA2B"], t["tcLocalBit"],
+                     t["data"] if use_data else None)
+
+
+def host_to_bcsc(d: dict, use_data: bool = False) -> BlockMatrix:
+    t = {k: torch.from_numpy(np.ascontiguousarray(d[k]).view(np.int32 if d[k].dtype == np.uint32 else
+                                                              (np.int64 if d[k].dtype == np.uint64 else d[k].dtype)))
+         .cuda() for k in ("colWindowOffset", "tcOffset", "sparseA2C", "tcLocalBit", "data")}
+    return wrap_bcsc(d["num_rows"], d["num_cols"], d["nnz"], d["num_TCBlocks"], d["num_colWindows"],
+                     t["colWindowOffset"], t["tcOffset"], t["sparseA2C"], t["tcLocalBit"],
+                     t["data"] if use_data else None)
+
+
+def bcsr_spmm(A: BlockMatrix, X: torch.Tensor, Y: torch.Tensor | None = None, accumulate: bool = False,
+              stream=None) -> torch.Tensor:
+    """Y[8*RW x F] (=|+=) A X, no atomics."""
+    F = X.shape[1]
+    if Y is None:
+        Y = torch.empty((A.view.num_rowWindows * 8, F), dtype=torch.float32, device=X.device)
+    check(_lib.lib().tcc_bcsr_spmm(ctypes.byref(A.view), X.data_ptr(), Y.data_ptr(), F, int(accumulate),
+                                   _stream(stream)))
+    return Y
+
+
+def bcsc_spmm(A: BlockMatrix, X: torch.Tensor, Y: torch.Tensor, stream=None) -> torch.Tensor:
+    """Y[num_rows x F] += A X with atomics."""
+    check(_lib.lib().tcc_bcsc_spmm(ctypes.byref(A.view), X.data_ptr(), Y.data_ptr(), X.shape[1], _stream(stream)))
+    return Y
+
+
+def bcsc_transpose_spmm(A: BlockMatrix, dY: torch.Tensor, dX: torch.Tensor | None = None, accumulate: bool = False,
+                        stream=None) -> torch.Tensor:
+    """dX[8*CW x F] (=|+=) A^T dY, no atomics."""
+    F = dY.shape[1]
+    if dX is None:
+        dX = torch.empty((A.view.num_colWindows * 8, F), dtype=torch.float32, device=dY.device)
+    check(_lib.lib().tcc_bcsc_transpose_spmm(ctypes.byref(A.view), dY.data_ptr(), dX.data_ptr(), F,
+                                             int(accumulate), _stream(stream)))
+    return dX
+
+
+def spmm_cnic_forward(bcsr: BlockMatrix, bcsc: BlockMatrix, X: torch.Tensor, denseC: torch.Tensor,
+                      stream=None) -> torch.Tensor:
+    check(_lib.lib().tcc_spmm_cnic_forward(ctypes.byref(bcsr.view), ctypes.byref(bcsc.view), X.data_ptr(),
+                                           denseC.data_ptr(), X.shape[1], _stream(stream)))
+    return denseC
+
+
+class FeatureSourceHandle:
+    """A tcc_feature_source plus references to the device tensors it points
+    into: the struct holds raw addresses, so the tensors must outlive every
+    launch that uses it (keep this object alive across those launches)."""
+
+    def __init__(self, struct: FeatureSource, keep: tuple):
+        self.struct = struct
+        self._keep = keep
+
+
+def feature_source(id_map: torch.Tensor, cache_search_map: torch.Tensor, gpu_cache_ptrs: torch.Tensor,
+                   gpu_node_capacity: int, cpu_features_dev_ptr: int, cpu_len: int) -> FeatureSourceHandle:
+    for t, name in ((id_map, "id_map"), (cache_search_map, "cache_search_map")):
+        if t.dtype != torch.int32 or not t.is_cuda or not t.is_contiguous():
+            raise TypeError(f"{name} must be a contiguous int32 device tensor")
+    if gpu_cache_ptrs.dtype != torch.int64 or not gpu_cache_ptrs.is_cuda:
+        raise TypeError("gpu_cache_ptrs must be an int64 device tensor of device pointers")
+    s = FeatureSource(id_map.data_ptr(), cache_search_map.data_ptr(), gpu_cache_ptrs.data_ptr(), gpu_node_capacity,
+                      cpu_features_dev_ptr, cpu_len, gpu_cache_ptrs.numel())
+    return FeatureSourceHandle(s, (id_map, cache_search_map, gpu_cache_ptrs))
+
+
+def spmm_cnic_forward_mixed(bcsr: BlockMatrix, bcsc: BlockMatrix, src: FeatureSourceHandle, denseC: torch.Tensor,
+                            F: int, stream=None) -> torch.Tensor:
+    check(_lib.lib().tcc_spmm_cnic_forward_mixed(ctypes.byref(bcsr.view), ctypes.byref(bcsc.view),
+                                                 ctypes.byref(src.struct), denseC.data_ptr(), F, _stream(stream)))
+    return denseC
+
+
+def bcsr_spmm_mixed(A: BlockMatrix, src: FeatureSourceHandle, Y: torch.Tensor, F: int, accumulate: bool = False,
+                    stream=None) -> torch.Tensor:
+    check(_lib.lib().tcc_bcsr_spmm_mixed(ctypes.byref(A.view), ctypes.byref(src.struct), Y.data_ptr(), F,
+                                         int(accumulate), _stream(stream)))
+    return Y

@@ -1,0 +1,269 @@
+"""GPU parity of the SpMM kernels against the CPU oracle, through the C-ABI.
+
+Tolerance: rel-L2 <= 1e-3 against the fp64 oracle on TF32-rounded inputs
+(the acceptance bound), and a tighter 1e-5 regression bound: the kernels
+round exactly the inputs the oracle rounds, so only fp32 summation order
+separates them.  The reference's own known-answer test
+(src/swtcf_spmm_main.cu:33-112) is checked with its own tolerances.
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+REL_L2 = 1e-3
+REL_L2_TIGHT = 1e-5
+
+
+def rel_l2(y, ref):
+    y = np.asarray(y, np.float64)
+    ref = np.asarray(ref, np.float64)
+    den = np.linalg.norm(ref)
+    return float(np.linalg.norm(y - ref) / (den if den > 0 else 1.0))
+
+
+def assert_close(y, ref, tight=True):
+    e = rel_l2(y, ref)
+    assert e <= REL_L2, e
+    if tight:
+        assert e <= REL_L2_TIGHT, e
+
+
+def random_coo(nd, ns, nnz, seed):
+    rng = np.random.default_rng(seed)
+    keys = np.sort(rng.choice(nd * ns, size=nnz, replace=False))
+    return (keys // ns).astype(np.uint32), (keys % ns).astype(np.uint32)
+
+
+def dev_u32(a):
+    return torch.from_numpy(np.ascontiguousarray(a, np.uint32).view(np.int32)).cuda()
+
+
+def build_swtcf(dst, src, rows, cols, S=16):
+    from tcc_amd import swtcf
+
+    m = swtcf.DeviceSWTCFMatrix(rows, cols, dst.size, S)
+    ws = swtcf.SWTCFConvertWorkspace(dst.size, cols, S)
+    swtcf.convertCOOToSWTCF(dev_u32(dst), dev_u32(src), dst.size, m, ws)
+    assert ws.device_error() == 0
+    return m
+
+
+# ------------------------------------------------------------------ SWTCF
+@pytest.mark.parametrize("tc", [12, 65])
+def test_swtcf_kat_reference_tolerances(gpu, oracle, tc):
+    """launchSWTCFSpMM with the reference's closed-form X and its tolerances."""
+    from tcc_amd import swtcf
+
+    dst, src = random_coo(900, 1500, 20000, 1)
+    m = build_swtcf(dst, src, 900, 1500)
+    X = torch.from_numpy(oracle.kat_fill_x(1500, 128)).cuda()
+    Y = torch.zeros((900, 128), device="cuda")
+    swtcf.launchSWTCFSpMM(m, X, Y, tc)
+    K = oracle.kat_expected(dst, src, 900, 128)
+    atol, rtol = (2e-4, 1e-4) if tc > 64 else (1e-2, 1e-2)
+    err = np.abs(Y.cpu().numpy() - K)
+    assert np.all(err <= atol + rtol * np.abs(K))
+
+
+@pytest.mark.parametrize("F", [1, 32, 100, 128, 200])
+@pytest.mark.parametrize("tc", [0, 12, 65])
+def test_swtcf_spmm_vs_oracle(gpu, oracle, F, tc):
+    from tcc_amd import swtcf
+
+    dst, src = random_coo(700, 1100, 15000, 2)
+    # a dense block so both threshold branches run
+    dd = np.repeat(np.arange(8, dtype=np.uint32), 8)
+    ss = np.tile(np.arange(16, 24, dtype=np.uint32), 8)
+    keys = np.unique(np.concatenate([dst.astype(np.int64) * 1100 + src, dd.astype(np.int64) * 1100 + ss]))
+    dst, src = (keys // 1100).astype(np.uint32), (keys % 1100).astype(np.uint32)
+    m = build_swtcf(dst, src, 700, 1100)
+    X = np.random.default_rng(3).standard_normal((1100, F)).astype(np.float32)
+    Y0 = np.random.default_rng(4).standard_normal((700, F)).astype(np.float32)  # Y += A X
+    Y = torch.from_numpy(Y0.copy()).cuda()
+    swtcf.swtcf_spmm(m, torch.from_numpy(X).cuda(), Y, tc)
+    ref = oracle.swtcf_convert(dst, src, 700, 1100, 16)
+    want = oracle.swtcf_spmm(ref, X, tc=tc, rows=700, Y=Y0.astype(np.float64))
+    assert_close(Y.cpu().numpy(), want)
+
+
+def test_swtcf_config1(gpu, oracle):
+    from tcc_amd import swtcf
+    from tcc_amd.graphs import make_features, uniform_graph
+
+    rows, cols = uniform_graph(4096, 16, 1)
+    dst, src = rows.numpy().astype(np.uint32), cols.numpy().astype(np.uint32)
+    m = build_swtcf(dst, src, 4096, 4096)
+    X = make_features(4096, 32, 1, dist="uniform")
+    Y = torch.zeros((4096, 32), device="cuda")
+    swtcf.swtcf_spmm(m, X.cuda(), Y, 12)
+    want = oracle.swtcf_spmm(oracle.swtcf_convert(dst, src, 4096, 4096, 16), X.numpy(), tc=12, rows=4096)
+    assert_close(Y.cpu().numpy(), want)
+
+
+def test_swtcf_quantized(gpu, oracle):
+    from tcc_amd import swtcf
+
+    dst, src = random_coo(500, 800, 9000, 5)
+    m = build_swtcf(dst, src, 500, 800)
+    rng = np.random.default_rng(6)
+    n_global = 1000
+    q = rng.integers(-128, 128, size=(n_global, 128), dtype=np.int8)
+    scales = rng.uniform(0.001, 0.1, n_global).astype(np.float32)
+    srcGlobal = rng.choice(n_global, size=800, replace=False).astype(np.uint32)
+    Y = torch.zeros((500, 128), device="cuda")
+    swtcf.launchSWTCFSpMMQuantized(m, torch.from_numpy(q).cuda(), torch.from_numpy(scales).cuda(),
+                                   dev_u32(srcGlobal), Y, 12)
+    Xdeq = q[srcGlobal].astype(np.float32) * scales[srcGlobal][:, None]  # src/swtcf_spmm.cu:317-323
+    want = oracle.swtcf_spmm(oracle.swtcf_convert(dst, src, 500, 800, 16), Xdeq, tc=12, rows=500)
+    assert_close(Y.cpu().numpy(), want)
+
+
+# ------------------------------------------------------------------ blocks
+def csr_of(dst, src, n, vals=None):
+    order = np.lexsort((src, dst))
+    rowptr = np.zeros(n + 1, np.int64)
+    rowptr[1:] = np.cumsum(np.bincount(dst, minlength=n))
+    return rowptr, src[order], None if vals is None else vals[order]
+
+
+def csc_of(dst, src, ncols, vals=None):
+    order = np.lexsort((dst, src))
+    colptr = np.zeros(ncols + 1, np.int64)
+    colptr[1:] = np.cumsum(np.bincount(src, minlength=ncols))
+    return colptr, dst[order], None if vals is None else vals[order]
+
+
+@pytest.mark.parametrize("values", [False, True])
+def test_coo_to_bcsr_bcsc_bit_exact(gpu, oracle, values):
+    from tcc_amd import swtcf
+
+    nr, nc = 1003, 1501
+    dst, src = random_coo(nr, nc, 25000, 7)
+    vals = np.random.default_rng(8).uniform(0.1, 1, dst.size).astype(np.float32) if values else None
+    perm = np.random.default_rng(9).permutation(dst.size)  # unsorted input
+    tv = None if vals is None else torch.from_numpy(vals[perm]).cuda()
+    A = swtcf.coo_to_bcsr(dev_u32(dst[perm]), dev_u32(src[perm]), tv, nr, nc).to_host()
+    rowptr, colind, v = csr_of(dst, src, nr, vals)
+    want = oracle.bcsr_build(nr, nc, rowptr, colind, v)
+    for k in ("rowWindowOffset", "tcOffset", "sparseA2B", "tcLocalBit"):
+        assert np.array_equal(A[k], want[k][:A[k].size]), k
+    assert A["num_TCBlocks"] == want["num_TCBlocks"]
+    if values:
+        assert np.array_equal(A["data"], want["data"])
+    B = swtcf.coo_to_bcsc(dev_u32(dst[perm]), dev_u32(src[perm]), tv, nr, nc).to_host()
+    colptr, rowind, cv = csc_of(dst, src, nc, vals)
+    wantc = oracle.bcsc_build(nr, nc, colptr, rowind, cv)
+    for k in ("colWindowOffset", "tcOffset", "sparseA2C", "tcLocalBit"):
+        assert np.array_equal(B[k], wantc[k][:B[k].size]), k
+    if values:
+        assert np.array_equal(B["data"], wantc["data"])
+
+
+@pytest.mark.parametrize("F", [1, 2, 32, 100, 128, 256, 602])
+@pytest.mark.parametrize("values", [False, True])
+def test_bcsr_bcsc_spmm_vs_oracle(gpu, oracle, F, values):
+    from tcc_amd import swtcf
+
+    nr, nc = 777, 901
+    dst, src = random_coo(nr, nc, 12000, 10 + F)
+    vals = np.random.default_rng(11).uniform(-1, 1, dst.size).astype(np.float32) if values else None
+    X = np.random.default_rng(12).standard_normal((nc, F)).astype(np.float32)
+    Xd = torch.from_numpy(X).cuda()
+    rowptr, colind, v = csr_of(dst, src, nr, vals)
+    want = oracle.csr_spmm(rowptr, colind, v, X, use_tf32=True)
+    tv = None if vals is None else torch.from_numpy(vals).cuda()
+    A = swtcf.coo_to_bcsr(dev_u32(dst), dev_u32(src), tv, nr, nc)
+    Y = swtcf.bcsr_spmm(A, Xd)
+    assert_close(Y.cpu().numpy()[:nr], want)
+    assert np.all(Y.cpu().numpy()[nr:] == 0)  # padding rows of the last window
+    # accumulate form
+    Y2 = swtcf.bcsr_spmm(A, Xd, Y.clone(), accumulate=True)
+    assert_close(Y2.cpu().numpy()[:nr], 2 * want)
+    Bc = swtcf.coo_to_bcsc(dev_u32(dst), dev_u32(src), tv, nr, nc)
+    Yc = torch.zeros((nr, F), device="cuda")
+    swtcf.bcsc_spmm(Bc, Xd, Yc)
+    assert_close(Yc.cpu().numpy(), want)
+    # backward: A^T dY via the BCSC as a gather
+    dY = np.random.default_rng(13).standard_normal((nr, F)).astype(np.float32)
+    colptr = np.zeros(nc + 1, np.int64)
+    order = np.lexsort((dst, src))
+    colptr[1:] = np.cumsum(np.bincount(src, minlength=nc))
+    wantT = oracle.csr_spmm(colptr, dst[order], None if vals is None else vals[order], dY, use_tf32=True)
+    dX = swtcf.bcsc_transpose_spmm(Bc, torch.from_numpy(dY).cuda())
+    assert_close(dX.cpu().numpy()[:nc], wantT)
+
+
+def test_oracle_built_blocks_consumed_identically(gpu, oracle):
+    """Kernels take any valid BCSR/BCSC (here the oracle's, uploaded as-is)."""
+    from tcc_amd import swtcf
+
+    nr, nc, F = 500, 640, 64
+    dst, src = random_coo(nr, nc, 7000, 14)
+    vals = np.random.default_rng(15).uniform(-1, 1, dst.size).astype(np.float32)
+    rowptr, colind, v = csr_of(dst, src, nr, vals)
+    d = oracle.bcsr_build(nr, nc, rowptr, colind, v)
+    X = np.random.default_rng(16).standard_normal((nc, F)).astype(np.float32)
+    Y = swtcf.bcsr_spmm(swtcf.host_to_bcsr(d, use_data=True), torch.from_numpy(X).cuda())
+    assert_close(Y.cpu().numpy(), oracle.bcsr_spmm(d, X, use_data=True))
+
+
+def test_spmm_cnic_forward_hot_cold_split(gpu, oracle):
+    """denseC = A_bcsr X + A_bcsc X (spmm_launcher.cu:203-271) with A split
+    into the edges of hot and cold sources."""
+    from tcc_amd import swtcf
+
+    nr = nc = 1200
+    F = 128
+    dst, src = random_coo(nr, nc, 20000, 17)
+    hot = np.random.default_rng(18).random(nc) < 0.3
+    h = hot[src]
+    A = swtcf.coo_to_bcsr(dev_u32(dst[h]), dev_u32(src[h]), None, nr, nc)
+    B = swtcf.coo_to_bcsc(dev_u32(dst[~h]), dev_u32(src[~h]), None, nr, nc)
+    X = np.random.default_rng(19).standard_normal((nc, F)).astype(np.float32)
+    denseC = torch.full(((A.view.num_rowWindows + 1) * 8, F), 7.0, device="cuda")  # garbage in
+    swtcf.spmm_cnic_forward(A, B, torch.from_numpy(X).cuda(), denseC)
+    rowptr, colind, _ = csr_of(dst, src, nr)
+    want = oracle.csr_spmm(rowptr, colind, None, X, use_tf32=True)
+    C = denseC.cpu().numpy()
+    assert_close(C[:nr], want)
+    assert np.all(C[nr:] == 0)
+
+
+def test_mixed_hot_cold_feature_source(gpu, oracle):
+    """First-layer form: hot rows from an HBM cache, cold rows zero-copy from
+    mapped pinned host memory (spmm_kernel.cu:129-153)."""
+    from tcc_amd import swtcf
+    from tcc_amd.hostmem import PinnedArray
+
+    nr = nc = 1000
+    F = 100
+    dst, src = random_coo(nr, nc, 15000, 20)
+    rng = np.random.default_rng(21)
+    feats = rng.standard_normal((nc, F)).astype(np.float32)  # global feature table, ids = identity
+    hot_ids = np.sort(rng.choice(nc, size=nc // 5, replace=False))
+    csm = np.full(nc, -1, np.int32)
+    csm[hot_ids] = np.arange(hot_ids.size, dtype=np.int32)
+    id_map = np.arange(nc, dtype=np.int32)
+    id_map[7] = -1  # a column with no feature row reads zeros
+    csm[7] = -1
+    hot_cache = torch.from_numpy(feats[hot_ids]).cuda()
+    cpu = PinnedArray((nc, F))
+    cpu.array[:] = feats
+    ptrs = torch.tensor([hot_cache.data_ptr()], dtype=torch.int64, device="cuda")
+    id_map_d = torch.from_numpy(id_map).cuda()
+    csm_d = torch.from_numpy(csm).cuda()
+    # the handle keeps id_map_d / csm_d / ptrs alive for the launch below
+    src_desc = swtcf.feature_source(id_map_d, csm_d, ptrs, hot_ids.size, cpu.device_ptr, nc * F)
+    hot_mask = csm[src] >= 0
+    A = swtcf.coo_to_bcsr(dev_u32(dst[hot_mask]), dev_u32(src[hot_mask]), None, nr, nc)
+    B = swtcf.coo_to_bcsc(dev_u32(dst[~hot_mask]), dev_u32(src[~hot_mask]), None, nr, nc)
+    denseC = torch.empty(((A.view.num_rowWindows + 1) * 8, F), device="cuda")
+    swtcf.spmm_cnic_forward_mixed(A, B, src_desc, denseC, F)
+    Xres = oracle.resolve_features(id_map, csm, feats[hot_ids], hot_ids.size, feats, F)
+    rowptr, colind, _ = csr_of(dst, src, nr)
+    want = oracle.csr_spmm(rowptr, colind, None, Xres, use_tf32=True)
+    assert_close(denseC.cpu().numpy()[:nr], want)
+    torch.cuda.synchronize()
+    cpu.free()

@@ -1,0 +1,166 @@
+"""The `spmm_cnic` extension: import/exports on CPU, and on the GPU every call
+form of the reference (spmm_cnic/src/bindings/module.cu:344-365 and
+train/tcgnn_conv_release.py:116-130, 324) against the oracle."""
+import ctypes
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+EXPORTS = ["forward_tensorcore_mixed", "forward_tensorcore", "read_cpu_feature_cache", "read_gpu0_feature_cache",
+           "initialize", "space_malloc", "finalize", "freeMatC"]
+
+
+def import_ext():
+    sys.path.insert(0, os.path.join(ROOT, "tcc_amd"))
+    try:
+        import spmm_cnic  # the name the training scripts import
+    finally:
+        sys.path.pop(0)
+    return spmm_cnic
+
+
+def test_extension_imports_and_exports():
+    m = import_ext()
+    for name in EXPORTS:
+        assert hasattr(m, name), name
+    # both call forms are overloads of the same names
+    assert "Overloaded function" in m.forward_tensorcore.__doc__
+    assert "Overloaded function" in m.forward_tensorcore_mixed.__doc__
+
+
+def _blocks(dst, src, nr, nc, vals=None):
+    import oracle
+
+    r64 = dst.astype(np.int64)
+    order = np.lexsort((src, dst))
+    rowptr = np.zeros(nr + 1, np.int64)
+    rowptr[1:] = np.cumsum(np.bincount(dst, minlength=nr))
+    bcsr = oracle.bcsr_build(nr, nc, rowptr, src[order], None if vals is None else vals[order])
+    order = np.lexsort((r64, src))
+    colptr = np.zeros(nc + 1, np.int64)
+    colptr[1:] = np.cumsum(np.bincount(src, minlength=nc))
+    bcsc = oracle.bcsc_build(nr, nc, colptr, dst[order], None if vals is None else vals[order])
+    return bcsr, bcsc
+
+
+def _dev(a):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint32:
+        a = a.view(np.int32)
+    if a.dtype == np.uint64:
+        a = a.view(np.int64)
+    return torch.from_numpy(a).cuda()
+
+
+def _args(bcsr, bcsc, with_data):
+    r = [bcsr["num_rows"], bcsr["num_cols"], bcsr["nnz"], bcsr["num_TCBlocks"], bcsr["num_rowWindows"],
+         _dev(bcsr["rowWindowOffset"]), _dev(bcsr["tcOffset"]), _dev(bcsr["sparseA2B"]), _dev(bcsr["tcLocalBit"])]
+    if with_data:
+        r.append(_dev(bcsr["data"]))
+    c = [bcsc["num_rows"], bcsc["num_cols"], bcsc["nnz"], bcsc["num_TCBlocks"], bcsc["num_colWindows"],
+         _dev(bcsc["colWindowOffset"]), _dev(bcsc["tcOffset"]), _dev(bcsc["sparseA2C"]), _dev(bcsc["tcLocalBit"])]
+    if with_data:
+        c.append(_dev(bcsc["data"]))
+    return r + c
+
+
+def _split(nr, nc, nnz, seed):
+    rng = np.random.default_rng(seed)
+    keys = np.sort(rng.choice(nr * nc, size=nnz, replace=False))
+    dst, src = (keys // nc).astype(np.uint32), (keys % nc).astype(np.uint32)
+    hot = rng.random(nc) < 0.25
+    return dst, src, hot
+
+
+def _want(dst, src, nr, X):
+    import oracle
+
+    order = np.lexsort((src, dst))
+    rowptr = np.zeros(nr + 1, np.int64)
+    rowptr[1:] = np.cumsum(np.bincount(dst, minlength=nr))
+    return oracle.csr_spmm(rowptr, src[order], None, X, use_tf32=True)
+
+
+def _rel(a, b):
+    return np.linalg.norm(a - b) / np.linalg.norm(b)
+
+
+@pytest.mark.gpu
+def test_forward_tensorcore_both_forms(gpu):
+    m = import_ext()
+    nr = nc = 700
+    F = 64
+    dst, src, hot = _split(nr, nc, 9000, 1)
+    h = hot[src]
+    bcsr, _ = _blocks(dst[h], src[h], nr, nc)
+    _, bcsc = _blocks(dst[~h], src[~h], nr, nc)
+    X = np.random.default_rng(2).standard_normal((nc, F)).astype(np.float32)
+    x = torch.from_numpy(X).cuda().flatten().contiguous()
+    want = _want(dst, src, nr, X)
+    # Python-caller form (train/tcgnn_conv_release.py:124-130)
+    out = m.forward_tensorcore(*_args(bcsr, bcsc, True), F, x)
+    assert out.shape == (nr * F,)
+    assert _rel(out.reshape(nr, F).cpu().numpy(), want) < 1e-5
+    m.freeMatC()
+    # compiled form with device_id and a space_malloc buffer (module.cu:192-273)
+    m.initialize(0)
+    caps = m.space_malloc(0, (bcsr["num_rowWindows"] + 1) * 8 * F)
+    out2 = m.forward_tensorcore(*_args(bcsr, bcsc, False), F, x, 0, caps[0])
+    assert _rel(out2.reshape(nr, F).cpu().numpy(), want) < 1e-5
+    torch.cuda.synchronize()
+    m.finalize(0)
+
+
+@pytest.mark.gpu
+def test_forward_tensorcore_mixed_forms(gpu):
+    from tcc_amd.hostmem import PinnedArray
+
+    m = import_ext()
+    nr = nc = 800
+    F = 100
+    dst, src, _ = _split(nr, nc, 10000, 3)
+    rng = np.random.default_rng(4)
+    feats = rng.standard_normal((nc, F)).astype(np.float32)
+    hot_ids = np.sort(rng.choice(nc, size=nc // 5, replace=False))
+    csm = np.full(nc, -1, np.int32)
+    csm[hot_ids] = np.arange(hot_ids.size, dtype=np.int32)
+    ids = np.arange(nc, dtype=np.int32)
+    hot_mask = csm[src] >= 0
+    bcsr, _ = _blocks(dst[hot_mask], src[hot_mask], nr, nc)
+    _, bcsc = _blocks(dst[~hot_mask], src[~hot_mask], nr, nc)
+    cache = torch.from_numpy(feats[hot_ids]).cuda()
+    ptr_table = torch.tensor([cache.data_ptr()], dtype=torch.int64, device="cuda")
+    cpu = PinnedArray((nc, F))
+    cpu.array[:] = feats
+    PyCapsule_New = ctypes.pythonapi.PyCapsule_New
+    PyCapsule_New.restype = ctypes.py_object
+    PyCapsule_New.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_void_p]
+    cpu_cap = PyCapsule_New(cpu._ptr.value, None, None)
+    gpu_cap = PyCapsule_New(ptr_table.data_ptr(), None, None)
+    want = _want(dst, src, nr, feats)
+    ids_d = torch.from_numpy(ids).cuda()
+    csm_d = torch.from_numpy(csm).cuda()
+    # Python-caller form (train/tcgnn_conv_release.py:116-122): 27 arguments
+    out = m.forward_tensorcore_mixed(*_args(bcsr, bcsc, True), nc * F, hot_ids.size, F,
+                                     ids_d, cpu_cap, csm_d, gpu_cap)
+    assert _rel(out.reshape(nr, F).cpu().numpy(), want) < 1e-5
+    m.freeMatC()
+    # compiled form with x (module.cu:100-190): computes with x
+    caps = m.space_malloc(0, (bcsr["num_rowWindows"] + 1) * 8 * F)
+    x = torch.from_numpy(feats).cuda().flatten()
+    out2 = m.forward_tensorcore_mixed(*_args(bcsr, bcsc, False), nc * F, hot_ids.size, F,
+                                      ids_d, cpu_cap, csm_d, gpu_cap,
+                                      x, 0, caps[0])
+    assert _rel(out2.reshape(nr, F).cpu().numpy(), want) < 1e-5
+    # mixed-memory compiled form (module.cu:21-97): reads the feature source
+    out3 = m.forward_tensorcore_mixed(*_args(bcsr, bcsc, False), nc * F, hot_ids.size, F,
+                                      ids_d, cpu_cap, csm_d, gpu_cap,
+                                      0, caps[1])
+    assert _rel(out3.reshape(nr, F).cpu().numpy(), want) < 1e-5
+    torch.cuda.synchronize()
+    m.finalize(0)
+    cpu.free()
