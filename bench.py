@@ -41,6 +41,8 @@ def parse():
     p.add_argument("--config", type=int, default=2, choices=sorted(WORKLOADS))
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-threads", type=int, default=0, help="0 = all host cores")
+    p.add_argument("--copy-calibration-mib", type=int, default=0,
+                   help="first run one plain device copy of this many MiB (scale for rocprofv3 FETCH/WRITE_SIZE)")
     return p.parse_args()
 
 
@@ -129,6 +131,15 @@ def main():
             swtcf.bcsr_spmm(A, X, Y)
 
         kernel = "gather_kernel"
+
+    if args.copy_calibration_mib:
+        nfl = args.copy_calibration_mib * (1 << 20) // 4
+        a_src = torch.ones(nfl, device="cuda")
+        a_dst = torch.empty_like(a_src)
+        torch.cuda.synchronize()
+        a_dst.copy_(a_src)  # reads and writes exactly copy_calibration_mib MiB
+        torch.cuda.synchronize()
+        del a_src, a_dst
 
     for _ in range(args.warmup):
         step()

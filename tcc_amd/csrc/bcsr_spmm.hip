@@ -43,6 +43,11 @@ struct GatherArgs {
     std::uint32_t F;
     std::uint32_t numChunks;
     int accumulate;
+    // work schedule (nullptr: one unit per window)
+    const std::uint64_t* schedule;
+    std::uint32_t numUnits;
+    std::uint32_t numSplitUnits;
+    std::uint32_t unitBlocks;
     // mixed feature source
     const std::int32_t* idMap;
     const std::int32_t* cacheSearchMap;
@@ -136,13 +141,99 @@ __device__ __forceinline__ const float* input_row(const GatherArgs& a, std::uint
     }
 }
 
+// A wave's unit of work: window w, blocks [b0, b1); `split` when other units
+// share the window (their partial sums are combined with atomics).
+struct Unit {
+    std::uint32_t w, b0, b1;
+    bool split;
+};
+
+__device__ __forceinline__ Unit unit_of(const std::uint32_t* winOffset, const std::uint64_t* schedule,
+                                        std::uint32_t unitBlocks, std::uint32_t u) {
+    Unit r;
+    if (schedule == nullptr) {
+        r.w = u;
+        r.b0 = winOffset[u];
+        r.b1 = winOffset[u + 1];
+        r.split = false;
+    } else {
+        const std::uint64_t e = schedule[u];
+        r.w = static_cast<std::uint32_t>(e >> 32);
+        const std::uint32_t j = static_cast<std::uint32_t>(e);
+        const std::uint32_t wb0 = winOffset[r.w], wb1 = winOffset[r.w + 1];
+        r.b0 = wb0 + j * unitBlocks;
+        r.b1 = min(r.b0 + unitBlocks, wb1);
+        r.split = (wb1 - wb0) > unitBlocks;
+    }
+    return r;
+}
+
+// The TF32-rounded input rows block b needs, in registers (x[C], zeros for
+// unused columns), plus its stored bitmap `raw` and the row-major view `bm`:
+// byte R of bm = the input columns C that output row R uses.
 template <int V, Src MODE>
+__device__ __forceinline__ void load_block(const GatherArgs& a, std::uint32_t b, std::uint32_t f0, bool active,
+                                           std::uint64_t& raw, std::uint64_t& bm, float (&x)[8][V]) {
+    raw = a.bits[b];
+    // Stored bit (r*8+c): BCSR = (output row r, column c); BCSC = (source row r,
+    // source column c), i.e. (input r, output c) for the A^T gather.
+    bm = (MODE == Src::Transposed) ? transpose8x8(raw) : raw;
+    std::uint32_t colmask = 0;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) colmask |= static_cast<std::uint32_t>(bm >> (8 * r)) & 0xFFu;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+#pragma unroll
+        for (int v = 0; v < V; ++v) x[c][v] = 0.0f;
+        if ((colmask >> c) & 1u) {
+            const std::uint32_t in = a.idx[static_cast<std::uint64_t>(b) * 8 + c];
+            if (in < a.numIn) {
+                const float* row = input_row<MODE>(a, in);
+                if (row != nullptr && active) {
+                    const Vec<V> t = load_vec<V>(row + f0);
+#pragma unroll
+                    for (int v = 0; v < V; ++v) x[c][v] = tf32_rna(t.v[v]);
+                }
+            }
+        }
+    }
+}
+
+// acc[R] += w(R,C) * x[C] over the block's nonzeros (uniform branches over
+// the bitmap); w = 1 without values, else the TF32-rounded stored value whose
+// rank is the number of stored nonzeros below its bit.
+template <int V, Src MODE, bool VALUES>
+__device__ __forceinline__ void accumulate_block(const GatherArgs& a, std::uint32_t b, std::uint64_t raw,
+                                                 std::uint64_t bm, const float (&x)[8][V], float (&acc)[8][V]) {
+    const float* vals = VALUES ? a.data + a.tcOffset[b] : nullptr;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        const std::uint32_t rb = static_cast<std::uint32_t>(bm >> (8 * r)) & 0xFFu;
+        if (rb == 0) continue;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            if (!(rb & (1u << c))) continue;
+            if constexpr (!VALUES) {
+#pragma unroll
+                for (int v = 0; v < V; ++v) acc[r][v] += x[c][v];
+            } else {
+                const unsigned stored = (MODE == Src::Transposed) ? (c * 8 + r) : (r * 8 + c);
+                const float w = tf32_rna(vals[__popcll(raw & ((1ull << stored) - 1ull))]);
+#pragma unroll
+                for (int v = 0; v < V; ++v) acc[r][v] = fmaf(w, x[c][v], acc[r][v]);
+            }
+        }
+    }
+}
+
+template <int V, Src MODE, bool VALUES>
 __global__ void __launch_bounds__(kThreads) gather_kernel(GatherArgs a) {
     const unsigned lane = __lane_id();
     const std::uint32_t gw = blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const std::uint32_t win = gw / a.numChunks;
-    const std::uint32_t chunk = gw - win * a.numChunks;
-    if (win >= a.numWindows) return;
+    const std::uint32_t unit = gw / a.numChunks;
+    const std::uint32_t chunk = gw - unit * a.numChunks;
+    if (unit >= a.numUnits) return;
+    const Unit u = unit_of(a.winOffset, a.schedule, a.unitBlocks, unit);
     const std::uint32_t f0 = chunk * (kWave * V) + lane * V;
     const bool active = f0 < a.F;
 
@@ -151,69 +242,54 @@ __global__ void __launch_bounds__(kThreads) gather_kernel(GatherArgs a) {
     for (int r = 0; r < 8; ++r)
 #pragma unroll
         for (int v = 0; v < V; ++v) acc[r][v] = 0.0f;
+    std::uint64_t touched = 0;  // union of the unit's row-major bitmaps
 
-    const std::uint32_t b0 = a.winOffset[win], b1 = a.winOffset[win + 1];
-    for (std::uint32_t b = b0; b < b1; ++b) {
-        const std::uint64_t raw = a.bits[b];
-        // Gather view: bit (R*8+C) = output row R, input column C.
-        const std::uint64_t bm = (MODE == Src::Transposed) ? transpose8x8(raw) : raw;
-        std::uint64_t cm = bm;
-        cm |= cm >> 32;
-        cm |= cm >> 16;
-        cm |= cm >> 8;
-        const std::uint32_t colmask = static_cast<std::uint32_t>(cm) & 0xFFu;
-        float x[8][V];
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-#pragma unroll
-            for (int v = 0; v < V; ++v) x[c][v] = 0.0f;
-            if (colmask & (1u << c)) {
-                const std::uint32_t in = a.idx[static_cast<std::uint64_t>(b) * 8 + c];
-                if (in < a.numIn) {
-                    const float* row = input_row<MODE>(a, in);
-                    if (row != nullptr && active) {
-                        const Vec<V> t = load_vec<V>(row + f0);
-#pragma unroll
-                        for (int v = 0; v < V; ++v) x[c][v] = tf32_rna(t.v[v]);
-                    }
-                }
-            }
-        }
-        if (a.data == nullptr) {
-#pragma unroll
-            for (int r = 0; r < 8; ++r) {
-                const std::uint32_t rb = static_cast<std::uint32_t>(bm >> (8 * r)) & 0xFFu;
-                if (rb == 0) continue;
-#pragma unroll
-                for (int c = 0; c < 8; ++c)
-                    if (rb & (1u << c))
-#pragma unroll
-                        for (int v = 0; v < V; ++v) acc[r][v] += x[c][v];
-            }
-        } else {
-            const float* vals = a.data + a.tcOffset[b];
-#pragma unroll
-            for (int r = 0; r < 8; ++r) {
-                const std::uint32_t rb = static_cast<std::uint32_t>(bm >> (8 * r)) & 0xFFu;
-                if (rb == 0) continue;
-#pragma unroll
-                for (int c = 0; c < 8; ++c) {
-                    if (rb & (1u << c)) {
-                        // value rank = set bits below this entry in the stored bitmap
-                        const unsigned bit = (MODE == Src::Transposed) ? (c * 8 + r) : (r * 8 + c);
-                        const std::uint64_t below = raw & ((1ull << bit) - 1ull);
-                        const float w = tf32_rna(vals[__popcll(below)]);
-#pragma unroll
-                        for (int v = 0; v < V; ++v) acc[r][v] = fmaf(w, x[c][v], acc[r][v]);
-                    }
-                }
-            }
+    std::uint32_t b = u.b0;
+    if constexpr (V <= 2) {
+        // two blocks per iteration: up to 16 independent row loads in flight
+        for (; b + 1 < u.b1; b += 2) {
+            std::uint64_t raw0, bm0, raw1, bm1;
+            float x0[8][V], x1[8][V];
+            load_block<V, MODE>(a, b, f0, active, raw0, bm0, x0);
+            load_block<V, MODE>(a, b + 1, f0, active, raw1, bm1, x1);
+            accumulate_block<V, MODE, VALUES>(a, b, raw0, bm0, x0, acc);
+            accumulate_block<V, MODE, VALUES>(a, b + 1, raw1, bm1, x1, acc);
+            touched |= bm0 | bm1;
         }
     }
+    for (; b < u.b1; ++b) {
+        std::uint64_t raw, bm;
+        float x[8][V];
+        load_block<V, MODE>(a, b, f0, active, raw, bm, x);
+        accumulate_block<V, MODE, VALUES>(a, b, raw, bm, x, acc);
+        touched |= bm;
+    }
     if (!active) return;
-    float* out = a.Y + static_cast<std::uint64_t>(win) * 8 * a.F + f0;
+    float* out = a.Y + static_cast<std::uint64_t>(u.w) * 8 * a.F + f0;
 #pragma unroll
-    for (int r = 0; r < 8; ++r) store_vec<V>(out + static_cast<std::uint64_t>(r) * a.F, acc[r], a.accumulate != 0);
+    for (int r = 0; r < 8; ++r) {
+        float* o = out + static_cast<std::uint64_t>(r) * a.F;
+        if (u.split) {
+            // rows of split windows were zeroed (or hold the accumulate input)
+            if (((touched >> (8 * r)) & 0xFFu) == 0) continue;
+#pragma unroll
+            for (int v = 0; v < V; ++v) atomic_add_f32(o + v, acc[r][v]);
+        } else {
+            store_vec<V>(o, acc[r], a.accumulate != 0);
+        }
+    }
+}
+
+// Zero the output rows of split windows before their units add into them
+// (only the unit with chunk index 0 of each split window does it).
+__global__ void zero_split_rows_kernel(const std::uint64_t* __restrict__ schedule, std::uint32_t numSplitUnits,
+                                       float* __restrict__ Y, std::uint32_t F) {
+    const std::uint32_t u = blockIdx.x;
+    if (u >= numSplitUnits) return;
+    const std::uint64_t e = schedule[u];
+    if (static_cast<std::uint32_t>(e) != 0) return;
+    float* p = Y + (e >> 32) * 8ull * F;
+    for (std::uint32_t i = threadIdx.x; i < 8u * F; i += blockDim.x) p[i] = 0.0f;
 }
 
 struct ScatterArgs {
@@ -229,6 +305,9 @@ struct ScatterArgs {
     std::uint32_t numCols;
     std::uint32_t F;
     std::uint32_t numChunks;
+    const std::uint64_t* schedule;
+    std::uint32_t numUnits;
+    std::uint32_t unitBlocks;
     // mixed feature source (first GCN layer)
     const std::int32_t* idMap;
     const std::int32_t* cacheSearchMap;
@@ -243,12 +322,14 @@ template <int V, bool MIXED>
 __global__ void __launch_bounds__(kThreads) scatter_kernel(ScatterArgs a) {
     const unsigned lane = __lane_id();
     const std::uint32_t gw = blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const std::uint32_t win = gw / a.numChunks;
-    const std::uint32_t chunk = gw - win * a.numChunks;
-    if (win >= a.numWindows) return;
+    const std::uint32_t unit = gw / a.numChunks;
+    const std::uint32_t chunk = gw - unit * a.numChunks;
+    if (unit >= a.numUnits) return;
+    const Unit u = unit_of(a.winOffset, a.schedule, a.unitBlocks, unit);
+    const std::uint32_t win = u.w;
     const std::uint32_t f0 = chunk * (kWave * V) + lane * V;
     const bool active = f0 < a.F;
-    const std::uint32_t b0 = a.winOffset[win], b1 = a.winOffset[win + 1];
+    const std::uint32_t b0 = u.b0, b1 = u.b1;
     if (b0 == b1 || !active) return;
 
     float x[8][V];
@@ -322,12 +403,24 @@ inline int pick_vec(std::uint32_t F, std::initializer_list<const void*> ptrs) {
 template <Src MODE>
 int launch_gather(GatherArgs a, int V, hipStream_t st) {
     a.numChunks = (a.F + kWave * V - 1) / (kWave * V);
-    const std::uint64_t waves = static_cast<std::uint64_t>(a.numWindows) * a.numChunks;
+    if (a.schedule == nullptr) a.numUnits = a.numWindows;
+    if (a.schedule != nullptr && a.numSplitUnits > 0 && !a.accumulate) {
+        hipLaunchKernelGGL(zero_split_rows_kernel, dim3(a.numSplitUnits), dim3(256), 0, st, a.schedule,
+                           a.numSplitUnits, a.Y, a.F);
+        TCC_LAUNCH_CHECK();
+    }
+    const std::uint64_t waves = static_cast<std::uint64_t>(a.numUnits) * a.numChunks;
     if (waves == 0) return TCC_OK;
     const dim3 grid(static_cast<unsigned>((waves + kWaves - 1) / kWaves));
-    if (V == 4) hipLaunchKernelGGL((gather_kernel<4, MODE>), grid, dim3(kThreads), 0, st, a);
-    else if (V == 2) hipLaunchKernelGGL((gather_kernel<2, MODE>), grid, dim3(kThreads), 0, st, a);
-    else hipLaunchKernelGGL((gather_kernel<1, MODE>), grid, dim3(kThreads), 0, st, a);
+    if (a.data != nullptr) {
+        if (V == 4) hipLaunchKernelGGL((gather_kernel<4, MODE, true>), grid, dim3(kThreads), 0, st, a);
+        else if (V == 2) hipLaunchKernelGGL((gather_kernel<2, MODE, true>), grid, dim3(kThreads), 0, st, a);
+        else hipLaunchKernelGGL((gather_kernel<1, MODE, true>), grid, dim3(kThreads), 0, st, a);
+    } else {
+        if (V == 4) hipLaunchKernelGGL((gather_kernel<4, MODE, false>), grid, dim3(kThreads), 0, st, a);
+        else if (V == 2) hipLaunchKernelGGL((gather_kernel<2, MODE, false>), grid, dim3(kThreads), 0, st, a);
+        else hipLaunchKernelGGL((gather_kernel<1, MODE, false>), grid, dim3(kThreads), 0, st, a);
+    }
     TCC_LAUNCH_CHECK();
     return TCC_OK;
 }
@@ -335,7 +428,8 @@ int launch_gather(GatherArgs a, int V, hipStream_t st) {
 template <bool MIXED>
 int launch_scatter(ScatterArgs a, int V, hipStream_t st) {
     a.numChunks = (a.F + kWave * V - 1) / (kWave * V);
-    const std::uint64_t waves = static_cast<std::uint64_t>(a.numWindows) * a.numChunks;
+    if (a.schedule == nullptr) a.numUnits = a.numWindows;
+    const std::uint64_t waves = static_cast<std::uint64_t>(a.numUnits) * a.numChunks;
     if (waves == 0) return TCC_OK;
     const dim3 grid(static_cast<unsigned>((waves + kWaves - 1) / kWaves));
     if (V == 4) hipLaunchKernelGGL((scatter_kernel<4, MIXED>), grid, dim3(kThreads), 0, st, a);
@@ -358,6 +452,10 @@ GatherArgs bcsr_args(const tcc_bcsr* A, const float* X, float* Y, std::uint32_t 
     a.numIn = A->num_cols;
     a.F = F;
     a.accumulate = accumulate;
+    a.schedule = A->schedule;
+    a.numUnits = A->numUnits;
+    a.numSplitUnits = A->numSplitUnits;
+    a.unitBlocks = A->unitBlocks;
     return a;
 }
 
@@ -374,17 +472,22 @@ ScatterArgs bcsc_args(const tcc_bcsc* A, const float* X, float* Y, std::uint32_t
     a.numRows = A->num_rows;
     a.numCols = A->num_cols;
     a.F = F;
+    a.schedule = A->schedule;
+    a.numUnits = A->numUnits;
+    a.unitBlocks = A->unitBlocks;
     return a;
 }
 
 bool bcsr_ok(const tcc_bcsr* A) {
     return A && (A->num_rowWindows == 0 || (A->rowWindowOffset && A->sparseA2B && A->tcLocalBit)) &&
-           (A->data == nullptr || A->tcOffset != nullptr);
+           (A->data == nullptr || A->tcOffset != nullptr) &&
+           (A->schedule == nullptr || (A->unitBlocks > 0 && A->numSplitUnits <= A->numUnits));
 }
 
 bool bcsc_ok(const tcc_bcsc* A) {
     return A && (A->num_colWindows == 0 || (A->colWindowOffset && A->sparseA2C && A->tcLocalBit)) &&
-           (A->data == nullptr || A->tcOffset != nullptr);
+           (A->data == nullptr || A->tcOffset != nullptr) &&
+           (A->schedule == nullptr || (A->unitBlocks > 0 && A->numSplitUnits <= A->numUnits));
 }
 
 }  // namespace
@@ -445,6 +548,10 @@ int tcc_bcsc_transpose_spmm(const tcc_bcsc* A, const float* dY, float* dX, std::
     a.numIn = A->num_rows;
     a.F = featureDim;
     a.accumulate = accumulate;
+    a.schedule = A->schedule;
+    a.numUnits = A->numUnits;
+    a.numSplitUnits = A->numSplitUnits;
+    a.unitBlocks = A->unitBlocks;
     const int V = pick_vec(featureDim, {dY, dX});
     return launch_gather<Src::Transposed>(a, V, as_stream(stream));
 }

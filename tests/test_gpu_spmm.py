@@ -267,3 +267,62 @@ def test_mixed_hot_cold_feature_source(gpu, oracle):
     assert_close(denseC.cpu().numpy()[:nr], want)
     torch.cuda.synchronize()
     cpu.free()
+
+
+# ------------------------------------------------------------------ work schedules
+def skewed_coo(nr, nc, seed):
+    """A few dense hub rows and hub columns over a sparse background."""
+    rng = np.random.default_rng(seed)
+    keys = set(rng.choice(nr * nc, size=6000, replace=False).tolist())
+    for r in (3, 4, 500):  # hub rows -> long BCSR windows
+        keys.update(r * nc + c for c in rng.choice(nc, size=nc // 2, replace=False).tolist())
+    for c in (7, 600):  # hub columns -> long BCSC windows
+        keys.update(r * nc + c for r in rng.choice(nr, size=nr // 2, replace=False).tolist())
+    k = np.array(sorted(keys), np.int64)
+    return (k // nc).astype(np.uint32), (k % nc).astype(np.uint32)
+
+
+@pytest.mark.parametrize("unit_blocks", [None, 1, 2, 3, 0])
+@pytest.mark.parametrize("F", [2, 64, 128, 256])
+def test_schedules_split_windows(gpu, oracle, unit_blocks, F):
+    """Windows split over several units add their partial sums atomically;
+    every schedule (and none) gives the same product."""
+    from tcc_amd import swtcf
+
+    nr, nc = 640, 900
+    dst, src = skewed_coo(nr, nc, 30 + F)
+    vals = np.random.default_rng(31).uniform(-1, 1, dst.size).astype(np.float32)
+    X = np.random.default_rng(32).standard_normal((nc, F)).astype(np.float32)
+    Xd = torch.from_numpy(X).cuda()
+    rowptr, colind, v = csr_of(dst, src, nr, vals)
+    want = oracle.csr_spmm(rowptr, colind, v, X, use_tf32=True)
+    A = swtcf.coo_to_bcsr(dev_u32(dst), dev_u32(src), torch.from_numpy(vals).cuda(), nr, nc)
+    A.set_schedule(unit_blocks)
+    if unit_blocks:
+        assert A.view.numSplitUnits > 0
+    Y = swtcf.bcsr_spmm(A, Xd, torch.full((A.view.num_rowWindows * 8, F), 9.0, device="cuda"))
+    assert_close(Y.cpu().numpy()[:nr], want)
+    Y2 = swtcf.bcsr_spmm(A, Xd, Y.clone(), accumulate=True)
+    assert_close(Y2.cpu().numpy()[:nr], 2 * want)
+    B = swtcf.coo_to_bcsc(dev_u32(dst), dev_u32(src), torch.from_numpy(vals).cuda(), nr, nc)
+    B.set_schedule(unit_blocks)
+    Yc = torch.zeros((nr, F), device="cuda")
+    swtcf.bcsc_spmm(B, Xd, Yc)
+    assert_close(Yc.cpu().numpy(), want)
+    dY = np.random.default_rng(33).standard_normal((nr, F)).astype(np.float32)
+    order = np.lexsort((dst, src))
+    colptr = np.zeros(nc + 1, np.int64)
+    colptr[1:] = np.cumsum(np.bincount(src, minlength=nc))
+    wantT = oracle.csr_spmm(colptr, dst[order], vals[order], dY, use_tf32=True)
+    dX = swtcf.bcsc_transpose_spmm(B, torch.from_numpy(dY).cuda(),
+                                   torch.full((B.view.num_colWindows * 8, F), 5.0, device="cuda"))
+    assert_close(dX.cpu().numpy()[:nc], wantT)
+
+
+def test_builder_attaches_schedule(gpu):
+    from tcc_amd import swtcf
+    from tcc_amd.graphs import rmat_graph
+
+    rows, cols = rmat_graph(20_000, 200_000, 5)
+    A = swtcf.coo_to_bcsr(rows.to(torch.int32).cuda(), cols.to(torch.int32).cuda(), None, 20_000, 20_000)
+    assert A.view.schedule and A.view.numUnits >= A.view.num_rowWindows and A.view.unitBlocks >= 16
