@@ -48,15 +48,11 @@ typedef struct tcc_bcsr {
     const uint32_t* sparseA2B;       /* [num_TCBlocks*8] */
     const uint64_t* tcLocalBit;      /* [num_TCBlocks] */
     const float* data;               /* [nnz] or NULL */
-    /* Optional work schedule (tcc_make_schedule; no reference counterpart).
-     * NULL: one unit of work per window.  Otherwise unit u covers blocks
-     * [off[w] + j*unitBlocks, min(off[w] + (j+1)*unitBlocks, off[w+1])) of
-     * window w, with schedule[u] = (w << 32) | j; the first numSplitUnits
-     * units belong to windows longer than unitBlocks, whose partial sums
-     * are combined with fp32 atomics. */
-    const uint64_t* schedule;
-    uint32_t numUnits;
-    uint32_t numSplitUnits;
+    /* Blocks per unit of work (no reference counterpart; 0 = automatic).
+     * The kernels cut the blocks into units of this many consecutive blocks,
+     * one wave each, regardless of window boundaries, so skewed windows are
+     * spread over many waves; a window split between units has its partial
+     * sums combined with fp32 atomics. */
     uint32_t unitBlocks;
 } tcc_bcsr;
 
@@ -72,10 +68,7 @@ typedef struct tcc_bcsc {
     const uint32_t* sparseA2C;       /* [num_TCBlocks*8] */
     const uint64_t* tcLocalBit;      /* [num_TCBlocks] */
     const float* data;               /* [nnz] or NULL */
-    const uint64_t* schedule;        /* optional, as in tcc_bcsr */
-    uint32_t numUnits;
-    uint32_t numSplitUnits;
-    uint32_t unitBlocks;
+    uint32_t unitBlocks;             /* as in tcc_bcsr */
 } tcc_bcsc;
 
 /* Where the first GCN layer reads feature row j from
@@ -98,9 +91,8 @@ typedef struct tcc_feature_source {
 } tcc_feature_source;
 
 /* Y[row-window rows x F] (=, or += when accumulate != 0) A_bcsr * X.
- * Row windows own their 8 output rows, so no atomics are used; with
- * accumulate == 0 every row 0..8*num_rowWindows-1 is written (empty windows
- * write zeros).  Y must hold 8*num_rowWindows*F floats.
+ * With accumulate == 0 every row 0..8*num_rowWindows-1 is written (empty
+ * windows write zeros).  Y must hold 8*num_rowWindows*F floats.
  * (tf32_spmm_bcsr, spmm_dispatcher.cu:167-232; kernel spmm_kernel.cu:1560-1842.) */
 int tcc_bcsr_spmm(const tcc_bcsr* A, const float* X, float* Y, uint32_t featureDim,
                   int accumulate, void* stream);
@@ -112,7 +104,7 @@ int tcc_bcsc_spmm(const tcc_bcsc* A, const float* X, float* Y, uint32_t featureD
 
 /* Transposed use of a BCSC for the backward pass: dX = A^T * dY, i.e.
  * dX[8w+c] (=, or +=) sum_b sum_r bit(r,c) * v * dY[sparseA2C[8b+r]] — a
- * gather with no atomics.  dX must hold 8*num_colWindows*F floats.  The
+ * gather (atomics only where a window is split between units).  dX must hold 8*num_colWindows*F floats.  The
  * reference computes this product with torch.sparse.mm
  * (train/tcgnn_conv_release.py:152); this is its block-sparse replacement. */
 int tcc_bcsc_transpose_spmm(const tcc_bcsc* A, const float* dY, float* dX,
@@ -136,18 +128,6 @@ int tcc_spmm_cnic_forward_mixed(const tcc_bcsr* bcsr, const tcc_bcsc* bcsc,
 int tcc_bcsr_spmm_mixed(const tcc_bcsr* A, const tcc_feature_source* src, float* Y,
                         uint32_t featureDim, int accumulate, void* stream);
 
-/* Builds a work schedule for a block matrix whose windows are given by the
- * device array dWindowOffset[numWindows+1] (rowWindowOffset of a BCSR or
- * colWindowOffset of a BCSC).  Power-law graphs put thousands of blocks in
- * a few windows; a schedule bounds the blocks any one wave walks by
- * unitBlocks (0 = choose from the block count) so those windows are spread
- * over many waves.  Split windows come first, longest first.  Copies the
- * offsets to the host (synchronises `stream`), allocates *dSchedule with
- * hipMalloc (free with tcc_block_release) and returns the counts. */
-int tcc_make_schedule(const uint32_t* dWindowOffset, uint32_t numWindows, uint32_t unitBlocks,
-                      uint64_t** dSchedule, uint32_t* numUnits, uint32_t* numSplitUnits,
-                      uint32_t* unitBlocksOut, void* stream);
-
 /* ---- construction ----
  * The reference receives these arrays from ipc_service (called at
  * train/tcgnn_conv_release.py:295-296), which is not part of its tree; these
@@ -156,10 +136,9 @@ int tcc_make_schedule(const uint32_t* dWindowOffset, uint32_t numWindows, uint32
  *   BCSR: per 8-row window, its distinct columns ascending, 8 per block.
  *   BCSC: per 8-source window, its rows by (degree desc, dst asc), 8 per
  *         block (the SWTCF row order with one window per super-window).
- * Each synchronises `stream` (to size the output), places all arrays and a
- * work schedule (as tcc_make_schedule with unitBlocks = 0) in one device
- * allocation returned in *allocation (free it with tcc_block_release) and
- * fills *out with views into it.  `data` is set only when dVal != NULL. */
+ * Each synchronises `stream` (to size the output), places all arrays in one
+ * device allocation returned in *allocation (free it with tcc_block_release)
+ * and fills *out with views into it.  `data` is set only when dVal != NULL. */
 int tcc_coo_to_bcsr(const uint32_t* dRow, const uint32_t* dCol, const float* dVal, uint32_t nnz,
                     uint32_t numRows, uint32_t numCols, tcc_bcsr* out, void** allocation, void* stream);
 int tcc_coo_to_bcsc(const uint32_t* dRow, const uint32_t* dCol, const float* dVal, uint32_t nnz,

@@ -41,7 +41,7 @@ class BCSR(ctypes.Structure):
     _fields_ = [
         ("num_rows", u32), ("num_cols", u32), ("nnz", u32), ("num_TCBlocks", u32), ("num_rowWindows", u32),
         ("rowWindowOffset", vp), ("tcOffset", vp), ("sparseA2B", vp), ("tcLocalBit", vp), ("data", vp),
-        ("schedule", vp), ("numUnits", u32), ("numSplitUnits", u32), ("unitBlocks", u32),
+        ("unitBlocks", u32),
     ]
 
 
@@ -50,7 +50,7 @@ class BCSC(ctypes.Structure):
     _fields_ = [
         ("num_rows", u32), ("num_cols", u32), ("nnz", u32), ("num_TCBlocks", u32), ("num_colWindows", u32),
         ("colWindowOffset", vp), ("tcOffset", vp), ("sparseA2C", vp), ("tcLocalBit", vp), ("data", vp),
-        ("schedule", vp), ("numUnits", u32), ("numSplitUnits", u32), ("unitBlocks", u32),
+        ("unitBlocks", u32),
     ]
 
 
@@ -84,8 +84,6 @@ SIGNATURES = {
     "tcc_coo_to_bcsr": (ctypes.c_int, [vp, vp, vp, u32, u32, u32, ctypes.POINTER(BCSR), ctypes.POINTER(vp), vp]),
     "tcc_coo_to_bcsc": (ctypes.c_int, [vp, vp, vp, u32, u32, u32, ctypes.POINTER(BCSC), ctypes.POINTER(vp), vp]),
     "tcc_block_release": (ctypes.c_int, [vp]),
-    "tcc_make_schedule": (ctypes.c_int, [vp, u32, u32, ctypes.POINTER(vp), ctypes.POINTER(u32), ctypes.POINTER(u32),
-                                         ctypes.POINTER(u32), vp]),
 }
 
 _lib = None

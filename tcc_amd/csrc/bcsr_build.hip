@@ -18,7 +18,6 @@
 #include "../../include/tcc_swtcf.h"
 #include "common.hpp"
 #include "primitives.hpp"
-#include "schedule.hpp"
 
 namespace tcc {
 namespace {
@@ -256,19 +255,9 @@ int tcc_coo_to_bcsr(const std::uint32_t* dRow, const std::uint32_t* dCol, const 
     }
     const std::uint32_t B = hostSmall[2];
 
-    // work schedule from the window offsets
-    std::vector<std::uint32_t> hostOff(static_cast<std::size_t>(RW) + 1);
-    TCC_HIP_CHECK(hipMemcpy(hostOff.data(), rwBlocks, 4ull * RW, hipMemcpyDeviceToHost));
-    hostOff[RW] = B;
-    const std::uint32_t K = auto_unit_blocks(B);
-    std::vector<std::uint64_t> units;
-    std::uint32_t numSplit = 0;
-    plan_units(hostOff.data(), RW, K, units, numSplit);
-
-    // outputs: rowWindowOffset[RW+1] tcOffset[B+1] sparseA2B[8B] tcLocalBit[B] data[E] schedule[U]
+    // outputs: rowWindowOffset[RW+1] tcOffset[B+1] sparseA2B[8B] tcLocalBit[B] data[E]
     const std::size_t outBytes = align_up(4 * (RW + 1)) + align_up(4 * (B + 1)) + align_up(32 * std::max(B, 1u)) +
-                                 align_up(8 * std::max(B, 1u)) + align_up(4 * En) +
-                                 align_up(8 * std::max<std::size_t>(units.size(), 1));
+                                 align_up(8 * std::max(B, 1u)) + align_up(4 * En);
     char* o = nullptr;
     TCC_HIP_CHECK(hipMalloc(&o, outBytes));
     char* q = o;
@@ -282,7 +271,6 @@ int tcc_coo_to_bcsr(const std::uint32_t* dRow, const std::uint32_t* dCol, const 
     auto* sparseA2B = reinterpret_cast<std::uint32_t*>(takeOut(32 * std::max(B, 1u)));
     auto* tcLocalBit = reinterpret_cast<std::uint64_t*>(takeOut(8 * std::max(B, 1u)));
     auto* data = reinterpret_cast<float*>(takeOut(4 * En));
-    auto* schedule = reinterpret_cast<std::uint64_t*>(takeOut(8 * std::max<std::size_t>(units.size(), 1)));
     auto fail = [&](int rc) {
         (void)hipFree(o);
         return rc;
@@ -290,9 +278,7 @@ int tcc_coo_to_bcsr(const std::uint32_t* dRow, const std::uint32_t* dCol, const 
     if (hipMemcpyAsync(rowWindowOffset, rwBlocks, 4 * RW, hipMemcpyDeviceToDevice, st) != hipSuccess ||
         hipMemcpyAsync(rowWindowOffset + RW, small + 2, 4, hipMemcpyDeviceToDevice, st) != hipSuccess ||
         fill<std::uint32_t>(sparseA2B, 8ull * B, TCC_SWTCF_INVALID_ROW_SLOT, st) != hipSuccess ||
-        fill<std::uint64_t>(tcLocalBit, B, 0ull, st) != hipSuccess ||
-        (!units.empty() &&
-         hipMemcpyAsync(schedule, units.data(), 8 * units.size(), hipMemcpyHostToDevice, st) != hipSuccess)) {
+        fill<std::uint64_t>(tcLocalBit, B, 0ull, st) != hipSuccess) {
         set_last_error("HIP error while initialising BCSR arrays");
         return fail(TCC_ERR_HIP);
     }
@@ -322,10 +308,6 @@ int tcc_coo_to_bcsr(const std::uint32_t* dRow, const std::uint32_t* dCol, const 
     out->sparseA2B = sparseA2B;
     out->tcLocalBit = tcLocalBit;
     out->data = dVal ? data : nullptr;
-    out->schedule = schedule;
-    out->numUnits = static_cast<std::uint32_t>(units.size());
-    out->numSplitUnits = numSplit;
-    out->unitBlocks = K;
     *allocation = o;
     return TCC_OK;
 }
@@ -367,15 +349,8 @@ int tcc_coo_to_bcsc(const std::uint32_t* dRow, const std::uint32_t* dCol, const 
     TCC_REQUIRE(hostErr == 0, TCC_ERR_INVALID_ARGUMENT,
                 "COO -> BCSC: converter error " + std::to_string(hostErr) + " (duplicates or indices out of range)");
 
-    std::vector<std::uint32_t> hostOff(static_cast<std::size_t>(CW) + 1);
-    TCC_HIP_CHECK(hipMemcpy(hostOff.data(), m.colWindowOffset, 4ull * (CW + 1), hipMemcpyDeviceToHost));
-    const std::uint32_t K = auto_unit_blocks(T);
-    std::vector<std::uint64_t> units;
-    std::uint32_t numSplit = 0;
-    plan_units(hostOff.data(), CW, K, units, numSplit);
     const std::size_t outBytes = align_up(4 * (CW + 1)) + align_up(4 * (T + 1)) + align_up(32 * std::max(T, 1u)) +
-                                 align_up(8 * std::max(T, 1u)) + align_up(4 * nnz) +
-                                 align_up(8 * std::max<std::size_t>(units.size(), 1)) + align_up(4 * std::max(U, 1u)) +
+                                 align_up(8 * std::max(T, 1u)) + align_up(4 * nnz) + align_up(4 * std::max(U, 1u)) +
                                  align_up(4 * std::max(T, 1u)) + align_up(4 * scan_temp_elems(T + 1));
     char* o = nullptr;
     TCC_HIP_CHECK(hipMalloc(&o, outBytes));
@@ -390,7 +365,6 @@ int tcc_coo_to_bcsc(const std::uint32_t* dRow, const std::uint32_t* dCol, const 
     auto* sparseA2C = reinterpret_cast<std::uint32_t*>(takeOut(32 * std::max(T, 1u)));
     auto* tcLocalBit = reinterpret_cast<std::uint64_t*>(takeOut(8 * std::max(T, 1u)));
     auto* data = reinterpret_cast<float*>(takeOut(4 * nnz));
-    auto* schedule = reinterpret_cast<std::uint64_t*>(takeOut(8 * std::max<std::size_t>(units.size(), 1)));
     auto* slotToLoc = reinterpret_cast<std::uint32_t*>(takeOut(4 * std::max(U, 1u)));  // scratch tail
     auto* counts = reinterpret_cast<std::uint32_t*>(takeOut(4 * std::max(T, 1u)));
     auto* temp = reinterpret_cast<std::uint32_t*>(takeOut(4 * scan_temp_elems(T + 1)));
@@ -400,9 +374,7 @@ int tcc_coo_to_bcsc(const std::uint32_t* dRow, const std::uint32_t* dCol, const 
     };
     if (hipMemcpyAsync(colWindowOffset, m.colWindowOffset, 4 * (CW + 1), hipMemcpyDeviceToDevice, st) !=
             hipSuccess ||
-        hipMemcpyAsync(tcLocalBit, m.tileLocalBit, 8ull * T, hipMemcpyDeviceToDevice, st) != hipSuccess ||
-        (!units.empty() &&
-         hipMemcpyAsync(schedule, units.data(), 8 * units.size(), hipMemcpyHostToDevice, st) != hipSuccess)) {
+        hipMemcpyAsync(tcLocalBit, m.tileLocalBit, 8ull * T, hipMemcpyDeviceToDevice, st) != hipSuccess) {
         set_last_error("HIP copy failed while building BCSC");
         return fail(TCC_ERR_HIP);
     }
@@ -430,10 +402,6 @@ int tcc_coo_to_bcsc(const std::uint32_t* dRow, const std::uint32_t* dCol, const 
     out->sparseA2C = sparseA2C;
     out->tcLocalBit = tcLocalBit;
     out->data = dVal ? data : nullptr;
-    out->schedule = schedule;
-    out->numUnits = static_cast<std::uint32_t>(units.size());
-    out->numSplitUnits = numSplit;
-    out->unitBlocks = K;
     *allocation = o;
     return TCC_OK;
 }

@@ -2,19 +2,30 @@
 // (reference: spmm_cnic/src/core/spmm_kernel.cu, spmm_dispatcher.cu,
 // spmm_launcher.cu).
 //
-// Gather (BCSR, mixed BCSR, BCSC-as-A^T): one wave per (8-row output window,
-// feature chunk of 64*V).  Block metadata (u64 bitmap, 8 indices, value
-// offset) is wave-uniform and read with scalar loads; each lane gathers V
-// consecutive features (V-wide vector loads) of the input rows named by the
-// block, rounds them to TF32, and accumulates the 8 output rows in registers.
-// Only the nonzeros of a block cost FMAs (uniform branches over the bitmap):
-// at the R-MAT densities of the target graphs a block holds ~8 of 64
-// entries, so a dense 8x8 contraction would waste ~7/8 of its work.  The
-// window owns its output rows, so results are stored without atomics.
+// Work split (merge-path over blocks): the blocks of a matrix are cut into
+// units of K consecutive blocks, whatever the window boundaries, so every
+// wave walks the same number of blocks however skewed the windows are (an
+// R-MAT row window can hold thousands of blocks).  A wave finds the first
+// window of its unit with a 64-way search over the window offsets, streams
+// the block metadata, and finishes a window whenever its blocks end.  A
+// window cut by a unit boundary is shared by several waves: its rows are
+// zeroed first and every wave adds its partial sums with fp32 atomics; all
+// other windows are stored directly.
 //
-// Scatter (BCSC): one wave per (8-source window, chunk) keeps the 8 source
-// rows in registers and adds each block row into Y with fp32 atomics, as the
-// reference does.
+// Gather (BCSR, mixed BCSR, BCSC read as A^T): one wave per (unit, chunk of
+// 64*V features).  Each lane holds V consecutive features of the 8 output
+// rows in registers.  Block metadata of 8 blocks is fetched with vector loads
+// one group ahead (input-row pointers, bitmaps, value offsets) and read with
+// v_readlane, so a block costs one round trip: its input rows (V-wide
+// loads, rounded to TF32) and its values.  Nonzeros are walked with uniform
+// branches over the bitmap: at the densities of the target graphs a block
+// holds ~8 of its 64 entries, ~1 per column, so neither a dense 8x8 VALU
+// contraction nor MFMA (which needs more than half the block set to beat
+// FMA) pays off.
+//
+// Scatter (BCSC forward): one wave per (unit, chunk); the 8 source rows of
+// the current window stay in registers and each block row is added into Y
+// with fp32 atomics, as the reference does.
 #include <algorithm>
 
 #include "../../include/tcc_spmm_cnic.h"
@@ -30,25 +41,8 @@ constexpr unsigned kWaves = kThreads / kWave;
 
 enum class Src { Plain, Mixed, Transposed };
 
-struct GatherArgs {
-    const std::uint32_t* winOffset;  // [numWindows+1]
-    const std::uint32_t* tcOffset;   // [blocks+1]
-    const std::uint32_t* idx;        // [8*blocks] input row of each block column
-    const std::uint64_t* bits;       // [blocks]
-    const float* data;               // values or nullptr
-    const float* X;                  // input rows (Plain / Transposed)
-    float* Y;                        // [8*numWindows x F]
-    std::uint32_t numWindows;
-    std::uint32_t numIn;  // idx values >= numIn are padding
-    std::uint32_t F;
-    std::uint32_t numChunks;
-    int accumulate;
-    // work schedule (nullptr: one unit per window)
-    const std::uint64_t* schedule;
-    std::uint32_t numUnits;
-    std::uint32_t numSplitUnits;
-    std::uint32_t unitBlocks;
-    // mixed feature source
+// Feature-source fields of the first GCN layer (tcc_feature_source).
+struct MixedArgs {
     const std::int32_t* idMap;
     const std::int32_t* cacheSearchMap;
     const float* const* gpuCache;
@@ -58,23 +52,39 @@ struct GatherArgs {
     std::uint32_t gpuCacheCount;
 };
 
+struct GatherArgs {
+    const std::uint32_t* winOffset;  // [numWindows+1]
+    const std::uint32_t* tcOffset;   // [blocks+1]
+    const std::uint32_t* idx;        // [8*blocks] input row of each block column
+    const std::uint64_t* bits;       // [blocks]
+    const float* data;               // values or nullptr
+    const float* X;                  // input rows (Plain / Transposed)
+    float* Y;                        // [8*numWindows x F]
+    std::uint32_t numWindows;
+    std::uint32_t numBlocks;
+    std::uint32_t numIn;  // idx values >= numIn are padding
+    std::uint32_t F;
+    std::uint32_t numChunks;
+    std::uint32_t unitBlocks;
+    std::uint32_t numUnits;
+    int accumulate;
+    MixedArgs mixed;
+};
+
 // Feature row of column `in` for the first-layer (mixed) form
 // (spmm_kernel.cu:129-153), or nullptr for a zero row.  Indices outside the
 // pointer table or past the host rows read zeros instead of faulting.
-__device__ __forceinline__ const float* mixed_row(const std::int32_t* idMap, const std::int32_t* csm,
-                                                  const float* const* gpuCache, std::int32_t cap,
-                                                  std::uint32_t cacheCount, const float* cpu, std::int64_t cpuLen,
-                                                  std::uint32_t F, std::uint32_t in) {
-    const std::int32_t g = csm[in];
+__device__ __forceinline__ const float* mixed_row(const MixedArgs& m, std::uint32_t F, std::uint32_t in) {
+    const std::int32_t g = m.cacheSearchMap[in];
     if (g >= 0) {
-        const std::int32_t d = g / cap;
-        if (cacheCount != 0 && static_cast<std::uint32_t>(d) >= cacheCount) return nullptr;
-        return gpuCache[d] + static_cast<std::int64_t>(g % cap) * F;
+        const std::int32_t d = g / m.gpuNodeCapacity;
+        if (m.gpuCacheCount != 0 && static_cast<std::uint32_t>(d) >= m.gpuCacheCount) return nullptr;
+        return m.gpuCache[d] + static_cast<std::int64_t>(g % m.gpuNodeCapacity) * F;
     }
-    const std::int32_t id = idMap[in];
-    if (id < 0 || cpu == nullptr) return nullptr;
-    if (cpuLen > 0 && (static_cast<std::int64_t>(id) + 1) * F > cpuLen) return nullptr;
-    return cpu + static_cast<std::int64_t>(id) * F;
+    const std::int32_t id = m.idMap[in];
+    if (id < 0 || m.cpuFeatures == nullptr) return nullptr;
+    if (m.cpuLen > 0 && (static_cast<std::int64_t>(id) + 1) * F > m.cpuLen) return nullptr;
+    return m.cpuFeatures + static_cast<std::int64_t>(id) * F;
 }
 
 template <int V>
@@ -130,82 +140,140 @@ __device__ __forceinline__ std::uint64_t transpose8x8(std::uint64_t x) {
     return x;
 }
 
-// Row base pointer of input `in` (wave-uniform), or nullptr for a zero row.
+__device__ __forceinline__ std::uint32_t lane_u32(std::uint32_t v, int l) {
+    return static_cast<std::uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), l));
+}
+
+__device__ __forceinline__ std::uint32_t uniform(std::uint32_t v) {
+    return static_cast<std::uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v)));
+}
+
+// First index i in [0, n) with off[i] >= key (n if there is none), for a
+// non-decreasing off[], computed by one wave: each round probes 64 evenly
+// spaced entries with one vector load and narrows the range to the gap the
+// ballot points at (3 rounds for 2^18 entries).
+__device__ std::uint32_t wave_lower_bound(const std::uint32_t* off, std::uint32_t n, std::uint32_t key) {
+    const unsigned lane = __lane_id();
+    std::uint32_t lo = 0, hi = n;  // answer in [lo, hi]
+    while (hi - lo > 64) {
+        const std::uint32_t step = (hi - lo + 63) / 64;
+        const std::uint32_t p = lo + (lane + 1) * step - 1;
+        const bool ge = p >= hi || off[p] >= key;
+        const std::uint64_t m = __ballot(ge);
+        if (m == 0) return hi;
+        const std::uint32_t L = static_cast<std::uint32_t>(__builtin_ctzll(m));
+        const std::uint32_t pL = lo + (L + 1) * step - 1;
+        lo = lo + L * step;
+        hi = min(pL, hi);
+    }
+    const std::uint32_t p = lo + lane;
+    const bool ge = p >= hi || off[p] >= key;
+    const std::uint64_t m = __ballot(ge);
+    return m == 0 ? hi : lo + static_cast<std::uint32_t>(__builtin_ctzll(m));
+}
+
+// The blocks [b0, b1) of unit u and the first window it finishes: the
+// window holding block b0, or (when windows start exactly at b0) the first
+// of them, empty ones included.
+struct UnitRange {
+    std::uint32_t b0, b1, w;
+    bool last;
+};
+
+__device__ __forceinline__ UnitRange unit_range(const std::uint32_t* winOffset, std::uint32_t numWindows,
+                                                std::uint32_t numBlocks, std::uint32_t K, std::uint32_t numUnits,
+                                                std::uint32_t u) {
+    UnitRange r;
+    r.b0 = u * K;
+    r.b1 = min(r.b0 + K, numBlocks);
+    r.last = u + 1 == numUnits;
+    const std::uint32_t lb = uniform(wave_lower_bound(winOffset, numWindows + 1, r.b0));
+    r.w = (lb <= numWindows && winOffset[lb] == r.b0) ? lb : lb - 1;
+    return r;
+}
+
+// Row base pointer of input `in` (nullptr for a zero row).
 template <Src MODE>
 __device__ __forceinline__ const float* input_row(const GatherArgs& a, std::uint32_t in) {
     if constexpr (MODE == Src::Mixed) {
-        return mixed_row(a.idMap, a.cacheSearchMap, a.gpuCache, a.gpuNodeCapacity, a.gpuCacheCount, a.cpuFeatures,
-                         a.cpuLen, a.F, in);
+        return mixed_row(a.mixed, a.F, in);
     } else {
         return a.X + static_cast<std::uint64_t>(in) * a.F;
     }
 }
 
-// A wave's unit of work: window w, blocks [b0, b1); `split` when other units
-// share the window (their partial sums are combined with atomics).
-struct Unit {
-    std::uint32_t w, b0, b1;
-    bool split;
+// Metadata of up to 8 consecutive blocks g..g+7, gathered with vector loads
+// one group ahead of its use: lane 8*k + c holds the input-row pointer of
+// column c of block g+k (null for padding or a missing row); lanes 0..7 hold
+// the bitmap and the value offset of block g+lane.
+struct GroupMeta {
+    std::uint32_t rowLo, rowHi;
+    std::uint32_t bitsLo, bitsHi;
+    std::uint32_t off;
 };
 
-__device__ __forceinline__ Unit unit_of(const std::uint32_t* winOffset, const std::uint64_t* schedule,
-                                        std::uint32_t unitBlocks, std::uint32_t u) {
-    Unit r;
-    if (schedule == nullptr) {
-        r.w = u;
-        r.b0 = winOffset[u];
-        r.b1 = winOffset[u + 1];
-        r.split = false;
-    } else {
-        const std::uint64_t e = schedule[u];
-        r.w = static_cast<std::uint32_t>(e >> 32);
-        const std::uint32_t j = static_cast<std::uint32_t>(e);
-        const std::uint32_t wb0 = winOffset[r.w], wb1 = winOffset[r.w + 1];
-        r.b0 = wb0 + j * unitBlocks;
-        r.b1 = min(r.b0 + unitBlocks, wb1);
-        r.split = (wb1 - wb0) > unitBlocks;
+template <Src MODE, bool VALUES>
+__device__ __forceinline__ GroupMeta load_group(const GatherArgs& a, std::uint32_t g, std::uint32_t end) {
+    const unsigned lane = __lane_id();
+    GroupMeta m;
+    const float* row = nullptr;
+    const std::uint32_t blk = g + lane / 8;
+    if (blk < end) {
+        const std::uint32_t in = a.idx[static_cast<std::uint64_t>(blk) * 8 + (lane & 7u)];
+        if (in < a.numIn) row = input_row<MODE>(a, in);
     }
-    return r;
+    const std::uint64_t rp = reinterpret_cast<std::uint64_t>(row);
+    m.rowLo = static_cast<std::uint32_t>(rp);
+    m.rowHi = static_cast<std::uint32_t>(rp >> 32);
+    const std::uint32_t bb = g + (lane & 7u);
+    std::uint64_t bits = 0;
+    std::uint32_t off = 0;
+    if (lane < 8 && bb < end) {
+        bits = a.bits[bb];
+        if constexpr (VALUES) off = a.tcOffset[bb];
+    }
+    m.bitsLo = static_cast<std::uint32_t>(bits);
+    m.bitsHi = static_cast<std::uint32_t>(bits >> 32);
+    m.off = off;
+    return m;
 }
 
-// The TF32-rounded input rows block b needs, in registers (x[C], zeros for
-// unused columns), plus its stored bitmap `raw` and the row-major view `bm`:
-// byte R of bm = the input columns C that output row R uses.
-template <int V, Src MODE>
-__device__ __forceinline__ void load_block(const GatherArgs& a, std::uint32_t b, std::uint32_t f0, bool active,
-                                           std::uint64_t& raw, std::uint64_t& bm, float (&x)[8][V]) {
-    raw = a.bits[b];
+// Block k of the group: its stored bitmap `raw`, the row-major view `bm`
+// (byte R = the input columns C that output row R uses), the TF32-rounded
+// input rows x[C] (zeros for padding), and its values (lane i = the value of
+// its i-th stored nonzero, TF32-rounded).
+template <int V, Src MODE, bool VALUES>
+__device__ __forceinline__ void load_block(const GatherArgs& a, const GroupMeta& m, int k, std::uint32_t laneOff,
+                                           std::uint64_t& raw, std::uint64_t& bm, float (&x)[8][V], float& vals) {
+    raw = (static_cast<std::uint64_t>(lane_u32(m.bitsHi, k)) << 32) | lane_u32(m.bitsLo, k);
     // Stored bit (r*8+c): BCSR = (output row r, column c); BCSC = (source row r,
     // source column c), i.e. (input r, output c) for the A^T gather.
     bm = (MODE == Src::Transposed) ? transpose8x8(raw) : raw;
-    std::uint32_t colmask = 0;
-#pragma unroll
-    for (int r = 0; r < 8; ++r) colmask |= static_cast<std::uint32_t>(bm >> (8 * r)) & 0xFFu;
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
+        const std::uint64_t rp = (static_cast<std::uint64_t>(lane_u32(m.rowHi, k * 8 + c)) << 32) |
+                                 lane_u32(m.rowLo, k * 8 + c);
 #pragma unroll
         for (int v = 0; v < V; ++v) x[c][v] = 0.0f;
-        if ((colmask >> c) & 1u) {
-            const std::uint32_t in = a.idx[static_cast<std::uint64_t>(b) * 8 + c];
-            if (in < a.numIn) {
-                const float* row = input_row<MODE>(a, in);
-                if (row != nullptr && active) {
-                    const Vec<V> t = load_vec<V>(row + f0);
+        if (rp != 0) {
+            const Vec<V> t = load_vec<V>(reinterpret_cast<const float*>(rp) + laneOff);
 #pragma unroll
-                    for (int v = 0; v < V; ++v) x[c][v] = tf32_rna(t.v[v]);
-                }
-            }
+            for (int v = 0; v < V; ++v) x[c][v] = tf32_rna(t.v[v]);
         }
+    }
+    vals = 0.0f;
+    if constexpr (VALUES) {
+        const std::uint32_t off = lane_u32(m.off, k);
+        if (__lane_id() < static_cast<unsigned>(__popcll(raw))) vals = tf32_rna(a.data[off + __lane_id()]);
     }
 }
 
 // acc[R] += w(R,C) * x[C] over the block's nonzeros (uniform branches over
-// the bitmap); w = 1 without values, else the TF32-rounded stored value whose
-// rank is the number of stored nonzeros below its bit.
+// the bitmap); w = 1 without values, else the value whose rank is the number
+// of stored nonzeros below its bit, read from `vals` with v_readlane.
 template <int V, Src MODE, bool VALUES>
-__device__ __forceinline__ void accumulate_block(const GatherArgs& a, std::uint32_t b, std::uint64_t raw,
-                                                 std::uint64_t bm, const float (&x)[8][V], float (&acc)[8][V]) {
-    const float* vals = VALUES ? a.data + a.tcOffset[b] : nullptr;
+__device__ __forceinline__ void accumulate_block(std::uint64_t raw, std::uint64_t bm, float vals,
+                                                 const float (&x)[8][V], float (&acc)[8][V]) {
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
         const std::uint32_t rb = static_cast<std::uint32_t>(bm >> (8 * r)) & 0xFFu;
@@ -218,7 +286,8 @@ __device__ __forceinline__ void accumulate_block(const GatherArgs& a, std::uint3
                 for (int v = 0; v < V; ++v) acc[r][v] += x[c][v];
             } else {
                 const unsigned stored = (MODE == Src::Transposed) ? (c * 8 + r) : (r * 8 + c);
-                const float w = tf32_rna(vals[__popcll(raw & ((1ull << stored) - 1ull))]);
+                const int rank = static_cast<int>(__popcll(raw & ((1ull << stored) - 1ull)));
+                const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(vals), rank));
 #pragma unroll
                 for (int v = 0; v < V; ++v) acc[r][v] = fmaf(w, x[c][v], acc[r][v]);
             }
@@ -226,70 +295,104 @@ __device__ __forceinline__ void accumulate_block(const GatherArgs& a, std::uint3
     }
 }
 
+// One wave per (unit, feature chunk of 64*V); waves are ordered chunk-major
+// so that the input rows one chunk touches stay in the last-level cache.
 template <int V, Src MODE, bool VALUES>
 __global__ void __launch_bounds__(kThreads) gather_kernel(GatherArgs a) {
     const unsigned lane = __lane_id();
-    const std::uint32_t gw = blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const std::uint32_t unit = gw / a.numChunks;
-    const std::uint32_t chunk = gw - unit * a.numChunks;
-    if (unit >= a.numUnits) return;
-    const Unit u = unit_of(a.winOffset, a.schedule, a.unitBlocks, unit);
+    const std::uint32_t gw = blockIdx.x * kWaves + uniform(threadIdx.x / kWave);
+    const std::uint32_t chunk = gw / a.numUnits;
+    const std::uint32_t unit = gw - chunk * a.numUnits;
+    if (chunk >= a.numChunks) return;
+    const UnitRange u = unit_range(a.winOffset, a.numWindows, a.numBlocks, a.unitBlocks, a.numUnits, unit);
+    if (u.w >= a.numWindows) return;  // offsets inconsistent with the block count
     const std::uint32_t f0 = chunk * (kWave * V) + lane * V;
     const bool active = f0 < a.F;
+    // inactive lanes read the row start (in bounds) and never store
+    const std::uint32_t laneOff = active ? f0 : 0u;
 
     float acc[8][V];
 #pragma unroll
     for (int r = 0; r < 8; ++r)
 #pragma unroll
         for (int v = 0; v < V; ++v) acc[r][v] = 0.0f;
-    std::uint64_t touched = 0;  // union of the unit's row-major bitmaps
+    std::uint64_t touched = 0;  // union of the current window's row-major bitmaps
 
-    std::uint32_t b = u.b0;
-    if constexpr (V <= 2) {
-        // two blocks per iteration: up to 16 independent row loads in flight
-        for (; b + 1 < u.b1; b += 2) {
-            std::uint64_t raw0, bm0, raw1, bm1;
-            float x0[8][V], x1[8][V];
-            load_block<V, MODE>(a, b, f0, active, raw0, bm0, x0);
-            load_block<V, MODE>(a, b + 1, f0, active, raw1, bm1, x1);
-            accumulate_block<V, MODE, VALUES>(a, b, raw0, bm0, x0, acc);
-            accumulate_block<V, MODE, VALUES>(a, b + 1, raw1, bm1, x1, acc);
-            touched |= bm0 | bm1;
+    std::uint32_t w = u.w;
+    std::uint32_t ws = a.winOffset[w], we = a.winOffset[w + 1];
+    // Finish window w: a window cut by a unit boundary is shared (rows
+    // pre-zeroed unless accumulating; atomics for the rows this unit
+    // touched), any other is stored whole.
+    auto flush = [&]() {
+        if (active) {
+            float* out = a.Y + static_cast<std::uint64_t>(w) * 8 * a.F + f0;
+            const bool shared = ws < u.b0 || we > u.b1;
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                float* o = out + static_cast<std::uint64_t>(r) * a.F;
+                if (shared) {
+                    if (((touched >> (8 * r)) & 0xFFu) == 0) continue;
+#pragma unroll
+                    for (int v = 0; v < V; ++v) atomic_add_f32(o + v, acc[r][v]);
+                } else {
+                    store_vec<V>(o, acc[r], a.accumulate != 0);
+                }
+            }
         }
-    }
-    for (; b < u.b1; ++b) {
-        std::uint64_t raw, bm;
-        float x[8][V];
-        load_block<V, MODE>(a, b, f0, active, raw, bm, x);
-        accumulate_block<V, MODE, VALUES>(a, b, raw, bm, x, acc);
-        touched |= bm;
-    }
-    if (!active) return;
-    float* out = a.Y + static_cast<std::uint64_t>(u.w) * 8 * a.F + f0;
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
-        float* o = out + static_cast<std::uint64_t>(r) * a.F;
-        if (u.split) {
-            // rows of split windows were zeroed (or hold the accumulate input)
-            if (((touched >> (8 * r)) & 0xFFu) == 0) continue;
+        for (int r = 0; r < 8; ++r)
 #pragma unroll
-            for (int v = 0; v < V; ++v) atomic_add_f32(o + v, acc[r][v]);
-        } else {
-            store_vec<V>(o, acc[r], a.accumulate != 0);
+            for (int v = 0; v < V; ++v) acc[r][v] = 0.0f;
+        touched = 0;
+    };
+
+    GroupMeta cur = load_group<MODE, VALUES>(a, u.b0, u.b1);
+    for (std::uint32_t g = u.b0; g < u.b1; g += 8) {
+        GroupMeta nxt = cur;
+        if (g + 8 < u.b1) nxt = load_group<MODE, VALUES>(a, g + 8, u.b1);
+        const int nb = static_cast<int>(min(8u, u.b1 - g));
+        for (int k = 0; k < nb; ++k) {
+            while (g + k >= we && w + 1 < a.numWindows) {  // the window ends before this block
+                flush();
+                ++w;
+                ws = we;
+                we = a.winOffset[w + 1];
+            }
+            std::uint64_t raw, bm;
+            float x[8][V], vv;
+            load_block<V, MODE, VALUES>(a, cur, k, laneOff, raw, bm, x, vv);
+            accumulate_block<V, MODE, VALUES>(raw, bm, vv, x, acc);
+            touched |= bm;
+        }
+        cur = nxt;
+    }
+    flush();
+    if (u.last) {
+        // trailing empty windows (offset == number of blocks)
+        while (++w < a.numWindows) {
+            ws = we = u.b1;
+            flush();
         }
     }
 }
 
-// Zero the output rows of split windows before their units add into them
-// (only the unit with chunk index 0 of each split window does it).
-__global__ void zero_split_rows_kernel(const std::uint64_t* __restrict__ schedule, std::uint32_t numSplitUnits,
-                                       float* __restrict__ Y, std::uint32_t F) {
-    const std::uint32_t u = blockIdx.x;
-    if (u >= numSplitUnits) return;
-    const std::uint64_t e = schedule[u];
-    if (static_cast<std::uint32_t>(e) != 0) return;
-    float* p = Y + (e >> 32) * 8ull * F;
-    for (std::uint32_t i = threadIdx.x; i < 8u * F; i += blockDim.x) p[i] = 0.0f;
+// Zero the rows of every window a unit boundary cuts (so that the units
+// sharing it can add into them).  One wave per boundary u*K, u >= 1; only the
+// first boundary inside a window zeroes it.
+__global__ void __launch_bounds__(kThreads) zero_shared_windows_kernel(const std::uint32_t* __restrict__ winOffset,
+                                                                      std::uint32_t numWindows, std::uint32_t K,
+                                                                      std::uint32_t numUnits, float* __restrict__ Y,
+                                                                      std::uint32_t F) {
+    const std::uint32_t u = 1 + blockIdx.x * kWaves + uniform(threadIdx.x / kWave);
+    if (u >= numUnits) return;
+    const std::uint32_t b0 = u * K;
+    const std::uint32_t lb = uniform(wave_lower_bound(winOffset, numWindows + 1, b0));
+    if (lb > numWindows) return;                    // offsets inconsistent with the block count
+    if (winOffset[lb] == b0) return;                // windows start at the boundary
+    const std::uint32_t w = lb - 1;
+    if (u >= 2 && winOffset[w] < b0 - K) return;  // boundary (u-1)*K cut it already
+    float* p = Y + static_cast<std::uint64_t>(w) * 8 * F;
+    for (std::uint32_t i = __lane_id(); i < 8u * F; i += kWave) p[i] = 0.0f;
 }
 
 struct ScatterArgs {
@@ -301,60 +404,76 @@ struct ScatterArgs {
     const float* X;
     float* Y;
     std::uint32_t numWindows;
+    std::uint32_t numBlocks;
     std::uint32_t numRows;
     std::uint32_t numCols;
     std::uint32_t F;
     std::uint32_t numChunks;
-    const std::uint64_t* schedule;
-    std::uint32_t numUnits;
     std::uint32_t unitBlocks;
-    // mixed feature source (first GCN layer)
-    const std::int32_t* idMap;
-    const std::int32_t* cacheSearchMap;
-    const float* const* gpuCache;
-    std::int32_t gpuNodeCapacity;
-    const float* cpuFeatures;
-    std::int64_t cpuLen;
-    std::uint32_t gpuCacheCount;
+    std::uint32_t numUnits;
+    MixedArgs mixed;
 };
 
+// The 8 source rows of window w, TF32-rounded (zeros past numCols).
 template <int V, bool MIXED>
-__global__ void __launch_bounds__(kThreads) scatter_kernel(ScatterArgs a) {
-    const unsigned lane = __lane_id();
-    const std::uint32_t gw = blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const std::uint32_t unit = gw / a.numChunks;
-    const std::uint32_t chunk = gw - unit * a.numChunks;
-    if (unit >= a.numUnits) return;
-    const Unit u = unit_of(a.winOffset, a.schedule, a.unitBlocks, unit);
-    const std::uint32_t win = u.w;
-    const std::uint32_t f0 = chunk * (kWave * V) + lane * V;
-    const bool active = f0 < a.F;
-    const std::uint32_t b0 = u.b0, b1 = u.b1;
-    if (b0 == b1 || !active) return;
-
-    float x[8][V];
+__device__ __forceinline__ void load_window_rows(const ScatterArgs& a, std::uint32_t w, std::uint32_t laneOff,
+                                                 float (&x)[8][V]) {
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-        const std::uint32_t col = win * 8 + c;
+        const std::uint32_t col = w * 8 + c;
 #pragma unroll
         for (int v = 0; v < V; ++v) x[c][v] = 0.0f;
         if (col < a.numCols) {
-            const float* row = a.X + static_cast<std::uint64_t>(col) * a.F;
+            const float* row;
             if constexpr (MIXED) {
                 // spmm_kernel.cu:521-595: the window's sources resolved once each.
-                row = mixed_row(a.idMap, a.cacheSearchMap, a.gpuCache, a.gpuNodeCapacity, a.gpuCacheCount,
-                                a.cpuFeatures, a.cpuLen, a.F, col);
+                row = mixed_row(a.mixed, a.F, col);
+            } else {
+                row = a.X + static_cast<std::uint64_t>(col) * a.F;
             }
             if (row != nullptr) {
-                const Vec<V> t = load_vec<V>(row + f0);
+                const Vec<V> t = load_vec<V>(row + laneOff);
 #pragma unroll
                 for (int v = 0; v < V; ++v) x[c][v] = tf32_rna(t.v[v]);
             }
         }
     }
-    for (std::uint32_t b = b0; b < b1; ++b) {
+}
+
+template <int V, bool MIXED, bool VALUES>
+__global__ void __launch_bounds__(kThreads) scatter_kernel(ScatterArgs a) {
+    const unsigned lane = __lane_id();
+    const std::uint32_t gw = blockIdx.x * kWaves + uniform(threadIdx.x / kWave);
+    const std::uint32_t chunk = gw / a.numUnits;
+    const std::uint32_t unit = gw - chunk * a.numUnits;
+    if (chunk >= a.numChunks) return;
+    const UnitRange u = unit_range(a.winOffset, a.numWindows, a.numBlocks, a.unitBlocks, a.numUnits, unit);
+    if (u.b0 >= u.b1 || u.w >= a.numWindows) return;
+    const std::uint32_t f0 = chunk * (kWave * V) + lane * V;
+    const bool active = f0 < a.F;
+    const std::uint32_t laneOff = active ? f0 : 0u;
+
+    std::uint32_t w = u.w;
+    std::uint32_t we = a.winOffset[w + 1];
+    while (we <= u.b0 && w + 1 < a.numWindows) {  // skip empty windows starting at b0
+        ++w;
+        we = a.winOffset[w + 1];
+    }
+    float x[8][V];
+    load_window_rows<V, MIXED>(a, w, laneOff, x);
+    for (std::uint32_t b = u.b0; b < u.b1; ++b) {
+        if (b >= we) {
+            do {
+                ++w;
+                we = a.winOffset[w + 1];
+            } while (b >= we && w + 1 < a.numWindows);
+            load_window_rows<V, MIXED>(a, w, laneOff, x);
+        }
         const std::uint64_t bm = a.bits[b];
-        const float* vals = a.data ? a.data + a.tcOffset[b] : nullptr;
+        float vals = 0.0f;
+        if constexpr (VALUES) {
+            if (lane < static_cast<unsigned>(__popcll(bm))) vals = tf32_rna(a.data[a.tcOffset[b] + lane]);
+        }
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
             const std::uint32_t rb = static_cast<std::uint32_t>(bm >> (8 * r)) & 0xFFu;
@@ -366,19 +485,22 @@ __global__ void __launch_bounds__(kThreads) scatter_kernel(ScatterArgs a) {
             for (int v = 0; v < V; ++v) s[v] = 0.0f;
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
-                if (rb & (1u << c)) {
-                    float w = 1.0f;
-                    if (vals) {
-                        const unsigned bit = r * 8 + c;
-                        w = tf32_rna(vals[__popcll(bm & ((1ull << bit) - 1ull))]);
-                    }
+                if (!(rb & (1u << c))) continue;
+                if constexpr (VALUES) {
+                    const int rank = static_cast<int>(__popcll(bm & ((1ull << (r * 8 + c)) - 1ull)));
+                    const float wv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(vals), rank));
 #pragma unroll
-                    for (int v = 0; v < V; ++v) s[v] = fmaf(w, x[c][v], s[v]);
+                    for (int v = 0; v < V; ++v) s[v] = fmaf(wv, x[c][v], s[v]);
+                } else {
+#pragma unroll
+                    for (int v = 0; v < V; ++v) s[v] += x[c][v];
                 }
             }
-            float* out = a.Y + static_cast<std::uint64_t>(row) * a.F + f0;
+            if (active) {
+                float* out = a.Y + static_cast<std::uint64_t>(row) * a.F + f0;
 #pragma unroll
-            for (int v = 0; v < V; ++v) atomic_add_f32(out + v, s[v]);
+                for (int v = 0; v < V; ++v) atomic_add_f32(out + v, s[v]);
+            }
         }
     }
 }
@@ -400,18 +522,30 @@ inline int pick_vec(std::uint32_t F, std::initializer_list<const void*> ptrs) {
     return 1;
 }
 
+// Blocks per unit: `requested` if nonzero, else enough units for about 64K
+// waves over all chunks (at least 8 blocks, at most 512, a power of two).
+inline std::uint32_t unit_blocks(std::uint32_t requested, std::uint32_t blocks, std::uint32_t chunks) {
+    if (requested != 0) return requested;
+    const std::uint64_t work = static_cast<std::uint64_t>(blocks) * chunks;
+    std::uint32_t K = 8;
+    while (K < 512 && work > static_cast<std::uint64_t>(K) * 65536) K *= 2;
+    return K;
+}
+
 template <Src MODE>
-int launch_gather(GatherArgs a, int V, hipStream_t st) {
+int launch_gather(GatherArgs a, int V, std::uint32_t requestedK, hipStream_t st) {
+    if (a.numWindows == 0) return TCC_OK;
     a.numChunks = (a.F + kWave * V - 1) / (kWave * V);
-    if (a.schedule == nullptr) a.numUnits = a.numWindows;
-    if (a.schedule != nullptr && a.numSplitUnits > 0 && !a.accumulate) {
-        hipLaunchKernelGGL(zero_split_rows_kernel, dim3(a.numSplitUnits), dim3(256), 0, st, a.schedule,
-                           a.numSplitUnits, a.Y, a.F);
+    a.unitBlocks = unit_blocks(requestedK, a.numBlocks, a.numChunks);
+    a.numUnits = std::max<std::uint32_t>(1, (a.numBlocks + a.unitBlocks - 1) / a.unitBlocks);
+    const std::uint64_t waves = static_cast<std::uint64_t>(a.numUnits) * a.numChunks;
+    TCC_REQUIRE(waves <= 0xFFFFFFFFull / kWaves, TCC_ERR_UNSUPPORTED, "SpMM launch too large");
+    if (a.numUnits > 1 && !a.accumulate) {
+        hipLaunchKernelGGL(zero_shared_windows_kernel, dim3(grid_for(a.numUnits - 1, kWaves)), dim3(kThreads), 0, st,
+                           a.winOffset, a.numWindows, a.unitBlocks, a.numUnits, a.Y, a.F);
         TCC_LAUNCH_CHECK();
     }
-    const std::uint64_t waves = static_cast<std::uint64_t>(a.numUnits) * a.numChunks;
-    if (waves == 0) return TCC_OK;
-    const dim3 grid(static_cast<unsigned>((waves + kWaves - 1) / kWaves));
+    const dim3 grid(grid_for(waves, kWaves));
     if (a.data != nullptr) {
         if (V == 4) hipLaunchKernelGGL((gather_kernel<4, MODE, true>), grid, dim3(kThreads), 0, st, a);
         else if (V == 2) hipLaunchKernelGGL((gather_kernel<2, MODE, true>), grid, dim3(kThreads), 0, st, a);
@@ -426,17 +560,37 @@ int launch_gather(GatherArgs a, int V, hipStream_t st) {
 }
 
 template <bool MIXED>
-int launch_scatter(ScatterArgs a, int V, hipStream_t st) {
+int launch_scatter(ScatterArgs a, int V, std::uint32_t requestedK, hipStream_t st) {
+    if (a.numWindows == 0 || a.numBlocks == 0) return TCC_OK;
     a.numChunks = (a.F + kWave * V - 1) / (kWave * V);
-    if (a.schedule == nullptr) a.numUnits = a.numWindows;
+    a.unitBlocks = unit_blocks(requestedK, a.numBlocks, a.numChunks);
+    a.numUnits = (a.numBlocks + a.unitBlocks - 1) / a.unitBlocks;
     const std::uint64_t waves = static_cast<std::uint64_t>(a.numUnits) * a.numChunks;
-    if (waves == 0) return TCC_OK;
-    const dim3 grid(static_cast<unsigned>((waves + kWaves - 1) / kWaves));
-    if (V == 4) hipLaunchKernelGGL((scatter_kernel<4, MIXED>), grid, dim3(kThreads), 0, st, a);
-    else if (V == 2) hipLaunchKernelGGL((scatter_kernel<2, MIXED>), grid, dim3(kThreads), 0, st, a);
-    else hipLaunchKernelGGL((scatter_kernel<1, MIXED>), grid, dim3(kThreads), 0, st, a);
+    TCC_REQUIRE(waves <= 0xFFFFFFFFull / kWaves, TCC_ERR_UNSUPPORTED, "SpMM launch too large");
+    const dim3 grid(grid_for(waves, kWaves));
+    if (a.data != nullptr) {
+        if (V == 4) hipLaunchKernelGGL((scatter_kernel<4, MIXED, true>), grid, dim3(kThreads), 0, st, a);
+        else if (V == 2) hipLaunchKernelGGL((scatter_kernel<2, MIXED, true>), grid, dim3(kThreads), 0, st, a);
+        else hipLaunchKernelGGL((scatter_kernel<1, MIXED, true>), grid, dim3(kThreads), 0, st, a);
+    } else {
+        if (V == 4) hipLaunchKernelGGL((scatter_kernel<4, MIXED, false>), grid, dim3(kThreads), 0, st, a);
+        else if (V == 2) hipLaunchKernelGGL((scatter_kernel<2, MIXED, false>), grid, dim3(kThreads), 0, st, a);
+        else hipLaunchKernelGGL((scatter_kernel<1, MIXED, false>), grid, dim3(kThreads), 0, st, a);
+    }
     TCC_LAUNCH_CHECK();
     return TCC_OK;
+}
+
+MixedArgs mixed_args(const tcc_feature_source* src) {
+    MixedArgs m{};
+    m.idMap = src->id_map;
+    m.cacheSearchMap = src->cache_search_map;
+    m.gpuCache = src->gpu_feature_cache;
+    m.gpuNodeCapacity = src->gpu_node_capacity;
+    m.cpuFeatures = src->cpu_features;
+    m.cpuLen = src->cpu_feature_len;
+    m.gpuCacheCount = src->gpu_feature_cache_count;
+    return m;
 }
 
 GatherArgs bcsr_args(const tcc_bcsr* A, const float* X, float* Y, std::uint32_t F, int accumulate) {
@@ -449,13 +603,10 @@ GatherArgs bcsr_args(const tcc_bcsr* A, const float* X, float* Y, std::uint32_t 
     a.X = X;
     a.Y = Y;
     a.numWindows = A->num_rowWindows;
+    a.numBlocks = A->num_TCBlocks;
     a.numIn = A->num_cols;
     a.F = F;
     a.accumulate = accumulate;
-    a.schedule = A->schedule;
-    a.numUnits = A->numUnits;
-    a.numSplitUnits = A->numSplitUnits;
-    a.unitBlocks = A->unitBlocks;
     return a;
 }
 
@@ -469,25 +620,21 @@ ScatterArgs bcsc_args(const tcc_bcsc* A, const float* X, float* Y, std::uint32_t
     a.X = X;
     a.Y = Y;
     a.numWindows = A->num_colWindows;
+    a.numBlocks = A->num_TCBlocks;
     a.numRows = A->num_rows;
     a.numCols = A->num_cols;
     a.F = F;
-    a.schedule = A->schedule;
-    a.numUnits = A->numUnits;
-    a.unitBlocks = A->unitBlocks;
     return a;
 }
 
 bool bcsr_ok(const tcc_bcsr* A) {
     return A && (A->num_rowWindows == 0 || (A->rowWindowOffset && A->sparseA2B && A->tcLocalBit)) &&
-           (A->data == nullptr || A->tcOffset != nullptr) &&
-           (A->schedule == nullptr || (A->unitBlocks > 0 && A->numSplitUnits <= A->numUnits));
+           (A->data == nullptr || A->tcOffset != nullptr);
 }
 
 bool bcsc_ok(const tcc_bcsc* A) {
     return A && (A->num_colWindows == 0 || (A->colWindowOffset && A->sparseA2C && A->tcLocalBit)) &&
-           (A->data == nullptr || A->tcOffset != nullptr) &&
-           (A->schedule == nullptr || (A->unitBlocks > 0 && A->numSplitUnits <= A->numUnits));
+           (A->data == nullptr || A->tcOffset != nullptr);
 }
 
 }  // namespace
@@ -502,7 +649,8 @@ int tcc_bcsr_spmm(const tcc_bcsr* A, const float* X, float* Y, std::uint32_t fea
     clear_last_error();
     TCC_REQUIRE(bcsr_ok(A) && X && Y && featureDim >= 1, TCC_ERR_INVALID_ARGUMENT, "invalid BCSR SpMM arguments");
     const int V = pick_vec(featureDim, {X, Y});
-    return launch_gather<Src::Plain>(bcsr_args(A, X, Y, featureDim, accumulate), V, as_stream(stream));
+    return launch_gather<Src::Plain>(bcsr_args(A, X, Y, featureDim, accumulate), V, A->unitBlocks,
+                                     as_stream(stream));
 }
 
 int tcc_bcsr_spmm_mixed(const tcc_bcsr* A, const tcc_feature_source* src, float* Y, std::uint32_t featureDim,
@@ -512,23 +660,18 @@ int tcc_bcsr_spmm_mixed(const tcc_bcsr* A, const tcc_feature_source* src, float*
                     src->gpu_feature_cache && src->gpu_node_capacity > 0,
                 TCC_ERR_INVALID_ARGUMENT, "invalid mixed BCSR SpMM arguments");
     GatherArgs a = bcsr_args(A, nullptr, Y, featureDim, accumulate);
-    a.idMap = src->id_map;
-    a.cacheSearchMap = src->cache_search_map;
-    a.gpuCache = src->gpu_feature_cache;
-    a.gpuNodeCapacity = src->gpu_node_capacity;
-    a.cpuFeatures = src->cpu_features;
-    a.cpuLen = src->cpu_feature_len;
-    a.gpuCacheCount = src->gpu_feature_cache_count;
+    a.mixed = mixed_args(src);
     // Hot-cache bases live in a device pointer table and are taken to be
     // 16-byte aligned (hipMalloc / torch allocations); host rows are checked.
     const int V = pick_vec(featureDim, {Y, src->cpu_features});
-    return launch_gather<Src::Mixed>(a, V, as_stream(stream));
+    return launch_gather<Src::Mixed>(a, V, A->unitBlocks, as_stream(stream));
 }
 
 int tcc_bcsc_spmm(const tcc_bcsc* A, const float* X, float* Y, std::uint32_t featureDim, void* stream) {
     clear_last_error();
     TCC_REQUIRE(bcsc_ok(A) && X && Y && featureDim >= 1, TCC_ERR_INVALID_ARGUMENT, "invalid BCSC SpMM arguments");
-    return launch_scatter<false>(bcsc_args(A, X, Y, featureDim), pick_vec(featureDim, {X, Y}), as_stream(stream));
+    return launch_scatter<false>(bcsc_args(A, X, Y, featureDim), pick_vec(featureDim, {X, Y}), A->unitBlocks,
+                                 as_stream(stream));
 }
 
 int tcc_bcsc_transpose_spmm(const tcc_bcsc* A, const float* dY, float* dX, std::uint32_t featureDim,
@@ -545,15 +688,12 @@ int tcc_bcsc_transpose_spmm(const tcc_bcsc* A, const float* dY, float* dX, std::
     a.X = dY;
     a.Y = dX;
     a.numWindows = A->num_colWindows;
+    a.numBlocks = A->num_TCBlocks;
     a.numIn = A->num_rows;
     a.F = featureDim;
     a.accumulate = accumulate;
-    a.schedule = A->schedule;
-    a.numUnits = A->numUnits;
-    a.numSplitUnits = A->numSplitUnits;
-    a.unitBlocks = A->unitBlocks;
     const int V = pick_vec(featureDim, {dY, dX});
-    return launch_gather<Src::Transposed>(a, V, as_stream(stream));
+    return launch_gather<Src::Transposed>(a, V, A->unitBlocks, as_stream(stream));
 }
 
 int tcc_spmm_cnic_forward(const tcc_bcsr* bcsr, const tcc_bcsc* bcsc, const float* X, float* denseC,
@@ -582,14 +722,8 @@ int tcc_spmm_cnic_forward_mixed(const tcc_bcsr* bcsr, const tcc_bcsc* bcsc, cons
     int rc = tcc_bcsr_spmm_mixed(bcsr, src, denseC, featureDim, 0, stream);
     if (rc) return rc;
     ScatterArgs b = bcsc_args(bcsc, nullptr, denseC, featureDim);
-    b.idMap = src->id_map;
-    b.cacheSearchMap = src->cache_search_map;
-    b.gpuCache = src->gpu_feature_cache;
-    b.gpuNodeCapacity = src->gpu_node_capacity;
-    b.cpuFeatures = src->cpu_features;
-    b.cpuLen = src->cpu_feature_len;
-    b.gpuCacheCount = src->gpu_feature_cache_count;
-    return launch_scatter<true>(b, pick_vec(featureDim, {denseC, src->cpu_features}), st);
+    b.mixed = mixed_args(src);
+    return launch_scatter<true>(b, pick_vec(featureDim, {denseC, src->cpu_features}), bcsc->unitBlocks, st);
 }
 
 }  // extern "C"

@@ -34,10 +34,8 @@ namespace {
 
 std::vector<torch::Tensor> g_outputs;  // Python-caller form outputs, released by freeMatC()
 std::vector<void*> g_spaces;           // space_malloc buffers, released by finalize()
-std::vector<void*> g_sched_prev;       // work schedules of earlier calls (maybe still in use)
-std::vector<void*> g_sched_cur;        // work schedules of the current call
 bool g_use_values = false;
-std::uint32_t g_balance_min_blocks = 65536;  // build a work schedule from this many blocks up
+std::uint32_t g_unit_blocks = 0;       // blocks per unit of work (0 = automatic)
 
 void check(int rc) {
     if (rc != 0) {
@@ -83,6 +81,7 @@ tcc_bcsr make_bcsr(std::uint32_t rows, std::uint32_t cols, std::uint32_t nnz, st
     b.sparseA2B = u32_ptr(a2b, "bcsr_sparseA2B");
     b.tcLocalBit = u64_ptr(bits, "bcsr_tcLocalBit");
     b.data = values_ptr(data);
+    b.unitBlocks = g_unit_blocks;
     return b;
 }
 
@@ -100,39 +99,8 @@ tcc_bcsc make_bcsc(std::uint32_t rows, std::uint32_t cols, std::uint32_t nnz, st
     b.sparseA2C = u32_ptr(a2c, "bcsc_sparseA2C");
     b.tcLocalBit = u64_ptr(bits, "bcsc_tcLocalBit");
     b.data = values_ptr(data);
+    b.unitBlocks = g_unit_blocks;
     return b;
-}
-
-// Work schedules for large block matrices (skewed graphs put thousands of
-// blocks in a few windows), built per call.  tcc_make_schedule drains the
-// stream before it returns, after which the schedules of earlier calls are no
-// longer in use and are freed.
-void begin_call() {
-    g_sched_prev.insert(g_sched_prev.end(), g_sched_cur.begin(), g_sched_cur.end());
-    g_sched_cur.clear();
-}
-
-template <typename M>
-void attach_schedule(M& A, const std::uint32_t* offsets, std::uint32_t windows, void* stream) {
-    if (A.num_TCBlocks < g_balance_min_blocks) return;
-    std::uint64_t* sched = nullptr;
-    std::uint32_t units = 0, split = 0, k = 0;
-    check(tcc_make_schedule(offsets, windows, 0, &sched, &units, &split, &k, stream));
-    // the stream is drained now: schedules of earlier calls are free to go
-    for (void* p : g_sched_prev) (void)hipFree(p);
-    g_sched_prev.clear();
-    g_sched_cur.push_back(sched);
-    A.schedule = sched;
-    A.numUnits = units;
-    A.numSplitUnits = split;
-    A.unitBlocks = k;
-}
-
-void release_schedules() {
-    for (void* p : g_sched_prev) (void)hipFree(p);
-    for (void* p : g_sched_cur) (void)hipFree(p);
-    g_sched_prev.clear();
-    g_sched_cur.clear();
 }
 
 // (num_rowWindows + 1) * 8 * F floats: spmm_launcher.cu:241-244
@@ -189,12 +157,9 @@ torch::Tensor fwd_mixed_bound(std::uint32_t r_rows, std::uint32_t r_cols, std::u
                               py::capsule gpu_ptr, torch::Tensor x, std::int32_t device_id, py::capsule denseC) {
     // module.cu:100-190 (the compiled variant computes with x; an empty x
     // selects the hot/cold feature source instead)
-    begin_call();
     tcc_bcsr A = make_bcsr(r_rows, r_cols, r_nnz, r_blk, r_win, r_rwo, r_tco, r_a2b, r_bits, nullptr);
     tcc_bcsc B = make_bcsc(c_rows, c_cols, c_nnz, c_blk, c_win, c_cwo, c_tco, c_a2c, c_bits, nullptr);
     float* C = static_cast<float*>(denseC.get_pointer());
-    attach_schedule(A, A.rowWindowOffset, A.num_rowWindows, stream_of(device_id));
-    attach_schedule(B, B.colWindowOffset, B.num_colWindows, stream_of(device_id));
     if (x.defined() && x.numel() > 0) {
         TORCH_CHECK(x.is_cuda() && x.is_contiguous() && x.scalar_type() == torch::kFloat32, "x must be fp32 on device");
         check(tcc_spmm_cnic_forward(&A, &B, x.data_ptr<float>(), C, F, stream_of(device_id)));
@@ -226,13 +191,10 @@ torch::Tensor fwd_bound(std::uint32_t r_rows, std::uint32_t r_cols, std::uint32_
                         torch::Tensor c_a2c, torch::Tensor c_bits, std::int32_t F, torch::Tensor x,
                         std::int32_t device_id, py::capsule denseC) {
     // module.cu:192-273
-    begin_call();
     tcc_bcsr A = make_bcsr(r_rows, r_cols, r_nnz, r_blk, r_win, r_rwo, r_tco, r_a2b, r_bits, nullptr);
     tcc_bcsc B = make_bcsc(c_rows, c_cols, c_nnz, c_blk, c_win, c_cwo, c_tco, c_a2c, c_bits, nullptr);
     TORCH_CHECK(x.is_cuda() && x.is_contiguous() && x.scalar_type() == torch::kFloat32, "x must be fp32 on device");
     float* C = static_cast<float*>(denseC.get_pointer());
-    attach_schedule(A, A.rowWindowOffset, A.num_rowWindows, stream_of(device_id));
-    attach_schedule(B, B.colWindowOffset, B.num_colWindows, stream_of(device_id));
     check(tcc_spmm_cnic_forward(&A, &B, x.data_ptr<float>(), C, F, stream_of(device_id)));
     return view_of(C, r_rows, F, current_device());
 }
@@ -256,14 +218,11 @@ torch::Tensor fwd_mixed_py(std::uint32_t r_rows, std::uint32_t r_cols, std::uint
                            std::int64_t cpu_len, std::int32_t cap, std::int32_t F, torch::Tensor id_map,
                            py::capsule cpu_ptr, torch::Tensor csm, py::capsule gpu_ptr) {
     // train/tcgnn_conv_release.py:116-122
-    begin_call();
     tcc_bcsr A = make_bcsr(r_rows, r_cols, r_nnz, r_blk, r_win, r_rwo, r_tco, r_a2b, r_bits, &r_data);
     tcc_bcsc B = make_bcsc(c_rows, c_cols, c_nnz, c_blk, c_win, c_cwo, c_tco, c_a2c, c_bits, &c_data);
     const tcc_feature_source s = feature_source(id_map, cpu_ptr, csm, gpu_ptr, cap, cpu_len);
     torch::Tensor out = alloc_output(r_win, F);
     void* st = stream_of(current_device());
-    attach_schedule(A, A.rowWindowOffset, A.num_rowWindows, st);
-    attach_schedule(B, B.colWindowOffset, B.num_colWindows, st);
     check(tcc_spmm_cnic_forward_mixed(&A, &B, &s, out.data_ptr<float>(), F, st));
     return out.narrow(0, 0, static_cast<std::int64_t>(r_rows) * F);
 }
@@ -275,14 +234,11 @@ torch::Tensor fwd_py(std::uint32_t r_rows, std::uint32_t r_cols, std::uint32_t r
                      torch::Tensor c_tco, torch::Tensor c_a2c, torch::Tensor c_bits, torch::Tensor c_data,
                      std::int32_t F, torch::Tensor x) {
     // train/tcgnn_conv_release.py:124-130
-    begin_call();
     tcc_bcsr A = make_bcsr(r_rows, r_cols, r_nnz, r_blk, r_win, r_rwo, r_tco, r_a2b, r_bits, &r_data);
     tcc_bcsc B = make_bcsc(c_rows, c_cols, c_nnz, c_blk, c_win, c_cwo, c_tco, c_a2c, c_bits, &c_data);
     TORCH_CHECK(x.is_cuda() && x.is_contiguous() && x.scalar_type() == torch::kFloat32, "x must be fp32 on device");
     torch::Tensor out = alloc_output(r_win, F);
     void* st = stream_of(current_device());
-    attach_schedule(A, A.rowWindowOffset, A.num_rowWindows, st);
-    attach_schedule(B, B.colWindowOffset, B.num_colWindows, st);
     check(tcc_spmm_cnic_forward(&A, &B, x.data_ptr<float>(), out.data_ptr<float>(), F, st));
     return out.narrow(0, 0, static_cast<std::int64_t>(r_rows) * F);
 }
@@ -318,15 +274,13 @@ void finalize(int device_id) {
     for (void* p : g_spaces) (void)hipFree(p);
     g_spaces.clear();
     g_outputs.clear();
-    release_schedules();
 }
 
 void freeMatC() {
     g_outputs.clear();
-    release_schedules();  // hipFree waits for the work that uses them
 }
 
-void set_balance_min_blocks(std::uint32_t blocks) { g_balance_min_blocks = blocks; }
+void set_unit_blocks(std::uint32_t blocks) { g_unit_blocks = blocks; }
 
 void set_use_values(bool on) { g_use_values = on; }
 
@@ -363,6 +317,6 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("finalize", &finalize, "free space_malloc buffers and outputs");
     m.def("freeMatC", &freeMatC, "release the outputs of the Python-caller form");
     m.def("set_use_values", &set_use_values, "read the per-block data values (default: all entries 1.0)");
-    m.def("set_balance_min_blocks", &set_balance_min_blocks,
-          "block count from which each call builds a work schedule (default 65536; 0 = always)");
+    m.def("set_unit_blocks", &set_unit_blocks,
+          "blocks each wave of work walks (default 0 = chosen from the block count)");
 }

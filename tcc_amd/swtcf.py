@@ -181,35 +181,15 @@ class BlockMatrix:
         self.view = view
         self._alloc = allocation
         self._keep = keep
-        self._sched_alloc = None
 
     def release(self) -> None:
         if self._alloc:
             check(_lib.lib().tcc_block_release(self._alloc))
             self._alloc = None
-        self._release_schedule()
 
-    def _release_schedule(self) -> None:
-        if self._sched_alloc:
-            torch.cuda.synchronize()
-            check(_lib.lib().tcc_block_release(self._sched_alloc))
-            self._sched_alloc = None
-
-    def set_schedule(self, unit_blocks: int | None, stream=None) -> "BlockMatrix":
-        """Replace the work schedule: unit_blocks=None drops it (one unit per
-        window), 0 picks the block count per unit automatically."""
-        self._release_schedule()
-        v = self.view
-        if unit_blocks is None:
-            v.schedule, v.numUnits, v.numSplitUnits, v.unitBlocks = None, 0, 0, 0
-            return self
-        off = v.rowWindowOffset if self.kind == "bcsr" else v.colWindowOffset
-        sched = ctypes.c_void_p()
-        nu, ns, k = ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_uint32()
-        check(_lib.lib().tcc_make_schedule(off, self.num_windows, unit_blocks, ctypes.byref(sched), ctypes.byref(nu),
-                                           ctypes.byref(ns), ctypes.byref(k), _stream(stream)))
-        self._sched_alloc = sched.value
-        v.schedule, v.numUnits, v.numSplitUnits, v.unitBlocks = sched.value, nu.value, ns.value, k.value
+    def set_unit_blocks(self, unit_blocks: int) -> "BlockMatrix":
+        """Blocks each wave of work walks (0 = chosen from the block count)."""
+        self.view.unitBlocks = int(unit_blocks)
         return self
 
     def __del__(self):

@@ -269,9 +269,10 @@ def test_mixed_hot_cold_feature_source(gpu, oracle):
     cpu.free()
 
 
-# ------------------------------------------------------------------ work schedules
+# ------------------------------------------------------------------ units of work
 def skewed_coo(nr, nc, seed):
-    """A few dense hub rows and hub columns over a sparse background."""
+    """A few dense hub rows and hub columns over a sparse background, with
+    bands of empty row/column windows inside and at the end."""
     rng = np.random.default_rng(seed)
     keys = set(rng.choice(nr * nc, size=6000, replace=False).tolist())
     for r in (3, 4, 500):  # hub rows -> long BCSR windows
@@ -279,14 +280,18 @@ def skewed_coo(nr, nc, seed):
     for c in (7, 600):  # hub columns -> long BCSC windows
         keys.update(r * nc + c for r in rng.choice(nr, size=nr // 2, replace=False).tolist())
     k = np.array(sorted(keys), np.int64)
-    return (k // nc).astype(np.uint32), (k % nc).astype(np.uint32)
+    r, c = k // nc, k % nc
+    keep = ~(((r >= 200) & (r < 264)) | (r >= 600) | ((c >= 300) & (c < 340)) | (c >= 880))
+    return r[keep].astype(np.uint32), c[keep].astype(np.uint32)
 
 
-@pytest.mark.parametrize("unit_blocks", [None, 1, 2, 3, 0])
-@pytest.mark.parametrize("F", [2, 64, 128, 256])
-def test_schedules_split_windows(gpu, oracle, unit_blocks, F):
-    """Windows split over several units add their partial sums atomically;
-    every schedule (and none) gives the same product."""
+@pytest.mark.parametrize("unit_blocks", [0, 1, 2, 3, 5, 8, 64])
+@pytest.mark.parametrize("F", [2, 64, 128, 256, 602])
+def test_units_split_windows(gpu, oracle, unit_blocks, F):
+    """Units of K consecutive blocks cut windows anywhere (empty windows
+    included); windows shared by several units add their partial sums
+    atomically into pre-zeroed rows.  Every K gives the oracle's product, for
+    the BCSR gather (= and +=), the BCSC scatter and the BCSC^T gather."""
     from tcc_amd import swtcf
 
     nr, nc = 640, 900
@@ -297,15 +302,13 @@ def test_schedules_split_windows(gpu, oracle, unit_blocks, F):
     rowptr, colind, v = csr_of(dst, src, nr, vals)
     want = oracle.csr_spmm(rowptr, colind, v, X, use_tf32=True)
     A = swtcf.coo_to_bcsr(dev_u32(dst), dev_u32(src), torch.from_numpy(vals).cuda(), nr, nc)
-    A.set_schedule(unit_blocks)
-    if unit_blocks:
-        assert A.view.numSplitUnits > 0
+    A.set_unit_blocks(unit_blocks)
     Y = swtcf.bcsr_spmm(A, Xd, torch.full((A.view.num_rowWindows * 8, F), 9.0, device="cuda"))
     assert_close(Y.cpu().numpy()[:nr], want)
     Y2 = swtcf.bcsr_spmm(A, Xd, Y.clone(), accumulate=True)
     assert_close(Y2.cpu().numpy()[:nr], 2 * want)
     B = swtcf.coo_to_bcsc(dev_u32(dst), dev_u32(src), torch.from_numpy(vals).cuda(), nr, nc)
-    B.set_schedule(unit_blocks)
+    B.set_unit_blocks(unit_blocks)
     Yc = torch.zeros((nr, F), device="cuda")
     swtcf.bcsc_spmm(B, Xd, Yc)
     assert_close(Yc.cpu().numpy(), want)
@@ -319,10 +322,36 @@ def test_schedules_split_windows(gpu, oracle, unit_blocks, F):
     assert_close(dX.cpu().numpy()[:nc], wantT)
 
 
-def test_builder_attaches_schedule(gpu):
+def test_all_windows_empty(gpu):
+    """A BCSR with no blocks writes zeros to every row (and += leaves Y)."""
     from tcc_amd import swtcf
-    from tcc_amd.graphs import rmat_graph
 
-    rows, cols = rmat_graph(20_000, 200_000, 5)
-    A = swtcf.coo_to_bcsr(rows.to(torch.int32).cuda(), cols.to(torch.int32).cuda(), None, 20_000, 20_000)
-    assert A.view.schedule and A.view.numUnits >= A.view.num_rowWindows and A.view.unitBlocks >= 16
+    RW, F = 37, 70
+    d = dict(num_rows=RW * 8, num_cols=50, nnz=0, num_TCBlocks=0, num_rowWindows=RW,
+             rowWindowOffset=np.zeros(RW + 1, np.uint32), tcOffset=np.zeros(1, np.uint32),
+             sparseA2B=np.full(8, 0xFFFFFFFF, np.uint32), tcLocalBit=np.zeros(1, np.uint64),
+             data=np.zeros(1, np.float32))
+    A = swtcf.host_to_bcsr(d)
+    X = torch.randn((50, F), device="cuda")
+    Y = swtcf.bcsr_spmm(A, X, torch.full((RW * 8, F), 3.0, device="cuda"))
+    assert torch.count_nonzero(Y).item() == 0
+    Y = swtcf.bcsr_spmm(A, X, torch.full((RW * 8, F), 3.0, device="cuda"), accumulate=True)
+    assert bool((Y == 3.0).all())
+
+
+def test_unit_sizes_agree_on_rmat(gpu):
+    """R-MAT windows of very different lengths: every unit size gives the
+    same product (to fp32 reassociation) as the automatic one."""
+    from tcc_amd import swtcf
+    from tcc_amd.graphs import make_features, rmat_graph, sym_norm_values
+
+    n = 20_000
+    rows, cols = rmat_graph(n, 200_000, 5)
+    vals = sym_norm_values(rows, cols, n)
+    A = swtcf.coo_to_bcsr(rows.to(torch.int32).cuda(), cols.to(torch.int32).cuda(), vals.cuda(), n, n)
+    X = make_features(n, 96, 5, device="cuda")
+    ref = swtcf.bcsr_spmm(A, X).clone()
+    for K in (1, 7, 8, 100, 4096):
+        A.set_unit_blocks(K)
+        Y = swtcf.bcsr_spmm(A, X)
+        assert rel_l2(Y.cpu().numpy(), ref.cpu().numpy()) < 1e-6, K
