@@ -249,6 +249,8 @@ __device__ __forceinline__ void load_block(const GatherArgs& a, const GroupMeta&
     // Stored bit (r*8+c): BCSR = (output row r, column c); BCSC = (source row r,
     // source column c), i.e. (input r, output c) for the A^T gather.
     bm = (MODE == Src::Transposed) ? transpose8x8(raw) : raw;
+    // All loads are issued before any result is used (rounding inside the
+    // branches would wait for each load in turn).
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
         const std::uint64_t rp = (static_cast<std::uint64_t>(lane_u32(m.rowHi, k * 8 + c)) << 32) |
@@ -258,14 +260,19 @@ __device__ __forceinline__ void load_block(const GatherArgs& a, const GroupMeta&
         if (rp != 0) {
             const Vec<V> t = load_vec<V>(reinterpret_cast<const float*>(rp) + laneOff);
 #pragma unroll
-            for (int v = 0; v < V; ++v) x[c][v] = tf32_rna(t.v[v]);
+            for (int v = 0; v < V; ++v) x[c][v] = t.v[v];
         }
     }
     vals = 0.0f;
     if constexpr (VALUES) {
         const std::uint32_t off = lane_u32(m.off, k);
-        if (__lane_id() < static_cast<unsigned>(__popcll(raw))) vals = tf32_rna(a.data[off + __lane_id()]);
+        if (__lane_id() < static_cast<unsigned>(__popcll(raw))) vals = a.data[off + __lane_id()];
     }
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+#pragma unroll
+        for (int v = 0; v < V; ++v) x[c][v] = tf32_rna(x[c][v]);
+    if constexpr (VALUES) vals = tf32_rna(vals);
 }
 
 // acc[R] += w(R,C) * x[C] over the block's nonzeros (uniform branches over
@@ -414,7 +421,8 @@ struct ScatterArgs {
     MixedArgs mixed;
 };
 
-// The 8 source rows of window w, TF32-rounded (zeros past numCols).
+// The 8 source rows of window w, TF32-rounded (zeros past numCols); all
+// loads are issued before any is rounded.
 template <int V, bool MIXED>
 __device__ __forceinline__ void load_window_rows(const ScatterArgs& a, std::uint32_t w, std::uint32_t laneOff,
                                                  float (&x)[8][V]) {
@@ -434,10 +442,14 @@ __device__ __forceinline__ void load_window_rows(const ScatterArgs& a, std::uint
             if (row != nullptr) {
                 const Vec<V> t = load_vec<V>(row + laneOff);
 #pragma unroll
-                for (int v = 0; v < V; ++v) x[c][v] = tf32_rna(t.v[v]);
+                for (int v = 0; v < V; ++v) x[c][v] = t.v[v];
             }
         }
     }
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+#pragma unroll
+        for (int v = 0; v < V; ++v) x[c][v] = tf32_rna(x[c][v]);
 }
 
 template <int V, bool MIXED, bool VALUES>
@@ -472,7 +484,8 @@ __global__ void __launch_bounds__(kThreads) scatter_kernel(ScatterArgs a) {
         const std::uint64_t bm = a.bits[b];
         float vals = 0.0f;
         if constexpr (VALUES) {
-            if (lane < static_cast<unsigned>(__popcll(bm))) vals = tf32_rna(a.data[a.tcOffset[b] + lane]);
+            if (lane < static_cast<unsigned>(__popcll(bm))) vals = a.data[a.tcOffset[b] + lane];
+            vals = tf32_rna(vals);
         }
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
@@ -522,13 +535,29 @@ inline int pick_vec(std::uint32_t F, std::initializer_list<const void*> ptrs) {
     return 1;
 }
 
-// Blocks per unit: `requested` if nonzero, else enough units for about 64K
-// waves over all chunks (at least 8 blocks, at most 512, a power of two).
+// Compute units of the current device (cached per device).
+inline std::uint32_t device_cus() {
+    static std::uint32_t cache[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cache[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cache[dev] = static_cast<std::uint32_t>(n);
+    }
+    return cache[dev];
+}
+
+// Blocks per unit: `requested` if nonzero, else about one wave of work per
+// wave slot of the device (32 per CU): fewer, longer units pay the per-wave
+// start (window search, first metadata group) less often, while more units
+// than slots only queue.  A power of two in [16, 1024].
 inline std::uint32_t unit_blocks(std::uint32_t requested, std::uint32_t blocks, std::uint32_t chunks) {
     if (requested != 0) return requested;
     const std::uint64_t work = static_cast<std::uint64_t>(blocks) * chunks;
-    std::uint32_t K = 8;
-    while (K < 512 && work > static_cast<std::uint64_t>(K) * 65536) K *= 2;
+    const std::uint64_t slots = static_cast<std::uint64_t>(device_cus()) * 32;
+    std::uint32_t K = 16;
+    while (K < 1024 && static_cast<std::uint64_t>(K) * slots < work) K *= 2;
     return K;
 }
 
