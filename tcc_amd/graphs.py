@@ -79,7 +79,8 @@ def to_csr_numpy(rows: torch.Tensor, cols: torch.Tensor, n_rows: int, vals: torc
     """(rowptr int64, colind uint32, vals float32|None) of edges sorted by (row, col)."""
     r = rows.cpu().numpy().astype(np.int64)
     c = cols.cpu().numpy().astype(np.int64)
-    order = np.lexsort((c, r))
+    key = r * (int(c.max()) + 1 if c.size else 1) + c
+    order = np.arange(r.size) if bool(np.all(key[1:] >= key[:-1])) else np.lexsort((c, r))
     rowptr = np.zeros(n_rows + 1, np.int64)
     np.cumsum(np.bincount(r, minlength=n_rows), out=rowptr[1:])
     v = None if vals is None else vals.cpu().numpy().astype(np.float32)[order]
