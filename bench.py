@@ -4,12 +4,21 @@
 Default workload ("config 2"): R-MAT graph, 169k
 nodes, 1.17M nnz, sym-normalised fp32 values, X = N(0,1) [169k x 128]; one
 step = one forward BCSR SpMM (Y = A X) over the whole graph, inputs resident
-in HBM.  --config 1/3 select the other single-GPU SpMM configurations.
+in HBM.  The other configurations:
+  --config 1  uniform 4096 x 16/row, F=32: SWTCF convert + SWTCF SpMM
+  --config 3  R-MAT 233k nodes, 114M nnz, F=602: BCSR SpMM
+  --config 4  R-MAT 2.45M nodes, 61.9M nnz, F=100, top-20% rows hot in HBM,
+              the rest zero-copy from pinned host memory: mixed SpMM
+              (BCSR over hot sources + BCSC over cold sources)
+  --config 5  2-layer GCN (100 -> 256 -> 2, ReLU) on the config-4 graph: one
+              full-graph training epoch (forward, loss, backward, Adam)
 
-Prints one JSON line with GFLOP/s (2*nnz*F per step), the HBM roofline of the
-kernel (algorithmic bytes 4F(n_src+n_dst) + 8 nnz + 4(n_dst+1) per launch
-over the HIP-event-timed launch duration) and the CPU baseline (the oracle's
-CSR SpMM on the host cores, the same matrix, checked against the GPU result).
+Prints one JSON line.  SpMM configurations report GFLOP/s (2*nnz*F per
+step), the HBM roofline of the dominant kernel (algorithmic bytes
+4F(n_src+n_dst) + 8 nnz + 4(n_dst+1) per launch over the HIP-event-timed
+step) and the CPU baseline (the oracle's CSR SpMM on the host cores over a
+bounded sample of the same matrix, also the parity check).  Config 5
+reports the epoch time in ms and each layer's forward+backward time.
 """
 from __future__ import annotations
 
@@ -24,12 +33,14 @@ sys.path.insert(0, ROOT)
 
 METRIC = "SpMM GFLOP/s (2·nnz·F) + % HBM roofline; GCN layer fwd+bwd ms at 1 GPU"
 HBM_PEAK_GBPS = 8000.0
-FP32_PEAK_TFLOPS = 157.3
+PCIE_PEAK_GBPS = 64.0  # PCIe Gen5 x16, one direction
 
 WORKLOADS = {
     1: "config1: uniform 4096 nodes x 16 nnz/row, F=32, SWTCF convert + SWTCF SpMM",
     2: "config2: R-MAT (0.57,0.19,0.19) 169k nodes, 1.17M nnz, sym-normalised, F=128, forward BCSR SpMM",
     3: "config3: R-MAT (0.57,0.19,0.19) 233k nodes, 114M nnz, sym-normalised, F=602, forward BCSR SpMM",
+    4: "config4: R-MAT 2.45M nodes, 61.9M nnz, F=100, top-20% rows hot in HBM, rest pinned host: mixed SpMM",
+    5: "config5: 2-layer GCN 100->256->2 (ReLU, dropout 0, Adam 0.003) on the config-4 graph, full-graph epoch",
 }
 
 
@@ -83,20 +94,66 @@ def cpu_baseline(rows, cols, vals, X, n, threads, Y_gpu, max_nnz):
     return t, threads, rel, R, nz
 
 
-def main():
-    args = parse()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path",
-              file=sys.stderr)
-        return 2
+def timed(step, steps, warmup):
+    """Mean ms per step over `steps` after `warmup`, timed with HIP events on
+    the current stream (every launch of the step goes to that stream)."""
     import torch
 
-    from tcc_amd import swtcf
-    from tcc_amd.graphs import CONFIGS, make_features, make_graph
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
 
-    assert torch.cuda.is_available(), "bench.py needs the GPU"
-    torch.cuda.set_device(0)
-    cfg = CONFIGS[args.config]
+
+def copy_calibration(mib):
+    import torch
+
+    nfl = mib * (1 << 20) // 4
+    a_src = torch.ones(nfl, device="cuda")
+    a_dst = torch.empty_like(a_src)
+    torch.cuda.synchronize()
+    a_dst.copy_(a_src)  # reads and writes exactly `mib` MiB
+    torch.cuda.synchronize()
+    del a_src, a_dst
+
+
+def traffic_of(config):
+    tf = os.path.join(ROOT, "profiles", f"traffic_config{config}.json")
+    if os.path.exists(tf):
+        with open(tf) as f:
+            return json.load(f).get("hbm_bytes_per_launch")
+    return None
+
+
+def line_for(args, value, unit, ms, dtype, config, roofline, cpu, extra, higher=True):
+    return {
+        "metric": METRIC, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 5), "higher_is_better": higher, "scaling": "weak", "vs_baseline": None,
+        "dtype": dtype, "data": "synthetic (seeded generator, see tcc_amd/graphs.py)", "config": config,
+        "roofline": roofline, "cpu_baseline": cpu, "extra": extra,
+    }
+
+
+def cpu_entry(t_cpu, threads, nz, nnz, R, F, config):
+    what = (f"whole config-{config} matrix ({nnz} nnz, F={F})" if nz == nnz else
+            f"rows 0..{R - 1} of config {config} ({nz} of {nnz} nnz, F={F})")
+    return {"value": round(2.0 * nz * F / t_cpu / 1e9, 3), "unit": "GFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{what}; oracle CSR SpMM, fp64 accumulation of TF32-rounded inputs, OpenMP over rows, "
+                      f"median of 5 after 1 warm-up",
+            "ms": round(t_cpu * 1e3, 3)}
+
+
+def bench_spmm(args, torch, swtcf, cfg):
+    """Configs 1-3: one SpMM per step."""
+    from tcc_amd.graphs import make_features, make_graph
+
     n, F = cfg["n"], cfg["F"]
     t0 = time.time()
     rows, cols, vals = make_graph(args.config, device="cuda")
@@ -106,21 +163,12 @@ def main():
     X = make_features(n, F, cfg["seed"], dist="uniform" if args.config == 1 else "normal", device="cuda")
     r32 = rows.to(torch.int32).contiguous()
     c32 = cols.to(torch.int32).contiguous()
-    stream = torch.cuda.current_stream()
-
     extra = {}
     if args.config == 1:
         m = swtcf.DeviceSWTCFMatrix(n, n, nnz, 16)
         ws = swtcf.SWTCFConvertWorkspace(nnz, n, 16)
         swtcf.convertCOOToSWTCF(r32, c32, nnz, m, ws)
-        torch.cuda.synchronize()
-        c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        c0.record(stream)
-        for _ in range(20):
-            swtcf.convertCOOToSWTCF(r32, c32, nnz, m, ws)
-        c1.record(stream)
-        torch.cuda.synchronize()
-        conv_ms = c0.elapsed_time(c1) / 20
+        conv_ms = timed(lambda: swtcf.convertCOOToSWTCF(r32, c32, nnz, m, ws), 20, 2)
         assert ws.device_error() == 0
         extra["convert_ms"] = round(conv_ms, 4)
         extra["convert_gedges_per_s"] = round(nnz / conv_ms / 1e6, 3)
@@ -139,75 +187,161 @@ def main():
             swtcf.bcsr_spmm(A, X, Y)
 
         kernel = "gather_kernel"
-
     if args.copy_calibration_mib:
-        nfl = args.copy_calibration_mib * (1 << 20) // 4
-        a_src = torch.ones(nfl, device="cuda")
-        a_dst = torch.empty_like(a_src)
-        torch.cuda.synchronize()
-        a_dst.copy_(a_src)  # reads and writes exactly copy_calibration_mib MiB
-        torch.cuda.synchronize()
-        del a_src, a_dst
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(args.steps):
-        step()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / args.steps
+        copy_calibration(args.copy_calibration_mib)
+    ms = timed(step, args.steps, args.warmup)
     flops = 2.0 * nnz * F
-    gflops = flops / (ms * 1e-3) / 1e9
     b_alg = bytes_alg(n, n, nnz, F)
     achieved = b_alg / (ms * 1e-3) / 1e9
-    traffic = None
-    tf = os.path.join(ROOT, "profiles", f"traffic_config{args.config}.json")
-    if os.path.exists(tf):
-        with open(tf) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
-
     if args.config == 1:
         torch.cuda.synchronize()
         Y.zero_()
         step()
     torch.cuda.synchronize()
-
     cpu = None
     if not args.no_cpu_baseline:
         t_cpu, threads, rel, R, nz = cpu_baseline(rows, cols, vals, X, n, args.cpu_threads, Y, 16_000_000)
-        whole = nz == nnz
-        what = (f"whole config-{args.config} matrix ({nnz} nnz, F={F})" if whole else
-                f"rows 0..{R - 1} of config {args.config} ({nz} of {nnz} nnz, F={F})")
-        cpu = {"value": round(2.0 * nz * F / t_cpu / 1e9, 3), "unit": "GFLOP/s", "cores": threads, "kind": "port",
-               "sample": f"{what}; oracle CSR SpMM, fp64 accumulation of TF32-rounded inputs, OpenMP over rows, "
-                         f"median of 5 after 1 warm-up",
-               "ms": round(t_cpu * 1e3, 3)}
+        cpu = cpu_entry(t_cpu, threads, nz, nnz, R, F, args.config)
         extra["parity_rel_l2_vs_cpu"] = rel
         extra["parity_rows"] = R
+    roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic_of(args.config), "kernel": kernel,
+                "bytes_alg_per_launch": b_alg}
+    config = {"workload": WORKLOADS[args.config], "n": n, "nnz": nnz, "F": F}
+    return line_for(args, round(flops / (ms * 1e-3) / 1e9, 3), "GFLOP/s", ms, "fp32", config, roofline, cpu, extra)
 
-    line = {
-        "metric": METRIC,
-        "value": round(gflops, 3),
-        "unit": "GFLOP/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "fp32",
-        "data": "synthetic (seeded generator, see tcc_amd/graphs.py)",
-        "config": {"workload": WORKLOADS[args.config], "n": n, "nnz": nnz, "F": F},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic, "kernel": kernel,
-                     "bytes_alg_per_launch": b_alg},
-        "cpu_baseline": cpu,
-        "extra": extra,
-    }
+
+def gcn_inputs(torch, cfg):
+    """Config-4/5 graph, features, hot/cold table and layer graphs."""
+    from tcc_amd import gcn
+    from tcc_amd.graphs import make_features, make_graph
+
+    n, F = cfg["n"], cfg["F"]
+    t0 = time.time()
+    rows, cols, _ = make_graph(4, device="cuda")
+    X = make_features(n, F, cfg["seed"], device="cuda")
+    table = gcn.FeatureTable(X, cols)
+    g1, g2 = gcn.build_gcn_graphs(rows, cols, n, table.hot)
+    torch.cuda.synchronize()
+    print(f"[bench] graph n={n} nnz={rows.numel()} F={F}: generated and blocked in {time.time() - t0:.1f}s",
+          file=sys.stderr, flush=True)
+    return rows, cols, X, table, g1, g2
+
+
+def bench_mixed(args, torch, swtcf, cfg):
+    """Config 4: the first-layer SpMM with hot rows from HBM and cold rows
+    read zero-copy from pinned host memory."""
+    n, F = cfg["n"], cfg["F"]
+    rows, cols, X, table, g1, _ = gcn_inputs(torch, cfg)
+    nnz = rows.numel()
+    Y = None
+
+    def step():
+        nonlocal Y
+        Y = g1.aggregate(F, source=table.source)
+
+    ms = timed(step, args.steps, args.warmup)
+    torch.cuda.synchronize()
+    cold_edge = ~table.hot[cols.long()]
+    hot_edges = int((~cold_edge).sum().item())
+    cold_rows_used = int(torch.unique(cols[cold_edge]).numel())
+    cold_bytes = 4.0 * F * cold_rows_used
+    extra = {"hot_rows": table.n_hot, "hot_edges": hot_edges, "cold_edges": nnz - hot_edges,
+             "bcsr_blocks": g1.bcsr.view.num_TCBlocks,
+             "bcsc_blocks": g1.bcsc.view.num_TCBlocks if g1.bcsc is not None else 0,
+             "host_link": {"cold_rows": cold_rows_used, "bytes_min": cold_bytes,
+                           "achieved_GBps": round(cold_bytes / (ms * 1e-3) / 1e9, 2),
+                           "peak_GBps": PCIE_PEAK_GBPS,
+                           "bound_ms": round(cold_bytes / (PCIE_PEAK_GBPS * 1e9) * 1e3, 3)}}
+    cpu = None
+    if not args.no_cpu_baseline:
+        t_cpu, threads, rel, R, nz = cpu_baseline(rows, cols, None, X, n, args.cpu_threads, Y, 16_000_000)
+        cpu = cpu_entry(t_cpu, threads, nz, nnz, R, F, 4)
+        extra["parity_rel_l2_vs_cpu"] = rel
+        extra["parity_rows"] = R
+    b_alg = bytes_alg(n, n, nnz, F)
+    achieved = b_alg / (ms * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic_of(4),
+                "kernel": "gather_kernel<Mixed> + scatter_kernel<Mixed>", "bytes_alg_per_launch": b_alg}
+    config = {"workload": WORKLOADS[4], "n": n, "nnz": nnz, "F": F}
+    table.free()
+    return line_for(args, round(2.0 * nnz * F / (ms * 1e-3) / 1e9, 3), "GFLOP/s", ms, "fp32", config, roofline,
+                    cpu, extra)
+
+
+def bench_gcn(args, torch, swtcf, cfg):
+    """Config 5: one full-graph GCN training epoch per step, plus each
+    layer's forward+backward time."""
+    from tcc_amd import gcn
+
+    n, F = cfg["n"], cfg["F"]
+    hidden, classes = 256, 2
+    rows, cols, X, table, g1, g2 = gcn_inputs(torch, cfg)
+    nnz = rows.numel()
+    torch.manual_seed(cfg["seed"])
+    model = gcn.GCN(F, hidden, classes, dropout=0.0).cuda()
+    labels = gcn.synthetic_labels(n, classes, cfg["seed"])
+    opt = torch.optim.Adam(model.parameters(), lr=0.003)
+    loss_fcn = torch.nn.CrossEntropyLoss()
+    losses = []
+
+    def epoch():
+        losses.append(gcn.train_epoch(model, g1, g2, table.source, labels, opt, loss_fcn))
+
+    steps = max(1, min(args.steps, 10))
+    warmup = max(1, min(args.warmup, 3))
+    ms = timed(epoch, steps, warmup)
+    first_loss, last_loss = float(losses[0].item()), float(losses[-1].item())
+
+    g_h = torch.randn((n, hidden), device="cuda")
+    g_c = torch.randn((n, classes), device="cuda")
+
+    def layer1():
+        model.zero_grad(set_to_none=True)
+        model.conv1(g1, source=table.source).backward(g_h)
+
+    x2 = torch.relu(model.conv1(g1, source=table.source)).detach().requires_grad_(True)
+
+    def layer2():
+        model.zero_grad(set_to_none=True)
+        x2.grad = None
+        model.conv_final(g2, x=x2).backward(g_c)
+
+    l1 = timed(layer1, steps, warmup)
+    l2 = timed(layer2, steps, warmup)
+    extra = {"layer1_fwd_bwd_ms": round(l1, 4), "layer2_fwd_bwd_ms": round(l2, 4),
+             "layer1": f"mixed SpMM F={F} (hot BCSR + cold BCSC) + GEMM {F}x{hidden}; backward dW GEMM",
+             "layer2": f"BCSR SpMM F={hidden} + GEMM {hidden}x{classes}; backward dW GEMM, A^T SpMM F={classes}, "
+                       f"GEMM {classes}x{hidden}",
+             "loss_first": first_loss, "loss_last": last_loss}
+    config = {"workload": WORKLOADS[5], "n": n, "nnz": nnz, "F": F, "hidden": hidden, "classes": classes}
+    table.free()
+    line = line_for(args, round(ms, 4), "ms", ms, "fp32", config, None, None, extra, higher=False)
+    line["steps"], line["warmup"] = steps, warmup
+    return line
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path",
+              file=sys.stderr)
+        return 2
+    import torch
+
+    from tcc_amd import swtcf
+    from tcc_amd.graphs import CONFIGS
+
+    assert torch.cuda.is_available(), "bench.py needs the GPU"
+    torch.cuda.set_device(0)
+    cfg = CONFIGS[args.config]
+    if args.config in (1, 2, 3):
+        line = bench_spmm(args, torch, swtcf, cfg)
+    elif args.config == 4:
+        line = bench_mixed(args, torch, swtcf, cfg)
+    else:
+        line = bench_gcn(args, torch, swtcf, cfg)
     print(json.dumps(line), flush=True)
     return 0
 

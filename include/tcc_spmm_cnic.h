@@ -17,9 +17,9 @@
  * kernels do, spmm_cnic/src/core/spmm_kernel.cu:96-102).  Otherwise the value
  * of bit i of block b is data[tcOffset[b] + popcount(bitmap & ((1<<i)-1))]
  * (the layout of the reference's commented-out value load, :88-101).
- * Products use TF32-rounded (round-to-nearest, ties away from zero, 10
- * mantissa bits) X and values with fp32 accumulation, reproducing the
- * reference's mma.m16n8k8 tf32 numerics.
+ * Forward products use TF32-rounded (round-to-nearest, ties away from zero,
+ * 10 mantissa bits) X and values with fp32 accumulation, reproducing the
+ * reference's mma.m16n8k8 tf32 numerics; the A^T product is plain fp32.
  *
  * Reference interface replaced: spmm_cnic/include/class.h:20-58 (views),
  * spmm_cnic/src/core/spmm_launcher.cu:30-271 (launch_spmm_kernel) and
@@ -104,9 +104,11 @@ int tcc_bcsc_spmm(const tcc_bcsc* A, const float* X, float* Y, uint32_t featureD
 
 /* Transposed use of a BCSC for the backward pass: dX = A^T * dY, i.e.
  * dX[8w+c] (=, or +=) sum_b sum_r bit(r,c) * v * dY[sparseA2C[8b+r]] — a
- * gather (atomics only where a window is split between units).  dX must hold 8*num_colWindows*F floats.  The
- * reference computes this product with torch.sparse.mm
- * (train/tcgnn_conv_release.py:152); this is its block-sparse replacement. */
+ * gather (atomics only where a window is split between units).
+ * dX must hold 8*num_colWindows*F floats.  The reference computes this
+ * product with torch.sparse.mm (train/tcgnn_conv_release.py:152); this is its
+ * block-sparse replacement, with the same plain fp32 products (no TF32
+ * rounding). */
 int tcc_bcsc_transpose_spmm(const tcc_bcsc* A, const float* dY, float* dX,
                             uint32_t featureDim, int accumulate, void* stream);
 

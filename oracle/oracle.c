@@ -695,9 +695,10 @@ void oracle_bcsc_spmm(uint32_t CWn, const uint32_t* colWindowOffset, const uint3
         }
 }
 
-/* Transposed BCSC use: dX[8w+c] += sum_b sum_r bit(r,c) * v * tf32(dY[sparseA2C[8b+r]]),
+/* Transposed BCSC use: dX[8w+c] += sum_b sum_r bit(r,c) * v * dY[sparseA2C[8b+r]],
  * rows >= num_rows skipped.  dX is fp64 [8*CW x F], accumulated into.  This is
- * A^T * dY of train/tcgnn_conv_release.py:152 on the BCSC layout. */
+ * A^T * dY of train/tcgnn_conv_release.py:152, where torch.sparse.mm
+ * multiplies the fp32 operands as given (no TF32 rounding of dY or v). */
 void oracle_bcsc_transpose_spmm(uint32_t CWn, const uint32_t* colWindowOffset, const uint32_t* tcOffset,
                                 const uint32_t* sparseA2C, const uint64_t* tcLocalBit,
                                 const float* data, uint32_t num_rows, const float* dY, uint32_t F,
@@ -710,10 +711,14 @@ void oracle_bcsc_transpose_spmm(uint32_t CWn, const uint32_t* colWindowOffset, c
                 const uint32_t r = bit / 8, c = bit % 8;
                 const uint32_t row = sparseA2C[(size_t)b * 8 + r];
                 if (row >= num_rows) continue;
-                const double v = block_value(data, tcOffset, b, bm, bit);
+                double v = 1.0;
+                if (data) {
+                    const uint64_t below = bit ? (bm & ((1ull << bit) - 1ull)) : 0ull;
+                    v = (double)data[tcOffset[b] + (uint32_t)__builtin_popcountll(below)];
+                }
                 double* x = dX + ((size_t)w * 8 + c) * F;
                 const float* y = dY + (size_t)row * F;
-                for (uint32_t f = 0; f < F; ++f) x[f] += v * (double)oracle_tf32(y[f]);
+                for (uint32_t f = 0; f < F; ++f) x[f] += v * (double)y[f];
             }
         }
 }

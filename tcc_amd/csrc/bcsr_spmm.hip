@@ -239,9 +239,9 @@ __device__ __forceinline__ GroupMeta load_group(const GatherArgs& a, std::uint32
 }
 
 // Block k of the group: its stored bitmap `raw`, the row-major view `bm`
-// (byte R = the input columns C that output row R uses), the TF32-rounded
-// input rows x[C] (zeros for padding), and its values (lane i = the value of
-// its i-th stored nonzero, TF32-rounded).
+// (byte R = the input columns C that output row R uses), the input rows x[C]
+// (zeros for padding) and its values (lane i = the value of its i-th stored
+// nonzero), TF32-rounded except for the A^T gather.
 template <int V, Src MODE, bool VALUES>
 __device__ __forceinline__ void load_block(const GatherArgs& a, const GroupMeta& m, int k, std::uint32_t laneOff,
                                            std::uint64_t& raw, std::uint64_t& bm, float (&x)[8][V], float& vals) {
@@ -268,11 +268,16 @@ __device__ __forceinline__ void load_block(const GatherArgs& a, const GroupMeta&
         const std::uint32_t off = lane_u32(m.off, k);
         if (__lane_id() < static_cast<unsigned>(__popcll(raw))) vals = a.data[off + __lane_id()];
     }
+    // The A^T product replaces torch.sparse.mm in the reference's backward
+    // (train/tcgnn_conv_release.py:152), which multiplies in plain fp32; the
+    // forward products reproduce its mma.m16n8k8 tf32 numerics.
+    if constexpr (MODE != Src::Transposed) {
 #pragma unroll
-    for (int c = 0; c < 8; ++c)
+        for (int c = 0; c < 8; ++c)
 #pragma unroll
-        for (int v = 0; v < V; ++v) x[c][v] = tf32_rna(x[c][v]);
-    if constexpr (VALUES) vals = tf32_rna(vals);
+            for (int v = 0; v < V; ++v) x[c][v] = tf32_rna(x[c][v]);
+        if constexpr (VALUES) vals = tf32_rna(vals);
+    }
 }
 
 // acc[R] += w(R,C) * x[C] over the block's nonzeros (uniform branches over

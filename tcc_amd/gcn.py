@@ -1,0 +1,197 @@
+"""Two-layer GCN on the block-sparse SpMM: the caller of the hot path
+(train/tcgnn_conv_release.py:49-250), on MI355X.
+
+CNICSPMMFunction mirrors the reference's autograd function
+(tcgnn_conv_release.py:49-166):
+  forward : AX = A·X with the spmm_cnic split (BCSR part + BCSC part,
+            spmm_launcher.cu:30-271), out = AX·W                (:130-134)
+  backward: dW = AXᵀ·dY, G = Aᵀ·dY, dX = G·Wᵀ                    (:147-154)
+The reference's G = torch.sparse.mm(Aᵀ, dY) over unit values (:139-142, :152)
+is the block-sparse transposed gather over a BCSC of the whole A
+(tcc_bcsc_transpose_spmm), and dX is computed only when the layer's input
+needs a gradient (the reference computes and discards it for the first
+layer, whose input is the feature table).
+
+The first layer reads X through the hot/cold feature source of
+spmm_kernel.cu:129-153: edges whose source row is hot (in the HBM feature
+cache) go to the BCSR gather, edges with cold sources to the BCSC scatter,
+which reads each cold row once per column window from mapped pinned host
+memory.  Later layers read device-resident X and put every edge in the
+BCSR gather.
+
+GCN = conv1 (first layer, F_in -> hidden), ReLU, dropout, conv_final
+(hidden -> classes), weights xavier-uniform (tcgnn_conv_release.py:168-250);
+trained with cross-entropy and Adam (:448-449).
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import swtcf
+from .hostmem import PinnedArray
+
+
+class LayerGraph:
+    """The block matrices of one layer's A [num_rows x num_cols]:
+    forward BCSR (edges whose source is on the device) and BCSC (edges whose
+    source is cold, or None), and the backward BCSC of every edge (shared
+    between layers over the same A)."""
+
+    def __init__(self, rows: torch.Tensor, cols: torch.Tensor, num_rows: int, num_cols: int,
+                 hot_src: torch.Tensor | None = None, backward_bcsc: swtcf.BlockMatrix | None = None):
+        rows, cols = rows.cuda(), cols.cuda()
+        r = rows.to(torch.int32).contiguous()
+        c = cols.to(torch.int32).contiguous()
+        self.num_rows, self.num_cols = num_rows, num_cols
+        if hot_src is None:
+            self.bcsr = swtcf.coo_to_bcsr(r, c, None, num_rows, num_cols)
+            self.bcsc = None
+        else:
+            h = hot_src[cols.long()]
+            self.bcsr = _bcsr_or_empty(r[h].contiguous(), c[h].contiguous(), num_rows, num_cols)
+            self.bcsc = _bcsc_or_empty(r[~h].contiguous(), c[~h].contiguous(), num_rows, num_cols)
+        self.bwd = backward_bcsc if backward_bcsc is not None else swtcf.coo_to_bcsc(r, c, None, num_rows, num_cols)
+
+    def aggregate(self, F: int, x: torch.Tensor | None = None, source=None) -> torch.Tensor:
+        """AX [num_rows x F] (a view of the (RW+1)*8-row denseC buffer)."""
+        RW = self.bcsr.view.num_rowWindows
+        denseC = torch.empty(((RW + 1) * 8, F), dtype=torch.float32, device="cuda")
+        if source is not None:
+            bcsc = self.bcsc if self.bcsc is not None else _EMPTY_BCSC
+            swtcf.spmm_cnic_forward_mixed(self.bcsr, bcsc, source, denseC, F)
+        elif self.bcsc is not None:
+            swtcf.spmm_cnic_forward(self.bcsr, self.bcsc, x, denseC)
+        else:
+            denseC[RW * 8:].zero_()
+            swtcf.bcsr_spmm(self.bcsr, x, denseC[: RW * 8])
+        return denseC[: self.num_rows]
+
+    def transpose_aggregate(self, dY: torch.Tensor) -> torch.Tensor:
+        """Aᵀ dY [num_cols x F]."""
+        out = swtcf.bcsc_transpose_spmm(self.bwd, dY.contiguous())
+        return out[: self.num_cols]
+
+
+def _bcsr_or_empty(r, c, num_rows, num_cols):
+    if r.numel() > 0:
+        return swtcf.coo_to_bcsr(r, c, None, num_rows, num_cols)
+    RW = (num_rows + 7) // 8
+    keep = (torch.zeros(RW + 1, dtype=torch.int32, device="cuda"), torch.zeros(1, dtype=torch.int32, device="cuda"),
+            torch.full((8,), -1, dtype=torch.int32, device="cuda"), torch.zeros(1, dtype=torch.int64, device="cuda"))
+    return swtcf.wrap_bcsr(num_rows, num_cols, 0, 0, RW, *keep)
+
+
+def _bcsc_or_empty(r, c, num_rows, num_cols):
+    if r.numel() > 0:
+        return swtcf.coo_to_bcsc(r, c, None, num_rows, num_cols)
+    return _EMPTY_BCSC
+
+
+class _EmptyBCSC:
+    view = swtcf.BCSC()  # no windows: the scatter launches nothing
+
+
+_EMPTY_BCSC = _EmptyBCSC()
+
+
+class CNICSPMMFunction(torch.autograd.Function):
+    """out = (A X) W with the reference's backward (tcgnn_conv_release.py:49-166)."""
+
+    @staticmethod
+    def forward(ctx, graph: LayerGraph, source, x, weights):
+        F = weights.shape[0]
+        AX = graph.aggregate(F, x=None if source is not None else x.contiguous(), source=source)
+        ctx.graph = graph
+        ctx.save_for_backward(AX, weights)
+        return torch.mm(AX, weights)
+
+    @staticmethod
+    def backward(ctx, d_output):
+        AX, weights = ctx.saved_tensors
+        grad_weights = torch.mm(AX.t(), d_output)
+        grad_x = None
+        if ctx.needs_input_grad[2]:
+            grad_sp = ctx.graph.transpose_aggregate(d_output)
+            grad_x = torch.mm(grad_sp, weights.t())
+        return None, None, grad_x, grad_weights
+
+
+class GCNConv(torch.nn.Module):
+    def __init__(self, input_dim: int, output_dim: int, first_layer: bool = False):
+        super().__init__()
+        self.first_layer = first_layer
+        self.weights = torch.nn.Parameter(torch.empty(input_dim, output_dim))
+        torch.nn.init.xavier_uniform_(self.weights)
+
+    def forward(self, graph: LayerGraph, source=None, x: torch.Tensor | None = None) -> torch.Tensor:
+        return CNICSPMMFunction.apply(graph, source if self.first_layer else None, x, self.weights)
+
+
+class GCN(torch.nn.Module):
+    def __init__(self, num_features: int, hidden_dim: int, num_classes: int, dropout: float = 0.0):
+        super().__init__()
+        self.conv1 = GCNConv(num_features, hidden_dim, first_layer=True)
+        self.conv_final = GCNConv(hidden_dim, num_classes)
+        self.dropout = torch.nn.Dropout(p=dropout)
+
+    def forward(self, g1: LayerGraph, g2: LayerGraph, source) -> torch.Tensor:
+        x = torch.relu(self.conv1(g1, source=source))
+        x = self.dropout(x)
+        return self.conv_final(g2, x=x)
+
+
+class FeatureTable:
+    """Features of every node: the hot rows (top `hot_fraction` of nodes by
+    in-degree as a source, ties by id) in an HBM cache, all rows in mapped
+    pinned host memory, and the tcc_feature_source that resolves them
+    (cache_search_map = hot rank or -1, id_map = identity)."""
+
+    def __init__(self, X: torch.Tensor, cols: torch.Tensor, hot_fraction: float = 0.2):
+        n, F = X.shape
+        deg = torch.bincount(cols.long().cuda(), minlength=n)
+        n_hot = max(1, int(round(n * hot_fraction)))
+        # degree descending, id ascending: sort by (-deg, id) through a stable sort
+        order = torch.sort(-deg, stable=True).indices
+        hot_ids = torch.sort(order[:n_hot]).values
+        self.hot = torch.zeros(n, dtype=torch.bool, device="cuda")
+        self.hot[hot_ids] = True
+        csm = torch.full((n,), -1, dtype=torch.int32, device="cuda")
+        csm[hot_ids] = torch.arange(n_hot, dtype=torch.int32, device="cuda")
+        self.cache = X.cuda()[hot_ids].contiguous()
+        self.host = PinnedArray((n, F))
+        self.host.array[:] = X.cpu().numpy()
+        self.ptrs = torch.tensor([self.cache.data_ptr()], dtype=torch.int64, device="cuda")
+        self.ids = torch.arange(n, dtype=torch.int32, device="cuda")
+        self.csm = csm
+        self.source = swtcf.feature_source(self.ids, csm, self.ptrs, n_hot, self.host.device_ptr, n * F)
+        self.n_hot = n_hot
+
+    def free(self) -> None:
+        self.host.free()
+
+
+def build_gcn_graphs(rows: torch.Tensor, cols: torch.Tensor, n: int, hot: torch.Tensor):
+    """(first-layer graph with the hot/cold split, later-layer graph), both
+    over the same A, sharing the backward BCSC."""
+    g2 = LayerGraph(rows, cols, n, n)
+    g1 = LayerGraph(rows, cols, n, n, hot_src=hot, backward_bcsc=g2.bwd)
+    return g1, g2
+
+
+def train_epoch(model: GCN, g1: LayerGraph, g2: LayerGraph, source, labels: torch.Tensor,
+                optimizer: torch.optim.Optimizer, loss_fcn) -> torch.Tensor:
+    """One full-graph step: forward, loss, backward, optimizer step
+    (train_one_step, tcgnn_conv_release.py:284-329)."""
+    pred = model(g1, g2, source)
+    loss = loss_fcn(pred, labels)
+    optimizer.zero_grad()
+    loss.backward()
+    optimizer.step()
+    return loss
+
+
+def synthetic_labels(n: int, num_classes: int, seed: int) -> torch.Tensor:
+    g = torch.Generator(device="cpu").manual_seed(seed + 2000)
+    return torch.randint(0, num_classes, (n,), generator=g).cuda()
+

@@ -1,0 +1,97 @@
+"""Two-layer GCN step (tcc_amd.gcn, mirroring train/tcgnn_conv_release.py:49-250)
+against a float64 numpy evaluation of the same formulas on a dense A:
+  forward  AX = A·tf32(X) (the spmm_cnic mma.m16n8k8 numerics), out = AX·W
+  backward dW = AXᵀ·dY, G = Aᵀ·dY in plain fp32 operands (torch.sparse.mm,
+           :152), dX = G·Wᵀ
+with a hot/cold feature table on the first layer.  Tolerance rel-L2 1e-4
+(fp32 GEMMs on the GPU against fp64)."""
+import numpy as np
+import pytest
+import torch
+
+REL = 1e-4
+
+
+def rel_l2(a, b):
+    return float(np.linalg.norm(np.asarray(a, np.float64) - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def tf32(a):
+    b = np.asarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    fin = (b & 0x7F800000) != 0x7F800000
+    r = np.where(fin, (b + 0x1000) & 0xFFFFE000, b).astype(np.uint32)
+    return r.view(np.float32).astype(np.float64)
+
+
+def reference_step(A, X, W1, W2, labels):
+    AX1 = A @ tf32(X)
+    H1 = AX1 @ W1
+    R = np.maximum(H1, 0.0)
+    AX2 = A @ tf32(R.astype(np.float32))
+    out = AX2 @ W2
+    m = out.max(axis=1, keepdims=True)
+    logp = out - m - np.log(np.exp(out - m).sum(axis=1, keepdims=True))
+    p = np.exp(logp)
+    n = out.shape[0]
+    loss = -np.mean(logp[np.arange(n), labels])
+    dout = p.copy()
+    dout[np.arange(n), labels] -= 1.0
+    dout /= n
+    dW2 = AX2.T @ dout
+    G2 = A.T @ dout.astype(np.float32).astype(np.float64)
+    dR = G2 @ W2.T
+    dH1 = dR * (H1 > 0)
+    dW1 = AX1.T @ dH1
+    return out, loss, dW1, dW2
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("hot_fraction", [0.2, 0.0, 1.0])
+def test_gcn_step_matches_dense_reference(gpu, hot_fraction):
+    from tcc_amd import gcn
+    from tcc_amd.graphs import rmat_graph
+
+    n, F, H, C = 1999, 20, 48, 3
+    rows, cols = rmat_graph(n, 25_000, 9)
+    torch.manual_seed(0)
+    X = torch.randn((n, F))
+    table = gcn.FeatureTable(X, cols, hot_fraction=hot_fraction)
+    g1, g2 = gcn.build_gcn_graphs(rows, cols, n, table.hot)
+    model = gcn.GCN(F, H, C).cuda()
+    labels = gcn.synthetic_labels(n, C, 1)
+    W1 = model.conv1.weights.detach().cpu().numpy().astype(np.float64)
+    W2 = model.conv_final.weights.detach().cpu().numpy().astype(np.float64)
+    pred = model(g1, g2, table.source)
+    loss = torch.nn.CrossEntropyLoss()(pred, labels)
+    loss.backward()
+    torch.cuda.synchronize()
+    A = np.zeros((n, n))
+    A[rows.numpy(), cols.numpy()] = 1.0
+    out, ref_loss, dW1, dW2 = reference_step(A, X.numpy(), W1, W2, labels.cpu().numpy())
+    assert rel_l2(pred.detach().cpu().numpy(), out) < REL
+    assert abs(loss.item() - ref_loss) < REL * abs(ref_loss)
+    assert rel_l2(model.conv1.weights.grad.cpu().numpy(), dW1) < REL
+    assert rel_l2(model.conv_final.weights.grad.cpu().numpy(), dW2) < REL
+    table.free()
+
+
+@pytest.mark.gpu
+def test_gcn_trains(gpu):
+    """A few Adam steps on a small graph lower the loss (the full training
+    step of tcgnn_conv_release.py:284-329)."""
+    from tcc_amd import gcn
+    from tcc_amd.graphs import rmat_graph
+
+    n, F = 3000, 16
+    rows, cols = rmat_graph(n, 30_000, 10)
+    torch.manual_seed(1)
+    X = torch.randn((n, F))
+    table = gcn.FeatureTable(X, cols)
+    g1, g2 = gcn.build_gcn_graphs(rows, cols, n, table.hot)
+    model = gcn.GCN(F, 64, 2).cuda()
+    labels = gcn.synthetic_labels(n, 2, 3)
+    opt = torch.optim.Adam(model.parameters(), lr=0.003)
+    loss_fcn = torch.nn.CrossEntropyLoss()
+    losses = [gcn.train_epoch(model, g1, g2, table.source, labels, opt, loss_fcn).item() for _ in range(30)]
+    assert losses[-1] < losses[0]
+    table.free()

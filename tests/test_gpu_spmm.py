@@ -190,7 +190,7 @@ def test_bcsr_bcsc_spmm_vs_oracle(gpu, oracle, F, values):
     colptr = np.zeros(nc + 1, np.int64)
     order = np.lexsort((dst, src))
     colptr[1:] = np.cumsum(np.bincount(src, minlength=nc))
-    wantT = oracle.csr_spmm(colptr, dst[order], None if vals is None else vals[order], dY, use_tf32=True)
+    wantT = oracle.csr_spmm(colptr, dst[order], None if vals is None else vals[order], dY, use_tf32=False)
     dX = swtcf.bcsc_transpose_spmm(Bc, torch.from_numpy(dY).cuda())
     assert_close(dX.cpu().numpy()[:nc], wantT)
 
@@ -316,7 +316,7 @@ def test_units_split_windows(gpu, oracle, unit_blocks, F):
     order = np.lexsort((dst, src))
     colptr = np.zeros(nc + 1, np.int64)
     colptr[1:] = np.cumsum(np.bincount(src, minlength=nc))
-    wantT = oracle.csr_spmm(colptr, dst[order], vals[order], dY, use_tf32=True)
+    wantT = oracle.csr_spmm(colptr, dst[order], vals[order], dY, use_tf32=False)
     dX = swtcf.bcsc_transpose_spmm(B, torch.from_numpy(dY).cuda(),
                                    torch.full((B.view.num_colWindows * 8, F), 5.0, device="cuda"))
     assert_close(dX.cpu().numpy()[:nc], wantT)

@@ -207,11 +207,16 @@ def test_block_spmm_oracles_match_csr(oracle, values):
     np.cumsum(np.bincount(c, minlength=77), out=colptr[1:])
     e = oracle.bcsc_build(45, 77, colptr, r[order].astype(np.uint32), None if vals is None else vals[order])
     np.testing.assert_allclose(oracle.bcsc_spmm(e, X, use_data=values), want, rtol=1e-12, atol=1e-12)
-    # A^T dY through the BCSC equals the dense transpose product
+    # A^T dY through the BCSC equals the dense transpose product in plain fp32
+    # operands (torch.sparse.mm of train/tcgnn_conv_release.py:152 rounds nothing)
     dY = np.random.default_rng(14).standard_normal((45, 4)).astype(np.float32)
-    At = dense_of(r, c, None if vals is None else oracle.tf32(vals), 45, 77).T
-    np.testing.assert_allclose(oracle.bcsc_transpose_spmm(e, dY, use_data=values)[:77],
-                               At @ oracle.tf32(dY).astype(np.float64), rtol=1e-12, atol=1e-12)
+    At = dense_of(r, c, vals, 45, 77).T
+    got = oracle.bcsc_transpose_spmm(e, dY, use_data=values)[:77]
+    np.testing.assert_allclose(got, At @ dY.astype(np.float64), rtol=1e-12, atol=1e-12)
+    # and differs from the TF32-rounded product (the planted-mistake check)
+    if values:
+        assert not np.allclose(got, dense_of(r, c, oracle.tf32(vals), 45, 77).T @ oracle.tf32(dY).astype(np.float64),
+                               rtol=1e-9, atol=1e-9)
 
 
 def test_resolve_features(oracle):
