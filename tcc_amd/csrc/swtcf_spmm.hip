@@ -1,13 +1,17 @@
 // SWTCF SpMM on gfx950 (reference: src/swtcf_spmm.cu).
 //
-// Y += A X with A in SWTCF.  One 256-thread workgroup (4 waves) per
-// (super-window, 64-feature chunk); each wave walks every 4th column window
-// of the super-window.  A wave keeps its window's 8 source rows of X in
-// registers (one feature per lane, fp32 and TF32-rounded copies), so X is read
-// exactly once.  Each tile row's sum goes to the super-window's LDS repeat
-// cache when its row is cached (LDS float atomics: 4 waves share the cache),
-// otherwise straight to Y with a global fp32 atomic.  The cache is flushed to
-// Y at the end, as in the reference (:248-264).
+// Y += A X with A in SWTCF.  One 1024-thread workgroup (16 waves) per
+// (super-window, 64-feature chunk); wave i walks column windows i, i+16, ...
+// of the super-window (one each for the reference's S = 16).  A wave keeps
+// its window's 8 source rows of X in registers (one feature per lane, fp32
+// and TF32-rounded copies), so X is read exactly once.  The destinations of
+// 8 tiles at a time are resolved with vector loads one group ahead (lane
+// 8k+r: tile k, row r -> row slot -> repeat-cache slot or global row), so a
+// tile row costs no dependent load.  Each tile row's sum goes to the
+// super-window's LDS repeat cache when its row is cached (LDS float atomics,
+// the 16 waves share the cache), otherwise straight to Y with a global fp32
+// atomic.  The cache is flushed to Y at the end, as in the reference
+// (:248-264).
 //
 // Numerics follow the reference per tile: popcount >= tcThreshold uses TF32
 // X (its mma.m16n8k8 path, :188-221), sparser tiles use fp32 X (:222-241);
@@ -20,9 +24,46 @@
 namespace tcc {
 namespace {
 
-constexpr unsigned kThreads = 256;
+constexpr unsigned kThreads = 1024;
 constexpr unsigned kWaves = kThreads / kWave;
 constexpr unsigned kChunk = kWave;  // features per workgroup
+constexpr std::uint32_t kCached = 0x80000000u;  // target = repeat-cache slot
+constexpr std::uint32_t kNoTarget = 0xFFFFFFFFu;
+
+__device__ __forceinline__ std::uint32_t lane_u32(std::uint32_t v, int l) {
+    return static_cast<std::uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), l));
+}
+
+// Tiles g..g+7 of a window ending at tile `end`: lane 8k+r holds the target
+// of row r of tile g+k (kCached | cache slot, the global row, or kNoTarget
+// for padding rows); lanes 0..7 hold the bitmaps of tiles g..g+7.
+struct TileGroup {
+    std::uint32_t target;
+    std::uint32_t bitsLo, bitsHi;
+};
+
+__device__ __forceinline__ TileGroup load_tiles(const std::uint32_t* __restrict__ tileRowSlot,
+                                                const std::uint64_t* __restrict__ tileLocalBit,
+                                                const std::uint8_t* __restrict__ rowCacheSlot,
+                                                const std::uint32_t* __restrict__ superWindowRows, std::uint32_t off,
+                                                std::uint32_t g, std::uint32_t end) {
+    const unsigned lane = __lane_id();
+    TileGroup m;
+    m.target = kNoTarget;
+    const std::uint32_t t = g + lane / 8;
+    if (t < end) {
+        const std::uint32_t slot = tileRowSlot[static_cast<std::uint64_t>(t) * 8 + (lane & 7u)];
+        if (slot != TCC_SWTCF_INVALID_ROW_SLOT) {
+            const std::uint8_t cs = rowCacheSlot[off + slot];
+            m.target = (cs != TCC_SWTCF_INVALID_CACHE_SLOT) ? (kCached | cs) : superWindowRows[off + slot];
+        }
+    }
+    std::uint64_t bits = 0;
+    if (lane < 8 && g + lane < end) bits = tileLocalBit[g + lane];
+    m.bitsLo = static_cast<std::uint32_t>(bits);
+    m.bitsHi = static_cast<std::uint32_t>(bits >> 32);
+    return m;
+}
 
 template <bool QUANT>
 __global__ void __launch_bounds__(kThreads) swtcf_spmm_kernel(
@@ -49,7 +90,9 @@ __global__ void __launch_bounds__(kThreads) swtcf_spmm_kernel(
     for (std::uint32_t wi = wave; wi < S; wi += kWaves) {
         const std::uint32_t w = s * S + wi;
         if (w >= CW) break;
+        const std::uint32_t t0 = colWindowOffset[w], t1 = colWindowOffset[w + 1];
         float xv[8], xt[8];
+        // all loads in flight before any is rounded
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
             const std::uint32_t col = w * 8 + c;
@@ -63,31 +106,37 @@ __global__ void __launch_bounds__(kThreads) swtcf_spmm_kernel(
                 }
             }
             xv[c] = v;
-            xt[c] = tf32_rna(v);
         }
-        const std::uint32_t t0 = colWindowOffset[w], t1 = colWindowOffset[w + 1];
-        for (std::uint32_t t = t0; t < t1; ++t) {
-            const std::uint64_t bm = tileLocalBit[t];
-            const bool dense = static_cast<std::uint32_t>(__popcll(bm)) >= tc;
 #pragma unroll
-            for (int r = 0; r < 8; ++r) {
-                const std::uint32_t rb = static_cast<std::uint32_t>(bm >> (8 * r)) & 0xFFu;
-                if (rb == 0) continue;
-                const std::uint32_t slot = tileRowSlot[static_cast<std::uint64_t>(t) * 8 + r];
-                if (slot == TCC_SWTCF_INVALID_ROW_SLOT) continue;
-                float sum = 0.0f;
+        for (int c = 0; c < 8; ++c) xt[c] = tf32_rna(xv[c]);
+        TileGroup cur = load_tiles(tileRowSlot, tileLocalBit, rowCacheSlot, superWindowRows, off, t0, t1);
+        for (std::uint32_t g = t0; g < t1; g += 8) {
+            TileGroup nxt = cur;
+            if (g + 8 < t1) nxt = load_tiles(tileRowSlot, tileLocalBit, rowCacheSlot, superWindowRows, off, g + 8, t1);
+            const int nt = static_cast<int>(min(8u, t1 - g));
+            for (int k = 0; k < nt; ++k) {
+                const std::uint64_t bm =
+                    (static_cast<std::uint64_t>(lane_u32(cur.bitsHi, k)) << 32) | lane_u32(cur.bitsLo, k);
+                const bool dense = static_cast<std::uint32_t>(__popcll(bm)) >= tc;
 #pragma unroll
-                for (int c = 0; c < 8; ++c)
-                    if (rb & (1u << c)) sum += dense ? xt[c] : xv[c];
-                if (!active || sum == 0.0f) continue;
-                const std::uint8_t cs = rowCacheSlot[off + slot];
-                if (cs != TCC_SWTCF_INVALID_CACHE_SLOT) {
-                    atomicAdd(&cache[cs][lane], sum);
-                } else {
-                    const std::uint32_t row = superWindowRows[off + slot];
-                    atomic_add_f32(&Y[static_cast<std::uint64_t>(row) * F + f], sum);
+                for (int r = 0; r < 8; ++r) {
+                    const std::uint32_t rb = static_cast<std::uint32_t>(bm >> (8 * r)) & 0xFFu;
+                    if (rb == 0) continue;
+                    const std::uint32_t target = lane_u32(cur.target, k * 8 + r);
+                    if (target == kNoTarget) continue;
+                    float sum = 0.0f;
+#pragma unroll
+                    for (int c = 0; c < 8; ++c)
+                        if (rb & (1u << c)) sum += dense ? xt[c] : xv[c];
+                    if (!active || sum == 0.0f) continue;
+                    if (target & kCached) {
+                        atomicAdd(&cache[target & 31u][lane], sum);
+                    } else {
+                        atomic_add_f32(&Y[static_cast<std::uint64_t>(target) * F + f], sum);
+                    }
                 }
             }
+            cur = nxt;
         }
     }
     __syncthreads();

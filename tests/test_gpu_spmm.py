@@ -88,6 +88,27 @@ def test_swtcf_spmm_vs_oracle(gpu, oracle, F, tc):
     assert_close(Y.cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("S", [1, 3, 32])
+def test_swtcf_spmm_super_window_sizes_skewed(gpu, oracle, S):
+    """Super-window sizes other than 16 (1 window per workgroup, 3, and two
+    windows per wave at 32) on an R-MAT graph whose hub windows hold many
+    tiles (several tile groups per window) and many repeated rows."""
+    from tcc_amd import swtcf
+    from tcc_amd.graphs import rmat_graph
+
+    n, F = 3000, 48
+    rows, cols = rmat_graph(n, 60_000, 21)
+    dst, src = rows.numpy().astype(np.uint32), cols.numpy().astype(np.uint32)
+    m = build_swtcf(dst, src, n, n, S=S)
+    X = np.random.default_rng(5).standard_normal((n, F)).astype(np.float32)
+    Y = torch.zeros((n, F), device="cuda")
+    swtcf.swtcf_spmm(m, torch.from_numpy(X).cuda(), Y, 12)
+    ref = oracle.swtcf_convert(dst, src, n, n, S)
+    assert int(np.max(np.diff(ref["colWindowOffset"]))) > 16  # windows with several tile groups
+    want = oracle.swtcf_spmm(ref, X, tc=12, rows=n)
+    assert_close(Y.cpu().numpy(), want)
+
+
 def test_swtcf_config1(gpu, oracle):
     from tcc_amd import swtcf
     from tcc_amd.graphs import make_features, uniform_graph
