@@ -34,6 +34,9 @@ sys.path.insert(0, ROOT)
 METRIC = "SpMM GFLOP/s (2·nnz·F) + % HBM roofline; GCN layer fwd+bwd ms at 1 GPU"
 HBM_PEAK_GBPS = 8000.0
 PCIE_PEAK_GBPS = 64.0  # PCIe Gen5 x16, one direction
+# Gathers per feature row from which packing X to TF32 first pays off
+# (measured: 441 -> 12% faster at config 3; 7.3 -> 23% slower at config 2).
+PACK_MIN_REUSE = 16.0
 
 WORKLOADS = {
     1: "config1: uniform 4096 nodes x 16 nnz/row, F=32, SWTCF convert + SWTCF SpMM",
@@ -179,14 +182,41 @@ def bench_spmm(args, torch, swtcf, cfg):
 
         kernel = "swtcf_spmm_kernel"
     else:
+        swtcf.coo_to_bcsr(r32, c32, vals, n, n).release()  # warm-up
+        torch.cuda.synchronize()
+        t_b = time.perf_counter()
         A = swtcf.coo_to_bcsr(r32, c32, vals, n, n)
+        torch.cuda.synchronize()
+        extra["bcsr_build_ms"] = round((time.perf_counter() - t_b) * 1e3, 3)
         Y = torch.empty((A.view.num_rowWindows * 8, F), device="cuda")
         extra["blocks"] = A.view.num_TCBlocks
+        reuse = 8.0 * A.view.num_TCBlocks / n  # feature-row gathers per row
+        extra["row_reuse"] = round(reuse, 2)
+        if reuse >= PACK_MIN_REUSE:
+            # each step packs X to TF32 rows of 2.5 B/element, then gathers them
+            buf = torch.empty(swtcf._lib.lib().tcc_tf32_packed_bytes(n, F) + 16, dtype=torch.uint8, device="cuda")
 
-        def step():
-            swtcf.bcsr_spmm(A, X, Y)
+            def step():
+                swtcf.bcsr_spmm_packed(A, swtcf.tf32_pack(X, out=buf), F, Y)
 
-        kernel = "gather_kernel"
+            kernel = "gather_kernel<Packed> (after tf32_pack_kernel, both timed)"
+            extra["path"] = "tf32_pack + packed gather"
+        else:
+            def step():
+                swtcf.bcsr_spmm(A, X, Y)
+
+            kernel = "gather_kernel"
+            extra["path"] = "fp32 gather"
+    if args.config in (2, 3):
+        # SWTCF conversion of the same COO (S = 16), GEdges/s as the
+        # reference's converter driver prints it (swtcf_convert_main.cu:417)
+        m = swtcf.DeviceSWTCFMatrix(n, n, nnz, 16)
+        ws = swtcf.SWTCFConvertWorkspace(nnz, n, 16)
+        conv_ms = timed(lambda: swtcf.convertCOOToSWTCF(r32, c32, nnz, m, ws), 5 if args.config == 2 else 3, 1)
+        assert ws.device_error() == 0
+        extra["convert_ms"] = round(conv_ms, 4)
+        extra["convert_gedges_per_s"] = round(nnz / conv_ms / 1e6, 3)
+        del m, ws
     if args.copy_calibration_mib:
         copy_calibration(args.copy_calibration_mib)
     ms = timed(step, args.steps, args.warmup)

@@ -84,6 +84,9 @@ SIGNATURES = {
     "tcc_coo_to_bcsr": (ctypes.c_int, [vp, vp, vp, u32, u32, u32, ctypes.POINTER(BCSR), ctypes.POINTER(vp), vp]),
     "tcc_coo_to_bcsc": (ctypes.c_int, [vp, vp, vp, u32, u32, u32, ctypes.POINTER(BCSC), ctypes.POINTER(vp), vp]),
     "tcc_block_release": (ctypes.c_int, [vp]),
+    "tcc_tf32_packed_bytes": (ctypes.c_size_t, [u32, u32]),
+    "tcc_tf32_pack": (ctypes.c_int, [vp, u32, u32, vp, vp]),
+    "tcc_bcsr_spmm_packed": (ctypes.c_int, [ctypes.POINTER(BCSR), vp, vp, u32, ctypes.c_int, vp]),
 }
 
 _lib = None

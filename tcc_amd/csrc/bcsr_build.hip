@@ -58,7 +58,7 @@ __global__ void bcsr_flags_kernel(const std::uint64_t* __restrict__ keys, std::u
     const bool head = e == 0 || (k >> 3) != (keys[e - 1] >> 3);
     if (e > 0 && k == keys[e - 1]) atomicMax(err, 2u);
     flags[e] = head ? 1u : 0u;
-    if (head) atomicAdd(&rwCount[static_cast<std::uint32_t>(k >> (colBits + 3))], 1u);
+    if (head) aggregated_increment(rwCount, static_cast<std::uint32_t>(k >> (colBits + 3)));
 }
 
 __global__ void blocks_per_window_kernel(const std::uint32_t* __restrict__ cnt, std::uint32_t n,

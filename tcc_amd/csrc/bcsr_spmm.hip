@@ -39,7 +39,9 @@ namespace {
 constexpr unsigned kThreads = 256;
 constexpr unsigned kWaves = kThreads / kWave;
 
-enum class Src { Plain, Mixed, Transposed };
+// Where a gather reads its input rows: fp32 X, the first layer's hot/cold
+// feature source, dY for the A^T product, or a packed TF32 copy of X.
+enum class Src { Plain, Mixed, Transposed, Packed };
 
 // Feature-source fields of the first GCN layer (tcc_feature_source).
 struct MixedArgs {
@@ -59,6 +61,8 @@ struct GatherArgs {
     const std::uint64_t* bits;       // [blocks]
     const float* data;               // values or nullptr
     const float* X;                  // input rows (Plain / Transposed)
+    const unsigned char* packed;     // packed TF32 rows (Packed)
+    std::uint32_t packedStride;      // bytes per packed row
     float* Y;                        // [8*numWindows x F]
     std::uint32_t numWindows;
     std::uint32_t numBlocks;
@@ -197,8 +201,64 @@ template <Src MODE>
 __device__ __forceinline__ const float* input_row(const GatherArgs& a, std::uint32_t in) {
     if constexpr (MODE == Src::Mixed) {
         return mixed_row(a.mixed, a.F, in);
+    } else if constexpr (MODE == Src::Packed) {
+        return reinterpret_cast<const float*>(a.packed + static_cast<std::uint64_t>(in) * a.packedStride);
     } else {
         return a.X + static_cast<std::uint64_t>(in) * a.F;
+    }
+}
+
+// Packed TF32 rows (tcc_tf32_pack): a TF32 value has 19 significant bits,
+// stored as its high 16 bits (sign, exponent, 7 mantissa bits; 2 bytes per
+// element, row-major) followed by the 3 low mantissa bits of element pairs
+// (element 2k in bits 0-2 and 2k+1 in bits 3-5 of byte k), rows padded to
+// 16 bytes: stride = roundup(2F + ceil(F/2), 16).  Exact: unpacking gives
+// the TF32 rounding of X bit for bit.
+__host__ __device__ constexpr std::uint64_t packed_stride(std::uint32_t F) {
+    return ((2ull * F + (F + 1) / 2) + 15) & ~15ull;
+}
+
+__device__ __forceinline__ float tf32_from(std::uint32_t hi16, std::uint32_t lo3) {
+    return __uint_as_float((hi16 << 16) | (lo3 << 13));
+}
+
+// The V features at element offset `f` of a packed row (f % V == 0): the
+// high halves and the low bits, loaded before any use.
+template <int V>
+struct PackedVec {
+    std::uint32_t hi[(V + 1) / 2];
+    std::uint32_t lo;
+};
+
+template <int V>
+__device__ __forceinline__ PackedVec<V> load_packed(const unsigned char* row, std::uint32_t F, std::uint32_t f) {
+    PackedVec<V> p;
+    if constexpr (V == 4) {
+        const uint2 h = *reinterpret_cast<const uint2*>(row + 2ull * f);
+        p.hi[0] = h.x;
+        p.hi[1] = h.y;
+        p.lo = *reinterpret_cast<const std::uint16_t*>(row + 2ull * F + f / 2);
+    } else if constexpr (V == 2) {
+        p.hi[0] = *reinterpret_cast<const std::uint32_t*>(row + 2ull * f);
+        p.lo = row[2ull * F + f / 2];
+    } else {
+        p.hi[0] = *reinterpret_cast<const std::uint16_t*>(row + 2ull * f);
+        p.lo = row[2ull * F + f / 2] >> (3 * (f & 1u));
+    }
+    return p;
+}
+
+template <int V>
+__device__ __forceinline__ void unpack(const PackedVec<V>& p, float* x) {
+    if constexpr (V == 1) {
+        x[0] = tf32_from(p.hi[0] & 0xFFFFu, p.lo & 7u);
+    } else {
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            const std::uint32_t h = p.hi[j / 2];
+            const std::uint32_t hi16 = (j & 1) ? (h >> 16) : (h & 0xFFFFu);
+            x[j] = tf32_from(hi16, (p.lo >> (8 * (j / 2) + 3 * (j & 1))) & 7u);
+        }
     }
 }
 
@@ -251,16 +311,29 @@ __device__ __forceinline__ void load_block(const GatherArgs& a, const GroupMeta&
     bm = (MODE == Src::Transposed) ? transpose8x8(raw) : raw;
     // All loads are issued before any result is used (rounding inside the
     // branches would wait for each load in turn).
+    if constexpr (MODE == Src::Packed) {
+        PackedVec<V> pk[8];
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-        const std::uint64_t rp = (static_cast<std::uint64_t>(lane_u32(m.rowHi, k * 8 + c)) << 32) |
-                                 lane_u32(m.rowLo, k * 8 + c);
+        for (int c = 0; c < 8; ++c) {
+            const std::uint64_t rp = (static_cast<std::uint64_t>(lane_u32(m.rowHi, k * 8 + c)) << 32) |
+                                     lane_u32(m.rowLo, k * 8 + c);
+            pk[c] = PackedVec<V>{};
+            if (rp != 0) pk[c] = load_packed<V>(reinterpret_cast<const unsigned char*>(rp), a.F, laneOff);
+        }
 #pragma unroll
-        for (int v = 0; v < V; ++v) x[c][v] = 0.0f;
-        if (rp != 0) {
-            const Vec<V> t = load_vec<V>(reinterpret_cast<const float*>(rp) + laneOff);
+        for (int c = 0; c < 8; ++c) unpack<V>(pk[c], x[c]);
+    } else {
 #pragma unroll
-            for (int v = 0; v < V; ++v) x[c][v] = t.v[v];
+        for (int c = 0; c < 8; ++c) {
+            const std::uint64_t rp = (static_cast<std::uint64_t>(lane_u32(m.rowHi, k * 8 + c)) << 32) |
+                                     lane_u32(m.rowLo, k * 8 + c);
+#pragma unroll
+            for (int v = 0; v < V; ++v) x[c][v] = 0.0f;
+            if (rp != 0) {
+                const Vec<V> t = load_vec<V>(reinterpret_cast<const float*>(rp) + laneOff);
+#pragma unroll
+                for (int v = 0; v < V; ++v) x[c][v] = t.v[v];
+            }
         }
     }
     vals = 0.0f;
@@ -270,14 +343,15 @@ __device__ __forceinline__ void load_block(const GatherArgs& a, const GroupMeta&
     }
     // The A^T product replaces torch.sparse.mm in the reference's backward
     // (train/tcgnn_conv_release.py:152), which multiplies in plain fp32; the
-    // forward products reproduce its mma.m16n8k8 tf32 numerics.
-    if constexpr (MODE != Src::Transposed) {
+    // forward products reproduce its mma.m16n8k8 tf32 numerics (packed rows
+    // hold TF32 values already).
+    if constexpr (MODE == Src::Plain || MODE == Src::Mixed) {
 #pragma unroll
         for (int c = 0; c < 8; ++c)
 #pragma unroll
             for (int v = 0; v < V; ++v) x[c][v] = tf32_rna(x[c][v]);
-        if constexpr (VALUES) vals = tf32_rna(vals);
     }
+    if constexpr (VALUES && MODE != Src::Transposed) vals = tf32_rna(vals);
 }
 
 // acc[R] += w(R,C) * x[C] over the block's nonzeros (uniform branches over
@@ -405,6 +479,28 @@ __global__ void __launch_bounds__(kThreads) zero_shared_windows_kernel(const std
     if (u >= 2 && winOffset[w] < b0 - K) return;  // boundary (u-1)*K cut it already
     float* p = Y + static_cast<std::uint64_t>(w) * 8 * F;
     for (std::uint32_t i = __lane_id(); i < 8u * F; i += kWave) p[i] = 0.0f;
+}
+
+// X [rows x F] fp32 -> packed TF32 rows (layout at packed_stride).  One
+// thread per element pair.
+__global__ void tf32_pack_kernel(const float* __restrict__ X, std::uint32_t rows, std::uint32_t F,
+                                 std::uint32_t pairs, unsigned char* __restrict__ out, std::uint64_t stride) {
+    const std::uint64_t i = static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const std::uint64_t r = i / pairs;
+    if (r >= rows) return;
+    const std::uint32_t p = static_cast<std::uint32_t>(i - r * pairs);
+    const std::uint32_t e = 2 * p;
+    const float* x = X + r * F;
+    const bool two = e + 1 < F;
+    const std::uint32_t b0 = __float_as_uint(tf32_rna(x[e]));
+    const std::uint32_t b1 = two ? __float_as_uint(tf32_rna(x[e + 1])) : 0u;
+    unsigned char* row = out + r * stride;
+    if (two) {
+        *reinterpret_cast<std::uint32_t*>(row + 4ull * p) = (b0 >> 16) | (b1 & 0xFFFF0000u);
+    } else {
+        *reinterpret_cast<std::uint16_t*>(row + 4ull * p) = static_cast<std::uint16_t>(b0 >> 16);
+    }
+    row[2ull * F + p] = static_cast<unsigned char>(((b0 >> 13) & 7u) | (((b1 >> 13) & 7u) << 3));
 }
 
 struct ScatterArgs {
@@ -685,6 +781,39 @@ int tcc_bcsr_spmm(const tcc_bcsr* A, const float* X, float* Y, std::uint32_t fea
     const int V = pick_vec(featureDim, {X, Y});
     return launch_gather<Src::Plain>(bcsr_args(A, X, Y, featureDim, accumulate), V, A->unitBlocks,
                                      as_stream(stream));
+}
+
+size_t tcc_tf32_packed_bytes(std::uint32_t rows, std::uint32_t featureDim) {
+    return static_cast<size_t>(rows) * packed_stride(featureDim);
+}
+
+int tcc_tf32_pack(const float* X, std::uint32_t rows, std::uint32_t featureDim, void* packed, void* stream) {
+    clear_last_error();
+    TCC_REQUIRE(X && packed && featureDim >= 1, TCC_ERR_INVALID_ARGUMENT, "invalid TF32 pack arguments");
+    TCC_REQUIRE(reinterpret_cast<std::uintptr_t>(packed) % 16 == 0, TCC_ERR_INVALID_ARGUMENT,
+                "packed buffer must be 16-byte aligned");
+    if (rows == 0) return TCC_OK;
+    const std::uint32_t pairs = (featureDim + 1) / 2;
+    const std::uint64_t n = static_cast<std::uint64_t>(rows) * pairs;
+    TCC_REQUIRE(n <= 0xFFFFFFFFull * 256, TCC_ERR_UNSUPPORTED, "TF32 pack too large");
+    hipLaunchKernelGGL(tf32_pack_kernel, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(stream), X, rows,
+                       featureDim, pairs, static_cast<unsigned char*>(packed), packed_stride(featureDim));
+    TCC_LAUNCH_CHECK();
+    return TCC_OK;
+}
+
+int tcc_bcsr_spmm_packed(const tcc_bcsr* A, const void* packedX, float* Y, std::uint32_t featureDim, int accumulate,
+                         void* stream) {
+    clear_last_error();
+    TCC_REQUIRE(bcsr_ok(A) && packedX && Y && featureDim >= 1, TCC_ERR_INVALID_ARGUMENT,
+                "invalid packed BCSR SpMM arguments");
+    TCC_REQUIRE(reinterpret_cast<std::uintptr_t>(packedX) % 16 == 0, TCC_ERR_INVALID_ARGUMENT,
+                "packed buffer must be 16-byte aligned");
+    GatherArgs a = bcsr_args(A, nullptr, Y, featureDim, accumulate);
+    a.packed = static_cast<const unsigned char*>(packedX);
+    a.packedStride = static_cast<std::uint32_t>(packed_stride(featureDim));
+    const int V = pick_vec(featureDim, {Y});
+    return launch_gather<Src::Packed>(a, V, A->unitBlocks, as_stream(stream));
 }
 
 int tcc_bcsr_spmm_mixed(const tcc_bcsr* A, const tcc_feature_source* src, float* Y, std::uint32_t featureDim,

@@ -74,6 +74,21 @@ __device__ __forceinline__ std::uint64_t match_peers(unsigned key, bool active) 
     return active ? peers : 0ull;
 }
 
+// counter[idx] += 1 for every calling lane, one atomic per distinct index
+// in the wave: sorted inputs put many lanes of a wave on the same few
+// counters, where per-lane atomics serialise.
+__device__ __forceinline__ void aggregated_increment(std::uint32_t* counter, std::uint32_t idx) {
+    std::uint64_t todo = __ballot(true);
+    while (todo) {
+        const int leader = __builtin_ctzll(todo);
+        const std::uint32_t lidx =
+            static_cast<std::uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(idx), leader));
+        const std::uint64_t same = __ballot(idx == lidx) & todo;
+        if (static_cast<int>(__lane_id()) == leader) atomicAdd(&counter[lidx], static_cast<std::uint32_t>(__popcll(same)));
+        todo &= ~same;
+    }
+}
+
 // fp32 atomic add to global memory (hardware global_atomic_add_f32; the
 // library is compiled with -munsafe-fp-atomics for coarse-grained memory).
 __device__ __forceinline__ void atomic_add_f32(float* p, float v) { unsafeAtomicAdd(p, v); }

@@ -62,7 +62,6 @@ struct Carve {
     std::uint32_t* wdBase;         // [CW*8]
     std::uint32_t* wActive;        // [CW]
     std::uint32_t* wTiles;         // [CW]
-    std::uint32_t* swRowCount;     // [SW]
     std::uint32_t* numRows;        // [1]
     std::uint32_t* temp;           // scan / sort scratch
     std::size_t bytes;
@@ -89,7 +88,6 @@ inline Carve carve(char* base, std::uint64_t E, std::uint64_t CW, std::uint64_t 
     c.wdBase = reinterpret_cast<std::uint32_t*>(take(4 * CW * 8));
     c.wActive = reinterpret_cast<std::uint32_t*>(take(4 * CW));
     c.wTiles = reinterpret_cast<std::uint32_t*>(take(4 * CW));
-    c.swRowCount = reinterpret_cast<std::uint32_t*>(take(4 * SW));
     c.numRows = reinterpret_cast<std::uint32_t*>(take(4 * 4));
     const std::uint64_t tempElems =
         std::max({radix_temp_elems(E), scan_temp_elems(E + 1), scan_temp_elems(CW + 1), scan_temp_elems(SW + 1)});
@@ -174,7 +172,7 @@ __global__ void group_finalize_kernel(const std::uint64_t* __restrict__ keys,
     const std::uint32_t wi = static_cast<std::uint32_t>(gk & ((1ull << wiBits) - 1ull));
     const std::uint32_t sw = static_cast<std::uint32_t>(gk >> (wiBits + dstBits));
     const std::uint32_t w = sw * S + wi;
-    atomicAdd(&wdCount[static_cast<std::uint64_t>(w) * 8 + deg - 1], 1u);
+    aggregated_increment(wdCount, w * 8 + deg - 1);
     groupInfo[g] = bits | (deg << 8);
     rowFlags[g] = (g == 0 || (gk >> wiBits) != (groupKey[g - 1] >> wiBits)) ? 1u : 0u;
 }
@@ -204,22 +202,32 @@ __global__ void row_emit_kernel(const std::uint64_t* __restrict__ groupKey,
                                 unsigned dstBits, std::uint32_t numSuperWindows,
                                 std::uint32_t* __restrict__ rowStartGroup,
                                 std::uint32_t* __restrict__ superWindowRows,
-                                std::uint32_t* __restrict__ swRowCount) {
+                                std::uint32_t* __restrict__ superWindowRowOffset) {
     const std::uint32_t g = blockIdx.x * blockDim.x + threadIdx.x;
     if (g >= E) return;
     const std::uint32_t G = *numGroups;
     if (g >= G) return;
+    const unsigned swShift = wiBits + dstBits;
     if (rowFlags[g]) {
         const std::uint32_t u = rowPos[g];
         const std::uint64_t gk = groupKey[g];
         const std::uint32_t dstMask = dstBits >= 32 ? 0xFFFFFFFFu : ((1u << dstBits) - 1u);
         const std::uint32_t d = static_cast<std::uint32_t>(gk >> wiBits) & dstMask;
-        const std::uint32_t sw = static_cast<std::uint32_t>(gk >> (wiBits + dstBits));
+        const std::uint32_t sw = static_cast<std::uint32_t>(gk >> swShift);
         rowStartGroup[u] = g;
         superWindowRows[u] = d;
-        if (sw < numSuperWindows) atomicAdd(&swRowCount[sw], 1u);
+        // Rows are sorted by super-window: the first row of super-window sw
+        // sets its offset, and those of the empty super-windows before it.
+        const std::int64_t prev = g == 0 ? -1 : static_cast<std::int64_t>(groupKey[g - 1] >> swShift);
+        for (std::int64_t t = prev + 1; t <= static_cast<std::int64_t>(sw) && t < numSuperWindows; ++t)
+            superWindowRowOffset[t] = u;
     }
-    if (g == G - 1) rowStartGroup[rowPos[g] + rowFlags[g]] = G;
+    if (g == G - 1) {
+        const std::uint32_t U = rowPos[g] + rowFlags[g];
+        rowStartGroup[U] = G;
+        const std::uint32_t sw = static_cast<std::uint32_t>(groupKey[g] >> swShift);
+        for (std::uint32_t t = sw + 1; t <= numSuperWindows; ++t) superWindowRowOffset[t] = U;
+    }
 }
 
 // Stable rank of `bin` among the active items of a 256-item chunk (item order
@@ -486,7 +494,7 @@ int tcc_swtcf_convert(const std::uint32_t* dDst, const std::uint32_t* dSrc, std:
                                       0xFFFFFFFFu, st));
     TCC_HIP_CHECK(fill<std::uint8_t>(m->superWindowCachedCount, SW, 0u, st));
     TCC_HIP_CHECK(fill<std::uint32_t>(c.wdCount, static_cast<std::uint64_t>(CW) * 8, 0u, st));
-    TCC_HIP_CHECK(fill<std::uint32_t>(c.swRowCount, SW, 0u, st));
+    TCC_HIP_CHECK(fill<std::uint32_t>(m->superWindowRowOffset, static_cast<std::uint64_t>(SW) + 1, 0u, st));
     TCC_HIP_CHECK(fill<std::uint32_t>(err, 1, 0u, st));
 
     // 1-2. keys, sort
@@ -520,10 +528,8 @@ int tcc_swtcf_convert(const std::uint32_t* dDst, const std::uint32_t* dSrc, std:
     TCC_HIP_CHECK(exclusive_scan(c.flags, c.pos, E, c.numRows, c.temp, st));
     hipLaunchKernelGGL(row_emit_kernel, dim3(grid_for(E, kThreads)), dim3(kThreads), 0, st, groupKey, c.flags,
                        c.pos, numGroups, E, kl.wiBits, kl.dstBits, SW, c.rowStartGroup, m->superWindowRows,
-                       c.swRowCount);
+                       m->superWindowRowOffset);
     TCC_LAUNCH_CHECK();
-    TCC_HIP_CHECK(exclusive_scan(c.swRowCount, m->superWindowRowOffset, SW, m->superWindowRowOffset + SW,
-                                 c.temp, st));
 
     // 6-7, 11-13. per super-window: row locations, slots, bitmaps, cache
     hipLaunchKernelGGL(super_window_kernel, dim3(SW), dim3(kThreads), 0, st, groupKey, c.groupInfo, c.flags,

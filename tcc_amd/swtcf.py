@@ -53,6 +53,13 @@ def _ptr(t) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+def _f32(t: torch.Tensor, name: str) -> torch.Tensor:
+    """A contiguous float32 device tensor (the kernels read raw fp32)."""
+    if t.dtype != torch.float32 or not t.is_cuda:
+        raise TypeError(f"{name} must be a float32 device tensor (got {t.dtype} on {t.device})")
+    return t.contiguous()
+
+
 def _u32(t: torch.Tensor) -> torch.Tensor:
     """int32/uint32 device tensor viewed as u32 storage (contiguous)."""
     if t.dtype not in (torch.int32, torch.uint32):
@@ -274,7 +281,8 @@ def host_to_bcsc(d: dict, use_data: bool = False) -> BlockMatrix:
 
 def bcsr_spmm(A: BlockMatrix, X: torch.Tensor, Y: torch.Tensor | None = None, accumulate: bool = False,
               stream=None) -> torch.Tensor:
-    """Y[8*RW x F] (=|+=) A X, no atomics."""
+    """Y[8*RW x F] (=|+=) A X."""
+    X = _f32(X, "X")
     F = X.shape[1]
     if Y is None:
         Y = torch.empty((A.view.num_rowWindows * 8, F), dtype=torch.float32, device=X.device)
@@ -283,15 +291,42 @@ def bcsr_spmm(A: BlockMatrix, X: torch.Tensor, Y: torch.Tensor | None = None, ac
     return Y
 
 
+def tf32_pack(X: torch.Tensor, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """TF32(X) packed in 2.5 bytes per element (tcc_tf32_pack); a uint8
+    device tensor of tcc_tf32_packed_bytes(rows, F) bytes."""
+    X = _f32(X, "X")
+    rows, F = X.shape
+    nbytes = _lib.lib().tcc_tf32_packed_bytes(rows, F)
+    if out is None:
+        out = torch.empty(nbytes + 16, dtype=torch.uint8, device=X.device)
+    base = out.data_ptr()
+    shift = (-base) % 16
+    packed = out[shift:shift + nbytes]
+    check(_lib.lib().tcc_tf32_pack(X.data_ptr(), rows, F, packed.data_ptr(), _stream(stream)))
+    return packed
+
+
+def bcsr_spmm_packed(A: BlockMatrix, packed: torch.Tensor, F: int, Y: torch.Tensor | None = None,
+                     accumulate: bool = False, stream=None) -> torch.Tensor:
+    """Y[8*RW x F] (=|+=) A X with X given by tf32_pack."""
+    if Y is None:
+        Y = torch.empty((A.view.num_rowWindows * 8, F), dtype=torch.float32, device=packed.device)
+    check(_lib.lib().tcc_bcsr_spmm_packed(ctypes.byref(A.view), packed.data_ptr(), Y.data_ptr(), F,
+                                          int(accumulate), _stream(stream)))
+    return Y
+
+
 def bcsc_spmm(A: BlockMatrix, X: torch.Tensor, Y: torch.Tensor, stream=None) -> torch.Tensor:
     """Y[num_rows x F] += A X with atomics."""
+    X = _f32(X, "X")
     check(_lib.lib().tcc_bcsc_spmm(ctypes.byref(A.view), X.data_ptr(), Y.data_ptr(), X.shape[1], _stream(stream)))
     return Y
 
 
 def bcsc_transpose_spmm(A: BlockMatrix, dY: torch.Tensor, dX: torch.Tensor | None = None, accumulate: bool = False,
                         stream=None) -> torch.Tensor:
-    """dX[8*CW x F] (=|+=) A^T dY, no atomics."""
+    """dX[8*CW x F] (=|+=) A^T dY."""
+    dY = _f32(dY, "dY")
     F = dY.shape[1]
     if dX is None:
         dX = torch.empty((A.view.num_colWindows * 8, F), dtype=torch.float32, device=dY.device)

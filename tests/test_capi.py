@@ -15,7 +15,7 @@ def declared_functions():
     names = set()
     for h in glob.glob(os.path.join(ROOT, "include", "tcc_*.h")):
         text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
-        names.update(re.findall(r"^\s*(?:int|const char\*)\s+(tcc_\w+)\s*\(", text, flags=re.M))
+        names.update(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(tcc_\w+)\s*\(", text, flags=re.M))
     return sorted(names)
 
 

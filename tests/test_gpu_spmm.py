@@ -376,3 +376,57 @@ def test_unit_sizes_agree_on_rmat(gpu):
         A.set_unit_blocks(K)
         Y = swtcf.bcsr_spmm(A, X)
         assert rel_l2(Y.cpu().numpy(), ref.cpu().numpy()) < 1e-6, K
+
+
+# ------------------------------------------------------------------ packed TF32 rows
+def unpack_host(buf, rows, F):
+    """Independent host reading of the packed layout (include/tcc_spmm_cnic.h):
+    per row 2F bytes of high halves, then the 3 low mantissa bits of element
+    pairs, rows padded to 16 bytes."""
+    stride = (2 * F + (F + 1) // 2 + 15) // 16 * 16
+    b = np.asarray(buf, np.uint8)[: rows * stride].reshape(rows, stride)
+    hi = b[:, : 2 * F].copy().view(np.uint16).astype(np.uint32)
+    lo_bytes = b[:, 2 * F: 2 * F + (F + 1) // 2].astype(np.uint32)
+    lo = np.empty((rows, F), np.uint32)
+    lo[:, 0::2] = lo_bytes[:, : (F + 1) // 2] & 7
+    lo[:, 1::2] = (lo_bytes[:, : F // 2] >> 3) & 7
+    return ((hi << 16) | (lo << 13)).astype(np.uint32)
+
+
+@pytest.mark.parametrize("F", [1, 2, 3, 7, 100, 128, 602])
+def test_tf32_pack_is_exact(gpu, oracle, F):
+    from tcc_amd import swtcf
+
+    rows = 37
+    rng = np.random.default_rng(F)
+    with np.errstate(over="ignore"):
+        X = (rng.standard_normal((rows, F)) * 10.0 ** rng.integers(-30, 30, (rows, F))).astype(np.float32)
+    special = np.array([0x3F801000, 0xBF801000, 0x3F800FFF, 0x3F7FF000, 0x7F7FF000, 0x00001000, 0x80000000,
+                        0x00000000, 0x7F800000, 0xFF800000], np.uint32).view(np.float32)
+    flat = X.reshape(-1)
+    flat[: min(special.size, flat.size)] = special[: flat.size]
+    packed = swtcf.tf32_pack(torch.from_numpy(X).cuda())
+    got = unpack_host(packed.cpu().numpy(), rows, F)
+    want = oracle.tf32(X).view(np.uint32)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("unit_blocks", [0, 3])
+@pytest.mark.parametrize("F", [1, 2, 64, 100, 128, 256, 602])
+def test_bcsr_spmm_packed(gpu, oracle, unit_blocks, F):
+    """The gather over packed rows gives the oracle's TF32 product (= and +=)."""
+    from tcc_amd import swtcf
+
+    nr, nc = 640, 900
+    dst, src = skewed_coo(nr, nc, 60 + F)
+    vals = np.random.default_rng(61).uniform(-1, 1, dst.size).astype(np.float32)
+    X = np.random.default_rng(62).standard_normal((nc, F)).astype(np.float32)
+    rowptr, colind, v = csr_of(dst, src, nr, vals)
+    want = oracle.csr_spmm(rowptr, colind, v, X, use_tf32=True)
+    A = swtcf.coo_to_bcsr(dev_u32(dst), dev_u32(src), torch.from_numpy(vals).cuda(), nr, nc)
+    A.set_unit_blocks(unit_blocks)
+    packed = swtcf.tf32_pack(torch.from_numpy(X).cuda())
+    Y = swtcf.bcsr_spmm_packed(A, packed, F, torch.full((A.view.num_rowWindows * 8, F), 7.0, device="cuda"))
+    assert_close(Y.cpu().numpy()[:nr], want)
+    Y2 = swtcf.bcsr_spmm_packed(A, packed, F, Y.clone(), accumulate=True)
+    assert_close(Y2.cpu().numpy()[:nr], 2 * want)
