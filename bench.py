@@ -342,8 +342,8 @@ def bench_gcn(args, torch, swtcf, cfg):
     l2 = timed(layer2, steps, warmup)
     extra = {"layer1_fwd_bwd_ms": round(l1, 4), "layer2_fwd_bwd_ms": round(l2, 4),
              "layer1": f"mixed SpMM F={F} (hot BCSR + cold BCSC) + GEMM {F}x{hidden}; backward dW GEMM",
-             "layer2": f"BCSR SpMM F={hidden} + GEMM {hidden}x{classes}; backward dW GEMM, A^T SpMM F={classes}, "
-                       f"GEMM {classes}x{hidden}",
+             "layer2": f"A(XW): GEMM {hidden}x{classes}, BCSR SpMM F={classes}; backward A^T SpMM F={classes}, "
+                       f"dW and dX GEMMs",
              "loss_first": first_loss, "loss_last": last_loss}
     config = {"workload": WORKLOADS[5], "n": n, "nnz": nnz, "F": F, "hidden": hidden, "classes": classes}
     table.free()

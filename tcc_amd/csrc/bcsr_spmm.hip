@@ -522,17 +522,41 @@ struct ScatterArgs {
     MixedArgs mixed;
 };
 
-// The 8 source rows of window w, TF32-rounded (zeros past numCols); all
-// loads are issued before any is rounded.
+// The source columns of a column window that blocks [lo, hi) use: the OR
+// over those blocks of their bitmaps' row bytes (one vector load per 64
+// blocks, 8 ballots).
+__device__ __forceinline__ std::uint32_t used_columns(const std::uint64_t* bits, std::uint32_t lo, std::uint32_t hi) {
+    std::uint32_t mask = 0;
+    for (std::uint32_t base = lo; base < hi && mask != 0xFFu; base += kWave) {
+        const std::uint32_t b = base + __lane_id();
+        std::uint32_t cols = 0;
+        if (b < hi) {
+            std::uint64_t bm = bits[b];
+            bm |= bm >> 32;
+            bm |= bm >> 16;
+            bm |= bm >> 8;
+            cols = static_cast<std::uint32_t>(bm) & 0xFFu;
+        }
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+            if (__ballot((cols >> c) & 1u)) mask |= 1u << c;
+    }
+    return mask;
+}
+
+// The source rows of window w that `used` names, TF32-rounded (zeros for
+// the others and past numCols); all loads are issued before any is rounded.
+// Skipping unused rows matters most for the first layer's cold rows, which
+// cross the host link.
 template <int V, bool MIXED>
-__device__ __forceinline__ void load_window_rows(const ScatterArgs& a, std::uint32_t w, std::uint32_t laneOff,
-                                                 float (&x)[8][V]) {
+__device__ __forceinline__ void load_window_rows(const ScatterArgs& a, std::uint32_t w, std::uint32_t used,
+                                                 std::uint32_t laneOff, float (&x)[8][V]) {
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
         const std::uint32_t col = w * 8 + c;
 #pragma unroll
         for (int v = 0; v < V; ++v) x[c][v] = 0.0f;
-        if (col < a.numCols) {
+        if (((used >> c) & 1u) && col < a.numCols) {
             const float* row;
             if constexpr (MIXED) {
                 // spmm_kernel.cu:521-595: the window's sources resolved once each.
@@ -573,14 +597,14 @@ __global__ void __launch_bounds__(kThreads) scatter_kernel(ScatterArgs a) {
         we = a.winOffset[w + 1];
     }
     float x[8][V];
-    load_window_rows<V, MIXED>(a, w, laneOff, x);
+    load_window_rows<V, MIXED>(a, w, used_columns(a.bits, u.b0, min(we, u.b1)), laneOff, x);
     for (std::uint32_t b = u.b0; b < u.b1; ++b) {
         if (b >= we) {
             do {
                 ++w;
                 we = a.winOffset[w + 1];
             } while (b >= we && w + 1 < a.numWindows);
-            load_window_rows<V, MIXED>(a, w, laneOff, x);
+            load_window_rows<V, MIXED>(a, w, used_columns(a.bits, b, min(we, u.b1)), laneOff, x);
         }
         const std::uint64_t bm = a.bits[b];
         float vals = 0.0f;

@@ -12,6 +12,12 @@ is the block-sparse transposed gather over a BCSC of the whole A
 needs a gradient (the reference computes and discards it for the first
 layer, whose input is the feature table).
 
+A later layer whose output is narrower than its input (the last layer:
+256 -> 2 classes) is evaluated as A·(X·W) instead of (A·X)·W — the same
+product in exact arithmetic, with the SpMM at the output width and the
+backward G = Aᵀ·dY, dW = Xᵀ·G, dX = G·Wᵀ (the aggregate-then-transform order
+of :133-134 would gather 256-wide rows for a 2-wide result).
+
 The first layer reads X through the hot/cold feature source of
 spmm_kernel.cu:129-153: edges whose source row is hot (in the HBM feature
 cache) go to the BCSR gather, edges with cold sources to the BCSC scatter,
@@ -117,6 +123,30 @@ class CNICSPMMFunction(torch.autograd.Function):
         return None, None, grad_x, grad_weights
 
 
+class TransformFirstFunction(torch.autograd.Function):
+    """out = A (X W), the same product as (A X) W associated the other way,
+    for layers whose output is narrower than their input: the SpMM then runs
+    at the output width (2 instead of 256 for the GCN's last layer).
+    Backward: G = Aᵀ dY (needed for dX in either order), dW = Xᵀ G,
+    dX = G Wᵀ — AX is never formed."""
+
+    @staticmethod
+    def forward(ctx, graph: LayerGraph, x, weights):
+        xw = torch.mm(x, weights).contiguous()
+        out = graph.aggregate(weights.shape[1], x=xw)
+        ctx.graph = graph
+        ctx.save_for_backward(x, weights)
+        return out
+
+    @staticmethod
+    def backward(ctx, d_output):
+        x, weights = ctx.saved_tensors
+        grad_sp = ctx.graph.transpose_aggregate(d_output)
+        grad_weights = torch.mm(x.t(), grad_sp)
+        grad_x = torch.mm(grad_sp, weights.t()) if ctx.needs_input_grad[1] else None
+        return None, grad_x, grad_weights
+
+
 class GCNConv(torch.nn.Module):
     def __init__(self, input_dim: int, output_dim: int, first_layer: bool = False):
         super().__init__()
@@ -125,6 +155,10 @@ class GCNConv(torch.nn.Module):
         torch.nn.init.xavier_uniform_(self.weights)
 
     def forward(self, graph: LayerGraph, source=None, x: torch.Tensor | None = None) -> torch.Tensor:
+        in_dim, out_dim = self.weights.shape
+        if not self.first_layer and out_dim < in_dim:
+            # A(XW) = (AX)W: aggregate at the narrower width
+            return TransformFirstFunction.apply(graph, x, self.weights)
         return CNICSPMMFunction.apply(graph, source if self.first_layer else None, x, self.weights)
 
 

@@ -23,12 +23,18 @@ def tf32(a):
     return r.view(np.float32).astype(np.float64)
 
 
-def reference_step(A, X, W1, W2, labels):
+def reference_step(A, X, W1, W2, labels, last_transform_first=True):
+    """Forward/backward of the two-layer GCN in float64 with the kernels'
+    rounding: TF32 operands into forward SpMMs, fp32 into the A^T product.
+    The last layer (256 -> classes) runs A·(R·W2) as tcc_amd.gcn does, or
+    (A·R)·W2 as the reference does (tcgnn_conv_release.py:133-134)."""
     AX1 = A @ tf32(X)
     H1 = AX1 @ W1
     R = np.maximum(H1, 0.0)
-    AX2 = A @ tf32(R.astype(np.float32))
-    out = AX2 @ W2
+    if last_transform_first:
+        out = A @ tf32((R @ W2).astype(np.float32))
+    else:
+        out = (A @ tf32(R.astype(np.float32))) @ W2
     m = out.max(axis=1, keepdims=True)
     logp = out - m - np.log(np.exp(out - m).sum(axis=1, keepdims=True))
     p = np.exp(logp)
@@ -37,8 +43,8 @@ def reference_step(A, X, W1, W2, labels):
     dout = p.copy()
     dout[np.arange(n), labels] -= 1.0
     dout /= n
-    dW2 = AX2.T @ dout
     G2 = A.T @ dout.astype(np.float32).astype(np.float64)
+    dW2 = R.T @ G2  # = (A R)^T dout
     dR = G2 @ W2.T
     dH1 = dR * (H1 > 0)
     dW1 = AX1.T @ dH1
@@ -72,6 +78,11 @@ def test_gcn_step_matches_dense_reference(gpu, hot_fraction):
     assert abs(loss.item() - ref_loss) < REL * abs(ref_loss)
     assert rel_l2(model.conv1.weights.grad.cpu().numpy(), dW1) < REL
     assert rel_l2(model.conv_final.weights.grad.cpu().numpy(), dW2) < REL
+    # the reference's association order agrees to the north_star tolerance
+    out_r, loss_r, dW1_r, dW2_r = reference_step(A, X.numpy(), W1, W2, labels.cpu().numpy(), False)
+    assert rel_l2(pred.detach().cpu().numpy(), out_r) < 1e-3
+    assert rel_l2(model.conv1.weights.grad.cpu().numpy(), dW1_r) < 1e-3
+    assert rel_l2(model.conv_final.weights.grad.cpu().numpy(), dW2_r) < 1e-3
     table.free()
 
 
