@@ -93,9 +93,31 @@ def build_extension() -> str:
     return out
 
 
+CLI_SOURCES = ["swtcf_convert_run.cpp", "swtcf_spmm_run.cpp"]
+
+
+def build_cli() -> list:
+    """The command-line drivers (tcc_amd/bin/swtcf_convert_run, swtcf_spmm_run):
+    host C++ over include/tcc_swtcf.hpp, linked against libtcc_swtcf.so."""
+    bindir = os.path.join(PKG, "bin")
+    os.makedirs(bindir, exist_ok=True)
+    outs = []
+    for src in CLI_SOURCES:
+        out = os.path.join(bindir, os.path.splitext(src)[0])
+        tmp = out + ".tmp"
+        _run(["g++", "-O2", "-std=c++17", "-Wall", "-D__HIP_PLATFORM_AMD__=1", f"-I{os.path.join(ROOT, 'include')}",
+              "-I/opt/rocm/include", os.path.join(PKG, "cli", src), "-o", tmp, f"-L{PKG}", "-ltcc_swtcf",
+              "-Wl,-rpath,$ORIGIN/..", "-L/opt/rocm/lib", "-lamdhip64", "-Wl,-rpath,/opt/rocm/lib"])
+        os.replace(tmp, out)
+        outs.append(out)
+    return outs
+
+
 def main(argv=None) -> int:
     argv = sys.argv[1:] if argv is None else argv
     print("building", build_library(), flush=True)
+    for out in build_cli():
+        print("building", out, flush=True)
     if "--no-ext" not in argv:
         print("building", build_extension(), flush=True)
     return 0
