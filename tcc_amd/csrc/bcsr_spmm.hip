@@ -481,6 +481,217 @@ __global__ void __launch_bounds__(kThreads) zero_shared_windows_kernel(const std
     for (std::uint32_t i = __lane_id(); i < 8u * F; i += kWave) p[i] = 0.0f;
 }
 
+// ------------------------------------------------------------ narrow gather
+// Gather for F <= 16 (the GCN's class-width products A(XW) and A^T dY).  One
+// wave per 64*V features would leave all but F lanes idle and pay a memory
+// round trip per block; here a wave takes 8 blocks per step instead.  Lane
+// 8k+j loads column j of block k (its input row, F features) and computes
+// output row j of block k from the 8 column values of block k, exchanged
+// within the 8-lane group with ds_swizzle.  Window sums stay in registers
+// per (block slot, row) and are reduced across the 8 slots when the window
+// ends.  Metadata is fetched two groups ahead and input rows one group
+// ahead.  Y is zero-filled first (or accumulated into), so empty windows
+// need no work and shared windows take atomics without a zeroing pass.
+
+// Column j of block g+k (lane 8k+j) and block g+k's bitmap / value offset.
+struct NarrowMeta {
+    std::uint32_t in;  // >= numIn: padding or past the unit
+    std::uint32_t bitsLo, bitsHi;
+    std::uint32_t off;
+};
+
+template <bool VALUES>
+__device__ __forceinline__ NarrowMeta narrow_meta(const GatherArgs& a, std::uint32_t g, std::uint32_t end) {
+    const unsigned lane = __lane_id();
+    const std::uint32_t b = g + (lane >> 3);
+    NarrowMeta m{0xFFFFFFFFu, 0u, 0u, 0u};
+    if (b < end) {
+        m.in = a.idx[static_cast<std::uint64_t>(b) * 8 + (lane & 7u)];
+        const std::uint64_t raw = a.bits[b];
+        m.bitsLo = static_cast<std::uint32_t>(raw);
+        m.bitsHi = static_cast<std::uint32_t>(raw >> 32);
+        if constexpr (VALUES) m.off = a.tcOffset[b];
+    }
+    return m;
+}
+
+// Input row `in` (FT >= F features, zeros past F and for a missing row),
+// with V-wide loads when F == FT and X is aligned for them (`vec`).
+template <int FT, Src MODE>
+__device__ __forceinline__ void narrow_row(const GatherArgs& a, std::uint32_t in, bool vec, float (&x)[FT]) {
+#pragma unroll
+    for (int f = 0; f < FT; ++f) x[f] = 0.0f;
+    if (in >= a.numIn) return;
+    const float* row = a.X + static_cast<std::uint64_t>(in) * a.F;
+    if (vec) {
+        constexpr int V = FT < 4 ? FT : 4;
+#pragma unroll
+        for (int f = 0; f < FT; f += V) {
+            const Vec<V> t = load_vec<V>(row + f);
+#pragma unroll
+            for (int v = 0; v < V; ++v) x[f + v] = t.v[v];
+        }
+    } else {
+#pragma unroll
+        for (int f = 0; f < FT; ++f)
+            if (static_cast<std::uint32_t>(f) < a.F) x[f] = row[f];
+    }
+}
+
+// p += w(j, C) * x(column C of this lane's block), for C = 0..7: the column
+// values come from lane (lane & ~7) | C (ds_swizzle bit mode inside each
+// 32-lane half: and-mask 0x18 keeps the block slot, or-mask C picks the lane).
+template <int C, int FT, bool VALUES>
+__device__ __forceinline__ void narrow_columns(const float (&x)[FT], std::uint32_t rb, const float (&wv)[8],
+                                               float (&p)[FT]) {
+    float xc[FT];
+#pragma unroll
+    for (int f = 0; f < FT; ++f) xc[f] = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x[f]), 0x18 | (C << 5)));
+    if ((rb >> C) & 1u) {
+#pragma unroll
+        for (int f = 0; f < FT; ++f) p[f] = VALUES ? fmaf(wv[C], xc[f], p[f]) : p[f] + xc[f];
+    }
+    if constexpr (C < 7) narrow_columns<C + 1, FT, VALUES>(x, rb, wv, p);
+}
+
+template <int FT, Src MODE, bool VALUES>
+__global__ void __launch_bounds__(kThreads) narrow_gather_kernel(GatherArgs a) {
+    const unsigned lane = __lane_id();
+    const unsigned slot = lane >> 3, j = lane & 7u;
+    const std::uint32_t unit = blockIdx.x * kWaves + uniform(threadIdx.x / kWave);
+    if (unit >= a.numUnits) return;
+    const UnitRange u = unit_range(a.winOffset, a.numWindows, a.numBlocks, a.unitBlocks, a.numUnits, unit);
+    if (u.b0 >= u.b1 || u.w >= a.numWindows) return;
+    constexpr int VA = FT < 4 ? FT : 4;
+    const bool vec = a.F == FT && (reinterpret_cast<std::uintptr_t>(a.X) % (4u * VA)) == 0;
+
+    // Window ends one vector load at a time: lane i holds winOffset[cbase+1+i]
+    // (all ones past the last window), cstart = winOffset[cbase].
+    std::uint32_t cbase = u.w, cstart = a.winOffset[u.w];
+    auto load_ends = [&]() {
+        const std::uint32_t i = cbase + 1 + lane;
+        return i <= a.numWindows ? a.winOffset[i] : 0xFFFFFFFFu;
+    };
+    std::uint32_t ends = load_ends();
+    std::uint32_t w = 0, ws = 0, we = 0;
+    // The window holding block b (empty windows skipped); false when the
+    // offsets end before b (inconsistent with the block count).
+    auto seek = [&](std::uint32_t b) {
+        for (;;) {
+            const unsigned cnt = static_cast<unsigned>(__popcll(__ballot(ends <= b)));
+            if (cnt < kWave) {
+                w = cbase + cnt;
+                we = lane_u32(ends, cnt);
+                ws = cnt ? lane_u32(ends, cnt - 1) : cstart;
+                return w < a.numWindows;
+            }
+            cstart = lane_u32(ends, kWave - 1);
+            cbase += kWave;
+            ends = load_ends();
+        }
+    };
+    if (!seek(u.b0)) return;
+
+    float acc[FT];
+#pragma unroll
+    for (int f = 0; f < FT; ++f) acc[f] = 0.0f;
+    bool touched = false;
+    bool open = false;  // blocks of window w accumulated since the last flush
+
+    auto flush = [&]() {
+        float s[FT];
+#pragma unroll
+        for (int f = 0; f < FT; ++f) {
+            s[f] = acc[f];
+            s[f] += __shfl_xor(s[f], 8);
+            s[f] += __shfl_xor(s[f], 16);
+            s[f] += __shfl_xor(s[f], 32);
+            acc[f] = 0.0f;
+        }
+        const std::uint64_t tm = __ballot(touched);
+        touched = false;
+        open = false;
+        if (lane < 8) {
+            float* o = a.Y + (static_cast<std::uint64_t>(w) * 8 + j) * a.F;
+            if (ws < u.b0 || we > u.b1) {  // shared with another unit
+                if ((tm >> j) & 0x0101010101010101ull) {
+#pragma unroll
+                    for (int f = 0; f < FT; ++f)
+                        if (static_cast<std::uint32_t>(f) < a.F) atomic_add_f32(o + f, s[f]);
+                }
+            } else {
+#pragma unroll
+                for (int f = 0; f < FT; ++f)
+                    if (static_cast<std::uint32_t>(f) < a.F) o[f] = a.accumulate ? o[f] + s[f] : s[f];
+            }
+        }
+    };
+
+    NarrowMeta m0 = narrow_meta<VALUES>(a, u.b0, u.b1);
+    NarrowMeta m1 = narrow_meta<VALUES>(a, u.b0 + 8, u.b1);
+    float x0[FT];
+    narrow_row<FT, MODE>(a, m0.in, vec, x0);
+    for (std::uint32_t g = u.b0; g < u.b1; g += 8) {
+        const NarrowMeta m2 = narrow_meta<VALUES>(a, g + 16, u.b1);
+        float x1[FT];
+        narrow_row<FT, MODE>(a, m1.in, vec, x1);
+
+        // Output row j of block g+slot.
+        const std::uint64_t raw = (static_cast<std::uint64_t>(m0.bitsHi) << 32) | m0.bitsLo;
+        const std::uint64_t bm = (MODE == Src::Transposed) ? transpose8x8(raw) : raw;
+        const std::uint32_t rb = static_cast<std::uint32_t>(bm >> (8 * j)) & 0xFFu;
+        float wv[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            wv[c] = 0.0f;
+            if constexpr (VALUES) {
+                if ((rb >> c) & 1u) {
+                    const unsigned stored = (MODE == Src::Transposed) ? (c * 8 + j) : (j * 8 + c);
+                    const unsigned rank = static_cast<unsigned>(__popcll(raw & ((1ull << stored) - 1ull)));
+                    wv[c] = a.data[m0.off + rank];
+                }
+            }
+        }
+        float x[FT];
+#pragma unroll
+        for (int f = 0; f < FT; ++f) x[f] = (MODE == Src::Transposed) ? x0[f] : tf32_rna(x0[f]);
+        if constexpr (VALUES && MODE != Src::Transposed) {
+#pragma unroll
+            for (int c = 0; c < 8; ++c) wv[c] = tf32_rna(wv[c]);
+        }
+        float p[FT];
+#pragma unroll
+        for (int f = 0; f < FT; ++f) p[f] = 0.0f;
+        narrow_columns<0, FT, VALUES>(x, rb, wv, p);
+
+        // Hand the 8 blocks to their windows (usually one).
+        const std::uint32_t n = min(8u, u.b1 - g);
+        std::uint32_t kk = 0;
+        for (;;) {
+            const std::uint32_t kend = min(n, we - g);
+            if (kend > kk) {
+                open = true;
+                if (slot >= kk && slot < kend) {
+#pragma unroll
+                    for (int f = 0; f < FT; ++f) acc[f] += p[f];
+                    touched |= rb != 0;
+                }
+            }
+            if (we > g + n) break;  // window w continues past this group
+            flush();
+            if (g + kend >= u.b1) break;  // the unit ends with window w
+            if (!seek(g + kend)) return;
+            kk = kend;
+            if (kk >= n) break;
+        }
+        m0 = m1;
+        m1 = m2;
+#pragma unroll
+        for (int f = 0; f < FT; ++f) x0[f] = x1[f];
+    }
+    if (open) flush();
+}
+
 // X [rows x F] fp32 -> packed TF32 rows (layout at packed_stride).  One
 // thread per element pair.
 __global__ void tf32_pack_kernel(const float* __restrict__ X, std::uint32_t rows, std::uint32_t F,
@@ -713,6 +924,44 @@ int launch_gather(GatherArgs a, int V, std::uint32_t requestedK, hipStream_t st)
     return TCC_OK;
 }
 
+// Feature widths the narrow gather takes (one wave per 8 blocks).
+constexpr std::uint32_t kNarrowMaxF = 16;
+
+// Blocks per unit of the narrow gather: `requested` if nonzero, else about
+// four units per wave slot (a unit's 8-block steps are short, so waves are
+// plentiful), a power of two in [64, 4096].
+inline std::uint32_t narrow_unit_blocks(std::uint32_t requested, std::uint32_t blocks) {
+    if (requested != 0) return requested;
+    const std::uint64_t units = static_cast<std::uint64_t>(device_cus()) * 32 * 4;
+    std::uint32_t K = 64;
+    while (K < 4096 && static_cast<std::uint64_t>(K) * units < blocks) K *= 2;
+    return K;
+}
+
+template <int FT, Src MODE>
+void narrow_dispatch(const GatherArgs& a, dim3 grid, hipStream_t st) {
+    if (a.data != nullptr) hipLaunchKernelGGL((narrow_gather_kernel<FT, MODE, true>), grid, dim3(kThreads), 0, st, a);
+    else hipLaunchKernelGGL((narrow_gather_kernel<FT, MODE, false>), grid, dim3(kThreads), 0, st, a);
+}
+
+template <Src MODE>
+int launch_narrow(GatherArgs a, std::uint32_t requestedK, hipStream_t st) {
+    static_assert(MODE == Src::Plain || MODE == Src::Transposed, "narrow gather reads X or dY");
+    if (a.numWindows == 0) return TCC_OK;
+    if (!a.accumulate) TCC_HIP_CHECK(fill<float>(a.Y, static_cast<std::uint64_t>(a.numWindows) * 8 * a.F, 0.0f, st));
+    if (a.numBlocks == 0) return TCC_OK;
+    a.numChunks = 1;
+    a.unitBlocks = narrow_unit_blocks(requestedK, a.numBlocks);
+    a.numUnits = (a.numBlocks + a.unitBlocks - 1) / a.unitBlocks;
+    const dim3 grid(grid_for(a.numUnits, kWaves));
+    if (a.F <= 2) narrow_dispatch<2, MODE>(a, grid, st);
+    else if (a.F <= 4) narrow_dispatch<4, MODE>(a, grid, st);
+    else if (a.F <= 8) narrow_dispatch<8, MODE>(a, grid, st);
+    else narrow_dispatch<16, MODE>(a, grid, st);
+    TCC_LAUNCH_CHECK();
+    return TCC_OK;
+}
+
 template <bool MIXED>
 int launch_scatter(ScatterArgs a, int V, std::uint32_t requestedK, hipStream_t st) {
     if (a.numWindows == 0 || a.numBlocks == 0) return TCC_OK;
@@ -802,6 +1051,8 @@ int tcc_bcsr_spmm(const tcc_bcsr* A, const float* X, float* Y, std::uint32_t fea
                   void* stream) {
     clear_last_error();
     TCC_REQUIRE(bcsr_ok(A) && X && Y && featureDim >= 1, TCC_ERR_INVALID_ARGUMENT, "invalid BCSR SpMM arguments");
+    if (featureDim <= kNarrowMaxF)
+        return launch_narrow<Src::Plain>(bcsr_args(A, X, Y, featureDim, accumulate), A->unitBlocks, as_stream(stream));
     const int V = pick_vec(featureDim, {X, Y});
     return launch_gather<Src::Plain>(bcsr_args(A, X, Y, featureDim, accumulate), V, A->unitBlocks,
                                      as_stream(stream));
@@ -879,6 +1130,7 @@ int tcc_bcsc_transpose_spmm(const tcc_bcsc* A, const float* dY, float* dX, std::
     a.numIn = A->num_rows;
     a.F = featureDim;
     a.accumulate = accumulate;
+    if (featureDim <= kNarrowMaxF) return launch_narrow<Src::Transposed>(a, A->unitBlocks, as_stream(stream));
     const int V = pick_vec(featureDim, {dY, dX});
     return launch_gather<Src::Transposed>(a, V, A->unitBlocks, as_stream(stream));
 }
