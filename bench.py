@@ -313,7 +313,7 @@ def bench_gcn(args, torch, swtcf, cfg):
     model = gcn.GCN(F, hidden, classes, dropout=0.0).cuda()
     labels = gcn.synthetic_labels(n, classes, cfg["seed"])
     opt = torch.optim.Adam(model.parameters(), lr=0.003)
-    loss_fcn = torch.nn.CrossEntropyLoss()
+    loss_fcn = gcn.cross_entropy
     losses = []
 
     def epoch():

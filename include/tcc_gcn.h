@@ -1,0 +1,47 @@
+/*
+ * tcc_gcn.h — C-ABI of the dense products of the GCN layer backward on
+ * MI355X (gfx950), beside the block-sparse SpMM of tcc_spmm_cnic.h.
+ *
+ * The weight gradient of a GCN layer is a tall-skinny transposed product
+ * over all graph nodes:
+ *   grad_weights = torch.mm(X_out.T, d_output)
+ *     (TAC_training_backend/train/tcgnn_conv_release.py:150: X_out [n x F_in]
+ *      is the aggregated input A·X, d_output [n x F_out])
+ * and, for a layer evaluated as A·(X·W), grad_weights = X^T (A^T dY).  With n
+ * in the millions and F in the hundreds, library GEMMs leave most of the
+ * GPU idle on this shape; tcc_dense_tn splits the n rows over workgroups,
+ * each accumulating its rows' product for a whole block of C with fp32
+ * MFMA, and sums the partial products in a fixed order (deterministic).
+ * Products and sums are fp32 (no TF32 rounding), as torch.mm in fp32.
+ *
+ * Errors as in tcc_swtcf.h: 0 or a TCC_ERR_* code, text in tcc_last_error().
+ */
+#ifndef TCC_GCN_H
+#define TCC_GCN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Bytes of device workspace tcc_dense_tn needs for these sizes on the
+ * current device (the split of K depends on its compute-unit count). */
+size_t tcc_dense_tn_workspace_bytes(uint32_t K, uint32_t M, uint32_t N);
+
+/* C[M x N] = A^T B (accumulate = 0) or C += A^T B (accumulate != 0), for
+ * row-major A [K x M] with row stride lda >= M, B [K x N] with ldb >= N and
+ * C with ldc >= N (strides in elements, below 2^28).  fp32 device pointers,
+ * 4-byte aligned; `workspace` is device memory of at least
+ * tcc_dense_tn_workspace_bytes(K, M, N) bytes, not shared with a concurrent
+ * call.  Asynchronous on `stream` (a hipStream_t; NULL = the null stream).
+ * Replaces torch.mm(X_out.T, d_output), tcgnn_conv_release.py:150. */
+int tcc_dense_tn(const float* A, uint32_t lda, const float* B, uint32_t ldb, float* C, uint32_t ldc, uint32_t K,
+                 uint32_t M, uint32_t N, int accumulate, void* workspace, size_t workspaceBytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TCC_GCN_H */

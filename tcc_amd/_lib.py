@@ -87,6 +87,8 @@ SIGNATURES = {
     "tcc_tf32_packed_bytes": (ctypes.c_size_t, [u32, u32]),
     "tcc_tf32_pack": (ctypes.c_int, [vp, u32, u32, vp, vp]),
     "tcc_bcsr_spmm_packed": (ctypes.c_int, [ctypes.POINTER(BCSR), vp, vp, u32, ctypes.c_int, vp]),
+    "tcc_dense_tn_workspace_bytes": (ctypes.c_size_t, [u32, u32, u32]),
+    "tcc_dense_tn": (ctypes.c_int, [vp, u32, vp, u32, vp, u32, u32, u32, u32, ctypes.c_int, vp, ctypes.c_size_t, vp]),
 }
 
 _lib = None

@@ -871,19 +871,6 @@ inline int pick_vec(std::uint32_t F, std::initializer_list<const void*> ptrs) {
     return 1;
 }
 
-// Compute units of the current device (cached per device).
-inline std::uint32_t device_cus() {
-    static std::uint32_t cache[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cache[dev] == 0) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cache[dev] = static_cast<std::uint32_t>(n);
-    }
-    return cache[dev];
-}
-
 // Blocks per unit: `requested` if nonzero, else about one wave of work per
 // wave slot of the device (32 per CU): fewer, longer units pay the per-wave
 // start (window search, first metadata group) less often, while more units

@@ -42,6 +42,19 @@ inline unsigned grid_for(std::uint64_t n, unsigned threads) {
     return static_cast<unsigned>((n + threads - 1) / threads);
 }
 
+// Compute units of the current device (cached per device).
+inline std::uint32_t device_cus() {
+    static std::uint32_t cache[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cache[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cache[dev] = static_cast<std::uint32_t>(n);
+    }
+    return cache[dev];
+}
+
 // ---------------------------------------------------------------- numerics
 // cvt.rna.tf32.f32 restated from its definition: round to nearest with ties
 // away from zero, keeping 10 explicit mantissa bits; inf and NaN unchanged.

@@ -1,0 +1,287 @@
+// Tall-skinny transposed products C = A^T B of the GCN layer backward, for
+// gfx950 (reference: torch.mm(X_out.T, d_output),
+// TAC_training_backend/train/tcgnn_conv_release.py:150).
+//
+// A [K x M] and B [K x N] are row-major with K = graph nodes (millions) and
+// M, N = layer widths (hundreds or less).  K is split over workgroups; each
+// accumulates the product of its rows for one block of C with
+// v_mfma_f32_16x16x4f32 (fp32 products and sums) and writes it to a partial
+// buffer, and a second kernel sums the partials in a fixed order.
+//
+// MFMA operand layout (16x16x4, fp32): lane l supplies A(i = l%16, k = l/16)
+// and B(k = l/16, j = l%16), and holds D(4*(l/16) + v, l%16) in accumulator
+// register v.  For C = A^T B the A operand of a 16x16 tile at (m0, n0) and
+// rows k..k+3 is A[k + l/16][m0 + l%16] and the B operand B[k + l/16][n0 + l%16]:
+// both are 16 consecutive floats of one input row per lane quarter, so the
+// operands are loaded straight from global memory without a transpose.
+// Columns past M (N) are clamped to the last one: they only feed rows
+// (columns) of C that are never stored.  Rows past K are zero.
+#include <algorithm>
+
+#include "../../include/tcc_gcn.h"
+#include "../../include/tcc_swtcf.h"
+#include "common.hpp"
+#include "primitives.hpp"
+
+namespace tcc {
+namespace {
+
+constexpr unsigned kTnThreads = 512;  // 8 waves
+constexpr unsigned kTnWaves = kTnThreads / kWave;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct TnArgs {
+    const float* A;
+    const float* B;
+    float* partial;  // [splits][M][N]
+    std::uint32_t lda, ldb;
+    std::uint32_t K, M, N;
+    std::uint32_t rowsPerSplit;
+    std::uint32_t blocksM;  // blocks of C along M
+};
+
+__device__ __forceinline__ std::uint32_t tn_uniform(std::uint32_t v) {
+    return static_cast<std::uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v)));
+}
+
+// Workgroup = WM x WN waves; a wave owns TM x TN tiles of 16x16, so a
+// workgroup covers a (16*TM*WM) x (16*TN*WN) block of C.  Each iteration
+// takes U steps of 4 rows; the next iteration's operands are loaded while
+// the current one is multiplied.
+template <int TM, int TN, int WM, int WN, int U>
+__global__ void __launch_bounds__(kTnThreads) tn_partial_kernel(TnArgs a) {
+    static_assert(WM * WN == static_cast<int>(kTnWaves), "8 waves per workgroup");
+    constexpr int BM = 16 * TM * WM, BN = 16 * TN * WN;
+    constexpr std::uint32_t kStep = 4 * U;
+    const unsigned lane = __lane_id();
+    const unsigned wave = tn_uniform(threadIdx.x / kWave);
+    const unsigned wm = wave % WM, wn = wave / WM;
+    const std::uint32_t cbm = blockIdx.y % a.blocksM, cbn = blockIdx.y / a.blocksM;
+    const std::uint32_t m0 = cbm * BM + wm * 16 * TM, n0 = cbn * BN + wn * 16 * TN;
+    const std::uint32_t k0 = blockIdx.x * a.rowsPerSplit;
+    const std::uint32_t k1 = min(a.K, k0 + a.rowsPerSplit);
+    const unsigned li = lane & 15u, lk = lane >> 4;
+
+    // Per-lane element offsets inside a 4-row step (row lk, clamped column).
+    std::uint32_t offA[TM], offB[TN];
+#pragma unroll
+    for (int t = 0; t < TM; ++t) offA[t] = lk * a.lda + min(m0 + 16 * t + li, a.M - 1);
+#pragma unroll
+    for (int t = 0; t < TN; ++t) offB[t] = lk * a.ldb + min(n0 + 16 * t + li, a.N - 1);
+
+    f32x4 acc[TM][TN];
+#pragma unroll
+    for (int t = 0; t < TM; ++t)
+#pragma unroll
+        for (int u = 0; u < TN; ++u) acc[t][u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto load_full = [&](std::uint32_t k, float (&xa)[U][TM], float (&xb)[U][TN]) {
+#pragma unroll
+        for (int s = 0; s < U; ++s) {
+            const float* ra = a.A + static_cast<std::uint64_t>(k + 4 * s) * a.lda;
+            const float* rb = a.B + static_cast<std::uint64_t>(k + 4 * s) * a.ldb;
+#pragma unroll
+            for (int t = 0; t < TM; ++t) xa[s][t] = ra[offA[t]];
+#pragma unroll
+            for (int t = 0; t < TN; ++t) xb[s][t] = rb[offB[t]];
+        }
+    };
+    auto multiply = [&](const float (&xa)[U][TM], const float (&xb)[U][TN]) {
+#pragma unroll
+        for (int s = 0; s < U; ++s)
+#pragma unroll
+            for (int t = 0; t < TM; ++t)
+#pragma unroll
+                for (int u = 0; u < TN; ++u)
+                    acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[s][t], xb[s][u], acc[t][u], 0, 0, 0);
+    };
+
+    // Two operand buffers in turn; loads are unconditional (past the last
+    // full iteration they repeat in-bounds rows and are not used), so the
+    // loads of one buffer stay in flight while the other is multiplied.
+    const std::uint32_t rows = k1 > k0 ? k1 - k0 : 0u;
+    const std::uint32_t nFull = rows / kStep;
+    float ca[U][TM], cb[U][TN], na[U][TM], nb[U][TN];
+    if (nFull > 0) load_full(k0, ca, cb);
+    std::uint32_t i = 0;
+    // (sched_barrier keeps the scheduler from sinking the loads to their
+    // uses, which it does to lower register pressure.)
+    for (; i + 1 < nFull; i += 2) {
+        const std::uint32_t k = k0 + i * kStep;
+        load_full(k + kStep, na, nb);
+        __builtin_amdgcn_sched_barrier(0);
+        multiply(ca, cb);
+        __builtin_amdgcn_sched_barrier(0);
+        load_full(i + 2 < nFull ? k + 2 * kStep : k + kStep, ca, cb);
+        __builtin_amdgcn_sched_barrier(0);
+        multiply(na, nb);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (i < nFull) multiply(ca, cb);
+    const std::uint32_t kt = k0 + nFull * kStep;
+    if (kt < k1) {  // last rows of the split: zeros past k1
+#pragma unroll
+        for (int s = 0; s < U; ++s) {
+            const bool in = kt + 4 * s + lk < k1;
+            const float* ra = a.A + static_cast<std::uint64_t>(kt + 4 * s) * a.lda;
+            const float* rb = a.B + static_cast<std::uint64_t>(kt + 4 * s) * a.ldb;
+#pragma unroll
+            for (int t = 0; t < TM; ++t) ca[s][t] = in ? ra[offA[t]] : 0.0f;
+#pragma unroll
+            for (int t = 0; t < TN; ++t) cb[s][t] = in ? rb[offB[t]] : 0.0f;
+        }
+        multiply(ca, cb);
+    }
+
+    // Tile (t, u): accumulator v of lane l is C(m0 + 16t + 4*(l/16) + v, n0 + 16u + l%16).
+    float* out = a.partial + static_cast<std::uint64_t>(blockIdx.x) * a.M * a.N;
+#pragma unroll
+    for (int t = 0; t < TM; ++t)
+#pragma unroll
+        for (int u = 0; u < TN; ++u) {
+            const std::uint32_t n = n0 + 16 * u + li;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const std::uint32_t m = m0 + 16 * t + 4 * lk + v;
+                if (m < a.M && n < a.N) out[static_cast<std::uint64_t>(m) * a.N + n] = acc[t][u][v];
+            }
+        }
+}
+
+// C[m][n] (=|+=) sum over splits of partial[s][m][n], splits added in a fixed
+// order: 16 elements per workgroup, 16 interleaved groups of splits summed
+// per thread, then the 16 group sums in order.
+__global__ void __launch_bounds__(256) tn_reduce_kernel(const float* __restrict__ partial, std::uint32_t splits,
+                                                        std::uint32_t M, std::uint32_t N, float* __restrict__ C,
+                                                        std::uint32_t ldc, int accumulate) {
+    __shared__ float part[16][17];
+    const std::uint64_t MN = static_cast<std::uint64_t>(M) * N;
+    const unsigned col = threadIdx.x & 15u, grp = threadIdx.x >> 4;
+    const std::uint64_t e = static_cast<std::uint64_t>(blockIdx.x) * 16 + col;
+    float s = 0.0f;
+    if (e < MN)
+        for (std::uint32_t sp = grp; sp < splits; sp += 16) s += partial[sp * MN + e];
+    part[grp][col] = s;
+    __syncthreads();
+    if (threadIdx.x < 16 && e < MN) {
+        float t = 0.0f;
+#pragma unroll
+        for (int g = 0; g < 16; ++g) t += part[g][col];
+        const std::uint32_t m = static_cast<std::uint32_t>(e / N), n = static_cast<std::uint32_t>(e % N);
+        float* c = C + static_cast<std::uint64_t>(m) * ldc + n;
+        *c = accumulate ? *c + t : t;
+    }
+}
+
+// Wave shapes by output shape: N <= 16 (a class-width gradient) puts the 8
+// waves along M, M <= 16 along N, anything else takes blocks of 16*TM x 256
+// with TM = 4, 7 or 8 tiles per wave (the fewest that cover M, so that a
+// 100-wide layer does not multiply a 128-wide tile column).
+enum class TnShape { Wide4, Wide7, Wide8, NarrowN, NarrowM };
+
+struct TnPlan {
+    TnShape shape;
+    std::uint32_t step;  // rows per iteration (4*U)
+    std::uint32_t BM, BN;
+    std::uint32_t blocksM, blocksN;
+    std::uint32_t splits, rowsPerSplit;
+};
+
+TnPlan tn_plan(std::uint32_t K, std::uint32_t M, std::uint32_t N) {
+    TnPlan p{};
+    if (N <= 16) {
+        p.shape = TnShape::NarrowN;  // TM=2, TN=1, WM=8, WN=1, U=8
+        p.step = 32, p.BM = 256, p.BN = 16;
+    } else if (M <= 16) {
+        p.shape = TnShape::NarrowM;  // TM=1, TN=2, WM=1, WN=8, U=8
+        p.step = 32, p.BM = 16, p.BN = 256;
+    } else {
+        // TM in {4, 7, 8}, TN=2, WM=1, WN=8, U=4
+        p.shape = M <= 64 ? TnShape::Wide4 : M <= 112 ? TnShape::Wide7 : TnShape::Wide8;
+        p.step = 16, p.BN = 256;
+        p.BM = p.shape == TnShape::Wide4 ? 64 : p.shape == TnShape::Wide7 ? 112 : 128;
+    }
+    p.blocksM = (M + p.BM - 1) / p.BM;
+    p.blocksN = (N + p.BN - 1) / p.BN;
+    const std::uint64_t blocks = static_cast<std::uint64_t>(p.blocksM) * p.blocksN;
+    // About two (Wide*) or four workgroups per compute unit in all.
+    const bool narrow = p.shape == TnShape::NarrowN || p.shape == TnShape::NarrowM;
+    const std::uint64_t target = static_cast<std::uint64_t>(device_cus()) * (narrow ? 4 : 2);
+    const std::uint64_t maxSplits = std::max<std::uint64_t>(1, (K + p.step - 1) / p.step);
+    std::uint64_t splits = std::min<std::uint64_t>(maxSplits, std::max<std::uint64_t>(1, (target + blocks - 1) / blocks));
+    std::uint64_t rps = (K + splits - 1) / splits;
+    rps = std::max<std::uint64_t>(p.step, (rps + p.step - 1) / p.step * p.step);
+    splits = std::max<std::uint64_t>(1, (K + rps - 1) / rps);
+    p.splits = static_cast<std::uint32_t>(splits);
+    p.rowsPerSplit = static_cast<std::uint32_t>(rps);
+    return p;
+}
+
+template <int TM, int TN, int WM, int WN, int U>
+void tn_launch(const TnArgs& a, const TnPlan& p, hipStream_t st) {
+    hipLaunchKernelGGL((tn_partial_kernel<TM, TN, WM, WN, U>), dim3(p.splits, p.blocksM * p.blocksN),
+                       dim3(kTnThreads), 0, st, a);
+}
+
+}  // namespace
+}  // namespace tcc
+
+using namespace tcc;
+
+extern "C" {
+
+size_t tcc_dense_tn_workspace_bytes(std::uint32_t K, std::uint32_t M, std::uint32_t N) {
+    if (K == 0 || M == 0 || N == 0) return 0;
+    const TnPlan p = tn_plan(K, M, N);
+    return static_cast<size_t>(p.splits) * M * N * sizeof(float);
+}
+
+int tcc_dense_tn(const float* A, std::uint32_t lda, const float* B, std::uint32_t ldb, float* C, std::uint32_t ldc,
+                 std::uint32_t K, std::uint32_t M, std::uint32_t N, int accumulate, void* workspace,
+                 size_t workspaceBytes, void* stream) {
+    clear_last_error();
+    TCC_REQUIRE(C && M >= 1 && N >= 1 && lda >= M && ldb >= N && ldc >= N, TCC_ERR_INVALID_ARGUMENT,
+                "invalid dense A^T B arguments");
+    TCC_REQUIRE(lda < (1u << 28) && ldb < (1u << 28) && ldc < (1u << 28), TCC_ERR_UNSUPPORTED,
+                "dense A^T B row strides must be below 2^28");
+    const hipStream_t st = as_stream(stream);
+    if (K == 0) {
+        if (accumulate) return TCC_OK;
+        for (std::uint32_t m = 0; m < M; ++m)  // C rows may be strided: clear row by row
+            TCC_HIP_CHECK(fill<float>(C + static_cast<std::uint64_t>(m) * ldc, N, 0.0f, st));
+        return TCC_OK;
+    }
+    TCC_REQUIRE(A && B && workspace, TCC_ERR_INVALID_ARGUMENT, "invalid dense A^T B arguments");
+    const TnPlan p = tn_plan(K, M, N);
+    TCC_REQUIRE(workspaceBytes >= static_cast<size_t>(p.splits) * M * N * sizeof(float), TCC_ERR_INVALID_ARGUMENT,
+                "dense A^T B workspace too small (tcc_dense_tn_workspace_bytes)");
+    TCC_REQUIRE(static_cast<std::uint64_t>(p.blocksM) * p.blocksN <= 65535, TCC_ERR_UNSUPPORTED,
+                "dense A^T B output too large");
+    TnArgs a{};
+    a.A = A;
+    a.B = B;
+    a.partial = static_cast<float*>(workspace);
+    a.lda = lda;
+    a.ldb = ldb;
+    a.K = K;
+    a.M = M;
+    a.N = N;
+    a.rowsPerSplit = p.rowsPerSplit;
+    a.blocksM = p.blocksM;
+    switch (p.shape) {
+        case TnShape::NarrowN: tn_launch<2, 1, 8, 1, 8>(a, p, st); break;
+        case TnShape::NarrowM: tn_launch<1, 2, 1, 8, 8>(a, p, st); break;
+        case TnShape::Wide4: tn_launch<4, 2, 1, 8, 4>(a, p, st); break;
+        case TnShape::Wide7: tn_launch<7, 2, 1, 8, 4>(a, p, st); break;
+        default: tn_launch<8, 2, 1, 8, 4>(a, p, st); break;
+    }
+    TCC_LAUNCH_CHECK();
+    const std::uint64_t MN = static_cast<std::uint64_t>(M) * N;
+    hipLaunchKernelGGL(tn_reduce_kernel, dim3(grid_for(MN, 16)), dim3(256), 0, st,
+                       static_cast<const float*>(workspace), p.splits, M, N, C, ldc, accumulate);
+    TCC_LAUNCH_CHECK();
+    return TCC_OK;
+}
+
+}  // extern "C"

@@ -6,6 +6,9 @@ CNICSPMMFunction mirrors the reference's autograd function
   forward : AX = A·X with the spmm_cnic split (BCSR part + BCSC part,
             spmm_launcher.cu:30-271), out = AX·W                (:130-134)
   backward: dW = AXᵀ·dY, G = Aᵀ·dY, dX = G·Wᵀ                    (:147-154)
+The weight gradients AXᵀ·dY and Xᵀ·G are tall-skinny products over all nodes
+(tcc_dense_tn: K split over workgroups on fp32 MFMA), where library GEMMs
+reach a fraction of the GPU on this shape.
 The reference's G = torch.sparse.mm(Aᵀ, dY) over unit values (:139-142, :152)
 is the block-sparse transposed gather over a BCSC of the whole A
 (tcc_bcsc_transpose_spmm), and dX is computed only when the layer's input
@@ -115,7 +118,7 @@ class CNICSPMMFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, d_output):
         AX, weights = ctx.saved_tensors
-        grad_weights = torch.mm(AX.t(), d_output)
+        grad_weights = swtcf.dense_tn(AX, d_output)  # AXᵀ·dY (:150)
         grad_x = None
         if ctx.needs_input_grad[2]:
             grad_sp = ctx.graph.transpose_aggregate(d_output)
@@ -142,7 +145,7 @@ class TransformFirstFunction(torch.autograd.Function):
     def backward(ctx, d_output):
         x, weights = ctx.saved_tensors
         grad_sp = ctx.graph.transpose_aggregate(d_output)
-        grad_weights = torch.mm(x.t(), grad_sp)
+        grad_weights = swtcf.dense_tn(x, grad_sp)  # Xᵀ·G
         grad_x = torch.mm(grad_sp, weights.t()) if ctx.needs_input_grad[1] else None
         return None, grad_x, grad_weights
 
@@ -213,8 +216,17 @@ def build_gcn_graphs(rows: torch.Tensor, cols: torch.Tensor, n: int, hot: torch.
     return g1, g2
 
 
+def cross_entropy(pred: torch.Tensor, labels: torch.Tensor) -> torch.Tensor:
+    """Mean cross-entropy of logits [n x C] against class ids: the value and
+    gradient of torch.nn.CrossEntropyLoss() (tcgnn_conv_release.py:437),
+    evaluated as log_softmax, gather and mean.  torch's 2-D nll_loss with mean
+    reduction runs its forward and backward in one workgroup (2.2 ms and
+    1.1 ms for 2.45M rows on MI355X); these run across the GPU."""
+    return -torch.log_softmax(pred, dim=1).gather(1, labels.view(-1, 1)).mean()
+
+
 def train_epoch(model: GCN, g1: LayerGraph, g2: LayerGraph, source, labels: torch.Tensor,
-                optimizer: torch.optim.Optimizer, loss_fcn) -> torch.Tensor:
+                optimizer: torch.optim.Optimizer, loss_fcn=cross_entropy) -> torch.Tensor:
     """One full-graph step: forward, loss, backward, optimizer step
     (train_one_step, tcgnn_conv_release.py:284-329)."""
     pred = model(g1, g2, source)

@@ -335,6 +335,36 @@ def bcsc_transpose_spmm(A: BlockMatrix, dY: torch.Tensor, dX: torch.Tensor | Non
     return dX
 
 
+def _rows(t: torch.Tensor, name: str) -> torch.Tensor:
+    """A float32 device matrix whose rows are contiguous (row stride free)."""
+    if t.dtype != torch.float32 or not t.is_cuda or t.dim() != 2:
+        raise TypeError(f"{name} must be a 2-D float32 device tensor (got {t.dtype} {tuple(t.shape)} on {t.device})")
+    if t.stride(1) != 1 or t.stride(0) < t.shape[1]:
+        t = t.contiguous()
+    return t
+
+
+def dense_tn(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor | None = None, accumulate: bool = False,
+             stream=None) -> torch.Tensor:
+    """C[M x N] (=|+=) A^T B for A [K x M], B [K x N] (tcc_dense_tn): the
+    weight gradient torch.mm(X_out.T, d_output) of the GCN layer backward
+    (train/tcgnn_conv_release.py:150), split over K on fp32 MFMA."""
+    A, B = _rows(A, "A"), _rows(B, "B")
+    K, M = A.shape
+    if B.shape[0] != K:
+        raise ValueError(f"A and B need the same number of rows (got {K} and {B.shape[0]})")
+    N = B.shape[1]
+    if C is None:
+        C = torch.empty((M, N), dtype=torch.float32, device=A.device)
+    elif C.shape != (M, N) or C.dtype != torch.float32 or C.stride(1) != 1:
+        raise ValueError(f"C must be a float32 [{M} x {N}] tensor with contiguous rows")
+    nbytes = _lib.lib().tcc_dense_tn_workspace_bytes(K, M, N)
+    ws = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=A.device)
+    check(_lib.lib().tcc_dense_tn(A.data_ptr(), A.stride(0), B.data_ptr(), B.stride(0), C.data_ptr(), C.stride(0),
+                                  K, M, N, int(accumulate), ws.data_ptr(), nbytes, _stream(stream)))
+    return C
+
+
 def spmm_cnic_forward(bcsr: BlockMatrix, bcsc: BlockMatrix, X: torch.Tensor, denseC: torch.Tensor,
                       stream=None) -> torch.Tensor:
     check(_lib.lib().tcc_spmm_cnic_forward(ctypes.byref(bcsr.view), ctypes.byref(bcsc.view), X.data_ptr(),

@@ -1,0 +1,111 @@
+"""tcc_dense_tn (C = A^T B over K rows: the GCN weight gradient
+torch.mm(X_out.T, d_output), train/tcgnn_conv_release.py:150) through the
+C-ABI, against float64 products of the same fp32 inputs.  Tolerance rel-L2
+1e-5: fp32 MFMA products and fp32 sums over K rows split into partials; a
+wrong row, column, tile or split index gives errors of order 1."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+REL = 1e-5
+
+
+def rel_l2(got, want):
+    got = got.double().cpu().numpy()
+    want = want.double().cpu().numpy()
+    return float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30))
+
+
+def inputs(K, M, N, seed):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    A = torch.randn(K, M, generator=g, dtype=torch.float32)
+    B = torch.randn(K, N, generator=g, dtype=torch.float32)
+    return A.cuda(), B.cuda()
+
+
+SHAPES = [
+    (1, 1, 1), (3, 5, 7), (4, 16, 16), (17, 100, 256), (33, 2, 256), (1000, 100, 256), (4099, 256, 2),
+    (777, 17, 300), (3001, 300, 40), (513, 8, 600), (100, 129, 257), (5000, 64, 64), (2047, 112, 512),
+    (200003, 100, 256), (150001, 256, 2), (65537, 2, 256),
+]
+
+
+@pytest.mark.parametrize("K,M,N", SHAPES)
+def test_dense_tn_matches_float64(K, M, N):
+    from tcc_amd import swtcf
+
+    A, B = inputs(K, M, N, K * 131 + M * 7 + N)
+    C = swtcf.dense_tn(A, B)
+    torch.cuda.synchronize()
+    assert rel_l2(C, A.double().t() @ B.double()) < REL
+
+
+def test_dense_tn_strided_rows_and_accumulate():
+    """Row strides above the width (a view of wider buffers, as the layer's
+    AX view of denseC) and C += A^T B into a strided C."""
+    from tcc_amd import swtcf
+
+    K, M, N = 9001, 100, 256
+    A0, B0 = inputs(K, M + 28, N + 3, 5)
+    A, B = A0[:, 3:3 + M], B0[:, :N]
+    assert A.stride(0) == M + 28 and B.stride(0) == N + 3
+    Cbig = torch.randn(M, N + 5, device="cuda")
+    C = Cbig[:, :N]
+    before = C.clone()
+    extra = Cbig[:, N:].clone()
+    swtcf.dense_tn(A, B, C, accumulate=True)
+    torch.cuda.synchronize()
+    want = before.double() + A.double().t() @ B.double()
+    assert rel_l2(C, want) < REL
+    assert torch.equal(Cbig[:, N:], extra)  # columns past N untouched
+    swtcf.dense_tn(A, B, C)
+    assert rel_l2(C, A.double().t() @ B.double()) < REL
+
+
+def test_dense_tn_repeat_is_deterministic():
+    """Partials are summed in a fixed order: two calls agree bit for bit."""
+    from tcc_amd import swtcf
+
+    A, B = inputs(300007, 100, 256, 11)
+    C1 = swtcf.dense_tn(A, B)
+    C2 = swtcf.dense_tn(A, B)
+    torch.cuda.synchronize()
+    assert torch.equal(C1, C2)
+
+
+def test_dense_tn_empty_k():
+    from tcc_amd import swtcf
+
+    A = torch.empty((0, 7), device="cuda")
+    B = torch.empty((0, 5), device="cuda")
+    C = torch.full((7, 5), 3.0, device="cuda")
+    swtcf.dense_tn(A, B, C, accumulate=True)
+    assert torch.all(C == 3.0)
+    swtcf.dense_tn(A, B, C)
+    assert torch.all(C == 0.0)
+
+
+def test_dense_tn_argument_errors():
+    from tcc_amd import _lib
+
+    L = _lib.lib()
+    A = torch.randn(64, 10, device="cuda")
+    B = torch.randn(64, 20, device="cuda")
+    C = torch.empty(10, 20, device="cuda")
+    need = L.tcc_dense_tn_workspace_bytes(64, 10, 20)
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    # lda below M
+    assert L.tcc_dense_tn(A.data_ptr(), 9, B.data_ptr(), 20, C.data_ptr(), 20, 64, 10, 20, 0, ws.data_ptr(), need,
+                          None) == 1
+    # workspace too small
+    assert L.tcc_dense_tn(A.data_ptr(), 10, B.data_ptr(), 20, C.data_ptr(), 20, 64, 10, 20, 0, ws.data_ptr(),
+                          need - 4, None) == 1
+    assert b"workspace too small" in L.tcc_last_error()
+    assert L.tcc_dense_tn(A.data_ptr(), 10, B.data_ptr(), 20, C.data_ptr(), 20, 64, 10, 20, 0, ws.data_ptr(), need,
+                          None) == 0
+    torch.cuda.synchronize()
+    assert rel_l2(C, A.double().t() @ B.double()) < REL

@@ -68,7 +68,7 @@ def test_gcn_step_matches_dense_reference(gpu, hot_fraction):
     W1 = model.conv1.weights.detach().cpu().numpy().astype(np.float64)
     W2 = model.conv_final.weights.detach().cpu().numpy().astype(np.float64)
     pred = model(g1, g2, table.source)
-    loss = torch.nn.CrossEntropyLoss()(pred, labels)
+    loss = gcn.cross_entropy(pred, labels)
     loss.backward()
     torch.cuda.synchronize()
     A = np.zeros((n, n))
@@ -102,7 +102,6 @@ def test_gcn_trains(gpu):
     model = gcn.GCN(F, 64, 2).cuda()
     labels = gcn.synthetic_labels(n, 2, 3)
     opt = torch.optim.Adam(model.parameters(), lr=0.003)
-    loss_fcn = torch.nn.CrossEntropyLoss()
-    losses = [gcn.train_epoch(model, g1, g2, table.source, labels, opt, loss_fcn).item() for _ in range(30)]
+    losses = [gcn.train_epoch(model, g1, g2, table.source, labels, opt).item() for _ in range(30)]
     assert losses[-1] < losses[0]
     table.free()
