@@ -72,6 +72,7 @@ struct GatherArgs {
     std::uint32_t unitBlocks;
     std::uint32_t numUnits;
     int accumulate;
+    int atomicOut;  // add every window into Y with atomics (Y zeroed by the caller)
     MixedArgs mixed;
 };
 
@@ -384,9 +385,8 @@ __device__ __forceinline__ void accumulate_block(std::uint64_t raw, std::uint64_
 // One wave per (unit, feature chunk of 64*V); waves are ordered chunk-major
 // so that the input rows one chunk touches stay in the last-level cache.
 template <int V, Src MODE, bool VALUES>
-__global__ void __launch_bounds__(kThreads) gather_kernel(GatherArgs a) {
+__device__ __forceinline__ void gather_body(const GatherArgs& a, std::uint32_t gw) {
     const unsigned lane = __lane_id();
-    const std::uint32_t gw = blockIdx.x * kWaves + uniform(threadIdx.x / kWave);
     const std::uint32_t chunk = gw / a.numUnits;
     const std::uint32_t unit = gw - chunk * a.numUnits;
     if (chunk >= a.numChunks) return;
@@ -412,7 +412,7 @@ __global__ void __launch_bounds__(kThreads) gather_kernel(GatherArgs a) {
     auto flush = [&]() {
         if (active) {
             float* out = a.Y + static_cast<std::uint64_t>(w) * 8 * a.F + f0;
-            const bool shared = ws < u.b0 || we > u.b1;
+            const bool shared = a.atomicOut || ws < u.b0 || we > u.b1;
 #pragma unroll
             for (int r = 0; r < 8; ++r) {
                 float* o = out + static_cast<std::uint64_t>(r) * a.F;
@@ -460,6 +460,11 @@ __global__ void __launch_bounds__(kThreads) gather_kernel(GatherArgs a) {
             flush();
         }
     }
+}
+
+template <int V, Src MODE, bool VALUES>
+__global__ void __launch_bounds__(kThreads) gather_kernel(GatherArgs a) {
+    gather_body<V, MODE, VALUES>(a, blockIdx.x * kWaves + uniform(threadIdx.x / kWave));
 }
 
 // Zero the rows of every window a unit boundary cuts (so that the units
@@ -789,9 +794,8 @@ __device__ __forceinline__ void load_window_rows(const ScatterArgs& a, std::uint
 }
 
 template <int V, bool MIXED, bool VALUES>
-__global__ void __launch_bounds__(kThreads) scatter_kernel(ScatterArgs a) {
+__device__ __forceinline__ void scatter_body(const ScatterArgs& a, std::uint32_t gw) {
     const unsigned lane = __lane_id();
-    const std::uint32_t gw = blockIdx.x * kWaves + uniform(threadIdx.x / kWave);
     const std::uint32_t chunk = gw / a.numUnits;
     const std::uint32_t unit = gw - chunk * a.numUnits;
     if (chunk >= a.numChunks) return;
@@ -854,6 +858,29 @@ __global__ void __launch_bounds__(kThreads) scatter_kernel(ScatterArgs a) {
     }
 }
 
+template <int V, bool MIXED, bool VALUES>
+__global__ void __launch_bounds__(kThreads) scatter_kernel(ScatterArgs a) {
+    scatter_body<V, MIXED, VALUES>(a, blockIdx.x * kWaves + uniform(threadIdx.x / kWave));
+}
+
+// The first layer's forward in one launch.  The reference runs the hot BCSR
+// gather and the cold BCSC scatter one after the other
+// (spmm_launcher.cu:30-271); here their workgroups are interleaved in
+// proportion to their counts, so that scatter waves, which wait on host
+// memory across the link, and gather waves, which stream HBM, run side by
+// side.  Both add into a zeroed Y with atomics.
+template <int V, bool GVALUES, bool SVALUES>
+__global__ void __launch_bounds__(kThreads) mixed_forward_kernel(GatherArgs g, ScatterArgs s, std::uint32_t gatherWGs,
+                                                                 std::uint32_t scatterWGs) {
+    const std::uint64_t total = static_cast<std::uint64_t>(gatherWGs) + scatterWGs;
+    const std::uint32_t i = blockIdx.x;
+    const auto before = static_cast<std::uint32_t>(static_cast<std::uint64_t>(i) * scatterWGs / total);
+    const auto upto = static_cast<std::uint32_t>(static_cast<std::uint64_t>(i + 1) * scatterWGs / total);
+    const std::uint32_t wave = uniform(threadIdx.x / kWave);
+    if (upto > before) scatter_body<V, true, SVALUES>(s, before * kWaves + wave);  // the before-th scatter group
+    else gather_body<V, Src::Mixed, GVALUES>(g, (i - before) * kWaves + wave);
+}
+
 // Vector width per lane: the narrowest V in {1,2,4} whose 64*V-feature chunk
 // covers F (so a wave's lanes are all busy), else the widest that divides F;
 // V-wide loads need F % V == 0 and 4V-byte aligned base pointers.
@@ -884,15 +911,30 @@ inline std::uint32_t unit_blocks(std::uint32_t requested, std::uint32_t blocks, 
     return K;
 }
 
-template <Src MODE>
-int launch_gather(GatherArgs a, int V, std::uint32_t requestedK, hipStream_t st) {
-    if (a.numWindows == 0) return TCC_OK;
+// Work split of a gather (chunks, unit size, units); its wave count.
+inline std::uint64_t plan_gather(GatherArgs& a, int V, std::uint32_t requestedK) {
+    if (a.numWindows == 0) return 0;
     a.numChunks = (a.F + kWave * V - 1) / (kWave * V);
     a.unitBlocks = unit_blocks(requestedK, a.numBlocks, a.numChunks);
     a.numUnits = std::max<std::uint32_t>(1, (a.numBlocks + a.unitBlocks - 1) / a.unitBlocks);
-    const std::uint64_t waves = static_cast<std::uint64_t>(a.numUnits) * a.numChunks;
+    return static_cast<std::uint64_t>(a.numUnits) * a.numChunks;
+}
+
+// Work split of a scatter; its wave count.
+inline std::uint64_t plan_scatter(ScatterArgs& a, int V, std::uint32_t requestedK) {
+    if (a.numWindows == 0 || a.numBlocks == 0) return 0;
+    a.numChunks = (a.F + kWave * V - 1) / (kWave * V);
+    a.unitBlocks = unit_blocks(requestedK, a.numBlocks, a.numChunks);
+    a.numUnits = (a.numBlocks + a.unitBlocks - 1) / a.unitBlocks;
+    return static_cast<std::uint64_t>(a.numUnits) * a.numChunks;
+}
+
+template <Src MODE>
+int launch_gather(GatherArgs a, int V, std::uint32_t requestedK, hipStream_t st) {
+    const std::uint64_t waves = plan_gather(a, V, requestedK);
+    if (waves == 0) return TCC_OK;
     TCC_REQUIRE(waves <= 0xFFFFFFFFull / kWaves, TCC_ERR_UNSUPPORTED, "SpMM launch too large");
-    if (a.numUnits > 1 && !a.accumulate) {
+    if (a.numUnits > 1 && !a.accumulate && !a.atomicOut) {
         hipLaunchKernelGGL(zero_shared_windows_kernel, dim3(grid_for(a.numUnits - 1, kWaves)), dim3(kThreads), 0, st,
                            a.winOffset, a.numWindows, a.unitBlocks, a.numUnits, a.Y, a.F);
         TCC_LAUNCH_CHECK();
@@ -951,11 +993,8 @@ int launch_narrow(GatherArgs a, std::uint32_t requestedK, hipStream_t st) {
 
 template <bool MIXED>
 int launch_scatter(ScatterArgs a, int V, std::uint32_t requestedK, hipStream_t st) {
-    if (a.numWindows == 0 || a.numBlocks == 0) return TCC_OK;
-    a.numChunks = (a.F + kWave * V - 1) / (kWave * V);
-    a.unitBlocks = unit_blocks(requestedK, a.numBlocks, a.numChunks);
-    a.numUnits = (a.numBlocks + a.unitBlocks - 1) / a.unitBlocks;
-    const std::uint64_t waves = static_cast<std::uint64_t>(a.numUnits) * a.numChunks;
+    const std::uint64_t waves = plan_scatter(a, V, requestedK);
+    if (waves == 0) return TCC_OK;
     TCC_REQUIRE(waves <= 0xFFFFFFFFull / kWaves, TCC_ERR_UNSUPPORTED, "SpMM launch too large");
     const dim3 grid(grid_for(waves, kWaves));
     if (a.data != nullptr) {
@@ -1142,14 +1181,39 @@ int tcc_spmm_cnic_forward_mixed(const tcc_bcsr* bcsr, const tcc_bcsc* bcsc, cons
     clear_last_error();
     TCC_REQUIRE(bcsr_ok(bcsr) && bcsc_ok(bcsc) && src && denseC && featureDim >= 1, TCC_ERR_INVALID_ARGUMENT,
                 "invalid spmm_cnic mixed forward arguments");
+    TCC_REQUIRE(src->id_map && src->cache_search_map && src->gpu_feature_cache && src->gpu_node_capacity > 0,
+                TCC_ERR_INVALID_ARGUMENT, "invalid spmm_cnic mixed forward feature source");
     const hipStream_t st = as_stream(stream);
     const std::uint64_t F = featureDim;
-    TCC_HIP_CHECK(fill<float>(denseC + static_cast<std::uint64_t>(bcsr->num_rowWindows) * 8 * F, 8 * F, 0.0f, st));
-    int rc = tcc_bcsr_spmm_mixed(bcsr, src, denseC, featureDim, 0, stream);
-    if (rc) return rc;
-    ScatterArgs b = bcsc_args(bcsc, nullptr, denseC, featureDim);
-    b.mixed = mixed_args(src);
-    return launch_scatter<true>(b, pick_vec(featureDim, {denseC, src->cpu_features}), bcsc->unitBlocks, st);
+    // denseC = 0 over its (num_rowWindows+1)*8 rows, then both parts add in.
+    TCC_HIP_CHECK(fill<float>(denseC, (static_cast<std::uint64_t>(bcsr->num_rowWindows) + 1) * 8 * F, 0.0f, st));
+    const int V = pick_vec(featureDim, {denseC, src->cpu_features});
+    GatherArgs g = bcsr_args(bcsr, nullptr, denseC, featureDim, 0);
+    g.mixed = mixed_args(src);
+    g.atomicOut = 1;
+    ScatterArgs s = bcsc_args(bcsc, nullptr, denseC, featureDim);
+    s.mixed = g.mixed;
+    const std::uint64_t gw = plan_gather(g, V, bcsr->unitBlocks);
+    const std::uint64_t sw = plan_scatter(s, V, bcsc->unitBlocks);
+    const std::uint64_t gWG = (gw + kWaves - 1) / kWaves, sWG = (sw + kWaves - 1) / kWaves;
+    if (gWG + sWG == 0) return TCC_OK;
+    TCC_REQUIRE(gWG + sWG <= 0x7FFFFFFFull, TCC_ERR_UNSUPPORTED, "SpMM launch too large");
+    const dim3 grid(static_cast<unsigned>(gWG + sWG));
+    const auto gn = static_cast<std::uint32_t>(gWG), sn = static_cast<std::uint32_t>(sWG);
+    const bool gv = g.data != nullptr, sv = s.data != nullptr;
+#define TCC_MIXED_LAUNCH(VV)                                                                                      \
+    do {                                                                                                          \
+        if (gv && sv) hipLaunchKernelGGL((mixed_forward_kernel<VV, true, true>), grid, dim3(kThreads), 0, st, g, s, gn, sn);   \
+        else if (gv) hipLaunchKernelGGL((mixed_forward_kernel<VV, true, false>), grid, dim3(kThreads), 0, st, g, s, gn, sn); \
+        else if (sv) hipLaunchKernelGGL((mixed_forward_kernel<VV, false, true>), grid, dim3(kThreads), 0, st, g, s, gn, sn); \
+        else hipLaunchKernelGGL((mixed_forward_kernel<VV, false, false>), grid, dim3(kThreads), 0, st, g, s, gn, sn);        \
+    } while (0)
+    if (V == 4) TCC_MIXED_LAUNCH(4);
+    else if (V == 2) TCC_MIXED_LAUNCH(2);
+    else TCC_MIXED_LAUNCH(1);
+#undef TCC_MIXED_LAUNCH
+    TCC_LAUNCH_CHECK();
+    return TCC_OK;
 }
 
 }  // extern "C"

@@ -26,9 +26,6 @@
 namespace tcc {
 namespace {
 
-constexpr unsigned kTnThreads = 512;  // 8 waves
-constexpr unsigned kTnWaves = kTnThreads / kWave;
-
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 struct TnArgs {
@@ -50,8 +47,7 @@ __device__ __forceinline__ std::uint32_t tn_uniform(std::uint32_t v) {
 // takes U steps of 4 rows; the next iteration's operands are loaded while
 // the current one is multiplied.
 template <int TM, int TN, int WM, int WN, int U>
-__global__ void __launch_bounds__(kTnThreads) tn_partial_kernel(TnArgs a) {
-    static_assert(WM * WN == static_cast<int>(kTnWaves), "8 waves per workgroup");
+__global__ void __launch_bounds__(kWave * WM * WN) tn_partial_kernel(TnArgs a) {
     constexpr int BM = 16 * TM * WM, BN = 16 * TN * WN;
     constexpr std::uint32_t kStep = 4 * U;
     const unsigned lane = __lane_id();
@@ -174,10 +170,15 @@ __global__ void __launch_bounds__(256) tn_reduce_kernel(const float* __restrict_
     }
 }
 
-// Wave shapes by output shape: N <= 16 (a class-width gradient) puts the 8
-// waves along M, M <= 16 along N, anything else takes blocks of 16*TM x 256
-// with TM = 4, 7 or 8 tiles per wave (the fewest that cover M, so that a
-// 100-wide layer does not multiply a 128-wide tile column).
+// Wave shapes by output shape (measured on MI355X, K = 2.45M rows):
+//  - anything wide: 4 waves side by side along N, each with TM x 4 tiles
+//    (TM = 4, 7 or 8, the fewest that cover M, so that a 100-wide layer does
+//    not multiply a 128-wide tile column); 4 tiles along N reuse each A
+//    operand 4 times from registers: 100x256 runs at ~100 TFLOP/s, against
+//    ~50 with 8 waves of 7x2 tiles;
+//  - N <= 16 (a class-width gradient): 4 waves along M with 4 x 1 tiles,
+//    eight workgroups per CU for memory parallelism (~5 TB/s for 256x2);
+//    M <= 16 the same along N.
 enum class TnShape { Wide4, Wide7, Wide8, NarrowN, NarrowM };
 
 struct TnPlan {
@@ -191,13 +192,13 @@ struct TnPlan {
 TnPlan tn_plan(std::uint32_t K, std::uint32_t M, std::uint32_t N) {
     TnPlan p{};
     if (N <= 16) {
-        p.shape = TnShape::NarrowN;  // TM=2, TN=1, WM=8, WN=1, U=8
+        p.shape = TnShape::NarrowN;  // TM=4, TN=1, WM=4, WN=1, U=8
         p.step = 32, p.BM = 256, p.BN = 16;
     } else if (M <= 16) {
-        p.shape = TnShape::NarrowM;  // TM=1, TN=2, WM=1, WN=8, U=8
+        p.shape = TnShape::NarrowM;  // TM=1, TN=4, WM=1, WN=4, U=8
         p.step = 32, p.BM = 16, p.BN = 256;
     } else {
-        // TM in {4, 7, 8}, TN=2, WM=1, WN=8, U=4
+        // TM in {4, 7, 8}, TN=4, WM=1, WN=4, U=4
         p.shape = M <= 64 ? TnShape::Wide4 : M <= 112 ? TnShape::Wide7 : TnShape::Wide8;
         p.step = 16, p.BN = 256;
         p.BM = p.shape == TnShape::Wide4 ? 64 : p.shape == TnShape::Wide7 ? 112 : 128;
@@ -205,9 +206,9 @@ TnPlan tn_plan(std::uint32_t K, std::uint32_t M, std::uint32_t N) {
     p.blocksM = (M + p.BM - 1) / p.BM;
     p.blocksN = (N + p.BN - 1) / p.BN;
     const std::uint64_t blocks = static_cast<std::uint64_t>(p.blocksM) * p.blocksN;
-    // About two (Wide*) or four workgroups per compute unit in all.
+    // About two (Wide*) or eight workgroups per compute unit in all.
     const bool narrow = p.shape == TnShape::NarrowN || p.shape == TnShape::NarrowM;
-    const std::uint64_t target = static_cast<std::uint64_t>(device_cus()) * (narrow ? 4 : 2);
+    const std::uint64_t target = static_cast<std::uint64_t>(device_cus()) * (narrow ? 8 : 2);
     const std::uint64_t maxSplits = std::max<std::uint64_t>(1, (K + p.step - 1) / p.step);
     std::uint64_t splits = std::min<std::uint64_t>(maxSplits, std::max<std::uint64_t>(1, (target + blocks - 1) / blocks));
     std::uint64_t rps = (K + splits - 1) / splits;
@@ -221,7 +222,7 @@ TnPlan tn_plan(std::uint32_t K, std::uint32_t M, std::uint32_t N) {
 template <int TM, int TN, int WM, int WN, int U>
 void tn_launch(const TnArgs& a, const TnPlan& p, hipStream_t st) {
     hipLaunchKernelGGL((tn_partial_kernel<TM, TN, WM, WN, U>), dim3(p.splits, p.blocksM * p.blocksN),
-                       dim3(kTnThreads), 0, st, a);
+                       dim3(kWave * WM * WN), 0, st, a);
 }
 
 }  // namespace
@@ -270,11 +271,11 @@ int tcc_dense_tn(const float* A, std::uint32_t lda, const float* B, std::uint32_
     a.rowsPerSplit = p.rowsPerSplit;
     a.blocksM = p.blocksM;
     switch (p.shape) {
-        case TnShape::NarrowN: tn_launch<2, 1, 8, 1, 8>(a, p, st); break;
-        case TnShape::NarrowM: tn_launch<1, 2, 1, 8, 8>(a, p, st); break;
-        case TnShape::Wide4: tn_launch<4, 2, 1, 8, 4>(a, p, st); break;
-        case TnShape::Wide7: tn_launch<7, 2, 1, 8, 4>(a, p, st); break;
-        default: tn_launch<8, 2, 1, 8, 4>(a, p, st); break;
+        case TnShape::NarrowN: tn_launch<4, 1, 4, 1, 8>(a, p, st); break;
+        case TnShape::NarrowM: tn_launch<1, 4, 1, 4, 8>(a, p, st); break;
+        case TnShape::Wide4: tn_launch<4, 4, 1, 4, 4>(a, p, st); break;
+        case TnShape::Wide7: tn_launch<7, 4, 1, 4, 4>(a, p, st); break;
+        default: tn_launch<8, 4, 1, 4, 4>(a, p, st); break;
     }
     TCC_LAUNCH_CHECK();
     const std::uint64_t MN = static_cast<std::uint64_t>(M) * N;
