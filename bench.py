@@ -347,7 +347,10 @@ def bench_gcn(args, torch, swtcf, cfg):
 
     l1 = timed(layer1, steps, warmup)
     l2 = timed(layer2, steps, warmup)
-    extra = {"layer1_fwd_bwd_ms": round(l1, 4), "layer2_fwd_bwd_ms": round(l2, 4),
+    extra = {"epoch": "TwoLayerFunction: mixed SpMM F=100, GEMM 100x256 + relu, GEMM 256x2, SpMM F=2; backward "
+                      "A^T SpMM F=2, then dW1 and dW2 in one pass (tcc_gcn_relu_grad), cross-entropy, Adam",
+             "layer_times": "each layer alone, through its own autograd function",
+             "layer1_fwd_bwd_ms": round(l1, 4), "layer2_fwd_bwd_ms": round(l2, 4),
              "layer1": f"mixed SpMM F={F} (hot BCSR + cold BCSC) + GEMM {F}x{hidden}; backward dW GEMM",
              "layer2": f"A(XW): GEMM {hidden}x{classes}, BCSR SpMM F={classes}; backward A^T SpMM F={classes}, "
                        f"dW and dX GEMMs",

@@ -40,6 +40,27 @@ size_t tcc_dense_tn_workspace_bytes(uint32_t K, uint32_t M, uint32_t N);
 int tcc_dense_tn(const float* A, uint32_t lda, const float* B, uint32_t ldb, float* C, uint32_t ldc, uint32_t K,
                  uint32_t M, uint32_t N, int accumulate, void* workspace, size_t workspaceBytes, void* stream);
 
+/* Bytes of device workspace tcc_gcn_relu_grad needs (current device). */
+size_t tcc_gcn_relu_grad_workspace_bytes(uint32_t K, uint32_t F, uint32_t Hd, uint32_t C);
+
+/* Both weight gradients of a two-layer GCN, conv_final(relu(conv1(X))), in
+ * one pass over the K node rows:
+ *   dW1 [F x Hd] = AX^T ((G W2^T) (.) [H > 0])
+ *   dW2 [Hd x C] = H^T G
+ * with AX [K x F] the first layer's aggregated input (row stride ldax),
+ * H [K x Hd] its relu output (ldh), G [K x C] = A^T dOut the second layer's
+ * aggregated output gradient (ldg) and W2 [Hd x C] row-major, C <= 8
+ * (TCC_ERR_UNSUPPORTED above).
+ * This is what the reference's autograd runs as four steps
+ * (train/tcgnn_conv_release.py:147-154 for each layer, with torch's relu
+ * backward between): grad_X = grad_sp @ weights.T of the second layer,
+ * the relu mask, and grad_weights = X_out.T @ d_output of both layers.
+ * Products and sums in fp32; dW1 and dW2 are overwritten.  `workspace` as
+ * for tcc_dense_tn, at least tcc_gcn_relu_grad_workspace_bytes bytes. */
+int tcc_gcn_relu_grad(const float* AX, uint32_t ldax, const float* H, uint32_t ldh, const float* G, uint32_t ldg,
+                      const float* W2, float* dW1, float* dW2, uint32_t K, uint32_t F, uint32_t Hd, uint32_t C,
+                      void* workspace, size_t workspaceBytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -36,6 +36,12 @@ struct TnArgs {
     std::uint32_t K, M, N;
     std::uint32_t rowsPerSplit;
     std::uint32_t blocksM;  // blocks of C along M
+    // Relu-gradient form only (see tn_partial_kernel): G [K x C] with row
+    // stride ldg, W2 [N x C], and the H^T G partials [splits][N][C].
+    const float* G;
+    const float* W2;
+    float* partial2;
+    std::uint32_t ldg, C;
 };
 
 __device__ __forceinline__ std::uint32_t tn_uniform(std::uint32_t v) {
@@ -46,9 +52,16 @@ __device__ __forceinline__ std::uint32_t tn_uniform(std::uint32_t v) {
 // workgroup covers a (16*TM*WM) x (16*TN*WN) block of C.  Each iteration
 // takes U steps of 4 rows; the next iteration's operands are loaded while
 // the current one is multiplied.
-template <int TM, int TN, int WM, int WN, int U>
+//
+// CT > 0 is the GCN relu-gradient form: B holds H (the relu output of the
+// layer, [K x N]) and the B operand is formed in registers as
+// (G W2^T) (.) [H > 0] from G [K x C] and W2 [N x C] (C <= CT), while H^T G
+// is summed beside it into partial2 -- the layer-1 weight gradient and the
+// layer-2 weight gradient of a two-layer GCN in one pass over its rows.
+template <int TM, int TN, int WM, int WN, int U, int CT>
 __global__ void __launch_bounds__(kWave * WM * WN) tn_partial_kernel(TnArgs a) {
     constexpr int BM = 16 * TM * WM, BN = 16 * TN * WN;
+    constexpr int GC = CT > 0 ? CT : 1;  // G columns held per row
     constexpr std::uint32_t kStep = 4 * U;
     const unsigned lane = __lane_id();
     const unsigned wave = tn_uniform(threadIdx.x / kWave);
@@ -65,6 +78,21 @@ __global__ void __launch_bounds__(kWave * WM * WN) tn_partial_kernel(TnArgs a) {
     for (int t = 0; t < TM; ++t) offA[t] = lk * a.lda + min(m0 + 16 * t + li, a.M - 1);
 #pragma unroll
     for (int t = 0; t < TN; ++t) offB[t] = lk * a.ldb + min(n0 + 16 * t + li, a.N - 1);
+    // Relu-gradient form: this lane's W2 rows, G column offsets (clamped).
+    float w2[TN][GC];
+    float dw2[TN][GC];
+    std::uint32_t offG[GC];
+#pragma unroll
+    for (int j = 0; j < GC; ++j) offG[j] = CT > 0 ? lk * a.ldg + min<std::uint32_t>(j, a.C - 1) : 0u;
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+#pragma unroll
+        for (int j = 0; j < GC; ++j) {
+            dw2[t][j] = 0.0f;
+            w2[t][j] = 0.0f;
+            if (CT > 0 && static_cast<std::uint32_t>(j) < a.C)
+                w2[t][j] = a.W2[static_cast<std::uint64_t>(min(n0 + 16 * t + li, a.N - 1)) * a.C + j];
+        }
 
     f32x4 acc[TM][TN];
 #pragma unroll
@@ -72,7 +100,7 @@ __global__ void __launch_bounds__(kWave * WM * WN) tn_partial_kernel(TnArgs a) {
 #pragma unroll
         for (int u = 0; u < TN; ++u) acc[t][u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    auto load_full = [&](std::uint32_t k, float (&xa)[U][TM], float (&xb)[U][TN]) {
+    auto load_full = [&](std::uint32_t k, float (&xa)[U][TM], float (&xb)[U][TN], float (&xg)[U][GC]) {
 #pragma unroll
         for (int s = 0; s < U; ++s) {
             const float* ra = a.A + static_cast<std::uint64_t>(k + 4 * s) * a.lda;
@@ -81,40 +109,67 @@ __global__ void __launch_bounds__(kWave * WM * WN) tn_partial_kernel(TnArgs a) {
             for (int t = 0; t < TM; ++t) xa[s][t] = ra[offA[t]];
 #pragma unroll
             for (int t = 0; t < TN; ++t) xb[s][t] = rb[offB[t]];
+            if constexpr (CT > 0) {
+                const float* rg = a.G + static_cast<std::uint64_t>(k + 4 * s) * a.ldg;
+#pragma unroll
+                for (int j = 0; j < GC; ++j) xg[s][j] = rg[offG[j]];
+            }
         }
     };
-    auto multiply = [&](const float (&xa)[U][TM], const float (&xb)[U][TN]) {
+    auto multiply = [&](const float (&xa)[U][TM], const float (&xb)[U][TN], const float (&xg)[U][GC]) {
 #pragma unroll
-        for (int s = 0; s < U; ++s)
+        for (int s = 0; s < U; ++s) {
+            float b[TN];
+#pragma unroll
+            for (int u = 0; u < TN; ++u) {
+                if constexpr (CT > 0) {
+                    // dOut1 = (G W2^T) (.) [H > 0]; dW2 += H^T G (columns past C have w2 = 0
+                    // and are never stored)
+                    float d = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < GC; ++j) {
+                        d = fmaf(xg[s][j], w2[u][j], d);
+                        dw2[u][j] = fmaf(xb[s][u], xg[s][j], dw2[u][j]);
+                    }
+                    b[u] = xb[s][u] > 0.0f ? d : 0.0f;
+                } else {
+                    b[u] = xb[s][u];
+                }
+            }
 #pragma unroll
             for (int t = 0; t < TM; ++t)
 #pragma unroll
                 for (int u = 0; u < TN; ++u)
-                    acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[s][t], xb[s][u], acc[t][u], 0, 0, 0);
+                    acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[s][t], b[u], acc[t][u], 0, 0, 0);
+        }
     };
 
     // Two operand buffers in turn; loads are unconditional (past the last
     // full iteration they repeat in-bounds rows and are not used), so the
     // loads of one buffer stay in flight while the other is multiplied.
-    const std::uint32_t rows = k1 > k0 ? k1 - k0 : 0u;
-    const std::uint32_t nFull = rows / kStep;
-    float ca[U][TM], cb[U][TN], na[U][TM], nb[U][TN];
-    if (nFull > 0) load_full(k0, ca, cb);
-    std::uint32_t i = 0;
     // (sched_barrier keeps the scheduler from sinking the loads to their
     // uses, which it does to lower register pressure.)
+    const std::uint32_t rows = k1 > k0 ? k1 - k0 : 0u;
+    const std::uint32_t nFull = rows / kStep;
+    float ca[U][TM], cb[U][TN], cg[U][GC], na[U][TM], nb[U][TN], ng[U][GC];
+#pragma unroll
+    for (int s = 0; s < U; ++s)
+#pragma unroll
+        for (int j = 0; j < GC; ++j) cg[s][j] = ng[s][j] = 0.0f;
+    if (nFull > 0) load_full(k0, ca, cb, cg);
+    std::uint32_t i = 0;
     for (; i + 1 < nFull; i += 2) {
         const std::uint32_t k = k0 + i * kStep;
-        load_full(k + kStep, na, nb);
+        load_full(k + kStep, na, nb, ng);
         __builtin_amdgcn_sched_barrier(0);
-        multiply(ca, cb);
+        multiply(ca, cb, cg);
         __builtin_amdgcn_sched_barrier(0);
-        load_full(i + 2 < nFull ? k + 2 * kStep : k + kStep, ca, cb);
+        load_full(i + 2 < nFull ? k + 2 * kStep : k + kStep, ca, cb, cg);
         __builtin_amdgcn_sched_barrier(0);
-        multiply(na, nb);
+        multiply(na, nb, ng);
         __builtin_amdgcn_sched_barrier(0);
     }
-    if (i < nFull) multiply(ca, cb);
+    if (i < nFull) multiply(ca, cb, cg);
     const std::uint32_t kt = k0 + nFull * kStep;
     if (kt < k1) {  // last rows of the split: zeros past k1
 #pragma unroll
@@ -126,8 +181,13 @@ __global__ void __launch_bounds__(kWave * WM * WN) tn_partial_kernel(TnArgs a) {
             for (int t = 0; t < TM; ++t) ca[s][t] = in ? ra[offA[t]] : 0.0f;
 #pragma unroll
             for (int t = 0; t < TN; ++t) cb[s][t] = in ? rb[offB[t]] : 0.0f;
+            if constexpr (CT > 0) {
+                const float* rg = a.G + static_cast<std::uint64_t>(kt + 4 * s) * a.ldg;
+#pragma unroll
+                for (int j = 0; j < GC; ++j) cg[s][j] = in ? rg[offG[j]] : 0.0f;
+            }
         }
-        multiply(ca, cb);
+        multiply(ca, cb, cg);
     }
 
     // Tile (t, u): accumulator v of lane l is C(m0 + 16t + 4*(l/16) + v, n0 + 16u + l%16).
@@ -143,6 +203,22 @@ __global__ void __launch_bounds__(kWave * WM * WN) tn_partial_kernel(TnArgs a) {
                 if (m < a.M && n < a.N) out[static_cast<std::uint64_t>(m) * a.N + n] = acc[t][u][v];
             }
         }
+    if constexpr (CT > 0) {
+        // H^T G of this split: column n = n0 + 16u + l%16 summed over the 4
+        // row quarters; one block row of C (cbm == 0, first wave row) writes it.
+        float* out2 = a.partial2 + static_cast<std::uint64_t>(blockIdx.x) * a.N * a.C;
+#pragma unroll
+        for (int u = 0; u < TN; ++u)
+#pragma unroll
+            for (int j = 0; j < GC; ++j) {
+                float v = dw2[u][j];
+                v += __shfl_xor(v, 16);
+                v += __shfl_xor(v, 32);
+                const std::uint32_t n = n0 + 16 * u + li;
+                if (cbm == 0 && wm == 0 && lk == 0 && n < a.N && static_cast<std::uint32_t>(j) < a.C)
+                    out2[static_cast<std::uint64_t>(n) * a.C + j] = v;
+            }
+    }
 }
 
 // C[m][n] (=|+=) sum over splits of partial[s][m][n], splits added in a fixed
@@ -189,7 +265,8 @@ struct TnPlan {
     std::uint32_t splits, rowsPerSplit;
 };
 
-TnPlan tn_plan(std::uint32_t K, std::uint32_t M, std::uint32_t N) {
+// Shape chosen from (M, N); block counts from (realM, realN) when given.
+TnPlan tn_plan(std::uint32_t K, std::uint32_t M, std::uint32_t N, std::uint32_t realM = 0, std::uint32_t realN = 0) {
     TnPlan p{};
     if (N <= 16) {
         p.shape = TnShape::NarrowN;  // TM=4, TN=1, WM=4, WN=1, U=8
@@ -203,6 +280,8 @@ TnPlan tn_plan(std::uint32_t K, std::uint32_t M, std::uint32_t N) {
         p.step = 16, p.BN = 256;
         p.BM = p.shape == TnShape::Wide4 ? 64 : p.shape == TnShape::Wide7 ? 112 : 128;
     }
+    if (realM != 0) M = realM;
+    if (realN != 0) N = realN;
     p.blocksM = (M + p.BM - 1) / p.BM;
     p.blocksN = (N + p.BN - 1) / p.BN;
     const std::uint64_t blocks = static_cast<std::uint64_t>(p.blocksM) * p.blocksN;
@@ -219,10 +298,15 @@ TnPlan tn_plan(std::uint32_t K, std::uint32_t M, std::uint32_t N) {
     return p;
 }
 
-template <int TM, int TN, int WM, int WN, int U>
+template <int TM, int TN, int WM, int WN, int U, int CT = 0>
 void tn_launch(const TnArgs& a, const TnPlan& p, hipStream_t st) {
-    hipLaunchKernelGGL((tn_partial_kernel<TM, TN, WM, WN, U>), dim3(p.splits, p.blocksM * p.blocksN),
+    hipLaunchKernelGGL((tn_partial_kernel<TM, TN, WM, WN, U, CT>), dim3(p.splits, p.blocksM * p.blocksN),
                        dim3(kWave * WM * WN), 0, st, a);
+}
+
+// The relu-gradient form always takes the wide shapes (N is the hidden width).
+TnPlan relu_grad_plan(std::uint32_t K, std::uint32_t F, std::uint32_t Hd) {
+    return tn_plan(K, std::max<std::uint32_t>(F, 17), std::max<std::uint32_t>(Hd, 17), F, Hd);
 }
 
 }  // namespace
@@ -281,6 +365,70 @@ int tcc_dense_tn(const float* A, std::uint32_t lda, const float* B, std::uint32_
     const std::uint64_t MN = static_cast<std::uint64_t>(M) * N;
     hipLaunchKernelGGL(tn_reduce_kernel, dim3(grid_for(MN, 16)), dim3(256), 0, st,
                        static_cast<const float*>(workspace), p.splits, M, N, C, ldc, accumulate);
+    TCC_LAUNCH_CHECK();
+    return TCC_OK;
+}
+
+size_t tcc_gcn_relu_grad_workspace_bytes(std::uint32_t K, std::uint32_t F, std::uint32_t Hd, std::uint32_t C) {
+    if (K == 0 || F == 0 || Hd == 0 || C == 0) return 0;
+    const TnPlan p = relu_grad_plan(K, F, Hd);
+    return static_cast<size_t>(p.splits) * (static_cast<size_t>(F) * Hd + static_cast<size_t>(Hd) * C) *
+           sizeof(float);
+}
+
+int tcc_gcn_relu_grad(const float* AX, std::uint32_t ldax, const float* H, std::uint32_t ldh, const float* G,
+                      std::uint32_t ldg, const float* W2, float* dW1, float* dW2, std::uint32_t K, std::uint32_t F,
+                      std::uint32_t Hd, std::uint32_t C, void* workspace, size_t workspaceBytes, void* stream) {
+    clear_last_error();
+    TCC_REQUIRE(dW1 && dW2 && W2 && F >= 1 && Hd >= 1 && C >= 1 && ldax >= F && ldh >= Hd && ldg >= C,
+                TCC_ERR_INVALID_ARGUMENT, "invalid GCN relu-gradient arguments");
+    TCC_REQUIRE(C <= 8, TCC_ERR_UNSUPPORTED, "GCN relu-gradient supports at most 8 classes");
+    TCC_REQUIRE(ldax < (1u << 28) && ldh < (1u << 28) && ldg < (1u << 28), TCC_ERR_UNSUPPORTED,
+                "GCN relu-gradient row strides must be below 2^28");
+    const hipStream_t st = as_stream(stream);
+    if (K == 0) {
+        TCC_HIP_CHECK(fill<float>(dW1, static_cast<std::uint64_t>(F) * Hd, 0.0f, st));
+        TCC_HIP_CHECK(fill<float>(dW2, static_cast<std::uint64_t>(Hd) * C, 0.0f, st));
+        return TCC_OK;
+    }
+    TCC_REQUIRE(AX && H && G && workspace, TCC_ERR_INVALID_ARGUMENT, "invalid GCN relu-gradient arguments");
+    const TnPlan p = relu_grad_plan(K, F, Hd);
+    const size_t need1 = static_cast<size_t>(p.splits) * F * Hd * sizeof(float);
+    const size_t need2 = static_cast<size_t>(p.splits) * Hd * C * sizeof(float);
+    TCC_REQUIRE(workspaceBytes >= need1 + need2, TCC_ERR_INVALID_ARGUMENT,
+                "GCN relu-gradient workspace too small (tcc_gcn_relu_grad_workspace_bytes)");
+    TCC_REQUIRE(static_cast<std::uint64_t>(p.blocksM) * p.blocksN <= 65535, TCC_ERR_UNSUPPORTED,
+                "GCN relu-gradient output too large");
+    TnArgs a{};
+    a.A = AX;
+    a.B = H;
+    a.partial = static_cast<float*>(workspace);
+    a.lda = ldax;
+    a.ldb = ldh;
+    a.K = K;
+    a.M = F;
+    a.N = Hd;
+    a.rowsPerSplit = p.rowsPerSplit;
+    a.blocksM = p.blocksM;
+    a.G = G;
+    a.W2 = W2;
+    a.partial2 = reinterpret_cast<float*>(static_cast<char*>(workspace) + need1);
+    a.ldg = ldg;
+    a.C = C;
+    // C <= 2: the wide tiles; up to 8 classes: 8 waves of TM x 2 tiles and 2
+    // steps per iteration, to hold the G rows in registers (same blocks).
+    const bool two = C <= 2;
+    switch (p.shape) {
+        case TnShape::Wide4: two ? tn_launch<4, 4, 1, 4, 4, 2>(a, p, st) : tn_launch<4, 2, 1, 8, 2, 8>(a, p, st); break;
+        case TnShape::Wide7: two ? tn_launch<7, 4, 1, 4, 4, 2>(a, p, st) : tn_launch<7, 2, 1, 8, 2, 8>(a, p, st); break;
+        default: two ? tn_launch<8, 4, 1, 4, 4, 2>(a, p, st) : tn_launch<8, 2, 1, 8, 2, 8>(a, p, st); break;
+    }
+    TCC_LAUNCH_CHECK();
+    hipLaunchKernelGGL(tn_reduce_kernel, dim3(grid_for(static_cast<std::uint64_t>(F) * Hd, 16)), dim3(256), 0, st,
+                       a.partial, p.splits, F, Hd, dW1, Hd, 0);
+    TCC_LAUNCH_CHECK();
+    hipLaunchKernelGGL(tn_reduce_kernel, dim3(grid_for(static_cast<std::uint64_t>(Hd) * C, 16)), dim3(256), 0, st,
+                       a.partial2, p.splits, Hd, C, dW2, C, 0);
     TCC_LAUNCH_CHECK();
     return TCC_OK;
 }

@@ -30,7 +30,9 @@ BCSR gather.
 
 GCN = conv1 (first layer, F_in -> hidden), ReLU, dropout, conv_final
 (hidden -> classes), weights xavier-uniform (tcgnn_conv_release.py:168-250);
-trained with cross-entropy and Adam (:448-449).
+trained with cross-entropy and Adam (:448-449).  Without dropout and with at
+most 8 classes the two layers run as one autograd node whose backward forms
+both weight gradients in one pass (TwoLayerFunction).
 """
 from __future__ import annotations
 
@@ -165,14 +167,52 @@ class GCNConv(torch.nn.Module):
         return CNICSPMMFunction.apply(graph, source if self.first_layer else None, x, self.weights)
 
 
+class TwoLayerFunction(torch.autograd.Function):
+    """conv_final(relu(conv1(X))) as one autograd node, for a last layer
+    narrower than the hidden one and no dropout (what the layer-by-layer
+    functions compute, with the backward fused):
+      forward : AX = A X (first-layer source), H = relu(AX W1), XW = H W2,
+                out = A XW
+      backward: G = Aᵀ dOut, then one pass over AX, H and G for
+                dW1 = AXᵀ((G W2ᵀ) ⊙ [H > 0]) and dW2 = Hᵀ G
+                (tcc_gcn_relu_grad): G W2ᵀ, the relu mask and the hidden
+                gradient are never written to memory."""
+
+    @staticmethod
+    def forward(ctx, g1: LayerGraph, g2: LayerGraph, source, w1, w2):
+        AX = g1.aggregate(w1.shape[0], source=source)
+        H = torch.relu(torch.mm(AX, w1))
+        out = g2.aggregate(w2.shape[1], x=torch.mm(H, w2).contiguous())
+        ctx.g2 = g2
+        ctx.save_for_backward(AX, H, w2)
+        return out
+
+    @staticmethod
+    def backward(ctx, d_output):
+        AX, H, w2 = ctx.saved_tensors
+        G = ctx.g2.transpose_aggregate(d_output)
+        dw1, dw2 = swtcf.gcn_relu_grad(AX, H, G, w2)
+        return None, None, None, dw1, dw2
+
+
+# Class counts the fused two-layer backward takes (tcc_gcn_relu_grad).
+FUSED_MAX_CLASSES = 8
+
+
 class GCN(torch.nn.Module):
-    def __init__(self, num_features: int, hidden_dim: int, num_classes: int, dropout: float = 0.0):
+    def __init__(self, num_features: int, hidden_dim: int, num_classes: int, dropout: float = 0.0,
+                 fused: bool = True):
         super().__init__()
         self.conv1 = GCNConv(num_features, hidden_dim, first_layer=True)
         self.conv_final = GCNConv(hidden_dim, num_classes)
         self.dropout = torch.nn.Dropout(p=dropout)
+        self.fused = fused
 
     def forward(self, g1: LayerGraph, g2: LayerGraph, source) -> torch.Tensor:
+        w1, w2 = self.conv1.weights, self.conv_final.weights
+        no_dropout = self.dropout.p == 0.0 or not self.training
+        if self.fused and no_dropout and w2.shape[1] < w2.shape[0] and w2.shape[1] <= FUSED_MAX_CLASSES:
+            return TwoLayerFunction.apply(g1, g2, source, w1, w2)
         x = torch.relu(self.conv1(g1, source=source))
         x = self.dropout(x)
         return self.conv_final(g2, x=x)

@@ -365,6 +365,28 @@ def dense_tn(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor | None = None, ac
     return C
 
 
+def gcn_relu_grad(AX: torch.Tensor, H: torch.Tensor, G: torch.Tensor, W2: torch.Tensor,
+                  stream=None) -> tuple[torch.Tensor, torch.Tensor]:
+    """(dW1, dW2) of conv_final(relu(conv1(X))) in one pass (tcc_gcn_relu_grad):
+    dW1 = AXᵀ((G W2ᵀ) ⊙ [H > 0]), dW2 = Hᵀ G, for AX [K x F], H [K x Hd],
+    G [K x C] and W2 [Hd x C]."""
+    AX, H, G = _rows(AX, "AX"), _rows(H, "H"), _rows(G, "G")
+    W2 = _f32(W2, "W2")
+    K, F = AX.shape
+    Hd, C = W2.shape
+    if H.shape != (K, Hd) or G.shape != (K, C):
+        raise ValueError(f"shape mismatch: AX {tuple(AX.shape)}, H {tuple(H.shape)}, G {tuple(G.shape)}, "
+                         f"W2 {tuple(W2.shape)}")
+    dW1 = torch.empty((F, Hd), dtype=torch.float32, device=AX.device)
+    dW2 = torch.empty((Hd, C), dtype=torch.float32, device=AX.device)
+    nbytes = _lib.lib().tcc_gcn_relu_grad_workspace_bytes(K, F, Hd, C)
+    ws = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=AX.device)
+    check(_lib.lib().tcc_gcn_relu_grad(AX.data_ptr(), AX.stride(0), H.data_ptr(), H.stride(0), G.data_ptr(),
+                                       G.stride(0), W2.data_ptr(), dW1.data_ptr(), dW2.data_ptr(), K, F, Hd, C,
+                                       ws.data_ptr(), nbytes, _stream(stream)))
+    return dW1, dW2
+
+
 def spmm_cnic_forward(bcsr: BlockMatrix, bcsc: BlockMatrix, X: torch.Tensor, denseC: torch.Tensor,
                       stream=None) -> torch.Tensor:
     check(_lib.lib().tcc_spmm_cnic_forward(ctypes.byref(bcsr.view), ctypes.byref(bcsc.view), X.data_ptr(),

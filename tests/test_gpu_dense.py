@@ -109,3 +109,50 @@ def test_dense_tn_argument_errors():
                           None) == 0
     torch.cuda.synchronize()
     assert rel_l2(C, A.double().t() @ B.double()) < REL
+
+
+RELU_SHAPES = [(64, 100, 256, 2), (50021, 100, 256, 2), (1999, 20, 48, 3), (3001, 130, 300, 8), (5, 7, 17, 1),
+               (20000, 8, 40, 5), (4099, 257, 129, 2)]
+
+
+@pytest.mark.parametrize("K,F,Hd,C", RELU_SHAPES)
+def test_gcn_relu_grad_matches_float64(K, F, Hd, C):
+    """dW1 = AXᵀ((G W2ᵀ) ⊙ [H > 0]) and dW2 = Hᵀ G against float64; H is a
+    relu output (about half zeros)."""
+    from tcc_amd import swtcf
+
+    g = torch.Generator(device="cpu").manual_seed(K + 7 * F + 13 * Hd + C)
+    AX = torch.randn(K, F, generator=g)
+    H = torch.relu(torch.randn(K, Hd, generator=g))
+    G = torch.randn(K, C, generator=g)
+    W2 = torch.randn(Hd, C, generator=g)
+    dW1, dW2 = swtcf.gcn_relu_grad(AX.cuda(), H.cuda(), G.cuda(), W2.cuda())
+    torch.cuda.synchronize()
+    d = (G.double() @ W2.double().t()) * (H > 0).double()
+    assert rel_l2(dW1, AX.double().t() @ d) < REL
+    assert rel_l2(dW2, H.double().t() @ G.double()) < REL
+
+
+def test_gcn_relu_grad_strided_and_limits():
+    from tcc_amd import _lib, swtcf
+
+    K, F, Hd, C = 7001, 100, 256, 2
+    g = torch.Generator(device="cpu").manual_seed(3)
+    AXw = torch.randn(K, F + 4, generator=g).cuda()
+    Hw = torch.relu(torch.randn(K, Hd + 8, generator=g)).cuda()
+    Gw = torch.randn(K, C + 1, generator=g).cuda()
+    W2 = torch.randn(Hd, C, generator=g).cuda()
+    AX, H, G = AXw[:, :F], Hw[:, 8:], Gw[:, 1:]
+    dW1, dW2 = swtcf.gcn_relu_grad(AX, H, G, W2)
+    torch.cuda.synchronize()
+    d = (G.double() @ W2.double().t()) * (H > 0).double()
+    assert rel_l2(dW1, AX.double().t() @ d) < REL
+    assert rel_l2(dW2, H.double().t() @ G.double()) < REL
+    L = _lib.lib()
+    W9 = torch.randn(Hd, 9, device="cuda")
+    G9 = torch.randn(K, 9, device="cuda")
+    out1 = torch.empty(F, Hd, device="cuda")
+    out2 = torch.empty(Hd, 9, device="cuda")
+    assert L.tcc_gcn_relu_grad(AX.data_ptr(), F + 4, H.data_ptr(), Hd + 8, G9.data_ptr(), 9, W9.data_ptr(),
+                               out1.data_ptr(), out2.data_ptr(), K, F, Hd, 9, None, 0, None) == 3
+    assert b"at most 8 classes" in L.tcc_last_error()

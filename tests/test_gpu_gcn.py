@@ -87,6 +87,35 @@ def test_gcn_step_matches_dense_reference(gpu, hot_fraction):
 
 
 @pytest.mark.gpu
+def test_fused_two_layer_matches_layer_by_layer(gpu):
+    """TwoLayerFunction (one autograd node, fused weight gradients) against
+    the layer-by-layer functions on the same weights: outputs and both
+    weight gradients within fp32 rounding."""
+    from tcc_amd import gcn
+    from tcc_amd.graphs import rmat_graph
+
+    n, F, H, C = 4093, 100, 256, 2
+    rows, cols = rmat_graph(n, 60_000, 21)
+    torch.manual_seed(2)
+    X = torch.randn((n, F))
+    table = gcn.FeatureTable(X, cols)
+    g1, g2 = gcn.build_gcn_graphs(rows, cols, n, table.hot)
+    model = gcn.GCN(F, H, C).cuda()
+    labels = gcn.synthetic_labels(n, C, 4)
+    res = []
+    for fused in (True, False):
+        model.fused = fused
+        model.zero_grad(set_to_none=True)
+        pred = model(g1, g2, table.source)
+        gcn.cross_entropy(pred, labels).backward()
+        res.append((pred.detach().clone(), model.conv1.weights.grad.clone(), model.conv_final.weights.grad.clone()))
+    torch.cuda.synchronize()
+    for a, b in zip(res[0], res[1]):
+        assert rel_l2(a.cpu().numpy(), b.double().cpu().numpy()) < 1e-5
+    table.free()
+
+
+@pytest.mark.gpu
 def test_gcn_trains(gpu):
     """A few Adam steps on a small graph lower the loss (the full training
     step of tcgnn_conv_release.py:284-329)."""
