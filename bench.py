@@ -347,8 +347,9 @@ def bench_gcn(args, torch, swtcf, cfg):
 
     l1 = timed(layer1, steps, warmup)
     l2 = timed(layer2, steps, warmup)
-    extra = {"epoch": "TwoLayerFunction: mixed SpMM F=100, GEMM 100x256 + relu, GEMM 256x2, SpMM F=2; backward "
-                      "A^T SpMM F=2, then dW1 and dW2 in one pass (tcc_gcn_relu_grad), cross-entropy, Adam",
+    extra = {"epoch": "TwoLayerFunction: mixed SpMM F=100 (one launch), relu(AX W1) and H W2 in one pass "
+                      "(tcc_gcn_relu_forward), SpMM F=2; backward A^T SpMM F=2, then dW1 and dW2 in one pass "
+                      "(tcc_gcn_relu_grad); cross-entropy, Adam",
              "layer_times": "each layer alone, through its own autograd function",
              "layer1_fwd_bwd_ms": round(l1, 4), "layer2_fwd_bwd_ms": round(l2, 4),
              "layer1": f"mixed SpMM F={F} (hot BCSR + cold BCSC) + GEMM {F}x{hidden}; backward dW GEMM",

@@ -40,6 +40,18 @@ size_t tcc_dense_tn_workspace_bytes(uint32_t K, uint32_t M, uint32_t N);
 int tcc_dense_tn(const float* A, uint32_t lda, const float* B, uint32_t ldb, float* C, uint32_t ldc, uint32_t K,
                  uint32_t M, uint32_t N, int accumulate, void* workspace, size_t workspaceBytes, void* stream);
 
+/* H = relu(AX W1) [K x Hd] and XW = H W2 [K x C] in one pass over the K
+ * rows of AX [K x F] (row strides ldax, ldh, ldxw; W1 [F x Hd] and W2
+ * [Hd x C] row-major): the first layer's transform and activation and the
+ * second layer's transform of a two-layer GCN, which the reference runs as
+ * X_gat = torch.mm(X_out, weights) (train/tcgnn_conv_release.py:134),
+ * self.relu (:231-238) and the last layer's torch.mm (:134 again) with H
+ * written and read back in between.  fp32 MFMA products and sums; relu
+ * keeps NaN (clamp_min).  F <= 128, Hd <= 256, C <= 4 (TCC_ERR_UNSUPPORTED
+ * above).  No workspace. */
+int tcc_gcn_relu_forward(const float* AX, uint32_t ldax, const float* W1, const float* W2, float* H, uint32_t ldh,
+                         float* XW, uint32_t ldxw, uint32_t K, uint32_t F, uint32_t Hd, uint32_t C, void* stream);
+
 /* Bytes of device workspace tcc_gcn_relu_grad needs (current device). */
 size_t tcc_gcn_relu_grad_workspace_bytes(uint32_t K, uint32_t F, uint32_t Hd, uint32_t C);
 

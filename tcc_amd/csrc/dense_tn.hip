@@ -221,6 +221,147 @@ __global__ void __launch_bounds__(kWave * WM * WN) tn_partial_kernel(TnArgs a) {
     }
 }
 
+// ---------------------------------------------------------------- forward
+// H = relu(AX W1) [K x Hd] and XW = H W2 [K x C] in one pass over the rows
+// of AX (the first layer's transform, its activation and the second layer's
+// transform of a two-layer GCN; tcgnn_conv_release.py:134 and :243-247).
+//
+// A wave computes 16 rows x 256 hidden units (16 tiles of 16x16) over
+// F <= 16*KB inputs with v_mfma_f32_16x16x4f32.  Lane (q = l/16, i = l%16)
+// loads AX[row0 + i][16b + 4q .. +3] as one float4 per block b of 16 inputs,
+// and MFMA step s of block b takes input 16b + 4q + s on lane quarter q: the
+// sum over the 16 inputs is the same in any order, so the four steps come
+// from one float4 instead of four strided loads.  The matching B operands,
+// W1[16b + 4q + s][16u + i] for s = 0..3, are one ds_read_b128 from W1^T
+// held in LDS (row pitch 16*KB + 4 floats: conflict-free b128 reads).
+// Relu, the store of H and the row sums of H W2 (a 16-lane butterfly) follow
+// in registers.  Workgroups (8 waves, one per CU for the LDS copy of W1^T)
+// are persistent over 16-row tiles, the next tile's AX rows loaded during
+// the current tile's products.
+struct ReluFwdArgs {
+    const float* AX;
+    const float* W1;  // [F x Hd]
+    const float* W2;  // [Hd x C]
+    float* H;
+    float* XW;
+    std::uint32_t ldax, ldh, ldxw;
+    std::uint32_t K, F, Hd, C;
+    std::uint32_t tiles;  // ceil(K / 16)
+    int vec;              // AX rows allow float4 loads
+};
+
+constexpr unsigned kFwdWaves = 8;
+constexpr int kFwdTiles = 16;  // 16 tiles of 16 hidden units per wave
+
+template <int KB>
+__device__ __forceinline__ void fwd_load_rows(const ReluFwdArgs& a, std::uint32_t tile, float4 (&x)[KB]) {
+    const unsigned lane = __lane_id();
+    const std::uint32_t row = tile * 16 + (lane & 15u);
+    const unsigned q = lane >> 4;
+#pragma unroll
+    for (int b = 0; b < KB; ++b) {
+        const std::uint32_t k = 16 * b + 4 * q;
+        x[b] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (row >= a.K || tile >= a.tiles) continue;
+        const float* p = a.AX + static_cast<std::uint64_t>(row) * a.ldax + k;
+        if (a.vec && k + 3 < a.F) {
+            x[b] = *reinterpret_cast<const float4*>(p);
+        } else {
+            if (k < a.F) x[b].x = p[0];
+            if (k + 1 < a.F) x[b].y = p[1];
+            if (k + 2 < a.F) x[b].z = p[2];
+            if (k + 3 < a.F) x[b].w = p[3];
+        }
+    }
+}
+
+template <int KB, int CT>
+__global__ void __launch_bounds__(kWave * kFwdWaves) gcn_relu_forward_kernel(ReluFwdArgs a) {
+    constexpr int KP = 16 * KB + 4;  // LDS row pitch of W1^T (floats)
+    extern __shared__ float w1t[];   // [256][KP], then W2 [256][CT]
+    const unsigned lane = __lane_id();
+    const unsigned i = lane & 15u, q = lane >> 4;
+    const unsigned wave = tn_uniform(threadIdx.x / kWave);
+
+    // W1^T into LDS, zeros past F and Hd.
+    for (std::uint32_t e = threadIdx.x; e < 256u * KP; e += blockDim.x) {
+        const std::uint32_t n = e / KP, k = e - n * KP;
+        w1t[e] = (n < a.Hd && k < a.F) ? a.W1[static_cast<std::uint64_t>(k) * a.Hd + n] : 0.0f;
+    }
+    // W2 [256][CT] after it, zeros past Hd and C.
+    float* w2 = w1t + 256 * KP;
+    for (std::uint32_t e = threadIdx.x; e < 256u * CT; e += blockDim.x) {
+        const std::uint32_t n = e / CT, j = e - n * CT;
+        w2[e] = (n < a.Hd && j < a.C) ? a.W2[static_cast<std::uint64_t>(n) * a.C + j] : 0.0f;
+    }
+    __syncthreads();
+
+    const std::uint32_t stride = gridDim.x * kFwdWaves;
+    std::uint32_t tile = blockIdx.x * kFwdWaves + wave;
+    float4 x[KB];
+    fwd_load_rows<KB>(a, tile, x);
+    for (; tile < a.tiles; tile += stride) {
+        float4 nx[KB];
+        fwd_load_rows<KB>(a, tile + stride, nx);  // past the last tile: zeros, no loads
+        __builtin_amdgcn_sched_barrier(0);
+        f32x4 acc[kFwdTiles];
+#pragma unroll
+        for (int u = 0; u < kFwdTiles; ++u) acc[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int b = 0; b < KB; ++b) {
+#pragma unroll
+            for (int u = 0; u < kFwdTiles; ++u) {
+                const float4 w = *reinterpret_cast<const float4*>(&w1t[(16 * u + i) * KP + 16 * b + 4 * q]);
+                acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[b].x, w.x, acc[u], 0, 0, 0);
+                acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[b].y, w.y, acc[u], 0, 0, 0);
+                acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[b].z, w.z, acc[u], 0, 0, 0);
+                acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[b].w, w.w, acc[u], 0, 0, 0);
+            }
+        }
+        // Lane holds H(row0 + 4q + v, 16u + i): relu (NaN kept, as clamp_min),
+        // store, and this lane's part of the row sums of H W2.
+        const std::uint32_t row0 = tile * 16 + 4 * q;
+        float xw[4][CT];
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+            for (int j = 0; j < CT; ++j) xw[v][j] = 0.0f;
+#pragma unroll
+        for (int u = 0; u < kFwdTiles; ++u) {
+            const std::uint32_t n = 16 * u + i;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float h = acc[u][v] < 0.0f ? 0.0f : acc[u][v];
+                if (row0 + v < a.K && n < a.Hd) a.H[static_cast<std::uint64_t>(row0 + v) * a.ldh + n] = h;
+#pragma unroll
+                for (int j = 0; j < CT; ++j) xw[v][j] = fmaf(h, w2[n * CT + j], xw[v][j]);
+            }
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+            for (int j = 0; j < CT; ++j) {
+                float t = xw[v][j];
+                t += __shfl_xor(t, 1);
+                t += __shfl_xor(t, 2);
+                t += __shfl_xor(t, 4);
+                t += __shfl_xor(t, 8);
+                if (i == 0 && row0 + v < a.K && static_cast<std::uint32_t>(j) < a.C)
+                    a.XW[static_cast<std::uint64_t>(row0 + v) * a.ldxw + j] = t;
+            }
+#pragma unroll
+        for (int b = 0; b < KB; ++b) x[b] = nx[b];
+    }
+}
+
+template <int KB, int CT>
+void relu_forward_launch(const ReluFwdArgs& a, hipStream_t st) {
+    const std::uint32_t lds = 256u * (16 * KB + 4 + CT) * sizeof(float);
+    const std::uint32_t grid = std::min<std::uint32_t>(device_cus(), (a.tiles + kFwdWaves - 1) / kFwdWaves);
+    hipLaunchKernelGGL((gcn_relu_forward_kernel<KB, CT>), dim3(std::max<std::uint32_t>(grid, 1)),
+                       dim3(kWave * kFwdWaves), lds, st, a);
+}
+
 // C[m][n] (=|+=) sum over splits of partial[s][m][n], splits added in a fixed
 // order: 16 elements per workgroup, 16 interleaved groups of splits summed
 // per thread, then the 16 group sums in order.
@@ -365,6 +506,40 @@ int tcc_dense_tn(const float* A, std::uint32_t lda, const float* B, std::uint32_
     const std::uint64_t MN = static_cast<std::uint64_t>(M) * N;
     hipLaunchKernelGGL(tn_reduce_kernel, dim3(grid_for(MN, 16)), dim3(256), 0, st,
                        static_cast<const float*>(workspace), p.splits, M, N, C, ldc, accumulate);
+    TCC_LAUNCH_CHECK();
+    return TCC_OK;
+}
+
+int tcc_gcn_relu_forward(const float* AX, std::uint32_t ldax, const float* W1, const float* W2, float* H,
+                         std::uint32_t ldh, float* XW, std::uint32_t ldxw, std::uint32_t K, std::uint32_t F,
+                         std::uint32_t Hd, std::uint32_t C, void* stream) {
+    clear_last_error();
+    TCC_REQUIRE(W1 && W2 && H && XW && F >= 1 && Hd >= 1 && C >= 1 && ldax >= F && ldh >= Hd && ldxw >= C,
+                TCC_ERR_INVALID_ARGUMENT, "invalid GCN relu-forward arguments");
+    TCC_REQUIRE(F <= 128 && Hd <= 256 && C <= 4, TCC_ERR_UNSUPPORTED,
+                "GCN relu-forward supports F <= 128, hidden <= 256 and at most 4 classes");
+    if (K == 0) return TCC_OK;
+    TCC_REQUIRE(AX != nullptr, TCC_ERR_INVALID_ARGUMENT, "invalid GCN relu-forward arguments");
+    ReluFwdArgs a{};
+    a.AX = AX;
+    a.W1 = W1;
+    a.W2 = W2;
+    a.H = H;
+    a.XW = XW;
+    a.ldax = ldax;
+    a.ldh = ldh;
+    a.ldxw = ldxw;
+    a.K = K;
+    a.F = F;
+    a.Hd = Hd;
+    a.C = C;
+    a.tiles = (K + 15) / 16;
+    a.vec = (ldax % 4 == 0) && (reinterpret_cast<std::uintptr_t>(AX) % 16 == 0);
+    const hipStream_t st = as_stream(stream);
+    const bool two = C <= 2;
+    if (F <= 64) two ? relu_forward_launch<4, 2>(a, st) : relu_forward_launch<4, 4>(a, st);
+    else if (F <= 112) two ? relu_forward_launch<7, 2>(a, st) : relu_forward_launch<7, 4>(a, st);
+    else two ? relu_forward_launch<8, 2>(a, st) : relu_forward_launch<8, 4>(a, st);
     TCC_LAUNCH_CHECK();
     return TCC_OK;
 }

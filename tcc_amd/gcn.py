@@ -171,8 +171,9 @@ class TwoLayerFunction(torch.autograd.Function):
     """conv_final(relu(conv1(X))) as one autograd node, for a last layer
     narrower than the hidden one and no dropout (what the layer-by-layer
     functions compute, with the backward fused):
-      forward : AX = A X (first-layer source), H = relu(AX W1), XW = H W2,
-                out = A XW
+      forward : AX = A X (first-layer source), then H = relu(AX W1) and
+                XW = H W2 in one pass (tcc_gcn_relu_forward, F <= 128,
+                hidden <= 256, classes <= 4), out = A XW
       backward: G = Aᵀ dOut, then one pass over AX, H and G for
                 dW1 = AXᵀ((G W2ᵀ) ⊙ [H > 0]) and dW2 = Hᵀ G
                 (tcc_gcn_relu_grad): G W2ᵀ, the relu mask and the hidden
@@ -181,8 +182,12 @@ class TwoLayerFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, g1: LayerGraph, g2: LayerGraph, source, w1, w2):
         AX = g1.aggregate(w1.shape[0], source=source)
-        H = torch.relu(torch.mm(AX, w1))
-        out = g2.aggregate(w2.shape[1], x=torch.mm(H, w2).contiguous())
+        if swtcf.gcn_relu_forward_supported(w1.shape[0], w1.shape[1], w2.shape[1]):
+            H, XW = swtcf.gcn_relu_forward(AX, w1, w2)  # one pass, H written once
+        else:
+            H = torch.relu(torch.mm(AX, w1))
+            XW = torch.mm(H, w2).contiguous()
+        out = g2.aggregate(w2.shape[1], x=XW)
         ctx.g2 = g2
         ctx.save_for_backward(AX, H, w2)
         return out

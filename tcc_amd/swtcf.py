@@ -365,6 +365,27 @@ def dense_tn(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor | None = None, ac
     return C
 
 
+def gcn_relu_forward_supported(F: int, Hd: int, C: int) -> bool:
+    return F <= 128 and Hd <= 256 and C <= 4
+
+
+def gcn_relu_forward(AX: torch.Tensor, W1: torch.Tensor, W2: torch.Tensor,
+                     stream=None) -> tuple[torch.Tensor, torch.Tensor]:
+    """(H, XW) = (relu(AX W1), H W2) in one pass (tcc_gcn_relu_forward), for
+    AX [K x F], W1 [F x Hd], W2 [Hd x C]."""
+    AX = _rows(AX, "AX")
+    W1, W2 = _f32(W1, "W1"), _f32(W2, "W2")
+    K, F = AX.shape
+    Hd, C = W2.shape
+    if W1.shape != (F, Hd):
+        raise ValueError(f"shape mismatch: AX {tuple(AX.shape)}, W1 {tuple(W1.shape)}, W2 {tuple(W2.shape)}")
+    H = torch.empty((K, Hd), dtype=torch.float32, device=AX.device)
+    XW = torch.empty((K, C), dtype=torch.float32, device=AX.device)
+    check(_lib.lib().tcc_gcn_relu_forward(AX.data_ptr(), AX.stride(0), W1.data_ptr(), W2.data_ptr(), H.data_ptr(),
+                                          Hd, XW.data_ptr(), C, K, F, Hd, C, _stream(stream)))
+    return H, XW
+
+
 def gcn_relu_grad(AX: torch.Tensor, H: torch.Tensor, G: torch.Tensor, W2: torch.Tensor,
                   stream=None) -> tuple[torch.Tensor, torch.Tensor]:
     """(dW1, dW2) of conv_final(relu(conv1(X))) in one pass (tcc_gcn_relu_grad):

@@ -156,3 +156,54 @@ def test_gcn_relu_grad_strided_and_limits():
     assert L.tcc_gcn_relu_grad(AX.data_ptr(), F + 4, H.data_ptr(), Hd + 8, G9.data_ptr(), 9, W9.data_ptr(),
                                out1.data_ptr(), out2.data_ptr(), K, F, Hd, 9, None, 0, None) == 3
     assert b"at most 8 classes" in L.tcc_last_error()
+
+
+FWD_SHAPES = [(16, 100, 256, 2), (50021, 100, 256, 2), (1999, 20, 48, 3), (3001, 128, 200, 4), (5, 7, 17, 1),
+              (20000, 64, 256, 2), (1, 1, 1, 1), (17, 113, 256, 4), (4093, 99, 256, 2)]
+
+
+@pytest.mark.parametrize("K,F,Hd,C", FWD_SHAPES)
+def test_gcn_relu_forward_matches_float64(K, F, Hd, C):
+    """H = relu(AX W1) and XW = H W2 against float64 (F = 99, 113: the
+    element-wise load path; F = 7: a partial input block)."""
+    from tcc_amd import swtcf
+
+    g = torch.Generator(device="cpu").manual_seed(K + 3 * F + 5 * Hd + C)
+    AX = torch.randn(K, F, generator=g)
+    W1 = torch.randn(F, Hd, generator=g) / F ** 0.5
+    W2 = torch.randn(Hd, C, generator=g)
+    H, XW = swtcf.gcn_relu_forward(AX.cuda(), W1.cuda(), W2.cuda())
+    torch.cuda.synchronize()
+    H64 = torch.relu(AX.double() @ W1.double())
+    assert rel_l2(H, H64) < REL
+    assert rel_l2(XW, H64 @ W2.double()) < REL
+
+
+def test_gcn_relu_forward_strided_nan_and_limits():
+    from tcc_amd import _lib, swtcf
+
+    K, F, Hd, C = 3001, 100, 256, 2
+    g = torch.Generator(device="cpu").manual_seed(9)
+    AXw = torch.randn(K, F + 12, generator=g)
+    AXw[77, 5] = float("nan")
+    AX = AXw[:, 4:4 + F]
+    W1 = torch.randn(F, Hd, generator=g) / 10
+    W2 = torch.randn(Hd, C, generator=g)
+    H, XW = swtcf.gcn_relu_forward(AX.cuda(), W1.cuda(), W2.cuda())
+    torch.cuda.synchronize()
+    H64 = torch.relu(AX.double() @ W1.double())
+    ok = torch.ones(K, dtype=torch.bool)
+    ok[77] = False
+    assert rel_l2(H[ok.cuda()], H64[ok]) < REL
+    assert rel_l2(XW[ok.cuda()], (H64 @ W2.double())[ok]) < REL
+    # relu keeps NaN (torch.relu is clamp_min), as does H W2
+    assert torch.isnan(H[77]).all() and torch.isnan(XW[77]).all()
+    L = _lib.lib()
+    X = torch.zeros(4, 129, device="cuda")
+    w1 = torch.zeros(129, 8, device="cuda")
+    w2 = torch.zeros(8, 2, device="cuda")
+    h = torch.empty(4, 8, device="cuda")
+    xw = torch.empty(4, 2, device="cuda")
+    assert L.tcc_gcn_relu_forward(X.data_ptr(), 129, w1.data_ptr(), w2.data_ptr(), h.data_ptr(), 8, xw.data_ptr(), 2,
+                                  4, 129, 8, 2, None) == 3
+    assert b"F <= 128" in L.tcc_last_error()
