@@ -1,8 +1,12 @@
 // SWTCF SpMM on gfx950 (reference: src/swtcf_spmm.cu).
 //
 // Y += A X with A in SWTCF.  One 1024-thread workgroup (16 waves) per
-// (super-window, 64-feature chunk); wave i walks column windows i, i+16, ...
-// of the super-window (one each for the reference's S = 16).  A wave keeps
+// (super-window, 64-feature chunk, part); wave i walks column windows i,
+// i+16, ... of the super-window (one each for the reference's S = 16), and
+// part z of Z takes the z-th slice of each window's tiles.  Z > 1 when there
+// are too few super-windows to fill the GPU (config 1: 32 super-windows on
+// 256 CUs); every part keeps its own LDS repeat cache and flushes it with
+// atomics, so the parts add up.  A wave keeps
 // its window's 8 source rows of X in registers (one feature per lane, fp32
 // and TF32-rounded copies), so X is read exactly once.  The destinations of
 // 8 tiles at a time are resolved with vector loads one group ahead (lane
@@ -77,6 +81,7 @@ __global__ void __launch_bounds__(kThreads) swtcf_spmm_kernel(
     __shared__ float cache[TCC_SWTCF_REPEAT_CACHE_SIZE][kChunk];
 
     const std::uint32_t s = blockIdx.x;
+    const std::uint32_t z = blockIdx.z, Z = gridDim.z;
     const unsigned lane = __lane_id();
     const unsigned wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const std::uint32_t f = blockIdx.y * kChunk + lane;
@@ -90,7 +95,10 @@ __global__ void __launch_bounds__(kThreads) swtcf_spmm_kernel(
     for (std::uint32_t wi = wave; wi < S; wi += kWaves) {
         const std::uint32_t w = s * S + wi;
         if (w >= CW) break;
-        const std::uint32_t t0 = colWindowOffset[w], t1 = colWindowOffset[w + 1];
+        const std::uint32_t w0 = colWindowOffset[w], w1 = colWindowOffset[w + 1];
+        const std::uint32_t per = (w1 - w0 + Z - 1) / Z;
+        const std::uint32_t t0 = min(w1, w0 + z * per), t1 = min(w1, t0 + per);
+        if (t0 >= t1) continue;
         float xv[8], xt[8];
         // all loads in flight before any is rounded
 #pragma unroll
@@ -156,7 +164,14 @@ __global__ void __launch_bounds__(kThreads) swtcf_spmm_kernel(
 template <bool QUANT>
 int launch(const tcc_swtcf_matrix* m, const float* X, const std::int8_t* qX, const float* scales,
            const std::uint32_t* srcGlobal, float* Y, std::uint32_t F, std::uint32_t tc, void* stream) {
-    const dim3 grid(m->numSuperWindows, (F + kChunk - 1) / kChunk);
+    // Parts per super-window: enough workgroups for two per CU, at most 8,
+    // and no more than one per 16 edges of an average window.
+    const std::uint32_t chunks = (F + kChunk - 1) / kChunk;
+    const std::uint64_t wgs = static_cast<std::uint64_t>(m->numSuperWindows) * chunks;
+    std::uint64_t Z = (2ull * device_cus() + wgs - 1) / wgs;
+    const std::uint64_t perWindow = m->numColWindows ? m->nnz / m->numColWindows : 0;
+    Z = std::max<std::uint64_t>(1, std::min<std::uint64_t>({Z, 8, perWindow / 16}));
+    const dim3 grid(m->numSuperWindows, chunks, static_cast<std::uint32_t>(Z));
     hipLaunchKernelGGL(swtcf_spmm_kernel<QUANT>, grid, dim3(kThreads), 0, as_stream(stream),
                        m->superWindowRowOffset, m->superWindowRows, m->superWindowRowCacheSlot,
                        m->superWindowCachedRowSlot, m->superWindowCachedCount, m->colWindowOffset, m->tileRowSlot,

@@ -290,6 +290,51 @@ def test_mixed_hot_cold_feature_source(gpu, oracle):
     cpu.free()
 
 
+@pytest.mark.parametrize("F,vals_hot,vals_cold,K", [(37, True, True, 0), (100, True, False, 3), (100, False, True, 0),
+                                                    (256, True, True, 5), (100, False, False, 2)])
+def test_mixed_forward_values_widths_units(gpu, oracle, F, vals_hot, vals_cold, K):
+    """The first-layer forward in one launch (hot gather and cold scatter
+    interleaved, both adding into a zeroed denseC): every value combination,
+    V = 1, 2, 4 and unit sizes that split windows, against the CSR oracle on
+    the resolved features."""
+    from tcc_amd import swtcf
+    from tcc_amd.hostmem import PinnedArray
+
+    nr = nc = 1500
+    dst, src = random_coo(nr, nc, 30000, 40 + F)
+    rng = np.random.default_rng(41 + F)
+    vals = rng.uniform(0.5, 1.5, dst.size).astype(np.float32)
+    feats = rng.standard_normal((nc, F)).astype(np.float32)
+    hot_ids = np.sort(rng.choice(nc, size=nc // 4, replace=False))
+    csm = np.full(nc, -1, np.int32)
+    csm[hot_ids] = np.arange(hot_ids.size, dtype=np.int32)
+    id_map = np.arange(nc, dtype=np.int32)
+    hot_cache = torch.from_numpy(feats[hot_ids]).cuda()
+    cpu = PinnedArray((nc, F))
+    cpu.array[:] = feats
+    ptrs = torch.tensor([hot_cache.data_ptr()], dtype=torch.int64, device="cuda")
+    id_map_d = torch.from_numpy(id_map).cuda()
+    csm_d = torch.from_numpy(csm).cuda()
+    src_desc = swtcf.feature_source(id_map_d, csm_d, ptrs, hot_ids.size, cpu.device_ptr, nc * F)
+    h = csm[src] >= 0
+    vh = torch.from_numpy(vals[h]).cuda() if vals_hot else None
+    vc = torch.from_numpy(vals[~h]).cuda() if vals_cold else None
+    A = swtcf.coo_to_bcsr(dev_u32(dst[h]), dev_u32(src[h]), vh, nr, nc)
+    B = swtcf.coo_to_bcsc(dev_u32(dst[~h]), dev_u32(src[~h]), vc, nr, nc)
+    A.set_unit_blocks(K)
+    B.set_unit_blocks(K)
+    denseC = torch.full(((A.view.num_rowWindows + 1) * 8, F), 3.0, device="cuda")  # garbage in
+    swtcf.spmm_cnic_forward_mixed(A, B, src_desc, denseC, F)
+    used = np.where(h, vals if vals_hot else 1.0, vals if vals_cold else 1.0).astype(np.float32)
+    rowptr, colind, v = csr_of(dst, src, nr, used)
+    want = oracle.csr_spmm(rowptr, colind, v, feats, use_tf32=True)
+    C = denseC.cpu().numpy()
+    assert_close(C[:nr], want)
+    assert np.all(C[nr:] == 0)
+    torch.cuda.synchronize()
+    cpu.free()
+
+
 # ------------------------------------------------------------------ units of work
 def skewed_coo(nr, nc, seed):
     """A few dense hub rows and hub columns over a sparse background, with
