@@ -27,6 +27,7 @@ import json
 import os
 import sys
 import time
+import warnings
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
@@ -95,6 +96,42 @@ def cpu_baseline(rows, cols, vals, X, n, threads, Y_gpu, max_nnz):
     yg = Y_gpu[:R].cpu().numpy().astype(np.float64)
     rel = float(np.linalg.norm(yg - Y) / max(np.linalg.norm(Y), 1e-30))
     return t, threads, rel, R, nz
+
+
+def torch_sparse_cpu(rows, cols, vals, X, n, threads, max_nnz):
+    """The reference's own SpMM call, torch.sparse.mm (train/tcgnn_conv_release.py:152),
+    on the host cores in fp32 with a CSR tensor, over the same leading-rows
+    sample as cpu_baseline: median of 5 after 1 warm-up."""
+    import numpy as np
+    import torch
+
+    from tcc_amd.graphs import to_csr_numpy
+
+    threads = threads or os.cpu_count() or 1
+    rowptr, colind, v = to_csr_numpy(rows, cols, n, vals)
+    R = max(1, min(n, int(np.searchsorted(rowptr, max_nnz, side="right")) - 1))
+    nz = int(rowptr[R])
+    vv = np.ones(nz, np.float32) if v is None else np.asarray(v[:nz], np.float32)
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")  # "sparse CSR support is in beta"
+        A = torch.sparse_csr_tensor(torch.from_numpy(rowptr[: R + 1].astype(np.int64)),
+                                    torch.from_numpy(colind[:nz].astype(np.int64)), torch.from_numpy(vv), size=(R, n))
+    Xc = X.cpu()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        torch.sparse.mm(A, Xc)
+        ts = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            torch.sparse.mm(A, Xc)
+            ts.append(time.perf_counter() - t0)
+    finally:
+        torch.set_num_threads(prev)
+    t = sorted(ts)[len(ts) // 2]
+    return {"value": round(2.0 * nz * X.shape[1] / t / 1e9, 3), "unit": "GFLOP/s", "cores": threads,
+            "ms": round(t * 1e3, 3), "nnz": nz,
+            "what": "torch.sparse.mm (CSR, fp32) on the host cores, the reference's own SpMM call, same sample"}
 
 
 def timed(step, steps, warmup):
@@ -234,6 +271,7 @@ def bench_spmm(args, torch, swtcf, cfg):
         cpu = cpu_entry(t_cpu, threads, nz, nnz, R, F, args.config)
         extra["parity_rel_l2_vs_cpu"] = rel
         extra["parity_rows"] = R
+        extra["cpu_torch_sparse_mm"] = torch_sparse_cpu(rows, cols, vals, X, n, args.cpu_threads, 16_000_000)
     roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic_of(args.config), "kernel": kernel,
                 "bytes_alg_per_launch": b_alg}
@@ -289,6 +327,7 @@ def bench_mixed(args, torch, swtcf, cfg):
         cpu = cpu_entry(t_cpu, threads, nz, nnz, R, F, 4)
         extra["parity_rel_l2_vs_cpu"] = rel
         extra["parity_rows"] = R
+        extra["cpu_torch_sparse_mm"] = torch_sparse_cpu(rows, cols, None, X, n, args.cpu_threads, 16_000_000)
     # One launch (mixed_forward_kernel) interleaves the HBM-bound hot gather
     # with the scatter of cold rows read across the host link; the link bounds
     # it: the cold rows' bytes over PCIe Gen5 x16 (64 GB/s per direction).

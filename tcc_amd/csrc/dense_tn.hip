@@ -401,7 +401,9 @@ __global__ void __launch_bounds__(256) tn_reduce_kernel(const float* __restrict_
 //    (TM = 4, 7 or 8, the fewest that cover M, so that a 100-wide layer does
 //    not multiply a 128-wide tile column); 4 tiles along N reuse each A
 //    operand 4 times from registers: 100x256 runs at ~100 TFLOP/s, against
-//    ~50 with 8 waves of 7x2 tiles;
+//    ~50 with 8 waves of 7x2 tiles.  These waves hold ~340 registers (one
+//    wave per SIMD); limiting them to 256 for two waves per SIMD measured
+//    1.6-1.9x slower;
 //  - N <= 16 (a class-width gradient): 4 waves along M with 4 x 1 tiles,
 //    eight workgroups per CU for memory parallelism (~5 TB/s for 256x2);
 //    M <= 16 the same along N.
