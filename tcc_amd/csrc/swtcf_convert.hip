@@ -148,33 +148,58 @@ __global__ void group_emit_kernel(const std::uint64_t* __restrict__ keys, std::u
 
 // countWindowDegreesKernel (:147-213) + buildTileBitmapsKernel's row bits
 // (:408-428) + the row-head flags of the distinct (super-window, dst) rows.
-__global__ void group_finalize_kernel(const std::uint64_t* __restrict__ keys,
-                                      const std::uint64_t* __restrict__ groupKey,
-                                      const std::uint32_t* __restrict__ groupStart,
-                                      const std::uint32_t* __restrict__ numGroups, std::uint32_t E,
-                                      std::uint32_t S, unsigned wiBits, unsigned dstBits,
-                                      std::uint32_t* __restrict__ groupInfo, std::uint32_t* __restrict__ wdCount,
-                                      std::uint32_t* __restrict__ rowFlags, std::uint32_t* __restrict__ err) {
-    const std::uint32_t g = blockIdx.x * blockDim.x + threadIdx.x;
-    if (g >= E) return;
+// A workgroup takes kFinalizeItems consecutive groups; groups are sorted by
+// super-window, so they fall in at most a few super-windows, and the
+// (window, degree) counts of its first two go to an LDS histogram flushed
+// with one global atomic per nonzero bin (per-wave global atomics on the
+// same 128 counters of a super-window serialised: 3.2 ms at 114M edges).
+constexpr unsigned kFinalizeItems = 2048;
+constexpr unsigned kFinalizeBins = TCC_SWTCF_MAX_SUPER_WINDOW_SIZE * 8;  // (wi, degree) of one super-window
+
+__global__ void __launch_bounds__(kThreads) group_finalize_kernel(
+    const std::uint64_t* __restrict__ keys, const std::uint64_t* __restrict__ groupKey,
+    const std::uint32_t* __restrict__ groupStart, const std::uint32_t* __restrict__ numGroups, std::uint32_t E,
+    std::uint32_t S, unsigned wiBits, unsigned dstBits, std::uint32_t* __restrict__ groupInfo,
+    std::uint32_t* __restrict__ wdCount, std::uint32_t* __restrict__ rowFlags, std::uint32_t* __restrict__ err) {
+    __shared__ std::uint32_t hist[2 * kFinalizeBins];
+    for (unsigned i = threadIdx.x; i < 2 * kFinalizeBins; i += kThreads) hist[i] = 0;
     const std::uint32_t G = *numGroups;
-    if (g >= G) {
-        rowFlags[g] = 0;
-        return;
+    const std::uint32_t g0 = blockIdx.x * kFinalizeItems;
+    const unsigned swShift = wiBits + dstBits;
+    const std::uint32_t swFirst = g0 < G ? static_cast<std::uint32_t>(groupKey[g0] >> swShift) : 0u;
+    __syncthreads();
+    for (unsigned it = 0; it < kFinalizeItems / kThreads; ++it) {
+        const std::uint32_t g = g0 + it * kThreads + threadIdx.x;
+        if (g >= E) break;
+        if (g >= G) {
+            rowFlags[g] = 0;
+            continue;
+        }
+        const std::uint32_t start = groupStart[g];
+        const std::uint32_t count = groupStart[g + 1] - start;
+        if (count == 0 || count > 8) atomicMax(err, static_cast<std::uint32_t>(TCC_DEVERR_DEGREE));
+        const std::uint32_t deg = count == 0 ? 1u : (count > 8 ? 8u : count);
+        std::uint32_t bits = 0;
+        for (std::uint32_t i = 0; i < deg; ++i) bits |= 1u << static_cast<unsigned>(keys[start + i] & 7u);
+        const std::uint64_t gk = groupKey[g];
+        const std::uint32_t wi = static_cast<std::uint32_t>(gk & ((1ull << wiBits) - 1ull));
+        const std::uint32_t sw = static_cast<std::uint32_t>(gk >> swShift);
+        const std::uint32_t local = sw - swFirst;
+        if (local < 2) {
+            atomicAdd(&hist[local * kFinalizeBins + wi * 8 + deg - 1], 1u);
+        } else {
+            atomicAdd(&wdCount[(static_cast<std::uint64_t>(sw) * S + wi) * 8 + deg - 1], 1u);
+        }
+        groupInfo[g] = bits | (deg << 8);
+        rowFlags[g] = (g == 0 || (gk >> wiBits) != (groupKey[g - 1] >> wiBits)) ? 1u : 0u;
     }
-    const std::uint32_t start = groupStart[g];
-    const std::uint32_t count = groupStart[g + 1] - start;
-    if (count == 0 || count > 8) atomicMax(err, static_cast<std::uint32_t>(TCC_DEVERR_DEGREE));
-    const std::uint32_t deg = count == 0 ? 1u : (count > 8 ? 8u : count);
-    std::uint32_t bits = 0;
-    for (std::uint32_t i = 0; i < deg; ++i) bits |= 1u << static_cast<unsigned>(keys[start + i] & 7u);
-    const std::uint64_t gk = groupKey[g];
-    const std::uint32_t wi = static_cast<std::uint32_t>(gk & ((1ull << wiBits) - 1ull));
-    const std::uint32_t sw = static_cast<std::uint32_t>(gk >> (wiBits + dstBits));
-    const std::uint32_t w = sw * S + wi;
-    aggregated_increment(wdCount, w * 8 + deg - 1);
-    groupInfo[g] = bits | (deg << 8);
-    rowFlags[g] = (g == 0 || (gk >> wiBits) != (groupKey[g - 1] >> wiBits)) ? 1u : 0u;
+    __syncthreads();
+    for (unsigned b = threadIdx.x; b < 2 * kFinalizeBins; b += kThreads) {
+        const std::uint32_t n = hist[b];
+        if (n == 0) continue;  // only bins of groups that exist (wi < S)
+        const std::uint32_t sw = swFirst + b / kFinalizeBins;
+        atomicAdd(&wdCount[static_cast<std::uint64_t>(sw) * S * 8 + (b % kFinalizeBins)], n);
+    }
 }
 
 // buildWindowMetadataKernel (:216-265): degree 8 first, then 7 ... 1.
@@ -233,7 +258,7 @@ __global__ void row_emit_kernel(const std::uint64_t* __restrict__ groupKey,
 // Stable rank of `bin` among the active items of a 256-item chunk (item order
 // = thread order), continuing the running per-bin counts in `run`.  Must be
 // called by all threads of the block.  `wcnt` is zero on entry and on exit.
-template <int NBITS>
+template <int NBITS, unsigned THREADS>
 __device__ std::uint32_t block_multisplit_rank(unsigned bin, bool active, std::uint32_t* run,
                                                std::uint32_t (*wcnt)[256]) {
     const unsigned wave = threadIdx.x / kWave;
@@ -251,7 +276,7 @@ __device__ std::uint32_t block_multisplit_rank(unsigned bin, bool active, std::u
     __syncthreads();
     for (unsigned b = threadIdx.x; b < (1u << NBITS); b += blockDim.x) {
         std::uint32_t t = 0;
-        for (int w = 0; w < static_cast<int>(kThreads / kWave); ++w) {
+        for (int w = 0; w < static_cast<int>(THREADS / kWave); ++w) {
             t += wcnt[w][b];
             wcnt[w][b] = 0;
         }
@@ -266,7 +291,8 @@ __device__ std::uint32_t block_multisplit_rank(unsigned bin, bool active, std::u
 //      fillValidTileRowSlotsKernel (:1003-1048) and the tile bitmaps
 //      (:430-455, written as one byte per tile row instead of atomicOr);
 //  (b) buildRepeatCacheMetadataKernel (:699-895) with the canonical order.
-__global__ void __launch_bounds__(kThreads) super_window_kernel(
+template <unsigned THREADS>
+__global__ void __launch_bounds__(THREADS) super_window_kernel(
     const std::uint64_t* __restrict__ groupKey, const std::uint32_t* __restrict__ groupInfo,
     const std::uint32_t* __restrict__ rowFlags, const std::uint32_t* __restrict__ rowPos,
     const std::uint32_t* __restrict__ rowStartGroup, const std::uint32_t* __restrict__ wdBase,
@@ -276,7 +302,7 @@ __global__ void __launch_bounds__(kThreads) super_window_kernel(
     std::uint32_t* __restrict__ cachedRowSlot, std::uint8_t* __restrict__ cachedCount,
     std::uint32_t* __restrict__ err) {
     __shared__ std::uint32_t run[256];
-    __shared__ std::uint32_t wcnt[kThreads / kWave][256];
+    __shared__ std::uint32_t wcnt[THREADS / kWave][256];
     __shared__ std::uint32_t occHist[TCC_SWTCF_MAX_SUPER_WINDOW_SIZE + 1];
     __shared__ std::uint32_t occBase[TCC_SWTCF_MAX_SUPER_WINDOW_SIZE + 1];
     __shared__ std::uint32_t repeatedTotal;
@@ -288,15 +314,15 @@ __global__ void __launch_bounds__(kThreads) super_window_kernel(
     const std::uint32_t g1 = rowStartGroup[off1];
     const std::uint64_t wiMask = (1ull << wiBits) - 1ull;
 
-    for (unsigned i = threadIdx.x; i < 256; i += kThreads) {
+    for (unsigned i = threadIdx.x; i < 256; i += THREADS) {
         run[i] = 0;
-        for (int w = 0; w < static_cast<int>(kThreads / kWave); ++w) wcnt[w][i] = 0;
+        for (int w = 0; w < static_cast<int>(THREADS / kWave); ++w) wcnt[w][i] = 0;
     }
     if (threadIdx.x <= TCC_SWTCF_MAX_SUPER_WINDOW_SIZE) occHist[threadIdx.x] = 0;
     __syncthreads();
 
     // (a) rows of every window of this super-window
-    for (std::uint32_t base = g0; base < g1; base += kThreads) {
+    for (std::uint32_t base = g0; base < g1; base += THREADS) {
         const std::uint32_t g = base + threadIdx.x;
         const bool active = g < g1;
         std::uint32_t info = 0, wi = 0, deg = 1;
@@ -306,7 +332,7 @@ __global__ void __launch_bounds__(kThreads) super_window_kernel(
             deg = info >> 8;
         }
         const unsigned bin = wi * 8 + (deg - 1);
-        const std::uint32_t rank = block_multisplit_rank<8>(bin, active, run, wcnt);
+        const std::uint32_t rank = block_multisplit_rank<8, THREADS>(bin, active, run, wcnt);
         if (active) {
             const std::uint32_t w = s * S + wi;
             if (w < numColWindows) {
@@ -321,7 +347,7 @@ __global__ void __launch_bounds__(kThreads) super_window_kernel(
     }
 
     // (b) repeat cache: occurrence histogram, descending bases, stable ranks
-    for (std::uint32_t u = off0 + threadIdx.x; u < off1; u += kThreads) {
+    for (std::uint32_t u = off0 + threadIdx.x; u < off1; u += THREADS) {
         const std::uint32_t occ = rowStartGroup[u + 1] - rowStartGroup[u];
         if (occ > TCC_SWTCF_MAX_SUPER_WINDOW_SIZE) {
             atomicMax(err, static_cast<std::uint32_t>(TCC_DEVERR_OCCURRENCE));
@@ -341,15 +367,15 @@ __global__ void __launch_bounds__(kThreads) super_window_kernel(
                                                        ? running
                                                        : TCC_SWTCF_REPEAT_CACHE_SIZE);
     }
-    for (unsigned i = threadIdx.x; i < 256; i += kThreads) run[i] = 0;
+    for (unsigned i = threadIdx.x; i < 256; i += THREADS) run[i] = 0;
     __syncthreads();
     if (repeatedTotal == 0) return;  // uniform across the block
-    for (std::uint32_t base = off0; base < off1; base += kThreads) {
+    for (std::uint32_t base = off0; base < off1; base += THREADS) {
         const std::uint32_t u = base + threadIdx.x;
         std::uint32_t occ = 0;
         if (u < off1) occ = rowStartGroup[u + 1] - rowStartGroup[u];
         const bool rep = u < off1 && occ > 1 && occ <= TCC_SWTCF_MAX_SUPER_WINDOW_SIZE;
-        const std::uint32_t rank = block_multisplit_rank<6>(rep ? occ : 0u, rep, run, wcnt);
+        const std::uint32_t rank = block_multisplit_rank<6, THREADS>(rep ? occ : 0u, rep, run, wcnt);
         if (rep) {
             const std::uint32_t cs = occBase[occ] + rank;
             if (cs < TCC_SWTCF_REPEAT_CACHE_SIZE) {
@@ -513,7 +539,7 @@ int tcc_swtcf_convert(const std::uint32_t* dDst, const std::uint32_t* dSrc, std:
     hipLaunchKernelGGL(group_emit_kernel, dim3(grid_for(E, kThreads)), dim3(kThreads), 0, st, sorted, E,
                        c.flags, c.pos, groupKey, c.groupStart);
     TCC_LAUNCH_CHECK();
-    hipLaunchKernelGGL(group_finalize_kernel, dim3(grid_for(E, kThreads)), dim3(kThreads), 0, st, sorted,
+    hipLaunchKernelGGL(group_finalize_kernel, dim3(grid_for(E, kFinalizeItems)), dim3(kThreads), 0, st, sorted,
                        groupKey, c.groupStart, numGroups, E, S, kl.wiBits, kl.dstBits, c.groupInfo, c.wdCount,
                        c.flags, err);
     TCC_LAUNCH_CHECK();
@@ -532,10 +558,16 @@ int tcc_swtcf_convert(const std::uint32_t* dDst, const std::uint32_t* dSrc, std:
     TCC_LAUNCH_CHECK();
 
     // 6-7, 11-13. per super-window: row locations, slots, bitmaps, cache
-    hipLaunchKernelGGL(super_window_kernel, dim3(SW), dim3(kThreads), 0, st, groupKey, c.groupInfo, c.flags,
-                       c.pos, c.rowStartGroup, c.wdBase, m->colWindowOffset, m->superWindowRowOffset, S,
-                       kl.wiBits, CW, m->tileRowSlot, reinterpret_cast<std::uint8_t*>(m->tileLocalBit),
-                       m->superWindowRowCacheSlot, m->superWindowCachedRowSlot, m->superWindowCachedCount, err);
+    // Super-windows with many groups (63k on average at 114M edges) walk them
+    // 1024 at a time; small ones keep 256-thread workgroups.
+    auto sw_launch = [&](auto kernel, unsigned threads) {
+        hipLaunchKernelGGL(kernel, dim3(SW), dim3(threads), 0, st, groupKey, c.groupInfo, c.flags, c.pos,
+                           c.rowStartGroup, c.wdBase, m->colWindowOffset, m->superWindowRowOffset, S, kl.wiBits, CW,
+                           m->tileRowSlot, reinterpret_cast<std::uint8_t*>(m->tileLocalBit),
+                           m->superWindowRowCacheSlot, m->superWindowCachedRowSlot, m->superWindowCachedCount, err);
+    };
+    if (E / std::max<std::uint64_t>(SW, 1) >= 8192) sw_launch(super_window_kernel<1024>, 1024);
+    else sw_launch(super_window_kernel<kThreads>, kThreads);
     TCC_LAUNCH_CHECK();
     hipLaunchKernelGGL(padding_kernel, dim3(grid_for(CW, kThreads)), dim3(kThreads), 0, st, c.wActive,
                        m->colWindowOffset, CW, m->tileRowSlot);
