@@ -190,6 +190,24 @@ def cpu_entry(t_cpu, threads, nz, nnz, R, F, config):
             "ms": round(t_cpu * 1e3, 3)}
 
 
+def swtcf_timings(torch, swtcf, m, X, n, nnz, F):
+    """The SWTCF SpMM of the config-2 graph at the reference's F = 128, S = 16
+    contract: fp32 X (launchSWTCFSpMM) and int8 X with per-row scales
+    (launchSWTCFSpMMQuantized, src/swtcf_spmm.cu:469-502).  Y += A X is
+    launched without zeroing Y between launches, as the reference times it
+    (swtcf_spmm_main.cu:203-247 sets Y once)."""
+    Y = torch.zeros((n, F), device="cuda")
+    fp32_ms = timed(lambda: swtcf.launchSWTCFSpMM(m, X, Y), 20, 3)
+    scale = X.abs().amax(dim=1).clamp_min(1e-30) / 127.0
+    q = torch.round(X / scale[:, None]).clamp(-127, 127).to(torch.int8).contiguous()
+    src_global = torch.arange(n, dtype=torch.int32, device="cuda")
+    q_ms = timed(lambda: swtcf.launchSWTCFSpMMQuantized(m, q, scale.contiguous(), src_global, Y), 20, 3)
+    gf = lambda ms: round(2.0 * nnz * F / (ms * 1e-3) / 1e9, 3)
+    return {"F": F, "S": 16, "fp32_ms": round(fp32_ms, 4), "fp32_gflops": gf(fp32_ms),
+            "int8_ms": round(q_ms, 4), "int8_gflops": gf(q_ms),
+            "X_bytes_fp32": 4 * n * F, "X_bytes_int8": n * F + 4 * n}
+
+
 def bench_spmm(args, torch, swtcf, cfg):
     """Configs 1-3: one SpMM per step."""
     from tcc_amd.graphs import make_features, make_graph
@@ -253,6 +271,8 @@ def bench_spmm(args, torch, swtcf, cfg):
         assert ws.device_error() == 0
         extra["convert_ms"] = round(conv_ms, 4)
         extra["convert_gedges_per_s"] = round(nnz / conv_ms / 1e6, 3)
+        if args.config == 2:
+            extra["swtcf"] = swtcf_timings(torch, swtcf, m, X, n, nnz, F)
         del m, ws
     if args.copy_calibration_mib:
         copy_calibration(args.copy_calibration_mib)
