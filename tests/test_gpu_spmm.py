@@ -182,9 +182,12 @@ def test_coo_to_bcsr_bcsc_bit_exact(gpu, oracle, values):
         assert np.array_equal(B["data"], wantc["data"])
 
 
-@pytest.mark.parametrize("F", [1, 2, 32, 100, 128, 256, 602])
+@pytest.mark.parametrize("F", [1, 2, 3, 5, 8, 13, 16, 17, 32, 100, 128, 256, 602])
 @pytest.mark.parametrize("values", [False, True])
 def test_bcsr_bcsc_spmm_vs_oracle(gpu, oracle, F, values):
+    """F <= 16 runs the narrow gather (8 blocks per wave step; F = 3, 13 take
+    the element-wise row loads, 8 and 16 the vector ones), F >= 17 the
+    feature-chunk gather."""
     from tcc_amd import swtcf
 
     nr, nc = 777, 901
@@ -352,7 +355,7 @@ def skewed_coo(nr, nc, seed):
 
 
 @pytest.mark.parametrize("unit_blocks", [0, 1, 2, 3, 5, 8, 64])
-@pytest.mark.parametrize("F", [2, 64, 128, 256, 602])
+@pytest.mark.parametrize("F", [2, 7, 13, 64, 128, 256, 602])
 def test_units_split_windows(gpu, oracle, unit_blocks, F):
     """Units of K consecutive blocks cut windows anywhere (empty windows
     included); windows shared by several units add their partial sums
