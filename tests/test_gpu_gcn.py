@@ -116,6 +116,64 @@ def test_fused_two_layer_matches_layer_by_layer(gpu):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("F,H,C", [(150, 64, 3), (40, 256, 8), (32, 48, 12)])
+def test_two_layer_paths_agree(gpu, F, H, C):
+    """The paths GCN.forward picks besides the fully fused one, each against
+    the layer-by-layer functions: F > 128 keeps torch's forward transform
+    inside TwoLayerFunction (fused backward), 8 classes take the 8-wide
+    relu-gradient tiles, 12 classes run layer by layer."""
+    from tcc_amd import gcn
+    from tcc_amd.graphs import rmat_graph
+
+    n = 2039
+    rows, cols = rmat_graph(n, 30_000, 23 + C)
+    torch.manual_seed(C)
+    X = torch.randn((n, F))
+    table = gcn.FeatureTable(X, cols)
+    g1, g2 = gcn.build_gcn_graphs(rows, cols, n, table.hot)
+    model = gcn.GCN(F, H, C).cuda()
+    labels = gcn.synthetic_labels(n, C, 5)
+    res = []
+    for fused in (True, False):
+        model.fused = fused
+        model.zero_grad(set_to_none=True)
+        pred = model(g1, g2, table.source)
+        gcn.cross_entropy(pred, labels).backward()
+        res.append((pred.detach().clone(), model.conv1.weights.grad.clone(), model.conv_final.weights.grad.clone()))
+    torch.cuda.synchronize()
+    for a, b in zip(res[0], res[1]):
+        assert rel_l2(a.cpu().numpy(), b.double().cpu().numpy()) < 1e-5
+    table.free()
+
+
+@pytest.mark.gpu
+def test_dropout_takes_the_layer_path(gpu):
+    """With dropout in training the model runs layer by layer (the mask sits
+    between the layers); in eval mode dropout is the identity and the fused
+    node runs: both give finite outputs and gradients."""
+    from tcc_amd import gcn
+    from tcc_amd.graphs import rmat_graph
+
+    n, F = 1500, 24
+    rows, cols = rmat_graph(n, 15_000, 31)
+    torch.manual_seed(3)
+    X = torch.randn((n, F))
+    table = gcn.FeatureTable(X, cols)
+    g1, g2 = gcn.build_gcn_graphs(rows, cols, n, table.hot)
+    model = gcn.GCN(F, 32, 2, dropout=0.5).cuda()
+    labels = gcn.synthetic_labels(n, 2, 6)
+    for train in (True, False):
+        model.train(train)
+        model.zero_grad(set_to_none=True)
+        loss = gcn.cross_entropy(model(g1, g2, table.source), labels)
+        loss.backward()
+        assert torch.isfinite(loss)
+        assert torch.isfinite(model.conv1.weights.grad).all()
+        assert torch.isfinite(model.conv_final.weights.grad).all()
+    table.free()
+
+
+@pytest.mark.gpu
 def test_gcn_trains(gpu):
     """A few Adam steps on a small graph lower the loss (the full training
     step of tcgnn_conv_release.py:284-329)."""
