@@ -99,14 +99,18 @@ int tcc_bcsr_spmm(const tcc_bcsr* A, const float* X, float* Y, uint32_t featureD
 
 /* ---- packed TF32 features (no reference counterpart) ----
  * A TF32 value has 19 significant bits.  tcc_tf32_pack writes TF32(X) of an
- * fp32 [rows x F] matrix in 2.5 bytes per element: per row, the high 16 bits
- * of each value (sign, exponent, 7 mantissa bits) followed by the 3 low
- * mantissa bits of element pairs (element 2k in bits 0-2, 2k+1 in bits 3-5 of
- * byte k), rows padded to 16 bytes.  The gather over packed rows reads 37.5%
- * fewer bytes per gathered row than fp32 X, with bit-identical products;
- * it pays off when rows are gathered more than about twice (8*num_TCBlocks
- * against num_cols).  The packed buffer must be 16-byte aligned and hold
- * tcc_tf32_packed_bytes(rows, F) bytes. */
+ * fp32 [rows x F] matrix in 2.5 bytes per element.  A row is cut into chunks
+ * of 256 features; a chunk of n features holds the high 16 bits of each
+ * value (sign, exponent, 7 mantissa bits; 2n bytes) followed by the 3 low
+ * mantissa bits of element pairs (element 2k in bits 0-2 and 2k+1 in bits
+ * 3-5 of byte k; ceil(n/2) bytes).  A full chunk is 640 bytes; the last is
+ * padded to 16 bytes; a row of more than one chunk is padded to 128 bytes,
+ * a single-chunk row to 16 (tcc_tf32_packed_bytes / rows).  The gather over
+ * packed rows reads 37.5% fewer bytes per gathered row than fp32 X, with
+ * bit-identical products, and each 256-feature chunk it loads covers whole
+ * 128-byte lines; it pays off when rows are gathered many times
+ * (8*num_TCBlocks against num_cols).  The packed buffer must be 16-byte
+ * aligned and hold tcc_tf32_packed_bytes(rows, F) bytes. */
 size_t tcc_tf32_packed_bytes(uint32_t rows, uint32_t featureDim);
 int tcc_tf32_pack(const float* X, uint32_t rows, uint32_t featureDim, void* packed, void* stream);
 

@@ -210,21 +210,47 @@ __device__ __forceinline__ const float* input_row(const GatherArgs& a, std::uint
 }
 
 // Packed TF32 rows (tcc_tf32_pack): a TF32 value has 19 significant bits,
-// stored as its high 16 bits (sign, exponent, 7 mantissa bits; 2 bytes per
-// element, row-major) followed by the 3 low mantissa bits of element pairs
-// (element 2k in bits 0-2 and 2k+1 in bits 3-5 of byte k), rows padded to
-// 16 bytes: stride = roundup(2F + ceil(F/2), 16).  Exact: unpacking gives
-// the TF32 rounding of X bit for bit.
+// stored as its high 16 bits (sign, exponent, 7 mantissa bits) and its 3 low
+// mantissa bits.  A row is cut into chunks of 256 features (the 64 lanes x 4
+// features one wave gathers); a chunk of n features holds the high halves
+// (2 bytes each) and then the low bits of element pairs (element 2k in bits
+// 0-2 and 2k+1 in bits 3-5 of byte k): a full chunk is 640 bytes, five
+// 128-byte lines, so a wave's chunk load touches exactly the lines it uses
+// once rows are 128-byte aligned.  The last chunk is padded to 16 bytes and
+// rows longer than one chunk to 128 bytes (single-chunk rows to 16).
+// Exact: unpacking gives the TF32 rounding of X bit for bit.
+constexpr std::uint32_t kPackChunk = 256;
+constexpr std::uint64_t kPackChunkBytes = 640;
+
+__host__ __device__ constexpr std::uint64_t packed_tail_bytes(std::uint32_t n) {
+    return ((2ull * n + (n + 1) / 2) + 15) & ~15ull;
+}
+
 __host__ __device__ constexpr std::uint64_t packed_stride(std::uint32_t F) {
-    return ((2ull * F + (F + 1) / 2) + 15) & ~15ull;
+    const std::uint64_t full = F / kPackChunk, tail = F % kPackChunk;
+    const std::uint64_t bytes = full * kPackChunkBytes + (tail ? packed_tail_bytes(static_cast<std::uint32_t>(tail)) : 0);
+    return F > kPackChunk ? ((bytes + 127) & ~127ull) : bytes;
+}
+
+// Byte offsets of element f's high half and of the low-bit byte of its pair.
+struct PackedAt {
+    std::uint64_t hi, lo;
+};
+
+__host__ __device__ inline PackedAt packed_at(std::uint32_t F, std::uint32_t f) {
+    const std::uint32_t c = f / kPackChunk, j = f % kPackChunk;
+    const std::uint32_t n = (F - c * kPackChunk) < kPackChunk ? (F - c * kPackChunk) : kPackChunk;
+    const std::uint64_t base = c * kPackChunkBytes;
+    return PackedAt{base + 2ull * j, base + 2ull * n + j / 2};
 }
 
 __device__ __forceinline__ float tf32_from(std::uint32_t hi16, std::uint32_t lo3) {
     return __uint_as_float((hi16 << 16) | (lo3 << 13));
 }
 
-// The V features at element offset `f` of a packed row (f % V == 0): the
-// high halves and the low bits, loaded before any use.
+// The V features at element offset `f` of a packed row (f % V == 0; the V
+// elements lie in one chunk): the high halves and the low bits, loaded
+// before any use.  Elements past F read padding and are never stored.
 template <int V>
 struct PackedVec {
     std::uint32_t hi[(V + 1) / 2];
@@ -234,17 +260,18 @@ struct PackedVec {
 template <int V>
 __device__ __forceinline__ PackedVec<V> load_packed(const unsigned char* row, std::uint32_t F, std::uint32_t f) {
     PackedVec<V> p;
+    const PackedAt at = packed_at(F, f);
     if constexpr (V == 4) {
-        const uint2 h = *reinterpret_cast<const uint2*>(row + 2ull * f);
+        const uint2 h = *reinterpret_cast<const uint2*>(row + at.hi);
         p.hi[0] = h.x;
         p.hi[1] = h.y;
-        p.lo = *reinterpret_cast<const std::uint16_t*>(row + 2ull * F + f / 2);
+        p.lo = *reinterpret_cast<const std::uint16_t*>(row + at.lo);
     } else if constexpr (V == 2) {
-        p.hi[0] = *reinterpret_cast<const std::uint32_t*>(row + 2ull * f);
-        p.lo = row[2ull * F + f / 2];
+        p.hi[0] = *reinterpret_cast<const std::uint32_t*>(row + at.hi);
+        p.lo = row[at.lo];
     } else {
-        p.hi[0] = *reinterpret_cast<const std::uint16_t*>(row + 2ull * f);
-        p.lo = row[2ull * F + f / 2] >> (3 * (f & 1u));
+        p.hi[0] = *reinterpret_cast<const std::uint16_t*>(row + at.hi);
+        p.lo = row[at.lo] >> (3 * (f & 1u));
     }
     return p;
 }
@@ -409,6 +436,9 @@ __device__ __forceinline__ void gather_body(const GatherArgs& a, std::uint32_t g
     // Finish window w: a window cut by a unit boundary is shared (rows
     // pre-zeroed unless accumulating; atomics for the rows this unit
     // touched), any other is stored whole.
+    // V-wide stores when F % V == 0 (then rows keep V-float alignment), else
+    // (the packed gather's 4-wide chunks over any F) one float at a time.
+    const bool vecStore = a.F % V == 0;
     auto flush = [&]() {
         if (active) {
             float* out = a.Y + static_cast<std::uint64_t>(w) * 8 * a.F + f0;
@@ -419,9 +449,14 @@ __device__ __forceinline__ void gather_body(const GatherArgs& a, std::uint32_t g
                 if (shared) {
                     if (((touched >> (8 * r)) & 0xFFu) == 0) continue;
 #pragma unroll
-                    for (int v = 0; v < V; ++v) atomic_add_f32(o + v, acc[r][v]);
-                } else {
+                    for (int v = 0; v < V; ++v)
+                        if (f0 + v < a.F) atomic_add_f32(o + v, acc[r][v]);
+                } else if (vecStore) {
                     store_vec<V>(o, acc[r], a.accumulate != 0);
+                } else {
+#pragma unroll
+                    for (int v = 0; v < V; ++v)
+                        if (f0 + v < a.F) o[v] = a.accumulate ? o[v] + acc[r][v] : acc[r][v];
                 }
             }
         }
@@ -711,12 +746,13 @@ __global__ void tf32_pack_kernel(const float* __restrict__ X, std::uint32_t rows
     const std::uint32_t b0 = __float_as_uint(tf32_rna(x[e]));
     const std::uint32_t b1 = two ? __float_as_uint(tf32_rna(x[e + 1])) : 0u;
     unsigned char* row = out + r * stride;
+    const PackedAt at = packed_at(F, e);  // e even: the pair lies in one chunk
     if (two) {
-        *reinterpret_cast<std::uint32_t*>(row + 4ull * p) = (b0 >> 16) | (b1 & 0xFFFF0000u);
+        *reinterpret_cast<std::uint32_t*>(row + at.hi) = (b0 >> 16) | (b1 & 0xFFFF0000u);
     } else {
-        *reinterpret_cast<std::uint16_t*>(row + 4ull * p) = static_cast<std::uint16_t>(b0 >> 16);
+        *reinterpret_cast<std::uint16_t*>(row + at.hi) = static_cast<std::uint16_t>(b0 >> 16);
     }
-    row[2ull * F + p] = static_cast<unsigned char>(((b0 >> 13) & 7u) | (((b1 >> 13) & 7u) << 3));
+    row[at.lo] = static_cast<unsigned char>(((b0 >> 13) & 7u) | (((b1 >> 13) & 7u) << 3));
 }
 
 struct ScatterArgs {
@@ -1113,7 +1149,9 @@ int tcc_bcsr_spmm_packed(const tcc_bcsr* A, const void* packedX, float* Y, std::
     GatherArgs a = bcsr_args(A, nullptr, Y, featureDim, accumulate);
     a.packed = static_cast<const unsigned char*>(packedX);
     a.packedStride = static_cast<std::uint32_t>(packed_stride(featureDim));
-    const int V = pick_vec(featureDim, {Y});
+    // Rows longer than one chunk are gathered a whole chunk (4 features a
+    // lane) at a time, whatever F % 4, so that each load covers its lines.
+    const int V = featureDim > kPackChunk ? 4 : pick_vec(featureDim, {Y});
     return launch_gather<Src::Packed>(a, V, A->unitBlocks, as_stream(stream));
 }
 

@@ -55,3 +55,16 @@ def test_host_side_argument_errors_without_gpu():
     m.numSuperWindows = 1
     assert L.tcc_swtcf_spmm(ctypes.byref(m), ctypes.c_void_p(16), ctypes.c_void_p(16), 12, None) == 3
     assert b"superWindowSize=16" in L.tcc_last_error()
+
+
+def test_packed_bytes_follow_the_documented_layout():
+    """tcc_tf32_packed_bytes = rows x the row stride of the packed layout of
+    include/tcc_spmm_cnic.h: 256-feature chunks of 640 bytes, the last padded
+    to 16 bytes, rows of more than one chunk padded to 128 (host-only call)."""
+    from tcc_amd import _lib
+
+    L = _lib.lib()
+    for F, stride in [(1, 16), (2, 16), (7, 32), (100, 256), (128, 320), (256, 640), (257, 768), (300, 768),
+                      (512, 1280), (513, 1408), (602, 1536)]:
+        assert L.tcc_tf32_packed_bytes(1, F) == stride, F
+        assert L.tcc_tf32_packed_bytes(37, F) == 37 * stride, F

@@ -427,21 +427,33 @@ def test_unit_sizes_agree_on_rmat(gpu):
 
 
 # ------------------------------------------------------------------ packed TF32 rows
+def packed_stride_host(F):
+    """Row stride of the packed layout (include/tcc_spmm_cnic.h)."""
+    full, tail = divmod(F, 256)
+    nbytes = full * 640 + ((2 * tail + (tail + 1) // 2 + 15) // 16 * 16 if tail else 0)
+    return (nbytes + 127) // 128 * 128 if F > 256 else nbytes
+
+
 def unpack_host(buf, rows, F):
     """Independent host reading of the packed layout (include/tcc_spmm_cnic.h):
-    per row 2F bytes of high halves, then the 3 low mantissa bits of element
-    pairs, rows padded to 16 bytes."""
-    stride = (2 * F + (F + 1) // 2 + 15) // 16 * 16
+    chunks of 256 features, each 2n bytes of high halves then the 3 low
+    mantissa bits of element pairs; full chunks 640 bytes."""
+    stride = packed_stride_host(F)
     b = np.asarray(buf, np.uint8)[: rows * stride].reshape(rows, stride)
-    hi = b[:, : 2 * F].copy().view(np.uint16).astype(np.uint32)
-    lo_bytes = b[:, 2 * F: 2 * F + (F + 1) // 2].astype(np.uint32)
-    lo = np.empty((rows, F), np.uint32)
-    lo[:, 0::2] = lo_bytes[:, : (F + 1) // 2] & 7
-    lo[:, 1::2] = (lo_bytes[:, : F // 2] >> 3) & 7
-    return ((hi << 16) | (lo << 13)).astype(np.uint32)
+    out = np.empty((rows, F), np.uint32)
+    for c0 in range(0, F, 256):
+        n = min(256, F - c0)
+        base = (c0 // 256) * 640
+        hi = b[:, base: base + 2 * n].copy().view(np.uint16).astype(np.uint32)
+        lo_bytes = b[:, base + 2 * n: base + 2 * n + (n + 1) // 2].astype(np.uint32)
+        lo = np.empty((rows, n), np.uint32)
+        lo[:, 0::2] = lo_bytes[:, : (n + 1) // 2] & 7
+        lo[:, 1::2] = (lo_bytes[:, : n // 2] >> 3) & 7
+        out[:, c0: c0 + n] = (hi << 16) | (lo << 13)
+    return out
 
 
-@pytest.mark.parametrize("F", [1, 2, 3, 7, 100, 128, 602])
+@pytest.mark.parametrize("F", [1, 2, 3, 7, 100, 128, 256, 257, 300, 513, 602])
 def test_tf32_pack_is_exact(gpu, oracle, F):
     from tcc_amd import swtcf
 
@@ -460,7 +472,7 @@ def test_tf32_pack_is_exact(gpu, oracle, F):
 
 
 @pytest.mark.parametrize("unit_blocks", [0, 3])
-@pytest.mark.parametrize("F", [1, 2, 64, 100, 128, 256, 602])
+@pytest.mark.parametrize("F", [1, 2, 64, 100, 128, 256, 257, 300, 513, 602])
 def test_bcsr_spmm_packed(gpu, oracle, unit_blocks, F):
     """The gather over packed rows gives the oracle's TF32 product (= and +=)."""
     from tcc_amd import swtcf
