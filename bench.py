@@ -316,6 +316,30 @@ def gcn_inputs(torch, cfg):
     return rows, cols, X, table, g1, g2
 
 
+def packed_rows_step(torch, table, X, cols, g1, F, Y_fp32, cold_rows_used, args):
+    """The same first-layer step with FeatureTable(packed=True): hot cache and
+    host rows as packed TF32 rows (an option of this build; the headline
+    keeps the reference's fp32 rows).  Checked against the fp32-row result."""
+    from tcc_amd import gcn, swtcf
+
+    ptable = gcn.FeatureTable(X, cols, packed=True)
+    assert torch.equal(ptable.hot, table.hot)
+    Yp = None
+
+    def step():
+        nonlocal Yp
+        Yp = g1.aggregate(F, source=ptable.source)
+
+    ms = timed(step, args.steps, args.warmup)
+    torch.cuda.synchronize()
+    rel = float((Yp - Y_fp32).norm() / Y_fp32.norm().clamp_min(1e-30))
+    row_bytes = swtcf._lib.lib().tcc_tf32_packed_bytes(1, F)
+    ptable.free()
+    link = cold_rows_used * row_bytes
+    return {"ms": round(ms, 4), "row_bytes": row_bytes, "cold_bytes": link,
+            "host_link_GBps": round(link / (ms * 1e-3) / 1e9, 2), "rel_l2_vs_fp32_rows": rel}
+
+
 def bench_mixed(args, torch, swtcf, cfg):
     """Config 4: the first-layer SpMM with hot rows from HBM and cold rows
     read zero-copy from pinned host memory."""
@@ -341,6 +365,7 @@ def bench_mixed(args, torch, swtcf, cfg):
                            "achieved_GBps": round(cold_bytes / (ms * 1e-3) / 1e9, 2),
                            "peak_GBps": PCIE_PEAK_GBPS,
                            "bound_ms": round(cold_bytes / (PCIE_PEAK_GBPS * 1e9) * 1e3, 3)}}
+    extra["packed_rows"] = packed_rows_step(torch, table, X, cols, g1, F, Y, cold_rows_used, args)
     cpu = None
     if not args.no_cpu_baseline:
         t_cpu, threads, rel, R, nz = cpu_baseline(rows, cols, None, X, n, args.cpu_threads, Y, 16_000_000)
@@ -406,10 +431,15 @@ def bench_gcn(args, torch, swtcf, cfg):
 
     l1 = timed(layer1, steps, warmup)
     l2 = timed(layer2, steps, warmup)
+    # the same epoch over a packed TF32 feature table (an option; see packed_rows_step)
+    ptable = gcn.FeatureTable(X, cols, packed=True)
+    ms_packed = timed(lambda: gcn.train_epoch(model, g1, g2, ptable.source, labels, opt, loss_fcn), steps, warmup)
+    ptable.free()
     extra = {"epoch": "TwoLayerFunction: mixed SpMM F=100 (one launch), relu(AX W1) and H W2 in one pass "
                       "(tcc_gcn_relu_forward), SpMM F=2; backward A^T SpMM F=2, then dW1 and dW2 in one pass "
                       "(tcc_gcn_relu_grad); cross-entropy, Adam",
              "layer_times": "each layer alone, through its own autograd function",
+             "epoch_ms_packed_feature_rows": round(ms_packed, 4),
              "layer1_fwd_bwd_ms": round(l1, 4), "layer2_fwd_bwd_ms": round(l2, 4),
              "layer1": f"mixed SpMM F={F} (hot BCSR + cold BCSC) + GEMM {F}x{hidden}; backward dW GEMM",
              "layer2": f"A(XW): GEMM {hidden}x{classes}, BCSR SpMM F={classes}; backward A^T SpMM F={classes}, "

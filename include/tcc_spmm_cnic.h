@@ -73,21 +73,31 @@ typedef struct tcc_bcsc {
 
 /* Where the first GCN layer reads feature row j from
  * (spmm_cnic/src/core/spmm_kernel.cu:129-153): g = cache_search_map[j];
- * g >= 0: hot row gpu_feature_cache[g / gpu_node_capacity] + (g % cap) * F
- * (device memory); g < 0: cold row cpu_features + id_map[j] * F, a device
+ * g >= 0: hot row (g % cap) of gpu_feature_cache[g / gpu_node_capacity]
+ * (device memory); g < 0: cold row id_map[j] of cpu_features, a device
  * pointer to mapped pinned host memory read zero-copy; id_map[j] < 0 reads
  * zeros.  Two bounds the reference does not check keep bad map values from
  * reading outside the tables: a cache index g / cap >= gpu_feature_cache_count
- * (when nonzero) and a host row past cpu_feature_len floats (when > 0) read
- * zeros.  On one GPU the pointer table has one entry. */
+ * (when nonzero) and a host row past cpu_feature_len features (when > 0)
+ * read zeros.  On one GPU the pointer table has one entry.
+ * Rows are F floats (row_format TCC_ROWS_FP32, the reference's layout) or,
+ * with TCC_ROWS_TF32_PACKED (no reference counterpart), TF32 rows packed by
+ * tcc_tf32_pack (tcc_tf32_packed_bytes(1, F) bytes each, tables 16-byte
+ * aligned): the products are the same bit for bit, since the first layer's
+ * products round X to TF32 anyway, and each row moves 2.5 instead of 4
+ * bytes per feature -- across PCIe for the cold rows. */
+#define TCC_ROWS_FP32 0u
+#define TCC_ROWS_TF32_PACKED 1u
+
 typedef struct tcc_feature_source {
     const int32_t* id_map;           /* device [num_cols] */
     const int32_t* cache_search_map; /* device [num_cols] */
     const float* const* gpu_feature_cache; /* device array of device pointers */
     int32_t gpu_node_capacity;
     const float* cpu_features;       /* device-visible pointer to pinned host rows */
-    int64_t cpu_feature_len;         /* floats available at cpu_features (<= 0: unchecked) */
+    int64_t cpu_feature_len;         /* features (rows x F) available at cpu_features (<= 0: unchecked) */
     uint32_t gpu_feature_cache_count; /* entries of gpu_feature_cache (0: unchecked) */
+    uint32_t row_format;             /* TCC_ROWS_FP32 (0) or TCC_ROWS_TF32_PACKED */
 } tcc_feature_source;
 
 /* Y[row-window rows x F] (=, or += when accumulate != 0) A_bcsr * X.

@@ -57,7 +57,7 @@ class BCSC(ctypes.Structure):
 class FeatureSource(ctypes.Structure):
     _fields_ = [
         ("id_map", vp), ("cache_search_map", vp), ("gpu_feature_cache", vp), ("gpu_node_capacity", i32),
-        ("cpu_features", vp), ("cpu_feature_len", i64), ("gpu_feature_cache_count", u32),
+        ("cpu_features", vp), ("cpu_feature_len", i64), ("gpu_feature_cache_count", u32), ("row_format", u32),
     ]
 
 

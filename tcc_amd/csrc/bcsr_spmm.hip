@@ -40,8 +40,9 @@ constexpr unsigned kThreads = 256;
 constexpr unsigned kWaves = kThreads / kWave;
 
 // Where a gather reads its input rows: fp32 X, the first layer's hot/cold
-// feature source, dY for the A^T product, or a packed TF32 copy of X.
-enum class Src { Plain, Mixed, Transposed, Packed };
+// feature source (fp32 or packed TF32 rows), dY for the A^T product, or a
+// packed TF32 copy of X.
+enum class Src { Plain, Mixed, MixedPacked, Transposed, Packed };
 
 // Feature-source fields of the first GCN layer (tcc_feature_source).
 struct MixedArgs {
@@ -52,6 +53,7 @@ struct MixedArgs {
     const float* cpuFeatures;
     std::int64_t cpuLen;
     std::uint32_t gpuCacheCount;
+    std::uint64_t rowBytes;  // 0: rows of F floats; else packed TF32 rows of this stride
 };
 
 struct GatherArgs {
@@ -79,17 +81,23 @@ struct GatherArgs {
 // Feature row of column `in` for the first-layer (mixed) form
 // (spmm_kernel.cu:129-153), or nullptr for a zero row.  Indices outside the
 // pointer table or past the host rows read zeros instead of faulting.
+__device__ __forceinline__ const float* table_row(const float* base, std::uint64_t rowBytes, std::uint32_t F,
+                                                  std::int64_t r) {
+    if (rowBytes == 0) return base + r * F;
+    return reinterpret_cast<const float*>(reinterpret_cast<const unsigned char*>(base) + r * rowBytes);
+}
+
 __device__ __forceinline__ const float* mixed_row(const MixedArgs& m, std::uint32_t F, std::uint32_t in) {
     const std::int32_t g = m.cacheSearchMap[in];
     if (g >= 0) {
         const std::int32_t d = g / m.gpuNodeCapacity;
         if (m.gpuCacheCount != 0 && static_cast<std::uint32_t>(d) >= m.gpuCacheCount) return nullptr;
-        return m.gpuCache[d] + static_cast<std::int64_t>(g % m.gpuNodeCapacity) * F;
+        return table_row(m.gpuCache[d], m.rowBytes, F, g % m.gpuNodeCapacity);
     }
     const std::int32_t id = m.idMap[in];
     if (id < 0 || m.cpuFeatures == nullptr) return nullptr;
     if (m.cpuLen > 0 && (static_cast<std::int64_t>(id) + 1) * F > m.cpuLen) return nullptr;
-    return m.cpuFeatures + static_cast<std::int64_t>(id) * F;
+    return table_row(m.cpuFeatures, m.rowBytes, F, id);
 }
 
 template <int V>
@@ -200,7 +208,7 @@ __device__ __forceinline__ UnitRange unit_range(const std::uint32_t* winOffset, 
 // Row base pointer of input `in` (nullptr for a zero row).
 template <Src MODE>
 __device__ __forceinline__ const float* input_row(const GatherArgs& a, std::uint32_t in) {
-    if constexpr (MODE == Src::Mixed) {
+    if constexpr (MODE == Src::Mixed || MODE == Src::MixedPacked) {
         return mixed_row(a.mixed, a.F, in);
     } else if constexpr (MODE == Src::Packed) {
         return reinterpret_cast<const float*>(a.packed + static_cast<std::uint64_t>(in) * a.packedStride);
@@ -339,7 +347,7 @@ __device__ __forceinline__ void load_block(const GatherArgs& a, const GroupMeta&
     bm = (MODE == Src::Transposed) ? transpose8x8(raw) : raw;
     // All loads are issued before any result is used (rounding inside the
     // branches would wait for each load in turn).
-    if constexpr (MODE == Src::Packed) {
+    if constexpr (MODE == Src::Packed || MODE == Src::MixedPacked) {
         PackedVec<V> pk[8];
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
@@ -800,9 +808,24 @@ __device__ __forceinline__ std::uint32_t used_columns(const std::uint64_t* bits,
 // the others and past numCols); all loads are issued before any is rounded.
 // Skipping unused rows matters most for the first layer's cold rows, which
 // cross the host link.
-template <int V, bool MIXED>
+template <int V, bool MIXED, bool PACKED = false>
 __device__ __forceinline__ void load_window_rows(const ScatterArgs& a, std::uint32_t w, std::uint32_t used,
                                                  std::uint32_t laneOff, float (&x)[8][V]) {
+    if constexpr (PACKED) {  // packed TF32 feature rows: no rounding needed
+        PackedVec<V> pk[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const std::uint32_t col = w * 8 + c;
+            pk[c] = PackedVec<V>{};
+            if (((used >> c) & 1u) && col < a.numCols) {
+                const float* row = mixed_row(a.mixed, a.F, col);
+                if (row != nullptr) pk[c] = load_packed<V>(reinterpret_cast<const unsigned char*>(row), a.F, laneOff);
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < 8; ++c) unpack<V>(pk[c], x[c]);
+        return;
+    }
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
         const std::uint32_t col = w * 8 + c;
@@ -829,7 +852,7 @@ __device__ __forceinline__ void load_window_rows(const ScatterArgs& a, std::uint
         for (int v = 0; v < V; ++v) x[c][v] = tf32_rna(x[c][v]);
 }
 
-template <int V, bool MIXED, bool VALUES>
+template <int V, bool MIXED, bool VALUES, bool PACKED = false>
 __device__ __forceinline__ void scatter_body(const ScatterArgs& a, std::uint32_t gw) {
     const unsigned lane = __lane_id();
     const std::uint32_t chunk = gw / a.numUnits;
@@ -848,14 +871,14 @@ __device__ __forceinline__ void scatter_body(const ScatterArgs& a, std::uint32_t
         we = a.winOffset[w + 1];
     }
     float x[8][V];
-    load_window_rows<V, MIXED>(a, w, used_columns(a.bits, u.b0, min(we, u.b1)), laneOff, x);
+    load_window_rows<V, MIXED, PACKED>(a, w, used_columns(a.bits, u.b0, min(we, u.b1)), laneOff, x);
     for (std::uint32_t b = u.b0; b < u.b1; ++b) {
         if (b >= we) {
             do {
                 ++w;
                 we = a.winOffset[w + 1];
             } while (b >= we && w + 1 < a.numWindows);
-            load_window_rows<V, MIXED>(a, w, used_columns(a.bits, b, min(we, u.b1)), laneOff, x);
+            load_window_rows<V, MIXED, PACKED>(a, w, used_columns(a.bits, b, min(we, u.b1)), laneOff, x);
         }
         const std::uint64_t bm = a.bits[b];
         float vals = 0.0f;
@@ -888,7 +911,8 @@ __device__ __forceinline__ void scatter_body(const ScatterArgs& a, std::uint32_t
             if (active) {
                 float* out = a.Y + static_cast<std::uint64_t>(row) * a.F + f0;
 #pragma unroll
-                for (int v = 0; v < V; ++v) atomic_add_f32(out + v, s[v]);
+                for (int v = 0; v < V; ++v)
+                    if (f0 + v < a.F) atomic_add_f32(out + v, s[v]);
             }
         }
     }
@@ -905,7 +929,7 @@ __global__ void __launch_bounds__(kThreads) scatter_kernel(ScatterArgs a) {
 // proportion to their counts, so that scatter waves, which wait on host
 // memory across the link, and gather waves, which stream HBM, run side by
 // side.  Both add into a zeroed Y with atomics.
-template <int V, bool GVALUES, bool SVALUES>
+template <int V, bool GVALUES, bool SVALUES, bool PACKED>
 __global__ void __launch_bounds__(kThreads) mixed_forward_kernel(GatherArgs g, ScatterArgs s, std::uint32_t gatherWGs,
                                                                  std::uint32_t scatterWGs) {
     const std::uint64_t total = static_cast<std::uint64_t>(gatherWGs) + scatterWGs;
@@ -913,8 +937,8 @@ __global__ void __launch_bounds__(kThreads) mixed_forward_kernel(GatherArgs g, S
     const auto before = static_cast<std::uint32_t>(static_cast<std::uint64_t>(i) * scatterWGs / total);
     const auto upto = static_cast<std::uint32_t>(static_cast<std::uint64_t>(i + 1) * scatterWGs / total);
     const std::uint32_t wave = uniform(threadIdx.x / kWave);
-    if (upto > before) scatter_body<V, true, SVALUES>(s, before * kWaves + wave);  // the before-th scatter group
-    else gather_body<V, Src::Mixed, GVALUES>(g, (i - before) * kWaves + wave);
+    if (upto > before) scatter_body<V, true, SVALUES, PACKED>(s, before * kWaves + wave);  // the before-th scatter group
+    else gather_body<V, PACKED ? Src::MixedPacked : Src::Mixed, GVALUES>(g, (i - before) * kWaves + wave);
 }
 
 // Vector width per lane: the narrowest V in {1,2,4} whose 64*V-feature chunk
@@ -1046,8 +1070,9 @@ int launch_scatter(ScatterArgs a, int V, std::uint32_t requestedK, hipStream_t s
     return TCC_OK;
 }
 
-MixedArgs mixed_args(const tcc_feature_source* src) {
+MixedArgs mixed_args(const tcc_feature_source* src, std::uint32_t F) {
     MixedArgs m{};
+    m.rowBytes = src->row_format == TCC_ROWS_TF32_PACKED ? packed_stride(F) : 0;
     m.idMap = src->id_map;
     m.cacheSearchMap = src->cache_search_map;
     m.gpuCache = src->gpu_feature_cache;
@@ -1090,6 +1115,22 @@ ScatterArgs bcsc_args(const tcc_bcsc* A, const float* X, float* Y, std::uint32_t
     a.numCols = A->num_cols;
     a.F = F;
     return a;
+}
+
+// Feature source checks: the fields every lookup reads, a known row format,
+// and 16-byte aligned host rows for packed tables.
+bool source_ok(const tcc_feature_source* src) {
+    if (!(src && src->id_map && src->cache_search_map && src->gpu_feature_cache && src->gpu_node_capacity > 0))
+        return false;
+    if (src->row_format == TCC_ROWS_FP32) return true;
+    return src->row_format == TCC_ROWS_TF32_PACKED && reinterpret_cast<std::uintptr_t>(src->cpu_features) % 16 == 0;
+}
+
+// Vector width of a first-layer product: packed rows longer than one chunk
+// are gathered a chunk at a time (4 features a lane), as tcc_bcsr_spmm_packed.
+int mixed_vec(const tcc_feature_source* src, std::uint32_t F, const float* Y) {
+    if (src->row_format == TCC_ROWS_TF32_PACKED) return F > kPackChunk ? 4 : pick_vec(F, {Y});
+    return pick_vec(F, {Y, src->cpu_features});
 }
 
 bool bcsr_ok(const tcc_bcsr* A) {
@@ -1158,14 +1199,15 @@ int tcc_bcsr_spmm_packed(const tcc_bcsr* A, const void* packedX, float* Y, std::
 int tcc_bcsr_spmm_mixed(const tcc_bcsr* A, const tcc_feature_source* src, float* Y, std::uint32_t featureDim,
                         int accumulate, void* stream) {
     clear_last_error();
-    TCC_REQUIRE(bcsr_ok(A) && src && Y && featureDim >= 1 && src->id_map && src->cache_search_map &&
-                    src->gpu_feature_cache && src->gpu_node_capacity > 0,
-                TCC_ERR_INVALID_ARGUMENT, "invalid mixed BCSR SpMM arguments");
+    TCC_REQUIRE(bcsr_ok(A) && source_ok(src) && Y && featureDim >= 1, TCC_ERR_INVALID_ARGUMENT,
+                "invalid mixed BCSR SpMM arguments");
     GatherArgs a = bcsr_args(A, nullptr, Y, featureDim, accumulate);
-    a.mixed = mixed_args(src);
+    a.mixed = mixed_args(src, featureDim);
     // Hot-cache bases live in a device pointer table and are taken to be
     // 16-byte aligned (hipMalloc / torch allocations); host rows are checked.
-    const int V = pick_vec(featureDim, {Y, src->cpu_features});
+    const int V = mixed_vec(src, featureDim, Y);
+    if (src->row_format == TCC_ROWS_TF32_PACKED)
+        return launch_gather<Src::MixedPacked>(a, V, A->unitBlocks, as_stream(stream));
     return launch_gather<Src::Mixed>(a, V, A->unitBlocks, as_stream(stream));
 }
 
@@ -1219,15 +1261,14 @@ int tcc_spmm_cnic_forward_mixed(const tcc_bcsr* bcsr, const tcc_bcsc* bcsc, cons
     clear_last_error();
     TCC_REQUIRE(bcsr_ok(bcsr) && bcsc_ok(bcsc) && src && denseC && featureDim >= 1, TCC_ERR_INVALID_ARGUMENT,
                 "invalid spmm_cnic mixed forward arguments");
-    TCC_REQUIRE(src->id_map && src->cache_search_map && src->gpu_feature_cache && src->gpu_node_capacity > 0,
-                TCC_ERR_INVALID_ARGUMENT, "invalid spmm_cnic mixed forward feature source");
+    TCC_REQUIRE(source_ok(src), TCC_ERR_INVALID_ARGUMENT, "invalid spmm_cnic mixed forward feature source");
     const hipStream_t st = as_stream(stream);
     const std::uint64_t F = featureDim;
     // denseC = 0 over its (num_rowWindows+1)*8 rows, then both parts add in.
     TCC_HIP_CHECK(fill<float>(denseC, (static_cast<std::uint64_t>(bcsr->num_rowWindows) + 1) * 8 * F, 0.0f, st));
-    const int V = pick_vec(featureDim, {denseC, src->cpu_features});
+    const int V = mixed_vec(src, featureDim, denseC);
     GatherArgs g = bcsr_args(bcsr, nullptr, denseC, featureDim, 0);
-    g.mixed = mixed_args(src);
+    g.mixed = mixed_args(src, featureDim);
     g.atomicOut = 1;
     ScatterArgs s = bcsc_args(bcsc, nullptr, denseC, featureDim);
     s.mixed = g.mixed;
@@ -1239,16 +1280,23 @@ int tcc_spmm_cnic_forward_mixed(const tcc_bcsr* bcsr, const tcc_bcsc* bcsc, cons
     const dim3 grid(static_cast<unsigned>(gWG + sWG));
     const auto gn = static_cast<std::uint32_t>(gWG), sn = static_cast<std::uint32_t>(sWG);
     const bool gv = g.data != nullptr, sv = s.data != nullptr;
-#define TCC_MIXED_LAUNCH(VV)                                                                                      \
-    do {                                                                                                          \
-        if (gv && sv) hipLaunchKernelGGL((mixed_forward_kernel<VV, true, true>), grid, dim3(kThreads), 0, st, g, s, gn, sn);   \
-        else if (gv) hipLaunchKernelGGL((mixed_forward_kernel<VV, true, false>), grid, dim3(kThreads), 0, st, g, s, gn, sn); \
-        else if (sv) hipLaunchKernelGGL((mixed_forward_kernel<VV, false, true>), grid, dim3(kThreads), 0, st, g, s, gn, sn); \
-        else hipLaunchKernelGGL((mixed_forward_kernel<VV, false, false>), grid, dim3(kThreads), 0, st, g, s, gn, sn);        \
+    const bool packed = src->row_format == TCC_ROWS_TF32_PACKED;
+#define TCC_MIXED_LAUNCH(VV, P)                                                                                          \
+    do {                                                                                                                 \
+        if (gv && sv) hipLaunchKernelGGL((mixed_forward_kernel<VV, true, true, P>), grid, dim3(kThreads), 0, st, g, s, gn, sn);   \
+        else if (gv) hipLaunchKernelGGL((mixed_forward_kernel<VV, true, false, P>), grid, dim3(kThreads), 0, st, g, s, gn, sn); \
+        else if (sv) hipLaunchKernelGGL((mixed_forward_kernel<VV, false, true, P>), grid, dim3(kThreads), 0, st, g, s, gn, sn); \
+        else hipLaunchKernelGGL((mixed_forward_kernel<VV, false, false, P>), grid, dim3(kThreads), 0, st, g, s, gn, sn);        \
     } while (0)
-    if (V == 4) TCC_MIXED_LAUNCH(4);
-    else if (V == 2) TCC_MIXED_LAUNCH(2);
-    else TCC_MIXED_LAUNCH(1);
+    if (packed) {
+        if (V == 4) TCC_MIXED_LAUNCH(4, true);
+        else if (V == 2) TCC_MIXED_LAUNCH(2, true);
+        else TCC_MIXED_LAUNCH(1, true);
+    } else {
+        if (V == 4) TCC_MIXED_LAUNCH(4, false);
+        else if (V == 2) TCC_MIXED_LAUNCH(2, false);
+        else TCC_MIXED_LAUNCH(1, false);
+    }
 #undef TCC_MIXED_LAUNCH
     TCC_LAUNCH_CHECK();
     return TCC_OK;

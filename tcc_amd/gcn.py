@@ -227,9 +227,14 @@ class FeatureTable:
     """Features of every node: the hot rows (top `hot_fraction` of nodes by
     in-degree as a source, ties by id) in an HBM cache, all rows in mapped
     pinned host memory, and the tcc_feature_source that resolves them
-    (cache_search_map = hot rank or -1, id_map = identity)."""
+    (cache_search_map = hot rank or -1, id_map = identity).
 
-    def __init__(self, X: torch.Tensor, cols: torch.Tensor, hot_fraction: float = 0.2):
+    packed=True stores both tables as TF32 rows packed by tcc_tf32_pack: the
+    first layer's products round X to TF32 anyway, so they are the same bit
+    for bit, and a cold row crosses the host link in 2.5 instead of 4 bytes
+    per feature.  The default keeps the reference's fp32 rows."""
+
+    def __init__(self, X: torch.Tensor, cols: torch.Tensor, hot_fraction: float = 0.2, packed: bool = False):
         n, F = X.shape
         deg = torch.bincount(cols.long().cuda(), minlength=n)
         n_hot = max(1, int(round(n * hot_fraction)))
@@ -240,14 +245,25 @@ class FeatureTable:
         self.hot[hot_ids] = True
         csm = torch.full((n,), -1, dtype=torch.int32, device="cuda")
         csm[hot_ids] = torch.arange(n_hot, dtype=torch.int32, device="cuda")
-        self.cache = X.cuda()[hot_ids].contiguous()
-        self.host = PinnedArray((n, F))
-        self.host.array[:] = X.cpu().numpy()
+        Xd = X.cuda()
+        if packed:
+            self.cache = swtcf.tf32_pack(Xd[hot_ids].contiguous())
+            rows = swtcf.tf32_pack(Xd)
+            self.host = PinnedArray((rows.numel(),), dtype=np.uint8)
+            self.host.array[:] = rows.cpu().numpy()
+            del rows
+        else:
+            self.cache = Xd[hot_ids].contiguous()
+            self.host = PinnedArray((n, F))
+            self.host.array[:] = X.cpu().numpy()
+        del Xd
         self.ptrs = torch.tensor([self.cache.data_ptr()], dtype=torch.int64, device="cuda")
         self.ids = torch.arange(n, dtype=torch.int32, device="cuda")
         self.csm = csm
-        self.source = swtcf.feature_source(self.ids, csm, self.ptrs, n_hot, self.host.device_ptr, n * F)
+        fmt = swtcf.ROWS_TF32_PACKED if packed else swtcf.ROWS_FP32
+        self.source = swtcf.feature_source(self.ids, csm, self.ptrs, n_hot, self.host.device_ptr, n * F, fmt)
         self.n_hot = n_hot
+        self.packed = packed
 
     def free(self) -> None:
         self.host.free()

@@ -425,15 +425,21 @@ class FeatureSourceHandle:
         self._keep = keep
 
 
+# tcc_feature_source.row_format
+ROWS_FP32 = 0
+ROWS_TF32_PACKED = 1
+
+
 def feature_source(id_map: torch.Tensor, cache_search_map: torch.Tensor, gpu_cache_ptrs: torch.Tensor,
-                   gpu_node_capacity: int, cpu_features_dev_ptr: int, cpu_len: int) -> FeatureSourceHandle:
+                   gpu_node_capacity: int, cpu_features_dev_ptr: int, cpu_len: int,
+                   row_format: int = ROWS_FP32) -> FeatureSourceHandle:
     for t, name in ((id_map, "id_map"), (cache_search_map, "cache_search_map")):
         if t.dtype != torch.int32 or not t.is_cuda or not t.is_contiguous():
             raise TypeError(f"{name} must be a contiguous int32 device tensor")
     if gpu_cache_ptrs.dtype != torch.int64 or not gpu_cache_ptrs.is_cuda:
         raise TypeError("gpu_cache_ptrs must be an int64 device tensor of device pointers")
     s = FeatureSource(id_map.data_ptr(), cache_search_map.data_ptr(), gpu_cache_ptrs.data_ptr(), gpu_node_capacity,
-                      cpu_features_dev_ptr, cpu_len, gpu_cache_ptrs.numel())
+                      cpu_features_dev_ptr, cpu_len, gpu_cache_ptrs.numel(), row_format)
     return FeatureSourceHandle(s, (id_map, cache_search_map, gpu_cache_ptrs))
 
 

@@ -147,6 +147,34 @@ def test_two_layer_paths_agree(gpu, F, H, C):
 
 
 @pytest.mark.gpu
+def test_packed_feature_table_gives_the_same_step(gpu):
+    """FeatureTable(packed=True) holds TF32 rows packed in 2.5 bytes: the
+    first layer rounds X to TF32 anyway, so the step agrees with the fp32
+    table (up to the atomics' summation order)."""
+    from tcc_amd import gcn
+    from tcc_amd.graphs import rmat_graph
+
+    n, F = 3001, 100
+    rows, cols = rmat_graph(n, 40_000, 41)
+    torch.manual_seed(4)
+    X = torch.randn((n, F))
+    res = []
+    for packed in (False, True):
+        table = gcn.FeatureTable(X, cols, packed=packed)
+        g1, g2 = gcn.build_gcn_graphs(rows, cols, n, table.hot)
+        torch.manual_seed(5)
+        model = gcn.GCN(F, 64, 2).cuda()
+        labels = gcn.synthetic_labels(n, 2, 7)
+        pred = model(g1, g2, table.source)
+        gcn.cross_entropy(pred, labels).backward()
+        torch.cuda.synchronize()
+        res.append((pred.detach().cpu(), model.conv1.weights.grad.cpu(), model.conv_final.weights.grad.cpu()))
+        table.free()
+    for a, b in zip(res[0], res[1]):
+        assert rel_l2(a.numpy(), b.double().numpy()) < 1e-5
+
+
+@pytest.mark.gpu
 def test_dropout_takes_the_layer_path(gpu):
     """With dropout in training the model runs layer by layer (the mask sits
     between the layers); in eval mode dropout is the identity and the fused

@@ -338,6 +338,57 @@ def test_mixed_forward_values_widths_units(gpu, oracle, F, vals_hot, vals_cold, 
     cpu.free()
 
 
+@pytest.mark.parametrize("F,values,K", [(37, True, 0), (100, False, 3), (256, True, 0), (301, True, 2),
+                                         (602, False, 0)])
+def test_mixed_forward_packed_rows(gpu, oracle, F, values, K):
+    """A feature source of packed TF32 rows (hot cache and host table in the
+    tcc_tf32_pack layout): the one-launch forward and the hot gather alone
+    give the oracle's TF32 product, as the fp32 rows do (F = 301, 602: 4-wide
+    chunks with a partial last lane)."""
+    from tcc_amd import swtcf
+    from tcc_amd.hostmem import PinnedArray
+
+    nr = nc = 1300
+    dst, src = random_coo(nr, nc, 26000, 70 + F)
+    rng = np.random.default_rng(71 + F)
+    vals = rng.uniform(0.5, 1.5, dst.size).astype(np.float32)
+    feats = rng.standard_normal((nc, F)).astype(np.float32)
+    hot_ids = np.sort(rng.choice(nc, size=nc // 3, replace=False))
+    csm = np.full(nc, -1, np.int32)
+    csm[hot_ids] = np.arange(hot_ids.size, dtype=np.int32)
+    id_map = np.arange(nc, dtype=np.int32)
+    hot_cache = swtcf.tf32_pack(torch.from_numpy(feats[hot_ids]).cuda())
+    rows = swtcf.tf32_pack(torch.from_numpy(feats).cuda()).cpu().numpy()
+    cpu = PinnedArray((rows.size,), dtype=np.uint8)
+    cpu.array[:] = rows
+    ptrs = torch.tensor([hot_cache.data_ptr()], dtype=torch.int64, device="cuda")
+    id_map_d = torch.from_numpy(id_map).cuda()
+    csm_d = torch.from_numpy(csm).cuda()
+    src_desc = swtcf.feature_source(id_map_d, csm_d, ptrs, hot_ids.size, cpu.device_ptr, nc * F,
+                                    swtcf.ROWS_TF32_PACKED)
+    h = csm[src] >= 0
+    vh = torch.from_numpy(vals[h]).cuda() if values else None
+    vc = torch.from_numpy(vals[~h]).cuda() if values else None
+    A = swtcf.coo_to_bcsr(dev_u32(dst[h]), dev_u32(src[h]), vh, nr, nc)
+    B = swtcf.coo_to_bcsc(dev_u32(dst[~h]), dev_u32(src[~h]), vc, nr, nc)
+    A.set_unit_blocks(K)
+    B.set_unit_blocks(K)
+    denseC = torch.full(((A.view.num_rowWindows + 1) * 8, F), 3.0, device="cuda")
+    swtcf.spmm_cnic_forward_mixed(A, B, src_desc, denseC, F)
+    used = vals if values else None
+    rowptr, colind, v = csr_of(dst, src, nr, used)
+    want = oracle.csr_spmm(rowptr, colind, v, feats, use_tf32=True)
+    C = denseC.cpu().numpy()
+    assert_close(C[:nr], want)
+    assert np.all(C[nr:] == 0)
+    # the hot gather alone (tcc_bcsr_spmm_mixed) over the hot edges
+    Yh = swtcf.bcsr_spmm_mixed(A, src_desc, torch.empty((A.view.num_rowWindows * 8, F), device="cuda"), F)
+    rp, ci, vv = csr_of(dst[h], src[h], nr, vals[h] if values else None)
+    assert_close(Yh.cpu().numpy()[:nr], oracle.csr_spmm(rp, ci, vv, feats, use_tf32=True))
+    torch.cuda.synchronize()
+    cpu.free()
+
+
 # ------------------------------------------------------------------ units of work
 def skewed_coo(nr, nc, seed):
     """A few dense hub rows and hub columns over a sparse background, with
