@@ -374,9 +374,11 @@ void relu_forward_launch(const ReluFwdArgs& a, hipStream_t st) {
 // C[m][n] (=|+=) sum over splits of partial[s][m][n], splits added in a fixed
 // order: 16 elements per workgroup, 16 interleaved groups of splits summed
 // per thread, then the 16 group sums in order.
+// With `transposed` the partials hold C^T (an M x N block of C^T is C's
+// N x M block): element (m, n) of the partials goes to C[n][m].
 __global__ void __launch_bounds__(256) tn_reduce_kernel(const float* __restrict__ partial, std::uint32_t splits,
                                                         std::uint32_t M, std::uint32_t N, float* __restrict__ C,
-                                                        std::uint32_t ldc, int accumulate) {
+                                                        std::uint32_t ldc, int accumulate, int transposed) {
     __shared__ float part[16][17];
     const std::uint64_t MN = static_cast<std::uint64_t>(M) * N;
     const unsigned col = threadIdx.x & 15u, grp = threadIdx.x >> 4;
@@ -391,7 +393,7 @@ __global__ void __launch_bounds__(256) tn_reduce_kernel(const float* __restrict_
 #pragma unroll
         for (int g = 0; g < 16; ++g) t += part[g][col];
         const std::uint32_t m = static_cast<std::uint32_t>(e / N), n = static_cast<std::uint32_t>(e % N);
-        float* c = C + static_cast<std::uint64_t>(m) * ldc + n;
+        float* c = transposed ? C + static_cast<std::uint64_t>(n) * ldc + m : C + static_cast<std::uint64_t>(m) * ldc + n;
         *c = accumulate ? *c + t : t;
     }
 }
@@ -400,10 +402,12 @@ __global__ void __launch_bounds__(256) tn_reduce_kernel(const float* __restrict_
 //  - anything wide: 4 waves side by side along N, each with TM x 4 tiles
 //    (TM = 4, 7 or 8, the fewest that cover M, so that a 100-wide layer does
 //    not multiply a 128-wide tile column); 4 tiles along N reuse each A
-//    operand 4 times from registers: 100x256 runs at ~100 TFLOP/s, against
+//    operand 4 times from registers: 100x256 runs at ~110 TFLOP/s, against
 //    ~50 with 8 waves of 7x2 tiles.  These waves hold ~340 registers (one
 //    wave per SIMD); limiting them to 256 for two waves per SIMD measured
-//    1.6-1.9x slower;
+//    1.6-1.9x slower.  Six 4-row steps per buffer (24 rows in flight ahead
+//    of the multiply) measured 1.14 ms against 1.23-1.32 with four; the
+//    relu-gradient form, at 256 VGPRs, keeps four;
 //  - N <= 16 (a class-width gradient): 4 waves along M with 4 x 1 tiles,
 //    eight workgroups per CU for memory parallelism (~5 TB/s for 256x2);
 //    M <= 16 the same along N.
@@ -417,8 +421,10 @@ struct TnPlan {
     std::uint32_t splits, rowsPerSplit;
 };
 
-// Shape chosen from (M, N); block counts from (realM, realN) when given.
-TnPlan tn_plan(std::uint32_t K, std::uint32_t M, std::uint32_t N, std::uint32_t realM = 0, std::uint32_t realN = 0) {
+// Shape chosen from (M, N); block counts from (realM, realN) and the rows per
+// iteration from `step` when given.
+TnPlan tn_plan(std::uint32_t K, std::uint32_t M, std::uint32_t N, std::uint32_t realM = 0, std::uint32_t realN = 0,
+               std::uint32_t step = 0) {
     TnPlan p{};
     if (N <= 16) {
         p.shape = TnShape::NarrowN;  // TM=4, TN=1, WM=4, WN=1, U=8
@@ -427,13 +433,14 @@ TnPlan tn_plan(std::uint32_t K, std::uint32_t M, std::uint32_t N, std::uint32_t 
         p.shape = TnShape::NarrowM;  // TM=1, TN=4, WM=1, WN=4, U=8
         p.step = 32, p.BM = 16, p.BN = 256;
     } else {
-        // TM in {4, 7, 8}, TN=4, WM=1, WN=4, U=4
+        // TM in {4, 7, 8}, TN=4, WM=1, WN=4, U=6 (U=4 for the relu-gradient form)
         p.shape = M <= 64 ? TnShape::Wide4 : M <= 112 ? TnShape::Wide7 : TnShape::Wide8;
-        p.step = 16, p.BN = 256;
+        p.step = 24, p.BN = 256;
         p.BM = p.shape == TnShape::Wide4 ? 64 : p.shape == TnShape::Wide7 ? 112 : 128;
     }
     if (realM != 0) M = realM;
     if (realN != 0) N = realN;
+    if (step != 0) p.step = step;
     p.blocksM = (M + p.BM - 1) / p.BM;
     p.blocksN = (N + p.BN - 1) / p.BN;
     const std::uint64_t blocks = static_cast<std::uint64_t>(p.blocksM) * p.blocksN;
@@ -450,15 +457,22 @@ TnPlan tn_plan(std::uint32_t K, std::uint32_t M, std::uint32_t N, std::uint32_t 
     return p;
 }
 
+// C = A^T B or, when N is the narrow side of a wide product (17..128 and
+// below M), C^T = B^T A: the wide tiles lay 4 waves of 64 columns along N,
+// so a narrow N would leave waves multiplying padding (602 x 64 ran at 10 ms
+// as C, 2.5x torch.mm).
+inline bool tn_swapped(std::uint32_t M, std::uint32_t N) { return M > 16 && N > 16 && N <= 128 && N < M; }
+
 template <int TM, int TN, int WM, int WN, int U, int CT = 0>
 void tn_launch(const TnArgs& a, const TnPlan& p, hipStream_t st) {
     hipLaunchKernelGGL((tn_partial_kernel<TM, TN, WM, WN, U, CT>), dim3(p.splits, p.blocksM * p.blocksN),
                        dim3(kWave * WM * WN), 0, st, a);
 }
 
-// The relu-gradient form always takes the wide shapes (N is the hidden width).
+// The relu-gradient form always takes the wide shapes (N is the hidden width)
+// with 16 rows per iteration (4 steps of 4; 8-class tiles take 2 x 4).
 TnPlan relu_grad_plan(std::uint32_t K, std::uint32_t F, std::uint32_t Hd) {
-    return tn_plan(K, std::max<std::uint32_t>(F, 17), std::max<std::uint32_t>(Hd, 17), F, Hd);
+    return tn_plan(K, std::max<std::uint32_t>(F, 17), std::max<std::uint32_t>(Hd, 17), F, Hd, 16);
 }
 
 }  // namespace
@@ -470,7 +484,7 @@ extern "C" {
 
 size_t tcc_dense_tn_workspace_bytes(std::uint32_t K, std::uint32_t M, std::uint32_t N) {
     if (K == 0 || M == 0 || N == 0) return 0;
-    const TnPlan p = tn_plan(K, M, N);
+    const TnPlan p = tn_swapped(M, N) ? tn_plan(K, N, M) : tn_plan(K, M, N);
     return static_cast<size_t>(p.splits) * M * N * sizeof(float);
 }
 
@@ -490,6 +504,12 @@ int tcc_dense_tn(const float* A, std::uint32_t lda, const float* B, std::uint32_
         return TCC_OK;
     }
     TCC_REQUIRE(A && B && workspace, TCC_ERR_INVALID_ARGUMENT, "invalid dense A^T B arguments");
+    const bool swapped = tn_swapped(M, N);
+    if (swapped) {  // C^T = B^T A
+        std::swap(A, B);
+        std::swap(lda, ldb);
+        std::swap(M, N);
+    }
     const TnPlan p = tn_plan(K, M, N);
     TCC_REQUIRE(workspaceBytes >= static_cast<size_t>(p.splits) * M * N * sizeof(float), TCC_ERR_INVALID_ARGUMENT,
                 "dense A^T B workspace too small (tcc_dense_tn_workspace_bytes)");
@@ -509,14 +529,14 @@ int tcc_dense_tn(const float* A, std::uint32_t lda, const float* B, std::uint32_
     switch (p.shape) {
         case TnShape::NarrowN: tn_launch<4, 1, 4, 1, 8>(a, p, st); break;
         case TnShape::NarrowM: tn_launch<1, 4, 1, 4, 8>(a, p, st); break;
-        case TnShape::Wide4: tn_launch<4, 4, 1, 4, 4>(a, p, st); break;
-        case TnShape::Wide7: tn_launch<7, 4, 1, 4, 4>(a, p, st); break;
-        default: tn_launch<8, 4, 1, 4, 4>(a, p, st); break;
+        case TnShape::Wide4: tn_launch<4, 4, 1, 4, 6>(a, p, st); break;
+        case TnShape::Wide7: tn_launch<7, 4, 1, 4, 6>(a, p, st); break;
+        default: tn_launch<8, 4, 1, 4, 6>(a, p, st); break;
     }
     TCC_LAUNCH_CHECK();
     const std::uint64_t MN = static_cast<std::uint64_t>(M) * N;
     hipLaunchKernelGGL(tn_reduce_kernel, dim3(grid_for(MN, 16)), dim3(256), 0, st,
-                       static_cast<const float*>(workspace), p.splits, M, N, C, ldc, accumulate);
+                       static_cast<const float*>(workspace), p.splits, M, N, C, ldc, accumulate, swapped ? 1 : 0);
     TCC_LAUNCH_CHECK();
     return TCC_OK;
 }
@@ -611,10 +631,10 @@ int tcc_gcn_relu_grad(const float* AX, std::uint32_t ldax, const float* H, std::
     }
     TCC_LAUNCH_CHECK();
     hipLaunchKernelGGL(tn_reduce_kernel, dim3(grid_for(static_cast<std::uint64_t>(F) * Hd, 16)), dim3(256), 0, st,
-                       a.partial, p.splits, F, Hd, dW1, Hd, 0);
+                       a.partial, p.splits, F, Hd, dW1, Hd, 0, 0);
     TCC_LAUNCH_CHECK();
     hipLaunchKernelGGL(tn_reduce_kernel, dim3(grid_for(static_cast<std::uint64_t>(Hd) * C, 16)), dim3(256), 0, st,
-                       a.partial2, p.splits, Hd, C, dW2, C, 0);
+                       a.partial2, p.splits, Hd, C, dW2, C, 0, 0);
     TCC_LAUNCH_CHECK();
     return TCC_OK;
 }

@@ -31,6 +31,7 @@ SHAPES = [
     (1, 1, 1), (3, 5, 7), (4, 16, 16), (17, 100, 256), (33, 2, 256), (1000, 100, 256), (4099, 256, 2),
     (777, 17, 300), (3001, 300, 40), (513, 8, 600), (100, 129, 257), (5000, 64, 64), (2047, 112, 512),
     (200003, 100, 256), (150001, 256, 2), (65537, 2, 256),
+    (50000, 602, 64), (3000, 200, 17), (4099, 130, 128),  # N narrow: computed as C^T = B^T A
 ]
 
 
@@ -44,12 +45,14 @@ def test_dense_tn_matches_float64(K, M, N):
     assert rel_l2(C, A.double().t() @ B.double()) < REL
 
 
-def test_dense_tn_strided_rows_and_accumulate():
+@pytest.mark.parametrize("M,N", [(100, 256), (256, 100)])
+def test_dense_tn_strided_rows_and_accumulate(M, N):
     """Row strides above the width (a view of wider buffers, as the layer's
-    AX view of denseC) and C += A^T B into a strided C."""
+    AX view of denseC) and C += A^T B into a strided C, in both orientations
+    (256 x 100 runs as C^T = B^T A)."""
     from tcc_amd import swtcf
 
-    K, M, N = 9001, 100, 256
+    K = 9001
     A0, B0 = inputs(K, M + 28, N + 3, 5)
     A, B = A0[:, 3:3 + M], B0[:, :N]
     assert A.stride(0) == M + 28 and B.stride(0) == N + 3
