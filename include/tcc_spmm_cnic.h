@@ -115,7 +115,9 @@ int tcc_bcsr_spmm(const tcc_bcsr* A, const float* X, float* Y, uint32_t featureD
  * mantissa bits of element pairs (element 2k in bits 0-2 and 2k+1 in bits
  * 3-5 of byte k; ceil(n/2) bytes).  A full chunk is 640 bytes; the last is
  * padded to 16 bytes; a row of more than one chunk is padded to 128 bytes,
- * a single-chunk row to 16 (tcc_tf32_packed_bytes / rows).  The gather over
+ * a single-chunk row to 16 (tcc_tf32_packed_bytes / rows).  A NaN is stored
+ * as a quiet NaN with its top 19 bits (the low payload bits do not fit); all
+ * other values, inf included, unpack to TF32(x) exactly.  The gather over
  * packed rows reads 37.5% fewer bytes per gathered row than fp32 X, with
  * bit-identical products, and each 256-feature chunk it loads covers whole
  * 128-byte lines; it pays off when rows are gathered many times

@@ -109,13 +109,13 @@ template <int V>
 __device__ __forceinline__ Vec<V> load_vec(const float* p) {
     Vec<V> r;
     if constexpr (V == 4) {
-        const float4 t = *reinterpret_cast<const float4*>(p);
+        const vf4 t = load_global<vf4>(p);
         r.v[0] = t.x; r.v[1] = t.y; r.v[2] = t.z; r.v[3] = t.w;
     } else if constexpr (V == 2) {
-        const float2 t = *reinterpret_cast<const float2*>(p);
+        const vf2 t = load_global<vf2>(p);
         r.v[0] = t.x; r.v[1] = t.y;
     } else {
-        r.v[0] = *p;
+        r.v[0] = load_global<float>(p);
     }
     return r;
 }
@@ -270,16 +270,16 @@ __device__ __forceinline__ PackedVec<V> load_packed(const unsigned char* row, st
     PackedVec<V> p;
     const PackedAt at = packed_at(F, f);
     if constexpr (V == 4) {
-        const uint2 h = *reinterpret_cast<const uint2*>(row + at.hi);
+        const vu2 h = load_global<vu2>(row + at.hi);
         p.hi[0] = h.x;
         p.hi[1] = h.y;
-        p.lo = *reinterpret_cast<const std::uint16_t*>(row + at.lo);
+        p.lo = load_global<std::uint16_t>(row + at.lo);
     } else if constexpr (V == 2) {
-        p.hi[0] = *reinterpret_cast<const std::uint32_t*>(row + at.hi);
-        p.lo = row[at.lo];
+        p.hi[0] = load_global<std::uint32_t>(row + at.hi);
+        p.lo = load_global<unsigned char>(row + at.lo);
     } else {
-        p.hi[0] = *reinterpret_cast<const std::uint16_t*>(row + at.hi);
-        p.lo = row[at.lo] >> (3 * (f & 1u));
+        p.hi[0] = load_global<std::uint16_t>(row + at.hi);
+        p.lo = load_global<unsigned char>(row + at.lo) >> (3 * (f & 1u));
     }
     return p;
 }
@@ -446,7 +446,9 @@ __device__ __forceinline__ void gather_body(const GatherArgs& a, std::uint32_t g
     // touched), any other is stored whole.
     // V-wide stores when F % V == 0 (then rows keep V-float alignment), else
     // (the packed gather's 4-wide chunks over any F) one float at a time.
-    const bool vecStore = a.F % V == 0;
+    // Only the packed sources pick V without F % V == 0.
+    constexpr bool kWhole = MODE != Src::Packed && MODE != Src::MixedPacked;
+    const bool vecStore = kWhole || a.F % V == 0;
     auto flush = [&]() {
         if (active) {
             float* out = a.Y + static_cast<std::uint64_t>(w) * 8 * a.F + f0;
@@ -458,7 +460,7 @@ __device__ __forceinline__ void gather_body(const GatherArgs& a, std::uint32_t g
                     if (((touched >> (8 * r)) & 0xFFu) == 0) continue;
 #pragma unroll
                     for (int v = 0; v < V; ++v)
-                        if (f0 + v < a.F) atomic_add_f32(o + v, acc[r][v]);
+                        if (kWhole || f0 + v < a.F) atomic_add_f32(o + v, acc[r][v]);
                 } else if (vecStore) {
                     store_vec<V>(o, acc[r], a.accumulate != 0);
                 } else {
@@ -751,8 +753,14 @@ __global__ void tf32_pack_kernel(const float* __restrict__ X, std::uint32_t rows
     const std::uint32_t e = 2 * p;
     const float* x = X + r * F;
     const bool two = e + 1 < F;
-    const std::uint32_t b0 = __float_as_uint(tf32_rna(x[e]));
-    const std::uint32_t b1 = two ? __float_as_uint(tf32_rna(x[e + 1])) : 0u;
+    // A NaN keeps its top 19 bits with the quiet bit set, so that a payload
+    // held only in the dropped low bits does not unpack as inf.
+    const auto pack_bits = [](float v) {
+        const std::uint32_t b = __float_as_uint(tf32_rna(v));
+        return __builtin_isnan(v) ? (b | 0x00400000u) : b;
+    };
+    const std::uint32_t b0 = pack_bits(x[e]);
+    const std::uint32_t b1 = two ? pack_bits(x[e + 1]) : 0u;
     unsigned char* row = out + r * stride;
     const PackedAt at = packed_at(F, e);  // e even: the pair lies in one chunk
     if (two) {

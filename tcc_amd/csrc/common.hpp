@@ -58,11 +58,30 @@ inline std::uint32_t device_cus() {
 // ---------------------------------------------------------------- numerics
 // cvt.rna.tf32.f32 restated from its definition: round to nearest with ties
 // away from zero, keeping 10 explicit mantissa bits; inf and NaN unchanged.
-// (Reference use: include/mma_tf32.cuh:17-22.)
+// (Reference use: include/mma_tf32.cuh:17-22.)  The add-and-mask maps +-inf
+// to themselves and carries the largest finite values into inf, as rounding
+// does, so only NaN (whose payload could carry into the sign) is passed
+// through: 4 instructions.
 __device__ __forceinline__ float tf32_rna(float x) {
     const std::uint32_t b = __float_as_uint(x);
-    const std::uint32_t r = ((b & 0x7F800000u) == 0x7F800000u) ? b : ((b + 0x1000u) & 0xFFFFE000u);
+    const std::uint32_t r = __builtin_isnan(x) ? b : ((b + 0x1000u) & 0xFFFFE000u);
     return __uint_as_float(r);
+}
+
+// ---------------------------------------------------------------- loads
+// A load through a global-address-space pointer.  Row pointers rebuilt from
+// integers (v_readlane of a pointer table) are generic to the compiler and
+// would become flat loads, which also count against the LDS/scalar wait
+// counter, so every wait for a scalar load would wait for them too.
+// T is a scalar or a clang vector type (vf2, vf4, vu2).
+using vf2 = float __attribute__((ext_vector_type(2)));
+using vf4 = float __attribute__((ext_vector_type(4)));
+using vu2 = std::uint32_t __attribute__((ext_vector_type(2)));
+
+template <typename T>
+__device__ __forceinline__ T load_global(const void* p) {
+    // through an integer: a direct cast of a generic pointer stays flat
+    return *(const __attribute__((address_space(1))) T*)(reinterpret_cast<std::uintptr_t>(p));
 }
 
 // ---------------------------------------------------------------- wave64

@@ -522,6 +522,23 @@ def test_tf32_pack_is_exact(gpu, oracle, F):
     assert np.array_equal(got, want)
 
 
+def test_tf32_pack_keeps_nan(gpu):
+    """NaN stays NaN in the packed rows, also when its payload lies only in
+    the 13 low bits that TF32 drops (it unpacks quiet, top 19 bits kept)."""
+    from tcc_amd import swtcf
+
+    F = 300
+    X = np.random.default_rng(5).standard_normal((3, F)).astype(np.float32)
+    nans = np.array([0x7F800001, 0xFF800001, 0x7FC00000, 0x7F801000, 0xFFFFFFFF, 0x7FFFF000], np.uint32)
+    X.reshape(-1)[[0, 7, 255, 256, 299, 600]] = nans.view(np.float32)
+    got = unpack_host(swtcf.tf32_pack(torch.from_numpy(X).cuda()).cpu().numpy(), 3, F)
+    isnan = np.isnan(X)
+    assert np.isnan(got.view(np.float32)[isnan]).all()
+    # sign and top bits kept, quiet bit set
+    assert np.array_equal(got[isnan], (nans & 0xFFFFE000) | 0x00400000)
+    assert np.array_equal(got[~isnan], (X[~isnan].view(np.uint32) + 0x1000) & 0xFFFFE000)
+
+
 @pytest.mark.parametrize("unit_blocks", [0, 3])
 @pytest.mark.parametrize("F", [1, 2, 64, 100, 128, 256, 257, 300, 513, 602])
 def test_bcsr_spmm_packed(gpu, oracle, unit_blocks, F):
