@@ -173,7 +173,8 @@ int tcc_bcsr_spmm_mixed(const tcc_bcsr* A, const tcc_feature_source* src, float*
  *         block (the SWTCF row order with one window per super-window).
  * Each synchronises `stream` (to size the output), places all arrays in one
  * device allocation returned in *allocation (free it with tcc_block_release)
- * and fills *out with views into it.  `data` is set only when dVal != NULL. */
+ * and fills *out with views into it.  `data` is set only when dVal != NULL.
+ * nnz = 0 gives empty windows and no blocks (dRow, dCol may then be NULL). */
 int tcc_coo_to_bcsr(const uint32_t* dRow, const uint32_t* dCol, const float* dVal, uint32_t nnz,
                     uint32_t numRows, uint32_t numCols, tcc_bcsr* out, void** allocation, void* stream);
 int tcc_coo_to_bcsc(const uint32_t* dRow, const uint32_t* dCol, const float* dVal, uint32_t nnz,

@@ -316,11 +316,35 @@ int tcc_coo_to_bcsc(const std::uint32_t* dRow, const std::uint32_t* dCol, const 
                     std::uint32_t numRows, std::uint32_t numCols, tcc_bcsc* out, void** allocation,
                     void* stream) {
     clear_last_error();
-    TCC_REQUIRE(out && allocation && numRows >= 1 && numCols >= 1 && nnz >= 1 && dRow && dCol,
+    TCC_REQUIRE(out && allocation && numRows >= 1 && numCols >= 1 && (nnz == 0 || (dRow && dCol)),
                 TCC_ERR_INVALID_ARGUMENT, "invalid COO -> BCSC arguments");
     const hipStream_t st = as_stream(stream);
     std::memset(out, 0, sizeof(*out));
     *allocation = nullptr;
+    if (nnz == 0) {
+        // every column window empty and no blocks, as tcc_coo_to_bcsr gives
+        // for no edges (the converter below needs at least one edge)
+        const std::uint32_t CW = (numCols + 7) / 8;
+        const std::size_t offBytes = align_up(4ull * (CW + 1));
+        char* o = nullptr;
+        TCC_HIP_CHECK(hipMalloc(&o, offBytes + align_up(4) + align_up(32) + align_up(8)));
+        if (fill<std::uint32_t>(reinterpret_cast<std::uint32_t*>(o), (offBytes + align_up(4) + align_up(32) + align_up(8)) / 4,
+                                0u, st) != hipSuccess ||
+            hipStreamSynchronize(st) != hipSuccess) {
+            (void)hipFree(o);
+            set_last_error("HIP error while building an empty BCSC");
+            return TCC_ERR_HIP;
+        }
+        out->num_rows = numRows;
+        out->num_cols = numCols;
+        out->num_colWindows = CW;
+        out->colWindowOffset = reinterpret_cast<std::uint32_t*>(o);
+        out->tcOffset = reinterpret_cast<std::uint32_t*>(o + offBytes);
+        out->sparseA2C = reinterpret_cast<std::uint32_t*>(o + offBytes + align_up(4));
+        out->tcLocalBit = reinterpret_cast<std::uint64_t*>(o + offBytes + align_up(4) + align_up(32));
+        *allocation = o;
+        return TCC_OK;
+    }
     tcc_swtcf_matrix m;
     tcc_swtcf_workspace ws;
     int rc = tcc_swtcf_alloc_matrix(&m, numRows, numCols, nnz, 1);

@@ -38,6 +38,8 @@ namespace {
 
 constexpr unsigned kThreads = 256;
 constexpr unsigned kWaves = kThreads / kWave;
+// Wave slots per compute unit (8 per SIMD).
+constexpr std::uint32_t kMaxWaves = 32;
 
 // Where a gather reads its input rows: fp32 X, the first layer's hot/cold
 // feature source (fp32 or packed TF32 rows), dY for the A^T product, or a
@@ -812,23 +814,43 @@ __device__ __forceinline__ std::uint32_t used_columns(const std::uint64_t* bits,
     return mask;
 }
 
-// The source rows of window w that `used` names, TF32-rounded (zeros for
-// the others and past numCols); all loads are issued before any is rounded.
+// Row pointers of window w's 8 source columns, resolved lane-parallel: lane
+// c < 8 holds column c's (null where `used` omits the column, past numCols
+// or without a row).  Resolving column by column put each lookup behind the
+// previous column's row load (loads complete in order), one host-link round
+// trip per column for the first layer's cold rows.
+template <bool MIXED>
+__device__ __forceinline__ std::uint64_t window_row_ptrs(const ScatterArgs& a, std::uint32_t w, std::uint32_t used) {
+    const unsigned lane = __lane_id();
+    const float* row = nullptr;
+    const std::uint32_t col = w * 8 + lane;
+    if (lane < 8 && ((used >> lane) & 1u) && col < a.numCols) {
+        if constexpr (MIXED) {
+            // spmm_kernel.cu:521-595: the window's sources resolved once each.
+            row = mixed_row(a.mixed, a.F, col);
+        } else {
+            row = a.X + static_cast<std::uint64_t>(col) * a.F;
+        }
+    }
+    return reinterpret_cast<std::uint64_t>(row);
+}
+
+// The window's source rows x[c] from window_row_ptrs (zeros for null), all
+// 8 loads issued before any is used; TF32-rounded unless packed as TF32.
 // Skipping unused rows matters most for the first layer's cold rows, which
 // cross the host link.
-template <int V, bool MIXED, bool PACKED = false>
-__device__ __forceinline__ void load_window_rows(const ScatterArgs& a, std::uint32_t w, std::uint32_t used,
-                                                 std::uint32_t laneOff, float (&x)[8][V]) {
+template <int V, bool PACKED>
+__device__ __forceinline__ void load_window_rows(const ScatterArgs& a, std::uint64_t rowPtrs, std::uint32_t laneOff,
+                                                 float (&x)[8][V]) {
+    const std::uint32_t lo = static_cast<std::uint32_t>(rowPtrs);
+    const std::uint32_t hi = static_cast<std::uint32_t>(rowPtrs >> 32);
     if constexpr (PACKED) {  // packed TF32 feature rows: no rounding needed
         PackedVec<V> pk[8];
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
-            const std::uint32_t col = w * 8 + c;
+            const std::uint64_t rp = (static_cast<std::uint64_t>(lane_u32(hi, c)) << 32) | lane_u32(lo, c);
             pk[c] = PackedVec<V>{};
-            if (((used >> c) & 1u) && col < a.numCols) {
-                const float* row = mixed_row(a.mixed, a.F, col);
-                if (row != nullptr) pk[c] = load_packed<V>(reinterpret_cast<const unsigned char*>(row), a.F, laneOff);
-            }
+            if (rp != 0) pk[c] = load_packed<V>(reinterpret_cast<const unsigned char*>(rp), a.F, laneOff);
         }
 #pragma unroll
         for (int c = 0; c < 8; ++c) unpack<V>(pk[c], x[c]);
@@ -836,28 +858,52 @@ __device__ __forceinline__ void load_window_rows(const ScatterArgs& a, std::uint
     }
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-        const std::uint32_t col = w * 8 + c;
+        const std::uint64_t rp = (static_cast<std::uint64_t>(lane_u32(hi, c)) << 32) | lane_u32(lo, c);
 #pragma unroll
         for (int v = 0; v < V; ++v) x[c][v] = 0.0f;
-        if (((used >> c) & 1u) && col < a.numCols) {
-            const float* row;
-            if constexpr (MIXED) {
-                // spmm_kernel.cu:521-595: the window's sources resolved once each.
-                row = mixed_row(a.mixed, a.F, col);
-            } else {
-                row = a.X + static_cast<std::uint64_t>(col) * a.F;
-            }
-            if (row != nullptr) {
-                const Vec<V> t = load_vec<V>(row + laneOff);
+        if (rp != 0) {
+            const Vec<V> t = load_vec<V>(reinterpret_cast<const float*>(rp) + laneOff);
 #pragma unroll
-                for (int v = 0; v < V; ++v) x[c][v] = t.v[v];
-            }
+            for (int v = 0; v < V; ++v) x[c][v] = t.v[v];
         }
     }
 #pragma unroll
     for (int c = 0; c < 8; ++c)
 #pragma unroll
         for (int v = 0; v < V; ++v) x[c][v] = tf32_rna(x[c][v]);
+}
+
+// Block b's metadata as one word per lane, read with v_readlane when the
+// block is processed: lanes 0-7 the output rows of its 8 block rows, lanes
+// 8-9 its bitmap and, with values, lanes 10-11 block b+1's bitmap and lane
+// 12 block b+1's value offset (so that b+1's values can be loaded while b
+// is processed).  Loaded one block ahead, before the block's atomics: loads
+// and atomics complete in order, so a load issued after them and used at
+// once would wait for all of them.
+template <bool VALUES>
+__device__ __forceinline__ std::uint32_t scatter_meta(const ScatterArgs& a, std::uint32_t b) {
+    const unsigned lane = __lane_id();
+    const std::uint32_t* bitsw = reinterpret_cast<const std::uint32_t*>(a.bits);
+    std::uint32_t m = 0;
+    if (lane < 8) {
+        m = a.idx[static_cast<std::uint64_t>(b) * 8 + lane];
+    } else if (lane < 10) {
+        m = bitsw[2ull * b + (lane - 8)];
+    } else if (VALUES && b + 1 < a.numBlocks) {
+        if (lane < 12) m = bitsw[2ull * (b + 1) + (lane - 10)];
+        else if (lane == 12) m = a.tcOffset[b + 1];
+    }
+    return m;
+}
+
+__device__ __forceinline__ std::uint64_t meta_bits(std::uint32_t m, int lane0) {
+    return (static_cast<std::uint64_t>(lane_u32(m, lane0 + 1)) << 32) | lane_u32(m, lane0);
+}
+
+// Lane i: the value of the i-th stored nonzero of a block with bitmap `bits`
+// whose values start at data[off] (unrounded; zero past its count).
+__device__ __forceinline__ float scatter_vals(const ScatterArgs& a, std::uint64_t bits, std::uint32_t off) {
+    return __lane_id() < static_cast<unsigned>(__popcll(bits)) ? a.data[off + __lane_id()] : 0.0f;
 }
 
 template <int V, bool MIXED, bool VALUES, bool PACKED = false>
@@ -879,26 +925,35 @@ __device__ __forceinline__ void scatter_body(const ScatterArgs& a, std::uint32_t
         we = a.winOffset[w + 1];
     }
     float x[8][V];
-    load_window_rows<V, MIXED, PACKED>(a, w, used_columns(a.bits, u.b0, min(we, u.b1)), laneOff, x);
+    load_window_rows<V, PACKED>(a, window_row_ptrs<MIXED>(a, w, used_columns(a.bits, u.b0, min(we, u.b1))), laneOff,
+                                x);
+    std::uint32_t cur = scatter_meta<VALUES>(a, u.b0);
+    float curVals = 0.0f;
+    if constexpr (VALUES) curVals = scatter_vals(a, a.bits[u.b0], a.tcOffset[u.b0]);
     for (std::uint32_t b = u.b0; b < u.b1; ++b) {
         if (b >= we) {
             do {
                 ++w;
                 we = a.winOffset[w + 1];
             } while (b >= we && w + 1 < a.numWindows);
-            load_window_rows<V, MIXED, PACKED>(a, w, used_columns(a.bits, b, min(we, u.b1)), laneOff, x);
+            load_window_rows<V, PACKED>(a, window_row_ptrs<MIXED>(a, w, used_columns(a.bits, b, min(we, u.b1))), laneOff,
+                                        x);
         }
-        const std::uint64_t bm = a.bits[b];
+        const std::uint64_t bm = meta_bits(cur, 8);
+        // the next block's metadata and values, loaded before this block's atomics
+        std::uint32_t nxt = cur;
+        float nxtVals = curVals;
+        if (b + 1 < u.b1) {
+            nxt = scatter_meta<VALUES>(a, b + 1);
+            if constexpr (VALUES) nxtVals = scatter_vals(a, meta_bits(cur, 10), lane_u32(cur, 12));
+        }
         float vals = 0.0f;
-        if constexpr (VALUES) {
-            if (lane < static_cast<unsigned>(__popcll(bm))) vals = a.data[a.tcOffset[b] + lane];
-            vals = tf32_rna(vals);
-        }
+        if constexpr (VALUES) vals = tf32_rna(curVals);
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
             const std::uint32_t rb = static_cast<std::uint32_t>(bm >> (8 * r)) & 0xFFu;
             if (rb == 0) continue;
-            const std::uint32_t row = a.idx[static_cast<std::uint64_t>(b) * 8 + r];
+            const std::uint32_t row = lane_u32(cur, r);
             if (row >= a.numRows) continue;  // spmm_kernel.cu:2025-2044
             float s[V];
 #pragma unroll
@@ -923,6 +978,8 @@ __device__ __forceinline__ void scatter_body(const ScatterArgs& a, std::uint32_t
                     if (f0 + v < a.F) atomic_add_f32(out + v, s[v]);
             }
         }
+        cur = nxt;
+        curVals = nxtVals;
     }
 }
 
@@ -933,20 +990,34 @@ __global__ void __launch_bounds__(kThreads) scatter_kernel(ScatterArgs a) {
 
 // The first layer's forward in one launch.  The reference runs the hot BCSR
 // gather and the cold BCSC scatter one after the other
-// (spmm_launcher.cu:30-271); here their workgroups are interleaved in
-// proportion to their counts, so that scatter waves, which wait on host
-// memory across the link, and gather waves, which stream HBM, run side by
-// side.  Both add into a zeroed Y with atomics.
+// (spmm_launcher.cu:30-271); here they run side by side.  `scatterWGs`
+// persistent scatter workgroups walk the scatter's (unit, chunk) waves with
+// a grid stride, so that a fixed number of waves keeps the host link busy
+// for the whole launch; the other workgroups are the gather's, streaming
+// HBM.  Workgroups are dispatched to the 8 XCDs round-robin, so the scatter
+// takes the workgroups i < 8*perXcd with i % 8 < xcds: it runs on `xcds`
+// XCDs of its own, apart from the gather's memory traffic (the two slowed
+// each other down when they shared compute units).  The placement only
+// affects speed: every scatter workgroup index is launched.  Both parts add
+// into a zeroed Y with atomics.
 template <int V, bool GVALUES, bool SVALUES, bool PACKED>
-__global__ void __launch_bounds__(kThreads) mixed_forward_kernel(GatherArgs g, ScatterArgs s, std::uint32_t gatherWGs,
-                                                                 std::uint32_t scatterWGs) {
-    const std::uint64_t total = static_cast<std::uint64_t>(gatherWGs) + scatterWGs;
+__global__ void __launch_bounds__(kThreads) mixed_forward_kernel(GatherArgs g, ScatterArgs s, std::uint32_t xcds,
+                                                                 std::uint32_t perXcd) {
     const std::uint32_t i = blockIdx.x;
-    const auto before = static_cast<std::uint32_t>(static_cast<std::uint64_t>(i) * scatterWGs / total);
-    const auto upto = static_cast<std::uint32_t>(static_cast<std::uint64_t>(i + 1) * scatterWGs / total);
     const std::uint32_t wave = uniform(threadIdx.x / kWave);
-    if (upto > before) scatter_body<V, true, SVALUES, PACKED>(s, before * kWaves + wave);  // the before-th scatter group
-    else gather_body<V, PACKED ? Src::MixedPacked : Src::Mixed, GVALUES>(g, (i - before) * kWaves + wave);
+    const std::uint32_t slot = i & 7u;
+    const bool head = i < 8u * perXcd;
+    if (head && slot < xcds) {
+        const std::uint32_t scatterWGs = xcds * perXcd;
+        const std::uint64_t waves = static_cast<std::uint64_t>(s.numUnits) * s.numChunks;
+        for (std::uint64_t gw = static_cast<std::uint64_t>((i >> 3) * xcds + slot) * kWaves + wave; gw < waves;
+             gw += static_cast<std::uint64_t>(scatterWGs) * kWaves)
+            scatter_body<V, true, SVALUES, PACKED>(s, static_cast<std::uint32_t>(gw));
+    } else if (g.numUnits != 0) {  // no gather units: no row windows
+        // scatter workgroups before i
+        const std::uint32_t before = head ? (i >> 3) * xcds + min(slot, xcds) : xcds * perXcd;
+        gather_body<V, PACKED ? Src::MixedPacked : Src::Mixed, GVALUES>(g, (i - before) * kWaves + wave);
+    }
 }
 
 // Vector width per lane: the narrowest V in {1,2,4} whose 64*V-feature chunk
@@ -1282,19 +1353,34 @@ int tcc_spmm_cnic_forward_mixed(const tcc_bcsr* bcsr, const tcc_bcsc* bcsc, cons
     s.mixed = g.mixed;
     const std::uint64_t gw = plan_gather(g, V, bcsr->unitBlocks);
     const std::uint64_t sw = plan_scatter(s, V, bcsc->unitBlocks);
-    const std::uint64_t gWG = (gw + kWaves - 1) / kWaves, sWG = (sw + kWaves - 1) / kWaves;
-    if (gWG + sWG == 0) return TCC_OK;
-    TCC_REQUIRE(gWG + sWG <= 0x7FFFFFFFull, TCC_ERR_UNSUPPORTED, "SpMM launch too large");
-    const dim3 grid(static_cast<unsigned>(gWG + sWG));
-    const auto gn = static_cast<std::uint32_t>(gWG), sn = static_cast<std::uint32_t>(sWG);
+    const std::uint64_t gWG = (gw + kWaves - 1) / kWaves;
+    std::uint64_t perXcd = 0;
+    std::uint32_t xcds = 0;
+    if (sw != 0) {
+        // The scatter's share of the XCDs, measured at config 4 (2.45M
+        // nodes, 20% hot): 2 of 8 with fp32 rows, 3 with packed rows, whose
+        // smaller lines need more requests in flight for the link's rate.
+        // At most the workgroups (8 per compute unit) of those XCDs, and no
+        // more than the scatter has waves.
+        xcds = src->row_format == TCC_ROWS_TF32_PACKED ? 3u : 2u;
+        const std::uint64_t perXcdMax = std::max<std::uint32_t>(1u, device_cus() / 8) * (kMaxWaves / kWaves);
+        perXcd = std::min<std::uint64_t>(perXcdMax, ((sw + kWaves - 1) / kWaves + xcds - 1) / xcds);
+    }
+    // the head of the grid holds the scatter's workgroups and the gather's
+    // first ones; pad it when the gather has fewer (they exit at once)
+    const std::uint64_t total = std::max<std::uint64_t>(gWG + xcds * perXcd, 8 * perXcd);
+    if (total == 0) return TCC_OK;
+    TCC_REQUIRE(total <= 0x7FFFFFFFull, TCC_ERR_UNSUPPORTED, "SpMM launch too large");
+    const dim3 grid(static_cast<unsigned>(total));
+    const auto px = static_cast<std::uint32_t>(perXcd);
     const bool gv = g.data != nullptr, sv = s.data != nullptr;
     const bool packed = src->row_format == TCC_ROWS_TF32_PACKED;
 #define TCC_MIXED_LAUNCH(VV, P)                                                                                          \
     do {                                                                                                                 \
-        if (gv && sv) hipLaunchKernelGGL((mixed_forward_kernel<VV, true, true, P>), grid, dim3(kThreads), 0, st, g, s, gn, sn);   \
-        else if (gv) hipLaunchKernelGGL((mixed_forward_kernel<VV, true, false, P>), grid, dim3(kThreads), 0, st, g, s, gn, sn); \
-        else if (sv) hipLaunchKernelGGL((mixed_forward_kernel<VV, false, true, P>), grid, dim3(kThreads), 0, st, g, s, gn, sn); \
-        else hipLaunchKernelGGL((mixed_forward_kernel<VV, false, false, P>), grid, dim3(kThreads), 0, st, g, s, gn, sn);        \
+        if (gv && sv) hipLaunchKernelGGL((mixed_forward_kernel<VV, true, true, P>), grid, dim3(kThreads), 0, st, g, s, xcds, px);   \
+        else if (gv) hipLaunchKernelGGL((mixed_forward_kernel<VV, true, false, P>), grid, dim3(kThreads), 0, st, g, s, xcds, px); \
+        else if (sv) hipLaunchKernelGGL((mixed_forward_kernel<VV, false, true, P>), grid, dim3(kThreads), 0, st, g, s, xcds, px); \
+        else hipLaunchKernelGGL((mixed_forward_kernel<VV, false, false, P>), grid, dim3(kThreads), 0, st, g, s, xcds, px);        \
     } while (0)
     if (packed) {
         if (V == 4) TCC_MIXED_LAUNCH(4, true);

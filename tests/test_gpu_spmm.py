@@ -338,6 +338,60 @@ def test_mixed_forward_values_widths_units(gpu, oracle, F, vals_hot, vals_cold, 
     cpu.free()
 
 
+@pytest.mark.parametrize("case", ["all_cold", "all_hot", "many_units", "many_units_packed"])
+def test_mixed_forward_extremes(gpu, oracle, case):
+    """The one-launch forward with no hot edges (no gather units), with no
+    cold edges (no scatter), and with more scatter units than its persistent
+    waves (K = 1 over ~9k cold blocks, so each scatter wave walks several)."""
+    from tcc_amd import swtcf
+    from tcc_amd.hostmem import PinnedArray
+
+    big = case.startswith("many_units")
+    nr = nc = 6000 if big else 1200
+    F = 100
+    dst, src = random_coo(nr, nc, 120000 if big else 20000, 71)
+    rng = np.random.default_rng(72)
+    feats = rng.standard_normal((nc, F)).astype(np.float32)
+    frac = {"all_cold": 0.0, "all_hot": 1.0}.get(case, 0.2)
+    hot_ids = np.sort(rng.choice(nc, size=int(nc * frac), replace=False))
+    csm = np.full(nc, -1, np.int32)
+    csm[hot_ids] = np.arange(hot_ids.size, dtype=np.int32)
+    id_map = np.arange(nc, dtype=np.int32)
+    packed = case == "many_units_packed"
+    if packed:
+        hot_cache = swtcf.tf32_pack(torch.from_numpy(feats[hot_ids]).cuda()) if hot_ids.size else None
+        row_bytes = packed_stride_host(F)
+        cpu = PinnedArray((nc * row_bytes,), np.uint8)
+        cpu.array[:] = swtcf.tf32_pack(torch.from_numpy(feats).cuda()).cpu().numpy()[: nc * row_bytes]
+        fmt = swtcf.ROWS_TF32_PACKED
+    else:
+        hot_cache = torch.from_numpy(feats[hot_ids]).cuda() if hot_ids.size else None
+        cpu = PinnedArray((nc, F))
+        cpu.array[:] = feats
+        fmt = swtcf.ROWS_FP32
+    keep = hot_cache if hot_cache is not None else torch.zeros(16, device="cuda")
+    ptrs = torch.tensor([keep.data_ptr()], dtype=torch.int64, device="cuda")
+    id_map_d = torch.from_numpy(id_map).cuda()
+    csm_d = torch.from_numpy(csm).cuda()
+    src_desc = swtcf.feature_source(id_map_d, csm_d, ptrs, max(hot_ids.size, 1), cpu.device_ptr, nc * F,
+                                    row_format=fmt)
+    h = csm[src] >= 0
+    A = swtcf.coo_to_bcsr(dev_u32(dst[h]), dev_u32(src[h]), None, nr, nc)
+    B = swtcf.coo_to_bcsc(dev_u32(dst[~h]), dev_u32(src[~h]), None, nr, nc)
+    if big:
+        B.set_unit_blocks(1)
+        assert B.view.num_TCBlocks > 4096
+    denseC = torch.full(((A.view.num_rowWindows + 1) * 8, F), 3.0, device="cuda")  # garbage in
+    swtcf.spmm_cnic_forward_mixed(A, B, src_desc, denseC, F)
+    rowptr, colind, _ = csr_of(dst, src, nr)
+    want = oracle.csr_spmm(rowptr, colind, None, feats, use_tf32=True)
+    C = denseC.cpu().numpy()
+    assert_close(C[:nr], want)
+    assert np.all(C[nr:] == 0)
+    torch.cuda.synchronize()
+    cpu.free()
+
+
 @pytest.mark.parametrize("F,values,K", [(37, True, 0), (100, False, 3), (256, True, 0), (301, True, 2),
                                          (602, False, 0)])
 def test_mixed_forward_packed_rows(gpu, oracle, F, values, K):
@@ -440,6 +494,25 @@ def test_units_split_windows(gpu, oracle, unit_blocks, F):
     dX = swtcf.bcsc_transpose_spmm(B, torch.from_numpy(dY).cuda(),
                                    torch.full((B.view.num_colWindows * 8, F), 5.0, device="cuda"))
     assert_close(dX.cpu().numpy()[:nc], wantT)
+
+
+def test_empty_coo_builders(gpu):
+    """No edges: both builders give empty windows and no blocks, and both
+    products leave zeros (BCSR =) or Y unchanged (BCSC +=)."""
+    from tcc_amd import swtcf
+
+    e = torch.empty(0, dtype=torch.int32, device="cuda")
+    A = swtcf.coo_to_bcsr(e, e, None, 20, 30)
+    B = swtcf.coo_to_bcsc(e, e, None, 20, 30)
+    assert A.view.num_TCBlocks == 0 and A.view.num_rowWindows == 3
+    assert B.view.num_TCBlocks == 0 and B.view.num_colWindows == 4
+    hb = B.to_host()
+    assert not hb["colWindowOffset"].any() and hb["colWindowOffset"].size == 5
+    X = torch.randn((30, 16), device="cuda")
+    assert torch.count_nonzero(swtcf.bcsr_spmm(A, X, torch.full((24, 16), 3.0, device="cuda"))).item() == 0
+    Y = torch.full((20, 16), 3.0, device="cuda")
+    swtcf.bcsc_spmm(B, X, Y)
+    assert bool((Y == 3.0).all())
 
 
 def test_all_windows_empty(gpu):
