@@ -123,23 +123,13 @@ __device__ __forceinline__ Vec<V> load_vec(const float* p) {
 }
 
 template <int V>
-__device__ __forceinline__ void store_vec(float* p, const float* v, bool add) {
+__device__ __forceinline__ void store_vec(float* p, const float* v) {
     if constexpr (V == 4) {
-        float4 t = make_float4(v[0], v[1], v[2], v[3]);
-        if (add) {
-            const float4 o = *reinterpret_cast<const float4*>(p);
-            t.x += o.x; t.y += o.y; t.z += o.z; t.w += o.w;
-        }
-        *reinterpret_cast<float4*>(p) = t;
+        *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
     } else if constexpr (V == 2) {
-        float2 t = make_float2(v[0], v[1]);
-        if (add) {
-            const float2 o = *reinterpret_cast<const float2*>(p);
-            t.x += o.x; t.y += o.y;
-        }
-        *reinterpret_cast<float2*>(p) = t;
+        *reinterpret_cast<float2*>(p) = make_float2(v[0], v[1]);
     } else {
-        *p = add ? (*p + v[0]) : v[0];
+        *p = v[0];
     }
 }
 
@@ -455,6 +445,16 @@ __device__ __forceinline__ void gather_body(const GatherArgs& a, std::uint32_t g
         if (active) {
             float* out = a.Y + static_cast<std::uint64_t>(w) * 8 * a.F + f0;
             const bool shared = a.atomicOut || ws < u.b0 || we > u.b1;
+            if (!shared && vecStore && a.accumulate) {
+                // Y += : all 8 rows loaded before any is added
+                Vec<V> prev[8];
+#pragma unroll
+                for (int r = 0; r < 8; ++r) prev[r] = load_vec<V>(out + static_cast<std::uint64_t>(r) * a.F);
+#pragma unroll
+                for (int r = 0; r < 8; ++r)
+#pragma unroll
+                    for (int v = 0; v < V; ++v) acc[r][v] += prev[r].v[v];
+            }
 #pragma unroll
             for (int r = 0; r < 8; ++r) {
                 float* o = out + static_cast<std::uint64_t>(r) * a.F;
@@ -464,7 +464,7 @@ __device__ __forceinline__ void gather_body(const GatherArgs& a, std::uint32_t g
                     for (int v = 0; v < V; ++v)
                         if (kWhole || f0 + v < a.F) atomic_add_f32(o + v, acc[r][v]);
                 } else if (vecStore) {
-                    store_vec<V>(o, acc[r], a.accumulate != 0);
+                    store_vec<V>(o, acc[r]);
                 } else {
 #pragma unroll
                     for (int v = 0; v < V; ++v)
