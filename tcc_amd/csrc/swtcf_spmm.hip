@@ -91,14 +91,10 @@ __global__ void __launch_bounds__(kThreads) swtcf_spmm_kernel(
         (&cache[0][0])[i] = 0.0f;
     __syncthreads();
 
+    // Tiles [t0, t1) of window w.
     const std::uint32_t off = superWindowRowOffset[s];
-    for (std::uint32_t wi = wave; wi < S; wi += kWaves) {
-        const std::uint32_t w = s * S + wi;
-        if (w >= CW) break;
-        const std::uint32_t w0 = colWindowOffset[w], w1 = colWindowOffset[w + 1];
-        const std::uint32_t per = (w1 - w0 + Z - 1) / Z;
-        const std::uint32_t t0 = min(w1, w0 + z * per), t1 = min(w1, t0 + per);
-        if (t0 >= t1) continue;
+    const auto process = [&](std::uint32_t w, std::uint32_t t0, std::uint32_t t1) {
+        TileGroup cur = load_tiles(tileRowSlot, tileLocalBit, rowCacheSlot, superWindowRows, off, t0, t1);
         float xv[8], xt[8];
         // all loads in flight before any is rounded
 #pragma unroll
@@ -117,7 +113,6 @@ __global__ void __launch_bounds__(kThreads) swtcf_spmm_kernel(
         }
 #pragma unroll
         for (int c = 0; c < 8; ++c) xt[c] = tf32_rna(xv[c]);
-        TileGroup cur = load_tiles(tileRowSlot, tileLocalBit, rowCacheSlot, superWindowRows, off, t0, t1);
         for (std::uint32_t g = t0; g < t1; g += 8) {
             TileGroup nxt = cur;
             if (g + 8 < t1) nxt = load_tiles(tileRowSlot, tileLocalBit, rowCacheSlot, superWindowRows, off, g + 8, t1);
@@ -145,6 +140,59 @@ __global__ void __launch_bounds__(kThreads) swtcf_spmm_kernel(
                 }
             }
             cur = nxt;
+        }
+    };
+
+    // Lane i holds the end of window i of the super-window (at most 32).
+    const std::uint32_t wBegin = s * S;
+    const std::uint32_t nw = min(S, CW - wBegin);
+    const std::uint32_t T0 = colWindowOffset[wBegin];
+    const std::uint32_t endv = lane < nw ? colWindowOffset[wBegin + lane + 1] : 0xFFFFFFFFu;
+    const std::uint32_t T1 = lane_u32(endv, static_cast<int>(nw) - 1);
+    std::uint32_t len = 0;  // tiles of window `lane`
+    {
+        const std::uint32_t prev = static_cast<std::uint32_t>(__shfl_up(static_cast<int>(endv), 1));
+        if (lane < nw) len = endv - (lane == 0 ? T0 : prev);
+    }
+    std::uint32_t longest = len;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1)
+        longest = max(longest, static_cast<std::uint32_t>(__shfl_xor(static_cast<int>(longest), d)));
+    if (static_cast<std::uint64_t>(longest) * nw <= 2ull * (T1 - T0)) {
+        // Balanced windows: wave i walks window i (and i+16, ...), part z
+        // the z-th slice of its tiles.
+        for (std::uint32_t wi = wave; wi < nw; wi += kWaves) {
+            const std::uint32_t w1 = lane_u32(endv, static_cast<int>(wi));
+            const std::uint32_t w0 = wi ? lane_u32(endv, static_cast<int>(wi) - 1) : T0;
+            const std::uint32_t per = (w1 - w0 + Z - 1) / Z;
+            const std::uint32_t t0 = min(w1, w0 + z * per), t1 = min(w1, t0 + per);
+            if (t0 < t1) process(wBegin + wi, t0, t1);
+        }
+    } else {
+        // A window longer than twice the mean (R-MAT hub sources make single
+        // windows thousands of tiles long): the super-window's tiles, which
+        // are contiguous, are cut into Z*kWaves equal ranges, one per wave
+        // of the Z parts, whatever the window boundaries.  A cut within half
+        // a range of a window boundary moves onto it, so that short windows
+        // are not split (each piece reloads its window's X rows); the cuts
+        // stay in order, so the ranges still partition the tiles.
+        const std::uint32_t parts = Z * kWaves, j = z * kWaves + wave;
+        const std::uint32_t per = (T1 - T0 + parts - 1) / parts;
+        const auto snap = [&](std::uint32_t x) {
+            const std::uint32_t before = static_cast<std::uint32_t>(__popcll(__ballot(endv <= x)));
+            const std::uint32_t lo = before ? lane_u32(endv, static_cast<int>(before) - 1) : T0;
+            const std::uint32_t hi = before < nw ? lane_u32(endv, static_cast<int>(before)) : T1;
+            if (x - lo <= hi - x) return x - lo <= per / 2 ? lo : x;
+            return hi - x <= per / 2 ? hi : x;
+        };
+        const std::uint32_t r0 = snap(min(T1, T0 + j * per)), r1 = snap(min(T1, T0 + (j + 1) * per));
+        // windows wholly before r0
+        std::uint32_t wi = static_cast<std::uint32_t>(__popcll(__ballot(endv <= r0)));
+        for (std::uint32_t t0 = r0; t0 < r1; ++wi) {
+            const std::uint32_t t1 = min(r1, lane_u32(endv, static_cast<int>(wi)));
+            if (t1 <= t0) continue;  // an empty window
+            process(wBegin + wi, t0, t1);
+            t0 = t1;
         }
     }
     __syncthreads();

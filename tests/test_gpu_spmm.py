@@ -109,6 +109,33 @@ def test_swtcf_spmm_super_window_sizes_skewed(gpu, oracle, S):
     assert_close(Y.cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("F", [64, 128, 200])
+def test_swtcf_hub_windows_split_across_waves(gpu, oracle, F):
+    """Super-windows whose windows are unbalanced (one source column with
+    ~3000 destinations, hundreds of tiles in one window) have their tiles cut
+    into equal ranges across the waves of several parts, cuts inside the hub
+    window and snapped to short windows' boundaries."""
+    from tcc_amd import swtcf
+
+    nr, nc = 6000, 700
+    rng = np.random.default_rng(31)
+    keys = set(rng.choice(nr * nc, size=20000, replace=False).tolist())
+    for c in (5, 300, 301):  # hub sources: long windows 0 and 37
+        keys.update(r * nc + c for r in rng.choice(nr, size=3000, replace=False).tolist())
+    k = np.array(sorted(keys), np.int64)
+    dst, src = (k // nc).astype(np.uint32), (k % nc).astype(np.uint32)
+    m = build_swtcf(dst, src, nr, nc)
+    ref = oracle.swtcf_convert(dst, src, nr, nc, 16)
+    lens = np.diff(ref["colWindowOffset"])
+    assert lens.max() > 8 * lens.mean()  # the split path
+    X = np.random.default_rng(32).standard_normal((nc, F)).astype(np.float32)
+    Y0 = np.random.default_rng(33).standard_normal((nr, F)).astype(np.float32)
+    Y = torch.from_numpy(Y0.copy()).cuda()
+    swtcf.swtcf_spmm(m, torch.from_numpy(X).cuda(), Y, 12)
+    want = oracle.swtcf_spmm(ref, X, tc=12, rows=nr, Y=Y0.astype(np.float64))
+    assert_close(Y.cpu().numpy(), want)
+
+
 def test_swtcf_config1(gpu, oracle):
     from tcc_amd import swtcf
     from tcc_amd.graphs import make_features, uniform_graph
