@@ -77,6 +77,10 @@ struct GatherArgs {
     std::uint32_t numUnits;
     int accumulate;
     int atomicOut;  // add every window into Y with atomics (Y zeroed by the caller)
+    // Features [featureBase, featureEnd) of this launch (featureEnd 0 = F):
+    // a packed gather launches its last, partial chunk on its own.
+    std::uint32_t featureBase;
+    std::uint32_t featureEnd;
     MixedArgs mixed;
 };
 
@@ -419,8 +423,8 @@ __device__ __forceinline__ void gather_body(const GatherArgs& a, std::uint32_t g
     if (chunk >= a.numChunks) return;
     const UnitRange u = unit_range(a.winOffset, a.numWindows, a.numBlocks, a.unitBlocks, a.numUnits, unit);
     if (u.w >= a.numWindows) return;  // offsets inconsistent with the block count
-    const std::uint32_t f0 = chunk * (kWave * V) + lane * V;
-    const bool active = f0 < a.F;
+    const std::uint32_t f0 = a.featureBase + chunk * (kWave * V) + lane * V;
+    const bool active = f0 < (a.featureEnd ? a.featureEnd : a.F);
     // inactive lanes read the row start (in bounds) and never store
     const std::uint32_t laneOff = active ? f0 : 0u;
 
@@ -1053,7 +1057,8 @@ inline std::uint32_t unit_blocks(std::uint32_t requested, std::uint32_t blocks, 
 // Work split of a gather (chunks, unit size, units); its wave count.
 inline std::uint64_t plan_gather(GatherArgs& a, int V, std::uint32_t requestedK) {
     if (a.numWindows == 0) return 0;
-    a.numChunks = (a.F + kWave * V - 1) / (kWave * V);
+    const std::uint32_t features = (a.featureEnd ? a.featureEnd : a.F) - a.featureBase;
+    a.numChunks = (features + kWave * V - 1) / (kWave * V);
     a.unitBlocks = unit_blocks(requestedK, a.numBlocks, a.numChunks);
     a.numUnits = std::max<std::uint32_t>(1, (a.numBlocks + a.unitBlocks - 1) / a.unitBlocks);
     return static_cast<std::uint64_t>(a.numUnits) * a.numChunks;
@@ -1068,12 +1073,14 @@ inline std::uint64_t plan_scatter(ScatterArgs& a, int V, std::uint32_t requested
     return static_cast<std::uint64_t>(a.numUnits) * a.numChunks;
 }
 
+// zeroShared = false: a second launch over other features of the same units
+// (their shared windows were zeroed, over all F features, by the first).
 template <Src MODE>
-int launch_gather(GatherArgs a, int V, std::uint32_t requestedK, hipStream_t st) {
+int launch_gather(GatherArgs a, int V, std::uint32_t requestedK, hipStream_t st, bool zeroShared = true) {
     const std::uint64_t waves = plan_gather(a, V, requestedK);
     if (waves == 0) return TCC_OK;
     TCC_REQUIRE(waves <= 0xFFFFFFFFull / kWaves, TCC_ERR_UNSUPPORTED, "SpMM launch too large");
-    if (a.numUnits > 1 && !a.accumulate && !a.atomicOut) {
+    if (zeroShared && a.numUnits > 1 && !a.accumulate && !a.atomicOut) {
         hipLaunchKernelGGL(zero_shared_windows_kernel, dim3(grid_for(a.numUnits - 1, kWaves)), dim3(kThreads), 0, st,
                            a.winOffset, a.numWindows, a.unitBlocks, a.numUnits, a.Y, a.F);
         TCC_LAUNCH_CHECK();
@@ -1271,8 +1278,23 @@ int tcc_bcsr_spmm_packed(const tcc_bcsr* A, const void* packedX, float* Y, std::
     a.packedStride = static_cast<std::uint32_t>(packed_stride(featureDim));
     // Rows longer than one chunk are gathered a whole chunk (4 features a
     // lane) at a time, whatever F % 4, so that each load covers its lines.
-    const int V = featureDim > kPackChunk ? 4 : pick_vec(featureDim, {Y});
-    return launch_gather<Src::Packed>(a, V, A->unitBlocks, as_stream(stream));
+    if (featureDim <= kPackChunk)
+        return launch_gather<Src::Packed>(a, pick_vec(featureDim, {Y}), A->unitBlocks, as_stream(stream));
+    // A last chunk of at most 128 features would leave most lanes of its
+    // 4-wide waves idle while costing as much as a full chunk (each block is
+    // one memory round trip either way): its waves run on their own, 2 or 1
+    // features a lane, over the same units, after the full chunks.
+    const std::uint32_t tail = featureDim % kPackChunk;
+    if (tail == 0 || tail > kPackChunk / 2) return launch_gather<Src::Packed>(a, 4, A->unitBlocks, as_stream(stream));
+    GatherArgs full = a;
+    full.featureEnd = featureDim - tail;
+    int rc = launch_gather<Src::Packed>(full, 4, A->unitBlocks, as_stream(stream));
+    if (rc) return rc;
+    GatherArgs last = a;
+    last.featureBase = featureDim - tail;
+    // the same units as the full chunks, so that the windows they share were zeroed
+    plan_gather(full, 4, A->unitBlocks);
+    return launch_gather<Src::Packed>(last, tail > kWave ? 2 : 1, full.unitBlocks, as_stream(stream), false);
 }
 
 int tcc_bcsr_spmm_mixed(const tcc_bcsr* A, const tcc_feature_source* src, float* Y, std::uint32_t featureDim,
