@@ -333,46 +333,67 @@ __device__ __forceinline__ GroupMeta load_group(const GatherArgs& a, std::uint32
 // Block k of the group: its stored bitmap `raw`, the row-major view `bm`
 // (byte R = the input columns C that output row R uses), the input rows x[C]
 // (zeros for padding) and its values (lane i = the value of its i-th stored
-// nonzero), TF32-rounded except for the A^T gather.
+// nonzero), TF32-rounded except for the A^T gather.  issue_block starts the
+// loads, finish_block uses them; load_block does both.
+template <int V, Src MODE>
+struct BlockLoad {
+    std::uint64_t raw;
+    float vals;
+    PackedVec<V> pk[8];  // packed sources
+    float x[8][V];       // fp32 sources
+};
+
 template <int V, Src MODE, bool VALUES>
-__device__ __forceinline__ void load_block(const GatherArgs& a, const GroupMeta& m, int k, std::uint32_t laneOff,
-                                           std::uint64_t& raw, std::uint64_t& bm, float (&x)[8][V], float& vals) {
-    raw = (static_cast<std::uint64_t>(lane_u32(m.bitsHi, k)) << 32) | lane_u32(m.bitsLo, k);
-    // Stored bit (r*8+c): BCSR = (output row r, column c); BCSC = (source row r,
-    // source column c), i.e. (input r, output c) for the A^T gather.
-    bm = (MODE == Src::Transposed) ? transpose8x8(raw) : raw;
+__device__ __forceinline__ void issue_block(const GatherArgs& a, const GroupMeta& m, int k, std::uint32_t laneOff,
+                                            BlockLoad<V, MODE>& b) {
+    b.raw = (static_cast<std::uint64_t>(lane_u32(m.bitsHi, k)) << 32) | lane_u32(m.bitsLo, k);
     // All loads are issued before any result is used (rounding inside the
     // branches would wait for each load in turn).
     if constexpr (MODE == Src::Packed || MODE == Src::MixedPacked) {
-        PackedVec<V> pk[8];
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
             const std::uint64_t rp = (static_cast<std::uint64_t>(lane_u32(m.rowHi, k * 8 + c)) << 32) |
                                      lane_u32(m.rowLo, k * 8 + c);
-            pk[c] = PackedVec<V>{};
-            if (rp != 0) pk[c] = load_packed<V>(reinterpret_cast<const unsigned char*>(rp), a.F, laneOff);
+            b.pk[c] = PackedVec<V>{};
+            if (rp != 0) b.pk[c] = load_packed<V>(reinterpret_cast<const unsigned char*>(rp), a.F, laneOff);
         }
-#pragma unroll
-        for (int c = 0; c < 8; ++c) unpack<V>(pk[c], x[c]);
     } else {
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
             const std::uint64_t rp = (static_cast<std::uint64_t>(lane_u32(m.rowHi, k * 8 + c)) << 32) |
                                      lane_u32(m.rowLo, k * 8 + c);
 #pragma unroll
-            for (int v = 0; v < V; ++v) x[c][v] = 0.0f;
+            for (int v = 0; v < V; ++v) b.x[c][v] = 0.0f;
             if (rp != 0) {
                 const Vec<V> t = load_vec<V>(reinterpret_cast<const float*>(rp) + laneOff);
 #pragma unroll
-                for (int v = 0; v < V; ++v) x[c][v] = t.v[v];
+                for (int v = 0; v < V; ++v) b.x[c][v] = t.v[v];
             }
         }
     }
-    vals = 0.0f;
+    b.vals = 0.0f;
     if constexpr (VALUES) {
         const std::uint32_t off = lane_u32(m.off, k);
-        if (__lane_id() < static_cast<unsigned>(__popcll(raw))) vals = a.data[off + __lane_id()];
+        if (__lane_id() < static_cast<unsigned>(__popcll(b.raw))) b.vals = a.data[off + __lane_id()];
     }
+}
+
+template <int V, Src MODE, bool VALUES>
+__device__ __forceinline__ void finish_block(const BlockLoad<V, MODE>& b, std::uint64_t& bm, float (&x)[8][V],
+                                             float& vals) {
+    // Stored bit (r*8+c): BCSR = (output row r, column c); BCSC = (source row r,
+    // source column c), i.e. (input r, output c) for the A^T gather.
+    bm = (MODE == Src::Transposed) ? transpose8x8(b.raw) : b.raw;
+    if constexpr (MODE == Src::Packed || MODE == Src::MixedPacked) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) unpack<V>(b.pk[c], x[c]);
+    } else {
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+#pragma unroll
+            for (int v = 0; v < V; ++v) x[c][v] = b.x[c][v];
+    }
+    vals = b.vals;
     // The A^T product replaces torch.sparse.mm in the reference's backward
     // (train/tcgnn_conv_release.py:152), which multiplies in plain fp32; the
     // forward products reproduce its mma.m16n8k8 tf32 numerics (packed rows
@@ -384,6 +405,15 @@ __device__ __forceinline__ void load_block(const GatherArgs& a, const GroupMeta&
             for (int v = 0; v < V; ++v) x[c][v] = tf32_rna(x[c][v]);
     }
     if constexpr (VALUES && MODE != Src::Transposed) vals = tf32_rna(vals);
+}
+
+template <int V, Src MODE, bool VALUES>
+__device__ __forceinline__ void load_block(const GatherArgs& a, const GroupMeta& m, int k, std::uint32_t laneOff,
+                                           std::uint64_t& raw, std::uint64_t& bm, float (&x)[8][V], float& vals) {
+    BlockLoad<V, MODE> b;
+    issue_block<V, MODE, VALUES>(a, m, k, laneOff, b);
+    finish_block<V, MODE, VALUES>(b, bm, x, vals);
+    raw = b.raw;
 }
 
 // acc[R] += w(R,C) * x[C] over the block's nonzeros (uniform branches over
