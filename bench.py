@@ -254,7 +254,7 @@ def bench_spmm(args, torch, swtcf, cfg):
             def step():
                 swtcf.bcsr_spmm_packed(A, swtcf.tf32_pack(X, out=buf), F, Y)
 
-            kernel = "gather_kernel<Packed> (after tf32_pack_kernel, both timed)"
+            kernel = "gather_kernel<Packed> (full chunks, then a last chunk of <= 128 features as its own launch; after tf32_pack_kernel, all timed)"
             extra["path"] = "tf32_pack + packed gather"
         else:
             def step():
