@@ -236,7 +236,8 @@ __global__ void __launch_bounds__(kWave * WM * WN) tn_partial_kernel(TnArgs a) {
 // held in LDS (row pitch 16*KB + 4 floats: conflict-free b128 reads).
 // Relu, the store of H and the row sums of H W2 (a 16-lane butterfly) follow
 // in registers.  Workgroups (one per CU for the LDS copy of W1^T, 12 waves:
-// 1.44 ms for 2.45M x 100 x 256 against 1.59-1.68 ms with 8) are persistent
+// 1.44 ms for 2.45M x 100 x 256 against 1.59-1.68 ms with 8, before the
+// interleaved MFMA steps below) are persistent
 // over 16-row tiles.
 struct ReluFwdArgs {
     const float* AX;
@@ -314,15 +315,25 @@ __global__ void __launch_bounds__(kWave * W) gcn_relu_forward_kernel(ReluFwdArgs
         f32x4 acc[kFwdTiles];
 #pragma unroll
         for (int u = 0; u < kFwdTiles; ++u) acc[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        // W1^T rows as float4 (KP % 4 == 0): ds_read_b128.  Each step s runs
+        // over 8 accumulators before the next, so no MFMA waits on the one
+        // before it.
+        const float4* w1t4 = reinterpret_cast<const float4*>(w1t);
 #pragma unroll
         for (int b = 0; b < KB; ++b) {
 #pragma unroll
-            for (int u = 0; u < kFwdTiles; ++u) {
-                const float4 w = *reinterpret_cast<const float4*>(&w1t[(16 * u + i) * KP + 16 * b + 4 * q]);
-                acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[b].x, w.x, acc[u], 0, 0, 0);
-                acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[b].y, w.y, acc[u], 0, 0, 0);
-                acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[b].z, w.z, acc[u], 0, 0, 0);
-                acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[b].w, w.w, acc[u], 0, 0, 0);
+            for (int h = 0; h < kFwdTiles; h += 8) {
+                float4 w[8];
+#pragma unroll
+                for (int t = 0; t < 8; ++t) w[t] = w1t4[(16 * (h + t) + i) * (KP / 4) + 4 * b + q];
+#pragma unroll
+                for (int t = 0; t < 8; ++t) acc[h + t] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[b].x, w[t].x, acc[h + t], 0, 0, 0);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) acc[h + t] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[b].y, w[t].y, acc[h + t], 0, 0, 0);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) acc[h + t] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[b].z, w[t].z, acc[h + t], 0, 0, 0);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) acc[h + t] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[b].w, w[t].w, acc[h + t], 0, 0, 0);
             }
         }
         // Lane holds H(row0 + 4q + v, 16u + i): relu (NaN kept, as clamp_min),
