@@ -38,6 +38,13 @@ PCIE_PEAK_GBPS = 64.0  # PCIe Gen5 x16, one direction
 # Gathers per feature row from which packing X to TF32 first pays off
 # (measured: 441 -> 12% faster at config 3; 7.3 -> 23% slower at config 2).
 PACK_MIN_REUSE = 16.0
+# Mean blocks per row window from which the phased BCSR (column phases
+# stacked, every window added with atomics) pays off, and its phase count
+# (measured: config 3, 441 blocks per window, 20.0 -> 17.5 ms with 4 phases
+# and 2-8 phases within 0.3 ms; config 2, 7.3 blocks per window, 78 -> 154 us
+# with 2).
+PHASE_MIN_BLOCKS_PER_WINDOW = 64.0
+PHASES = 4
 
 WORKLOADS = {
     1: "config1: uniform 4096 nodes x 16 nnz/row, F=32, SWTCF convert + SWTCF SpMM",
@@ -243,10 +250,22 @@ def bench_spmm(args, torch, swtcf, cfg):
         A = swtcf.coo_to_bcsr(r32, c32, vals, n, n)
         torch.cuda.synchronize()
         extra["bcsr_build_ms"] = round((time.perf_counter() - t_b) * 1e3, 3)
-        Y = torch.empty((A.view.num_rowWindows * 8, F), device="cuda")
         extra["blocks"] = A.view.num_TCBlocks
         reuse = 8.0 * A.view.num_TCBlocks / n  # feature-row gathers per row
         extra["row_reuse"] = round(reuse, 2)
+        per_window = A.view.num_TCBlocks / max(1, A.view.num_rowWindows)
+        extra["blocks_per_window"] = round(per_window, 1)
+        if per_window >= PHASE_MIN_BLOCKS_PER_WINDOW:
+            # long windows: the phased BCSR of the same COO, built once
+            t_p = time.perf_counter()
+            Ap = swtcf.coo_to_bcsr(r32, c32, vals, n, n, phases=PHASES)
+            torch.cuda.synchronize()
+            extra["phased_build_ms"] = round((time.perf_counter() - t_p) * 1e3, 3)
+            extra["phases"] = PHASES
+            A.release()
+            A = Ap
+        Y = torch.empty((A.out_windows * 8, F), device="cuda")
+        phased = f" over the {A.phases}-phase BCSR (Y zero-filled first)" if A.phases > 1 else ""
         if reuse >= PACK_MIN_REUSE:
             # each step packs X to TF32 rows of 2.5 B/element, then gathers them
             buf = torch.empty(swtcf._lib.lib().tcc_tf32_packed_bytes(n, F) + 16, dtype=torch.uint8, device="cuda")
@@ -254,14 +273,15 @@ def bench_spmm(args, torch, swtcf, cfg):
             def step():
                 swtcf.bcsr_spmm_packed(A, swtcf.tf32_pack(X, out=buf), F, Y)
 
-            kernel = "gather_kernel<Packed> (full chunks, then a last chunk of <= 128 features as its own launch; after tf32_pack_kernel, all timed)"
-            extra["path"] = "tf32_pack + packed gather"
+            kernel = ("gather_kernel<Packed> (full chunks, then a last chunk of <= 128 features as its own launch; "
+                      f"after tf32_pack_kernel, all timed){phased}")
+            extra["path"] = "tf32_pack + packed gather" + phased
         else:
             def step():
                 swtcf.bcsr_spmm(A, X, Y)
 
-            kernel = "gather_kernel"
-            extra["path"] = "fp32 gather"
+            kernel = "gather_kernel" + phased
+            extra["path"] = "fp32 gather" + phased
     if args.config in (2, 3):
         # SWTCF conversion of the same COO (S = 16), GEdges/s as the
         # reference's converter driver prints it (swtcf_convert_main.cu:417)

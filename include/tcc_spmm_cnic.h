@@ -54,6 +54,15 @@ typedef struct tcc_bcsr {
      * spread over many waves; a window split between units has its partial
      * sums combined with fp32 atomics. */
     uint32_t unitBlocks;
+    /* Column phases (no reference counterpart; 0 and 1 = an ordinary BCSR).
+     * With P > 1 the arrays hold P row windows per 8 output rows: the
+     * matrix's column slices [p*num_cols/P, (p+1)*num_cols/P) stacked
+     * vertically, built by tcc_coo_to_bcsr_phased.  num_rowWindows is then P
+     * times ceil(num_rows / 8) and window w adds into output window
+     * w % (num_rowWindows / P).  Only tcc_bcsr_spmm and tcc_bcsr_spmm_packed
+     * take such a matrix (the others return TCC_ERR_UNSUPPORTED); their Y has
+     * 8 * num_rowWindows / P rows. */
+    uint32_t phases;
 } tcc_bcsr;
 
 /* BCSC<T> (spmm_cnic/include/class.h:39-58) plus the optional value array. */
@@ -179,6 +188,15 @@ int tcc_coo_to_bcsr(const uint32_t* dRow, const uint32_t* dCol, const float* dVa
                     uint32_t numRows, uint32_t numCols, tcc_bcsr* out, void** allocation, void* stream);
 int tcc_coo_to_bcsc(const uint32_t* dRow, const uint32_t* dCol, const float* dVal, uint32_t nnz,
                     uint32_t numRows, uint32_t numCols, tcc_bcsc* out, void** allocation, void* stream);
+/* A phased BCSR (see tcc_bcsr.phases; no reference counterpart): the same
+ * product as tcc_coo_to_bcsr's, with the blocks ordered column phase first,
+ * so that the waves of one gather in flight together read rows of one phase
+ * of the columns, which the L2 and the last-level cache then hold.  Worth it
+ * where windows are long (hundreds of blocks per window); every window is
+ * then added into Y with atomics.  phases 0 or 1 = tcc_coo_to_bcsr. */
+int tcc_coo_to_bcsr_phased(const uint32_t* dRow, const uint32_t* dCol, const float* dVal, uint32_t nnz,
+                           uint32_t numRows, uint32_t numCols, uint32_t phases, tcc_bcsr* out,
+                           void** allocation, void* stream);
 int tcc_block_release(void* allocation);
 
 #ifdef __cplusplus

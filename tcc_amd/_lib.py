@@ -41,7 +41,7 @@ class BCSR(ctypes.Structure):
     _fields_ = [
         ("num_rows", u32), ("num_cols", u32), ("nnz", u32), ("num_TCBlocks", u32), ("num_rowWindows", u32),
         ("rowWindowOffset", vp), ("tcOffset", vp), ("sparseA2B", vp), ("tcLocalBit", vp), ("data", vp),
-        ("unitBlocks", u32),
+        ("unitBlocks", u32), ("phases", u32),
     ]
 
 
@@ -82,6 +82,8 @@ SIGNATURES = {
     "tcc_spmm_cnic_forward_mixed": (ctypes.c_int, [ctypes.POINTER(BCSR), ctypes.POINTER(BCSC),
                                                    ctypes.POINTER(FeatureSource), vp, u32, vp]),
     "tcc_coo_to_bcsr": (ctypes.c_int, [vp, vp, vp, u32, u32, u32, ctypes.POINTER(BCSR), ctypes.POINTER(vp), vp]),
+    "tcc_coo_to_bcsr_phased": (ctypes.c_int, [vp, vp, vp, u32, u32, u32, u32, ctypes.POINTER(BCSR),
+                                              ctypes.POINTER(vp), vp]),
     "tcc_coo_to_bcsc": (ctypes.c_int, [vp, vp, vp, u32, u32, u32, ctypes.POINTER(BCSC), ctypes.POINTER(vp), vp]),
     "tcc_block_release": (ctypes.c_int, [vp]),
     "tcc_tf32_packed_bytes": (ctypes.c_size_t, [u32, u32]),

@@ -32,8 +32,13 @@ inline unsigned ceil_log2(std::uint64_t x) {
 
 inline std::size_t align_up(std::size_t x) { return (x + 255) & ~std::size_t(255); }
 
+// Sort key (row window, column, row in window).  With phases > 1 the row
+// window of an edge is phase(c) * windowsPerPhase + r / 8, where column c is
+// in phase c * phases / numCols: the matrix is built as its column slices
+// stacked vertically.
 __global__ void bcsr_keys_kernel(const std::uint32_t* __restrict__ row, const std::uint32_t* __restrict__ col,
                                  std::uint32_t E, std::uint32_t numRows, std::uint32_t numCols, unsigned colBits,
+                                 std::uint32_t phases, std::uint32_t windowsPerPhase,
                                  std::uint64_t* __restrict__ keys, std::uint32_t* __restrict__ perm,
                                  std::uint32_t* __restrict__ err) {
     const std::uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
@@ -44,7 +49,9 @@ __global__ void bcsr_keys_kernel(const std::uint32_t* __restrict__ row, const st
         r = 0;
         c = 0;
     }
-    keys[e] = ((static_cast<std::uint64_t>(r >> 3) << colBits | c) << 3) | (r & 7u);
+    const std::uint64_t phase = static_cast<std::uint64_t>(c) * phases / numCols;
+    const std::uint64_t w = phase * windowsPerPhase + (r >> 3);
+    keys[e] = ((w << colBits | c) << 3) | (r & 7u);
     perm[e] = e;
 }
 
@@ -181,11 +188,21 @@ int tcc_block_release(void* allocation) {
 int tcc_coo_to_bcsr(const std::uint32_t* dRow, const std::uint32_t* dCol, const float* dVal, std::uint32_t nnz,
                     std::uint32_t numRows, std::uint32_t numCols, tcc_bcsr* out, void** allocation,
                     void* stream) {
+    return tcc_coo_to_bcsr_phased(dRow, dCol, dVal, nnz, numRows, numCols, 1, out, allocation, stream);
+}
+
+int tcc_coo_to_bcsr_phased(const std::uint32_t* dRow, const std::uint32_t* dCol, const float* dVal,
+                           std::uint32_t nnz, std::uint32_t numRows, std::uint32_t numCols, std::uint32_t phases,
+                           tcc_bcsr* out, void** allocation, void* stream) {
     clear_last_error();
     TCC_REQUIRE(out && allocation && numRows >= 1 && numCols >= 1 && (nnz == 0 || (dRow && dCol)),
                 TCC_ERR_INVALID_ARGUMENT, "invalid COO -> BCSR arguments");
+    if (phases == 0) phases = 1;
     const hipStream_t st = as_stream(stream);
-    const std::uint32_t E = nnz, RW = (numRows + 7) / 8;
+    const std::uint32_t windowsPerPhase = (numRows + 7) / 8;
+    TCC_REQUIRE(static_cast<std::uint64_t>(windowsPerPhase) * phases < 0xFFFFFFFFull, TCC_ERR_UNSUPPORTED,
+                "too many row windows for the phase count");
+    const std::uint32_t E = nnz, RW = windowsPerPhase * phases;
     const unsigned colBits = std::max(1u, ceil_log2(numCols));
     TCC_REQUIRE(ceil_log2(RW) + colBits + 3 <= 64, TCC_ERR_UNSUPPORTED, "BCSR key exceeds 64 bits");
     std::memset(out, 0, sizeof(*out));
@@ -229,7 +246,7 @@ int tcc_coo_to_bcsr(const std::uint32_t* dRow, const std::uint32_t* dCol, const 
     std::uint32_t* perm = permA;
     if (E > 0) {
         hipLaunchKernelGGL(bcsr_keys_kernel, dim3(grid_for(E, kThreads)), dim3(kThreads), 0, st, dRow, dCol, E,
-                           numRows, numCols, colBits, keysA, permA, small);
+                           numRows, numCols, colBits, phases, windowsPerPhase, keysA, permA, small);
         TCC_LAUNCH_CHECK();
         TCC_HIP_CHECK(radix_sort_pairs(keysA, keysB, permA, permB, E, ceil_log2(RW) + colBits + 3, temp, &sorted,
                                        &perm, st));
@@ -308,6 +325,7 @@ int tcc_coo_to_bcsr(const std::uint32_t* dRow, const std::uint32_t* dCol, const 
     out->sparseA2B = sparseA2B;
     out->tcLocalBit = tcLocalBit;
     out->data = dVal ? data : nullptr;
+    out->phases = phases;
     *allocation = o;
     return TCC_OK;
 }

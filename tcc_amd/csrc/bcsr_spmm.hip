@@ -82,6 +82,9 @@ struct GatherArgs {
     std::uint32_t featureBase;
     std::uint32_t featureEnd;
     MixedArgs mixed;
+    // Windows of the output (0: numWindows).  A phased matrix has `phases`
+    // row windows per output window, window w adding into window w % outWindows.
+    std::uint32_t outWindows;
 };
 
 // Feature row of column `in` for the first-layer (mixed) form
@@ -458,6 +461,7 @@ __device__ __forceinline__ void gather_body(const GatherArgs& a, std::uint32_t g
     // inactive lanes read the row start (in bounds) and never store
     const std::uint32_t laneOff = active ? f0 : 0u;
 
+    __shared__ float flushStage[V == 4 ? kWaves * kWave * V : 1];
     float acc[8][V];
 #pragma unroll
     for (int r = 0; r < 8; ++r)
@@ -476,9 +480,37 @@ __device__ __forceinline__ void gather_body(const GatherArgs& a, std::uint32_t g
     constexpr bool kWhole = MODE != Src::Packed && MODE != Src::MixedPacked;
     const bool vecStore = kWhole || a.F % V == 0;
     auto flush = [&]() {
-        if (active) {
-            float* out = a.Y + static_cast<std::uint64_t>(w) * 8 * a.F + f0;
-            const bool shared = a.atomicOut || ws < u.b0 || we > u.b1;
+        const std::uint32_t ow = a.outWindows ? w % a.outWindows : w;
+        const bool shared = a.atomicOut || ws < u.b0 || we > u.b1;  // wave-uniform
+        if (V == 4 && shared) {
+            // A row's 256 sums pass through LDS so that each atomic
+            // instruction adds 64 consecutive floats (lane l: feature
+            // 64j + l of the chunk) rather than every 4th float of 1 KB: a
+            // quarter of the L2 requests.  On config 3 with every window
+            // added atomically, 20.7 -> 19.9 ms.  (At V = 2 the staging
+            // costs the 64-VGPR kernels a wave per SIMD.)  Every lane takes
+            // part, active or not: lane l adds the features below the
+            // launch's end, whose owners (lane (64j + l) / 4) are active.
+            float* st = flushStage + uniform(threadIdx.x / kWave) * (kWave * V);
+            const std::uint32_t cb = f0 - lane * V;
+            const std::uint32_t fe = a.featureEnd ? a.featureEnd : a.F;
+            float* rb = a.Y + static_cast<std::uint64_t>(ow) * 8 * a.F + cb;
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                if (((touched >> (8 * r)) & 0xFFu) == 0) continue;
+                store_vec<V>(st + lane * V, acc[r]);
+                __builtin_amdgcn_wave_barrier();
+                float t[V];
+#pragma unroll
+                for (int j = 0; j < V; ++j) t[j] = st[kWave * j + lane];
+                __builtin_amdgcn_wave_barrier();
+#pragma unroll
+                for (int j = 0; j < V; ++j)
+                    if (cb + kWave * j + lane < fe)
+                        atomic_add_f32(rb + static_cast<std::uint64_t>(r) * a.F + kWave * j + lane, t[j]);
+            }
+        } else if (active) {
+            float* out = a.Y + static_cast<std::uint64_t>(ow) * 8 * a.F + f0;
             if (!shared && vecStore && a.accumulate) {
                 // Y += : all 8 rows loaded before any is added
                 Vec<V> prev[8];
@@ -1072,24 +1104,33 @@ inline int pick_vec(std::uint32_t F, std::initializer_list<const void*> ptrs) {
 }
 
 // Blocks per unit: `requested` if nonzero, else about one wave of work per
-// wave slot of the device (32 per CU): fewer, longer units pay the per-wave
-// start (window search, first metadata group) less often, while more units
-// than slots only queue.  A power of two in [16, 1024].
-inline std::uint32_t unit_blocks(std::uint32_t requested, std::uint32_t blocks, std::uint32_t chunks) {
+// wave slot of the device (32 per CU), a power of two in [16, maxK]: fewer,
+// longer units pay the per-wave start (window search, first metadata group)
+// less often.  Gathers from device rows cap units at 128 blocks: past that
+// the waves in flight spread over more of the rows (config 3: 21.3 ms with
+// 1024-block units, 20.0 ms with 128).  The first-layer forward, whose cold
+// rows come over the host link, and the scatters keep 1024 (config 4:
+// 9.1 ms, against 10.4 ms with 128).
+constexpr std::uint32_t kDeviceRowsMaxUnit = 128;
+constexpr std::uint32_t kHostLinkMaxUnit = 1024;
+
+inline std::uint32_t unit_blocks(std::uint32_t requested, std::uint32_t blocks, std::uint32_t chunks,
+                                 std::uint32_t maxK) {
     if (requested != 0) return requested;
     const std::uint64_t work = static_cast<std::uint64_t>(blocks) * chunks;
     const std::uint64_t slots = static_cast<std::uint64_t>(device_cus()) * 32;
     std::uint32_t K = 16;
-    while (K < 1024 && static_cast<std::uint64_t>(K) * slots < work) K *= 2;
+    while (K < maxK && static_cast<std::uint64_t>(K) * slots < work) K *= 2;
     return K;
 }
 
 // Work split of a gather (chunks, unit size, units); its wave count.
-inline std::uint64_t plan_gather(GatherArgs& a, int V, std::uint32_t requestedK) {
+inline std::uint64_t plan_gather(GatherArgs& a, int V, std::uint32_t requestedK,
+                                 std::uint32_t maxK = kDeviceRowsMaxUnit) {
     if (a.numWindows == 0) return 0;
     const std::uint32_t features = (a.featureEnd ? a.featureEnd : a.F) - a.featureBase;
     a.numChunks = (features + kWave * V - 1) / (kWave * V);
-    a.unitBlocks = unit_blocks(requestedK, a.numBlocks, a.numChunks);
+    a.unitBlocks = unit_blocks(requestedK, a.numBlocks, a.numChunks, maxK);
     a.numUnits = std::max<std::uint32_t>(1, (a.numBlocks + a.unitBlocks - 1) / a.unitBlocks);
     return static_cast<std::uint64_t>(a.numUnits) * a.numChunks;
 }
@@ -1098,7 +1139,7 @@ inline std::uint64_t plan_gather(GatherArgs& a, int V, std::uint32_t requestedK)
 inline std::uint64_t plan_scatter(ScatterArgs& a, int V, std::uint32_t requestedK) {
     if (a.numWindows == 0 || a.numBlocks == 0) return 0;
     a.numChunks = (a.F + kWave * V - 1) / (kWave * V);
-    a.unitBlocks = unit_blocks(requestedK, a.numBlocks, a.numChunks);
+    a.unitBlocks = unit_blocks(requestedK, a.numBlocks, a.numChunks, kHostLinkMaxUnit);
     a.numUnits = (a.numBlocks + a.unitBlocks - 1) / a.unitBlocks;
     return static_cast<std::uint64_t>(a.numUnits) * a.numChunks;
 }
@@ -1107,7 +1148,8 @@ inline std::uint64_t plan_scatter(ScatterArgs& a, int V, std::uint32_t requested
 // (their shared windows were zeroed, over all F features, by the first).
 template <Src MODE>
 int launch_gather(GatherArgs a, int V, std::uint32_t requestedK, hipStream_t st, bool zeroShared = true) {
-    const std::uint64_t waves = plan_gather(a, V, requestedK);
+    constexpr bool kHostRows = MODE == Src::Mixed || MODE == Src::MixedPacked;
+    const std::uint64_t waves = plan_gather(a, V, requestedK, kHostRows ? kHostLinkMaxUnit : kDeviceRowsMaxUnit);
     if (waves == 0) return TCC_OK;
     TCC_REQUIRE(waves <= 0xFFFFFFFFull / kWaves, TCC_ERR_UNSUPPORTED, "SpMM launch too large");
     if (zeroShared && a.numUnits > 1 && !a.accumulate && !a.atomicOut) {
@@ -1213,7 +1255,17 @@ GatherArgs bcsr_args(const tcc_bcsr* A, const float* X, float* Y, std::uint32_t 
     a.numIn = A->num_cols;
     a.F = F;
     a.accumulate = accumulate;
+    if (A->phases > 1) {  // phased: every window adds into window w % outWindows
+        a.outWindows = A->num_rowWindows / A->phases;
+        a.atomicOut = 1;
+    }
     return a;
+}
+
+// Y of a phased product receives atomics only: zero it first unless adding.
+hipError_t zero_phased_output(const GatherArgs& a, hipStream_t st) {
+    if (a.outWindows == 0 || a.accumulate) return hipSuccess;
+    return fill<float>(a.Y, static_cast<std::uint64_t>(a.outWindows) * 8 * a.F, 0.0f, st);
 }
 
 ScatterArgs bcsc_args(const tcc_bcsc* A, const float* X, float* Y, std::uint32_t F) {
@@ -1251,7 +1303,8 @@ int mixed_vec(const tcc_feature_source* src, std::uint32_t F, const float* Y) {
 
 bool bcsr_ok(const tcc_bcsr* A) {
     return A && (A->num_rowWindows == 0 || (A->rowWindowOffset && A->sparseA2B && A->tcLocalBit)) &&
-           (A->data == nullptr || A->tcOffset != nullptr);
+           (A->data == nullptr || A->tcOffset != nullptr) &&
+           (A->phases <= 1 || A->num_rowWindows % A->phases == 0);
 }
 
 bool bcsc_ok(const tcc_bcsc* A) {
@@ -1270,11 +1323,11 @@ int tcc_bcsr_spmm(const tcc_bcsr* A, const float* X, float* Y, std::uint32_t fea
                   void* stream) {
     clear_last_error();
     TCC_REQUIRE(bcsr_ok(A) && X && Y && featureDim >= 1, TCC_ERR_INVALID_ARGUMENT, "invalid BCSR SpMM arguments");
-    if (featureDim <= kNarrowMaxF)
+    if (featureDim <= kNarrowMaxF && A->phases <= 1)
         return launch_narrow<Src::Plain>(bcsr_args(A, X, Y, featureDim, accumulate), A->unitBlocks, as_stream(stream));
-    const int V = pick_vec(featureDim, {X, Y});
-    return launch_gather<Src::Plain>(bcsr_args(A, X, Y, featureDim, accumulate), V, A->unitBlocks,
-                                     as_stream(stream));
+    const GatherArgs a = bcsr_args(A, X, Y, featureDim, accumulate);
+    TCC_HIP_CHECK(zero_phased_output(a, as_stream(stream)));
+    return launch_gather<Src::Plain>(a, pick_vec(featureDim, {X, Y}), A->unitBlocks, as_stream(stream));
 }
 
 size_t tcc_tf32_packed_bytes(std::uint32_t rows, std::uint32_t featureDim) {
@@ -1304,6 +1357,7 @@ int tcc_bcsr_spmm_packed(const tcc_bcsr* A, const void* packedX, float* Y, std::
     TCC_REQUIRE(reinterpret_cast<std::uintptr_t>(packedX) % 16 == 0, TCC_ERR_INVALID_ARGUMENT,
                 "packed buffer must be 16-byte aligned");
     GatherArgs a = bcsr_args(A, nullptr, Y, featureDim, accumulate);
+    TCC_HIP_CHECK(zero_phased_output(a, as_stream(stream)));
     a.packed = static_cast<const unsigned char*>(packedX);
     a.packedStride = static_cast<std::uint32_t>(packed_stride(featureDim));
     // Rows longer than one chunk are gathered a whole chunk (4 features a
@@ -1332,6 +1386,7 @@ int tcc_bcsr_spmm_mixed(const tcc_bcsr* A, const tcc_feature_source* src, float*
     clear_last_error();
     TCC_REQUIRE(bcsr_ok(A) && source_ok(src) && Y && featureDim >= 1, TCC_ERR_INVALID_ARGUMENT,
                 "invalid mixed BCSR SpMM arguments");
+    TCC_REQUIRE(A->phases <= 1, TCC_ERR_UNSUPPORTED, "the mixed SpMM takes an ordinary (unphased) BCSR");
     GatherArgs a = bcsr_args(A, nullptr, Y, featureDim, accumulate);
     a.mixed = mixed_args(src, featureDim);
     // Hot-cache bases live in a device pointer table and are taken to be
@@ -1377,6 +1432,7 @@ int tcc_spmm_cnic_forward(const tcc_bcsr* bcsr, const tcc_bcsc* bcsc, const floa
     clear_last_error();
     TCC_REQUIRE(bcsr_ok(bcsr) && bcsc_ok(bcsc) && X && denseC && featureDim >= 1, TCC_ERR_INVALID_ARGUMENT,
                 "invalid spmm_cnic forward arguments");
+    TCC_REQUIRE(bcsr->phases <= 1, TCC_ERR_UNSUPPORTED, "spmm_cnic forward takes an ordinary (unphased) BCSR");
     const hipStream_t st = as_stream(stream);
     const std::uint64_t F = featureDim;
     // denseC holds (num_rowWindows+1)*8 rows (spmm_launcher.cu:241-244); the
@@ -1393,6 +1449,7 @@ int tcc_spmm_cnic_forward_mixed(const tcc_bcsr* bcsr, const tcc_bcsc* bcsc, cons
     TCC_REQUIRE(bcsr_ok(bcsr) && bcsc_ok(bcsc) && src && denseC && featureDim >= 1, TCC_ERR_INVALID_ARGUMENT,
                 "invalid spmm_cnic mixed forward arguments");
     TCC_REQUIRE(source_ok(src), TCC_ERR_INVALID_ARGUMENT, "invalid spmm_cnic mixed forward feature source");
+    TCC_REQUIRE(bcsr->phases <= 1, TCC_ERR_UNSUPPORTED, "spmm_cnic forward takes an ordinary (unphased) BCSR");
     const hipStream_t st = as_stream(stream);
     const std::uint64_t F = featureDim;
     // denseC = 0 over its (num_rowWindows+1)*8 rows, then both parts add in.
@@ -1403,7 +1460,7 @@ int tcc_spmm_cnic_forward_mixed(const tcc_bcsr* bcsr, const tcc_bcsc* bcsc, cons
     g.atomicOut = 1;
     ScatterArgs s = bcsc_args(bcsc, nullptr, denseC, featureDim);
     s.mixed = g.mixed;
-    const std::uint64_t gw = plan_gather(g, V, bcsr->unitBlocks);
+    const std::uint64_t gw = plan_gather(g, V, bcsr->unitBlocks, kHostLinkMaxUnit);
     const std::uint64_t sw = plan_scatter(s, V, bcsc->unitBlocks);
     const std::uint64_t gWG = (gw + kWaves - 1) / kWaves;
     std::uint64_t perXcd = 0;

@@ -209,6 +209,16 @@ class BlockMatrix:
     def num_windows(self) -> int:
         return self.view.num_rowWindows if self.kind == "bcsr" else self.view.num_colWindows
 
+    @property
+    def phases(self) -> int:
+        return max(1, self.view.phases) if self.kind == "bcsr" else 1
+
+    @property
+    def out_windows(self) -> int:
+        """8-row windows of the product's output (a phased BCSR has
+        `phases` row windows per output window)."""
+        return self.num_windows // self.phases
+
     def to_host(self) -> dict:
         torch.cuda.synchronize()
         v = self.view
@@ -224,15 +234,20 @@ class BlockMatrix:
         }
         d.update(num_rows=v.num_rows, num_cols=v.num_cols, nnz=v.nnz, num_TCBlocks=B)
         d["num_rowWindows" if self.kind == "bcsr" else "num_colWindows"] = W
+        if self.kind == "bcsr":
+            d["phases"] = self.phases
         return d
 
 
 def coo_to_bcsr(row: torch.Tensor, col: torch.Tensor, val: torch.Tensor | None, num_rows: int, num_cols: int,
-                stream=None) -> BlockMatrix:
+                stream=None, phases: int = 1) -> BlockMatrix:
+    """BCSR of the COO matrix; phases > 1 builds the phased form
+    (tcc_coo_to_bcsr_phased), taken by bcsr_spmm and bcsr_spmm_packed."""
     view = BCSR()
     alloc = ctypes.c_void_p()
-    check(_lib.lib().tcc_coo_to_bcsr(_u32(row).data_ptr(), _u32(col).data_ptr(), _ptr(val), row.numel(), num_rows,
-                                     num_cols, ctypes.byref(view), ctypes.byref(alloc), _stream(stream)))
+    check(_lib.lib().tcc_coo_to_bcsr_phased(_u32(row).data_ptr(), _u32(col).data_ptr(), _ptr(val), row.numel(),
+                                            num_rows, num_cols, int(phases), ctypes.byref(view), ctypes.byref(alloc),
+                                            _stream(stream)))
     return BlockMatrix("bcsr", view, alloc.value)
 
 
@@ -246,10 +261,10 @@ def coo_to_bcsc(row: torch.Tensor, col: torch.Tensor, val: torch.Tensor | None, 
 
 
 def wrap_bcsr(num_rows, num_cols, nnz, num_TCBlocks, num_rowWindows, rowWindowOffset, tcOffset, sparseA2B,
-              tcLocalBit, data=None) -> BlockMatrix:
+              tcLocalBit, data=None, phases: int = 1) -> BlockMatrix:
     """View caller-owned device tensors as a BCSR (no copy)."""
     v = BCSR(num_rows, num_cols, nnz, num_TCBlocks, num_rowWindows, _ptr(rowWindowOffset), _ptr(tcOffset),
-             _ptr(sparseA2B), _ptr(tcLocalBit), _ptr(data))
+             _ptr(sparseA2B), _ptr(tcLocalBit), _ptr(data), 0, int(phases))
     return BlockMatrix("bcsr", v, None, keep=(rowWindowOffset, tcOffset, sparseA2B, tcLocalBit, data))
 
 
@@ -267,7 +282,7 @@ def host_to_bcsr(d: dict, use_data: bool = False) -> BlockMatrix:
          .cuda() for k in ("rowWindowOffset", "tcOffset", "sparseA2B", "tcLocalBit", "data")}
     return wrap_bcsr(d["num_rows"], d["num_cols"], d["nnz"], d["num_TCBlocks"], d["num_rowWindows"],
                      t["rowWindowOffset"], t["tcOffset"], t["sparseA2B"], t["tcLocalBit"],
-                     t["data"] if use_data else None)
+                     t["data"] if use_data else None, d.get("phases", 1))
 
 
 def host_to_bcsc(d: dict, use_data: bool = False) -> BlockMatrix:
@@ -281,11 +296,11 @@ def host_to_bcsc(d: dict, use_data: bool = False) -> BlockMatrix:
 
 def bcsr_spmm(A: BlockMatrix, X: torch.Tensor, Y: torch.Tensor | None = None, accumulate: bool = False,
               stream=None) -> torch.Tensor:
-    """Y[8*RW x F] (=|+=) A X."""
+    """Y[8*W x F] (=|+=) A X, W = A.out_windows."""
     X = _f32(X, "X")
     F = X.shape[1]
     if Y is None:
-        Y = torch.empty((A.view.num_rowWindows * 8, F), dtype=torch.float32, device=X.device)
+        Y = torch.empty((A.out_windows * 8, F), dtype=torch.float32, device=X.device)
     check(_lib.lib().tcc_bcsr_spmm(ctypes.byref(A.view), X.data_ptr(), Y.data_ptr(), F, int(accumulate),
                                    _stream(stream)))
     return Y
@@ -308,9 +323,9 @@ def tf32_pack(X: torch.Tensor, out: torch.Tensor | None = None, stream=None) -> 
 
 def bcsr_spmm_packed(A: BlockMatrix, packed: torch.Tensor, F: int, Y: torch.Tensor | None = None,
                      accumulate: bool = False, stream=None) -> torch.Tensor:
-    """Y[8*RW x F] (=|+=) A X with X given by tf32_pack."""
+    """Y[8*W x F] (=|+=) A X with X given by tf32_pack, W = A.out_windows."""
     if Y is None:
-        Y = torch.empty((A.view.num_rowWindows * 8, F), dtype=torch.float32, device=packed.device)
+        Y = torch.empty((A.out_windows * 8, F), dtype=torch.float32, device=packed.device)
     check(_lib.lib().tcc_bcsr_spmm_packed(ctypes.byref(A.view), packed.data_ptr(), Y.data_ptr(), F,
                                           int(accumulate), _stream(stream)))
     return Y
