@@ -1,6 +1,7 @@
 """HIP-graph capture of the library's launches (torch.cuda.CUDAGraph over
 the kernels the C-ABI enqueues on the current stream): the BCSR gather with
 its shared-window zero pass, the packed gather with its separate last chunk,
+the gathers over a phased BCSR (zero fill of Y, then atomics only),
 the one-launch first-layer forward (fill + mixed kernel), the SWTCF SpMM,
 the narrow and transposed gathers and the split-K dense products.  None of
 them allocates, synchronises or records a memset, so each captures as is.
@@ -89,6 +90,30 @@ def test_graph_bcsr_gathers():
     g, out = capture(run)
     replay_and_check(g, out, [X, X3], lambda: [swtcf.bcsr_spmm(A, X), swtcf.bcsr_spmm_packed(A, swtcf.tf32_pack(X3), 300)],
                      exact=False)
+
+
+def test_graph_phased_gathers():
+    """A 4-phase BCSR at F = 300 (a full chunk and a 44-feature last chunk):
+    the Y zero fill and the all-atomic plain and packed gathers."""
+    from tcc_amd import swtcf
+
+    nr, nc, F = 700, 900, 300
+    dst, src = random_coo(nr, nc, 30000, 9)
+    vals = torch.from_numpy(np.random.default_rng(10).uniform(-1, 1, dst.size).astype(np.float32)).cuda()
+    A = swtcf.coo_to_bcsr(dev_u32(dst), dev_u32(src), vals, nr, nc, phases=4).set_unit_blocks(5)
+    X = torch.randn(nc, F, device="cuda")
+    Y = torch.empty(A.out_windows * 8, F, device="cuda")
+    Yp = torch.empty_like(Y)
+    P = torch.empty(swtcf._lib.lib().tcc_tf32_packed_bytes(nc, F) + 16, dtype=torch.uint8, device="cuda")
+
+    def run():
+        swtcf.bcsr_spmm(A, X, Y)
+        swtcf.bcsr_spmm_packed(A, swtcf.tf32_pack(X, out=P), F, Yp)
+        return Y, Yp
+
+    g, out = capture(run)
+    replay_and_check(g, out, [X], lambda: [swtcf.bcsr_spmm(A, X), swtcf.bcsr_spmm_packed(A, swtcf.tf32_pack(X), F)],
+                     exact=False, seed=11)
 
 
 def test_graph_mixed_forward():
