@@ -93,6 +93,19 @@ __global__ void __launch_bounds__(kThreads) swtcf_spmm_kernel(
 
     // Tiles [t0, t1) of window w.
     const std::uint32_t off = superWindowRowOffset[s];
+    // The repeat cache's target rows (wave i flushes slots i and i + 16),
+    // resolved before the tiles so that their loads overlap the tiles
+    // instead of following the barrier.  Slots past the cached count hold
+    // the invalid slot.
+    static_assert(TCC_SWTCF_REPEAT_CACHE_SIZE == 2 * kWaves, "two repeat-cache slots per wave");
+    const std::uint32_t cached = cachedCount[s];
+    std::uint32_t flushRow[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const std::uint32_t slot =
+            cachedRowSlot[static_cast<std::uint64_t>(s) * TCC_SWTCF_REPEAT_CACHE_SIZE + wave + k * kWaves];
+        flushRow[k] = slot != TCC_SWTCF_INVALID_ROW_SLOT ? superWindowRows[off + slot] : kNoTarget;
+    }
     const auto process = [&](std::uint32_t w, std::uint32_t t0, std::uint32_t t1) {
         TileGroup cur = load_tiles(tileRowSlot, tileLocalBit, rowCacheSlot, superWindowRows, off, t0, t1);
         float xv[8], xt[8];
@@ -196,16 +209,12 @@ __global__ void __launch_bounds__(kThreads) swtcf_spmm_kernel(
         }
     }
     __syncthreads();
-    const std::uint32_t cached = cachedCount[s];
-    for (unsigned i = threadIdx.x; i < cached * kChunk; i += kThreads) {
-        const unsigned cs = i / kChunk, fl = i % kChunk;
-        const std::uint32_t ff = blockIdx.y * kChunk + fl;
-        const float v = cache[cs][fl];
-        if (ff < F && v != 0.0f) {
-            const std::uint32_t slot = cachedRowSlot[static_cast<std::uint64_t>(s) * TCC_SWTCF_REPEAT_CACHE_SIZE + cs];
-            const std::uint32_t row = superWindowRows[off + slot];
-            atomic_add_f32(&Y[static_cast<std::uint64_t>(row) * F + ff], v);
-        }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const std::uint32_t cs = wave + k * kWaves;
+        if (cs >= cached || flushRow[k] == kNoTarget) continue;
+        const float v = cache[cs][lane];
+        if (active && v != 0.0f) atomic_add_f32(&Y[static_cast<std::uint64_t>(flushRow[k]) * F + f], v);
     }
 }
 
