@@ -596,8 +596,8 @@ __global__ void __launch_bounds__(kThreads) zero_shared_windows_kernel(const std
     const std::uint32_t w = lb - 1;
     if (u >= 2 && winOffset[w] < b0 - K) return;  // boundary (u-1)*K cut it already
     float* p = Y + static_cast<std::uint64_t>(w) * 8 * F;
-    if ((F & 3u) == 0 && (reinterpret_cast<std::uintptr_t>(Y) & 15u) == 0) {
-        // a window's 8 rows are 32F bytes: 16-byte aligned with Y
+    if ((reinterpret_cast<std::uintptr_t>(Y) & 15u) == 0) {
+        // a window's 8 rows are one block of 8F floats (2F float4s), 16-byte aligned with Y
         float4* q = reinterpret_cast<float4*>(p);
         for (std::uint32_t i = __lane_id(); i < 2u * F; i += kWave) q[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     } else {
