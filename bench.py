@@ -58,14 +58,23 @@ WORKLOADS = {
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=50)
-    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--steps", type=int, default=None,
+                   help="timed steps (default: 500 for the microsecond configs 1-2, else 50)")
+    p.add_argument("--warmup", type=int, default=None, help="untimed steps (default: 50 for configs 1-2, else 10)")
     p.add_argument("--config", type=int, default=2, choices=sorted(WORKLOADS))
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-threads", type=int, default=0, help="0 = all host cores")
     p.add_argument("--copy-calibration-mib", type=int, default=0,
                    help="first run one plain device copy of this many MiB (scale for rocprofv3 FETCH/WRITE_SIZE)")
-    return p.parse_args()
+    args = p.parse_args()
+    # A config-2 step is ~80 us: 500 of them time 40 ms of steady-state work
+    # (50 took 4 ms, short enough for the clock ramp to show).
+    short = args.config in (1, 2)
+    if args.steps is None:
+        args.steps = 500 if short else 50
+    if args.warmup is None:
+        args.warmup = 50 if short else 10
+    return args
 
 
 def bytes_alg(n_src, n_dst, nnz, F):
