@@ -58,8 +58,9 @@ __device__ __forceinline__ std::uint32_t tn_uniform(std::uint32_t v) {
 // (G W2^T) (.) [H > 0] from G [K x C] and W2 [N x C] (C <= CT), while H^T G
 // is summed beside it into partial2 -- the layer-1 weight gradient and the
 // layer-2 weight gradient of a two-layer GCN in one pass over its rows.
-template <int TM, int TN, int WM, int WN, int U, int CT>
+template <int TM, int TN, int WM, int WN, int U, int CT, bool VB = false>
 __global__ void __launch_bounds__(kWave * WM * WN) tn_partial_kernel(TnArgs a) {
+    static_assert(!VB || TN % 4 == 0, "a float4 of B feeds four N tiles");
     constexpr int BM = 16 * TM * WM, BN = 16 * TN * WN;
     constexpr int GC = CT > 0 ? CT : 1;  // G columns held per row
     constexpr std::uint32_t kStep = 4 * U;
@@ -71,13 +72,23 @@ __global__ void __launch_bounds__(kWave * WM * WN) tn_partial_kernel(TnArgs a) {
     const std::uint32_t k0 = blockIdx.x * a.rowsPerSplit;
     const std::uint32_t k1 = min(a.K, k0 + a.rowsPerSplit);
     const unsigned li = lane & 15u, lk = lane >> 4;
+    // Column of N tile u on this lane: 16u + l%16; with VB, tile u = 4g + t
+    // takes column 64g + 4(l%16) + t, so that one float4 load from a row of B
+    // feeds four tiles (a quarter of the load instructions, each costing the
+    // same address-processing time whatever its width).
+    const auto ncol = [&](int u) -> std::uint32_t {
+        return VB ? n0 + 64 * (u / 4) + 4 * li + (u % 4) : n0 + 16 * u + li;
+    };
 
-    // Per-lane element offsets inside a 4-row step (row lk, clamped column).
+    // Per-lane element offsets inside a 4-row step (row lk, clamped column;
+    // with VB the float4's start, clamped to the row's last 4 columns: a
+    // clamped float4 only feeds columns past N, which are never stored).
     std::uint32_t offA[TM], offB[TN];
 #pragma unroll
     for (int t = 0; t < TM; ++t) offA[t] = lk * a.lda + min(m0 + 16 * t + li, a.M - 1);
 #pragma unroll
-    for (int t = 0; t < TN; ++t) offB[t] = lk * a.ldb + min(n0 + 16 * t + li, a.N - 1);
+    for (int t = 0; t < TN; ++t)
+        offB[t] = VB ? lk * a.ldb + min(n0 + 64 * (t / 4) + 4 * li, a.N - 4) : lk * a.ldb + min(ncol(t), a.N - 1);
     // Relu-gradient form: this lane's W2 rows, G column offsets (clamped).
     float w2[TN][GC];
     float dw2[TN][GC];
@@ -91,7 +102,7 @@ __global__ void __launch_bounds__(kWave * WM * WN) tn_partial_kernel(TnArgs a) {
             dw2[t][j] = 0.0f;
             w2[t][j] = 0.0f;
             if (CT > 0 && static_cast<std::uint32_t>(j) < a.C)
-                w2[t][j] = a.W2[static_cast<std::uint64_t>(min(n0 + 16 * t + li, a.N - 1)) * a.C + j];
+                w2[t][j] = a.W2[static_cast<std::uint64_t>(min(ncol(t), a.N - 1)) * a.C + j];
         }
 
     f32x4 acc[TM][TN];
@@ -107,8 +118,19 @@ __global__ void __launch_bounds__(kWave * WM * WN) tn_partial_kernel(TnArgs a) {
             const float* rb = a.B + static_cast<std::uint64_t>(k + 4 * s) * a.ldb;
 #pragma unroll
             for (int t = 0; t < TM; ++t) xa[s][t] = ra[offA[t]];
+            if constexpr (VB) {
 #pragma unroll
-            for (int t = 0; t < TN; ++t) xb[s][t] = rb[offB[t]];
+                for (int g = 0; g < TN / 4; ++g) {
+                    const float4 v = *reinterpret_cast<const float4*>(rb + offB[4 * g]);
+                    xb[s][4 * g] = v.x;
+                    xb[s][4 * g + 1] = v.y;
+                    xb[s][4 * g + 2] = v.z;
+                    xb[s][4 * g + 3] = v.w;
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < TN; ++t) xb[s][t] = rb[offB[t]];
+            }
             if constexpr (CT > 0) {
                 const float* rg = a.G + static_cast<std::uint64_t>(k + 4 * s) * a.ldg;
 #pragma unroll
@@ -179,8 +201,20 @@ __global__ void __launch_bounds__(kWave * WM * WN) tn_partial_kernel(TnArgs a) {
             const float* rb = a.B + static_cast<std::uint64_t>(kt + 4 * s) * a.ldb;
 #pragma unroll
             for (int t = 0; t < TM; ++t) ca[s][t] = in ? ra[offA[t]] : 0.0f;
+            if constexpr (VB) {
 #pragma unroll
-            for (int t = 0; t < TN; ++t) cb[s][t] = in ? rb[offB[t]] : 0.0f;
+                for (int g = 0; g < TN / 4; ++g) {
+                    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    if (in) v = *reinterpret_cast<const float4*>(rb + offB[4 * g]);
+                    cb[s][4 * g] = v.x;
+                    cb[s][4 * g + 1] = v.y;
+                    cb[s][4 * g + 2] = v.z;
+                    cb[s][4 * g + 3] = v.w;
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < TN; ++t) cb[s][t] = in ? rb[offB[t]] : 0.0f;
+            }
             if constexpr (CT > 0) {
                 const float* rg = a.G + static_cast<std::uint64_t>(kt + 4 * s) * a.ldg;
 #pragma unroll
@@ -190,13 +224,13 @@ __global__ void __launch_bounds__(kWave * WM * WN) tn_partial_kernel(TnArgs a) {
         multiply(ca, cb, cg);
     }
 
-    // Tile (t, u): accumulator v of lane l is C(m0 + 16t + 4*(l/16) + v, n0 + 16u + l%16).
+    // Tile (t, u): accumulator v of lane l is C(m0 + 16t + 4*(l/16) + v, ncol(u)).
     float* out = a.partial + static_cast<std::uint64_t>(blockIdx.x) * a.M * a.N;
 #pragma unroll
     for (int t = 0; t < TM; ++t)
 #pragma unroll
         for (int u = 0; u < TN; ++u) {
-            const std::uint32_t n = n0 + 16 * u + li;
+            const std::uint32_t n = ncol(u);
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const std::uint32_t m = m0 + 16 * t + 4 * lk + v;
@@ -204,8 +238,8 @@ __global__ void __launch_bounds__(kWave * WM * WN) tn_partial_kernel(TnArgs a) {
             }
         }
     if constexpr (CT > 0) {
-        // H^T G of this split: column n = n0 + 16u + l%16 summed over the 4
-        // row quarters; one block row of C (cbm == 0, first wave row) writes it.
+        // H^T G of this split: column n = ncol(u) summed over the 4 row
+        // quarters; one block row of C (cbm == 0, first wave row) writes it.
         float* out2 = a.partial2 + static_cast<std::uint64_t>(blockIdx.x) * a.N * a.C;
 #pragma unroll
         for (int u = 0; u < TN; ++u)
@@ -214,7 +248,7 @@ __global__ void __launch_bounds__(kWave * WM * WN) tn_partial_kernel(TnArgs a) {
                 float v = dw2[u][j];
                 v += __shfl_xor(v, 16);
                 v += __shfl_xor(v, 32);
-                const std::uint32_t n = n0 + 16 * u + li;
+                const std::uint32_t n = ncol(u);
                 if (cbm == 0 && wm == 0 && lk == 0 && n < a.N && static_cast<std::uint32_t>(j) < a.C)
                     out2[static_cast<std::uint64_t>(n) * a.C + j] = v;
             }
@@ -474,9 +508,9 @@ TnPlan tn_plan(std::uint32_t K, std::uint32_t M, std::uint32_t N, std::uint32_t 
 // as C, 2.5x torch.mm).
 inline bool tn_swapped(std::uint32_t M, std::uint32_t N) { return M > 16 && N > 16 && N <= 128 && N < M; }
 
-template <int TM, int TN, int WM, int WN, int U, int CT = 0>
+template <int TM, int TN, int WM, int WN, int U, int CT = 0, bool VB = false>
 void tn_launch(const TnArgs& a, const TnPlan& p, hipStream_t st) {
-    hipLaunchKernelGGL((tn_partial_kernel<TM, TN, WM, WN, U, CT>), dim3(p.splits, p.blocksM * p.blocksN),
+    hipLaunchKernelGGL((tn_partial_kernel<TM, TN, WM, WN, U, CT, VB>), dim3(p.splits, p.blocksM * p.blocksN),
                        dim3(kWave * WM * WN), 0, st, a);
 }
 
@@ -635,10 +669,21 @@ int tcc_gcn_relu_grad(const float* AX, std::uint32_t ldax, const float* H, std::
     // C <= 2: the wide tiles; up to 8 classes: 8 waves of TM x 2 tiles and 2
     // steps per iteration, to hold the G rows in registers (same blocks).
     const bool two = C <= 2;
+    // H rows as float4 when they allow 16-byte loads (4 | Hd, 4 | ldh, H aligned)
+    const bool vb = Hd % 4 == 0 && ldh % 4 == 0 && reinterpret_cast<std::uintptr_t>(H) % 16 == 0;
     switch (p.shape) {
-        case TnShape::Wide4: two ? tn_launch<4, 4, 1, 4, 4, 2>(a, p, st) : tn_launch<4, 2, 1, 8, 2, 8>(a, p, st); break;
-        case TnShape::Wide7: two ? tn_launch<7, 4, 1, 4, 4, 2>(a, p, st) : tn_launch<7, 2, 1, 8, 2, 8>(a, p, st); break;
-        default: two ? tn_launch<8, 4, 1, 4, 4, 2>(a, p, st) : tn_launch<8, 2, 1, 8, 2, 8>(a, p, st); break;
+        case TnShape::Wide4:
+            if (two && vb) tn_launch<4, 4, 1, 4, 4, 2, true>(a, p, st);
+            else two ? tn_launch<4, 4, 1, 4, 4, 2>(a, p, st) : tn_launch<4, 2, 1, 8, 2, 8>(a, p, st);
+            break;
+        case TnShape::Wide7:
+            if (two && vb) tn_launch<7, 4, 1, 4, 4, 2, true>(a, p, st);
+            else two ? tn_launch<7, 4, 1, 4, 4, 2>(a, p, st) : tn_launch<7, 2, 1, 8, 2, 8>(a, p, st);
+            break;
+        default:
+            if (two && vb) tn_launch<8, 4, 1, 4, 4, 2, true>(a, p, st);
+            else two ? tn_launch<8, 4, 1, 4, 4, 2>(a, p, st) : tn_launch<8, 2, 1, 8, 2, 8>(a, p, st);
+            break;
     }
     TCC_LAUNCH_CHECK();
     hipLaunchKernelGGL(tn_reduce_kernel, dim3(grid_for(static_cast<std::uint64_t>(F) * Hd, 16)), dim3(256), 0, st,
