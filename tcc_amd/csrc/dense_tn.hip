@@ -571,12 +571,15 @@ int tcc_dense_tn(const float* A, std::uint32_t lda, const float* B, std::uint32_
     a.N = N;
     a.rowsPerSplit = p.rowsPerSplit;
     a.blocksM = p.blocksM;
+    // B rows as float4 feeding four interleaved N tiles (as the relu-gradient
+    // form) when they allow 16-byte loads
+    const bool vb = N % 4 == 0 && ldb % 4 == 0 && reinterpret_cast<std::uintptr_t>(B) % 16 == 0;
     switch (p.shape) {
         case TnShape::NarrowN: tn_launch<4, 1, 4, 1, 8>(a, p, st); break;
         case TnShape::NarrowM: tn_launch<1, 4, 1, 4, 8>(a, p, st); break;
-        case TnShape::Wide4: tn_launch<4, 4, 1, 4, 6>(a, p, st); break;
-        case TnShape::Wide7: tn_launch<7, 4, 1, 4, 6>(a, p, st); break;
-        default: tn_launch<8, 4, 1, 4, 6>(a, p, st); break;
+        case TnShape::Wide4: vb ? tn_launch<4, 4, 1, 4, 6, 0, true>(a, p, st) : tn_launch<4, 4, 1, 4, 6>(a, p, st); break;
+        case TnShape::Wide7: vb ? tn_launch<7, 4, 1, 4, 6, 0, true>(a, p, st) : tn_launch<7, 4, 1, 4, 6>(a, p, st); break;
+        default: vb ? tn_launch<8, 4, 1, 4, 6, 0, true>(a, p, st) : tn_launch<8, 4, 1, 4, 6>(a, p, st); break;
     }
     TCC_LAUNCH_CHECK();
     const std::uint64_t MN = static_cast<std::uint64_t>(M) * N;
