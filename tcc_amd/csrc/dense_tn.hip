@@ -58,9 +58,10 @@ __device__ __forceinline__ std::uint32_t tn_uniform(std::uint32_t v) {
 // (G W2^T) (.) [H > 0] from G [K x C] and W2 [N x C] (C <= CT), while H^T G
 // is summed beside it into partial2 -- the layer-1 weight gradient and the
 // layer-2 weight gradient of a two-layer GCN in one pass over its rows.
-template <int TM, int TN, int WM, int WN, int U, int CT, bool VB = false>
+template <int TM, int TN, int WM, int WN, int U, int CT, bool VB = false, bool VA = false>
 __global__ void __launch_bounds__(kWave * WM * WN) tn_partial_kernel(TnArgs a) {
     static_assert(!VB || TN % 4 == 0, "a float4 of B feeds four N tiles");
+    constexpr int TA = VA ? TM / 4 : 0;  // groups of four M tiles fed by one float4 of A
     constexpr int BM = 16 * TM * WM, BN = 16 * TN * WN;
     constexpr int GC = CT > 0 ? CT : 1;  // G columns held per row
     constexpr std::uint32_t kStep = 4 * U;
@@ -79,13 +80,19 @@ __global__ void __launch_bounds__(kWave * WM * WN) tn_partial_kernel(TnArgs a) {
     const auto ncol = [&](int u) -> std::uint32_t {
         return VB ? n0 + 64 * (u / 4) + 4 * li + (u % 4) : n0 + 16 * u + li;
     };
+    // Row r of M tile t: 16t + r, or with VA, for the first 4*TA tiles
+    // (t = 4h + e), 64h + 4r + e (one float4 of an A row feeds four tiles).
+    const auto mrow = [&](int t, unsigned r) -> std::uint32_t {
+        return t < 4 * TA ? m0 + 64 * (t / 4) + 4 * r + (t % 4) : m0 + 16 * t + r;
+    };
 
     // Per-lane element offsets inside a 4-row step (row lk, clamped column;
     // with VB the float4's start, clamped to the row's last 4 columns: a
     // clamped float4 only feeds columns past N, which are never stored).
     std::uint32_t offA[TM], offB[TN];
 #pragma unroll
-    for (int t = 0; t < TM; ++t) offA[t] = lk * a.lda + min(m0 + 16 * t + li, a.M - 1);
+    for (int t = 0; t < TM; ++t)
+        offA[t] = t < 4 * TA ? lk * a.lda + min(m0 + 64 * (t / 4) + 4 * li, a.M - 4) : lk * a.lda + min(mrow(t, li), a.M - 1);
 #pragma unroll
     for (int t = 0; t < TN; ++t)
         offB[t] = VB ? lk * a.ldb + min(n0 + 64 * (t / 4) + 4 * li, a.N - 4) : lk * a.ldb + min(ncol(t), a.N - 1);
@@ -117,7 +124,15 @@ __global__ void __launch_bounds__(kWave * WM * WN) tn_partial_kernel(TnArgs a) {
             const float* ra = a.A + static_cast<std::uint64_t>(k + 4 * s) * a.lda;
             const float* rb = a.B + static_cast<std::uint64_t>(k + 4 * s) * a.ldb;
 #pragma unroll
-            for (int t = 0; t < TM; ++t) xa[s][t] = ra[offA[t]];
+            for (int h = 0; h < TA; ++h) {
+                const float4 v = *reinterpret_cast<const float4*>(ra + offA[4 * h]);
+                xa[s][4 * h] = v.x;
+                xa[s][4 * h + 1] = v.y;
+                xa[s][4 * h + 2] = v.z;
+                xa[s][4 * h + 3] = v.w;
+            }
+#pragma unroll
+            for (int t = 4 * TA; t < TM; ++t) xa[s][t] = ra[offA[t]];
             if constexpr (VB) {
 #pragma unroll
                 for (int g = 0; g < TN / 4; ++g) {
@@ -200,7 +215,16 @@ __global__ void __launch_bounds__(kWave * WM * WN) tn_partial_kernel(TnArgs a) {
             const float* ra = a.A + static_cast<std::uint64_t>(kt + 4 * s) * a.lda;
             const float* rb = a.B + static_cast<std::uint64_t>(kt + 4 * s) * a.ldb;
 #pragma unroll
-            for (int t = 0; t < TM; ++t) ca[s][t] = in ? ra[offA[t]] : 0.0f;
+            for (int h = 0; h < TA; ++h) {
+                float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (in) v = *reinterpret_cast<const float4*>(ra + offA[4 * h]);
+                ca[s][4 * h] = v.x;
+                ca[s][4 * h + 1] = v.y;
+                ca[s][4 * h + 2] = v.z;
+                ca[s][4 * h + 3] = v.w;
+            }
+#pragma unroll
+            for (int t = 4 * TA; t < TM; ++t) ca[s][t] = in ? ra[offA[t]] : 0.0f;
             if constexpr (VB) {
 #pragma unroll
                 for (int g = 0; g < TN / 4; ++g) {
@@ -224,7 +248,7 @@ __global__ void __launch_bounds__(kWave * WM * WN) tn_partial_kernel(TnArgs a) {
         multiply(ca, cb, cg);
     }
 
-    // Tile (t, u): accumulator v of lane l is C(m0 + 16t + 4*(l/16) + v, ncol(u)).
+    // Tile (t, u): accumulator v of lane l is C(mrow(t, 4*(l/16) + v), ncol(u)).
     float* out = a.partial + static_cast<std::uint64_t>(blockIdx.x) * a.M * a.N;
 #pragma unroll
     for (int t = 0; t < TM; ++t)
@@ -233,7 +257,7 @@ __global__ void __launch_bounds__(kWave * WM * WN) tn_partial_kernel(TnArgs a) {
             const std::uint32_t n = ncol(u);
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const std::uint32_t m = m0 + 16 * t + 4 * lk + v;
+                const std::uint32_t m = mrow(t, 4 * lk + v);
                 if (m < a.M && n < a.N) out[static_cast<std::uint64_t>(m) * a.N + n] = acc[t][u][v];
             }
         }
@@ -508,9 +532,9 @@ TnPlan tn_plan(std::uint32_t K, std::uint32_t M, std::uint32_t N, std::uint32_t 
 // as C, 2.5x torch.mm).
 inline bool tn_swapped(std::uint32_t M, std::uint32_t N) { return M > 16 && N > 16 && N <= 128 && N < M; }
 
-template <int TM, int TN, int WM, int WN, int U, int CT = 0, bool VB = false>
+template <int TM, int TN, int WM, int WN, int U, int CT = 0, bool VB = false, bool VA = false>
 void tn_launch(const TnArgs& a, const TnPlan& p, hipStream_t st) {
-    hipLaunchKernelGGL((tn_partial_kernel<TM, TN, WM, WN, U, CT, VB>), dim3(p.splits, p.blocksM * p.blocksN),
+    hipLaunchKernelGGL((tn_partial_kernel<TM, TN, WM, WN, U, CT, VB, VA>), dim3(p.splits, p.blocksM * p.blocksN),
                        dim3(kWave * WM * WN), 0, st, a);
 }
 
@@ -574,12 +598,23 @@ int tcc_dense_tn(const float* A, std::uint32_t lda, const float* B, std::uint32_
     // B rows as float4 feeding four interleaved N tiles (as the relu-gradient
     // form) when they allow 16-byte loads
     const bool vb = N % 4 == 0 && ldb % 4 == 0 && reinterpret_cast<std::uintptr_t>(B) % 16 == 0;
+    // and A rows likewise feeding four interleaved M tiles
+    const bool va = vb && M % 4 == 0 && lda % 4 == 0 && reinterpret_cast<std::uintptr_t>(A) % 16 == 0;
     switch (p.shape) {
         case TnShape::NarrowN: tn_launch<4, 1, 4, 1, 8>(a, p, st); break;
         case TnShape::NarrowM: tn_launch<1, 4, 1, 4, 8>(a, p, st); break;
-        case TnShape::Wide4: vb ? tn_launch<4, 4, 1, 4, 6, 0, true>(a, p, st) : tn_launch<4, 4, 1, 4, 6>(a, p, st); break;
-        case TnShape::Wide7: vb ? tn_launch<7, 4, 1, 4, 6, 0, true>(a, p, st) : tn_launch<7, 4, 1, 4, 6>(a, p, st); break;
-        default: vb ? tn_launch<8, 4, 1, 4, 6, 0, true>(a, p, st) : tn_launch<8, 4, 1, 4, 6>(a, p, st); break;
+        case TnShape::Wide4:
+            if (va) tn_launch<4, 4, 1, 4, 6, 0, true, true>(a, p, st);
+            else vb ? tn_launch<4, 4, 1, 4, 6, 0, true>(a, p, st) : tn_launch<4, 4, 1, 4, 6>(a, p, st);
+            break;
+        case TnShape::Wide7:
+            if (va) tn_launch<7, 4, 1, 4, 6, 0, true, true>(a, p, st);
+            else vb ? tn_launch<7, 4, 1, 4, 6, 0, true>(a, p, st) : tn_launch<7, 4, 1, 4, 6>(a, p, st);
+            break;
+        default:
+            if (va) tn_launch<8, 4, 1, 4, 6, 0, true, true>(a, p, st);
+            else vb ? tn_launch<8, 4, 1, 4, 6, 0, true>(a, p, st) : tn_launch<8, 4, 1, 4, 6>(a, p, st);
+            break;
     }
     TCC_LAUNCH_CHECK();
     const std::uint64_t MN = static_cast<std::uint64_t>(M) * N;
@@ -674,17 +709,21 @@ int tcc_gcn_relu_grad(const float* AX, std::uint32_t ldax, const float* H, std::
     const bool two = C <= 2;
     // H rows as float4 when they allow 16-byte loads (4 | Hd, 4 | ldh, H aligned)
     const bool vb = Hd % 4 == 0 && ldh % 4 == 0 && reinterpret_cast<std::uintptr_t>(H) % 16 == 0;
+    const bool va = two && vb && F % 4 == 0 && ldax % 4 == 0 && reinterpret_cast<std::uintptr_t>(AX) % 16 == 0;
     switch (p.shape) {
         case TnShape::Wide4:
-            if (two && vb) tn_launch<4, 4, 1, 4, 4, 2, true>(a, p, st);
+            if (va) tn_launch<4, 4, 1, 4, 4, 2, true, true>(a, p, st);
+            else if (two && vb) tn_launch<4, 4, 1, 4, 4, 2, true>(a, p, st);
             else two ? tn_launch<4, 4, 1, 4, 4, 2>(a, p, st) : tn_launch<4, 2, 1, 8, 2, 8>(a, p, st);
             break;
         case TnShape::Wide7:
-            if (two && vb) tn_launch<7, 4, 1, 4, 4, 2, true>(a, p, st);
+            if (va) tn_launch<7, 4, 1, 4, 4, 2, true, true>(a, p, st);
+            else if (two && vb) tn_launch<7, 4, 1, 4, 4, 2, true>(a, p, st);
             else two ? tn_launch<7, 4, 1, 4, 4, 2>(a, p, st) : tn_launch<7, 2, 1, 8, 2, 8>(a, p, st);
             break;
         default:
-            if (two && vb) tn_launch<8, 4, 1, 4, 4, 2, true>(a, p, st);
+            if (va) tn_launch<8, 4, 1, 4, 4, 2, true, true>(a, p, st);
+            else if (two && vb) tn_launch<8, 4, 1, 4, 4, 2, true>(a, p, st);
             else two ? tn_launch<8, 4, 1, 4, 4, 2>(a, p, st) : tn_launch<8, 2, 1, 8, 2, 8>(a, p, st);
             break;
     }
