@@ -1,0 +1,106 @@
+"""Products at BASELINE.json's full sizes, through size-independent
+properties (the oracle's CSR SpMM would take minutes here).
+
+Checksum of checksums: for Y = A X, the column sums of Y satisfy
+1^T Y = (1^T A) X, so per feature f
+    sum_i Y[i, f] = sum_j c_j X[j, f],   c_j = sum_i a_ij,
+with the forward products' TF32 rounding applied to a_ij and X on the right
+(the oracle's tf32).  The left side is summed on the device in fp64; the
+right side in numpy fp64 from the COO.  A missing or doubled window or unit
+moves the checksum by ~1e-3 relative (config 2: one 31-edge window, 2e-3;
+a single edge ~7e-5); the products agree with it to 1e-8 to 3e-8.  For the transposed product (plain fp32), 1^T (A^T dY) = (A 1)^T dY.
+Config 3 also checks the 4-phase BCSR against the ordinary one, element by
+element.
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-6  # measured 1e-8 to 3e-8; one window of 31 edges left out moves it by 2e-3
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
+
+
+def graph(cfg_id):
+    from tcc_amd.graphs import CONFIGS, make_features, make_graph
+
+    cfg = CONFIGS[cfg_id]
+    n, F = cfg["n"], cfg["F"]
+    rows, cols, vals = make_graph(cfg_id, device="cuda")
+    r32 = rows.to(torch.int32).contiguous()
+    c32 = cols.to(torch.int32).contiguous()
+    X = make_features(n, F, cfg_id, device="cuda")
+    return n, F, r32, c32, vals, X
+
+
+def column_sums(oracle, idx, vals, n, tf32):
+    v = vals.cpu().numpy().astype(np.float32)
+    if tf32:
+        v = oracle.tf32(v)
+    return np.bincount(idx.cpu().numpy().astype(np.int64), weights=v.astype(np.float64), minlength=n)
+
+
+def device_checksum(Y, rows):
+    return Y[:rows].double().sum(dim=0).cpu().numpy()
+
+
+def test_fullsize_config2_checksums(gpu, oracle):
+    from tcc_amd import swtcf
+
+    n, F, r32, c32, vals, X = graph(2)
+    print(f"config 2: n={n} nnz={r32.numel()} F={F}", flush=True)
+    A = swtcf.coo_to_bcsr(r32, c32, vals, n, n)
+    Y = swtcf.bcsr_spmm(A, X)
+    c = column_sums(oracle, c32, vals, n, tf32=True)
+    Xt = oracle.tf32(X.cpu().numpy()).astype(np.float64)
+    want = c @ Xt
+    got = device_checksum(Y, n)
+    print(f"forward checksum rel-L2 {rel_l2(got, want):.2e}", flush=True)
+    assert rel_l2(got, want) <= TOL, "forward"
+    assert torch.count_nonzero(Y[n:]).item() == 0
+    # the check's reach: the expected side without one row window's edges
+    # (a mistake planted in the reference, not in the product) must fail it
+    rows_np = r32.cpu().numpy()
+    drop = (rows_np // 8) == 1000
+    assert drop.any()
+    vals_kept = torch.where(torch.from_numpy(drop).cuda(), torch.zeros_like(vals), vals)
+    c_drop = column_sums(oracle, c32, vals_kept, n, tf32=True)
+    miss = rel_l2(got, c_drop @ Xt)
+    print(f"one window ({int(drop.sum())} edges) left out of the reference: rel-L2 {miss:.2e}", flush=True)
+    assert miss > 100 * TOL
+
+    B = swtcf.coo_to_bcsc(r32, c32, vals, n, n)
+    dY = torch.randn(n, F, device="cuda")
+    dX = swtcf.bcsc_transpose_spmm(B, dY)
+    r = column_sums(oracle, r32, vals, n, tf32=False)  # row sums of A
+    wantT = r @ dY.cpu().numpy().astype(np.float64)
+    print(f"transpose checksum rel-L2 {rel_l2(device_checksum(dX, n), wantT):.2e}", flush=True)
+    assert rel_l2(device_checksum(dX, n), wantT) <= TOL, "transpose"
+
+
+def test_fullsize_config3_packed_phased(gpu, oracle):
+    from tcc_amd import swtcf
+
+    n, F, r32, c32, vals, X = graph(3)
+    print(f"config 3: n={n} nnz={r32.numel()} F={F}", flush=True)
+    c = column_sums(oracle, c32, vals, n, tf32=True)
+    want = c @ oracle.tf32(X.cpu().numpy()).astype(np.float64)
+    P = swtcf.tf32_pack(X)
+    del X
+    A4 = swtcf.coo_to_bcsr(r32, c32, vals, n, n, phases=4)
+    Y4 = swtcf.bcsr_spmm_packed(A4, P, F)
+    print(f"4 phases: checksum rel-L2 {rel_l2(device_checksum(Y4, n), want):.2e}", flush=True)
+    assert rel_l2(device_checksum(Y4, n), want) <= TOL, "4 phases"
+    A4.release()
+    A1 = swtcf.coo_to_bcsr(r32, c32, vals, n, n)
+    Y1 = swtcf.bcsr_spmm_packed(A1, P, F)
+    assert rel_l2(device_checksum(Y1, n), want) <= TOL, "ordinary"
+    d = ((Y4[:n].double() - Y1[:n].double()).norm() / Y1[:n].double().norm()).item()
+    print(f"phased against ordinary: rel-L2 {d:.2e}", flush=True)
+    assert d <= 1e-6, f"phased against ordinary: {d}"
