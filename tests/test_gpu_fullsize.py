@@ -104,3 +104,42 @@ def test_fullsize_config3_packed_phased(gpu, oracle):
     d = ((Y4[:n].double() - Y1[:n].double()).norm() / Y1[:n].double().norm()).item()
     print(f"phased against ordinary: rel-L2 {d:.2e}", flush=True)
     assert d <= 1e-6, f"phased against ordinary: {d}"
+
+
+def test_fullsize_config4_mixed_and_narrow(gpu, oracle):
+    """The GCN graph (2.45M nodes, 61.9M edges, no values: every a_ij = 1):
+    the first-layer product over the hot/cold feature table (fp32 and packed
+    host rows), the second layer's F = 2 product and its transpose."""
+    from tcc_amd import gcn, swtcf
+    from tcc_amd.graphs import CONFIGS, make_features, make_graph
+
+    cfg = CONFIGS[4]
+    n, F = cfg["n"], cfg["F"]
+    rows, cols, _ = make_graph(4, device="cuda")
+    print(f"config 4: n={n} nnz={rows.numel()} F={F}", flush=True)
+    X = make_features(n, F, cfg["seed"], device="cuda")
+    table = gcn.FeatureTable(X, cols)
+    g1, g2 = gcn.build_gcn_graphs(rows, cols, n, table.hot)
+    indeg = np.bincount(cols.cpu().numpy().astype(np.int64), minlength=n).astype(np.float64)
+    outdeg = np.bincount(rows.cpu().numpy().astype(np.int64), minlength=n).astype(np.float64)
+    want = indeg @ oracle.tf32(X.cpu().numpy()).astype(np.float64)
+
+    got = g1.aggregate(F, source=table.source).double().sum(dim=0).cpu().numpy()
+    print(f"mixed, fp32 host rows: checksum rel-L2 {rel_l2(got, want):.2e}", flush=True)
+    assert rel_l2(got, want) <= TOL, "mixed fp32"
+    ptable = gcn.FeatureTable(X, cols, packed=True)
+    got = g1.aggregate(F, source=ptable.source).double().sum(dim=0).cpu().numpy()
+    print(f"mixed, packed host rows: checksum rel-L2 {rel_l2(got, want):.2e}", flush=True)
+    assert rel_l2(got, want) <= TOL, "mixed packed"
+
+    XW = torch.randn(n, 2, device="cuda")
+    got = g2.aggregate(2, x=XW).double().sum(dim=0).cpu().numpy()
+    want2 = indeg @ oracle.tf32(XW.cpu().numpy()).astype(np.float64)
+    print(f"narrow F=2: checksum rel-L2 {rel_l2(got, want2):.2e}", flush=True)
+    assert rel_l2(got, want2) <= TOL, "narrow"
+    dY = torch.randn(n, 2, device="cuda")
+    dX = swtcf.bcsc_transpose_spmm(g2.bwd, dY)
+    got = dX[:n].double().sum(dim=0).cpu().numpy()
+    wantT = outdeg @ dY.cpu().numpy().astype(np.float64)
+    print(f"narrow transpose F=2: checksum rel-L2 {rel_l2(got, wantT):.2e}", flush=True)
+    assert rel_l2(got, wantT) <= TOL, "narrow transpose"
