@@ -143,3 +143,46 @@ def test_fullsize_config4_mixed_and_narrow(gpu, oracle):
     wantT = outdeg @ dY.cpu().numpy().astype(np.float64)
     print(f"narrow transpose F=2: checksum rel-L2 {rel_l2(got, wantT):.2e}", flush=True)
     assert rel_l2(got, wantT) <= TOL, "narrow transpose"
+
+
+def test_fullsize_config3_swtcf(gpu, oracle):
+    """convertCOOToSWTCF and the SWTCF SpMM on the config-3 graph (114M
+    edges, unit values; F = 128 for time): every edge is exactly one tile
+    bit, the product passes the checksum, and it equals the BCSR gather's
+    element by element.  X holds TF32 values already, so the SWTCF path's
+    per-tile choice between TF32 and fp32 inputs does not change it."""
+    from tcc_amd import swtcf
+    from tcc_amd.graphs import CONFIGS, make_graph
+
+    n = CONFIGS[3]["n"]
+    F = 128
+    rows, cols, _ = make_graph(3, device="cuda")
+    r32 = rows.to(torch.int32).contiguous()
+    c32 = cols.to(torch.int32).contiguous()
+    nnz = r32.numel()
+    del rows
+    print(f"config 3 SWTCF: n={n} nnz={nnz} F={F}", flush=True)
+    m = swtcf.DeviceSWTCFMatrix(n, n, nnz, 16)
+    ws = swtcf.SWTCFConvertWorkspace(nnz, n, 16)
+    swtcf.convertCOOToSWTCF(r32, c32, nnz, m, ws)
+    assert ws.device_error() == 0
+    h = m.to_host()
+    bits = int(np.unpackbits(h["tileLocalBit"].view(np.uint8)).sum())
+    print(f"tiles {h['numTiles']}, tile bits {bits}", flush=True)
+    assert bits == nnz
+    assert np.all(np.diff(h["colWindowOffset"].astype(np.int64)) >= 0)
+
+    X = oracle.tf32(np.random.default_rng(33).standard_normal((n, F)).astype(np.float32))
+    Xd = torch.from_numpy(X).cuda()
+    Ys = torch.zeros(n, F, device="cuda")
+    swtcf.swtcf_spmm(m, Xd, Ys, 12)
+    indeg = np.bincount(c32.cpu().numpy().astype(np.int64), minlength=n).astype(np.float64)
+    want = indeg @ X.astype(np.float64)
+    got = Ys.double().sum(dim=0).cpu().numpy()
+    print(f"SWTCF checksum rel-L2 {rel_l2(got, want):.2e}", flush=True)
+    assert rel_l2(got, want) <= TOL
+    A = swtcf.coo_to_bcsr(r32, c32, None, n, n)
+    Yb = swtcf.bcsr_spmm(A, Xd)[:n]
+    d = ((Ys.double() - Yb.double()).norm() / Yb.double().norm()).item()
+    print(f"SWTCF against the BCSR gather: rel-L2 {d:.2e}", flush=True)
+    assert d <= 1e-6
