@@ -1,28 +1,35 @@
 #!/usr/bin/env python3
 """Benchmark of the SWTCF / spmm_cnic hot path on one MI355X.
 
-Default workload ("config 2"): R-MAT graph, 169k
-nodes, 1.17M nnz, sym-normalised fp32 values, X = N(0,1) [169k x 128]; one
-step = one forward BCSR SpMM (Y = A X) over the whole graph, inputs resident
-in HBM.  The other configurations:
-  --config 1  uniform 4096 x 16/row, F=32: SWTCF convert + SWTCF SpMM
-  --config 3  R-MAT 233k nodes, 114M nnz, F=602: BCSR SpMM
-  --config 4  R-MAT 2.45M nodes, 61.9M nnz, F=100, top-20% rows hot in HBM,
-              the rest zero-copy from pinned host memory: mixed SpMM
-              (BCSR over hot sources + BCSC over cold sources)
-  --config 5  2-layer GCN (100 -> 256 -> 2, ReLU) on the config-4 graph: one
-              full-graph training epoch (forward, loss, backward, Adam)
+Default workload ("config 3", the north star's
+target and the largest single-GPU configuration): R-MAT graph, 233k nodes,
+114M nnz, sym-normalised fp32 values, X = N(0,1) [233k x 602]; one step = one
+SpMM Y = A X over the whole graph with TF32 numerics, inputs resident in HBM
+(the TF32 packing of X and the zero fill of Y are inside the step).  The same
+run also times, under `extra`:
+  config2  R-MAT 169k nodes, 1.17M nnz, F=128: forward BCSR SpMM
+  config5  2-layer GCN (100 -> 256 -> 2, ReLU) on the config-4 graph: one
+           full-graph training epoch, and each layer's forward+backward
+Other configurations as the main line: --config 1 (uniform 4096 x 16/row,
+F=32: SWTCF convert + SWTCF SpMM), 2, 4 (2.45M nodes, 61.9M nnz, F=100, top-20%
+rows hot in HBM, the rest zero-copy from pinned host memory: mixed SpMM), 5.
 
 Prints one JSON line.  SpMM configurations report GFLOP/s (2*nnz*F per
-step), the HBM roofline of the dominant kernel (algorithmic bytes
-4F(n_src+n_dst) + 8 nnz + 4(n_dst+1) per launch over the HIP-event-timed
-step) and the CPU baseline (the oracle's CSR SpMM on the host cores over a
-bounded sample of the same matrix, also the parity check).  Config 5
-reports the epoch time in ms and each layer's forward+backward time.
+step) and the roofline of BASELINE.md: with the algorithmic bytes
+4F(n_src+n_dst) + 8 nnz + 4(n_dst+1) and AI = flops / bytes, the roof is
+min(157.3 TFLOP/s, AI * 8 TB/s); config 3 (AI 67.5) is bound by the fp32
+roof, config 2 (AI 1.6) by HBM.  The counter-measured DRAM traffic of the
+step's kernels (rocprofv3 FETCH_SIZE + WRITE_SIZE, profiles/) is reported
+beside it.  The CPU baseline is the reference's own SpMM call,
+torch.sparse.mm (train/tcgnn_conv_release.py:152), on the host cores over a
+bounded sample of the same matrix; the oracle's CSR loop is timed beside it
+and checks the GPU result on that sample.
 """
 from __future__ import annotations
 
 import argparse
+import copy
+import hashlib
 import json
 import os
 import sys
@@ -34,7 +41,9 @@ sys.path.insert(0, ROOT)
 
 METRIC = "SpMM GFLOP/s (2·nnz·F) + % HBM roofline; GCN layer fwd+bwd ms at 1 GPU"
 HBM_PEAK_GBPS = 8000.0
+FP32_PEAK_TFLOPS = 157.3  # MI355X fp32 (vector = matrix)
 PCIE_PEAK_GBPS = 64.0  # PCIe Gen5 x16, one direction
+NORTH_STAR_DRAM_FRAC = 0.60  # config 3: ">= 60% of peak HBM bandwidth"
 # Gathers per feature row from which packing X to TF32 first pays off
 # (measured: 441 -> 12% faster at config 3; 7.3 -> 23% slower at config 2).
 PACK_MIN_REUSE = 16.0
@@ -45,28 +54,31 @@ PACK_MIN_REUSE = 16.0
 # with 2).
 PHASE_MIN_BLOCKS_PER_WINDOW = 64.0
 PHASES = 4
+CPU_SAMPLE_NNZ = 16_000_000
 
 WORKLOADS = {
     1: "config1: uniform 4096 nodes x 16 nnz/row, F=32, SWTCF convert + SWTCF SpMM",
     2: "config2: R-MAT (0.57,0.19,0.19) 169k nodes, 1.17M nnz, sym-normalised, F=128, forward BCSR SpMM",
-    3: "config3: R-MAT (0.57,0.19,0.19) 233k nodes, 114M nnz, sym-normalised, F=602, forward BCSR SpMM",
+    3: "config3: R-MAT (0.57,0.19,0.19) 233k nodes, 114M nnz, sym-normalised, F=602, SpMM (HBM-bound regime)",
     4: "config4: R-MAT 2.45M nodes, 61.9M nnz, F=100, top-20% rows hot in HBM, rest pinned host: mixed SpMM",
     5: "config5: 2-layer GCN 100->256->2 (ReLU, dropout 0, Adam 0.003) on the config-4 graph, full-graph epoch",
 }
 
 
-def parse():
+def parse(argv=None):
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=None,
                    help="timed steps (default: 500 for the microsecond configs 1-2, else 50)")
     p.add_argument("--warmup", type=int, default=None, help="untimed steps (default: 50 for configs 1-2, else 10)")
-    p.add_argument("--config", type=int, default=2, choices=sorted(WORKLOADS))
+    p.add_argument("--config", type=int, default=3, choices=sorted(WORKLOADS))
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-extra", action="store_true",
+                   help="config 3: skip the config-2 and config-5 timings under `extra`")
     p.add_argument("--cpu-threads", type=int, default=0, help="0 = all host cores")
     p.add_argument("--copy-calibration-mib", type=int, default=0,
                    help="first run one plain device copy of this many MiB (scale for rocprofv3 FETCH/WRITE_SIZE)")
-    args = p.parse_args()
+    args = p.parse_args(argv)
     # A config-2 step is ~80 us: 500 of them time 40 ms of steady-state work
     # (50 took 4 ms, short enough for the clock ramp to show).
     short = args.config in (1, 2)
@@ -81,29 +93,78 @@ def bytes_alg(n_src, n_dst, nnz, F):
     return 4.0 * F * (n_src + n_dst) + 8.0 * nnz + 4.0 * (n_dst + 1)
 
 
-def cpu_baseline(rows, cols, vals, X, n, threads, Y_gpu, max_nnz):
+def roofline(flops, b_alg, ms, traffic, kernel):
+    """BASELINE.md's roofline: AI = flops / algorithmic bytes, roof =
+    min(fp32 peak, AI * HBM peak).  `achieved` is the step's rate in the
+    binding roof's unit, so frac = achieved / peak = (flops/t) / roof.
+    `traffic` is the counter-measured HBM bytes of the step's kernels."""
+    t = ms * 1e-3
+    ai = flops / b_alg
+    if FP32_PEAK_TFLOPS * 1e12 <= ai * HBM_PEAK_GBPS * 1e9:
+        bound, achieved, peak, unit = "mfma", flops / t / 1e12, FP32_PEAK_TFLOPS, "TFLOP/s"
+    else:
+        bound, achieved, peak, unit = "hbm", b_alg / t / 1e9, HBM_PEAK_GBPS, "GB/s"
+    r = {"bound": bound, "achieved": round(achieved, 4), "peak": peak, "unit": unit, "frac": round(achieved / peak, 4),
+         "traffic": None if traffic is None else traffic["hbm_bytes_per_launch"], "kernel": kernel,
+         "arith_intensity": round(ai, 3), "bytes_alg_per_launch": b_alg, "flops_per_launch": flops,
+         "roof": "min(157.3 TFLOP/s fp32, AI x 8 TB/s) (BASELINE.md)"}
+    if bound == "mfma":
+        r["fp32"] = "fp32 FMA/MFMA peak 157.3 TFLOP/s; the kernels contract on the VALU (fp32 FMA)"
+    if traffic is not None:
+        gbps = traffic["hbm_bytes_per_launch"] / t / 1e9
+        r["dram"] = {"GBps": round(gbps, 1), "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),
+                     "north_star_target_frac": NORTH_STAR_DRAM_FRAC, "source": traffic["file"],
+                     "what": "rocprofv3 FETCH_SIZE + WRITE_SIZE of the step's kernels (scaled by a 1 GiB copy) "
+                             "over this run's event-timed step"}
+    return r
+
+
+def _sha16(path):
+    with open(os.path.join(ROOT, path), "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()[:16]
+
+
+def traffic_of(config):
+    """Counter-measured HBM bytes per step from profiles/traffic_config<N>.json,
+    only when the kernel sources it was measured on are the ones built now."""
+    name = f"profiles/traffic_config{config}.json"
+    path = os.path.join(ROOT, name)
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        d = json.load(f)
+    srcs = d.get("sources")
+    if not srcs or any(_sha16(p) != h for p, h in srcs.items()):
+        return None  # measured on other kernel sources
+    return {"hbm_bytes_per_launch": d["hbm_bytes_per_launch"], "file": name}
+
+
+def csr_sample(rows, cols, vals, n, max_nnz):
+    """The leading rows of the matrix holding at most max_nnz nonzeros (the
+    whole matrix when it is smaller), as CSR numpy arrays."""
+    import numpy as np
+
+    from tcc_amd.graphs import to_csr_numpy
+
+    rowptr, colind, v = to_csr_numpy(rows, cols, n, vals)
+    R = max(1, min(n, int(np.searchsorted(rowptr, max_nnz, side="right")) - 1))
+    nz = int(rowptr[R])
+    return (R, nz, np.ascontiguousarray(rowptr[: R + 1]), np.ascontiguousarray(colind[:nz]),
+            None if v is None else np.ascontiguousarray(v[:nz]))
+
+
+def oracle_cpu(sample, X, threads, Y_gpu):
     """The oracle's CSR SpMM (OpenMP, fp64 accumulation of TF32-rounded
-    inputs) on the host cores over the leading rows holding at most max_nnz
-    nonzeros (the whole matrix when it is smaller): median of 5 after 1
-    warm-up.  Also the parity check of the GPU result on those rows (rel-L2).
-    Returns (seconds, threads, rel_l2, rows, nnz) of the sample."""
+    inputs) over the sample: median of 5 after 1 warm-up; also the parity
+    check of the GPU result on those rows (rel-L2)."""
     import numpy as np
 
     import oracle
-    from tcc_amd.graphs import to_csr_numpy
 
-    threads = threads or os.cpu_count() or 1
-    rowptr, colind, v = to_csr_numpy(rows, cols, n, vals)
-    R = int(np.searchsorted(rowptr, max_nnz, side="right")) - 1
-    R = max(1, min(n, R))
-    nz = int(rowptr[R])
-    rp = np.ascontiguousarray(rowptr[: R + 1])
-    ci = np.ascontiguousarray(colind[:nz])
-    vv = None if v is None else np.ascontiguousarray(v[:nz])
+    R, nz, rp, ci, vv = sample
     Xc = X.cpu().numpy()
     oracle.csr_spmm(rp, ci, vv, Xc, use_tf32=True, threads=threads)
-    ts = []
-    Y = None
+    ts, Y = [], None
     for _ in range(5):
         t0 = time.perf_counter()
         Y = oracle.csr_spmm(rp, ci, vv, Xc, use_tf32=True, threads=threads)
@@ -111,27 +172,25 @@ def cpu_baseline(rows, cols, vals, X, n, threads, Y_gpu, max_nnz):
     t = sorted(ts)[len(ts) // 2]
     yg = Y_gpu[:R].cpu().numpy().astype(np.float64)
     rel = float(np.linalg.norm(yg - Y) / max(np.linalg.norm(Y), 1e-30))
-    return t, threads, rel, R, nz
+    F = X.shape[1]
+    return {"value": round(2.0 * nz * F / t / 1e9, 3), "unit": "GFLOP/s", "cores": threads, "ms": round(t * 1e3, 3),
+            "what": "oracle CSR SpMM (fp64 accumulation of TF32-rounded inputs, OpenMP over rows), same sample, "
+                    "median of 5 after 1 warm-up"}, rel
 
 
-def torch_sparse_cpu(rows, cols, vals, X, n, threads, max_nnz):
+def torch_sparse_cpu(sample, X, n, threads):
     """The reference's own SpMM call, torch.sparse.mm (train/tcgnn_conv_release.py:152),
-    on the host cores in fp32 with a CSR tensor, over the same leading-rows
-    sample as cpu_baseline: median of 5 after 1 warm-up."""
+    on the host cores in fp32 with a CSR tensor over the sample: median of 5
+    after 1 warm-up.  Returns seconds."""
     import numpy as np
     import torch
 
-    from tcc_amd.graphs import to_csr_numpy
-
-    threads = threads or os.cpu_count() or 1
-    rowptr, colind, v = to_csr_numpy(rows, cols, n, vals)
-    R = max(1, min(n, int(np.searchsorted(rowptr, max_nnz, side="right")) - 1))
-    nz = int(rowptr[R])
-    vv = np.ones(nz, np.float32) if v is None else np.asarray(v[:nz], np.float32)
+    R, nz, rp, ci, vv = sample
+    vv = np.ones(nz, np.float32) if vv is None else np.asarray(vv, np.float32)
     with warnings.catch_warnings():
         warnings.simplefilter("ignore")  # "sparse CSR support is in beta"
-        A = torch.sparse_csr_tensor(torch.from_numpy(rowptr[: R + 1].astype(np.int64)),
-                                    torch.from_numpy(colind[:nz].astype(np.int64)), torch.from_numpy(vv), size=(R, n))
+        A = torch.sparse_csr_tensor(torch.from_numpy(rp.astype(np.int64)), torch.from_numpy(ci.astype(np.int64)),
+                                    torch.from_numpy(vv), size=(R, n))
     Xc = X.cpu()
     prev = torch.get_num_threads()
     torch.set_num_threads(threads)
@@ -144,10 +203,28 @@ def torch_sparse_cpu(rows, cols, vals, X, n, threads, max_nnz):
             ts.append(time.perf_counter() - t0)
     finally:
         torch.set_num_threads(prev)
-    t = sorted(ts)[len(ts) // 2]
-    return {"value": round(2.0 * nz * X.shape[1] / t / 1e9, 3), "unit": "GFLOP/s", "cores": threads,
-            "ms": round(t * 1e3, 3), "nnz": nz,
-            "what": "torch.sparse.mm (CSR, fp32) on the host cores, the reference's own SpMM call, same sample"}
+    return sorted(ts)[len(ts) // 2]
+
+
+def cpu_baselines(args, rows, cols, vals, X, n, Y_gpu, config, extra):
+    """cpu_baseline = torch.sparse.mm over the sample; the oracle loop and
+    the parity of the GPU result on the sample go to `extra`."""
+    threads = args.cpu_threads or os.cpu_count() or 1
+    sample = csr_sample(rows, cols, vals, n, CPU_SAMPLE_NNZ)
+    R, nz = sample[0], sample[1]
+    nnz, F = rows.numel(), X.shape[1]
+    t = torch_sparse_cpu(sample, X, n, threads)
+    what = (f"whole config-{config} matrix ({nnz} nnz, F={F})" if nz == nnz else
+            f"rows 0..{R - 1} of config {config} ({nz} of {nnz} nnz, F={F})")
+    cpu = {"value": round(2.0 * nz * F / t / 1e9, 3), "unit": "GFLOP/s", "cores": threads, "kind": "reference",
+           "sample": f"{what}; torch.sparse.mm (CSR, fp32), the reference's own SpMM call "
+                     f"(train/tcgnn_conv_release.py:152), median of 5 after 1 warm-up",
+           "ms": round(t * 1e3, 3)}
+    o, rel = oracle_cpu(sample, X, threads, Y_gpu)
+    extra["cpu_oracle"] = o
+    extra["parity_rel_l2_vs_oracle"] = rel
+    extra["parity_rows"] = R
+    return cpu
 
 
 def timed(step, steps, warmup):
@@ -180,30 +257,13 @@ def copy_calibration(mib):
     del a_src, a_dst
 
 
-def traffic_of(config):
-    tf = os.path.join(ROOT, "profiles", f"traffic_config{config}.json")
-    if os.path.exists(tf):
-        with open(tf) as f:
-            return json.load(f).get("hbm_bytes_per_launch")
-    return None
-
-
-def line_for(args, value, unit, ms, dtype, config, roofline, cpu, extra, higher=True):
+def line_for(args, value, unit, ms, dtype, config, roof, cpu, extra, higher=True):
     return {
         "metric": METRIC, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms, 5), "higher_is_better": higher, "scaling": "weak", "vs_baseline": None,
         "dtype": dtype, "data": "synthetic (seeded generator, see tcc_amd/graphs.py)", "config": config,
-        "roofline": roofline, "cpu_baseline": cpu, "extra": extra,
+        "roofline": roof, "cpu_baseline": cpu, "extra": extra,
     }
-
-
-def cpu_entry(t_cpu, threads, nz, nnz, R, F, config):
-    what = (f"whole config-{config} matrix ({nnz} nnz, F={F})" if nz == nnz else
-            f"rows 0..{R - 1} of config {config} ({nz} of {nnz} nnz, F={F})")
-    return {"value": round(2.0 * nz * F / t_cpu / 1e9, 3), "unit": "GFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"{what}; oracle CSR SpMM, fp64 accumulation of TF32-rounded inputs, OpenMP over rows, "
-                      f"median of 5 after 1 warm-up",
-            "ms": round(t_cpu * 1e3, 3)}
 
 
 def swtcf_timings(torch, swtcf, m, X, n, nnz, F):
@@ -307,8 +367,6 @@ def bench_spmm(args, torch, swtcf, cfg):
         copy_calibration(args.copy_calibration_mib)
     ms = timed(step, args.steps, args.warmup)
     flops = 2.0 * nnz * F
-    b_alg = bytes_alg(n, n, nnz, F)
-    achieved = b_alg / (ms * 1e-3) / 1e9
     if args.config == 1:
         torch.cuda.synchronize()
         Y.zero_()
@@ -316,16 +374,10 @@ def bench_spmm(args, torch, swtcf, cfg):
     torch.cuda.synchronize()
     cpu = None
     if not args.no_cpu_baseline:
-        t_cpu, threads, rel, R, nz = cpu_baseline(rows, cols, vals, X, n, args.cpu_threads, Y, 16_000_000)
-        cpu = cpu_entry(t_cpu, threads, nz, nnz, R, F, args.config)
-        extra["parity_rel_l2_vs_cpu"] = rel
-        extra["parity_rows"] = R
-        extra["cpu_torch_sparse_mm"] = torch_sparse_cpu(rows, cols, vals, X, n, args.cpu_threads, 16_000_000)
-    roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic_of(args.config), "kernel": kernel,
-                "bytes_alg_per_launch": b_alg}
+        cpu = cpu_baselines(args, rows, cols, vals, X, n, Y, args.config, extra)
+    roof = roofline(flops, bytes_alg(n, n, nnz, F), ms, traffic_of(args.config), kernel)
     config = {"workload": WORKLOADS[args.config], "n": n, "nnz": nnz, "F": F}
-    return line_for(args, round(flops / (ms * 1e-3) / 1e9, 3), "GFLOP/s", ms, "fp32", config, roofline, cpu, extra)
+    return line_for(args, round(flops / (ms * 1e-3) / 1e9, 3), "GFLOP/s", ms, "fp32", config, roof, cpu, extra)
 
 
 def gcn_inputs(torch, cfg):
@@ -397,38 +449,36 @@ def bench_mixed(args, torch, swtcf, cfg):
     extra["packed_rows"] = packed_rows_step(torch, table, X, cols, g1, F, Y, cold_rows_used, args)
     cpu = None
     if not args.no_cpu_baseline:
-        t_cpu, threads, rel, R, nz = cpu_baseline(rows, cols, None, X, n, args.cpu_threads, Y, 16_000_000)
-        cpu = cpu_entry(t_cpu, threads, nz, nnz, R, F, 4)
-        extra["parity_rel_l2_vs_cpu"] = rel
-        extra["parity_rows"] = R
-        extra["cpu_torch_sparse_mm"] = torch_sparse_cpu(rows, cols, None, X, n, args.cpu_threads, 16_000_000)
+        cpu = cpu_baselines(args, rows, cols, None, X, n, Y, 4, extra)
     # One launch (mixed_forward_kernel) interleaves the HBM-bound hot gather
     # with the scatter of cold rows read across the host link; the link bounds
     # it: the cold rows' bytes over PCIe Gen5 x16 (64 GB/s per direction).
     b_alg = bytes_alg(n, n, nnz, F)
     hbm_achieved = b_alg / (ms * 1e-3) / 1e9
     link_achieved = cold_bytes / (ms * 1e-3) / 1e9
-    roofline = {"bound": "host_link", "achieved": round(link_achieved, 2), "peak": PCIE_PEAK_GBPS, "unit": "GB/s",
-                "frac": round(link_achieved / PCIE_PEAK_GBPS, 4), "traffic": None,
-                "kernel": "mixed_forward_kernel (gather_body<Mixed> + scatter_body<Mixed>)",
-                "bytes_alg_per_launch": cold_bytes,
-                "hbm": {"achieved": round(hbm_achieved, 2), "peak": HBM_PEAK_GBPS,
-                        "frac": round(hbm_achieved / HBM_PEAK_GBPS, 4), "bytes_alg_per_launch": b_alg}}
+    traffic = traffic_of(4)
+    roof = {"bound": "host_link", "achieved": round(link_achieved, 2), "peak": PCIE_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(link_achieved / PCIE_PEAK_GBPS, 4),
+            "traffic": None if traffic is None else traffic["hbm_bytes_per_launch"],
+            "kernel": "mixed_forward_kernel (gather_body<Mixed> + scatter_body<Mixed>)",
+            "bytes_alg_per_launch": cold_bytes,
+            "hbm": {"achieved": round(hbm_achieved, 2), "peak": HBM_PEAK_GBPS,
+                    "frac": round(hbm_achieved / HBM_PEAK_GBPS, 4), "bytes_alg_per_launch": b_alg}}
     config = {"workload": WORKLOADS[4], "n": n, "nnz": nnz, "F": F}
     table.free()
-    return line_for(args, round(2.0 * nnz * F / (ms * 1e-3) / 1e9, 3), "GFLOP/s", ms, "fp32", config, roofline,
+    return line_for(args, round(2.0 * nnz * F / (ms * 1e-3) / 1e9, 3), "GFLOP/s", ms, "fp32", config, roof,
                     cpu, extra)
 
 
-def bench_gcn(args, torch, swtcf, cfg):
-    """Config 5: one full-graph GCN training epoch per step, plus each
-    layer's forward+backward time."""
+def gcn_timings(args, torch, cfg):
+    """Config 5: one full-graph GCN training epoch per step (at most 10 timed
+    after 3), each layer's forward+backward alone, and the epoch over packed
+    TF32 feature rows.  Returns (epoch ms, steps, warmup, extra)."""
     from tcc_amd import gcn
 
     n, F = cfg["n"], cfg["F"]
     hidden, classes = 256, 2
     rows, cols, X, table, g1, g2 = gcn_inputs(torch, cfg)
-    nnz = rows.numel()
     torch.manual_seed(cfg["seed"])
     model = gcn.GCN(F, hidden, classes, dropout=0.0).cuda()
     labels = gcn.synthetic_labels(n, classes, cfg["seed"])
@@ -474,11 +524,40 @@ def bench_gcn(args, torch, swtcf, cfg):
              "layer2": f"A(XW): GEMM {hidden}x{classes}, BCSR SpMM F={classes}; backward A^T SpMM F={classes}, "
                        f"dW and dX GEMMs",
              "loss_first": first_loss, "loss_last": last_loss}
-    config = {"workload": WORKLOADS[5], "n": n, "nnz": nnz, "F": F, "hidden": hidden, "classes": classes}
     table.free()
+    return ms, steps, warmup, extra, rows.numel()
+
+
+def bench_gcn(args, torch, swtcf, cfg):
+    n, F = cfg["n"], cfg["F"]
+    ms, steps, warmup, extra, nnz = gcn_timings(args, torch, cfg)
+    config = {"workload": WORKLOADS[5], "n": n, "nnz": nnz, "F": F, "hidden": 256, "classes": 2}
     line = line_for(args, round(ms, 4), "ms", ms, "fp32", config, None, None, extra, higher=False)
     line["steps"], line["warmup"] = steps, warmup
     return line
+
+
+def extra_configs(args, torch, swtcf):
+    """Config 2's step and config 5's epoch and layer times, for the config-3
+    line's `extra` (each with its own default step counts)."""
+    from tcc_amd.graphs import CONFIGS
+
+    out = {}
+    a2 = copy.copy(args)
+    a2.config, a2.steps, a2.warmup, a2.no_cpu_baseline, a2.copy_calibration_mib = 2, 500, 50, True, 0
+    l2 = bench_spmm(a2, torch, swtcf, CONFIGS[2])
+    out["config2"] = {"workload": WORKLOADS[2], "ms_per_step": l2["ms_per_step"], "GFLOPs": l2["value"],
+                      "steps": 500, "warmup": 50, "roofline": l2["roofline"], "path": l2["extra"].get("path"),
+                      "convert_ms": l2["extra"].get("convert_ms"), "swtcf": l2["extra"].get("swtcf")}
+    torch.cuda.empty_cache()
+    a5 = copy.copy(args)
+    a5.config, a5.steps, a5.warmup = 5, 10, 3
+    ms, steps, warmup, e5, _ = gcn_timings(a5, torch, CONFIGS[5])
+    out["config5"] = {"workload": WORKLOADS[5], "epoch_ms": round(ms, 4), "steps": steps, "warmup": warmup,
+                      "layer1_fwd_bwd_ms": e5["layer1_fwd_bwd_ms"], "layer2_fwd_bwd_ms": e5["layer2_fwd_bwd_ms"],
+                      "epoch_ms_packed_feature_rows": e5["epoch_ms_packed_feature_rows"],
+                      "loss_first": e5["loss_first"], "loss_last": e5["loss_last"], "epoch": e5["epoch"]}
+    return out
 
 
 def main():
@@ -501,6 +580,9 @@ def main():
         line = bench_mixed(args, torch, swtcf, cfg)
     else:
         line = bench_gcn(args, torch, swtcf, cfg)
+    if args.config == 3 and not args.no_extra:
+        torch.cuda.empty_cache()
+        line["extra"].update(extra_configs(args, torch, swtcf))
     print(json.dumps(line), flush=True)
     return 0
 
