@@ -85,10 +85,14 @@ typedef struct tcc_bcsc {
  * g >= 0: hot row (g % cap) of gpu_feature_cache[g / gpu_node_capacity]
  * (device memory); g < 0: cold row id_map[j] of cpu_features, a device
  * pointer to mapped pinned host memory read zero-copy; id_map[j] < 0 reads
- * zeros.  Two bounds the reference does not check keep bad map values from
- * reading outside the tables: a cache index g / cap >= gpu_feature_cache_count
- * (when nonzero) and a host row past cpu_feature_len features (when > 0)
- * read zeros.  On one GPU the pointer table has one entry.
+ * zeros.  The reference checks neither table bound and reads outside the
+ * tables on bad map values; here three lookups are refused instead: a cache
+ * index g / cap >= gpu_feature_cache_count (when nonzero), a host row past
+ * cpu_feature_len features (when > 0), and a cold row when cpu_features is
+ * NULL.  A refused lookup reads zeros and, when device_error is set, writes
+ * TCC_DEVERR_FEATURE_INDEX there (device memory, read by the caller after
+ * synchronising; it is never cleared by the kernels).  On one GPU the
+ * pointer table has one entry.
  * Rows are F floats (row_format TCC_ROWS_FP32, the reference's layout) or,
  * with TCC_ROWS_TF32_PACKED (no reference counterpart), TF32 rows packed by
  * tcc_tf32_pack (tcc_tf32_packed_bytes(1, F) bytes each, tables 16-byte
@@ -97,6 +101,7 @@ typedef struct tcc_bcsc {
  * bytes per feature -- across PCIe for the cold rows. */
 #define TCC_ROWS_FP32 0u
 #define TCC_ROWS_TF32_PACKED 1u
+#define TCC_DEVERR_FEATURE_INDEX 7u /* a feature lookup outside its table (read as zeros) */
 
 typedef struct tcc_feature_source {
     const int32_t* id_map;           /* device [num_cols] */
@@ -107,6 +112,7 @@ typedef struct tcc_feature_source {
     int64_t cpu_feature_len;         /* features (rows x F) available at cpu_features (<= 0: unchecked) */
     uint32_t gpu_feature_cache_count; /* entries of gpu_feature_cache (0: unchecked) */
     uint32_t row_format;             /* TCC_ROWS_FP32 (0) or TCC_ROWS_TF32_PACKED */
+    uint32_t* device_error;          /* device [1] or NULL: TCC_DEVERR_FEATURE_INDEX on a refused lookup */
 } tcc_feature_source;
 
 /* Y[row-window rows x F] (=, or += when accumulate != 0) A_bcsr * X.
@@ -198,6 +204,60 @@ int tcc_coo_to_bcsr_phased(const uint32_t* dRow, const uint32_t* dCol, const flo
                            uint32_t numRows, uint32_t numCols, uint32_t phases, tcc_bcsr* out,
                            void** allocation, void* stream);
 int tcc_block_release(void* allocation);
+
+/* ---- row super-window BCSR (no reference counterpart) ----
+ * The product tf32_spmm_bcsr computes (spmm_dispatcher.cu:167-232), laid out
+ * for graphs whose rows share columns unevenly (R-MAT hubs).  Rows are
+ * ordered by degree (descending, ties by row id) and cut into super-windows
+ * of 64 rows (8 row windows of 8); rowOrder[64*g + s] is the original row of
+ * slot s of super-window g (0xFFFFFFFF past num_rows).  Super-window g lists
+ * its distinct source columns in pairs [groupOffset[g], groupOffset[g+1]),
+ * ordered by the columns' degree rank (descending degree, ties by id):
+ * pairCol[p] is the column (row of X) and pairMask[p] bit 8w+r says that row
+ * r of window w uses it.  With values, the pair's values follow in mask-bit
+ * order from data[pairValue[p]].  The SpMM fetches each column's feature row
+ * once per pair and shares it among the super-window's 8 row windows through
+ * LDS, where the ordinary BCSR fetches it once per (window, column).
+ * Work is cut into units of at most unit_pairs consecutive pairs of one
+ * super-window: units[3u], units[3u+1], units[3u+2] = super-window, first
+ * pair, end pair.  With num_phases P > 1 the column ranks are cut into P
+ * ranges holding about equal numbers of pairs, units do not cross a range,
+ * and units are listed range first (then by super-window): the workgroups
+ * in flight together read the feature rows of one range, which the L2 then
+ * holds.  A super-window with more than one unit receives its units'
+ * partial sums with fp32 atomics.  Products are the forward products' (TF32
+ * X and values, fp32 accumulation) and land in the original row order. */
+typedef struct tcc_sw_bcsr {
+    uint32_t num_rows;
+    uint32_t num_cols;
+    uint32_t nnz;
+    uint32_t num_groups;          /* super-windows: ceil(num_rows / 64) */
+    uint32_t num_pairs;           /* (super-window, column) pairs */
+    uint32_t num_units;
+    uint32_t unit_pairs;          /* pairs per unit (at most) */
+    uint32_t num_phases;          /* column-rank ranges the units are ordered by (1 = none) */
+    const uint32_t* rowOrder;     /* [64*num_groups] */
+    const uint32_t* groupOffset;  /* [num_groups+1] */
+    const uint32_t* pairCol;      /* [num_pairs] */
+    const uint64_t* pairMask;     /* [num_pairs] */
+    const uint32_t* pairValue;    /* [num_pairs] offset of the pair's first value in data */
+    const float* data;            /* [nnz] or NULL (all ones) */
+    const uint32_t* units;        /* [3*num_units] */
+} tcc_sw_bcsr;
+
+/* Build the super-window BCSR of a device COO (row = destination, col =
+ * source, no duplicate pairs; dVal may be NULL).  unitPairs = 0 takes 2048;
+ * phases 0 or 1 = none, at most 16.  Synchronises `stream`; one device
+ * allocation returned in *allocation (free with tcc_block_release). */
+int tcc_coo_to_sw_bcsr(const uint32_t* dRow, const uint32_t* dCol, const float* dVal, uint32_t nnz,
+                       uint32_t numRows, uint32_t numCols, uint32_t unitPairs, uint32_t phases,
+                       tcc_sw_bcsr* out, void** allocation, void* stream);
+
+/* Y[num_rows x F] (=, or += when accumulate != 0) A * X with X given packed
+ * by tcc_tf32_pack (num_cols rows, 16-byte aligned).  Every row of Y is
+ * written (rows without entries get zeros unless accumulating). */
+int tcc_sw_bcsr_spmm_packed(const tcc_sw_bcsr* A, const void* packedX, float* Y, uint32_t featureDim,
+                            int accumulate, void* stream);
 
 #ifdef __cplusplus
 }

@@ -65,9 +65,30 @@ typedef struct {
     uint32_t lc;  /* src & 7 */
 } edge_t;
 
-static int cmp_edge(const void* a, const void* b) {
-    uint64_t x = ((const edge_t*)a)->key, y = ((const edge_t*)b)->key;
-    return x < y ? -1 : (x > y ? 1 : 0);
+/* Stable LSD radix sort of edges by key, 8 bits per pass, as the
+ * reference's CUB SortPairs over bits 0-64 (swtcf_convert.cu:1951-1966);
+ * passes whose byte is the same for every key are skipped.  Stable, so
+ * equal keys keep their input order. */
+static void sort_edges(edge_t* e, uint32_t n) {
+    if (n < 2) return;
+    edge_t* tmp = (edge_t*)malloc(sizeof(edge_t) * (size_t)n);
+    edge_t* src = e;
+    edge_t* dst = tmp;
+    for (int shift = 0; shift < 64; shift += 8) {
+        size_t count[257] = {0};
+        for (uint32_t i = 0; i < n; ++i) count[((src[i].key >> shift) & 0xFFu) + 1]++;
+        int single = 0;
+        for (int d = 0; d < 256; ++d)
+            if (count[d + 1] == n) single = 1;
+        if (single) continue;
+        for (int d = 0; d < 256; ++d) count[d + 1] += count[d];
+        for (uint32_t i = 0; i < n; ++i) dst[count[(src[i].key >> shift) & 0xFFu]++] = src[i];
+        edge_t* t = src;
+        src = dst;
+        dst = t;
+    }
+    if (src != e) memcpy(e, src, sizeof(edge_t) * (size_t)n);
+    free(tmp);
 }
 
 typedef struct {
@@ -114,7 +135,7 @@ int oracle_swtcf_convert(const uint32_t* dst, const uint32_t* src, uint32_t E, u
         edges[e].key = ((uint64_t)(src[e] >> 3) << 32) | dst[e];
         edges[e].lc = src[e] & 7u;
     }
-    qsort(edges, E, sizeof(edge_t), cmp_edge);
+    sort_edges(edges, E);
     group_t* groups = (group_t*)malloc(sizeof(group_t) * (size_t)(E ? E : 1));
     uint32_t G = 0;
     for (uint32_t e = 0; e < E;) {

@@ -54,10 +54,20 @@ class BCSC(ctypes.Structure):
     ]
 
 
+class SWBCSR(ctypes.Structure):
+    """tcc_sw_bcsr: the row super-window BCSR (no reference counterpart)."""
+    _fields_ = [
+        ("num_rows", u32), ("num_cols", u32), ("nnz", u32), ("num_groups", u32), ("num_pairs", u32),
+        ("num_units", u32), ("unit_pairs", u32), ("num_phases", u32), ("rowOrder", vp), ("groupOffset", vp), ("pairCol", vp),
+        ("pairMask", vp), ("pairValue", vp), ("data", vp), ("units", vp),
+    ]
+
+
 class FeatureSource(ctypes.Structure):
     _fields_ = [
         ("id_map", vp), ("cache_search_map", vp), ("gpu_feature_cache", vp), ("gpu_node_capacity", i32),
         ("cpu_features", vp), ("cpu_feature_len", i64), ("gpu_feature_cache_count", u32), ("row_format", u32),
+        ("device_error", vp),
     ]
 
 
@@ -89,6 +99,9 @@ SIGNATURES = {
     "tcc_tf32_packed_bytes": (ctypes.c_size_t, [u32, u32]),
     "tcc_tf32_pack": (ctypes.c_int, [vp, u32, u32, vp, vp]),
     "tcc_bcsr_spmm_packed": (ctypes.c_int, [ctypes.POINTER(BCSR), vp, vp, u32, ctypes.c_int, vp]),
+    "tcc_coo_to_sw_bcsr": (ctypes.c_int, [vp, vp, vp, u32, u32, u32, u32, u32, ctypes.POINTER(SWBCSR),
+                                          ctypes.POINTER(vp), vp]),
+    "tcc_sw_bcsr_spmm_packed": (ctypes.c_int, [ctypes.POINTER(SWBCSR), vp, vp, u32, ctypes.c_int, vp]),
     "tcc_dense_tn_workspace_bytes": (ctypes.c_size_t, [u32, u32, u32]),
     "tcc_dense_tn": (ctypes.c_int, [vp, u32, vp, u32, vp, u32, u32, u32, u32, ctypes.c_int, vp, ctypes.c_size_t, vp]),
     "tcc_gcn_relu_forward": (ctypes.c_int, [vp, u32, vp, vp, vp, u32, vp, u32, u32, u32, u32, u32, vp]),

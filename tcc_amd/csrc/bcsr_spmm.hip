@@ -56,6 +56,7 @@ struct MixedArgs {
     std::int64_t cpuLen;
     std::uint32_t gpuCacheCount;
     std::uint64_t rowBytes;  // 0: rows of F floats; else packed TF32 rows of this stride
+    std::uint32_t* deviceError;  // receives TCC_DEVERR_FEATURE_INDEX on a refused lookup (or nullptr)
 };
 
 struct GatherArgs {
@@ -88,24 +89,31 @@ struct GatherArgs {
 };
 
 // Feature row of column `in` for the first-layer (mixed) form
-// (spmm_kernel.cu:129-153), or nullptr for a zero row.  Indices outside the
-// pointer table or past the host rows read zeros instead of faulting.
+// (spmm_kernel.cu:129-153), or nullptr for a zero row: id_map < 0 (a column
+// without a feature row), or a lookup outside its table, which is refused
+// (read as zeros, and recorded in deviceError) instead of faulting.
 __device__ __forceinline__ const float* table_row(const float* base, std::uint64_t rowBytes, std::uint32_t F,
                                                   std::int64_t r) {
     if (rowBytes == 0) return base + r * F;
     return reinterpret_cast<const float*>(reinterpret_cast<const unsigned char*>(base) + r * rowBytes);
 }
 
+__device__ __forceinline__ const float* refused(const MixedArgs& m) {
+    if (m.deviceError) atomicOr(m.deviceError, TCC_DEVERR_FEATURE_INDEX);
+    return nullptr;
+}
+
 __device__ __forceinline__ const float* mixed_row(const MixedArgs& m, std::uint32_t F, std::uint32_t in) {
     const std::int32_t g = m.cacheSearchMap[in];
     if (g >= 0) {
         const std::int32_t d = g / m.gpuNodeCapacity;
-        if (m.gpuCacheCount != 0 && static_cast<std::uint32_t>(d) >= m.gpuCacheCount) return nullptr;
+        if (m.gpuCacheCount != 0 && static_cast<std::uint32_t>(d) >= m.gpuCacheCount) return refused(m);
         return table_row(m.gpuCache[d], m.rowBytes, F, g % m.gpuNodeCapacity);
     }
     const std::int32_t id = m.idMap[in];
-    if (id < 0 || m.cpuFeatures == nullptr) return nullptr;
-    if (m.cpuLen > 0 && (static_cast<std::int64_t>(id) + 1) * F > m.cpuLen) return nullptr;
+    if (id < 0) return nullptr;
+    if (m.cpuFeatures == nullptr) return refused(m);
+    if (m.cpuLen > 0 && (static_cast<std::int64_t>(id) + 1) * F > m.cpuLen) return refused(m);
     return table_row(m.cpuFeatures, m.rowBytes, F, id);
 }
 
@@ -1251,6 +1259,7 @@ MixedArgs mixed_args(const tcc_feature_source* src, std::uint32_t F) {
     m.cpuFeatures = src->cpu_features;
     m.cpuLen = src->cpu_feature_len;
     m.gpuCacheCount = src->gpu_feature_cache_count;
+    m.deviceError = src->device_error;
     return m;
 }
 

@@ -73,10 +73,11 @@ __device__ __forceinline__ float tf32_rna(float x) {
 // integers (v_readlane of a pointer table) are generic to the compiler and
 // would become flat loads, which also count against the LDS/scalar wait
 // counter, so every wait for a scalar load would wait for them too.
-// T is a scalar or a clang vector type (vf2, vf4, vu2).
+// T is a scalar or a clang vector type (vf2, vf4, vu2, vu4).
 using vf2 = float __attribute__((ext_vector_type(2)));
 using vf4 = float __attribute__((ext_vector_type(4)));
 using vu2 = std::uint32_t __attribute__((ext_vector_type(2)));
+using vu4 = std::uint32_t __attribute__((ext_vector_type(4)));
 
 template <typename T>
 __device__ __forceinline__ T load_global(const void* p) {

@@ -119,9 +119,25 @@ int current_device() {
     return d;
 }
 
+// One error word per device for the feature lookups of this module's
+// products (tcc_feature_source.device_error), allocated by initialize() or
+// at the first product on the device; read and cleared by feature_error().
+std::uint32_t* g_error_word[64] = {};
+
+std::uint32_t* error_word(int device) {
+    TORCH_CHECK(device >= 0 && device < 64, "spmm_cnic: device id out of range");
+    if (g_error_word[device] == nullptr) {
+        void* p = nullptr;
+        if (hipMalloc(&p, sizeof(std::uint32_t)) != hipSuccess || hipMemset(p, 0, sizeof(std::uint32_t)) != hipSuccess)
+            throw std::runtime_error("spmm_cnic: cannot allocate the feature error word");
+        g_error_word[device] = static_cast<std::uint32_t*>(p);
+    }
+    return g_error_word[device];
+}
+
 tcc_feature_source feature_source(const torch::Tensor& id_map, py::capsule cpu_ptr,
                                   const torch::Tensor& cache_search_map, py::capsule gpu_ptr,
-                                  std::int32_t gpu_node_capacity, std::int64_t cpu_len) {
+                                  std::int32_t gpu_node_capacity) {
     TORCH_CHECK(id_map.is_cuda() && id_map.scalar_type() == torch::kInt32 && id_map.is_contiguous(),
                 "id_map must be a contiguous int32 device tensor");
     TORCH_CHECK(cache_search_map.is_cuda() && cache_search_map.scalar_type() == torch::kInt32 &&
@@ -141,8 +157,14 @@ tcc_feature_source feature_source(const torch::Tensor& id_map, py::capsule cpu_p
         throw std::runtime_error("spmm_cnic: cpu_feature_cache_ptr is not mapped pinned host memory");
     }
     s.cpu_features = static_cast<const float*>(dev);
-    s.cpu_feature_len = cpu_len;
+    // cpu_float_feature_len is accepted and ignored, as the reference's
+    // kernels ignore it (module.cu:27,75 never pass it on): its producer is
+    // outside the reference, so its unit (floats or rows) is unknown, and a
+    // bound taken in the wrong unit would refuse valid rows.  Host rows are
+    // therefore not bounds-checked in this form.
+    s.cpu_feature_len = 0;
     s.gpu_feature_cache_count = 1;  // one GPU: the clique's pointer table has a single entry
+    s.device_error = error_word(current_device());
     return s;
 }
 
@@ -164,7 +186,7 @@ torch::Tensor fwd_mixed_bound(std::uint32_t r_rows, std::uint32_t r_cols, std::u
         TORCH_CHECK(x.is_cuda() && x.is_contiguous() && x.scalar_type() == torch::kFloat32, "x must be fp32 on device");
         check(tcc_spmm_cnic_forward(&A, &B, x.data_ptr<float>(), C, F, stream_of(device_id)));
     } else {
-        const tcc_feature_source s = feature_source(id_map, cpu_ptr, csm, gpu_ptr, cap, cpu_len);
+        const tcc_feature_source s = feature_source(id_map, cpu_ptr, csm, gpu_ptr, cap);
         check(tcc_spmm_cnic_forward_mixed(&A, &B, &s, C, F, stream_of(device_id)));
     }
     return view_of(C, r_rows, F, current_device());
@@ -220,7 +242,7 @@ torch::Tensor fwd_mixed_py(std::uint32_t r_rows, std::uint32_t r_cols, std::uint
     // train/tcgnn_conv_release.py:116-122
     tcc_bcsr A = make_bcsr(r_rows, r_cols, r_nnz, r_blk, r_win, r_rwo, r_tco, r_a2b, r_bits, &r_data);
     tcc_bcsc B = make_bcsc(c_rows, c_cols, c_nnz, c_blk, c_win, c_cwo, c_tco, c_a2c, c_bits, &c_data);
-    const tcc_feature_source s = feature_source(id_map, cpu_ptr, csm, gpu_ptr, cap, cpu_len);
+    const tcc_feature_source s = feature_source(id_map, cpu_ptr, csm, gpu_ptr, cap);
     torch::Tensor out = alloc_output(r_win, F);
     void* st = stream_of(current_device());
     check(tcc_spmm_cnic_forward_mixed(&A, &B, &s, out.data_ptr<float>(), F, st));
@@ -249,6 +271,20 @@ void initialize(int device_id) {
     // module.cu:299-304; work is ordered on torch's current stream instead of
     // two private streams, so the returned tensors are safe to use at once.
     if (hipSetDevice(device_id) != hipSuccess) throw std::runtime_error("spmm_cnic: hipSetDevice failed");
+    (void)error_word(device_id);
+}
+
+// No reference counterpart: TCC_DEVERR_FEATURE_INDEX (7) if a first-layer
+// product on the device looked up a feature row outside its table (read as
+// zeros) since the last call, else 0.  Synchronises the device and clears
+// the word.
+std::uint32_t feature_error(int device_id) {
+    std::uint32_t* w = error_word(device_id);
+    std::uint32_t v = 0;
+    if (hipSetDevice(device_id) != hipSuccess || hipDeviceSynchronize() != hipSuccess ||
+        hipMemcpy(&v, w, sizeof(v), hipMemcpyDeviceToHost) != hipSuccess || hipMemset(w, 0, sizeof(v)) != hipSuccess)
+        throw std::runtime_error("spmm_cnic: cannot read the feature error word");
+    return v;
 }
 
 std::vector<py::capsule> space_malloc(int device_id, std::uint32_t denseC_size) {
@@ -316,6 +352,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("space_malloc", &space_malloc, "two zeroed denseC buffers (capsules)");
     m.def("finalize", &finalize, "free space_malloc buffers and outputs");
     m.def("freeMatC", &freeMatC, "release the outputs of the Python-caller form");
+    m.def("feature_error", &feature_error,
+          "7 (TCC_DEVERR_FEATURE_INDEX) if a feature lookup fell outside its table since the last call, else 0");
     m.def("set_use_values", &set_use_values, "read the per-block data values (default: all entries 1.0)");
     m.def("set_unit_blocks", &set_unit_blocks,
           "blocks each wave of work walks (default 0 = chosen from the block count)");

@@ -261,9 +261,16 @@ class FeatureTable:
         self.ids = torch.arange(n, dtype=torch.int32, device="cuda")
         self.csm = csm
         fmt = swtcf.ROWS_TF32_PACKED if packed else swtcf.ROWS_FP32
-        self.source = swtcf.feature_source(self.ids, csm, self.ptrs, n_hot, self.host.device_ptr, n * F, fmt)
+        self.device_error = torch.zeros(1, dtype=torch.int32, device="cuda")
+        self.source = swtcf.feature_source(self.ids, csm, self.ptrs, n_hot, self.host.device_ptr, n * F, fmt,
+                                           device_error=self.device_error)
         self.n_hot = n_hot
         self.packed = packed
+
+    def error(self) -> int:
+        """TCC_DEVERR_FEATURE_INDEX if a lookup fell outside the tables since
+        the table was made (synchronises the device), else 0."""
+        return int(self.device_error.item())
 
     def free(self) -> None:
         self.host.free()

@@ -12,12 +12,13 @@ import numpy as np
 import torch
 
 from . import _lib
-from ._lib import BCSC, BCSR, FeatureSource, SWTCFMatrix, SWTCFWorkspace, check
+from ._lib import BCSC, BCSR, SWBCSR, FeatureSource, SWTCFMatrix, SWTCFWorkspace, check
 
 INVALID_ROW_SLOT = 0xFFFFFFFF
 INVALID_CACHE_SLOT = 0xFF
 REPEAT_CACHE_SIZE = 32
 DEFAULT_TC_THRESHOLD = 12
+DEVERR_FEATURE_INDEX = 7  # TCC_DEVERR_FEATURE_INDEX
 FEATURE_DIM = 128
 
 
@@ -331,6 +332,66 @@ def bcsr_spmm_packed(A: BlockMatrix, packed: torch.Tensor, F: int, Y: torch.Tens
     return Y
 
 
+class SuperWindowBCSR:
+    """A row super-window BCSR built on the device by tcc_coo_to_sw_bcsr
+    (owns one allocation): rows in degree order, 64 per super-window, each
+    super-window's distinct columns with 64-bit row masks."""
+
+    def __init__(self, view: SWBCSR, allocation):
+        self.view = view
+        self._alloc = allocation
+
+    def release(self) -> None:
+        if self._alloc:
+            check(_lib.lib().tcc_block_release(self._alloc))
+            self._alloc = None
+
+    def __del__(self):
+        try:
+            self.release()
+        except Exception:
+            pass
+
+    def to_host(self) -> dict:
+        torch.cuda.synchronize()
+        v = self.view
+        G, P, U = v.num_groups, v.num_pairs, v.num_units
+        return {
+            "rowOrder": _download(v.rowOrder, 64 * G, np.uint32),
+            "groupOffset": _download(v.groupOffset, G + 1, np.uint32),
+            "pairCol": _download(v.pairCol, P, np.uint32),
+            "pairMask": _download(v.pairMask, P, np.uint64),
+            "pairValue": _download(v.pairValue, P, np.uint32) if v.data else None,
+            "data": _download(v.data, v.nnz, np.float32) if v.data else None,
+            "units": _download(v.units, 3 * U, np.uint32).reshape(U, 3),
+            "num_rows": v.num_rows, "num_cols": v.num_cols, "nnz": v.nnz, "num_groups": G, "num_pairs": P,
+            "num_units": U, "unit_pairs": v.unit_pairs, "num_phases": v.num_phases,
+        }
+
+
+def coo_to_sw_bcsr(row: torch.Tensor, col: torch.Tensor, val: torch.Tensor | None, num_rows: int, num_cols: int,
+                   unit_pairs: int = 0, phases: int = 1, stream=None) -> SuperWindowBCSR:
+    """The row super-window BCSR of the COO matrix (tcc_coo_to_sw_bcsr)."""
+    view = SWBCSR()
+    alloc = ctypes.c_void_p()
+    check(_lib.lib().tcc_coo_to_sw_bcsr(_u32(row).data_ptr() if row.numel() else None,
+                                        _u32(col).data_ptr() if col.numel() else None, _ptr(val), row.numel(),
+                                        num_rows, num_cols, int(unit_pairs), int(phases), ctypes.byref(view),
+                                        ctypes.byref(alloc),
+                                        _stream(stream)))
+    return SuperWindowBCSR(view, alloc.value)
+
+
+def sw_bcsr_spmm_packed(A: SuperWindowBCSR, packed: torch.Tensor, F: int, Y: torch.Tensor | None = None,
+                        accumulate: bool = False, stream=None) -> torch.Tensor:
+    """Y[num_rows x F] (=|+=) A X with X packed by tf32_pack."""
+    if Y is None:
+        Y = torch.empty((A.view.num_rows, F), dtype=torch.float32, device=packed.device)
+    check(_lib.lib().tcc_sw_bcsr_spmm_packed(ctypes.byref(A.view), packed.data_ptr(), Y.data_ptr(), F,
+                                             int(accumulate), _stream(stream)))
+    return Y
+
+
 def bcsc_spmm(A: BlockMatrix, X: torch.Tensor, Y: torch.Tensor, stream=None) -> torch.Tensor:
     """Y[num_rows x F] += A X with atomics."""
     X = _f32(X, "X")
@@ -447,15 +508,21 @@ ROWS_TF32_PACKED = 1
 
 def feature_source(id_map: torch.Tensor, cache_search_map: torch.Tensor, gpu_cache_ptrs: torch.Tensor,
                    gpu_node_capacity: int, cpu_features_dev_ptr: int, cpu_len: int,
-                   row_format: int = ROWS_FP32) -> FeatureSourceHandle:
+                   row_format: int = ROWS_FP32, device_error: torch.Tensor | None = None) -> FeatureSourceHandle:
+    """tcc_feature_source over device tensors; `device_error` (one int32 on
+    the device, or None) receives TCC_DEVERR_FEATURE_INDEX when a lookup
+    falls outside its table."""
     for t, name in ((id_map, "id_map"), (cache_search_map, "cache_search_map")):
         if t.dtype != torch.int32 or not t.is_cuda or not t.is_contiguous():
             raise TypeError(f"{name} must be a contiguous int32 device tensor")
     if gpu_cache_ptrs.dtype != torch.int64 or not gpu_cache_ptrs.is_cuda:
         raise TypeError("gpu_cache_ptrs must be an int64 device tensor of device pointers")
+    if device_error is not None and (device_error.dtype != torch.int32 or not device_error.is_cuda):
+        raise TypeError("device_error must be an int32 device tensor")
     s = FeatureSource(id_map.data_ptr(), cache_search_map.data_ptr(), gpu_cache_ptrs.data_ptr(), gpu_node_capacity,
-                      cpu_features_dev_ptr, cpu_len, gpu_cache_ptrs.numel(), row_format)
-    return FeatureSourceHandle(s, (id_map, cache_search_map, gpu_cache_ptrs))
+                      cpu_features_dev_ptr, cpu_len, gpu_cache_ptrs.numel(), row_format,
+                      None if device_error is None else device_error.data_ptr())
+    return FeatureSourceHandle(s, (id_map, cache_search_map, gpu_cache_ptrs, device_error))
 
 
 def spmm_cnic_forward_mixed(bcsr: BlockMatrix, bcsc: BlockMatrix, src: FeatureSourceHandle, denseC: torch.Tensor,

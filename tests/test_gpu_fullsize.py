@@ -1,16 +1,25 @@
-"""Products at BASELINE.json's full sizes, through size-independent
-properties (the oracle's CSR SpMM would take minutes here).
+"""Products and conversions at BASELINE.json's full sizes.
 
-Checksum of checksums: for Y = A X, the column sums of Y satisfy
-1^T Y = (1^T A) X, so per feature f
-    sum_i Y[i, f] = sum_j c_j X[j, f],   c_j = sum_i a_ij,
-with the forward products' TF32 rounding applied to a_ij and X on the right
-(the oracle's tf32).  The left side is summed on the device in fp64; the
-right side in numpy fp64 from the COO.  A missing or doubled window or unit
-moves the checksum by ~1e-3 relative (config 2: one 31-edge window, 2e-3;
-a single edge ~7e-5); the products agree with it to 1e-8 to 3e-8.  For the transposed product (plain fp32), 1^T (A^T dY) = (A 1)^T dY.
-Config 3 also checks the 4-phase BCSR against the ordinary one, element by
-element.
+Three checks, each able to see a misrouted row:
+
+- Weighted checksum of checksums: for Y = A X and seeded random fp64 row
+  weights r, r^T Y = (r^T A) X, i.e. per feature f
+      sum_i r_i Y[i, f] = sum_j c_j X[j, f],   c_j = sum_i r_i a_ij,
+  with the forward products' TF32 rounding applied to a_ij and X on the
+  right.  The left side is formed on the device in fp64, the right side in
+  numpy fp64 from the COO.  A partial sum landing in the wrong output row
+  changes the left side by (r_i - r_k) times that sum, so the check fails on
+  a swap of two output rows (planted in a copy of the result below), not
+  only on missing data.  For the transposed product (plain fp32)
+  s^T (A^T dY) = (A s)^T dY.
+- Rows against the oracle: the fp64 CSR oracle on TF32-rounded inputs over
+  a seeded sample of output rows holding at least 1M nonzeros (the hub row
+  included), element by element at rel-L2 <= 1e-5 (north_star bound 1e-3).
+- The converter: the 114M-edge SWTCF of config 3 against the C oracle's
+  canonical form, every array bit for bit.
+
+Config 5's training step runs once at full size against a float64
+evaluation of the same formulas (scipy sparse products, fp64 GEMMs).
 """
 import numpy as np
 import pytest
@@ -18,7 +27,12 @@ import torch
 
 pytestmark = pytest.mark.gpu
 
-TOL = 1e-6  # measured 1e-8 to 3e-8; one window of 31 edges left out moves it by 2e-3
+# Weighted checksums: measured 3e-8 to 2e-7 for the forward products, 1.4e-6
+# for the F = 2 transposed product (2 sums over hub columns of ~1e5 fp32
+# terms each); a swap of two output rows moves them by 6e-3 to 3e-2.
+TOL = 1e-5
+ROW_TOL = 1e-5  # oracle rows: measured ~1e-7 (north_star bound 1e-3)
+SAMPLE_NNZ = 1_000_000
 
 
 def rel_l2(a, b):
@@ -35,80 +49,188 @@ def graph(cfg_id):
     rows, cols, vals = make_graph(cfg_id, device="cuda")
     r32 = rows.to(torch.int32).contiguous()
     c32 = cols.to(torch.int32).contiguous()
-    X = make_features(n, F, cfg_id, device="cuda")
+    X = make_features(n, F, cfg["seed"], device="cuda")
     return n, F, r32, c32, vals, X
 
 
-def column_sums(oracle, idx, vals, n, tf32):
-    v = vals.cpu().numpy().astype(np.float32)
-    if tf32:
-        v = oracle.tf32(v)
-    return np.bincount(idx.cpu().numpy().astype(np.int64), weights=v.astype(np.float64), minlength=n)
+def weights(n, seed):
+    return np.random.default_rng(seed).standard_normal(n)
 
 
-def device_checksum(Y, rows):
-    return Y[:rows].double().sum(dim=0).cpu().numpy()
+def weighted_want(oracle, rows, cols, vals, n_in, r, Xin, tf32):
+    """(r^T A) X in fp64 from the COO (rows = output index of each entry)."""
+    a = np.ones(rows.size, np.float64) if vals is None else vals.astype(np.float64)
+    if tf32 and vals is not None:
+        a = oracle.tf32(vals.astype(np.float32)).astype(np.float64)
+    c = np.bincount(cols, weights=r[rows] * a, minlength=n_in)
+    Xt = oracle.tf32(Xin) if tf32 else Xin
+    return c @ Xt.astype(np.float64)
 
 
-def test_fullsize_config2_checksums(gpu, oracle):
+def weighted_got(Y, r_dev, n):
+    return torch.mv(Y[:n].double().t(), r_dev).cpu().numpy()
+
+
+def check_weighted(oracle, Y, n, rows, cols, vals, n_in, Xin, seed, tf32=True, what=""):
+    r = weights(n, seed)
+    r_dev = torch.from_numpy(r).cuda()
+    want = weighted_want(oracle, rows, cols, vals, n_in, r, Xin, tf32)
+    e = rel_l2(weighted_got(Y, r_dev, n), want)
+    print(f"{what}: weighted checksum rel-L2 {e:.2e}", flush=True)
+    assert e <= TOL, what
+    return r_dev, want
+
+
+def check_swap_fails(Y, n, r_dev, want, i, k, what=""):
+    """A copy of Y with output rows i and k swapped fails the check (the
+    planted mistake shows what the check can see)."""
+    Z = Y[:n].clone()
+    Z[[i, k]] = Z[[k, i]]
+    e = rel_l2(weighted_got(Z, r_dev, n), want)
+    print(f"{what}: rows {i} and {k} swapped: rel-L2 {e:.2e}", flush=True)
+    assert e > 100 * TOL, what
+
+
+def sample_rows(rows_np, n, seed, min_nnz=SAMPLE_NNZ):
+    """Seeded sample of output rows holding at least min_nnz nonzeros (the
+    highest-degree row first)."""
+    deg = np.bincount(rows_np, minlength=n)
+    rng = np.random.default_rng(seed)
+    order = rng.permutation(n)
+    top = int(np.argmax(deg))
+    order = np.concatenate([[top], order[order != top]])
+    k = int(np.searchsorted(np.cumsum(deg[order]), min_nnz)) + 1
+    return np.sort(order[:k])
+
+
+def check_rows(oracle, Y, rows_np, cols_np, vals_np, n, Xin, seed, what="", tf32=True):
+    """Output rows of a seeded >= 1M-nnz sample against the CSR oracle
+    (TF32-rounded operands for the forward products, plain fp32 for A^T)."""
+    sel = sample_rows(rows_np, n, seed)
+    keep = np.isin(rows_np, sel)
+    r, c = rows_np[keep], cols_np[keep]
+    v = None if vals_np is None else vals_np[keep]
+    pos = np.searchsorted(sel, r)
+    order = np.lexsort((c, pos))
+    rowptr = np.zeros(sel.size + 1, np.int64)
+    np.cumsum(np.bincount(pos, minlength=sel.size), out=rowptr[1:])
+    want = oracle.csr_spmm(rowptr, c[order].astype(np.uint32), None if v is None else v[order], Xin, use_tf32=tf32)
+    got = Y[torch.from_numpy(sel).cuda()].cpu().numpy()
+    e = rel_l2(got, want)
+    print(f"{what}: {sel.size} rows, {int(keep.sum())} nnz against the oracle: rel-L2 {e:.2e}", flush=True)
+    assert int(keep.sum()) >= SAMPLE_NNZ
+    assert e <= ROW_TOL, what
+
+
+def test_fullsize_config2(gpu, oracle):
     from tcc_amd import swtcf
 
     n, F, r32, c32, vals, X = graph(2)
     print(f"config 2: n={n} nnz={r32.numel()} F={F}", flush=True)
+    rows, cols, v = r32.cpu().numpy(), c32.cpu().numpy(), vals.cpu().numpy()
+    Xh = X.cpu().numpy()
     A = swtcf.coo_to_bcsr(r32, c32, vals, n, n)
     Y = swtcf.bcsr_spmm(A, X)
-    c = column_sums(oracle, c32, vals, n, tf32=True)
-    Xt = oracle.tf32(X.cpu().numpy()).astype(np.float64)
-    want = c @ Xt
-    got = device_checksum(Y, n)
-    print(f"forward checksum rel-L2 {rel_l2(got, want):.2e}", flush=True)
-    assert rel_l2(got, want) <= TOL, "forward"
+    r_dev, want = check_weighted(oracle, Y, n, rows, cols, v, n, Xh, 21, what="config 2 BCSR gather")
     assert torch.count_nonzero(Y[n:]).item() == 0
-    # the check's reach: the expected side without one row window's edges
-    # (a mistake planted in the reference, not in the product) must fail it
-    rows_np = r32.cpu().numpy()
-    drop = (rows_np // 8) == 1000
-    assert drop.any()
-    vals_kept = torch.where(torch.from_numpy(drop).cuda(), torch.zeros_like(vals), vals)
-    c_drop = column_sums(oracle, c32, vals_kept, n, tf32=True)
-    miss = rel_l2(got, c_drop @ Xt)
-    print(f"one window ({int(drop.sum())} edges) left out of the reference: rel-L2 {miss:.2e}", flush=True)
-    assert miss > 100 * TOL
+    hub = int(np.argmax(np.bincount(rows, minlength=n)))
+    check_swap_fails(Y, n, r_dev, want, hub, (hub + 1) % n, what="config 2")
+    check_rows(oracle, Y, rows, cols, v, n, Xh, 22, what="config 2 BCSR gather")
 
     B = swtcf.coo_to_bcsc(r32, c32, vals, n, n)
     dY = torch.randn(n, F, device="cuda")
     dX = swtcf.bcsc_transpose_spmm(B, dY)
-    r = column_sums(oracle, r32, vals, n, tf32=False)  # row sums of A
-    wantT = r @ dY.cpu().numpy().astype(np.float64)
-    print(f"transpose checksum rel-L2 {rel_l2(device_checksum(dX, n), wantT):.2e}", flush=True)
-    assert rel_l2(device_checksum(dX, n), wantT) <= TOL, "transpose"
+    # s^T (A^T dY) = (A s)^T dY: the transposed product's output index is the column
+    check_weighted(oracle, dX, n, cols, rows, v, n, dY.cpu().numpy(), 23, tf32=False,
+                   what="config 2 transposed gather")
+    check_rows(oracle, dX, cols, rows, v, n, dY.cpu().numpy(), 24, what="config 2 transposed gather", tf32=False)
 
 
-def test_fullsize_config3_packed_phased(gpu, oracle):
+def test_fullsize_config3_bcsr(gpu, oracle):
+    """The packed gather over the ordinary and the 4-phase BCSR (the bench's
+    path), and the fp32 gather."""
     from tcc_amd import swtcf
 
     n, F, r32, c32, vals, X = graph(3)
     print(f"config 3: n={n} nnz={r32.numel()} F={F}", flush=True)
-    c = column_sums(oracle, c32, vals, n, tf32=True)
-    want = c @ oracle.tf32(X.cpu().numpy()).astype(np.float64)
+    rows, cols, v = r32.cpu().numpy(), c32.cpu().numpy(), vals.cpu().numpy()
+    Xh = X.cpu().numpy()
+    hub = int(np.argmax(np.bincount(rows, minlength=n)))
     P = swtcf.tf32_pack(X)
-    del X
     A4 = swtcf.coo_to_bcsr(r32, c32, vals, n, n, phases=4)
     Y4 = swtcf.bcsr_spmm_packed(A4, P, F)
-    print(f"4 phases: checksum rel-L2 {rel_l2(device_checksum(Y4, n), want):.2e}", flush=True)
-    assert rel_l2(device_checksum(Y4, n), want) <= TOL, "4 phases"
+    r_dev, want = check_weighted(oracle, Y4, n, rows, cols, v, n, Xh, 31, what="config 3 packed, 4 phases")
+    check_swap_fails(Y4, n, r_dev, want, hub, (hub + 7) % n, what="config 3")
+    check_rows(oracle, Y4, rows, cols, v, n, Xh, 32, what="config 3 packed, 4 phases")
     A4.release()
+    del Y4
     A1 = swtcf.coo_to_bcsr(r32, c32, vals, n, n)
     Y1 = swtcf.bcsr_spmm_packed(A1, P, F)
-    assert rel_l2(device_checksum(Y1, n), want) <= TOL, "ordinary"
-    d = ((Y4[:n].double() - Y1[:n].double()).norm() / Y1[:n].double().norm()).item()
-    print(f"phased against ordinary: rel-L2 {d:.2e}", flush=True)
-    assert d <= 1e-6, f"phased against ordinary: {d}"
+    check_weighted(oracle, Y1, n, rows, cols, v, n, Xh, 31, what="config 3 packed, ordinary")
+    del Y1, P
+    Yf = swtcf.bcsr_spmm(A1, X)
+    check_weighted(oracle, Yf, n, rows, cols, v, n, Xh, 31, what="config 3 fp32 gather")
+
+
+def test_fullsize_config3_super_window(gpu, oracle):
+    """The row super-window BCSR at config 3 (degree-sorted rows, 64-row
+    super-windows, 4 column phases)."""
+    from tcc_amd import swtcf
+
+    n, F, r32, c32, vals, X = graph(3)
+    rows, cols, v = r32.cpu().numpy(), c32.cpu().numpy(), vals.cpu().numpy()
+    Xh = X.cpu().numpy()
+    P = swtcf.tf32_pack(X)
+    S = swtcf.coo_to_sw_bcsr(r32, c32, vals, n, n, phases=4)
+    print(f"config 3 super-window BCSR: {S.view.num_pairs} pairs, {S.view.num_units} units", flush=True)
+    Y = swtcf.sw_bcsr_spmm_packed(S, P, F)
+    r_dev, want = check_weighted(oracle, Y, n, rows, cols, v, n, Xh, 33, what="config 3 super-window")
+    hub = int(np.argmax(np.bincount(rows, minlength=n)))
+    check_swap_fails(Y, n, r_dev, want, hub, (hub + 3) % n, what="config 3 super-window")
+    check_rows(oracle, Y, rows, cols, v, n, Xh, 34, what="config 3 super-window")
+
+
+def test_fullsize_config3_swtcf_bit_exact(gpu, oracle):
+    """convertCOOToSWTCF of the config-3 graph (114M edges, S = 16) against
+    the C oracle's canonical form, every array bit for bit; then the SWTCF
+    SpMM (F = 128) through the weighted checksum."""
+    from tcc_amd import swtcf
+    from tcc_amd.graphs import CONFIGS, make_graph
+
+    n = CONFIGS[3]["n"]
+    rows, cols, _ = make_graph(3, device="cuda")
+    r32 = rows.to(torch.int32).contiguous()
+    c32 = cols.to(torch.int32).contiguous()
+    del rows, cols
+    nnz = r32.numel()
+    print(f"config 3 SWTCF: n={n} nnz={nnz}", flush=True)
+    m = swtcf.DeviceSWTCFMatrix(n, n, nnz, 16)
+    ws = swtcf.SWTCFConvertWorkspace(nnz, n, 16)
+    swtcf.convertCOOToSWTCF(r32, c32, nnz, m, ws)
+    assert ws.device_error() == 0
+    got = m.to_host()
+    dst = r32.cpu().numpy().view(np.uint32)
+    src = c32.cpu().numpy().view(np.uint32)
+    print("oracle conversion (host)...", flush=True)
+    ref = oracle.swtcf_convert(dst, src, n, n, 16)
+    assert ref["err"] == 0
+    want = oracle.swtcf_valid_extents(ref)
+    del ref
+    for k, vv in want.items():
+        assert np.array_equal(got[k], vv), f"SWTCF array {k} differs from the oracle"
+    print(f"bit-exact: {got['numTiles']} tiles, {got['numRows']} super-window rows", flush=True)
+    del want, got
+
+    F = 128
+    Xh = oracle.tf32(np.random.default_rng(35).standard_normal((n, F)).astype(np.float32))
+    Ys = torch.zeros(n, F, device="cuda")
+    swtcf.swtcf_spmm(m, torch.from_numpy(Xh).cuda(), Ys, 12)
+    check_weighted(oracle, Ys, n, dst, src, None, n, Xh, 36, what="config 3 SWTCF SpMM")
 
 
 def test_fullsize_config4_mixed_and_narrow(gpu, oracle):
-    """The GCN graph (2.45M nodes, 61.9M edges, no values: every a_ij = 1):
-    the first-layer product over the hot/cold feature table (fp32 and packed
+    """The GCN graph (2.45M nodes, 61.9M edges, every a_ij = 1): the
+    first-layer product over the hot/cold feature table (fp32 and packed
     host rows), the second layer's F = 2 product and its transpose."""
     from tcc_amd import gcn, swtcf
     from tcc_amd.graphs import CONFIGS, make_features, make_graph
@@ -118,71 +240,98 @@ def test_fullsize_config4_mixed_and_narrow(gpu, oracle):
     rows, cols, _ = make_graph(4, device="cuda")
     print(f"config 4: n={n} nnz={rows.numel()} F={F}", flush=True)
     X = make_features(n, F, cfg["seed"], device="cuda")
+    Xh = X.cpu().numpy()
+    rows_np, cols_np = rows.cpu().numpy(), cols.cpu().numpy()
     table = gcn.FeatureTable(X, cols)
     g1, g2 = gcn.build_gcn_graphs(rows, cols, n, table.hot)
-    indeg = np.bincount(cols.cpu().numpy().astype(np.int64), minlength=n).astype(np.float64)
-    outdeg = np.bincount(rows.cpu().numpy().astype(np.int64), minlength=n).astype(np.float64)
-    want = indeg @ oracle.tf32(X.cpu().numpy()).astype(np.float64)
+    hub = int(np.argmax(np.bincount(rows_np, minlength=n)))
 
-    got = g1.aggregate(F, source=table.source).double().sum(dim=0).cpu().numpy()
-    print(f"mixed, fp32 host rows: checksum rel-L2 {rel_l2(got, want):.2e}", flush=True)
-    assert rel_l2(got, want) <= TOL, "mixed fp32"
+    Y = g1.aggregate(F, source=table.source)
+    r_dev, want = check_weighted(oracle, Y, n, rows_np, cols_np, None, n, Xh, 41, what="config 4 mixed, fp32 rows")
+    check_swap_fails(Y, n, r_dev, want, hub, (hub + 5) % n, what="config 4 mixed")
+    check_rows(oracle, Y, rows_np, cols_np, None, n, Xh, 42, what="config 4 mixed, fp32 rows")
+    assert table.error() == 0
+    del Y
     ptable = gcn.FeatureTable(X, cols, packed=True)
-    got = g1.aggregate(F, source=ptable.source).double().sum(dim=0).cpu().numpy()
-    print(f"mixed, packed host rows: checksum rel-L2 {rel_l2(got, want):.2e}", flush=True)
-    assert rel_l2(got, want) <= TOL, "mixed packed"
+    Yp = g1.aggregate(F, source=ptable.source)
+    check_weighted(oracle, Yp, n, rows_np, cols_np, None, n, Xh, 41, what="config 4 mixed, packed rows")
+    check_rows(oracle, Yp, rows_np, cols_np, None, n, Xh, 43, what="config 4 mixed, packed rows")
+    assert ptable.error() == 0
+    del Yp
+    ptable.free()
 
     XW = torch.randn(n, 2, device="cuda")
-    got = g2.aggregate(2, x=XW).double().sum(dim=0).cpu().numpy()
-    want2 = indeg @ oracle.tf32(XW.cpu().numpy()).astype(np.float64)
-    print(f"narrow F=2: checksum rel-L2 {rel_l2(got, want2):.2e}", flush=True)
-    assert rel_l2(got, want2) <= TOL, "narrow"
+    Y2 = g2.aggregate(2, x=XW)
+    check_weighted(oracle, Y2, n, rows_np, cols_np, None, n, XW.cpu().numpy(), 44, what="config 4 narrow F=2")
     dY = torch.randn(n, 2, device="cuda")
     dX = swtcf.bcsc_transpose_spmm(g2.bwd, dY)
-    got = dX[:n].double().sum(dim=0).cpu().numpy()
-    wantT = outdeg @ dY.cpu().numpy().astype(np.float64)
-    print(f"narrow transpose F=2: checksum rel-L2 {rel_l2(got, wantT):.2e}", flush=True)
-    assert rel_l2(got, wantT) <= TOL, "narrow transpose"
+    check_weighted(oracle, dX, n, cols_np, rows_np, None, n, dY.cpu().numpy(), 45, tf32=False,
+                   what="config 4 narrow transpose F=2")
+    check_rows(oracle, dX, cols_np, rows_np, None, n, dY.cpu().numpy(), 46, what="config 4 narrow transpose F=2",
+               tf32=False)
+    check_rows(oracle, Y2, rows_np, cols_np, None, n, XW.cpu().numpy(), 47, what="config 4 narrow F=2")
+    table.free()
 
 
-def test_fullsize_config3_swtcf(gpu, oracle):
-    """convertCOOToSWTCF and the SWTCF SpMM on the config-3 graph (114M
-    edges, unit values; F = 128 for time): every edge is exactly one tile
-    bit, the product passes the checksum, and it equals the BCSR gather's
-    element by element.  X holds TF32 values already, so the SWTCF path's
-    per-tile choice between TF32 and fp32 inputs does not change it."""
-    from tcc_amd import swtcf
-    from tcc_amd.graphs import CONFIGS, make_graph
+def test_fullsize_config5_training_step(gpu):
+    """One full-graph training step of the 2-layer GCN (100 -> 256 -> 2) on
+    the 2.45M-node graph, fused path (TwoLayerFunction), against a float64
+    evaluation of the same formulas: scipy fp64 sparse products with the
+    kernels' rounding (TF32 into the forward SpMMs, fp32 into A^T), fp64
+    GEMMs.  rel-L2 <= 1e-4 as the small-graph test."""
+    import scipy.sparse as sp
 
-    n = CONFIGS[3]["n"]
-    F = 128
-    rows, cols, _ = make_graph(3, device="cuda")
-    r32 = rows.to(torch.int32).contiguous()
-    c32 = cols.to(torch.int32).contiguous()
-    nnz = r32.numel()
-    del rows
-    print(f"config 3 SWTCF: n={n} nnz={nnz} F={F}", flush=True)
-    m = swtcf.DeviceSWTCFMatrix(n, n, nnz, 16)
-    ws = swtcf.SWTCFConvertWorkspace(nnz, n, 16)
-    swtcf.convertCOOToSWTCF(r32, c32, nnz, m, ws)
-    assert ws.device_error() == 0
-    h = m.to_host()
-    bits = int(np.unpackbits(h["tileLocalBit"].view(np.uint8)).sum())
-    print(f"tiles {h['numTiles']}, tile bits {bits}", flush=True)
-    assert bits == nnz
-    assert np.all(np.diff(h["colWindowOffset"].astype(np.int64)) >= 0)
+    from tcc_amd import gcn
+    from tcc_amd.graphs import CONFIGS, make_features, make_graph
 
-    X = oracle.tf32(np.random.default_rng(33).standard_normal((n, F)).astype(np.float32))
-    Xd = torch.from_numpy(X).cuda()
-    Ys = torch.zeros(n, F, device="cuda")
-    swtcf.swtcf_spmm(m, Xd, Ys, 12)
-    indeg = np.bincount(c32.cpu().numpy().astype(np.int64), minlength=n).astype(np.float64)
-    want = indeg @ X.astype(np.float64)
-    got = Ys.double().sum(dim=0).cpu().numpy()
-    print(f"SWTCF checksum rel-L2 {rel_l2(got, want):.2e}", flush=True)
-    assert rel_l2(got, want) <= TOL
-    A = swtcf.coo_to_bcsr(r32, c32, None, n, n)
-    Yb = swtcf.bcsr_spmm(A, Xd)[:n]
-    d = ((Ys.double() - Yb.double()).norm() / Yb.double().norm()).item()
-    print(f"SWTCF against the BCSR gather: rel-L2 {d:.2e}", flush=True)
-    assert d <= 1e-6
+    cfg = CONFIGS[5]
+    n, F, Hd, C = cfg["n"], cfg["F"], 256, 2
+    rows, cols, _ = make_graph(5, device="cuda")
+    print(f"config 5: n={n} nnz={rows.numel()} F={F} hidden={Hd} classes={C}", flush=True)
+    X = make_features(n, F, cfg["seed"], device="cuda")
+    table = gcn.FeatureTable(X, cols)
+    g1, g2 = gcn.build_gcn_graphs(rows, cols, n, table.hot)
+    torch.manual_seed(cfg["seed"])
+    model = gcn.GCN(F, Hd, C, dropout=0.0).cuda()
+    assert model.fused
+    labels = gcn.synthetic_labels(n, C, cfg["seed"])
+    W1 = model.conv1.weights.detach().double()
+    W2 = model.conv_final.weights.detach().double()
+    pred = model(g1, g2, table.source)
+    loss = gcn.cross_entropy(pred, labels)
+    loss.backward()
+    torch.cuda.synchronize()
+    assert table.error() == 0
+
+    def tf32(t):
+        b = t.float().contiguous().view(torch.int32)
+        fin = (b & 0x7F800000) != 0x7F800000
+        r = torch.where(fin, (b + 0x1000) & -0x2000, b)
+        return r.view(torch.float32).double()
+
+    A = sp.csr_matrix((np.ones(rows.numel()), (rows.cpu().numpy(), cols.cpu().numpy())), shape=(n, n))
+    At = A.T.tocsr()
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    AX1 = dev(A @ tf32(X).cpu().numpy())
+    H1 = AX1 @ W1
+    R = torch.clamp_min(H1, 0.0)
+    out = dev(A @ tf32(R @ W2).cpu().numpy())
+    logp = torch.log_softmax(out, dim=1)
+    ref_loss = -logp[torch.arange(n, device="cuda"), labels].mean()
+    dout = torch.softmax(out, dim=1)
+    dout[torch.arange(n, device="cuda"), labels] -= 1.0
+    dout /= n
+    G2 = dev(At @ dout.float().double().cpu().numpy())
+    dW2 = R.t() @ G2
+    dH1 = (G2 @ W2.t()) * (H1 > 0)
+    dW1 = AX1.t() @ dH1
+    e_out = rel_l2(pred.detach().double().cpu().numpy(), out.cpu().numpy())
+    e_dw1 = rel_l2(model.conv1.weights.grad.double().cpu().numpy(), dW1.cpu().numpy())
+    e_dw2 = rel_l2(model.conv_final.weights.grad.double().cpu().numpy(), dW2.cpu().numpy())
+    print(f"config 5 step: out {e_out:.2e}, loss {loss.item():.6f} vs {ref_loss.item():.6f}, dW1 {e_dw1:.2e}, "
+          f"dW2 {e_dw2:.2e}", flush=True)
+    assert e_out < 1e-4
+    assert abs(loss.item() - ref_loss.item()) < 1e-4 * abs(ref_loss.item())
+    assert e_dw1 < 1e-4
+    assert e_dw2 < 1e-4
+    table.free()

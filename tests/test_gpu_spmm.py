@@ -320,6 +320,71 @@ def test_mixed_hot_cold_feature_source(gpu, oracle):
     cpu.free()
 
 
+@pytest.mark.parametrize("packed", [False, True])
+def test_mixed_refused_lookups_read_zeros_and_set_the_error(gpu, oracle, packed):
+    """Lookups outside their table (a cache index past the pointer table, a
+    host row past cpu_feature_len) are refused by the kernels' own bounds
+    checks: they read zeros and write TCC_DEVERR_FEATURE_INDEX to the
+    source's error word; a source without bad entries leaves it at 0."""
+    from tcc_amd import swtcf
+    from tcc_amd.hostmem import PinnedArray
+
+    nr = nc = 600
+    F = 64
+    dst, src = random_coo(nr, nc, 8000, 31)
+    rng = np.random.default_rng(32)
+    feats = rng.standard_normal((nc, F)).astype(np.float32)
+    hot_ids = np.sort(rng.choice(nc, size=nc // 4, replace=False))
+    csm = np.full(nc, -1, np.int32)
+    csm[hot_ids] = np.arange(hot_ids.size, dtype=np.int32)
+    id_map = np.arange(nc, dtype=np.int32)
+    cold = np.setdiff1d(np.arange(nc), hot_ids)
+    bad_cache = int(hot_ids[3])  # cache index cap + 3: pointer-table entry 1 of 1
+    bad_host = int(cold[5])      # host row past the table's last row
+    csm[bad_cache] = hot_ids.size + 3
+    cpu_rows = nc                # cpu_feature_len covers rows 0 .. nc-1
+    id_map[bad_host] = nc
+    if packed:
+        stride = packed_stride_host(F)
+        hot_cache = swtcf.tf32_pack(torch.from_numpy(feats[hot_ids]).cuda())
+        cpu = PinnedArray((nc * stride,), np.uint8)
+        cpu.array[:] = swtcf.tf32_pack(torch.from_numpy(feats).cuda()).cpu().numpy()[: nc * stride]
+        fmt = swtcf.ROWS_TF32_PACKED
+    else:
+        hot_cache = torch.from_numpy(feats[hot_ids]).cuda()
+        cpu = PinnedArray((nc, F))
+        cpu.array[:] = feats
+        fmt = swtcf.ROWS_FP32
+    ptrs = torch.tensor([hot_cache.data_ptr()], dtype=torch.int64, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    print(f"refused lookups: packed={packed} bad cache column {bad_cache}, bad host column {bad_host}", flush=True)
+    src_desc = swtcf.feature_source(torch.from_numpy(id_map).cuda(), torch.from_numpy(csm).cuda(), ptrs,
+                                    hot_ids.size, cpu.device_ptr, cpu_rows * F, row_format=fmt, device_error=err)
+    hot_mask = csm[src] >= 0
+    A = swtcf.coo_to_bcsr(dev_u32(dst[hot_mask]), dev_u32(src[hot_mask]), None, nr, nc)
+    B = swtcf.coo_to_bcsc(dev_u32(dst[~hot_mask]), dev_u32(src[~hot_mask]), None, nr, nc)
+    assert np.any(src == bad_cache) and np.any(src == bad_host)
+    denseC = torch.empty(((A.view.num_rowWindows + 1) * 8, F), device="cuda")
+    swtcf.spmm_cnic_forward_mixed(A, B, src_desc, denseC, F)
+    X = feats.copy()
+    X[bad_cache] = 0.0
+    X[bad_host] = 0.0
+    rowptr, colind, _ = csr_of(dst, src, nr)
+    assert_close(denseC.cpu().numpy()[:nr], oracle.csr_spmm(rowptr, colind, None, X, use_tf32=True))
+    assert int(err.item()) == swtcf.DEVERR_FEATURE_INDEX
+    # the same matrices over a valid source: no error
+    csm_ok = np.full(nc, -1, np.int32)
+    csm_ok[hot_ids] = np.arange(hot_ids.size, dtype=np.int32)
+    err.zero_()
+    ok = swtcf.feature_source(torch.from_numpy(np.arange(nc, dtype=np.int32)).cuda(), torch.from_numpy(csm_ok).cuda(),
+                              ptrs, hot_ids.size, cpu.device_ptr, nc * F, row_format=fmt, device_error=err)
+    swtcf.spmm_cnic_forward_mixed(A, B, ok, denseC, F)
+    assert_close(denseC.cpu().numpy()[:nr], oracle.csr_spmm(rowptr, colind, None, feats, use_tf32=True))
+    assert int(err.item()) == 0
+    torch.cuda.synchronize()
+    cpu.free()
+
+
 @pytest.mark.parametrize("F,vals_hot,vals_cold,K", [(37, True, True, 0), (100, True, False, 3), (100, False, True, 0),
                                                     (256, True, True, 5), (100, False, False, 2)])
 def test_mixed_forward_values_widths_units(gpu, oracle, F, vals_hot, vals_cold, K):

@@ -161,6 +161,8 @@ def test_forward_tensorcore_mixed_forms(gpu):
                                       ids_d, cpu_cap, csm_d, gpu_cap,
                                       0, caps[1])
     assert _rel(out3.reshape(nr, F).cpu().numpy(), want) < 1e-5
+    # valid maps: no lookup was refused
+    assert m.feature_error(0) == 0
     torch.cuda.synchronize()
     m.finalize(0)
     cpu.free()
