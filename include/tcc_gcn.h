@@ -40,6 +40,22 @@ size_t tcc_dense_tn_workspace_bytes(uint32_t K, uint32_t M, uint32_t N);
 int tcc_dense_tn(const float* A, uint32_t lda, const float* B, uint32_t ldb, float* C, uint32_t ldc, uint32_t K,
                  uint32_t M, uint32_t N, int accumulate, void* workspace, size_t workspaceBytes, void* stream);
 
+/* tcc_dense_tn without a workspace and without any allocation.  No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory, such as code under HIP graph capture (a captured training
+ * step) or a serving loop that forbids hipMalloc.  The partial products go
+ * to a fixed device array inside the library, TCC_DENSE_TN_NOALLOC_SCRATCH_BYTES
+ * (16 MiB) per GPU, held until the process ends; the split of K is capped so
+ * that they fit (fewer splits than tcc_dense_tn picks only when its
+ * workspace would exceed 16 MiB; the result is then the same up to fp32
+ * summation order, else bit for bit).  Returns TCC_ERR_UNSUPPORTED when
+ * M x N floats exceed the array.  Every call on a GPU shares that GPU's
+ * array: calls that overlap on one GPU (on different streams, or from
+ * different threads) race and must be serialised by the caller. */
+#define TCC_DENSE_TN_NOALLOC_SCRATCH_BYTES (16u << 20)
+int tcc_dense_tn_noalloc(const float* A, uint32_t lda, const float* B, uint32_t ldb, float* C, uint32_t ldc,
+                         uint32_t K, uint32_t M, uint32_t N, int accumulate, void* stream);
+
 /* H = relu(AX W1) [K x Hd] and XW = H W2 [K x C] in one pass over the K
  * rows of AX [K x F] (row strides ldax, ldh, ldxw; W1 [F x Hd] and W2
  * [Hd x C] row-major): the first layer's transform and activation and the

@@ -104,6 +104,7 @@ SIGNATURES = {
     "tcc_sw_bcsr_spmm_packed": (ctypes.c_int, [ctypes.POINTER(SWBCSR), vp, vp, u32, ctypes.c_int, vp]),
     "tcc_dense_tn_workspace_bytes": (ctypes.c_size_t, [u32, u32, u32]),
     "tcc_dense_tn": (ctypes.c_int, [vp, u32, vp, u32, vp, u32, u32, u32, u32, ctypes.c_int, vp, ctypes.c_size_t, vp]),
+    "tcc_dense_tn_noalloc": (ctypes.c_int, [vp, u32, vp, u32, vp, u32, u32, u32, u32, ctypes.c_int, vp]),
     "tcc_gcn_relu_forward": (ctypes.c_int, [vp, u32, vp, vp, vp, u32, vp, u32, u32, u32, u32, u32, vp]),
     "tcc_gcn_relu_grad_workspace_bytes": (ctypes.c_size_t, [u32, u32, u32, u32]),
     "tcc_gcn_relu_grad": (ctypes.c_int, [vp, u32, vp, u32, vp, u32, vp, vp, vp, u32, u32, u32, u32, vp, ctypes.c_size_t,

@@ -17,6 +17,7 @@
 // Columns past M (N) are clamped to the last one: they only feed rows
 // (columns) of C that are never stored.  Rows past K are zero.
 #include <algorithm>
+#include <mutex>
 
 #include "../../include/tcc_gcn.h"
 #include "../../include/tcc_swtcf.h"
@@ -493,7 +494,7 @@ struct TnPlan {
 // Shape chosen from (M, N); block counts from (realM, realN) and the rows per
 // iteration from `step` when given.
 TnPlan tn_plan(std::uint32_t K, std::uint32_t M, std::uint32_t N, std::uint32_t realM = 0, std::uint32_t realN = 0,
-               std::uint32_t step = 0) {
+               std::uint32_t step = 0, std::uint64_t splitCap = 0) {
     TnPlan p{};
     if (N <= 16) {
         p.shape = TnShape::NarrowN;  // TM=4, TN=1, WM=4, WN=1, U=8
@@ -518,6 +519,7 @@ TnPlan tn_plan(std::uint32_t K, std::uint32_t M, std::uint32_t N, std::uint32_t 
     const std::uint64_t target = static_cast<std::uint64_t>(device_cus()) * (narrow ? 8 : 2);
     const std::uint64_t maxSplits = std::max<std::uint64_t>(1, (K + p.step - 1) / p.step);
     std::uint64_t splits = std::min<std::uint64_t>(maxSplits, std::max<std::uint64_t>(1, (target + blocks - 1) / blocks));
+    if (splitCap != 0) splits = std::min(splits, splitCap);
     std::uint64_t rps = (K + splits - 1) / splits;
     rps = std::max<std::uint64_t>(p.step, (rps + p.step - 1) / p.step * p.step);
     splits = std::max<std::uint64_t>(1, (K + rps - 1) / rps);
@@ -557,15 +559,20 @@ size_t tcc_dense_tn_workspace_bytes(std::uint32_t K, std::uint32_t M, std::uint3
     return static_cast<size_t>(p.splits) * M * N * sizeof(float);
 }
 
-int tcc_dense_tn(const float* A, std::uint32_t lda, const float* B, std::uint32_t ldb, float* C, std::uint32_t ldc,
-                 std::uint32_t K, std::uint32_t M, std::uint32_t N, int accumulate, void* workspace,
-                 size_t workspaceBytes, void* stream) {
-    clear_last_error();
+}  // extern "C"
+
+namespace tcc {
+namespace {
+
+// C = A^T B (or +=) with the partial products in `workspace`; splitCap
+// bounds the split of K (0 = none) so that the partials fit a fixed buffer.
+int dense_tn_impl(const float* A, std::uint32_t lda, const float* B, std::uint32_t ldb, float* C, std::uint32_t ldc,
+                  std::uint32_t K, std::uint32_t M, std::uint32_t N, int accumulate, void* workspace,
+                  size_t workspaceBytes, std::uint64_t splitCapBytes, hipStream_t st) {
     TCC_REQUIRE(C && M >= 1 && N >= 1 && lda >= M && ldb >= N && ldc >= N, TCC_ERR_INVALID_ARGUMENT,
                 "invalid dense A^T B arguments");
     TCC_REQUIRE(lda < (1u << 28) && ldb < (1u << 28) && ldc < (1u << 28), TCC_ERR_UNSUPPORTED,
                 "dense A^T B row strides must be below 2^28");
-    const hipStream_t st = as_stream(stream);
     if (K == 0) {
         if (accumulate) return TCC_OK;
         for (std::uint32_t m = 0; m < M; ++m)  // C rows may be strided: clear row by row
@@ -579,7 +586,8 @@ int tcc_dense_tn(const float* A, std::uint32_t lda, const float* B, std::uint32_
         std::swap(lda, ldb);
         std::swap(M, N);
     }
-    const TnPlan p = tn_plan(K, M, N);
+    const std::uint64_t splitBytes = static_cast<std::uint64_t>(M) * N * sizeof(float);
+    const TnPlan p = tn_plan(K, M, N, 0, 0, 0, splitCapBytes ? splitCapBytes / splitBytes : 0);
     TCC_REQUIRE(workspaceBytes >= static_cast<size_t>(p.splits) * M * N * sizeof(float), TCC_ERR_INVALID_ARGUMENT,
                 "dense A^T B workspace too small (tcc_dense_tn_workspace_bytes)");
     TCC_REQUIRE(static_cast<std::uint64_t>(p.blocksM) * p.blocksN <= 65535, TCC_ERR_UNSUPPORTED,
@@ -622,6 +630,59 @@ int tcc_dense_tn(const float* A, std::uint32_t lda, const float* B, std::uint32_
                        static_cast<const float*>(workspace), p.splits, M, N, C, ldc, accumulate, swapped ? 1 : 0);
     TCC_LAUNCH_CHECK();
     return TCC_OK;
+}
+
+// Scratch of tcc_dense_tn_noalloc: the partial products, in device memory of
+// the library's code object (one copy per GPU, held until the process ends).
+constexpr std::size_t kTnScratchBytes = static_cast<std::size_t>(TCC_DENSE_TN_NOALLOC_SCRATCH_BYTES);
+__device__ __align__(256) float tn_scratch[kTnScratchBytes / sizeof(float)];
+
+// Device address of tn_scratch on the current device, looked up once per
+// device (host code must not pass the symbol itself to a kernel: in host
+// code it names a host-side stand-in).
+int tn_scratch_address(float** out) {
+    static std::mutex mu;
+    static float* addr[64] = {};
+    int dev = 0;
+    TCC_HIP_CHECK(hipGetDevice(&dev));
+    TCC_REQUIRE(dev >= 0 && dev < 64, TCC_ERR_UNSUPPORTED, "device index out of range");
+    std::lock_guard<std::mutex> lock(mu);
+    if (addr[dev] == nullptr) {
+        void* p = nullptr;
+        TCC_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(tn_scratch)));
+        TCC_REQUIRE(p != nullptr, TCC_ERR_HIP, "no device address for the dense A^T B scratch");
+        addr[dev] = static_cast<float*>(p);
+    }
+    *out = addr[dev];
+    return TCC_OK;
+}
+
+}  // namespace
+}  // namespace tcc
+
+extern "C" {
+
+int tcc_dense_tn(const float* A, std::uint32_t lda, const float* B, std::uint32_t ldb, float* C, std::uint32_t ldc,
+                 std::uint32_t K, std::uint32_t M, std::uint32_t N, int accumulate, void* workspace,
+                 size_t workspaceBytes, void* stream) {
+    clear_last_error();
+    return dense_tn_impl(A, lda, B, ldb, C, ldc, K, M, N, accumulate, workspace, workspaceBytes, 0,
+                         as_stream(stream));
+}
+
+int tcc_dense_tn_noalloc(const float* A, std::uint32_t lda, const float* B, std::uint32_t ldb, float* C,
+                         std::uint32_t ldc, std::uint32_t K, std::uint32_t M, std::uint32_t N, int accumulate,
+                         void* stream) {
+    clear_last_error();
+    TCC_REQUIRE(static_cast<std::uint64_t>(M) * N * sizeof(float) <= kTnScratchBytes, TCC_ERR_UNSUPPORTED,
+                "dense A^T B without allocation: M x N above the 16 MiB scratch (4M floats)");
+    float* scratch = nullptr;
+    if (K > 0) {
+        const int rc = tn_scratch_address(&scratch);
+        if (rc) return rc;
+    }
+    return dense_tn_impl(A, lda, B, ldb, C, ldc, K, M, N, accumulate, scratch, kTnScratchBytes, kTnScratchBytes,
+                         as_stream(stream));
 }
 
 int tcc_gcn_relu_forward(const float* AX, std::uint32_t ldax, const float* W1, const float* W2, float* H,
