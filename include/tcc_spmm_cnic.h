@@ -259,6 +259,71 @@ int tcc_coo_to_sw_bcsr(const uint32_t* dRow, const uint32_t* dCol, const float* 
 int tcc_sw_bcsr_spmm_packed(const tcc_sw_bcsr* A, const void* packedX, float* Y, uint32_t featureDim,
                             int accumulate, void* stream);
 
+/* ---- dense hub tiles + sparse remainder (no reference counterpart) ----
+ * The product tf32_spmm_bcsr computes, for graphs with a dense core (R-MAT
+ * hubs).  Rows and columns are ranked by degree (descending, ties by index)
+ * and the reordered matrix is cut into 16x16 tiles; tiles holding at least
+ * minTileNnz entries are stored densely (TF32-rounded values, zeros
+ * included) and multiplied with fp32 MFMA (v_mfma_f32_16x16x4f32), the other
+ * entries form an ordinary or phased BCSR (`rest`) for the gather kernels.
+ *   rowOrder[16b + i]: original row of row i of row block b (0xFFFFFFFF past
+ *     num_rows); hubColOrder[r]: original column of column rank r < hub_cols;
+ *   row block b's tiles are [rowBlockOffset[b], rowBlockOffset[b+1]); tile t
+ *     covers column ranks 16*tileCol[t] .. +15;
+ *   tileVals[256t + 4l + s] = A(row l%16, column 4s + l/16) of tile t (the
+ *     MFMA A operand of lane l at step s);
+ *   units[3u .. 3u+2] = row block, first tile, end tile (at most unit_tiles
+ *     tiles); a row block held by more than one unit receives fp32 atomics. */
+typedef struct tcc_hub_tiles {
+    uint32_t num_rows;
+    uint32_t num_cols;
+    uint32_t nnz;                   /* entries held in the tiles */
+    uint32_t num_row_blocks;        /* ceil(num_rows / 16) */
+    uint32_t num_tiles;
+    uint32_t num_units;
+    uint32_t unit_tiles;
+    uint32_t hub_cols;              /* column ranks the tiles cover: [0, hub_cols) */
+    const uint32_t* rowOrder;       /* [16*num_row_blocks] */
+    const uint32_t* hubColOrder;    /* [hub_cols] */
+    const uint32_t* rowBlockOffset; /* [num_row_blocks+1] */
+    const uint32_t* tileCol;        /* [num_tiles] */
+    const float* tileVals;          /* [256*num_tiles] */
+    const uint32_t* units;          /* [3*num_units] */
+} tcc_hub_tiles;
+
+typedef struct tcc_hybrid {
+    tcc_hub_tiles tiles;
+    tcc_bcsr rest;                  /* every entry outside the dense tiles */
+    void* tilesAllocation;          /* device allocations (tcc_hybrid_release) */
+    void* restAllocation;
+} tcc_hybrid;
+
+/* Build the hybrid of a device COO (row = destination, col = source, no
+ * duplicate pairs; dVal may be NULL).  minTileNnz 0 = 32, unitTiles 0 = 32,
+ * phases as tcc_coo_to_bcsr_phased for the remainder.  Synchronises
+ * `stream`; free with tcc_hybrid_release. */
+int tcc_coo_to_hybrid(const uint32_t* dRow, const uint32_t* dCol, const float* dVal, uint32_t nnz,
+                      uint32_t numRows, uint32_t numCols, uint32_t minTileNnz, uint32_t unitTiles,
+                      uint32_t phases, tcc_hybrid* out, void* stream);
+int tcc_hybrid_release(tcc_hybrid* H);
+
+/* Bytes of device workspace tcc_hybrid_spmm needs for F features: the
+ * remainder's packed TF32 rows and the hub columns' TF32 rows. */
+size_t tcc_hybrid_workspace_bytes(const tcc_hybrid* H, uint32_t featureDim);
+
+/* Y (=, or += when accumulate != 0) A X for fp32 X [num_cols x F]: the
+ * remainder's gather (which writes or adds every row of Y), then the tiles
+ * added into Y.  Y holds 8*ceil(num_rows/8) rows of F floats (as for the
+ * remainder's BCSR); workspace 16-byte aligned, at least
+ * tcc_hybrid_workspace_bytes(H, F) bytes, not shared with a concurrent call. */
+int tcc_hybrid_spmm(const tcc_hybrid* H, const float* X, float* Y, uint32_t featureDim, int accumulate,
+                    void* workspace, size_t workspaceBytes, void* stream);
+
+/* The tiles' part alone: Y[num_rows x F] += A_tiles X (workspace of at
+ * least hub_cols * roundup(F, 64) floats, 16-byte aligned). */
+int tcc_hub_tiles_spmm(const tcc_hub_tiles* T, const float* X, float* Y, uint32_t featureDim, void* workspace,
+                       size_t workspaceBytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

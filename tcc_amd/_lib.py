@@ -63,6 +63,20 @@ class SWBCSR(ctypes.Structure):
     ]
 
 
+class HubTiles(ctypes.Structure):
+    """tcc_hub_tiles: dense 16x16 tiles of the degree-sorted matrix (no reference counterpart)."""
+    _fields_ = [
+        ("num_rows", u32), ("num_cols", u32), ("nnz", u32), ("num_row_blocks", u32), ("num_tiles", u32),
+        ("num_units", u32), ("unit_tiles", u32), ("hub_cols", u32), ("rowOrder", vp), ("hubColOrder", vp),
+        ("rowBlockOffset", vp), ("tileCol", vp), ("tileVals", vp), ("units", vp),
+    ]
+
+
+class Hybrid(ctypes.Structure):
+    """tcc_hybrid: hub tiles + the remainder's BCSR."""
+    _fields_ = [("tiles", HubTiles), ("rest", BCSR), ("tilesAllocation", vp), ("restAllocation", vp)]
+
+
 class FeatureSource(ctypes.Structure):
     _fields_ = [
         ("id_map", vp), ("cache_search_map", vp), ("gpu_feature_cache", vp), ("gpu_node_capacity", i32),
@@ -102,6 +116,11 @@ SIGNATURES = {
     "tcc_coo_to_sw_bcsr": (ctypes.c_int, [vp, vp, vp, u32, u32, u32, u32, u32, ctypes.POINTER(SWBCSR),
                                           ctypes.POINTER(vp), vp]),
     "tcc_sw_bcsr_spmm_packed": (ctypes.c_int, [ctypes.POINTER(SWBCSR), vp, vp, u32, ctypes.c_int, vp]),
+    "tcc_coo_to_hybrid": (ctypes.c_int, [vp, vp, vp, u32, u32, u32, u32, u32, u32, ctypes.POINTER(Hybrid), vp]),
+    "tcc_hybrid_release": (ctypes.c_int, [ctypes.POINTER(Hybrid)]),
+    "tcc_hybrid_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Hybrid), u32]),
+    "tcc_hybrid_spmm": (ctypes.c_int, [ctypes.POINTER(Hybrid), vp, vp, u32, ctypes.c_int, vp, ctypes.c_size_t, vp]),
+    "tcc_hub_tiles_spmm": (ctypes.c_int, [ctypes.POINTER(HubTiles), vp, vp, u32, vp, ctypes.c_size_t, vp]),
     "tcc_dense_tn_workspace_bytes": (ctypes.c_size_t, [u32, u32, u32]),
     "tcc_dense_tn": (ctypes.c_int, [vp, u32, vp, u32, vp, u32, u32, u32, u32, ctypes.c_int, vp, ctypes.c_size_t, vp]),
     "tcc_dense_tn_noalloc": (ctypes.c_int, [vp, u32, vp, u32, vp, u32, u32, u32, u32, ctypes.c_int, vp]),

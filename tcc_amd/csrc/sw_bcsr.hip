@@ -31,6 +31,7 @@
 #include "../../include/tcc_spmm_cnic.h"
 #include "../../include/tcc_swtcf.h"
 #include "common.hpp"
+#include "degree_rank.hpp"
 #include "primitives.hpp"
 
 namespace tcc {
@@ -64,40 +65,6 @@ __host__ __device__ constexpr std::uint64_t packed_row_stride(std::uint32_t F) {
 }
 
 // ---------------------------------------------------------------- builder
-
-__global__ void degree_kernel(const std::uint32_t* __restrict__ idx, std::uint32_t E, std::uint32_t limit,
-                              std::uint32_t* __restrict__ deg, std::uint32_t* __restrict__ err) {
-    const std::uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= E) return;
-    const std::uint32_t v = idx[e];
-    if (v >= limit) {
-        atomicMax(err, 1u);
-        return;
-    }
-    atomicAdd(&deg[v], 1u);
-}
-
-// key = (~deg << idBits) | id: ascending order = degree descending, ids ascending.
-__global__ void degree_keys_kernel(const std::uint32_t* __restrict__ deg, std::uint32_t n, unsigned idBits,
-                                   std::uint64_t* __restrict__ keys) {
-    const std::uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) keys[i] = (static_cast<std::uint64_t>(0xFFFFFFFFu - deg[i]) << idBits) | i;
-}
-
-// order[s] = id at sorted position s; rank[id] = s.  Positions past n (the
-// last super-window's padding) get 0xFFFFFFFF in `order`.
-__global__ void order_rank_kernel(const std::uint64_t* __restrict__ sorted, std::uint32_t n, std::uint32_t padded,
-                                  unsigned idBits, std::uint32_t* __restrict__ order, std::uint32_t* __restrict__ rank) {
-    const std::uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
-    if (s >= padded) return;
-    if (s >= n) {
-        if (order) order[s] = TCC_SWTCF_INVALID_ROW_SLOT;
-        return;
-    }
-    const std::uint32_t id = static_cast<std::uint32_t>(sorted[s] & ((1ull << idBits) - 1ull));
-    if (order) order[s] = id;
-    rank[id] = s;
-}
 
 // Edge key (super-window, column rank, row in super-window); payload = edge.
 __global__ void sw_keys_kernel(const std::uint32_t* __restrict__ row, const std::uint32_t* __restrict__ col,
@@ -619,28 +586,12 @@ int tcc_coo_to_sw_bcsr(const std::uint32_t* dRow, const std::uint32_t* dCol, con
     DevBuf<std::uint32_t> rowOrderTmp;
     TCC_HIP_CHECK(hipMalloc(&rowOrderTmp.p, 4ull * padded));
     if (E > 0) {
-        hipLaunchKernelGGL(degree_kernel, dim3(grid_for(E, kBuildThreads)), dim3(kBuildThreads), 0, st, dRow, E,
-                           numRows, rowDeg, small);
-        hipLaunchKernelGGL(degree_kernel, dim3(grid_for(E, kBuildThreads)), dim3(kBuildThreads), 0, st, dCol, E,
-                           numCols, colDeg, small);
-        TCC_LAUNCH_CHECK();
+        TCC_HIP_CHECK(degree_histogram(dRow, E, numRows, rowDeg, small, st));
+        TCC_HIP_CHECK(degree_histogram(dCol, E, numCols, colDeg, small, st));
     }
     // row and column ranks: degree descending, ids ascending
-    std::uint64_t* sorted = nullptr;
-    hipLaunchKernelGGL(degree_keys_kernel, dim3(grid_for(numRows, kBuildThreads)), dim3(kBuildThreads), 0, st, rowDeg,
-                       numRows, rowBits, keysA);
-    TCC_LAUNCH_CHECK();
-    TCC_HIP_CHECK(radix_sort(keysA, keysB, numRows, 32 + rowBits, temp, &sorted, st));
-    hipLaunchKernelGGL(order_rank_kernel, dim3(grid_for(padded, kBuildThreads)), dim3(kBuildThreads), 0, st, sorted,
-                       numRows, padded, rowBits, rowOrderTmp.p, rowRank);
-    TCC_LAUNCH_CHECK();
-    hipLaunchKernelGGL(degree_keys_kernel, dim3(grid_for(numCols, kBuildThreads)), dim3(kBuildThreads), 0, st, colDeg,
-                       numCols, colBits, keysA);
-    TCC_LAUNCH_CHECK();
-    TCC_HIP_CHECK(radix_sort(keysA, keysB, numCols, 32 + colBits, temp, &sorted, st));
-    hipLaunchKernelGGL(order_rank_kernel, dim3(grid_for(numCols, kBuildThreads)), dim3(kBuildThreads), 0, st, sorted,
-                       numCols, numCols, colBits, nullptr, colRank);
-    TCC_LAUNCH_CHECK();
+    TCC_HIP_CHECK(degree_ranks(rowDeg, numRows, padded, rowRank, rowOrderTmp.p, keysA, keysB, temp, st));
+    TCC_HIP_CHECK(degree_ranks(colDeg, numCols, numCols, colRank, nullptr, keysA, keysB, temp, st));
 
     // Error check before the edge keys read the ranks of their indices.
     std::uint32_t hostSmall[4] = {0, 0, 0, 0};
@@ -649,6 +600,7 @@ int tcc_coo_to_sw_bcsr(const std::uint32_t* dRow, const std::uint32_t* dCol, con
     TCC_REQUIRE(hostSmall[0] == 0, TCC_ERR_INVALID_ARGUMENT, "COO index out of range");
 
     std::uint32_t* perm = permA;
+    std::uint64_t* sorted = keysA;
     if (E > 0) {
         hipLaunchKernelGGL(sw_keys_kernel, dim3(grid_for(E, kBuildThreads)), dim3(kBuildThreads), 0, st, dRow, dCol, E,
                            rowRank, colRank, colBits, keysA, permA);

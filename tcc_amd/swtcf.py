@@ -12,7 +12,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from ._lib import BCSC, BCSR, SWBCSR, FeatureSource, SWTCFMatrix, SWTCFWorkspace, check
+from ._lib import BCSC, BCSR, SWBCSR, FeatureSource, Hybrid, SWTCFMatrix, SWTCFWorkspace, check
 
 INVALID_ROW_SLOT = 0xFFFFFFFF
 INVALID_CACHE_SLOT = 0xFF
@@ -389,6 +389,77 @@ def sw_bcsr_spmm_packed(A: SuperWindowBCSR, packed: torch.Tensor, F: int, Y: tor
         Y = torch.empty((A.view.num_rows, F), dtype=torch.float32, device=packed.device)
     check(_lib.lib().tcc_sw_bcsr_spmm_packed(ctypes.byref(A.view), packed.data_ptr(), Y.data_ptr(), F,
                                              int(accumulate), _stream(stream)))
+    return Y
+
+
+class HybridMatrix:
+    """Dense hub tiles (MFMA) + the remainder's BCSR, built on the device by
+    tcc_coo_to_hybrid; owns both allocations."""
+
+    def __init__(self, view: Hybrid):
+        self.view = view
+        self.rest = BlockMatrix("bcsr", view.rest)  # a view: the allocation stays with the hybrid
+
+    def release(self) -> None:
+        if self.view.tilesAllocation or self.view.restAllocation:
+            check(_lib.lib().tcc_hybrid_release(ctypes.byref(self.view)))
+
+    def __del__(self):
+        try:
+            self.release()
+        except Exception:
+            pass
+
+    @property
+    def out_rows(self) -> int:
+        """Rows of Y: 8 per output row window of the remainder's BCSR."""
+        return self.rest.out_windows * 8
+
+    def workspace_bytes(self, F: int) -> int:
+        return int(_lib.lib().tcc_hybrid_workspace_bytes(ctypes.byref(self.view), F))
+
+    def to_host(self) -> dict:
+        torch.cuda.synchronize()
+        t = self.view.tiles
+        RB, T, U = t.num_row_blocks, t.num_tiles, t.num_units
+        return {
+            "rowOrder": _download(t.rowOrder, 16 * RB, np.uint32),
+            "hubColOrder": _download(t.hubColOrder, t.hub_cols, np.uint32),
+            "rowBlockOffset": _download(t.rowBlockOffset, RB + 1, np.uint32),
+            "tileCol": _download(t.tileCol, T, np.uint32),
+            "tileVals": _download(t.tileVals, 256 * T, np.float32).reshape(T, 64, 4),
+            "units": _download(t.units, 3 * U, np.uint32).reshape(U, 3),
+            "num_tiles": T, "num_units": U, "hub_cols": t.hub_cols, "tile_nnz": t.nnz, "unit_tiles": t.unit_tiles,
+            "rest": self.rest.to_host(),
+        }
+
+
+def coo_to_hybrid(row: torch.Tensor, col: torch.Tensor, val: torch.Tensor | None, num_rows: int, num_cols: int,
+                  min_tile_nnz: int = 0, unit_tiles: int = 0, phases: int = 1, stream=None) -> HybridMatrix:
+    """Dense hub tiles + remainder BCSR of the COO matrix (tcc_coo_to_hybrid)."""
+    view = Hybrid()
+    check(_lib.lib().tcc_coo_to_hybrid(_u32(row).data_ptr() if row.numel() else None,
+                                       _u32(col).data_ptr() if col.numel() else None, _ptr(val), row.numel(),
+                                       num_rows, num_cols, int(min_tile_nnz), int(unit_tiles), int(phases),
+                                       ctypes.byref(view), _stream(stream)))
+    return HybridMatrix(view)
+
+
+def hybrid_spmm(H: HybridMatrix, X: torch.Tensor, Y: torch.Tensor | None = None, accumulate: bool = False,
+                workspace: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """Y[out_rows x F] (=|+=) A X (tcc_hybrid_spmm); `workspace` (uint8,
+    at least H.workspace_bytes(F) + 16 bytes) is allocated when not given."""
+    X = _f32(X, "X")
+    F = X.shape[1]
+    if Y is None:
+        Y = torch.empty((H.out_rows, F), dtype=torch.float32, device=X.device)
+    need = H.workspace_bytes(F)
+    if workspace is None:
+        workspace = torch.empty(need + 16, dtype=torch.uint8, device=X.device)
+    base = workspace.data_ptr()
+    shift = (-base) % 16
+    check(_lib.lib().tcc_hybrid_spmm(ctypes.byref(H.view), X.data_ptr(), Y.data_ptr(), F, int(accumulate),
+                                     base + shift, workspace.numel() - shift, _stream(stream)))
     return Y
 
 
