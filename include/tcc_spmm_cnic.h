@@ -273,7 +273,9 @@ int tcc_sw_bcsr_spmm_packed(const tcc_sw_bcsr* A, const void* packedX, float* Y,
  *   tileVals[256t + 4l + s] = A(row l%16, column 4s + l/16) of tile t (the
  *     MFMA A operand of lane l at step s);
  *   units[3u .. 3u+2] = row block, first tile, end tile (at most unit_tiles
- *     tiles); a row block held by more than one unit receives fp32 atomics. */
+ *     tiles, 1..64); a row block held by more than one unit has its units'
+ *     sums stored in the workspace and added into Y by a reduction pass
+ *     (no atomics: the sum order is fixed). */
 typedef struct tcc_hub_tiles {
     uint32_t num_rows;
     uint32_t num_cols;
@@ -299,8 +301,8 @@ typedef struct tcc_hybrid {
 } tcc_hybrid;
 
 /* Build the hybrid of a device COO (row = destination, col = source, no
- * duplicate pairs; dVal may be NULL).  minTileNnz 0 = 32, unitTiles 0 = 32,
- * phases as tcc_coo_to_bcsr_phased for the remainder.  Synchronises
+ * duplicate pairs; dVal may be NULL).  minTileNnz 0 = 32 (at most 256),
+ * unitTiles 0 = 32 (at most 64), phases as tcc_coo_to_bcsr_phased for the remainder.  Synchronises
  * `stream`; free with tcc_hybrid_release. */
 int tcc_coo_to_hybrid(const uint32_t* dRow, const uint32_t* dCol, const float* dVal, uint32_t nnz,
                       uint32_t numRows, uint32_t numCols, uint32_t minTileNnz, uint32_t unitTiles,
@@ -308,8 +310,13 @@ int tcc_coo_to_hybrid(const uint32_t* dRow, const uint32_t* dCol, const float* d
 int tcc_hybrid_release(tcc_hybrid* H);
 
 /* Bytes of device workspace tcc_hybrid_spmm needs for F features: the
- * remainder's packed TF32 rows and the hub columns' TF32 rows. */
+ * remainder's packed TF32 rows and tcc_hub_tiles_workspace_bytes. */
 size_t tcc_hybrid_workspace_bytes(const tcc_hybrid* H, uint32_t featureDim);
+
+/* Bytes of device workspace tcc_hub_tiles_spmm needs for F features: the hub
+ * columns' TF32 rows (hub_cols x roundup(F, 64) floats) and one 16-row
+ * partial sum per unit (num_units x 16 x roundup(F, 64) floats). */
+size_t tcc_hub_tiles_workspace_bytes(const tcc_hub_tiles* T, uint32_t featureDim);
 
 /* Y (=, or += when accumulate != 0) A X for fp32 X [num_cols x F]: the
  * remainder's gather (which writes or adds every row of Y), then the tiles
@@ -319,8 +326,8 @@ size_t tcc_hybrid_workspace_bytes(const tcc_hybrid* H, uint32_t featureDim);
 int tcc_hybrid_spmm(const tcc_hybrid* H, const float* X, float* Y, uint32_t featureDim, int accumulate,
                     void* workspace, size_t workspaceBytes, void* stream);
 
-/* The tiles' part alone: Y[num_rows x F] += A_tiles X (workspace of at
- * least hub_cols * roundup(F, 64) floats, 16-byte aligned). */
+/* The tiles' part alone: Y[num_rows x F] += A_tiles X (workspace 16-byte
+ * aligned, at least tcc_hub_tiles_workspace_bytes(T, F) bytes). */
 int tcc_hub_tiles_spmm(const tcc_hub_tiles* T, const float* X, float* Y, uint32_t featureDim, void* workspace,
                        size_t workspaceBytes, void* stream);
 

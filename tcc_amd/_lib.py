@@ -119,6 +119,7 @@ SIGNATURES = {
     "tcc_coo_to_hybrid": (ctypes.c_int, [vp, vp, vp, u32, u32, u32, u32, u32, u32, ctypes.POINTER(Hybrid), vp]),
     "tcc_hybrid_release": (ctypes.c_int, [ctypes.POINTER(Hybrid)]),
     "tcc_hybrid_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Hybrid), u32]),
+    "tcc_hub_tiles_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(HubTiles), u32]),
     "tcc_hybrid_spmm": (ctypes.c_int, [ctypes.POINTER(Hybrid), vp, vp, u32, ctypes.c_int, vp, ctypes.c_size_t, vp]),
     "tcc_hub_tiles_spmm": (ctypes.c_int, [ctypes.POINTER(HubTiles), vp, vp, u32, vp, ctypes.c_size_t, vp]),
     "tcc_dense_tn_workspace_bytes": (ctypes.c_size_t, [u32, u32, u32]),

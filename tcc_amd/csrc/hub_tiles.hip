@@ -46,6 +46,8 @@ constexpr std::uint32_t kTile = 16;
 constexpr std::uint32_t kTileVals = kTile * kTile;  // floats per tile
 constexpr std::uint32_t kSlice = 64;                // features per wave
 constexpr std::uint32_t kDefaultUnitTiles = 32;
+constexpr std::uint32_t kMaxUnitTiles = 64;         // a unit's tile columns sit one per lane
+constexpr int kStages = 3;                          // tiles in flight per wave, the current one included
 constexpr std::uint32_t kDefaultMinTileNnz = 32;
 constexpr unsigned kThreads = 256;
 
@@ -194,13 +196,54 @@ struct TileArgs {
     const float* Xh;
     std::uint32_t ldh;  // Xh row stride (a multiple of 64)
     float* Y;
+    float* partials;    // [num_units][16][ldh]: sums of the units of shared row blocks
     std::uint32_t F;
     std::uint32_t numUnits;
     std::uint32_t slices;
+    std::uint32_t unitTiles;
 };
 
-// One wave per (unit, 64-feature slice), unit-major: waves of one unit read
-// the same tiles.  Adds A_tiles X into Y.
+// One tile's operands for one wave: A (lane l: A(l%16, 4s + l/16), s = 0..3)
+// and four 4-row steps of Xh (lane l: row 4s + l/16, features 4(l%16)..+3).
+struct TileOperands {
+    f32x4 a;
+    f32x4 b[4];
+};
+
+// Row r (0..15) of row block b in Y, or nullptr for the padding of the
+// last block.
+__device__ __forceinline__ float* y_row(const TileArgs& a, std::uint32_t b, unsigned r) {
+    const std::uint32_t orow = a.rowOrder[static_cast<std::uint64_t>(b) * kTile + r];
+    return orow == TCC_SWTCF_INVALID_ROW_SLOT ? nullptr : a.Y + static_cast<std::uint64_t>(orow) * a.F;
+}
+
+// Y[row][f..f+3] += s (features below F only).
+__device__ __forceinline__ void add_quad(float* row, std::uint32_t f, std::uint32_t F, bool vec, const f32x4& s) {
+    if (!row || f >= F) return;
+    float* out = row + f;
+    if (vec) {
+        f32x4 y = load_global<vf4>(out);
+        y += s;
+        *reinterpret_cast<f32x4*>(out) = y;
+    } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (f + u < F) out[u] += s[u];
+    }
+}
+
+// One wave per (unit of at most 64 tiles of one row block, 64-feature
+// slice), unit-major, so the waves of one unit (one workgroup for F <= 256)
+// read the same tiles.  The unit's tile columns sit one per lane and are read
+// with readlane; operands are loaded NS - 1 tiles ahead into a ring of NS
+// stages, every load unconditional (clamped to the unit's last tile): loads
+// complete in order, so a conditional load, a copy between stages or a
+// branch out of the ring would make the wave wait for the newest one; the
+// last trip's tiles past the unit's end multiply a zero A instead.  A row
+// block held by one unit adds its sums into Y; the units of a shared row
+// block store theirs in `partials` for hub_reduce_kernel (no atomics, and a
+// sum order that does not depend on scheduling).
+template <int NS>
 __global__ void __launch_bounds__(kThreads) hub_tiles_kernel(TileArgs a) {
     const unsigned lane = __lane_id();
     const std::uint32_t w = blockIdx.x * (kThreads / kWave) +
@@ -208,63 +251,97 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_kernel(TileArgs a) {
     const std::uint32_t unit = w / a.slices, slice = w - unit * a.slices;
     if (unit >= a.numUnits) return;
     const std::uint32_t b = a.units[3ull * unit], t0 = a.units[3ull * unit + 1], t1 = a.units[3ull * unit + 2];
+    if (t0 >= t1) return;
     const bool shared = t0 != a.rowBlockOffset[b] || t1 != a.rowBlockOffset[b + 1];
     const std::uint32_t f0 = slice * kSlice;
     const unsigned li = lane & 15u, lk = lane >> 4;
+    const std::uint32_t last = t1 - 1;
+    const int cols = static_cast<int>(a.tileCol[min(t0 + lane, last)]);
     // this lane's B element offset in a 4-row step: row lk, features 4*li..+3
     const float* xb = a.Xh + static_cast<std::uint64_t>(lk) * a.ldh + f0 + 4 * li;
+    const float* av = a.tileVals + 4 * lane;
 
+    auto load = [&](std::uint32_t t, TileOperands& o) {
+        const std::uint32_t col = static_cast<std::uint32_t>(__builtin_amdgcn_readlane(cols, static_cast<int>(t - t0)));
+        o.a = load_global<vf4>(av + static_cast<std::uint64_t>(t) * kTileVals);
+        const float* rb = xb + static_cast<std::uint64_t>(col) * kTile * a.ldh;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) o.b[s] = load_global<vf4>(rb + static_cast<std::uint64_t>(4 * s) * a.ldh);
+    };
     f32x4 acc[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) acc[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    auto load = [&](std::uint32_t t, f32x4& av, f32x4 (&bv)[4]) {
-        av = load_global<vf4>(a.tileVals + static_cast<std::uint64_t>(t) * kTileVals + 4 * lane);
-        const float* rowBase = xb + static_cast<std::uint64_t>(a.tileCol[t]) * kTile * a.ldh;
+    // a tile past the unit's end (the ring's tail) adds A = 0
+    auto mma = [&](const TileOperands& o, bool live) {
 #pragma unroll
-        for (int s = 0; s < 4; ++s) bv[s] = load_global<vf4>(rowBase + static_cast<std::uint64_t>(4 * s) * a.ldh);
+        for (int s = 0; s < 4; ++s) {
+            const float as = live ? o.a[s] : 0.0f;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(as, o.b[s][u], acc[u], 0, 0, 0);
+        }
     };
-    if (t0 < t1) {
-        f32x4 av, bv[4];
-        load(t0, av, bv);
-        for (std::uint32_t t = t0; t < t1; ++t) {
-            f32x4 an = av, bn[4];
+
+    TileOperands ring[NS];
 #pragma unroll
-            for (int s = 0; s < 4; ++s) bn[s] = bv[s];
-            if (t + 1 < t1) load(t + 1, an, bn);
+    for (int j = 0; j < NS - 1; ++j) {
+        load(min(t0 + j, last), ring[j]);
+        __builtin_amdgcn_sched_barrier(0);  // stage j's loads before stage j+1's
+    }
+    for (std::uint32_t t = t0; t < t1; t += NS) {
 #pragma unroll
-            for (int s = 0; s < 4; ++s)
-#pragma unroll
-                for (int u = 0; u < 4; ++u) acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s], bv[s][u], acc[u], 0, 0, 0);
-            av = an;
-#pragma unroll
-            for (int s = 0; s < 4; ++s) bv[s] = bn[s];
+        for (int j = 0; j < NS; ++j) {
+            load(min(t + j + NS - 1, last), ring[(j + NS - 1) % NS]);
+            // keep the loads ahead of the products (the scheduler would
+            // sink them next to their use to save registers)
+            __builtin_amdgcn_sched_barrier(0);
+            mma(ring[j], t + j < t1);
         }
     }
+
     // D(4*lk + v, li) of N tile u: row 16b + 4*lk + v, feature f0 + 4*li + u.
     const std::uint32_t f = f0 + 4 * li;
+    if (shared) {
+        float* p = a.partials + (static_cast<std::uint64_t>(unit) * kTile + 4 * lk) * a.ldh + f;
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+            *reinterpret_cast<f32x4*>(p + static_cast<std::uint64_t>(v) * a.ldh) =
+                f32x4{acc[0][v], acc[1][v], acc[2][v], acc[3][v]};
+        return;
+    }
     const bool vec = a.F % 4 == 0 && (reinterpret_cast<std::uintptr_t>(a.Y) & 15u) == 0;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-        const std::uint32_t orow = a.rowOrder[static_cast<std::uint64_t>(b) * kTile + 4 * lk + v];
-        if (orow == TCC_SWTCF_INVALID_ROW_SLOT || f >= a.F) continue;
-        float* out = a.Y + static_cast<std::uint64_t>(orow) * a.F + f;
-        if (shared) {
+    for (int v = 0; v < 4; ++v)
+        add_quad(y_row(a, b, 4 * lk + v), f, a.F, vec, f32x4{acc[0][v], acc[1][v], acc[2][v], acc[3][v]});
+}
+
+// Y rows of a shared row block += the sum of its units' partials, one
+// workgroup per (unit, slice) of which only the row block's first unit
+// works: thread q sums row q/16, features 4(q%16)..+3 of the slice over the
+// block's units (ceil(tiles / unitTiles) of them, consecutive), eight loads
+// in flight.
+__global__ void __launch_bounds__(kThreads) hub_reduce_kernel(TileArgs a) {
+    const std::uint32_t unit = blockIdx.x / a.slices, slice = blockIdx.x - unit * a.slices;
+    const std::uint32_t b = a.units[3ull * unit], t0 = a.units[3ull * unit + 1];
+    const std::uint32_t tb0 = a.rowBlockOffset[b], tb1 = a.rowBlockOffset[b + 1];
+    if (t0 != tb0 || a.units[3ull * unit + 2] == tb1) return;  // not the first unit of a shared row block
+    const std::uint32_t nu = (tb1 - tb0 + a.unitTiles - 1) / a.unitTiles;
+    const unsigned r = threadIdx.x / 16, q = threadIdx.x % 16;
+    const std::uint32_t f = slice * kSlice + 4 * q;
+    const float* p = a.partials + (static_cast<std::uint64_t>(unit) * kTile + r) * a.ldh + f;
+    const std::uint64_t stride = static_cast<std::uint64_t>(kTile) * a.ldh;
+    constexpr std::uint32_t kIn = 8;
+    f32x4 s[kIn];
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
-                if (f + u < a.F) atomic_add_f32(out + u, acc[u][v]);
-        } else if (vec) {
-            float4 y = *reinterpret_cast<const float4*>(out);
-            y.x += acc[0][v];
-            y.y += acc[1][v];
-            y.z += acc[2][v];
-            y.w += acc[3][v];
-            *reinterpret_cast<float4*>(out) = y;
-        } else {
+    for (std::uint32_t j = 0; j < kIn; ++j) s[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    std::uint32_t k = 0;
+    for (; k + kIn <= nu; k += kIn)
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
-                if (f + u < a.F) out[u] += acc[u][v];
-        }
-    }
+        for (std::uint32_t j = 0; j < kIn; ++j) s[j] += load_global<vf4>(p + (k + j) * stride);
+    for (; k < nu; ++k) s[0] += load_global<vf4>(p + k * stride);
+#pragma unroll
+    for (std::uint32_t j = 1; j < kIn; ++j) s[0] += s[j];
+    const bool vec = a.F % 4 == 0 && (reinterpret_cast<std::uintptr_t>(a.Y) & 15u) == 0;
+    add_quad(y_row(a, b, r), f, a.F, vec, s[0]);
 }
 
 inline std::uint32_t hub_ldh(std::uint32_t F) { return (F + kSlice - 1) / kSlice * kSlice; }
@@ -294,6 +371,7 @@ int tcc_coo_to_hybrid(const std::uint32_t* dRow, const std::uint32_t* dCol, cons
     if (minTileNnz == 0) minTileNnz = kDefaultMinTileNnz;
     if (unitTiles == 0) unitTiles = kDefaultUnitTiles;
     TCC_REQUIRE(minTileNnz <= kTileVals, TCC_ERR_INVALID_ARGUMENT, "hybrid: minTileNnz above 256 leaves no tile");
+    TCC_REQUIRE(unitTiles <= kMaxUnitTiles, TCC_ERR_INVALID_ARGUMENT, "hybrid: unitTiles above 64");
     const hipStream_t st = as_stream(stream);
     std::memset(out, 0, sizeof(*out));
     const std::uint32_t E = nnz;
@@ -476,7 +554,14 @@ int tcc_coo_to_hybrid(const std::uint32_t* dRow, const std::uint32_t* dCol, cons
 size_t tcc_hybrid_workspace_bytes(const tcc_hybrid* H, std::uint32_t featureDim) {
     if (!H || featureDim == 0) return 0;
     return align_up(tcc_tf32_packed_bytes(H->rest.num_cols, featureDim) + 16) +
-           static_cast<size_t>(H->tiles.hub_cols) * hub_ldh(featureDim) * sizeof(float);
+           tcc_hub_tiles_workspace_bytes(&H->tiles, featureDim);
+}
+
+size_t tcc_hub_tiles_workspace_bytes(const tcc_hub_tiles* T, std::uint32_t featureDim) {
+    if (!T || featureDim == 0) return 0;
+    const std::size_t ldh = hub_ldh(featureDim);
+    return align_up(static_cast<size_t>(T->hub_cols) * ldh * sizeof(float)) +
+           static_cast<size_t>(T->num_units) * kTile * ldh * sizeof(float);
 }
 
 int tcc_hub_tiles_spmm(const tcc_hub_tiles* T, const float* X, float* Y, std::uint32_t featureDim, void* workspace,
@@ -487,9 +572,11 @@ int tcc_hub_tiles_spmm(const tcc_hub_tiles* T, const float* X, float* Y, std::ui
     if (T->num_units == 0) return TCC_OK;
     TCC_REQUIRE(T->tileCol && T->tileVals && T->units && T->hubColOrder, TCC_ERR_INVALID_ARGUMENT,
                 "invalid hub tiles SpMM arguments");
+    TCC_REQUIRE(T->unit_tiles >= 1 && T->unit_tiles <= kMaxUnitTiles, TCC_ERR_INVALID_ARGUMENT,
+                "hub tiles: unit_tiles must be 1..64");
     const std::uint32_t ldh = hub_ldh(featureDim);
-    const std::uint64_t need = static_cast<std::uint64_t>(T->hub_cols) * ldh * sizeof(float);
-    TCC_REQUIRE(workspace && workspaceBytes >= need && reinterpret_cast<std::uintptr_t>(workspace) % 16 == 0,
+    TCC_REQUIRE(workspace && workspaceBytes >= tcc_hub_tiles_workspace_bytes(T, featureDim) &&
+                    reinterpret_cast<std::uintptr_t>(workspace) % 16 == 0,
                 TCC_ERR_INVALID_ARGUMENT, "hub tiles SpMM workspace too small or misaligned");
     const hipStream_t st = as_stream(stream);
     float* Xh = static_cast<float*>(workspace);
@@ -506,12 +593,16 @@ int tcc_hub_tiles_spmm(const tcc_hub_tiles* T, const float* X, float* Y, std::ui
     a.Xh = Xh;
     a.ldh = ldh;
     a.Y = Y;
+    a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + align_up(n * sizeof(float)));
     a.F = featureDim;
     a.numUnits = T->num_units;
     a.slices = ldh / kSlice;
+    a.unitTiles = T->unit_tiles;
     const std::uint64_t waves = static_cast<std::uint64_t>(a.numUnits) * a.slices;
     TCC_REQUIRE(waves <= 0x7FFFFFFFull, TCC_ERR_UNSUPPORTED, "hub tiles SpMM launch too large");
-    hipLaunchKernelGGL(hub_tiles_kernel, dim3(grid_for(waves, kThreads / kWave)), dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL(hub_tiles_kernel<kStages>, dim3(grid_for(waves, kThreads / kWave)), dim3(kThreads), 0, st, a);
+    TCC_LAUNCH_CHECK();
+    hipLaunchKernelGGL(hub_reduce_kernel, dim3(static_cast<std::uint32_t>(waves)), dim3(kThreads), 0, st, a);
     TCC_LAUNCH_CHECK();
     return TCC_OK;
 }

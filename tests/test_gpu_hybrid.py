@@ -10,7 +10,8 @@ Checked through the C-ABI:
   exactly those entries;
 - the products against the fp64 CSR oracle on TF32-rounded inputs (rel-L2
   <= 1e-5), Y = AX and Y += AX, over thresholds from 1 (every tile dense) to
-  256 (no tile dense), shared row blocks (unit_tiles 1: atomics), phased
+  256 (no tile dense), row blocks shared by up to hundreds of units (their
+  partial sums reduced in a second pass), unit sizes 1 to 64, phased
   remainders, F from 1 to 700, values or none, hubs or uniform;
 - no edges, duplicate edges and out-of-range indices.
 """
@@ -150,6 +151,7 @@ CASES = [
     (64, 64, 4096, False, 64, 0, 1, True, 1),
     (64, 64, 4096, False, 64, 1, 1, False, 3),
     (777, 1500, 40000, True, 16, 5, 2, True, 700),
+    (400, 2000, 60000, True, 4, 64, 1, True, 130),   # 64-tile units, long shared row blocks
     (60, 60, 0, False, 32, 0, 1, True, 64),
 ]
 
@@ -193,6 +195,9 @@ def test_hybrid_errors(gpu):
         swtcf.coo_to_hybrid(dev_u32(np.array([0, 9], np.uint32)), dev_u32(np.array([0, 1], np.uint32)), None, 4, 4)
     with pytest.raises(_lib.TccError, match="out of range"):
         swtcf.coo_to_hybrid(dev_u32(np.array([0, 1], np.uint32)), dev_u32(np.array([0, 4], np.uint32)), None, 4, 4)
+    with pytest.raises(_lib.TccError, match="unitTiles above 64"):
+        swtcf.coo_to_hybrid(dev_u32(np.array([0], np.uint32)), dev_u32(np.array([1], np.uint32)), None, 4, 4,
+                            unit_tiles=65)
     H = swtcf.coo_to_hybrid(dev_u32(np.array([0], np.uint32)), dev_u32(np.array([1], np.uint32)), None, 4, 4)
     X = torch.ones(4, 8, device="cuda")
     small = torch.empty(8, dtype=torch.uint8, device="cuda")
