@@ -266,31 +266,38 @@ int tcc_sw_bcsr_spmm_packed(const tcc_sw_bcsr* A, const void* packedX, float* Y,
  * minTileNnz entries are stored densely (TF32-rounded values, zeros
  * included) and multiplied with fp32 MFMA (v_mfma_f32_16x16x4f32), the other
  * entries form an ordinary or phased BCSR (`rest`) for the gather kernels.
- *   rowOrder[16b + i]: original row of row i of row block b (0xFFFFFFFF past
- *     num_rows); hubColOrder[r]: original column of column rank r < hub_cols;
- *   row block b's tiles are [rowBlockOffset[b], rowBlockOffset[b+1]); tile t
- *     covers column ranks 16*tileCol[t] .. +15;
- *   tileVals[256t + 4l + s] = A(row l%16, column 4s + l/16) of tile t (the
- *     MFMA A operand of lane l at step s);
- *   units[3u .. 3u+2] = row block, first tile, end tile (at most unit_tiles
- *     tiles, 1..64); a row block held by more than one unit has its units'
- *     sums stored in the workspace and added into Y by a reduction pass
- *     (no atomics: the sum order is fixed). */
+ * Row blocks (16 rows) are grouped G at a time; a step of a group is a
+ * column block where at least one of its G tiles is dense, and holds all G
+ * (zeros for the tiles that are not), so that one load of the step's 16
+ * feature rows serves G tiles.
+ *   rowOrder[16(G g + j) + i]: original row of row i of row block j of group
+ *     g (0xFFFFFFFF past num_rows); hubColOrder[r]: original column of column
+ *     rank r < hub_cols;
+ *   group g's steps are [groupStepOffset[g], groupStepOffset[g+1]); step p
+ *     covers column ranks 16*stepCol[p] .. +15;
+ *   tileVals[256(G p + j) + 4l + s] = A(row l%16, column 4s + l/16) of the
+ *     tile of row block j at step p (the MFMA A operand of lane l at step s);
+ *   units[3u .. 3u+2] = group, first step, end step (at most unit_steps
+ *     steps, 1..64); a group held by more than one unit has its units' sums
+ *     stored in the workspace and added into Y by a reduction pass (no
+ *     atomics: the sum order is fixed). */
 typedef struct tcc_hub_tiles {
     uint32_t num_rows;
     uint32_t num_cols;
-    uint32_t nnz;                   /* entries held in the tiles */
-    uint32_t num_row_blocks;        /* ceil(num_rows / 16) */
-    uint32_t num_tiles;
+    uint32_t nnz;                    /* entries held in the tiles */
+    uint32_t group_blocks;           /* G: row blocks per group, 1, 2, 4 or 8 */
+    uint32_t num_groups;             /* ceil(ceil(num_rows / 16) / G) */
+    uint32_t num_steps;
+    uint32_t num_tiles;              /* dense tiles (at most G * num_steps) */
     uint32_t num_units;
-    uint32_t unit_tiles;
-    uint32_t hub_cols;              /* column ranks the tiles cover: [0, hub_cols) */
-    const uint32_t* rowOrder;       /* [16*num_row_blocks] */
-    const uint32_t* hubColOrder;    /* [hub_cols] */
-    const uint32_t* rowBlockOffset; /* [num_row_blocks+1] */
-    const uint32_t* tileCol;        /* [num_tiles] */
-    const float* tileVals;          /* [256*num_tiles] */
-    const uint32_t* units;          /* [3*num_units] */
+    uint32_t unit_steps;
+    uint32_t hub_cols;               /* column ranks the tiles cover: [0, hub_cols) */
+    const uint32_t* rowOrder;        /* [16*G*num_groups] */
+    const uint32_t* hubColOrder;     /* [hub_cols] */
+    const uint32_t* groupStepOffset; /* [num_groups+1] */
+    const uint32_t* stepCol;         /* [num_steps] */
+    const float* tileVals;           /* [256*G*(num_steps+1)]: the last step zeros */
+    const uint32_t* units;           /* [3*num_units] */
 } tcc_hub_tiles;
 
 typedef struct tcc_hybrid {
@@ -302,11 +309,12 @@ typedef struct tcc_hybrid {
 
 /* Build the hybrid of a device COO (row = destination, col = source, no
  * duplicate pairs; dVal may be NULL).  minTileNnz 0 = 32 (at most 256),
- * unitTiles 0 = 32 (at most 64), phases as tcc_coo_to_bcsr_phased for the remainder.  Synchronises
- * `stream`; free with tcc_hybrid_release. */
+ * groupBlocks 0 = 4 (1, 2, 4 or 8), unitSteps 0 = 32 (at most 64), phases
+ * as tcc_coo_to_bcsr_phased for the remainder.  Synchronises `stream`; free
+ * with tcc_hybrid_release. */
 int tcc_coo_to_hybrid(const uint32_t* dRow, const uint32_t* dCol, const float* dVal, uint32_t nnz,
-                      uint32_t numRows, uint32_t numCols, uint32_t minTileNnz, uint32_t unitTiles,
-                      uint32_t phases, tcc_hybrid* out, void* stream);
+                      uint32_t numRows, uint32_t numCols, uint32_t minTileNnz, uint32_t groupBlocks,
+                      uint32_t unitSteps, uint32_t phases, tcc_hybrid* out, void* stream);
 int tcc_hybrid_release(tcc_hybrid* H);
 
 /* Bytes of device workspace tcc_hybrid_spmm needs for F features: the
@@ -314,8 +322,8 @@ int tcc_hybrid_release(tcc_hybrid* H);
 size_t tcc_hybrid_workspace_bytes(const tcc_hybrid* H, uint32_t featureDim);
 
 /* Bytes of device workspace tcc_hub_tiles_spmm needs for F features: the hub
- * columns' TF32 rows (hub_cols x roundup(F, 64) floats) and one 16-row
- * partial sum per unit (num_units x 16 x roundup(F, 64) floats). */
+ * columns' TF32 rows (hub_cols x roundup(F, 64) floats) and one 16G-row
+ * partial sum per unit (num_units x 16G x roundup(F, 64) floats). */
 size_t tcc_hub_tiles_workspace_bytes(const tcc_hub_tiles* T, uint32_t featureDim);
 
 /* Y (=, or += when accumulate != 0) A X for fp32 X [num_cols x F]: the

@@ -421,27 +421,29 @@ class HybridMatrix:
     def to_host(self) -> dict:
         torch.cuda.synchronize()
         t = self.view.tiles
-        RB, T, U = t.num_row_blocks, t.num_tiles, t.num_units
+        G, NG, S, U = t.group_blocks, t.num_groups, t.num_steps, t.num_units
         return {
-            "rowOrder": _download(t.rowOrder, 16 * RB, np.uint32),
+            "rowOrder": _download(t.rowOrder, 16 * G * NG, np.uint32),
             "hubColOrder": _download(t.hubColOrder, t.hub_cols, np.uint32),
-            "rowBlockOffset": _download(t.rowBlockOffset, RB + 1, np.uint32),
-            "tileCol": _download(t.tileCol, T, np.uint32),
-            "tileVals": _download(t.tileVals, 256 * T, np.float32).reshape(T, 64, 4),
+            "groupStepOffset": _download(t.groupStepOffset, NG + 1, np.uint32),
+            "stepCol": _download(t.stepCol, S, np.uint32),
+            "tileVals": _download(t.tileVals, 256 * G * S, np.float32).reshape(S, G, 64, 4),
             "units": _download(t.units, 3 * U, np.uint32).reshape(U, 3),
-            "num_tiles": T, "num_units": U, "hub_cols": t.hub_cols, "tile_nnz": t.nnz, "unit_tiles": t.unit_tiles,
+            "group_blocks": G, "num_groups": NG, "num_steps": S, "num_tiles": t.num_tiles, "num_units": U,
+            "hub_cols": t.hub_cols, "tile_nnz": t.nnz, "unit_steps": t.unit_steps,
             "rest": self.rest.to_host(),
         }
 
 
 def coo_to_hybrid(row: torch.Tensor, col: torch.Tensor, val: torch.Tensor | None, num_rows: int, num_cols: int,
-                  min_tile_nnz: int = 0, unit_tiles: int = 0, phases: int = 1, stream=None) -> HybridMatrix:
+                  min_tile_nnz: int = 0, group_blocks: int = 0, unit_steps: int = 0, phases: int = 1,
+                  stream=None) -> HybridMatrix:
     """Dense hub tiles + remainder BCSR of the COO matrix (tcc_coo_to_hybrid)."""
     view = Hybrid()
     check(_lib.lib().tcc_coo_to_hybrid(_u32(row).data_ptr() if row.numel() else None,
                                        _u32(col).data_ptr() if col.numel() else None, _ptr(val), row.numel(),
-                                       num_rows, num_cols, int(min_tile_nnz), int(unit_tiles), int(phases),
-                                       ctypes.byref(view), _stream(stream)))
+                                       num_rows, num_cols, int(min_tile_nnz), int(group_blocks), int(unit_steps),
+                                       int(phases), ctypes.byref(view), _stream(stream)))
     return HybridMatrix(view)
 
 

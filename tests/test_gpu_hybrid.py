@@ -4,13 +4,15 @@ Checked through the C-ABI:
 - the arrays, exactly, against an independent numpy construction of the
   layout include/tcc_spmm_cnic.h states: rows and columns ranked by degree
   (descending, then index); 16x16 tiles of the reordered matrix with at
-  least min_tile_nnz entries, sorted by (row block, column block); values
-  TF32-rounded at A(row l%16, column 4s + l/16) -> tileVals[t][l][s]; units
-  of unit_tiles tiles; the other entries' BCSR equal to the oracle's BCSR of
-  exactly those entries;
+  least min_tile_nnz entries; steps = the (group of G row blocks, column
+  block) pairs holding one, sorted; values TF32-rounded at A(row l%16,
+  column 4s + l/16) -> tileVals[step][row block % G][l][s], zeros in the
+  other slots; units of unit_steps steps; the other entries' BCSR equal to
+  the oracle's BCSR of exactly those entries;
 - the products against the fp64 CSR oracle on TF32-rounded inputs (rel-L2
   <= 1e-5), Y = AX and Y += AX, over thresholds from 1 (every tile dense) to
-  256 (no tile dense), row blocks shared by up to hundreds of units (their
+  256 (no tile dense), groups of 1, 2, 4 and 8 row blocks (row counts that
+  leave the last group partly empty), groups shared by many units (their
   partial sums reduced in a second pass), unit sizes 1 to 64, phased
   remainders, F from 1 to 700, values or none, hubs or uniform;
 - no edges, duplicate edges and out-of-range indices.
@@ -56,7 +58,7 @@ def tf32(a):
     return np.where(fin, (b + 0x1000) & 0xFFFFE000, b).astype(np.uint32).view(np.float32)
 
 
-def reference_layout(dst, src, vals, nr, nc, min_nnz, unit_tiles):
+def reference_layout(dst, src, vals, nr, nc, min_nnz, G, unit_steps):
     dst = dst.astype(np.int64)
     src = src.astype(np.int64)
     rorder = np.lexsort((np.arange(nr), -np.bincount(dst, minlength=nr)))
@@ -66,29 +68,33 @@ def reference_layout(dst, src, vals, nr, nc, min_nnz, unit_tiles):
     crank = np.empty(nc, np.int64)
     crank[corder] = np.arange(nc)
     RB, CB = (nr + 15) // 16, (nc + 15) // 16
-    row_order = np.full(16 * RB, 0xFFFFFFFF, np.uint32)
+    NG = (RB + G - 1) // G
+    row_order = np.full(16 * G * NG, 0xFFFFFFFF, np.uint32)
     row_order[:nr] = rorder
     rr, cr = rrank[dst], crank[src]
-    tile = (rr // 16) * CB + cr // 16
+    rb, cb = rr // 16, cr // 16
+    tile = rb * CB + cb
     keys, counts = np.unique(tile, return_counts=True)
     dense_keys = keys[counts >= min_nnz]
     in_dense = np.isin(tile, dense_keys)
-    tid = np.searchsorted(dense_keys, tile[in_dense])
+    step_keys = np.unique((dense_keys // CB) // G * CB + dense_keys % CB)  # (group, column block), sorted
+    S = step_keys.size
+    sid = np.searchsorted(step_keys, (rb[in_dense] // G) * CB + cb[in_dense])
     vals_all = np.ones(dst.size, np.float32) if vals is None else vals
-    tv = np.zeros((dense_keys.size, 64, 4), np.float32)
+    tv = np.zeros((S, G, 64, 4), np.float32)
     i, j = rr[in_dense] % 16, cr[in_dense] % 16
-    tv[tid, i + 16 * (j % 4), j // 4] = tf32(vals_all[in_dense])
-    rb, cb = dense_keys // CB, dense_keys % CB
-    rbo = np.searchsorted(rb, np.arange(RB + 1)).astype(np.uint32)
+    tv[sid, rb[in_dense] % G, i + 16 * (j % 4), j // 4] = tf32(vals_all[in_dense])
+    sg, sc = step_keys // CB, step_keys % CB
+    gso = np.searchsorted(sg, np.arange(NG + 1)).astype(np.uint32)
     units = []
-    for b in range(RB):
-        t0, t1 = int(rbo[b]), int(rbo[b + 1])
-        for k in range(-(-(t1 - t0) // unit_tiles)):
-            units.append((b, t0 + k * unit_tiles, min(t0 + (k + 1) * unit_tiles, t1)))
-    hub_cols = min(16 * (int(cb.max()) + 1), nc) if cb.size else 0
-    return dict(rowOrder=row_order, hubColOrder=corder[:hub_cols].astype(np.uint32), rowBlockOffset=rbo,
-                tileCol=cb.astype(np.uint32), tileVals=tv, units=np.array(units, np.uint32).reshape(-1, 3),
-                hub_cols=hub_cols, rest=~in_dense)
+    for g in range(NG):
+        p0, p1 = int(gso[g]), int(gso[g + 1])
+        for k in range(-(-(p1 - p0) // unit_steps)):
+            units.append((g, p0 + k * unit_steps, min(p0 + (k + 1) * unit_steps, p1)))
+    hub_cols = min(16 * (int(sc.max()) + 1), nc) if S else 0
+    return dict(rowOrder=row_order, hubColOrder=corder[:hub_cols].astype(np.uint32), groupStepOffset=gso,
+                stepCol=sc.astype(np.uint32), tileVals=tv, units=np.array(units, np.uint32).reshape(-1, 3),
+                hub_cols=hub_cols, num_tiles=int(dense_keys.size), rest=~in_dense)
 
 
 def oracle_product(oracle, dst, src, vals, nr, X):
@@ -98,26 +104,29 @@ def oracle_product(oracle, dst, src, vals, nr, X):
     return oracle.csr_spmm(rowptr, src[order], None if vals is None else vals[order], X, use_tf32=True)
 
 
-@pytest.mark.parametrize("nr, nc, nnz, hubs, min_nnz, unit_tiles, values", [
-    (500, 700, 30000, True, 32, 4, True),
-    (500, 700, 30000, True, 8, 0, False),
-    (129, 33, 2000, False, 1, 3, True),      # every occupied tile dense
-    (300, 300, 5000, True, 256, 0, True),    # no tile dense: all in the remainder
-    (17, 1000, 3000, True, 20, 1, True),
-    (60, 60, 0, False, 32, 0, True),
+@pytest.mark.parametrize("nr, nc, nnz, hubs, min_nnz, G, unit_steps, values", [
+    (500, 700, 30000, True, 32, 4, 4, True),
+    (500, 700, 30000, True, 8, 8, 0, False),
+    (129, 33, 2000, False, 1, 2, 3, True),     # every occupied tile dense; a partly empty last group
+    (300, 300, 5000, True, 256, 4, 0, True),   # no tile dense: all in the remainder
+    (17, 1000, 3000, True, 20, 1, 1, True),
+    (40, 900, 9000, True, 6, 8, 64, True),     # fewer rows than one group
+    (60, 60, 0, False, 32, 0, 0, True),
 ])
-def test_arrays_match_numpy_layout(gpu, oracle, nr, nc, nnz, hubs, min_nnz, unit_tiles, values):
+def test_arrays_match_numpy_layout(gpu, oracle, nr, nc, nnz, hubs, min_nnz, G, unit_steps, values):
     from tcc_amd import swtcf
 
     dst, src = random_coo(nr, nc, nnz, nr * 3 + nc + nnz, hubs)
     vals = np.random.default_rng(9).uniform(-1, 1, dst.size).astype(np.float32) if values else None
     H = swtcf.coo_to_hybrid(dev_u32(dst), dev_u32(src), None if vals is None else torch.from_numpy(vals).cuda(), nr, nc,
-                            min_tile_nnz=min_nnz, unit_tiles=unit_tiles)
+                            min_tile_nnz=min_nnz, group_blocks=G, unit_steps=unit_steps)
     h = H.to_host()
-    want = reference_layout(dst, src, vals, nr, nc, min_nnz, unit_tiles or 32)
-    print(f"hybrid layout nr={nr} nc={nc} nnz={nnz}: {h['num_tiles']} tiles, {h['tile_nnz']} tile entries", flush=True)
-    assert h["hub_cols"] == want["hub_cols"] and h["unit_tiles"] == (unit_tiles or 32)
-    for k in ("rowOrder", "hubColOrder", "rowBlockOffset", "tileCol", "units"):
+    want = reference_layout(dst, src, vals, nr, nc, min_nnz, G or 4, unit_steps or 32)
+    print(f"hybrid layout nr={nr} nc={nc} nnz={nnz} G={G}: {h['num_steps']} steps, {h['num_tiles']} tiles, "
+          f"{h['tile_nnz']} tile entries", flush=True)
+    assert h["group_blocks"] == (G or 4) and h["unit_steps"] == (unit_steps or 32)
+    assert h["hub_cols"] == want["hub_cols"] and h["num_tiles"] == want["num_tiles"]
+    for k in ("rowOrder", "hubColOrder", "groupStepOffset", "stepCol", "units"):
         assert np.array_equal(h[k], want[k]), k
     assert np.array_equal(h["tileVals"], want["tileVals"])
     assert h["tile_nnz"] == int((~want["rest"]).sum())
@@ -140,34 +149,35 @@ def test_arrays_match_numpy_layout(gpu, oracle, nr, nc, nnz, hubs, min_nnz, unit
 
 
 CASES = [
-    # nr, nc, nnz, hubs, min_nnz, unit_tiles, phases, values, F
-    (500, 700, 30000, True, 32, 0, 1, True, 602),
-    (500, 700, 30000, True, 32, 1, 4, True, 602),
-    (500, 700, 30000, True, 8, 3, 1, False, 90),
-    (1000, 900, 60000, True, 24, 0, 4, True, 256),
-    (1000, 900, 60000, True, 24, 2, 1, True, 257),
-    (129, 33, 2000, False, 1, 3, 1, True, 64),
-    (300, 300, 5000, True, 256, 0, 1, True, 100),
-    (64, 64, 4096, False, 64, 0, 1, True, 1),
-    (64, 64, 4096, False, 64, 1, 1, False, 3),
-    (777, 1500, 40000, True, 16, 5, 2, True, 700),
-    (400, 2000, 60000, True, 4, 64, 1, True, 130),   # 64-tile units, long shared row blocks
-    (60, 60, 0, False, 32, 0, 1, True, 64),
+    # nr, nc, nnz, hubs, min_nnz, G, unit_steps, phases, values, F
+    (500, 700, 30000, True, 32, 4, 0, 1, True, 602),
+    (500, 700, 30000, True, 32, 4, 1, 4, True, 602),
+    (500, 700, 30000, True, 8, 2, 3, 1, False, 90),
+    (1000, 900, 60000, True, 24, 8, 0, 4, True, 256),
+    (1000, 900, 60000, True, 24, 1, 2, 1, True, 257),
+    (129, 33, 2000, False, 1, 8, 3, 1, True, 64),
+    (300, 300, 5000, True, 256, 4, 0, 1, True, 100),
+    (64, 64, 4096, False, 64, 4, 0, 1, True, 1),
+    (64, 64, 4096, False, 64, 2, 1, 1, False, 3),
+    (777, 1500, 40000, True, 16, 4, 5, 2, True, 700),
+    (400, 2000, 60000, True, 4, 8, 64, 1, True, 130),   # 64-step units, long shared groups
+    (40, 900, 9000, True, 6, 8, 7, 1, True, 48),        # fewer rows than one group
+    (60, 60, 0, False, 32, 4, 0, 1, True, 64),
 ]
 
 
-@pytest.mark.parametrize("nr, nc, nnz, hubs, min_nnz, unit_tiles, phases, values, F", CASES)
-def test_hybrid_spmm_vs_oracle(gpu, oracle, nr, nc, nnz, hubs, min_nnz, unit_tiles, phases, values, F):
+@pytest.mark.parametrize("nr, nc, nnz, hubs, min_nnz, G, unit_steps, phases, values, F", CASES)
+def test_hybrid_spmm_vs_oracle(gpu, oracle, nr, nc, nnz, hubs, min_nnz, G, unit_steps, phases, values, F):
     from tcc_amd import swtcf
 
-    print(f"hybrid nr={nr} nc={nc} nnz={nnz} min_nnz={min_nnz} unit_tiles={unit_tiles} phases={phases} "
+    print(f"hybrid nr={nr} nc={nc} nnz={nnz} min_nnz={min_nnz} G={G} unit_steps={unit_steps} phases={phases} "
           f"values={values} F={F}", flush=True)
     dst, src = random_coo(nr, nc, nnz, 5 * nr + nc + F, hubs)
     rng = np.random.default_rng(F + nnz + min_nnz)
     vals = rng.uniform(-1, 1, dst.size).astype(np.float32) if values else None
     X = rng.standard_normal((nc, F)).astype(np.float32)
     H = swtcf.coo_to_hybrid(dev_u32(dst), dev_u32(src), None if vals is None else torch.from_numpy(vals).cuda(), nr, nc,
-                            min_tile_nnz=min_nnz, unit_tiles=unit_tiles, phases=phases)
+                            min_tile_nnz=min_nnz, group_blocks=G, unit_steps=unit_steps, phases=phases)
     Xd = torch.from_numpy(X).cuda()
     Y = swtcf.hybrid_spmm(H, Xd)
     want = oracle_product(oracle, dst, src, vals, nr, X)
@@ -195,9 +205,12 @@ def test_hybrid_errors(gpu):
         swtcf.coo_to_hybrid(dev_u32(np.array([0, 9], np.uint32)), dev_u32(np.array([0, 1], np.uint32)), None, 4, 4)
     with pytest.raises(_lib.TccError, match="out of range"):
         swtcf.coo_to_hybrid(dev_u32(np.array([0, 1], np.uint32)), dev_u32(np.array([0, 4], np.uint32)), None, 4, 4)
-    with pytest.raises(_lib.TccError, match="unitTiles above 64"):
+    with pytest.raises(_lib.TccError, match="unitSteps above 64"):
         swtcf.coo_to_hybrid(dev_u32(np.array([0], np.uint32)), dev_u32(np.array([1], np.uint32)), None, 4, 4,
-                            unit_tiles=65)
+                            unit_steps=65)
+    with pytest.raises(_lib.TccError, match="groupBlocks"):
+        swtcf.coo_to_hybrid(dev_u32(np.array([0], np.uint32)), dev_u32(np.array([1], np.uint32)), None, 4, 4,
+                            group_blocks=3)
     H = swtcf.coo_to_hybrid(dev_u32(np.array([0], np.uint32)), dev_u32(np.array([1], np.uint32)), None, 4, 4)
     X = torch.ones(4, 8, device="cuda")
     small = torch.empty(8, dtype=torch.uint8, device="cuda")
