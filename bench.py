@@ -54,6 +54,14 @@ PACK_MIN_REUSE = 16.0
 # with 2).
 PHASE_MIN_BLOCKS_PER_WINDOW = 64.0
 PHASES = 4
+# The same long-window (skewed) graphs hold a dense core once rows and
+# columns are ordered by degree: 16x16 tiles of at least HUB_MIN_TILE_NNZ
+# entries go to fp32 MFMA in groups of HUB_GROUP_BLOCKS row blocks, the rest
+# to the phased gather (measured at config 3: 17.35 ms phased gather alone ->
+# 13.4 ms; thresholds 16 / 24 / 32 / 64 -> 13.8 / 14.9 / 13.5 / 14.6 ms,
+# groups 1 / 2 / 4 / 8 -> 14.2 / 13.7 / 13.5 / 14.5 ms).
+HUB_MIN_TILE_NNZ = 32
+HUB_GROUP_BLOCKS = 4
 CPU_SAMPLE_NNZ = 16_000_000
 
 WORKLOADS = {
@@ -78,7 +86,12 @@ def parse(argv=None):
     p.add_argument("--cpu-threads", type=int, default=0, help="0 = all host cores")
     p.add_argument("--copy-calibration-mib", type=int, default=0,
                    help="first run one plain device copy of this many MiB (scale for rocprofv3 FETCH/WRITE_SIZE)")
+    p.add_argument("--profile-step", action="store_true",
+                   help="for counter runs: only the timed step's kernels run (warmup + steps times); no CPU "
+                        "baseline, comparisons, conversions or extra configs")
     args = p.parse_args(argv)
+    if args.profile_step:
+        args.no_cpu_baseline = args.no_extra = True
     # A config-2 step is ~80 us: 500 of them time 40 ms of steady-state work
     # (50 took 4 ms, short enough for the clock ramp to show).
     short = args.config in (1, 2)
@@ -324,6 +337,7 @@ def bench_spmm(args, torch, swtcf, cfg):
         extra["row_reuse"] = round(reuse, 2)
         per_window = A.view.num_TCBlocks / max(1, A.view.num_rowWindows)
         extra["blocks_per_window"] = round(per_window, 1)
+        H = None
         if per_window >= PHASE_MIN_BLOCKS_PER_WINDOW:
             # long windows: the phased BCSR of the same COO, built once
             t_p = time.perf_counter()
@@ -333,9 +347,40 @@ def bench_spmm(args, torch, swtcf, cfg):
             extra["phases"] = PHASES
             A.release()
             A = Ap
+            # ... and the hybrid: dense hub tiles on MFMA + the phased gather of the rest
+            t_h = time.perf_counter()
+            H = swtcf.coo_to_hybrid(r32, c32, vals, n, n, min_tile_nnz=HUB_MIN_TILE_NNZ,
+                                    group_blocks=HUB_GROUP_BLOCKS, phases=PHASES)
+            torch.cuda.synchronize()
+            extra["hybrid_build_ms"] = round((time.perf_counter() - t_h) * 1e3, 3)
+            t = H.view.tiles
+            extra["hub"] = {"min_tile_nnz": HUB_MIN_TILE_NNZ, "group_blocks": t.group_blocks, "tiles": t.num_tiles,
+                            "steps": t.num_steps, "units": t.num_units, "hub_cols": t.hub_cols, "tile_nnz": t.nnz,
+                            "tile_nnz_frac": round(t.nnz / nnz, 4), "rest_blocks": H.rest.view.num_TCBlocks,
+                            "mfma_flops_per_step": 2.0 * 256 * t.group_blocks * t.num_steps * F}
         Y = torch.empty((A.out_windows * 8, F), device="cuda")
         phased = f" over the {A.phases}-phase BCSR (Y zero-filled first)" if A.phases > 1 else ""
-        if reuse >= PACK_MIN_REUSE:
+        if H is not None:
+            if not args.profile_step:
+                # the phased gather alone, timed in the same run for comparison
+                buf = torch.empty(swtcf._lib.lib().tcc_tf32_packed_bytes(n, F) + 16, dtype=torch.uint8,
+                                  device="cuda")
+                extra["phased_gather_ms"] = round(
+                    timed(lambda: swtcf.bcsr_spmm_packed(A, swtcf.tf32_pack(X, out=buf), F, Y), 10, 2), 4)
+                del buf
+            A.release()
+            Y = torch.empty((H.out_rows, F), device="cuda")
+            hws = torch.empty(H.workspace_bytes(F) + 16, dtype=torch.uint8, device="cuda")
+
+            def step():
+                swtcf.hybrid_spmm(H, X, Y, workspace=hws)
+
+            kernel = (f"hub_tiles_kernel<{H.view.tiles.group_blocks}, 2> (fp32 MFMA) + hub_reduce_kernel + "
+                      "hub_rows_kernel, after the remainder's tf32_pack_kernel + gather_kernel<Packed> over the "
+                      f"{H.rest.phases}-phase BCSR (all timed)")
+            extra["path"] = (f"hybrid: dense hub tiles (>= {HUB_MIN_TILE_NNZ} nnz) on fp32 MFMA + packed gather of the "
+                             f"remainder over its {H.rest.phases}-phase BCSR")
+        elif reuse >= PACK_MIN_REUSE:
             # each step packs X to TF32 rows of 2.5 B/element, then gathers them
             buf = torch.empty(swtcf._lib.lib().tcc_tf32_packed_bytes(n, F) + 16, dtype=torch.uint8, device="cuda")
 
@@ -351,7 +396,7 @@ def bench_spmm(args, torch, swtcf, cfg):
 
             kernel = "gather_kernel" + phased
             extra["path"] = "fp32 gather" + phased
-    if args.config in (2, 3):
+    if args.config in (2, 3) and not args.profile_step:
         # SWTCF conversion of the same COO (S = 16), GEdges/s as the
         # reference's converter driver prints it (swtcf_convert_main.cu:417)
         m = swtcf.DeviceSWTCFMatrix(n, n, nnz, 16)
@@ -365,6 +410,8 @@ def bench_spmm(args, torch, swtcf, cfg):
         del m, ws
     if args.copy_calibration_mib:
         copy_calibration(args.copy_calibration_mib)
+    if args.profile_step:
+        print(f"[bench] profile-step: the step runs {args.warmup + args.steps} times", file=sys.stderr, flush=True)
     ms = timed(step, args.steps, args.warmup)
     flops = 2.0 * nnz * F
     if args.config == 1:

@@ -309,7 +309,7 @@ typedef struct tcc_hybrid {
 
 /* Build the hybrid of a device COO (row = destination, col = source, no
  * duplicate pairs; dVal may be NULL).  minTileNnz 0 = 32 (at most 256),
- * groupBlocks 0 = 4 (1, 2, 4 or 8), unitSteps 0 = 32 (at most 64), phases
+ * groupBlocks 0 = 4 (1, 2, 4 or 8), unitSteps 0 = 64 (at most 64), phases
  * as tcc_coo_to_bcsr_phased for the remainder.  Synchronises `stream`; free
  * with tcc_hybrid_release. */
 int tcc_coo_to_hybrid(const uint32_t* dRow, const uint32_t* dCol, const float* dVal, uint32_t nnz,

@@ -54,7 +54,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr std::uint32_t kTile = 16;
 constexpr std::uint32_t kTileVals = kTile * kTile;  // floats per tile
 constexpr std::uint32_t kSlice = 64;                // features per wave
-constexpr std::uint32_t kDefaultUnitSteps = 32;
+constexpr std::uint32_t kDefaultUnitSteps = 64;
 constexpr std::uint32_t kMaxUnitSteps = 64;         // a unit's step columns sit one per lane
 constexpr std::uint32_t kDefaultMinTileNnz = 32;
 constexpr std::uint32_t kDefaultGroupBlocks = 4;

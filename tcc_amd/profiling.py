@@ -1,0 +1,175 @@
+"""Reduce rocprofv3 output of bench.py runs to the summaries kept under
+profiles/ (kernel-time tables and the counter-measured HBM traffic that
+bench.py's roofline reports).
+
+    python -m tcc_amd.profiling stats --csv <kernel_stats.csv> --title T --command C [--kernels REGEX]
+        --out profiles/<name>.md
+    python -m tcc_amd.profiling traffic --config N --fetch <FETCH_SIZE counter csv> --write <WRITE_SIZE csv>
+        [--hits <TCC_HIT_sum TCC_MISS_sum csv>] --stats <kernel_stats.csv> --kernels REGEX --launches L
+        --command C --out profiles/traffic_configN.json
+
+The counter runs profile `bench.py --profile-step --copy-calibration-mib
+1024`: only the timed step's kernels run L = warmup + steps times, and one
+1 GiB device copy gives the factors that turn FETCH_SIZE / WRITE_SIZE (KiB
+per dispatch) into bytes.
+"""
+from __future__ import annotations
+
+import argparse
+import collections
+import csv
+import hashlib
+import json
+import os
+import re
+import sys
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+KIB = 1024
+COPY_KERNEL = "copyBuffer"
+
+
+def kernel_key(name: str) -> str:
+    """A kernel's name without its argument list and namespaces
+    ("gather_kernel<4, Packed, values>")."""
+    name = name.replace("(anonymous namespace)::", "").replace("tcc::", "")
+    name = re.sub(r"^void ", "", name)
+    depth, out = 0, []
+    for ch in name:  # drop the parenthesised argument list, keep template arguments
+        if ch == "(" and depth == 0 and out and out[-1] not in "<,":
+            break
+        out.append(ch)
+        depth += ch == "<"
+        depth -= ch == ">"
+    return "".join(out).strip()
+
+
+def read_counters(path: str) -> dict:
+    """{kernel key: {counter: [value per dispatch]}} from a counter-collection csv."""
+    per = collections.defaultdict(lambda: collections.defaultdict(list))
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            per[kernel_key(r["Kernel_Name"])][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    return per
+
+
+def read_stats(path: str) -> list[dict]:
+    with open(path) as f:
+        rows = list(csv.DictReader(f))
+    out = [{"kernel": kernel_key(r["Name"]), "calls": int(r["Calls"]), "avg_ms": float(r["AverageNs"]) / 1e6,
+            "total_ms": float(r["TotalDurationNs"]) / 1e6, "pct": float(r["Percentage"])} for r in rows]
+    return sorted(out, key=lambda r: -r["total_ms"])
+
+
+def sources_sha() -> dict:
+    """sha256[:16] of every kernel source: a traffic file holds only while they are unchanged."""
+    out = {}
+    for d in ("tcc_amd/csrc", "include"):
+        for name in sorted(os.listdir(os.path.join(ROOT, d))):
+            if name.endswith((".hip", ".hpp", ".h", ".cpp")):
+                with open(os.path.join(ROOT, d, name), "rb") as f:
+                    out[f"{d}/{name}"] = hashlib.sha256(f.read()).hexdigest()[:16]
+    return out
+
+
+def _short(name: str, width: int = 72) -> str:
+    return name if len(name) <= width else name[: width - 3] + "..."
+
+
+def stats_md(args) -> str:
+    rows = read_stats(args.csv)
+    total = sum(r["total_ms"] for r in rows)
+    lines = [f"# {args.title}", "", "Command (from the repository root on the GPU box, TMPDIR=/tmp):", "", "```",
+             args.command, "```", ""]
+    if args.kernels:
+        pat = re.compile(args.kernels)
+        step = [r for r in rows if pat.search(r["kernel"])]
+        lines += [f"Step kernels (`{args.kernels}`):", "", "| kernel | calls | avg ms |", "|---|---:|---:|"]
+        lines += [f"| `{r['kernel']}` | {r['calls']} | {r['avg_ms']:.4f} |" for r in step]
+        lines += [f"| **sum of averages** | | **{sum(r['avg_ms'] for r in step):.4f}** |", ""]
+    lines += ["All kernels, by total time:", "",
+              "| kernel | calls | avg ms | total ms | % of GPU time |", "|---|---:|---:|---:|---:|"]
+    for r in rows[: args.top]:
+        lines.append(f"| `{_short(r['kernel'])}` | {r['calls']} | {r['avg_ms']:.4f} | {r['total_ms']:.2f} | "
+                     f"{100 * r['total_ms'] / total:.1f} |")
+    if args.note:
+        lines += ["", args.note]
+    return "\n".join(lines) + "\n"
+
+
+def traffic_json(args) -> dict:
+    fetch, write = read_counters(args.fetch), read_counters(args.write)
+    hits = read_counters(args.hits) if args.hits else {}
+    stats = {r["kernel"]: r for r in read_stats(args.stats)}
+    copy_f = [v for k, c in fetch.items() if COPY_KERNEL in k for v in c.get("FETCH_SIZE", [])]
+    copy_w = [v for k, c in write.items() if COPY_KERNEL in k for v in c.get("WRITE_SIZE", [])]
+    if not copy_f or not copy_w:
+        raise SystemExit("no copy-calibration dispatch in the counter files (run bench.py with --copy-calibration-mib)")
+    gib_kib = (1 << 30) / KIB
+    ff, fw = gib_kib / max(copy_f), gib_kib / max(copy_w)
+    pat = re.compile(args.kernels)
+    per, total = {}, 0.0
+    for k in sorted(set(fetch) | set(write)):
+        if not pat.search(k) or COPY_KERNEL in k:
+            continue
+        f = fetch.get(k, {}).get("FETCH_SIZE", [])
+        w = write.get(k, {}).get("WRITE_SIZE", [])
+        b = (sum(f) * ff + sum(w) * fw) * KIB / args.launches
+        total += b
+        e = {"dispatches": len(f), "fetch_kib_raw_sum": round(sum(f)), "write_kib_raw_sum": round(sum(w)),
+             "hbm_bytes_per_step": round(b)}
+        h = hits.get(k, {})
+        if h.get("TCC_HIT_sum") and h.get("TCC_MISS_sum"):
+            hs, ms = sum(h["TCC_HIT_sum"]), sum(h["TCC_MISS_sum"])
+            e["l2_hit_rate"] = round(hs / (hs + ms), 4)
+        if k in stats:
+            e["avg_ms_rocprof"] = round(stats[k]["avg_ms"], 6)
+            e["calls_rocprof"] = stats[k]["calls"]
+        per[k] = e
+    # the stats may come from another run: average launch time x dispatches per step
+    step_ms = sum(stats[k]["avg_ms"] * per[k]["dispatches"] / args.launches for k in per if k in stats) or None
+    out = {"config": args.config, "kernels": args.kernels, "launches": args.launches,
+           "hbm_bytes_per_launch": round(total), "per_kernel": per,
+           "copy_calibration": {"bytes": 1 << 30, "fetch_kib": round(max(copy_f)), "write_kib": round(max(copy_w)),
+                                "fetch_scale": round(ff, 4), "write_scale": round(fw, 4)},
+           "step_kernel_ms_rocprof": None if step_ms is None else round(step_ms, 6),
+           "command": args.command, "sources": sources_sha()}
+    if step_ms:
+        out["dram_side_GBps"] = round(total / (step_ms * 1e-3) / 1e9, 1)
+    return out
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    s = sub.add_parser("stats")
+    s.add_argument("--csv", required=True)
+    s.add_argument("--title", required=True)
+    s.add_argument("--command", required=True)
+    s.add_argument("--note", default="")
+    s.add_argument("--kernels", default="", help="regex over kernel names: the step's kernels, listed first")
+    s.add_argument("--top", type=int, default=15)
+    s.add_argument("--out", required=True)
+    t = sub.add_parser("traffic")
+    t.add_argument("--config", type=int, required=True)
+    t.add_argument("--fetch", required=True)
+    t.add_argument("--write", required=True)
+    t.add_argument("--hits")
+    t.add_argument("--stats", required=True)
+    t.add_argument("--kernels", required=True, help="regex over kernel names: the step's kernels")
+    t.add_argument("--launches", type=int, required=True, help="step executions in the profiled run")
+    t.add_argument("--command", required=True)
+    t.add_argument("--out", required=True)
+    args = ap.parse_args(argv)
+    if args.cmd == "stats":
+        text = stats_md(args)
+    else:
+        text = json.dumps(traffic_json(args), indent=1) + "\n"
+    with open(args.out, "w") as f:
+        f.write(text)
+    sys.stdout.write(text)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -15,6 +15,8 @@ Three checks, each able to see a misrouted row:
 - Rows against the oracle: the fp64 CSR oracle on TF32-rounded inputs over
   a seeded sample of output rows holding at least 1M nonzeros (the hub row
   included), element by element at rel-L2 <= 1e-5 (north_star bound 1e-3).
+- Every config-3 format the bench or the API offers (BCSR, 4-phase BCSR,
+  row super-window BCSR, dense hub tiles + remainder).
 - The converter: the 114M-edge SWTCF of config 3 against the C oracle's
   canonical form, every array bit for bit.
 
@@ -188,6 +190,31 @@ def test_fullsize_config3_super_window(gpu, oracle):
     hub = int(np.argmax(np.bincount(rows, minlength=n)))
     check_swap_fails(Y, n, r_dev, want, hub, (hub + 3) % n, what="config 3 super-window")
     check_rows(oracle, Y, rows, cols, v, n, Xh, 34, what="config 3 super-window")
+
+
+def test_fullsize_config3_hybrid(gpu, oracle):
+    """The bench's path at config 3: dense hub tiles (>= 32 nnz, groups of 4
+    row blocks) on MFMA plus the packed gather of the remainder over its
+    4-phase BCSR; Y = AX and Y += AX."""
+    from tcc_amd import swtcf
+
+    n, F, r32, c32, vals, X = graph(3)
+    rows, cols, v = r32.cpu().numpy(), c32.cpu().numpy(), vals.cpu().numpy()
+    Xh = X.cpu().numpy()
+    H = swtcf.coo_to_hybrid(r32, c32, vals, n, n, min_tile_nnz=32, group_blocks=4, phases=4)
+    t = H.view.tiles
+    print(f"config 3 hybrid: {t.num_tiles} tiles in {t.num_steps} steps, {t.nnz} tile entries, "
+          f"{H.rest.view.nnz} in the remainder", flush=True)
+    assert t.nnz + H.rest.view.nnz == r32.numel() and t.nnz > r32.numel() // 3
+    Y = swtcf.hybrid_spmm(H, X)
+    r_dev, want = check_weighted(oracle, Y, n, rows, cols, v, n, Xh, 35, what="config 3 hybrid")
+    hub = int(np.argmax(np.bincount(rows, minlength=n)))
+    check_swap_fails(Y, n, r_dev, want, hub, (hub + 5) % n, what="config 3 hybrid")
+    check_rows(oracle, Y, rows, cols, v, n, Xh, 36, what="config 3 hybrid")
+    # Y += AX over a copy of AX: 2 AX
+    Y2 = Y.clone()
+    swtcf.hybrid_spmm(H, X, Y2, accumulate=True)
+    check_weighted(oracle, Y2 * 0.5, n, rows, cols, v, n, Xh, 35, what="config 3 hybrid, accumulate")
 
 
 def test_fullsize_config3_swtcf_bit_exact(gpu, oracle):

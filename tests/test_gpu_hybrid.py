@@ -121,10 +121,10 @@ def test_arrays_match_numpy_layout(gpu, oracle, nr, nc, nnz, hubs, min_nnz, G, u
     H = swtcf.coo_to_hybrid(dev_u32(dst), dev_u32(src), None if vals is None else torch.from_numpy(vals).cuda(), nr, nc,
                             min_tile_nnz=min_nnz, group_blocks=G, unit_steps=unit_steps)
     h = H.to_host()
-    want = reference_layout(dst, src, vals, nr, nc, min_nnz, G or 4, unit_steps or 32)
+    want = reference_layout(dst, src, vals, nr, nc, min_nnz, G or 4, unit_steps or 64)
     print(f"hybrid layout nr={nr} nc={nc} nnz={nnz} G={G}: {h['num_steps']} steps, {h['num_tiles']} tiles, "
           f"{h['tile_nnz']} tile entries", flush=True)
-    assert h["group_blocks"] == (G or 4) and h["unit_steps"] == (unit_steps or 32)
+    assert h["group_blocks"] == (G or 4) and h["unit_steps"] == (unit_steps or 64)
     assert h["hub_cols"] == want["hub_cols"] and h["num_tiles"] == want["num_tiles"]
     for k in ("rowOrder", "hubColOrder", "groupStepOffset", "stepCol", "units"):
         assert np.array_equal(h[k], want[k]), k

@@ -1,0 +1,71 @@
+"""tcc_amd.profiling: rocprofv3 csv reductions behind the profiles/ files
+(synthetic csv files; no GPU)."""
+import csv
+import json
+
+from tcc_amd import profiling
+
+
+def test_kernel_key_strips_arguments_and_namespaces():
+    k = profiling.kernel_key("void tcc::(anonymous namespace)::gather_kernel<4, (tcc::(anonymous namespace)::Src)2, "
+                             "true>(tcc::(anonymous namespace)::GatherArgs)")
+    assert k == "gather_kernel<4, (Src)2, true>"
+    assert profiling.kernel_key("tcc::(anonymous namespace)::hub_reduce_kernel(tcc::(anonymous namespace)::TileArgs, "
+                                "unsigned int)") == "hub_reduce_kernel"
+    assert profiling.kernel_key("__amd_rocclr_copyBuffer") == "__amd_rocclr_copyBuffer"
+
+
+def _counters(path, rows):
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"])
+        w.writeheader()
+        for i, (name, counter, value) in enumerate(rows):
+            w.writerow({"Dispatch_Id": i, "Kernel_Name": name, "Counter_Name": counter, "Counter_Value": value})
+
+
+def _stats(path, rows):
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Name", "Calls", "TotalDurationNs", "AverageNs", "Percentage"])
+        w.writeheader()
+        for name, calls, avg_ns in rows:
+            w.writerow({"Name": name, "Calls": calls, "TotalDurationNs": calls * avg_ns, "AverageNs": avg_ns,
+                        "Percentage": 0})
+
+
+def test_traffic_scales_by_the_copy_and_divides_by_launches(tmp_path):
+    g = "void tcc::(anonymous namespace)::gather_kernel<4>(tcc::(anonymous namespace)::GatherArgs)"
+    h = "void tcc::(anonymous namespace)::hub_tiles_kernel<4, 2>(tcc::(anonymous namespace)::TileArgs)"
+    other = "tcc::(anonymous namespace)::degree_kernel(unsigned int const*)"
+    copy = "__amd_rocclr_copyBuffer"
+    # the 1 GiB copy reads FETCH_SIZE 512 Ki (factor 2) and WRITE_SIZE 1 Gi KiB... (factor 1)
+    _counters(tmp_path / "f.csv", [(copy, "FETCH_SIZE", 524288), (g, "FETCH_SIZE", 100), (g, "FETCH_SIZE", 300),
+                                   (h, "FETCH_SIZE", 50), (h, "FETCH_SIZE", 50), (other, "FETCH_SIZE", 1e9)])
+    _counters(tmp_path / "w.csv", [(copy, "WRITE_SIZE", 1048576), (g, "WRITE_SIZE", 10), (g, "WRITE_SIZE", 10),
+                                   (h, "WRITE_SIZE", 4), (h, "WRITE_SIZE", 4), (other, "WRITE_SIZE", 1e9)])
+    _counters(tmp_path / "hm.csv", [(g, "TCC_HIT_sum", 3), (g, "TCC_MISS_sum", 1)])
+    _stats(tmp_path / "s.csv", [(g, 2, 2_000_000), (h, 2, 1_000_000), (other, 1, 5_000_000)])
+    out = tmp_path / "t.json"
+    profiling.main(["traffic", "--config", "3", "--fetch", str(tmp_path / "f.csv"), "--write", str(tmp_path / "w.csv"),
+                    "--hits", str(tmp_path / "hm.csv"), "--stats", str(tmp_path / "s.csv"),
+                    "--kernels", "gather_kernel|hub_", "--launches", "2", "--command", "cmd", "--out", str(out)])
+    d = json.loads(out.read_text())
+    gather = (400 * 2 + 20 * 1) * 1024 / 2
+    hub = (100 * 2 + 8 * 1) * 1024 / 2
+    assert d["per_kernel"]["gather_kernel<4>"]["hbm_bytes_per_step"] == round(gather)
+    assert d["per_kernel"]["hub_tiles_kernel<4, 2>"]["hbm_bytes_per_step"] == round(hub)
+    assert d["hbm_bytes_per_launch"] == round(gather + hub)
+    assert d["per_kernel"]["gather_kernel<4>"]["l2_hit_rate"] == 0.75
+    assert "degree_kernel" not in d["per_kernel"]
+    assert d["copy_calibration"]["fetch_scale"] == 2.0 and d["copy_calibration"]["write_scale"] == 1.0
+    assert d["step_kernel_ms_rocprof"] == 3.0  # 2 ms + 1 ms, one dispatch each per step
+    assert "tcc_amd/csrc/hub_tiles.hip" in d["sources"] and d["command"] == "cmd"
+
+
+def test_stats_table(tmp_path):
+    _stats(tmp_path / "s.csv", [("void tcc::a_kernel(int)", 4, 1_500_000), ("void tcc::b_kernel(int)", 1, 500_000)])
+    out = tmp_path / "s.md"
+    profiling.main(["stats", "--csv", str(tmp_path / "s.csv"), "--title", "T", "--command", "python bench.py",
+                    "--out", str(out)])
+    text = out.read_text()
+    assert "python bench.py" in text
+    assert "| `a_kernel` | 4 | 1.5000 | 6.00 | 92.3 |" in text
