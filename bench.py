@@ -56,12 +56,14 @@ PHASE_MIN_BLOCKS_PER_WINDOW = 64.0
 PHASES = 4
 # The same long-window (skewed) graphs hold a dense core once rows and
 # columns are ordered by degree: 16x16 tiles of at least HUB_MIN_TILE_NNZ
-# entries go to fp32 MFMA in groups of HUB_GROUP_BLOCKS row blocks, the rest
-# to the phased gather (measured at config 3: 17.35 ms phased gather alone ->
-# 13.4 ms; thresholds 16 / 24 / 32 / 64 -> 13.8 / 14.9 / 13.5 / 14.6 ms,
-# groups 1 / 2 / 4 / 8 -> 14.2 / 13.7 / 13.5 / 14.5 ms).
-HUB_MIN_TILE_NNZ = 32
-HUB_GROUP_BLOCKS = 4
+# entries go to MFMA in groups of HUB_GROUP_BLOCKS row blocks, each TF32
+# operand split into two bf16 (four exact bf16 products, fp32 accumulation),
+# the rest to the phased gather.  Measured at config 3 (step ms): phased
+# gather alone 17.35; fp32 MFMA tiles, 32 nnz, G = 4: 13.40; split tiles,
+# G = 4: 12.43 / 12.31 / 11.30 / 13.75 at 32 / 24 / 16 / 8 nnz; G = 8:
+# 11.05 / 10.88 / 11.72 / 12.43 at 20 / 16 / 12 / 8 nnz.
+HUB_MIN_TILE_NNZ = 16
+HUB_GROUP_BLOCKS = 8
 CPU_SAMPLE_NNZ = 16_000_000
 
 WORKLOADS = {
@@ -350,11 +352,13 @@ def bench_spmm(args, torch, swtcf, cfg):
             # ... and the hybrid: dense hub tiles on MFMA + the phased gather of the rest
             t_h = time.perf_counter()
             H = swtcf.coo_to_hybrid(r32, c32, vals, n, n, min_tile_nnz=HUB_MIN_TILE_NNZ,
-                                    group_blocks=HUB_GROUP_BLOCKS, phases=PHASES)
+                                    group_blocks=HUB_GROUP_BLOCKS, tile_format=swtcf.TILES_BF16X2, phases=PHASES)
             torch.cuda.synchronize()
             extra["hybrid_build_ms"] = round((time.perf_counter() - t_h) * 1e3, 3)
             t = H.view.tiles
-            extra["hub"] = {"min_tile_nnz": HUB_MIN_TILE_NNZ, "group_blocks": t.group_blocks, "tiles": t.num_tiles,
+            extra["hub"] = {"min_tile_nnz": HUB_MIN_TILE_NNZ, "group_blocks": t.group_blocks,
+                            "tile_format": "bf16x2 (TF32 = bf16 hi + bf16 lo, v_mfma_f32_16x16x32_bf16)",
+                            "tiles": t.num_tiles,
                             "steps": t.num_steps, "units": t.num_units, "hub_cols": t.hub_cols, "tile_nnz": t.nnz,
                             "tile_nnz_frac": round(t.nnz / nnz, 4), "rest_blocks": H.rest.view.num_TCBlocks,
                             "mfma_flops_per_step": 2.0 * 256 * t.group_blocks * t.num_steps * F}
@@ -375,11 +379,12 @@ def bench_spmm(args, torch, swtcf, cfg):
             def step():
                 swtcf.hybrid_spmm(H, X, Y, workspace=hws)
 
-            kernel = (f"hub_tiles_kernel<{H.view.tiles.group_blocks}, 2> (fp32 MFMA) + hub_reduce_kernel + "
-                      "hub_rows_kernel, after the remainder's tf32_pack_kernel + gather_kernel<Packed> over the "
-                      f"{H.rest.phases}-phase BCSR (all timed)")
-            extra["path"] = (f"hybrid: dense hub tiles (>= {HUB_MIN_TILE_NNZ} nnz) on fp32 MFMA + packed gather of the "
-                             f"remainder over its {H.rest.phases}-phase BCSR")
+            kernel = (f"hub_tiles_split_kernel<{H.view.tiles.group_blocks}, 2> (bf16 MFMA on split TF32) + "
+                      "hub_reduce_kernel + hub_rows_split_kernel, after the remainder's tf32_pack_kernel + "
+                      f"gather_kernel<Packed> over the {H.rest.phases}-phase BCSR (all timed)")
+            extra["path"] = (f"hybrid: dense hub tiles (>= {HUB_MIN_TILE_NNZ} nnz, groups of {HUB_GROUP_BLOCKS}) on "
+                             f"bf16 MFMA over split TF32 + packed gather of the remainder over its "
+                             f"{H.rest.phases}-phase BCSR")
         elif reuse >= PACK_MIN_REUSE:
             # each step packs X to TF32 rows of 2.5 B/element, then gathers them
             buf = torch.empty(swtcf._lib.lib().tcc_tf32_packed_bytes(n, F) + 16, dtype=torch.uint8, device="cuda")

@@ -281,6 +281,9 @@ int tcc_sw_bcsr_spmm_packed(const tcc_sw_bcsr* A, const void* packedX, float* Y,
  *     steps, 1..64); a group held by more than one unit has its units' sums
  *     stored in the workspace and added into Y by a reduction pass (no
  *     atomics: the sum order is fixed). */
+#define TCC_TILES_FP32 0u   /* tileVals in the fp32 MFMA's A-operand order (above) */
+#define TCC_TILES_BF16X2 1u /* each tile 256 bf16 hi then 256 bf16 lo, row-major: hi + lo = the TF32 value */
+
 typedef struct tcc_hub_tiles {
     uint32_t num_rows;
     uint32_t num_cols;
@@ -292,11 +295,12 @@ typedef struct tcc_hub_tiles {
     uint32_t num_units;
     uint32_t unit_steps;
     uint32_t hub_cols;               /* column ranks the tiles cover: [0, hub_cols) */
+    uint32_t tile_format;            /* TCC_TILES_FP32 or TCC_TILES_BF16X2 */
     const uint32_t* rowOrder;        /* [16*G*num_groups] */
     const uint32_t* hubColOrder;     /* [hub_cols] */
     const uint32_t* groupStepOffset; /* [num_groups+1] */
     const uint32_t* stepCol;         /* [num_steps] */
-    const float* tileVals;           /* [256*G*(num_steps+1)]: the last step zeros */
+    const float* tileVals;           /* [256*G*(num_steps+1)] (1 KB a tile in either format): the last step zeros */
     const uint32_t* units;           /* [3*num_units] */
 } tcc_hub_tiles;
 
@@ -308,13 +312,16 @@ typedef struct tcc_hybrid {
 } tcc_hybrid;
 
 /* Build the hybrid of a device COO (row = destination, col = source, no
- * duplicate pairs; dVal may be NULL).  minTileNnz 0 = 32 (at most 256),
- * groupBlocks 0 = 4 (1, 2, 4 or 8), unitSteps 0 = 64 (at most 64), phases
+ * duplicate pairs; dVal may be NULL).  minTileNnz 0 = 16 (at most 256),
+ * groupBlocks 0 = 8 (1, 2, 4 or 8), unitSteps 0 = 64 (at most 64), tileFormat
+ * TCC_TILES_FP32 (products on v_mfma_f32_16x16x4f32) or TCC_TILES_BF16X2
+ * (each TF32 operand as two bf16, four exact bf16 products on
+ * v_mfma_f32_16x16x32_bf16, fp32 accumulation), phases
  * as tcc_coo_to_bcsr_phased for the remainder.  Synchronises `stream`; free
  * with tcc_hybrid_release. */
 int tcc_coo_to_hybrid(const uint32_t* dRow, const uint32_t* dCol, const float* dVal, uint32_t nnz,
                       uint32_t numRows, uint32_t numCols, uint32_t minTileNnz, uint32_t groupBlocks,
-                      uint32_t unitSteps, uint32_t phases, tcc_hybrid* out, void* stream);
+                      uint32_t unitSteps, uint32_t tileFormat, uint32_t phases, tcc_hybrid* out, void* stream);
 int tcc_hybrid_release(tcc_hybrid* H);
 
 /* Bytes of device workspace tcc_hybrid_spmm needs for F features: the

@@ -68,6 +68,7 @@ class HubTiles(ctypes.Structure):
     _fields_ = [
         ("num_rows", u32), ("num_cols", u32), ("nnz", u32), ("group_blocks", u32), ("num_groups", u32),
         ("num_steps", u32), ("num_tiles", u32), ("num_units", u32), ("unit_steps", u32), ("hub_cols", u32),
+        ("tile_format", u32),
         ("rowOrder", vp), ("hubColOrder", vp), ("groupStepOffset", vp), ("stepCol", vp), ("tileVals", vp),
         ("units", vp),
     ]
@@ -117,7 +118,8 @@ SIGNATURES = {
     "tcc_coo_to_sw_bcsr": (ctypes.c_int, [vp, vp, vp, u32, u32, u32, u32, u32, ctypes.POINTER(SWBCSR),
                                           ctypes.POINTER(vp), vp]),
     "tcc_sw_bcsr_spmm_packed": (ctypes.c_int, [ctypes.POINTER(SWBCSR), vp, vp, u32, ctypes.c_int, vp]),
-    "tcc_coo_to_hybrid": (ctypes.c_int, [vp, vp, vp, u32, u32, u32, u32, u32, u32, u32, ctypes.POINTER(Hybrid), vp]),
+    "tcc_coo_to_hybrid": (ctypes.c_int, [vp, vp, vp, u32, u32, u32, u32, u32, u32, u32, u32, ctypes.POINTER(Hybrid),
+                                         vp]),
     "tcc_hybrid_release": (ctypes.c_int, [ctypes.POINTER(Hybrid)]),
     "tcc_hybrid_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Hybrid), u32]),
     "tcc_hub_tiles_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(HubTiles), u32]),

@@ -56,13 +56,28 @@ constexpr std::uint32_t kTileVals = kTile * kTile;  // floats per tile
 constexpr std::uint32_t kSlice = 64;                // features per wave
 constexpr std::uint32_t kDefaultUnitSteps = 64;
 constexpr std::uint32_t kMaxUnitSteps = 64;         // a unit's step columns sit one per lane
-constexpr std::uint32_t kDefaultMinTileNnz = 32;
-constexpr std::uint32_t kDefaultGroupBlocks = 4;
+constexpr std::uint32_t kDefaultMinTileNnz = 16;
+constexpr std::uint32_t kDefaultGroupBlocks = 8;
 constexpr unsigned kThreads = 256;
 
 inline std::size_t align_up(std::size_t x) { return (x + 255) & ~std::size_t(255); }
 
 inline bool valid_group(std::uint32_t g) { return g == 1 || g == 2 || g == 4 || g == 8; }
+
+// bf16 halves of a TF32 value: hi = its top 16 bits (sign, exponent, 7
+// mantissa bits), lo = the exact remainder (at most 3 significant bits);
+// a non-finite value keeps lo = 0.  hi + lo == x for every TF32 x whose
+// remainder is a normal or zero fp32 (|x| >= 2^-116).
+__device__ __forceinline__ void bf16_split(float x, std::uint16_t& hi, std::uint16_t& lo) {
+    const std::uint32_t b = __float_as_uint(x);
+    hi = static_cast<std::uint16_t>(b >> 16);
+    if ((b & 0x7F800000u) == 0x7F800000u) {
+        lo = 0;
+        return;
+    }
+    const float r = x - __uint_as_float(b & 0xFFFF0000u);
+    lo = static_cast<std::uint16_t>(__float_as_uint(r) >> 16);
+}
 
 // ---------------------------------------------------------------- builder
 
@@ -184,7 +199,7 @@ __global__ void place_entries_kernel(const std::uint64_t* __restrict__ keys, con
                                      const std::uint32_t* __restrict__ pos, const std::uint32_t* __restrict__ dense,
                                      const std::uint32_t* __restrict__ slot, const std::uint32_t* __restrict__ restPos,
                                      const std::uint32_t* __restrict__ row, const std::uint32_t* __restrict__ col,
-                                     const float* __restrict__ val, float* __restrict__ tileVals,
+                                     const float* __restrict__ val, float* __restrict__ tileVals, bool split,
                                      std::uint32_t* __restrict__ restRow, std::uint32_t* __restrict__ restCol,
                                      float* __restrict__ restVal) {
     const std::uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
@@ -194,8 +209,17 @@ __global__ void place_entries_kernel(const std::uint64_t* __restrict__ keys, con
     const float v = val ? val[src] : 1.0f;
     if (dense[t]) {
         const std::uint32_t i = static_cast<std::uint32_t>(keys[e] >> 4) & 15u, j = static_cast<std::uint32_t>(keys[e]) & 15u;
-        const std::uint32_t lane = i + 16 * (j % 4), step = j / 4;
-        tileVals[static_cast<std::uint64_t>(slot[t]) * kTileVals + 4 * lane + step] = tf32_rna(v);
+        if (split) {
+            // bf16 tile: hi[i][j] at 2(16i + j) bytes, lo 512 bytes further
+            std::uint16_t hi, lo;
+            bf16_split(tf32_rna(v), hi, lo);
+            std::uint16_t* tile = reinterpret_cast<std::uint16_t*>(tileVals + static_cast<std::uint64_t>(slot[t]) * kTileVals);
+            tile[16 * i + j] = hi;
+            tile[256 + 16 * i + j] = lo;
+        } else {
+            const std::uint32_t lane = i + 16 * (j % 4), step = j / 4;
+            tileVals[static_cast<std::uint64_t>(slot[t]) * kTileVals + 4 * lane + step] = tf32_rna(v);
+        }
     } else {
         const std::uint32_t p = restPos[e];
         restRow[p] = row[src];
@@ -229,16 +253,23 @@ struct DevBuf {
 
 // ---------------------------------------------------------------- SpMM
 
-// Xh[r][f] = TF32(X[hubColOrder[r]][f]) for f < F, 0 for F <= f < ldh; one
-// thread per 4 features (ldh is a multiple of 64).
+// Xh[r][f] = TF32(X[hubColOrder[r]][f]) for r < hubCols and f < F, 0 for
+// the other f < ldh and the rows up to hubRows (the last column block's
+// ranks past the last column); one thread per 4 features (ldh is a
+// multiple of 64).
 __global__ void hub_rows_kernel(const float* __restrict__ X, std::uint32_t F, const std::uint32_t* __restrict__ order,
-                                std::uint32_t hubCols, std::uint32_t ldh, bool vec, float* __restrict__ Xh) {
+                                std::uint32_t hubCols, std::uint32_t hubRows, std::uint32_t ldh, bool vec,
+                                float* __restrict__ Xh) {
     const std::uint64_t i = static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     const std::uint32_t q = ldh / 4;
     const std::uint32_t r = static_cast<std::uint32_t>(i / q), f = 4 * static_cast<std::uint32_t>(i % q);
-    if (r >= hubCols) return;
-    const float* x = X + static_cast<std::uint64_t>(order[r]) * F + f;
+    if (r >= hubRows) return;
     f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (r >= hubCols) {
+        *reinterpret_cast<f32x4*>(Xh + static_cast<std::uint64_t>(r) * ldh + f) = v;
+        return;
+    }
+    const float* x = X + static_cast<std::uint64_t>(order[r]) * F + f;
     if (vec && f + 4 <= F) {
         v = load_global<vf4>(x);
     } else {
@@ -415,6 +446,159 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_kernel(TileArgs a) {
         }
 }
 
+// Split tiles (TCC_TILES_BF16X2).  A TF32 value is exactly hi + lo with
+// both bf16, and a bf16 product is exact in fp32, so a·x = ah·xh + ah·xl +
+// al·xh + al·xl accumulates in fp32 like the fp32 MFMA of TF32 operands, at
+// four bf16 products per TF32 one: v_mfma_f32_16x16x32_bf16 runs 16x the
+// fp32 MFMA's rate.  Per tile and 16 features the products are two K=32
+// MFMAs over k' = (lane group q = l/16, element e): lanes q = 0,1 carry
+// k = 8q+e of xh and lanes q = 2,3 the same k of xl, against ah (first
+// MFMA) or al (second) of column k = 8(q%2)+e on every lane group
+// (D[i][j] = sum_q sum_e A[lane i+16q][e] B[lane j+16q][e], checked on the
+// GPU).  Xs holds the hub rows transposed per column block:
+// Xs[cb][f] = 16 hi then 16 lo bf16 of rows 16cb..16cb+15 (64 bytes), so
+// that lane (j + 16q) of N tile u reads 16 bytes at
+// Xs[cb][f0 + 16u + j] + 32(q/2) + 16(q%2).
+__global__ void hub_rows_split_kernel(const float* __restrict__ X, std::uint32_t F,
+                                      const std::uint32_t* __restrict__ order, std::uint32_t hubCols,
+                                      std::uint32_t hubRows, std::uint32_t ldh, std::uint16_t* __restrict__ Xs) {
+    const std::uint64_t i = static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const std::uint32_t cb = static_cast<std::uint32_t>(i / ldh), f = static_cast<std::uint32_t>(i % ldh);
+    if (cb >= hubRows / kTile) return;
+    vu4 hi[2], lo[2];
+#pragma unroll
+    for (int k = 0; k < 16; k += 2) {
+        std::uint16_t h0 = 0, l0 = 0, h1 = 0, l1 = 0;
+        const std::uint32_t r = cb * kTile + k;
+        if (f < F && r < hubCols) bf16_split(tf32_rna(X[static_cast<std::uint64_t>(order[r]) * F + f]), h0, l0);
+        if (f < F && r + 1 < hubCols) bf16_split(tf32_rna(X[static_cast<std::uint64_t>(order[r + 1]) * F + f]), h1, l1);
+        hi[k / 8][(k % 8) / 2] = static_cast<std::uint32_t>(h0) | static_cast<std::uint32_t>(h1) << 16;
+        lo[k / 8][(k % 8) / 2] = static_cast<std::uint32_t>(l0) | static_cast<std::uint32_t>(l1) << 16;
+    }
+    vu4* out = reinterpret_cast<vu4*>(Xs + (static_cast<std::uint64_t>(cb) * ldh + f) * 32);
+    out[0] = hi[0];
+    out[1] = hi[1];
+    out[2] = lo[0];
+    out[3] = lo[1];
+}
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+template <int G>
+struct SplitOperands {
+    vu4 ah[G];
+    vu4 al[G];
+    vu4 b[4];
+};
+
+// As hub_tiles_kernel, over split tiles: per step 2G loads of A (hi, lo),
+// four of Xs, and 8G bf16 MFMAs.  D of N tile u holds rows 4q + v,
+// feature f0 + 16u + (l%16).
+template <int G, int NS>
+__global__ void __launch_bounds__(kThreads) hub_tiles_split_kernel(TileArgs a) {
+    const unsigned lane = __lane_id();
+    const std::uint32_t w = blockIdx.x * (kThreads / kWave) +
+                            static_cast<std::uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave)));
+    const std::uint32_t unit = w / a.slices, slice = w - unit * a.slices;
+    if (unit >= a.numUnits) return;
+    const std::uint32_t g = a.units[3ull * unit], p0 = a.units[3ull * unit + 1], p1 = a.units[3ull * unit + 2];
+    if (p0 >= p1) return;
+    const bool shared = p0 != a.groupStepOffset[g] || p1 != a.groupStepOffset[g + 1];
+    const std::uint32_t f0 = slice * kSlice;
+    const unsigned li = lane & 15u, lq = lane >> 4;
+    const std::uint32_t last = p1 - 1;
+    const int cols = static_cast<int>(a.stepCol[min(p0 + lane, last)]);
+    const char* xb = reinterpret_cast<const char*>(a.Xh) + (static_cast<std::uint64_t>(f0 + li) * 64 + (lq >> 1) * 32 +
+                                                           (lq & 1u) * 16);
+    const std::uint64_t cbStride = static_cast<std::uint64_t>(a.ldh) * 64;
+    const char* ab = reinterpret_cast<const char*>(a.tileVals) + li * 32 + (lq & 1u) * 16;
+
+    auto load = [&](std::uint32_t p, SplitOperands<G>& o) {
+        const std::uint32_t pa = p <= last ? p : a.zeroStep;
+        const std::uint32_t col =
+            static_cast<std::uint32_t>(__builtin_amdgcn_readlane(cols, static_cast<int>(min(p, last) - p0)));
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            const char* t = ab + (static_cast<std::uint64_t>(pa) * G + j) * (kTileVals * 4);
+            o.ah[j] = load_global<vu4>(t);
+            o.al[j] = load_global<vu4>(t + 512);
+        }
+        const char* rb = xb + col * cbStride;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) o.b[u] = load_global<vu4>(rb + u * 16 * 64);
+    };
+    f32x4 acc[G][4];
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[j][u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    auto mma = [&](const SplitOperands<G>& o) {
+#pragma unroll
+        for (int j = 0; j < G; ++j)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const bf16x8 bu = __builtin_bit_cast(bf16x8, o.b[u]);
+                acc[j][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, o.ah[j]), bu, acc[j][u], 0,
+                                                                    0, 0);
+                acc[j][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, o.al[j]), bu, acc[j][u], 0,
+                                                                    0, 0);
+            }
+    };
+
+    SplitOperands<G> ring[NS];
+#pragma unroll
+    for (int k = 0; k < NS - 1; ++k) {
+        load(p0 + k, ring[k]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    for (std::uint32_t p = p0; p < p1; p += NS) {
+#pragma unroll
+        for (int k = 0; k < NS; ++k) {
+            load(p + k + NS - 1, ring[(k + NS - 1) % NS]);
+            __builtin_amdgcn_sched_barrier(0);
+            mma(ring[k]);
+        }
+    }
+
+    // D(4*lq + v, li) of N tile u of row block j: row 16j + 4lq + v of the
+    // group, feature f0 + 16u + li.
+    if (shared) {
+        float* base = a.partials + (static_cast<std::uint64_t>(unit) * G * kTile + 4 * lq) * a.ldh + f0 + li;
+#pragma unroll
+        for (int j = 0; j < G; ++j)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+#pragma unroll
+                for (int u = 0; u < 4; ++u) base[static_cast<std::uint64_t>(16 * j + v) * a.ldh + 16 * u] = acc[j][u][v];
+        return;
+    }
+    vu4 rows[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+        rows[j] = load_global<vu4>(a.rowOrder + static_cast<std::uint64_t>(g) * G * kTile + 16 * j + 4 * lq);
+    // one row block at a time: its 16 Y values loaded before any is stored
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+        float y[4][4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const std::uint32_t f = f0 + 16 * u + li;
+                const bool live = rows[j][v] != TCC_SWTCF_INVALID_ROW_SLOT && f < a.F;
+                y[v][u] = live ? a.Y[static_cast<std::uint64_t>(rows[j][v]) * a.F + f] : 0.0f;
+            }
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const std::uint32_t f = f0 + 16 * u + li;
+                if (rows[j][v] != TCC_SWTCF_INVALID_ROW_SLOT && f < a.F)
+                    a.Y[static_cast<std::uint64_t>(rows[j][v]) * a.F + f] = y[v][u] + acc[j][u][v];
+            }
+    }
+}
+
 // Y rows of a shared group += the sum of its units' partials, one workgroup
 // per (unit, slice, row block j of the group) of which only the group's
 // first unit works: thread q sums row 16j + q/16, features 4(q%16)..+3 of
@@ -452,13 +636,20 @@ __global__ void __launch_bounds__(kThreads) hub_reduce_kernel(TileArgs a, std::u
 
 inline std::uint32_t hub_ldh(std::uint32_t F) { return (F + kSlice - 1) / kSlice * kSlice; }
 
+// rows of Xh: the hub columns rounded up to whole column blocks
+inline std::uint32_t hub_rows(std::uint32_t hubCols) { return (hubCols + kTile - 1) / kTile * kTile; }
+
 // Two steps in flight (three stages) for the small groups; the larger
 // groups keep their 4 G accumulator tiles and two stages within two or
 // three waves per SIMD.
 template <int G>
-hipError_t launch_tiles(const TileArgs& a, std::uint64_t waves, hipStream_t st) {
+hipError_t launch_tiles(const TileArgs& a, std::uint64_t waves, bool split, hipStream_t st) {
     constexpr int NS = G <= 2 ? 3 : 2;
-    hipLaunchKernelGGL((hub_tiles_kernel<G, NS>), dim3(grid_for(waves, kThreads / kWave)), dim3(kThreads), 0, st, a);
+    if (split)
+        hipLaunchKernelGGL((hub_tiles_split_kernel<G, NS>), dim3(grid_for(waves, kThreads / kWave)), dim3(kThreads), 0,
+                           st, a);
+    else
+        hipLaunchKernelGGL((hub_tiles_kernel<G, NS>), dim3(grid_for(waves, kThreads / kWave)), dim3(kThreads), 0, st, a);
     return hipGetLastError();
 }
 
@@ -480,7 +671,8 @@ int tcc_hybrid_release(tcc_hybrid* H) {
 
 int tcc_coo_to_hybrid(const std::uint32_t* dRow, const std::uint32_t* dCol, const float* dVal, std::uint32_t nnz,
                       std::uint32_t numRows, std::uint32_t numCols, std::uint32_t minTileNnz, std::uint32_t groupBlocks,
-                      std::uint32_t unitSteps, std::uint32_t phases, tcc_hybrid* out, void* stream) {
+                      std::uint32_t unitSteps, std::uint32_t tileFormat, std::uint32_t phases, tcc_hybrid* out,
+                      void* stream) {
     clear_last_error();
     TCC_REQUIRE(out && numRows >= 1 && numCols >= 1 && (nnz == 0 || (dRow && dCol)), TCC_ERR_INVALID_ARGUMENT,
                 "invalid COO -> hybrid arguments");
@@ -490,6 +682,8 @@ int tcc_coo_to_hybrid(const std::uint32_t* dRow, const std::uint32_t* dCol, cons
     TCC_REQUIRE(minTileNnz <= kTileVals, TCC_ERR_INVALID_ARGUMENT, "hybrid: minTileNnz above 256 leaves no tile");
     TCC_REQUIRE(valid_group(groupBlocks), TCC_ERR_INVALID_ARGUMENT, "hybrid: groupBlocks must be 1, 2, 4 or 8");
     TCC_REQUIRE(unitSteps <= kMaxUnitSteps, TCC_ERR_INVALID_ARGUMENT, "hybrid: unitSteps above 64");
+    TCC_REQUIRE(tileFormat == TCC_TILES_FP32 || tileFormat == TCC_TILES_BF16X2, TCC_ERR_INVALID_ARGUMENT,
+                "hybrid: unknown tileFormat");
     const hipStream_t st = as_stream(stream);
     std::memset(out, 0, sizeof(*out));
     const std::uint32_t E = nnz;
@@ -645,8 +839,8 @@ int tcc_coo_to_hybrid(const std::uint32_t* dRow, const std::uint32_t* dCol, cons
         hipLaunchKernelGGL(tile_slots_kernel, dim3(grid_for(E, kThreads)), dim3(kThreads), 0, st, sorted, tileStart,
                            small + 1, dense, stepHead, stepPos, G, CB, slot, oStepCol);
         hipLaunchKernelGGL(place_entries_kernel, dim3(grid_for(E, kThreads)), dim3(kThreads), 0, st, sorted, perm, E,
-                           flags, pos, dense, slot, restPos, dRow, dCol, dVal, oTileVals, restRow, restCol,
-                           dVal ? restVal : nullptr);
+                           flags, pos, dense, slot, restPos, dRow, dCol, dVal, oTileVals,
+                           tileFormat == TCC_TILES_BF16X2, restRow, restCol, dVal ? restVal : nullptr);
     }
     hipLaunchKernelGGL(group_units_kernel, dim3(grid_for(NG, kThreads)), dim3(kThreads), 0, st, oGroupStepOffset,
                        oUnitFirst, NG, unitSteps, oUnits);
@@ -672,6 +866,7 @@ int tcc_coo_to_hybrid(const std::uint32_t* dRow, const std::uint32_t* dCol, cons
     T.num_units = NU;
     T.unit_steps = unitSteps;
     T.hub_cols = hubCols;
+    T.tile_format = tileFormat;
     T.rowOrder = oRowOrder;
     T.hubColOrder = oHubCols;
     T.groupStepOffset = oGroupStepOffset;
@@ -687,7 +882,7 @@ int tcc_coo_to_hybrid(const std::uint32_t* dRow, const std::uint32_t* dCol, cons
 size_t tcc_hub_tiles_workspace_bytes(const tcc_hub_tiles* T, std::uint32_t featureDim) {
     if (!T || featureDim == 0) return 0;
     const std::size_t ldh = hub_ldh(featureDim);
-    return align_up(static_cast<size_t>(T->hub_cols) * ldh * sizeof(float)) +
+    return align_up(static_cast<size_t>(hub_rows(T->hub_cols)) * ldh * sizeof(float)) +
            static_cast<size_t>(T->num_units) * T->group_blocks * kTile * ldh * sizeof(float);
 }
 
@@ -707,16 +902,25 @@ int tcc_hub_tiles_spmm(const tcc_hub_tiles* T, const float* X, float* Y, std::ui
                 "invalid hub tiles SpMM arguments");
     TCC_REQUIRE(valid_group(T->group_blocks) && T->unit_steps >= 1 && T->unit_steps <= kMaxUnitSteps,
                 TCC_ERR_INVALID_ARGUMENT, "hub tiles: group_blocks must be 1, 2, 4 or 8 and unit_steps 1..64");
+    TCC_REQUIRE(T->tile_format == TCC_TILES_FP32 || T->tile_format == TCC_TILES_BF16X2, TCC_ERR_INVALID_ARGUMENT,
+                "hub tiles: unknown tile_format");
+    const bool split = T->tile_format == TCC_TILES_BF16X2;
     const std::uint32_t ldh = hub_ldh(featureDim);
     TCC_REQUIRE(workspace && workspaceBytes >= tcc_hub_tiles_workspace_bytes(T, featureDim) &&
                     reinterpret_cast<std::uintptr_t>(workspace) % 16 == 0,
                 TCC_ERR_INVALID_ARGUMENT, "hub tiles SpMM workspace too small or misaligned");
     const hipStream_t st = as_stream(stream);
     float* Xh = static_cast<float*>(workspace);
-    const std::uint64_t n = static_cast<std::uint64_t>(T->hub_cols) * ldh;
-    const bool vecX = featureDim % 4 == 0 && (reinterpret_cast<std::uintptr_t>(X) & 15u) == 0;
-    hipLaunchKernelGGL(hub_rows_kernel, dim3(grid_for(n / 4, kThreads)), dim3(kThreads), 0, st, X, featureDim,
-                       T->hubColOrder, T->hub_cols, ldh, vecX, Xh);
+    const std::uint32_t hubRows = hub_rows(T->hub_cols);
+    const std::uint64_t n = static_cast<std::uint64_t>(hubRows) * ldh;
+    if (split) {
+        hipLaunchKernelGGL(hub_rows_split_kernel, dim3(grid_for(n / kTile, kThreads)), dim3(kThreads), 0, st, X,
+                           featureDim, T->hubColOrder, T->hub_cols, hubRows, ldh, reinterpret_cast<std::uint16_t*>(Xh));
+    } else {
+        const bool vecX = featureDim % 4 == 0 && (reinterpret_cast<std::uintptr_t>(X) & 15u) == 0;
+        hipLaunchKernelGGL(hub_rows_kernel, dim3(grid_for(n / 4, kThreads)), dim3(kThreads), 0, st, X, featureDim,
+                           T->hubColOrder, T->hub_cols, hubRows, ldh, vecX, Xh);
+    }
     TCC_LAUNCH_CHECK();
     TileArgs a{};
     a.rowOrder = T->rowOrder;
@@ -737,10 +941,10 @@ int tcc_hub_tiles_spmm(const tcc_hub_tiles* T, const float* X, float* Y, std::ui
     TCC_REQUIRE(waves <= 0x7FFFFFFFull, TCC_ERR_UNSUPPORTED, "hub tiles SpMM launch too large");
     hipError_t e;
     switch (T->group_blocks) {
-        case 1: e = launch_tiles<1>(a, waves, st); break;
-        case 2: e = launch_tiles<2>(a, waves, st); break;
-        case 4: e = launch_tiles<4>(a, waves, st); break;
-        default: e = launch_tiles<8>(a, waves, st); break;
+        case 1: e = launch_tiles<1>(a, waves, split, st); break;
+        case 2: e = launch_tiles<2>(a, waves, split, st); break;
+        case 4: e = launch_tiles<4>(a, waves, split, st); break;
+        default: e = launch_tiles<8>(a, waves, split, st); break;
     }
     TCC_HIP_CHECK(e);
     const std::uint64_t reduceBlocks = waves * T->group_blocks;

@@ -19,6 +19,7 @@ INVALID_CACHE_SLOT = 0xFF
 REPEAT_CACHE_SIZE = 32
 DEFAULT_TC_THRESHOLD = 12
 DEVERR_FEATURE_INDEX = 7  # TCC_DEVERR_FEATURE_INDEX
+TILES_FP32, TILES_BF16X2 = 0, 1  # TCC_TILES_*
 FEATURE_DIM = 128
 
 
@@ -427,7 +428,9 @@ class HybridMatrix:
             "hubColOrder": _download(t.hubColOrder, t.hub_cols, np.uint32),
             "groupStepOffset": _download(t.groupStepOffset, NG + 1, np.uint32),
             "stepCol": _download(t.stepCol, S, np.uint32),
-            "tileVals": _download(t.tileVals, 256 * G * S, np.float32).reshape(S, G, 64, 4),
+            "tileVals": (_download(t.tileVals, 256 * G * S, np.float32).reshape(S, G, 64, 4) if t.tile_format == TILES_FP32
+                         else _download(t.tileVals, 512 * G * S, np.uint16).reshape(S, G, 2, 16, 16)),
+            "tile_format": t.tile_format,
             "units": _download(t.units, 3 * U, np.uint32).reshape(U, 3),
             "group_blocks": G, "num_groups": NG, "num_steps": S, "num_tiles": t.num_tiles, "num_units": U,
             "hub_cols": t.hub_cols, "tile_nnz": t.nnz, "unit_steps": t.unit_steps,
@@ -436,14 +439,14 @@ class HybridMatrix:
 
 
 def coo_to_hybrid(row: torch.Tensor, col: torch.Tensor, val: torch.Tensor | None, num_rows: int, num_cols: int,
-                  min_tile_nnz: int = 0, group_blocks: int = 0, unit_steps: int = 0, phases: int = 1,
-                  stream=None) -> HybridMatrix:
+                  min_tile_nnz: int = 0, group_blocks: int = 0, unit_steps: int = 0, tile_format: int = TILES_BF16X2,
+                  phases: int = 1, stream=None) -> HybridMatrix:
     """Dense hub tiles + remainder BCSR of the COO matrix (tcc_coo_to_hybrid)."""
     view = Hybrid()
     check(_lib.lib().tcc_coo_to_hybrid(_u32(row).data_ptr() if row.numel() else None,
                                        _u32(col).data_ptr() if col.numel() else None, _ptr(val), row.numel(),
                                        num_rows, num_cols, int(min_tile_nnz), int(group_blocks), int(unit_steps),
-                                       int(phases), ctypes.byref(view), _stream(stream)))
+                                       int(tile_format), int(phases), ctypes.byref(view), _stream(stream)))
     return HybridMatrix(view)
 
 

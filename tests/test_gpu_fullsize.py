@@ -192,19 +192,22 @@ def test_fullsize_config3_super_window(gpu, oracle):
     check_rows(oracle, Y, rows, cols, v, n, Xh, 34, what="config 3 super-window")
 
 
-def test_fullsize_config3_hybrid(gpu, oracle):
-    """The bench's path at config 3: dense hub tiles (>= 32 nnz, groups of 4
-    row blocks) on MFMA plus the packed gather of the remainder over its
-    4-phase BCSR; Y = AX and Y += AX."""
+@pytest.mark.parametrize("min_nnz, G, split", [(16, 8, True), (32, 4, False)])
+def test_fullsize_config3_hybrid(gpu, oracle, min_nnz, G, split):
+    """The bench's path at config 3: dense hub tiles (>= 16 nnz, groups of 8
+    row blocks, TF32 split into bf16 halves) on MFMA plus the packed gather of
+    the remainder over its 4-phase BCSR; and the fp32-MFMA tiles (>= 32 nnz,
+    groups of 4).  Y = AX and Y += AX."""
     from tcc_amd import swtcf
 
     n, F, r32, c32, vals, X = graph(3)
     rows, cols, v = r32.cpu().numpy(), c32.cpu().numpy(), vals.cpu().numpy()
     Xh = X.cpu().numpy()
-    H = swtcf.coo_to_hybrid(r32, c32, vals, n, n, min_tile_nnz=32, group_blocks=4, phases=4)
+    H = swtcf.coo_to_hybrid(r32, c32, vals, n, n, min_tile_nnz=min_nnz, group_blocks=G, phases=4,
+                            tile_format=swtcf.TILES_BF16X2 if split else swtcf.TILES_FP32)
     t = H.view.tiles
-    print(f"config 3 hybrid: {t.num_tiles} tiles in {t.num_steps} steps, {t.nnz} tile entries, "
-          f"{H.rest.view.nnz} in the remainder", flush=True)
+    print(f"config 3 hybrid (min {min_nnz}, G {G}, split {split}): {t.num_tiles} tiles in {t.num_steps} steps, "
+          f"{t.nnz} tile entries, {H.rest.view.nnz} in the remainder", flush=True)
     assert t.nnz + H.rest.view.nnz == r32.numel() and t.nnz > r32.numel() // 3
     Y = swtcf.hybrid_spmm(H, X)
     r_dev, want = check_weighted(oracle, Y, n, rows, cols, v, n, Xh, 35, what="config 3 hybrid")

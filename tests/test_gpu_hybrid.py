@@ -10,7 +10,8 @@ Checked through the C-ABI:
   other slots; units of unit_steps steps; the other entries' BCSR equal to
   the oracle's BCSR of exactly those entries;
 - the products against the fp64 CSR oracle on TF32-rounded inputs (rel-L2
-  <= 1e-5), Y = AX and Y += AX, over thresholds from 1 (every tile dense) to
+  <= 1e-5) for both tile formats (fp32 A operand; TF32 split into two bf16,
+  four exact bf16 products), in a workspace of NaN bytes, Y = AX and Y += AX, over thresholds from 1 (every tile dense) to
   256 (no tile dense), groups of 1, 2, 4 and 8 row blocks (row counts that
   leave the last group partly empty), groups shared by many units (their
   partial sums reduced in a second pass), unit sizes 1 to 64, phased
@@ -58,7 +59,16 @@ def tf32(a):
     return np.where(fin, (b + 0x1000) & 0xFFFFE000, b).astype(np.uint32).view(np.float32)
 
 
-def reference_layout(dst, src, vals, nr, nc, min_nnz, G, unit_steps):
+def bf16_split(x):
+    """hi = top 16 bits of the TF32 value, lo = top 16 bits of the exact remainder (0 for inf/NaN)."""
+    b = np.asarray(x, np.float32).view(np.uint32)
+    hi = (b >> 16).astype(np.uint16)
+    rest = (np.asarray(x, np.float32) - (b & 0xFFFF0000).view(np.float32)).view(np.uint32)
+    lo = np.where((b & 0x7F800000) == 0x7F800000, 0, rest >> 16).astype(np.uint16)
+    return hi, lo
+
+
+def reference_layout(dst, src, vals, nr, nc, min_nnz, G, unit_steps, split=False):
     dst = dst.astype(np.int64)
     src = src.astype(np.int64)
     rorder = np.lexsort((np.arange(nr), -np.bincount(dst, minlength=nr)))
@@ -81,9 +91,15 @@ def reference_layout(dst, src, vals, nr, nc, min_nnz, G, unit_steps):
     S = step_keys.size
     sid = np.searchsorted(step_keys, (rb[in_dense] // G) * CB + cb[in_dense])
     vals_all = np.ones(dst.size, np.float32) if vals is None else vals
-    tv = np.zeros((S, G, 64, 4), np.float32)
     i, j = rr[in_dense] % 16, cr[in_dense] % 16
-    tv[sid, rb[in_dense] % G, i + 16 * (j % 4), j // 4] = tf32(vals_all[in_dense])
+    if split:  # [step][row block][hi, lo][row][column], bf16 bits
+        tv = np.zeros((S, G, 2, 16, 16), np.uint16)
+        hi, lo = bf16_split(tf32(vals_all[in_dense]))
+        tv[sid, rb[in_dense] % G, 0, i, j] = hi
+        tv[sid, rb[in_dense] % G, 1, i, j] = lo
+    else:  # the fp32 MFMA's A operand: [step][row block][lane][k-step]
+        tv = np.zeros((S, G, 64, 4), np.float32)
+        tv[sid, rb[in_dense] % G, i + 16 * (j % 4), j // 4] = tf32(vals_all[in_dense])
     sg, sc = step_keys // CB, step_keys % CB
     gso = np.searchsorted(sg, np.arange(NG + 1)).astype(np.uint32)
     units = []
@@ -104,6 +120,7 @@ def oracle_product(oracle, dst, src, vals, nr, X):
     return oracle.csr_spmm(rowptr, src[order], None if vals is None else vals[order], X, use_tf32=True)
 
 
+@pytest.mark.parametrize("split", [False, True])
 @pytest.mark.parametrize("nr, nc, nnz, hubs, min_nnz, G, unit_steps, values", [
     (500, 700, 30000, True, 32, 4, 4, True),
     (500, 700, 30000, True, 8, 8, 0, False),
@@ -113,18 +130,20 @@ def oracle_product(oracle, dst, src, vals, nr, X):
     (40, 900, 9000, True, 6, 8, 64, True),     # fewer rows than one group
     (60, 60, 0, False, 32, 0, 0, True),
 ])
-def test_arrays_match_numpy_layout(gpu, oracle, nr, nc, nnz, hubs, min_nnz, G, unit_steps, values):
+def test_arrays_match_numpy_layout(gpu, oracle, nr, nc, nnz, hubs, min_nnz, G, unit_steps, values, split):
     from tcc_amd import swtcf
 
     dst, src = random_coo(nr, nc, nnz, nr * 3 + nc + nnz, hubs)
     vals = np.random.default_rng(9).uniform(-1, 1, dst.size).astype(np.float32) if values else None
     H = swtcf.coo_to_hybrid(dev_u32(dst), dev_u32(src), None if vals is None else torch.from_numpy(vals).cuda(), nr, nc,
-                            min_tile_nnz=min_nnz, group_blocks=G, unit_steps=unit_steps)
+                            min_tile_nnz=min_nnz, group_blocks=G, unit_steps=unit_steps,
+                            tile_format=swtcf.TILES_BF16X2 if split else swtcf.TILES_FP32)
     h = H.to_host()
-    want = reference_layout(dst, src, vals, nr, nc, min_nnz, G or 4, unit_steps or 64)
+    want = reference_layout(dst, src, vals, nr, nc, min_nnz, G or 8, unit_steps or 64, split)
+    assert h["tile_format"] == (1 if split else 0)
     print(f"hybrid layout nr={nr} nc={nc} nnz={nnz} G={G}: {h['num_steps']} steps, {h['num_tiles']} tiles, "
           f"{h['tile_nnz']} tile entries", flush=True)
-    assert h["group_blocks"] == (G or 4) and h["unit_steps"] == (unit_steps or 64)
+    assert h["group_blocks"] == (G or 8) and h["unit_steps"] == (unit_steps or 64)
     assert h["hub_cols"] == want["hub_cols"] and h["num_tiles"] == want["num_tiles"]
     for k in ("rowOrder", "hubColOrder", "groupStepOffset", "stepCol", "units"):
         assert np.array_equal(h[k], want[k]), k
@@ -166,20 +185,24 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("split", [False, True])
 @pytest.mark.parametrize("nr, nc, nnz, hubs, min_nnz, G, unit_steps, phases, values, F", CASES)
-def test_hybrid_spmm_vs_oracle(gpu, oracle, nr, nc, nnz, hubs, min_nnz, G, unit_steps, phases, values, F):
+def test_hybrid_spmm_vs_oracle(gpu, oracle, nr, nc, nnz, hubs, min_nnz, G, unit_steps, phases, values, F, split):
     from tcc_amd import swtcf
 
     print(f"hybrid nr={nr} nc={nc} nnz={nnz} min_nnz={min_nnz} G={G} unit_steps={unit_steps} phases={phases} "
-          f"values={values} F={F}", flush=True)
+          f"values={values} F={F} split={split}", flush=True)
     dst, src = random_coo(nr, nc, nnz, 5 * nr + nc + F, hubs)
     rng = np.random.default_rng(F + nnz + min_nnz)
     vals = rng.uniform(-1, 1, dst.size).astype(np.float32) if values else None
     X = rng.standard_normal((nc, F)).astype(np.float32)
     H = swtcf.coo_to_hybrid(dev_u32(dst), dev_u32(src), None if vals is None else torch.from_numpy(vals).cuda(), nr, nc,
-                            min_tile_nnz=min_nnz, group_blocks=G, unit_steps=unit_steps, phases=phases)
+                            min_tile_nnz=min_nnz, group_blocks=G, unit_steps=unit_steps, phases=phases,
+                            tile_format=swtcf.TILES_BF16X2 if split else swtcf.TILES_FP32)
     Xd = torch.from_numpy(X).cuda()
-    Y = swtcf.hybrid_spmm(H, Xd)
+    # a workspace of NaN bytes: no product may read what it did not write
+    ws = torch.full((H.workspace_bytes(F) + 16,), 255, dtype=torch.uint8, device="cuda")
+    Y = swtcf.hybrid_spmm(H, Xd, workspace=ws)
     want = oracle_product(oracle, dst, src, vals, nr, X)
     got = Y.cpu().numpy()
     assert got.shape[0] >= nr
@@ -188,11 +211,11 @@ def test_hybrid_spmm_vs_oracle(gpu, oracle, nr, nc, nnz, hubs, min_nnz, G, unit_
     assert not np.any(got[nr:])
     Y0 = rng.standard_normal(got.shape).astype(np.float32)
     Yd = torch.from_numpy(Y0).cuda()
-    swtcf.hybrid_spmm(H, Xd, Yd, accumulate=True)
+    swtcf.hybrid_spmm(H, Xd, Yd, accumulate=True, workspace=ws)
     e = rel_l2(Yd.cpu().numpy()[:nr], want + Y0[:nr])
     assert e <= REL, f"accumulate rel-L2 {e}"
     # a second product into the same Y (tiles add into the remainder's fill)
-    swtcf.hybrid_spmm(H, Xd, Y)
+    swtcf.hybrid_spmm(H, Xd, Y, workspace=ws)
     assert rel_l2(Y.cpu().numpy()[:nr], want) <= REL
 
 
@@ -208,6 +231,9 @@ def test_hybrid_errors(gpu):
     with pytest.raises(_lib.TccError, match="unitSteps above 64"):
         swtcf.coo_to_hybrid(dev_u32(np.array([0], np.uint32)), dev_u32(np.array([1], np.uint32)), None, 4, 4,
                             unit_steps=65)
+    with pytest.raises(_lib.TccError, match="tileFormat"):
+        swtcf.coo_to_hybrid(dev_u32(np.array([0], np.uint32)), dev_u32(np.array([1], np.uint32)), None, 4, 4,
+                            tile_format=2)
     with pytest.raises(_lib.TccError, match="groupBlocks"):
         swtcf.coo_to_hybrid(dev_u32(np.array([0], np.uint32)), dev_u32(np.array([1], np.uint32)), None, 4, 4,
                             group_blocks=3)
