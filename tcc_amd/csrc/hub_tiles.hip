@@ -450,15 +450,11 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_kernel(TileArgs a) {
 // both bf16, and a bf16 product is exact in fp32, so a·x = ah·xh + ah·xl +
 // al·xh + al·xl accumulates in fp32 like the fp32 MFMA of TF32 operands, at
 // four bf16 products per TF32 one: v_mfma_f32_16x16x32_bf16 runs 16x the
-// fp32 MFMA's rate.  Per tile and 16 features the products are two K=32
-// MFMAs over k' = (lane group q = l/16, element e): lanes q = 0,1 carry
-// k = 8q+e of xh and lanes q = 2,3 the same k of xl, against ah (first
-// MFMA) or al (second) of column k = 8(q%2)+e on every lane group
-// (D[i][j] = sum_q sum_e A[lane i+16q][e] B[lane j+16q][e], checked on the
-// GPU).  Xs holds the hub rows transposed per column block:
-// Xs[cb][f] = 16 hi then 16 lo bf16 of rows 16cb..16cb+15 (64 bytes), so
-// that lane (j + 16q) of N tile u reads 16 bytes at
-// Xs[cb][f0 + 16u + j] + 32(q/2) + 16(q%2).
+// fp32 MFMA's rate (D[i][j] = sum_q sum_e A[lane i+16q][e] B[lane j+16q][e]
+// over lane groups q = l/16 and elements e, checked on the GPU).  Xs holds
+// the hub rows transposed per column block: Xs[cb][f] = 16 hi then 16 lo
+// bf16 of rows 16cb..16cb+15 (64 bytes), so that a lane's 8 values of one
+// k-half are one 16-byte load.
 __global__ void hub_rows_split_kernel(const float* __restrict__ X, std::uint32_t F,
                                       const std::uint32_t* __restrict__ order, std::uint32_t hubCols,
                                       std::uint32_t hubRows, std::uint32_t ldh, std::uint16_t* __restrict__ Xs) {
@@ -486,14 +482,18 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 template <int G>
 struct SplitOperands {
-    vu4 ah[G];
-    vu4 al[G];
-    vu4 b[4];
+    vu4 a[G];      // lane group q < 2: ah of k = 8q..8q+7; q >= 2: al of k = 8(q-2)..
+    vu4 bh[4];     // xh of k = 8(q%2)..8(q%2)+7, feature f0 + 16u + l%16
+    vu4 bl[4];     // xl of the same k and feature
 };
 
-// As hub_tiles_kernel, over split tiles: per step 2G loads of A (hi, lo),
-// four of Xs, and 8G bf16 MFMAs.  D of N tile u holds rows 4q + v,
-// feature f0 + 16u + (l%16).
+// As hub_tiles_kernel, over split tiles.  Per tile and 16 features, two
+// K = 32 MFMAs over k' = (lane group q, element e): A' = [ah | al] (lane
+// groups 0-1 ah, 2-3 al, of k = 8(q%2) + e) against B = [xh ; xh], then
+// against [xl ; xl]: ah·xh + al·xh, then ah·xl + al·xl.  Every A lane
+// reads its own 16 bytes of the tile (no lane duplicates another), two
+// 16-byte loads of Xs per N tile.  D of N tile u holds rows 4q + v, feature
+// f0 + 16u + (l%16).
 template <int G, int NS>
 __global__ void __launch_bounds__(kThreads) hub_tiles_split_kernel(TileArgs a) {
     const unsigned lane = __lane_id();
@@ -508,24 +508,24 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_split_kernel(TileArgs a) {
     const unsigned li = lane & 15u, lq = lane >> 4;
     const std::uint32_t last = p1 - 1;
     const int cols = static_cast<int>(a.stepCol[min(p0 + lane, last)]);
-    const char* xb = reinterpret_cast<const char*>(a.Xh) + (static_cast<std::uint64_t>(f0 + li) * 64 + (lq >> 1) * 32 +
-                                                           (lq & 1u) * 16);
+    // Xs: 16 hi then 16 lo bf16 per (column block, feature); this lane's k-half
+    const char* xb = reinterpret_cast<const char*>(a.Xh) + (static_cast<std::uint64_t>(f0 + li) * 64 + (lq & 1u) * 16);
     const std::uint64_t cbStride = static_cast<std::uint64_t>(a.ldh) * 64;
-    const char* ab = reinterpret_cast<const char*>(a.tileVals) + li * 32 + (lq & 1u) * 16;
+    // tile: 256 hi then 256 lo bf16, row-major; this lane's row li, k-half, hi or lo
+    const char* ab = reinterpret_cast<const char*>(a.tileVals) + (lq >> 1) * 512 + li * 32 + (lq & 1u) * 16;
 
     auto load = [&](std::uint32_t p, SplitOperands<G>& o) {
         const std::uint32_t pa = p <= last ? p : a.zeroStep;
         const std::uint32_t col =
             static_cast<std::uint32_t>(__builtin_amdgcn_readlane(cols, static_cast<int>(min(p, last) - p0)));
 #pragma unroll
-        for (int j = 0; j < G; ++j) {
-            const char* t = ab + (static_cast<std::uint64_t>(pa) * G + j) * (kTileVals * 4);
-            o.ah[j] = load_global<vu4>(t);
-            o.al[j] = load_global<vu4>(t + 512);
-        }
+        for (int j = 0; j < G; ++j) o.a[j] = load_global<vu4>(ab + (static_cast<std::uint64_t>(pa) * G + j) * (kTileVals * 4));
         const char* rb = xb + col * cbStride;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) o.b[u] = load_global<vu4>(rb + u * 16 * 64);
+        for (int u = 0; u < 4; ++u) {
+            o.bh[u] = load_global<vu4>(rb + u * 16 * 64);
+            o.bl[u] = load_global<vu4>(rb + u * 16 * 64 + 32);
+        }
     };
     f32x4 acc[G][4];
 #pragma unroll
@@ -537,10 +537,10 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_split_kernel(TileArgs a) {
         for (int j = 0; j < G; ++j)
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                const bf16x8 bu = __builtin_bit_cast(bf16x8, o.b[u]);
-                acc[j][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, o.ah[j]), bu, acc[j][u], 0,
+                const bf16x8 aj = __builtin_bit_cast(bf16x8, o.a[j]);
+                acc[j][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aj, __builtin_bit_cast(bf16x8, o.bh[u]), acc[j][u], 0,
                                                                     0, 0);
-                acc[j][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, o.al[j]), bu, acc[j][u], 0,
+                acc[j][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aj, __builtin_bit_cast(bf16x8, o.bl[u]), acc[j][u], 0,
                                                                     0, 0);
             }
     };
@@ -645,8 +645,9 @@ inline std::uint32_t hub_rows(std::uint32_t hubCols) { return (hubCols + kTile -
 template <int G>
 hipError_t launch_tiles(const TileArgs& a, std::uint64_t waves, bool split, hipStream_t st) {
     constexpr int NS = G <= 2 ? 3 : 2;
+    // split tiles: two stages (a third measured slower at G = 4, equal at G = 8)
     if (split)
-        hipLaunchKernelGGL((hub_tiles_split_kernel<G, NS>), dim3(grid_for(waves, kThreads / kWave)), dim3(kThreads), 0,
+        hipLaunchKernelGGL((hub_tiles_split_kernel<G, 2>), dim3(grid_for(waves, kThreads / kWave)), dim3(kThreads), 0,
                            st, a);
     else
         hipLaunchKernelGGL((hub_tiles_kernel<G, NS>), dim3(grid_for(waves, kThreads / kWave)), dim3(kThreads), 0, st, a);
