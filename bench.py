@@ -88,6 +88,9 @@ def parse(argv=None):
     p.add_argument("--cpu-threads", type=int, default=0, help="0 = all host cores")
     p.add_argument("--copy-calibration-mib", type=int, default=0,
                    help="first run one plain device copy of this many MiB (scale for rocprofv3 FETCH/WRITE_SIZE)")
+    p.add_argument("--profile-convert", action="store_true",
+                   help="configs 1-3: time only convertCOOToSWTCF (S = 16), warmup + steps conversions, and print "
+                        "one JSON line (for rocprofv3 runs of the converter)")
     p.add_argument("--profile-step", action="store_true",
                    help="for counter runs: only the timed step's kernels run (warmup + steps times); no CPU "
                         "baseline, comparisons, conversions or extra configs")
@@ -261,13 +264,20 @@ def timed(step, steps, warmup):
 
 
 def copy_calibration(mib):
+    """One calibration_copy_kernel dispatch reading and writing exactly `mib`
+    MiB (tcc_calibration_copy), after which the source is evicted from the
+    caches by writing a second buffer of the same size."""
     import torch
+
+    from tcc_amd import _lib
 
     nfl = mib * (1 << 20) // 4
     a_src = torch.ones(nfl, device="cuda")
     a_dst = torch.empty_like(a_src)
+    a_dst.fill_(2.0)  # evicts a_src from the L2 and the last-level cache
     torch.cuda.synchronize()
-    a_dst.copy_(a_src)  # reads and writes exactly `mib` MiB
+    _lib.check(_lib.lib().tcc_calibration_copy(a_dst.data_ptr(), a_src.data_ptr(), nfl * 4,
+                                               torch.cuda.current_stream().cuda_stream))
     torch.cuda.synchronize()
     del a_src, a_dst
 
@@ -297,6 +307,28 @@ def swtcf_timings(torch, swtcf, m, X, n, nnz, F):
     return {"F": F, "S": 16, "fp32_ms": round(fp32_ms, 4), "fp32_gflops": gf(fp32_ms),
             "int8_ms": round(q_ms, 4), "int8_gflops": gf(q_ms),
             "X_bytes_fp32": 4 * n * F, "X_bytes_int8": n * F + 4 * n}
+
+
+def bench_convert(args, torch, swtcf, cfg):
+    """convertCOOToSWTCF (S = 16) of the config's COO alone: warmup + steps
+    conversions, the timed ones between HIP events."""
+    from tcc_amd.graphs import make_graph
+
+    if args.config not in (1, 2, 3):
+        raise SystemExit("--profile-convert takes configs 1-3")
+    n = cfg["n"]
+    rows, cols, _ = make_graph(args.config, device="cuda")
+    r32 = rows.to(torch.int32).contiguous()
+    c32 = cols.to(torch.int32).contiguous()
+    nnz = rows.numel()
+    del rows, cols
+    m = swtcf.DeviceSWTCFMatrix(n, n, nnz, 16)
+    ws = swtcf.SWTCFConvertWorkspace(nnz, n, 16)
+    ms = timed(lambda: swtcf.convertCOOToSWTCF(r32, c32, nnz, m, ws), args.steps, args.warmup)
+    assert ws.device_error() == 0
+    return {"metric": "convertCOOToSWTCF ms (S = 16)", "value": round(ms, 4), "unit": "ms", "steps": args.steps,
+            "warmup": args.warmup, "gedges_per_s": round(nnz / ms / 1e6, 3),
+            "config": {"workload": WORKLOADS[args.config], "n": n, "nnz": nnz}}
 
 
 def bench_spmm(args, torch, swtcf, cfg):
@@ -485,6 +517,8 @@ def bench_mixed(args, torch, swtcf, cfg):
         nonlocal Y
         Y = g1.aggregate(F, source=table.source)
 
+    if args.copy_calibration_mib:
+        copy_calibration(args.copy_calibration_mib)
     ms = timed(step, args.steps, args.warmup)
     torch.cuda.synchronize()
     cold_edge = ~table.hot[cols.long()]
@@ -498,7 +532,8 @@ def bench_mixed(args, torch, swtcf, cfg):
                            "achieved_GBps": round(cold_bytes / (ms * 1e-3) / 1e9, 2),
                            "peak_GBps": PCIE_PEAK_GBPS,
                            "bound_ms": round(cold_bytes / (PCIE_PEAK_GBPS * 1e9) * 1e3, 3)}}
-    extra["packed_rows"] = packed_rows_step(torch, table, X, cols, g1, F, Y, cold_rows_used, args)
+    if not args.profile_step:
+        extra["packed_rows"] = packed_rows_step(torch, table, X, cols, g1, F, Y, cold_rows_used, args)
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baselines(args, rows, cols, None, X, n, Y, 4, extra)
@@ -543,8 +578,13 @@ def gcn_timings(args, torch, cfg):
 
     steps = max(1, min(args.steps, 10))
     warmup = max(1, min(args.warmup, 3))
+    if args.profile_step:
+        print(f"[bench] profile-step: the epoch runs {warmup + steps} times", file=sys.stderr, flush=True)
     ms = timed(epoch, steps, warmup)
     first_loss, last_loss = float(losses[0].item()), float(losses[-1].item())
+    if args.profile_step:
+        table.free()
+        return ms, steps, warmup, {"loss_first": first_loss, "loss_last": last_loss}, rows.numel()
 
     g_h = torch.randn((n, hidden), device="cuda")
     g_c = torch.randn((n, classes), device="cuda")
@@ -626,6 +666,9 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs the GPU"
     torch.cuda.set_device(0)
     cfg = CONFIGS[args.config]
+    if args.profile_convert:
+        print(json.dumps(bench_convert(args, torch, swtcf, cfg)), flush=True)
+        return 0
     if args.config in (1, 2, 3):
         line = bench_spmm(args, torch, swtcf, cfg)
     elif args.config == 4:

@@ -141,6 +141,13 @@ int tcc_swtcf_spmm_quantized(const tcc_swtcf_matrix* m, const int8_t* quantizedX
 /* Text of the last host-side error on this thread ("" if none). */
 const char* tcc_last_error(void);
 
+/* A plain device copy of `bytes` (a multiple of 16; both pointers 16-byte
+ * aligned) by calibration_copy_kernel, whose HBM traffic is known (bytes read,
+ * bytes written): the reference run that scales rocprofv3's FETCH_SIZE and
+ * WRITE_SIZE into bytes (bench.py --copy-calibration-mib).  No reference
+ * counterpart. */
+int tcc_calibration_copy(void* dst, const void* src, size_t bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

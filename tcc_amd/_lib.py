@@ -126,6 +126,7 @@ SIGNATURES = {
     "tcc_hybrid_spmm": (ctypes.c_int, [ctypes.POINTER(Hybrid), vp, vp, u32, ctypes.c_int, vp, ctypes.c_size_t, vp]),
     "tcc_hub_tiles_spmm": (ctypes.c_int, [ctypes.POINTER(HubTiles), vp, vp, u32, vp, ctypes.c_size_t, vp]),
     "tcc_dense_tn_workspace_bytes": (ctypes.c_size_t, [u32, u32, u32]),
+    "tcc_calibration_copy": (ctypes.c_int, [vp, vp, ctypes.c_size_t, vp]),
     "tcc_dense_tn": (ctypes.c_int, [vp, u32, vp, u32, vp, u32, u32, u32, u32, ctypes.c_int, vp, ctypes.c_size_t, vp]),
     "tcc_dense_tn_noalloc": (ctypes.c_int, [vp, u32, vp, u32, vp, u32, u32, u32, u32, ctypes.c_int, vp]),
     "tcc_gcn_relu_forward": (ctypes.c_int, [vp, u32, vp, vp, vp, u32, vp, u32, u32, u32, u32, u32, vp]),

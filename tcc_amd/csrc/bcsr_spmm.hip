@@ -833,6 +833,13 @@ __global__ void __launch_bounds__(kThreads) narrow_gather_kernel(GatherArgs a) {
 
 // X [rows x F] fp32 -> packed TF32 rows (layout at packed_stride).  One
 // thread per element pair.
+// A grid-stride 16-byte copy (tcc_calibration_copy).
+__global__ void calibration_copy_kernel(vu4* __restrict__ dst, const vu4* __restrict__ src, std::uint64_t n) {
+    const std::uint64_t stride = static_cast<std::uint64_t>(gridDim.x) * blockDim.x;
+    for (std::uint64_t i = static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+        dst[i] = load_global<vu4>(src + i);
+}
+
 __global__ void tf32_pack_kernel(const float* __restrict__ X, std::uint32_t rows, std::uint32_t F,
                                  std::uint32_t pairs, unsigned char* __restrict__ out, std::uint64_t stride) {
     const std::uint64_t i = static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -1354,6 +1361,19 @@ int tcc_bcsr_spmm(const tcc_bcsr* A, const float* X, float* Y, std::uint32_t fea
 
 size_t tcc_tf32_packed_bytes(std::uint32_t rows, std::uint32_t featureDim) {
     return static_cast<size_t>(rows) * packed_stride(featureDim);
+}
+
+int tcc_calibration_copy(void* dst, const void* src, size_t bytes, void* stream) {
+    clear_last_error();
+    TCC_REQUIRE(bytes % 16 == 0 && (bytes == 0 || (dst && src)) && reinterpret_cast<std::uintptr_t>(dst) % 16 == 0 &&
+                    reinterpret_cast<std::uintptr_t>(src) % 16 == 0,
+                TCC_ERR_INVALID_ARGUMENT, "calibration copy: 16-byte multiples and alignment");
+    if (bytes == 0) return TCC_OK;
+    const std::uint64_t n = bytes / 16;
+    hipLaunchKernelGGL(calibration_copy_kernel, dim3(static_cast<unsigned>(std::min<std::uint64_t>((n + 255) / 256, 65536))),
+                       dim3(256), 0, as_stream(stream), static_cast<vu4*>(dst), static_cast<const vu4*>(src), n);
+    TCC_LAUNCH_CHECK();
+    return TCC_OK;
 }
 
 int tcc_tf32_pack(const float* X, std::uint32_t rows, std::uint32_t featureDim, void* packed, void* stream) {

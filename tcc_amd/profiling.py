@@ -4,6 +4,8 @@ bench.py's roofline reports).
 
     python -m tcc_amd.profiling stats --csv <kernel_stats.csv> --title T --command C [--kernels REGEX]
         --out profiles/<name>.md
+    python -m tcc_amd.profiling counters --csv <counter csv> --kernels REGEX --title T --command C
+        --out profiles/<name>.md
     python -m tcc_amd.profiling traffic --config N --fetch <FETCH_SIZE counter csv> --write <WRITE_SIZE csv>
         [--hits <TCC_HIT_sum TCC_MISS_sum csv>] --stats <kernel_stats.csv> --kernels REGEX --launches L
         --command C --out profiles/traffic_configN.json
@@ -11,7 +13,9 @@ bench.py's roofline reports).
 The counter runs profile `bench.py --profile-step --copy-calibration-mib
 1024`: only the timed step's kernels run L = warmup + steps times, and one
 1 GiB device copy gives the factors that turn FETCH_SIZE / WRITE_SIZE (KiB
-per dispatch) into bytes.
+per dispatch) into bytes (calibration_copy_kernel: known bytes read and
+written, unlike the runtime's blit copies, whose counters vary with what the
+process copied before).
 """
 from __future__ import annotations
 
@@ -26,7 +30,7 @@ import sys
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 KIB = 1024
-COPY_KERNEL = "copyBuffer"
+COPY_KERNEL = "calibration_copy_kernel"
 
 
 def kernel_key(name: str) -> str:
@@ -84,14 +88,59 @@ def stats_md(args) -> str:
     if args.kernels:
         pat = re.compile(args.kernels)
         step = [r for r in rows if pat.search(r["kernel"])]
-        lines += [f"Step kernels (`{args.kernels}`):", "", "| kernel | calls | avg ms |", "|---|---:|---:|"]
-        lines += [f"| `{r['kernel']}` | {r['calls']} | {r['avg_ms']:.4f} |" for r in step]
-        lines += [f"| **sum of averages** | | **{sum(r['avg_ms'] for r in step):.4f}** |", ""]
+        if args.launches:
+            L = args.launches
+            lines += [f"Step kernels (`{args.kernels}`), {L} steps:", "", "| kernel | calls | avg ms | ms per step |",
+                      "|---|---:|---:|---:|"]
+            lines += [f"| `{r['kernel']}` | {r['calls']} | {r['avg_ms']:.4f} | {r['total_ms'] / L:.4f} |" for r in step]
+            lines += [f"| **per step** | | | **{sum(r['total_ms'] for r in step) / L:.4f}** |", ""]
+        else:
+            lines += [f"Step kernels (`{args.kernels}`):", "", "| kernel | calls | avg ms |", "|---|---:|---:|"]
+            lines += [f"| `{r['kernel']}` | {r['calls']} | {r['avg_ms']:.4f} |" for r in step]
+            lines += [f"| **sum of averages** | | **{sum(r['avg_ms'] for r in step):.4f}** |", ""]
     lines += ["All kernels, by total time:", "",
               "| kernel | calls | avg ms | total ms | % of GPU time |", "|---|---:|---:|---:|---:|"]
     for r in rows[: args.top]:
         lines.append(f"| `{_short(r['kernel'])}` | {r['calls']} | {r['avg_ms']:.4f} | {r['total_ms']:.2f} | "
                      f"{100 * r['total_ms'] / total:.1f} |")
+    if args.note:
+        lines += ["", args.note]
+    return "\n".join(lines) + "\n"
+
+
+XCDS, SIMDS = 8, 1024  # MI355X: GRBM_GUI_ACTIVE is summed over the XCDs; 256 CUs x 4 SIMDs
+
+
+def counters_md(args) -> str:
+    """Per-kernel means of one counter pass, with the MFMA-busy fraction
+    SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / XCDs x SIMDs) and the
+    dependency-wait fraction SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES when present."""
+    per = read_counters(args.csv)
+    pat = re.compile(args.kernels)
+    names = sorted({c for k, cs in per.items() if pat.search(k) for c in cs})
+    lines = [f"# {args.title}", "", "Command (from the repository root on the GPU box, TMPDIR=/tmp):", "", "```",
+             args.command, "```", "", "Means per dispatch:", ""]
+    extra = []
+    if "SQ_VALU_MFMA_BUSY_CYCLES" in names and "GRBM_GUI_ACTIVE" in names:
+        extra.append("MFMA busy")
+    if "SQ_WAIT_INST_ANY" in names and "SQ_WAVE_CYCLES" in names:
+        extra.append("wait / wave cycles")
+    lines.append("| kernel | dispatches | " + " | ".join(names + extra) + " |")
+    lines.append("|---|---:|" + "---:|" * (len(names) + len(extra)))
+    for k in sorted(per):
+        if not pat.search(k):
+            continue
+        c = per[k]
+        mean = {n: sum(c[n]) / len(c[n]) for n in names if c.get(n)}
+        cells = [f"{mean[n]:,.0f}" if n in mean else "" for n in names]
+        if "MFMA busy" in extra:
+            gui = mean.get("GRBM_GUI_ACTIVE", 0)
+            cells.append(f"{mean.get('SQ_VALU_MFMA_BUSY_CYCLES', 0) / (gui / XCDS * SIMDS):.3f}" if gui else "")
+        if "wait / wave cycles" in extra:
+            wc = mean.get("SQ_WAVE_CYCLES", 0)
+            cells.append(f"{mean.get('SQ_WAIT_INST_ANY', 0) / wc:.3f}" if wc else "")
+        n_disp = max(len(v) for v in c.values())
+        lines.append(f"| `{_short(k)}` | {n_disp} | " + " | ".join(cells) + " |")
     if args.note:
         lines += ["", args.note]
     return "\n".join(lines) + "\n"
@@ -104,7 +153,8 @@ def traffic_json(args) -> dict:
     copy_f = [v for k, c in fetch.items() if COPY_KERNEL in k for v in c.get("FETCH_SIZE", [])]
     copy_w = [v for k, c in write.items() if COPY_KERNEL in k for v in c.get("WRITE_SIZE", [])]
     if not copy_f or not copy_w:
-        raise SystemExit("no copy-calibration dispatch in the counter files (run bench.py with --copy-calibration-mib)")
+        raise SystemExit("no calibration_copy_kernel dispatch in the counter files (run bench.py with "
+                         "--copy-calibration-mib)")
     gib_kib = (1 << 30) / KIB
     ff, fw = gib_kib / max(copy_f), gib_kib / max(copy_w)
     pat = re.compile(args.kernels)
@@ -148,8 +198,16 @@ def main(argv=None) -> int:
     s.add_argument("--command", required=True)
     s.add_argument("--note", default="")
     s.add_argument("--kernels", default="", help="regex over kernel names: the step's kernels, listed first")
+    s.add_argument("--launches", type=int, default=0, help="steps in the run: report each kernel's time per step")
     s.add_argument("--top", type=int, default=15)
     s.add_argument("--out", required=True)
+    c = sub.add_parser("counters")
+    c.add_argument("--csv", required=True)
+    c.add_argument("--kernels", required=True)
+    c.add_argument("--title", required=True)
+    c.add_argument("--command", required=True)
+    c.add_argument("--note", default="")
+    c.add_argument("--out", required=True)
     t = sub.add_parser("traffic")
     t.add_argument("--config", type=int, required=True)
     t.add_argument("--fetch", required=True)
@@ -163,6 +221,8 @@ def main(argv=None) -> int:
     args = ap.parse_args(argv)
     if args.cmd == "stats":
         text = stats_md(args)
+    elif args.cmd == "counters":
+        text = counters_md(args)
     else:
         text = json.dumps(traffic_json(args), indent=1) + "\n"
     with open(args.out, "w") as f:

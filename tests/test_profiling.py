@@ -13,6 +13,8 @@ def test_kernel_key_strips_arguments_and_namespaces():
     assert profiling.kernel_key("tcc::(anonymous namespace)::hub_reduce_kernel(tcc::(anonymous namespace)::TileArgs, "
                                 "unsigned int)") == "hub_reduce_kernel"
     assert profiling.kernel_key("__amd_rocclr_copyBuffer") == "__amd_rocclr_copyBuffer"
+    assert profiling.kernel_key("tcc::(anonymous namespace)::calibration_copy_kernel(unsigned int __vector(4)*, "
+                                "unsigned long)") == "calibration_copy_kernel"
 
 
 def _counters(path, rows):
@@ -36,7 +38,7 @@ def test_traffic_scales_by_the_copy_and_divides_by_launches(tmp_path):
     g = "void tcc::(anonymous namespace)::gather_kernel<4>(tcc::(anonymous namespace)::GatherArgs)"
     h = "void tcc::(anonymous namespace)::hub_tiles_kernel<4, 2>(tcc::(anonymous namespace)::TileArgs)"
     other = "tcc::(anonymous namespace)::degree_kernel(unsigned int const*)"
-    copy = "__amd_rocclr_copyBuffer"
+    copy = "tcc::(anonymous namespace)::calibration_copy_kernel(unsigned int __vector(4)*, unsigned int const __vector(4)*, unsigned long)"
     # the 1 GiB copy reads FETCH_SIZE 512 Ki (factor 2) and WRITE_SIZE 1 Gi KiB... (factor 1)
     _counters(tmp_path / "f.csv", [(copy, "FETCH_SIZE", 524288), (g, "FETCH_SIZE", 100), (g, "FETCH_SIZE", 300),
                                    (h, "FETCH_SIZE", 50), (h, "FETCH_SIZE", 50), (other, "FETCH_SIZE", 1e9)])
@@ -69,3 +71,17 @@ def test_stats_table(tmp_path):
     text = out.read_text()
     assert "python bench.py" in text
     assert "| `a_kernel` | 4 | 1.5000 | 6.00 | 92.3 |" in text
+
+
+def test_counters_table_mfma_busy(tmp_path):
+    k = "void tcc::(anonymous namespace)::dense_tn_kernel<4>(tcc::(anonymous namespace)::TnArgs)"
+    # 2 dispatches; GRBM_GUI_ACTIVE summed over 8 XCDs: 8 * 1000 cycles; busy 1024 SIMDs * 500
+    _counters(tmp_path / "c.csv", [(k, "GRBM_GUI_ACTIVE", 8000), (k, "GRBM_GUI_ACTIVE", 8000),
+                                   (k, "SQ_VALU_MFMA_BUSY_CYCLES", 512000), (k, "SQ_VALU_MFMA_BUSY_CYCLES", 512000),
+                                   (k, "SQ_WAIT_INST_ANY", 30), (k, "SQ_WAIT_INST_ANY", 30),
+                                   (k, "SQ_WAVE_CYCLES", 120), (k, "SQ_WAVE_CYCLES", 120)])
+    out = tmp_path / "c.md"
+    profiling.main(["counters", "--csv", str(tmp_path / "c.csv"), "--kernels", "dense_tn", "--title", "T",
+                    "--command", "cmd", "--out", str(out)])
+    row = [ln for ln in out.read_text().splitlines() if ln.startswith("| `dense_tn_kernel<4>`")][0]
+    assert row.endswith("| 0.500 | 0.250 |") and "| 2 |" in row
