@@ -88,6 +88,10 @@ def parse(argv=None):
     p.add_argument("--cpu-threads", type=int, default=0, help="0 = all host cores")
     p.add_argument("--copy-calibration-mib", type=int, default=0,
                    help="first run one plain device copy of this many MiB (scale for rocprofv3 FETCH/WRITE_SIZE)")
+    p.add_argument("--swtcf-ab", action="store_true",
+                   help="SWTCF SpMM: VALU path against MFMA for dense tiles, synthetic tiles of k = 8..64 entries")
+    p.add_argument("--swtcf-int8", action="store_true",
+                   help="SWTCF SpMM on the config-3 graph at F = 128: fp32 X against int8 X")
     p.add_argument("--profile-convert", action="store_true",
                    help="configs 1-3: time only convertCOOToSWTCF (S = 16), warmup + steps conversions, and print "
                         "one JSON line (for rocprofv3 runs of the converter)")
@@ -307,6 +311,113 @@ def swtcf_timings(torch, swtcf, m, X, n, nnz, F):
     return {"F": F, "S": 16, "fp32_ms": round(fp32_ms, 4), "fp32_gflops": gf(fp32_ms),
             "int8_ms": round(q_ms, 4), "int8_gflops": gf(q_ms),
             "X_bytes_fp32": 4 * n * F, "X_bytes_int8": n * F + 4 * n}
+
+
+def bench_swtcf_ab(args, torch, swtcf):
+    """SWTCF SpMM, VALU path against fp32 MFMA for dense tiles
+    (tcc_swtcf_spmm_mfma), on synthetic matrices whose 8x8 tiles all hold k
+    entries: 2048 rows x 2048 windows of 8 columns, every row holding k/8
+    random columns of every window (so each window's 256 tiles hold k
+    entries), F = 128, tcThreshold 0 (TF32 X on both paths)."""
+    R, CW, F = 2048, 2048, 128
+    out = {"metric": "SWTCF SpMM ms, VALU vs MFMA for tiles of k entries", "rows": R, "windows": CW, "F": F,
+           "tiles": R // 8 * CW, "steps": args.steps, "warmup": args.warmup, "per_k": []}
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    X = torch.randn((8 * CW, F), device="cuda", generator=gen)
+    for k in (8, 16, 24, 32, 40, 48, 56, 64):
+        pick = torch.rand((R, CW, 8), device="cuda", generator=gen).argsort(dim=2)[:, :, : k // 8]
+        dst = torch.arange(R, device="cuda", dtype=torch.int32).view(R, 1, 1).expand(R, CW, k // 8)
+        src = (torch.arange(CW, device="cuda", dtype=torch.int32).view(1, CW, 1) * 8 + pick.to(torch.int32))
+        order = torch.argsort(dst.reshape(-1).to(torch.int64) * (8 * CW) + src.reshape(-1))
+        d32 = dst.reshape(-1)[order].contiguous()
+        s32 = src.reshape(-1)[order].contiguous()
+        nnz = d32.numel()
+        m = swtcf.DeviceSWTCFMatrix(R, 8 * CW, nnz, 16)
+        ws = swtcf.SWTCFConvertWorkspace(nnz, 8 * CW, 16)
+        swtcf.convertCOOToSWTCF(d32, s32, nnz, m, ws)
+        assert ws.device_error() == 0
+        Ya = torch.zeros((R, F), device="cuda")
+        Yb = torch.zeros((R, F), device="cuda")
+        swtcf.swtcf_spmm_mfma(m, X, Ya, 0, 65)
+        swtcf.swtcf_spmm_mfma(m, X, Yb, 0, k)
+        torch.cuda.synchronize()
+        diff = ((Ya.double() - Yb.double()).norm() / Ya.double().norm()).item()
+        t_valu = timed(lambda: swtcf.swtcf_spmm_mfma(m, X, Ya, 0, 65), args.steps, args.warmup)
+        t_mfma = timed(lambda: swtcf.swtcf_spmm_mfma(m, X, Yb, 0, k), args.steps, args.warmup)
+        out["per_k"].append({"k": k, "nnz": nnz, "valu_ms": round(t_valu, 4), "mfma_ms": round(t_mfma, 4),
+                             "mfma_over_valu": round(t_mfma / t_valu, 3), "rel_l2_mfma_vs_valu": diff})
+        print(f"[bench] swtcf A/B k={k}: VALU {t_valu:.4f} ms, MFMA {t_mfma:.4f} ms", file=sys.stderr, flush=True)
+        del m, ws, Ya, Yb, pick, dst, src, order, d32, s32
+        torch.cuda.empty_cache()
+    # the benchmark graphs at F = 128, tcThreshold 12: VALU, then MFMA for
+    # tiles of >= 12 (the reference's tensor-core threshold) and >= 32
+    from tcc_amd.graphs import CONFIGS, make_graph
+
+    out["graphs"] = []
+    for c in (1, 2, 3):
+        n = CONFIGS[c]["n"]
+        rows, cols, _ = make_graph(c, device="cuda")
+        r32 = rows.to(torch.int32).contiguous()
+        c32 = cols.to(torch.int32).contiguous()
+        nnz = rows.numel()
+        del rows, cols
+        m = swtcf.DeviceSWTCFMatrix(n, n, nnz, 16)
+        ws = swtcf.SWTCFConvertWorkspace(nnz, n, 16)
+        swtcf.convertCOOToSWTCF(r32, c32, nnz, m, ws)
+        assert ws.device_error() == 0
+        del ws
+        Xg = torch.randn((n, F), device="cuda", generator=gen)
+        Y = torch.zeros((n, F), device="cuda")
+        steps, warmup = (args.steps, args.warmup) if c == 3 else (10 * args.steps, 10 * args.warmup)
+        e = {"config": c, "n": n, "nnz": nnz}
+        for mf in (65, 12, 32):
+            e[f"ms_mfma_ge_{mf}" if mf <= 64 else "ms_valu"] = round(
+                timed(lambda: swtcf.swtcf_spmm_mfma(m, Xg, Y, 12, mf), steps, warmup), 4)
+        out["graphs"].append(e)
+        print(f"[bench] swtcf A/B config {c}: {e}", file=sys.stderr, flush=True)
+        del m, Xg, Y, r32, c32
+        torch.cuda.empty_cache()
+    return out
+
+
+def bench_swtcf_int8(args, torch, swtcf):
+    """launchSWTCFSpMMQuantized (int8 X, per-row scales) against
+    launchSWTCFSpMM (fp32 X) on the config-3 graph at the reference's
+    F = 128, tcThreshold 12."""
+    from tcc_amd.graphs import CONFIGS, make_graph
+
+    n = CONFIGS[3]["n"]
+    rows, cols, _ = make_graph(3, device="cuda")
+    r32 = rows.to(torch.int32).contiguous()
+    c32 = cols.to(torch.int32).contiguous()
+    nnz = rows.numel()
+    del rows, cols
+    m = swtcf.DeviceSWTCFMatrix(n, n, nnz, 16)
+    ws = swtcf.SWTCFConvertWorkspace(nnz, n, 16)
+    swtcf.convertCOOToSWTCF(r32, c32, nnz, m, ws)
+    assert ws.device_error() == 0
+    del ws
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    X = torch.randn((n, 128), device="cuda", generator=gen)
+    scales = X.abs().amax(dim=1).clamp_min(1e-30) / 127.0
+    q = torch.round(X / scales[:, None]).clamp(-127, 127).to(torch.int8).contiguous()
+    srcGlobal = torch.arange(n, device="cuda", dtype=torch.int32)
+    Yf = torch.zeros((n, 128), device="cuda")
+    Yq = torch.zeros((n, 128), device="cuda")
+    t_f = timed(lambda: swtcf.launchSWTCFSpMM(m, X, Yf, 12), args.steps, args.warmup)
+    t_q = timed(lambda: swtcf.launchSWTCFSpMMQuantized(m, q, scales, srcGlobal, Yq, 12), args.steps, args.warmup)
+    Yf.zero_()
+    Yq.zero_()
+    swtcf.launchSWTCFSpMM(m, (q.float() * scales[:, None]).contiguous(), Yf, 12)
+    swtcf.launchSWTCFSpMMQuantized(m, q, scales, srcGlobal, Yq, 12)
+    torch.cuda.synchronize()
+    diff = ((Yq.double() - Yf.double()).norm() / Yf.double().norm()).item()
+    flops = 2.0 * nnz * 128
+    return {"metric": "SWTCF SpMM ms at F = 128, fp32 X vs int8 X", "n": n, "nnz": nnz, "F": 128,
+            "steps": args.steps, "warmup": args.warmup, "fp32_ms": round(t_f, 4), "int8_ms": round(t_q, 4),
+            "fp32_GFLOPs": round(flops / t_f / 1e6, 1), "int8_GFLOPs": round(flops / t_q / 1e6, 1),
+            "X_bytes_fp32": n * 128 * 4, "X_bytes_int8": n * 128 + 4 * n,
+            "rel_l2_int8_vs_fp32_on_dequantized_X": diff}
 
 
 def bench_convert(args, torch, swtcf, cfg):
@@ -668,6 +779,12 @@ def main():
     cfg = CONFIGS[args.config]
     if args.profile_convert:
         print(json.dumps(bench_convert(args, torch, swtcf, cfg)), flush=True)
+        return 0
+    if args.swtcf_ab:
+        print(json.dumps(bench_swtcf_ab(args, torch, swtcf)), flush=True)
+        return 0
+    if args.swtcf_int8:
+        print(json.dumps(bench_swtcf_int8(args, torch, swtcf)), flush=True)
         return 0
     if args.config in (1, 2, 3):
         line = bench_spmm(args, torch, swtcf, cfg)

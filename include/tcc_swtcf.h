@@ -132,6 +132,15 @@ int tcc_swtcf_spmm(const tcc_swtcf_matrix* m, const float* X, float* Y,
 int tcc_swtcf_spmm_f(const tcc_swtcf_matrix* m, const float* X, float* Y,
                      uint32_t featureDim, uint32_t tcThreshold, void* stream);
 
+/* tcc_swtcf_spmm_f with tiles of at least max(mfmaThreshold, tcThreshold)
+ * entries multiplied on fp32 MFMA (v_mfma_f32_16x16x4f32, two tiles of a
+ * window per instruction) instead of the vector ALUs; mfmaThreshold > 64
+ * never does.  Same numerics (TF32 X for those tiles), sums in another
+ * order.  No reference counterpart: the A/B of the reference's tensor-core
+ * split (src/swtcf_spmm.cu:188-241) on this GPU. */
+int tcc_swtcf_spmm_mfma(const tcc_swtcf_matrix* m, const float* X, float* Y, uint32_t featureDim,
+                        uint32_t tcThreshold, uint32_t mfmaThreshold, void* stream);
+
 /* launchSWTCFSpMMQuantized: X[src][f] = q[srcGlobal[src]*128+f] * scales[srcGlobal[src]]
  * (src/swtcf_spmm.cu:317-323), otherwise as tcc_swtcf_spmm. */
 int tcc_swtcf_spmm_quantized(const tcc_swtcf_matrix* m, const int8_t* quantizedX,

@@ -98,6 +98,7 @@ SIGNATURES = {
                                          vp]),
     "tcc_swtcf_spmm": (ctypes.c_int, [ctypes.POINTER(SWTCFMatrix), vp, vp, u32, vp]),
     "tcc_swtcf_spmm_f": (ctypes.c_int, [ctypes.POINTER(SWTCFMatrix), vp, vp, u32, u32, vp]),
+    "tcc_swtcf_spmm_mfma": (ctypes.c_int, [ctypes.POINTER(SWTCFMatrix), vp, vp, u32, u32, u32, vp]),
     "tcc_swtcf_spmm_quantized": (ctypes.c_int, [ctypes.POINTER(SWTCFMatrix), vp, vp, vp, vp, u32, vp]),
     "tcc_bcsr_spmm": (ctypes.c_int, [ctypes.POINTER(BCSR), vp, vp, u32, ctypes.c_int, vp]),
     "tcc_bcsr_spmm_mixed": (ctypes.c_int, [ctypes.POINTER(BCSR), ctypes.POINTER(FeatureSource), vp, u32,

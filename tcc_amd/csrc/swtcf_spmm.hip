@@ -69,7 +69,17 @@ __device__ __forceinline__ TileGroup load_tiles(const std::uint32_t* __restrict_
     return m;
 }
 
-template <bool QUANT>
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// MF: tiles holding at least max(mf, tc) entries are multiplied on fp32 MFMA
+// (v_mfma_f32_16x16x4f32), two tiles of the window per instruction (rows
+// 0-7 one tile, 8-15 the other; a lone tile pairs with an empty one).  The
+// window's TF32 X rows in the B layout (lane l: row 4s + l/16, feature
+// 16u + l%16 of the chunk) are gathered once per window with ds_bpermute;
+// A is the tiles' bitmap as 0/1.  Each lane then holds 4 tile rows x 1
+// feature per N tile, added to Y (or the repeat cache) like the VALU path's
+// row sums.
+template <bool QUANT, bool MF>
 __global__ void __launch_bounds__(kThreads) swtcf_spmm_kernel(
     const std::uint32_t* __restrict__ superWindowRowOffset, const std::uint32_t* __restrict__ superWindowRows,
     const std::uint8_t* __restrict__ rowCacheSlot, const std::uint32_t* __restrict__ cachedRowSlot,
@@ -77,7 +87,7 @@ __global__ void __launch_bounds__(kThreads) swtcf_spmm_kernel(
     const std::uint32_t* __restrict__ tileRowSlot, const std::uint64_t* __restrict__ tileLocalBit,
     const float* __restrict__ X, const std::int8_t* __restrict__ qX, const float* __restrict__ scales,
     const std::uint32_t* __restrict__ srcGlobal, float* __restrict__ Y, std::uint32_t cols, std::uint32_t CW,
-    std::uint32_t S, std::uint32_t F, std::uint32_t tc) {
+    std::uint32_t S, std::uint32_t F, std::uint32_t tc, std::uint32_t mf) {
     __shared__ float cache[TCC_SWTCF_REPEAT_CACHE_SIZE][kChunk];
 
     const std::uint32_t s = blockIdx.x;
@@ -126,13 +136,83 @@ __global__ void __launch_bounds__(kThreads) swtcf_spmm_kernel(
         }
 #pragma unroll
         for (int c = 0; c < 8; ++c) xt[c] = tf32_rna(xv[c]);
+        float bv[2][4];  // MF: the window's TF32 rows as MFMA B operands (k-step s, N tile u)
+        if constexpr (MF) {
+            const unsigned q = lane >> 4, j = lane & 15u;
+#pragma unroll
+            for (int st = 0; st < 2; ++st)
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int src = static_cast<int>((16 * u + j) * 4);
+                    float pick = 0.0f;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const float t =
+                            __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(xt[4 * st + k])));
+                        pick = q == static_cast<unsigned>(k) ? t : pick;
+                    }
+                    bv[st][u] = pick;
+                }
+        }
+        const std::uint32_t mfEff = max(mf, tc);
+        // MF: tiles ka and kb (kb < 0: none) of the current group on MFMA
+        const auto mfma_pair = [&](const TileGroup& grp, int ka, int kb) {
+            const unsigned i = lane & 15u, q = lane >> 4;
+            const std::uint64_t ba = (static_cast<std::uint64_t>(lane_u32(grp.bitsHi, ka)) << 32) | lane_u32(grp.bitsLo, ka);
+            const std::uint64_t bb =
+                kb < 0 ? 0ull : (static_cast<std::uint64_t>(lane_u32(grp.bitsHi, kb)) << 32) | lane_u32(grp.bitsLo, kb);
+            const std::uint64_t bt = i < 8 ? ba : bb;
+            const unsigned sh = 8 * (i & 7u);
+            f32x4 acc[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                const float a = ((bt >> (sh + 4 * st + q)) & 1ull) ? 1.0f : 0.0f;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bv[st][u], acc[u], 0, 0, 0);
+            }
+            // D(4q + v, i) of N tile u: row 4q + v of the pair, feature 16u + i of the chunk
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const unsigned rho = 4 * q + v;
+                const int tile = rho < 8 ? ka : kb;
+                const int srcLane = tile < 0 ? 0 : tile * 8 + static_cast<int>(rho & 7u);
+                std::uint32_t target = static_cast<std::uint32_t>(
+                    __builtin_amdgcn_ds_bpermute(srcLane * 4, static_cast<int>(grp.target)));
+                if (tile < 0) target = kNoTarget;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const float val = acc[u][v];
+                    const std::uint32_t fu = blockIdx.y * kChunk + 16 * u + i;
+                    if (target == kNoTarget || fu >= F || val == 0.0f) continue;
+                    if (target & kCached) {
+                        atomicAdd(&cache[target & 31u][16 * u + i], val);
+                    } else {
+                        atomic_add_f32(&Y[static_cast<std::uint64_t>(target) * F + fu], val);
+                    }
+                }
+            }
+        };
         for (std::uint32_t g = t0; g < t1; g += 8) {
             TileGroup nxt = cur;
             if (g + 8 < t1) nxt = load_tiles(tileRowSlot, tileLocalBit, rowCacheSlot, superWindowRows, off, g + 8, t1);
             const int nt = static_cast<int>(min(8u, t1 - g));
+            int pend = -1;  // MF: a tile of this group waiting for its MFMA partner
             for (int k = 0; k < nt; ++k) {
                 const std::uint64_t bm =
                     (static_cast<std::uint64_t>(lane_u32(cur.bitsHi, k)) << 32) | lane_u32(cur.bitsLo, k);
+                if constexpr (MF) {
+                    if (static_cast<std::uint32_t>(__popcll(bm)) >= mfEff) {
+                        if (pend < 0) {
+                            pend = k;
+                        } else {
+                            mfma_pair(cur, pend, k);
+                            pend = -1;
+                        }
+                        continue;
+                    }
+                }
                 const bool dense = static_cast<std::uint32_t>(__popcll(bm)) >= tc;
 #pragma unroll
                 for (int r = 0; r < 8; ++r) {
@@ -151,6 +231,9 @@ __global__ void __launch_bounds__(kThreads) swtcf_spmm_kernel(
                         atomic_add_f32(&Y[static_cast<std::uint64_t>(target) * F + f], sum);
                     }
                 }
+            }
+            if constexpr (MF) {
+                if (pend >= 0) mfma_pair(cur, pend, -1);
             }
             cur = nxt;
         }
@@ -218,9 +301,10 @@ __global__ void __launch_bounds__(kThreads) swtcf_spmm_kernel(
     }
 }
 
-template <bool QUANT>
+template <bool QUANT, bool MF = false>
 int launch(const tcc_swtcf_matrix* m, const float* X, const std::int8_t* qX, const float* scales,
-           const std::uint32_t* srcGlobal, float* Y, std::uint32_t F, std::uint32_t tc, void* stream) {
+           const std::uint32_t* srcGlobal, float* Y, std::uint32_t F, std::uint32_t tc, void* stream,
+           std::uint32_t mf = 0xFFFFFFFFu) {
     // Parts per super-window: enough workgroups for two per CU, at most 8,
     // and no more than one per 16 edges of an average window.
     const std::uint32_t chunks = (F + kChunk - 1) / kChunk;
@@ -229,11 +313,11 @@ int launch(const tcc_swtcf_matrix* m, const float* X, const std::int8_t* qX, con
     const std::uint64_t perWindow = m->numColWindows ? m->nnz / m->numColWindows : 0;
     Z = std::max<std::uint64_t>(1, std::min<std::uint64_t>({Z, 8, perWindow / 16}));
     const dim3 grid(m->numSuperWindows, chunks, static_cast<std::uint32_t>(Z));
-    hipLaunchKernelGGL(swtcf_spmm_kernel<QUANT>, grid, dim3(kThreads), 0, as_stream(stream),
+    hipLaunchKernelGGL((swtcf_spmm_kernel<QUANT, MF>), grid, dim3(kThreads), 0, as_stream(stream),
                        m->superWindowRowOffset, m->superWindowRows, m->superWindowRowCacheSlot,
                        m->superWindowCachedRowSlot, m->superWindowCachedCount, m->colWindowOffset, m->tileRowSlot,
                        m->tileLocalBit, X, qX, scales, srcGlobal, Y, m->cols, m->numColWindows,
-                       m->superWindowSize, F, tc);
+                       m->superWindowSize, F, tc, mf);
     TCC_LAUNCH_CHECK();
     return TCC_OK;
 }
@@ -253,6 +337,17 @@ int tcc_swtcf_spmm_f(const tcc_swtcf_matrix* m, const float* X, float* Y, std::u
                     m->superWindowSize <= TCC_SWTCF_MAX_SUPER_WINDOW_SIZE,
                 TCC_ERR_INVALID_ARGUMENT, "invalid SWTCF SpMM arguments");
     return launch<false>(m, X, nullptr, nullptr, nullptr, Y, featureDim, tcThreshold, stream);
+}
+
+int tcc_swtcf_spmm_mfma(const tcc_swtcf_matrix* m, const float* X, float* Y, std::uint32_t featureDim,
+                        std::uint32_t tcThreshold, std::uint32_t mfmaThreshold, void* stream) {
+    clear_last_error();
+    TCC_REQUIRE(m && X && Y, TCC_ERR_INVALID_ARGUMENT, "null argument");
+    TCC_REQUIRE(featureDim >= 1 && m->numSuperWindows >= 1 && m->superWindowSize >= 1 &&
+                    m->superWindowSize <= TCC_SWTCF_MAX_SUPER_WINDOW_SIZE,
+                TCC_ERR_INVALID_ARGUMENT, "invalid SWTCF SpMM arguments");
+    if (mfmaThreshold > 64) return launch<false>(m, X, nullptr, nullptr, nullptr, Y, featureDim, tcThreshold, stream);
+    return launch<false, true>(m, X, nullptr, nullptr, nullptr, Y, featureDim, tcThreshold, stream, mfmaThreshold);
 }
 
 int tcc_swtcf_spmm(const tcc_swtcf_matrix* m, const float* X, float* Y, std::uint32_t tcThreshold,

@@ -171,6 +171,15 @@ def swtcf_spmm(matrix: DeviceSWTCFMatrix, X: torch.Tensor, Y: torch.Tensor,
                                       _stream(stream)))
 
 
+def swtcf_spmm_mfma(matrix: DeviceSWTCFMatrix, X: torch.Tensor, Y: torch.Tensor,
+                    tcThreshold: int = DEFAULT_TC_THRESHOLD, mfmaThreshold: int = 65, stream=None) -> None:
+    """Y += A X with tiles of >= max(mfmaThreshold, tcThreshold) entries on
+    fp32 MFMA (tcc_swtcf_spmm_mfma; > 64: never)."""
+    F = X.shape[1]
+    check(_lib.lib().tcc_swtcf_spmm_mfma(ctypes.byref(matrix.m), X.data_ptr(), Y.data_ptr(), F, tcThreshold,
+                                         mfmaThreshold, _stream(stream)))
+
+
 def launchSWTCFSpMMQuantized(matrix: DeviceSWTCFMatrix, quantizedX: torch.Tensor, scales: torch.Tensor,
                              srcGlobal: torch.Tensor, Y: torch.Tensor, tcThreshold: int = DEFAULT_TC_THRESHOLD,
                              stream=None) -> None:

@@ -136,6 +136,37 @@ def test_swtcf_hub_windows_split_across_waves(gpu, oracle, F):
     assert_close(Y.cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("F", [1, 48, 100, 200])
+@pytest.mark.parametrize("mf", [0, 12, 32, 64, 65])
+def test_swtcf_spmm_mfma_vs_oracle(gpu, oracle, mf, F):
+    """tcc_swtcf_spmm_mfma: tiles of >= max(mf, tc) entries on fp32 MFMA,
+    two per instruction, on a graph with dense 8x8 blocks of every density
+    (8..64 entries, odd and even counts per window so that a tile is left
+    without a partner), an R-MAT part (repeat-cache rows, long windows) and
+    Y += A X; against the oracle's TF32 numerics for those tiles."""
+    from tcc_amd import swtcf
+    from tcc_amd.graphs import rmat_graph
+
+    n = 2000
+    rows, cols = rmat_graph(n, 30_000, 41)
+    keys = set((rows.numpy().astype(np.int64) * n + cols.numpy()).tolist())
+    rng = np.random.default_rng(42)
+    for b, k in enumerate([8, 16, 24, 32, 40, 48, 56, 64, 64, 33, 47, 12]):
+        r0, c0 = 8 * (10 + b), 8 * (3 + (b % 5))  # several blocks share a window
+        for bit in rng.choice(64, size=k, replace=False):
+            keys.add((r0 + bit // 8) * n + c0 + bit % 8)
+    key = np.array(sorted(keys), np.int64)
+    dst, src = (key // n).astype(np.uint32), (key % n).astype(np.uint32)
+    m = build_swtcf(dst, src, n, n)
+    X = np.random.default_rng(43).standard_normal((n, F)).astype(np.float32)
+    Y0 = np.random.default_rng(44).standard_normal((n, F)).astype(np.float32)
+    Y = torch.from_numpy(Y0.copy()).cuda()
+    swtcf.swtcf_spmm_mfma(m, torch.from_numpy(X).cuda(), Y, 12, mf)
+    ref = oracle.swtcf_convert(dst, src, n, n, 16)
+    want = oracle.swtcf_spmm(ref, X, tc=12, rows=n, Y=Y0.astype(np.float64))
+    assert_close(Y.cpu().numpy(), want)
+
+
 def test_swtcf_config1(gpu, oracle):
     from tcc_amd import swtcf
     from tcc_amd.graphs import make_features, uniform_graph
