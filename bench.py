@@ -95,6 +95,9 @@ def parse(argv=None):
     p.add_argument("--profile-convert", action="store_true",
                    help="configs 1-3: time only convertCOOToSWTCF (S = 16), warmup + steps conversions, and print "
                         "one JSON line (for rocprofv3 runs of the converter)")
+    p.add_argument("--convert-order", choices=("both", "dst-src", "shuffled"), default="both",
+                   help="with --profile-convert: time the COO in the generator's (dst, src) order, the same COO "
+                        "shuffled (every digit of the sort runs), or both")
     p.add_argument("--profile-step", action="store_true",
                    help="for counter runs: only the timed step's kernels run (warmup + steps times); no CPU "
                         "baseline, comparisons, conversions or extra configs")
@@ -435,11 +438,26 @@ def bench_convert(args, torch, swtcf, cfg):
     del rows, cols
     m = swtcf.DeviceSWTCFMatrix(n, n, nnz, 16)
     ws = swtcf.SWTCFConvertWorkspace(nnz, n, 16)
-    ms = timed(lambda: swtcf.convertCOOToSWTCF(r32, c32, nnz, m, ws), args.steps, args.warmup)
-    assert ws.device_error() == 0
-    return {"metric": "convertCOOToSWTCF ms (S = 16)", "value": round(ms, 4), "unit": "ms", "steps": args.steps,
-            "warmup": args.warmup, "gedges_per_s": round(nnz / ms / 1e6, 3),
-            "config": {"workload": WORKLOADS[args.config], "n": n, "nnz": nnz}}
+    out = {"metric": "convertCOOToSWTCF ms (S = 16)", "unit": "ms", "steps": args.steps, "warmup": args.warmup,
+           "config": {"workload": WORKLOADS[args.config], "n": n, "nnz": nnz}}
+    if args.convert_order in ("both", "dst-src"):
+        # the generator lists the COO in (dst, src) order: the sort's sw digits alone order it
+        ms = timed(lambda: swtcf.convertCOOToSWTCF(r32, c32, nnz, m, ws), args.steps, args.warmup)
+        assert ws.device_error() == 0
+        out.update(value=round(ms, 4), gedges_per_s=round(nnz / ms / 1e6, 3), input_order="(dst, src)")
+    if args.convert_order in ("both", "shuffled"):
+        # the same COO in random order: every digit of the sort runs
+        perm = torch.randperm(nnz, device="cuda", generator=torch.Generator(device="cuda").manual_seed(5))
+        r32, c32 = r32[perm].contiguous(), c32[perm].contiguous()
+        del perm
+        ms_s = timed(lambda: swtcf.convertCOOToSWTCF(r32, c32, nnz, m, ws), args.steps, args.warmup)
+        assert ws.device_error() == 0
+        key = "shuffled_ms" if "value" in out else "value"
+        out[key] = round(ms_s, 4)
+        out["shuffled_gedges_per_s"] = round(nnz / ms_s / 1e6, 3)
+        if key == "value":
+            out["input_order"] = "shuffled"
+    return out
 
 
 def bench_spmm(args, torch, swtcf, cfg):

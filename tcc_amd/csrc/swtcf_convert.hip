@@ -1,24 +1,34 @@
 // COO -> SWTCF conversion on gfx950 (reference: src/swtcf_convert.cu).
 //
 // Design (deterministic, no hash table, no atomic ranks):
-//   1. One stable LSD radix sort of a packed edge key
-//        key = sw | dst | wi | lc     (sw = super-window, wi = window in sw,
-//                                      lc = src & 7; high to low bits)
-//      sized to the bits the matrix needs (a 233k x 233k graph with S = 16
-//      needs 36 bits = 5 passes).
-//   2. Run boundaries of key>>3 are the (window, dst) groups (degree = run
-//      length, bitmap = OR of 1<<lc); runs of key>>(3+wiBits) are the
-//      distinct (super-window, dst) rows, already in dst-ascending slot order,
-//      and their run length in groups is the occurrence count.
-//   3. Per super-window, one workgroup walks its groups in order and gives
-//      each its rank inside its (window, degree) bucket with a stable
-//      wave-ballot multisplit, which is exactly the canonical
-//      (degree desc, dst asc) row order; then it ranks the repeated rows by
-//      (occurrence desc, slot asc) for the repeat cache.
-// Degree histograms use atomics only to count, which is order-independent.
+//   1. Each edge becomes a 64-bit element  sw << kb | dst << loBits | lo
+//      (sw = super-window = src / 8S, lo = src - 8S * sw, kb = dstBits +
+//      loBits), and a stable LSD radix sort puts the elements in
+//      (sw, dst, lo) order: the digits of the low kb bits first, then those
+//      of sw.  A COO already ordered by (dst, src) -- listed row by row, as
+//      CSR gives it -- needs only the sw digits, since a stable partition of
+//      that order by sw is the whole sort: the first pass detects such input
+//      and the low-digit passes then return at once.
+//   2. The elements of one super-window form a segment, cut into tiles of
+//      4096 that never straddle two segments.  In a segment, runs of key >> 3
+//      are the (window, dst) groups (degree = run length, bitmap = OR of
+//      1 << (lo & 7)), runs of key >> loBits are the distinct rows in slot
+//      (dst ascending) order, and the groups of a row are its occurrences.
+//   3. A count pass takes, per tile, the group heads per (window, degree),
+//      the row heads and the repeated rows per occurrence count; one scan
+//      over (bin, tile) gives each tile its offsets inside its segment, and
+//      the segment totals give each window its degree-bucket bases (degree 8
+//      first) and each super-window its repeat-cache bases.
+//   4. An emit pass finds the tile's heads again and writes every output in
+//      place: a head's rank in its bin is the tile's offset plus the earlier
+//      heads of the tile in that bin, which is the canonical (degree desc,
+//      dst asc) tile-row order and (occurrence desc, slot asc) cache order.
+// Atomics only count (LDS histograms, error flags), so the output is the
+// same run to run and equal to the CPU oracle's canonical form.
 #include <algorithm>
 #include <cstring>
 #include <new>
+#include <vector>
 
 #include "../../include/tcc_swtcf.h"
 #include "common.hpp"
@@ -29,6 +39,24 @@ namespace tcc {
 namespace {
 
 constexpr unsigned kThreads = 256;
+constexpr unsigned kWaves = kThreads / kWave;  // 4
+constexpr unsigned kRounds = 16;
+constexpr unsigned kTile = kThreads * kRounds;  // elements per sort tile and per segment tile
+constexpr unsigned kSpan = kWave * kRounds;     // consecutive elements of one wave
+constexpr unsigned kMaxLowDigit = 9;            // bits per pass over dst/lo
+constexpr unsigned kMaxTopDigit = 8;            // bits per pass over sw
+constexpr unsigned kMaxBins = 1u << kMaxLowDigit;
+constexpr unsigned kMaxS = TCC_SWTCF_MAX_SUPER_WINDOW_SIZE;
+constexpr unsigned kCache = TCC_SWTCF_REPEAT_CACHE_SIZE;
+// Elements past a tile's end that its heads read: a row has at most 8S
+// elements unless a group has more than 8 (which raises the degree error).
+constexpr unsigned kLookahead = 8 * kMaxS + 8;
+// Counter bins of a segment tile: [0, 8S) group heads by (wi, degree - 1);
+// 8S row heads; 8S + occ - 1 repeated rows by occurrence occ in [2, 32];
+// 8S + 32 all group heads.
+constexpr unsigned kOccBins = kMaxS - 1;
+__host__ __device__ inline unsigned num_bins(unsigned S) { return 8 * S + 33; }
+constexpr unsigned kOccStride = kMaxS + 1;  // occBase[s * 33 + occ]
 
 inline unsigned ceil_log2(std::uint64_t x) {
     unsigned b = 0;
@@ -36,40 +64,71 @@ inline unsigned ceil_log2(std::uint64_t x) {
     return b;
 }
 
-struct KeyLayout {
-    unsigned wiBits, dstBits, swBits, total;
+// Element packing and the range checks of buildEdgeKeysKernel (:104-144).
+struct ElemParams {
+    std::uint32_t rows, cols;
+    std::uint32_t span;  // 8S sources per super-window
+    unsigned loBits, kb;
 };
 
-inline KeyLayout key_layout(std::uint32_t rows, std::uint32_t S, std::uint32_t numSuperWindows) {
-    KeyLayout k;
-    k.wiBits = ceil_log2(S);
-    k.dstBits = rows ? std::max(1u, ceil_log2(rows)) : 32u;
-    k.swBits = ceil_log2(numSuperWindows);
-    k.total = k.swBits + k.dstBits + k.wiBits + 3;
-    return k;
+struct Digit {
+    unsigned shift, bits;
+};
+
+struct Plan {
+    ElemParams ep;
+    unsigned swBits;
+    std::vector<Digit> low, top;
+};
+
+inline void split_digits(unsigned shift, unsigned bits, unsigned maxBits, std::vector<Digit>& out) {
+    const unsigned passes = (bits + maxBits - 1) / maxBits;
+    for (unsigned p = 0; p < passes; ++p) {
+        const unsigned w = bits / passes + (p < bits % passes ? 1u : 0u);
+        out.push_back({shift, w});
+        shift += w;
+    }
 }
+
+inline Plan make_plan(std::uint32_t rows, std::uint32_t cols, std::uint32_t S, std::uint32_t numSuperWindows) {
+    Plan p;
+    p.ep.rows = rows;
+    p.ep.cols = cols;
+    p.ep.span = 8 * S;
+    p.ep.loBits = std::max(3u, ceil_log2(8ull * S));
+    const unsigned dstBits = rows ? std::max(1u, ceil_log2(rows)) : 32u;
+    p.ep.kb = dstBits + p.ep.loBits;
+    p.swBits = std::max(1u, ceil_log2(numSuperWindows));
+    split_digits(0, p.ep.kb, kMaxLowDigit, p.low);
+    split_digits(p.ep.kb, p.swBits, kMaxTopDigit, p.top);
+    return p;
+}
+
+inline std::uint64_t sort_tiles(std::uint64_t E) { return std::max<std::uint64_t>(1, (E + kTile - 1) / kTile); }
+inline std::uint64_t segment_tiles_max(std::uint64_t E, std::uint64_t SW) { return (E + kTile - 1) / kTile + SW; }
 
 // Byte layout of the workspace scratch allocation.
 struct Carve {
-    std::uint64_t* keysA;
-    std::uint64_t* keysB;
-    std::uint32_t* flags;          // [E+1] group heads, then row heads
-    std::uint32_t* pos;            // [E+1] exclusive scans of flags
-    std::uint32_t* groupStart;     // [E+1]
-    std::uint32_t* groupInfo;      // [E]   bits | degree << 8
-    std::uint32_t* rowStartGroup;  // [E+1]
-    std::uint32_t* wdCount;        // [CW*8]
-    std::uint32_t* wdBase;         // [CW*8]
-    std::uint32_t* wActive;        // [CW]
-    std::uint32_t* wTiles;         // [CW]
-    std::uint32_t* numRows;        // [1]
-    std::uint32_t* temp;           // scan / sort scratch
+    std::uint64_t* elemA;
+    std::uint64_t* elemB;
+    std::uint32_t* histLow;    // [512 * sortTiles] digit counts, (digit, tile) order
+    std::uint32_t* histTop;    // [512 * sortTiles]
+    std::uint32_t* counters;   // [bins * TM + 1] segment-tile counts, (bin, tile) order
+    std::uint32_t* segStart;   // [SW+1]
+    std::uint32_t* firstTile;  // [SW+1]
+    std::uint32_t* wdBase;     // [CW*8]
+    std::uint32_t* wActive;    // [CW]
+    std::uint32_t* wTiles;     // [CW]
+    std::uint32_t* occBase;    // [SW*33]
+    std::uint32_t* flags;      // [4]: [0] = input not in (dst, src) order
+    std::uint32_t* tileFlags;  // [sortTiles]: the input pass's tile is out of order
+    std::uint32_t* temp;       // scan scratch
     std::size_t bytes;
 };
 
 inline std::size_t align_up(std::size_t x) { return (x + 255) & ~std::size_t(255); }
 
-inline Carve carve(char* base, std::uint64_t E, std::uint64_t CW, std::uint64_t SW) {
+inline Carve carve(char* base, std::uint64_t E, std::uint64_t CW, std::uint64_t SW, std::uint32_t S) {
     Carve c{};
     std::size_t off = 0;
     auto take = [&](std::size_t bytes) {
@@ -77,326 +136,629 @@ inline Carve carve(char* base, std::uint64_t E, std::uint64_t CW, std::uint64_t 
         off = align_up(off + bytes);
         return p;
     };
-    c.keysA = reinterpret_cast<std::uint64_t*>(take(8 * E));
-    c.keysB = reinterpret_cast<std::uint64_t*>(take(8 * E));
-    c.flags = reinterpret_cast<std::uint32_t*>(take(4 * (E + 1)));
-    c.pos = reinterpret_cast<std::uint32_t*>(take(4 * (E + 1)));
-    c.groupStart = reinterpret_cast<std::uint32_t*>(take(4 * (E + 1)));
-    c.groupInfo = reinterpret_cast<std::uint32_t*>(take(4 * E));
-    c.rowStartGroup = reinterpret_cast<std::uint32_t*>(take(4 * (E + 1)));
-    c.wdCount = reinterpret_cast<std::uint32_t*>(take(4 * CW * 8));
+    const std::uint64_t hist = static_cast<std::uint64_t>(kMaxBins) * sort_tiles(E);
+    const std::uint64_t cnt = static_cast<std::uint64_t>(num_bins(S)) * segment_tiles_max(E, SW) + 1;
+    c.elemA = reinterpret_cast<std::uint64_t*>(take(8 * E));
+    c.elemB = reinterpret_cast<std::uint64_t*>(take(8 * E));
+    c.histLow = reinterpret_cast<std::uint32_t*>(take(4 * hist));
+    c.histTop = reinterpret_cast<std::uint32_t*>(take(4 * hist));
+    c.counters = reinterpret_cast<std::uint32_t*>(take(4 * cnt));
+    c.segStart = reinterpret_cast<std::uint32_t*>(take(4 * (SW + 1)));
+    c.firstTile = reinterpret_cast<std::uint32_t*>(take(4 * (SW + 1)));
     c.wdBase = reinterpret_cast<std::uint32_t*>(take(4 * CW * 8));
     c.wActive = reinterpret_cast<std::uint32_t*>(take(4 * CW));
     c.wTiles = reinterpret_cast<std::uint32_t*>(take(4 * CW));
-    c.numRows = reinterpret_cast<std::uint32_t*>(take(4 * 4));
-    const std::uint64_t tempElems =
-        std::max({radix_temp_elems(E), scan_temp_elems(E + 1), scan_temp_elems(CW + 1), scan_temp_elems(SW + 1)});
+    c.occBase = reinterpret_cast<std::uint32_t*>(take(4 * SW * kOccStride));
+    c.flags = reinterpret_cast<std::uint32_t*>(take(4 * 4));
+    c.tileFlags = reinterpret_cast<std::uint32_t*>(take(4 * sort_tiles(E)));
+    const std::uint64_t tempElems = std::max({scan_temp_elems(hist), scan_temp_elems(cnt), scan_temp_elems(CW + 1),
+                                              scan_temp_elems(SW + 1)});
     c.temp = reinterpret_cast<std::uint32_t*>(take(4 * tempElems));
     c.bytes = off;
     return c;
 }
 
-// ---------------------------------------------------------------- kernels
+// ---------------------------------------------------------------- sort
 
-// buildEdgeKeysKernel (:104-144), with the super-window split folded into the
-// key and range checks the reference does not make.
-__global__ void build_keys_kernel(const std::uint32_t* __restrict__ dst, const std::uint32_t* __restrict__ src,
-                                  std::uint32_t E, std::uint32_t rows, std::uint32_t cols, std::uint32_t S,
-                                  unsigned wiBits, unsigned dstBits, std::uint64_t* __restrict__ keys,
-                                  std::uint32_t* __restrict__ err) {
-    const std::uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= E) return;
-    std::uint32_t s = src[e], d = dst[e];
-    bool bad = false;
-    if (s >= cols) {
-        atomicMax(err, static_cast<std::uint32_t>(TCC_DEVERR_SRC_RANGE));
-        bad = true;
-    }
-    if (rows != 0 && d >= rows) {
-        atomicMax(err, static_cast<std::uint32_t>(TCC_DEVERR_DST_RANGE));
-        bad = true;
-    }
-    if (bad) {  // keep every later index in range; the result is flagged invalid
-        s = 0;
+__device__ __forceinline__ bool edge_in_range(std::uint32_t d, std::uint32_t s, const ElemParams& p) {
+    return s < p.cols && (p.rows == 0 || d < p.rows);
+}
+
+// Out-of-range edges become (0, 0), so every later index stays in range; the
+// input pass flags the conversion as invalid.
+__device__ __forceinline__ std::uint64_t make_elem(std::uint32_t d, std::uint32_t s, const ElemParams& p) {
+    if (!edge_in_range(d, s, p)) {
         d = 0;
+        s = 0;
     }
-    const std::uint32_t w = s >> 3;
-    const std::uint32_t sw = w / S;
-    const std::uint32_t wi = w - sw * S;
-    keys[e] = (((((static_cast<std::uint64_t>(sw) << dstBits) | d) << wiBits) | wi) << 3) | (s & 7u);
+    const std::uint32_t sw = s / p.span;
+    const std::uint32_t lo = s - sw * p.span;
+    return (static_cast<std::uint64_t>(sw) << p.kb) | (static_cast<std::uint64_t>(d) << p.loBits) | lo;
 }
 
-__global__ void group_flags_kernel(const std::uint64_t* __restrict__ keys, std::uint32_t E,
-                                   std::uint32_t* __restrict__ flags) {
-    const std::uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= E) return;
-    flags[e] = (e == 0 || (keys[e] >> 3) != (keys[e - 1] >> 3)) ? 1u : 0u;
+__device__ __forceinline__ unsigned digit_of(std::uint64_t e, Digit d) {
+    return static_cast<unsigned>(e >> d.shift) & ((1u << d.bits) - 1u);
 }
 
-// RLE of (window, dst) runs (the reference's DeviceRunLengthEncode, :1977-1990).
-__global__ void group_emit_kernel(const std::uint64_t* __restrict__ keys, std::uint32_t E,
-                                  const std::uint32_t* __restrict__ flags, const std::uint32_t* __restrict__ pos,
-                                  std::uint64_t* __restrict__ groupKey, std::uint32_t* __restrict__ groupStart) {
-    const std::uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= E) return;
-    if (flags[e]) {
-        groupKey[pos[e]] = keys[e] >> 3;
-        groupStart[pos[e]] = e;
+// Lanes (among `active`) whose nbits-wide key equals this lane's.
+__device__ __forceinline__ std::uint64_t match_peers_bits(unsigned key, bool active, unsigned nbits) {
+    std::uint64_t peers = __ballot(active);
+    for (unsigned b = 0; b < nbits; ++b) {
+        const bool bit = (key >> b) & 1u;
+        const std::uint64_t m = __ballot(bit);
+        peers &= bit ? m : ~m;
     }
-    if (e == E - 1) groupStart[pos[e] + flags[e]] = E;
+    return active ? peers : 0ull;
 }
 
-// countWindowDegreesKernel (:147-213) + buildTileBitmapsKernel's row bits
-// (:408-428) + the row-head flags of the distinct (super-window, dst) rows.
-// A workgroup takes kFinalizeItems consecutive groups; groups are sorted by
-// super-window, so they fall in at most a few super-windows, and the
-// (window, degree) counts of its first two go to an LDS histogram flushed
-// with one global atomic per nonzero bin (per-wave global atomics on the
-// same 128 counters of a super-window serialised: 3.2 ms at 114M edges).
-constexpr unsigned kFinalizeItems = 2048;
-constexpr unsigned kFinalizeBins = TCC_SWTCF_MAX_SUPER_WINDOW_SIZE * 8;  // (wi, degree) of one super-window
-
-__global__ void __launch_bounds__(kThreads) group_finalize_kernel(
-    const std::uint64_t* __restrict__ keys, const std::uint64_t* __restrict__ groupKey,
-    const std::uint32_t* __restrict__ groupStart, const std::uint32_t* __restrict__ numGroups, std::uint32_t E,
-    std::uint32_t S, unsigned wiBits, unsigned dstBits, std::uint32_t* __restrict__ groupInfo,
-    std::uint32_t* __restrict__ wdCount, std::uint32_t* __restrict__ rowFlags, std::uint32_t* __restrict__ err) {
-    __shared__ std::uint32_t hist[2 * kFinalizeBins];
-    for (unsigned i = threadIdx.x; i < 2 * kFinalizeBins; i += kThreads) hist[i] = 0;
-    const std::uint32_t G = *numGroups;
-    const std::uint32_t g0 = blockIdx.x * kFinalizeItems;
-    const unsigned swShift = wiBits + dstBits;
-    const std::uint32_t swFirst = g0 < G ? static_cast<std::uint32_t>(groupKey[g0] >> swShift) : 0u;
-    __syncthreads();
-    for (unsigned it = 0; it < kFinalizeItems / kThreads; ++it) {
-        const std::uint32_t g = g0 + it * kThreads + threadIdx.x;
-        if (g >= E) break;
-        if (g >= G) {
-            rowFlags[g] = 0;
-            continue;
-        }
-        const std::uint32_t start = groupStart[g];
-        const std::uint32_t count = groupStart[g + 1] - start;
-        if (count == 0 || count > 8) atomicMax(err, static_cast<std::uint32_t>(TCC_DEVERR_DEGREE));
-        const std::uint32_t deg = count == 0 ? 1u : (count > 8 ? 8u : count);
-        std::uint32_t bits = 0;
-        for (std::uint32_t i = 0; i < deg; ++i) bits |= 1u << static_cast<unsigned>(keys[start + i] & 7u);
-        const std::uint64_t gk = groupKey[g];
-        const std::uint32_t wi = static_cast<std::uint32_t>(gk & ((1ull << wiBits) - 1ull));
-        const std::uint32_t sw = static_cast<std::uint32_t>(gk >> swShift);
-        const std::uint32_t local = sw - swFirst;
-        if (local < 2) {
-            atomicAdd(&hist[local * kFinalizeBins + wi * 8 + deg - 1], 1u);
-        } else {
-            atomicAdd(&wdCount[(static_cast<std::uint64_t>(sw) * S + wi) * 8 + deg - 1], 1u);
-        }
-        groupInfo[g] = bits | (deg << 8);
-        rowFlags[g] = (g == 0 || (gk >> wiBits) != (groupKey[g - 1] >> wiBits)) ? 1u : 0u;
+// Reads the COO once: range checks, whether it is in (dst, src) order, and
+// the per-tile counts of the first low digit and of the first sw digit (the
+// latter is the first pass's histogram when the input is in order).
+__global__ void __launch_bounds__(kThreads) input_pass_kernel(const std::uint32_t* __restrict__ dst,
+                                                             const std::uint32_t* __restrict__ src, std::uint32_t n,
+                                                             ElemParams ep, Digit low, std::uint32_t* __restrict__ histLow,
+                                                             Digit top, std::uint32_t* __restrict__ histTop,
+                                                             unsigned tiles, std::uint32_t* __restrict__ tileOut,
+                                                             std::uint32_t* __restrict__ err) {
+    __shared__ std::uint32_t hl[kWaves][kMaxBins];
+    __shared__ std::uint32_t ht[kWaves][kMaxBins];
+    const unsigned lane = __lane_id();
+    const unsigned wave = threadIdx.x / kWave;
+    for (unsigned i = threadIdx.x; i < kWaves * kMaxBins; i += kThreads) {
+        (&hl[0][0])[i] = 0;
+        (&ht[0][0])[i] = 0;
     }
     __syncthreads();
-    for (unsigned b = threadIdx.x; b < 2 * kFinalizeBins; b += kThreads) {
-        const std::uint32_t n = hist[b];
-        if (n == 0) continue;  // only bins of groups that exist (wi < S)
-        const std::uint32_t sw = swFirst + b / kFinalizeBins;
-        atomicAdd(&wdCount[static_cast<std::uint64_t>(sw) * S * 8 + (b % kFinalizeBins)], n);
+    const std::uint64_t base = static_cast<std::uint64_t>(blockIdx.x) * kTile + wave * kSpan;
+    bool outOfOrder = false, srcBad = false, dstBad = false;
+#pragma unroll 4
+    for (unsigned r = 0; r < kRounds; ++r) {
+        const std::uint64_t i = base + r * kWave + lane;
+        const bool valid = i < n;
+        const std::uint32_t d = valid ? dst[i] : 0u;
+        const std::uint32_t s = valid ? src[i] : 0u;
+        std::uint32_t pd = __shfl_up(d, 1, kWave);
+        std::uint32_t ps = __shfl_up(s, 1, kWave);
+        if (lane == 0 && valid && i > 0) {
+            pd = dst[i - 1];
+            ps = src[i - 1];
+        }
+        if (valid) {
+            if (i > 0 && (d < pd || (d == pd && s < ps))) outOfOrder = true;
+            srcBad |= s >= ep.cols;
+            dstBad |= ep.rows != 0 && d >= ep.rows;
+            const std::uint64_t e = make_elem(d, s, ep);
+            atomicAdd(&hl[wave][digit_of(e, low)], 1u);
+            atomicAdd(&ht[wave][digit_of(e, top)], 1u);
+        }
+    }
+    __shared__ std::uint32_t waveOut[kWaves];
+    const std::uint64_t anyOut = __ballot(outOfOrder);
+    if (lane == 0) waveOut[wave] = anyOut != 0;
+    if (srcBad) atomicMax(err, static_cast<std::uint32_t>(TCC_DEVERR_SRC_RANGE));
+    if (dstBad) atomicMax(err, static_cast<std::uint32_t>(TCC_DEVERR_DST_RANGE));
+    __syncthreads();
+    // one word per tile (a flag on one address from every wave serialises)
+    if (threadIdx.x == 0) tileOut[blockIdx.x] = waveOut[0] | waveOut[1] | waveOut[2] | waveOut[3];
+    for (unsigned b = threadIdx.x; b < (1u << low.bits); b += kThreads) {
+        std::uint32_t t = 0;
+        for (unsigned w = 0; w < kWaves; ++w) t += hl[w][b];
+        histLow[static_cast<std::uint64_t>(b) * tiles + blockIdx.x] = t;
+    }
+    for (unsigned b = threadIdx.x; b < (1u << top.bits); b += kThreads) {
+        std::uint32_t t = 0;
+        for (unsigned w = 0; w < kWaves; ++w) t += ht[w][b];
+        histTop[static_cast<std::uint64_t>(b) * tiles + blockIdx.x] = t;
     }
 }
 
-// buildWindowMetadataKernel (:216-265): degree 8 first, then 7 ... 1.
-__global__ void window_meta_kernel(const std::uint32_t* __restrict__ wdCount, std::uint32_t* __restrict__ wdBase,
-                                   std::uint32_t* __restrict__ wActive, std::uint32_t* __restrict__ wTiles,
-                                   std::uint32_t CW) {
+// unsorted = OR of the input pass's per-tile flags (one workgroup).
+__global__ void __launch_bounds__(kThreads) any_kernel(const std::uint32_t* __restrict__ flags, unsigned n,
+                                                      std::uint32_t* __restrict__ out) {
+    __shared__ std::uint32_t waveAny[kWaves];
+    std::uint32_t v = 0;
+    for (unsigned i = threadIdx.x; i < n; i += kThreads) v |= flags[i];
+    const std::uint64_t b = __ballot(v != 0);
+    if (__lane_id() == 0) waveAny[threadIdx.x / kWave] = b != 0;
+    __syncthreads();
+    if (threadIdx.x == 0) *out = waveAny[0] | waveAny[1] | waveAny[2] | waveAny[3];
+}
+
+// Per-tile digit counts of an element array.  With onlyUnsorted, returns at
+// once when the input pass found the COO in (dst, src) order.
+__global__ void __launch_bounds__(kThreads) elem_hist_kernel(const std::uint64_t* __restrict__ in, std::uint32_t n,
+                                                            Digit dg, std::uint32_t* __restrict__ hist,
+                                                            unsigned tiles, const std::uint32_t* __restrict__ unsorted,
+                                                            int onlyUnsorted) {
+    __shared__ std::uint32_t h[kWaves][kMaxBins];
+    if (onlyUnsorted && *unsorted == 0u) return;
+    const unsigned lane = __lane_id();
+    const unsigned wave = threadIdx.x / kWave;
+    for (unsigned i = threadIdx.x; i < kWaves * kMaxBins; i += kThreads) (&h[0][0])[i] = 0;
+    __syncthreads();
+    const std::uint64_t base = static_cast<std::uint64_t>(blockIdx.x) * kTile + wave * kSpan;
+#pragma unroll 4
+    for (unsigned r = 0; r < kRounds; ++r) {
+        const std::uint64_t i = base + r * kWave + lane;
+        if (i < n) atomicAdd(&h[wave][digit_of(in[i], dg)], 1u);
+    }
+    __syncthreads();
+    for (unsigned b = threadIdx.x; b < (1u << dg.bits); b += kThreads) {
+        std::uint32_t t = 0;
+        for (unsigned w = 0; w < kWaves; ++w) t += h[w][b];
+        hist[static_cast<std::uint64_t>(b) * tiles + blockIdx.x] = t;
+    }
+}
+
+struct ScatterArgs {
+    const std::uint64_t* in;
+    std::uint64_t* out;
+    const std::uint32_t* dst;
+    const std::uint32_t* src;
+    ElemParams ep;
+    std::uint32_t n;
+    Digit dg;
+    const std::uint32_t* histScan;  // exclusive scan of the (digit, tile) counts
+    unsigned tiles;
+    const std::uint32_t* unsorted;
+    int onlyUnsorted;  // return at once for a COO in (dst, src) order
+    int source;        // 0: `in`; 1: the COO; 2: the COO if it is in order, else `in`
+};
+
+// Stable scatter of one digit: position = the (digit, tile) offset + the
+// same digit's count in earlier waves of the tile + earlier lanes and rounds
+// of this wave.  Written from the lanes (staging the tile in LDS by digit
+// measured no faster for 8-byte keys).
+__global__ void __launch_bounds__(kThreads) elem_scatter_kernel(ScatterArgs a) {
+    __shared__ std::uint32_t cnt[kWaves][kMaxBins];
+    if (a.onlyUnsorted && *a.unsorted == 0u) return;
+    const bool coo = a.source == 1 || (a.source == 2 && *a.unsorted == 0u);
+    const unsigned lane = __lane_id();
+    const unsigned wave = threadIdx.x / kWave;
+    const unsigned bins = 1u << a.dg.bits;
+    for (unsigned i = threadIdx.x; i < kWaves * kMaxBins; i += kThreads) (&cnt[0][0])[i] = 0;
+    __syncthreads();
+    const std::uint64_t base = static_cast<std::uint64_t>(blockIdx.x) * kTile + wave * kSpan;
+    const std::uint64_t lt = lanemask_lt();
+    std::uint64_t k[kRounds];
+    std::uint32_t rank[kRounds];
+#pragma unroll
+    for (unsigned r = 0; r < kRounds; ++r) {
+        const std::uint64_t i = base + r * kWave + lane;
+        const bool valid = i < a.n;
+        if (coo) k[r] = valid ? make_elem(a.dst[i], a.src[i], a.ep) : 0ull;
+        else k[r] = valid ? a.in[i] : 0ull;
+        const unsigned d = digit_of(k[r], a.dg);
+        const std::uint64_t peers = match_peers_bits(d, valid, a.dg.bits);
+        const std::uint32_t before = cnt[wave][d];
+        rank[r] = before + static_cast<std::uint32_t>(__popcll(peers & lt));
+        // one lane per digit group publishes the new count; every lane of the
+        // wave read cnt[] above before this write is issued
+        if (valid && (peers & lt) == 0) cnt[wave][d] = before + static_cast<std::uint32_t>(__popcll(peers));
+    }
+    __syncthreads();
+    for (unsigned d = threadIdx.x; d < bins; d += kThreads) {
+        std::uint32_t run = a.histScan[static_cast<std::uint64_t>(d) * a.tiles + blockIdx.x];
+        for (unsigned w = 0; w < kWaves; ++w) {
+            const std::uint32_t c = cnt[w][d];
+            cnt[w][d] = run;  // absolute base of (wave w, digit d)
+            run += c;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (unsigned r = 0; r < kRounds; ++r) {
+        const std::uint64_t i = base + r * kWave + lane;
+        if (i < a.n) a.out[cnt[wave][digit_of(k[r], a.dg)] + rank[r]] = k[r];
+    }
+}
+
+// ---------------------------------------------------------------- segments
+
+// segStart[s] = first element of super-window s (the sorted order's run
+// boundaries of sw); empty super-windows get the next one's start.
+__global__ void segment_bounds_kernel(const std::uint64_t* __restrict__ el, std::uint32_t n, unsigned kb,
+                                      std::uint32_t SW, std::uint32_t* __restrict__ segStart) {
+    const std::uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n) return;
+    const std::uint32_t sw = min(static_cast<std::uint32_t>(el[e] >> kb), SW - 1);
+    const std::int64_t prev = e == 0 ? -1 : static_cast<std::int64_t>(min(static_cast<std::uint32_t>(el[e - 1] >> kb), SW - 1));
+    for (std::int64_t t = prev + 1; t <= static_cast<std::int64_t>(sw); ++t) segStart[t] = e;
+    if (e == n - 1)
+        for (std::uint32_t t = sw + 1; t <= SW; ++t) segStart[t] = n;
+}
+
+__global__ void segment_tiles_kernel(const std::uint32_t* __restrict__ segStart, std::uint32_t SW,
+                                     std::uint32_t* __restrict__ tileCount) {
+    const std::uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s < SW) tileCount[s] = (segStart[s + 1] - segStart[s] + kTile - 1) / kTile;
+}
+
+struct TileArgs {
+    const std::uint64_t* el;
+    std::uint32_t n;    // elements
+    std::uint32_t cap;  // the matrix's edge capacity (bounds of the row and tile-row arrays)
+    std::uint64_t keyMask;  // the low kb bits: dst << loBits | lo
+    unsigned loBits;
+    std::uint32_t S, SW, CW;
+    const std::uint32_t* segStart;
+    const std::uint32_t* firstTile;  // [SW+1] exclusive scan of tiles per segment
+    std::uint32_t* counters;         // [bins][TM] (+1), scanned before the emit pass
+    std::uint32_t TM;
+    std::uint32_t* err;
+    // emit pass
+    const std::uint32_t* wdBase;
+    const std::uint32_t* colWindowOffset;
+    const std::uint32_t* occBase;
+    std::uint32_t* tileRowSlot;
+    std::uint8_t* tileBytes;
+    std::uint32_t* superWindowRows;
+    std::uint8_t* rowCacheSlot;
+    std::uint32_t* cachedRowSlot;
+};
+
+struct TileRange {
+    std::uint32_t s, start, n, avail;
+};
+
+constexpr unsigned kKeySlots = 1 + kTile + kLookahead;
+constexpr unsigned kFlagWords = (kTile + kLookahead + kWave - 1) / kWave;
+constexpr unsigned kLoadIters = (kKeySlots + kThreads - 1) / kThreads;
+
+// The keys of a segment tile and its head bitmaps.  K is u32 when the keys
+// have at most 31 bits (so that the ~0 sentinel never equals a key shifted
+// right), else u64.
+template <typename K>
+struct TileKeys {
+    K key[kKeySlots];                 // key[0]: element before the tile, or ~0; key[1 + i]: element i
+    std::uint64_t group[kFlagWords];  // bit i: element i starts a (window, dst) group
+    std::uint64_t row[kFlagWords];    // bit i: element i starts a row
+};
+
+// Segment tile t: its super-window (the last s with firstTile[s] <= t, never
+// an empty one), its elements, up to kLookahead elements past its end
+// (within the segment), and the head bits of all of them.
+template <typename K>
+__device__ TileRange load_tile(const TileArgs& a, unsigned t, TileKeys<K>& tk) {
+    std::uint32_t lo = 0, hi = a.SW;  // firstTile[lo] <= t < firstTile[hi]
+    while (hi - lo > 1) {
+        const std::uint32_t mid = (lo + hi) / 2;
+        if (a.firstTile[mid] <= t) lo = mid;
+        else hi = mid;
+    }
+    TileRange r;
+    r.s = lo;
+    const std::uint32_t segEnd = min(a.segStart[lo + 1], a.n);
+    const std::uint32_t segBegin = min(a.segStart[lo], segEnd);
+    r.start = min(segBegin + (t - a.firstTile[lo]) * kTile, segEnd);
+    r.n = min(kTile, segEnd - r.start);
+    r.avail = min(r.n + kLookahead, segEnd - r.start);
+    const bool hasPrev = r.start > segBegin;
+#pragma unroll
+    for (unsigned q = 0; q < kLoadIters; ++q) {
+        const unsigned j = q * kThreads + threadIdx.x;
+        if (j <= r.avail) {
+            K v = static_cast<K>(~0ull);
+            if (j > 0 || hasPrev) v = static_cast<K>(a.el[r.start - 1 + j] & a.keyMask);
+            tk.key[j] = v;
+        }
+    }
+    __syncthreads();
+    const unsigned lane = __lane_id();
+    for (unsigned base = (threadIdx.x / kWave) * kWave; base < r.avail; base += kThreads) {
+        const unsigned j = base + lane;
+        bool g = false, h = false;
+        if (j < r.avail) {
+            const K x = tk.key[j + 1], p = tk.key[j];
+            g = (x >> 3) != (p >> 3);
+            h = (x >> a.loBits) != (p >> a.loBits);
+        }
+        const std::uint64_t gb = __ballot(g), rb = __ballot(h);
+        if (lane == 0) {
+            tk.group[base / kWave] = gb;
+            tk.row[base / kWave] = rb;
+        }
+    }
+    __syncthreads();
+    return r;
+}
+
+__device__ __forceinline__ bool bit_at(const std::uint64_t* w, unsigned i) { return (w[i >> 6] >> (i & 63)) & 1ull; }
+
+// First set bit in [from, limit), or limit.
+__device__ __forceinline__ unsigned next_bit(const std::uint64_t* w, unsigned from, unsigned limit) {
+    if (from >= limit) return limit;
+    unsigned k = from >> 6;
+    std::uint64_t m = w[k] & (~0ull << (from & 63));
+    while (m == 0) {
+        ++k;
+        if (k * 64 >= limit) return limit;
+        m = w[k];
+    }
+    return min(k * 64 + static_cast<unsigned>(__builtin_ctzll(m)), limit);
+}
+
+// Set bits in [from, to).
+__device__ __forceinline__ unsigned count_bits(const std::uint64_t* w, unsigned from, unsigned to) {
+    unsigned c = 0;
+    for (unsigned k = from >> 6; k * 64 < to; ++k) {
+        std::uint64_t m = w[k];
+        if (k == (from >> 6)) m &= ~0ull << (from & 63);
+        if (to - k * 64 < 64) m &= (1ull << (to - k * 64)) - 1ull;
+        c += static_cast<unsigned>(__popcll(m));
+    }
+    return c;
+}
+
+struct Head {
+    bool gh, rh;     // first element of its (window, dst) group / of its row
+    unsigned count;  // group: elements, up to 9 (more than 8 is the degree error)
+    unsigned bits;   // group: OR of 1 << (lo & 7) over its first 8 elements
+    unsigned occ;    // row: groups in the row
+};
+
+// Element i of the tile; elements [0, avail) are loaded.  A group ends at
+// the next group head (a row head is one too), a row at the next row head.
+template <bool BITS, typename K>
+__device__ __forceinline__ Head head_at(const TileKeys<K>& tk, unsigned i, unsigned avail) {
+    Head h{};
+    h.gh = bit_at(tk.group, i);
+    h.rh = bit_at(tk.row, i);
+    if (h.gh) {
+        h.count = next_bit(tk.group, i + 1, min(avail, i + 9)) - i;
+        if constexpr (BITS) {
+            const unsigned deg = min(h.count, 8u);
+            unsigned bits = 0;
+#pragma unroll
+            for (unsigned q = 0; q < 8; ++q)
+                if (q < deg) bits |= 1u << static_cast<unsigned>(tk.key[i + 1 + q] & 7u);
+            h.bits = bits;
+        }
+    }
+    if (h.rh) h.occ = count_bits(tk.group, i, next_bit(tk.row, i + 1, avail));
+    return h;
+}
+
+// countWindowDegreesKernel (:147-213) and the occurrence counts of
+// buildRepeatCacheMetadataKernel (:699-895), per segment tile.
+template <typename K>
+__global__ void __launch_bounds__(kThreads) tile_count_kernel(TileArgs a) {
+    __shared__ TileKeys<K> tk;
+    __shared__ std::uint32_t hist[8 * kMaxS + 33];
+    const unsigned t = blockIdx.x;
+    const unsigned nb = num_bins(a.S);
+    if (t >= a.firstTile[a.SW]) {  // past the last tile: empty columns of the scan
+        for (unsigned b = threadIdx.x; b < nb; b += kThreads) a.counters[static_cast<std::uint64_t>(b) * a.TM + t] = 0;
+        return;
+    }
+    for (unsigned b = threadIdx.x; b < nb; b += kThreads) hist[b] = 0;
+    const TileRange r = load_tile(a, t, tk);
+    const std::uint32_t loMask = (1u << a.loBits) - 1u;
+    const unsigned rowBin = 8 * a.S, groupBin = 8 * a.S + 32;
+    std::uint32_t groups = 0, rows = 0;
+    bool degErr = false, occErr = false;
+    for (unsigned i = threadIdx.x; i < r.n; i += kThreads) {
+        const Head h = head_at<false>(tk, i, r.avail);
+        if (h.gh) {
+            degErr |= h.count > 8;
+            const unsigned deg = min(h.count, 8u);
+            const unsigned wi = (static_cast<std::uint32_t>(tk.key[i + 1]) & loMask) >> 3;
+            atomicAdd(&hist[wi * 8 + deg - 1], 1u);
+            ++groups;
+        }
+        if (h.rh) {
+            ++rows;
+            if (h.occ > kMaxS) occErr = true;
+            else if (h.occ >= 2) atomicAdd(&hist[rowBin + h.occ - 1], 1u);
+        }
+    }
+    if (degErr) atomicMax(a.err, static_cast<std::uint32_t>(TCC_DEVERR_DEGREE));
+    if (occErr) atomicMax(a.err, static_cast<std::uint32_t>(TCC_DEVERR_OCCURRENCE));
+    if (groups) atomicAdd(&hist[groupBin], groups);
+    if (rows) atomicAdd(&hist[rowBin], rows);
+    __syncthreads();
+    for (unsigned b = threadIdx.x; b < nb; b += kThreads) a.counters[static_cast<std::uint64_t>(b) * a.TM + t] = hist[b];
+}
+
+// buildWindowMetadataKernel (:216-265): per window, the degree-bucket bases
+// (degree 8 first) from its super-window's totals.
+__global__ void window_meta_kernel(const std::uint32_t* __restrict__ P, std::uint32_t TM,
+                                   const std::uint32_t* __restrict__ firstTile, std::uint32_t S, std::uint32_t CW,
+                                   std::uint32_t* __restrict__ wdBase, std::uint32_t* __restrict__ wActive,
+                                   std::uint32_t* __restrict__ wTiles) {
     const std::uint32_t w = blockIdx.x * blockDim.x + threadIdx.x;
     if (w >= CW) return;
+    const std::uint32_t s = w / S, wi = w - s * S;
+    const std::uint32_t t0 = firstTile[s], t1 = firstTile[s + 1];
     std::uint32_t running = 0;
     for (int d = 7; d >= 0; --d) {
-        const std::uint64_t i = static_cast<std::uint64_t>(w) * 8 + d;
-        wdBase[i] = running;
-        running += wdCount[i];
+        const std::uint64_t b = static_cast<std::uint64_t>(wi * 8 + d) * TM;
+        wdBase[static_cast<std::uint64_t>(w) * 8 + d] = running;
+        running += P[b + t1] - P[b + t0];
     }
     wActive[w] = running;
     wTiles[w] = (running + 7) / 8;
 }
 
-// Distinct (super-window, dst) rows: superWindowRows in slot order and the
-// per-super-window row counts (the reference's hash insert + slot assignment,
-// :459-681, as a sorted run encoding).
-__global__ void row_emit_kernel(const std::uint64_t* __restrict__ groupKey,
-                                const std::uint32_t* __restrict__ rowFlags, const std::uint32_t* __restrict__ rowPos,
-                                const std::uint32_t* __restrict__ numGroups, std::uint32_t E, unsigned wiBits,
-                                unsigned dstBits, std::uint32_t numSuperWindows,
-                                std::uint32_t* __restrict__ rowStartGroup,
-                                std::uint32_t* __restrict__ superWindowRows,
-                                std::uint32_t* __restrict__ superWindowRowOffset) {
-    const std::uint32_t g = blockIdx.x * blockDim.x + threadIdx.x;
-    if (g >= E) return;
-    const std::uint32_t G = *numGroups;
-    if (g >= G) return;
-    const unsigned swShift = wiBits + dstBits;
-    if (rowFlags[g]) {
-        const std::uint32_t u = rowPos[g];
-        const std::uint64_t gk = groupKey[g];
-        const std::uint32_t dstMask = dstBits >= 32 ? 0xFFFFFFFFu : ((1u << dstBits) - 1u);
-        const std::uint32_t d = static_cast<std::uint32_t>(gk >> wiBits) & dstMask;
-        const std::uint32_t sw = static_cast<std::uint32_t>(gk >> swShift);
-        rowStartGroup[u] = g;
-        superWindowRows[u] = d;
-        // Rows are sorted by super-window: the first row of super-window sw
-        // sets its offset, and those of the empty super-windows before it.
-        const std::int64_t prev = g == 0 ? -1 : static_cast<std::int64_t>(groupKey[g - 1] >> swShift);
-        for (std::int64_t t = prev + 1; t <= static_cast<std::int64_t>(sw) && t < numSuperWindows; ++t)
-            superWindowRowOffset[t] = u;
+// Per super-window: superWindowRowOffset, the repeat-cache bases
+// (occurrence 32 first) and the cached count; thread SW writes the totals.
+__global__ void super_window_meta_kernel(const std::uint32_t* __restrict__ P, std::uint32_t TM,
+                                         const std::uint32_t* __restrict__ firstTile, std::uint32_t S,
+                                         std::uint32_t SW, std::uint32_t* __restrict__ occBase,
+                                         std::uint32_t* __restrict__ superWindowRowOffset,
+                                         std::uint8_t* __restrict__ cachedCount,
+                                         std::uint32_t* __restrict__ numGroups) {
+    const std::uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s > SW) return;
+    const std::uint64_t rowBin = static_cast<std::uint64_t>(8 * S) * TM;
+    superWindowRowOffset[s] = P[rowBin + firstTile[s]] - P[rowBin];
+    if (s == SW) {
+        const std::uint64_t groupBin = static_cast<std::uint64_t>(8 * S + 32) * TM;
+        *numGroups = P[groupBin + TM] - P[groupBin];
+        return;
     }
-    if (g == G - 1) {
-        const std::uint32_t U = rowPos[g] + rowFlags[g];
-        rowStartGroup[U] = G;
-        const std::uint32_t sw = static_cast<std::uint32_t>(groupKey[g] >> swShift);
-        for (std::uint32_t t = sw + 1; t <= numSuperWindows; ++t) superWindowRowOffset[t] = U;
+    const std::uint32_t t0 = firstTile[s], t1 = firstTile[s + 1];
+    std::uint32_t running = 0;
+    for (unsigned occ = kMaxS; occ >= 2; --occ) {
+        const std::uint64_t b = static_cast<std::uint64_t>(8 * S + occ - 1) * TM;
+        occBase[static_cast<std::uint64_t>(s) * kOccStride + occ] = running;
+        running += P[b + t1] - P[b + t0];
     }
+    cachedCount[s] = static_cast<std::uint8_t>(running < kCache ? running : kCache);
 }
 
-// Stable rank of `bin` among the active items of a 256-item chunk (item order
-// = thread order), continuing the running per-bin counts in `run`.  Must be
-// called by all threads of the block.  `wcnt` is zero on entry and on exit.
-template <int NBITS, unsigned THREADS>
-__device__ std::uint32_t block_multisplit_rank(unsigned bin, bool active, std::uint32_t* run,
-                                               std::uint32_t (*wcnt)[256]) {
+// assignGroupLocationsKernel (:292-376), fillValidTileRowSlotsKernel
+// (:1003-1048), the tile bitmaps (:430-455, one byte per tile row), the
+// super-window rows (:459-681) and the repeat cache (:699-895), per segment
+// tile.  Wave w ranks elements [1024 w, 1024 w + 1024) of the tile in 16
+// rounds of 64, so ranks follow element order.
+template <typename K>
+__global__ void __launch_bounds__(kThreads) tile_emit_kernel(TileArgs a) {
+    __shared__ TileKeys<K> tk;
+    __shared__ std::uint32_t cntG[kWaves][8 * kMaxS];
+    __shared__ std::uint32_t cntO[kWaves][kOccBins + 1];
+    __shared__ std::uint32_t info[kTile];          // head facts of element i
+    __shared__ std::uint64_t baseG[8 * kMaxS];   // tile-row index of the bin's first head in this tile
+    __shared__ std::uint32_t baseO[kOccBins + 1];  // cache slot of the bin's first repeated row in this tile
+    __shared__ std::uint32_t rowsW[kWaves];
+    const unsigned t = blockIdx.x;
+    if (t >= a.firstTile[a.SW]) return;
+    const TileRange r = load_tile(a, t, tk);
+    const std::uint32_t s = r.s;
+    const std::uint32_t t0 = a.firstTile[s];
+    const unsigned groupBins = 8 * a.S;
+    for (unsigned b = threadIdx.x; b < groupBins; b += kThreads) {
+        // bin b = (wi, degree - 1): the window's degree-bucket base, plus the
+        // bucket's heads in the segment's earlier tiles
+        const std::uint64_t o = static_cast<std::uint64_t>(b) * a.TM;
+        const std::uint32_t w = s * a.S + b / 8;
+        const std::uint32_t rel = a.counters[o + t] - a.counters[o + t0];
+        baseG[b] = w < a.CW ? static_cast<std::uint64_t>(a.colWindowOffset[w]) * 8 +
+                                  a.wdBase[static_cast<std::uint64_t>(w) * 8 + b % 8] + rel
+                            : 0;
+        for (unsigned v = 0; v < kWaves; ++v) cntG[v][b] = 0;
+    }
+    for (unsigned b = threadIdx.x; b < kOccBins; b += kThreads) {
+        const std::uint64_t o = static_cast<std::uint64_t>(groupBins + 1 + b) * a.TM;
+        baseO[b] = a.occBase[static_cast<std::uint64_t>(s) * kOccStride + b + 2] + a.counters[o + t] -
+                   a.counters[o + t0];
+        for (unsigned v = 0; v < kWaves; ++v) cntO[v][b] = 0;
+    }
+    const std::uint64_t rowBin = static_cast<std::uint64_t>(groupBins) * a.TM;
+    const std::uint32_t rowBase = a.counters[rowBin + t] - a.counters[rowBin];
+    const std::uint32_t off0 = a.counters[rowBin + t0] - a.counters[rowBin];
+    __syncthreads();
+
+    const unsigned lane = __lane_id();
     const unsigned wave = threadIdx.x / kWave;
     const std::uint64_t lt = lanemask_lt();
-    const std::uint64_t peers = match_peers<NBITS>(bin, active);
-    const std::uint32_t rin = static_cast<std::uint32_t>(__popcll(peers & lt));
-    if (active && (peers & lt) == 0) wcnt[wave][bin] = static_cast<std::uint32_t>(__popcll(peers));
-    __syncthreads();
-    std::uint32_t rank = 0;
-    if (active) {
-        std::uint32_t cross = 0;
-        for (unsigned w = 0; w < wave; ++w) cross += wcnt[w][bin];
-        rank = run[bin] + cross + rin;
+    const std::uint32_t loMask = (1u << a.loBits) - 1u;
+    // info[i] = gh | rh << 1 | rep << 2 | degree << 3 | bits << 7 | wi << 15 |
+    // (occ - 2) << 20, for the tile's elements
+    for (unsigned i = threadIdx.x; i < r.n; i += kThreads) {
+        const Head h = head_at<true>(tk, i, r.avail);
+        const unsigned deg = h.gh ? min(h.count, 8u) : 1u;
+        const bool rep = h.rh && h.occ >= 2 && h.occ <= kMaxS;
+        const unsigned wi = (static_cast<std::uint32_t>(tk.key[i + 1]) & loMask) >> 3;
+        info[i] = (h.gh ? 1u : 0u) | (h.rh ? 2u : 0u) | (rep ? 4u : 0u) | (deg << 3) |
+                     ((h.gh ? h.bits : 0u) << 7) | (min(wi, 31u) << 15) | ((rep ? h.occ - 2 : 0u) << 20);
     }
     __syncthreads();
-    for (unsigned b = threadIdx.x; b < (1u << NBITS); b += blockDim.x) {
-        std::uint32_t t = 0;
-        for (int w = 0; w < static_cast<int>(THREADS / kWave); ++w) {
-            t += wcnt[w][b];
-            wcnt[w][b] = 0;
+    // ranks per round: group rank | occurrence rank << 10 | rows of the wave
+    // up to and including the element << 20 (ranks within the wave)
+    std::uint32_t ranks[kRounds];
+    std::uint32_t rowRun = 0;
+#pragma unroll
+    for (unsigned r0 = 0; r0 < kRounds; ++r0) {
+        const unsigned i = wave * kSpan + r0 * kWave + lane;
+        const std::uint32_t f = i < r.n ? info[i] : 0u;
+        const bool gh = f & 1u, rh = f & 2u, rep = f & 4u;
+        const unsigned gbin = gh ? ((f >> 15) & 31u) * 8 + ((f >> 3) & 15u) - 1 : 0u;
+        const std::uint64_t pg = match_peers<8>(gbin, gh);
+        const std::uint32_t bg = cntG[wave][gbin];
+        const std::uint32_t rg = bg + static_cast<std::uint32_t>(__popcll(pg & lt));
+        if (gh && (pg & lt) == 0) cntG[wave][gbin] = bg + static_cast<std::uint32_t>(__popcll(pg));
+        const unsigned obin = (f >> 20) & 31u;
+        const std::uint64_t po = match_peers<5>(obin, rep);
+        const std::uint32_t bo = cntO[wave][obin];
+        const std::uint32_t ro = bo + static_cast<std::uint32_t>(__popcll(po & lt));
+        if (rep && (po & lt) == 0) cntO[wave][obin] = bo + static_cast<std::uint32_t>(__popcll(po));
+        const std::uint64_t rb = __ballot(rh);
+        const std::uint32_t rowsAt = rowRun + static_cast<std::uint32_t>(__popcll(rb & lt)) + (rh ? 1u : 0u);
+        rowRun += static_cast<std::uint32_t>(__popcll(rb));
+        ranks[r0] = rg | (ro << 10) | (rowsAt << 20);
+    }
+    if (lane == 0) rowsW[wave] = rowRun;
+    __syncthreads();
+    for (unsigned b = threadIdx.x; b < groupBins; b += kThreads) {
+        std::uint32_t run = 0;
+        for (unsigned w = 0; w < kWaves; ++w) {
+            const std::uint32_t c = cntG[w][b];
+            cntG[w][b] = run;
+            run += c;
         }
-        run[b] += t;
     }
-    __syncthreads();
-    return rank;
-}
-
-// One workgroup per super-window:
-//  (a) assignGroupLocationsKernel (:292-376) with the canonical rank,
-//      fillValidTileRowSlotsKernel (:1003-1048) and the tile bitmaps
-//      (:430-455, written as one byte per tile row instead of atomicOr);
-//  (b) buildRepeatCacheMetadataKernel (:699-895) with the canonical order.
-template <unsigned THREADS>
-__global__ void __launch_bounds__(THREADS) super_window_kernel(
-    const std::uint64_t* __restrict__ groupKey, const std::uint32_t* __restrict__ groupInfo,
-    const std::uint32_t* __restrict__ rowFlags, const std::uint32_t* __restrict__ rowPos,
-    const std::uint32_t* __restrict__ rowStartGroup, const std::uint32_t* __restrict__ wdBase,
-    const std::uint32_t* __restrict__ colWindowOffset, const std::uint32_t* __restrict__ superWindowRowOffset,
-    std::uint32_t S, unsigned wiBits, std::uint32_t numColWindows, std::uint32_t* __restrict__ tileRowSlot,
-    std::uint8_t* __restrict__ tileBytes, std::uint8_t* __restrict__ rowCacheSlot,
-    std::uint32_t* __restrict__ cachedRowSlot, std::uint8_t* __restrict__ cachedCount,
-    std::uint32_t* __restrict__ err) {
-    __shared__ std::uint32_t run[256];
-    __shared__ std::uint32_t wcnt[THREADS / kWave][256];
-    __shared__ std::uint32_t occHist[TCC_SWTCF_MAX_SUPER_WINDOW_SIZE + 1];
-    __shared__ std::uint32_t occBase[TCC_SWTCF_MAX_SUPER_WINDOW_SIZE + 1];
-    __shared__ std::uint32_t repeatedTotal;
-
-    const std::uint32_t s = blockIdx.x;
-    const std::uint32_t off0 = superWindowRowOffset[s];
-    const std::uint32_t off1 = superWindowRowOffset[s + 1];
-    const std::uint32_t g0 = rowStartGroup[off0];
-    const std::uint32_t g1 = rowStartGroup[off1];
-    const std::uint64_t wiMask = (1ull << wiBits) - 1ull;
-
-    for (unsigned i = threadIdx.x; i < 256; i += THREADS) {
-        run[i] = 0;
-        for (int w = 0; w < static_cast<int>(THREADS / kWave); ++w) wcnt[w][i] = 0;
-    }
-    if (threadIdx.x <= TCC_SWTCF_MAX_SUPER_WINDOW_SIZE) occHist[threadIdx.x] = 0;
-    __syncthreads();
-
-    // (a) rows of every window of this super-window
-    for (std::uint32_t base = g0; base < g1; base += THREADS) {
-        const std::uint32_t g = base + threadIdx.x;
-        const bool active = g < g1;
-        std::uint32_t info = 0, wi = 0, deg = 1;
-        if (active) {
-            info = groupInfo[g];
-            wi = static_cast<std::uint32_t>(groupKey[g] & wiMask);
-            deg = info >> 8;
+    for (unsigned b = threadIdx.x; b < kOccBins; b += kThreads) {
+        std::uint32_t run = 0;
+        for (unsigned w = 0; w < kWaves; ++w) {
+            const std::uint32_t c = cntO[w][b];
+            cntO[w][b] = run;
+            run += c;
         }
-        const unsigned bin = wi * 8 + (deg - 1);
-        const std::uint32_t rank = block_multisplit_rank<8, THREADS>(bin, active, run, wcnt);
-        if (active) {
-            const std::uint32_t w = s * S + wi;
-            if (w < numColWindows) {
-                const std::uint32_t reordered = wdBase[static_cast<std::uint64_t>(w) * 8 + deg - 1] + rank;
-                const std::uint64_t loc = static_cast<std::uint64_t>(colWindowOffset[w] + reordered / 8) * 8 +
-                                          (reordered & 7u);
-                const std::uint32_t u = rowPos[g] + rowFlags[g] - 1;
-                tileRowSlot[loc] = u - off0;
-                tileBytes[loc] = static_cast<std::uint8_t>(info & 0xFFu);
+    }
+    __syncthreads();
+    std::uint32_t rowOff = rowBase;
+    for (unsigned w = 0; w < wave; ++w) rowOff += rowsW[w];
+#pragma unroll
+    for (unsigned r0 = 0; r0 < kRounds; ++r0) {
+        const unsigned i = wave * kSpan + r0 * kWave + lane;
+        if (i >= r.n) continue;
+        const std::uint32_t f = info[i];
+        if ((f & 3u) == 0) continue;
+        const std::uint32_t u = rowOff + (ranks[r0] >> 20) - 1;  // this element's row
+        const std::uint32_t slot = u - off0;
+        const unsigned wi = (f >> 15) & 31u;
+        if ((f & 1u) && wi < a.S) {
+            // tiles of a window are consecutive: tile-row index = 8 x the
+            // window's first tile + the rank among its groups
+            const unsigned gbin = wi * 8 + ((f >> 3) & 15u) - 1;
+            const std::uint64_t loc = baseG[gbin] + cntG[wave][gbin] + (ranks[r0] & 0x3FFu);
+            if (loc < 8ull * a.cap) {
+                a.tileRowSlot[loc] = slot;
+                a.tileBytes[loc] = static_cast<std::uint8_t>((f >> 7) & 0xFFu);
             }
         }
-    }
-
-    // (b) repeat cache: occurrence histogram, descending bases, stable ranks
-    for (std::uint32_t u = off0 + threadIdx.x; u < off1; u += THREADS) {
-        const std::uint32_t occ = rowStartGroup[u + 1] - rowStartGroup[u];
-        if (occ > TCC_SWTCF_MAX_SUPER_WINDOW_SIZE) {
-            atomicMax(err, static_cast<std::uint32_t>(TCC_DEVERR_OCCURRENCE));
-        } else if (occ > 1) {
-            atomicAdd(&occHist[occ], 1u);
-        }
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        std::uint32_t running = 0;
-        for (int o = TCC_SWTCF_MAX_SUPER_WINDOW_SIZE; o >= 2; --o) {
-            occBase[o] = running;
-            running += occHist[o];
-        }
-        repeatedTotal = running;
-        cachedCount[s] = static_cast<std::uint8_t>(running < TCC_SWTCF_REPEAT_CACHE_SIZE
-                                                       ? running
-                                                       : TCC_SWTCF_REPEAT_CACHE_SIZE);
-    }
-    for (unsigned i = threadIdx.x; i < 256; i += THREADS) run[i] = 0;
-    __syncthreads();
-    if (repeatedTotal == 0) return;  // uniform across the block
-    for (std::uint32_t base = off0; base < off1; base += THREADS) {
-        const std::uint32_t u = base + threadIdx.x;
-        std::uint32_t occ = 0;
-        if (u < off1) occ = rowStartGroup[u + 1] - rowStartGroup[u];
-        const bool rep = u < off1 && occ > 1 && occ <= TCC_SWTCF_MAX_SUPER_WINDOW_SIZE;
-        const std::uint32_t rank = block_multisplit_rank<6, THREADS>(rep ? occ : 0u, rep, run, wcnt);
-        if (rep) {
-            const std::uint32_t cs = occBase[occ] + rank;
-            if (cs < TCC_SWTCF_REPEAT_CACHE_SIZE) {
-                rowCacheSlot[u] = static_cast<std::uint8_t>(cs);
-                cachedRowSlot[static_cast<std::uint64_t>(s) * TCC_SWTCF_REPEAT_CACHE_SIZE + cs] = u - off0;
+        if ((f & 2u) && u < a.cap) {
+            a.superWindowRows[u] = static_cast<std::uint32_t>(tk.key[i + 1] >> a.loBits);
+            std::uint8_t cs8 = static_cast<std::uint8_t>(TCC_SWTCF_INVALID_CACHE_SLOT);
+            if (f & 4u) {
+                const unsigned obin = (f >> 20) & 31u;
+                const std::uint32_t cs = baseO[obin] + cntO[wave][obin] + ((ranks[r0] >> 10) & 0x3FFu);
+                if (cs < kCache) {
+                    cs8 = static_cast<std::uint8_t>(cs);
+                    a.cachedRowSlot[static_cast<std::uint64_t>(s) * kCache + cs] = slot;
+                }
             }
+            a.rowCacheSlot[u] = cs8;
         }
     }
 }
 
-// fillPaddingTileRowSlotsKernel (:1051-1107).
+// fillPaddingTileRowSlotsKernel (:1051-1107), and zero bitmap bytes for the
+// padding rows of each window's last tile.
 __global__ void padding_kernel(const std::uint32_t* __restrict__ wActive,
                                const std::uint32_t* __restrict__ colWindowOffset, std::uint32_t CW,
-                               std::uint32_t* __restrict__ tileRowSlot) {
+                               std::uint32_t* __restrict__ tileRowSlot, std::uint8_t* __restrict__ tileBytes) {
     const std::uint32_t w = blockIdx.x * blockDim.x + threadIdx.x;
     if (w >= CW) return;
     const std::uint32_t active = wActive[w];
     const std::uint32_t rem = active & 7u;
     if (active == 0 || rem == 0) return;
     const std::uint64_t last = colWindowOffset[w + 1] - 1;
-    for (std::uint32_t lr = rem; lr < 8; ++lr) tileRowSlot[last * 8 + lr] = TCC_SWTCF_INVALID_ROW_SLOT;
+    for (std::uint32_t lr = rem; lr < 8; ++lr) {
+        tileRowSlot[last * 8 + lr] = TCC_SWTCF_INVALID_ROW_SLOT;
+        tileBytes[last * 8 + lr] = 0;
+    }
 }
 
 }  // namespace
@@ -470,7 +832,7 @@ int tcc_swtcf_alloc_workspace(tcc_swtcf_workspace* ws, std::uint32_t edgeCapacit
     ws->numColWindows = (numSrc + 7) / 8;
     ws->numSuperWindows = (ws->numColWindows + superWindowSize - 1) / superWindowSize;
     ws->superWindowSize = superWindowSize;
-    const Carve c = carve(nullptr, edgeCapacity, ws->numColWindows, ws->numSuperWindows);
+    const Carve c = carve(nullptr, edgeCapacity, ws->numColWindows, ws->numSuperWindows, superWindowSize);
     const std::size_t bytes = c.bytes + 256;  // + deviceNumGroups / deviceError
     char* base = nullptr;
     if (hipMalloc(&base, bytes) != hipSuccess) {
@@ -506,71 +868,111 @@ int tcc_swtcf_convert(const std::uint32_t* dDst, const std::uint32_t* dSrc, std:
                 TCC_ERR_INVALID_ARGUMENT, "workspace was sized for a different matrix");
     const hipStream_t st = as_stream(streamArg);
     const std::uint32_t E = numEdges, CW = m->numColWindows, SW = m->numSuperWindows, S = m->superWindowSize;
-    const KeyLayout kl = key_layout(m->rows, S, SW);
-    TCC_REQUIRE(kl.total <= 64, TCC_ERR_UNSUPPORTED, "packed sort key exceeds 64 bits");
+    const Plan plan = make_plan(m->rows, m->cols, S, SW);
+    TCC_REQUIRE(plan.ep.kb + plan.swBits <= 64, TCC_ERR_UNSUPPORTED, "packed sort key exceeds 64 bits");
     const Carve c = carve(static_cast<char*>(ws->scratch), ws->edgeCapacity, ws->numColWindows,
-                          ws->numSuperWindows);
+                          ws->numSuperWindows, S);
     std::uint32_t* err = ws->deviceError;
-    std::uint32_t* numGroups = ws->deviceNumGroups;
+    std::uint32_t* unsorted = c.flags;
+    const unsigned tiles = static_cast<unsigned>(sort_tiles(E));
 
-    // Reset per-conversion state (:1789-1919), with fill kernels.
-    TCC_HIP_CHECK(fill<std::uint64_t>(m->tileLocalBit, m->nnz, 0ull, st));
-    TCC_HIP_CHECK(fill<std::uint8_t>(m->superWindowRowCacheSlot, m->nnz, 0xFFu, st));
-    TCC_HIP_CHECK(fill<std::uint32_t>(m->superWindowCachedRowSlot, static_cast<std::uint64_t>(SW) * 32,
-                                      0xFFFFFFFFu, st));
-    TCC_HIP_CHECK(fill<std::uint8_t>(m->superWindowCachedCount, SW, 0u, st));
-    TCC_HIP_CHECK(fill<std::uint32_t>(c.wdCount, static_cast<std::uint64_t>(CW) * 8, 0u, st));
-    TCC_HIP_CHECK(fill<std::uint32_t>(m->superWindowRowOffset, static_cast<std::uint64_t>(SW) + 1, 0u, st));
+    // Per-conversion state (:1789-1919), with fill kernels.  Every row of
+    // every tile up to colWindowOffset[CW], and every super-window row, is
+    // written below; the rest of the arrays is left as it was.
+    TCC_HIP_CHECK(fill<std::uint32_t>(m->superWindowCachedRowSlot, static_cast<std::uint64_t>(SW) * kCache,
+                                      TCC_SWTCF_INVALID_ROW_SLOT, st));
     TCC_HIP_CHECK(fill<std::uint32_t>(err, 1, 0u, st));
 
-    // 1-2. keys, sort
-    hipLaunchKernelGGL(build_keys_kernel, dim3(grid_for(E, kThreads)), dim3(kThreads), 0, st, dDst, dSrc, E,
-                       m->rows, m->cols, S, kl.wiBits, kl.dstBits, c.keysA, err);
+    // 1. sort: the COO's checks and first histograms, the low digits (skipped
+    // for a COO in (dst, src) order), then the sw digits.
+    hipLaunchKernelGGL(input_pass_kernel, dim3(tiles), dim3(kThreads), 0, st, dDst, dSrc, E, plan.ep, plan.low[0],
+                       c.histLow, plan.top[0], c.histTop, tiles, c.tileFlags, err);
     TCC_LAUNCH_CHECK();
-    std::uint64_t* sorted = nullptr;
-    TCC_HIP_CHECK(radix_sort(c.keysA, c.keysB, E, kl.total, c.temp, &sorted, st));
-    std::uint64_t* groupKey = (sorted == c.keysA) ? c.keysB : c.keysA;
+    hipLaunchKernelGGL(any_kernel, dim3(1), dim3(kThreads), 0, st, c.tileFlags, tiles, unsorted);
+    TCC_LAUNCH_CHECK();
+    std::uint64_t* bufs[2] = {c.elemA, c.elemB};
+    int next = 0;
+    const std::uint64_t* cur = nullptr;
+    auto scatter = [&](const Digit& dg, std::uint32_t* hist, int onlyUnsorted, int source) -> int {
+        TCC_HIP_CHECK(exclusive_scan(hist, hist, (1ull << dg.bits) * tiles, nullptr, c.temp, st));
+        ScatterArgs a{cur, bufs[next], dDst, dSrc, plan.ep, E, dg, hist, tiles, unsorted, onlyUnsorted, source};
+        hipLaunchKernelGGL(elem_scatter_kernel, dim3(tiles), dim3(kThreads), 0, st, a);
+        TCC_LAUNCH_CHECK();
+        cur = bufs[next];
+        next ^= 1;
+        return TCC_OK;
+    };
+    for (std::size_t p = 0; p < plan.low.size(); ++p) {
+        if (p > 0) {
+            hipLaunchKernelGGL(elem_hist_kernel, dim3(tiles), dim3(kThreads), 0, st, cur, E, plan.low[p], c.histLow,
+                               tiles, unsorted, 1);
+            TCC_LAUNCH_CHECK();
+        }
+        if (int rc = scatter(plan.low[p], c.histLow, 1, p == 0 ? 1 : 0)) return rc;
+    }
+    for (std::size_t p = 0; p < plan.top.size(); ++p) {
+        // pass 0's counts came from the input pass for a COO in order
+        hipLaunchKernelGGL(elem_hist_kernel, dim3(tiles), dim3(kThreads), 0, st, cur, E, plan.top[p], c.histTop,
+                           tiles, unsorted, p == 0 ? 1 : 0);
+        TCC_LAUNCH_CHECK();
+        if (int rc = scatter(plan.top[p], c.histTop, 0, p == 0 ? 2 : 0)) return rc;
+    }
+    const std::uint64_t* sorted = cur;
 
-    // 3. groups
-    hipLaunchKernelGGL(group_flags_kernel, dim3(grid_for(E, kThreads)), dim3(kThreads), 0, st, sorted, E,
-                       c.flags);
+    // 2. segments (super-windows) and their tiles
+    hipLaunchKernelGGL(segment_bounds_kernel, dim3(grid_for(E, kThreads)), dim3(kThreads), 0, st, sorted, E,
+                       plan.ep.kb, SW, c.segStart);
     TCC_LAUNCH_CHECK();
-    TCC_HIP_CHECK(exclusive_scan(c.flags, c.pos, E, numGroups, c.temp, st));
-    hipLaunchKernelGGL(group_emit_kernel, dim3(grid_for(E, kThreads)), dim3(kThreads), 0, st, sorted, E,
-                       c.flags, c.pos, groupKey, c.groupStart);
+    hipLaunchKernelGGL(segment_tiles_kernel, dim3(grid_for(SW, kThreads)), dim3(kThreads), 0, st, c.segStart, SW,
+                       c.firstTile);
     TCC_LAUNCH_CHECK();
-    hipLaunchKernelGGL(group_finalize_kernel, dim3(grid_for(E, kFinalizeItems)), dim3(kThreads), 0, st, sorted,
-                       groupKey, c.groupStart, numGroups, E, S, kl.wiBits, kl.dstBits, c.groupInfo, c.wdCount,
-                       c.flags, err);
-    TCC_LAUNCH_CHECK();
+    TCC_HIP_CHECK(exclusive_scan(c.firstTile, c.firstTile, SW, c.firstTile + SW, c.temp, st));
+    const std::uint32_t TM = static_cast<std::uint32_t>(segment_tiles_max(E, SW));
+    const std::uint64_t nCounters = static_cast<std::uint64_t>(num_bins(S)) * TM;
+    TileArgs ta{};
+    ta.el = sorted;
+    ta.n = E;
+    ta.cap = m->nnz;
+    ta.keyMask = (1ull << plan.ep.kb) - 1ull;
+    ta.loBits = plan.ep.loBits;
+    ta.S = S;
+    ta.SW = SW;
+    ta.CW = CW;
+    ta.segStart = c.segStart;
+    ta.firstTile = c.firstTile;
+    ta.counters = c.counters;
+    ta.TM = TM;
+    ta.err = err;
+    ta.wdBase = c.wdBase;
+    ta.colWindowOffset = m->colWindowOffset;
+    ta.occBase = c.occBase;
+    ta.tileRowSlot = m->tileRowSlot;
+    ta.tileBytes = reinterpret_cast<std::uint8_t*>(m->tileLocalBit);
+    ta.superWindowRows = m->superWindowRows;
+    ta.rowCacheSlot = m->superWindowRowCacheSlot;
+    ta.cachedRowSlot = m->superWindowCachedRowSlot;
 
-    // 4-5. window metadata, colWindowOffset
-    hipLaunchKernelGGL(window_meta_kernel, dim3(grid_for(CW, kThreads)), dim3(kThreads), 0, st, c.wdCount,
-                       c.wdBase, c.wActive, c.wTiles, CW);
+    // 3. counts, their scan, window and super-window bases
+    const bool narrow = plan.ep.kb <= 31;  // keys fit u32 with room for the ~0 sentinel
+    if (narrow) hipLaunchKernelGGL(tile_count_kernel<std::uint32_t>, dim3(TM), dim3(kThreads), 0, st, ta);
+    else hipLaunchKernelGGL(tile_count_kernel<std::uint64_t>, dim3(TM), dim3(kThreads), 0, st, ta);
+    TCC_LAUNCH_CHECK();
+    TCC_HIP_CHECK(exclusive_scan(c.counters, c.counters, nCounters, c.counters + nCounters, c.temp, st));
+    hipLaunchKernelGGL(window_meta_kernel, dim3(grid_for(CW, kThreads)), dim3(kThreads), 0, st, c.counters, TM,
+                       c.firstTile, S, CW, c.wdBase, c.wActive, c.wTiles);
     TCC_LAUNCH_CHECK();
     TCC_HIP_CHECK(exclusive_scan(c.wTiles, m->colWindowOffset, CW, m->colWindowOffset + CW, c.temp, st));
-
-    // 8-10. distinct super-window rows, superWindowRowOffset
-    TCC_HIP_CHECK(exclusive_scan(c.flags, c.pos, E, c.numRows, c.temp, st));
-    hipLaunchKernelGGL(row_emit_kernel, dim3(grid_for(E, kThreads)), dim3(kThreads), 0, st, groupKey, c.flags,
-                       c.pos, numGroups, E, kl.wiBits, kl.dstBits, SW, c.rowStartGroup, m->superWindowRows,
-                       m->superWindowRowOffset);
+    hipLaunchKernelGGL(super_window_meta_kernel, dim3(grid_for(SW + 1, kThreads)), dim3(kThreads), 0, st, c.counters,
+                       TM, c.firstTile, S, SW, c.occBase, m->superWindowRowOffset, m->superWindowCachedCount,
+                       ws->deviceNumGroups);
     TCC_LAUNCH_CHECK();
 
-    // 6-7, 11-13. per super-window: row locations, slots, bitmaps, cache
-    // Super-windows with many groups (63k on average at 114M edges) walk them
-    // 1024 at a time; small ones keep 256-thread workgroups.
-    auto sw_launch = [&](auto kernel, unsigned threads) {
-        hipLaunchKernelGGL(kernel, dim3(SW), dim3(threads), 0, st, groupKey, c.groupInfo, c.flags, c.pos,
-                           c.rowStartGroup, c.wdBase, m->colWindowOffset, m->superWindowRowOffset, S, kl.wiBits, CW,
-                           m->tileRowSlot, reinterpret_cast<std::uint8_t*>(m->tileLocalBit),
-                           m->superWindowRowCacheSlot, m->superWindowCachedRowSlot, m->superWindowCachedCount, err);
-    };
-    if (E / std::max<std::uint64_t>(SW, 1) >= 8192) sw_launch(super_window_kernel<1024>, 1024);
-    else sw_launch(super_window_kernel<kThreads>, kThreads);
+    // 4. every output in place, then the padding rows
+    if (narrow) hipLaunchKernelGGL(tile_emit_kernel<std::uint32_t>, dim3(TM), dim3(kThreads), 0, st, ta);
+    else hipLaunchKernelGGL(tile_emit_kernel<std::uint64_t>, dim3(TM), dim3(kThreads), 0, st, ta);
     TCC_LAUNCH_CHECK();
     hipLaunchKernelGGL(padding_kernel, dim3(grid_for(CW, kThreads)), dim3(kThreads), 0, st, c.wActive,
-                       m->colWindowOffset, CW, m->tileRowSlot);
+                       m->colWindowOffset, CW, m->tileRowSlot, reinterpret_cast<std::uint8_t*>(m->tileLocalBit));
     TCC_LAUNCH_CHECK();
     return TCC_OK;
 }

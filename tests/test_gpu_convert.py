@@ -140,3 +140,60 @@ def test_reference_api_errors(gpu):
     d = torch.zeros(8, dtype=torch.int32, device="cuda")
     with pytest.raises(TccError, match="invalid COO"):
         swtcf.convertCOOToSWTCF(d, d, 5, m, ws)  # more edges than the capacity
+
+
+def _hub_graph(rows, cols, seed):
+    """Every 97th row is a hub touching about 60% of the columns, the rest
+    hold about 6 edges each; returned in (dst, src) order."""
+    rng = np.random.default_rng(seed)
+    dense = rng.random((rows, cols)) < np.where(np.arange(rows)[:, None] % 97 == 0, 0.6, 6.0 / cols)
+    dst, src = np.nonzero(dense)
+    return dst.astype(np.uint32), src.astype(np.uint32)
+
+
+@pytest.mark.parametrize("S", [16, 3])
+def test_multi_tile_segments_sorted_and_shuffled(gpu, oracle, S):
+    """Super-windows of many 4096-element tiles, hub rows of up to 8S elements
+    across tile ends: a COO in (dst, src) order (the sort's one-digit path)
+    and the same COO shuffled (every digit) give the oracle's arrays."""
+    rows, cols = 40_000, 256
+    dst, src = _hub_graph(rows, cols, 7 + S)
+    ref = oracle.swtcf_convert(dst, src, rows, cols, S)
+    per_sw = np.bincount(src // (8 * S))
+    assert per_sw.max() > 6 * 4096  # many tiles per super-window
+    m, err, ng = convert_gpu(dst, src, rows, cols, S)
+    assert err == 0 and ng == ref["numGroups"]
+    assert_same(oracle, m, ref)
+    perm = np.random.default_rng(S).permutation(dst.size)
+    m2, err2, ng2 = convert_gpu(dst[perm], src[perm], rows, cols, S)
+    assert err2 == 0 and ng2 == ref["numGroups"]
+    assert_same(oracle, m2, ref)
+
+
+@pytest.mark.parametrize("pos", [1, 63, 64, 1023, 1024, 4095, 4096, 8191])
+def test_one_pair_out_of_order(gpu, oracle, pos):
+    """A (dst, src)-ordered COO with one adjacent pair swapped, at lane, wave
+    and tile boundaries: the input pass must see it, or the one-digit sort
+    would leave that pair out of order."""
+    rows, cols = 3_000, 1_000
+    rng = np.random.default_rng(pos)
+    keys = np.sort(rng.choice(rows * cols, size=12_000, replace=False))
+    dst, src = (keys // cols).astype(np.uint32), (keys % cols).astype(np.uint32)
+    dst[[pos - 1, pos]] = dst[[pos, pos - 1]]
+    src[[pos - 1, pos]] = src[[pos, pos - 1]]
+    m, err, _ = convert_gpu(dst, src, rows, cols, 16)
+    assert err == 0
+    assert_same(oracle, m, oracle.swtcf_convert(dst, src, rows, cols, 16))
+
+
+def test_rows_unknown_wide_keys(gpu, oracle):
+    """rows = 0 (no destination bound): 32 destination bits, so the element
+    keys pass 32 bits and take five low-digit passes."""
+    rows, cols = 5_000, 2_000
+    rng = np.random.default_rng(11)
+    keys = rng.choice(rows * cols, size=30_000, replace=False)
+    dst, src = (keys // cols).astype(np.uint32), (keys % cols).astype(np.uint32)
+    dst = (dst * 811_371).astype(np.uint32)  # destinations far above 2**24
+    m, err, _ = convert_gpu(dst, src, 0, cols, 16)
+    assert err == 0
+    assert_same(oracle, m, oracle.swtcf_convert(dst, src, 0, cols, 16))
