@@ -176,6 +176,8 @@ __device__ __forceinline__ std::uint64_t make_elem(std::uint32_t d, std::uint32_
     return (static_cast<std::uint64_t>(sw) << p.kb) | (static_cast<std::uint64_t>(d) << p.loBits) | lo;
 }
 
+__device__ __forceinline__ std::uint64_t clamp_to(std::uint64_t i, std::uint64_t last) { return i < last ? i : last; }
+
 __device__ __forceinline__ unsigned digit_of(std::uint64_t e, Digit d) {
     return static_cast<unsigned>(e >> d.shift) & ((1u << d.bits) - 1u);
 }
@@ -211,17 +213,26 @@ __global__ void __launch_bounds__(kThreads) input_pass_kernel(const std::uint32_
     __syncthreads();
     const std::uint64_t base = static_cast<std::uint64_t>(blockIdx.x) * kTile + wave * kSpan;
     bool outOfOrder = false, srcBad = false, dstBad = false;
-#pragma unroll 4
+    std::uint32_t dv[kRounds], sv[kRounds];
+#pragma unroll
+    for (unsigned r = 0; r < kRounds; ++r) {
+        const std::uint64_t i = clamp_to(base + r * kWave + lane, n - 1);
+        dv[r] = dst[i];
+        sv[r] = src[i];
+    }
+    // the element before the wave's first (itself for element 0)
+    const std::uint64_t before = base > 0 ? clamp_to(base - 1, n - 1) : 0;
+    const std::uint32_t d0 = dst[before], s0 = src[before];
+#pragma unroll
     for (unsigned r = 0; r < kRounds; ++r) {
         const std::uint64_t i = base + r * kWave + lane;
         const bool valid = i < n;
-        const std::uint32_t d = valid ? dst[i] : 0u;
-        const std::uint32_t s = valid ? src[i] : 0u;
+        const std::uint32_t d = dv[r], s = sv[r];
         std::uint32_t pd = __shfl_up(d, 1, kWave);
         std::uint32_t ps = __shfl_up(s, 1, kWave);
-        if (lane == 0 && valid && i > 0) {
-            pd = dst[i - 1];
-            ps = src[i - 1];
+        if (lane == 0) {
+            pd = r == 0 ? d0 : static_cast<std::uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(dv[r > 0 ? r - 1 : 0]), kWave - 1));
+            ps = r == 0 ? s0 : static_cast<std::uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(sv[r > 0 ? r - 1 : 0]), kWave - 1));
         }
         if (valid) {
             if (i > 0 && (d < pd || (d == pd && s < ps))) outOfOrder = true;
@@ -276,12 +287,13 @@ __global__ void __launch_bounds__(kThreads) elem_hist_kernel(const std::uint64_t
     const unsigned wave = threadIdx.x / kWave;
     for (unsigned i = threadIdx.x; i < kWaves * kMaxBins; i += kThreads) (&h[0][0])[i] = 0;
     __syncthreads();
-    const std::uint64_t base = static_cast<std::uint64_t>(blockIdx.x) * kTile + wave * kSpan;
-#pragma unroll 4
-    for (unsigned r = 0; r < kRounds; ++r) {
-        const std::uint64_t i = base + r * kWave + lane;
-        if (i < n) atomicAdd(&h[wave][digit_of(in[i], dg)], 1u);
-    }
+    const std::uint64_t base = static_cast<std::uint64_t>(blockIdx.x) * kTile + wave * kSpan + lane;
+    std::uint64_t k[kRounds];
+#pragma unroll
+    for (unsigned r = 0; r < kRounds; ++r) k[r] = in[clamp_to(base + r * kWave, n - 1)];
+#pragma unroll
+    for (unsigned r = 0; r < kRounds; ++r)
+        if (base + r * kWave < n) atomicAdd(&h[wave][digit_of(k[r], dg)], 1u);
     __syncthreads();
     for (unsigned b = threadIdx.x; b < (1u << dg.bits); b += kThreads) {
         std::uint32_t t = 0;
@@ -305,12 +317,40 @@ struct ScatterArgs {
     int source;        // 0: `in`; 1: the COO; 2: the COO if it is in order, else `in`
 };
 
+// The 16 rounds' elements of a lane (element first + 64 r), all loads
+// issued before any is used: indices past the end are clamped to the last
+// element (those lanes take no part in what follows).
+__device__ __forceinline__ void load_elems(const ScatterArgs& a, bool coo, std::uint64_t first,
+                                           std::uint64_t (&k)[kRounds]) {
+    const std::uint64_t last = a.n - 1;
+    if (coo) {
+        std::uint32_t d[kRounds], s[kRounds];
+#pragma unroll
+        for (unsigned r = 0; r < kRounds; ++r) {
+            const std::uint64_t i = clamp_to(first + r * kWave, last);
+            d[r] = a.dst[i];
+            s[r] = a.src[i];
+        }
+#pragma unroll
+        for (unsigned r = 0; r < kRounds; ++r) k[r] = make_elem(d[r], s[r], a.ep);
+    } else {
+#pragma unroll
+        for (unsigned r = 0; r < kRounds; ++r) k[r] = a.in[clamp_to(first + r * kWave, last)];
+    }
+}
+
 // Stable scatter of one digit: position = the (digit, tile) offset + the
 // same digit's count in earlier waves of the tile + earlier lanes and rounds
-// of this wave.  Written from the lanes (staging the tile in LDS by digit
-// measured no faster for 8-byte keys).
+// of this wave.  The tile is first ordered by digit in LDS and then written
+// out in that order, so that consecutive lanes write consecutive addresses
+// of a digit's run (6.18 against 6.47 ms for a shuffled 114M-edge
+// conversion with each lane writing its own elements).
 __global__ void __launch_bounds__(kThreads) elem_scatter_kernel(ScatterArgs a) {
     __shared__ std::uint32_t cnt[kWaves][kMaxBins];
+    __shared__ std::uint32_t gbase[kMaxBins];   // global start of (digit, this tile)
+    __shared__ std::uint32_t tstart[kMaxBins];  // start of the digit's run in the tile
+    __shared__ std::uint32_t waveSum[kWaves];
+    __shared__ std::uint64_t stage[kTile];
     if (a.onlyUnsorted && *a.unsorted == 0u) return;
     const bool coo = a.source == 1 || (a.source == 2 && *a.unsorted == 0u);
     const unsigned lane = __lane_id();
@@ -318,16 +358,16 @@ __global__ void __launch_bounds__(kThreads) elem_scatter_kernel(ScatterArgs a) {
     const unsigned bins = 1u << a.dg.bits;
     for (unsigned i = threadIdx.x; i < kWaves * kMaxBins; i += kThreads) (&cnt[0][0])[i] = 0;
     __syncthreads();
-    const std::uint64_t base = static_cast<std::uint64_t>(blockIdx.x) * kTile + wave * kSpan;
+    const std::uint64_t tile0 = static_cast<std::uint64_t>(blockIdx.x) * kTile;
+    const std::uint64_t base = tile0 + wave * kSpan;
     const std::uint64_t lt = lanemask_lt();
     std::uint64_t k[kRounds];
     std::uint32_t rank[kRounds];
+    load_elems(a, coo, base + lane, k);
 #pragma unroll
     for (unsigned r = 0; r < kRounds; ++r) {
         const std::uint64_t i = base + r * kWave + lane;
         const bool valid = i < a.n;
-        if (coo) k[r] = valid ? make_elem(a.dst[i], a.src[i], a.ep) : 0ull;
-        else k[r] = valid ? a.in[i] : 0ull;
         const unsigned d = digit_of(k[r], a.dg);
         const std::uint64_t peers = match_peers_bits(d, valid, a.dg.bits);
         const std::uint32_t before = cnt[wave][d];
@@ -337,19 +377,52 @@ __global__ void __launch_bounds__(kThreads) elem_scatter_kernel(ScatterArgs a) {
         if (valid && (peers & lt) == 0) cnt[wave][d] = before + static_cast<std::uint32_t>(__popcll(peers));
     }
     __syncthreads();
-    for (unsigned d = threadIdx.x; d < bins; d += kThreads) {
-        std::uint32_t run = a.histScan[static_cast<std::uint64_t>(d) * a.tiles + blockIdx.x];
-        for (unsigned w = 0; w < kWaves; ++w) {
-            const std::uint32_t c = cnt[w][d];
-            cnt[w][d] = run;  // absolute base of (wave w, digit d)
-            run += c;
-        }
-    }
-    __syncthreads();
+    {
+        // thread j holds digits 2j and 2j + 1: their per-wave offsets within
+        // the digit's run, and the runs' starts (an exclusive scan of the
+        // digits' tile counts, in digit order)
+        std::uint32_t tot[2] = {0, 0};
 #pragma unroll
-    for (unsigned r = 0; r < kRounds; ++r) {
-        const std::uint64_t i = base + r * kWave + lane;
-        if (i < a.n) a.out[cnt[wave][digit_of(k[r], a.dg)] + rank[r]] = k[r];
+        for (unsigned q = 0; q < 2; ++q) {
+            const unsigned d = 2 * threadIdx.x + q;
+            if (d < bins) {
+                for (unsigned w = 0; w < kWaves; ++w) {
+                    const std::uint32_t c = cnt[w][d];
+                    cnt[w][d] = tot[q];
+                    tot[q] += c;
+                }
+                gbase[d] = a.histScan[static_cast<std::uint64_t>(d) * a.tiles + blockIdx.x];
+            }
+        }
+        const std::uint32_t pair = tot[0] + tot[1];
+        std::uint32_t inc = pair;
+#pragma unroll
+        for (unsigned o = 1; o < kWave; o <<= 1) {
+            const std::uint32_t y = __shfl_up(inc, o, kWave);
+            if (lane >= o) inc += y;
+        }
+        if (lane == kWave - 1) waveSum[wave] = inc;
+        __syncthreads();
+        std::uint32_t off = inc - pair;
+        for (unsigned w = 0; w < wave; ++w) off += waveSum[w];
+        if (2 * threadIdx.x < bins) tstart[2 * threadIdx.x] = off;
+        if (2 * threadIdx.x + 1 < bins) tstart[2 * threadIdx.x + 1] = off + tot[0];
+        __syncthreads();
+#pragma unroll
+        for (unsigned r = 0; r < kRounds; ++r) {
+            const std::uint64_t i = base + r * kWave + lane;
+            if (i < a.n) {
+                const unsigned d = digit_of(k[r], a.dg);
+                stage[tstart[d] + cnt[wave][d] + rank[r]] = k[r];
+            }
+        }
+        __syncthreads();
+        const std::uint32_t count = static_cast<std::uint32_t>(clamp_to(kTile, a.n - tile0));
+        for (std::uint32_t p = threadIdx.x; p < count; p += kThreads) {
+            const std::uint64_t key = stage[p];
+            const unsigned d = digit_of(key, a.dg);
+            a.out[gbase[d] + (p - tstart[d])] = key;
+        }
     }
 }
 
@@ -403,7 +476,12 @@ struct TileRange {
 
 constexpr unsigned kKeySlots = 1 + kTile + kLookahead;
 constexpr unsigned kFlagWords = (kTile + kLookahead + kWave - 1) / kWave;
-constexpr unsigned kLoadIters = (kKeySlots + kThreads - 1) / kThreads;
+// The emit pass runs 8 waves on a tile (8 rounds of 64 each): half the
+// per-lane rank registers of 4 waves, so twice the waves per SIMD.
+constexpr unsigned kEmitThreads = 512;
+constexpr unsigned kEmitWaves = kEmitThreads / kWave;
+constexpr unsigned kEmitRounds = kTile / kEmitThreads;
+constexpr unsigned kEmitSpan = kWave * kEmitRounds;
 
 // The keys of a segment tile and its head bitmaps.  K is u32 when the keys
 // have at most 31 bits (so that the ~0 sentinel never equals a key shifted
@@ -411,15 +489,19 @@ constexpr unsigned kLoadIters = (kKeySlots + kThreads - 1) / kThreads;
 template <typename K>
 struct TileKeys {
     K key[kKeySlots];                 // key[0]: element before the tile, or ~0; key[1 + i]: element i
-    std::uint64_t group[kFlagWords];  // bit i: element i starts a (window, dst) group
-    std::uint64_t row[kFlagWords];    // bit i: element i starts a row
+    // bit i: element i starts a (window, dst) group / a row; two spare words
+    // so that 64-bit windows may read past the last one written (those bits
+    // lie at or past avail and are masked)
+    std::uint64_t group[kFlagWords + 2];
+    std::uint64_t row[kFlagWords + 2];
 };
 
 // Segment tile t: its super-window (the last s with firstTile[s] <= t, never
 // an empty one), its elements, up to kLookahead elements past its end
 // (within the segment), and the head bits of all of them.
-template <typename K>
+template <unsigned THREADS, typename K>
 __device__ TileRange load_tile(const TileArgs& a, unsigned t, TileKeys<K>& tk) {
+    constexpr unsigned kLoadIters = (kKeySlots + THREADS - 1) / THREADS;
     std::uint32_t lo = 0, hi = a.SW;  // firstTile[lo] <= t < firstTile[hi]
     while (hi - lo > 1) {
         const std::uint32_t mid = (lo + hi) / 2;
@@ -434,18 +516,29 @@ __device__ TileRange load_tile(const TileArgs& a, unsigned t, TileKeys<K>& tk) {
     r.n = min(kTile, segEnd - r.start);
     r.avail = min(r.n + kLookahead, segEnd - r.start);
     const bool hasPrev = r.start > segBegin;
+    // all loads issued before any is stored: indices clamped into the
+    // segment, the slot before a segment's first element set to ~0 after
+    std::uint64_t v[kLoadIters];
+    const std::uint32_t first = hasPrev ? r.start - 1 : r.start;
 #pragma unroll
     for (unsigned q = 0; q < kLoadIters; ++q) {
-        const unsigned j = q * kThreads + threadIdx.x;
-        if (j <= r.avail) {
-            K v = static_cast<K>(~0ull);
-            if (j > 0 || hasPrev) v = static_cast<K>(a.el[r.start - 1 + j] & a.keyMask);
-            tk.key[j] = v;
+        const unsigned j = q * THREADS + threadIdx.x;
+        v[q] = a.el[min(first + j, segEnd > 0 ? segEnd - 1 : 0u)];
+    }
+#pragma unroll
+    for (unsigned q = 0; q < kLoadIters; ++q) {
+        const unsigned j = q * THREADS + threadIdx.x;
+        // key[j] = element start - 1 + j
+        if (hasPrev) {
+            if (j <= r.avail) tk.key[j] = static_cast<K>(v[q] & a.keyMask);
+        } else if (j < r.avail) {
+            tk.key[j + 1] = static_cast<K>(v[q] & a.keyMask);
         }
     }
+    if (!hasPrev && threadIdx.x == 0) tk.key[0] = static_cast<K>(~0ull);
     __syncthreads();
     const unsigned lane = __lane_id();
-    for (unsigned base = (threadIdx.x / kWave) * kWave; base < r.avail; base += kThreads) {
+    for (unsigned base = (threadIdx.x / kWave) * kWave; base < r.avail; base += THREADS) {
         const unsigned j = base + lane;
         bool g = false, h = false;
         if (j < r.avail) {
@@ -497,25 +590,48 @@ struct Head {
     unsigned occ;    // row: groups in the row
 };
 
+// Bits [i, i + 64) of a bitmap.
+__device__ __forceinline__ std::uint64_t window64(const std::uint64_t* w, unsigned i) {
+    const unsigned k = i >> 6, sh = i & 63;
+    const std::uint64_t lo = w[k], hi = w[k + 1];
+    return sh ? (lo >> sh) | (hi << (64 - sh)) : lo;
+}
+
 // Element i of the tile; elements [0, avail) are loaded.  A group ends at
-// the next group head (a row head is one too), a row at the next row head.
+// the next group head (a row head is one too), a row at the next row head:
+// both found in a 64-bit window of the head bits (groups have at most 9
+// elements here; rows longer than 64 take the word loop).
 template <bool BITS, typename K>
 __device__ __forceinline__ Head head_at(const TileKeys<K>& tk, unsigned i, unsigned avail) {
     Head h{};
     h.gh = bit_at(tk.group, i);
     h.rh = bit_at(tk.row, i);
     if (h.gh) {
-        h.count = next_bit(tk.group, i + 1, min(avail, i + 9)) - i;
+        const std::uint64_t after = window64(tk.group, i + 1) | (1ull << 8);
+        h.count = min(static_cast<unsigned>(__builtin_ctzll(after)) + 1, avail - i);
         if constexpr (BITS) {
             const unsigned deg = min(h.count, 8u);
+            // eight unconditional reads (slots past the loaded elements are
+            // in the array and masked), so they issue together
             unsigned bits = 0;
 #pragma unroll
-            for (unsigned q = 0; q < 8; ++q)
-                if (q < deg) bits |= 1u << static_cast<unsigned>(tk.key[i + 1 + q] & 7u);
+            for (unsigned q = 0; q < 8; ++q) {
+                const unsigned b = 1u << static_cast<unsigned>(tk.key[i + 1 + q] & 7u);
+                bits |= q < deg ? b : 0u;
+            }
             h.bits = bits;
         }
     }
-    if (h.rh) h.occ = count_bits(tk.group, i, next_bit(tk.row, i + 1, avail));
+    if (h.rh) {
+        const std::uint64_t after = window64(tk.row, i + 1);
+        if (after != 0 && static_cast<unsigned>(__builtin_ctzll(after)) + 1 <= avail - i) {
+            const unsigned len = static_cast<unsigned>(__builtin_ctzll(after)) + 1;  // <= 64
+            const std::uint64_t mask = len == 64 ? ~0ull : (1ull << len) - 1ull;
+            h.occ = static_cast<unsigned>(__popcll(window64(tk.group, i) & mask));
+        } else {
+            h.occ = count_bits(tk.group, i, next_bit(tk.row, i + 1, avail));
+        }
+    }
     return h;
 }
 
@@ -532,7 +648,7 @@ __global__ void __launch_bounds__(kThreads) tile_count_kernel(TileArgs a) {
         return;
     }
     for (unsigned b = threadIdx.x; b < nb; b += kThreads) hist[b] = 0;
-    const TileRange r = load_tile(a, t, tk);
+    const TileRange r = load_tile<kThreads>(a, t, tk);
     const std::uint32_t loMask = (1u << a.loBits) - 1u;
     const unsigned rowBin = 8 * a.S, groupBin = 8 * a.S + 32;
     std::uint32_t groups = 0, rows = 0;
@@ -610,24 +726,24 @@ __global__ void super_window_meta_kernel(const std::uint32_t* __restrict__ P, st
 // assignGroupLocationsKernel (:292-376), fillValidTileRowSlotsKernel
 // (:1003-1048), the tile bitmaps (:430-455, one byte per tile row), the
 // super-window rows (:459-681) and the repeat cache (:699-895), per segment
-// tile.  Wave w ranks elements [1024 w, 1024 w + 1024) of the tile in 16
-// rounds of 64, so ranks follow element order.
+// tile.  Wave w ranks elements [512 w, 512 w + 512) of the tile in 8 rounds
+// of 64, so ranks follow element order.
 template <typename K>
-__global__ void __launch_bounds__(kThreads) tile_emit_kernel(TileArgs a) {
+__global__ void __launch_bounds__(kEmitThreads) tile_emit_kernel(TileArgs a) {
     __shared__ TileKeys<K> tk;
-    __shared__ std::uint32_t cntG[kWaves][8 * kMaxS];
-    __shared__ std::uint32_t cntO[kWaves][kOccBins + 1];
+    __shared__ std::uint32_t cntG[kEmitWaves][8 * kMaxS];
+    __shared__ std::uint32_t cntO[kEmitWaves][kOccBins + 1];
     __shared__ std::uint32_t info[kTile];          // head facts of element i
     __shared__ std::uint64_t baseG[8 * kMaxS];   // tile-row index of the bin's first head in this tile
     __shared__ std::uint32_t baseO[kOccBins + 1];  // cache slot of the bin's first repeated row in this tile
-    __shared__ std::uint32_t rowsW[kWaves];
+    __shared__ std::uint32_t rowsW[kEmitWaves];
     const unsigned t = blockIdx.x;
     if (t >= a.firstTile[a.SW]) return;
-    const TileRange r = load_tile(a, t, tk);
+    const TileRange r = load_tile<kEmitThreads>(a, t, tk);
     const std::uint32_t s = r.s;
     const std::uint32_t t0 = a.firstTile[s];
     const unsigned groupBins = 8 * a.S;
-    for (unsigned b = threadIdx.x; b < groupBins; b += kThreads) {
+    for (unsigned b = threadIdx.x; b < groupBins; b += kEmitThreads) {
         // bin b = (wi, degree - 1): the window's degree-bucket base, plus the
         // bucket's heads in the segment's earlier tiles
         const std::uint64_t o = static_cast<std::uint64_t>(b) * a.TM;
@@ -636,13 +752,13 @@ __global__ void __launch_bounds__(kThreads) tile_emit_kernel(TileArgs a) {
         baseG[b] = w < a.CW ? static_cast<std::uint64_t>(a.colWindowOffset[w]) * 8 +
                                   a.wdBase[static_cast<std::uint64_t>(w) * 8 + b % 8] + rel
                             : 0;
-        for (unsigned v = 0; v < kWaves; ++v) cntG[v][b] = 0;
+        for (unsigned v = 0; v < kEmitWaves; ++v) cntG[v][b] = 0;
     }
-    for (unsigned b = threadIdx.x; b < kOccBins; b += kThreads) {
+    for (unsigned b = threadIdx.x; b < kOccBins; b += kEmitThreads) {
         const std::uint64_t o = static_cast<std::uint64_t>(groupBins + 1 + b) * a.TM;
         baseO[b] = a.occBase[static_cast<std::uint64_t>(s) * kOccStride + b + 2] + a.counters[o + t] -
                    a.counters[o + t0];
-        for (unsigned v = 0; v < kWaves; ++v) cntO[v][b] = 0;
+        for (unsigned v = 0; v < kEmitWaves; ++v) cntO[v][b] = 0;
     }
     const std::uint64_t rowBin = static_cast<std::uint64_t>(groupBins) * a.TM;
     const std::uint32_t rowBase = a.counters[rowBin + t] - a.counters[rowBin];
@@ -655,7 +771,7 @@ __global__ void __launch_bounds__(kThreads) tile_emit_kernel(TileArgs a) {
     const std::uint32_t loMask = (1u << a.loBits) - 1u;
     // info[i] = gh | rh << 1 | rep << 2 | degree << 3 | bits << 7 | wi << 15 |
     // (occ - 2) << 20, for the tile's elements
-    for (unsigned i = threadIdx.x; i < r.n; i += kThreads) {
+    for (unsigned i = threadIdx.x; i < r.n; i += kEmitThreads) {
         const Head h = head_at<true>(tk, i, r.avail);
         const unsigned deg = h.gh ? min(h.count, 8u) : 1u;
         const bool rep = h.rh && h.occ >= 2 && h.occ <= kMaxS;
@@ -666,11 +782,11 @@ __global__ void __launch_bounds__(kThreads) tile_emit_kernel(TileArgs a) {
     __syncthreads();
     // ranks per round: group rank | occurrence rank << 10 | rows of the wave
     // up to and including the element << 20 (ranks within the wave)
-    std::uint32_t ranks[kRounds];
+    std::uint32_t ranks[kEmitRounds];
     std::uint32_t rowRun = 0;
 #pragma unroll
-    for (unsigned r0 = 0; r0 < kRounds; ++r0) {
-        const unsigned i = wave * kSpan + r0 * kWave + lane;
+    for (unsigned r0 = 0; r0 < kEmitRounds; ++r0) {
+        const unsigned i = wave * kEmitSpan + r0 * kWave + lane;
         const std::uint32_t f = i < r.n ? info[i] : 0u;
         const bool gh = f & 1u, rh = f & 2u, rep = f & 4u;
         const unsigned gbin = gh ? ((f >> 15) & 31u) * 8 + ((f >> 3) & 15u) - 1 : 0u;
@@ -690,17 +806,17 @@ __global__ void __launch_bounds__(kThreads) tile_emit_kernel(TileArgs a) {
     }
     if (lane == 0) rowsW[wave] = rowRun;
     __syncthreads();
-    for (unsigned b = threadIdx.x; b < groupBins; b += kThreads) {
+    for (unsigned b = threadIdx.x; b < groupBins; b += kEmitThreads) {
         std::uint32_t run = 0;
-        for (unsigned w = 0; w < kWaves; ++w) {
+        for (unsigned w = 0; w < kEmitWaves; ++w) {
             const std::uint32_t c = cntG[w][b];
             cntG[w][b] = run;
             run += c;
         }
     }
-    for (unsigned b = threadIdx.x; b < kOccBins; b += kThreads) {
+    for (unsigned b = threadIdx.x; b < kOccBins; b += kEmitThreads) {
         std::uint32_t run = 0;
-        for (unsigned w = 0; w < kWaves; ++w) {
+        for (unsigned w = 0; w < kEmitWaves; ++w) {
             const std::uint32_t c = cntO[w][b];
             cntO[w][b] = run;
             run += c;
@@ -710,8 +826,8 @@ __global__ void __launch_bounds__(kThreads) tile_emit_kernel(TileArgs a) {
     std::uint32_t rowOff = rowBase;
     for (unsigned w = 0; w < wave; ++w) rowOff += rowsW[w];
 #pragma unroll
-    for (unsigned r0 = 0; r0 < kRounds; ++r0) {
-        const unsigned i = wave * kSpan + r0 * kWave + lane;
+    for (unsigned r0 = 0; r0 < kEmitRounds; ++r0) {
+        const unsigned i = wave * kEmitSpan + r0 * kWave + lane;
         if (i >= r.n) continue;
         const std::uint32_t f = info[i];
         if ((f & 3u) == 0) continue;
@@ -968,8 +1084,8 @@ int tcc_swtcf_convert(const std::uint32_t* dDst, const std::uint32_t* dSrc, std:
     TCC_LAUNCH_CHECK();
 
     // 4. every output in place, then the padding rows
-    if (narrow) hipLaunchKernelGGL(tile_emit_kernel<std::uint32_t>, dim3(TM), dim3(kThreads), 0, st, ta);
-    else hipLaunchKernelGGL(tile_emit_kernel<std::uint64_t>, dim3(TM), dim3(kThreads), 0, st, ta);
+    if (narrow) hipLaunchKernelGGL(tile_emit_kernel<std::uint32_t>, dim3(TM), dim3(kEmitThreads), 0, st, ta);
+    else hipLaunchKernelGGL(tile_emit_kernel<std::uint64_t>, dim3(TM), dim3(kEmitThreads), 0, st, ta);
     TCC_LAUNCH_CHECK();
     hipLaunchKernelGGL(padding_kernel, dim3(grid_for(CW, kThreads)), dim3(kThreads), 0, st, c.wActive,
                        m->colWindowOffset, CW, m->tileRowSlot, reinterpret_cast<std::uint8_t*>(m->tileLocalBit));
