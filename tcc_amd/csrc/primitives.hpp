@@ -36,10 +36,14 @@ __device__ __forceinline__ std::uint32_t wave_inclusive_scan(std::uint32_t v) {
     return v;
 }
 
+// With `skip` given, the scan kernels return at once while *skip is 0 (a
+// scan whose input a skipped pass would have written).
 __global__ void __launch_bounds__(kPrimThreads) scan_reduce_kernel(const std::uint32_t* __restrict__ in,
                                                                   std::uint64_t n,
-                                                                  std::uint32_t* __restrict__ partial) {
+                                                                  std::uint32_t* __restrict__ partial,
+                                                                  const std::uint32_t* __restrict__ skip) {
     __shared__ std::uint32_t waveSum[kPrimWaves];
+    if (skip && *skip == 0u) return;
     const unsigned lane = __lane_id();
     const unsigned wave = threadIdx.x / kWave;
     const std::uint64_t base = static_cast<std::uint64_t>(blockIdx.x) * kPrimTile + wave * kWaveSpan;
@@ -66,8 +70,10 @@ __global__ void __launch_bounds__(kPrimThreads) scan_tiles_kernel(const std::uin
                                                                  std::uint32_t* __restrict__ out,
                                                                  std::uint64_t n,
                                                                  const std::uint32_t* __restrict__ tileOffset,
-                                                                 std::uint32_t* __restrict__ total) {
+                                                                 std::uint32_t* __restrict__ total,
+                                                                 const std::uint32_t* __restrict__ skip) {
     __shared__ std::uint32_t waveSum[kPrimWaves];
+    if (skip && *skip == 0u) return;
     const unsigned lane = __lane_id();
     const unsigned wave = threadIdx.x / kWave;
     const std::uint64_t base = static_cast<std::uint64_t>(blockIdx.x) * kPrimTile + wave * kWaveSpan;
@@ -111,24 +117,26 @@ inline std::uint64_t scan_temp_elems(std::uint64_t n) {
 
 // out[i] = sum_{j<i} in[i]; *total = sum of all (if total != nullptr).
 // `out` may alias `in`.  n == 0 writes *total = 0 via a one-item launch.
+// With `skip`, nothing is done while *skip is 0 (read on the device).
 inline hipError_t exclusive_scan(const std::uint32_t* in, std::uint32_t* out, std::uint64_t n,
-                                 std::uint32_t* total, std::uint32_t* temp, hipStream_t stream) {
+                                 std::uint32_t* total, std::uint32_t* temp, hipStream_t stream,
+                                 const std::uint32_t* skip = nullptr) {
     if (n <= static_cast<std::uint64_t>(kPrimTile)) {
         hipLaunchKernelGGL(scan_tiles_kernel, dim3(1), dim3(kPrimThreads), 0, stream, in, out, n,
-                           nullptr, total);
+                           nullptr, total, skip);
         return hipGetLastError();
     }
     const std::uint64_t tiles = (n + kPrimTile - 1) / kPrimTile;
     std::uint32_t* partial = temp;
     std::uint32_t* partialScan = temp + tiles;
     hipLaunchKernelGGL(scan_reduce_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kPrimThreads), 0,
-                       stream, in, n, partial);
+                       stream, in, n, partial, skip);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    e = exclusive_scan(partial, partialScan, tiles, nullptr, temp + 2 * tiles, stream);
+    e = exclusive_scan(partial, partialScan, tiles, nullptr, temp + 2 * tiles, stream, skip);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(scan_tiles_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kPrimThreads), 0,
-                       stream, in, out, n, partialScan, total);
+                       stream, in, out, n, partialScan, total, skip);
     return hipGetLastError();
 }
 

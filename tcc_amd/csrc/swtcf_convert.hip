@@ -69,6 +69,7 @@ struct ElemParams {
     std::uint32_t rows, cols;
     std::uint32_t span;  // 8S sources per super-window
     unsigned loBits, kb;
+    unsigned spanShift;  // log2(span) when span is a power of two, else 0
 };
 
 struct Digit {
@@ -96,6 +97,7 @@ inline Plan make_plan(std::uint32_t rows, std::uint32_t cols, std::uint32_t S, s
     p.ep.cols = cols;
     p.ep.span = 8 * S;
     p.ep.loBits = std::max(3u, ceil_log2(8ull * S));
+    p.ep.spanShift = (1u << p.ep.loBits) == p.ep.span ? p.ep.loBits : 0u;
     const unsigned dstBits = rows ? std::max(1u, ceil_log2(rows)) : 32u;
     p.ep.kb = dstBits + p.ep.loBits;
     p.swBits = std::max(1u, ceil_log2(numSuperWindows));
@@ -107,6 +109,12 @@ inline Plan make_plan(std::uint32_t rows, std::uint32_t cols, std::uint32_t S, s
 inline std::uint64_t sort_tiles(std::uint64_t E) { return std::max<std::uint64_t>(1, (E + kTile - 1) / kTile); }
 inline std::uint64_t segment_tiles_max(std::uint64_t E, std::uint64_t SW) { return (E + kTile - 1) / kTile + SW; }
 
+// What a segment tile's workgroup needs first, in one 16-byte load: its
+// super-window, first element, the super-window's end and first tile.
+struct TileInfo {
+    std::uint32_t s, start, segEnd, firstTile;
+};
+
 // Byte layout of the workspace scratch allocation.
 struct Carve {
     std::uint64_t* elemA;
@@ -116,12 +124,12 @@ struct Carve {
     std::uint32_t* counters;   // [bins * TM + 1] segment-tile counts, (bin, tile) order
     std::uint32_t* segStart;   // [SW+1]
     std::uint32_t* firstTile;  // [SW+1]
+    TileInfo* tileInfo;        // [TM]
     std::uint32_t* wdBase;     // [CW*8]
     std::uint32_t* wActive;    // [CW]
     std::uint32_t* wTiles;     // [CW]
     std::uint32_t* occBase;    // [SW*33]
     std::uint32_t* flags;      // [4]: [0] = input not in (dst, src) order
-    std::uint32_t* tileFlags;  // [sortTiles]: the input pass's tile is out of order
     std::uint32_t* temp;       // scan scratch
     std::size_t bytes;
 };
@@ -145,12 +153,12 @@ inline Carve carve(char* base, std::uint64_t E, std::uint64_t CW, std::uint64_t 
     c.counters = reinterpret_cast<std::uint32_t*>(take(4 * cnt));
     c.segStart = reinterpret_cast<std::uint32_t*>(take(4 * (SW + 1)));
     c.firstTile = reinterpret_cast<std::uint32_t*>(take(4 * (SW + 1)));
+    c.tileInfo = reinterpret_cast<TileInfo*>(take(sizeof(TileInfo) * segment_tiles_max(E, SW)));
     c.wdBase = reinterpret_cast<std::uint32_t*>(take(4 * CW * 8));
     c.wActive = reinterpret_cast<std::uint32_t*>(take(4 * CW));
     c.wTiles = reinterpret_cast<std::uint32_t*>(take(4 * CW));
     c.occBase = reinterpret_cast<std::uint32_t*>(take(4 * SW * kOccStride));
     c.flags = reinterpret_cast<std::uint32_t*>(take(4 * 4));
-    c.tileFlags = reinterpret_cast<std::uint32_t*>(take(4 * sort_tiles(E)));
     const std::uint64_t tempElems = std::max({scan_temp_elems(hist), scan_temp_elems(cnt), scan_temp_elems(CW + 1),
                                               scan_temp_elems(SW + 1)});
     c.temp = reinterpret_cast<std::uint32_t*>(take(4 * tempElems));
@@ -171,7 +179,7 @@ __device__ __forceinline__ std::uint64_t make_elem(std::uint32_t d, std::uint32_
         d = 0;
         s = 0;
     }
-    const std::uint32_t sw = s / p.span;
+    const std::uint32_t sw = p.spanShift ? s >> p.spanShift : s / p.span;
     const std::uint32_t lo = s - sw * p.span;
     return (static_cast<std::uint64_t>(sw) << p.kb) | (static_cast<std::uint64_t>(d) << p.loBits) | lo;
 }
@@ -200,7 +208,7 @@ __global__ void __launch_bounds__(kThreads) input_pass_kernel(const std::uint32_
                                                              const std::uint32_t* __restrict__ src, std::uint32_t n,
                                                              ElemParams ep, Digit low, std::uint32_t* __restrict__ histLow,
                                                              Digit top, std::uint32_t* __restrict__ histTop,
-                                                             unsigned tiles, std::uint32_t* __restrict__ tileOut,
+                                                             unsigned tiles, std::uint32_t* __restrict__ unsorted,
                                                              std::uint32_t* __restrict__ err) {
     __shared__ std::uint32_t hl[kWaves][kMaxBins];
     __shared__ std::uint32_t ht[kWaves][kMaxBins];
@@ -249,8 +257,11 @@ __global__ void __launch_bounds__(kThreads) input_pass_kernel(const std::uint32_
     if (srcBad) atomicMax(err, static_cast<std::uint32_t>(TCC_DEVERR_SRC_RANGE));
     if (dstBad) atomicMax(err, static_cast<std::uint32_t>(TCC_DEVERR_DST_RANGE));
     __syncthreads();
-    // one word per tile (a flag on one address from every wave serialises)
-    if (threadIdx.x == 0) tileOut[blockIdx.x] = waveOut[0] | waveOut[1] | waveOut[2] | waveOut[3];
+    // one atomic per workgroup, and none once the flag is seen set (atomics
+    // on one address from every wave serialise)
+    if (threadIdx.x == 0 && (waveOut[0] | waveOut[1] | waveOut[2] | waveOut[3]) &&
+        __hip_atomic_load(unsorted, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u)
+        atomicOr(unsorted, 1u);
     for (unsigned b = threadIdx.x; b < (1u << low.bits); b += kThreads) {
         std::uint32_t t = 0;
         for (unsigned w = 0; w < kWaves; ++w) t += hl[w][b];
@@ -261,18 +272,6 @@ __global__ void __launch_bounds__(kThreads) input_pass_kernel(const std::uint32_
         for (unsigned w = 0; w < kWaves; ++w) t += ht[w][b];
         histTop[static_cast<std::uint64_t>(b) * tiles + blockIdx.x] = t;
     }
-}
-
-// unsorted = OR of the input pass's per-tile flags (one workgroup).
-__global__ void __launch_bounds__(kThreads) any_kernel(const std::uint32_t* __restrict__ flags, unsigned n,
-                                                      std::uint32_t* __restrict__ out) {
-    __shared__ std::uint32_t waveAny[kWaves];
-    std::uint32_t v = 0;
-    for (unsigned i = threadIdx.x; i < n; i += kThreads) v |= flags[i];
-    const std::uint64_t b = __ballot(v != 0);
-    if (__lane_id() == 0) waveAny[threadIdx.x / kWave] = b != 0;
-    __syncthreads();
-    if (threadIdx.x == 0) *out = waveAny[0] | waveAny[1] | waveAny[2] | waveAny[3];
 }
 
 // Per-tile digit counts of an element array.  With onlyUnsorted, returns at
@@ -315,6 +314,13 @@ struct ScatterArgs {
     const std::uint32_t* unsorted;
     int onlyUnsorted;  // return at once for a COO in (dst, src) order
     int source;        // 0: `in`; 1: the COO; 2: the COO if it is in order, else `in`
+    // last pass only (else null): the low kb bits of each element go to
+    // out32 instead of `out` (keys of at most 31 bits), and segStart[sw]
+    // takes the smallest position of the elements that may start super-window
+    // sw (atomicMin; it holds n before the pass)
+    std::uint32_t* out32;
+    std::uint32_t* segStart;
+    std::uint64_t keyMask;
 };
 
 // The 16 rounds' elements of a lane (element first + 64 r), all loads
@@ -421,24 +427,43 @@ __global__ void __launch_bounds__(kThreads) elem_scatter_kernel(ScatterArgs a) {
         for (std::uint32_t p = threadIdx.x; p < count; p += kThreads) {
             const std::uint64_t key = stage[p];
             const unsigned d = digit_of(key, a.dg);
-            a.out[gbase[d] + (p - tstart[d])] = key;
+            const std::uint32_t pos = gbase[d] + (p - tstart[d]);
+            if (a.out32) a.out32[pos] = static_cast<std::uint32_t>(key & a.keyMask);
+            else a.out[pos] = key;
+            if (a.segStart) {
+                // a digit's run in the tile is in (sw, key) order, the earlier
+                // passes having sorted every lower bit: only its first element
+                // and elements whose sw differs from their neighbour's may
+                // start a super-window
+                const std::uint32_t sw = static_cast<std::uint32_t>(key >> a.ep.kb);
+                if (p == tstart[d] || static_cast<std::uint32_t>(stage[p - 1] >> a.ep.kb) != sw)
+                    atomicMin(&a.segStart[sw], pos);
+            }
         }
     }
 }
 
 // ---------------------------------------------------------------- segments
 
-// segStart[s] = first element of super-window s (the sorted order's run
-// boundaries of sw); empty super-windows get the next one's start.
-__global__ void segment_bounds_kernel(const std::uint64_t* __restrict__ el, std::uint32_t n, unsigned kb,
-                                      std::uint32_t SW, std::uint32_t* __restrict__ segStart) {
-    const std::uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= n) return;
-    const std::uint32_t sw = min(static_cast<std::uint32_t>(el[e] >> kb), SW - 1);
-    const std::int64_t prev = e == 0 ? -1 : static_cast<std::int64_t>(min(static_cast<std::uint32_t>(el[e - 1] >> kb), SW - 1));
-    for (std::int64_t t = prev + 1; t <= static_cast<std::int64_t>(sw); ++t) segStart[t] = e;
-    if (e == n - 1)
-        for (std::uint32_t t = sw + 1; t <= SW; ++t) segStart[t] = n;
+// segStart[s] = min(segStart[s], segStart[s + 1]) from the end, in one
+// workgroup: an empty super-window (still n after the last pass) gets the
+// next one's start, and segStart[SW] stays n.
+__global__ void __launch_bounds__(kThreads) segment_fix_kernel(std::uint32_t* __restrict__ segStart,
+                                                               std::uint32_t SW) {
+    __shared__ std::uint32_t chunkMin[kThreads];
+    const std::uint32_t total = SW + 1;
+    const std::uint32_t chunk = (total + kThreads - 1) / kThreads;
+    const std::uint32_t b = min(threadIdx.x * chunk, total), e = min(b + chunk, total);
+    std::uint32_t m = 0xFFFFFFFFu;
+    for (std::uint32_t i = b; i < e; ++i) m = min(m, segStart[i]);
+    chunkMin[threadIdx.x] = m;
+    __syncthreads();
+    std::uint32_t run = 0xFFFFFFFFu;  // min over the later chunks
+    for (unsigned t = threadIdx.x + 1; t < kThreads; ++t) run = min(run, chunkMin[t]);
+    for (std::uint32_t i = e; i > b; --i) {
+        run = min(run, segStart[i - 1]);
+        segStart[i - 1] = run;
+    }
 }
 
 __global__ void segment_tiles_kernel(const std::uint32_t* __restrict__ segStart, std::uint32_t SW,
@@ -447,8 +472,18 @@ __global__ void segment_tiles_kernel(const std::uint32_t* __restrict__ segStart,
     if (s < SW) tileCount[s] = (segStart[s + 1] - segStart[s] + kTile - 1) / kTile;
 }
 
+__global__ void tile_info_kernel(const std::uint32_t* __restrict__ segStart,
+                                 const std::uint32_t* __restrict__ firstTile, std::uint32_t SW,
+                                 TileInfo* __restrict__ info) {
+    const std::uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= SW) return;
+    const std::uint32_t t0 = firstTile[s], t1 = firstTile[s + 1], b = segStart[s], e = segStart[s + 1];
+    for (std::uint32_t t = t0; t < t1; ++t) info[t] = TileInfo{s, b + (t - t0) * kTile, e, t0};
+}
+
 struct TileArgs {
-    const std::uint64_t* el;
+    const std::uint64_t* el;      // the sorted elements (keys of more than 31 bits)
+    const std::uint32_t* keys32;  // or their low kb bits
     std::uint32_t n;    // elements
     std::uint32_t cap;  // the matrix's edge capacity (bounds of the row and tile-row arrays)
     std::uint64_t keyMask;  // the low kb bits: dst << loBits | lo
@@ -456,7 +491,9 @@ struct TileArgs {
     std::uint32_t S, SW, CW;
     const std::uint32_t* segStart;
     const std::uint32_t* firstTile;  // [SW+1] exclusive scan of tiles per segment
+    const TileInfo* tileInfo;        // [tiles]
     std::uint32_t* counters;         // [bins][TM] (+1), scanned before the emit pass
+    std::uint32_t* info;             // [n] head facts of each element (count pass -> emit pass)
     std::uint32_t TM;
     std::uint32_t* err;
     // emit pass
@@ -471,7 +508,7 @@ struct TileArgs {
 };
 
 struct TileRange {
-    std::uint32_t s, start, n, avail;
+    std::uint32_t s, t0, start, n, avail;
 };
 
 constexpr unsigned kKeySlots = 1 + kTile + kLookahead;
@@ -496,26 +533,19 @@ struct TileKeys {
     std::uint64_t row[kFlagWords + 2];
 };
 
-// Segment tile t: its super-window (the last s with firstTile[s] <= t, never
-// an empty one), its elements, up to kLookahead elements past its end
-// (within the segment), and the head bits of all of them.
+// Segment tile t: its elements, up to kLookahead elements past its end
+// (within the super-window), and the head bits of all of them.
 template <unsigned THREADS, typename K>
-__device__ TileRange load_tile(const TileArgs& a, unsigned t, TileKeys<K>& tk) {
+__device__ TileRange load_tile(const TileArgs& a, unsigned t, const TileInfo& ti, TileKeys<K>& tk) {
     constexpr unsigned kLoadIters = (kKeySlots + THREADS - 1) / THREADS;
-    std::uint32_t lo = 0, hi = a.SW;  // firstTile[lo] <= t < firstTile[hi]
-    while (hi - lo > 1) {
-        const std::uint32_t mid = (lo + hi) / 2;
-        if (a.firstTile[mid] <= t) lo = mid;
-        else hi = mid;
-    }
     TileRange r;
-    r.s = lo;
-    const std::uint32_t segEnd = min(a.segStart[lo + 1], a.n);
-    const std::uint32_t segBegin = min(a.segStart[lo], segEnd);
-    r.start = min(segBegin + (t - a.firstTile[lo]) * kTile, segEnd);
+    r.s = ti.s;
+    r.t0 = ti.firstTile;
+    const std::uint32_t segEnd = min(ti.segEnd, a.n);
+    r.start = min(ti.start, segEnd);
     r.n = min(kTile, segEnd - r.start);
     r.avail = min(r.n + kLookahead, segEnd - r.start);
-    const bool hasPrev = r.start > segBegin;
+    const bool hasPrev = t > ti.firstTile;
     // all loads issued before any is stored: indices clamped into the
     // segment, the slot before a segment's first element set to ~0 after
     std::uint64_t v[kLoadIters];
@@ -523,7 +553,9 @@ __device__ TileRange load_tile(const TileArgs& a, unsigned t, TileKeys<K>& tk) {
 #pragma unroll
     for (unsigned q = 0; q < kLoadIters; ++q) {
         const unsigned j = q * THREADS + threadIdx.x;
-        v[q] = a.el[min(first + j, segEnd > 0 ? segEnd - 1 : 0u)];
+        const std::uint32_t e = min(first + j, segEnd > 0 ? segEnd - 1 : 0u);
+        if constexpr (sizeof(K) == 4) v[q] = a.keys32[e];
+        else v[q] = a.el[e];
     }
 #pragma unroll
     for (unsigned q = 0; q < kLoadIters; ++q) {
@@ -582,6 +614,11 @@ __device__ __forceinline__ unsigned count_bits(const std::uint64_t* w, unsigned 
     }
     return c;
 }
+
+// Head facts of an element, one u32 written by the count pass for the emit
+// pass: group head | row head << 1 | repeated row << 2 | degree << 3 |
+// group bitmap << 7 | wi << 15 | (occurrences - 2) << 20.
+constexpr std::uint32_t kInfoGroup = 1u, kInfoRow = 2u, kInfoRepeat = 4u;
 
 struct Head {
     bool gh, rh;     // first element of its (window, dst) group / of its row
@@ -643,30 +680,37 @@ __global__ void __launch_bounds__(kThreads) tile_count_kernel(TileArgs a) {
     __shared__ std::uint32_t hist[8 * kMaxS + 33];
     const unsigned t = blockIdx.x;
     const unsigned nb = num_bins(a.S);
-    if (t >= a.firstTile[a.SW]) {  // past the last tile: empty columns of the scan
+    // both loads before the branch (tileInfo past the last tile is unused)
+    const std::uint32_t numTiles = a.firstTile[a.SW];
+    const TileInfo ti = a.tileInfo[t];
+    if (t >= numTiles) {  // past the last tile: empty columns of the scan
         for (unsigned b = threadIdx.x; b < nb; b += kThreads) a.counters[static_cast<std::uint64_t>(b) * a.TM + t] = 0;
         return;
     }
     for (unsigned b = threadIdx.x; b < nb; b += kThreads) hist[b] = 0;
-    const TileRange r = load_tile<kThreads>(a, t, tk);
+    const TileRange r = load_tile<kThreads>(a, t, ti, tk);
     const std::uint32_t loMask = (1u << a.loBits) - 1u;
     const unsigned rowBin = 8 * a.S, groupBin = 8 * a.S + 32;
     std::uint32_t groups = 0, rows = 0;
     bool degErr = false, occErr = false;
     for (unsigned i = threadIdx.x; i < r.n; i += kThreads) {
-        const Head h = head_at<false>(tk, i, r.avail);
+        const Head h = head_at<true>(tk, i, r.avail);
+        const unsigned deg = h.gh ? min(h.count, 8u) : 1u;
+        const unsigned wi = (static_cast<std::uint32_t>(tk.key[i + 1]) & loMask) >> 3;
+        const bool rep = h.rh && h.occ >= 2 && h.occ <= kMaxS;
         if (h.gh) {
             degErr |= h.count > 8;
-            const unsigned deg = min(h.count, 8u);
-            const unsigned wi = (static_cast<std::uint32_t>(tk.key[i + 1]) & loMask) >> 3;
             atomicAdd(&hist[wi * 8 + deg - 1], 1u);
             ++groups;
         }
         if (h.rh) {
             ++rows;
-            if (h.occ > kMaxS) occErr = true;
-            else if (h.occ >= 2) atomicAdd(&hist[rowBin + h.occ - 1], 1u);
+            occErr |= h.occ > kMaxS;
+            if (rep) atomicAdd(&hist[rowBin + h.occ - 1], 1u);
         }
+        a.info[r.start + i] = (h.gh ? kInfoGroup : 0u) | (h.rh ? kInfoRow : 0u) | (rep ? kInfoRepeat : 0u) |
+                              (deg << 3) | ((h.gh ? h.bits : 0u) << 7) | (min(wi, 31u) << 15) |
+                              ((rep ? h.occ - 2 : 0u) << 20);
     }
     if (degErr) atomicMax(a.err, static_cast<std::uint32_t>(TCC_DEVERR_DEGREE));
     if (occErr) atomicMax(a.err, static_cast<std::uint32_t>(TCC_DEVERR_OCCURRENCE));
@@ -726,22 +770,38 @@ __global__ void super_window_meta_kernel(const std::uint32_t* __restrict__ P, st
 // assignGroupLocationsKernel (:292-376), fillValidTileRowSlotsKernel
 // (:1003-1048), the tile bitmaps (:430-455, one byte per tile row), the
 // super-window rows (:459-681) and the repeat cache (:699-895), per segment
-// tile.  Wave w ranks elements [512 w, 512 w + 512) of the tile in 8 rounds
-// of 64, so ranks follow element order.
+// tile, from the head facts of the count pass.  Wave w ranks elements
+// [512 w, 512 w + 512) of the tile in 8 rounds of 64, so ranks follow
+// element order.
 template <typename K>
 __global__ void __launch_bounds__(kEmitThreads) tile_emit_kernel(TileArgs a) {
-    __shared__ TileKeys<K> tk;
     __shared__ std::uint32_t cntG[kEmitWaves][8 * kMaxS];
     __shared__ std::uint32_t cntO[kEmitWaves][kOccBins + 1];
-    __shared__ std::uint32_t info[kTile];          // head facts of element i
     __shared__ std::uint64_t baseG[8 * kMaxS];   // tile-row index of the bin's first head in this tile
     __shared__ std::uint32_t baseO[kOccBins + 1];  // cache slot of the bin's first repeated row in this tile
     __shared__ std::uint32_t rowsW[kEmitWaves];
     const unsigned t = blockIdx.x;
-    if (t >= a.firstTile[a.SW]) return;
-    const TileRange r = load_tile<kEmitThreads>(a, t, tk);
-    const std::uint32_t s = r.s;
-    const std::uint32_t t0 = a.firstTile[s];
+    const std::uint32_t numTiles = a.firstTile[a.SW];
+    const TileInfo ti = a.tileInfo[t];
+    if (t >= numTiles) return;
+    const std::uint32_t s = ti.s, t0 = ti.firstTile;
+    const std::uint32_t segEnd = min(ti.segEnd, a.n);
+    const std::uint32_t start = min(ti.start, segEnd);
+    const std::uint32_t n = min(kTile, segEnd - start);
+    const unsigned lane = __lane_id();
+    const unsigned wave = threadIdx.x / kWave;
+    // the wave's head facts and keys, loaded first
+    std::uint32_t f[kEmitRounds];
+    K key[kEmitRounds];
+#pragma unroll
+    for (unsigned r0 = 0; r0 < kEmitRounds; ++r0) {
+        const unsigned i = wave * kEmitSpan + r0 * kWave + lane;
+        const std::uint32_t e = start + min(i, n - 1);
+        f[r0] = a.info[e];
+        if constexpr (sizeof(K) == 4) key[r0] = a.keys32[e];
+        else key[r0] = a.el[e] & a.keyMask;
+        if (i >= n) f[r0] = 0;
+    }
     const unsigned groupBins = 8 * a.S;
     for (unsigned b = threadIdx.x; b < groupBins; b += kEmitThreads) {
         // bin b = (wi, degree - 1): the window's degree-bucket base, plus the
@@ -765,40 +825,28 @@ __global__ void __launch_bounds__(kEmitThreads) tile_emit_kernel(TileArgs a) {
     const std::uint32_t off0 = a.counters[rowBin + t0] - a.counters[rowBin];
     __syncthreads();
 
-    const unsigned lane = __lane_id();
-    const unsigned wave = threadIdx.x / kWave;
     const std::uint64_t lt = lanemask_lt();
-    const std::uint32_t loMask = (1u << a.loBits) - 1u;
-    // info[i] = gh | rh << 1 | rep << 2 | degree << 3 | bits << 7 | wi << 15 |
-    // (occ - 2) << 20, for the tile's elements
-    for (unsigned i = threadIdx.x; i < r.n; i += kEmitThreads) {
-        const Head h = head_at<true>(tk, i, r.avail);
-        const unsigned deg = h.gh ? min(h.count, 8u) : 1u;
-        const bool rep = h.rh && h.occ >= 2 && h.occ <= kMaxS;
-        const unsigned wi = (static_cast<std::uint32_t>(tk.key[i + 1]) & loMask) >> 3;
-        info[i] = (h.gh ? 1u : 0u) | (h.rh ? 2u : 0u) | (rep ? 4u : 0u) | (deg << 3) |
-                     ((h.gh ? h.bits : 0u) << 7) | (min(wi, 31u) << 15) | ((rep ? h.occ - 2 : 0u) << 20);
-    }
-    __syncthreads();
     // ranks per round: group rank | occurrence rank << 10 | rows of the wave
     // up to and including the element << 20 (ranks within the wave)
     std::uint32_t ranks[kEmitRounds];
     std::uint32_t rowRun = 0;
 #pragma unroll
     for (unsigned r0 = 0; r0 < kEmitRounds; ++r0) {
-        const unsigned i = wave * kEmitSpan + r0 * kWave + lane;
-        const std::uint32_t f = i < r.n ? info[i] : 0u;
-        const bool gh = f & 1u, rh = f & 2u, rep = f & 4u;
-        const unsigned gbin = gh ? ((f >> 15) & 31u) * 8 + ((f >> 3) & 15u) - 1 : 0u;
+        const std::uint32_t fr = f[r0];
+        const bool gh = fr & kInfoGroup, rh = fr & kInfoRow, rep = fr & kInfoRepeat;
+        const unsigned gbin = gh ? ((fr >> 15) & 31u) * 8 + ((fr >> 3) & 15u) - 1 : 0u;
         const std::uint64_t pg = match_peers<8>(gbin, gh);
         const std::uint32_t bg = cntG[wave][gbin];
         const std::uint32_t rg = bg + static_cast<std::uint32_t>(__popcll(pg & lt));
         if (gh && (pg & lt) == 0) cntG[wave][gbin] = bg + static_cast<std::uint32_t>(__popcll(pg));
-        const unsigned obin = (f >> 20) & 31u;
-        const std::uint64_t po = match_peers<5>(obin, rep);
-        const std::uint32_t bo = cntO[wave][obin];
-        const std::uint32_t ro = bo + static_cast<std::uint32_t>(__popcll(po & lt));
-        if (rep && (po & lt) == 0) cntO[wave][obin] = bo + static_cast<std::uint32_t>(__popcll(po));
+        std::uint32_t ro = 0;
+        if (__ballot(rep)) {  // repeated rows are rare: most rounds skip this
+            const unsigned obin = (fr >> 20) & 31u;
+            const std::uint64_t po = match_peers<5>(obin, rep);
+            const std::uint32_t bo = cntO[wave][obin];
+            ro = bo + static_cast<std::uint32_t>(__popcll(po & lt));
+            if (rep && (po & lt) == 0) cntO[wave][obin] = bo + static_cast<std::uint32_t>(__popcll(po));
+        }
         const std::uint64_t rb = __ballot(rh);
         const std::uint32_t rowsAt = rowRun + static_cast<std::uint32_t>(__popcll(rb & lt)) + (rh ? 1u : 0u);
         rowRun += static_cast<std::uint32_t>(__popcll(rb));
@@ -827,28 +875,26 @@ __global__ void __launch_bounds__(kEmitThreads) tile_emit_kernel(TileArgs a) {
     for (unsigned w = 0; w < wave; ++w) rowOff += rowsW[w];
 #pragma unroll
     for (unsigned r0 = 0; r0 < kEmitRounds; ++r0) {
-        const unsigned i = wave * kEmitSpan + r0 * kWave + lane;
-        if (i >= r.n) continue;
-        const std::uint32_t f = info[i];
-        if ((f & 3u) == 0) continue;
+        const std::uint32_t fr = f[r0];
+        if ((fr & (kInfoGroup | kInfoRow)) == 0) continue;
         const std::uint32_t u = rowOff + (ranks[r0] >> 20) - 1;  // this element's row
         const std::uint32_t slot = u - off0;
-        const unsigned wi = (f >> 15) & 31u;
-        if ((f & 1u) && wi < a.S) {
+        const unsigned wi = (fr >> 15) & 31u;
+        if ((fr & kInfoGroup) && wi < a.S) {
             // tiles of a window are consecutive: tile-row index = 8 x the
             // window's first tile + the rank among its groups
-            const unsigned gbin = wi * 8 + ((f >> 3) & 15u) - 1;
+            const unsigned gbin = wi * 8 + ((fr >> 3) & 15u) - 1;
             const std::uint64_t loc = baseG[gbin] + cntG[wave][gbin] + (ranks[r0] & 0x3FFu);
             if (loc < 8ull * a.cap) {
                 a.tileRowSlot[loc] = slot;
-                a.tileBytes[loc] = static_cast<std::uint8_t>((f >> 7) & 0xFFu);
+                a.tileBytes[loc] = static_cast<std::uint8_t>((fr >> 7) & 0xFFu);
             }
         }
-        if ((f & 2u) && u < a.cap) {
-            a.superWindowRows[u] = static_cast<std::uint32_t>(tk.key[i + 1] >> a.loBits);
+        if ((fr & kInfoRow) && u < a.cap) {
+            a.superWindowRows[u] = static_cast<std::uint32_t>(key[r0] >> a.loBits);
             std::uint8_t cs8 = static_cast<std::uint8_t>(TCC_SWTCF_INVALID_CACHE_SLOT);
-            if (f & 4u) {
-                const unsigned obin = (f >> 20) & 31u;
+            if (fr & kInfoRepeat) {
+                const unsigned obin = (fr >> 20) & 31u;
                 const std::uint32_t cs = baseO[obin] + cntO[wave][obin] + ((ranks[r0] >> 10) & 0x3FFu);
                 if (cs < kCache) {
                     cs8 = static_cast<std::uint8_t>(cs);
@@ -998,20 +1044,24 @@ int tcc_swtcf_convert(const std::uint32_t* dDst, const std::uint32_t* dSrc, std:
     TCC_HIP_CHECK(fill<std::uint32_t>(m->superWindowCachedRowSlot, static_cast<std::uint64_t>(SW) * kCache,
                                       TCC_SWTCF_INVALID_ROW_SLOT, st));
     TCC_HIP_CHECK(fill<std::uint32_t>(err, 1, 0u, st));
+    TCC_HIP_CHECK(fill<std::uint32_t>(unsorted, 1, 0u, st));
+    TCC_HIP_CHECK(fill<std::uint32_t>(c.segStart, static_cast<std::uint64_t>(SW) + 1, E, st));
 
     // 1. sort: the COO's checks and first histograms, the low digits (skipped
     // for a COO in (dst, src) order), then the sw digits.
     hipLaunchKernelGGL(input_pass_kernel, dim3(tiles), dim3(kThreads), 0, st, dDst, dSrc, E, plan.ep, plan.low[0],
-                       c.histLow, plan.top[0], c.histTop, tiles, c.tileFlags, err);
-    TCC_LAUNCH_CHECK();
-    hipLaunchKernelGGL(any_kernel, dim3(1), dim3(kThreads), 0, st, c.tileFlags, tiles, unsorted);
+                       c.histLow, plan.top[0], c.histTop, tiles, unsorted, err);
     TCC_LAUNCH_CHECK();
     std::uint64_t* bufs[2] = {c.elemA, c.elemB};
     int next = 0;
     const std::uint64_t* cur = nullptr;
-    auto scatter = [&](const Digit& dg, std::uint32_t* hist, int onlyUnsorted, int source) -> int {
-        TCC_HIP_CHECK(exclusive_scan(hist, hist, (1ull << dg.bits) * tiles, nullptr, c.temp, st));
-        ScatterArgs a{cur, bufs[next], dDst, dSrc, plan.ep, E, dg, hist, tiles, unsorted, onlyUnsorted, source};
+    const bool narrow = plan.ep.kb <= 31;  // keys fit u32 with room for the ~0 sentinel
+    auto scatter = [&](const Digit& dg, std::uint32_t* hist, int onlyUnsorted, int source, bool last) -> int {
+        TCC_HIP_CHECK(exclusive_scan(hist, hist, (1ull << dg.bits) * tiles, nullptr, c.temp, st,
+                                     onlyUnsorted ? unsorted : nullptr));
+        ScatterArgs a{cur, bufs[next], dDst, dSrc, plan.ep, E, dg, hist, tiles, unsorted, onlyUnsorted, source,
+                      last && narrow ? reinterpret_cast<std::uint32_t*>(bufs[next]) : nullptr,
+                      last ? c.segStart : nullptr, (1ull << plan.ep.kb) - 1ull};
         hipLaunchKernelGGL(elem_scatter_kernel, dim3(tiles), dim3(kThreads), 0, st, a);
         TCC_LAUNCH_CHECK();
         cur = bufs[next];
@@ -1024,29 +1074,35 @@ int tcc_swtcf_convert(const std::uint32_t* dDst, const std::uint32_t* dSrc, std:
                                tiles, unsorted, 1);
             TCC_LAUNCH_CHECK();
         }
-        if (int rc = scatter(plan.low[p], c.histLow, 1, p == 0 ? 1 : 0)) return rc;
+        if (int rc = scatter(plan.low[p], c.histLow, 1, p == 0 ? 1 : 0, false)) return rc;
     }
     for (std::size_t p = 0; p < plan.top.size(); ++p) {
         // pass 0's counts came from the input pass for a COO in order
         hipLaunchKernelGGL(elem_hist_kernel, dim3(tiles), dim3(kThreads), 0, st, cur, E, plan.top[p], c.histTop,
                            tiles, unsorted, p == 0 ? 1 : 0);
         TCC_LAUNCH_CHECK();
-        if (int rc = scatter(plan.top[p], c.histTop, 0, p == 0 ? 2 : 0)) return rc;
+        if (int rc = scatter(plan.top[p], c.histTop, 0, p == 0 ? 2 : 0, p + 1 == plan.top.size())) return rc;
     }
-    const std::uint64_t* sorted = cur;
+    const std::uint64_t* sorted = cur;  // u32 keys when narrow
 
     // 2. segments (super-windows) and their tiles
-    hipLaunchKernelGGL(segment_bounds_kernel, dim3(grid_for(E, kThreads)), dim3(kThreads), 0, st, sorted, E,
-                       plan.ep.kb, SW, c.segStart);
+    hipLaunchKernelGGL(segment_fix_kernel, dim3(1), dim3(kThreads), 0, st, c.segStart, SW);
     TCC_LAUNCH_CHECK();
     hipLaunchKernelGGL(segment_tiles_kernel, dim3(grid_for(SW, kThreads)), dim3(kThreads), 0, st, c.segStart, SW,
                        c.firstTile);
     TCC_LAUNCH_CHECK();
     TCC_HIP_CHECK(exclusive_scan(c.firstTile, c.firstTile, SW, c.firstTile + SW, c.temp, st));
+    hipLaunchKernelGGL(tile_info_kernel, dim3(grid_for(SW, kThreads)), dim3(kThreads), 0, st, c.segStart,
+                       c.firstTile, SW, c.tileInfo);
+    TCC_LAUNCH_CHECK();
     const std::uint32_t TM = static_cast<std::uint32_t>(segment_tiles_max(E, SW));
     const std::uint64_t nCounters = static_cast<std::uint64_t>(num_bins(S)) * TM;
     TileArgs ta{};
     ta.el = sorted;
+    ta.keys32 = reinterpret_cast<const std::uint32_t*>(sorted);
+    // head facts: after the u32 keys in the same buffer, or in the other one
+    ta.info = narrow ? reinterpret_cast<std::uint32_t*>(const_cast<std::uint64_t*>(sorted)) + E
+                     : reinterpret_cast<std::uint32_t*>(sorted == c.elemA ? c.elemB : c.elemA);
     ta.n = E;
     ta.cap = m->nnz;
     ta.keyMask = (1ull << plan.ep.kb) - 1ull;
@@ -1056,6 +1112,7 @@ int tcc_swtcf_convert(const std::uint32_t* dDst, const std::uint32_t* dSrc, std:
     ta.CW = CW;
     ta.segStart = c.segStart;
     ta.firstTile = c.firstTile;
+    ta.tileInfo = c.tileInfo;
     ta.counters = c.counters;
     ta.TM = TM;
     ta.err = err;
@@ -1069,7 +1126,6 @@ int tcc_swtcf_convert(const std::uint32_t* dDst, const std::uint32_t* dSrc, std:
     ta.cachedRowSlot = m->superWindowCachedRowSlot;
 
     // 3. counts, their scan, window and super-window bases
-    const bool narrow = plan.ep.kb <= 31;  // keys fit u32 with room for the ~0 sentinel
     if (narrow) hipLaunchKernelGGL(tile_count_kernel<std::uint32_t>, dim3(TM), dim3(kThreads), 0, st, ta);
     else hipLaunchKernelGGL(tile_count_kernel<std::uint64_t>, dim3(TM), dim3(kThreads), 0, st, ta);
     TCC_LAUNCH_CHECK();
