@@ -134,7 +134,8 @@ def roofline(flops, b_alg, ms, traffic, kernel):
          "arith_intensity": round(ai, 3), "bytes_alg_per_launch": b_alg, "flops_per_launch": flops,
          "roof": "min(157.3 TFLOP/s fp32, AI x 8 TB/s) (BASELINE.md)"}
     if bound == "mfma":
-        r["fp32"] = "fp32 FMA/MFMA peak 157.3 TFLOP/s; the kernels contract on the VALU (fp32 FMA)"
+        r["fp32"] = ("fp32 peak 157.3 TFLOP/s, BASELINE.md's roof for this metric; which unit each kernel uses "
+                     "(VALU fp32 FMA, fp32 MFMA, bf16 MFMA over split TF32) is in `kernel`")
     if traffic is not None:
         gbps = traffic["hbm_bytes_per_launch"] / t / 1e9
         r["dram"] = {"GBps": round(gbps, 1), "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),

@@ -65,14 +65,48 @@ def read_stats(path: str) -> list[dict]:
     return sorted(out, key=lambda r: -r["total_ms"])
 
 
-def sources_sha() -> dict:
-    """sha256[:16] of every kernel source: a traffic file holds only while they are unchanged."""
+def _sha(rel: str) -> str:
+    with open(os.path.join(ROOT, rel), "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()[:16]
+
+
+def kernel_sources(kernels) -> list[str]:
+    """The source files that define the given kernels (by the base name of
+    each key, as a __global__ function of tcc_amd/csrc/*.hip or *.hpp), with
+    every file they include from this repository, transitively."""
+    csrc = os.path.join(ROOT, "tcc_amd", "csrc")
+    texts = {f"tcc_amd/csrc/{n}": open(os.path.join(csrc, n)).read()
+             for n in sorted(os.listdir(csrc)) if n.endswith((".hip", ".hpp", ".cpp"))}
+    found = set()
+    for k in kernels:
+        base = re.split(r"[<(]", k, maxsplit=1)[0].strip()
+        pat = re.compile(r"__global__[^;{]*?\b" + re.escape(base) + r"\s*\(", re.S)
+        found |= {rel for rel, text in texts.items() if pat.search(text)}
+    todo, seen = sorted(found), set()
+    while todo:
+        rel = todo.pop()
+        if rel in seen:
+            continue
+        seen.add(rel)
+        text = texts.get(rel) or open(os.path.join(ROOT, rel)).read()
+        for inc in re.findall(r'#include\s+"([^"]+)"', text):
+            dep = os.path.normpath(os.path.join(os.path.dirname(rel), inc))
+            if os.path.exists(os.path.join(ROOT, dep)) and dep not in seen:
+                todo.append(dep)
+    return sorted(seen)
+
+
+def sources_sha(kernels=None) -> dict:
+    """sha256[:16] of the sources a traffic file depends on (the files that
+    define its kernels and what they include; every kernel source when
+    `kernels` is None): the file holds only while they are unchanged."""
+    if kernels is not None:
+        return {rel: _sha(rel) for rel in kernel_sources(kernels)}
     out = {}
     for d in ("tcc_amd/csrc", "include"):
         for name in sorted(os.listdir(os.path.join(ROOT, d))):
             if name.endswith((".hip", ".hpp", ".h", ".cpp")):
-                with open(os.path.join(ROOT, d, name), "rb") as f:
-                    out[f"{d}/{name}"] = hashlib.sha256(f.read()).hexdigest()[:16]
+                out[f"{d}/{name}"] = _sha(f"{d}/{name}")
     return out
 
 
@@ -183,7 +217,7 @@ def traffic_json(args) -> dict:
            "copy_calibration": {"bytes": 1 << 30, "fetch_kib": round(max(copy_f)), "write_kib": round(max(copy_w)),
                                 "fetch_scale": round(ff, 4), "write_scale": round(fw, 4)},
            "step_kernel_ms_rocprof": None if step_ms is None else round(step_ms, 6),
-           "command": args.command, "sources": sources_sha()}
+           "command": args.command, "sources": sources_sha(list(per))}
     if step_ms:
         out["dram_side_GBps"] = round(total / (step_ms * 1e-3) / 1e9, 1)
     return out

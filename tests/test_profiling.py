@@ -85,3 +85,13 @@ def test_counters_table_mfma_busy(tmp_path):
                     "--command", "cmd", "--out", str(out)])
     row = [ln for ln in out.read_text().splitlines() if ln.startswith("| `dense_tn_kernel<4>`")][0]
     assert row.endswith("| 0.500 | 0.250 |") and "| 2 |" in row
+
+
+def test_kernel_sources_follow_definitions_and_includes():
+    srcs = profiling.kernel_sources(["gather_kernel<4, (Src)2, true>", "hub_reduce_kernel"])
+    assert "tcc_amd/csrc/bcsr_spmm.hip" in srcs and "tcc_amd/csrc/hub_tiles.hip" in srcs
+    assert "tcc_amd/csrc/common.hpp" in srcs  # included by both
+    assert "tcc_amd/csrc/swtcf_convert.hip" not in srcs  # defines none of them
+    sha = profiling.sources_sha(["tile_emit_kernel<unsigned int>"])
+    assert list(sha) == profiling.kernel_sources(["tile_emit_kernel"])
+    assert "tcc_amd/csrc/swtcf_convert.hip" in sha and "tcc_amd/csrc/hub_tiles.hip" not in sha
