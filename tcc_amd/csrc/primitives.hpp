@@ -25,6 +25,30 @@ constexpr int kPrimRounds = 16;
 constexpr int kPrimTile = kPrimThreads * kPrimRounds;  // 4096
 constexpr int kWaveSpan = kWave * kPrimRounds;         // 1024
 
+// ------------------------------------------------------------------ loads
+
+// A lane's 16 rounds (element first + 64 r), every load issued before any
+// is used; elements at or past n read as 0.  (Loads under per-round bounds
+// branches were each waited for in turn.)
+template <typename T>
+__device__ __forceinline__ void prim_load(const T* __restrict__ p, std::uint64_t first, std::uint64_t n,
+                                          T (&v)[kPrimRounds]) {
+    if (n == 0) {  // nothing to read (an empty scan still writes its total)
+#pragma unroll
+        for (int r = 0; r < kPrimRounds; ++r) v[r] = T(0);
+        return;
+    }
+    const std::uint64_t last = n - 1;
+#pragma unroll
+    for (int r = 0; r < kPrimRounds; ++r) {
+        const std::uint64_t i = first + r * kWave;
+        v[r] = p[i < last ? i : last];
+    }
+#pragma unroll
+    for (int r = 0; r < kPrimRounds; ++r)
+        if (first + r * kWave >= n) v[r] = T(0);
+}
+
 // ------------------------------------------------------------------ scan
 
 __device__ __forceinline__ std::uint32_t wave_inclusive_scan(std::uint32_t v) {
@@ -47,12 +71,11 @@ __global__ void __launch_bounds__(kPrimThreads) scan_reduce_kernel(const std::ui
     const unsigned lane = __lane_id();
     const unsigned wave = threadIdx.x / kWave;
     const std::uint64_t base = static_cast<std::uint64_t>(blockIdx.x) * kPrimTile + wave * kWaveSpan;
+    std::uint32_t v[kPrimRounds];
+    prim_load(in, base + lane, n, v);
     std::uint32_t s = 0;
 #pragma unroll
-    for (int r = 0; r < kPrimRounds; ++r) {
-        const std::uint64_t i = base + r * kWave + lane;
-        if (i < n) s += in[i];
-    }
+    for (int r = 0; r < kPrimRounds; ++r) s += v[r];
 #pragma unroll
     for (int d = kWave / 2; d > 0; d >>= 1) s += __shfl_xor(s, d, kWave);
     if (lane == 0) waveSum[wave] = s;
@@ -78,11 +101,11 @@ __global__ void __launch_bounds__(kPrimThreads) scan_tiles_kernel(const std::uin
     const unsigned wave = threadIdx.x / kWave;
     const std::uint64_t base = static_cast<std::uint64_t>(blockIdx.x) * kPrimTile + wave * kWaveSpan;
     std::uint32_t pre[kPrimRounds];
+    prim_load(in, base + lane, n, pre);
     std::uint32_t carry = 0;
 #pragma unroll
     for (int r = 0; r < kPrimRounds; ++r) {
-        const std::uint64_t i = base + r * kWave + lane;
-        const std::uint32_t v = (i < n) ? in[i] : 0u;
+        const std::uint32_t v = pre[r];
         const std::uint32_t inc = wave_inclusive_scan(v);
         pre[r] = carry + inc - v;
         carry += __shfl(inc, kWave - 1, kWave);
@@ -155,11 +178,12 @@ __global__ void __launch_bounds__(kPrimThreads) radix_hist_kernel(const std::uin
     for (int i = threadIdx.x; i < kPrimWaves * kRadixBins; i += kPrimThreads) (&h[0][0])[i] = 0;
     __syncthreads();
     const std::uint64_t base = static_cast<std::uint64_t>(blockIdx.x) * kPrimTile + wave * kWaveSpan;
-#pragma unroll 4
+    std::uint64_t k[kPrimRounds];
+    prim_load(keys, base + lane, n, k);
+#pragma unroll
     for (int r = 0; r < kPrimRounds; ++r) {
-        const std::uint64_t i = base + r * kWave + lane;
-        if (i < n) {
-            const unsigned d = static_cast<unsigned>(keys[i] >> shift) & (kRadixBins - 1);
+        if (base + r * kWave + lane < n) {
+            const unsigned d = static_cast<unsigned>(k[r] >> shift) & (kRadixBins - 1);
             atomicAdd(&h[wave][d], 1u);
         }
     }
@@ -205,12 +229,12 @@ __global__ void __launch_bounds__(kPrimThreads) radix_scatter_kernel(const std::
     std::uint64_t k[kPrimRounds];
     std::uint32_t v[kPrimRounds];
     std::uint32_t rank[kPrimRounds];
+    prim_load(keysIn, base + lane, n, k);
+    if constexpr (PAYLOAD) prim_load(valsIn, base + lane, n, v);
 #pragma unroll
     for (int r = 0; r < kPrimRounds; ++r) {
         const std::uint64_t i = base + r * kWave + lane;
         const bool valid = i < n;
-        k[r] = valid ? keysIn[i] : 0ull;
-        if constexpr (PAYLOAD) v[r] = valid ? valsIn[i] : 0u;
         const unsigned d = static_cast<unsigned>(k[r] >> shift) & (kRadixBins - 1);
         const std::uint64_t peers = match_peers<kRadixBits>(d, valid);
         const std::uint32_t before = cnt[wave][d];
