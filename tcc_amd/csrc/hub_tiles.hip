@@ -461,13 +461,22 @@ __global__ void hub_rows_split_kernel(const float* __restrict__ X, std::uint32_t
     const std::uint64_t i = static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     const std::uint32_t cb = static_cast<std::uint32_t>(i / ldh), f = static_cast<std::uint32_t>(i % ldh);
     if (cb >= hubRows / kTile) return;
+    // the 16 rows' values loaded before any is used (clamped indices,
+    // zeroed after): loads under their bounds branches were each waited for
+    std::uint32_t src[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) src[k] = order[min(cb * kTile + k, hubCols > 0 ? hubCols - 1 : 0u)];
+    const std::uint32_t fc = min(f, F > 0 ? F - 1 : 0u);
+    float x[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) x[k] = X[static_cast<std::uint64_t>(src[k]) * F + fc];
     vu4 hi[2], lo[2];
 #pragma unroll
     for (int k = 0; k < 16; k += 2) {
         std::uint16_t h0 = 0, l0 = 0, h1 = 0, l1 = 0;
         const std::uint32_t r = cb * kTile + k;
-        if (f < F && r < hubCols) bf16_split(tf32_rna(X[static_cast<std::uint64_t>(order[r]) * F + f]), h0, l0);
-        if (f < F && r + 1 < hubCols) bf16_split(tf32_rna(X[static_cast<std::uint64_t>(order[r + 1]) * F + f]), h1, l1);
+        if (f < F && r < hubCols) bf16_split(tf32_rna(x[k]), h0, l0);
+        if (f < F && r + 1 < hubCols) bf16_split(tf32_rna(x[k + 1]), h1, l1);
         hi[k / 8][(k % 8) / 2] = static_cast<std::uint32_t>(h0) | static_cast<std::uint32_t>(h1) << 16;
         lo[k / 8][(k % 8) / 2] = static_cast<std::uint32_t>(l0) | static_cast<std::uint32_t>(l1) << 16;
     }
@@ -482,18 +491,19 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 template <int G>
 struct SplitOperands {
-    vu4 a[G];      // lane group q < 2: ah of k = 8q..8q+7; q >= 2: al of k = 8(q-2)..
-    vu4 bh[4];     // xh of k = 8(q%2)..8(q%2)+7, feature f0 + 16u + l%16
-    vu4 bl[4];     // xl of the same k and feature
+    vu4 a[G];  // lane group q < 2: ah of k = 8q..8q+7; q >= 2: al of k = 8(q-2)..
+    vu4 b[4];  // N tile u, feature f0 + 16u + l%16: q < 2 xh of k-half q, q >= 2 xl of k-half q-2
 };
 
 // As hub_tiles_kernel, over split tiles.  Per tile and 16 features, two
 // K = 32 MFMAs over k' = (lane group q, element e): A' = [ah | al] (lane
 // groups 0-1 ah, 2-3 al, of k = 8(q%2) + e) against B = [xh ; xh], then
-// against [xl ; xl]: ah·xh + al·xh, then ah·xl + al·xl.  Every A lane
-// reads its own 16 bytes of the tile (no lane duplicates another), two
-// 16-byte loads of Xs per N tile.  D of N tile u holds rows 4q + v, feature
-// f0 + 16u + (l%16).
+// against [xl ; xl]: ah·xh + al·xh, then ah·xl + al·xl.  Every lane reads
+// its own 16 bytes of the tile and of Xs: lanes 0-31 the xh and lanes 32-63
+// the xl of their k-half, and v_permlane32_swap of that register with a
+// copy of itself gives [xh ; xh] in one and [xl ; xl] in the other (lanes
+// 32-63 of the first take lanes 0-31 of the second, and the reverse; checked
+// on the GPU).  D of N tile u holds rows 4q + v, feature f0 + 16u + (l%16).
 template <int G, int NS>
 __global__ void __launch_bounds__(kThreads) hub_tiles_split_kernel(TileArgs a) {
     const unsigned lane = __lane_id();
@@ -508,8 +518,9 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_split_kernel(TileArgs a) {
     const unsigned li = lane & 15u, lq = lane >> 4;
     const std::uint32_t last = p1 - 1;
     const int cols = static_cast<int>(a.stepCol[min(p0 + lane, last)]);
-    // Xs: 16 hi then 16 lo bf16 per (column block, feature); this lane's k-half
-    const char* xb = reinterpret_cast<const char*>(a.Xh) + (static_cast<std::uint64_t>(f0 + li) * 64 + (lq & 1u) * 16);
+    // Xs: 16 hi then 16 lo bf16 per (column block, feature); lane group q
+    // reads bytes 16q..16q+15 (q < 2: xh of k-half q; q >= 2: xl of k-half q-2)
+    const char* xb = reinterpret_cast<const char*>(a.Xh) + (static_cast<std::uint64_t>(f0 + li) * 64 + lq * 16);
     const std::uint64_t cbStride = static_cast<std::uint64_t>(a.ldh) * 64;
     // tile: 256 hi then 256 lo bf16, row-major; this lane's row li, k-half, hi or lo
     const char* ab = reinterpret_cast<const char*>(a.tileVals) + (lq >> 1) * 512 + li * 32 + (lq & 1u) * 16;
@@ -522,10 +533,7 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_split_kernel(TileArgs a) {
         for (int j = 0; j < G; ++j) o.a[j] = load_global<vu4>(ab + (static_cast<std::uint64_t>(pa) * G + j) * (kTileVals * 4));
         const char* rb = xb + col * cbStride;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            o.bh[u] = load_global<vu4>(rb + u * 16 * 64);
-            o.bl[u] = load_global<vu4>(rb + u * 16 * 64 + 32);
-        }
+        for (int u = 0; u < 4; ++u) o.b[u] = load_global<vu4>(rb + u * 16 * 64);
     };
     f32x4 acc[G][4];
 #pragma unroll
@@ -534,15 +542,21 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_split_kernel(TileArgs a) {
         for (int u = 0; u < 4; ++u) acc[j][u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     auto mma = [&](const SplitOperands<G>& o) {
 #pragma unroll
-        for (int j = 0; j < G; ++j)
+        for (int u = 0; u < 4; ++u) {
+            vu4 bh, bl;  // [xh ; xh] and [xl ; xl]
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const bf16x8 aj = __builtin_bit_cast(bf16x8, o.a[j]);
-                acc[j][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aj, __builtin_bit_cast(bf16x8, o.bh[u]), acc[j][u], 0,
-                                                                    0, 0);
-                acc[j][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aj, __builtin_bit_cast(bf16x8, o.bl[u]), acc[j][u], 0,
-                                                                    0, 0);
+            for (int r = 0; r < 4; ++r) {
+                const auto sw = __builtin_amdgcn_permlane32_swap(o.b[u][r], o.b[u][r], false, false);
+                bh[r] = sw[0];
+                bl[r] = sw[1];
             }
+#pragma unroll
+            for (int j = 0; j < G; ++j) {
+                const bf16x8 aj = __builtin_bit_cast(bf16x8, o.a[j]);
+                acc[j][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aj, __builtin_bit_cast(bf16x8, bh), acc[j][u], 0, 0, 0);
+                acc[j][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aj, __builtin_bit_cast(bf16x8, bl), acc[j][u], 0, 0, 0);
+            }
+        }
     };
 
     SplitOperands<G> ring[NS];
