@@ -144,7 +144,9 @@ inline Carve carve(char* base, std::uint64_t E, std::uint64_t CW, std::uint64_t 
         off = align_up(off + bytes);
         return p;
     };
-    const std::uint64_t hist = static_cast<std::uint64_t>(kMaxBins) * sort_tiles(E);
+    // digit counts per sort tile, or (the 32-bit flow's segmented passes)
+    // per segment tile, with room for the scan's total
+    const std::uint64_t hist = static_cast<std::uint64_t>(kMaxBins) * segment_tiles_max(E, SW) + 1;
     const std::uint64_t cnt = static_cast<std::uint64_t>(num_bins(S)) * segment_tiles_max(E, SW) + 1;
     c.elemA = reinterpret_cast<std::uint64_t*>(take(8 * E));
     c.elemB = reinterpret_cast<std::uint64_t*>(take(8 * E));
@@ -247,7 +249,7 @@ __global__ void __launch_bounds__(kThreads) input_pass_kernel(const std::uint32_
             srcBad |= s >= ep.cols;
             dstBad |= ep.rows != 0 && d >= ep.rows;
             const std::uint64_t e = make_elem(d, s, ep);
-            atomicAdd(&hl[wave][digit_of(e, low)], 1u);
+            if (low.bits) atomicAdd(&hl[wave][digit_of(e, low)], 1u);
             atomicAdd(&ht[wave][digit_of(e, top)], 1u);
         }
     }
@@ -262,7 +264,7 @@ __global__ void __launch_bounds__(kThreads) input_pass_kernel(const std::uint32_
     if (threadIdx.x == 0 && (waveOut[0] | waveOut[1] | waveOut[2] | waveOut[3]) &&
         __hip_atomic_load(unsorted, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u)
         atomicOr(unsorted, 1u);
-    for (unsigned b = threadIdx.x; b < (1u << low.bits); b += kThreads) {
+    for (unsigned b = threadIdx.x; low.bits && b < (1u << low.bits); b += kThreads) {
         std::uint32_t t = 0;
         for (unsigned w = 0; w < kWaves; ++w) t += hl[w][b];
         histLow[static_cast<std::uint64_t>(b) * tiles + blockIdx.x] = t;
@@ -274,9 +276,11 @@ __global__ void __launch_bounds__(kThreads) input_pass_kernel(const std::uint32_
     }
 }
 
-// Per-tile digit counts of an element array.  With onlyUnsorted, returns at
-// once when the input pass found the COO in (dst, src) order.
-__global__ void __launch_bounds__(kThreads) elem_hist_kernel(const std::uint64_t* __restrict__ in, std::uint32_t n,
+// Per-tile digit counts of an element array (u64 elements, or u32 ones of
+// the 32-bit flow).  With onlyUnsorted, returns at once when the input pass
+// found the COO in (dst, src) order.
+template <typename T>
+__global__ void __launch_bounds__(kThreads) elem_hist_kernel(const T* __restrict__ in, std::uint32_t n,
                                                             Digit dg, std::uint32_t* __restrict__ hist,
                                                             unsigned tiles, const std::uint32_t* __restrict__ unsorted,
                                                             int onlyUnsorted) {
@@ -287,12 +291,12 @@ __global__ void __launch_bounds__(kThreads) elem_hist_kernel(const std::uint64_t
     for (unsigned i = threadIdx.x; i < kWaves * kMaxBins; i += kThreads) (&h[0][0])[i] = 0;
     __syncthreads();
     const std::uint64_t base = static_cast<std::uint64_t>(blockIdx.x) * kTile + wave * kSpan + lane;
-    std::uint64_t k[kRounds];
+    T k[kRounds];
 #pragma unroll
     for (unsigned r = 0; r < kRounds; ++r) k[r] = in[clamp_to(base + r * kWave, n - 1)];
 #pragma unroll
     for (unsigned r = 0; r < kRounds; ++r)
-        if (base + r * kWave < n) atomicAdd(&h[wave][digit_of(k[r], dg)], 1u);
+        if (base + r * kWave < n) atomicAdd(&h[wave][digit_of(static_cast<std::uint64_t>(k[r]), dg)], 1u);
     __syncthreads();
     for (unsigned b = threadIdx.x; b < (1u << dg.bits); b += kThreads) {
         std::uint32_t t = 0;
@@ -313,23 +317,51 @@ struct ScatterArgs {
     unsigned tiles;
     const std::uint32_t* unsorted;
     int onlyUnsorted;  // return at once for a COO in (dst, src) order
-    int source;        // 0: `in`; 1: the COO; 2: the COO if it is in order, else `in`
-    // last pass only (else null): the low kb bits of each element go to
-    // out32 instead of `out` (keys of at most 31 bits), and segStart[sw]
-    // takes the smallest position of the elements that may start super-window
-    // sw (atomicMin; it holds n before the pass)
+    // 0: `in`; 1: the COO; 2: the COO if it is in order, else `in`; 3: the
+    // u32 elements `in32` of the 32-bit flow's first pass (sw >> w0 << kb |
+    // key), sw's low w0 bits being that pass's digit, which its output order
+    // gives: the digit run [d0Start[d], d0Start[d + 1]) holding the position
+    int source;
+    // out32 (else null): u32 output instead of `out`; outMode 1 writes the
+    // key (the low kb bits, at most 31), outMode 2 writes sw >> w0 << kb | key
     std::uint32_t* out32;
+    int outMode;
+    // last pass only (else null): segStart[sw] takes the smallest position
+    // of the elements that may start super-window sw (atomicMin; it holds n
+    // before the pass)
     std::uint32_t* segStart;
     std::uint64_t keyMask;
+    const std::uint32_t* in32;
+    const std::uint32_t* d0Scan;  // source 3: the first pass's scanned counts, d0Start[d] = d0Scan[d * tiles]
+    unsigned w0;                  // bits of the first pass's digit
 };
 
 // The 16 rounds' elements of a lane (element first + 64 r), all loads
 // issued before any is used: indices past the end are clamped to the last
 // element (those lanes take no part in what follows).
 __device__ __forceinline__ void load_elems(const ScatterArgs& a, bool coo, std::uint64_t first,
-                                           std::uint64_t (&k)[kRounds]) {
+                                           std::uint64_t (&k)[kRounds], const std::uint32_t* d0s) {
     const std::uint64_t last = a.n - 1;
-    if (coo) {
+    if (a.source == 3) {
+        std::uint32_t e[kRounds];
+#pragma unroll
+        for (unsigned r = 0; r < kRounds; ++r) e[r] = a.in32[clamp_to(first + r * kWave, last)];
+        const unsigned kb = a.ep.kb;
+        const std::uint32_t keyMask = static_cast<std::uint32_t>(a.keyMask);
+#pragma unroll
+        for (unsigned r = 0; r < kRounds; ++r) {
+            // the digit run holding this position: the last d with d0Start[d] <= i
+            const std::uint32_t i = static_cast<std::uint32_t>(clamp_to(first + r * kWave, last));
+            unsigned lo = 0, hi = 1u << a.w0;
+            while (hi - lo > 1) {
+                const unsigned mid = (lo + hi) / 2;
+                if (d0s[mid] <= i) lo = mid;
+                else hi = mid;
+            }
+            const std::uint64_t sw = (static_cast<std::uint64_t>(e[r] >> kb) << a.w0) | lo;
+            k[r] = (sw << kb) | (e[r] & keyMask);
+        }
+    } else if (coo) {
         std::uint32_t d[kRounds], s[kRounds];
 #pragma unroll
         for (unsigned r = 0; r < kRounds; ++r) {
@@ -357,8 +389,14 @@ __global__ void __launch_bounds__(kThreads) elem_scatter_kernel(ScatterArgs a) {
     __shared__ std::uint32_t tstart[kMaxBins];  // start of the digit's run in the tile
     __shared__ std::uint32_t waveSum[kWaves];
     __shared__ std::uint64_t stage[kTile];
+    __shared__ std::uint32_t d0s[(1u << kMaxTopDigit) + 1];
     if (a.onlyUnsorted && *a.unsorted == 0u) return;
     const bool coo = a.source == 1 || (a.source == 2 && *a.unsorted == 0u);
+    if (a.source == 3) {
+        for (unsigned d = threadIdx.x; d < (1u << a.w0); d += kThreads)
+            d0s[d] = a.d0Scan[static_cast<std::uint64_t>(d) * a.tiles];
+        __syncthreads();
+    }
     const unsigned lane = __lane_id();
     const unsigned wave = threadIdx.x / kWave;
     const unsigned bins = 1u << a.dg.bits;
@@ -369,7 +407,7 @@ __global__ void __launch_bounds__(kThreads) elem_scatter_kernel(ScatterArgs a) {
     const std::uint64_t lt = lanemask_lt();
     std::uint64_t k[kRounds];
     std::uint32_t rank[kRounds];
-    load_elems(a, coo, base + lane, k);
+    load_elems(a, coo, base + lane, k, d0s);
 #pragma unroll
     for (unsigned r = 0; r < kRounds; ++r) {
         const std::uint64_t i = base + r * kWave + lane;
@@ -428,8 +466,10 @@ __global__ void __launch_bounds__(kThreads) elem_scatter_kernel(ScatterArgs a) {
             const std::uint64_t key = stage[p];
             const unsigned d = digit_of(key, a.dg);
             const std::uint32_t pos = gbase[d] + (p - tstart[d]);
-            if (a.out32) a.out32[pos] = static_cast<std::uint32_t>(key & a.keyMask);
-            else a.out[pos] = key;
+            if (!a.out32) a.out[pos] = key;
+            else if (a.outMode == 1) a.out32[pos] = static_cast<std::uint32_t>(key & a.keyMask);
+            else
+                a.out32[pos] = static_cast<std::uint32_t>(((key >> (a.ep.kb + a.w0)) << a.ep.kb) | (key & a.keyMask));
             if (a.segStart) {
                 // a digit's run in the tile is in (sw, key) order, the earlier
                 // passes having sorted every lower bit: only its first element
@@ -481,9 +521,163 @@ __global__ void tile_info_kernel(const std::uint32_t* __restrict__ segStart,
     for (std::uint32_t t = t0; t < t1; ++t) info[t] = TileInfo{s, b + (t - t0) * kTile, e, t0};
 }
 
+// ---------------------------------------------------------------- segmented passes
+
+// The 32-bit flow partitions by sw first and then, for a COO out of (dst,
+// src) order, sorts each super-window's keys: stable LSD passes over u32
+// keys whose tiles are the segment tiles, so that a key's position is its
+// segment's start + the segment's keys of smaller digits + the same digit's
+// keys in the segment's earlier tiles + its rank in the tile.
+struct SegPassArgs {
+    const std::uint32_t* in;
+    std::uint32_t* out;
+    const TileInfo* tileInfo;
+    const std::uint32_t* firstTile;
+    const std::uint32_t* segStart;
+    std::uint32_t n, SW, TM;
+    Digit dg;
+    std::uint32_t* counters;  // [bins][TM] + 1: per-tile digit counts, scanned between the two kernels
+    const std::uint32_t* unsorted;
+};
+
+// A segment tile's keys, 16 rounds a wave (indices clamped into the tile).
+__device__ __forceinline__ void load_seg_keys(const std::uint32_t* __restrict__ in, std::uint32_t start,
+                                              std::uint32_t n, unsigned wave, unsigned lane,
+                                              std::uint32_t (&k)[kRounds]) {
+    const std::uint32_t last = start + (n > 0 ? n - 1 : 0u);
+#pragma unroll
+    for (unsigned r = 0; r < kRounds; ++r) k[r] = in[min(start + wave * kSpan + r * kWave + lane, last)];
+}
+
+__global__ void __launch_bounds__(kThreads) seg_hist_kernel(SegPassArgs a) {
+    __shared__ std::uint32_t h[kWaves][kMaxBins];
+    if (*a.unsorted == 0u) return;
+    const unsigned t = blockIdx.x, bins = 1u << a.dg.bits;
+    const std::uint32_t numTiles = a.firstTile[a.SW];
+    const TileInfo ti = a.tileInfo[t];
+    if (t >= numTiles) {  // past the last tile: empty columns of the scan
+        for (unsigned b = threadIdx.x; b < bins; b += kThreads) a.counters[static_cast<std::uint64_t>(b) * a.TM + t] = 0;
+        return;
+    }
+    const unsigned lane = __lane_id(), wave = threadIdx.x / kWave;
+    for (unsigned i = threadIdx.x; i < kWaves * kMaxBins; i += kThreads) (&h[0][0])[i] = 0;
+    __syncthreads();
+    const std::uint32_t segEnd = min(ti.segEnd, a.n), start = min(ti.start, segEnd);
+    const std::uint32_t n = min(kTile, segEnd - start);
+    std::uint32_t k[kRounds];
+    load_seg_keys(a.in, start, n, wave, lane, k);
+#pragma unroll
+    for (unsigned r = 0; r < kRounds; ++r)
+        if (wave * kSpan + r * kWave + lane < n) atomicAdd(&h[wave][digit_of(k[r], a.dg)], 1u);
+    __syncthreads();
+    for (unsigned b = threadIdx.x; b < bins; b += kThreads) {
+        std::uint32_t c = 0;
+        for (unsigned w = 0; w < kWaves; ++w) c += h[w][b];
+        a.counters[static_cast<std::uint64_t>(b) * a.TM + t] = c;
+    }
+}
+
+// Exclusive scan over the block of one value per thread (thread order).
+__device__ __forceinline__ std::uint32_t block_exclusive_scan(std::uint32_t v, std::uint32_t* waveSum) {
+    const unsigned lane = __lane_id(), wave = threadIdx.x / kWave;
+    std::uint32_t inc = v;
+#pragma unroll
+    for (unsigned o = 1; o < kWave; o <<= 1) {
+        const std::uint32_t y = __shfl_up(inc, o, kWave);
+        if (lane >= o) inc += y;
+    }
+    if (lane == kWave - 1) waveSum[wave] = inc;
+    __syncthreads();
+    std::uint32_t off = inc - v;
+    for (unsigned w = 0; w < wave; ++w) off += waveSum[w];
+    __syncthreads();  // waveSum free for the next scan
+    return off;
+}
+
+__global__ void __launch_bounds__(kThreads) seg_scatter_kernel(SegPassArgs a) {
+    __shared__ std::uint32_t cnt[kWaves][kMaxBins];
+    __shared__ std::uint32_t gbase[kMaxBins];   // output position of the digit's first key of this tile
+    __shared__ std::uint32_t tstart[kMaxBins];  // start of the digit's run in the staged tile
+    __shared__ std::uint32_t waveSum[kWaves];
+    __shared__ std::uint32_t stage[kTile];
+    if (*a.unsorted == 0u) return;
+    const unsigned t = blockIdx.x, bins = 1u << a.dg.bits;
+    const std::uint32_t numTiles = a.firstTile[a.SW];
+    const TileInfo ti = a.tileInfo[t];
+    if (t >= numTiles) return;
+    const unsigned lane = __lane_id(), wave = threadIdx.x / kWave;
+    const std::uint32_t s = ti.s, t0 = ti.firstTile;
+    const std::uint32_t t1 = a.firstTile[s + 1], segBegin = a.segStart[s];
+    const std::uint32_t segEnd = min(ti.segEnd, a.n), start = min(ti.start, segEnd);
+    const std::uint32_t n = min(kTile, segEnd - start);
+    for (unsigned i = threadIdx.x; i < kWaves * kMaxBins; i += kThreads) (&cnt[0][0])[i] = 0;
+    __syncthreads();
+    std::uint32_t k[kRounds], rank[kRounds];
+    load_seg_keys(a.in, start, n, wave, lane, k);
+    const std::uint64_t lt = lanemask_lt();
+#pragma unroll
+    for (unsigned r = 0; r < kRounds; ++r) {
+        const bool valid = wave * kSpan + r * kWave + lane < n;
+        const unsigned d = digit_of(k[r], a.dg);
+        const std::uint64_t peers = match_peers_bits(d, valid, a.dg.bits);
+        const std::uint32_t before = cnt[wave][d];
+        rank[r] = before + static_cast<std::uint32_t>(__popcll(peers & lt));
+        if (valid && (peers & lt) == 0) cnt[wave][d] = before + static_cast<std::uint32_t>(__popcll(peers));
+    }
+    __syncthreads();
+    // thread j holds digits 2j and 2j + 1: per-wave offsets within the
+    // digit's run, the runs' starts in the tile, and the digits' bases in the
+    // segment (its keys of smaller digits + this digit's in earlier tiles)
+    std::uint32_t tot[2] = {0, 0}, segTot[2] = {0, 0}, earlier[2] = {0, 0};
+#pragma unroll
+    for (unsigned q = 0; q < 2; ++q) {
+        const unsigned d = 2 * threadIdx.x + q;
+        if (d < bins) {
+            for (unsigned w = 0; w < kWaves; ++w) {
+                const std::uint32_t c = cnt[w][d];
+                cnt[w][d] = tot[q];
+                tot[q] += c;
+            }
+            const std::uint64_t row = static_cast<std::uint64_t>(d) * a.TM;
+            const std::uint32_t p0 = a.counters[row + t0];
+            segTot[q] = a.counters[row + t1] - p0;
+            earlier[q] = a.counters[row + t] - p0;
+        }
+    }
+    const std::uint32_t ts = block_exclusive_scan(tot[0] + tot[1], waveSum);
+    const std::uint32_t sp = block_exclusive_scan(segTot[0] + segTot[1], waveSum);
+    if (2 * threadIdx.x < bins) {
+        tstart[2 * threadIdx.x] = ts;
+        gbase[2 * threadIdx.x] = segBegin + sp + earlier[0];
+    }
+    if (2 * threadIdx.x + 1 < bins) {
+        tstart[2 * threadIdx.x + 1] = ts + tot[0];
+        gbase[2 * threadIdx.x + 1] = segBegin + sp + segTot[0] + earlier[1];
+    }
+    __syncthreads();
+#pragma unroll
+    for (unsigned r = 0; r < kRounds; ++r) {
+        if (wave * kSpan + r * kWave + lane < n) {
+            const unsigned d = digit_of(k[r], a.dg);
+            stage[tstart[d] + cnt[wave][d] + rank[r]] = k[r];
+        }
+    }
+    __syncthreads();
+    for (std::uint32_t p = threadIdx.x; p < n; p += kThreads) {
+        const std::uint32_t key = stage[p];
+        const unsigned d = digit_of(key, a.dg);
+        a.out[gbase[d] + (p - tstart[d])] = key;
+    }
+}
+
 struct TileArgs {
     const std::uint64_t* el;      // the sorted elements (keys of more than 31 bits)
     const std::uint32_t* keys32;  // or their low kb bits
+    // the 32-bit flow: the keys are in keys32Unsorted when the segmented
+    // passes ran (a COO out of order, *unsorted set), else in keys32; the
+    // head facts then follow them in the same buffer (null: keys32 and info)
+    const std::uint32_t* keys32Unsorted;
+    const std::uint32_t* unsorted;
     std::uint32_t n;    // elements
     std::uint32_t cap;  // the matrix's edge capacity (bounds of the row and tile-row arrays)
     std::uint64_t keyMask;  // the low kb bits: dst << loBits | lo
@@ -494,6 +688,13 @@ struct TileArgs {
     const TileInfo* tileInfo;        // [tiles]
     std::uint32_t* counters;         // [bins][TM] (+1), scanned before the emit pass
     std::uint32_t* info;             // [n] head facts of each element (count pass -> emit pass)
+
+    __device__ const std::uint32_t* keys() const {
+        return unsorted && *unsorted ? keys32Unsorted : keys32;
+    }
+    __device__ std::uint32_t* facts() const {
+        return unsorted ? const_cast<std::uint32_t*>(keys()) + n : info;
+    }
     std::uint32_t TM;
     std::uint32_t* err;
     // emit pass
@@ -550,11 +751,12 @@ __device__ TileRange load_tile(const TileArgs& a, unsigned t, const TileInfo& ti
     // segment, the slot before a segment's first element set to ~0 after
     std::uint64_t v[kLoadIters];
     const std::uint32_t first = hasPrev ? r.start - 1 : r.start;
+    const std::uint32_t* keys32 = a.keys();
 #pragma unroll
     for (unsigned q = 0; q < kLoadIters; ++q) {
         const unsigned j = q * THREADS + threadIdx.x;
         const std::uint32_t e = min(first + j, segEnd > 0 ? segEnd - 1 : 0u);
-        if constexpr (sizeof(K) == 4) v[q] = a.keys32[e];
+        if constexpr (sizeof(K) == 4) v[q] = keys32[e];
         else v[q] = a.el[e];
     }
 #pragma unroll
@@ -689,6 +891,7 @@ __global__ void __launch_bounds__(kThreads) tile_count_kernel(TileArgs a) {
     }
     for (unsigned b = threadIdx.x; b < nb; b += kThreads) hist[b] = 0;
     const TileRange r = load_tile<kThreads>(a, t, ti, tk);
+    std::uint32_t* facts = a.facts();
     const std::uint32_t loMask = (1u << a.loBits) - 1u;
     const unsigned rowBin = 8 * a.S, groupBin = 8 * a.S + 32;
     std::uint32_t groups = 0, rows = 0;
@@ -708,7 +911,7 @@ __global__ void __launch_bounds__(kThreads) tile_count_kernel(TileArgs a) {
             occErr |= h.occ > kMaxS;
             if (rep) atomicAdd(&hist[rowBin + h.occ - 1], 1u);
         }
-        a.info[r.start + i] = (h.gh ? kInfoGroup : 0u) | (h.rh ? kInfoRow : 0u) | (rep ? kInfoRepeat : 0u) |
+        facts[r.start + i] = (h.gh ? kInfoGroup : 0u) | (h.rh ? kInfoRow : 0u) | (rep ? kInfoRepeat : 0u) |
                               (deg << 3) | ((h.gh ? h.bits : 0u) << 7) | (min(wi, 31u) << 15) |
                               ((rep ? h.occ - 2 : 0u) << 20);
     }
@@ -793,12 +996,14 @@ __global__ void __launch_bounds__(kEmitThreads) tile_emit_kernel(TileArgs a) {
     // the wave's head facts and keys, loaded first
     std::uint32_t f[kEmitRounds];
     K key[kEmitRounds];
+    const std::uint32_t* keys32 = a.keys();
+    const std::uint32_t* facts = a.facts();
 #pragma unroll
     for (unsigned r0 = 0; r0 < kEmitRounds; ++r0) {
         const unsigned i = wave * kEmitSpan + r0 * kWave + lane;
         const std::uint32_t e = start + min(i, n - 1);
-        f[r0] = a.info[e];
-        if constexpr (sizeof(K) == 4) key[r0] = a.keys32[e];
+        f[r0] = facts[e];
+        if constexpr (sizeof(K) == 4) key[r0] = keys32[e];
         else key[r0] = a.el[e] & a.keyMask;
         if (i >= n) f[r0] = 0;
     }
@@ -1047,43 +1252,75 @@ int tcc_swtcf_convert(const std::uint32_t* dDst, const std::uint32_t* dSrc, std:
     TCC_HIP_CHECK(fill<std::uint32_t>(unsorted, 1, 0u, st));
     TCC_HIP_CHECK(fill<std::uint32_t>(c.segStart, static_cast<std::uint64_t>(SW) + 1, E, st));
 
-    // 1. sort: the COO's checks and first histograms, the low digits (skipped
-    // for a COO in (dst, src) order), then the sw digits.
-    hipLaunchKernelGGL(input_pass_kernel, dim3(tiles), dim3(kThreads), 0, st, dDst, dSrc, E, plan.ep, plan.low[0],
-                       c.histLow, plan.top[0], c.histTop, tiles, unsorted, err);
+    // 1. sort.  The 32-bit flow (keys of at most 31 bits, and the first sw
+    // pass's output sw >> w0 << kb | key within 32 bits): the sw digits
+    // first, from the COO, then -- only for a COO out of (dst, src) order --
+    // the low digits per super-window (step 2).  Otherwise 64-bit elements:
+    // the low digits (skipped for a COO in order), then the sw digits.
+    const bool narrow = plan.ep.kb <= 31;  // keys fit u32 with room for the ~0 sentinel
+    const unsigned w0 = plan.top[0].bits;
+    const bool flow32 = narrow && (plan.top.size() == 1 ||
+                                   (plan.top.size() == 2 && plan.swBits - w0 + plan.ep.kb <= 32));
+    hipLaunchKernelGGL(input_pass_kernel, dim3(tiles), dim3(kThreads), 0, st, dDst, dSrc, E, plan.ep,
+                       flow32 ? Digit{0, 0} : plan.low[0], c.histLow, plan.top[0], c.histTop, tiles, unsorted, err);
     TCC_LAUNCH_CHECK();
     std::uint64_t* bufs[2] = {c.elemA, c.elemB};
+    std::uint32_t* A32 = reinterpret_cast<std::uint32_t*>(c.elemA);
+    std::uint32_t* B32 = reinterpret_cast<std::uint32_t*>(c.elemB);
+    const std::uint64_t keyMask = (1ull << plan.ep.kb) - 1ull;
     int next = 0;
     const std::uint64_t* cur = nullptr;
-    const bool narrow = plan.ep.kb <= 31;  // keys fit u32 with room for the ~0 sentinel
     auto scatter = [&](const Digit& dg, std::uint32_t* hist, int onlyUnsorted, int source, bool last) -> int {
         TCC_HIP_CHECK(exclusive_scan(hist, hist, (1ull << dg.bits) * tiles, nullptr, c.temp, st,
                                      onlyUnsorted ? unsorted : nullptr));
         ScatterArgs a{cur, bufs[next], dDst, dSrc, plan.ep, E, dg, hist, tiles, unsorted, onlyUnsorted, source,
-                      last && narrow ? reinterpret_cast<std::uint32_t*>(bufs[next]) : nullptr,
-                      last ? c.segStart : nullptr, (1ull << plan.ep.kb) - 1ull};
+                      last && narrow ? reinterpret_cast<std::uint32_t*>(bufs[next]) : nullptr, 1,
+                      last ? c.segStart : nullptr, keyMask, nullptr, nullptr, w0};
         hipLaunchKernelGGL(elem_scatter_kernel, dim3(tiles), dim3(kThreads), 0, st, a);
         TCC_LAUNCH_CHECK();
         cur = bufs[next];
         next ^= 1;
         return TCC_OK;
     };
-    for (std::size_t p = 0; p < plan.low.size(); ++p) {
-        if (p > 0) {
-            hipLaunchKernelGGL(elem_hist_kernel, dim3(tiles), dim3(kThreads), 0, st, cur, E, plan.low[p], c.histLow,
-                               tiles, unsorted, 1);
+    if (flow32) {
+        // sw pass 0 from the COO (counts from the input pass): the keys and
+        // segment heads if it is the only one, else sw >> w0 << kb | key
+        const bool one = plan.top.size() == 1;
+        TCC_HIP_CHECK(exclusive_scan(c.histTop, c.histTop, (1ull << w0) * tiles, nullptr, c.temp, st));
+        ScatterArgs a0{nullptr, nullptr, dDst, dSrc, plan.ep, E, plan.top[0], c.histTop, tiles, unsorted, 0, 1,
+                       one ? B32 : A32, one ? 1 : 2, one ? c.segStart : nullptr, keyMask, nullptr, nullptr, w0};
+        hipLaunchKernelGGL(elem_scatter_kernel, dim3(tiles), dim3(kThreads), 0, st, a0);
+        TCC_LAUNCH_CHECK();
+        if (!one) {
+            // sw pass 1: sw's low w0 bits from the position in pass 0's output
+            const Digit d1{plan.ep.kb, plan.top[1].bits};  // sw >> w0 in the u32 elements
+            hipLaunchKernelGGL(elem_hist_kernel<std::uint32_t>, dim3(tiles), dim3(kThreads), 0, st, A32, E, d1,
+                               c.histLow, tiles, unsorted, 0);
+            TCC_LAUNCH_CHECK();
+            TCC_HIP_CHECK(exclusive_scan(c.histLow, c.histLow, (1ull << d1.bits) * tiles, nullptr, c.temp, st));
+            ScatterArgs a1{nullptr, nullptr, dDst, dSrc, plan.ep, E, plan.top[1], c.histLow, tiles, unsorted, 0, 3,
+                           B32, 1, c.segStart, keyMask, A32, c.histTop, w0};
+            hipLaunchKernelGGL(elem_scatter_kernel, dim3(tiles), dim3(kThreads), 0, st, a1);
             TCC_LAUNCH_CHECK();
         }
-        if (int rc = scatter(plan.low[p], c.histLow, 1, p == 0 ? 1 : 0, false)) return rc;
+    } else {
+        for (std::size_t p = 0; p < plan.low.size(); ++p) {
+            if (p > 0) {
+                hipLaunchKernelGGL(elem_hist_kernel<std::uint64_t>, dim3(tiles), dim3(kThreads), 0, st, cur, E,
+                                   plan.low[p], c.histLow, tiles, unsorted, 1);
+                TCC_LAUNCH_CHECK();
+            }
+            if (int rc = scatter(plan.low[p], c.histLow, 1, p == 0 ? 1 : 0, false)) return rc;
+        }
+        for (std::size_t p = 0; p < plan.top.size(); ++p) {
+            // pass 0's counts came from the input pass for a COO in order
+            hipLaunchKernelGGL(elem_hist_kernel<std::uint64_t>, dim3(tiles), dim3(kThreads), 0, st, cur, E,
+                               plan.top[p], c.histTop, tiles, unsorted, p == 0 ? 1 : 0);
+            TCC_LAUNCH_CHECK();
+            if (int rc = scatter(plan.top[p], c.histTop, 0, p == 0 ? 2 : 0, p + 1 == plan.top.size())) return rc;
+        }
     }
-    for (std::size_t p = 0; p < plan.top.size(); ++p) {
-        // pass 0's counts came from the input pass for a COO in order
-        hipLaunchKernelGGL(elem_hist_kernel, dim3(tiles), dim3(kThreads), 0, st, cur, E, plan.top[p], c.histTop,
-                           tiles, unsorted, p == 0 ? 1 : 0);
-        TCC_LAUNCH_CHECK();
-        if (int rc = scatter(plan.top[p], c.histTop, 0, p == 0 ? 2 : 0, p + 1 == plan.top.size())) return rc;
-    }
-    const std::uint64_t* sorted = cur;  // u32 keys when narrow
+    const std::uint64_t* sorted = flow32 ? c.elemB : cur;  // u32 keys when narrow
 
     // 2. segments (super-windows) and their tiles
     hipLaunchKernelGGL(segment_fix_kernel, dim3(1), dim3(kThreads), 0, st, c.segStart, SW);
@@ -1097,12 +1334,33 @@ int tcc_swtcf_convert(const std::uint32_t* dDst, const std::uint32_t* dSrc, std:
     TCC_LAUNCH_CHECK();
     const std::uint32_t TM = static_cast<std::uint32_t>(segment_tiles_max(E, SW));
     const std::uint64_t nCounters = static_cast<std::uint64_t>(num_bins(S)) * TM;
+    if (flow32) {
+        // the low digits per super-window, each pass returning at once for a
+        // COO in (dst, src) order: B32 -> A32 -> B32 ...
+        std::uint32_t* src = B32;
+        std::uint32_t* dst = A32;
+        for (const Digit& dg : plan.low) {
+            SegPassArgs sa{src, dst, c.tileInfo, c.firstTile, c.segStart, E, SW, TM, dg, c.histLow, unsorted};
+            const std::uint64_t nc = (1ull << dg.bits) * TM;
+            hipLaunchKernelGGL(seg_hist_kernel, dim3(TM), dim3(kThreads), 0, st, sa);
+            TCC_LAUNCH_CHECK();
+            TCC_HIP_CHECK(exclusive_scan(c.histLow, c.histLow, nc, c.histLow + nc, c.temp, st, unsorted));
+            hipLaunchKernelGGL(seg_scatter_kernel, dim3(TM), dim3(kThreads), 0, st, sa);
+            TCC_LAUNCH_CHECK();
+            std::swap(src, dst);
+        }
+    }
     TileArgs ta{};
     ta.el = sorted;
     ta.keys32 = reinterpret_cast<const std::uint32_t*>(sorted);
     // head facts: after the u32 keys in the same buffer, or in the other one
     ta.info = narrow ? reinterpret_cast<std::uint32_t*>(const_cast<std::uint64_t*>(sorted)) + E
                      : reinterpret_cast<std::uint32_t*>(sorted == c.elemA ? c.elemB : c.elemA);
+    if (flow32) {
+        ta.keys32 = B32;  // a COO in order: the sw passes' output
+        ta.keys32Unsorted = plan.low.size() % 2 ? A32 : B32;
+        ta.unsorted = unsorted;
+    }
     ta.n = E;
     ta.cap = m->nnz;
     ta.keyMask = (1ull << plan.ep.kb) - 1ull;

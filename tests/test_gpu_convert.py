@@ -197,3 +197,22 @@ def test_rows_unknown_wide_keys(gpu, oracle):
     m, err, _ = convert_gpu(dst, src, 0, cols, 16)
     assert err == 0
     assert_same(oracle, m, oracle.swtcf_convert(dst, src, 0, cols, 16))
+
+
+@pytest.mark.parametrize("rows", [5_000, 0])
+@pytest.mark.parametrize("S", [1, 16])
+def test_two_sw_passes_sorted_and_shuffled(gpu, oracle, S, rows):
+    """Enough super-windows for two sw passes, in order and shuffled.  With
+    rows = 5000 the keys fit 32 bits: the second sw pass rebuilds each
+    element's low sw bits from its position in the first's output, and the
+    shuffled COO takes the per-super-window low-digit passes.  With rows = 0
+    (32 destination bits) the 64-bit elements take every digit."""
+    n_dst, cols = 5_000, 300_000
+    rng = np.random.default_rng(40 + S)
+    keys = np.sort(rng.choice(n_dst * cols, size=200_000, replace=False))
+    dst, src = (keys // cols).astype(np.uint32), (keys % cols).astype(np.uint32)
+    ref = oracle.swtcf_convert(dst, src, rows, cols, S)
+    for order in (np.arange(dst.size), np.random.default_rng(S).permutation(dst.size)):
+        m, err, ng = convert_gpu(dst[order], src[order], rows, cols, S)
+        assert err == 0 and ng == ref["numGroups"]
+        assert_same(oracle, m, ref)
