@@ -313,7 +313,7 @@ typedef struct tcc_hybrid {
 
 /* Build the hybrid of a device COO (row = destination, col = source, no
  * duplicate pairs; dVal may be NULL).  minTileNnz 0 = 16 (at most 256),
- * groupBlocks 0 = 8 (1, 2, 4 or 8), unitSteps 0 = 64 (at most 64), tileFormat
+ * groupBlocks 0 = 8 (1, 2, 4 or 8), unitSteps 0 = 128 (at most 256), tileFormat
  * TCC_TILES_FP32 (products on v_mfma_f32_16x16x4f32) or TCC_TILES_BF16X2
  * (each TF32 operand as two bf16, four exact bf16 products on
  * v_mfma_f32_16x16x32_bf16, fp32 accumulation), phases

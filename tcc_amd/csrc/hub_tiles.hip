@@ -54,8 +54,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr std::uint32_t kTile = 16;
 constexpr std::uint32_t kTileVals = kTile * kTile;  // floats per tile
 constexpr std::uint32_t kSlice = 64;                // features per wave
-constexpr std::uint32_t kDefaultUnitSteps = 64;
-constexpr std::uint32_t kMaxUnitSteps = 64;         // a unit's step columns sit one per lane
+constexpr std::uint32_t kDefaultUnitSteps = 128;
+constexpr std::uint32_t kMaxUnitSteps = 256;        // a unit's step columns sit one per lane, in four registers
+constexpr int kColRegs = kMaxUnitSteps / 64;
 constexpr std::uint32_t kDefaultMinTileNnz = 16;
 constexpr std::uint32_t kDefaultGroupBlocks = 8;
 constexpr unsigned kThreads = 256;
@@ -323,7 +324,7 @@ __device__ __forceinline__ void add_quad(float* row, std::uint32_t f, std::uint3
     }
 }
 
-// One wave per (unit of at most 64 steps of one group, 64-feature slice),
+// One wave per (unit of at most 256 steps of one group, 64-feature slice),
 // unit-major, so the waves of one unit (one workgroup for F <= 256) read the
 // same tiles.  The unit's step columns sit one per lane and are read with
 // readlane; operands are loaded NS - 1 steps ahead into a ring of NS
@@ -334,6 +335,24 @@ __device__ __forceinline__ void add_quad(float* row, std::uint32_t f, std::uint3
 // held by one unit adds its sums into Y; the units of a shared group store
 // theirs in `partials` for hub_reduce_kernel (no atomics, and a sum order
 // that does not depend on scheduling).
+// The unit's step columns, one per lane: register k holds steps 64k..64k+63.
+__device__ __forceinline__ void load_step_cols(const std::uint32_t* stepCol, std::uint32_t p0, std::uint32_t last,
+                                               int (&cols)[kColRegs]) {
+#pragma unroll
+    for (int k = 0; k < kColRegs; ++k) cols[k] = static_cast<int>(stepCol[min(p0 + 64u * k + __lane_id(), last)]);
+}
+
+// Column block of step q of the unit (q uniform): lane q % 64 of register q / 64.
+__device__ __forceinline__ std::uint32_t step_col(const int (&cols)[kColRegs], std::uint32_t q) {
+    int c = __builtin_amdgcn_readlane(cols[0], static_cast<int>(q & 63u));
+#pragma unroll
+    for (int k = 1; k < kColRegs; ++k) {
+        const int ck = __builtin_amdgcn_readlane(cols[k], static_cast<int>(q & 63u));
+        c = (q >> 6) == static_cast<std::uint32_t>(k) ? ck : c;
+    }
+    return static_cast<std::uint32_t>(c);
+}
+
 template <int G, int NS>
 __global__ void __launch_bounds__(kThreads) hub_tiles_kernel(TileArgs a) {
     const unsigned lane = __lane_id();
@@ -347,7 +366,8 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_kernel(TileArgs a) {
     const std::uint32_t f0 = slice * kSlice;
     const unsigned li = lane & 15u, lk = lane >> 4;
     const std::uint32_t last = p1 - 1;
-    const int cols = static_cast<int>(a.stepCol[min(p0 + lane, last)]);
+    int cols[kColRegs];
+    load_step_cols(a.stepCol, p0, last, cols);
     // this lane's B element offset in a 4-row step: row lk, features 4*li..+3
     const float* xb = a.Xh + static_cast<std::uint64_t>(lk) * a.ldh + f0 + 4 * li;
     const float* av = a.tileVals + 4 * lane;
@@ -356,8 +376,7 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_kernel(TileArgs a) {
     // the zero step, so the products add nothing
     auto load = [&](std::uint32_t p, StepOperands<G>& o) {
         const std::uint32_t pa = p <= last ? p : a.zeroStep;
-        const std::uint32_t col =
-            static_cast<std::uint32_t>(__builtin_amdgcn_readlane(cols, static_cast<int>(min(p, last) - p0)));
+        const std::uint32_t col = step_col(cols, min(p, last) - p0);
 #pragma unroll
         for (int j = 0; j < G; ++j)
             o.a[j] = load_global<vf4>(av + (static_cast<std::uint64_t>(pa) * G + j) * kTileVals);
@@ -517,7 +536,8 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_split_kernel(TileArgs a) {
     const std::uint32_t f0 = slice * kSlice;
     const unsigned li = lane & 15u, lq = lane >> 4;
     const std::uint32_t last = p1 - 1;
-    const int cols = static_cast<int>(a.stepCol[min(p0 + lane, last)]);
+    int cols[kColRegs];
+    load_step_cols(a.stepCol, p0, last, cols);
     // Xs: 16 hi then 16 lo bf16 per (column block, feature); lane group q
     // reads bytes 16q..16q+15 (q < 2: xh of k-half q; q >= 2: xl of k-half q-2)
     const char* xb = reinterpret_cast<const char*>(a.Xh) + (static_cast<std::uint64_t>(f0 + li) * 64 + lq * 16);
@@ -527,8 +547,7 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_split_kernel(TileArgs a) {
 
     auto load = [&](std::uint32_t p, SplitOperands<G>& o) {
         const std::uint32_t pa = p <= last ? p : a.zeroStep;
-        const std::uint32_t col =
-            static_cast<std::uint32_t>(__builtin_amdgcn_readlane(cols, static_cast<int>(min(p, last) - p0)));
+        const std::uint32_t col = step_col(cols, min(p, last) - p0);
 #pragma unroll
         for (int j = 0; j < G; ++j) o.a[j] = load_global<vu4>(ab + (static_cast<std::uint64_t>(pa) * G + j) * (kTileVals * 4));
         const char* rb = xb + col * cbStride;
@@ -696,7 +715,7 @@ int tcc_coo_to_hybrid(const std::uint32_t* dRow, const std::uint32_t* dCol, cons
     if (unitSteps == 0) unitSteps = kDefaultUnitSteps;
     TCC_REQUIRE(minTileNnz <= kTileVals, TCC_ERR_INVALID_ARGUMENT, "hybrid: minTileNnz above 256 leaves no tile");
     TCC_REQUIRE(valid_group(groupBlocks), TCC_ERR_INVALID_ARGUMENT, "hybrid: groupBlocks must be 1, 2, 4 or 8");
-    TCC_REQUIRE(unitSteps <= kMaxUnitSteps, TCC_ERR_INVALID_ARGUMENT, "hybrid: unitSteps above 64");
+    TCC_REQUIRE(unitSteps <= kMaxUnitSteps, TCC_ERR_INVALID_ARGUMENT, "hybrid: unitSteps above 256");
     TCC_REQUIRE(tileFormat == TCC_TILES_FP32 || tileFormat == TCC_TILES_BF16X2, TCC_ERR_INVALID_ARGUMENT,
                 "hybrid: unknown tileFormat");
     const hipStream_t st = as_stream(stream);
@@ -916,7 +935,7 @@ int tcc_hub_tiles_spmm(const tcc_hub_tiles* T, const float* X, float* Y, std::ui
     TCC_REQUIRE(T->stepCol && T->tileVals && T->units && T->hubColOrder, TCC_ERR_INVALID_ARGUMENT,
                 "invalid hub tiles SpMM arguments");
     TCC_REQUIRE(valid_group(T->group_blocks) && T->unit_steps >= 1 && T->unit_steps <= kMaxUnitSteps,
-                TCC_ERR_INVALID_ARGUMENT, "hub tiles: group_blocks must be 1, 2, 4 or 8 and unit_steps 1..64");
+                TCC_ERR_INVALID_ARGUMENT, "hub tiles: group_blocks must be 1, 2, 4 or 8 and unit_steps 1..256");
     TCC_REQUIRE(T->tile_format == TCC_TILES_FP32 || T->tile_format == TCC_TILES_BF16X2, TCC_ERR_INVALID_ARGUMENT,
                 "hub tiles: unknown tile_format");
     const bool split = T->tile_format == TCC_TILES_BF16X2;

@@ -38,6 +38,9 @@ def dev_u32(a):
     return torch.from_numpy(np.ascontiguousarray(a, np.uint32).view(np.int32)).cuda()
 
 
+DEFAULT_UNIT_STEPS = 128  # the builder's unitSteps = 0
+
+
 def random_coo(nr, nc, nnz, seed, hubs):
     rng = np.random.default_rng(seed)
     nnz = max(0, min(nnz, nr * nc))
@@ -128,6 +131,7 @@ def oracle_product(oracle, dst, src, vals, nr, X):
     (300, 300, 5000, True, 256, 4, 0, True),   # no tile dense: all in the remainder
     (17, 1000, 3000, True, 20, 1, 1, True),
     (40, 900, 9000, True, 6, 8, 64, True),     # fewer rows than one group
+    (300, 4000, 60000, True, 4, 8, 100, True),  # units past 64 steps (the second register of step columns)
     (60, 60, 0, False, 32, 0, 0, True),
 ])
 def test_arrays_match_numpy_layout(gpu, oracle, nr, nc, nnz, hubs, min_nnz, G, unit_steps, values, split):
@@ -139,11 +143,11 @@ def test_arrays_match_numpy_layout(gpu, oracle, nr, nc, nnz, hubs, min_nnz, G, u
                             min_tile_nnz=min_nnz, group_blocks=G, unit_steps=unit_steps,
                             tile_format=swtcf.TILES_BF16X2 if split else swtcf.TILES_FP32)
     h = H.to_host()
-    want = reference_layout(dst, src, vals, nr, nc, min_nnz, G or 8, unit_steps or 64, split)
+    want = reference_layout(dst, src, vals, nr, nc, min_nnz, G or 8, unit_steps or DEFAULT_UNIT_STEPS, split)
     assert h["tile_format"] == (1 if split else 0)
     print(f"hybrid layout nr={nr} nc={nc} nnz={nnz} G={G}: {h['num_steps']} steps, {h['num_tiles']} tiles, "
           f"{h['tile_nnz']} tile entries", flush=True)
-    assert h["group_blocks"] == (G or 8) and h["unit_steps"] == (unit_steps or 64)
+    assert h["group_blocks"] == (G or 8) and h["unit_steps"] == (unit_steps or DEFAULT_UNIT_STEPS)
     assert h["hub_cols"] == want["hub_cols"] and h["num_tiles"] == want["num_tiles"]
     for k in ("rowOrder", "hubColOrder", "groupStepOffset", "stepCol", "units"):
         assert np.array_equal(h[k], want[k]), k
@@ -180,6 +184,9 @@ CASES = [
     (64, 64, 4096, False, 64, 2, 1, 1, False, 3),
     (777, 1500, 40000, True, 16, 4, 5, 2, True, 700),
     (400, 2000, 60000, True, 4, 8, 64, 1, True, 130),   # 64-step units, long shared groups
+    (400, 4000, 120000, True, 4, 8, 0, 1, True, 130),   # 128-step units (the default), long shared groups
+    (400, 4000, 120000, True, 4, 4, 100, 2, True, 70),  # 100-step units
+    (400, 8000, 200000, True, 4, 8, 256, 1, True, 96),  # 256-step units: all four registers of step columns
     (40, 900, 9000, True, 6, 8, 7, 1, True, 48),        # fewer rows than one group
     (60, 60, 0, False, 32, 4, 0, 1, True, 64),
 ]
@@ -228,9 +235,9 @@ def test_hybrid_errors(gpu):
         swtcf.coo_to_hybrid(dev_u32(np.array([0, 9], np.uint32)), dev_u32(np.array([0, 1], np.uint32)), None, 4, 4)
     with pytest.raises(_lib.TccError, match="out of range"):
         swtcf.coo_to_hybrid(dev_u32(np.array([0, 1], np.uint32)), dev_u32(np.array([0, 4], np.uint32)), None, 4, 4)
-    with pytest.raises(_lib.TccError, match="unitSteps above 64"):
+    with pytest.raises(_lib.TccError, match="unitSteps above 256"):
         swtcf.coo_to_hybrid(dev_u32(np.array([0], np.uint32)), dev_u32(np.array([1], np.uint32)), None, 4, 4,
-                            unit_steps=65)
+                            unit_steps=257)
     with pytest.raises(_lib.TccError, match="tileFormat"):
         swtcf.coo_to_hybrid(dev_u32(np.array([0], np.uint32)), dev_u32(np.array([1], np.uint32)), None, 4, 4,
                             tile_format=2)
