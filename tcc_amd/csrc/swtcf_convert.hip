@@ -348,18 +348,27 @@ __device__ __forceinline__ void load_elems(const ScatterArgs& a, bool coo, std::
         for (unsigned r = 0; r < kRounds; ++r) e[r] = a.in32[clamp_to(first + r * kWave, last)];
         const unsigned kb = a.ep.kb;
         const std::uint32_t keyMask = static_cast<std::uint32_t>(a.keyMask);
+        const unsigned runs = 1u << a.w0;
+        // the digit run holding a position: the last d with d0Start[d] <= i.
+        // One search for the wave's first position (the same for every lane),
+        // then each round steps forward from the previous round's last lane:
+        // positions only grow, and a run spans many tiles.
+        const std::uint32_t i0 = static_cast<std::uint32_t>(
+            clamp_to(first - __lane_id(), last));  // lane 0's position in round 0
+        unsigned lo = 0, hi = runs;
+        while (hi - lo > 1) {
+            const unsigned mid = (lo + hi) / 2;
+            if (d0s[mid] <= i0) lo = mid;
+            else hi = mid;
+        }
+        unsigned d = lo;
 #pragma unroll
         for (unsigned r = 0; r < kRounds; ++r) {
-            // the digit run holding this position: the last d with d0Start[d] <= i
             const std::uint32_t i = static_cast<std::uint32_t>(clamp_to(first + r * kWave, last));
-            unsigned lo = 0, hi = 1u << a.w0;
-            while (hi - lo > 1) {
-                const unsigned mid = (lo + hi) / 2;
-                if (d0s[mid] <= i) lo = mid;
-                else hi = mid;
-            }
-            const std::uint64_t sw = (static_cast<std::uint64_t>(e[r] >> kb) << a.w0) | lo;
+            while (d + 1 < runs && d0s[d + 1] <= i) ++d;
+            const std::uint64_t sw = (static_cast<std::uint64_t>(e[r] >> kb) << a.w0) | d;
             k[r] = (sw << kb) | (e[r] & keyMask);
+            d = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(d), kWave - 1));
         }
     } else if (coo) {
         std::uint32_t d[kRounds], s[kRounds];
@@ -840,7 +849,7 @@ __device__ __forceinline__ std::uint64_t window64(const std::uint64_t* w, unsign
 // the next group head (a row head is one too), a row at the next row head:
 // both found in a 64-bit window of the head bits (groups have at most 9
 // elements here; rows longer than 64 take the word loop).
-template <bool BITS, typename K>
+template <typename K>
 __device__ __forceinline__ Head head_at(const TileKeys<K>& tk, unsigned i, unsigned avail) {
     Head h{};
     h.gh = bit_at(tk.group, i);
@@ -848,18 +857,16 @@ __device__ __forceinline__ Head head_at(const TileKeys<K>& tk, unsigned i, unsig
     if (h.gh) {
         const std::uint64_t after = window64(tk.group, i + 1) | (1ull << 8);
         h.count = min(static_cast<unsigned>(__builtin_ctzll(after)) + 1, avail - i);
-        if constexpr (BITS) {
-            const unsigned deg = min(h.count, 8u);
-            // eight unconditional reads (slots past the loaded elements are
-            // in the array and masked), so they issue together
-            unsigned bits = 0;
+        const unsigned deg = min(h.count, 8u);
+        // eight unconditional reads (slots past the loaded elements are in
+        // the array and masked), so they issue together
+        unsigned bits = 0;
 #pragma unroll
-            for (unsigned q = 0; q < 8; ++q) {
-                const unsigned b = 1u << static_cast<unsigned>(tk.key[i + 1 + q] & 7u);
-                bits |= q < deg ? b : 0u;
-            }
-            h.bits = bits;
+        for (unsigned q = 0; q < 8; ++q) {
+            const unsigned b = 1u << static_cast<unsigned>(tk.key[i + 1 + q] & 7u);
+            bits |= q < deg ? b : 0u;
         }
+        h.bits = bits;
     }
     if (h.rh) {
         const std::uint64_t after = window64(tk.row, i + 1);
@@ -897,7 +904,7 @@ __global__ void __launch_bounds__(kThreads) tile_count_kernel(TileArgs a) {
     std::uint32_t groups = 0, rows = 0;
     bool degErr = false, occErr = false;
     for (unsigned i = threadIdx.x; i < r.n; i += kThreads) {
-        const Head h = head_at<true>(tk, i, r.avail);
+        const Head h = head_at(tk, i, r.avail);
         const unsigned deg = h.gh ? min(h.count, 8u) : 1u;
         const unsigned wi = (static_cast<std::uint32_t>(tk.key[i + 1]) & loMask) >> 3;
         const bool rep = h.rh && h.occ >= 2 && h.occ <= kMaxS;
