@@ -119,8 +119,8 @@ struct TileInfo {
 struct Carve {
     std::uint64_t* elemA;
     std::uint64_t* elemB;
-    std::uint32_t* histLow;    // [512 * sortTiles] digit counts, (digit, tile) order
-    std::uint32_t* histTop;    // [512 * sortTiles]
+    std::uint32_t* histLow;    // [512 * TM + 1] digit counts, (digit, tile) order, per sort or segment tile
+    std::uint32_t* histTop;    // [512 * TM + 1]
     std::uint32_t* counters;   // [bins * TM + 1] segment-tile counts, (bin, tile) order
     std::uint32_t* segStart;   // [SW+1]
     std::uint32_t* firstTile;  // [SW+1]
