@@ -60,6 +60,20 @@ constexpr int kColRegs = kMaxUnitSteps / 64;
 constexpr std::uint32_t kDefaultMinTileNnz = 16;
 constexpr std::uint32_t kDefaultGroupBlocks = 8;
 constexpr unsigned kThreads = 256;
+constexpr std::uint32_t kXcds = 8;
+
+// Workgroups go to the 8 XCDs round-robin (workgroup b to XCD b % 8).  The
+// tile kernels deal units to XCDs the same way, unit u to XCD u % 8, and lay
+// the waves of an XCD's units (their 64-feature slices, which read the same
+// tiles) over that XCD's consecutive workgroups, so that one L2 holds a
+// unit's tiles for all its slices.  Config 3: the split kernel's fetch fell
+// from 14.0 to 10.1 GB per launch and its time from 2.04 to 1.77 ms, against
+// one unit's slices on consecutive waves, which straddled XCDs.  The grid is
+// kXcds * tiles_blocks_per_xcd().
+__host__ __device__ inline std::uint32_t tiles_blocks_per_xcd(std::uint32_t numUnits, std::uint32_t slices) {
+    const std::uint32_t unitsPerXcd = (numUnits + kXcds - 1) / kXcds;
+    return (unitsPerXcd * slices + kThreads / kWave - 1) / (kThreads / kWave);
+}
 
 inline std::size_t align_up(std::size_t x) { return (x + 255) & ~std::size_t(255); }
 
@@ -300,6 +314,15 @@ struct TileArgs {
     std::uint32_t unitSteps;
 };
 
+// This wave's unit and 64-feature slice (unit >= numUnits: no work).
+__device__ __forceinline__ void tile_wave(const TileArgs& a, std::uint32_t& unit, std::uint32_t& slice) {
+    const std::uint32_t wx = blockIdx.x / kXcds * (kThreads / kWave) +
+                             static_cast<std::uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave)));
+    const std::uint32_t j = wx / a.slices;
+    slice = wx - j * a.slices;
+    unit = j * kXcds + blockIdx.x % kXcds;
+}
+
 // One step's operands for one wave: A of the G tiles (lane l: A(l%16,
 // 4s + l/16), s = 0..3) and four 4-row steps of Xh (lane l: row 4s + l/16,
 // features 4(l%16)..+3).
@@ -325,8 +348,8 @@ __device__ __forceinline__ void add_quad(float* row, std::uint32_t f, std::uint3
 }
 
 // One wave per (unit of at most 256 steps of one group, 64-feature slice),
-// unit-major, so the waves of one unit (one workgroup for F <= 256) read the
-// same tiles.  The unit's step columns sit one per lane and are read with
+// the slices of a unit on one XCD (tile_wave), so that they read the same
+// tiles through one L2.  The unit's step columns sit one per lane and are read with
 // readlane; operands are loaded NS - 1 steps ahead into a ring of NS
 // stages, every load unconditional: loads complete in order, so a
 // conditional load, a copy between stages or a branch out of the ring would
@@ -356,9 +379,8 @@ __device__ __forceinline__ std::uint32_t step_col(const int (&cols)[kColRegs], s
 template <int G, int NS>
 __global__ void __launch_bounds__(kThreads) hub_tiles_kernel(TileArgs a) {
     const unsigned lane = __lane_id();
-    const std::uint32_t w = blockIdx.x * (kThreads / kWave) +
-                            static_cast<std::uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave)));
-    const std::uint32_t unit = w / a.slices, slice = w - unit * a.slices;
+    std::uint32_t unit, slice;
+    tile_wave(a, unit, slice);
     if (unit >= a.numUnits) return;
     const std::uint32_t g = a.units[3ull * unit], p0 = a.units[3ull * unit + 1], p1 = a.units[3ull * unit + 2];
     if (p0 >= p1) return;
@@ -526,9 +548,8 @@ struct SplitOperands {
 template <int G, int NS>
 __global__ void __launch_bounds__(kThreads) hub_tiles_split_kernel(TileArgs a) {
     const unsigned lane = __lane_id();
-    const std::uint32_t w = blockIdx.x * (kThreads / kWave) +
-                            static_cast<std::uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave)));
-    const std::uint32_t unit = w / a.slices, slice = w - unit * a.slices;
+    std::uint32_t unit, slice;
+    tile_wave(a, unit, slice);
     if (unit >= a.numUnits) return;
     const std::uint32_t g = a.units[3ull * unit], p0 = a.units[3ull * unit + 1], p1 = a.units[3ull * unit + 2];
     if (p0 >= p1) return;
@@ -674,16 +695,19 @@ inline std::uint32_t hub_rows(std::uint32_t hubCols) { return (hubCols + kTile -
 
 // Two steps in flight (three stages) for the small groups; the larger
 // groups keep their 4 G accumulator tiles and two stages within two or
-// three waves per SIMD.
+// more waves per SIMD (the accumulators sit in arch VGPRs: the library
+// builds this file with -amdgpu-mfma-vgpr-form, and the split kernel takes
+// 244 registers at G = 8 where the AGPR form took 392).
 template <int G>
-hipError_t launch_tiles(const TileArgs& a, std::uint64_t waves, bool split, hipStream_t st) {
+hipError_t launch_tiles(const TileArgs& a, bool split, hipStream_t st) {
     constexpr int NS = G <= 2 ? 3 : 2;
     // split tiles: two stages (a third measured slower at G = 4, equal at G = 8)
     if (split)
-        hipLaunchKernelGGL((hub_tiles_split_kernel<G, 2>), dim3(grid_for(waves, kThreads / kWave)), dim3(kThreads), 0,
-                           st, a);
+        hipLaunchKernelGGL((hub_tiles_split_kernel<G, 2>), dim3(kXcds * tiles_blocks_per_xcd(a.numUnits, a.slices)),
+                           dim3(kThreads), 0, st, a);
     else
-        hipLaunchKernelGGL((hub_tiles_kernel<G, NS>), dim3(grid_for(waves, kThreads / kWave)), dim3(kThreads), 0, st, a);
+        hipLaunchKernelGGL((hub_tiles_kernel<G, NS>), dim3(kXcds * tiles_blocks_per_xcd(a.numUnits, a.slices)),
+                           dim3(kThreads), 0, st, a);
     return hipGetLastError();
 }
 
@@ -975,10 +999,10 @@ int tcc_hub_tiles_spmm(const tcc_hub_tiles* T, const float* X, float* Y, std::ui
     TCC_REQUIRE(waves <= 0x7FFFFFFFull, TCC_ERR_UNSUPPORTED, "hub tiles SpMM launch too large");
     hipError_t e;
     switch (T->group_blocks) {
-        case 1: e = launch_tiles<1>(a, waves, split, st); break;
-        case 2: e = launch_tiles<2>(a, waves, split, st); break;
-        case 4: e = launch_tiles<4>(a, waves, split, st); break;
-        default: e = launch_tiles<8>(a, waves, split, st); break;
+        case 1: e = launch_tiles<1>(a, split, st); break;
+        case 2: e = launch_tiles<2>(a, split, st); break;
+        case 4: e = launch_tiles<4>(a, split, st); break;
+        default: e = launch_tiles<8>(a, split, st); break;
     }
     TCC_HIP_CHECK(e);
     const std::uint64_t reduceBlocks = waves * T->group_blocks;
