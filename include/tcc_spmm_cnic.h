@@ -278,9 +278,13 @@ int tcc_sw_bcsr_spmm_packed(const tcc_sw_bcsr* A, const void* packedX, float* Y,
  *   tileVals[256(G p + j) + 4l + s] = A(row l%16, column 4s + l/16) of the
  *     tile of row block j at step p (the MFMA A operand of lane l at step s);
  *   units[3u .. 3u+2] = group, first step, end step (at most unit_steps
- *     steps, 1..64); a group held by more than one unit has its units' sums
+ *     steps, 1..256); a group held by more than one unit has its units' sums
  *     stored in the workspace and added into Y by a reduction pass (no
- *     atomics: the sum order is fixed). */
+ *     atomics: the sum order is fixed);
+ *   unitOrder[i]: the unit the SpMM launches i-th, the units sorted by the
+ *     column block of their first step (stable), so that units running at
+ *     the same time read the same feature rows; NULL launches them in
+ *     index order (the products do not depend on it). */
 #define TCC_TILES_FP32 0u   /* tileVals in the fp32 MFMA's A-operand order (above) */
 #define TCC_TILES_BF16X2 1u /* each tile 256 bf16 hi then 256 bf16 lo, row-major: hi + lo = the TF32 value */
 
@@ -302,6 +306,7 @@ typedef struct tcc_hub_tiles {
     const uint32_t* stepCol;         /* [num_steps] */
     const float* tileVals;           /* [256*G*(num_steps+1)] (1 KB a tile in either format): the last step zeros */
     const uint32_t* units;           /* [3*num_units] */
+    const uint32_t* unitOrder;       /* [num_units] or NULL */
 } tcc_hub_tiles;
 
 typedef struct tcc_hybrid {

@@ -70,7 +70,7 @@ class HubTiles(ctypes.Structure):
         ("num_steps", u32), ("num_tiles", u32), ("num_units", u32), ("unit_steps", u32), ("hub_cols", u32),
         ("tile_format", u32),
         ("rowOrder", vp), ("hubColOrder", vp), ("groupStepOffset", vp), ("stepCol", vp), ("tileVals", vp),
-        ("units", vp),
+        ("units", vp), ("unitOrder", vp),
     ]
 
 

@@ -441,6 +441,7 @@ class HybridMatrix:
                          else _download(t.tileVals, 512 * G * S, np.uint16).reshape(S, G, 2, 16, 16)),
             "tile_format": t.tile_format,
             "units": _download(t.units, 3 * U, np.uint32).reshape(U, 3),
+            "unitOrder": _download(t.unitOrder, U, np.uint32),
             "group_blocks": G, "num_groups": NG, "num_steps": S, "num_tiles": t.num_tiles, "num_units": U,
             "hub_cols": t.hub_cols, "tile_nnz": t.nnz, "unit_steps": t.unit_steps,
             "rest": self.rest.to_host(),

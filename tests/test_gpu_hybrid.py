@@ -7,14 +7,17 @@ Checked through the C-ABI:
   least min_tile_nnz entries; steps = the (group of G row blocks, column
   block) pairs holding one, sorted; values TF32-rounded at A(row l%16,
   column 4s + l/16) -> tileVals[step][row block % G][l][s], zeros in the
-  other slots; units of unit_steps steps; the other entries' BCSR equal to
-  the oracle's BCSR of exactly those entries;
+  other slots; units of unit_steps steps and their launch order (by the
+  column block of their first step, stable); the other entries' BCSR equal
+  to the oracle's BCSR of exactly those entries;
 - the products against the fp64 CSR oracle on TF32-rounded inputs (rel-L2
   <= 1e-5) for both tile formats (fp32 A operand; TF32 split into two bf16,
-  four exact bf16 products), in a workspace of NaN bytes, Y = AX and Y += AX, over thresholds from 1 (every tile dense) to
+  four exact bf16 products), in a workspace of NaN bytes, Y = AX and Y += AX,
+  the units launched in their stored order or (NULL order) in index order,
+  over thresholds from 1 (every tile dense) to
   256 (no tile dense), groups of 1, 2, 4 and 8 row blocks (row counts that
   leave the last group partly empty), groups shared by many units (their
-  partial sums reduced in a second pass), unit sizes 1 to 64, phased
+  partial sums reduced in a second pass), unit sizes 1 to 256, phased
   remainders, F from 1 to 700, values or none, hubs or uniform;
 - no edges, duplicate edges and out-of-range indices.
 """
@@ -111,8 +114,11 @@ def reference_layout(dst, src, vals, nr, nc, min_nnz, G, unit_steps, split=False
         for k in range(-(-(p1 - p0) // unit_steps)):
             units.append((g, p0 + k * unit_steps, min(p0 + (k + 1) * unit_steps, p1)))
     hub_cols = min(16 * (int(sc.max()) + 1), nc) if S else 0
+    units = np.array(units, np.uint32).reshape(-1, 3)
+    # launch order: by the column block of each unit's first step, ties in unit order
+    unit_order = np.argsort(sc[units[:, 1]] if len(units) else units[:, 1], kind="stable").astype(np.uint32)
     return dict(rowOrder=row_order, hubColOrder=corder[:hub_cols].astype(np.uint32), groupStepOffset=gso,
-                stepCol=sc.astype(np.uint32), tileVals=tv, units=np.array(units, np.uint32).reshape(-1, 3),
+                stepCol=sc.astype(np.uint32), tileVals=tv, units=units, unitOrder=unit_order,
                 hub_cols=hub_cols, num_tiles=int(dense_keys.size), rest=~in_dense)
 
 
@@ -149,7 +155,7 @@ def test_arrays_match_numpy_layout(gpu, oracle, nr, nc, nnz, hubs, min_nnz, G, u
           f"{h['tile_nnz']} tile entries", flush=True)
     assert h["group_blocks"] == (G or 8) and h["unit_steps"] == (unit_steps or DEFAULT_UNIT_STEPS)
     assert h["hub_cols"] == want["hub_cols"] and h["num_tiles"] == want["num_tiles"]
-    for k in ("rowOrder", "hubColOrder", "groupStepOffset", "stepCol", "units"):
+    for k in ("rowOrder", "hubColOrder", "groupStepOffset", "stepCol", "units", "unitOrder"):
         assert np.array_equal(h[k], want[k]), k
     assert np.array_equal(h["tileVals"], want["tileVals"])
     assert h["tile_nnz"] == int((~want["rest"]).sum())
@@ -224,6 +230,15 @@ def test_hybrid_spmm_vs_oracle(gpu, oracle, nr, nc, nnz, hubs, min_nnz, G, unit_
     # a second product into the same Y (tiles add into the remainder's fill)
     swtcf.hybrid_spmm(H, Xd, Y, workspace=ws)
     assert rel_l2(Y.cpu().numpy()[:nr], want) <= REL
+    # without a launch order (NULL: units in index order); not bit for bit,
+    # since the remainder's split windows add through fp32 atomics
+    order = H.view.tiles.unitOrder
+    H.view.tiles.unitOrder = None
+    try:
+        Yn = swtcf.hybrid_spmm(H, Xd, workspace=ws)
+    finally:
+        H.view.tiles.unitOrder = order
+    assert rel_l2(Yn.cpu().numpy()[:nr], want) <= REL
 
 
 def test_hybrid_errors(gpu):
