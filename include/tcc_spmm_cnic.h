@@ -117,7 +117,9 @@ typedef struct tcc_feature_source {
 
 /* Y[row-window rows x F] (=, or += when accumulate != 0) A_bcsr * X.
  * With accumulate == 0 every row 0..8*num_rowWindows-1 is written (empty
- * windows write zeros).  Y must hold 8*num_rowWindows*F floats.
+ * windows write zeros).  Y must hold 8*num_rowWindows*F floats.  Here and in
+ * every BCSR/BCSC product and tcc_tf32_pack, 1 <= featureDim < 2^30 (rows
+ * are addressed with 32-bit byte offsets); larger is an argument error.
  * (tf32_spmm_bcsr, spmm_dispatcher.cu:167-232; kernel spmm_kernel.cu:1560-1842.) */
 int tcc_bcsr_spmm(const tcc_bcsr* A, const float* X, float* Y, uint32_t featureDim,
                   int accumulate, void* stream);

@@ -55,6 +55,10 @@ def test_host_side_argument_errors_without_gpu():
     m.numSuperWindows = 1
     assert L.tcc_swtcf_spmm(ctypes.byref(m), ctypes.c_void_p(16), ctypes.c_void_p(16), 12, None) == 3
     assert b"superWindowSize=16" in L.tcc_last_error()
+    # feature rows are addressed with 32-bit byte offsets: F below 2^30
+    assert L.tcc_tf32_pack(ctypes.c_void_p(16), 4, 1 << 30, ctypes.c_void_p(16), None) == 1
+    assert b"invalid TF32 pack arguments" in L.tcc_last_error()
+    assert L.tcc_tf32_pack(ctypes.c_void_p(16), 4, 0, ctypes.c_void_p(16), None) == 1
 
 
 def test_packed_bytes_follow_the_documented_layout():
