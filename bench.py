@@ -256,19 +256,29 @@ def cpu_baselines(args, rows, cols, vals, X, n, Y_gpu, config, extra):
 def timed(step, steps, warmup):
     """Mean ms per step over `steps` after `warmup`, timed with HIP events on
     the current stream (every launch of the step goes to that stream)."""
+    return timed_stats(step, steps, warmup)[0]
+
+
+def timed_stats(step, steps, warmup):
+    """(mean, median) ms per step, as `timed`, with an event between steps
+    (the reference's drivers report both, swtcf_spmm_main.cu:203-247); the
+    mean is first to last event over `steps`."""
+    import statistics
+
     import torch
 
     stream = torch.cuda.current_stream()
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(steps):
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    ev[0].record(stream)
+    for i in range(steps):
         step()
-    e1.record(stream)
+        ev[i + 1].record(stream)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps
+    per = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
+    return ev[0].elapsed_time(ev[steps]) / steps, statistics.median(per)
 
 
 def copy_calibration(mib):
@@ -290,10 +300,11 @@ def copy_calibration(mib):
     del a_src, a_dst
 
 
-def line_for(args, value, unit, ms, dtype, config, roof, cpu, extra, higher=True):
+def line_for(args, value, unit, ms, dtype, config, roof, cpu, extra, higher=True, median=None):
     return {
         "metric": METRIC, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(ms, 5), "higher_is_better": higher, "scaling": "weak", "vs_baseline": None,
+        "ms_per_step": round(ms, 5), "median_ms_per_step": None if median is None else round(median, 5),
+        "higher_is_better": higher, "scaling": "weak", "vs_baseline": None,
         "dtype": dtype, "data": "synthetic (seeded generator, see tcc_amd/graphs.py)", "config": config,
         "roofline": roof, "cpu_baseline": cpu, "extra": extra,
     }
@@ -579,7 +590,7 @@ def bench_spmm(args, torch, swtcf, cfg):
         copy_calibration(args.copy_calibration_mib)
     if args.profile_step:
         print(f"[bench] profile-step: the step runs {args.warmup + args.steps} times", file=sys.stderr, flush=True)
-    ms = timed(step, args.steps, args.warmup)
+    ms, median = timed_stats(step, args.steps, args.warmup)
     flops = 2.0 * nnz * F
     if args.config == 1:
         torch.cuda.synchronize()
@@ -591,7 +602,8 @@ def bench_spmm(args, torch, swtcf, cfg):
         cpu = cpu_baselines(args, rows, cols, vals, X, n, Y, args.config, extra)
     roof = roofline(flops, bytes_alg(n, n, nnz, F), ms, traffic_of(args.config), kernel)
     config = {"workload": WORKLOADS[args.config], "n": n, "nnz": nnz, "F": F}
-    return line_for(args, round(flops / (ms * 1e-3) / 1e9, 3), "GFLOP/s", ms, "fp32", config, roof, cpu, extra)
+    return line_for(args, round(flops / (ms * 1e-3) / 1e9, 3), "GFLOP/s", ms, "fp32", config, roof, cpu, extra,
+                    median=median)
 
 
 def gcn_inputs(torch, cfg):
@@ -649,7 +661,7 @@ def bench_mixed(args, torch, swtcf, cfg):
 
     if args.copy_calibration_mib:
         copy_calibration(args.copy_calibration_mib)
-    ms = timed(step, args.steps, args.warmup)
+    ms, median = timed_stats(step, args.steps, args.warmup)
     torch.cuda.synchronize()
     cold_edge = ~table.hot[cols.long()]
     hot_edges = int((~cold_edge).sum().item())
@@ -684,7 +696,7 @@ def bench_mixed(args, torch, swtcf, cfg):
     config = {"workload": WORKLOADS[4], "n": n, "nnz": nnz, "F": F}
     table.free()
     return line_for(args, round(2.0 * nnz * F / (ms * 1e-3) / 1e9, 3), "GFLOP/s", ms, "fp32", config, roof,
-                    cpu, extra)
+                    cpu, extra, median=median)
 
 
 def gcn_timings(args, torch, cfg):
@@ -710,7 +722,7 @@ def gcn_timings(args, torch, cfg):
     warmup = max(1, min(args.warmup, 3))
     if args.profile_step:
         print(f"[bench] profile-step: the epoch runs {warmup + steps} times", file=sys.stderr, flush=True)
-    ms = timed(epoch, steps, warmup)
+    ms, median = timed_stats(epoch, steps, warmup)
     first_loss, last_loss = float(losses[0].item()), float(losses[-1].item())
     if args.profile_step:
         table.free()
@@ -739,6 +751,7 @@ def gcn_timings(args, torch, cfg):
     extra = {"epoch": "TwoLayerFunction: mixed SpMM F=100 (one launch), relu(AX W1) and H W2 in one pass "
                       "(tcc_gcn_relu_forward), SpMM F=2; backward A^T SpMM F=2, then dW1 and dW2 in one pass "
                       "(tcc_gcn_relu_grad); cross-entropy, Adam",
+             "epoch_median_ms": round(median, 4),
              "layer_times": "each layer alone, through its own autograd function",
              "epoch_ms_packed_feature_rows": round(ms_packed, 4),
              "layer1_fwd_bwd_ms": round(l1, 4), "layer2_fwd_bwd_ms": round(l2, 4),
@@ -754,7 +767,8 @@ def bench_gcn(args, torch, swtcf, cfg):
     n, F = cfg["n"], cfg["F"]
     ms, steps, warmup, extra, nnz = gcn_timings(args, torch, cfg)
     config = {"workload": WORKLOADS[5], "n": n, "nnz": nnz, "F": F, "hidden": 256, "classes": 2}
-    line = line_for(args, round(ms, 4), "ms", ms, "fp32", config, None, None, extra, higher=False)
+    line = line_for(args, round(ms, 4), "ms", ms, "fp32", config, None, None, extra, higher=False,
+                    median=extra.get("epoch_median_ms"))
     line["steps"], line["warmup"] = steps, warmup
     return line
 
@@ -775,7 +789,8 @@ def extra_configs(args, torch, swtcf):
     a5 = copy.copy(args)
     a5.config, a5.steps, a5.warmup = 5, 10, 3
     ms, steps, warmup, e5, _ = gcn_timings(a5, torch, CONFIGS[5])
-    out["config5"] = {"workload": WORKLOADS[5], "epoch_ms": round(ms, 4), "steps": steps, "warmup": warmup,
+    out["config5"] = {"workload": WORKLOADS[5], "epoch_ms": round(ms, 4), "epoch_median_ms": e5["epoch_median_ms"],
+                      "steps": steps, "warmup": warmup,
                       "layer1_fwd_bwd_ms": e5["layer1_fwd_bwd_ms"], "layer2_fwd_bwd_ms": e5["layer2_fwd_bwd_ms"],
                       "epoch_ms_packed_feature_rows": e5["epoch_ms_packed_feature_rows"],
                       "loss_first": e5["loss_first"], "loss_last": e5["loss_last"], "epoch": e5["epoch"]}

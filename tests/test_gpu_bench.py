@@ -25,6 +25,8 @@ def test_bench_line_config2():
     assert d["n_gpus"] == 1 and d["steps"] == 5 and d["warmup"] == 1
     assert d["unit"] == "GFLOP/s" and d["higher_is_better"] is True and d["vs_baseline"] is None
     assert d["value"] > 0 and d["ms_per_step"] > 0
+    # the median of the per-step event times, beside the mean
+    assert 0 < d["median_ms_per_step"] <= 2 * d["ms_per_step"]
     # GFLOP/s = 2 nnz F / step time
     c = d["config"]
     assert "workload" in c and c["F"] == 128
