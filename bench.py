@@ -98,6 +98,8 @@ def parse(argv=None):
     p.add_argument("--convert-order", choices=("both", "dst-src", "shuffled"), default="both",
                    help="with --profile-convert: time the COO in the generator's (dst, src) order, the same COO "
                         "shuffled (every digit of the sort runs), or both")
+    p.add_argument("--no-hybrid", action="store_true",
+                   help="config 3: the phased packed gather alone (no dense hub tiles), the path before them")
     p.add_argument("--profile-step", action="store_true",
                    help="for counter runs: only the timed step's kernels run (warmup + steps times); no CPU "
                         "baseline, comparisons, conversions or extra configs")
@@ -522,6 +524,7 @@ def bench_spmm(args, torch, swtcf, cfg):
             extra["phases"] = PHASES
             A.release()
             A = Ap
+        if per_window >= PHASE_MIN_BLOCKS_PER_WINDOW and not args.no_hybrid:
             # ... and the hybrid: dense hub tiles on MFMA + the phased gather of the rest
             t_h = time.perf_counter()
             H = swtcf.coo_to_hybrid(r32, c32, vals, n, n, min_tile_nnz=HUB_MIN_TILE_NNZ,
@@ -600,7 +603,8 @@ def bench_spmm(args, torch, swtcf, cfg):
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baselines(args, rows, cols, vals, X, n, Y, args.config, extra)
-    roof = roofline(flops, bytes_alg(n, n, nnz, F), ms, traffic_of(args.config), kernel)
+    # the traffic files hold the default path's kernels
+    roof = roofline(flops, bytes_alg(n, n, nnz, F), ms, None if args.no_hybrid else traffic_of(args.config), kernel)
     config = {"workload": WORKLOADS[args.config], "n": n, "nnz": nnz, "F": F}
     return line_for(args, round(flops / (ms * 1e-3) / 1e9, 3), "GFLOP/s", ms, "fp32", config, roof, cpu, extra,
                     median=median)
