@@ -392,13 +392,28 @@ __device__ __forceinline__ void load_elems(const ScatterArgs& a, bool coo, std::
 // out in that order, so that consecutive lanes write consecutive addresses
 // of a digit's run (6.18 against 6.47 ms for a shuffled 114M-edge
 // conversion with each lane writing its own elements).
+//
+// S32 (the 32-bit flow's super-window passes, which write u32 output): the
+// tile is staged as its u32 output words, each element's digit and, for the
+// segment heads of the last pass, the low w0 bits of its super-window (the
+// first pass's digit), 6 bytes an element instead of the 8 of the whole
+// key, with digits of at most kMaxTopDigit bits: 31 instead of 46 KB of LDS,
+// so four workgroups fit a compute unit instead of three.  The super-window
+// of a staged element is (digit << w0) | low bits for source 3, and the digit
+// itself for a single pass over all of sw's bits (source 1).
+template <bool S32>
 __global__ void __launch_bounds__(kThreads) elem_scatter_kernel(ScatterArgs a) {
-    __shared__ std::uint32_t cnt[kWaves][kMaxBins];
-    __shared__ std::uint32_t gbase[kMaxBins];   // global start of (digit, this tile)
-    __shared__ std::uint32_t tstart[kMaxBins];  // start of the digit's run in the tile
+    constexpr unsigned kB = S32 ? (1u << kMaxTopDigit) : kMaxBins;
+    __shared__ std::uint32_t cnt[kWaves][kB];
+    __shared__ std::uint32_t gbase[kB];   // global start of (digit, this tile)
+    __shared__ std::uint32_t tstart[kB];  // start of the digit's run in the tile
     __shared__ std::uint32_t waveSum[kWaves];
-    __shared__ std::uint64_t stage[kTile];
+    __shared__ __attribute__((aligned(8))) unsigned char stageRaw[S32 ? 6 * kTile : 8 * kTile];
     __shared__ std::uint32_t d0s[(1u << kMaxTopDigit) + 1];
+    std::uint64_t* const stage = reinterpret_cast<std::uint64_t*>(stageRaw);        // !S32: the keys
+    std::uint32_t* const stageV = reinterpret_cast<std::uint32_t*>(stageRaw);       // S32: output words
+    unsigned char* const stageD = stageRaw + 4 * kTile;                             // S32: digits
+    unsigned char* const stageLo = stageRaw + 5 * kTile;                            // S32: sw's low w0 bits
     if (a.onlyUnsorted && *a.unsorted == 0u) return;
     const bool coo = a.source == 1 || (a.source == 2 && *a.unsorted == 0u);
     if (a.source == 3) {
@@ -409,7 +424,7 @@ __global__ void __launch_bounds__(kThreads) elem_scatter_kernel(ScatterArgs a) {
     const unsigned lane = __lane_id();
     const unsigned wave = threadIdx.x / kWave;
     const unsigned bins = 1u << a.dg.bits;
-    for (unsigned i = threadIdx.x; i < kWaves * kMaxBins; i += kThreads) (&cnt[0][0])[i] = 0;
+    for (unsigned i = threadIdx.x; i < kWaves * kB; i += kThreads) (&cnt[0][0])[i] = 0;
     __syncthreads();
     const std::uint64_t tile0 = static_cast<std::uint64_t>(blockIdx.x) * kTile;
     const std::uint64_t base = tile0 + wave * kSpan;
@@ -466,11 +481,40 @@ __global__ void __launch_bounds__(kThreads) elem_scatter_kernel(ScatterArgs a) {
             const std::uint64_t i = base + r * kWave + lane;
             if (i < a.n) {
                 const unsigned d = digit_of(k[r], a.dg);
-                stage[tstart[d] + cnt[wave][d] + rank[r]] = k[r];
+                const unsigned q = tstart[d] + cnt[wave][d] + rank[r];
+                if constexpr (S32) {
+                    const std::uint64_t key = k[r];
+                    stageV[q] = a.outMode == 1
+                                    ? static_cast<std::uint32_t>(key & a.keyMask)
+                                    : static_cast<std::uint32_t>(((key >> (a.ep.kb + a.w0)) << a.ep.kb) |
+                                                                 (key & a.keyMask));
+                    stageD[q] = static_cast<unsigned char>(d);
+                    stageLo[q] = static_cast<unsigned char>((key >> a.ep.kb) & ((1u << a.w0) - 1u));
+                } else {
+                    stage[q] = k[r];
+                }
             }
         }
         __syncthreads();
         const std::uint32_t count = static_cast<std::uint32_t>(clamp_to(kTile, a.n - tile0));
+        if constexpr (S32) {
+            // the element's super-window: (digit << w0) | its low bits after the
+            // first pass (source 3), else the digit (one pass over all of sw)
+            const auto sw_of = [&](std::uint32_t p) -> std::uint32_t {
+                const std::uint32_t d = stageD[p];
+                return a.source == 3 ? (d << a.w0) | stageLo[p] : d;
+            };
+            for (std::uint32_t p = threadIdx.x; p < count; p += kThreads) {
+                const unsigned d = stageD[p];
+                const std::uint32_t pos = gbase[d] + (p - tstart[d]);
+                a.out32[pos] = stageV[p];
+                if (a.segStart) {
+                    const std::uint32_t sw = sw_of(p);
+                    if (p == tstart[d] || sw_of(p - 1) != sw) atomicMin(&a.segStart[sw], pos);
+                }
+            }
+            return;
+        }
         for (std::uint32_t p = threadIdx.x; p < count; p += kThreads) {
             const std::uint64_t key = stage[p];
             const unsigned d = digit_of(key, a.dg);
@@ -1283,7 +1327,7 @@ int tcc_swtcf_convert(const std::uint32_t* dDst, const std::uint32_t* dSrc, std:
         ScatterArgs a{cur, bufs[next], dDst, dSrc, plan.ep, E, dg, hist, tiles, unsorted, onlyUnsorted, source,
                       last && narrow ? reinterpret_cast<std::uint32_t*>(bufs[next]) : nullptr, 1,
                       last ? c.segStart : nullptr, keyMask, nullptr, nullptr, w0};
-        hipLaunchKernelGGL(elem_scatter_kernel, dim3(tiles), dim3(kThreads), 0, st, a);
+        hipLaunchKernelGGL(elem_scatter_kernel<false>, dim3(tiles), dim3(kThreads), 0, st, a);
         TCC_LAUNCH_CHECK();
         cur = bufs[next];
         next ^= 1;
@@ -1296,7 +1340,7 @@ int tcc_swtcf_convert(const std::uint32_t* dDst, const std::uint32_t* dSrc, std:
         TCC_HIP_CHECK(exclusive_scan(c.histTop, c.histTop, (1ull << w0) * tiles, nullptr, c.temp, st));
         ScatterArgs a0{nullptr, nullptr, dDst, dSrc, plan.ep, E, plan.top[0], c.histTop, tiles, unsorted, 0, 1,
                        one ? B32 : A32, one ? 1 : 2, one ? c.segStart : nullptr, keyMask, nullptr, nullptr, w0};
-        hipLaunchKernelGGL(elem_scatter_kernel, dim3(tiles), dim3(kThreads), 0, st, a0);
+        hipLaunchKernelGGL(elem_scatter_kernel<true>, dim3(tiles), dim3(kThreads), 0, st, a0);
         TCC_LAUNCH_CHECK();
         if (!one) {
             // sw pass 1: sw's low w0 bits from the position in pass 0's output
@@ -1307,7 +1351,7 @@ int tcc_swtcf_convert(const std::uint32_t* dDst, const std::uint32_t* dSrc, std:
             TCC_HIP_CHECK(exclusive_scan(c.histLow, c.histLow, (1ull << d1.bits) * tiles, nullptr, c.temp, st));
             ScatterArgs a1{nullptr, nullptr, dDst, dSrc, plan.ep, E, plan.top[1], c.histLow, tiles, unsorted, 0, 3,
                            B32, 1, c.segStart, keyMask, A32, c.histTop, w0};
-            hipLaunchKernelGGL(elem_scatter_kernel, dim3(tiles), dim3(kThreads), 0, st, a1);
+            hipLaunchKernelGGL(elem_scatter_kernel<true>, dim3(tiles), dim3(kThreads), 0, st, a1);
             TCC_LAUNCH_CHECK();
         }
     } else {
