@@ -863,31 +863,51 @@ __global__ void calibration_copy_kernel(vu4* __restrict__ dst, const vu4* __rest
         dst[i] = load_global<vu4>(src + i);
 }
 
+// One thread per 4 consecutive features of a row (they lie in one chunk):
+// one 8-byte store of their high halves and one 2-byte store of the low bits
+// of their two pairs (features past F: the high halves and pair bytes of the
+// valid ones only, as the layout's padding is left as it is).
 __global__ void tf32_pack_kernel(const float* __restrict__ X, std::uint32_t rows, std::uint32_t F,
-                                 std::uint32_t pairs, unsigned char* __restrict__ out, std::uint64_t stride) {
+                                 std::uint32_t quads, unsigned char* __restrict__ out, std::uint64_t stride,
+                                 bool vec2) {
     const std::uint64_t i = static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    const std::uint64_t r = i / pairs;
+    const std::uint64_t r = i / quads;
     if (r >= rows) return;
-    const std::uint32_t p = static_cast<std::uint32_t>(i - r * pairs);
-    const std::uint32_t e = 2 * p;
-    const float* x = X + r * F;
-    const bool two = e + 1 < F;
+    const std::uint32_t e = 4 * static_cast<std::uint32_t>(i - r * quads);
+    const std::uint32_t valid = min(4u, F - e);
+    const float* x = X + r * F + e;
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (vec2 && valid == 4) {
+        const vf2 a = load_global<vf2>(x), b = load_global<vf2>(x + 2);
+        v[0] = a.x; v[1] = a.y; v[2] = b.x; v[3] = b.y;
+    } else {
+#pragma unroll
+        for (unsigned k = 0; k < 4; ++k)
+            if (k < valid) v[k] = x[k];
+    }
     // A NaN keeps its top 19 bits with the quiet bit set, so that a payload
     // held only in the dropped low bits does not unpack as inf.
-    const auto pack_bits = [](float v) {
-        const std::uint32_t b = __float_as_uint(tf32_rna(v));
-        return __builtin_isnan(v) ? (b | 0x00400000u) : b;
-    };
-    const std::uint32_t b0 = pack_bits(x[e]);
-    const std::uint32_t b1 = two ? pack_bits(x[e + 1]) : 0u;
-    unsigned char* row = out + r * stride;
-    const PackedAt at = packed_at(F, e);  // e even: the pair lies in one chunk
-    if (two) {
-        *reinterpret_cast<std::uint32_t*>(row + at.hi) = (b0 >> 16) | (b1 & 0xFFFF0000u);
-    } else {
-        *reinterpret_cast<std::uint16_t*>(row + at.hi) = static_cast<std::uint16_t>(b0 >> 16);
+    std::uint32_t b[4];
+#pragma unroll
+    for (unsigned k = 0; k < 4; ++k) {
+        const std::uint32_t t = __float_as_uint(tf32_rna(v[k]));
+        b[k] = k < valid ? (__builtin_isnan(v[k]) ? (t | 0x00400000u) : t) : 0u;
     }
-    row[at.lo] = static_cast<unsigned char>(((b0 >> 13) & 7u) | (((b1 >> 13) & 7u) << 3));
+    const auto lo_byte = [](std::uint32_t b0, std::uint32_t b1) {
+        return static_cast<unsigned char>(((b0 >> 13) & 7u) | (((b1 >> 13) & 7u) << 3));
+    };
+    unsigned char* row = out + r * stride;
+    const PackedAt at = packed_at(F, e);  // e % 4 == 0: 8-byte aligned high halves, 2-byte aligned pair bytes
+    if (valid == 4) {
+        *reinterpret_cast<vu2*>(row + at.hi) = vu2{(b[0] >> 16) | (b[1] & 0xFFFF0000u), (b[2] >> 16) | (b[3] & 0xFFFF0000u)};
+        *reinterpret_cast<std::uint16_t*>(row + at.lo) =
+            static_cast<std::uint16_t>(lo_byte(b[0], b[1]) | (lo_byte(b[2], b[3]) << 8));
+    } else {
+        for (unsigned k = 0; k < valid; ++k)
+            *reinterpret_cast<std::uint16_t*>(row + at.hi + 2 * k) = static_cast<std::uint16_t>(b[k] >> 16);
+        row[at.lo] = lo_byte(b[0], b[1]);
+        if (valid > 2) row[at.lo + 1] = lo_byte(b[2], b[3]);
+    }
 }
 
 struct ScatterArgs {
@@ -1406,11 +1426,13 @@ int tcc_tf32_pack(const float* X, std::uint32_t rows, std::uint32_t featureDim, 
     TCC_REQUIRE(reinterpret_cast<std::uintptr_t>(packed) % 16 == 0, TCC_ERR_INVALID_ARGUMENT,
                 "packed buffer must be 16-byte aligned");
     if (rows == 0) return TCC_OK;
-    const std::uint32_t pairs = (featureDim + 1) / 2;
-    const std::uint64_t n = static_cast<std::uint64_t>(rows) * pairs;
+    const std::uint32_t quads = (featureDim + 3) / 4;
+    const std::uint64_t n = static_cast<std::uint64_t>(rows) * quads;
     TCC_REQUIRE(n <= 0xFFFFFFFFull * 256, TCC_ERR_UNSUPPORTED, "TF32 pack too large");
+    // two 8-byte loads a thread when every row starts 8-byte aligned
+    const bool vec2 = featureDim % 2 == 0 && reinterpret_cast<std::uintptr_t>(X) % 8 == 0;
     hipLaunchKernelGGL(tf32_pack_kernel, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(stream), X, rows,
-                       featureDim, pairs, static_cast<unsigned char*>(packed), packed_stride(featureDim));
+                       featureDim, quads, static_cast<unsigned char*>(packed), packed_stride(featureDim), vec2);
     TCC_LAUNCH_CHECK();
     return TCC_OK;
 }
