@@ -774,8 +774,11 @@ __global__ void __launch_bounds__(kThreads) narrow_gather_kernel(GatherArgs a) {
         touched = false;
         open = false;
         if (lane < 8) {
-            float* o = a.Y + (static_cast<std::uint64_t>(w) * 8 + j) * a.F;
-            if (ws < u.b0 || we > u.b1) {  // shared with another unit
+            // a phased matrix folds window w into output window w % outWindows,
+            // which every phase adds into (atomics into a zeroed Y)
+            const std::uint32_t ow = a.outWindows ? w % a.outWindows : w;
+            float* o = a.Y + (static_cast<std::uint64_t>(ow) * 8 + j) * a.F;
+            if (a.atomicOut || ws < u.b0 || we > u.b1) {  // shared with another unit or phase
                 if ((tm >> j) & 0x0101010101010101ull) {
 #pragma unroll
                     for (int f = 0; f < FT; ++f)
@@ -854,8 +857,6 @@ __global__ void __launch_bounds__(kThreads) narrow_gather_kernel(GatherArgs a) {
     if (open) flush();
 }
 
-// X [rows x F] fp32 -> packed TF32 rows (layout at packed_stride).  One
-// thread per element pair.
 // A grid-stride 16-byte copy (tcc_calibration_copy).
 __global__ void calibration_copy_kernel(vu4* __restrict__ dst, const vu4* __restrict__ src, std::uint64_t n) {
     const std::uint64_t stride = static_cast<std::uint64_t>(gridDim.x) * blockDim.x;
@@ -1266,7 +1267,8 @@ template <Src MODE>
 int launch_narrow(GatherArgs a, std::uint32_t requestedK, hipStream_t st) {
     static_assert(MODE == Src::Plain || MODE == Src::Transposed, "narrow gather reads X or dY");
     if (a.numWindows == 0) return TCC_OK;
-    if (!a.accumulate) TCC_HIP_CHECK(fill<float>(a.Y, static_cast<std::uint64_t>(a.numWindows) * 8 * a.F, 0.0f, st));
+    const std::uint64_t outWindows = a.outWindows ? a.outWindows : a.numWindows;
+    if (!a.accumulate) TCC_HIP_CHECK(fill<float>(a.Y, outWindows * 8 * a.F, 0.0f, st));
     if (a.numBlocks == 0) return TCC_OK;
     a.numChunks = 1;
     a.unitBlocks = narrow_unit_blocks(requestedK, a.numBlocks);
@@ -1396,7 +1398,7 @@ int tcc_bcsr_spmm(const tcc_bcsr* A, const float* X, float* Y, std::uint32_t fea
     clear_last_error();
     TCC_REQUIRE(bcsr_ok(A) && X && Y && feature_dim_ok(featureDim), TCC_ERR_INVALID_ARGUMENT,
                 "invalid BCSR SpMM arguments");
-    if (featureDim <= kNarrowMaxF && A->phases <= 1)
+    if (featureDim <= kNarrowMaxF)
         return launch_narrow<Src::Plain>(bcsr_args(A, X, Y, featureDim, accumulate), A->unitBlocks, as_stream(stream));
     const GatherArgs a = bcsr_args(A, X, Y, featureDim, accumulate);
     TCC_HIP_CHECK(zero_phased_output(a, as_stream(stream)));

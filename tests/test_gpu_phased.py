@@ -5,8 +5,8 @@ Checked against the ordinary build and the CSR oracle, through the C-ABI:
 - the arrays: every window of phase p holds only columns of phase p
   (c * P // num_cols == p), and per output window the phases together hold
   exactly the ordinary BCSR's (column, row, value) entries;
-- the products: bcsr_spmm (also F <= 16, which a phased matrix gathers with
-  the general kernel) and bcsr_spmm_packed, Y = AX and Y += AX, against the
+- the products: bcsr_spmm (also F <= 16, the narrow kernel, whose windows
+  then all add into a zeroed Y) and bcsr_spmm_packed, Y = AX and Y += AX, against the
   fp64 oracle on TF32-rounded inputs at rel-L2 <= 1e-5, as test_gpu_spmm;
 - edge cases: no edges, fewer columns than phases, one phase;
 - entry points that take no phased matrix return TCC_ERR_UNSUPPORTED.
@@ -103,7 +103,9 @@ CASES = [
     (640, 500, 9000, 300, 3, False, False, 16),
     (1201, 900, 40000, 64, 8, True, True, 5),
     (333, 3, 700, 32, 8, False, True, 0),  # fewer columns than phases
-    (2048, 2048, 15000, 5, 4, True, True, 0),  # F <= 16: the general kernel
+    (2048, 2048, 15000, 5, 4, True, True, 0),  # F <= 16: the narrow kernel
+    (3000, 2500, 40000, 2, 8, True, True, 0),  # F = 2, as a GCN's last layer
+    (1100, 1700, 30000, 16, 3, True, False, 9),  # F = 16, units cutting windows
     (900, 1100, 12000, 1, 2, False, True, 7),
     (1500, 1500, 25000, 256, 16, True, False, 2),
 ]
