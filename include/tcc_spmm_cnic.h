@@ -324,8 +324,9 @@ typedef struct tcc_hybrid {
  * TCC_TILES_FP32 (products on v_mfma_f32_16x16x4f32) or TCC_TILES_BF16X2
  * (each TF32 operand as two bf16, four exact bf16 products on
  * v_mfma_f32_16x16x32_bf16, fp32 accumulation), phases
- * as tcc_coo_to_bcsr_phased for the remainder.  Synchronises `stream`; free
- * with tcc_hybrid_release. */
+ * as tcc_coo_to_bcsr_phased for the remainder (whose unitBlocks is set to
+ * 64; a caller may change it).  Synchronises `stream`; free with
+ * tcc_hybrid_release. */
 int tcc_coo_to_hybrid(const uint32_t* dRow, const uint32_t* dCol, const float* dVal, uint32_t nnz,
                       uint32_t numRows, uint32_t numCols, uint32_t minTileNnz, uint32_t groupBlocks,
                       uint32_t unitSteps, uint32_t tileFormat, uint32_t phases, tcc_hybrid* out, void* stream);

@@ -55,6 +55,11 @@ constexpr std::uint32_t kTile = 16;
 constexpr std::uint32_t kTileVals = kTile * kTile;  // floats per tile
 constexpr std::uint32_t kSlice = 64;                // features per wave
 constexpr std::uint32_t kDefaultUnitSteps = 128;
+// The remainder's gather: units of 64 blocks (config 3: 9.40-9.44 ms per
+// step at 48-80 blocks, 9.58 at the 128 that tcc_bcsr's automatic choice
+// gives its 4.95M blocks, 9.52 at 32; the whole phased matrix, 12.9M
+// blocks, keeps 128).
+constexpr std::uint32_t kRestUnitBlocks = 64;
 constexpr std::uint32_t kMaxUnitSteps = 256;        // a unit's step columns sit one per lane, in four registers
 constexpr int kColRegs = kMaxUnitSteps / 64;
 constexpr std::uint32_t kDefaultMinTileNnz = 16;
@@ -957,6 +962,7 @@ int tcc_coo_to_hybrid(const std::uint32_t* dRow, const std::uint32_t* dCol, cons
     const int rc = tcc_coo_to_bcsr_phased(NR ? restRow : nullptr, NR ? restCol : nullptr, dVal ? restVal : nullptr, NR,
                                           numRows, numCols, phases, &rest, &restAlloc, stream);
     if (rc) return fail(rc);
+    rest.unitBlocks = kRestUnitBlocks;
 
     tcc_hub_tiles& T = out->tiles;
     T.num_rows = numRows;
