@@ -489,8 +489,11 @@ __device__ __forceinline__ void gather_body(const GatherArgs& a, std::uint32_t g
     if (u.w >= a.numWindows) return;  // offsets inconsistent with the block count
     const std::uint32_t f0 = a.featureBase + chunk * (kWave * V) + lane * V;
     const bool active = f0 < (a.featureEnd ? a.featureEnd : a.F);
-    // inactive lanes read the row start (in bounds) and never store
-    const std::uint32_t laneOff = active ? f0 : 0u;
+    // Inactive lanes read lane 0's features (active, so in bounds, and on
+    // the lines the wave loads anyway) and never store.  Reading the row
+    // start instead fetched two more lines per row in a tail launch
+    // (features 512-601 of config 3: 13.5 GB fetched for about 10 GB).
+    const std::uint32_t laneOff = active ? f0 : f0 - lane * V;
 
     __shared__ float flushStage[V == 4 ? kWaves * kWave * V : 1];
     float acc[8][V];
@@ -1054,7 +1057,7 @@ __device__ __forceinline__ void scatter_body(const ScatterArgs& a, std::uint32_t
     if (u.b0 >= u.b1 || u.w >= a.numWindows) return;
     const std::uint32_t f0 = chunk * (kWave * V) + lane * V;
     const bool active = f0 < a.F;
-    const std::uint32_t laneOff = active ? f0 : 0u;
+    const std::uint32_t laneOff = active ? f0 : f0 - lane * V;  // inactive: lane 0's features
 
     std::uint32_t w = u.w;
     std::uint32_t we = a.winOffset[w + 1];
