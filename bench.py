@@ -15,7 +15,7 @@ F=32: SWTCF convert + SWTCF SpMM), 2, 4 (2.45M nodes, 61.9M nnz, F=100, top-20%
 rows hot in HBM, the rest zero-copy from pinned host memory: mixed SpMM), 5.
 
 Prints one JSON line.  SpMM configurations report GFLOP/s (2*nnz*F per
-step) and the roofline of BASELINE.md: with the algorithmic bytes
+step) and their roofline: with the algorithmic bytes
 4F(n_src+n_dst) + 8 nnz + 4(n_dst+1) and AI = flops / bytes, the roof is
 min(157.3 TFLOP/s, AI * 8 TB/s); config 3 (AI 67.5) is bound by the fp32
 roof, config 2 (AI 1.6) by HBM.  The counter-measured DRAM traffic of the
@@ -121,7 +121,7 @@ def bytes_alg(n_src, n_dst, nnz, F):
 
 
 def roofline(flops, b_alg, ms, traffic, kernel):
-    """BASELINE.md's roofline: AI = flops / algorithmic bytes, roof =
+    """The metric's roofline: AI = flops / algorithmic bytes, roof =
     min(fp32 peak, AI * HBM peak).  `achieved` is the step's rate in the
     binding roof's unit, so frac = achieved / peak = (flops/t) / roof.
     `traffic` is the counter-measured HBM bytes of the step's kernels."""
@@ -134,9 +134,9 @@ def roofline(flops, b_alg, ms, traffic, kernel):
     r = {"bound": bound, "achieved": round(achieved, 4), "peak": peak, "unit": unit, "frac": round(achieved / peak, 4),
          "traffic": None if traffic is None else traffic["hbm_bytes_per_launch"], "kernel": kernel,
          "arith_intensity": round(ai, 3), "bytes_alg_per_launch": b_alg, "flops_per_launch": flops,
-         "roof": "min(157.3 TFLOP/s fp32, AI x 8 TB/s) (BASELINE.md)"}
+         "roof": "min(157.3 TFLOP/s fp32, AI x 8 TB/s)"}
     if bound == "mfma":
-        r["fp32"] = ("fp32 peak 157.3 TFLOP/s, BASELINE.md's roof for this metric; which unit each kernel uses "
+        r["fp32"] = ("fp32 peak 157.3 TFLOP/s, the roof for this metric; which unit each kernel uses "
                      "(VALU fp32 FMA, fp32 MFMA, bf16 MFMA over split TF32) is in `kernel`")
     if traffic is not None:
         gbps = traffic["hbm_bytes_per_launch"] / t / 1e9

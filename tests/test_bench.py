@@ -1,7 +1,7 @@
 """bench.py's command line and roofline arithmetic (no GPU): one GPU only,
 the default configuration (config 3) and step counts (500 timed after 50
 warm-up steps for the microsecond configs 1-2, 50 after 10 for the others),
-and BASELINE.md's roofline min(157.3 TFLOP/s, AI x 8 TB/s)."""
+and the roofline min(157.3 TFLOP/s, AI x 8 TB/s)."""
 import json
 import os
 import subprocess
