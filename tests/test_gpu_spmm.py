@@ -736,9 +736,12 @@ def test_tf32_pack_keeps_nan(gpu):
 
 
 @pytest.mark.parametrize("unit_blocks", [0, 3])
-@pytest.mark.parametrize("F", [1, 2, 64, 100, 128, 256, 257, 300, 513, 602])
+@pytest.mark.parametrize("F", [1, 2, 64, 100, 128, 256, 257, 300, 400, 513, 602, 700])
 def test_bcsr_spmm_packed(gpu, oracle, unit_blocks, F):
-    """The gather over packed rows gives the oracle's TF32 product (= and +=)."""
+    """The gather over packed rows gives the oracle's TF32 product (= and +=).
+    F past a whole chunk: a last chunk of at most 128 features in its own
+    launch at 1 or 2 features a lane (257, 300, 513, 602); a longer one in
+    the 4-feature launch, with its lanes past F idle (400, 700)."""
     from tcc_amd import swtcf
 
     nr, nc = 640, 900
