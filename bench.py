@@ -43,7 +43,6 @@ METRIC = "SpMM GFLOP/s (2·nnz·F) + % HBM roofline; GCN layer fwd+bwd ms at 1 G
 HBM_PEAK_GBPS = 8000.0
 FP32_PEAK_TFLOPS = 157.3  # MI355X fp32 (vector = matrix)
 PCIE_PEAK_GBPS = 64.0  # PCIe Gen5 x16, one direction
-NORTH_STAR_DRAM_FRAC = 0.60  # config 3: ">= 60% of peak HBM bandwidth"
 # Gathers per feature row from which packing X to TF32 first pays off
 # (measured: 441 -> 12% faster at config 3; 7.3 -> 23% slower at config 2).
 PACK_MIN_REUSE = 16.0
@@ -55,15 +54,20 @@ PACK_MIN_REUSE = 16.0
 PHASE_MIN_BLOCKS_PER_WINDOW = 64.0
 PHASES = 4
 # The same long-window (skewed) graphs hold a dense core once rows and
-# columns are ordered by degree: 16x16 tiles of at least HUB_MIN_TILE_NNZ
-# entries go to MFMA in groups of HUB_GROUP_BLOCKS row blocks, each TF32
-# operand split into two bf16 (four exact bf16 products, fp32 accumulation),
-# the rest to the phased gather.  Measured at config 3 (step ms): phased
-# gather alone 17.35; fp32 MFMA tiles, 32 nnz, G = 4: 13.40; split tiles,
-# G = 4: 12.43 / 12.31 / 11.30 / 13.75 at 32 / 24 / 16 / 8 nnz; G = 8:
-# 11.05 / 10.88 / 11.72 / 12.43 at 20 / 16 / 12 / 8 nnz.
+# columns are ordered by degree.  Config 3's values are sym-normalised,
+# v_ij = r_i c_j with r = rowdeg^-1/2 and c = coldeg^-1/2, so the product
+# is diag(r) P diag(c) X over the pattern P: steps (256 rows x 16 columns of
+# the reordered matrix) holding at least the builder's default of entries go
+# to binary tiles on bf16 MFMA over the split TF32(c X), the rest to the
+# phased gather of the packed TF32(c X) rows, each row sum scaled by r
+# (tcc_coo_to_hybrid_scaled).  Measured at config 3 (step ms): phased gather
+# alone 17.35; valued split tiles (each TF32 value as two bf16, four bf16
+# products) 8.86 at 16 nnz a tile, groups of 8; binary tiles 6.76 at 64
+# entries a step.  The valued hybrid is timed beside it under `extra`.
 HUB_MIN_TILE_NNZ = 16
 HUB_GROUP_BLOCKS = 8
+BINARY_MIN_STEP_NNZ = 64
+BINARY_GROUP_BLOCKS = 16
 CPU_SAMPLE_NNZ = 16_000_000
 
 WORKLOADS = {
@@ -138,12 +142,15 @@ def roofline(flops, b_alg, ms, traffic, kernel):
     if bound == "mfma":
         r["fp32"] = ("fp32 peak 157.3 TFLOP/s, the roof for this metric; which unit each kernel uses "
                      "(VALU fp32 FMA, fp32 MFMA, bf16 MFMA over split TF32) is in `kernel`")
+    r["hbm_fraction_alg"] = round(b_alg / t / 1e9 / HBM_PEAK_GBPS, 4)
     if traffic is not None:
         gbps = traffic["hbm_bytes_per_launch"] / t / 1e9
-        r["dram"] = {"GBps": round(gbps, 1), "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),
-                     "north_star_target_frac": NORTH_STAR_DRAM_FRAC, "source": traffic["file"],
-                     "what": "rocprofv3 FETCH_SIZE + WRITE_SIZE of the step's kernels (scaled by a 1 GiB copy) "
-                             "over this run's event-timed step"}
+        r["l2_fabric_traffic"] = {
+            "GBps": round(gbps, 1), "bytes_per_step": traffic["hbm_bytes_per_launch"], "source": traffic["file"],
+            "what": "rocprofv3 FETCH_SIZE + WRITE_SIZE of the step's kernels (scaled by a 1 GiB copy) over this "
+                    "run's event-timed step: requests from the L2 to the fabric, Infinity Cache hits included, "
+                    "so re-reads of rows count as often as they are fetched; not an efficiency figure (the "
+                    "roofline fraction is)"}
     return r
 
 
@@ -496,6 +503,13 @@ def bench_spmm(args, torch, swtcf, cfg):
         assert ws.device_error() == 0
         extra["convert_ms"] = round(conv_ms, 4)
         extra["convert_gedges_per_s"] = round(nnz / conv_ms / 1e6, 3)
+        perm = torch.randperm(nnz, device="cuda", generator=torch.Generator(device="cuda").manual_seed(5))
+        rs32, cs32 = r32[perm].contiguous(), c32[perm].contiguous()
+        conv_s = timed(lambda: swtcf.convertCOOToSWTCF(rs32, cs32, nnz, m, ws), 20, 2)
+        assert ws.device_error() == 0
+        extra["convert_shuffled_ms"] = round(conv_s, 4)
+        # the matrix of the COO in its own order, for the SpMM below
+        swtcf.convertCOOToSWTCF(r32, c32, nnz, m, ws)
         Y = torch.zeros((n, F), device="cuda")
 
         def step():
@@ -525,29 +539,48 @@ def bench_spmm(args, torch, swtcf, cfg):
             A.release()
             A = Ap
         if per_window >= PHASE_MIN_BLOCKS_PER_WINDOW and not args.no_hybrid:
-            # ... and the hybrid: dense hub tiles on MFMA + the phased gather of the rest
+            # ... and the hybrid: binary hub tiles on MFMA + the phased gather
+            # of the rest, the sym-normalised values as row and column scales
+            from tcc_amd.graphs import sym_norm_scales
+
+            rs, cs = sym_norm_scales(rows, cols, n)
+            # the scales reproduce the values: v_ij against fp32(r_i c_j)
+            fact = ((rs[rows] * cs[cols] - vals).abs() / vals.abs()).max().item()
             t_h = time.perf_counter()
-            H = swtcf.coo_to_hybrid(r32, c32, vals, n, n, min_tile_nnz=HUB_MIN_TILE_NNZ,
-                                    group_blocks=HUB_GROUP_BLOCKS, tile_format=swtcf.TILES_BF16X2, phases=PHASES)
+            H = swtcf.coo_to_hybrid_scaled(r32, c32, n, n, rs, cs, min_step_nnz=BINARY_MIN_STEP_NNZ,
+                                           group_blocks=BINARY_GROUP_BLOCKS, phases=PHASES)
             torch.cuda.synchronize()
             extra["hybrid_build_ms"] = round((time.perf_counter() - t_h) * 1e3, 3)
             t = H.view.tiles
-            extra["hub"] = {"min_tile_nnz": HUB_MIN_TILE_NNZ, "group_blocks": t.group_blocks,
-                            "tile_format": "bf16x2 (TF32 = bf16 hi + bf16 lo, v_mfma_f32_16x16x32_bf16)",
-                            "tiles": t.num_tiles,
-                            "steps": t.num_steps, "units": t.num_units, "hub_cols": t.hub_cols, "tile_nnz": t.nnz,
-                            "tile_nnz_frac": round(t.nnz / nnz, 4), "rest_blocks": H.rest.view.num_TCBlocks,
-                            "mfma_flops_per_step": 2.0 * 256 * t.group_blocks * t.num_steps * F}
+            extra["hub"] = {"format": "binary 16x16 patterns, multiplied as 32-row tiles on "
+                                      "v_mfma_f32_32x32x16_bf16 against bf16 hi/lo of TF32(c X); rows scaled by r",
+                            "min_step_nnz": BINARY_MIN_STEP_NNZ, "group_blocks": t.group_blocks,
+                            "steps": t.num_steps, "units": t.num_units, "partial_units": t.num_partial_units,
+                            "hub_cols": t.hub_cols, "tile_nnz": t.nnz, "tile_nnz_frac": round(t.nnz / nnz, 4),
+                            "rest_blocks": H.rest.view.num_TCBlocks,
+                            "bf16_mfma_flops_per_step": 4.0 * 256 * t.group_blocks * t.num_steps * F,
+                            "values_as_scales_max_rel_diff": fact}
         Y = torch.empty((A.out_windows * 8, F), device="cuda")
         phased = f" over the {A.phases}-phase BCSR (Y zero-filled first)" if A.phases > 1 else ""
         if H is not None:
             if not args.profile_step:
-                # the phased gather alone, timed in the same run for comparison
+                # the phased gather alone and the valued hybrid (each TF32
+                # value split into two bf16 tiles), timed in the same run
                 buf = torch.empty(swtcf._lib.lib().tcc_tf32_packed_bytes(n, F) + 16, dtype=torch.uint8,
                                   device="cuda")
                 extra["phased_gather_ms"] = round(
                     timed(lambda: swtcf.bcsr_spmm_packed(A, swtcf.tf32_pack(X, out=buf), F, Y), 10, 2), 4)
                 del buf
+                Hv = swtcf.coo_to_hybrid(r32, c32, vals, n, n, min_tile_nnz=HUB_MIN_TILE_NNZ,
+                                         group_blocks=HUB_GROUP_BLOCKS, tile_format=swtcf.TILES_BF16X2,
+                                         phases=PHASES)
+                Yv = torch.empty((Hv.out_rows, F), device="cuda")
+                vws = torch.empty(Hv.workspace_bytes(F) + 16, dtype=torch.uint8, device="cuda")
+                extra["valued_hybrid_ms"] = round(timed(lambda: swtcf.hybrid_spmm(Hv, X, Yv, workspace=vws), 10, 2), 4)
+                extra["valued_hybrid"] = (f"split-TF32 value tiles (>= {HUB_MIN_TILE_NNZ} nnz, groups of "
+                                          f"{HUB_GROUP_BLOCKS}) + packed gather of the valued remainder")
+                Hv.release()
+                del Yv, vws
             A.release()
             Y = torch.empty((H.out_rows, F), device="cuda")
             hws = torch.empty(H.workspace_bytes(F) + 16, dtype=torch.uint8, device="cuda")
@@ -555,12 +588,13 @@ def bench_spmm(args, torch, swtcf, cfg):
             def step():
                 swtcf.hybrid_spmm(H, X, Y, workspace=hws)
 
-            kernel = (f"hub_tiles_split_kernel<{H.view.tiles.group_blocks}, 2> (bf16 MFMA on split TF32) + "
-                      "hub_reduce_kernel + hub_rows_split_kernel, after the remainder's tf32_pack_kernel + "
-                      f"gather_kernel<Packed> over the {H.rest.phases}-phase BCSR (all timed)")
-            extra["path"] = (f"hybrid: dense hub tiles (>= {HUB_MIN_TILE_NNZ} nnz, groups of {HUB_GROUP_BLOCKS}) on "
-                             f"bf16 MFMA over split TF32 + packed gather of the remainder over its "
-                             f"{H.rest.phases}-phase BCSR")
+            kernel = (f"hub_tiles_binary_kernel<{H.view.tiles.group_blocks}, 1, 3> (bf16 MFMA 32x32x16 over "
+                      "split TF32(c X)) + hub_reduce_kernel + hub_rows_split_kernel, after the remainder's "
+                      f"tf32_pack_kernel (column-scaled) + gather_kernel<Packed> over the {H.rest.phases}-phase "
+                      "BCSR (row-scaled sums; all timed)")
+            extra["path"] = (f"binary hybrid: steps of >= {BINARY_MIN_STEP_NNZ} entries as pattern tiles on bf16 "
+                             f"MFMA over split TF32(c X) + packed gather of the remainder's pattern over its "
+                             f"{H.rest.phases}-phase BCSR; A = diag(r) P diag(c) with the sym-norm scales")
         elif reuse >= PACK_MIN_REUSE:
             # each step packs X to TF32 rows of 2.5 B/element, then gathers them
             buf = torch.empty(swtcf._lib.lib().tcc_tf32_packed_bytes(n, F) + 16, dtype=torch.uint8, device="cuda")
@@ -582,10 +616,21 @@ def bench_spmm(args, torch, swtcf, cfg):
         # reference's converter driver prints it (swtcf_convert_main.cu:417)
         m = swtcf.DeviceSWTCFMatrix(n, n, nnz, 16)
         ws = swtcf.SWTCFConvertWorkspace(nnz, n, 16)
-        conv_ms = timed(lambda: swtcf.convertCOOToSWTCF(r32, c32, nnz, m, ws), 5 if args.config == 2 else 3, 1)
+        reps = 5 if args.config == 2 else 3
+        conv_ms = timed(lambda: swtcf.convertCOOToSWTCF(r32, c32, nnz, m, ws), reps, 1)
         assert ws.device_error() == 0
         extra["convert_ms"] = round(conv_ms, 4)
         extra["convert_gedges_per_s"] = round(nnz / conv_ms / 1e6, 3)
+        extra["convert_input_order"] = "(dst, src), as the generator lists the COO"
+        # the same COO shuffled: every digit of the sort runs
+        perm = torch.randperm(nnz, device="cuda", generator=torch.Generator(device="cuda").manual_seed(5))
+        rs32, cs32 = r32[perm].contiguous(), c32[perm].contiguous()
+        del perm
+        conv_s = timed(lambda: swtcf.convertCOOToSWTCF(rs32, cs32, nnz, m, ws), reps, 1)
+        assert ws.device_error() == 0
+        extra["convert_shuffled_ms"] = round(conv_s, 4)
+        extra["convert_shuffled_gedges_per_s"] = round(nnz / conv_s / 1e6, 3)
+        del rs32, cs32
         if args.config == 2:
             extra["swtcf"] = swtcf_timings(torch, swtcf, m, X, n, nnz, F)
         del m, ws
@@ -778,17 +823,33 @@ def bench_gcn(args, torch, swtcf, cfg):
 
 
 def extra_configs(args, torch, swtcf):
-    """Config 2's step and config 5's epoch and layer times, for the config-3
-    line's `extra` (each with its own default step counts)."""
+    """Configs 1, 2 and 4's steps and config 5's epoch and layer times, for
+    the config-3 line's `extra` (each with its own default step counts)."""
     from tcc_amd.graphs import CONFIGS
 
     out = {}
+    a1 = copy.copy(args)
+    a1.config, a1.steps, a1.warmup, a1.no_cpu_baseline, a1.copy_calibration_mib = 1, 500, 50, True, 0
+    l1 = bench_spmm(a1, torch, swtcf, CONFIGS[1])
+    out["config1"] = {"workload": WORKLOADS[1], "ms_per_step": l1["ms_per_step"], "GFLOPs": l1["value"],
+                      "steps": 500, "warmup": 50, "roofline": l1["roofline"], "path": "launchSWTCFSpMM (S = 16)",
+                      "convert_ms": l1["extra"].get("convert_ms"),
+                      "convert_shuffled_ms": l1["extra"].get("convert_shuffled_ms")}
+    torch.cuda.empty_cache()
     a2 = copy.copy(args)
     a2.config, a2.steps, a2.warmup, a2.no_cpu_baseline, a2.copy_calibration_mib = 2, 500, 50, True, 0
     l2 = bench_spmm(a2, torch, swtcf, CONFIGS[2])
     out["config2"] = {"workload": WORKLOADS[2], "ms_per_step": l2["ms_per_step"], "GFLOPs": l2["value"],
                       "steps": 500, "warmup": 50, "roofline": l2["roofline"], "path": l2["extra"].get("path"),
-                      "convert_ms": l2["extra"].get("convert_ms"), "swtcf": l2["extra"].get("swtcf")}
+                      "convert_ms": l2["extra"].get("convert_ms"),
+                      "convert_shuffled_ms": l2["extra"].get("convert_shuffled_ms"), "swtcf": l2["extra"].get("swtcf")}
+    torch.cuda.empty_cache()
+    a4 = copy.copy(args)
+    a4.config, a4.steps, a4.warmup, a4.no_cpu_baseline, a4.copy_calibration_mib = 4, 20, 3, True, 0
+    l4 = bench_mixed(a4, torch, swtcf, CONFIGS[4])
+    out["config4"] = {"workload": WORKLOADS[4], "ms_per_step": l4["ms_per_step"], "GFLOPs": l4["value"],
+                      "steps": 20, "warmup": 3, "roofline": l4["roofline"],
+                      "packed_rows": l4["extra"].get("packed_rows")}
     torch.cuda.empty_cache()
     a5 = copy.copy(args)
     a5.config, a5.steps, a5.warmup = 5, 10, 3

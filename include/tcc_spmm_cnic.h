@@ -207,60 +207,6 @@ int tcc_coo_to_bcsr_phased(const uint32_t* dRow, const uint32_t* dCol, const flo
                            void** allocation, void* stream);
 int tcc_block_release(void* allocation);
 
-/* ---- row super-window BCSR (no reference counterpart) ----
- * The product tf32_spmm_bcsr computes (spmm_dispatcher.cu:167-232), laid out
- * for graphs whose rows share columns unevenly (R-MAT hubs).  Rows are
- * ordered by degree (descending, ties by row id) and cut into super-windows
- * of 64 rows (8 row windows of 8); rowOrder[64*g + s] is the original row of
- * slot s of super-window g (0xFFFFFFFF past num_rows).  Super-window g lists
- * its distinct source columns in pairs [groupOffset[g], groupOffset[g+1]),
- * ordered by the columns' degree rank (descending degree, ties by id):
- * pairCol[p] is the column (row of X) and pairMask[p] bit 8w+r says that row
- * r of window w uses it.  With values, the pair's values follow in mask-bit
- * order from data[pairValue[p]].  The SpMM fetches each column's feature row
- * once per pair and shares it among the super-window's 8 row windows through
- * LDS, where the ordinary BCSR fetches it once per (window, column).
- * Work is cut into units of at most unit_pairs consecutive pairs of one
- * super-window: units[3u], units[3u+1], units[3u+2] = super-window, first
- * pair, end pair.  With num_phases P > 1 the column ranks are cut into P
- * ranges holding about equal numbers of pairs, units do not cross a range,
- * and units are listed range first (then by super-window): the workgroups
- * in flight together read the feature rows of one range, which the L2 then
- * holds.  A super-window with more than one unit receives its units'
- * partial sums with fp32 atomics.  Products are the forward products' (TF32
- * X and values, fp32 accumulation) and land in the original row order. */
-typedef struct tcc_sw_bcsr {
-    uint32_t num_rows;
-    uint32_t num_cols;
-    uint32_t nnz;
-    uint32_t num_groups;          /* super-windows: ceil(num_rows / 64) */
-    uint32_t num_pairs;           /* (super-window, column) pairs */
-    uint32_t num_units;
-    uint32_t unit_pairs;          /* pairs per unit (at most) */
-    uint32_t num_phases;          /* column-rank ranges the units are ordered by (1 = none) */
-    const uint32_t* rowOrder;     /* [64*num_groups] */
-    const uint32_t* groupOffset;  /* [num_groups+1] */
-    const uint32_t* pairCol;      /* [num_pairs] */
-    const uint64_t* pairMask;     /* [num_pairs] */
-    const uint32_t* pairValue;    /* [num_pairs] offset of the pair's first value in data */
-    const float* data;            /* [nnz] or NULL (all ones) */
-    const uint32_t* units;        /* [3*num_units] */
-} tcc_sw_bcsr;
-
-/* Build the super-window BCSR of a device COO (row = destination, col =
- * source, no duplicate pairs; dVal may be NULL).  unitPairs = 0 takes 2048;
- * phases 0 or 1 = none, at most 16.  Synchronises `stream`; one device
- * allocation returned in *allocation (free with tcc_block_release). */
-int tcc_coo_to_sw_bcsr(const uint32_t* dRow, const uint32_t* dCol, const float* dVal, uint32_t nnz,
-                       uint32_t numRows, uint32_t numCols, uint32_t unitPairs, uint32_t phases,
-                       tcc_sw_bcsr* out, void** allocation, void* stream);
-
-/* Y[num_rows x F] (=, or += when accumulate != 0) A * X with X given packed
- * by tcc_tf32_pack (num_cols rows, 16-byte aligned).  Every row of Y is
- * written (rows without entries get zeros unless accumulating). */
-int tcc_sw_bcsr_spmm_packed(const tcc_sw_bcsr* A, const void* packedX, float* Y, uint32_t featureDim,
-                            int accumulate, void* stream);
-
 /* ---- dense hub tiles + sparse remainder (no reference counterpart) ----
  * The product tf32_spmm_bcsr computes, for graphs with a dense core (R-MAT
  * hubs).  Rows and columns are ranked by degree (descending, ties by index)
@@ -280,15 +226,36 @@ int tcc_sw_bcsr_spmm_packed(const tcc_sw_bcsr* A, const void* packedX, float* Y,
  *   tileVals[256(G p + j) + 4l + s] = A(row l%16, column 4s + l/16) of the
  *     tile of row block j at step p (the MFMA A operand of lane l at step s);
  *   units[3u .. 3u+2] = group, first step, end step (at most unit_steps
- *     steps, 1..256); a group held by more than one unit has its units' sums
- *     stored in the workspace and added into Y by a reduction pass (no
- *     atomics: the sum order is fixed);
+ *     steps); a group held by more than one unit (a shared group) has its
+ *     units' sums stored in the workspace and added into Y by a reduction
+ *     pass (no atomics: the sum order is fixed);
+ *   unitPartial[u]: the workspace slot of unit u's partial sum (the units
+ *     of shared groups, numbered in unit order), 0xFFFFFFFF for a unit that
+ *     holds its whole group; sharedGroups[3s .. 3s+2] = group, slot of its
+ *     first unit, number of units (consecutive units and slots), for the
+ *     num_shared_groups shared groups;
  *   unitOrder[i]: the unit the SpMM launches i-th, the units sorted by the
  *     column block of their first step (stable), so that units running at
  *     the same time read the same feature rows; NULL launches them in
- *     index order (the products do not depend on it). */
+ *     index order (the products do not depend on it).
+ * Binary tiles (TCC_TILES_BINARY, tcc_coo_to_hybrid_scaled) hold the
+ * pattern of A only, with A = diag(rowScale) P diag(colScale) (the scales
+ * NULL for ones).  A step is chosen when its G tiles together hold at least
+ * minStepNnz entries, and then every entry of the step is stored, 32 bytes
+ * a 16x16 tile; the SpMM multiplies 32-row tiles (row blocks 2t and 2t+1):
+ *   tileMasks, step p's G*32 bytes at byte 32*G*p: byte l*(G/2) + j/2, with
+ *     l = 16*(j%2) + i + 32*h, holds in bit e the entry (row i, column
+ *     8h + e) of row block j (the G/2 bytes lane l of the SpMM's wave reads:
+ *     row 16*(j%2) + i of 32-row tile j/2, column half h);
+ *   rowScale[16(G g + j) + i]: the scale of row i of row block j of group g
+ *     (rowOrder's order, 0 past num_rows); colScale[c]: the scale of column
+ *     c (original order).
+ * The products multiply TF32(colScale[c] * X[c]) (split into two exact
+ * bf16 halves) by the pattern on v_mfma_f32_32x32x16_bf16, then scale each
+ * row's fp32 sum by rowScale. */
 #define TCC_TILES_FP32 0u   /* tileVals in the fp32 MFMA's A-operand order (above) */
 #define TCC_TILES_BF16X2 1u /* each tile 256 bf16 hi then 256 bf16 lo, row-major: hi + lo = the TF32 value */
+#define TCC_TILES_BINARY 2u /* each tile its 256-bit pattern (tileMasks); values from rowScale and colScale */
 
 typedef struct tcc_hub_tiles {
     uint32_t num_rows;
@@ -301,14 +268,21 @@ typedef struct tcc_hub_tiles {
     uint32_t num_units;
     uint32_t unit_steps;
     uint32_t hub_cols;               /* column ranks the tiles cover: [0, hub_cols) */
-    uint32_t tile_format;            /* TCC_TILES_FP32 or TCC_TILES_BF16X2 */
+    uint32_t tile_format;            /* TCC_TILES_FP32, TCC_TILES_BF16X2 or TCC_TILES_BINARY */
     const uint32_t* rowOrder;        /* [16*G*num_groups] */
     const uint32_t* hubColOrder;     /* [hub_cols] */
     const uint32_t* groupStepOffset; /* [num_groups+1] */
     const uint32_t* stepCol;         /* [num_steps] */
-    const float* tileVals;           /* [256*G*(num_steps+1)] (1 KB a tile in either format): the last step zeros */
+    const float* tileVals;           /* [256*G*(num_steps+1)] (1 KB a tile; FP32, BF16X2): the last step zeros */
     const uint32_t* units;           /* [3*num_units] */
     const uint32_t* unitOrder;       /* [num_units] or NULL */
+    uint32_t num_partial_units;      /* units of shared groups (workspace partial sums) */
+    uint32_t num_shared_groups;
+    const uint32_t* unitPartial;     /* [num_units] */
+    const uint32_t* sharedGroups;    /* [3*num_shared_groups] */
+    const uint32_t* tileMasks;       /* BINARY: [8*G*(num_steps+1)] words, the last step zeros; else NULL */
+    const float* rowScale;           /* BINARY: [16*G*num_groups] or NULL (ones) */
+    const float* colScale;           /* BINARY: [num_cols] or NULL (ones) */
 } tcc_hub_tiles;
 
 typedef struct tcc_hybrid {
@@ -316,6 +290,10 @@ typedef struct tcc_hybrid {
     tcc_bcsr rest;                  /* every entry outside the dense tiles */
     void* tilesAllocation;          /* device allocations (tcc_hybrid_release) */
     void* restAllocation;
+    /* BINARY: the row scales in row order for the remainder's gather
+     * ([8*ceil(num_rows/8)], 0 past num_rows), or NULL (ones); the
+     * remainder's columns take tiles.colScale. */
+    const float* restRowScale;
 } tcc_hybrid;
 
 /* Build the hybrid of a device COO (row = destination, col = source, no
@@ -330,6 +308,21 @@ typedef struct tcc_hybrid {
 int tcc_coo_to_hybrid(const uint32_t* dRow, const uint32_t* dCol, const float* dVal, uint32_t nnz,
                       uint32_t numRows, uint32_t numCols, uint32_t minTileNnz, uint32_t groupBlocks,
                       uint32_t unitSteps, uint32_t tileFormat, uint32_t phases, tcc_hybrid* out, void* stream);
+
+/* The hybrid of the matrix diag(rowScale) P diag(colScale), P the pattern
+ * of a device COO (row = destination, col = source, no duplicate pairs;
+ * dRowScale [numRows] and dColScale [numCols] device arrays, either NULL
+ * for ones), with binary tiles (TCC_TILES_BINARY): steps of at least
+ * minStepNnz entries (0 = 64), groupBlocks 8 or 16 (0 = 16), unitSteps
+ * 0 = 512 (any number: the SpMM reads a unit's step list 256 steps at a
+ * time), phases as tcc_coo_to_hybrid.  The remainder holds the pattern
+ * (data NULL); its gather reads the column-scaled packed rows and scales
+ * its row sums.  The scales are copied.  Synchronises `stream`; free with
+ * tcc_hybrid_release. */
+int tcc_coo_to_hybrid_scaled(const uint32_t* dRow, const uint32_t* dCol, uint32_t nnz, uint32_t numRows,
+                             uint32_t numCols, const float* dRowScale, const float* dColScale, uint32_t minStepNnz,
+                             uint32_t groupBlocks, uint32_t unitSteps, uint32_t phases, tcc_hybrid* out,
+                             void* stream);
 int tcc_hybrid_release(tcc_hybrid* H);
 
 /* Bytes of device workspace tcc_hybrid_spmm needs for F features: the
@@ -338,7 +331,8 @@ size_t tcc_hybrid_workspace_bytes(const tcc_hybrid* H, uint32_t featureDim);
 
 /* Bytes of device workspace tcc_hub_tiles_spmm needs for F features: the hub
  * columns' TF32 rows (hub_cols x roundup(F, 64) floats) and one 16G-row
- * partial sum per unit (num_units x 16G x roundup(F, 64) floats). */
+ * partial sum per unit of a shared group (num_partial_units x 16G x
+ * roundup(F, 64) floats). */
 size_t tcc_hub_tiles_workspace_bytes(const tcc_hub_tiles* T, uint32_t featureDim);
 
 /* Y (=, or += when accumulate != 0) A X for fp32 X [num_cols x F]: the

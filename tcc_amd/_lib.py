@@ -54,15 +54,6 @@ class BCSC(ctypes.Structure):
     ]
 
 
-class SWBCSR(ctypes.Structure):
-    """tcc_sw_bcsr: the row super-window BCSR (no reference counterpart)."""
-    _fields_ = [
-        ("num_rows", u32), ("num_cols", u32), ("nnz", u32), ("num_groups", u32), ("num_pairs", u32),
-        ("num_units", u32), ("unit_pairs", u32), ("num_phases", u32), ("rowOrder", vp), ("groupOffset", vp), ("pairCol", vp),
-        ("pairMask", vp), ("pairValue", vp), ("data", vp), ("units", vp),
-    ]
-
-
 class HubTiles(ctypes.Structure):
     """tcc_hub_tiles: dense 16x16 tiles of the degree-sorted matrix (no reference counterpart)."""
     _fields_ = [
@@ -71,12 +62,15 @@ class HubTiles(ctypes.Structure):
         ("tile_format", u32),
         ("rowOrder", vp), ("hubColOrder", vp), ("groupStepOffset", vp), ("stepCol", vp), ("tileVals", vp),
         ("units", vp), ("unitOrder", vp),
+        ("num_partial_units", u32), ("num_shared_groups", u32), ("unitPartial", vp), ("sharedGroups", vp),
+        ("tileMasks", vp), ("rowScale", vp), ("colScale", vp),
     ]
 
 
 class Hybrid(ctypes.Structure):
     """tcc_hybrid: hub tiles + the remainder's BCSR."""
-    _fields_ = [("tiles", HubTiles), ("rest", BCSR), ("tilesAllocation", vp), ("restAllocation", vp)]
+    _fields_ = [("tiles", HubTiles), ("rest", BCSR), ("tilesAllocation", vp), ("restAllocation", vp),
+                ("restRowScale", vp)]
 
 
 class FeatureSource(ctypes.Structure):
@@ -116,11 +110,10 @@ SIGNATURES = {
     "tcc_tf32_packed_bytes": (ctypes.c_size_t, [u32, u32]),
     "tcc_tf32_pack": (ctypes.c_int, [vp, u32, u32, vp, vp]),
     "tcc_bcsr_spmm_packed": (ctypes.c_int, [ctypes.POINTER(BCSR), vp, vp, u32, ctypes.c_int, vp]),
-    "tcc_coo_to_sw_bcsr": (ctypes.c_int, [vp, vp, vp, u32, u32, u32, u32, u32, ctypes.POINTER(SWBCSR),
-                                          ctypes.POINTER(vp), vp]),
-    "tcc_sw_bcsr_spmm_packed": (ctypes.c_int, [ctypes.POINTER(SWBCSR), vp, vp, u32, ctypes.c_int, vp]),
     "tcc_coo_to_hybrid": (ctypes.c_int, [vp, vp, vp, u32, u32, u32, u32, u32, u32, u32, u32, ctypes.POINTER(Hybrid),
                                          vp]),
+    "tcc_coo_to_hybrid_scaled": (ctypes.c_int, [vp, vp, u32, u32, u32, vp, vp, u32, u32, u32, u32,
+                                                 ctypes.POINTER(Hybrid), vp]),
     "tcc_hybrid_release": (ctypes.c_int, [ctypes.POINTER(Hybrid)]),
     "tcc_hybrid_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Hybrid), u32]),
     "tcc_hub_tiles_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(HubTiles), u32]),

@@ -22,7 +22,7 @@ BUILD = os.path.join(ROOT, "_build", "tcc_amd")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("TCC_OFFLOAD_ARCH", "gfx950")
 
-LIB_SOURCES = ["swtcf_convert.hip", "swtcf_spmm.hip", "bcsr_spmm.hip", "bcsr_build.hip", "sw_bcsr.hip", "hub_tiles.hip",
+LIB_SOURCES = ["swtcf_convert.hip", "swtcf_spmm.hip", "bcsr_spmm.hip", "bcsr_build.hip", "hub_tiles.hip",
                "dense_tn.hip",
                "errors.cpp"]
 LIB_NAME = "libtcc_swtcf.so"

@@ -31,6 +31,7 @@
 #include "../../include/tcc_spmm_cnic.h"
 #include "../../include/tcc_swtcf.h"
 #include "common.hpp"
+#include "gather_ops.hpp"
 #include "primitives.hpp"
 
 namespace tcc {
@@ -86,6 +87,10 @@ struct GatherArgs {
     // Windows of the output (0: numWindows).  A phased matrix has `phases`
     // row windows per output window, window w adding into window w % outWindows.
     std::uint32_t outWindows;
+    // Output row scales, or nullptr: row 8*ow + r of Y receives
+    // rowScale[8*ow + r] * (its sum), so that A = diag(rowScale) * B for a
+    // pattern (or valued) B; 8 entries per output window.
+    const float* rowScale;
 };
 
 // Feature row of column `in` for the first-layer (mixed) form
@@ -516,6 +521,16 @@ __device__ __forceinline__ void gather_body(const GatherArgs& a, std::uint32_t g
     auto flush = [&]() {
         const std::uint32_t ow = a.outWindows ? w % a.outWindows : w;
         const bool shared = a.atomicOut || ws < u.b0 || we > u.b1;  // wave-uniform
+        if (a.rowScale) {
+            // the window's 8 row scales (wave-uniform loads), applied to the
+            // partial sum before it is stored or added
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                const float s = a.rowScale[static_cast<std::uint64_t>(ow) * 8 + r];
+#pragma unroll
+                for (int v = 0; v < V; ++v) acc[r][v] *= s;
+            }
+        }
         if (V == 4 && shared) {
             // A row's 256 sums pass through LDS so that each atomic
             // instruction adds 64 consecutive floats (lane l: feature
@@ -870,10 +885,12 @@ __global__ void calibration_copy_kernel(vu4* __restrict__ dst, const vu4* __rest
 // One thread per 4 consecutive features of a row (they lie in one chunk):
 // one 8-byte store of their high halves and one 2-byte store of the low bits
 // of their two pairs (features past F: the high halves and pair bytes of the
-// valid ones only, as the layout's padding is left as it is).
+// valid ones only, as the layout's padding is left as it is).  With
+// colScale, row r is packed as TF32(colScale[r] * X[r]) (the fp32 product,
+// then rounded).
 __global__ void tf32_pack_kernel(const float* __restrict__ X, std::uint32_t rows, std::uint32_t F,
                                  std::uint32_t quads, unsigned char* __restrict__ out, std::uint64_t stride,
-                                 bool vec2) {
+                                 bool vec2, const float* __restrict__ colScale) {
     const std::uint64_t i = static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     const std::uint64_t r = i / quads;
     if (r >= rows) return;
@@ -888,6 +905,11 @@ __global__ void tf32_pack_kernel(const float* __restrict__ X, std::uint32_t rows
 #pragma unroll
         for (unsigned k = 0; k < 4; ++k)
             if (k < valid) v[k] = x[k];
+    }
+    if (colScale) {
+        const float s = colScale[r];
+#pragma unroll
+        for (unsigned k = 0; k < 4; ++k) v[k] *= s;
     }
     // A NaN keeps its top 19 bits with the quiet bit set, so that a payload
     // held only in the dropped low bits does not unpack as inf.
@@ -1390,6 +1412,70 @@ bool bcsc_ok(const tcc_bcsc* A) {
 }
 
 }  // namespace
+
+// ---------------------------------------------------------------- scaled forms (gather_ops.hpp)
+
+int bcsr_spmm_scaled(const tcc_bcsr* A, const float* X, float* Y, std::uint32_t featureDim, int accumulate,
+                     const float* rowScale, hipStream_t st) {
+    TCC_REQUIRE(bcsr_ok(A) && X && Y && feature_dim_ok(featureDim), TCC_ERR_INVALID_ARGUMENT,
+                "invalid BCSR SpMM arguments");
+    // the narrow gather has no row scales: scaled products take the wide one
+    if (featureDim <= kNarrowMaxF && rowScale == nullptr)
+        return launch_narrow<Src::Plain>(bcsr_args(A, X, Y, featureDim, accumulate), A->unitBlocks, st);
+    GatherArgs a = bcsr_args(A, X, Y, featureDim, accumulate);
+    a.rowScale = rowScale;
+    TCC_HIP_CHECK(zero_phased_output(a, st));
+    return launch_gather<Src::Plain>(a, pick_vec(featureDim, {X, Y}), A->unitBlocks, st);
+}
+
+int tf32_pack_scaled(const float* X, std::uint32_t rows, std::uint32_t featureDim, const float* colScale,
+                     void* packed, hipStream_t st) {
+    TCC_REQUIRE(X && packed && feature_dim_ok(featureDim), TCC_ERR_INVALID_ARGUMENT, "invalid TF32 pack arguments");
+    TCC_REQUIRE(reinterpret_cast<std::uintptr_t>(packed) % 16 == 0, TCC_ERR_INVALID_ARGUMENT,
+                "packed buffer must be 16-byte aligned");
+    if (rows == 0) return TCC_OK;
+    const std::uint32_t quads = (featureDim + 3) / 4;
+    const std::uint64_t n = static_cast<std::uint64_t>(rows) * quads;
+    TCC_REQUIRE(n <= 0xFFFFFFFFull * 256, TCC_ERR_UNSUPPORTED, "TF32 pack too large");
+    // two 8-byte loads a thread when every row starts 8-byte aligned
+    const bool vec2 = featureDim % 2 == 0 && reinterpret_cast<std::uintptr_t>(X) % 8 == 0;
+    hipLaunchKernelGGL(tf32_pack_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, X, rows, featureDim, quads,
+                       static_cast<unsigned char*>(packed), packed_stride(featureDim), vec2, colScale);
+    TCC_LAUNCH_CHECK();
+    return TCC_OK;
+}
+
+int bcsr_spmm_packed_scaled(const tcc_bcsr* A, const void* packedX, float* Y, std::uint32_t featureDim,
+                            int accumulate, const float* rowScale, hipStream_t st) {
+    TCC_REQUIRE(bcsr_ok(A) && packedX && Y && feature_dim_ok(featureDim), TCC_ERR_INVALID_ARGUMENT,
+                "invalid packed BCSR SpMM arguments");
+    TCC_REQUIRE(reinterpret_cast<std::uintptr_t>(packedX) % 16 == 0, TCC_ERR_INVALID_ARGUMENT,
+                "packed buffer must be 16-byte aligned");
+    GatherArgs a = bcsr_args(A, nullptr, Y, featureDim, accumulate);
+    a.rowScale = rowScale;
+    TCC_HIP_CHECK(zero_phased_output(a, st));
+    a.packed = static_cast<const unsigned char*>(packedX);
+    a.packedStride = static_cast<std::uint32_t>(packed_stride(featureDim));
+    // Rows longer than one chunk are gathered a whole chunk (4 features a
+    // lane) at a time, whatever F % 4, so that each load covers its lines.
+    if (featureDim <= kPackChunk) return launch_gather<Src::Packed>(a, pick_vec(featureDim, {Y}), A->unitBlocks, st);
+    // A last chunk of at most 128 features would leave most lanes of its
+    // 4-wide waves idle while costing as much as a full chunk (each block is
+    // one memory round trip either way): its waves run on their own, 2 or 1
+    // features a lane, over the same units, after the full chunks.
+    const std::uint32_t tail = featureDim % kPackChunk;
+    if (tail == 0 || tail > kPackChunk / 2) return launch_gather<Src::Packed>(a, 4, A->unitBlocks, st);
+    GatherArgs full = a;
+    full.featureEnd = featureDim - tail;
+    int rc = launch_gather<Src::Packed>(full, 4, A->unitBlocks, st);
+    if (rc) return rc;
+    GatherArgs last = a;
+    last.featureBase = featureDim - tail;
+    // the same units as the full chunks, so that the windows they share were zeroed
+    plan_gather(full, 4, A->unitBlocks);
+    return launch_gather<Src::Packed>(last, tail > kWave ? 2 : 1, full.unitBlocks, st, false);
+}
+
 }  // namespace tcc
 
 using namespace tcc;
@@ -1399,13 +1485,7 @@ extern "C" {
 int tcc_bcsr_spmm(const tcc_bcsr* A, const float* X, float* Y, std::uint32_t featureDim, int accumulate,
                   void* stream) {
     clear_last_error();
-    TCC_REQUIRE(bcsr_ok(A) && X && Y && feature_dim_ok(featureDim), TCC_ERR_INVALID_ARGUMENT,
-                "invalid BCSR SpMM arguments");
-    if (featureDim <= kNarrowMaxF)
-        return launch_narrow<Src::Plain>(bcsr_args(A, X, Y, featureDim, accumulate), A->unitBlocks, as_stream(stream));
-    const GatherArgs a = bcsr_args(A, X, Y, featureDim, accumulate);
-    TCC_HIP_CHECK(zero_phased_output(a, as_stream(stream)));
-    return launch_gather<Src::Plain>(a, pick_vec(featureDim, {X, Y}), A->unitBlocks, as_stream(stream));
+    return bcsr_spmm_scaled(A, X, Y, featureDim, accumulate, nullptr, as_stream(stream));
 }
 
 size_t tcc_tf32_packed_bytes(std::uint32_t rows, std::uint32_t featureDim) {
@@ -1427,51 +1507,13 @@ int tcc_calibration_copy(void* dst, const void* src, size_t bytes, void* stream)
 
 int tcc_tf32_pack(const float* X, std::uint32_t rows, std::uint32_t featureDim, void* packed, void* stream) {
     clear_last_error();
-    TCC_REQUIRE(X && packed && feature_dim_ok(featureDim), TCC_ERR_INVALID_ARGUMENT, "invalid TF32 pack arguments");
-    TCC_REQUIRE(reinterpret_cast<std::uintptr_t>(packed) % 16 == 0, TCC_ERR_INVALID_ARGUMENT,
-                "packed buffer must be 16-byte aligned");
-    if (rows == 0) return TCC_OK;
-    const std::uint32_t quads = (featureDim + 3) / 4;
-    const std::uint64_t n = static_cast<std::uint64_t>(rows) * quads;
-    TCC_REQUIRE(n <= 0xFFFFFFFFull * 256, TCC_ERR_UNSUPPORTED, "TF32 pack too large");
-    // two 8-byte loads a thread when every row starts 8-byte aligned
-    const bool vec2 = featureDim % 2 == 0 && reinterpret_cast<std::uintptr_t>(X) % 8 == 0;
-    hipLaunchKernelGGL(tf32_pack_kernel, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(stream), X, rows,
-                       featureDim, quads, static_cast<unsigned char*>(packed), packed_stride(featureDim), vec2);
-    TCC_LAUNCH_CHECK();
-    return TCC_OK;
+    return tf32_pack_scaled(X, rows, featureDim, nullptr, packed, as_stream(stream));
 }
 
 int tcc_bcsr_spmm_packed(const tcc_bcsr* A, const void* packedX, float* Y, std::uint32_t featureDim, int accumulate,
                          void* stream) {
     clear_last_error();
-    TCC_REQUIRE(bcsr_ok(A) && packedX && Y && feature_dim_ok(featureDim), TCC_ERR_INVALID_ARGUMENT,
-                "invalid packed BCSR SpMM arguments");
-    TCC_REQUIRE(reinterpret_cast<std::uintptr_t>(packedX) % 16 == 0, TCC_ERR_INVALID_ARGUMENT,
-                "packed buffer must be 16-byte aligned");
-    GatherArgs a = bcsr_args(A, nullptr, Y, featureDim, accumulate);
-    TCC_HIP_CHECK(zero_phased_output(a, as_stream(stream)));
-    a.packed = static_cast<const unsigned char*>(packedX);
-    a.packedStride = static_cast<std::uint32_t>(packed_stride(featureDim));
-    // Rows longer than one chunk are gathered a whole chunk (4 features a
-    // lane) at a time, whatever F % 4, so that each load covers its lines.
-    if (featureDim <= kPackChunk)
-        return launch_gather<Src::Packed>(a, pick_vec(featureDim, {Y}), A->unitBlocks, as_stream(stream));
-    // A last chunk of at most 128 features would leave most lanes of its
-    // 4-wide waves idle while costing as much as a full chunk (each block is
-    // one memory round trip either way): its waves run on their own, 2 or 1
-    // features a lane, over the same units, after the full chunks.
-    const std::uint32_t tail = featureDim % kPackChunk;
-    if (tail == 0 || tail > kPackChunk / 2) return launch_gather<Src::Packed>(a, 4, A->unitBlocks, as_stream(stream));
-    GatherArgs full = a;
-    full.featureEnd = featureDim - tail;
-    int rc = launch_gather<Src::Packed>(full, 4, A->unitBlocks, as_stream(stream));
-    if (rc) return rc;
-    GatherArgs last = a;
-    last.featureBase = featureDim - tail;
-    // the same units as the full chunks, so that the windows they share were zeroed
-    plan_gather(full, 4, A->unitBlocks);
-    return launch_gather<Src::Packed>(last, tail > kWave ? 2 : 1, full.unitBlocks, as_stream(stream), false);
+    return bcsr_spmm_packed_scaled(A, packedX, Y, featureDim, accumulate, nullptr, as_stream(stream));
 }
 
 int tcc_bcsr_spmm_mixed(const tcc_bcsr* A, const tcc_feature_source* src, float* Y, std::uint32_t featureDim,

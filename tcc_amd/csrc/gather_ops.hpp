@@ -1,0 +1,29 @@
+// Row- and column-scaled forms of the BCSR gathers and the TF32 pack
+// (bcsr_spmm.hip), for products A X with A = diag(rowScale) * B *
+// diag(colScale) over a pattern (or valued) B: X's rows are scaled while
+// they are packed, and each output row's sum is scaled before it is stored
+// or added.  The C-ABI entry points are these with null scales.  They set
+// the library's last error and return its codes like the entry points.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "../../include/tcc_spmm_cnic.h"
+
+namespace tcc {
+
+// tcc_bcsr_spmm; rowScale (nullptr: none) has 8 entries per output window.
+int bcsr_spmm_scaled(const tcc_bcsr* A, const float* X, float* Y, std::uint32_t featureDim, int accumulate,
+                     const float* rowScale, hipStream_t st);
+
+// tcc_tf32_pack of colScale[r] * X[r] (colScale nullptr: X itself).
+int tf32_pack_scaled(const float* X, std::uint32_t rows, std::uint32_t featureDim, const float* colScale,
+                     void* packed, hipStream_t st);
+
+// tcc_bcsr_spmm_packed; rowScale as bcsr_spmm_scaled.
+int bcsr_spmm_packed_scaled(const tcc_bcsr* A, const void* packedX, float* Y, std::uint32_t featureDim,
+                            int accumulate, const float* rowScale, hipStream_t st);
+
+}  // namespace tcc

@@ -44,6 +44,7 @@
 #include "../../include/tcc_swtcf.h"
 #include "common.hpp"
 #include "degree_rank.hpp"
+#include "gather_ops.hpp"
 #include "primitives.hpp"
 
 namespace tcc {
@@ -64,6 +65,16 @@ constexpr std::uint32_t kMaxUnitSteps = 256;        // a unit's step columns sit
 constexpr int kColRegs = kMaxUnitSteps / 64;
 constexpr std::uint32_t kDefaultMinTileNnz = 16;
 constexpr std::uint32_t kDefaultGroupBlocks = 8;
+// Binary tiles: steps of at least 64 entries, groups of 16 row blocks,
+// units of up to 512 steps (the kernel reads a unit's step list 256 steps
+// at a time, so units are not bound by kMaxUnitSteps).  Config 3 (step ms,
+// 512-step units): 10.58 / 7.91 / 7.20 / 6.78 / 6.76 at 8 / 16 / 32 / 48 /
+// 64 entries with G = 16; 7.49 / 6.93 at 16 / 32 with G = 8; 7.29 / 7.20 /
+// 7.31 with 256 / 512 / 1024-step units at 32 entries.
+constexpr std::uint32_t kDefaultMinStepNnz = 64;
+constexpr std::uint32_t kDefaultBinaryGroupBlocks = 16;
+constexpr std::uint32_t kDefaultBinaryUnitSteps = 512;
+constexpr std::uint32_t kNoSlot = 0xFFFFFFFFu;
 constexpr unsigned kThreads = 256;
 constexpr std::uint32_t kXcds = 8;
 
@@ -83,6 +94,7 @@ __host__ __device__ inline std::uint32_t tiles_blocks_per_xcd(std::uint32_t numU
 inline std::size_t align_up(std::size_t x) { return (x + 255) & ~std::size_t(255); }
 
 inline bool valid_group(std::uint32_t g) { return g == 1 || g == 2 || g == 4 || g == 8; }
+inline bool valid_binary_group(std::uint32_t g) { return g == 8 || g == 16; }
 
 // bf16 halves of a TF32 value: hi = its top 16 bits (sign, exponent, 7
 // mantissa bits), lo = the exact remainder (at most 3 significant bits);
@@ -138,18 +150,30 @@ __device__ __forceinline__ std::uint64_t tile_index(const std::uint64_t* keys, c
     return keys[tileStart[t]] >> 8;
 }
 
-// dense[t] = tile t holds at least minNnz entries; the number of dense
-// tiles; the largest column block of a dense tile (+1).
+// dense[t] = tile t holds at least minNnz entries and its step (its group's
+// G tiles of the same column block, adjacent in the sorted order) at least
+// minStepNnz; the number of dense tiles; the largest column block of a
+// dense tile (+1).
 __global__ void dense_tiles_kernel(const std::uint64_t* __restrict__ keys, const std::uint32_t* __restrict__ tileStart,
                                    const std::uint32_t* __restrict__ numTiles, std::uint32_t E, std::uint32_t minNnz,
-                                   std::uint32_t colBlocks, std::uint32_t G, std::uint32_t* __restrict__ dense,
-                                   std::uint32_t* __restrict__ denseCount, std::uint32_t* __restrict__ hubBlocks) {
+                                   std::uint32_t minStepNnz, std::uint32_t colBlocks, std::uint32_t G,
+                                   std::uint32_t* __restrict__ dense, std::uint32_t* __restrict__ denseCount,
+                                   std::uint32_t* __restrict__ hubBlocks) {
     const std::uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
     bool d = false;
     if (t < *numTiles) {
+        const std::uint32_t nt = *numTiles;
         const std::uint32_t s = tileStart[t];
-        const std::uint32_t e = t + 1 < *numTiles ? tileStart[t + 1] : E;
+        const std::uint32_t e = t + 1 < nt ? tileStart[t + 1] : E;
         d = e - s >= minNnz;
+        if (d && minStepNnz > e - s) {
+            // the step's entries: its tiles before and after t (at most G - 1 each way)
+            const std::uint64_t step = (keys[s] >> 8) / G;
+            std::uint32_t first = t, end = t + 1;
+            while (first > 0 && (keys[tileStart[first - 1]] >> 8) / G == step) --first;
+            while (end < nt && (keys[tileStart[end]] >> 8) / G == step) ++end;
+            d = (end < nt ? tileStart[end] : E) - tileStart[first] >= minStepNnz;
+        }
         dense[t] = d ? 1u : 0u;
         if (d) atomicMax(hubBlocks, static_cast<std::uint32_t>((keys[s] >> 8) / G % colBlocks) + 1u);
     }
@@ -212,14 +236,15 @@ __global__ void units_per_group_kernel(const std::uint32_t* __restrict__ groupSt
     if (g < NG) units[g] = (groupSteps[g] + unitSteps - 1) / unitSteps;
 }
 
-// Dense tiles' values (TF32-rounded) into the A-operand order of their
-// slots, the others into the remainder COO.
+// Dense tiles' entries into their slots (TF32-rounded values in the
+// A-operand order, or pattern bits), the others into the remainder COO.
 __global__ void place_entries_kernel(const std::uint64_t* __restrict__ keys, const std::uint32_t* __restrict__ perm,
                                      std::uint32_t E, const std::uint32_t* __restrict__ flags,
                                      const std::uint32_t* __restrict__ pos, const std::uint32_t* __restrict__ dense,
                                      const std::uint32_t* __restrict__ slot, const std::uint32_t* __restrict__ restPos,
                                      const std::uint32_t* __restrict__ row, const std::uint32_t* __restrict__ col,
-                                     const float* __restrict__ val, float* __restrict__ tileVals, bool split,
+                                     const float* __restrict__ val, float* __restrict__ tileVals,
+                                     std::uint32_t format, std::uint32_t G, std::uint32_t* __restrict__ tileMasks,
                                      std::uint32_t* __restrict__ restRow, std::uint32_t* __restrict__ restCol,
                                      float* __restrict__ restVal) {
     const std::uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
@@ -229,7 +254,13 @@ __global__ void place_entries_kernel(const std::uint64_t* __restrict__ keys, con
     const float v = val ? val[src] : 1.0f;
     if (dense[t]) {
         const std::uint32_t i = static_cast<std::uint32_t>(keys[e] >> 4) & 15u, j = static_cast<std::uint32_t>(keys[e]) & 15u;
-        if (split) {
+        if (format == TCC_TILES_BINARY) {
+            // step s's G*32 bytes: byte l*(G/2) + rb/2, l = 16*(rb%2) + i + 32*(j/8), bit j%8
+            const std::uint32_t step = slot[t] / G, rb = slot[t] % G;
+            const std::uint64_t byte = static_cast<std::uint64_t>(step) * G * 32 +
+                                       (16 * (rb % 2) + i + 32 * (j / 8)) * (G / 2) + rb / 2;
+            atomicOr(&tileMasks[byte / 4], 1u << (8 * (byte % 4) + j % 8));
+        } else if (format == TCC_TILES_BF16X2) {
             // bf16 tile: hi[i][j] at 2(16i + j) bytes, lo 512 bytes further
             std::uint16_t hi, lo;
             bf16_split(tf32_rna(v), hi, lo);
@@ -272,6 +303,57 @@ __global__ void unit_order_keys_kernel(const std::uint32_t* __restrict__ units, 
     if (u >= NU) return;
     keys[u] = stepCol[units[3ull * u + 1]];
     order[u] = u;
+}
+
+// Units of shared groups (groups held by more than one unit) get
+// consecutive partial-sum slots in unit order: flags per group and per unit
+// for two scans, then the slots and the list of shared groups.
+__global__ void shared_groups_kernel(const std::uint32_t* __restrict__ unitFirst, std::uint32_t NG,
+                                     std::uint32_t* __restrict__ groupShared) {
+    const std::uint32_t g = blockIdx.x * blockDim.x + threadIdx.x;
+    if (g < NG) groupShared[g] = unitFirst[g + 1] - unitFirst[g] > 1 ? 1u : 0u;
+}
+
+__global__ void shared_units_kernel(const std::uint32_t* __restrict__ units, std::uint32_t NU,
+                                    const std::uint32_t* __restrict__ groupShared, std::uint32_t* __restrict__ unitShared) {
+    const std::uint32_t u = blockIdx.x * blockDim.x + threadIdx.x;
+    if (u < NU) unitShared[u] = groupShared[units[3ull * u]];
+}
+
+__global__ void partial_slots_kernel(std::uint32_t NU, const std::uint32_t* __restrict__ unitShared,
+                                     const std::uint32_t* __restrict__ unitPos, std::uint32_t* __restrict__ unitPartial) {
+    const std::uint32_t u = blockIdx.x * blockDim.x + threadIdx.x;
+    if (u < NU) unitPartial[u] = unitShared[u] ? unitPos[u] : kNoSlot;
+}
+
+// sharedGroups[3s .. 3s+2] = group, slot of its first unit, its units
+__global__ void shared_group_list_kernel(const std::uint32_t* __restrict__ unitFirst, std::uint32_t NG,
+                                         const std::uint32_t* __restrict__ groupShared,
+                                         const std::uint32_t* __restrict__ groupPos,
+                                         const std::uint32_t* __restrict__ unitPos,
+                                         std::uint32_t* __restrict__ sharedGroups) {
+    const std::uint32_t g = blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= NG || !groupShared[g]) return;
+    const std::uint64_t s = 3ull * groupPos[g];
+    sharedGroups[s] = g;
+    sharedGroups[s + 1] = unitPos[unitFirst[g]];
+    sharedGroups[s + 2] = unitFirst[g + 1] - unitFirst[g];
+}
+
+// out[s] = scale of row rowOrder[s] (0 for the slots past the last row)
+__global__ void ordered_scale_kernel(const std::uint32_t* __restrict__ rowOrder, std::uint32_t n,
+                                     const float* __restrict__ scale, float* __restrict__ out) {
+    const std::uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const std::uint32_t r = rowOrder[i];
+    out[i] = r != TCC_SWTCF_INVALID_ROW_SLOT ? scale[r] : 0.0f;
+}
+
+// out[i] = in[i] for i < n, 0 up to `padded`
+__global__ void padded_copy_kernel(const float* __restrict__ in, std::uint32_t n, std::uint32_t padded,
+                                   float* __restrict__ out) {
+    const std::uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < padded) out[i] = i < n ? in[i] : 0.0f;
 }
 
 template <typename T>
@@ -318,16 +400,19 @@ struct TileArgs {
     const std::uint32_t* groupStepOffset;
     const std::uint32_t* stepCol;
     const float* tileVals;
+    const std::uint32_t* tileMasks;  // binary tiles
+    const float* rowScale;           // binary tiles: row scales in rowOrder's order, or null
     const std::uint32_t* units;
+    const std::uint32_t* unitPartial;   // partial-sum slot of each unit (kNoSlot: it holds its group)
+    const std::uint32_t* sharedGroups;  // (group, first slot, units) of each shared group
     const float* Xh;
     std::uint32_t ldh;  // Xh row stride (a multiple of 64)
     float* Y;
-    float* partials;    // [num_units][16 G][ldh]: sums of the units of shared groups
+    float* partials;    // [num_partial_units][16 G][ldh]: sums of the units of shared groups
     std::uint32_t zeroStep;  // num_steps: a step of G zero tiles after the last
     std::uint32_t F;
     std::uint32_t numUnits;
-    std::uint32_t slices;
-    std::uint32_t unitSteps;
+    std::uint32_t slices;    // feature slices per unit (ldh / features per wave)
     const std::uint32_t* unitOrder;  // launch order of the units, or null
 };
 
@@ -405,7 +490,8 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_kernel(TileArgs a) {
     if (unit >= a.numUnits) return;
     const std::uint32_t g = a.units[3ull * unit], p0 = a.units[3ull * unit + 1], p1 = a.units[3ull * unit + 2];
     if (p0 >= p1) return;
-    const bool shared = p0 != a.groupStepOffset[g] || p1 != a.groupStepOffset[g + 1];
+    const std::uint32_t pslot = a.unitPartial[unit];
+    const bool shared = pslot != kNoSlot;
     const std::uint32_t f0 = slice * kSlice;
     const unsigned li = lane & 15u, lk = lane >> 4;
     const std::uint32_t last = p1 - 1;
@@ -463,7 +549,7 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_kernel(TileArgs a) {
     // group, feature f0 + 4*li + u.
     const std::uint32_t f = f0 + 4 * li;
     if (shared) {
-        float* base = a.partials + (static_cast<std::uint64_t>(unit) * G * kTile + 4 * lk) * a.ldh + f;
+        float* base = a.partials + (static_cast<std::uint64_t>(pslot) * G * kTile + 4 * lk) * a.ldh + f;
 #pragma unroll
         for (int j = 0; j < G; ++j)
 #pragma unroll
@@ -517,9 +603,11 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_kernel(TileArgs a) {
 // the hub rows transposed per column block: Xs[cb][f] = 16 hi then 16 lo
 // bf16 of rows 16cb..16cb+15 (64 bytes), so that a lane's 8 values of one
 // k-half are one 16-byte load.
+// With colScale (binary tiles), column c's row is TF32(colScale[c] * X[c]).
 __global__ void hub_rows_split_kernel(const float* __restrict__ X, std::uint32_t F,
                                       const std::uint32_t* __restrict__ order, std::uint32_t hubCols,
-                                      std::uint32_t hubRows, std::uint32_t ldh, std::uint16_t* __restrict__ Xs) {
+                                      std::uint32_t hubRows, std::uint32_t ldh, const float* __restrict__ colScale,
+                                      std::uint16_t* __restrict__ Xs) {
     const std::uint64_t i = static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     const std::uint32_t cb = static_cast<std::uint32_t>(i / ldh), f = static_cast<std::uint32_t>(i % ldh);
     if (cb >= hubRows / kTile) return;
@@ -532,6 +620,10 @@ __global__ void hub_rows_split_kernel(const float* __restrict__ X, std::uint32_t
     float x[16];
 #pragma unroll
     for (int k = 0; k < 16; ++k) x[k] = X[static_cast<std::uint64_t>(src[k]) * F + fc];
+    if (colScale) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) x[k] *= colScale[src[k]];
+    }
     vu4 hi[2], lo[2];
 #pragma unroll
     for (int k = 0; k < 16; k += 2) {
@@ -574,7 +666,8 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_split_kernel(TileArgs a) {
     if (unit >= a.numUnits) return;
     const std::uint32_t g = a.units[3ull * unit], p0 = a.units[3ull * unit + 1], p1 = a.units[3ull * unit + 2];
     if (p0 >= p1) return;
-    const bool shared = p0 != a.groupStepOffset[g] || p1 != a.groupStepOffset[g + 1];
+    const std::uint32_t pslot = a.unitPartial[unit];
+    const bool shared = pslot != kNoSlot;
     const std::uint32_t f0 = slice * kSlice;
     const unsigned li = lane & 15u, lq = lane >> 4;
     const std::uint32_t last = p1 - 1;
@@ -638,7 +731,7 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_split_kernel(TileArgs a) {
     // D(4*lq + v, li) of N tile u of row block j: row 16j + 4lq + v of the
     // group, feature f0 + 16u + li.
     if (shared) {
-        float* base = a.partials + (static_cast<std::uint64_t>(unit) * G * kTile + 4 * lq) * a.ldh + f0 + li;
+        float* base = a.partials + (static_cast<std::uint64_t>(pslot) * G * kTile + 4 * lq) * a.ldh + f0 + li;
 #pragma unroll
         for (int j = 0; j < G; ++j)
 #pragma unroll
@@ -674,24 +767,202 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_split_kernel(TileArgs a) {
     }
 }
 
-// Y rows of a shared group += the sum of its units' partials, one workgroup
-// per (unit, slice, row block j of the group) of which only the group's
-// first unit works: thread q sums row 16j + q/16, features 4(q%16)..+3 of
-// the slice over the group's units (ceil(steps / unitSteps) of them,
-// consecutive), sixteen loads in flight (the core's first groups have
-// hundreds of units).
+// Binary tiles (TCC_TILES_BINARY).  The reference's tensor-core operand is
+// the block's bitmap as {0, 1} (src/swtcf_spmm.cu:193-200); here the
+// patterns of 32-row tiles (row blocks 2t and 2t+1 of a group) are the A
+// operand of v_mfma_f32_32x32x16_bf16 (lane l: row l%32, columns
+// 8(l/32)..+7 of the tile's 16; B lane l: column 8(l/32) + e, feature l%32;
+// D lane l register r: row 8(r/4) + 4(l/32) + r%4, feature l%32; checked on
+// the GPU), and the values come as row and column scales: Xs holds
+// TF32(colScale[c] * X[c]) split into bf16 halves, so one MFMA against the
+// halves' high parts and one against their low parts form
+// sum_c P[i][c] * TF32(c x) exactly in fp32 products, and the row scale is
+// applied to the fp32 sum when it is stored.
+//
+// Expansion: lane l's byte of tile t (8 bits: row l%32, column half l/32)
+// becomes 8 bf16 of 0 or 1.0 through two 8-byte reads of a 16-entry table
+// in LDS, one per 4-bit half.  Each step's lookups for all its tiles are
+// issued together, before its MFMAs, so that their latency is paid once a
+// step (2 G/2 reads; an 8-byte read of 64 lanes is 4 LDS cycles against 64
+// MFMA cycles of the two products per tile).  Every tile of a step is
+// multiplied: the builder stores every entry of a chosen step, and steps
+// are nearly full (config 3: 7.97 of 8 tiles a step).
+//
+// One wave per (unit, slice of 32 NT features): per step, the G/2 pattern
+// bytes of its lane (one 8- or 4-byte load) and 2 NT 16-byte Xs loads, then
+// G NT MFMAs.  A unit's steps are read 256 at a time (step columns one per
+// lane in four registers); loads run NS - 1 steps ahead in a ring of NS
+// stages, as in the valued kernels.
+template <int G, int NT>
+struct BinaryStage {
+    std::uint32_t m[G / 8];  // this lane's G/2 pattern bytes (byte t: 32-row tile t)
+    vu4 h[NT];               // N tile u: xh of columns 8(l/32)..+7, feature f0 + 32u + l%32
+    vu4 lo[NT];              // the same columns' xl
+};
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <int G, int NT, int NS>
+__global__ void __launch_bounds__(kThreads) hub_tiles_binary_kernel(TileArgs a) {
+    static_assert(G == 8 || G == 16, "binary tiles: G is 8 or 16");
+    constexpr int T = G / 2;  // 32-row tiles a step
+    // lut[x] = 4 bf16 (0 or 1.0) of the 4 bits of x, low bit first
+    __shared__ vu2 lut[16];
+    if (threadIdx.x < 16) {
+        const unsigned x = threadIdx.x;
+        auto pair = [](unsigned y) { return ((y & 1u) ? 0x3F80u : 0u) | ((y & 2u) ? 0x3F800000u : 0u); };
+        lut[x] = vu2{pair(x & 3u), pair(x >> 2)};
+    }
+    __syncthreads();
+    const char* lutBytes = reinterpret_cast<const char*>(lut);
+    const unsigned lane = __lane_id();
+    std::uint32_t unit, slice;
+    tile_wave(a, unit, slice);
+    if (unit >= a.numUnits) return;
+    const std::uint32_t g = a.units[3ull * unit], p0 = a.units[3ull * unit + 1], p1 = a.units[3ull * unit + 2];
+    if (p0 >= p1) return;
+    const std::uint32_t pslot = a.unitPartial[unit];
+    const std::uint32_t f0 = slice * (32 * NT);
+    const unsigned lj = lane & 31u, lh = lane >> 5;
+    // Xs: 16 hi then 16 lo bf16 per (column block, feature); this lane's
+    // column half of each
+    const char* xb = reinterpret_cast<const char*>(a.Xh) + (static_cast<std::uint64_t>(f0 + lj) * 64 + lh * 16);
+    const std::uint64_t cbStride = static_cast<std::uint64_t>(a.ldh) * 64;
+    const std::uint32_t* mb = a.tileMasks + lane * (G / 8);
+
+    f32x16 acc[T][NT];
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int u = 0; u < NT; ++u)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[t][u][r] = 0.0f;
+
+    for (std::uint32_t c0 = p0; c0 < p1; c0 += kMaxUnitSteps) {
+        const std::uint32_t last = min(c0 + kMaxUnitSteps, p1) - 1;
+        int cols[kColRegs];
+        load_step_cols(a.stepCol, c0, last, cols);
+        auto load = [&](std::uint32_t p, BinaryStage<G, NT>& o) {
+            const std::uint32_t pa = p <= last ? p : a.zeroStep;
+            const std::uint32_t col = step_col(cols, min(p, last) - c0);
+            const std::uint32_t* mp = mb + static_cast<std::uint64_t>(pa) * (8 * G);
+            if constexpr (G == 16) {
+                const vu2 w = load_global<vu2>(mp);
+                o.m[0] = w.x;
+                o.m[1] = w.y;
+            } else {
+                o.m[0] = load_global<std::uint32_t>(mp);
+            }
+            const char* rb = xb + col * cbStride;
+#pragma unroll
+            for (int u = 0; u < NT; ++u) {
+                o.h[u] = load_global<vu4>(rb + u * 32 * 64);
+                o.lo[u] = load_global<vu4>(rb + u * 32 * 64 + 32);
+            }
+        };
+        auto mma = [&](const BinaryStage<G, NT>& o) {
+            // every tile's lookups first: byte addresses 8 * nibble
+            vu4 A[T];
+#pragma unroll
+            for (int w = 0; w < G / 8; ++w) {
+                const std::uint32_t al = (o.m[w] << 3) & 0x78787878u, ah = (o.m[w] >> 1) & 0x78787878u;
+#pragma unroll
+                for (int q = 0; q < 4 && 4 * w + q < T; ++q) {
+                    const vu2 x0 = *reinterpret_cast<const vu2*>(lutBytes + ((al >> (8 * q)) & 0xFFu));
+                    const vu2 x1 = *reinterpret_cast<const vu2*>(lutBytes + ((ah >> (8 * q)) & 0xFFu));
+                    A[4 * w + q] = vu4{x0.x, x0.y, x1.x, x1.y};
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                const bf16x8 av = __builtin_bit_cast(bf16x8, A[t]);
+#pragma unroll
+                for (int u = 0; u < NT; ++u) {
+                    acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, o.h[u]),
+                                                                        acc[t][u], 0, 0, 0);
+                    acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, o.lo[u]),
+                                                                        acc[t][u], 0, 0, 0);
+                }
+            }
+        };
+
+        BinaryStage<G, NT> ring[NS];
+#pragma unroll
+        for (int k = 0; k < NS - 1; ++k) {
+            load(c0 + k, ring[k]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // steps past `last` (the ring's tail) multiply the zero step's patterns
+        for (std::uint32_t p = c0; p <= last; p += NS) {
+#pragma unroll
+            for (int k = 0; k < NS; ++k) {
+                load(p + k + NS - 1, ring[(k + NS - 1) % NS]);
+                __builtin_amdgcn_sched_barrier(0);
+                mma(ring[k]);
+            }
+        }
+    }
+
+    // D register r of tile t, N tile u: row 32t + 8(r/4) + 4lh + r%4 of the
+    // group, feature f0 + 32u + lj.
+    if (pslot != kNoSlot) {
+        float* base = a.partials + (static_cast<std::uint64_t>(pslot) * G * kTile + 4 * lh) * a.ldh + f0 + lj;
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+#pragma unroll
+                for (int u = 0; u < NT; ++u)
+                    base[static_cast<std::uint64_t>(32 * t + 8 * (r / 4) + r % 4) * a.ldh + 32 * u] = acc[t][u][r];
+        return;
+    }
+    // four rows at a time (one 16-byte load of their order and scales), their
+    // Y values loaded before any is stored
+    const std::uint64_t gs = static_cast<std::uint64_t>(g) * G * kTile + 4 * lh;
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+            const std::uint64_t s4 = gs + 32 * t + 8 * rq;
+            const vu4 rows = load_global<vu4>(a.rowOrder + s4);
+            const f32x4 rsc = a.rowScale ? load_global<vf4>(a.rowScale + s4) : f32x4{1.0f, 1.0f, 1.0f, 1.0f};
+            float y[4][NT];
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+#pragma unroll
+                for (int u = 0; u < NT; ++u) {
+                    const std::uint32_t f = f0 + 32 * u + lj;
+                    const bool live = rows[v] != TCC_SWTCF_INVALID_ROW_SLOT && f < a.F;
+                    y[v][u] = live ? a.Y[static_cast<std::uint64_t>(rows[v]) * a.F + f] : 0.0f;
+                }
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+#pragma unroll
+                for (int u = 0; u < NT; ++u) {
+                    const std::uint32_t f = f0 + 32 * u + lj;
+                    if (rows[v] != TCC_SWTCF_INVALID_ROW_SLOT && f < a.F)
+                        a.Y[static_cast<std::uint64_t>(rows[v]) * a.F + f] = y[v][u] + rsc[v] * acc[t][u][4 * rq + v];
+                }
+        }
+}
+
+// Y rows of a shared group += the sum of its units' partials (times the
+// row scales of binary tiles), one workgroup per (shared group, 64-feature
+// slice, row block j of the group): thread q sums row 16j + q/16, features
+// 4(q%16)..+3 of the slice over the group's units in unit order (their
+// slots are consecutive), sixteen loads in flight (the core's first groups
+// have dozens of units).
 __global__ void __launch_bounds__(kThreads) hub_reduce_kernel(TileArgs a, std::uint32_t G) {
-    const std::uint32_t blocksPerUnit = a.slices * G;
-    const std::uint32_t unit = blockIdx.x / blocksPerUnit, rest = blockIdx.x - unit * blocksPerUnit;
+    const std::uint32_t rslices = a.ldh / kSlice;
+    const std::uint32_t per = rslices * G;
+    const std::uint32_t sg = blockIdx.x / per, rest = blockIdx.x - sg * per;
     const std::uint32_t slice = rest / G, j = rest - slice * G;
-    const std::uint32_t g = a.units[3ull * unit], p0 = a.units[3ull * unit + 1];
-    const std::uint32_t gs0 = a.groupStepOffset[g], gs1 = a.groupStepOffset[g + 1];
-    if (p0 != gs0 || a.units[3ull * unit + 2] == gs1) return;  // not the first unit of a shared group
-    const std::uint32_t nu = (gs1 - gs0 + a.unitSteps - 1) / a.unitSteps;
+    const std::uint32_t g = a.sharedGroups[3ull * sg], slot0 = a.sharedGroups[3ull * sg + 1];
+    const std::uint32_t nu = a.sharedGroups[3ull * sg + 2];
     const std::uint32_t f = slice * kSlice + 4 * (threadIdx.x % 16);
     const unsigned r = 16 * j + threadIdx.x / 16;
     const std::uint64_t stride = static_cast<std::uint64_t>(G) * kTile * a.ldh;  // one unit's partials
-    const float* p = a.partials + (static_cast<std::uint64_t>(unit) * G * kTile + r) * a.ldh + f;
+    const float* p = a.partials + (static_cast<std::uint64_t>(slot0) * G * kTile + r) * a.ldh + f;
     constexpr std::uint32_t kIn = 16;
     f32x4 s[kIn];
 #pragma unroll
@@ -703,8 +974,10 @@ __global__ void __launch_bounds__(kThreads) hub_reduce_kernel(TileArgs a, std::u
     for (; k < nu; ++k) s[0] += load_global<vf4>(p + k * stride);
 #pragma unroll
     for (std::uint32_t i = 1; i < kIn; ++i) s[0] += s[i];
-    const std::uint32_t orow = a.rowOrder[static_cast<std::uint64_t>(g) * G * kTile + r];
+    const std::uint64_t slotRow = static_cast<std::uint64_t>(g) * G * kTile + r;
+    const std::uint32_t orow = a.rowOrder[slotRow];
     if (orow == TCC_SWTCF_INVALID_ROW_SLOT) return;
+    if (a.rowScale) s[0] *= a.rowScale[slotRow];
     const bool vec = a.F % 4 == 0 && (reinterpret_cast<std::uintptr_t>(a.Y) & 15u) == 0;
     add_quad(a.Y + static_cast<std::uint64_t>(orow) * a.F, f, a.F, vec, s[0]);
 }
@@ -732,41 +1005,45 @@ hipError_t launch_tiles(const TileArgs& a, bool split, hipStream_t st) {
     return hipGetLastError();
 }
 
-}  // namespace
-}  // namespace tcc
+// Binary tiles: G/2 32-row tiles by NT 32-feature N tiles of 16
+// accumulators (128 registers): one N tile at G = 16 (32 features a wave),
+// two at G = 8 (64 features a wave).
+constexpr int binary_nt(std::uint32_t G) { return G == 16 ? 1 : 2; }
+constexpr int kBinaryStages = 3;
 
-using namespace tcc;
-
-extern "C" {
-
-int tcc_hybrid_release(tcc_hybrid* H) {
-    clear_last_error();
-    if (!H) return TCC_OK;
-    if (H->tilesAllocation) TCC_HIP_CHECK(hipFree(H->tilesAllocation));
-    if (H->restAllocation) TCC_HIP_CHECK(hipFree(H->restAllocation));
-    std::memset(H, 0, sizeof(*H));
-    return TCC_OK;
+hipError_t launch_binary(const TileArgs& a, std::uint32_t G, hipStream_t st) {
+    const dim3 grid(kXcds * tiles_blocks_per_xcd(a.numUnits, a.slices));
+    if (G == 16)
+        hipLaunchKernelGGL((hub_tiles_binary_kernel<16, binary_nt(16), kBinaryStages>), grid, dim3(kThreads), 0, st, a);
+    else
+        hipLaunchKernelGGL((hub_tiles_binary_kernel<8, binary_nt(8), kBinaryStages>), grid, dim3(kThreads), 0, st, a);
+    return hipGetLastError();
 }
 
-int tcc_coo_to_hybrid(const std::uint32_t* dRow, const std::uint32_t* dCol, const float* dVal, std::uint32_t nnz,
-                      std::uint32_t numRows, std::uint32_t numCols, std::uint32_t minTileNnz, std::uint32_t groupBlocks,
-                      std::uint32_t unitSteps, std::uint32_t tileFormat, std::uint32_t phases, tcc_hybrid* out,
-                      void* stream) {
-    clear_last_error();
-    TCC_REQUIRE(out && numRows >= 1 && numCols >= 1 && (nnz == 0 || (dRow && dCol)), TCC_ERR_INVALID_ARGUMENT,
-                "invalid COO -> hybrid arguments");
-    if (minTileNnz == 0) minTileNnz = kDefaultMinTileNnz;
-    if (groupBlocks == 0) groupBlocks = kDefaultGroupBlocks;
-    if (unitSteps == 0) unitSteps = kDefaultUnitSteps;
-    TCC_REQUIRE(minTileNnz <= kTileVals, TCC_ERR_INVALID_ARGUMENT, "hybrid: minTileNnz above 256 leaves no tile");
-    TCC_REQUIRE(valid_group(groupBlocks), TCC_ERR_INVALID_ARGUMENT, "hybrid: groupBlocks must be 1, 2, 4 or 8");
-    TCC_REQUIRE(unitSteps <= kMaxUnitSteps, TCC_ERR_INVALID_ARGUMENT, "hybrid: unitSteps above 256");
-    TCC_REQUIRE(tileFormat == TCC_TILES_FP32 || tileFormat == TCC_TILES_BF16X2, TCC_ERR_INVALID_ARGUMENT,
-                "hybrid: unknown tileFormat");
+struct HybridParams {
+    const std::uint32_t* row;
+    const std::uint32_t* col;
+    const float* val;
+    std::uint32_t nnz;
+    std::uint32_t numRows;
+    std::uint32_t numCols;
+    std::uint32_t minStepNnz;
+    std::uint32_t minTileNnz;
+    std::uint32_t G;
+    std::uint32_t unitSteps;
+    std::uint32_t format;
+    std::uint32_t phases;
+    const float* rowScale;  // binary tiles
+    const float* colScale;
+};
+
+// The hub tiles and the remainder's (phased) BCSR of a device COO; see
+// tcc_coo_to_hybrid and tcc_coo_to_hybrid_scaled.
+int build_hybrid(const HybridParams& P, tcc_hybrid* out, void* stream) {
     const hipStream_t st = as_stream(stream);
+    const bool binary = P.format == TCC_TILES_BINARY;
     std::memset(out, 0, sizeof(*out));
-    const std::uint32_t E = nnz;
-    const std::uint32_t G = groupBlocks;
+    const std::uint32_t E = P.nnz, numRows = P.numRows, numCols = P.numCols, G = P.G;
     const std::uint32_t RB = (numRows + kTile - 1) / kTile;
     const std::uint32_t NG = (RB + G - 1) / G;
     const std::uint32_t rowSlots = NG * G * kTile;
@@ -832,8 +1109,8 @@ int tcc_coo_to_hybrid(const std::uint32_t* dRow, const std::uint32_t* dCol, cons
     // (tile count) are set below
     TCC_HIP_CHECK(fill<std::uint32_t>(dense, En, 0u, st));
     TCC_HIP_CHECK(fill<std::uint32_t>(stepHead, En, 0u, st));
-    TCC_HIP_CHECK(degree_histogram(dRow, E, numRows, rowDeg, small, st));
-    TCC_HIP_CHECK(degree_histogram(dCol, E, numCols, colDeg, small, st));
+    TCC_HIP_CHECK(degree_histogram(P.row, E, numRows, rowDeg, small, st));
+    TCC_HIP_CHECK(degree_histogram(P.col, E, numCols, colDeg, small, st));
     std::uint32_t hostSmall[8] = {};
     TCC_HIP_CHECK(hipMemcpyAsync(hostSmall, small, sizeof(hostSmall), hipMemcpyDeviceToHost, st));
     TCC_HIP_CHECK(hipStreamSynchronize(st));
@@ -844,8 +1121,8 @@ int tcc_coo_to_hybrid(const std::uint32_t* dRow, const std::uint32_t* dCol, cons
     std::uint64_t* sorted = keysA;
     std::uint32_t* perm = permA;
     if (E > 0) {
-        hipLaunchKernelGGL(tile_keys_kernel, dim3(grid_for(E, kThreads)), dim3(kThreads), 0, st, dRow, dCol, E, rowRank,
-                           colRank, CB, G, keysA, permA);
+        hipLaunchKernelGGL(tile_keys_kernel, dim3(grid_for(E, kThreads)), dim3(kThreads), 0, st, P.row, P.col, E,
+                           rowRank, colRank, CB, G, keysA, permA);
         TCC_LAUNCH_CHECK();
         TCC_HIP_CHECK(radix_sort_pairs(keysA, keysB, permA, permB, E, tileBits + 8, temp, &sorted, &perm, st));
         hipLaunchKernelGGL(tile_heads_kernel, dim3(grid_for(E, kThreads)), dim3(kThreads), 0, st, sorted, E, flags, small);
@@ -854,7 +1131,7 @@ int tcc_coo_to_hybrid(const std::uint32_t* dRow, const std::uint32_t* dCol, cons
         hipLaunchKernelGGL(tile_start_kernel, dim3(grid_for(E, kThreads)), dim3(kThreads), 0, st, flags, pos, E,
                            tileStart);
         hipLaunchKernelGGL(dense_tiles_kernel, dim3(grid_for(E, kThreads)), dim3(kThreads), 0, st, sorted, tileStart,
-                           small + 1, E, minTileNnz, CB, G, dense, small + 6, small + 5);
+                           small + 1, E, P.minTileNnz, P.minStepNnz, CB, G, dense, small + 6, small + 5);
         hipLaunchKernelGGL(step_heads_kernel, dim3(grid_for(E, kThreads)), dim3(kThreads), 0, st, sorted, tileStart,
                            small + 1, dense, G, CB, stepHead, groupSteps);
         TCC_LAUNCH_CHECK();
@@ -866,7 +1143,7 @@ int tcc_coo_to_hybrid(const std::uint32_t* dRow, const std::uint32_t* dCol, cons
         TCC_HIP_CHECK(exclusive_scan(restFlag, restPos, E, small + 3, temp, st));
     }
     hipLaunchKernelGGL(units_per_group_kernel, dim3(grid_for(NG, kThreads)), dim3(kThreads), 0, st, groupSteps, NG,
-                       unitSteps, unitCount);
+                       P.unitSteps, unitCount);
     TCC_LAUNCH_CHECK();
     TCC_HIP_CHECK(exclusive_scan(unitCount, unitCount, NG, small + 4, temp, st));
     TCC_HIP_CHECK(hipMemcpyAsync(hostSmall, small, sizeof(hostSmall), hipMemcpyDeviceToHost, st));
@@ -880,13 +1157,22 @@ int tcc_coo_to_hybrid(const std::uint32_t* dRow, const std::uint32_t* dCol, cons
     const std::uint32_t hubCols = std::min(hostSmall[5] * kTile, numCols);
 
     // tiles part: rowOrder[rowSlots] hubColOrder[hubCols] groupStepOffset[NG+1] unitFirst[NG+1] stepCol[NS]
-    // units[3 NU] unitOrder[NU] tileVals[256 G NS]
+    // units[3 NU] unitOrder[NU] unitPartial[NU] sharedGroups[3 NG] then the format's tiles (one more step, of
+    // zeros, that the kernels' ring tail reads): tileVals[256 G (NS+1)], or tileMasks[8 G (NS+1)] and the
+    // scales
     const std::uint64_t NSn = std::max<std::uint32_t>(NS, 1);
-    // tileVals holds one more step, of zeros (the kernel's ring tail reads it)
-    const std::size_t tilesBytes = align_up(4ull * rowSlots) + align_up(4ull * std::max(hubCols, 1u)) +
-                                   align_up(4ull * (NG + 1)) + align_up(4ull * (NG + 1)) + align_up(4 * NSn) +
-                                   align_up(12ull * std::max(NU, 1u)) + align_up(4ull * std::max(NU, 1u)) +
-                                   align_up(4ull * kTileVals * G * (NS + 1));
+    const std::uint64_t NUn = std::max<std::uint32_t>(NU, 1);
+    const std::uint32_t paddedRows = (numRows + 7) / 8 * 8;
+    std::size_t tilesBytes = align_up(4ull * rowSlots) + align_up(4ull * std::max(hubCols, 1u)) +
+                             align_up(4ull * (NG + 1)) + align_up(4ull * (NG + 1)) + align_up(4 * NSn) +
+                             align_up(12 * NUn) + align_up(4 * NUn) + align_up(4 * NUn) + align_up(12ull * NG);
+    if (binary) {
+        tilesBytes += align_up(32ull * G * (NS + 1));
+        if (P.rowScale) tilesBytes += align_up(4ull * rowSlots) + align_up(4ull * paddedRows);
+        if (P.colScale) tilesBytes += align_up(4ull * numCols);
+    } else {
+        tilesBytes += align_up(4ull * kTileVals * G * (NS + 1));
+    }
     char* o = nullptr;
     TCC_HIP_CHECK(hipMalloc(&o, tilesBytes));
     char* q = o;
@@ -900,19 +1186,47 @@ int tcc_coo_to_hybrid(const std::uint32_t* dRow, const std::uint32_t* dCol, cons
     auto* oGroupStepOffset = reinterpret_cast<std::uint32_t*>(takeOut(4ull * (NG + 1)));
     auto* oUnitFirst = reinterpret_cast<std::uint32_t*>(takeOut(4ull * (NG + 1)));
     auto* oStepCol = reinterpret_cast<std::uint32_t*>(takeOut(4 * NSn));
-    auto* oUnits = reinterpret_cast<std::uint32_t*>(takeOut(12ull * std::max(NU, 1u)));
-    auto* oUnitOrder = reinterpret_cast<std::uint32_t*>(takeOut(4ull * std::max(NU, 1u)));
-    auto* oTileVals = reinterpret_cast<float*>(takeOut(4ull * kTileVals * G * (NS + 1)));
+    auto* oUnits = reinterpret_cast<std::uint32_t*>(takeOut(12 * NUn));
+    auto* oUnitOrder = reinterpret_cast<std::uint32_t*>(takeOut(4 * NUn));
+    auto* oUnitPartial = reinterpret_cast<std::uint32_t*>(takeOut(4 * NUn));
+    auto* oSharedGroups = reinterpret_cast<std::uint32_t*>(takeOut(12ull * NG));
+    float* oTileVals = nullptr;
+    std::uint32_t* oTileMasks = nullptr;
+    float *oRowScale = nullptr, *oRestRowScale = nullptr, *oColScale = nullptr;
+    if (binary) {
+        oTileMasks = reinterpret_cast<std::uint32_t*>(takeOut(32ull * G * (NS + 1)));
+        if (P.rowScale) {
+            oRowScale = reinterpret_cast<float*>(takeOut(4ull * rowSlots));
+            oRestRowScale = reinterpret_cast<float*>(takeOut(4ull * paddedRows));
+        }
+        if (P.colScale) oColScale = reinterpret_cast<float*>(takeOut(4ull * numCols));
+    } else {
+        oTileVals = reinterpret_cast<float*>(takeOut(4ull * kTileVals * G * (NS + 1)));
+    }
     auto fail = [&](int rc) {
         (void)hipFree(o);
         return rc;
     };
-    if (hipMemcpyAsync(oRowOrder, rowOrder, 4ull * rowSlots, hipMemcpyDeviceToDevice, st) != hipSuccess ||
-        (hubCols && hipMemcpyAsync(oHubCols, colOrder, 4ull * hubCols, hipMemcpyDeviceToDevice, st) != hipSuccess) ||
-        exclusive_scan(groupSteps, oGroupStepOffset, NG, oGroupStepOffset + NG, temp, st) != hipSuccess ||
-        hipMemcpyAsync(oUnitFirst, unitCount, 4ull * NG, hipMemcpyDeviceToDevice, st) != hipSuccess ||
-        hipMemcpyAsync(oUnitFirst + NG, small + 4, 4, hipMemcpyDeviceToDevice, st) != hipSuccess ||
-        fill<float>(oTileVals, kTileVals * G * (NS + 1ull), 0.0f, st) != hipSuccess) {
+    bool ok = hipMemcpyAsync(oRowOrder, rowOrder, 4ull * rowSlots, hipMemcpyDeviceToDevice, st) == hipSuccess &&
+              (!hubCols || hipMemcpyAsync(oHubCols, colOrder, 4ull * hubCols, hipMemcpyDeviceToDevice, st) == hipSuccess) &&
+              exclusive_scan(groupSteps, oGroupStepOffset, NG, oGroupStepOffset + NG, temp, st) == hipSuccess &&
+              hipMemcpyAsync(oUnitFirst, unitCount, 4ull * NG, hipMemcpyDeviceToDevice, st) == hipSuccess &&
+              hipMemcpyAsync(oUnitFirst + NG, small + 4, 4, hipMemcpyDeviceToDevice, st) == hipSuccess;
+    if (binary) {
+        ok = ok && fill<std::uint32_t>(oTileMasks, 8ull * G * (NS + 1), 0u, st) == hipSuccess;
+        if (ok && P.rowScale) {
+            hipLaunchKernelGGL(ordered_scale_kernel, dim3(grid_for(rowSlots, kThreads)), dim3(kThreads), 0, st,
+                               oRowOrder, rowSlots, P.rowScale, oRowScale);
+            hipLaunchKernelGGL(padded_copy_kernel, dim3(grid_for(paddedRows, kThreads)), dim3(kThreads), 0, st,
+                               P.rowScale, numRows, paddedRows, oRestRowScale);
+        }
+        if (ok && P.colScale)
+            hipLaunchKernelGGL(padded_copy_kernel, dim3(grid_for(numCols, kThreads)), dim3(kThreads), 0, st,
+                               P.colScale, numCols, numCols, oColScale);
+    } else {
+        ok = ok && fill<float>(oTileVals, kTileVals * G * (NS + 1ull), 0.0f, st) == hipSuccess;
+    }
+    if (!ok || hipGetLastError() != hipSuccess) {
         set_last_error("HIP error while initialising the hub tiles");
         return fail(TCC_ERR_HIP);
     }
@@ -920,11 +1234,48 @@ int tcc_coo_to_hybrid(const std::uint32_t* dRow, const std::uint32_t* dCol, cons
         hipLaunchKernelGGL(tile_slots_kernel, dim3(grid_for(E, kThreads)), dim3(kThreads), 0, st, sorted, tileStart,
                            small + 1, dense, stepHead, stepPos, G, CB, slot, oStepCol);
         hipLaunchKernelGGL(place_entries_kernel, dim3(grid_for(E, kThreads)), dim3(kThreads), 0, st, sorted, perm, E,
-                           flags, pos, dense, slot, restPos, dRow, dCol, dVal, oTileVals,
-                           tileFormat == TCC_TILES_BF16X2, restRow, restCol, dVal ? restVal : nullptr);
+                           flags, pos, dense, slot, restPos, P.row, P.col, P.val, oTileVals, P.format, G, oTileMasks,
+                           restRow, restCol, P.val ? restVal : nullptr);
     }
     hipLaunchKernelGGL(group_units_kernel, dim3(grid_for(NG, kThreads)), dim3(kThreads), 0, st, oGroupStepOffset,
-                       oUnitFirst, NG, unitSteps, oUnits);
+                       oUnitFirst, NG, P.unitSteps, oUnits);
+    // partial-sum slots of the units of shared groups, and the shared groups
+    std::uint32_t shared[2] = {};  // units with a slot, shared groups
+    DevBuf<char> slotScratch;
+    {
+        const std::uint64_t n = std::max<std::uint64_t>(NU, NG) + 1;
+        const std::size_t bytes = 4 * align_up(4 * n) + align_up(4 * scan_temp_elems(n)) + 256;
+        if (hipMalloc(&slotScratch.p, bytes) != hipSuccess) {
+            set_last_error("out of device memory for the hub tiles' partial slots");
+            return fail(TCC_ERR_NO_MEMORY);
+        }
+        auto* groupShared = reinterpret_cast<std::uint32_t*>(slotScratch.p);
+        auto* groupPos = reinterpret_cast<std::uint32_t*>(slotScratch.p + align_up(4 * n));
+        auto* unitShared = reinterpret_cast<std::uint32_t*>(slotScratch.p + 2 * align_up(4 * n));
+        auto* unitPos = reinterpret_cast<std::uint32_t*>(slotScratch.p + 3 * align_up(4 * n));
+        auto* totals = reinterpret_cast<std::uint32_t*>(slotScratch.p + 4 * align_up(4 * n));
+        auto* scanTemp = reinterpret_cast<std::uint32_t*>(slotScratch.p + 4 * align_up(4 * n) + 256);
+        hipLaunchKernelGGL(shared_groups_kernel, dim3(grid_for(NG, kThreads)), dim3(kThreads), 0, st, oUnitFirst, NG,
+                           groupShared);
+        ok = exclusive_scan(groupShared, groupPos, NG, totals + 1, scanTemp, st) == hipSuccess;
+        if (ok && NU > 0) {
+            hipLaunchKernelGGL(shared_units_kernel, dim3(grid_for(NU, kThreads)), dim3(kThreads), 0, st, oUnits, NU,
+                               groupShared, unitShared);
+            ok = exclusive_scan(unitShared, unitPos, NU, totals, scanTemp, st) == hipSuccess;
+            hipLaunchKernelGGL(partial_slots_kernel, dim3(grid_for(NU, kThreads)), dim3(kThreads), 0, st, NU,
+                               unitShared, unitPos, oUnitPartial);
+            hipLaunchKernelGGL(shared_group_list_kernel, dim3(grid_for(NG, kThreads)), dim3(kThreads), 0, st,
+                               oUnitFirst, NG, groupShared, groupPos, unitPos, oSharedGroups);
+        } else if (ok) {
+            ok = fill<std::uint32_t>(totals, 1, 0u, st) == hipSuccess;
+        }
+        ok = ok && hipGetLastError() == hipSuccess &&
+             hipMemcpyAsync(shared, totals, sizeof(shared), hipMemcpyDeviceToHost, st) == hipSuccess;
+        if (!ok) {
+            set_last_error("HIP error while numbering the hub tiles' partial sums");
+            return fail(TCC_ERR_HIP);
+        }
+    }
     // launch order: units by the column block of their first step (stable)
     DevBuf<char> orderScratch;
     if (NU > 0) {
@@ -959,8 +1310,9 @@ int tcc_coo_to_hybrid(const std::uint32_t* dRow, const std::uint32_t* dCol, cons
     // the remainder: an ordinary or phased BCSR of the entries outside dense tiles
     tcc_bcsr rest{};
     void* restAlloc = nullptr;
-    const int rc = tcc_coo_to_bcsr_phased(NR ? restRow : nullptr, NR ? restCol : nullptr, dVal ? restVal : nullptr, NR,
-                                          numRows, numCols, phases, &rest, &restAlloc, stream);
+    const float* rv = P.val ? restVal : nullptr;
+    const int rc = tcc_coo_to_bcsr_phased(NR ? restRow : nullptr, NR ? restCol : nullptr, rv, NR, numRows, numCols,
+                                          P.phases, &rest, &restAlloc, stream);
     if (rc) return fail(rc);
     rest.unitBlocks = kRestUnitBlocks;
 
@@ -973,9 +1325,9 @@ int tcc_coo_to_hybrid(const std::uint32_t* dRow, const std::uint32_t* dCol, cons
     T.num_steps = NS;
     T.num_tiles = ND;
     T.num_units = NU;
-    T.unit_steps = unitSteps;
+    T.unit_steps = P.unitSteps;
     T.hub_cols = hubCols;
-    T.tile_format = tileFormat;
+    T.tile_format = P.format;
     T.rowOrder = oRowOrder;
     T.hubColOrder = oHubCols;
     T.groupStepOffset = oGroupStepOffset;
@@ -983,17 +1335,109 @@ int tcc_coo_to_hybrid(const std::uint32_t* dRow, const std::uint32_t* dCol, cons
     T.tileVals = oTileVals;
     T.units = oUnits;
     T.unitOrder = oUnitOrder;
+    T.num_partial_units = NU > 0 ? shared[0] : 0;
+    T.num_shared_groups = shared[1];
+    T.unitPartial = oUnitPartial;
+    T.sharedGroups = oSharedGroups;
+    T.tileMasks = oTileMasks;
+    T.rowScale = oRowScale;
+    T.colScale = oColScale;
     out->rest = rest;
     out->tilesAllocation = o;
     out->restAllocation = restAlloc;
+    out->restRowScale = oRestRowScale;
     return TCC_OK;
+}
+
+bool tiles_ok(const tcc_hub_tiles* T) {
+    if (T->tile_format == TCC_TILES_BINARY)
+        return valid_binary_group(T->group_blocks) && T->unit_steps >= 1 && T->tileMasks;
+    return (T->tile_format == TCC_TILES_FP32 || T->tile_format == TCC_TILES_BF16X2) && valid_group(T->group_blocks) &&
+           T->unit_steps >= 1 && T->unit_steps <= kMaxUnitSteps && T->tileVals;
+}
+
+}  // namespace
+}  // namespace tcc
+
+using namespace tcc;
+
+extern "C" {
+
+int tcc_hybrid_release(tcc_hybrid* H) {
+    clear_last_error();
+    if (!H) return TCC_OK;
+    if (H->tilesAllocation) TCC_HIP_CHECK(hipFree(H->tilesAllocation));
+    if (H->restAllocation) TCC_HIP_CHECK(hipFree(H->restAllocation));
+    std::memset(H, 0, sizeof(*H));
+    return TCC_OK;
+}
+
+int tcc_coo_to_hybrid(const std::uint32_t* dRow, const std::uint32_t* dCol, const float* dVal, std::uint32_t nnz,
+                      std::uint32_t numRows, std::uint32_t numCols, std::uint32_t minTileNnz, std::uint32_t groupBlocks,
+                      std::uint32_t unitSteps, std::uint32_t tileFormat, std::uint32_t phases, tcc_hybrid* out,
+                      void* stream) {
+    clear_last_error();
+    TCC_REQUIRE(out && numRows >= 1 && numCols >= 1 && (nnz == 0 || (dRow && dCol)), TCC_ERR_INVALID_ARGUMENT,
+                "invalid COO -> hybrid arguments");
+    if (minTileNnz == 0) minTileNnz = kDefaultMinTileNnz;
+    if (groupBlocks == 0) groupBlocks = kDefaultGroupBlocks;
+    if (unitSteps == 0) unitSteps = kDefaultUnitSteps;
+    TCC_REQUIRE(minTileNnz <= kTileVals, TCC_ERR_INVALID_ARGUMENT, "hybrid: minTileNnz above 256 leaves no tile");
+    TCC_REQUIRE(valid_group(groupBlocks), TCC_ERR_INVALID_ARGUMENT, "hybrid: groupBlocks must be 1, 2, 4 or 8");
+    TCC_REQUIRE(unitSteps <= kMaxUnitSteps, TCC_ERR_INVALID_ARGUMENT, "hybrid: unitSteps above 256");
+    TCC_REQUIRE(tileFormat == TCC_TILES_FP32 || tileFormat == TCC_TILES_BF16X2, TCC_ERR_INVALID_ARGUMENT,
+                "hybrid: tileFormat must be TCC_TILES_FP32 or TCC_TILES_BF16X2 (binary tiles: "
+                "tcc_coo_to_hybrid_scaled)");
+    HybridParams P{};
+    P.row = dRow;
+    P.col = dCol;
+    P.val = dVal;
+    P.nnz = nnz;
+    P.numRows = numRows;
+    P.numCols = numCols;
+    P.minStepNnz = 0;
+    P.minTileNnz = minTileNnz;
+    P.G = groupBlocks;
+    P.unitSteps = unitSteps;
+    P.format = tileFormat;
+    P.phases = phases;
+    return build_hybrid(P, out, stream);
+}
+
+int tcc_coo_to_hybrid_scaled(const std::uint32_t* dRow, const std::uint32_t* dCol, std::uint32_t nnz,
+                             std::uint32_t numRows, std::uint32_t numCols, const float* dRowScale,
+                             const float* dColScale, std::uint32_t minStepNnz, std::uint32_t groupBlocks,
+                             std::uint32_t unitSteps, std::uint32_t phases, tcc_hybrid* out, void* stream) {
+    clear_last_error();
+    TCC_REQUIRE(out && numRows >= 1 && numCols >= 1 && (nnz == 0 || (dRow && dCol)), TCC_ERR_INVALID_ARGUMENT,
+                "invalid COO -> hybrid arguments");
+    if (minStepNnz == 0) minStepNnz = kDefaultMinStepNnz;
+    if (groupBlocks == 0) groupBlocks = kDefaultBinaryGroupBlocks;
+    if (unitSteps == 0) unitSteps = kDefaultBinaryUnitSteps;
+    TCC_REQUIRE(valid_binary_group(groupBlocks), TCC_ERR_INVALID_ARGUMENT,
+                "hybrid: binary tiles take groupBlocks 8 or 16");
+    HybridParams P{};
+    P.row = dRow;
+    P.col = dCol;
+    P.nnz = nnz;
+    P.numRows = numRows;
+    P.numCols = numCols;
+    P.minStepNnz = minStepNnz;
+    P.minTileNnz = 1;  // every entry of a chosen step
+    P.G = groupBlocks;
+    P.unitSteps = unitSteps;
+    P.format = TCC_TILES_BINARY;
+    P.phases = phases;
+    P.rowScale = dRowScale;
+    P.colScale = dColScale;
+    return build_hybrid(P, out, stream);
 }
 
 size_t tcc_hub_tiles_workspace_bytes(const tcc_hub_tiles* T, std::uint32_t featureDim) {
     if (!T || featureDim == 0) return 0;
     const std::size_t ldh = hub_ldh(featureDim);
     return align_up(static_cast<size_t>(hub_rows(T->hub_cols)) * ldh * sizeof(float)) +
-           static_cast<size_t>(T->num_units) * T->group_blocks * kTile * ldh * sizeof(float);
+           static_cast<size_t>(T->num_partial_units) * T->group_blocks * kTile * ldh * sizeof(float);
 }
 
 size_t tcc_hybrid_workspace_bytes(const tcc_hybrid* H, std::uint32_t featureDim) {
@@ -1008,12 +1452,13 @@ int tcc_hub_tiles_spmm(const tcc_hub_tiles* T, const float* X, float* Y, std::ui
     TCC_REQUIRE(T && X && Y && featureDim >= 1 && T->rowOrder && T->groupStepOffset, TCC_ERR_INVALID_ARGUMENT,
                 "invalid hub tiles SpMM arguments");
     if (T->num_units == 0) return TCC_OK;
-    TCC_REQUIRE(T->stepCol && T->tileVals && T->units && T->hubColOrder, TCC_ERR_INVALID_ARGUMENT,
-                "invalid hub tiles SpMM arguments");
-    TCC_REQUIRE(valid_group(T->group_blocks) && T->unit_steps >= 1 && T->unit_steps <= kMaxUnitSteps,
-                TCC_ERR_INVALID_ARGUMENT, "hub tiles: group_blocks must be 1, 2, 4 or 8 and unit_steps 1..256");
-    TCC_REQUIRE(T->tile_format == TCC_TILES_FP32 || T->tile_format == TCC_TILES_BF16X2, TCC_ERR_INVALID_ARGUMENT,
-                "hub tiles: unknown tile_format");
+    TCC_REQUIRE(T->stepCol && T->units && T->hubColOrder && T->unitPartial &&
+                    (T->num_shared_groups == 0 || T->sharedGroups),
+                TCC_ERR_INVALID_ARGUMENT, "invalid hub tiles SpMM arguments");
+    TCC_REQUIRE(tiles_ok(T), TCC_ERR_INVALID_ARGUMENT,
+                "hub tiles: group_blocks must be 1, 2, 4 or 8 and unit_steps 1..256 (binary tiles: 8 or 16, any "
+                "unit_steps), with the arrays of a known tile_format");
+    const bool binary = T->tile_format == TCC_TILES_BINARY;
     const bool split = T->tile_format == TCC_TILES_BF16X2;
     const std::uint32_t ldh = hub_ldh(featureDim);
     TCC_REQUIRE(workspace && workspaceBytes >= tcc_hub_tiles_workspace_bytes(T, featureDim) &&
@@ -1023,9 +1468,10 @@ int tcc_hub_tiles_spmm(const tcc_hub_tiles* T, const float* X, float* Y, std::ui
     float* Xh = static_cast<float*>(workspace);
     const std::uint32_t hubRows = hub_rows(T->hub_cols);
     const std::uint64_t n = static_cast<std::uint64_t>(hubRows) * ldh;
-    if (split) {
+    if (split || binary) {
         hipLaunchKernelGGL(hub_rows_split_kernel, dim3(grid_for(n / kTile, kThreads)), dim3(kThreads), 0, st, X,
-                           featureDim, T->hubColOrder, T->hub_cols, hubRows, ldh, reinterpret_cast<std::uint16_t*>(Xh));
+                           featureDim, T->hubColOrder, T->hub_cols, hubRows, ldh, binary ? T->colScale : nullptr,
+                           reinterpret_cast<std::uint16_t*>(Xh));
     } else {
         const bool vecX = featureDim % 4 == 0 && (reinterpret_cast<std::uintptr_t>(X) & 15u) == 0;
         hipLaunchKernelGGL(hub_rows_kernel, dim3(grid_for(n / 4, kThreads)), dim3(kThreads), 0, st, X, featureDim,
@@ -1037,7 +1483,11 @@ int tcc_hub_tiles_spmm(const tcc_hub_tiles* T, const float* X, float* Y, std::ui
     a.groupStepOffset = T->groupStepOffset;
     a.stepCol = T->stepCol;
     a.tileVals = T->tileVals;
+    a.tileMasks = T->tileMasks;
+    a.rowScale = binary ? T->rowScale : nullptr;
     a.units = T->units;
+    a.unitPartial = T->unitPartial;
+    a.sharedGroups = T->sharedGroups;
     a.unitOrder = T->unitOrder;
     a.Xh = Xh;
     a.ldh = ldh;
@@ -1046,19 +1496,23 @@ int tcc_hub_tiles_spmm(const tcc_hub_tiles* T, const float* X, float* Y, std::ui
     a.zeroStep = T->num_steps;
     a.F = featureDim;
     a.numUnits = T->num_units;
-    a.slices = ldh / kSlice;
-    a.unitSteps = T->unit_steps;
+    a.slices = ldh / (binary ? 32u * binary_nt(T->group_blocks) : kSlice);
     const std::uint64_t waves = static_cast<std::uint64_t>(a.numUnits) * a.slices;
     TCC_REQUIRE(waves <= 0x7FFFFFFFull, TCC_ERR_UNSUPPORTED, "hub tiles SpMM launch too large");
     hipError_t e;
-    switch (T->group_blocks) {
-        case 1: e = launch_tiles<1>(a, split, st); break;
-        case 2: e = launch_tiles<2>(a, split, st); break;
-        case 4: e = launch_tiles<4>(a, split, st); break;
-        default: e = launch_tiles<8>(a, split, st); break;
+    if (binary) {
+        e = launch_binary(a, T->group_blocks, st);
+    } else {
+        switch (T->group_blocks) {
+            case 1: e = launch_tiles<1>(a, split, st); break;
+            case 2: e = launch_tiles<2>(a, split, st); break;
+            case 4: e = launch_tiles<4>(a, split, st); break;
+            default: e = launch_tiles<8>(a, split, st); break;
+        }
     }
     TCC_HIP_CHECK(e);
-    const std::uint64_t reduceBlocks = waves * T->group_blocks;
+    if (T->num_shared_groups == 0) return TCC_OK;
+    const std::uint64_t reduceBlocks = static_cast<std::uint64_t>(T->num_shared_groups) * (ldh / kSlice) * T->group_blocks;
     TCC_REQUIRE(reduceBlocks <= 0x7FFFFFFFull, TCC_ERR_UNSUPPORTED, "hub tiles SpMM launch too large");
     hipLaunchKernelGGL(hub_reduce_kernel, dim3(static_cast<std::uint32_t>(reduceBlocks)), dim3(kThreads), 0, st, a,
                        T->group_blocks);
@@ -1075,16 +1529,22 @@ int tcc_hybrid_spmm(const tcc_hybrid* H, const float* X, float* Y, std::uint32_t
                 TCC_ERR_INVALID_ARGUMENT, "hybrid SpMM workspace too small or misaligned (tcc_hybrid_workspace_bytes)");
     // The remainder's product writes (or adds into) Y, over packed TF32 rows
     // when its rows are gathered often (8 blocks per column on average,
-    // 16 gathers per row), else over X; then the tiles add theirs.
+    // 16 gathers per row) or its columns are scaled, else over X; then the
+    // tiles add theirs.  Binary tiles' scales apply to the remainder too:
+    // column scales while packing, row scales to each row's sum.
+    const bool binary = H->tiles.tile_format == TCC_TILES_BINARY;
+    const float* colScale = binary ? H->tiles.colScale : nullptr;
+    const float* rowScale = binary ? H->restRowScale : nullptr;
+    const hipStream_t st = as_stream(stream);
     const std::uint64_t gathers = 8ull * H->rest.num_TCBlocks;
     const std::size_t packedBytes = align_up(tcc_tf32_packed_bytes(H->rest.num_cols, featureDim) + 16);
     int rc;
-    if (gathers >= 16ull * H->rest.num_cols) {
-        rc = tcc_tf32_pack(X, H->rest.num_cols, featureDim, workspace, stream);
+    if (colScale || gathers >= 16ull * H->rest.num_cols) {
+        rc = tf32_pack_scaled(X, H->rest.num_cols, featureDim, colScale, workspace, st);
         if (rc) return rc;
-        rc = tcc_bcsr_spmm_packed(&H->rest, workspace, Y, featureDim, accumulate, stream);
+        rc = bcsr_spmm_packed_scaled(&H->rest, workspace, Y, featureDim, accumulate, rowScale, st);
     } else {
-        rc = tcc_bcsr_spmm(&H->rest, X, Y, featureDim, accumulate, stream);
+        rc = bcsr_spmm_scaled(&H->rest, X, Y, featureDim, accumulate, rowScale, st);
     }
     if (rc) return rc;
     return tcc_hub_tiles_spmm(&H->tiles, X, Y, featureDim, static_cast<char*>(workspace) + packedBytes,

@@ -75,6 +75,17 @@ def sym_norm_values(rows: torch.Tensor, cols: torch.Tensor, n: int) -> torch.Ten
     return (1.0 / torch.sqrt(rd[rows] * cd[cols])).to(torch.float32)
 
 
+def sym_norm_scales(rows: torch.Tensor, cols: torch.Tensor, n: int):
+    """(r, c) fp32 with r_i = rowdeg_i^-1/2, c_j = coldeg_j^-1/2 (0 for an
+    empty row or column): sym_norm_values' v_ij = r_i c_j as row and column
+    scales (each fp32 product within 2 ulp of v_ij)."""
+    rd = torch.bincount(rows, minlength=n).to(torch.float64)
+    cd = torch.bincount(cols, minlength=n).to(torch.float64)
+    r = torch.where(rd > 0, 1.0 / torch.sqrt(rd.clamp_min(1.0)), torch.zeros_like(rd))
+    c = torch.where(cd > 0, 1.0 / torch.sqrt(cd.clamp_min(1.0)), torch.zeros_like(cd))
+    return r.to(torch.float32), c.to(torch.float32)
+
+
 def to_csr_numpy(rows: torch.Tensor, cols: torch.Tensor, n_rows: int, vals: torch.Tensor | None = None):
     """(rowptr int64, colind uint32, vals float32|None) of edges sorted by (row, col)."""
     r = rows.cpu().numpy().astype(np.int64)

@@ -12,14 +12,14 @@ import numpy as np
 import torch
 
 from . import _lib
-from ._lib import BCSC, BCSR, SWBCSR, FeatureSource, Hybrid, SWTCFMatrix, SWTCFWorkspace, check
+from ._lib import BCSC, BCSR, FeatureSource, Hybrid, SWTCFMatrix, SWTCFWorkspace, check
 
 INVALID_ROW_SLOT = 0xFFFFFFFF
 INVALID_CACHE_SLOT = 0xFF
 REPEAT_CACHE_SIZE = 32
 DEFAULT_TC_THRESHOLD = 12
 DEVERR_FEATURE_INDEX = 7  # TCC_DEVERR_FEATURE_INDEX
-TILES_FP32, TILES_BF16X2 = 0, 1  # TCC_TILES_*
+TILES_FP32, TILES_BF16X2, TILES_BINARY = 0, 1, 2  # TCC_TILES_*
 FEATURE_DIM = 128
 
 
@@ -342,66 +342,6 @@ def bcsr_spmm_packed(A: BlockMatrix, packed: torch.Tensor, F: int, Y: torch.Tens
     return Y
 
 
-class SuperWindowBCSR:
-    """A row super-window BCSR built on the device by tcc_coo_to_sw_bcsr
-    (owns one allocation): rows in degree order, 64 per super-window, each
-    super-window's distinct columns with 64-bit row masks."""
-
-    def __init__(self, view: SWBCSR, allocation):
-        self.view = view
-        self._alloc = allocation
-
-    def release(self) -> None:
-        if self._alloc:
-            check(_lib.lib().tcc_block_release(self._alloc))
-            self._alloc = None
-
-    def __del__(self):
-        try:
-            self.release()
-        except Exception:
-            pass
-
-    def to_host(self) -> dict:
-        torch.cuda.synchronize()
-        v = self.view
-        G, P, U = v.num_groups, v.num_pairs, v.num_units
-        return {
-            "rowOrder": _download(v.rowOrder, 64 * G, np.uint32),
-            "groupOffset": _download(v.groupOffset, G + 1, np.uint32),
-            "pairCol": _download(v.pairCol, P, np.uint32),
-            "pairMask": _download(v.pairMask, P, np.uint64),
-            "pairValue": _download(v.pairValue, P, np.uint32) if v.data else None,
-            "data": _download(v.data, v.nnz, np.float32) if v.data else None,
-            "units": _download(v.units, 3 * U, np.uint32).reshape(U, 3),
-            "num_rows": v.num_rows, "num_cols": v.num_cols, "nnz": v.nnz, "num_groups": G, "num_pairs": P,
-            "num_units": U, "unit_pairs": v.unit_pairs, "num_phases": v.num_phases,
-        }
-
-
-def coo_to_sw_bcsr(row: torch.Tensor, col: torch.Tensor, val: torch.Tensor | None, num_rows: int, num_cols: int,
-                   unit_pairs: int = 0, phases: int = 1, stream=None) -> SuperWindowBCSR:
-    """The row super-window BCSR of the COO matrix (tcc_coo_to_sw_bcsr)."""
-    view = SWBCSR()
-    alloc = ctypes.c_void_p()
-    check(_lib.lib().tcc_coo_to_sw_bcsr(_u32(row).data_ptr() if row.numel() else None,
-                                        _u32(col).data_ptr() if col.numel() else None, _ptr(val), row.numel(),
-                                        num_rows, num_cols, int(unit_pairs), int(phases), ctypes.byref(view),
-                                        ctypes.byref(alloc),
-                                        _stream(stream)))
-    return SuperWindowBCSR(view, alloc.value)
-
-
-def sw_bcsr_spmm_packed(A: SuperWindowBCSR, packed: torch.Tensor, F: int, Y: torch.Tensor | None = None,
-                        accumulate: bool = False, stream=None) -> torch.Tensor:
-    """Y[num_rows x F] (=|+=) A X with X packed by tf32_pack."""
-    if Y is None:
-        Y = torch.empty((A.view.num_rows, F), dtype=torch.float32, device=packed.device)
-    check(_lib.lib().tcc_sw_bcsr_spmm_packed(ctypes.byref(A.view), packed.data_ptr(), Y.data_ptr(), F,
-                                             int(accumulate), _stream(stream)))
-    return Y
-
-
 class HybridMatrix:
     """Dense hub tiles (MFMA) + the remainder's BCSR, built on the device by
     tcc_coo_to_hybrid; owns both allocations."""
@@ -432,20 +372,35 @@ class HybridMatrix:
         torch.cuda.synchronize()
         t = self.view.tiles
         G, NG, S, U = t.group_blocks, t.num_groups, t.num_steps, t.num_units
-        return {
+        NSG = t.num_shared_groups
+        d = {
             "rowOrder": _download(t.rowOrder, 16 * G * NG, np.uint32),
             "hubColOrder": _download(t.hubColOrder, t.hub_cols, np.uint32),
             "groupStepOffset": _download(t.groupStepOffset, NG + 1, np.uint32),
             "stepCol": _download(t.stepCol, S, np.uint32),
-            "tileVals": (_download(t.tileVals, 256 * G * S, np.float32).reshape(S, G, 64, 4) if t.tile_format == TILES_FP32
-                         else _download(t.tileVals, 512 * G * S, np.uint16).reshape(S, G, 2, 16, 16)),
             "tile_format": t.tile_format,
             "units": _download(t.units, 3 * U, np.uint32).reshape(U, 3),
             "unitOrder": _download(t.unitOrder, U, np.uint32),
+            "unitPartial": _download(t.unitPartial, U, np.uint32),
+            "sharedGroups": _download(t.sharedGroups, 3 * NSG, np.uint32).reshape(NSG, 3),
+            "num_partial_units": t.num_partial_units, "num_shared_groups": NSG,
             "group_blocks": G, "num_groups": NG, "num_steps": S, "num_tiles": t.num_tiles, "num_units": U,
             "hub_cols": t.hub_cols, "tile_nnz": t.nnz, "unit_steps": t.unit_steps,
             "rest": self.rest.to_host(),
         }
+        if t.tile_format == TILES_BINARY:
+            # step p's G*32 bytes (with the zero step after the last)
+            d["tileMasks"] = _download(t.tileMasks, 8 * G * (S + 1), np.uint32).view(np.uint8).reshape(S + 1, 32 * G)
+            d["rowScale"] = None if not t.rowScale else _download(t.rowScale, 16 * G * NG, np.float32)
+            d["colScale"] = None if not t.colScale else _download(t.colScale, t.num_cols, np.float32)
+            n8 = (t.num_rows + 7) // 8 * 8
+            d["restRowScale"] = None if not self.view.restRowScale else _download(self.view.restRowScale, n8,
+                                                                                   np.float32)
+        elif t.tile_format == TILES_FP32:
+            d["tileVals"] = _download(t.tileVals, 256 * G * S, np.float32).reshape(S, G, 64, 4)
+        else:
+            d["tileVals"] = _download(t.tileVals, 512 * G * S, np.uint16).reshape(S, G, 2, 16, 16)
+        return d
 
 
 def coo_to_hybrid(row: torch.Tensor, col: torch.Tensor, val: torch.Tensor | None, num_rows: int, num_cols: int,
@@ -457,6 +412,27 @@ def coo_to_hybrid(row: torch.Tensor, col: torch.Tensor, val: torch.Tensor | None
                                        _u32(col).data_ptr() if col.numel() else None, _ptr(val), row.numel(),
                                        num_rows, num_cols, int(min_tile_nnz), int(group_blocks), int(unit_steps),
                                        int(tile_format), int(phases), ctypes.byref(view), _stream(stream)))
+    return HybridMatrix(view)
+
+
+def coo_to_hybrid_scaled(row: torch.Tensor, col: torch.Tensor, num_rows: int, num_cols: int,
+                         row_scale: torch.Tensor | None = None, col_scale: torch.Tensor | None = None,
+                         min_step_nnz: int = 0, group_blocks: int = 0, unit_steps: int = 0, phases: int = 1,
+                         stream=None) -> HybridMatrix:
+    """Binary hub tiles + pattern remainder of diag(row_scale) P diag(col_scale),
+    P the COO's pattern (tcc_coo_to_hybrid_scaled); the scales are copied."""
+    rs = None if row_scale is None else _f32(row_scale.reshape(-1), "row_scale")
+    cs = None if col_scale is None else _f32(col_scale.reshape(-1), "col_scale")
+    if rs is not None and rs.shape[0] != num_rows:
+        raise ValueError("row_scale must have num_rows entries")
+    if cs is not None and cs.shape[0] != num_cols:
+        raise ValueError("col_scale must have num_cols entries")
+    view = Hybrid()
+    check(_lib.lib().tcc_coo_to_hybrid_scaled(_u32(row).data_ptr() if row.numel() else None,
+                                              _u32(col).data_ptr() if col.numel() else None, row.numel(),
+                                              num_rows, num_cols, _ptr(rs), _ptr(cs), int(min_step_nnz),
+                                              int(group_blocks), int(unit_steps), int(phases), ctypes.byref(view),
+                                              _stream(stream)))
     return HybridMatrix(view)
 
 

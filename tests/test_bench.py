@@ -51,7 +51,8 @@ def test_roofline_config3_is_fp32_bound():
     assert abs(r["achieved"] - flops / 1e-2 / 1e12) < 1e-3
     # frac = (flops / t) / min(157.3 TF, AI * 8 TB/s)
     assert abs(r["frac"] - (flops / 1e-2) / min(157.3e12, flops / b * 8e12)) < 1e-4
-    assert r["traffic"] is None and "dram" not in r
+    assert r["traffic"] is None and "l2_fabric_traffic" not in r
+    assert abs(r["hbm_fraction_alg"] - b / 1e-2 / 8e12) < 1e-4
 
 
 def test_roofline_config2_is_hbm_bound():
@@ -65,7 +66,8 @@ def test_roofline_config2_is_hbm_bound():
     assert abs(r["achieved"] - b / 0.08e-3 / 1e9) < 1e-2
     assert abs(r["frac"] - (flops / 0.08e-3) / min(157.3e12, flops / b * 8e12)) < 1e-4
     assert r["traffic"] == 4e8
-    assert abs(r["dram"]["GBps"] - 4e8 / 0.08e-3 / 1e9) < 0.1
+    assert abs(r["l2_fabric_traffic"]["GBps"] - 4e8 / 0.08e-3 / 1e9) < 0.1
+    assert abs(r["hbm_fraction_alg"] - b / 0.08e-3 / 8e12) < 1e-4
 
 
 def test_traffic_files_name_their_sources():

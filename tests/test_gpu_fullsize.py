@@ -16,7 +16,8 @@ Three checks, each able to see a misrouted row:
   a seeded sample of output rows holding at least 1M nonzeros (the hub row
   included), element by element at rel-L2 <= 1e-5 (north_star bound 1e-3).
 - Every config-3 format the bench or the API offers (BCSR, 4-phase BCSR,
-  row super-window BCSR, dense hub tiles + remainder).
+  valued hub tiles + remainder, binary hub tiles with the sym-norm values as
+  row and column scales + remainder).
 - The converter: the 114M-edge SWTCF of config 3 against the C oracle's
   canonical form, every array bit for bit.
 
@@ -174,24 +175,6 @@ def test_fullsize_config3_bcsr(gpu, oracle):
     check_weighted(oracle, Yf, n, rows, cols, v, n, Xh, 31, what="config 3 fp32 gather")
 
 
-def test_fullsize_config3_super_window(gpu, oracle):
-    """The row super-window BCSR at config 3 (degree-sorted rows, 64-row
-    super-windows, 4 column phases)."""
-    from tcc_amd import swtcf
-
-    n, F, r32, c32, vals, X = graph(3)
-    rows, cols, v = r32.cpu().numpy(), c32.cpu().numpy(), vals.cpu().numpy()
-    Xh = X.cpu().numpy()
-    P = swtcf.tf32_pack(X)
-    S = swtcf.coo_to_sw_bcsr(r32, c32, vals, n, n, phases=4)
-    print(f"config 3 super-window BCSR: {S.view.num_pairs} pairs, {S.view.num_units} units", flush=True)
-    Y = swtcf.sw_bcsr_spmm_packed(S, P, F)
-    r_dev, want = check_weighted(oracle, Y, n, rows, cols, v, n, Xh, 33, what="config 3 super-window")
-    hub = int(np.argmax(np.bincount(rows, minlength=n)))
-    check_swap_fails(Y, n, r_dev, want, hub, (hub + 3) % n, what="config 3 super-window")
-    check_rows(oracle, Y, rows, cols, v, n, Xh, 34, what="config 3 super-window")
-
-
 @pytest.mark.parametrize("min_nnz, G, split", [(16, 8, True), (32, 4, False)])
 def test_fullsize_config3_hybrid(gpu, oracle, min_nnz, G, split):
     """The bench's path at config 3: dense hub tiles (>= 16 nnz, groups of 8
@@ -220,10 +203,73 @@ def test_fullsize_config3_hybrid(gpu, oracle, min_nnz, G, split):
     check_weighted(oracle, Y2 * 0.5, n, rows, cols, v, n, Xh, 35, what="config 3 hybrid, accumulate")
 
 
+def test_fullsize_config3_binary_hybrid(gpu, oracle):
+    """The bench's path at config 3: binary hub tiles (steps of >= 64
+    entries, groups of 16 row blocks) with the sym-normalised values as row
+    and column scales, plus the packed gather of the remainder's pattern
+    over its 4-phase BCSR.  The reference numerics of this form are
+    r_i sum_j P_ij TF32(fp32(c_j X_j)): the weighted checksum and the oracle
+    rows are taken against them (rel-L2 <= 1e-5), and the oracle rows also
+    against the TF32 CSR oracle over the values (north_star bound 1e-3).
+    Y = AX and Y += AX."""
+    from tcc_amd import swtcf
+    from tcc_amd.graphs import sym_norm_scales
+
+    n, F, r32, c32, vals, X = graph(3)
+    rows_t, cols_t = r32.long(), c32.long()
+    rs, cs = sym_norm_scales(rows_t, cols_t, n)
+    rows, cols, v = r32.cpu().numpy(), c32.cpu().numpy(), vals.cpu().numpy()
+    r_np, c_np = rs.cpu().numpy(), cs.cpu().numpy()
+    H = swtcf.coo_to_hybrid_scaled(r32, c32, n, n, rs, cs, min_step_nnz=64, group_blocks=16, phases=4)
+    t = H.view.tiles
+    print(f"config 3 binary hybrid: {t.num_steps} steps, {t.nnz} tile entries, {H.rest.view.nnz} in the remainder, "
+          f"{t.num_units} units ({t.num_partial_units} with partial sums)", flush=True)
+    assert t.nnz + H.rest.view.nnz == r32.numel() and t.nnz > r32.numel() // 2
+    Y = swtcf.hybrid_spmm(H, X)
+    Xh = X.cpu().numpy()
+    Xs = oracle.tf32((Xh * c_np[:, None]).astype(np.float32))  # TF32(fp32(c_j X_j))
+    w = weights(n, 37)
+    w_dev = torch.from_numpy(w).cuda()
+    want = np.bincount(cols, weights=w[rows] * r_np[rows].astype(np.float64), minlength=n) @ Xs.astype(np.float64)
+    e = rel_l2(weighted_got(Y, w_dev, n), want)
+    print(f"config 3 binary hybrid: weighted checksum rel-L2 {e:.2e}", flush=True)
+    assert e <= TOL
+    hub = int(np.argmax(np.bincount(rows, minlength=n)))
+    check_swap_fails(Y, n, w_dev, want, hub, (hub + 5) % n, what="config 3 binary hybrid")
+    # oracle rows: the pattern over TF32(c X), times r
+    sel = sample_rows(rows, n, 38)
+    keep = np.isin(rows, sel)
+    rr, cc, vv = rows[keep], cols[keep], v[keep]
+    pos = np.searchsorted(sel, rr)
+    order = np.lexsort((cc, pos))
+    rowptr = np.zeros(sel.size + 1, np.int64)
+    np.cumsum(np.bincount(pos, minlength=sel.size), out=rowptr[1:])
+    ref = oracle.csr_spmm(rowptr, cc[order].astype(np.uint32), None, Xs, use_tf32=True) * \
+        r_np[sel, None].astype(np.float64)
+    got = Y[torch.from_numpy(sel).cuda()].cpu().numpy()
+    e = rel_l2(got, ref)
+    ref_v = oracle.csr_spmm(rowptr, cc[order].astype(np.uint32), vv[order], Xh, use_tf32=True)
+    e_v = rel_l2(got, ref_v)
+    print(f"config 3 binary hybrid: {sel.size} rows, {int(keep.sum())} nnz: rel-L2 {e:.2e} against r TF32(c X), "
+          f"{e_v:.2e} against the TF32 CSR oracle over the values", flush=True)
+    assert int(keep.sum()) >= SAMPLE_NNZ
+    assert e <= ROW_TOL
+    assert e_v <= 1e-3
+    Y2 = Y.clone()
+    swtcf.hybrid_spmm(H, X, Y2, accumulate=True)
+    e = rel_l2(weighted_got(Y2 * 0.5, w_dev, n), want)
+    print(f"config 3 binary hybrid, accumulate: weighted checksum rel-L2 {e:.2e}", flush=True)
+    assert e <= TOL
+
+
 def test_fullsize_config3_swtcf_bit_exact(gpu, oracle):
     """convertCOOToSWTCF of the config-3 graph (114M edges, S = 16) against
-    the C oracle's canonical form, every array bit for bit; then the SWTCF
-    SpMM (F = 128) through the weighted checksum."""
+    the C oracle's canonical form, every array bit for bit, for the COO in
+    the generator's (dst, src) order (the sort's super-window digits alone
+    order it) and for the same COO under a seeded permutation (every digit
+    runs: the per-super-window low passes of a COO out of order); the
+    canonical form does not depend on the input order.  Then the SWTCF SpMM
+    (F = 128) through the weighted checksum."""
     from tcc_amd import swtcf
     from tcc_amd.graphs import CONFIGS, make_graph
 
@@ -249,6 +295,17 @@ def test_fullsize_config3_swtcf_bit_exact(gpu, oracle):
     for k, vv in want.items():
         assert np.array_equal(got[k], vv), f"SWTCF array {k} differs from the oracle"
     print(f"bit-exact: {got['numTiles']} tiles, {got['numRows']} super-window rows", flush=True)
+    del got
+    perm = torch.randperm(nnz, device="cuda", generator=torch.Generator(device="cuda").manual_seed(77))
+    ms = swtcf.DeviceSWTCFMatrix(n, n, nnz, 16)
+    swtcf.convertCOOToSWTCF(r32[perm].contiguous(), c32[perm].contiguous(), nnz, ms, ws)
+    del perm
+    assert ws.device_error() == 0
+    got = ms.to_host()
+    for k, vv in want.items():
+        assert np.array_equal(got[k], vv), f"SWTCF array {k} of the shuffled COO differs from the oracle"
+    print("shuffled COO: bit-exact", flush=True)
+    ms.free()
     del want, got
 
     F = 128
