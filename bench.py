@@ -481,6 +481,63 @@ def bench_convert(args, torch, swtcf, cfg):
     return out
 
 
+def extension_timings(torch, swtcf, r32, c32, n, F, X):
+    """Config 3 through the reference's own entry point, spmm_cnic's
+    forward_tensorcore (train/tcgnn_conv_release.py:124-130), called
+    unchanged on the whole graph as a BCSR (values not read, as the
+    reference's kernels read none; an empty BCSC): the default path (x packed
+    to TF32 rows when rows are gathered >= 16 times) and a per-graph plan
+    (set_graph_plans), with the plan's one-time build."""
+    sys.path.insert(0, os.path.join(ROOT, "tcc_amd"))
+    try:
+        import spmm_cnic
+    finally:
+        sys.path.pop(0)
+
+    import numpy as np
+
+    def tensors(d, kind):
+        def dev(arr):
+            arr = np.ascontiguousarray(arr)
+            view = np.int32 if arr.dtype == np.uint32 else (np.int64 if arr.dtype == np.uint64 else arr.dtype)
+            return torch.from_numpy(arr.view(view)).cuda()
+
+        w, i = ("rowWindowOffset", "sparseA2B") if kind == "bcsr" else ("colWindowOffset", "sparseA2C")
+        nw = d["num_rowWindows"] if kind == "bcsr" else d["num_colWindows"]
+        return [d["num_rows"], d["num_cols"], d["nnz"], d["num_TCBlocks"], nw, dev(d[w]), dev(d["tcOffset"]),
+                dev(d[i]), dev(d["tcLocalBit"]), torch.zeros(1, device="cuda")]
+
+    A = swtcf.coo_to_bcsr(r32, c32, None, n, n)
+    B = swtcf.coo_to_bcsc(r32[:0], c32[:0], None, n, n)
+    args = tensors(A.to_host(), "bcsr") + tensors(B.to_host(), "bcsc")
+    A.release()
+    B.release()
+    x = X.flatten()
+    flops = 2.0 * r32.numel() * F
+    out = {"entry": "spmm_cnic.forward_tensorcore (Python-caller form), whole graph as BCSR, empty BCSC"}
+
+    def step():
+        spmm_cnic.forward_tensorcore(*args, F, x)
+        spmm_cnic.freeMatC()
+
+    ms = timed(step, 10, 2)
+    out["packed_x_ms"] = round(ms, 4)
+    out["packed_x_GFLOPs"] = round(flops / ms / 1e6, 1)
+    spmm_cnic.set_graph_plans(1)
+    try:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        step()
+        torch.cuda.synchronize()
+        out["plan_first_call_ms"] = round((time.perf_counter() - t0) * 1e3, 2)
+        ms = timed(step, 20, 2)
+        out["plan_ms"] = round(ms, 4)
+        out["plan_GFLOPs"] = round(flops / ms / 1e6, 1)
+    finally:
+        spmm_cnic.set_graph_plans(0)
+    return out
+
+
 def bench_spmm(args, torch, swtcf, cfg):
     """Configs 1-3: one SpMM per step."""
     from tcc_amd.graphs import make_features, make_graph
@@ -634,6 +691,9 @@ def bench_spmm(args, torch, swtcf, cfg):
         if args.config == 2:
             extra["swtcf"] = swtcf_timings(torch, swtcf, m, X, n, nnz, F)
         del m, ws
+        if args.config == 3:
+            torch.cuda.empty_cache()
+            extra["extension"] = extension_timings(torch, swtcf, r32, c32, n, F, X)
     if args.copy_calibration_mib:
         copy_calibration(args.copy_calibration_mib)
     if args.profile_step:

@@ -169,6 +169,18 @@ int tcc_bcsc_transpose_spmm(const tcc_bcsc* A, const float* dY, float* dX,
 int tcc_spmm_cnic_forward(const tcc_bcsr* bcsr, const tcc_bcsc* bcsc, const float* X,
                           float* denseC, uint32_t featureDim, void* stream);
 
+/* tcc_spmm_cnic_forward with a caller-owned workspace (no reference
+ * counterpart; the spmm_cnic extension's forward_tensorcore uses it): when
+ * the BCSR gathers each input row at least 16 times on average, X is first
+ * packed to exact TF32 rows in the workspace (tcc_tf32_pack) and the BCSR
+ * part gathers those (the same products, fewer bytes: config 3, 36.7 ->
+ * 21.5 ms).  tcc_spmm_cnic_forward_workspace_bytes gives the bytes that
+ * enable it (0: packing would not pay); a smaller or NULL workspace takes
+ * the fp32 gather.  The workspace must not be shared with a concurrent call. */
+size_t tcc_spmm_cnic_forward_workspace_bytes(const tcc_bcsr* bcsr, uint32_t featureDim);
+int tcc_spmm_cnic_forward_ws(const tcc_bcsr* bcsr, const tcc_bcsc* bcsc, const float* X, float* denseC,
+                             uint32_t featureDim, void* workspace, size_t workspaceBytes, void* stream);
+
 /* launch_spmm_kernel, first-layer (mixed memory) form
  * (spmm_launcher.cu:30-112 with the mixed kernels of spmm_kernel.cu:7-794):
  * as tcc_spmm_cnic_forward, with feature rows resolved through `src`. */
@@ -324,6 +336,21 @@ int tcc_coo_to_hybrid_scaled(const uint32_t* dRow, const uint32_t* dCol, uint32_
                              uint32_t groupBlocks, uint32_t unitSteps, uint32_t phases, tcc_hybrid* out,
                              void* stream);
 int tcc_hybrid_release(tcc_hybrid* H);
+
+/* The hybrid of a BCSR's own entries (no reference counterpart: a per-graph
+ * plan for callers that hold the reference's BCSR arrays and multiply by the
+ * same graph many times, such as full-graph training).  With useValues = 0
+ * the entries count as 1.0, as the reference's kernels read them
+ * (spmm_kernel.cu:96-102): binary tiles (tcc_coo_to_hybrid_scaled without
+ * scales, minStepNnz 0 = 64); else the values of `data` (value of bit i of
+ * block b = data[tcOffset[b] + rank]) in split-TF32 tiles (tcc_coo_to_hybrid,
+ * TCC_TILES_BF16X2, minTileNnz 16, groups of 8).  Bits in padding columns
+ * (>= num_cols) or rows (>= num_rows) are ignored, as the gather ignores
+ * them.  phases as tcc_coo_to_hybrid (0 = 4 when windows hold at least 64
+ * blocks on average, else 1).  Synchronises `stream`; the BCSR may be freed
+ * afterwards (the hybrid holds its own arrays); free with tcc_hybrid_release. */
+int tcc_hybrid_from_bcsr(const tcc_bcsr* A, int useValues, uint32_t minStepNnz, uint32_t phases, tcc_hybrid* out,
+                         void* stream);
 
 /* Bytes of device workspace tcc_hybrid_spmm needs for F features: the
  * remainder's packed TF32 rows and tcc_hub_tiles_workspace_bytes. */

@@ -115,6 +115,11 @@ SIGNATURES = {
     "tcc_coo_to_hybrid_scaled": (ctypes.c_int, [vp, vp, u32, u32, u32, vp, vp, u32, u32, u32, u32,
                                                  ctypes.POINTER(Hybrid), vp]),
     "tcc_hybrid_release": (ctypes.c_int, [ctypes.POINTER(Hybrid)]),
+    "tcc_hybrid_from_bcsr": (ctypes.c_int, [ctypes.POINTER(BCSR), ctypes.c_int, u32, u32, ctypes.POINTER(Hybrid),
+                                            vp]),
+    "tcc_spmm_cnic_forward_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(BCSR), u32]),
+    "tcc_spmm_cnic_forward_ws": (ctypes.c_int, [ctypes.POINTER(BCSR), ctypes.POINTER(BCSC), vp, vp, u32, vp,
+                                                ctypes.c_size_t, vp]),
     "tcc_hybrid_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Hybrid), u32]),
     "tcc_hub_tiles_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(HubTiles), u32]),
     "tcc_hybrid_spmm": (ctypes.c_int, [ctypes.POINTER(Hybrid), vp, vp, u32, ctypes.c_int, vp, ctypes.c_size_t, vp]),

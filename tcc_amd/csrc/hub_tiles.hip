@@ -356,6 +356,57 @@ __global__ void padded_copy_kernel(const float* __restrict__ in, std::uint32_t n
     if (i < padded) out[i] = i < n ? in[i] : 0.0f;
 }
 
+// A BCSR's entries as a COO (tcc_hybrid_from_bcsr): block b's window is
+// the last w with rowWindowOffset[w] <= b; its valid bits are those whose
+// column slot names a column (< numCols) and whose row is < numRows.
+__device__ __forceinline__ std::uint32_t block_window(const std::uint32_t* winOffset, std::uint32_t W, std::uint32_t b) {
+    std::uint32_t lo = 0, hi = W;  // winOffset[lo] <= b < winOffset[hi]
+    while (hi - lo > 1) {
+        const std::uint32_t mid = lo + (hi - lo) / 2;
+        if (winOffset[mid] <= b) lo = mid;
+        else hi = mid;
+    }
+    return lo;
+}
+
+__device__ __forceinline__ std::uint64_t block_valid_bits(const tcc_bcsr& A, std::uint32_t b, std::uint32_t w) {
+    std::uint64_t colMask = 0, rowMask = 0;
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+        if (A.sparseA2B[8ull * b + c] < A.num_cols) colMask |= 0x0101010101010101ull << c;
+#pragma unroll
+    for (int r = 0; r < 8; ++r)
+        if (8ull * w + r < A.num_rows) rowMask |= 0xFFull << (8 * r);
+    return A.tcLocalBit[b] & colMask & rowMask;
+}
+
+__global__ void bcsr_entry_counts_kernel(tcc_bcsr A, std::uint32_t* __restrict__ counts) {
+    const std::uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= A.num_TCBlocks) return;
+    const std::uint32_t w = block_window(A.rowWindowOffset, A.num_rowWindows, b);
+    counts[b] = static_cast<std::uint32_t>(__popcll(block_valid_bits(A, b, w)));
+}
+
+__global__ void bcsr_expand_kernel(tcc_bcsr A, const std::uint32_t* __restrict__ offset, bool values,
+                                   std::uint32_t* __restrict__ row, std::uint32_t* __restrict__ col,
+                                   float* __restrict__ val) {
+    const std::uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= A.num_TCBlocks) return;
+    const std::uint32_t w = block_window(A.rowWindowOffset, A.num_rowWindows, b);
+    const std::uint64_t stored = A.tcLocalBit[b];
+    std::uint64_t m = block_valid_bits(A, b, w);
+    std::uint32_t k = offset[b];
+    while (m) {
+        const unsigned i = static_cast<unsigned>(__builtin_ctzll(m));
+        m &= m - 1;
+        row[k] = 8 * w + i / 8;
+        col[k] = A.sparseA2B[8ull * b + i % 8];
+        // values follow the stored bits in ascending order (data[tcOffset[b] + rank])
+        if (values) val[k] = A.data[A.tcOffset[b] + __popcll(stored & ((1ull << i) - 1ull))];
+        ++k;
+    }
+}
+
 template <typename T>
 struct DevBuf {
     T* p = nullptr;
@@ -1430,6 +1481,68 @@ int tcc_coo_to_hybrid_scaled(const std::uint32_t* dRow, const std::uint32_t* dCo
     P.phases = phases;
     P.rowScale = dRowScale;
     P.colScale = dColScale;
+    return build_hybrid(P, out, stream);
+}
+
+int tcc_hybrid_from_bcsr(const tcc_bcsr* A, int useValues, std::uint32_t minStepNnz, std::uint32_t phases,
+                         tcc_hybrid* out, void* stream) {
+    clear_last_error();
+    TCC_REQUIRE(A && out && A->num_rows >= 1 && A->num_cols >= 1 && A->phases <= 1 &&
+                    (A->num_TCBlocks == 0 || (A->rowWindowOffset && A->sparseA2B && A->tcLocalBit)) &&
+                    (!useValues || (A->data && A->tcOffset)),
+                TCC_ERR_INVALID_ARGUMENT, "invalid BCSR -> hybrid arguments (an ordinary BCSR; data for values)");
+    const hipStream_t st = as_stream(stream);
+    const std::uint32_t B = A->num_TCBlocks;
+    if (phases == 0) phases = A->num_rowWindows && B >= 64ull * A->num_rowWindows ? 4 : 1;
+    // block counts, their scan, then the entries
+    DevBuf<char> scratch;
+    const std::uint64_t Bn = std::max<std::uint32_t>(B, 1);
+    const std::size_t headBytes = 2 * align_up(4 * (Bn + 1)) + align_up(4 * scan_temp_elems(Bn + 1)) + 256;
+    TCC_HIP_CHECK(hipMalloc(&scratch.p, headBytes));
+    auto* counts = reinterpret_cast<std::uint32_t*>(scratch.p);
+    auto* offset = reinterpret_cast<std::uint32_t*>(scratch.p + align_up(4 * (Bn + 1)));
+    auto* total = reinterpret_cast<std::uint32_t*>(scratch.p + 2 * align_up(4 * (Bn + 1)));
+    auto* temp = reinterpret_cast<std::uint32_t*>(scratch.p + 2 * align_up(4 * (Bn + 1)) + 256);
+    std::uint32_t E = 0;
+    if (B > 0) {
+        hipLaunchKernelGGL(bcsr_entry_counts_kernel, dim3(grid_for(B, kThreads)), dim3(kThreads), 0, st, *A, counts);
+        TCC_LAUNCH_CHECK();
+        TCC_HIP_CHECK(exclusive_scan(counts, offset, B, total, temp, st));
+        TCC_HIP_CHECK(hipMemcpyAsync(&E, total, 4, hipMemcpyDeviceToHost, st));
+        TCC_HIP_CHECK(hipStreamSynchronize(st));
+    }
+    DevBuf<char> coo;
+    const std::uint64_t En = std::max<std::uint32_t>(E, 1);
+    TCC_HIP_CHECK(hipMalloc(&coo.p, 3 * align_up(4 * En)));
+    auto* row = reinterpret_cast<std::uint32_t*>(coo.p);
+    auto* col = reinterpret_cast<std::uint32_t*>(coo.p + align_up(4 * En));
+    auto* val = reinterpret_cast<float*>(coo.p + 2 * align_up(4 * En));
+    if (E > 0) {
+        hipLaunchKernelGGL(bcsr_expand_kernel, dim3(grid_for(B, kThreads)), dim3(kThreads), 0, st, *A, offset,
+                           useValues != 0, row, col, val);
+        TCC_LAUNCH_CHECK();
+    }
+    HybridParams P{};
+    P.row = E ? row : nullptr;
+    P.col = E ? col : nullptr;
+    P.nnz = E;
+    P.numRows = A->num_rows;
+    P.numCols = A->num_cols;
+    P.phases = phases;
+    if (useValues) {
+        P.val = val;
+        P.minStepNnz = 0;
+        P.minTileNnz = kDefaultMinTileNnz;
+        P.G = kDefaultGroupBlocks;
+        P.unitSteps = kDefaultUnitSteps;
+        P.format = TCC_TILES_BF16X2;
+    } else {
+        P.minStepNnz = minStepNnz ? minStepNnz : kDefaultMinStepNnz;
+        P.minTileNnz = 1;
+        P.G = kDefaultBinaryGroupBlocks;
+        P.unitSteps = kDefaultBinaryUnitSteps;
+        P.format = TCC_TILES_BINARY;
+    }
     return build_hybrid(P, out, stream);
 }
 

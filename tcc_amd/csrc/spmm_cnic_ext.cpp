@@ -15,11 +15,20 @@
 // (spmm_kernel.cu:96-102); by default the `data` tensors are therefore not
 // read, so results equal the reference's.  set_use_values(True) makes the
 // kernels use them (value of bit i of block b = data[tcOffset[b] + rank]).
+//
+// forward_tensorcore (both forms) packs x into exact TF32 rows first when
+// the BCSR gathers each row at least 16 times (tcc_spmm_cnic_forward_ws,
+// the buffer from torch's caching allocator on the current stream).  With
+// set_graph_plans(n > 0) it also keeps a per-graph plan for up to n graphs
+// (tcc_hybrid_from_bcsr: dense degree-ordered tiles on MFMA plus the gather
+// of the rest), found again by the BCSR arrays' device pointers and sizes;
+// a caller that rewrites a graph's arrays in place calls release_plans().
 #include <torch/extension.h>
 
 #include <c10/hip/HIPStream.h>
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <stdexcept>
 #include <string>
@@ -36,6 +45,20 @@ std::vector<torch::Tensor> g_outputs;  // Python-caller form outputs, released b
 std::vector<void*> g_spaces;           // space_malloc buffers, released by finalize()
 bool g_use_values = false;
 std::uint32_t g_unit_blocks = 0;       // blocks per unit of work (0 = automatic)
+
+// Per-graph plans, most recently used last (set_graph_plans).
+struct Plan {
+    int device;
+    const void* rwo;
+    const void* a2b;
+    const void* bits;
+    const void* data;
+    std::uint32_t rows, cols, blocks, windows;
+    bool values;
+    tcc_hybrid H;
+};
+std::vector<Plan> g_plans;
+std::size_t g_max_plans = 0;
 
 void check(int rc) {
     if (rc != 0) {
@@ -168,6 +191,86 @@ tcc_feature_source feature_source(const torch::Tensor& id_map, py::capsule cpu_p
     return s;
 }
 
+// ---------------------------------------------------------------- the non-mixed forward
+
+torch::Tensor device_bytes(std::size_t n, int device) {
+    return torch::empty({static_cast<std::int64_t>(n)},
+                        torch::TensorOptions().dtype(torch::kUInt8).device(torch::kCUDA, device));
+}
+
+void* aligned16(const torch::Tensor& t) {
+    return reinterpret_cast<void*>((reinterpret_cast<std::uintptr_t>(t.data_ptr()) + 15) & ~std::uintptr_t(15));
+}
+
+void drop_plan(Plan& p) {
+    // hipFree waits for the work in flight that may still read the arrays
+    if (tcc_hybrid_release(&p.H) != 0) throw std::runtime_error(std::string("spmm_cnic: ") + tcc_last_error());
+}
+
+void release_plans() {
+    for (Plan& p : g_plans) drop_plan(p);
+    g_plans.clear();
+}
+
+void set_graph_plans(std::int64_t n) {
+    TORCH_CHECK(n >= 0, "set_graph_plans: a count of plans (0 = none)");
+    g_max_plans = static_cast<std::size_t>(n);
+    while (g_plans.size() > g_max_plans) {
+        drop_plan(g_plans.front());
+        g_plans.erase(g_plans.begin());
+    }
+}
+
+std::int64_t graph_plans() { return static_cast<std::int64_t>(g_plans.size()); }
+
+// The plan of A's graph on `device`: found by its arrays and sizes, or built.
+const tcc_hybrid& plan_for(const tcc_bcsr& A, int device, void* st) {
+    const bool values = A.data != nullptr;
+    for (std::size_t i = 0; i < g_plans.size(); ++i) {
+        const Plan& p = g_plans[i];
+        if (p.device == device && p.rwo == A.rowWindowOffset && p.a2b == A.sparseA2B && p.bits == A.tcLocalBit &&
+            p.data == A.data && p.rows == A.num_rows && p.cols == A.num_cols && p.blocks == A.num_TCBlocks &&
+            p.windows == A.num_rowWindows && p.values == values) {
+            std::rotate(g_plans.begin() + static_cast<std::ptrdiff_t>(i), g_plans.begin() + static_cast<std::ptrdiff_t>(i) + 1,
+                        g_plans.end());
+            return g_plans.back().H;
+        }
+    }
+    if (g_plans.size() >= g_max_plans) {
+        drop_plan(g_plans.front());
+        g_plans.erase(g_plans.begin());
+    }
+    Plan p{device, A.rowWindowOffset, A.sparseA2B, A.tcLocalBit, A.data, A.num_rows, A.num_cols, A.num_TCBlocks,
+           A.num_rowWindows, values, tcc_hybrid{}};
+    check(tcc_hybrid_from_bcsr(&A, values ? 1 : 0, 0, 0, &p.H, st));
+    g_plans.push_back(p);
+    return g_plans.back().H;
+}
+
+// denseC[(r_win+1)*8*F] = A x + B x (launch_spmm_kernel, spmm_launcher.cu:203-271)
+void forward(const tcc_bcsr& A, const tcc_bcsc& B, const torch::Tensor& x, float* C, std::int32_t F, int device) {
+    TORCH_CHECK(x.is_cuda() && x.is_contiguous() && x.scalar_type() == torch::kFloat32, "x must be fp32 on device");
+    void* st = stream_of(device);
+    const float* X = x.data_ptr<float>();
+    if (g_max_plans > 0 && A.num_TCBlocks > 0 && A.phases <= 1) {
+        const tcc_hybrid& H = plan_for(A, device, st);
+        const std::size_t need = tcc_hybrid_workspace_bytes(&H, static_cast<std::uint32_t>(F));
+        torch::Tensor ws = device_bytes(need + 16, device);
+        check(tcc_hybrid_spmm(&H, X, C, static_cast<std::uint32_t>(F), 0, aligned16(ws), need, st));
+        // rows past the plan's 8-row windows (the reference's extra window and any more) are zero
+        const std::int64_t done = static_cast<std::int64_t>(H.rest.num_rowWindows / std::max(1u, H.rest.phases)) * 8 * F;
+        const std::int64_t all = denseC_elems(A.num_rowWindows, F);
+        if (all > done) view_of(C, static_cast<std::uint32_t>(all / F), F, device).narrow(0, done, all - done).zero_();
+        check(tcc_bcsc_spmm(&B, X, C, static_cast<std::uint32_t>(F), st));
+        return;
+    }
+    const std::size_t need = tcc_spmm_cnic_forward_workspace_bytes(&A, static_cast<std::uint32_t>(F));
+    torch::Tensor ws;
+    if (need) ws = device_bytes(need, device);
+    check(tcc_spmm_cnic_forward_ws(&A, &B, X, C, static_cast<std::uint32_t>(F), need ? ws.data_ptr() : nullptr, need,
+                                   st));
+}
+
 // ---------------------------------------------------------------- compiled form
 
 torch::Tensor fwd_mixed_bound(std::uint32_t r_rows, std::uint32_t r_cols, std::uint32_t r_nnz, std::uint32_t r_blk,
@@ -183,8 +286,7 @@ torch::Tensor fwd_mixed_bound(std::uint32_t r_rows, std::uint32_t r_cols, std::u
     tcc_bcsc B = make_bcsc(c_rows, c_cols, c_nnz, c_blk, c_win, c_cwo, c_tco, c_a2c, c_bits, nullptr);
     float* C = static_cast<float*>(denseC.get_pointer());
     if (x.defined() && x.numel() > 0) {
-        TORCH_CHECK(x.is_cuda() && x.is_contiguous() && x.scalar_type() == torch::kFloat32, "x must be fp32 on device");
-        check(tcc_spmm_cnic_forward(&A, &B, x.data_ptr<float>(), C, F, stream_of(device_id)));
+        forward(A, B, x, C, F, device_id);
     } else {
         const tcc_feature_source s = feature_source(id_map, cpu_ptr, csm, gpu_ptr, cap);
         check(tcc_spmm_cnic_forward_mixed(&A, &B, &s, C, F, stream_of(device_id)));
@@ -215,9 +317,8 @@ torch::Tensor fwd_bound(std::uint32_t r_rows, std::uint32_t r_cols, std::uint32_
     // module.cu:192-273
     tcc_bcsr A = make_bcsr(r_rows, r_cols, r_nnz, r_blk, r_win, r_rwo, r_tco, r_a2b, r_bits, nullptr);
     tcc_bcsc B = make_bcsc(c_rows, c_cols, c_nnz, c_blk, c_win, c_cwo, c_tco, c_a2c, c_bits, nullptr);
-    TORCH_CHECK(x.is_cuda() && x.is_contiguous() && x.scalar_type() == torch::kFloat32, "x must be fp32 on device");
     float* C = static_cast<float*>(denseC.get_pointer());
-    check(tcc_spmm_cnic_forward(&A, &B, x.data_ptr<float>(), C, F, stream_of(device_id)));
+    forward(A, B, x, C, F, device_id);
     return view_of(C, r_rows, F, current_device());
 }
 
@@ -258,10 +359,8 @@ torch::Tensor fwd_py(std::uint32_t r_rows, std::uint32_t r_cols, std::uint32_t r
     // train/tcgnn_conv_release.py:124-130
     tcc_bcsr A = make_bcsr(r_rows, r_cols, r_nnz, r_blk, r_win, r_rwo, r_tco, r_a2b, r_bits, &r_data);
     tcc_bcsc B = make_bcsc(c_rows, c_cols, c_nnz, c_blk, c_win, c_cwo, c_tco, c_a2c, c_bits, &c_data);
-    TORCH_CHECK(x.is_cuda() && x.is_contiguous() && x.scalar_type() == torch::kFloat32, "x must be fp32 on device");
     torch::Tensor out = alloc_output(r_win, F);
-    void* st = stream_of(current_device());
-    check(tcc_spmm_cnic_forward(&A, &B, x.data_ptr<float>(), out.data_ptr<float>(), F, st));
+    forward(A, B, x, out.data_ptr<float>(), F, current_device());
     return out.narrow(0, 0, static_cast<std::int64_t>(r_rows) * F);
 }
 
@@ -310,6 +409,7 @@ void finalize(int device_id) {
     for (void* p : g_spaces) (void)hipFree(p);
     g_spaces.clear();
     g_outputs.clear();
+    release_plans();
 }
 
 void freeMatC() {
@@ -357,4 +457,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("set_use_values", &set_use_values, "read the per-block data values (default: all entries 1.0)");
     m.def("set_unit_blocks", &set_unit_blocks,
           "blocks each wave of work walks (default 0 = chosen from the block count)");
+    m.def("set_graph_plans", &set_graph_plans,
+          "keep per-graph plans (dense tiles on MFMA + gather) for up to n graphs, found by their BCSR arrays "
+          "(0, the default: none; plans beyond n are released, least recently used first)");
+    m.def("release_plans", &release_plans, "release every per-graph plan (after rewriting a graph's arrays in place)");
+    m.def("graph_plans", &graph_plans, "the number of per-graph plans held");
 }

@@ -436,6 +436,18 @@ def coo_to_hybrid_scaled(row: torch.Tensor, col: torch.Tensor, num_rows: int, nu
     return HybridMatrix(view)
 
 
+def hybrid_from_bcsr(A: BlockMatrix, use_values: bool = False, min_step_nnz: int = 0, phases: int = 0,
+                     stream=None) -> HybridMatrix:
+    """The hybrid of a BCSR's own entries (tcc_hybrid_from_bcsr): binary
+    tiles over its pattern, or split-TF32 value tiles with use_values."""
+    if A.kind != "bcsr":
+        raise TypeError("hybrid_from_bcsr takes a BCSR")
+    view = Hybrid()
+    check(_lib.lib().tcc_hybrid_from_bcsr(ctypes.byref(A.view), int(use_values), int(min_step_nnz), int(phases),
+                                          ctypes.byref(view), _stream(stream)))
+    return HybridMatrix(view)
+
+
 def hybrid_spmm(H: HybridMatrix, X: torch.Tensor, Y: torch.Tensor | None = None, accumulate: bool = False,
                 workspace: torch.Tensor | None = None, stream=None) -> torch.Tensor:
     """Y[out_rows x F] (=|+=) A X (tcc_hybrid_spmm); `workspace` (uint8,

@@ -262,6 +262,71 @@ def test_fullsize_config3_binary_hybrid(gpu, oracle):
     assert e <= TOL
 
 
+def _extension():
+    import os
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    sys.path.insert(0, os.path.join(root, "tcc_amd"))
+    try:
+        import spmm_cnic
+    finally:
+        sys.path.pop(0)
+    return spmm_cnic
+
+
+def _ext_args(d, kind):
+    """The 9 (or 10 with data) tensor/int arguments of one matrix in the
+    reference's extension call (train/tcgnn_conv_release.py:116-130)."""
+    def dev(a):
+        a = np.ascontiguousarray(a)
+        return torch.from_numpy(a.view(np.int32) if a.dtype == np.uint32 else
+                                (a.view(np.int64) if a.dtype == np.uint64 else a)).cuda()
+
+    w = "rowWindowOffset" if kind == "bcsr" else "colWindowOffset"
+    i = "sparseA2B" if kind == "bcsr" else "sparseA2C"
+    nw = d["num_rowWindows"] if kind == "bcsr" else d["num_colWindows"]
+    data = d["data"] if d["data"] is not None else np.zeros(1, np.float32)
+    return [d["num_rows"], d["num_cols"], d["nnz"], d["num_TCBlocks"], nw, dev(d[w]), dev(d["tcOffset"]), dev(d[i]),
+            dev(d["tcLocalBit"]), dev(data)]
+
+
+def test_fullsize_config3_extension(gpu, oracle):
+    """spmm_cnic.forward_tensorcore, called as the reference's training
+    script calls it, on config 3's BCSR (the whole graph; an empty BCSC;
+    values not read, as the reference's kernels read none): the default path
+    (x packed to exact TF32 rows, the packed gather) and a per-graph plan
+    (set_graph_plans: binary tiles + gather); each against >= 1M-nnz oracle
+    rows of the pattern product and the weighted checksum."""
+    from tcc_amd import swtcf
+
+    m = _extension()
+    n, F, r32, c32, vals, X = graph(3)
+    rows, cols = r32.cpu().numpy(), c32.cpu().numpy()
+    Xh = X.cpu().numpy()
+    A = swtcf.coo_to_bcsr(r32, c32, None, n, n)
+    B = swtcf.coo_to_bcsc(r32[:0], c32[:0], None, n, n)
+    args = _ext_args(A.to_host(), "bcsr") + _ext_args(B.to_host(), "bcsc")
+    A.release()
+    x = X.flatten()
+    hub = int(np.argmax(np.bincount(rows, minlength=n)))
+    try:
+        for plans in (0, 1):
+            m.set_graph_plans(plans)
+            out = m.forward_tensorcore(*args, F, x)
+            Y = out.reshape(n, F)
+            what = f"config 3 forward_tensorcore, {'a per-graph plan' if plans else 'packed x'}"
+            r_dev, want = check_weighted(oracle, Y, n, rows, cols, None, n, Xh, 39, what=what)
+            check_swap_fails(Y, n, r_dev, want, hub, (hub + 9) % n, what=what)
+            check_rows(oracle, Y, rows, cols, None, n, Xh, 40, what=what)
+            if plans:
+                assert m.graph_plans() == 1
+            m.freeMatC()
+    finally:
+        m.set_graph_plans(0)
+        m.freeMatC()
+
+
 def test_fullsize_config3_swtcf_bit_exact(gpu, oracle):
     """convertCOOToSWTCF of the config-3 graph (114M edges, S = 16) against
     the C oracle's canonical form, every array bit for bit, for the COO in

@@ -11,7 +11,7 @@ import torch
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 EXPORTS = ["forward_tensorcore_mixed", "forward_tensorcore", "read_cpu_feature_cache", "read_gpu0_feature_cache",
-           "initialize", "space_malloc", "finalize", "freeMatC"]
+           "initialize", "space_malloc", "finalize", "freeMatC", "set_graph_plans", "release_plans", "graph_plans"]
 
 
 def import_ext():
@@ -166,3 +166,118 @@ def test_forward_tensorcore_mixed_forms(gpu):
     torch.cuda.synchronize()
     m.finalize(0)
     cpu.free()
+
+
+def _hub_coo(nr, nc, nnz, seed):
+    from test_gpu_hybrid import random_coo
+
+    return random_coo(nr, nc, nnz, seed, True)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("F", [100, 602])
+def test_forward_tensorcore_packs_x_for_high_reuse(gpu, F):
+    """Rows gathered >= 16 times on average: the extension packs x into exact
+    TF32 rows first (tcc_spmm_cnic_forward_ws); the product is the same."""
+    from tcc_amd import _lib, swtcf
+
+    m = import_ext()
+    nr, nc = 2000, 300
+    dst, src, hot = _split(nr, nc, 60000, 5)
+    h = hot[src]
+    bcsr, _ = _blocks(dst[h], src[h], nr, nc)
+    _, bcsc = _blocks(dst[~h], src[~h], nr, nc)
+    A = swtcf.host_to_bcsr(bcsr)
+    need = _lib.lib().tcc_spmm_cnic_forward_workspace_bytes(ctypes.byref(A.view), F)
+    assert need == _lib.lib().tcc_tf32_packed_bytes(nc, F) + 16  # packing pays here
+    X = np.random.default_rng(6).standard_normal((nc, F)).astype(np.float32)
+    out = m.forward_tensorcore(*_args(bcsr, bcsc, True), F, torch.from_numpy(X).cuda().flatten())
+    assert _rel(out.reshape(nr, F).cpu().numpy(), _want(dst, src, nr, X)) < 1e-5
+    m.freeMatC()
+
+
+@pytest.mark.gpu
+def test_hybrid_from_bcsr_matches_the_coo_build(gpu, oracle):
+    """tcc_hybrid_from_bcsr of the oracle's BCSR holds exactly the arrays of
+    the binary hybrid built from the same COO; with values, the split-TF32
+    hybrid's product equals the oracle's."""
+    from test_gpu_hybrid import dev_u32
+    from tcc_amd import swtcf
+
+    nr, nc, F = 700, 900, 96
+    dst, src = _hub_coo(nr, nc, 60000, 31)
+    vals = np.random.default_rng(32).uniform(-1, 1, dst.size).astype(np.float32)
+    bcsr, _ = _blocks(dst, src, nr, nc, vals)
+    A = swtcf.host_to_bcsr(bcsr, use_data=True)
+    Hb = swtcf.hybrid_from_bcsr(A, min_step_nnz=16)
+    Hc = swtcf.coo_to_hybrid_scaled(dev_u32(dst), dev_u32(src), nr, nc, min_step_nnz=16, phases=1)
+    hb, hc = Hb.to_host(), Hc.to_host()
+    for k in ("rowOrder", "hubColOrder", "groupStepOffset", "stepCol", "units", "unitOrder", "unitPartial",
+              "sharedGroups", "tileMasks"):
+        assert np.array_equal(hb[k], hc[k]), k
+    for k in ("rowWindowOffset", "sparseA2B", "tcLocalBit"):
+        assert np.array_equal(hb["rest"][k], hc["rest"][k]), k
+    X = np.random.default_rng(33).standard_normal((nc, F)).astype(np.float32)
+    Xd = torch.from_numpy(X).cuda()
+    assert _rel(swtcf.hybrid_spmm(Hb, Xd).cpu().numpy()[:nr], _want(dst, src, nr, X)) < 1e-5
+    Hv = swtcf.hybrid_from_bcsr(A, use_values=True)
+    order = np.lexsort((src, dst))
+    rowptr = np.zeros(nr + 1, np.int64)
+    rowptr[1:] = np.cumsum(np.bincount(dst, minlength=nr))
+    want_v = oracle.csr_spmm(rowptr, src[order], vals[order], X, use_tf32=True)
+    assert _rel(swtcf.hybrid_spmm(Hv, Xd).cpu().numpy()[:nr], want_v) < 1e-5
+
+
+@pytest.mark.gpu
+def test_forward_tensorcore_graph_plans(gpu, oracle):
+    """set_graph_plans: the extension keeps a per-graph plan (dense tiles on
+    MFMA + gather), finds it again by the BCSR arrays, keeps at most n, and
+    drops them on release_plans(); with set_use_values the plan holds the
+    values.  Every product against the oracle."""
+    m = import_ext()
+    nr, nc, F = 600, 700, 130
+    graphs = []
+    for seed in (41, 42, 43):
+        dst, src = _hub_coo(nr, nc, 50000, seed)
+        bcsr, bcsc = _blocks(dst, src, nr, nc)
+        empty = _blocks(np.zeros(0, np.uint32), np.zeros(0, np.uint32), nr, nc)[1]
+        graphs.append((dst, src, _args(bcsr, empty, True)))
+    X = np.random.default_rng(44).standard_normal((nc, F)).astype(np.float32)
+    x = torch.from_numpy(X).cuda().flatten()
+    try:
+        m.set_graph_plans(2)
+        for _ in range(2):  # the second call finds the plan
+            dst, src, args = graphs[0]
+            out = m.forward_tensorcore(*args, F, x)
+            assert _rel(out.reshape(nr, F).cpu().numpy(), _want(dst, src, nr, X)) < 1e-5
+            assert m.graph_plans() == 1
+        for dst, src, args in graphs[1:]:
+            out = m.forward_tensorcore(*args, F, x)
+            assert _rel(out.reshape(nr, F).cpu().numpy(), _want(dst, src, nr, X)) < 1e-5
+        assert m.graph_plans() == 2  # the least recently used one was released
+        # the compiled form with its caller-owned denseC
+        dst, src, args = graphs[2]
+        args_nodata = args[:9] + args[10:19]
+        caps = m.space_malloc(0, (int(args[4]) + 1) * 8 * F)
+        out = m.forward_tensorcore(*args_nodata, F, x, 0, caps[0])
+        assert _rel(out.reshape(nr, F).cpu().numpy(), _want(dst, src, nr, X)) < 1e-5
+        # values: a plan of its own, over the data tensors
+        dst, src, _ = graphs[0]
+        vals = np.random.default_rng(45).uniform(-1, 1, dst.size).astype(np.float32)
+        bcsr, _ = _blocks(dst, src, nr, nc, vals)
+        empty = _blocks(np.zeros(0, np.uint32), np.zeros(0, np.uint32), nr, nc)[1]
+        m.set_use_values(True)
+        out = m.forward_tensorcore(*_args(bcsr, empty, True), F, x)
+        order = np.lexsort((src, dst))
+        rowptr = np.zeros(nr + 1, np.int64)
+        rowptr[1:] = np.cumsum(np.bincount(dst, minlength=nr))
+        want_v = oracle.csr_spmm(rowptr, src[order], vals[order], X, use_tf32=True)
+        assert _rel(out.reshape(nr, F).cpu().numpy(), want_v) < 1e-5
+        m.release_plans()
+        assert m.graph_plans() == 0
+    finally:
+        m.set_use_values(False)
+        m.set_graph_plans(0)
+        m.freeMatC()
+        torch.cuda.synchronize()
+        m.finalize(0)
