@@ -269,8 +269,11 @@ class FeatureTable:
 
     def error(self) -> int:
         """TCC_DEVERR_FEATURE_INDEX if a lookup fell outside the tables since
-        the table was made (synchronises the device), else 0."""
-        return int(self.device_error.item())
+        the last call (or since the table was made), else 0; synchronises
+        the device and clears the word, as spmm_cnic.feature_error does."""
+        v = int(self.device_error.item())
+        self.device_error.zero_()
+        return v
 
     def free(self) -> None:
         self.host.free()

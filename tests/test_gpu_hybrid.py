@@ -264,3 +264,43 @@ def test_hybrid_errors(gpu):
     small = torch.empty(8, dtype=torch.uint8, device="cuda")
     with pytest.raises(_lib.TccError, match="workspace"):
         swtcf.hybrid_spmm(H, X, workspace=small)
+
+
+def test_split_tiles_inf_in_hub_column(gpu, oracle):
+    """Valued (split-TF32) tiles multiply every tile slot of a step, zeros
+    included: an Inf in a hub column's feature row gives NaN to the rows
+    without an entry in that column in every group with a step in its column
+    block (0 * Inf in the tiles' products), Inf or NaN to those with one
+    there (NaN when the value's low bf16 half is 0: al * Inf), Inf to rows
+    whose entry is in the remainder, and leaves every other row finite and
+    exact."""
+    from tcc_amd import swtcf
+
+    nr, nc, F, G = 400, 500, 8, 8
+    dst, src = random_coo(nr, nc, 20000, 23, True)
+    vals = np.random.default_rng(2).uniform(0.5, 1.5, dst.size).astype(np.float32)
+    H = swtcf.coo_to_hybrid(dev_u32(dst), dev_u32(src), torch.from_numpy(vals).cuda(), nr, nc, min_tile_nnz=16,
+                            group_blocks=G, tile_format=swtcf.TILES_BF16X2)
+    h = H.to_host()
+    c0 = int(h["hubColOrder"][0])  # rank 0: column block 0
+    X = np.random.default_rng(5).standard_normal((nc, F)).astype(np.float32)
+    X[c0, 0] = np.inf
+    Y = swtcf.hybrid_spmm(H, torch.from_numpy(X).cuda()).cpu().numpy()[:nr]
+    has = np.zeros(nr, bool)
+    has[dst[src == c0].astype(np.int64)] = True
+    exposed = np.zeros(nr, bool)
+    gso, steps = h["groupStepOffset"], h["stepCol"]
+    for g in range(h["num_groups"]):
+        if np.any(steps[gso[g]:gso[g + 1]] == 0):
+            rows = h["rowOrder"][16 * G * g: 16 * G * (g + 1)]
+            exposed[rows[rows != 0xFFFFFFFF].astype(np.int64)] = True
+    assert has.any() and (exposed & ~has).any()
+    assert np.all(np.isposinf(Y[has & ~exposed, 0]))
+    assert np.all(np.isposinf(Y[has & exposed, 0]) | np.isnan(Y[has & exposed, 0]))
+    assert np.all(np.isnan(Y[exposed & ~has, 0]))
+    assert np.all(np.isfinite(Y[~(has | exposed), 0]))
+    X[c0, 0] = 0.0
+    want = oracle_product(oracle, dst, src, vals, nr, X)
+    keep = ~(has | exposed)
+    assert rel_l2(Y[:, 1:], want[:, 1:]) <= REL
+    assert rel_l2(Y[keep, 0], want[keep, 0]) <= REL

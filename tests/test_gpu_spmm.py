@@ -757,3 +757,29 @@ def test_bcsr_spmm_packed(gpu, oracle, unit_blocks, F):
     assert_close(Y.cpu().numpy()[:nr], want)
     Y2 = swtcf.bcsr_spmm_packed(A, packed, F, Y.clone(), accumulate=True)
     assert_close(Y2.cpu().numpy()[:nr], 2 * want)
+
+
+def test_feature_table_error_is_read_and_cleared(gpu):
+    """FeatureTable.error() returns TCC_DEVERR_FEATURE_INDEX after a refused
+    lookup (a host row past the table, planted in id_map) and clears it: the
+    next call, with no refused lookup since, returns 0."""
+    from tcc_amd import gcn, swtcf
+
+    rng = np.random.default_rng(12)
+    n, F = 500, 16
+    keys = np.sort(rng.choice(n * n, size=6000, replace=False))
+    rows = torch.from_numpy(keys // n).cuda()
+    cols = torch.from_numpy(keys % n).cuda()
+    X = torch.randn(n, F, device="cuda")
+    table = gcn.FeatureTable(X, cols)
+    g1, _ = gcn.build_gcn_graphs(rows, cols, n, table.hot)
+    g1.aggregate(F, source=table.source)
+    assert table.error() == 0
+    j = int(cols[~table.hot[cols]][0])  # a cold column with an edge
+    table.ids[j] = n + 5  # its host row past the table: refused, read as zeros
+    g1.aggregate(F, source=table.source)
+    assert table.error() == swtcf.DEVERR_FEATURE_INDEX
+    assert table.error() == 0
+    table.ids[j] = j
+    torch.cuda.synchronize()
+    table.free()

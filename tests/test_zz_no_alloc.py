@@ -97,3 +97,33 @@ def test_noalloc_k0_and_limit(gpu):
                                 stream())
     assert rc == 3
     assert b"16 MiB" in L.tcc_last_error()
+
+
+def test_noalloc_under_graph_capture(gpu):
+    """tcc_dense_tn_noalloc captured in a HIP graph (torch.cuda.CUDAGraph).
+    Its first call on a device looks up the device array's address, so one
+    uncaptured call comes first; then each of three replays, with new inputs
+    written eagerly and a synchronisation between them, equals an eager
+    tcc_dense_tn on the same inputs."""
+    K, M, N = 20_000, 100, 64
+    g = torch.Generator(device="cuda").manual_seed(11)
+    A = torch.randn(K, M, device="cuda", generator=g)
+    B = torch.randn(K, N, device="cuda", generator=g)
+    C = torch.empty(M, N, device="cuda")
+    without_allocation(A, B, C, False)  # outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        without_allocation(A, B, C, False)
+    for k in range(3):
+        A.copy_(torch.randn(K, M, device="cuda", generator=g))
+        B.copy_(torch.randn(K, N, device="cuda", generator=g))
+        ref = torch.empty(M, N, device="cuda")
+        with_workspace(A, B, ref, False)
+        torch.cuda.synchronize()
+        C.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        print(f"noalloc graph replay {k}: rel-L2 {rel_l2(C, ref):.2e}", flush=True)
+        assert rel_l2(C, ref) <= 1e-6
+        assert rel_l2(C, A.double().t() @ B.double()) <= 1e-5
