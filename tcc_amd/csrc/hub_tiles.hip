@@ -832,10 +832,9 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_split_kernel(TileArgs a) {
 //
 // Expansion: lane l's byte of tile t (8 bits: row l%32, column half l/32)
 // becomes 8 bf16 of 0 or 1.0 through two 8-byte reads of a 16-entry table
-// in LDS, one per 4-bit half.  Each step's lookups for all its tiles are
-// issued together, before its MFMAs, so that their latency is paid once a
-// step (2 G/2 reads; an 8-byte read of 64 lanes is 4 LDS cycles against 64
-// MFMA cycles of the two products per tile).  Every tile of a step is
+// in LDS, one per 4-bit half.  The next step's lookups run between this
+// step's products (2 G/2 reads; an 8-byte read of 64 lanes is 4 LDS cycles
+// against 64 MFMA cycles of the two products per tile).  Every tile of a step is
 // multiplied: the builder stores every entry of a chosen step, and steps
 // are nearly full (config 3: 7.97 of 8 tiles a step).
 //
@@ -911,19 +910,22 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_binary_kernel(TileArgs a) 
                 o.lo[u] = load_global<vu4>(rb + u * 32 * 64 + 32);
             }
         };
-        auto mma = [&](const BinaryStage<G, NT>& o) {
-            // every tile's lookups first: byte addresses 8 * nibble
-            vu4 A[T];
+        // every tile's lookups of one step: byte addresses 8 * nibble
+        auto expand = [&](const BinaryStage<G, NT>& o, vu4 (&A)[T]) {
 #pragma unroll
             for (int w = 0; w < G / 8; ++w) {
                 const std::uint32_t al = (o.m[w] << 3) & 0x78787878u, ah = (o.m[w] >> 1) & 0x78787878u;
 #pragma unroll
                 for (int q = 0; q < 4 && 4 * w + q < T; ++q) {
-                    const vu2 x0 = *reinterpret_cast<const vu2*>(lutBytes + ((al >> (8 * q)) & 0xFFu));
-                    const vu2 x1 = *reinterpret_cast<const vu2*>(lutBytes + ((ah >> (8 * q)) & 0xFFu));
+                    const std::uint32_t il = q == 0 ? (al & 0xFFu) : __builtin_amdgcn_ubfe(al, 8 * q, 8);
+                    const std::uint32_t ih = q == 0 ? (ah & 0xFFu) : __builtin_amdgcn_ubfe(ah, 8 * q, 8);
+                    const vu2 x0 = *reinterpret_cast<const vu2*>(lutBytes + il);
+                    const vu2 x1 = *reinterpret_cast<const vu2*>(lutBytes + ih);
                     A[4 * w + q] = vu4{x0.x, x0.y, x1.x, x1.y};
                 }
             }
+        };
+        auto mma = [&](const vu4 (&A)[T], const BinaryStage<G, NT>& o) {
 #pragma unroll
             for (int t = 0; t < T; ++t) {
                 const bf16x8 av = __builtin_bit_cast(bf16x8, A[t]);
@@ -943,13 +945,32 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_binary_kernel(TileArgs a) 
             load(c0 + k, ring[k]);
             __builtin_amdgcn_sched_barrier(0);
         }
-        // steps past `last` (the ring's tail) multiply the zero step's patterns
+        // A step's operands are expanded while the previous step's products
+        // run (the lookups' latency hides behind the MFMAs; expanded before
+        // each step's products: 6.77 ms against 6.71).  Steps past `last`
+        // (the ring's tail) multiply the zero step's patterns.
+        vu4 A[T];
+        expand(ring[0], A);
         for (std::uint32_t p = c0; p <= last; p += NS) {
 #pragma unroll
             for (int k = 0; k < NS; ++k) {
                 load(p + k + NS - 1, ring[(k + NS - 1) % NS]);
                 __builtin_amdgcn_sched_barrier(0);
-                mma(ring[k]);
+                mma(A, ring[k]);
+                expand(ring[(k + 1) % NS], A);
+                // one MFMA, then one lookup and two VALU instructions, and so
+                // on: the next step's lookups run between this step's
+                // products (issued in a block they left the lookups' latency
+                // on every step's path: config 3 hybrid step 6.71 -> 6.60 ms;
+                // every tile's high-half products before the low-half ones
+                // measured 6.68)
+#pragma unroll
+                for (int i = 0; i < 2 * T * NT; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
     }
@@ -1060,7 +1081,9 @@ hipError_t launch_tiles(const TileArgs& a, bool split, hipStream_t st) {
 // accumulators (128 registers): one N tile at G = 16 (32 features a wave),
 // two at G = 8 (64 features a wave).
 constexpr int binary_nt(std::uint32_t G) { return G == 16 ? 1 : 2; }
-constexpr int kBinaryStages = 3;
+// Loads run three steps ahead (config 3, 64-entry steps: 6.60 ms per
+// hybrid step against 6.62 with two steps ahead).
+constexpr int kBinaryStages = 4;
 
 hipError_t launch_binary(const TileArgs& a, std::uint32_t G, hipStream_t st) {
     const dim3 grid(kXcds * tiles_blocks_per_xcd(a.numUnits, a.slices));
