@@ -96,6 +96,13 @@ def parse(argv=None):
                    help="SWTCF SpMM: VALU path against MFMA for dense tiles, synthetic tiles of k = 8..64 entries")
     p.add_argument("--swtcf-int8", action="store_true",
                    help="SWTCF SpMM on the config-3 graph at F = 128: fp32 X against int8 X")
+    p.add_argument("--swtcf-step", choices=("fp32", "int8"), default=None,
+                   help="configs 2-3: the step is launchSWTCFSpMM (fp32 X) or launchSWTCFSpMMQuantized (int8 X "
+                        "with per-row scales) over the SWTCF (S = 16) of the config's graph at the reference's "
+                        "F = 128 (for counter runs of the SWTCF SpMM)")
+    p.add_argument("--atomic-probe-mib", type=int, default=0,
+                   help="time tcc_calibration_atomic over a buffer of this many MiB (rows of 128 floats, 64-float "
+                        "segments at random rows: the SWTCF SpMM's output pattern) and print one JSON line")
     p.add_argument("--profile-convert", action="store_true",
                    help="configs 1-3: time only convertCOOToSWTCF (S = 16), warmup + steps conversions, and print "
                         "one JSON line (for rocprofv3 runs of the converter)")
@@ -538,6 +545,65 @@ def extension_timings(torch, swtcf, r32, c32, n, F, X):
     return out
 
 
+def bench_swtcf_step(args, torch, swtcf, cfg):
+    """Configs 2-3 (--swtcf-step): one launchSWTCFSpMM (or its int8 form) per
+    step over the SWTCF (S = 16) of the config's graph at F = 128, Y += A X
+    without zeroing Y between steps, as the reference's driver times it
+    (swtcf_spmm_main.cu:203-247)."""
+    from tcc_amd.graphs import make_graph
+
+    n, F = cfg["n"], 128
+    rows, cols, _ = make_graph(args.config, device="cuda")
+    r32 = rows.to(torch.int32).contiguous()
+    c32 = cols.to(torch.int32).contiguous()
+    nnz = rows.numel()
+    del rows, cols
+    m = swtcf.DeviceSWTCFMatrix(n, n, nnz, 16)
+    ws = swtcf.SWTCFConvertWorkspace(nnz, n, 16)
+    swtcf.convertCOOToSWTCF(r32, c32, nnz, m, ws)
+    assert ws.device_error() == 0
+    del ws
+    X = torch.randn((n, F), device="cuda", generator=torch.Generator(device="cuda").manual_seed(11))
+    Y = torch.zeros((n, F), device="cuda")
+    if args.swtcf_step == "fp32":
+        step = lambda: swtcf.launchSWTCFSpMM(m, X, Y, 12)
+        kernel = "swtcf_spmm_kernel (launchSWTCFSpMM, fp32 X)"
+    else:
+        scales = X.abs().amax(dim=1).clamp_min(1e-30) / 127.0
+        q = torch.round(X / scales[:, None]).clamp(-127, 127).to(torch.int8).contiguous()
+        src_global = torch.arange(n, dtype=torch.int32, device="cuda")
+        step = lambda: swtcf.launchSWTCFSpMMQuantized(m, q, scales.contiguous(), src_global, Y, 12)
+        kernel = "swtcf_spmm_kernel (launchSWTCFSpMMQuantized, int8 X, per-row scales)"
+    if args.copy_calibration_mib:
+        copy_calibration(args.copy_calibration_mib)
+    ms, median = timed_stats(step, args.steps, args.warmup)
+    flops = 2.0 * nnz * F
+    roof = roofline(flops, bytes_alg(n, n, nnz, F), ms, None, kernel)
+    config = {"workload": WORKLOADS[args.config] + "; SWTCF SpMM at F = 128, S = 16", "n": n, "nnz": nnz, "F": F}
+    return line_for(args, round(flops / (ms * 1e-3) / 1e9, 3), "GFLOP/s", ms, "fp32" if args.swtcf_step == "fp32"
+                    else "int8", config, roof, None, {"path": kernel}, median=median)
+
+
+def atomic_probe(args, torch, swtcf):
+    """tcc_calibration_atomic over a buffer of args.atomic_probe_mib MiB:
+    atomics per second for 64-float segments at random rows (rows of 128
+    floats, as the SWTCF SpMM's Y at F = 128)."""
+    from tcc_amd import _lib
+
+    rows = max(1, args.atomic_probe_mib * (1 << 20) // 512)
+    dst = torch.zeros(rows * 128, device="cuda")
+    waves = 1 << 22  # 268M atomic adds
+    st = torch.cuda.current_stream().cuda_stream
+    step = lambda: _lib.check(_lib.lib().tcc_calibration_atomic(dst.data_ptr(), rows, 128, waves, st))
+    ms, median = timed_stats(step, args.steps, args.warmup)
+    n = waves * 64
+    return {"metric": "fp32 atomic adds per second (tcc_calibration_atomic)", "buffer_mib": args.atomic_probe_mib,
+            "rows": rows, "atomics_per_launch": n, "ms": round(ms, 4), "median_ms": round(median, 4),
+            "G_atomics_per_s": round(n / (ms * 1e-3) / 1e9, 2),
+            "payload_GBps": round(4.0 * n / (ms * 1e-3) / 1e9, 1),
+            "pattern": "wave w: 64 consecutive floats (256 B) of a pseudo-random row of 128 floats, one per lane"}
+
+
 def bench_spmm(args, torch, swtcf, cfg):
     """Configs 1-3: one SpMM per step."""
     from tcc_amd.graphs import make_features, make_graph
@@ -944,6 +1010,14 @@ def main():
         return 0
     if args.swtcf_int8:
         print(json.dumps(bench_swtcf_int8(args, torch, swtcf)), flush=True)
+        return 0
+    if args.atomic_probe_mib:
+        print(json.dumps(atomic_probe(args, torch, swtcf)), flush=True)
+        return 0
+    if args.swtcf_step:
+        if args.config not in (2, 3):
+            raise SystemExit("--swtcf-step takes configs 2-3 (config 1's step is the SWTCF SpMM already)")
+        print(json.dumps(bench_swtcf_step(args, torch, swtcf, cfg)), flush=True)
         return 0
     if args.config in (1, 2, 3):
         line = bench_spmm(args, torch, swtcf, cfg)

@@ -157,6 +157,13 @@ const char* tcc_last_error(void);
  * counterpart. */
 int tcc_calibration_copy(void* dst, const void* src, size_t bytes, void* stream);
 
+/* The L2's fp32 atomic rate for the SpMM's output pattern (no reference
+ * counterpart; bench.py --atomic-probe-mib): `waves` waves each add 1.0 to
+ * 64 consecutive floats (one 256-byte segment, one per lane) of a
+ * pseudo-random row of `rowFloats` floats (a multiple of 64) among `rows`
+ * rows of dst, as a tile row's sums go to Y in the SWTCF SpMM. */
+int tcc_calibration_atomic(float* dst, uint32_t rows, uint32_t rowFloats, uint64_t waves, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -115,6 +115,7 @@ SIGNATURES = {
     "tcc_coo_to_hybrid_scaled": (ctypes.c_int, [vp, vp, u32, u32, u32, vp, vp, u32, u32, u32, u32,
                                                  ctypes.POINTER(Hybrid), vp]),
     "tcc_hybrid_release": (ctypes.c_int, [ctypes.POINTER(Hybrid)]),
+    "tcc_calibration_atomic": (ctypes.c_int, [vp, u32, u32, ctypes.c_uint64, vp]),
     "tcc_hybrid_from_bcsr": (ctypes.c_int, [ctypes.POINTER(BCSR), ctypes.c_int, u32, u32, ctypes.POINTER(Hybrid),
                                             vp]),
     "tcc_spmm_cnic_forward_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(BCSR), u32]),

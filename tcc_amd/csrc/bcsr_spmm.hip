@@ -882,6 +882,19 @@ __global__ void calibration_copy_kernel(vu4* __restrict__ dst, const vu4* __rest
         dst[i] = load_global<vu4>(src + i);
 }
 
+// Wave w adds 1.0 to the 64 floats of segment w % (rowFloats / 64) of row
+// hash(w) % rows, one per lane (tcc_calibration_atomic).
+__global__ void calibration_atomic_kernel(float* __restrict__ dst, std::uint32_t rows, std::uint32_t rowFloats,
+                                          std::uint64_t waves) {
+    const std::uint64_t w = (static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
+    if (w >= waves) return;
+    std::uint64_t h = w * 0x9E3779B97F4A7C15ull;  // a multiplicative hash spreads the rows
+    h ^= h >> 29;
+    const std::uint32_t row = static_cast<std::uint32_t>(h % rows);
+    const std::uint32_t seg = static_cast<std::uint32_t>(w % (rowFloats / kWave));
+    atomic_add_f32(dst + static_cast<std::uint64_t>(row) * rowFloats + seg * kWave + __lane_id(), 1.0f);
+}
+
 // One thread per 4 consecutive features of a row (they lie in one chunk):
 // one 8-byte store of their high halves and one 2-byte store of the low bits
 // of their two pairs (features past F: the high halves and pair bytes of the
@@ -1507,6 +1520,19 @@ int tcc_calibration_copy(void* dst, const void* src, size_t bytes, void* stream)
     const std::uint64_t n = bytes / 16;
     hipLaunchKernelGGL(calibration_copy_kernel, dim3(static_cast<unsigned>(std::min<std::uint64_t>((n + 255) / 256, 65536))),
                        dim3(256), 0, as_stream(stream), static_cast<vu4*>(dst), static_cast<const vu4*>(src), n);
+    TCC_LAUNCH_CHECK();
+    return TCC_OK;
+}
+
+int tcc_calibration_atomic(float* dst, std::uint32_t rows, std::uint32_t rowFloats, std::uint64_t waves,
+                           void* stream) {
+    clear_last_error();
+    TCC_REQUIRE(dst && rows > 0 && rowFloats >= kWave && rowFloats % kWave == 0, TCC_ERR_INVALID_ARGUMENT,
+                "calibration atomic: rows > 0, rowFloats a multiple of 64");
+    if (waves == 0) return TCC_OK;
+    TCC_REQUIRE(waves <= 0xFFFFFFFFull / kWaves * kWaves, TCC_ERR_UNSUPPORTED, "calibration atomic: too many waves");
+    hipLaunchKernelGGL(calibration_atomic_kernel, dim3(grid_for(waves * kWave, kThreads)), dim3(kThreads), 0,
+                       as_stream(stream), dst, rows, rowFloats, waves);
     TCC_LAUNCH_CHECK();
     return TCC_OK;
 }
