@@ -711,7 +711,8 @@ def bench_spmm(args, torch, swtcf, cfg):
             def step():
                 swtcf.hybrid_spmm(H, X, Y, workspace=hws)
 
-            kernel = (f"hub_tiles_binary_kernel<{H.view.tiles.group_blocks}, 1, 3> (bf16 MFMA 32x32x16 over "
+            G = H.view.tiles.group_blocks
+            kernel = (f"hub_tiles_binary_kernel<{G}, {1 if G == 16 else 2}, 4> (bf16 MFMA 32x32x16 over "
                       "split TF32(c X)) + hub_reduce_kernel + hub_rows_split_kernel, after the remainder's "
                       f"tf32_pack_kernel (column-scaled) + gather_kernel<Packed> over the {H.rest.phases}-phase "
                       "BCSR (row-scaled sums; all timed)")
