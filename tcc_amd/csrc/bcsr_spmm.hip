@@ -900,13 +900,13 @@ __global__ void calibration_atomic_kernel(float* __restrict__ dst, std::uint32_t
 // of their two pairs (features past F: the high halves and pair bytes of the
 // valid ones only, as the layout's padding is left as it is).  With
 // colScale, row r is packed as TF32(colScale[r] * X[r]) (the fp32 product,
-// then rounded).
-__global__ void tf32_pack_kernel(const float* __restrict__ X, std::uint32_t rows, std::uint32_t F,
-                                 std::uint32_t quads, unsigned char* __restrict__ out, std::uint64_t stride,
-                                 bool vec2, const float* __restrict__ colScale) {
-    const std::uint64_t i = static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    const std::uint64_t r = i / quads;
-    if (r >= rows) return;
+// then rounded).  This is thread i's quad: row r, features 4 (i - r quads)
+// and on; with smax, the quad's largest finite magnitude goes into its
+// slice's LDS maximum.
+__device__ __forceinline__ void pack_quad_body(const float* __restrict__ X, std::uint32_t F, std::uint32_t quads,
+                                               unsigned char* __restrict__ out, std::uint64_t stride, bool vec2,
+                                               const float* __restrict__ colScale, std::uint32_t* smax,
+                                               std::uint32_t W, std::uint64_t i, std::uint64_t r) {
     const std::uint32_t e = 4 * static_cast<std::uint32_t>(i - r * quads);
     const std::uint32_t valid = min(4u, F - e);
     const float* x = X + r * F + e;
@@ -932,6 +932,13 @@ __global__ void tf32_pack_kernel(const float* __restrict__ X, std::uint32_t rows
         const std::uint32_t t = __float_as_uint(tf32_rna(v[k]));
         b[k] = k < valid ? (__builtin_isnan(v[k]) ? (t | 0x00400000u) : t) : 0u;
     }
+    if (smax) {
+        std::uint32_t m = 0;
+#pragma unroll
+        for (unsigned k = 0; k < 4; ++k)
+            if ((b[k] & 0x7FFFFFFFu) < 0x7F800000u) m = max(m, b[k] & 0x7FFFFFFFu);
+        if (m) atomicMax(&smax[e / W], m);
+    }
     const auto lo_byte = [](std::uint32_t b0, std::uint32_t b1) {
         return static_cast<unsigned char>(((b0 >> 13) & 7u) | (((b1 >> 13) & 7u) << 3));
     };
@@ -946,6 +953,29 @@ __global__ void tf32_pack_kernel(const float* __restrict__ X, std::uint32_t rows
             *reinterpret_cast<std::uint16_t*>(row + at.hi + 2 * k) = static_cast<std::uint16_t>(b[k] >> 16);
         row[at.lo] = lo_byte(b[0], b[1]);
         if (valid > 2) row[at.lo + 1] = lo_byte(b[2], b[3]);
+    }
+}
+
+// With sliceMax (non-null, zeroed by the caller), the largest finite |TF32
+// value| bits of each slice of W features (W % 4 == 0) over all rows go to
+// sliceMax[(blockIdx.x % kPackSliceMaxRows) * slices + s] through atomicMax:
+// each workgroup gathers its own in LDS first.
+__global__ void tf32_pack_kernel(const float* __restrict__ X, std::uint32_t rows, std::uint32_t F,
+                                 std::uint32_t quads, unsigned char* __restrict__ out, std::uint64_t stride,
+                                 bool vec2, const float* __restrict__ colScale, std::uint32_t* __restrict__ sliceMax,
+                                 std::uint32_t W, std::uint32_t slices) {
+    extern __shared__ std::uint32_t smax[];
+    if (sliceMax) {  // uniform
+        for (std::uint32_t s = threadIdx.x; s < slices; s += blockDim.x) smax[s] = 0;
+        __syncthreads();
+    }
+    const std::uint64_t i = static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const std::uint64_t r = i / quads;
+    if (r < rows) pack_quad_body(X, F, quads, out, stride, vec2, colScale, sliceMax ? smax : nullptr, W, i, r);
+    if (sliceMax) {
+        __syncthreads();
+        for (std::uint32_t s = threadIdx.x; s < slices; s += blockDim.x)
+            if (smax[s]) atomicMax(&sliceMax[(blockIdx.x % kPackSliceMaxRows) * slices + s], smax[s]);
     }
 }
 
@@ -1448,7 +1478,8 @@ int bcsr_spmm_scaled(const tcc_bcsr* A, const float* X, float* Y, std::uint32_t 
 }
 
 int tf32_pack_scaled(const float* X, std::uint32_t rows, std::uint32_t featureDim, const float* colScale,
-                     void* packed, hipStream_t st) {
+                     void* packed, hipStream_t st, std::uint32_t* sliceMax, std::uint32_t sliceWidth,
+                     std::uint32_t slices) {
     TCC_REQUIRE(X && packed && feature_dim_ok(featureDim), TCC_ERR_INVALID_ARGUMENT, "invalid TF32 pack arguments");
     TCC_REQUIRE(reinterpret_cast<std::uintptr_t>(packed) % 16 == 0, TCC_ERR_INVALID_ARGUMENT,
                 "packed buffer must be 16-byte aligned");
@@ -1458,8 +1489,16 @@ int tf32_pack_scaled(const float* X, std::uint32_t rows, std::uint32_t featureDi
     TCC_REQUIRE(n <= 0xFFFFFFFFull * 256, TCC_ERR_UNSUPPORTED, "TF32 pack too large");
     // two 8-byte loads a thread when every row starts 8-byte aligned
     const bool vec2 = featureDim % 2 == 0 && reinterpret_cast<std::uintptr_t>(X) % 8 == 0;
-    hipLaunchKernelGGL(tf32_pack_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, X, rows, featureDim, quads,
-                       static_cast<unsigned char*>(packed), packed_stride(featureDim), vec2, colScale);
+    if (sliceMax) {
+        TCC_REQUIRE(sliceWidth % 4 == 0 && sliceWidth > 0 && slices > 0 && slices <= kPackMaxSlices &&
+                        static_cast<std::uint64_t>(slices) * sliceWidth >= featureDim,
+                    TCC_ERR_INVALID_ARGUMENT, "invalid slice maxima of the TF32 pack");
+        TCC_HIP_CHECK(fill<std::uint32_t>(sliceMax, static_cast<std::uint64_t>(kPackSliceMaxRows) * slices, 0u, st));
+    }
+    hipLaunchKernelGGL(tf32_pack_kernel, dim3(grid_for(n, 256)), dim3(256),
+                       sliceMax ? slices * sizeof(std::uint32_t) : 0, st, X, rows, featureDim, quads,
+                       static_cast<unsigned char*>(packed), packed_stride(featureDim), vec2, colScale, sliceMax,
+                       sliceWidth, slices);
     TCC_LAUNCH_CHECK();
     return TCC_OK;
 }

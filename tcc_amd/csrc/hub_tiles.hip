@@ -39,6 +39,7 @@
 // remainder's gather runs first and fills Y; the tiles are added into it.
 #include <algorithm>
 #include <cstring>
+#include <type_traits>
 
 #include "../../include/tcc_spmm_cnic.h"
 #include "../../include/tcc_swtcf.h"
@@ -104,6 +105,9 @@ __device__ __forceinline__ void bf16_split(float x, std::uint16_t& hi, std::uint
     const std::uint32_t b = __float_as_uint(x);
     hi = static_cast<std::uint16_t>(b >> 16);
     if ((b & 0x7F800000u) == 0x7F800000u) {
+        // inf keeps lo = 0 (x - hi would be NaN); a NaN whose payload lies
+        // in the low half keeps NaN through the quiet bit
+        if (b & 0x007FFFFFu) hi |= 0x0040u;
         lo = 0;
         return;
     }
@@ -465,6 +469,11 @@ struct TileArgs {
     std::uint32_t numUnits;
     std::uint32_t slices;    // feature slices per unit (ldh / features per wave)
     const std::uint32_t* unitOrder;  // launch order of the units, or null
+    // Binary tiles over half records (hub_rows_half_kernel): per (column
+    // block, slice) 1 where Xs holds fp16 values, and per slice the factor
+    // 2^-e that undoes the slice's scale; null: bf16 records throughout.
+    const unsigned char* halfFlags;
+    const float* sliceDown;
 };
 
 // This wave's unit and 64-feature slice (unit >= numUnits: no work).  The
@@ -520,6 +529,21 @@ __device__ __forceinline__ void load_step_cols(const std::uint32_t* stepCol, std
                                                int (&cols)[kColRegs]) {
 #pragma unroll
     for (int k = 0; k < kColRegs; ++k) cols[k] = static_cast<int>(stepCol[min(p0 + 64u * k + __lane_id(), last)]);
+}
+
+// As load_step_cols, with bit 31 of each step's entry set where the step's
+// column block holds half records for this wave's slice (flags non-null).
+__device__ __forceinline__ void load_step_cols_flagged(const std::uint32_t* stepCol, std::uint32_t p0,
+                                                       std::uint32_t last, int (&cols)[kColRegs],
+                                                       const unsigned char* flags, std::uint32_t slices,
+                                                       std::uint32_t slice) {
+    load_step_cols(stepCol, p0, last, cols);
+    if (!flags) return;
+#pragma unroll
+    for (int k = 0; k < kColRegs; ++k) {
+        const std::uint32_t c = static_cast<std::uint32_t>(cols[k]);
+        if (flags[static_cast<std::uint64_t>(c) * slices + slice]) cols[k] = static_cast<int>(c | 0x80000000u);
+    }
 }
 
 // Column block of step q of the unit (q uniform): lane q % 64 of register q / 64.
@@ -692,6 +716,156 @@ __global__ void hub_rows_split_kernel(const float* __restrict__ X, std::uint32_t
     out[3] = lo[1];
 }
 
+// Half records for binary tiles.  The hub rows' TF32 values x (of
+// colScale[c] * X[c]) are multiplied by 2^e, one e per slice of W features
+// (a wave's slice), chosen from the slice's largest finite |x| over the hub
+// rows so that it maps into [2^15, 2^16): e = 15 - E for a largest magnitude
+// in [2^E, 2^(E+1)), at least 0 and at most 126 (0 for a slice without
+// one).  A (column block, slice) record set whose every 2^e x is an fp16
+// value (no finite value overflows; a value below 2^(-14-e) must lie on the
+// fp16 grid) holds those fp16 values in its hi slots, and its flag is 1;
+// any other keeps the exact bf16 halves of 2^e x.  Both are exact, and the
+// tile kernel multiplies its sums by 2^-e.
+//
+// hub_absmax_kernel: thread i takes 4 consecutive features of hub row
+// i / quads (the flat (row, quad) range cut into one stretch per workgroup,
+// walked 256 quads at a time), the workgroup's largest finite |x| bits per
+// slice gathered with LDS atomics, then added by atomicMax into row
+// blockIdx.x % kPackSliceMaxRows of partial[kPackSliceMaxRows][slices] (zeroed
+// first; the remainder's TF32 pack fills the same rows over all columns
+// when a hybrid runs one).  hub_scale_kernel (one workgroup per slice)
+// reduces the rows into 2^e and 2^-e.
+__global__ void __launch_bounds__(kThreads) hub_absmax_kernel(const float* __restrict__ X, std::uint32_t F,
+                                                             const std::uint32_t* __restrict__ order,
+                                                             std::uint32_t hubCols, const float* __restrict__ colScale,
+                                                             std::uint32_t W, std::uint32_t slices,
+                                                             std::uint32_t* __restrict__ partial) {
+    extern __shared__ std::uint32_t smax[];
+    for (std::uint32_t s = threadIdx.x; s < slices; s += blockDim.x) smax[s] = 0;
+    __syncthreads();
+    const std::uint32_t quads = (F + 3) / 4;
+    const std::uint64_t total = static_cast<std::uint64_t>(hubCols) * quads;
+    const std::uint64_t per = (total + gridDim.x - 1) / gridDim.x;
+    const std::uint64_t begin = per * blockIdx.x, end = min(total, begin + per);
+    // four quads a thread at a time, their loads issued together
+    constexpr std::uint32_t kItems = 4;
+    for (std::uint64_t i0 = begin + threadIdx.x; i0 < end; i0 += kItems * blockDim.x) {
+        std::uint32_t src[kItems], f[kItems];
+#pragma unroll
+        for (std::uint32_t j = 0; j < kItems; ++j) {
+            const std::uint64_t i = min(i0 + j * blockDim.x, end - 1);
+            f[j] = 4 * static_cast<std::uint32_t>(i % quads);
+            src[j] = order[i / quads];
+        }
+        float v[kItems][4], sc[kItems];
+#pragma unroll
+        for (std::uint32_t j = 0; j < kItems; ++j) {
+            sc[j] = colScale ? colScale[src[j]] : 1.0f;
+            const float* x = X + static_cast<std::uint64_t>(src[j]) * F;
+#pragma unroll
+            for (std::uint32_t k = 0; k < 4; ++k) v[j][k] = x[min(f[j] + k, F - 1)];
+        }
+#pragma unroll
+        for (std::uint32_t j = 0; j < kItems; ++j) {
+            if (i0 + j * blockDim.x >= end) break;
+            std::uint32_t m = 0;
+#pragma unroll
+            for (std::uint32_t k = 0; k < 4; ++k) {
+                const std::uint32_t b = __float_as_uint(tf32_rna(v[j][k] * sc[j])) & 0x7FFFFFFFu;
+                if (f[j] + k < F && b < 0x7F800000u) m = max(m, b);
+            }
+            if (m) atomicMax(&smax[f[j] / W], m);
+        }
+    }
+    __syncthreads();
+    for (std::uint32_t s = threadIdx.x; s < slices; s += blockDim.x)
+        if (smax[s]) atomicMax(&partial[(blockIdx.x % kPackSliceMaxRows) * slices + s], smax[s]);
+}
+
+__global__ void __launch_bounds__(kThreads) hub_scale_kernel(const std::uint32_t* __restrict__ partial,
+                                                            std::uint32_t blocks, std::uint32_t slices,
+                                                            float* __restrict__ up, float* __restrict__ down) {
+    __shared__ std::uint32_t wmax[kThreads / kWave];
+    const std::uint32_t s = blockIdx.x;
+    std::uint32_t m = 0;
+    for (std::uint32_t b = threadIdx.x; b < blocks; b += blockDim.x)
+        m = max(m, partial[static_cast<std::uint64_t>(b) * slices + s]);
+#pragma unroll
+    for (int d = kWave / 2; d > 0; d >>= 1)
+        m = max(m, static_cast<std::uint32_t>(__shfl_xor(static_cast<int>(m), d, kWave)));
+    if (__lane_id() == 0) wmax[threadIdx.x / kWave] = m;
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    for (std::uint32_t w = 1; w < kThreads / kWave; ++w) m = max(m, wmax[w]);
+    const int e = m == 0 ? 0 : max(0, min(126, 15 - (static_cast<int>(m >> 23) - 127)));
+    up[s] = __uint_as_float(static_cast<std::uint32_t>(127 + e) << 23);
+    down[s] = __uint_as_float(static_cast<std::uint32_t>(127 - e) << 23);
+}
+
+// As hub_rows_split_kernel over 2^e-scaled values, with half records where
+// exact (above).  Thread (column block, feature f), W = 32 or 64 features a
+// slice: the lanes of one slice agree through a ballot.
+__global__ void hub_rows_half_kernel(const float* __restrict__ X, std::uint32_t F,
+                                     const std::uint32_t* __restrict__ order, std::uint32_t hubCols,
+                                     std::uint32_t hubRows, std::uint32_t ldh, const float* __restrict__ colScale,
+                                     const float* __restrict__ up, std::uint32_t W, std::uint16_t* __restrict__ Xs,
+                                     unsigned char* __restrict__ flags) {
+    const std::uint64_t i = static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const std::uint32_t cb = static_cast<std::uint32_t>(i / ldh), f = static_cast<std::uint32_t>(i % ldh);
+    if (cb >= hubRows / kTile) return;  // whole waves: ldh is a multiple of 64
+    std::uint32_t src[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) src[k] = order[min(cb * kTile + k, hubCols > 0 ? hubCols - 1 : 0u)];
+    const std::uint32_t fc = min(f, F > 0 ? F - 1 : 0u);
+    float x[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) x[k] = X[static_cast<std::uint64_t>(src[k]) * F + fc];
+    if (colScale) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) x[k] *= colScale[src[k]];
+    }
+    const float sc = up[f / W];
+    float t[16];
+    bool exact = true;
+    std::uint16_t h[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const bool live = f < F && cb * kTile + k < hubCols;
+        t[k] = live ? tf32_rna(x[k]) * sc : 0.0f;
+        const _Float16 hk = static_cast<_Float16>(t[k]);
+        h[k] = __builtin_bit_cast(std::uint16_t, hk);
+        exact &= __builtin_isnan(t[k]) || __float_as_uint(static_cast<float>(hk)) == __float_as_uint(t[k]);
+    }
+    // the slice's lanes: all 64 (W = 64) or this lane's half-wave (W = 32)
+    const std::uint64_t bad = __ballot(!exact);
+    const unsigned lane = __lane_id();
+    const bool half = W >= kWave ? bad == 0 : ((bad >> (lane & 32u)) & 0xFFFFFFFFull) == 0;
+    vu4* out = reinterpret_cast<vu4*>(Xs + (static_cast<std::uint64_t>(cb) * ldh + f) * 32);
+    if (half) {
+        vu4 hv[2];
+#pragma unroll
+        for (int k = 0; k < 16; k += 2)
+            hv[k / 8][(k % 8) / 2] = static_cast<std::uint32_t>(h[k]) | static_cast<std::uint32_t>(h[k + 1]) << 16;
+        out[0] = hv[0];
+        out[1] = hv[1];
+    } else {
+        vu4 hi[2], lo[2];
+#pragma unroll
+        for (int k = 0; k < 16; k += 2) {
+            std::uint16_t h0, l0, h1, l1;
+            bf16_split(t[k], h0, l0);
+            bf16_split(t[k + 1], h1, l1);
+            hi[k / 8][(k % 8) / 2] = static_cast<std::uint32_t>(h0) | static_cast<std::uint32_t>(h1) << 16;
+            lo[k / 8][(k % 8) / 2] = static_cast<std::uint32_t>(l0) | static_cast<std::uint32_t>(l1) << 16;
+        }
+        out[0] = hi[0];
+        out[1] = hi[1];
+        out[2] = lo[0];
+        out[3] = lo[1];
+    }
+    if (f % W == 0) flags[static_cast<std::uint64_t>(cb) * (ldh / W) + f / W] = half ? 1 : 0;
+}
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 template <int G>
@@ -821,47 +995,56 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_split_kernel(TileArgs a) {
 // Binary tiles (TCC_TILES_BINARY).  The reference's tensor-core operand is
 // the block's bitmap as {0, 1} (src/swtcf_spmm.cu:193-200); here the
 // patterns of 32-row tiles (row blocks 2t and 2t+1 of a group) are the A
-// operand of v_mfma_f32_32x32x16_bf16 (lane l: row l%32, columns
+// operand of v_mfma_f32_32x32x16_f16 or _bf16 (lane l: row l%32, columns
 // 8(l/32)..+7 of the tile's 16; B lane l: column 8(l/32) + e, feature l%32;
 // D lane l register r: row 8(r/4) + 4(l/32) + r%4, feature l%32; checked on
-// the GPU), and the values come as row and column scales: Xs holds
-// TF32(colScale[c] * X[c]) split into bf16 halves, so one MFMA against the
-// halves' high parts and one against their low parts form
-// sum_c P[i][c] * TF32(c x) exactly in fp32 products, and the row scale is
-// applied to the fp32 sum when it is stored.
+// the GPU), and the values come as row and column scales.  Xs holds
+// 2^e TF32(colScale[c] * X[c]) (e per slice, hub_rows_half_kernel): as fp16
+// values where that is exact for the (column block, slice), one f16 MFMA a
+// tile, else as bf16 halves, one MFMA against the high parts and one
+// against the low parts.  Either way sum_c P[i][c] 2^e TF32(c x) is formed
+// from exact products in fp32; the sum is multiplied by 2^-e, and by the
+// row scale when it is stored.
 //
 // Expansion: lane l's byte of tile t (8 bits: row l%32, column half l/32)
-// becomes 8 bf16 of 0 or 1.0 through two 8-byte reads of a 16-entry table
-// in LDS, one per 4-bit half.  The next step's lookups run between this
-// step's products (2 G/2 reads; an 8-byte read of 64 lanes is 4 LDS cycles
-// against 64 MFMA cycles of the two products per tile).  Every tile of a step is
-// multiplied: the builder stores every entry of a chosen step, and steps
+// becomes 8 fp16 or bf16 of 0 or 1.0 through two 8-byte reads of a
+// 16-entry table in LDS, one per 4-bit half.  The next step's lookups run
+// between this step's products (2 G/2 reads; an 8-byte read of 64 lanes is
+// 4 LDS cycles against 32 MFMA cycles of a product).  Every tile of a step
+// is multiplied: the builder stores every entry of a chosen step, and steps
 // are nearly full (config 3: 7.97 of 8 tiles a step).
 //
-// One wave per (unit, slice of 32 NT features): per step, the G/2 pattern
-// bytes of its lane (one 8- or 4-byte load) and 2 NT 16-byte Xs loads, then
-// G NT MFMAs.  A unit's steps are read 256 at a time (step columns one per
-// lane in four registers); loads run NS - 1 steps ahead in a ring of NS
-// stages, as in the valued kernels.
+// One wave per (unit, slice of 32 NT features).  A unit's steps are taken
+// 256 at a time (step columns one per lane in four registers), listed by
+// record kind, and multiplied in two passes: the fp16 steps (the G/2
+// pattern bytes of its lane, one 8- or 4-byte load, and NT 16-byte Xs
+// loads, then G NT / 2 MFMAs) and then the bf16 steps (2 NT Xs loads, G NT
+// MFMAs).  Loads run NS - 1 steps ahead in a ring of NS stages, as in the
+// valued kernels.
 template <int G, int NT>
 struct BinaryStage {
     std::uint32_t m[G / 8];  // this lane's G/2 pattern bytes (byte t: 32-row tile t)
-    vu4 h[NT];               // N tile u: xh of columns 8(l/32)..+7, feature f0 + 32u + l%32
-    vu4 lo[NT];              // the same columns' xl
+    vu4 h[NT];               // N tile u: xh (or the fp16 x) of columns 8(l/32)..+7, feature f0 + 32u + l%32
+    vu4 lo[NT];              // the same columns' xl (bf16 records)
 };
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 template <int G, int NT, int NS>
 __global__ void __launch_bounds__(kThreads) hub_tiles_binary_kernel(TileArgs a) {
     static_assert(G == 8 || G == 16, "binary tiles: G is 8 or 16");
     constexpr int T = G / 2;  // 32-row tiles a step
-    // lut[x] = 4 bf16 (0 or 1.0) of the 4 bits of x, low bit first
-    __shared__ vu2 lut[16];
-    if (threadIdx.x < 16) {
-        const unsigned x = threadIdx.x;
-        auto pair = [](unsigned y) { return ((y & 1u) ? 0x3F80u : 0u) | ((y & 2u) ? 0x3F800000u : 0u); };
-        lut[x] = vu2{pair(x & 3u), pair(x >> 2)};
+    // lut[x] = 4 fp16 (0 or 1.0) of the 4 bits of x, low bit first, then
+    // lut[16 + x] the same in bf16
+    __shared__ vu2 lut[32];
+    // each wave's steps of the current stretch: fp16 steps from the front,
+    // bf16 steps from the back, as (column block << 8 | step - c0)
+    __shared__ std::uint32_t stepList[kThreads / kWave][kMaxUnitSteps];
+    if (threadIdx.x < 32) {
+        const unsigned x = threadIdx.x & 15u, one = threadIdx.x < 16 ? 0x3C00u : 0x3F80u;
+        auto pair = [one](unsigned y) { return ((y & 1u) ? one : 0u) | ((y & 2u) ? one << 16 : 0u); };
+        lut[threadIdx.x] = vu2{pair(x & 3u), pair(x >> 2)};
     }
     __syncthreads();
     const char* lutBytes = reinterpret_cast<const char*>(lut);
@@ -874,11 +1057,12 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_binary_kernel(TileArgs a) 
     const std::uint32_t pslot = a.unitPartial[unit];
     const std::uint32_t f0 = slice * (32 * NT);
     const unsigned lj = lane & 31u, lh = lane >> 5;
-    // Xs: 16 hi then 16 lo bf16 per (column block, feature); this lane's
+    // Xs: 16 hi then 16 lo values per (column block, feature); this lane's
     // column half of each
     const char* xb = reinterpret_cast<const char*>(a.Xh) + (static_cast<std::uint64_t>(f0 + lj) * 64 + lh * 16);
     const std::uint64_t cbStride = static_cast<std::uint64_t>(a.ldh) * 64;
     const std::uint32_t* mb = a.tileMasks + lane * (G / 8);
+    std::uint32_t* list = stepList[threadIdx.x / kWave];
 
     f32x16 acc[T][NT];
 #pragma unroll
@@ -888,13 +1072,20 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_binary_kernel(TileArgs a) 
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[t][u][r] = 0.0f;
 
-    for (std::uint32_t c0 = p0; c0 < p1; c0 += kMaxUnitSteps) {
-        const std::uint32_t last = min(c0 + kMaxUnitSteps, p1) - 1;
-        int cols[kColRegs];
-        load_step_cols(a.stepCol, c0, last, cols);
-        auto load = [&](std::uint32_t p, BinaryStage<G, NT>& o) {
-            const std::uint32_t pa = p <= last ? p : a.zeroStep;
-            const std::uint32_t col = step_col(cols, min(p, last) - c0);
+    // One pass of the ring over `count` listed steps (entry i at base[i]),
+    // all fp16 (HALF) or all bf16 records: the two kinds of product stay in
+    // separate loops (one loop holding both took the accumulators out of
+    // place, 230 AGPRs and one wave per SIMD).
+    auto run = [&](auto halfTag, const int (&ents)[kColRegs], std::uint32_t count, std::uint32_t c0) {
+        constexpr bool HALF = decltype(halfTag)::value;
+        const char* lb = lutBytes + (HALF ? 0 : 128);
+        // Listed step i (i >= count: the zero step, multiplying zeros by
+        // zeros; B read from a real step's column would turn an inf there
+        // into NaN in every row).
+        auto load = [&](std::uint32_t i, BinaryStage<G, NT>& o) {
+            const bool live = i < count;
+            const std::uint32_t e = step_col(ents, live ? i : 0);
+            const std::uint32_t pa = live ? c0 + (e & 0xFFu) : a.zeroStep;
             const std::uint32_t* mp = mb + static_cast<std::uint64_t>(pa) * (8 * G);
             if constexpr (G == 16) {
                 const vu2 w = load_global<vu2>(mp);
@@ -903,11 +1094,11 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_binary_kernel(TileArgs a) 
             } else {
                 o.m[0] = load_global<std::uint32_t>(mp);
             }
-            const char* rb = xb + col * cbStride;
+            const char* rb = xb + static_cast<std::uint64_t>(e >> 8) * cbStride;
 #pragma unroll
             for (int u = 0; u < NT; ++u) {
-                o.h[u] = load_global<vu4>(rb + u * 32 * 64);
-                o.lo[u] = load_global<vu4>(rb + u * 32 * 64 + 32);
+                o.h[u] = live ? load_global<vu4>(rb + u * 32 * 64) : vu4{0u, 0u, 0u, 0u};
+                o.lo[u] = HALF || !live ? vu4{0u, 0u, 0u, 0u} : load_global<vu4>(rb + u * 32 * 64 + 32);
             }
         };
         // every tile's lookups of one step: byte addresses 8 * nibble
@@ -919,8 +1110,8 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_binary_kernel(TileArgs a) 
                 for (int q = 0; q < 4 && 4 * w + q < T; ++q) {
                     const std::uint32_t il = q == 0 ? (al & 0xFFu) : __builtin_amdgcn_ubfe(al, 8 * q, 8);
                     const std::uint32_t ih = q == 0 ? (ah & 0xFFu) : __builtin_amdgcn_ubfe(ah, 8 * q, 8);
-                    const vu2 x0 = *reinterpret_cast<const vu2*>(lutBytes + il);
-                    const vu2 x1 = *reinterpret_cast<const vu2*>(lutBytes + ih);
+                    const vu2 x0 = *reinterpret_cast<const vu2*>(lb + il);
+                    const vu2 x1 = *reinterpret_cast<const vu2*>(lb + ih);
                     A[4 * w + q] = vu4{x0.x, x0.y, x1.x, x1.y};
                 }
             }
@@ -928,13 +1119,18 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_binary_kernel(TileArgs a) 
         auto mma = [&](const vu4 (&A)[T], const BinaryStage<G, NT>& o) {
 #pragma unroll
             for (int t = 0; t < T; ++t) {
-                const bf16x8 av = __builtin_bit_cast(bf16x8, A[t]);
 #pragma unroll
                 for (int u = 0; u < NT; ++u) {
-                    acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, o.h[u]),
-                                                                        acc[t][u], 0, 0, 0);
-                    acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, o.lo[u]),
-                                                                        acc[t][u], 0, 0, 0);
+                    if constexpr (HALF) {
+                        acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                            __builtin_bit_cast(f16x8, A[t]), __builtin_bit_cast(f16x8, o.h[u]), acc[t][u], 0, 0, 0);
+                    } else {
+                        const bf16x8 av = __builtin_bit_cast(bf16x8, A[t]);
+                        acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, o.h[u]),
+                                                                            acc[t][u], 0, 0, 0);
+                        acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, o.lo[u]),
+                                                                            acc[t][u], 0, 0, 0);
+                    }
                 }
             }
         };
@@ -942,37 +1138,83 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_binary_kernel(TileArgs a) 
         BinaryStage<G, NT> ring[NS];
 #pragma unroll
         for (int k = 0; k < NS - 1; ++k) {
-            load(c0 + k, ring[k]);
+            load(k, ring[k]);
             __builtin_amdgcn_sched_barrier(0);
         }
         // A step's operands are expanded while the previous step's products
         // run (the lookups' latency hides behind the MFMAs; expanded before
-        // each step's products: 6.77 ms against 6.71).  Steps past `last`
-        // (the ring's tail) multiply the zero step's patterns.
+        // each step's products: 6.77 ms against 6.71).
         vu4 A[T];
         expand(ring[0], A);
-        for (std::uint32_t p = c0; p <= last; p += NS) {
+        for (std::uint32_t i = 0; i < count; i += NS) {
 #pragma unroll
             for (int k = 0; k < NS; ++k) {
-                load(p + k + NS - 1, ring[(k + NS - 1) % NS]);
+                load(i + k + NS - 1, ring[(k + NS - 1) % NS]);
                 __builtin_amdgcn_sched_barrier(0);
                 mma(A, ring[k]);
                 expand(ring[(k + 1) % NS], A);
-                // one MFMA, then one lookup and two VALU instructions, and so
-                // on: the next step's lookups run between this step's
-                // products (issued in a block they left the lookups' latency
-                // on every step's path: config 3 hybrid step 6.71 -> 6.60 ms;
-                // every tile's high-half products before the low-half ones
-                // measured 6.68)
+                // one MFMA, then lookups and VALU instructions of the next
+                // step's expansion, and so on: the next step's lookups run
+                // between this step's products (issued in a block they left
+                // the lookups' latency on every step's path: config 3 hybrid
+                // step 6.71 -> 6.60 ms; every tile's high-half products
+                // before the low-half ones measured 6.68)
+                constexpr int kMfma = (HALF ? 1 : 2) * T * NT;
 #pragma unroll
-                for (int i = 0; i < 2 * T * NT; ++i) {
+                for (int j = 0; j < kMfma; ++j) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, HALF ? 2 : 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, HALF ? 4 : 2, 0);
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
+    };
+
+    for (std::uint32_t c0 = p0; c0 < p1; c0 += kMaxUnitSteps) {
+        const std::uint32_t last = min(c0 + kMaxUnitSteps, p1) - 1;
+        int cols[kColRegs];
+        load_step_cols_flagged(a.stepCol, c0, last, cols, a.halfFlags, a.slices, slice);
+        // the stretch's steps listed by kind, in step order within each
+        std::uint32_t nh = 0, nf = 0;
+#pragma unroll
+        for (int k = 0; k < kColRegs; ++k) {
+            const std::uint32_t q = 64u * k + lane;
+            const bool valid = c0 + q <= last;
+            const std::uint32_t cw = static_cast<std::uint32_t>(cols[k]);
+            const bool isHalf = valid && (cw >> 31) != 0, isFull = valid && (cw >> 31) == 0;
+            const std::uint64_t bh = __ballot(isHalf), bf = __ballot(isFull);
+            const std::uint32_t entry = (cw & 0x7FFFFFFFu) << 8 | q;
+            if (isHalf) list[nh + __builtin_amdgcn_mbcnt_hi(static_cast<std::uint32_t>(bh >> 32),
+                                                           __builtin_amdgcn_mbcnt_lo(static_cast<std::uint32_t>(bh), 0u))] = entry;
+            if (isFull) list[kMaxUnitSteps - 1 - (nf + __builtin_amdgcn_mbcnt_hi(static_cast<std::uint32_t>(bf >> 32),
+                                                           __builtin_amdgcn_mbcnt_lo(static_cast<std::uint32_t>(bf), 0u)))] = entry;
+            nh += static_cast<std::uint32_t>(__popcll(bh));
+            nf += static_cast<std::uint32_t>(__popcll(bf));
+        }
+        __builtin_amdgcn_wave_barrier();
+        // the lists back in registers, entry i in lane i % 64 of register i / 64
+        int ents[kColRegs];
+        if (nh) {
+#pragma unroll
+            for (int k = 0; k < kColRegs; ++k) ents[k] = static_cast<int>(list[64 * k + lane]);
+            run(std::true_type{}, ents, nh, c0);
+        }
+        if (nf) {
+#pragma unroll
+            for (int k = 0; k < kColRegs; ++k)
+                ents[k] = static_cast<int>(list[min(kMaxUnitSteps - nf + 64 * k + lane, kMaxUnitSteps - 1)]);
+            run(std::false_type{}, ents, nf, c0);
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+    // the slice's scale undone (an exact power of two)
+    if (a.sliceDown) {
+        const float down = a.sliceDown[slice];
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int u = 0; u < NT; ++u) acc[t][u] *= down;
     }
 
     // D register r of tile t, N tile u: row 32t + 8(r/4) + 4lh + r%4 of the
@@ -1569,11 +1811,34 @@ int tcc_hybrid_from_bcsr(const tcc_bcsr* A, int useValues, std::uint32_t minStep
     return build_hybrid(P, out, stream);
 }
 
+// Binary tiles' half records: the per-workgroup maxima of hub_absmax_kernel,
+// 2^e and 2^-e per slice, and a flag per (column block, slice).
+constexpr std::uint32_t kAbsmaxBlocks = 2048;
+constexpr std::uint32_t kMaxHalfSlices = kPackMaxSlices;
+
+struct HalfSpace {
+    std::size_t partial, up, down, flags, bytes;
+};
+
+inline HalfSpace half_space(std::uint32_t hubRows, std::uint32_t slices) {
+    HalfSpace h;
+    h.partial = 0;
+    h.up = align_up(std::size_t(4) * kPackSliceMaxRows * slices);
+    h.down = h.up + align_up(std::size_t(4) * slices);
+    h.flags = h.down + align_up(std::size_t(4) * slices);
+    h.bytes = h.flags + align_up(static_cast<std::size_t>(hubRows / kTile) * slices);
+    return h;
+}
+
 size_t tcc_hub_tiles_workspace_bytes(const tcc_hub_tiles* T, std::uint32_t featureDim) {
     if (!T || featureDim == 0) return 0;
     const std::size_t ldh = hub_ldh(featureDim);
-    return align_up(static_cast<size_t>(hub_rows(T->hub_cols)) * ldh * sizeof(float)) +
-           static_cast<size_t>(T->num_partial_units) * T->group_blocks * kTile * ldh * sizeof(float);
+    std::size_t bytes = align_up(static_cast<size_t>(hub_rows(T->hub_cols)) * ldh * sizeof(float)) +
+                        align_up(static_cast<size_t>(T->num_partial_units) * T->group_blocks * kTile * ldh * sizeof(float));
+    const std::uint32_t slices = static_cast<std::uint32_t>(ldh / (32u * binary_nt(T->group_blocks)));
+    if (T->tile_format == TCC_TILES_BINARY && slices <= kMaxHalfSlices)
+        bytes += half_space(hub_rows(T->hub_cols), slices).bytes;
+    return bytes;
 }
 
 size_t tcc_hybrid_workspace_bytes(const tcc_hybrid* H, std::uint32_t featureDim) {
@@ -1582,9 +1847,26 @@ size_t tcc_hybrid_workspace_bytes(const tcc_hybrid* H, std::uint32_t featureDim)
            tcc_hub_tiles_workspace_bytes(&H->tiles, featureDim);
 }
 
-int tcc_hub_tiles_spmm(const tcc_hub_tiles* T, const float* X, float* Y, std::uint32_t featureDim, void* workspace,
-                       size_t workspaceBytes, void* stream) {
-    clear_last_error();
+// Where the slice maxima of binary tiles' half records sit in a tiles
+// workspace, with the slice width and count (nullptr: bf16 records, no
+// maxima).
+static std::uint32_t* hub_slice_max(const tcc_hub_tiles* T, std::uint32_t featureDim, void* workspace,
+                                    std::uint32_t& W, std::uint32_t& slices) {
+    if (T->tile_format != TCC_TILES_BINARY) return nullptr;
+    const std::uint32_t ldh = hub_ldh(featureDim);
+    W = 32u * binary_nt(T->group_blocks);
+    slices = ldh / W;
+    if (slices > kMaxHalfSlices) return nullptr;
+    const std::uint64_t n = static_cast<std::uint64_t>(hub_rows(T->hub_cols)) * ldh;
+    char* halfBase = static_cast<char*>(workspace) + align_up(n * sizeof(float)) +
+                     align_up(static_cast<size_t>(T->num_partial_units) * T->group_blocks * kTile * ldh * sizeof(float));
+    return reinterpret_cast<std::uint32_t*>(halfBase + half_space(hub_rows(T->hub_cols), slices).partial);
+}
+
+// tcc_hub_tiles_spmm; maxReady: the slice maxima of half records are in the
+// workspace already (the hybrid's remainder pack gathered them).
+static int hub_tiles_spmm(const tcc_hub_tiles* T, const float* X, float* Y, std::uint32_t featureDim, void* workspace,
+                          size_t workspaceBytes, void* stream, bool maxReady) {
     TCC_REQUIRE(T && X && Y && featureDim >= 1 && T->rowOrder && T->groupStepOffset, TCC_ERR_INVALID_ARGUMENT,
                 "invalid hub tiles SpMM arguments");
     if (T->num_units == 0) return TCC_OK;
@@ -1604,7 +1886,34 @@ int tcc_hub_tiles_spmm(const tcc_hub_tiles* T, const float* X, float* Y, std::ui
     float* Xh = static_cast<float*>(workspace);
     const std::uint32_t hubRows = hub_rows(T->hub_cols);
     const std::uint64_t n = static_cast<std::uint64_t>(hubRows) * ldh;
-    if (split || binary) {
+    const std::uint32_t slices = ldh / (binary ? 32u * binary_nt(T->group_blocks) : kSlice);
+    char* halfBase = static_cast<char*>(workspace) + align_up(n * sizeof(float)) +
+                     align_up(static_cast<size_t>(T->num_partial_units) * T->group_blocks * kTile * ldh * sizeof(float));
+    const HalfSpace hs = half_space(hubRows, slices);
+    // Binary tiles take half records unless the slices' maxima would not fit
+    // one workgroup's LDS (F above 2^19); then bf16 records throughout.
+    const bool halfRecords = binary && slices <= kMaxHalfSlices;
+    if (halfRecords) {
+        // half records: each slice's scale from its largest magnitude, then
+        // fp16 records where exact and bf16 halves elsewhere
+        const std::uint32_t W = ldh / slices;
+        std::uint32_t* partial = reinterpret_cast<std::uint32_t*>(halfBase + hs.partial);
+        float* up = reinterpret_cast<float*>(halfBase + hs.up);
+        float* down = reinterpret_cast<float*>(halfBase + hs.down);
+        unsigned char* flags = reinterpret_cast<unsigned char*>(halfBase + hs.flags);
+        if (!maxReady) {
+            TCC_HIP_CHECK(fill<std::uint32_t>(partial, static_cast<std::uint64_t>(kPackSliceMaxRows) * slices, 0u, st));
+            hipLaunchKernelGGL(hub_absmax_kernel, dim3(kAbsmaxBlocks), dim3(kThreads), slices * sizeof(std::uint32_t),
+                               st, X, featureDim, T->hubColOrder, T->hub_cols, T->colScale, W, slices, partial);
+            TCC_LAUNCH_CHECK();
+        }
+        hipLaunchKernelGGL(hub_scale_kernel, dim3(slices), dim3(kThreads), 0, st, partial, kPackSliceMaxRows, slices, up,
+                           down);
+        TCC_LAUNCH_CHECK();
+        hipLaunchKernelGGL(hub_rows_half_kernel, dim3(grid_for(n / kTile, kThreads)), dim3(kThreads), 0, st, X,
+                           featureDim, T->hubColOrder, T->hub_cols, hubRows, ldh, T->colScale, up, W,
+                           reinterpret_cast<std::uint16_t*>(Xh), flags);
+    } else if (split || binary) {
         hipLaunchKernelGGL(hub_rows_split_kernel, dim3(grid_for(n / kTile, kThreads)), dim3(kThreads), 0, st, X,
                            featureDim, T->hubColOrder, T->hub_cols, hubRows, ldh, binary ? T->colScale : nullptr,
                            reinterpret_cast<std::uint16_t*>(Xh));
@@ -1632,7 +1941,11 @@ int tcc_hub_tiles_spmm(const tcc_hub_tiles* T, const float* X, float* Y, std::ui
     a.zeroStep = T->num_steps;
     a.F = featureDim;
     a.numUnits = T->num_units;
-    a.slices = ldh / (binary ? 32u * binary_nt(T->group_blocks) : kSlice);
+    a.slices = slices;
+    if (halfRecords) {
+        a.halfFlags = reinterpret_cast<const unsigned char*>(halfBase + hs.flags);
+        a.sliceDown = reinterpret_cast<const float*>(halfBase + hs.down);
+    }
     const std::uint64_t waves = static_cast<std::uint64_t>(a.numUnits) * a.slices;
     TCC_REQUIRE(waves <= 0x7FFFFFFFull, TCC_ERR_UNSUPPORTED, "hub tiles SpMM launch too large");
     hipError_t e;
@@ -1656,6 +1969,12 @@ int tcc_hub_tiles_spmm(const tcc_hub_tiles* T, const float* X, float* Y, std::ui
     return TCC_OK;
 }
 
+int tcc_hub_tiles_spmm(const tcc_hub_tiles* T, const float* X, float* Y, std::uint32_t featureDim, void* workspace,
+                       size_t workspaceBytes, void* stream) {
+    clear_last_error();
+    return hub_tiles_spmm(T, X, Y, featureDim, workspace, workspaceBytes, stream, false);
+}
+
 int tcc_hybrid_spmm(const tcc_hybrid* H, const float* X, float* Y, std::uint32_t featureDim, int accumulate,
                     void* workspace, size_t workspaceBytes, void* stream) {
     clear_last_error();
@@ -1675,16 +1994,22 @@ int tcc_hybrid_spmm(const tcc_hybrid* H, const float* X, float* Y, std::uint32_t
     const std::uint64_t gathers = 8ull * H->rest.num_TCBlocks;
     const std::size_t packedBytes = align_up(tcc_tf32_packed_bytes(H->rest.num_cols, featureDim) + 16);
     int rc;
+    // The tiles' half records take each slice's largest magnitude: the pack
+    // of every column's scaled row gathers it on the way.
+    void* tilesWs = static_cast<char*>(workspace) + packedBytes;
+    std::uint32_t W = 0, slices = 0;
+    std::uint32_t* sliceMax = hub_slice_max(&H->tiles, featureDim, tilesWs, W, slices);
+    bool maxReady = false;
     if (colScale || gathers >= 16ull * H->rest.num_cols) {
-        rc = tf32_pack_scaled(X, H->rest.num_cols, featureDim, colScale, workspace, st);
+        rc = tf32_pack_scaled(X, H->rest.num_cols, featureDim, colScale, workspace, st, sliceMax, W, slices);
         if (rc) return rc;
+        maxReady = sliceMax != nullptr;
         rc = bcsr_spmm_packed_scaled(&H->rest, workspace, Y, featureDim, accumulate, rowScale, st);
     } else {
         rc = bcsr_spmm_scaled(&H->rest, X, Y, featureDim, accumulate, rowScale, st);
     }
     if (rc) return rc;
-    return tcc_hub_tiles_spmm(&H->tiles, X, Y, featureDim, static_cast<char*>(workspace) + packedBytes,
-                              workspaceBytes - packedBytes, stream);
+    return hub_tiles_spmm(&H->tiles, X, Y, featureDim, tilesWs, workspaceBytes - packedBytes, stream, maxReady);
 }
 
 }  // extern "C"

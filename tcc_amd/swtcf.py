@@ -466,6 +466,23 @@ def hybrid_spmm(H: HybridMatrix, X: torch.Tensor, Y: torch.Tensor | None = None,
     return Y
 
 
+def hub_tiles_spmm(H: HybridMatrix, X: torch.Tensor, Y: torch.Tensor, workspace: torch.Tensor | None = None,
+                   stream=None) -> torch.Tensor:
+    """Y[out_rows x F] += the hub tiles' share of A X alone
+    (tcc_hub_tiles_spmm, without the remainder); `workspace` as hybrid_spmm,
+    at least tcc_hub_tiles_workspace_bytes + 16 bytes."""
+    X = _f32(X, "X")
+    F = X.shape[1]
+    need = int(_lib.lib().tcc_hub_tiles_workspace_bytes(ctypes.byref(H.view.tiles), F))
+    if workspace is None:
+        workspace = torch.empty(need + 16, dtype=torch.uint8, device=X.device)
+    base = workspace.data_ptr()
+    shift = (-base) % 16
+    check(_lib.lib().tcc_hub_tiles_spmm(ctypes.byref(H.view.tiles), X.data_ptr(), Y.data_ptr(), F, base + shift,
+                                        workspace.numel() - shift, _stream(stream)))
+    return Y
+
+
 def bcsc_spmm(A: BlockMatrix, X: torch.Tensor, Y: torch.Tensor, stream=None) -> torch.Tensor:
     """Y[num_rows x F] += A X with atomics."""
     X = _f32(X, "X")

@@ -27,6 +27,10 @@ Checked through the C-ABI:
 - an Inf in a hub column's feature row: rows with that column get Inf, the
   other rows of every group with a step in its column block get NaN (0 * Inf
   in the tiles' products), every other row stays finite;
+- half records: fp16 values of 2^e x where exact for a whole (column block,
+  32-feature slice), the bf16 halves elsewhere, both in one product (a
+  feature below the fp16 grid and one above its range), through the hybrid
+  and through tcc_hub_tiles_spmm alone;
 - argument errors.
 """
 import numpy as np
@@ -293,6 +297,67 @@ def test_binary_inf_in_hub_column(gpu, oracle, G):
     assert rel_l2(Y[:, 1:], want[:, 1:]) <= REL
     keep = ~(has | exposed)
     assert rel_l2(Y[keep, 0], want[keep, 0]) <= REL
+
+
+def mixed_range_features(nc, F, seed):
+    """N(0, 1) features with feature 0 at 1e-20 of that and feature 40 at
+    1e30: with one power-of-two scale per 32-feature slice, the fp16 form of
+    2^e x is inexact in every record of the slices holding them (feature 0
+    falls below the fp16 grid, feature 40 above its range), so those slices
+    take the bf16 halves and the others fp16."""
+    X = np.random.default_rng(seed).standard_normal((nc, F)).astype(np.float32)
+    X[:, 0] *= np.float32(1e-20)
+    if F > 40:
+        X[:, 40] *= np.float32(1e30)
+    return X
+
+
+def column_rel(Y, want, cols):
+    return max(rel_l2(Y[:, j], want[:, j]) for j in cols)
+
+
+@pytest.mark.parametrize("G, scale", [(16, "symnorm"), (8, "random"), (16, "none")])
+def test_binary_half_and_bf16_records(gpu, oracle, G, scale):
+    """The tiles multiply fp16 records where 2^e x is exact in fp16 and
+    the bf16 halves elsewhere, in one product: the tiny feature 0, the huge
+    feature 40 and every other feature each within 1e-5 of the scaled
+    oracle, column by column."""
+    from tcc_amd import swtcf
+
+    nr, nc, F = 700, 900, 100
+    dst, src = random_coo(nr, nc, 60000, 31, True)
+    r, c = scales(nr, nc, dst, src, scale, 7)
+    H = build(swtcf, dst, src, nr, nc, r, c, min_step_nnz=16, group_blocks=G)
+    assert H.view.tiles.num_steps > 0
+    X = mixed_range_features(nc, F, 3)
+    want = scaled_product(oracle, dst, src, nr, X, r, c)
+    Y = swtcf.hybrid_spmm(H, torch.from_numpy(X).cuda()).cpu().numpy()[:nr].astype(np.float64)
+    assert column_rel(Y, want, [0]) <= REL and column_rel(Y, want, [40]) <= REL
+    assert column_rel(Y, want, [j for j in range(F) if j not in (0, 40)]) <= REL
+
+
+@pytest.mark.parametrize("G", [8, 16])
+def test_binary_tiles_alone(gpu, oracle, G):
+    """tcc_hub_tiles_spmm on its own (its slice scales from its own pass
+    over the hub rows, not the remainder's pack): Y += the product of the
+    tile entries only, against the scaled oracle of exactly those entries,
+    with the mixed-range features above."""
+    from tcc_amd import swtcf
+
+    nr, nc, F = 500, 700, 72
+    dst, src = random_coo(nr, nc, 40000, 37, True)
+    r, c = scales(nr, nc, dst, src, "symnorm", 1)
+    H = build(swtcf, dst, src, nr, nc, r, c, min_step_nnz=16, group_blocks=G)
+    lay = reference_binary_layout(dst, src, nr, nc, 16, G, DEFAULT_UNIT_STEPS, r, c)
+    tile = ~lay["rest"]
+    assert tile.any() and (~tile).any()
+    X = mixed_range_features(nc, F, 4)
+    Y0 = np.random.default_rng(9).standard_normal((H.out_rows, F)).astype(np.float32)
+    Y = swtcf.hub_tiles_spmm(H, torch.from_numpy(X).cuda(), torch.from_numpy(Y0).cuda()).cpu().numpy()
+    want = scaled_product(oracle, dst[tile], src[tile], nr, X, r, c) + Y0[:nr].astype(np.float64)
+    got = Y[:nr].astype(np.float64)
+    assert column_rel(got, want, [0]) <= REL and column_rel(got, want, [40]) <= REL
+    assert column_rel(got, want, [j for j in range(F) if j not in (0, 40)]) <= REL
 
 
 def test_binary_errors(gpu):
