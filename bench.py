@@ -57,16 +57,17 @@ PHASES = 4
 # columns are ordered by degree.  Config 3's values are sym-normalised,
 # v_ij = r_i c_j with r = rowdeg^-1/2 and c = coldeg^-1/2, so the product
 # is diag(r) P diag(c) X over the pattern P: steps (256 rows x 16 columns of
-# the reordered matrix) holding at least the builder's default of entries go
-# to binary tiles on bf16 MFMA over the split TF32(c X), the rest to the
-# phased gather of the packed TF32(c X) rows, each row sum scaled by r
-# (tcc_coo_to_hybrid_scaled).  Measured at config 3 (step ms): phased gather
-# alone 17.35; valued split tiles (each TF32 value as two bf16, four bf16
-# products) 8.86 at 16 nnz a tile, groups of 8; binary tiles 6.76 at 64
-# entries a step.  The valued hybrid is timed beside it under `extra`.
+# the reordered matrix) holding at least BINARY_MIN_STEP_NNZ entries go to
+# binary tiles on MFMA over 2^e TF32(c X) (fp16 where exact, else bf16
+# halves), the rest to the phased gather of the packed TF32(c X) rows, each
+# row sum scaled by r (tcc_coo_to_hybrid_scaled).  Measured at config 3
+# (step ms): phased gather alone 17.35; valued split tiles (each TF32 value
+# as two bf16, four bf16 products) 8.86 at 16 nnz a tile, groups of 8;
+# binary tiles with bf16 halves only 6.56 at 64 entries a step, with fp16
+# records 6.22 at 40.  The valued hybrid is timed beside it under `extra`.
 HUB_MIN_TILE_NNZ = 16
 HUB_GROUP_BLOCKS = 8
-BINARY_MIN_STEP_NNZ = 64
+BINARY_MIN_STEP_NNZ = 40
 BINARY_GROUP_BLOCKS = 16
 CPU_SAMPLE_NNZ = 16_000_000
 
@@ -676,12 +677,14 @@ def bench_spmm(args, torch, swtcf, cfg):
             extra["hybrid_build_ms"] = round((time.perf_counter() - t_h) * 1e3, 3)
             t = H.view.tiles
             extra["hub"] = {"format": "binary 16x16 patterns, multiplied as 32-row tiles on "
-                                      "v_mfma_f32_32x32x16_bf16 against bf16 hi/lo of TF32(c X); rows scaled by r",
+                                      "v_mfma_f32_32x32x16_f16 against fp16 2^e TF32(c X) where exact (else "
+                                      "_bf16 against its bf16 halves); rows scaled by 2^-e r",
                             "min_step_nnz": BINARY_MIN_STEP_NNZ, "group_blocks": t.group_blocks,
                             "steps": t.num_steps, "units": t.num_units, "partial_units": t.num_partial_units,
                             "hub_cols": t.hub_cols, "tile_nnz": t.nnz, "tile_nnz_frac": round(t.nnz / nnz, 4),
                             "rest_blocks": H.rest.view.num_TCBlocks,
-                            "bf16_mfma_flops_per_step": 4.0 * 256 * t.group_blocks * t.num_steps * F,
+                            # one f16 MFMA a tile and feature slice (two bf16 for a bf16 record)
+                            "mfma_flops_per_step_fp16_records": 2.0 * 256 * t.group_blocks * t.num_steps * F,
                             "values_as_scales_max_rel_diff": fact}
         Y = torch.empty((A.out_windows * 8, F), device="cuda")
         phased = f" over the {A.phases}-phase BCSR (Y zero-filled first)" if A.phases > 1 else ""
@@ -712,12 +715,14 @@ def bench_spmm(args, torch, swtcf, cfg):
                 swtcf.hybrid_spmm(H, X, Y, workspace=hws)
 
             G = H.view.tiles.group_blocks
-            kernel = (f"hub_tiles_binary_kernel<{G}, {1 if G == 16 else 2}, 4> (bf16 MFMA 32x32x16 over "
-                      "split TF32(c X)) + hub_reduce_kernel + hub_rows_split_kernel, after the remainder's "
-                      f"tf32_pack_kernel (column-scaled) + gather_kernel<Packed> over the {H.rest.phases}-phase "
+            kernel = (f"hub_tiles_binary_kernel<{G}, {1 if G == 16 else 2}, 4> (f16 MFMA 32x32x16 over "
+                      "2^e TF32(c X), bf16 halves where fp16 is not exact) + hub_reduce_kernel + "
+                      "hub_rows_half_kernel + hub_scale_kernel, after the remainder's tf32_pack_kernel "
+                      f"(column-scaled, slice maxima) + gather_kernel<Packed> over the {H.rest.phases}-phase "
                       "BCSR (row-scaled sums; all timed)")
-            extra["path"] = (f"binary hybrid: steps of >= {BINARY_MIN_STEP_NNZ} entries as pattern tiles on bf16 "
-                             f"MFMA over split TF32(c X) + packed gather of the remainder's pattern over its "
+            extra["path"] = (f"binary hybrid: steps of >= {BINARY_MIN_STEP_NNZ} entries as pattern tiles on MFMA "
+                             f"over 2^e TF32(c X) (fp16 where exact, else bf16 halves) + packed gather of the "
+                             f"remainder's pattern over its "
                              f"{H.rest.phases}-phase BCSR; A = diag(r) P diag(c) with the sym-norm scales")
         elif reuse >= PACK_MIN_REUSE:
             # each step packs X to TF32 rows of 2.5 B/element, then gathers them

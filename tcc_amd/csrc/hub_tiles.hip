@@ -66,13 +66,14 @@ constexpr std::uint32_t kMaxUnitSteps = 256;        // a unit's step columns sit
 constexpr int kColRegs = kMaxUnitSteps / 64;
 constexpr std::uint32_t kDefaultMinTileNnz = 16;
 constexpr std::uint32_t kDefaultGroupBlocks = 8;
-// Binary tiles: steps of at least 64 entries, groups of 16 row blocks,
+// Binary tiles: steps of at least 40 entries, groups of 16 row blocks,
 // units of up to 512 steps (the kernel reads a unit's step list 256 steps
 // at a time, so units are not bound by kMaxUnitSteps).  Config 3 (step ms,
-// 512-step units): 10.58 / 7.91 / 7.20 / 6.78 / 6.76 at 8 / 16 / 32 / 48 /
-// 64 entries with G = 16; 7.49 / 6.93 at 16 / 32 with G = 8; 7.29 / 7.20 /
-// 7.31 with 256 / 512 / 1024-step units at 32 entries.
-constexpr std::uint32_t kDefaultMinStepNnz = 64;
+// 512-step units, G = 16, fp16 records): 6.33 / 6.22 / 6.22 / 6.28 / 6.28
+// at 24 / 32 / 40 / 48 / 64 entries; 6.71 at 32 with G = 8; 6.32 with
+// 384-step units at 48.  (With bf16 records only: 10.58 / 7.91 / 7.20 /
+// 6.78 / 6.76 at 8 / 16 / 32 / 48 / 64 entries.)
+constexpr std::uint32_t kDefaultMinStepNnz = 40;
 constexpr std::uint32_t kDefaultBinaryGroupBlocks = 16;
 constexpr std::uint32_t kDefaultBinaryUnitSteps = 512;
 constexpr std::uint32_t kNoSlot = 0xFFFFFFFFu;
