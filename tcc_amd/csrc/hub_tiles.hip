@@ -475,6 +475,10 @@ struct TileArgs {
     // 2^-e that undoes the slice's scale; null: bf16 records throughout.
     const unsigned char* halfFlags;
     const float* sliceDown;
+    // Binary tiles: store the sums into Y instead of adding them (the
+    // hybrid's remainder adds into Y after; hub_zero_rows_kernel zeroes the
+    // rows no unit writes).
+    int storeY;
 };
 
 // This wave's unit and 64-feature slice (unit >= numUnits: no work).  The
@@ -500,17 +504,18 @@ struct StepOperands {
 };
 
 // Y[row][f..f+3] += s (features below F only).
-__device__ __forceinline__ void add_quad(float* row, std::uint32_t f, std::uint32_t F, bool vec, const f32x4& s) {
+__device__ __forceinline__ void add_quad(float* row, std::uint32_t f, std::uint32_t F, bool vec, const f32x4& s,
+                                         bool store = false) {
     if (!row || f >= F) return;
     float* out = row + f;
     if (vec) {
-        f32x4 y = load_global<vf4>(out);
+        f32x4 y = store ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : load_global<vf4>(out);
         y += s;
         *reinterpret_cast<f32x4*>(out) = y;
     } else {
 #pragma unroll
         for (int u = 0; u < 4; ++u)
-            if (f + u < F) out[u] += s[u];
+            if (f + u < F) out[u] = store ? s[u] : out[u] + s[u];
     }
 }
 
@@ -843,12 +848,14 @@ __global__ void hub_rows_half_kernel(const float* __restrict__ X, std::uint32_t 
     const bool half = W >= kWave ? bad == 0 : ((bad >> (lane & 32u)) & 0xFFFFFFFFull) == 0;
     vu4* out = reinterpret_cast<vu4*>(Xs + (static_cast<std::uint64_t>(cb) * ldh + f) * 32);
     if (half) {
+        // dense: feature j of the slice at 32 j bytes of the slice's region
+        vu4* hout = reinterpret_cast<vu4*>(Xs + (static_cast<std::uint64_t>(cb) * ldh + f / W * W) * 32 + (f % W) * 16);
         vu4 hv[2];
 #pragma unroll
         for (int k = 0; k < 16; k += 2)
             hv[k / 8][(k % 8) / 2] = static_cast<std::uint32_t>(h[k]) | static_cast<std::uint32_t>(h[k + 1]) << 16;
-        out[0] = hv[0];
-        out[1] = hv[1];
+        hout[0] = hv[0];
+        hout[1] = hv[1];
     } else {
         vu4 hi[2], lo[2];
 #pragma unroll
@@ -1058,9 +1065,11 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_binary_kernel(TileArgs a) 
     const std::uint32_t pslot = a.unitPartial[unit];
     const std::uint32_t f0 = slice * (32 * NT);
     const unsigned lj = lane & 31u, lh = lane >> 5;
-    // Xs: 16 hi then 16 lo values per (column block, feature); this lane's
-    // column half of each
+    // Xs per (column block, slice): bf16 records of 16 hi then 16 lo values
+    // per feature (64 bytes), or fp16 records of 16 values per feature (32
+    // bytes, the slice's first half); this lane's column half of each
     const char* xb = reinterpret_cast<const char*>(a.Xh) + (static_cast<std::uint64_t>(f0 + lj) * 64 + lh * 16);
+    const char* xbh = reinterpret_cast<const char*>(a.Xh) + (static_cast<std::uint64_t>(f0) * 64 + lj * 32 + lh * 16);
     const std::uint64_t cbStride = static_cast<std::uint64_t>(a.ldh) * 64;
     const std::uint32_t* mb = a.tileMasks + lane * (G / 8);
     std::uint32_t* list = stepList[threadIdx.x / kWave];
@@ -1095,10 +1104,10 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_binary_kernel(TileArgs a) 
             } else {
                 o.m[0] = load_global<std::uint32_t>(mp);
             }
-            const char* rb = xb + static_cast<std::uint64_t>(e >> 8) * cbStride;
+            const char* rb = (HALF ? xbh : xb) + static_cast<std::uint64_t>(e >> 8) * cbStride;
 #pragma unroll
             for (int u = 0; u < NT; ++u) {
-                o.h[u] = live ? load_global<vu4>(rb + u * 32 * 64) : vu4{0u, 0u, 0u, 0u};
+                o.h[u] = live ? load_global<vu4>(rb + u * 32 * (HALF ? 32 : 64)) : vu4{0u, 0u, 0u, 0u};
                 o.lo[u] = HALF || !live ? vu4{0u, 0u, 0u, 0u} : load_global<vu4>(rb + u * 32 * 64 + 32);
             }
         };
@@ -1247,7 +1256,7 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_binary_kernel(TileArgs a) 
 #pragma unroll
                 for (int u = 0; u < NT; ++u) {
                     const std::uint32_t f = f0 + 32 * u + lj;
-                    const bool live = rows[v] != TCC_SWTCF_INVALID_ROW_SLOT && f < a.F;
+                    const bool live = rows[v] != TCC_SWTCF_INVALID_ROW_SLOT && f < a.F && !a.storeY;
                     y[v][u] = live ? a.Y[static_cast<std::uint64_t>(rows[v]) * a.F + f] : 0.0f;
                 }
 #pragma unroll
@@ -1294,7 +1303,29 @@ __global__ void __launch_bounds__(kThreads) hub_reduce_kernel(TileArgs a, std::u
     if (orow == TCC_SWTCF_INVALID_ROW_SLOT) return;
     if (a.rowScale) s[0] *= a.rowScale[slotRow];
     const bool vec = a.F % 4 == 0 && (reinterpret_cast<std::uintptr_t>(a.Y) & 15u) == 0;
-    add_quad(a.Y + static_cast<std::uint64_t>(orow) * a.F, f, a.F, vec, s[0]);
+    add_quad(a.Y + static_cast<std::uint64_t>(orow) * a.F, f, a.F, vec, s[0], a.storeY != 0);
+}
+
+// With storeY: zero the Y rows no unit writes, those of the groups without
+// steps and the padding rows numRows..outRows-1: wave w of the grid takes row
+// slot w (slots of rowOrder first, then the padding rows), a row of F floats
+// in coalesced stores.
+__global__ void __launch_bounds__(kThreads) hub_zero_rows_kernel(TileArgs a, std::uint32_t G, std::uint32_t numSlots,
+                                                                std::uint32_t numRows, std::uint32_t outRows) {
+    const std::uint32_t w = (blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+    std::uint32_t row;
+    if (w < numSlots) {
+        const std::uint32_t g = w / (G * kTile);
+        if (a.groupStepOffset[g + 1] > a.groupStepOffset[g]) return;  // its units write its rows
+        row = a.rowOrder[w];
+        if (row == TCC_SWTCF_INVALID_ROW_SLOT) return;
+    } else if (w < numSlots + (outRows - numRows)) {
+        row = numRows + (w - numSlots);
+    } else {
+        return;
+    }
+    float* y = a.Y + static_cast<std::uint64_t>(row) * a.F;
+    for (std::uint32_t f = __lane_id(); f < a.F; f += kWave) y[f] = 0.0f;
 }
 
 inline std::uint32_t hub_ldh(std::uint32_t F) { return (F + kSlice - 1) / kSlice * kSlice; }
@@ -1867,10 +1898,15 @@ static std::uint32_t* hub_slice_max(const tcc_hub_tiles* T, std::uint32_t featur
 // tcc_hub_tiles_spmm; maxReady: the slice maxima of half records are in the
 // workspace already (the hybrid's remainder pack gathered them).
 static int hub_tiles_spmm(const tcc_hub_tiles* T, const float* X, float* Y, std::uint32_t featureDim, void* workspace,
-                          size_t workspaceBytes, void* stream, bool maxReady) {
+                          size_t workspaceBytes, void* stream, bool maxReady, bool storeY = false,
+                          std::uint32_t outRows = 0) {
     TCC_REQUIRE(T && X && Y && featureDim >= 1 && T->rowOrder && T->groupStepOffset, TCC_ERR_INVALID_ARGUMENT,
                 "invalid hub tiles SpMM arguments");
-    if (T->num_units == 0) return TCC_OK;
+    if (T->num_units == 0) {
+        // storeY: no unit writes any row
+        if (storeY) TCC_HIP_CHECK(fill<float>(Y, static_cast<std::uint64_t>(outRows) * featureDim, 0.0f, as_stream(stream)));
+        return TCC_OK;
+    }
     TCC_REQUIRE(T->stepCol && T->units && T->hubColOrder && T->unitPartial &&
                     (T->num_shared_groups == 0 || T->sharedGroups),
                 TCC_ERR_INVALID_ARGUMENT, "invalid hub tiles SpMM arguments");
@@ -1943,6 +1979,7 @@ static int hub_tiles_spmm(const tcc_hub_tiles* T, const float* X, float* Y, std:
     a.F = featureDim;
     a.numUnits = T->num_units;
     a.slices = slices;
+    a.storeY = storeY ? 1 : 0;
     if (halfRecords) {
         a.halfFlags = reinterpret_cast<const unsigned char*>(halfBase + hs.flags);
         a.sliceDown = reinterpret_cast<const float*>(halfBase + hs.down);
@@ -1961,6 +1998,14 @@ static int hub_tiles_spmm(const tcc_hub_tiles* T, const float* X, float* Y, std:
         }
     }
     TCC_HIP_CHECK(e);
+    if (storeY) {
+        TCC_REQUIRE(outRows >= T->num_rows, TCC_ERR_INVALID_ARGUMENT, "hub tiles SpMM: fewer output rows than rows");
+        const std::uint32_t numSlots = T->num_groups * T->group_blocks * kTile;
+        const std::uint64_t waves = static_cast<std::uint64_t>(numSlots) + (outRows - T->num_rows);
+        hipLaunchKernelGGL(hub_zero_rows_kernel, dim3(grid_for(waves * kWave, kThreads)), dim3(kThreads), 0, st, a,
+                           T->group_blocks, numSlots, T->num_rows, outRows);
+        TCC_LAUNCH_CHECK();
+    }
     if (T->num_shared_groups == 0) return TCC_OK;
     const std::uint64_t reduceBlocks = static_cast<std::uint64_t>(T->num_shared_groups) * (ldh / kSlice) * T->group_blocks;
     TCC_REQUIRE(reduceBlocks <= 0x7FFFFFFFull, TCC_ERR_UNSUPPORTED, "hub tiles SpMM launch too large");
@@ -1983,34 +2028,46 @@ int tcc_hybrid_spmm(const tcc_hybrid* H, const float* X, float* Y, std::uint32_t
     TCC_REQUIRE(workspaceBytes >= tcc_hybrid_workspace_bytes(H, featureDim) &&
                     reinterpret_cast<std::uintptr_t>(workspace) % 16 == 0,
                 TCC_ERR_INVALID_ARGUMENT, "hybrid SpMM workspace too small or misaligned (tcc_hybrid_workspace_bytes)");
-    // The remainder's product writes (or adds into) Y, over packed TF32 rows
-    // when its rows are gathered often (8 blocks per column on average,
-    // 16 gathers per row) or its columns are scaled, else over X; then the
-    // tiles add theirs.  Binary tiles' scales apply to the remainder too:
-    // column scales while packing, row scales to each row's sum.
+    // The remainder's product runs over packed TF32 rows when its rows are
+    // gathered often (8 blocks per column on average, 16 gathers per row) or
+    // its columns are scaled, else over X.  Binary tiles' scales apply to the
+    // remainder too: column scales while packing, row scales to each row's
+    // sum.  Binary tiles without accumulate run first and store their sums
+    // (zeros in the rows no unit writes), and the remainder then adds into
+    // Y: no zero fill of Y for the phased remainder's atomics, and no reads
+    // of Y in the tiles' stores.  Otherwise the remainder writes (or adds
+    // into) Y and the tiles add theirs.
     const bool binary = H->tiles.tile_format == TCC_TILES_BINARY;
     const float* colScale = binary ? H->tiles.colScale : nullptr;
     const float* rowScale = binary ? H->restRowScale : nullptr;
     const hipStream_t st = as_stream(stream);
     const std::uint64_t gathers = 8ull * H->rest.num_TCBlocks;
     const std::size_t packedBytes = align_up(tcc_tf32_packed_bytes(H->rest.num_cols, featureDim) + 16);
+    const bool packs = colScale || gathers >= 16ull * H->rest.num_cols;
     int rc;
     // The tiles' half records take each slice's largest magnitude: the pack
     // of every column's scaled row gathers it on the way.
     void* tilesWs = static_cast<char*>(workspace) + packedBytes;
+    const size_t tilesBytes = workspaceBytes - packedBytes;
     std::uint32_t W = 0, slices = 0;
     std::uint32_t* sliceMax = hub_slice_max(&H->tiles, featureDim, tilesWs, W, slices);
     bool maxReady = false;
-    if (colScale || gathers >= 16ull * H->rest.num_cols) {
+    if (packs) {
         rc = tf32_pack_scaled(X, H->rest.num_cols, featureDim, colScale, workspace, st, sliceMax, W, slices);
         if (rc) return rc;
         maxReady = sliceMax != nullptr;
-        rc = bcsr_spmm_packed_scaled(&H->rest, workspace, Y, featureDim, accumulate, rowScale, st);
-    } else {
-        rc = bcsr_spmm_scaled(&H->rest, X, Y, featureDim, accumulate, rowScale, st);
     }
-    if (rc) return rc;
-    return hub_tiles_spmm(&H->tiles, X, Y, featureDim, tilesWs, workspaceBytes - packedBytes, stream, maxReady);
+    const bool tilesFirst = binary && !accumulate;
+    if (tilesFirst) {
+        const std::uint32_t outRows = H->rest.num_rowWindows / std::max(1u, H->rest.phases) * 8;
+        rc = hub_tiles_spmm(&H->tiles, X, Y, featureDim, tilesWs, tilesBytes, stream, maxReady, true, outRows);
+        if (rc) return rc;
+    }
+    const int restAccumulate = tilesFirst ? 1 : accumulate;
+    rc = packs ? bcsr_spmm_packed_scaled(&H->rest, workspace, Y, featureDim, restAccumulate, rowScale, st)
+               : bcsr_spmm_scaled(&H->rest, X, Y, featureDim, restAccumulate, rowScale, st);
+    if (rc || tilesFirst) return rc;
+    return hub_tiles_spmm(&H->tiles, X, Y, featureDim, tilesWs, tilesBytes, stream, maxReady);
 }
 
 }  // extern "C"
