@@ -63,11 +63,13 @@ PHASES = 4
 # row sum scaled by r (tcc_coo_to_hybrid_scaled).  Measured at config 3
 # (step ms): phased gather alone 17.35; valued split tiles (each TF32 value
 # as two bf16, four bf16 products) 8.86 at 16 nnz a tile, groups of 8;
-# binary tiles with bf16 halves only 6.56 at 64 entries a step, with fp16
-# records 6.22 at 40.  The valued hybrid is timed beside it under `extra`.
+# binary tiles with bf16 halves only 6.56 at 64 entries a step; with fp16
+# records, the tiles before the remainder, 5.72 at 36 entries and 768-step
+# units (the builder's defaults).  The valued hybrid is timed beside it
+# under `extra`.
 HUB_MIN_TILE_NNZ = 16
 HUB_GROUP_BLOCKS = 8
-BINARY_MIN_STEP_NNZ = 40
+BINARY_MIN_STEP_NNZ = 36
 BINARY_GROUP_BLOCKS = 16
 CPU_SAMPLE_NNZ = 16_000_000
 

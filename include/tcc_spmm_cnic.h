@@ -325,8 +325,8 @@ int tcc_coo_to_hybrid(const uint32_t* dRow, const uint32_t* dCol, const float* d
  * of a device COO (row = destination, col = source, no duplicate pairs;
  * dRowScale [numRows] and dColScale [numCols] device arrays, either NULL
  * for ones), with binary tiles (TCC_TILES_BINARY): steps of at least
- * minStepNnz entries (0 = 40), groupBlocks 8 or 16 (0 = 16), unitSteps
- * 0 = 512 (any number: the SpMM reads a unit's step list 256 steps at a
+ * minStepNnz entries (0 = 36), groupBlocks 8 or 16 (0 = 16), unitSteps
+ * 0 = 768 (any number: the SpMM reads a unit's step list 256 steps at a
  * time), phases as tcc_coo_to_hybrid.  The remainder holds the pattern
  * (data NULL); its gather reads the column-scaled packed rows and scales
  * its row sums.  The scales are copied.  Synchronises `stream`; free with
@@ -342,7 +342,7 @@ int tcc_hybrid_release(tcc_hybrid* H);
  * same graph many times, such as full-graph training).  With useValues = 0
  * the entries count as 1.0, as the reference's kernels read them
  * (spmm_kernel.cu:96-102): binary tiles (tcc_coo_to_hybrid_scaled without
- * scales, minStepNnz 0 = 40); else the values of `data` (value of bit i of
+ * scales, minStepNnz 0 = 36); else the values of `data` (value of bit i of
  * block b = data[tcOffset[b] + rank]) in split-TF32 tiles (tcc_coo_to_hybrid,
  * TCC_TILES_BF16X2, minTileNnz 16, groups of 8).  Bits in padding columns
  * (>= num_cols) or rows (>= num_rows) are ignored, as the gather ignores

@@ -66,16 +66,17 @@ constexpr std::uint32_t kMaxUnitSteps = 256;        // a unit's step columns sit
 constexpr int kColRegs = kMaxUnitSteps / 64;
 constexpr std::uint32_t kDefaultMinTileNnz = 16;
 constexpr std::uint32_t kDefaultGroupBlocks = 8;
-// Binary tiles: steps of at least 40 entries, groups of 16 row blocks,
-// units of up to 512 steps (the kernel reads a unit's step list 256 steps
-// at a time, so units are not bound by kMaxUnitSteps).  Config 3 (step ms,
-// 512-step units, G = 16, fp16 records): 6.33 / 6.22 / 6.22 / 6.28 / 6.28
-// at 24 / 32 / 40 / 48 / 64 entries; 6.71 at 32 with G = 8; 6.32 with
-// 384-step units at 48.  (With bf16 records only: 10.58 / 7.91 / 7.20 /
-// 6.78 / 6.76 at 8 / 16 / 32 / 48 / 64 entries.)
-constexpr std::uint32_t kDefaultMinStepNnz = 40;
+// Binary tiles: steps of at least 36 entries, groups of 16 row blocks,
+// units of up to 768 steps (the kernel reads a unit's step list 256 steps
+// at a time, so units are not bound by kMaxUnitSteps).  Config 3, step ms
+// with G = 16 (fp16 records, the tiles first): 5.87 / 5.86 / 5.79 / 5.81 /
+// 5.91 / 5.96 at 24 / 28 / 32 / 40 / 48 / 64 entries with 512-step units;
+// 5.87 / 5.78 / 5.73 / 5.72 / 5.78 at 24 / 28 / 32 / 36 / 40 with 768-step
+// units; 5.82 at 32 with 1024.  G = 8 took 6.58 at best (24 entries, one
+// 32-feature N tile a wave, 3 waves per SIMD).
+constexpr std::uint32_t kDefaultMinStepNnz = 36;
 constexpr std::uint32_t kDefaultBinaryGroupBlocks = 16;
-constexpr std::uint32_t kDefaultBinaryUnitSteps = 512;
+constexpr std::uint32_t kDefaultBinaryUnitSteps = 768;
 constexpr std::uint32_t kNoSlot = 0xFFFFFFFFu;
 constexpr unsigned kThreads = 256;
 constexpr std::uint32_t kXcds = 8;

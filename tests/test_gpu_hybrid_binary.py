@@ -43,7 +43,7 @@ pytestmark = pytest.mark.gpu
 
 REL = 1e-5
 NORTH_STAR = 1e-3
-DEFAULT_MIN_STEP, DEFAULT_G, DEFAULT_UNIT_STEPS = 40, 16, 512
+DEFAULT_MIN_STEP, DEFAULT_G, DEFAULT_UNIT_STEPS = 36, 16, 768
 
 
 def reference_binary_layout(dst, src, nr, nc, min_step, G, unit_steps, r=None, c=None):
