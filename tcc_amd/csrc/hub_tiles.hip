@@ -1016,10 +1016,10 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_split_kernel(TileArgs a) {
 // row scale when it is stored.
 //
 // Expansion: lane l's byte of tile t (8 bits: row l%32, column half l/32)
-// becomes 8 fp16 or bf16 of 0 or 1.0 through two 8-byte reads of a
-// 16-entry table in LDS, one per 4-bit half.  The next step's lookups run
-// between this step's products (2 G/2 reads; an 8-byte read of 64 lanes is
-// 4 LDS cycles against 32 MFMA cycles of a product).  Every tile of a step
+// becomes 8 fp16 or bf16 of 0 or 1.0 through one 16-byte read of a
+// 256-entry table in LDS (two 8-byte reads of a 16-entry table, one per
+// 4-bit half, took the tile kernel 2.03 ms against 1.87 at config 3).  The
+// next step's lookups run between this step's products (G/2 reads).  Every tile of a step
 // is multiplied: the builder stores every entry of a chosen step, and steps
 // are nearly full (config 3: 7.97 of 8 tiles a step).
 //
@@ -1044,16 +1044,16 @@ template <int G, int NT, int NS>
 __global__ void __launch_bounds__(kThreads) hub_tiles_binary_kernel(TileArgs a) {
     static_assert(G == 8 || G == 16, "binary tiles: G is 8 or 16");
     constexpr int T = G / 2;  // 32-row tiles a step
-    // lut[x] = 4 fp16 (0 or 1.0) of the 4 bits of x, low bit first, then
-    // lut[16 + x] the same in bf16
-    __shared__ vu2 lut[32];
+    // lut[x] = 8 fp16 (0 or 1.0) of the 8 bits of x, low bit first, then
+    // lut[256 + x] the same in bf16
+    __shared__ vu4 lut[512];
     // each wave's steps of the current stretch: fp16 steps from the front,
     // bf16 steps from the back, as (column block << 8 | step - c0)
     __shared__ std::uint32_t stepList[kThreads / kWave][kMaxUnitSteps];
-    if (threadIdx.x < 32) {
-        const unsigned x = threadIdx.x & 15u, one = threadIdx.x < 16 ? 0x3C00u : 0x3F80u;
+    for (unsigned e = threadIdx.x; e < 512; e += blockDim.x) {
+        const unsigned x = e & 255u, one = e < 256 ? 0x3C00u : 0x3F80u;
         auto pair = [one](unsigned y) { return ((y & 1u) ? one : 0u) | ((y & 2u) ? one << 16 : 0u); };
-        lut[threadIdx.x] = vu2{pair(x & 3u), pair(x >> 2)};
+        lut[e] = vu4{pair(x & 3u), pair((x >> 2) & 3u), pair((x >> 4) & 3u), pair(x >> 6)};
     }
     __syncthreads();
     const char* lutBytes = reinterpret_cast<const char*>(lut);
@@ -1089,7 +1089,7 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_binary_kernel(TileArgs a) 
     // place, 230 AGPRs and one wave per SIMD).
     auto run = [&](auto halfTag, const int (&ents)[kColRegs], std::uint32_t count, std::uint32_t c0) {
         constexpr bool HALF = decltype(halfTag)::value;
-        const char* lb = lutBytes + (HALF ? 0 : 128);
+        const char* lb = lutBytes + (HALF ? 0 : 4096);
         // Listed step i (i >= count: the zero step, multiplying zeros by
         // zeros; B read from a real step's column would turn an inf there
         // into NaN in every row).
@@ -1116,14 +1116,10 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_binary_kernel(TileArgs a) 
         auto expand = [&](const BinaryStage<G, NT>& o, vu4 (&A)[T]) {
 #pragma unroll
             for (int w = 0; w < G / 8; ++w) {
-                const std::uint32_t al = (o.m[w] << 3) & 0x78787878u, ah = (o.m[w] >> 1) & 0x78787878u;
 #pragma unroll
                 for (int q = 0; q < 4 && 4 * w + q < T; ++q) {
-                    const std::uint32_t il = q == 0 ? (al & 0xFFu) : __builtin_amdgcn_ubfe(al, 8 * q, 8);
-                    const std::uint32_t ih = q == 0 ? (ah & 0xFFu) : __builtin_amdgcn_ubfe(ah, 8 * q, 8);
-                    const vu2 x0 = *reinterpret_cast<const vu2*>(lb + il);
-                    const vu2 x1 = *reinterpret_cast<const vu2*>(lb + ih);
-                    A[4 * w + q] = vu4{x0.x, x0.y, x1.x, x1.y};
+                    const std::uint32_t b = q == 0 ? (o.m[w] & 0xFFu) : __builtin_amdgcn_ubfe(o.m[w], 8 * q, 8);
+                    A[4 * w + q] = *reinterpret_cast<const vu4*>(lb + (b << 4));
                 }
             }
         };
@@ -1164,7 +1160,7 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_binary_kernel(TileArgs a) 
                 __builtin_amdgcn_sched_barrier(0);
                 mma(A, ring[k]);
                 expand(ring[(k + 1) % NS], A);
-                // one MFMA, then lookups and VALU instructions of the next
+                // one MFMA, then a lookup and VALU instructions of the next
                 // step's expansion, and so on: the next step's lookups run
                 // between this step's products (issued in a block they left
                 // the lookups' latency on every step's path: config 3 hybrid
@@ -1174,8 +1170,8 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_binary_kernel(TileArgs a) 
 #pragma unroll
                 for (int j = 0; j < kMfma; ++j) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x100, HALF ? 2 : 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, HALF ? 4 : 2, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, HALF ? 2 : 1, 0);
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
