@@ -262,9 +262,13 @@ int tcc_block_release(void* allocation);
  *   rowScale[16(G g + j) + i]: the scale of row i of row block j of group g
  *     (rowOrder's order, 0 past num_rows); colScale[c]: the scale of column
  *     c (original order).
- * The products multiply TF32(colScale[c] * X[c]) (split into two exact
- * bf16 halves) by the pattern on v_mfma_f32_32x32x16_bf16, then scale each
- * row's fp32 sum by rowScale. */
+ * The products multiply 2^e TF32(colScale[c] * X[c]), with one power of two
+ * e per 32-feature slice chosen from the slice's largest magnitude, by the
+ * pattern: on v_mfma_f32_32x32x16_f16 for a (16-column block, slice) whose
+ * values are all fp16 values, and as two exact bf16 halves on
+ * v_mfma_f32_32x32x16_bf16 for any other; each row's fp32 sum is then
+ * scaled by 2^-e and rowScale.  Both forms are exact, so the sums are those
+ * of the TF32 values. */
 #define TCC_TILES_FP32 0u   /* tileVals in the fp32 MFMA's A-operand order (above) */
 #define TCC_TILES_BF16X2 1u /* each tile 256 bf16 hi then 256 bf16 lo, row-major: hi + lo = the TF32 value */
 #define TCC_TILES_BINARY 2u /* each tile its 256-bit pattern (tileMasks); values from rowScale and colScale */
@@ -357,16 +361,21 @@ int tcc_hybrid_from_bcsr(const tcc_bcsr* A, int useValues, uint32_t minStepNnz, 
 size_t tcc_hybrid_workspace_bytes(const tcc_hybrid* H, uint32_t featureDim);
 
 /* Bytes of device workspace tcc_hub_tiles_spmm needs for F features: the hub
- * columns' TF32 rows (hub_cols x roundup(F, 64) floats) and one 16G-row
- * partial sum per unit of a shared group (num_partial_units x 16G x
- * roundup(F, 64) floats). */
+ * columns' TF32 rows (roundup(hub_cols, 16) x roundup(F, 64) floats), one
+ * 16G-row partial sum per unit of a shared group (num_partial_units x 16G x
+ * roundup(F, 64) floats) and, for binary tiles, the half records' slice
+ * maxima, scales and flags (64 + 2 words per 32-feature slice and one byte
+ * per (16-column block, slice)). */
 size_t tcc_hub_tiles_workspace_bytes(const tcc_hub_tiles* T, uint32_t featureDim);
 
-/* Y (=, or += when accumulate != 0) A X for fp32 X [num_cols x F]: the
- * remainder's gather (which writes or adds every row of Y), then the tiles
- * added into Y.  Y holds 8*ceil(num_rows/8) rows of F floats (as for the
- * remainder's BCSR); workspace 16-byte aligned, at least
- * tcc_hybrid_workspace_bytes(H, F) bytes, not shared with a concurrent call. */
+/* Y (=, or += when accumulate != 0) A X for fp32 X [num_cols x F].  Value
+ * tiles, or accumulate: the remainder's gather (which writes or adds every
+ * row of Y), then the tiles added into Y.  Binary tiles without
+ * accumulate: the tiles first, storing their rows (and zeros in every row
+ * no tile group covers), then the remainder added into Y.  Y holds
+ * 8*ceil(num_rows/8) rows of F floats (as for the remainder's BCSR);
+ * workspace 16-byte aligned, at least tcc_hybrid_workspace_bytes(H, F)
+ * bytes, not shared with a concurrent call. */
 int tcc_hybrid_spmm(const tcc_hybrid* H, const float* X, float* Y, uint32_t featureDim, int accumulate,
                     void* workspace, size_t workspaceBytes, void* stream);
 
