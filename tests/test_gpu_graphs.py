@@ -3,7 +3,10 @@ the kernels the C-ABI enqueues on the current stream): the BCSR gather with
 its shared-window zero pass, the packed gather with its separate last chunk,
 the gathers over a phased BCSR (zero fill of Y, then atomics only),
 the one-launch first-layer forward (fill + mixed kernel), the SWTCF SpMM,
-the narrow and transposed gathers and the split-K dense products.  None of
+the narrow and transposed gathers, the split-K dense products and the
+hybrids (binary tiles with their slice maxima, half records and zero rows,
+stored first, then the remainder's atomics; value tiles after the
+remainder).  None of
 them allocates, synchronises or records a memset, so each captures as is.
 Each graph is replayed several times with eager work in between, new inputs
 written into the captured buffers before each replay, and every replay is
@@ -218,3 +221,39 @@ def test_graph_dense_products():
     # fixed-order split-K sums: replays equal the eager call bit for bit
     replay_and_check(g, out, [Am, Bm, AX, G], lambda: [swtcf.dense_tn(Am, Bm), *swtcf.gcn_relu_grad(AX, H, G, W2)],
                      exact=True, seed=8)
+
+
+def test_graph_hybrids():
+    """The binary hybrid at F = 300 (the remainder's pack with the slice
+    maxima, the slice scales, half records, the tiles stored first with the
+    rows they do not cover zeroed, then the 4-phase remainder's atomics) and
+    the split value-tile hybrid (the remainder first, then the tiles added),
+    each with its workspace allocated before capture."""
+    from tcc_amd import swtcf
+
+    nr, nc, F = 700, 900, 300
+    dst, src = random_coo(nr, nc, 30000, 21)
+    rng = np.random.default_rng(22)
+    rs = torch.from_numpy(rng.uniform(0.1, 1.0, nr).astype(np.float32)).cuda()
+    cs = torch.from_numpy(rng.uniform(0.1, 1.0, nc).astype(np.float32)).cuda()
+    vals = torch.from_numpy(rng.uniform(-1, 1, dst.size).astype(np.float32)).cuda()
+    Hb = swtcf.coo_to_hybrid_scaled(dev_u32(dst), dev_u32(src), nr, nc, rs, cs, min_step_nnz=190, group_blocks=16,
+                                    phases=4)
+    Hv = swtcf.coo_to_hybrid(dev_u32(dst), dev_u32(src), vals, nr, nc, min_tile_nnz=12, group_blocks=8,
+                             tile_format=swtcf.TILES_BF16X2, phases=4)
+    for H in (Hb, Hv):
+        assert H.view.tiles.num_steps > 0 and H.rest.view.num_TCBlocks > 0
+    X = torch.randn(nc, F, device="cuda")
+    wb = torch.empty(Hb.workspace_bytes(F) + 16, dtype=torch.uint8, device="cuda")
+    wv = torch.empty(Hv.workspace_bytes(F) + 16, dtype=torch.uint8, device="cuda")
+    Yb = torch.empty(Hb.out_rows, F, device="cuda")
+    Yv = torch.empty(Hv.out_rows, F, device="cuda")
+
+    def run():
+        swtcf.hybrid_spmm(Hb, X, Yb, workspace=wb)
+        swtcf.hybrid_spmm(Hv, X, Yv, workspace=wv)
+        return Yb, Yv
+
+    g, out = capture(run)
+    replay_and_check(g, out, [X], lambda: [swtcf.hybrid_spmm(Hb, X), swtcf.hybrid_spmm(Hv, X)], exact=False,
+                     seed=23)
