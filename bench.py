@@ -63,13 +63,14 @@ PHASES = 4
 # row sum scaled by r (tcc_coo_to_hybrid_scaled).  Measured at config 3
 # (step ms): phased gather alone 17.35; valued split tiles (each TF32 value
 # as two bf16, four bf16 products) 8.86 at 16 nnz a tile, groups of 8;
-# binary tiles with bf16 halves only 6.56 at 64 entries a step; with fp16
-# records, the tiles before the remainder, 5.72 at 36 entries and 768-step
-# units (the builder's defaults).  The valued hybrid is timed beside it
-# under `extra`.
+# binary tiles on dense MFMA with bf16 halves only 6.56 at 64 entries a
+# 16-column step; with fp16 records, the tiles before the remainder, 5.52
+# at 36 entries; on the 2:4 sparse MFMA over 32-column steps, 4.99 at 40
+# entries and 768-step units (the builder's defaults).  The valued hybrid
+# is timed beside it under `extra`.
 HUB_MIN_TILE_NNZ = 16
 HUB_GROUP_BLOCKS = 8
-BINARY_MIN_STEP_NNZ = 36
+BINARY_MIN_STEP_NNZ = 40
 BINARY_GROUP_BLOCKS = 16
 CPU_SAMPLE_NNZ = 16_000_000
 
@@ -678,15 +679,18 @@ def bench_spmm(args, torch, swtcf, cfg):
             torch.cuda.synchronize()
             extra["hybrid_build_ms"] = round((time.perf_counter() - t_h) * 1e3, 3)
             t = H.view.tiles
-            extra["hub"] = {"format": "binary 16x16 patterns, multiplied as 32-row tiles on "
-                                      "v_mfma_f32_32x32x16_f16 against fp16 2^e TF32(c X) where exact (else "
-                                      "_bf16 against its bf16 halves); rows scaled by 2^-e r",
+            extra["hub"] = {"format": "binary patterns of 32-row by 32-column tiles as 2:4 operands of "
+                                      "v_smfmac_f32_32x32x32_f16 against fp16 2^e TF32(c X) where exact (else "
+                                      "_bf16 against its bf16 halves), a second layer where a group of four "
+                                      "columns holds more than two entries; rows scaled by 2^-e r",
                             "min_step_nnz": BINARY_MIN_STEP_NNZ, "group_blocks": t.group_blocks,
-                            "steps": t.num_steps, "units": t.num_units, "partial_units": t.num_partial_units,
+                            "sub_steps": t.num_steps, "units": t.num_units, "partial_units": t.num_partial_units,
                             "hub_cols": t.hub_cols, "tile_nnz": t.nnz, "tile_nnz_frac": round(t.nnz / nnz, 4),
                             "rest_blocks": H.rest.view.num_TCBlocks,
-                            # one f16 MFMA a tile and feature slice (two bf16 for a bf16 record)
-                            "mfma_flops_per_step_fp16_records": 2.0 * 256 * t.group_blocks * t.num_steps * F,
+                            # one sparse f16 MFMA (32x32x32, 2:4) a tile and 32-feature slice (two
+                            # bf16 for a bf16 record): dense-equivalent flops, zeros included
+                            "smfmac_dense_equiv_flops_fp16_records": 1024.0 * t.group_blocks * t.num_steps
+                            * (-(-F // 32) * 32),
                             "values_as_scales_max_rel_diff": fact}
         Y = torch.empty((A.out_windows * 8, F), device="cuda")
         phased = f" over the {A.phases}-phase BCSR (Y zero-filled first)" if A.phases > 1 else ""
@@ -717,12 +721,13 @@ def bench_spmm(args, torch, swtcf, cfg):
                 swtcf.hybrid_spmm(H, X, Y, workspace=hws)
 
             G = H.view.tiles.group_blocks
-            kernel = (f"hub_tiles_binary_kernel<{G}, {1 if G == 16 else 2}, 4> (f16 MFMA 32x32x16 over "
-                      "2^e TF32(c X), bf16 halves where fp16 is not exact) + hub_reduce_kernel + "
+            kernel = (f"hub_tiles_binary_kernel<{G}, {1 if G == 16 else 2}, 4> (2:4 sparse f16 MFMA "
+                      "32x32x32 over 2^e TF32(c X), bf16 halves where fp16 is not exact) + hub_reduce_kernel + "
                       "hub_rows_half_kernel + hub_scale_kernel, after the remainder's tf32_pack_kernel "
                       f"(column-scaled, slice maxima) + gather_kernel<Packed> over the {H.rest.phases}-phase "
                       "BCSR (row-scaled sums; all timed)")
-            extra["path"] = (f"binary hybrid: steps of >= {BINARY_MIN_STEP_NNZ} entries as pattern tiles on MFMA "
+            extra["path"] = (f"binary hybrid: 32-column steps of >= {BINARY_MIN_STEP_NNZ} entries as pattern tiles "
+                             f"on the sparse MFMA "
                              f"over 2^e TF32(c X) (fp16 where exact, else bf16 halves) + packed gather of the "
                              f"remainder's pattern over its "
                              f"{H.rest.phases}-phase BCSR; A = diag(r) P diag(c) with the sym-norm scales")

@@ -252,26 +252,38 @@ int tcc_block_release(void* allocation);
  *     index order (the products do not depend on it).
  * Binary tiles (TCC_TILES_BINARY, tcc_coo_to_hybrid_scaled) hold the
  * pattern of A only, with A = diag(rowScale) P diag(colScale) (the scales
- * NULL for ones).  A step is chosen when its G tiles together hold at least
- * minStepNnz entries, and then every entry of the step is stored, 32 bytes
- * a 16x16 tile; the SpMM multiplies 32-row tiles (row blocks 2t and 2t+1):
- *   tileMasks, step p's G*32 bytes at byte 32*G*p: byte l*(G/2) + j/2, with
- *     l = 16*(j%2) + i + 32*h, holds in bit e the entry (row i, column
- *     8h + e) of row block j (the G/2 bytes lane l of the SpMM's wave reads:
- *     row 16*(j%2) + i of 32-row tile j/2, column half h);
+ * NULL for ones).  Their step is a group's G row blocks by a pair of
+ * 16-column blocks (32 column ranks, 32*stepCol[p] .. +31); a step is
+ * chosen when its tiles together hold at least minStepNnz entries, and then
+ * every entry of the step is stored, as operands of the 2:4 sparse MFMA
+ * (v_smfmac_f32_32x32x32_f16 / _bf16) over 32-row tiles (row blocks 2t and
+ * 2t+1).  Lane l of the SpMM's wave covers row l%32 of each tile and, with
+ * c = l/32, columns 8c..8c+7 of both 16-column blocks, as four groups of
+ * four columns (k = 0, 1: columns 8c + 4k..+3 of block 0; k = 2, 3:
+ * columns 8c + 4(k-2)..+3 of block 1); group k's entries take value slots
+ * 2k and 2k+1, two at most, so a step in which some group holds three or
+ * four entries takes two sub-steps of the same columns (layer 0: each
+ * group's lowest two entries, layer 1: the rest).  Sub-steps are what
+ * groupStepOffset, stepCol, units and num_steps count:
+ *   tileMasks, sub-step p's 96*G bytes at byte 96*G*p: at byte
+ *     l*(G/2) + t the value mask of lane l in tile t (bit j: slot j is 1,
+ *     else 0), and at byte 32*G + l*G + 2t the slots' positions in their
+ *     groups (2 bits a slot, slot j in bits 2j..2j+1, increasing within a
+ *     group; a slot without an entry has value 0 and an unused position);
  *   rowScale[16(G g + j) + i]: the scale of row i of row block j of group g
  *     (rowOrder's order, 0 past num_rows); colScale[c]: the scale of column
  *     c (original order).
  * The products multiply 2^e TF32(colScale[c] * X[c]), with one power of two
  * e per 32-feature slice chosen from the slice's largest magnitude, by the
- * pattern: on v_mfma_f32_32x32x16_f16 for a (16-column block, slice) whose
- * values are all fp16 values, and as two exact bf16 halves on
- * v_mfma_f32_32x32x16_bf16 for any other; each row's fp32 sum is then
- * scaled by 2^-e and rowScale.  Both forms are exact, so the sums are those
- * of the TF32 values. */
+ * pattern: on the f16 form for a (column-block pair, slice) whose values
+ * are all fp16 values, and as two exact bf16 halves on the bf16 form for
+ * any other; each row's fp32 sum is then scaled by 2^-e and rowScale.  Both
+ * forms are exact, so the sums are those of the TF32 values.  A zero value
+ * slot multiplies the column its position names: an Inf or NaN in a hub
+ * column's feature row can reach rows without an entry in that column. */
 #define TCC_TILES_FP32 0u   /* tileVals in the fp32 MFMA's A-operand order (above) */
 #define TCC_TILES_BF16X2 1u /* each tile 256 bf16 hi then 256 bf16 lo, row-major: hi + lo = the TF32 value */
-#define TCC_TILES_BINARY 2u /* each tile its 256-bit pattern (tileMasks); values from rowScale and colScale */
+#define TCC_TILES_BINARY 2u /* the pattern as sparse-MFMA operands (tileMasks); values from rowScale and colScale */
 
 typedef struct tcc_hub_tiles {
     uint32_t num_rows;
@@ -296,7 +308,7 @@ typedef struct tcc_hub_tiles {
     uint32_t num_shared_groups;
     const uint32_t* unitPartial;     /* [num_units] */
     const uint32_t* sharedGroups;    /* [3*num_shared_groups] */
-    const uint32_t* tileMasks;       /* BINARY: [8*G*(num_steps+1)] words, the last step zeros; else NULL */
+    const uint32_t* tileMasks;       /* BINARY: [24*G*(num_steps+1)] words, the last sub-step zeros; else NULL */
     const float* rowScale;           /* BINARY: [16*G*num_groups] or NULL (ones) */
     const float* colScale;           /* BINARY: [num_cols] or NULL (ones) */
 } tcc_hub_tiles;
@@ -329,7 +341,7 @@ int tcc_coo_to_hybrid(const uint32_t* dRow, const uint32_t* dCol, const float* d
  * of a device COO (row = destination, col = source, no duplicate pairs;
  * dRowScale [numRows] and dColScale [numCols] device arrays, either NULL
  * for ones), with binary tiles (TCC_TILES_BINARY): steps of at least
- * minStepNnz entries (0 = 36), groupBlocks 8 or 16 (0 = 16), unitSteps
+ * minStepNnz entries (0 = 40), groupBlocks 8 or 16 (0 = 16), unitSteps
  * 0 = 768 (any number: the SpMM reads a unit's step list 256 steps at a
  * time), phases as tcc_coo_to_hybrid.  The remainder holds the pattern
  * (data NULL); its gather reads the column-scaled packed rows and scales
@@ -346,7 +358,7 @@ int tcc_hybrid_release(tcc_hybrid* H);
  * same graph many times, such as full-graph training).  With useValues = 0
  * the entries count as 1.0, as the reference's kernels read them
  * (spmm_kernel.cu:96-102): binary tiles (tcc_coo_to_hybrid_scaled without
- * scales, minStepNnz 0 = 36); else the values of `data` (value of bit i of
+ * scales, minStepNnz 0 = 40); else the values of `data` (value of bit i of
  * block b = data[tcOffset[b] + rank]) in split-TF32 tiles (tcc_coo_to_hybrid,
  * TCC_TILES_BF16X2, minTileNnz 16, groups of 8).  Bits in padding columns
  * (>= num_cols) or rows (>= num_rows) are ignored, as the gather ignores

@@ -66,15 +66,14 @@ constexpr std::uint32_t kMaxUnitSteps = 256;        // a unit's step columns sit
 constexpr int kColRegs = kMaxUnitSteps / 64;
 constexpr std::uint32_t kDefaultMinTileNnz = 16;
 constexpr std::uint32_t kDefaultGroupBlocks = 8;
-// Binary tiles: steps of at least 36 entries, groups of 16 row blocks,
-// units of up to 768 steps (the kernel reads a unit's step list 256 steps
-// at a time, so units are not bound by kMaxUnitSteps).  Config 3, step ms
-// with G = 16 (fp16 records, the tiles first): 5.87 / 5.86 / 5.79 / 5.81 /
-// 5.91 / 5.96 at 24 / 28 / 32 / 40 / 48 / 64 entries with 512-step units;
-// 5.87 / 5.78 / 5.73 / 5.72 / 5.78 at 24 / 28 / 32 / 36 / 40 with 768-step
-// units; 5.82 at 32 with 1024.  G = 8 took 6.58 at best (24 entries, one
-// 32-feature N tile a wave, 3 waves per SIMD).
-constexpr std::uint32_t kDefaultMinStepNnz = 36;
+// Binary tiles: steps (16 row blocks by a pair of 16-column blocks) of at
+// least 40 entries, groups of 16 row blocks, units of up to 768 sub-steps
+// (the kernel reads a unit's step list 256 steps at a time, so units are
+// not bound by kMaxUnitSteps).  Config 3, step ms with G = 16 on the
+// sparse MFMA: 5.33 / 5.14 / 5.01 / 5.04 / 4.99 / 5.03 / 5.06 at 24 / 28 /
+// 32 / 36 / 40 / 48 / 64 entries with 768-step units; 5.00 at 40 with 512,
+// 5.10 with 1024.
+constexpr std::uint32_t kDefaultMinStepNnz = 40;
 constexpr std::uint32_t kDefaultBinaryGroupBlocks = 16;
 constexpr std::uint32_t kDefaultBinaryUnitSteps = 768;
 constexpr std::uint32_t kNoSlot = 0xFFFFFFFFu;
@@ -156,13 +155,13 @@ __device__ __forceinline__ std::uint64_t tile_index(const std::uint64_t* keys, c
     return keys[tileStart[t]] >> 8;
 }
 
-// dense[t] = tile t holds at least minNnz entries and its step (its group's
-// G tiles of the same column block, adjacent in the sorted order) at least
-// minStepNnz; the number of dense tiles; the largest column block of a
-// dense tile (+1).
+// dense[t] = tile t holds at least minNnz entries and its step (the
+// stepTiles tiles of one group and step column, adjacent in the sorted
+// order) at least minStepNnz; the number of dense tiles; the largest step
+// column of a dense tile (+1).
 __global__ void dense_tiles_kernel(const std::uint64_t* __restrict__ keys, const std::uint32_t* __restrict__ tileStart,
                                    const std::uint32_t* __restrict__ numTiles, std::uint32_t E, std::uint32_t minNnz,
-                                   std::uint32_t minStepNnz, std::uint32_t colBlocks, std::uint32_t G,
+                                   std::uint32_t minStepNnz, std::uint32_t colSteps, std::uint32_t stepTiles,
                                    std::uint32_t* __restrict__ dense, std::uint32_t* __restrict__ denseCount,
                                    std::uint32_t* __restrict__ hubBlocks) {
     const std::uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
@@ -173,15 +172,15 @@ __global__ void dense_tiles_kernel(const std::uint64_t* __restrict__ keys, const
         const std::uint32_t e = t + 1 < nt ? tileStart[t + 1] : E;
         d = e - s >= minNnz;
         if (d && minStepNnz > e - s) {
-            // the step's entries: its tiles before and after t (at most G - 1 each way)
-            const std::uint64_t step = (keys[s] >> 8) / G;
+            // the step's entries: its tiles before and after t (at most stepTiles - 1 each way)
+            const std::uint64_t step = (keys[s] >> 8) / stepTiles;
             std::uint32_t first = t, end = t + 1;
-            while (first > 0 && (keys[tileStart[first - 1]] >> 8) / G == step) --first;
-            while (end < nt && (keys[tileStart[end]] >> 8) / G == step) ++end;
+            while (first > 0 && (keys[tileStart[first - 1]] >> 8) / stepTiles == step) --first;
+            while (end < nt && (keys[tileStart[end]] >> 8) / stepTiles == step) ++end;
             d = (end < nt ? tileStart[end] : E) - tileStart[first] >= minStepNnz;
         }
         dense[t] = d ? 1u : 0u;
-        if (d) atomicMax(hubBlocks, static_cast<std::uint32_t>((keys[s] >> 8) / G % colBlocks) + 1u);
+        if (d) atomicMax(hubBlocks, static_cast<std::uint32_t>((keys[s] >> 8) / stepTiles % colSteps) + 1u);
     }
     const std::uint64_t m = __ballot(d);
     if (m && __lane_id() == static_cast<unsigned>(__builtin_ctzll(m)))
@@ -189,43 +188,44 @@ __global__ void dense_tiles_kernel(const std::uint64_t* __restrict__ keys, const
 }
 
 // stepHead[t] = tile t is dense and no earlier dense tile shares its step
-// (the tiles of a step are adjacent, at most G of them); per group, its
-// number of steps.
+// (the tiles of a step are adjacent, at most stepTiles of them); per group,
+// its number of steps.
 __global__ void step_heads_kernel(const std::uint64_t* __restrict__ keys, const std::uint32_t* __restrict__ tileStart,
                                   const std::uint32_t* __restrict__ numTiles, const std::uint32_t* __restrict__ dense,
-                                  std::uint32_t G, std::uint32_t colBlocks, std::uint32_t* __restrict__ stepHead,
+                                  std::uint32_t stepTiles, std::uint32_t colSteps, std::uint32_t* __restrict__ stepHead,
                                   std::uint32_t* __restrict__ groupSteps) {
     const std::uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= *numTiles) return;
     std::uint32_t head = 0;
     if (dense[t]) {
-        const std::uint64_t step = tile_index(keys, tileStart, t) / G;
+        const std::uint64_t step = tile_index(keys, tileStart, t) / stepTiles;
         head = 1;
         for (std::uint32_t b = t; b > 0; --b) {
-            if (tile_index(keys, tileStart, b - 1) / G != step) break;
+            if (tile_index(keys, tileStart, b - 1) / stepTiles != step) break;
             if (dense[b - 1]) {
                 head = 0;
                 break;
             }
         }
-        if (head) atomicAdd(&groupSteps[step / colBlocks], 1u);
+        if (head) atomicAdd(&groupSteps[step / colSteps], 1u);
     }
     stepHead[t] = head;
 }
 
-// Per dense tile: its slot (step * G + row block % G) and, for step heads,
-// the step's column block.
+// Per dense tile: its slot (step * stepTiles + tile % stepTiles) and, for
+// step heads, the step's column (a 16-column block, or a pair of them for
+// binary tiles).
 __global__ void tile_slots_kernel(const std::uint64_t* __restrict__ keys, const std::uint32_t* __restrict__ tileStart,
                                   const std::uint32_t* __restrict__ numTiles, const std::uint32_t* __restrict__ dense,
                                   const std::uint32_t* __restrict__ stepHead, const std::uint32_t* __restrict__ stepPos,
-                                  std::uint32_t G, std::uint32_t colBlocks, std::uint32_t* __restrict__ slot,
+                                  std::uint32_t stepTiles, std::uint32_t colSteps, std::uint32_t* __restrict__ slot,
                                   std::uint32_t* __restrict__ stepCol) {
     const std::uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= *numTiles || !dense[t]) return;
     const std::uint64_t tile = tile_index(keys, tileStart, t);
     const std::uint32_t step = stepPos[t] + stepHead[t] - 1;  // heads up to and including t, minus one
-    slot[t] = step * G + static_cast<std::uint32_t>(tile % G);
-    if (stepHead[t]) stepCol[step] = static_cast<std::uint32_t>(tile / G % colBlocks);
+    slot[t] = step * stepTiles + static_cast<std::uint32_t>(tile % stepTiles);
+    if (stepHead[t]) stepCol[step] = static_cast<std::uint32_t>(tile / stepTiles % colSteps);
 }
 
 // Per edge: 1 if it stays in the sparse remainder.
@@ -261,10 +261,11 @@ __global__ void place_entries_kernel(const std::uint64_t* __restrict__ keys, con
     if (dense[t]) {
         const std::uint32_t i = static_cast<std::uint32_t>(keys[e] >> 4) & 15u, j = static_cast<std::uint32_t>(keys[e]) & 15u;
         if (format == TCC_TILES_BINARY) {
-            // step s's G*32 bytes: byte l*(G/2) + rb/2, l = 16*(rb%2) + i + 32*(j/8), bit j%8
-            const std::uint32_t step = slot[t] / G, rb = slot[t] % G;
-            const std::uint64_t byte = static_cast<std::uint64_t>(step) * G * 32 +
-                                       (16 * (rb % 2) + i + 32 * (j / 8)) * (G / 2) + rb / 2;
+            // the step's raw bits (binary_encode_kernel's input): 32 G bytes
+            // per 16-column half h of the step, byte l*(G/2) + rb/2 with
+            // l = 16*(rb%2) + i + 32*(j/8), bit j%8
+            const std::uint32_t step = slot[t] / (2 * G), q = slot[t] % (2 * G), h = q / G, rb = q % G;
+            const std::uint64_t byte = (2ull * step + h) * G * 32 + (16 * (rb % 2) + i + 32 * (j / 8)) * (G / 2) + rb / 2;
             atomicOr(&tileMasks[byte / 4], 1u << (8 * (byte % 4) + j % 8));
         } else if (format == TCC_TILES_BF16X2) {
             // bf16 tile: hi[i][j] at 2(16i + j) bytes, lo 512 bytes further
@@ -282,6 +283,125 @@ __global__ void place_entries_kernel(const std::uint64_t* __restrict__ keys, con
         restRow[p] = row[src];
         restCol[p] = col[src];
         if (restVal) restVal[p] = v;
+    }
+}
+
+// ---- binary tiles: the pattern as operands of the 2:4 sparse MFMA
+//
+// v_smfmac_f32_32x32x32_f16 multiplies a 32x32 A held as two values of each
+// group of four consecutive columns (8 values a lane and 2-bit positions)
+// by a dense 32x32 B.  A binary step covers 32 columns (two 16-column
+// blocks, h = 0 and 1) of G/2 32-row tiles; lane l of the wave supplies
+// row l%32 of each tile and, with c = l/32, columns 8c..8c+7 of both
+// halves: value slots 2k and 2k+1 of the lane hold the entries of its
+// nibble k (k = 0, 1: columns 8c + 4k..+3 of half 0; k = 2, 3: columns
+// 8c + 4(k-2)..+3 of half 1), and B's lane l holds the 16 columns of half
+// c for feature l%32.  A nibble with more than two entries does not fit:
+// such a step takes a second layer, the same columns with each nibble's
+// entries past its lowest two.
+
+// Lane bytes of a step's raw half h (G/2 bytes: one per 32-row tile).
+__device__ __forceinline__ std::uint64_t raw_lane_bytes(const std::uint32_t* raw, std::uint32_t G, std::uint64_t step,
+                                                        std::uint32_t h, unsigned lane) {
+    const std::uint32_t* p = raw + ((2 * step + h) * G * 32 + lane * (G / 2)) / 4;
+    if (G != 16) return *p;
+    const vu2 v = load_global<vu2>(p);
+    return v.x | static_cast<std::uint64_t>(v.y) << 32;
+}
+
+// Nibbles of x holding more than two set bits.
+__device__ __forceinline__ bool crowded_nibble(std::uint64_t x) {
+    std::uint64_t c = x - ((x >> 1) & 0x5555555555555555ull);
+    c = (c & 0x3333333333333333ull) + ((c >> 2) & 0x3333333333333333ull);  // per-nibble counts, 0..4
+    return ((c + 0x1111111111111111ull) & 0xCCCCCCCCCCCCCCCCull) != 0;      // count + 1 >= 4
+}
+
+// layers[s] = 2 when a nibble of step s holds more than two entries, else 1
+// (one wave per step).
+__global__ void binary_layers_kernel(const std::uint32_t* __restrict__ raw, std::uint32_t NS, std::uint32_t G,
+                                     std::uint32_t* __restrict__ layers) {
+    const std::uint64_t s = (static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
+    if (s >= NS) return;
+    const unsigned lane = __lane_id();
+    const bool crowded = crowded_nibble(raw_lane_bytes(raw, G, s, 0, lane)) || crowded_nibble(raw_lane_bytes(raw, G, s, 1, lane));
+    const std::uint64_t any = __ballot(crowded);
+    if (lane == 0) layers[s] = any ? 2u : 1u;
+}
+
+// subOffset[g] = first sub-step of group g (g <= NG); groupSub[g] = its
+// sub-steps (steps and second layers).
+__global__ void sub_offsets_kernel(const std::uint32_t* __restrict__ stepOffset, const std::uint32_t* __restrict__ subPos,
+                                   std::uint32_t NG, std::uint32_t* __restrict__ subOffset,
+                                   std::uint32_t* __restrict__ groupSub) {
+    const std::uint32_t g = blockIdx.x * blockDim.x + threadIdx.x;
+    if (g > NG) return;
+    subOffset[g] = subPos[stepOffset[g]];
+    if (g < NG) groupSub[g] = subPos[stepOffset[g + 1]] - subPos[stepOffset[g]];
+}
+
+// Two value slots of one nibble's entries in a layer (layer 0: the lowest
+// two set bits, layer 1: the rest): value bits (slot 0 in bit 0) and the
+// slots' positions (2 bits each, slot 0 low).  Positions increase; a slot
+// without an entry holds 0 and points at an unused position.
+__device__ __forceinline__ void encode_nibble(unsigned nib, int layer, unsigned& vals, unsigned& pos) {
+    const unsigned l1 = nib & (0u - nib), r1 = nib & ~l1, l2 = r1 & (0u - r1);
+    const unsigned sel = layer ? nib & ~(l1 | l2) : (l1 | l2);
+    const int n = __builtin_popcount(sel);
+    if (n == 2) {
+        const unsigned p0 = static_cast<unsigned>(__builtin_ctz(sel)), p1 = static_cast<unsigned>(__builtin_ctz(sel & (sel - 1)));
+        vals = 3u;
+        pos = p0 | p1 << 2;
+    } else if (n == 1) {
+        const unsigned p = static_cast<unsigned>(__builtin_ctz(sel));
+        vals = p < 3 ? 1u : 2u;
+        pos = p < 3 ? (p | 3u << 2) : (2u | 3u << 2);
+    } else {
+        vals = 0u;
+        pos = 0u | 1u << 2;
+    }
+}
+
+// Sub-step records (one wave per step): the step's layers at sub-steps
+// subPos[s].., each 96 G bytes: lane l's G/2 value-mask bytes at l*(G/2)
+// (byte t: tile t, bit j: value slot j is 1.0), then at 32 G + l*G the
+// 16-bit positions of tile t at byte 2t (slot j in bits 2j..2j+1).
+__global__ void binary_encode_kernel(const std::uint32_t* __restrict__ raw, std::uint32_t NS, std::uint32_t G,
+                                     const std::uint32_t* __restrict__ subPos, const std::uint32_t* __restrict__ stepColIn,
+                                     std::uint32_t* __restrict__ out, std::uint32_t* __restrict__ stepCol) {
+    const std::uint64_t s = (static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
+    if (s >= NS) return;
+    const unsigned lane = __lane_id();
+    const std::uint64_t w0 = raw_lane_bytes(raw, G, s, 0, lane), w1 = raw_lane_bytes(raw, G, s, 1, lane);
+    const std::uint32_t sub0 = subPos[s], layers = subPos[s + 1] - sub0;
+    const std::uint32_t T = G / 2;
+    for (std::uint32_t L = 0; L < layers; ++L) {
+        std::uint64_t masks = 0;
+        std::uint32_t idx[8] = {};
+        for (std::uint32_t t = 0; t < T; ++t) {
+            const unsigned b0 = static_cast<unsigned>(w0 >> (8 * t)) & 0xFFu, b1 = static_cast<unsigned>(w1 >> (8 * t)) & 0xFFu;
+            const unsigned nib[4] = {b0 & 15u, b0 >> 4, b1 & 15u, b1 >> 4};
+            unsigned m = 0, p = 0;
+            for (int k = 0; k < 4; ++k) {
+                unsigned v, q;
+                encode_nibble(nib[k], static_cast<int>(L), v, q);
+                m |= v << (2 * k);
+                p |= q << (4 * k);
+            }
+            masks |= static_cast<std::uint64_t>(m) << (8 * t);
+            idx[t] = p;
+        }
+        std::uint32_t* rec = out + (static_cast<std::uint64_t>(sub0) + L) * 24 * G;
+        std::uint32_t* mp = rec + lane * (G / 8);
+        std::uint32_t* ip = rec + 8 * G + lane * (G / 4);
+        if (G == 16) {
+            *reinterpret_cast<vu2*>(mp) = vu2{static_cast<std::uint32_t>(masks), static_cast<std::uint32_t>(masks >> 32)};
+            *reinterpret_cast<vu4*>(ip) = vu4{idx[0] | idx[1] << 16, idx[2] | idx[3] << 16, idx[4] | idx[5] << 16,
+                                              idx[6] | idx[7] << 16};
+        } else {
+            *mp = static_cast<std::uint32_t>(masks);
+            *reinterpret_cast<vu2*>(ip) = vu2{idx[0] | idx[1] << 16, idx[2] | idx[3] << 16};
+        }
+        if (lane == 0) stepCol[sub0 + L] = stepColIn[s];
     }
 }
 
@@ -480,6 +600,7 @@ struct TileArgs {
     // hybrid's remainder adds into Y after; hub_zero_rows_kernel zeroes the
     // rows no unit writes).
     int storeY;
+    std::uint32_t zeroCol;  // binary tiles: the column-block pair of zeros in Xs (the zero step's)
 };
 
 // This wave's unit and 64-feature slice (unit >= numUnits: no work).  The
@@ -810,69 +931,74 @@ __global__ void __launch_bounds__(kThreads) hub_scale_kernel(const std::uint32_t
 }
 
 // As hub_rows_split_kernel over 2^e-scaled values, with half records where
-// exact (above).  Thread (column block, feature f), W = 32 or 64 features a
-// slice: the lanes of one slice agree through a ballot.
-__global__ void hub_rows_half_kernel(const float* __restrict__ X, std::uint32_t F,
+// exact (above).  Thread (pair of column blocks, feature f), W = 32 or 64
+// features a slice: the lanes of one slice agree through a ballot, so that
+// both column blocks of a binary step hold one form.
+__global__ void __launch_bounds__(kThreads) hub_rows_half_kernel(const float* __restrict__ X, std::uint32_t F,
                                      const std::uint32_t* __restrict__ order, std::uint32_t hubCols,
                                      std::uint32_t hubRows, std::uint32_t ldh, const float* __restrict__ colScale,
                                      const float* __restrict__ up, std::uint32_t W, std::uint16_t* __restrict__ Xs,
                                      unsigned char* __restrict__ flags) {
+    constexpr std::uint32_t kC = 2 * kTile;
     const std::uint64_t i = static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    const std::uint32_t cb = static_cast<std::uint32_t>(i / ldh), f = static_cast<std::uint32_t>(i % ldh);
-    if (cb >= hubRows / kTile) return;  // whole waves: ldh is a multiple of 64
-    std::uint32_t src[16];
+    const std::uint32_t pr = static_cast<std::uint32_t>(i / ldh), f = static_cast<std::uint32_t>(i % ldh);
+    if (pr >= hubRows / kC) return;  // whole waves: ldh is a multiple of 64
+    std::uint32_t src[kC];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) src[k] = order[min(cb * kTile + k, hubCols > 0 ? hubCols - 1 : 0u)];
+    for (std::uint32_t k = 0; k < kC; ++k) src[k] = order[min(pr * kC + k, hubCols > 0 ? hubCols - 1 : 0u)];
     const std::uint32_t fc = min(f, F > 0 ? F - 1 : 0u);
-    float x[16];
+    float t[kC];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) x[k] = X[static_cast<std::uint64_t>(src[k]) * F + fc];
+    for (std::uint32_t k = 0; k < kC; ++k) t[k] = X[static_cast<std::uint64_t>(src[k]) * F + fc];
     if (colScale) {
 #pragma unroll
-        for (int k = 0; k < 16; ++k) x[k] *= colScale[src[k]];
+        for (std::uint32_t k = 0; k < kC; ++k) t[k] *= colScale[src[k]];
     }
     const float sc = up[f / W];
-    float t[16];
     bool exact = true;
-    std::uint16_t h[16];
+    std::uint32_t h[kC / 2];  // fp16 pairs
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-        const bool live = f < F && cb * kTile + k < hubCols;
-        t[k] = live ? tf32_rna(x[k]) * sc : 0.0f;
+    for (std::uint32_t k = 0; k < kC; ++k) {
+        const bool live = f < F && pr * kC + k < hubCols;
+        t[k] = live ? tf32_rna(t[k]) * sc : 0.0f;
         const _Float16 hk = static_cast<_Float16>(t[k]);
-        h[k] = __builtin_bit_cast(std::uint16_t, hk);
+        const std::uint32_t hb = __builtin_bit_cast(std::uint16_t, hk);
+        h[k / 2] = k % 2 ? h[k / 2] | hb << 16 : hb;
         exact &= __builtin_isnan(t[k]) || __float_as_uint(static_cast<float>(hk)) == __float_as_uint(t[k]);
     }
     // the slice's lanes: all 64 (W = 64) or this lane's half-wave (W = 32)
     const std::uint64_t bad = __ballot(!exact);
     const unsigned lane = __lane_id();
     const bool half = W >= kWave ? bad == 0 : ((bad >> (lane & 32u)) & 0xFFFFFFFFull) == 0;
-    vu4* out = reinterpret_cast<vu4*>(Xs + (static_cast<std::uint64_t>(cb) * ldh + f) * 32);
-    if (half) {
-        // dense: feature j of the slice at 32 j bytes of the slice's region
-        vu4* hout = reinterpret_cast<vu4*>(Xs + (static_cast<std::uint64_t>(cb) * ldh + f / W * W) * 32 + (f % W) * 16);
-        vu4 hv[2];
+    // a pair past the hub columns (the zero step's) is zero in both forms:
+    // the bf16 layout's 64 bytes per feature cover the fp16 one
+    const bool zeroPair = pr * kC >= hubCols;
 #pragma unroll
-        for (int k = 0; k < 16; k += 2)
-            hv[k / 8][(k % 8) / 2] = static_cast<std::uint32_t>(h[k]) | static_cast<std::uint32_t>(h[k + 1]) << 16;
-        hout[0] = hv[0];
-        hout[1] = hv[1];
-    } else {
-        vu4 hi[2], lo[2];
+    for (std::uint32_t q = 0; q < 2; ++q) {
+        const std::uint64_t cb = 2ull * pr + q;
+        if (half && !zeroPair) {
+            // dense: feature j of the slice at 32 j bytes of the slice's region
+            vu4* hout = reinterpret_cast<vu4*>(Xs + (cb * ldh + f / W * W) * 32 + (f % W) * 16);
+            hout[0] = vu4{h[8 * q], h[8 * q + 1], h[8 * q + 2], h[8 * q + 3]};
+            hout[1] = vu4{h[8 * q + 4], h[8 * q + 5], h[8 * q + 6], h[8 * q + 7]};
+        } else {
+            vu4 hi[2], lo[2];
 #pragma unroll
-        for (int k = 0; k < 16; k += 2) {
-            std::uint16_t h0, l0, h1, l1;
-            bf16_split(t[k], h0, l0);
-            bf16_split(t[k + 1], h1, l1);
-            hi[k / 8][(k % 8) / 2] = static_cast<std::uint32_t>(h0) | static_cast<std::uint32_t>(h1) << 16;
-            lo[k / 8][(k % 8) / 2] = static_cast<std::uint32_t>(l0) | static_cast<std::uint32_t>(l1) << 16;
+            for (std::uint32_t k = 0; k < kTile; k += 2) {
+                std::uint16_t h0, l0, h1, l1;
+                bf16_split(t[kTile * q + k], h0, l0);
+                bf16_split(t[kTile * q + k + 1], h1, l1);
+                hi[k / 8][(k % 8) / 2] = static_cast<std::uint32_t>(h0) | static_cast<std::uint32_t>(h1) << 16;
+                lo[k / 8][(k % 8) / 2] = static_cast<std::uint32_t>(l0) | static_cast<std::uint32_t>(l1) << 16;
+            }
+            vu4* out = reinterpret_cast<vu4*>(Xs + (cb * ldh + f) * 32);
+            out[0] = hi[0];
+            out[1] = hi[1];
+            out[2] = lo[0];
+            out[3] = lo[1];
         }
-        out[0] = hi[0];
-        out[1] = hi[1];
-        out[2] = lo[0];
-        out[3] = lo[1];
     }
-    if (f % W == 0) flags[static_cast<std::uint64_t>(cb) * (ldh / W) + f / W] = half ? 1 : 0;
+    if (f % W == 0) flags[static_cast<std::uint64_t>(pr) * (ldh / W) + f / W] = half ? 1 : 0;
 }
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -1003,42 +1129,65 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_split_kernel(TileArgs a) {
 
 // Binary tiles (TCC_TILES_BINARY).  The reference's tensor-core operand is
 // the block's bitmap as {0, 1} (src/swtcf_spmm.cu:193-200); here the
-// patterns of 32-row tiles (row blocks 2t and 2t+1 of a group) are the A
-// operand of v_mfma_f32_32x32x16_f16 or _bf16 (lane l: row l%32, columns
-// 8(l/32)..+7 of the tile's 16; B lane l: column 8(l/32) + e, feature l%32;
-// D lane l register r: row 8(r/4) + 4(l/32) + r%4, feature l%32; checked on
-// the GPU), and the values come as row and column scales.  Xs holds
-// 2^e TF32(colScale[c] * X[c]) (e per slice, hub_rows_half_kernel): as fp16
-// values where that is exact for the (column block, slice), one f16 MFMA a
-// tile, else as bf16 halves, one MFMA against the high parts and one
-// against the low parts.  Either way sum_c P[i][c] 2^e TF32(c x) is formed
-// from exact products in fp32; the sum is multiplied by 2^-e, and by the
-// row scale when it is stored.
+// patterns of 32-row tiles (row blocks 2t and 2t+1 of a group) by 32
+// columns (a pair of 16-column blocks) are the sparse A operand of
+// v_smfmac_f32_32x32x32_f16 or _bf16: two value slots per group of four
+// columns, with their positions (binary_encode_kernel; a step whose groups
+// hold more entries has a second layer).  Lane l supplies row l%32 of the
+// tile, slots 0-3 for columns 8(l/32)..+7 of column block 0 and slots 4-7
+// for the same columns of block 1; B lane l holds the 16 columns of block
+// l/32 for feature l%32; D lane l register r is row 8(r/4) + 4(l/32) + r%4,
+// feature l%32 (all checked on the GPU).  The values come as row and column
+// scales.  Xs holds 2^e TF32(colScale[c] * X[c]) (e per slice,
+// hub_rows_half_kernel): as fp16 values where that is exact for the
+// (column-block pair, slice), one f16 product a tile, else as bf16 halves,
+// one product against the high parts and one against the low parts.
+// Either way sum_c P[i][c] 2^e TF32(c x) is formed from exact products in
+// fp32; the sum is multiplied by 2^-e, and by the row scale when it is
+// stored.
 //
-// Expansion: lane l's byte of tile t (8 bits: row l%32, column half l/32)
-// becomes 8 fp16 or bf16 of 0 or 1.0 through one 16-byte read of a
-// 256-entry table in LDS (two 8-byte reads of a 16-entry table, one per
-// 4-bit half, took the tile kernel 2.03 ms against 1.87 at config 3).  The
-// next step's lookups run between this step's products (G/2 reads).  Every tile of a step
-// is multiplied: the builder stores every entry of a chosen step, and steps
-// are nearly full (config 3: 7.97 of 8 tiles a step).
+// Expansion: lane l's value-mask byte of tile t (slot j is 1.0 where bit j
+// is set) becomes 8 fp16 or bf16 of 0 or 1.0 through one 16-byte read of a
+// 256-entry table in LDS; the positions go to the MFMA as they are stored
+// (tiles 2u and 2u+1 in the halves of one register).  The next step's
+// lookups run between this step's products (G/2 reads).  Every tile of a
+// step is multiplied.
 //
 // One wave per (unit, slice of 32 NT features).  A unit's steps are taken
 // 256 at a time (step columns one per lane in four registers), listed by
-// record kind, and multiplied in two passes: the fp16 steps (the G/2
-// pattern bytes of its lane, one 8- or 4-byte load, and NT 16-byte Xs
-// loads, then G NT / 2 MFMAs) and then the bf16 steps (2 NT Xs loads, G NT
-// MFMAs).  Loads run NS - 1 steps ahead in a ring of NS stages, as in the
-// valued kernels.
+// record kind, and multiplied in two passes: the fp16 steps (the lane's
+// G/2 mask bytes and G bytes of positions, and 2 NT 16-byte Xs loads, then
+// G NT / 2 MFMAs) and then the bf16 steps (4 NT Xs loads, G NT MFMAs).
+// Loads run NS - 1 steps ahead in a ring of NS stages (2 for the bf16
+// steps, whose stages are twice the registers), as in the valued kernels.
 template <int G, int NT>
 struct BinaryStage {
-    std::uint32_t m[G / 8];  // this lane's G/2 pattern bytes (byte t: 32-row tile t)
-    vu4 h[NT];               // N tile u: xh (or the fp16 x) of columns 8(l/32)..+7, feature f0 + 32u + l%32
-    vu4 lo[NT];              // the same columns' xl (bf16 records)
+    std::uint32_t m[G / 8];   // this lane's G/2 value-mask bytes (byte t: 32-row tile t)
+    std::uint32_t ix[G / 4];  // positions: tile t in bits 16(t%2).. of word t/2
+    vu4 h[NT][2];             // N tile u: 16 fp16 x (or bf16 xh) of column block l/32, feature f0 + 32u + l%32
+    vu4 lo[NT][2];            // the same columns' xl (bf16 records)
 };
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x16 __attribute__((ext_vector_type(16)));
+typedef std::uint32_t vu8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ vu8 join8(const vu4& a, const vu4& b) {
+    return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// acc += A B on the sparse MFMA; HI selects the upper 16 position bits of ix.
+template <bool HALF, int HI>
+__device__ __forceinline__ f32x16 smfmac(const vu4& A, const vu8& B, const f32x16& acc, std::uint32_t ix) {
+    if constexpr (HALF)
+        return __builtin_amdgcn_smfmac_f32_32x32x32_f16(__builtin_bit_cast(f16x8, A), __builtin_bit_cast(f16x16, B), acc,
+                                                        static_cast<int>(ix), 0, HI);
+    else
+        return __builtin_amdgcn_smfmac_f32_32x32x32_bf16(__builtin_bit_cast(bf16x8, A), __builtin_bit_cast(bf16x16, B),
+                                                         acc, static_cast<int>(ix), 0, HI);
+}
 
 template <int G, int NT, int NS>
 __global__ void __launch_bounds__(kThreads) hub_tiles_binary_kernel(TileArgs a) {
@@ -1048,7 +1197,7 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_binary_kernel(TileArgs a) 
     // lut[256 + x] the same in bf16
     __shared__ vu4 lut[512];
     // each wave's steps of the current stretch: fp16 steps from the front,
-    // bf16 steps from the back, as (column block << 8 | step - c0)
+    // bf16 steps from the back, as (column-block pair << 8 | step - c0)
     __shared__ std::uint32_t stepList[kThreads / kWave][kMaxUnitSteps];
     for (unsigned e = threadIdx.x; e < 512; e += blockDim.x) {
         const unsigned x = e & 255u, one = e < 256 ? 0x3C00u : 0x3F80u;
@@ -1068,11 +1217,13 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_binary_kernel(TileArgs a) 
     const unsigned lj = lane & 31u, lh = lane >> 5;
     // Xs per (column block, slice): bf16 records of 16 hi then 16 lo values
     // per feature (64 bytes), or fp16 records of 16 values per feature (32
-    // bytes, the slice's first half); this lane's column half of each
-    const char* xb = reinterpret_cast<const char*>(a.Xh) + (static_cast<std::uint64_t>(f0 + lj) * 64 + lh * 16);
-    const char* xbh = reinterpret_cast<const char*>(a.Xh) + (static_cast<std::uint64_t>(f0) * 64 + lj * 32 + lh * 16);
+    // bytes, the slice's first half); this lane's column block of the pair
     const std::uint64_t cbStride = static_cast<std::uint64_t>(a.ldh) * 64;
+    const char* xb = reinterpret_cast<const char*>(a.Xh) + (lh * cbStride + static_cast<std::uint64_t>(f0 + lj) * 64);
+    const char* xbh = reinterpret_cast<const char*>(a.Xh) + (lh * cbStride + static_cast<std::uint64_t>(f0) * 64 + lj * 32);
+    // sub-step records of 96 G bytes: value masks (G/2 bytes a lane), then positions (G bytes a lane)
     const std::uint32_t* mb = a.tileMasks + lane * (G / 8);
+    const std::uint32_t* ib = a.tileMasks + 8 * G + lane * (G / 4);
     std::uint32_t* list = stepList[threadIdx.x / kWave];
 
     f32x16 acc[T][NT];
@@ -1089,6 +1240,7 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_binary_kernel(TileArgs a) 
     // place, 230 AGPRs and one wave per SIMD).
     auto run = [&](auto halfTag, const int (&ents)[kColRegs], std::uint32_t count, std::uint32_t c0) {
         constexpr bool HALF = decltype(halfTag)::value;
+        constexpr int K = HALF ? NS : 2;  // ring stages
         const char* lb = lutBytes + (HALF ? 0 : 4096);
         // Listed step i (i >= count: the zero step, multiplying zeros by
         // zeros; B read from a real step's column would turn an inf there
@@ -1097,22 +1249,39 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_binary_kernel(TileArgs a) 
             const bool live = i < count;
             const std::uint32_t e = step_col(ents, live ? i : 0);
             const std::uint32_t pa = live ? c0 + (e & 0xFFu) : a.zeroStep;
-            const std::uint32_t* mp = mb + static_cast<std::uint64_t>(pa) * (8 * G);
+            const std::uint32_t col = live ? e >> 8 : a.zeroCol;
+            const std::uint64_t rec = static_cast<std::uint64_t>(pa) * (24 * G);
             if constexpr (G == 16) {
-                const vu2 w = load_global<vu2>(mp);
+                const vu2 w = load_global<vu2>(mb + rec);
                 o.m[0] = w.x;
                 o.m[1] = w.y;
+                const vu4 q = load_global<vu4>(ib + rec);
+                o.ix[0] = q.x;
+                o.ix[1] = q.y;
+                o.ix[2] = q.z;
+                o.ix[3] = q.w;
             } else {
-                o.m[0] = load_global<std::uint32_t>(mp);
+                o.m[0] = load_global<std::uint32_t>(mb + rec);
+                const vu2 q = load_global<vu2>(ib + rec);
+                o.ix[0] = q.x;
+                o.ix[1] = q.y;
             }
-            const char* rb = (HALF ? xbh : xb) + static_cast<std::uint64_t>(e >> 8) * cbStride;
+            // unconditional loads (the zero step reads the pair of zeros):
+            // a load under a branch split the ring into blocks that waited
+            // for each step's loads before its products
+            const char* rb = (HALF ? xbh : xb) + static_cast<std::uint64_t>(col) * 2 * cbStride;
 #pragma unroll
             for (int u = 0; u < NT; ++u) {
-                o.h[u] = live ? load_global<vu4>(rb + u * 32 * (HALF ? 32 : 64)) : vu4{0u, 0u, 0u, 0u};
-                o.lo[u] = HALF || !live ? vu4{0u, 0u, 0u, 0u} : load_global<vu4>(rb + u * 32 * 64 + 32);
+                const char* ru = rb + u * 32 * (HALF ? 32 : 64);
+                o.h[u][0] = load_global<vu4>(ru);
+                o.h[u][1] = load_global<vu4>(ru + 16);
+                if constexpr (!HALF) {
+                    o.lo[u][0] = load_global<vu4>(ru + 32);
+                    o.lo[u][1] = load_global<vu4>(ru + 48);
+                }
             }
         };
-        // every tile's lookups of one step: byte addresses 8 * nibble
+        // every tile's lookups of one step: byte addresses 16 * mask byte
         auto expand = [&](const BinaryStage<G, NT>& o, vu4 (&A)[T]) {
 #pragma unroll
             for (int w = 0; w < G / 8; ++w) {
@@ -1128,44 +1297,39 @@ __global__ void __launch_bounds__(kThreads) hub_tiles_binary_kernel(TileArgs a) 
             for (int t = 0; t < T; ++t) {
 #pragma unroll
                 for (int u = 0; u < NT; ++u) {
-                    if constexpr (HALF) {
-                        acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                            __builtin_bit_cast(f16x8, A[t]), __builtin_bit_cast(f16x8, o.h[u]), acc[t][u], 0, 0, 0);
-                    } else {
-                        const bf16x8 av = __builtin_bit_cast(bf16x8, A[t]);
-                        acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, o.h[u]),
-                                                                            acc[t][u], 0, 0, 0);
-                        acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, o.lo[u]),
-                                                                            acc[t][u], 0, 0, 0);
+                    const std::uint32_t ix = o.ix[t / 2];
+                    const vu8 bh = join8(o.h[u][0], o.h[u][1]);
+                    if (t % 2) acc[t][u] = smfmac<HALF, 1>(A[t], bh, acc[t][u], ix);
+                    else acc[t][u] = smfmac<HALF, 0>(A[t], bh, acc[t][u], ix);
+                    if constexpr (!HALF) {
+                        const vu8 bl = join8(o.lo[u][0], o.lo[u][1]);
+                        if (t % 2) acc[t][u] = smfmac<HALF, 1>(A[t], bl, acc[t][u], ix);
+                        else acc[t][u] = smfmac<HALF, 0>(A[t], bl, acc[t][u], ix);
                     }
                 }
             }
         };
 
-        BinaryStage<G, NT> ring[NS];
+        BinaryStage<G, NT> ring[K];
 #pragma unroll
-        for (int k = 0; k < NS - 1; ++k) {
+        for (int k = 0; k < K - 1; ++k) {
             load(k, ring[k]);
             __builtin_amdgcn_sched_barrier(0);
         }
         // A step's operands are expanded while the previous step's products
-        // run (the lookups' latency hides behind the MFMAs; expanded before
-        // each step's products: 6.77 ms against 6.71).
+        // run (the lookups' latency hides behind the MFMAs).
         vu4 A[T];
         expand(ring[0], A);
-        for (std::uint32_t i = 0; i < count; i += NS) {
+        for (std::uint32_t i = 0; i < count; i += K) {
 #pragma unroll
-            for (int k = 0; k < NS; ++k) {
-                load(i + k + NS - 1, ring[(k + NS - 1) % NS]);
+            for (int k = 0; k < K; ++k) {
+                load(i + k + K - 1, ring[(k + K - 1) % K]);
                 __builtin_amdgcn_sched_barrier(0);
                 mma(A, ring[k]);
-                expand(ring[(k + 1) % NS], A);
+                expand(ring[(k + 1) % K], A);
                 // one MFMA, then a lookup and VALU instructions of the next
                 // step's expansion, and so on: the next step's lookups run
-                // between this step's products (issued in a block they left
-                // the lookups' latency on every step's path: config 3 hybrid
-                // step 6.71 -> 6.60 ms; every tile's high-half products
-                // before the low-half ones measured 6.68)
+                // between this step's products
                 constexpr int kMfma = (HALF ? 1 : 2) * T * NT;
 #pragma unroll
                 for (int j = 0; j < kMfma; ++j) {
@@ -1327,8 +1491,13 @@ __global__ void __launch_bounds__(kThreads) hub_zero_rows_kernel(TileArgs a, std
 
 inline std::uint32_t hub_ldh(std::uint32_t F) { return (F + kSlice - 1) / kSlice * kSlice; }
 
-// rows of Xh: the hub columns rounded up to whole column blocks
-inline std::uint32_t hub_rows(std::uint32_t hubCols) { return (hubCols + kTile - 1) / kTile * kTile; }
+// rows of Xh: the hub columns rounded up to whole column blocks; for
+// binary tiles to pairs of them, plus one pair of zeros (the zero step's
+// columns: every load of the ring's tail reads a real address)
+inline std::uint32_t hub_rows(const tcc_hub_tiles* T) {
+    if (T->tile_format == TCC_TILES_BINARY) return (T->hub_cols + 2 * kTile - 1) / (2 * kTile) * (2 * kTile) + 2 * kTile;
+    return (T->hub_cols + kTile - 1) / kTile * kTile;
+}
 
 // Two steps in flight (three stages) for the small groups; the larger
 // groups keep their 4 G accumulator tiles and two stages within two or
@@ -1352,8 +1521,9 @@ hipError_t launch_tiles(const TileArgs& a, bool split, hipStream_t st) {
 // accumulators (128 registers): one N tile at G = 16 (32 features a wave),
 // two at G = 8 (64 features a wave).
 constexpr int binary_nt(std::uint32_t G) { return G == 16 ? 1 : 2; }
-// Loads run three steps ahead (config 3, 64-entry steps: 6.60 ms per
-// hybrid step against 6.62 with two steps ahead).
+// Loads of fp16 steps run three steps ahead (bf16 steps, whose stages hold
+// twice the registers, one step ahead): 242 registers at G = 16, two waves
+// per SIMD.
 constexpr int kBinaryStages = 4;
 
 hipError_t launch_binary(const TileArgs& a, std::uint32_t G, hipStream_t st) {
@@ -1392,7 +1562,9 @@ int build_hybrid(const HybridParams& P, tcc_hybrid* out, void* stream) {
     const std::uint32_t RB = (numRows + kTile - 1) / kTile;
     const std::uint32_t NG = (RB + G - 1) / G;
     const std::uint32_t rowSlots = NG * G * kTile;
-    const std::uint32_t CB = (numCols + kTile - 1) / kTile;
+    // binary steps pair 16-column blocks: the block count rounded up to even
+    const std::uint32_t CB = (numCols + kTile - 1) / kTile + (binary ? ((numCols + kTile - 1) / kTile) % 2 : 0);
+    const std::uint32_t stepTiles = binary ? 2 * G : G, colSteps = binary ? CB / 2 : CB;
     const std::uint64_t En = std::max<std::uint32_t>(E, 1);
     const std::uint64_t Vn = std::max<std::uint64_t>({En, rowSlots, numCols});
     const unsigned tileBits = std::max(1u, rank_bits(static_cast<std::uint64_t>(NG) * CB * G));
@@ -1437,7 +1609,7 @@ int build_hybrid(const HybridParams& P, tcc_hybrid* out, void* stream) {
         restCol = reinterpret_cast<std::uint32_t*>(take(4 * En));
         restVal = reinterpret_cast<float*>(take(4 * En));
         temp = reinterpret_cast<std::uint32_t*>(take(4 * tempElems));
-        // [0]=err [1]=tiles [2]=steps [3]=rest [4]=units [5]=hubBlocks [6]=dense tiles
+        // [0]=err [1]=tiles [2]=steps [3]=rest [4]=units [5]=hubBlocks [6]=dense tiles [7]=sub-steps
         small = reinterpret_cast<std::uint32_t*>(take(256));
         return off;
     };
@@ -1476,9 +1648,9 @@ int build_hybrid(const HybridParams& P, tcc_hybrid* out, void* stream) {
         hipLaunchKernelGGL(tile_start_kernel, dim3(grid_for(E, kThreads)), dim3(kThreads), 0, st, flags, pos, E,
                            tileStart);
         hipLaunchKernelGGL(dense_tiles_kernel, dim3(grid_for(E, kThreads)), dim3(kThreads), 0, st, sorted, tileStart,
-                           small + 1, E, P.minTileNnz, P.minStepNnz, CB, G, dense, small + 6, small + 5);
+                           small + 1, E, P.minTileNnz, P.minStepNnz, colSteps, stepTiles, dense, small + 6, small + 5);
         hipLaunchKernelGGL(step_heads_kernel, dim3(grid_for(E, kThreads)), dim3(kThreads), 0, st, sorted, tileStart,
-                           small + 1, dense, G, CB, stepHead, groupSteps);
+                           small + 1, dense, stepTiles, colSteps, stepHead, groupSteps);
         TCC_LAUNCH_CHECK();
         // step positions over the E-sized head array (zero past the tile count)
         TCC_HIP_CHECK(exclusive_scan(stepHead, stepPos, E, small + 2, temp, st));
@@ -1487,32 +1659,88 @@ int build_hybrid(const HybridParams& P, tcc_hybrid* out, void* stream) {
         TCC_LAUNCH_CHECK();
         TCC_HIP_CHECK(exclusive_scan(restFlag, restPos, E, small + 3, temp, st));
     }
-    hipLaunchKernelGGL(units_per_group_kernel, dim3(grid_for(NG, kThreads)), dim3(kThreads), 0, st, groupSteps, NG,
-                       P.unitSteps, unitCount);
-    TCC_LAUNCH_CHECK();
-    TCC_HIP_CHECK(exclusive_scan(unitCount, unitCount, NG, small + 4, temp, st));
+    if (!binary) {
+        hipLaunchKernelGGL(units_per_group_kernel, dim3(grid_for(NG, kThreads)), dim3(kThreads), 0, st, groupSteps, NG,
+                           P.unitSteps, unitCount);
+        TCC_LAUNCH_CHECK();
+        TCC_HIP_CHECK(exclusive_scan(unitCount, unitCount, NG, small + 4, temp, st));
+    }
     TCC_HIP_CHECK(hipMemcpyAsync(hostSmall, small, sizeof(hostSmall), hipMemcpyDeviceToHost, st));
     TCC_HIP_CHECK(hipStreamSynchronize(st));
     TCC_REQUIRE(hostSmall[0] == 0, TCC_ERR_INVALID_ARGUMENT,
                 hostSmall[0] == 2 ? "duplicate (row, col) entries in the COO input" : "COO index out of range");
     const std::uint32_t NS = E > 0 ? hostSmall[2] : 0;
     const std::uint32_t NR = E > 0 ? hostSmall[3] : 0;
-    const std::uint32_t NU = hostSmall[4];
     const std::uint32_t ND = E > 0 ? hostSmall[6] : 0;
-    const std::uint32_t hubCols = std::min(hostSmall[5] * kTile, numCols);
+    const std::uint32_t hubCols = std::min(hostSmall[5] * (binary ? 2 * kTile : kTile), numCols);
+
+    // Binary tiles: the steps' raw bits, their layers (a second one where a
+    // nibble holds more than two entries) and the sub-steps the units cut.
+    std::uint32_t NSS = NS;  // sub-steps
+    DevBuf<char> binScratch;
+    std::uint32_t *raw = nullptr, *stepColTmp = nullptr, *subPos = nullptr, *subOffset = nullptr;
+    if (binary) {
+        const std::uint64_t NS1 = static_cast<std::uint64_t>(NS) + 1;
+        std::uint32_t *stepOffset, *layers, *groupSub;
+        auto carveBin = [&](char* base) {
+            std::size_t off = 0;
+            auto take = [&](std::size_t bytes) {
+                char* p = base ? base + off : nullptr;
+                off += align_up(bytes);
+                return reinterpret_cast<std::uint32_t*>(p);
+            };
+            raw = take(64ull * G * NS1);
+            stepColTmp = take(4 * NS1);
+            stepOffset = take(4ull * (NG + 1));
+            layers = take(4 * NS1);
+            subPos = take(4 * NS1);
+            subOffset = take(4ull * (NG + 1));
+            groupSub = take(4ull * (NG + 1));
+            return off;
+        };
+        TCC_HIP_CHECK(hipMalloc(&binScratch.p, carveBin(nullptr)));
+        carveBin(binScratch.p);
+        TCC_HIP_CHECK(fill<std::uint32_t>(raw, 16ull * G * NS1, 0u, st));
+        if (E > 0) {
+            hipLaunchKernelGGL(tile_slots_kernel, dim3(grid_for(E, kThreads)), dim3(kThreads), 0, st, sorted, tileStart,
+                               small + 1, dense, stepHead, stepPos, stepTiles, colSteps, slot, stepColTmp);
+            hipLaunchKernelGGL(place_entries_kernel, dim3(grid_for(E, kThreads)), dim3(kThreads), 0, st, sorted, perm,
+                               E, flags, pos, dense, slot, restPos, P.row, P.col, P.val, nullptr, P.format, G, raw,
+                               restRow, restCol, P.val ? restVal : nullptr);
+            TCC_LAUNCH_CHECK();
+        }
+        TCC_HIP_CHECK(exclusive_scan(groupSteps, stepOffset, NG, stepOffset + NG, temp, st));
+        if (NS > 0) {
+            hipLaunchKernelGGL(binary_layers_kernel, dim3(grid_for(static_cast<std::uint64_t>(NS) * kWave, kThreads)),
+                               dim3(kThreads), 0, st, raw, NS, G, layers);
+            TCC_LAUNCH_CHECK();
+        }
+        TCC_HIP_CHECK(exclusive_scan(layers, subPos, NS, subPos + NS, temp, st));
+        hipLaunchKernelGGL(sub_offsets_kernel, dim3(grid_for(NG + 1, kThreads)), dim3(kThreads), 0, st, stepOffset,
+                           subPos, NG, subOffset, groupSub);
+        hipLaunchKernelGGL(units_per_group_kernel, dim3(grid_for(NG, kThreads)), dim3(kThreads), 0, st, groupSub, NG,
+                           P.unitSteps, unitCount);
+        TCC_LAUNCH_CHECK();
+        TCC_HIP_CHECK(exclusive_scan(unitCount, unitCount, NG, small + 4, temp, st));
+        TCC_HIP_CHECK(hipMemcpyAsync(small + 7, subPos + NS, 4, hipMemcpyDeviceToDevice, st));
+        TCC_HIP_CHECK(hipMemcpyAsync(hostSmall, small, sizeof(hostSmall), hipMemcpyDeviceToHost, st));
+        TCC_HIP_CHECK(hipStreamSynchronize(st));
+        NSS = hostSmall[7];
+    }
+    const std::uint32_t NU = hostSmall[4];
 
     // tiles part: rowOrder[rowSlots] hubColOrder[hubCols] groupStepOffset[NG+1] unitFirst[NG+1] stepCol[NS]
     // units[3 NU] unitOrder[NU] unitPartial[NU] sharedGroups[3 NG] then the format's tiles (one more step, of
     // zeros, that the kernels' ring tail reads): tileVals[256 G (NS+1)], or tileMasks[8 G (NS+1)] and the
     // scales
-    const std::uint64_t NSn = std::max<std::uint32_t>(NS, 1);
+    const std::uint64_t NSn = std::max<std::uint32_t>(NSS, 1);
     const std::uint64_t NUn = std::max<std::uint32_t>(NU, 1);
     const std::uint32_t paddedRows = (numRows + 7) / 8 * 8;
     std::size_t tilesBytes = align_up(4ull * rowSlots) + align_up(4ull * std::max(hubCols, 1u)) +
                              align_up(4ull * (NG + 1)) + align_up(4ull * (NG + 1)) + align_up(4 * NSn) +
                              align_up(12 * NUn) + align_up(4 * NUn) + align_up(4 * NUn) + align_up(12ull * NG);
     if (binary) {
-        tilesBytes += align_up(32ull * G * (NS + 1));
+        tilesBytes += align_up(96ull * G * (NSS + 1));
         if (P.rowScale) tilesBytes += align_up(4ull * rowSlots) + align_up(4ull * paddedRows);
         if (P.colScale) tilesBytes += align_up(4ull * numCols);
     } else {
@@ -1539,7 +1767,7 @@ int build_hybrid(const HybridParams& P, tcc_hybrid* out, void* stream) {
     std::uint32_t* oTileMasks = nullptr;
     float *oRowScale = nullptr, *oRestRowScale = nullptr, *oColScale = nullptr;
     if (binary) {
-        oTileMasks = reinterpret_cast<std::uint32_t*>(takeOut(32ull * G * (NS + 1)));
+        oTileMasks = reinterpret_cast<std::uint32_t*>(takeOut(96ull * G * (NSS + 1)));
         if (P.rowScale) {
             oRowScale = reinterpret_cast<float*>(takeOut(4ull * rowSlots));
             oRestRowScale = reinterpret_cast<float*>(takeOut(4ull * paddedRows));
@@ -1554,11 +1782,15 @@ int build_hybrid(const HybridParams& P, tcc_hybrid* out, void* stream) {
     };
     bool ok = hipMemcpyAsync(oRowOrder, rowOrder, 4ull * rowSlots, hipMemcpyDeviceToDevice, st) == hipSuccess &&
               (!hubCols || hipMemcpyAsync(oHubCols, colOrder, 4ull * hubCols, hipMemcpyDeviceToDevice, st) == hipSuccess) &&
-              exclusive_scan(groupSteps, oGroupStepOffset, NG, oGroupStepOffset + NG, temp, st) == hipSuccess &&
+              (binary ? hipMemcpyAsync(oGroupStepOffset, subOffset, 4ull * (NG + 1), hipMemcpyDeviceToDevice, st)
+                      : exclusive_scan(groupSteps, oGroupStepOffset, NG, oGroupStepOffset + NG, temp, st)) == hipSuccess &&
               hipMemcpyAsync(oUnitFirst, unitCount, 4ull * NG, hipMemcpyDeviceToDevice, st) == hipSuccess &&
               hipMemcpyAsync(oUnitFirst + NG, small + 4, 4, hipMemcpyDeviceToDevice, st) == hipSuccess;
     if (binary) {
-        ok = ok && fill<std::uint32_t>(oTileMasks, 8ull * G * (NS + 1), 0u, st) == hipSuccess;
+        ok = ok && fill<std::uint32_t>(oTileMasks, 24ull * G * (NSS + 1), 0u, st) == hipSuccess;
+        if (ok && NS > 0)
+            hipLaunchKernelGGL(binary_encode_kernel, dim3(grid_for(static_cast<std::uint64_t>(NS) * kWave, kThreads)),
+                               dim3(kThreads), 0, st, raw, NS, G, subPos, stepColTmp, oTileMasks, oStepCol);
         if (ok && P.rowScale) {
             hipLaunchKernelGGL(ordered_scale_kernel, dim3(grid_for(rowSlots, kThreads)), dim3(kThreads), 0, st,
                                oRowOrder, rowSlots, P.rowScale, oRowScale);
@@ -1575,9 +1807,9 @@ int build_hybrid(const HybridParams& P, tcc_hybrid* out, void* stream) {
         set_last_error("HIP error while initialising the hub tiles");
         return fail(TCC_ERR_HIP);
     }
-    if (E > 0) {
+    if (E > 0 && !binary) {
         hipLaunchKernelGGL(tile_slots_kernel, dim3(grid_for(E, kThreads)), dim3(kThreads), 0, st, sorted, tileStart,
-                           small + 1, dense, stepHead, stepPos, G, CB, slot, oStepCol);
+                           small + 1, dense, stepHead, stepPos, stepTiles, colSteps, slot, oStepCol);
         hipLaunchKernelGGL(place_entries_kernel, dim3(grid_for(E, kThreads)), dim3(kThreads), 0, st, sorted, perm, E,
                            flags, pos, dense, slot, restPos, P.row, P.col, P.val, oTileVals, P.format, G, oTileMasks,
                            restRow, restCol, P.val ? restVal : nullptr);
@@ -1667,7 +1899,7 @@ int build_hybrid(const HybridParams& P, tcc_hybrid* out, void* stream) {
     T.nnz = E - NR;
     T.group_blocks = G;
     T.num_groups = NG;
-    T.num_steps = NS;
+    T.num_steps = NSS;
     T.num_tiles = ND;
     T.num_units = NU;
     T.unit_steps = P.unitSteps;
@@ -1862,11 +2094,11 @@ inline HalfSpace half_space(std::uint32_t hubRows, std::uint32_t slices) {
 size_t tcc_hub_tiles_workspace_bytes(const tcc_hub_tiles* T, std::uint32_t featureDim) {
     if (!T || featureDim == 0) return 0;
     const std::size_t ldh = hub_ldh(featureDim);
-    std::size_t bytes = align_up(static_cast<size_t>(hub_rows(T->hub_cols)) * ldh * sizeof(float)) +
+    std::size_t bytes = align_up(static_cast<size_t>(hub_rows(T)) * ldh * sizeof(float)) +
                         align_up(static_cast<size_t>(T->num_partial_units) * T->group_blocks * kTile * ldh * sizeof(float));
     const std::uint32_t slices = static_cast<std::uint32_t>(ldh / (32u * binary_nt(T->group_blocks)));
     if (T->tile_format == TCC_TILES_BINARY && slices <= kMaxHalfSlices)
-        bytes += half_space(hub_rows(T->hub_cols), slices).bytes;
+        bytes += half_space(hub_rows(T), slices).bytes;
     return bytes;
 }
 
@@ -1886,10 +2118,10 @@ static std::uint32_t* hub_slice_max(const tcc_hub_tiles* T, std::uint32_t featur
     W = 32u * binary_nt(T->group_blocks);
     slices = ldh / W;
     if (slices > kMaxHalfSlices) return nullptr;
-    const std::uint64_t n = static_cast<std::uint64_t>(hub_rows(T->hub_cols)) * ldh;
+    const std::uint64_t n = static_cast<std::uint64_t>(hub_rows(T)) * ldh;
     char* halfBase = static_cast<char*>(workspace) + align_up(n * sizeof(float)) +
                      align_up(static_cast<size_t>(T->num_partial_units) * T->group_blocks * kTile * ldh * sizeof(float));
-    return reinterpret_cast<std::uint32_t*>(halfBase + half_space(hub_rows(T->hub_cols), slices).partial);
+    return reinterpret_cast<std::uint32_t*>(halfBase + half_space(hub_rows(T), slices).partial);
 }
 
 // tcc_hub_tiles_spmm; maxReady: the slice maxima of half records are in the
@@ -1918,7 +2150,7 @@ static int hub_tiles_spmm(const tcc_hub_tiles* T, const float* X, float* Y, std:
                 TCC_ERR_INVALID_ARGUMENT, "hub tiles SpMM workspace too small or misaligned");
     const hipStream_t st = as_stream(stream);
     float* Xh = static_cast<float*>(workspace);
-    const std::uint32_t hubRows = hub_rows(T->hub_cols);
+    const std::uint32_t hubRows = hub_rows(T);
     const std::uint64_t n = static_cast<std::uint64_t>(hubRows) * ldh;
     const std::uint32_t slices = ldh / (binary ? 32u * binary_nt(T->group_blocks) : kSlice);
     char* halfBase = static_cast<char*>(workspace) + align_up(n * sizeof(float)) +
@@ -1944,7 +2176,7 @@ static int hub_tiles_spmm(const tcc_hub_tiles* T, const float* X, float* Y, std:
         hipLaunchKernelGGL(hub_scale_kernel, dim3(slices), dim3(kThreads), 0, st, partial, kPackSliceMaxRows, slices, up,
                            down);
         TCC_LAUNCH_CHECK();
-        hipLaunchKernelGGL(hub_rows_half_kernel, dim3(grid_for(n / kTile, kThreads)), dim3(kThreads), 0, st, X,
+        hipLaunchKernelGGL(hub_rows_half_kernel, dim3(grid_for(n / (2 * kTile), kThreads)), dim3(kThreads), 0, st, X,
                            featureDim, T->hubColOrder, T->hub_cols, hubRows, ldh, T->colScale, up, W,
                            reinterpret_cast<std::uint16_t*>(Xh), flags);
     } else if (split || binary) {
@@ -1977,6 +2209,7 @@ static int hub_tiles_spmm(const tcc_hub_tiles* T, const float* X, float* Y, std:
     a.numUnits = T->num_units;
     a.slices = slices;
     a.storeY = storeY ? 1 : 0;
+    a.zeroCol = binary ? hubRows / (2 * kTile) - 1 : 0;
     if (halfRecords) {
         a.halfFlags = reinterpret_cast<const unsigned char*>(halfBase + hs.flags);
         a.sliceDown = reinterpret_cast<const float*>(halfBase + hs.down);

@@ -389,8 +389,8 @@ class HybridMatrix:
             "rest": self.rest.to_host(),
         }
         if t.tile_format == TILES_BINARY:
-            # step p's G*32 bytes (with the zero step after the last)
-            d["tileMasks"] = _download(t.tileMasks, 8 * G * (S + 1), np.uint32).view(np.uint8).reshape(S + 1, 32 * G)
+            # sub-step p's 96 G bytes (value masks, then positions; with the zero sub-step after the last)
+            d["tileMasks"] = _download(t.tileMasks, 24 * G * (S + 1), np.uint32).view(np.uint8).reshape(S + 1, 96 * G)
             d["rowScale"] = None if not t.rowScale else _download(t.rowScale, 16 * G * NG, np.float32)
             d["colScale"] = None if not t.colScale else _download(t.colScale, t.num_cols, np.float32)
             n8 = (t.num_rows + 7) // 8 * 8

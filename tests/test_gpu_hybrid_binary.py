@@ -8,13 +8,14 @@ column scales, A = diag(r) P diag(c).
 Checked through the C-ABI:
 - the arrays, exactly, against an independent numpy construction of the
   layout include/tcc_spmm_cnic.h states: steps = (group of G row blocks,
-  column block) whose tiles hold at least min_step_nnz entries together,
-  every entry of such a step stored as bit k%8 of byte
-  (16*(j%2) + i + 32*(k/8))*(G/2) + j/2 of the step's bytes (row block j,
-  row i, column k); units, their launch order, the partial-sum slots of
-  shared groups and the shared-group list; the scales in rowOrder's order
-  and in row order; the remainder equal to the oracle's BCSR of exactly the
-  other entries, without values;
+  pair of 16-column blocks) whose tiles hold at least min_step_nnz entries
+  together, every entry of such a step stored in sub-step records of the
+  2:4 sparse MFMA's operands (per lane and 32-row tile a value-mask byte
+  and 16 bits of positions, two value slots per group of four columns, a
+  second layer where a group holds more than two entries); units, their
+  launch order, the partial-sum slots of shared groups and the shared-group
+  list; the scales in rowOrder's order and in row order; the remainder
+  equal to the oracle's BCSR of exactly the other entries, without values;
 - the products, against the fp64 CSR oracle over the pattern and the
   column-scaled, TF32-rounded X, times the row scales (rel-L2 <= 1e-5: the
   tiles' bf16 halves of TF32(c x) are exact, the sums fp32), and against the
@@ -24,11 +25,11 @@ Checked through the C-ABI:
   thresholds from 1 to 256, units of 1 to 3000 steps (the kernel reads
   a unit's step list 256 steps at a time), phased remainders, F from 1 to
   700, hubs or uniform, a fully dense corner;
-- an Inf in a hub column's feature row: rows with that column get Inf, the
-  other rows of every group with a step in its column block get NaN (0 * Inf
+- an Inf in a hub column's feature row: rows with that column get Inf (or
+  NaN), the rows a zero value slot pointing at it reaches get NaN (0 * Inf
   in the tiles' products), every other row stays finite;
-- half records: fp16 values of 2^e x where exact for a whole (column block,
-  32-feature slice), the bf16 halves elsewhere, both in one product (a
+- half records: fp16 values of 2^e x where exact for a whole (column-block
+  pair, 32-feature slice), the bf16 halves elsewhere, both in one product (a
   feature below the fp16 grid and one above its range), through the hybrid
   and through tcc_hub_tiles_spmm alone;
 - argument errors.
@@ -43,10 +44,38 @@ pytestmark = pytest.mark.gpu
 
 REL = 1e-5
 NORTH_STAR = 1e-3
-DEFAULT_MIN_STEP, DEFAULT_G, DEFAULT_UNIT_STEPS = 36, 16, 768
+DEFAULT_MIN_STEP, DEFAULT_G, DEFAULT_UNIT_STEPS = 40, 16, 768
+
+
+def _nibble_tables():
+    """(values, positions)[layer][nibble]: the two value slots a nibble's
+    entries take in a layer (layer 0: its lowest two set bits, layer 1: the
+    rest), as the sparse MFMA reads them: value bits (slot 0 low) and 2-bit
+    positions (slot 0 low), increasing, a slot without an entry on an unused
+    position."""
+    vals = np.zeros((2, 16), np.uint32)
+    pos = np.zeros((2, 16), np.uint32)
+    for nib in range(16):
+        bits = [p for p in range(4) if nib >> p & 1]
+        for layer, sel in enumerate((bits[:2], bits[2:])):
+            if len(sel) == 2:
+                v, (p0, p1) = 3, sel
+            elif len(sel) == 1:
+                v, (p0, p1) = (1, (sel[0], 3)) if sel[0] < 3 else (2, (2, 3))
+            else:
+                v, (p0, p1) = 0, (0, 1)
+            vals[layer, nib], pos[layer, nib] = v, p0 | p1 << 2
+    return vals, pos
+
+
+NIB_VALS, NIB_POS = _nibble_tables()
 
 
 def reference_binary_layout(dst, src, nr, nc, min_step, G, unit_steps, r=None, c=None):
+    """The layout include/tcc_spmm_cnic.h states for binary tiles: steps of
+    G row blocks by a pair of 16-column blocks, the pattern in sub-step
+    records of value masks and positions (a second layer where a group of
+    four columns holds more than two entries)."""
     dst = dst.astype(np.int64)
     src = src.astype(np.int64)
     rorder = np.lexsort((np.arange(nr), -np.bincount(dst, minlength=nr)))
@@ -56,28 +85,49 @@ def reference_binary_layout(dst, src, nr, nc, min_step, G, unit_steps, r=None, c
     crank = np.empty(nc, np.int64)
     crank[corder] = np.arange(nc)
     RB, CB = (nr + 15) // 16, (nc + 15) // 16
+    CB += CB % 2
+    CP = CB // 2
     NG = (RB + G - 1) // G
+    T = G // 2
     row_order = np.full(16 * G * NG, 0xFFFFFFFF, np.uint32)
     row_order[:nr] = rorder
     rr, cr = rrank[dst], crank[src]
     rb, cb = rr // 16, cr // 16
     tile = rb * CB + cb
     tkeys, tcounts = np.unique(tile, return_counts=True)
-    tstep = (tkeys // CB) // G * CB + tkeys % CB
+    tstep = (tkeys // CB) // G * CP + (tkeys % CB) // 2
     skeys, sinv = np.unique(tstep, return_inverse=True)
     snnz = np.bincount(sinv, weights=tcounts).astype(np.int64) if tkeys.size else np.zeros(0, np.int64)
     dense_tile = snnz[sinv] >= min_step if tkeys.size else np.zeros(0, bool)
     dense_keys = tkeys[dense_tile]
     in_dense = np.isin(tile, dense_keys)
-    step_keys = np.unique((dense_keys // CB) // G * CB + dense_keys % CB)
+    step_keys = np.unique((dense_keys // CB) // G * CP + (dense_keys % CB) // 2)
     S = step_keys.size
-    masks = np.zeros((S + 1, 32 * G), np.uint8)
-    sid = np.searchsorted(step_keys, (rb[in_dense] // G) * CB + cb[in_dense])
+    raw = np.zeros((S, 2, 32 * G), np.uint8)
+    sid = np.searchsorted(step_keys, (rb[in_dense] // G) * CP + cb[in_dense] // 2)
     j, i, k = rb[in_dense] % G, rr[in_dense] % 16, cr[in_dense] % 16
     byte = (16 * (j % 2) + i + 32 * (k // 8)) * (G // 2) + j // 2
-    np.bitwise_or.at(masks, (sid, byte), (1 << (k % 8)).astype(np.uint8))
-    sg, sc = step_keys // CB, step_keys % CB
-    gso = np.searchsorted(sg, np.arange(NG + 1)).astype(np.uint32)
+    np.bitwise_or.at(raw, (sid, cb[in_dense] % 2, byte), (1 << (k % 8)).astype(np.uint8))
+    lanes = raw.reshape(S, 2, 64, T).astype(np.uint32)  # [step, half, lane, tile]
+    nib = np.stack([lanes[:, 0] & 15, lanes[:, 0] >> 4, lanes[:, 1] & 15, lanes[:, 1] >> 4], -1)  # [S, lane, tile, 4]
+    crowded = (np.array([bin(x).count("1") for x in range(16)])[nib] > 2).reshape(S, 64 * T * 4).any(1)
+    layers = np.where(crowded, 2, 1)
+    sub_step = np.repeat(np.arange(S), layers)
+    sub_layer = np.concatenate([np.arange(n) for n in layers]) if S else np.zeros(0, np.int64)
+    SS = sub_step.size
+    recs = np.zeros((SS + 1, 96 * G), np.uint8)
+    for q in range(SS):
+        n4 = nib[sub_step[q]]
+        L = sub_layer[q]
+        m = (NIB_VALS[L][n4] << (2 * np.arange(4))).sum(-1)        # [lane, tile] value masks
+        ix = (NIB_POS[L][n4] << (4 * np.arange(4))).sum(-1)        # [lane, tile] 16-bit positions
+        recs[q, :32 * G] = m.astype(np.uint8).reshape(-1)
+        recs[q, 32 * G:] = ix.astype("<u2").reshape(-1).view(np.uint8)
+    sg, sp = step_keys // CP, step_keys % CP
+    gso_steps = np.searchsorted(sg, np.arange(NG + 1))
+    sub_pos = np.concatenate([[0], np.cumsum(layers)]).astype(np.int64)
+    gso = sub_pos[gso_steps].astype(np.uint32)
+    sc = sp[sub_step]
     units, partial, shared = [], [], []
     slots = 0  # partial-sum slots handed out so far (units of shared groups, in unit order)
     for g in range(NG):
@@ -91,11 +141,11 @@ def reference_binary_layout(dst, src, nr, nc, min_step, G, unit_steps, r=None, c
             slots += 1 if nu > 1 else 0
     units = np.array(units, np.uint32).reshape(-1, 3)
     unit_order = np.argsort(sc[units[:, 1]] if len(units) else units[:, 1], kind="stable").astype(np.uint32)
-    hub_cols = min(16 * (int(sc.max()) + 1), nc) if S else 0
+    hub_cols = min(32 * (int(sp.max()) + 1), nc) if S else 0
     d = dict(rowOrder=row_order, hubColOrder=corder[:hub_cols].astype(np.uint32), groupStepOffset=gso,
-             stepCol=sc.astype(np.uint32), tileMasks=masks, units=units, unitOrder=unit_order,
+             stepCol=sc.astype(np.uint32), tileMasks=recs, units=units, unitOrder=unit_order,
              unitPartial=np.array(partial, np.uint32), sharedGroups=np.array(shared, np.uint32).reshape(-1, 3),
-             hub_cols=hub_cols, num_tiles=int(dense_keys.size), rest=~in_dense)
+             hub_cols=hub_cols, num_tiles=int(dense_keys.size), rest=~in_dense, layers=layers)
     if r is not None:
         rs = np.zeros(16 * G * NG, np.float32)
         rs[:nr] = r[rorder]
@@ -143,6 +193,7 @@ def build(swtcf, dst, src, nr, nc, r, c, **kw):
     (300, 4000, 60000, True, 4, 8, 300, "random"),  # units past 256 steps (step list in two reads)
     (600, 5000, 150000, True, 16, 16, 3000, "symnorm"),
     (60, 60, 0, False, 32, 16, 0, "random"),
+    (64, 64, 4096, False, 64, 16, 0, "none"),        # a fully dense corner: every step in two layers
 ])
 def test_binary_arrays_match_numpy_layout(gpu, oracle, nr, nc, nnz, hubs, min_step, G, unit_steps, scale):
     from tcc_amd import swtcf
@@ -152,9 +203,12 @@ def test_binary_arrays_match_numpy_layout(gpu, oracle, nr, nc, nnz, hubs, min_st
     H = build(swtcf, dst, src, nr, nc, r, c, min_step_nnz=min_step, group_blocks=G, unit_steps=unit_steps)
     h = H.to_host()
     want = reference_binary_layout(dst, src, nr, nc, min_step, G, unit_steps or DEFAULT_UNIT_STEPS, r, c)
-    print(f"binary layout nr={nr} nc={nc} nnz={nnz} step>={min_step} G={G}: {h['num_steps']} steps, "
+    print(f"binary layout nr={nr} nc={nc} nnz={nnz} step>={min_step} G={G}: {h['num_steps']} sub-steps "
+          f"({int((want['layers'] == 2).sum())} second layers), "
           f"{h['num_tiles']} tiles, {h['tile_nnz']} tile entries, {h['num_shared_groups']} shared groups", flush=True)
     assert h["tile_format"] == swtcf.TILES_BINARY
+    if nnz == nr * nc:
+        assert np.all(want["layers"] == 2)
     assert h["group_blocks"] == G and h["unit_steps"] == (unit_steps or DEFAULT_UNIT_STEPS)
     assert h["hub_cols"] == want["hub_cols"] and h["num_tiles"] == want["num_tiles"]
     for k in ("rowOrder", "hubColOrder", "groupStepOffset", "stepCol", "units", "unitOrder", "unitPartial",
@@ -264,11 +318,38 @@ def test_binary_symnorm_error_against_tf32_values(gpu, oracle):
     assert 1e-5 < e_values <= NORTH_STAR
 
 
+def zero_slot_rows(h, G, pair, half, col):
+    """Rows that a value slot of 0 pointing at column `col` of block `half`
+    of column pair `pair` reaches in some sub-step: 0 * X[col] enters their
+    sums (lane l < 32 holds columns 0..7 of each block, l >= 32 columns
+    8..15; slots 4*half + 2*(c%8 // 4) .. +1 cover column c)."""
+    T = G // 2
+    recs, gso, steps = h["tileMasks"], h["groupStepOffset"], h["stepCol"]
+    lanes = np.arange(32) + 32 * (col // 8)
+    k = 2 * half + (col % 8) // 4  # nibble of the lane
+    rows = set()
+    for g in range(h["num_groups"]):
+        for q in range(int(gso[g]), int(gso[g + 1])):
+            if steps[q] != pair:
+                continue
+            m = recs[q, :32 * G].reshape(64, T).astype(np.uint32)[lanes]
+            ix = recs[q, 32 * G:].view("<u2").reshape(64, T).astype(np.uint32)[lanes]
+            hit = np.zeros(m.shape, bool)
+            for slot in (2 * k, 2 * k + 1):
+                hit |= ((m >> slot) & 1 == 0) & ((ix >> (2 * slot)) & 3 == col % 4)
+            for lane, t in zip(*np.nonzero(hit)):
+                r = int(h["rowOrder"][16 * G * g + 32 * t + lane % 32])
+                if r != 0xFFFFFFFF:
+                    rows.add(r)
+    return np.array(sorted(rows), np.int64)
+
+
 @pytest.mark.parametrize("G", [8, 16])
 def test_binary_inf_in_hub_column(gpu, oracle, G):
     """An Inf in a hub column's feature row: rows with an entry in that
-    column get Inf; the other rows of every group with a step in its column
-    block get NaN (0 * Inf inside the tiles' products, as inside the
+    column get Inf (or NaN, where a second layer's empty slot also points
+    at it); the other rows that a zero value slot pointing at that column
+    reaches get NaN (0 * Inf inside the tiles' products, as inside the
     reference's 8x8 mma blocks); every other row stays finite and exact."""
     from tcc_amd import swtcf
 
@@ -276,20 +357,16 @@ def test_binary_inf_in_hub_column(gpu, oracle, G):
     dst, src = random_coo(nr, nc, 20000, 23, True)
     H = build(swtcf, dst, src, nr, nc, None, None, min_step_nnz=8, group_blocks=G)
     h = H.to_host()
-    c0 = int(h["hubColOrder"][0])  # the highest-degree column: rank 0, column block 0
+    c0 = int(h["hubColOrder"][0])  # the highest-degree column: rank 0, column 0 of block 0 of pair 0
     X = np.random.default_rng(5).standard_normal((nc, F)).astype(np.float32)
     X[c0, 0] = np.inf
     Y = swtcf.hybrid_spmm(H, torch.from_numpy(X).cuda()).cpu().numpy()[:nr]
     has = np.zeros(nr, bool)
     has[dst[src == c0].astype(np.int64)] = True
     exposed = np.zeros(nr, bool)
-    gso, steps = h["groupStepOffset"], h["stepCol"]
-    for g in range(h["num_groups"]):
-        if np.any(steps[gso[g]:gso[g + 1]] == 0):
-            rows = h["rowOrder"][16 * G * g: 16 * G * (g + 1)]
-            exposed[rows[rows != 0xFFFFFFFF].astype(np.int64)] = True
-    assert has.any() and (exposed & ~has).any()
-    assert np.all(np.isposinf(Y[has, 0]))
+    exposed[zero_slot_rows(h, G, 0, 0, 0)] = True
+    assert has.any() and (exposed & ~has).any() and (~(has | exposed)).any()
+    assert not np.any(np.isfinite(Y[has, 0])) and not np.any(np.isneginf(Y[has, 0]))
     assert np.all(np.isnan(Y[exposed & ~has, 0]))
     assert np.all(np.isfinite(Y[~(has | exposed), 0]))
     X[c0, 0] = 0.0
@@ -331,7 +408,9 @@ def test_binary_half_and_bf16_records(gpu, oracle, G, scale):
     assert H.view.tiles.num_steps > 0
     X = mixed_range_features(nc, F, 3)
     want = scaled_product(oracle, dst, src, nr, X, r, c)
-    Y = swtcf.hybrid_spmm(H, torch.from_numpy(X).cuda()).cpu().numpy()[:nr].astype(np.float64)
+    # a workspace of NaN bytes: the bf16 steps' ring tail reads the zero pair in its bf16 form
+    ws = torch.full((H.workspace_bytes(F) + 16,), 255, dtype=torch.uint8, device="cuda")
+    Y = swtcf.hybrid_spmm(H, torch.from_numpy(X).cuda(), workspace=ws).cpu().numpy()[:nr].astype(np.float64)
     assert column_rel(Y, want, [0]) <= REL and column_rel(Y, want, [40]) <= REL
     assert column_rel(Y, want, [j for j in range(F) if j not in (0, 40)]) <= REL
 
@@ -353,7 +432,8 @@ def test_binary_tiles_alone(gpu, oracle, G):
     assert tile.any() and (~tile).any()
     X = mixed_range_features(nc, F, 4)
     Y0 = np.random.default_rng(9).standard_normal((H.out_rows, F)).astype(np.float32)
-    Y = swtcf.hub_tiles_spmm(H, torch.from_numpy(X).cuda(), torch.from_numpy(Y0).cuda()).cpu().numpy()
+    ws = torch.full((H.workspace_bytes(F) + 16,), 255, dtype=torch.uint8, device="cuda")
+    Y = swtcf.hub_tiles_spmm(H, torch.from_numpy(X).cuda(), torch.from_numpy(Y0).cuda(), workspace=ws).cpu().numpy()
     want = scaled_product(oracle, dst[tile], src[tile], nr, X, r, c) + Y0[:nr].astype(np.float64)
     got = Y[:nr].astype(np.float64)
     assert column_rel(got, want, [0]) <= REL and column_rel(got, want, [40]) <= REL
