@@ -362,8 +362,8 @@ int tcc_hybrid_release(tcc_hybrid* H);
  * block b = data[tcOffset[b] + rank]) in split-TF32 tiles (tcc_coo_to_hybrid,
  * TCC_TILES_BF16X2, minTileNnz 16, groups of 8).  Bits in padding columns
  * (>= num_cols) or rows (>= num_rows) are ignored, as the gather ignores
- * them.  phases as tcc_coo_to_hybrid (0 = 4 when windows hold at least 64
- * blocks on average, else 1).  Synchronises `stream`; the BCSR may be freed
+ * them.  phases as tcc_coo_to_hybrid (0: when windows hold at least 64
+ * blocks on average, 2 for binary tiles and 4 for value tiles, else 1).  Synchronises `stream`; the BCSR may be freed
  * afterwards (the hybrid holds its own arrays); free with tcc_hybrid_release. */
 int tcc_hybrid_from_bcsr(const tcc_bcsr* A, int useValues, uint32_t minStepNnz, uint32_t phases, tcc_hybrid* out,
                          void* stream);

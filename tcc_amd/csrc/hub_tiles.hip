@@ -2019,7 +2019,10 @@ int tcc_hybrid_from_bcsr(const tcc_bcsr* A, int useValues, std::uint32_t minStep
                 TCC_ERR_INVALID_ARGUMENT, "invalid BCSR -> hybrid arguments (an ordinary BCSR; data for values)");
     const hipStream_t st = as_stream(stream);
     const std::uint32_t B = A->num_TCBlocks;
-    if (phases == 0) phases = A->num_rowWindows && B >= 64ull * A->num_rowWindows ? 4 : 1;
+    // long windows take a phased remainder: 2 phases behind binary tiles
+    // (config 3 step 4.76 ms against 4.99 with 4 and 4.79 with 1; the
+    // remainder holds 9.8% of the entries), 4 behind value tiles (35%)
+    if (phases == 0) phases = A->num_rowWindows && B >= 64ull * A->num_rowWindows ? (useValues ? 4 : 2) : 1;
     // block counts, their scan, then the entries
     DevBuf<char> scratch;
     const std::uint64_t Bn = std::max<std::uint32_t>(B, 1);

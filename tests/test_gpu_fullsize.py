@@ -207,7 +207,7 @@ def test_fullsize_config3_binary_hybrid(gpu, oracle):
     """The bench's path at config 3: binary hub tiles (steps of >= 40
     entries, groups of 16 row blocks) with the sym-normalised values as row
     and column scales, plus the packed gather of the remainder's pattern
-    over its 4-phase BCSR.  The reference numerics of this form are
+    over its 2-phase BCSR.  The reference numerics of this form are
     r_i sum_j P_ij TF32(fp32(c_j X_j)): the weighted checksum and the oracle
     rows are taken against them (rel-L2 <= 1e-5), and the oracle rows also
     against the TF32 CSR oracle over the values (north_star bound 1e-3).
@@ -220,7 +220,7 @@ def test_fullsize_config3_binary_hybrid(gpu, oracle):
     rs, cs = sym_norm_scales(rows_t, cols_t, n)
     rows, cols, v = r32.cpu().numpy(), c32.cpu().numpy(), vals.cpu().numpy()
     r_np, c_np = rs.cpu().numpy(), cs.cpu().numpy()
-    H = swtcf.coo_to_hybrid_scaled(r32, c32, n, n, rs, cs, min_step_nnz=40, group_blocks=16, phases=4)
+    H = swtcf.coo_to_hybrid_scaled(r32, c32, n, n, rs, cs, min_step_nnz=40, group_blocks=16, phases=2)
     t = H.view.tiles
     print(f"config 3 binary hybrid: {t.num_steps} steps, {t.nnz} tile entries, {H.rest.view.nnz} in the remainder, "
           f"{t.num_units} units ({t.num_partial_units} with partial sums)", flush=True)
