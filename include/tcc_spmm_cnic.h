@@ -248,7 +248,9 @@ int tcc_block_release(void* allocation);
  *     num_shared_groups shared groups;
  *   unitOrder[i]: the unit the SpMM launches i-th, the units sorted by the
  *     column block of their first step (stable), so that units running at
- *     the same time read the same feature rows; NULL launches them in
+ *     the same time read the same feature rows; for binary tiles first by
+ *     size, in buckets of 128 steps, the largest first (a long unit
+ *     launched last would hold the grid's tail); NULL launches them in
  *     index order (the products do not depend on it).
  * Binary tiles (TCC_TILES_BINARY, tcc_coo_to_hybrid_scaled) hold the
  * pattern of A only, with A = diag(rowScale) P diag(colScale) (the scales

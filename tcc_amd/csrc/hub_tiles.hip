@@ -421,13 +421,21 @@ __global__ void group_units_kernel(const std::uint32_t* __restrict__ groupStepOf
 }
 
 // Sort keys of the launch order: the column block of each unit's first step
-// (a unit has at least one step), the unit index as payload.
+// (a unit has at least one step), the unit index as payload.  With
+// bySize, the units come in buckets of 128 steps, the largest first, and by
+// column within a bucket: a long unit launched last would hold the grid's
+// tail (binary tiles, config 3: 4.76 -> 4.68 ms per hybrid step).
+constexpr std::uint32_t kOrderBucketSteps = 128;
+constexpr std::uint32_t kOrderBuckets = 1u << 16;
+
 __global__ void unit_order_keys_kernel(const std::uint32_t* __restrict__ units, const std::uint32_t* __restrict__ stepCol,
-                                       std::uint32_t NU, std::uint64_t* __restrict__ keys,
-                                       std::uint32_t* __restrict__ order) {
+                                       std::uint32_t NU, bool bySize, unsigned colBits,
+                                       std::uint64_t* __restrict__ keys, std::uint32_t* __restrict__ order) {
     const std::uint32_t u = blockIdx.x * blockDim.x + threadIdx.x;
     if (u >= NU) return;
-    keys[u] = stepCol[units[3ull * u + 1]];
+    const std::uint32_t first = units[3ull * u + 1], end = units[3ull * u + 2];
+    const std::uint64_t bucket = min((end - first) / kOrderBucketSteps, kOrderBuckets - 1);
+    keys[u] = (bySize ? (kOrderBuckets - 1 - bucket) << colBits : 0) | stepCol[first];
     order[u] = u;
 }
 
@@ -1853,7 +1861,8 @@ int build_hybrid(const HybridParams& P, tcc_hybrid* out, void* stream) {
             return fail(TCC_ERR_HIP);
         }
     }
-    // launch order: units by the column block of their first step (stable)
+    // launch order: units by the column block of their first step (stable);
+    // binary tiles: the largest size bucket first
     DevBuf<char> orderScratch;
     if (NU > 0) {
         const std::uint64_t tempElems = radix_temp_elems(NU);
@@ -1865,10 +1874,11 @@ int build_hybrid(const HybridParams& P, tcc_hybrid* out, void* stream) {
         auto* keys = reinterpret_cast<std::uint64_t*>(orderScratch.p);
         auto* vals = reinterpret_cast<std::uint32_t*>(orderScratch.p + align_up(16ull * NU));
         auto* sortTemp = reinterpret_cast<std::uint32_t*>(orderScratch.p + align_up(16ull * NU) + align_up(4ull * NU));
-        hipLaunchKernelGGL(unit_order_keys_kernel, dim3(grid_for(NU, kThreads)), dim3(kThreads), 0, st, oUnits, oStepCol,
-                           NU, keys, oUnitOrder);
         unsigned bits = 0;
         while (bits < 32 && (static_cast<std::uint64_t>(CB) - 1) >> bits) ++bits;
+        hipLaunchKernelGGL(unit_order_keys_kernel, dim3(grid_for(NU, kThreads)), dim3(kThreads), 0, st, oUnits, oStepCol,
+                           NU, binary, bits, keys, oUnitOrder);
+        if (binary) bits += 16;
         std::uint64_t* sortedKeys = nullptr;
         std::uint32_t* sortedOrder = nullptr;
         if (hipGetLastError() != hipSuccess ||

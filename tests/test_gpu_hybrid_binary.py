@@ -140,7 +140,10 @@ def reference_binary_layout(dst, src, nr, nc, min_step, G, unit_steps, r=None, c
             partial.append(slots if nu > 1 else 0xFFFFFFFF)
             slots += 1 if nu > 1 else 0
     units = np.array(units, np.uint32).reshape(-1, 3)
-    unit_order = np.argsort(sc[units[:, 1]] if len(units) else units[:, 1], kind="stable").astype(np.uint32)
+    # launch order: buckets of 128 sub-steps, the largest first, then the column pair of the first sub-step
+    size = units[:, 2].astype(np.int64) - units[:, 1]
+    unit_order = (np.lexsort((sc[units[:, 1]], -np.minimum(size // 128, 65535))) if len(units)
+                  else np.zeros(0, np.int64)).astype(np.uint32)
     hub_cols = min(32 * (int(sp.max()) + 1), nc) if S else 0
     d = dict(rowOrder=row_order, hubColOrder=corder[:hub_cols].astype(np.uint32), groupStepOffset=gso,
              stepCol=sc.astype(np.uint32), tileMasks=recs, units=units, unitOrder=unit_order,
