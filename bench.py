@@ -107,6 +107,9 @@ def parse(argv=None):
                    help="configs 2-3: the step is launchSWTCFSpMM (fp32 X) or launchSWTCFSpMMQuantized (int8 X "
                         "with per-row scales) over the SWTCF (S = 16) of the config's graph at the reference's "
                         "F = 128 (for counter runs of the SWTCF SpMM)")
+    p.add_argument("--no-swtcf-plans", action="store_true",
+                   help="with --swtcf-step: the SWTCF kernel on every launch (tcc_swtcf_set_plans(0)), not the "
+                        "plan later launches over one large matrix take")
     p.add_argument("--atomic-probe-mib", type=int, default=0,
                    help="time tcc_calibration_atomic over a buffer of this many MiB (rows of 128 floats, 64-float "
                         "segments at random rows: the SWTCF SpMM's output pattern) and print one JSON line")
@@ -349,6 +352,38 @@ def swtcf_timings(torch, swtcf, m, X, n, nnz, F):
     return {"F": F, "S": 16, "fp32_ms": round(fp32_ms, 4), "fp32_gflops": gf(fp32_ms),
             "int8_ms": round(q_ms, 4), "int8_gflops": gf(q_ms),
             "X_bytes_fp32": 4 * n * F, "X_bytes_int8": n * F + 4 * n}
+
+
+def swtcf_plan_timings(torch, swtcf, m, n, nnz):
+    """launchSWTCFSpMM on the config-3 graph at the reference's F = 128,
+    S = 16: the SWTCF kernel (plans off) and the kept plan (the second call
+    on the matrix builds it: the binary hybrid of the same pattern), Y += A X
+    without zeroing Y between launches, as the reference times it."""
+    L = swtcf._lib.lib()
+    F = 128
+    X = torch.randn((n, F), device="cuda", generator=torch.Generator(device="cuda").manual_seed(11))
+    Y = torch.zeros((n, F), device="cuda")
+    step = lambda: swtcf.launchSWTCFSpMM(m, X, Y, 12)
+    L.tcc_swtcf_set_plans(0)
+    kernel_ms = timed(step, 3, 1)
+    L.tcc_swtcf_set_plans(1)
+    L.tcc_swtcf_release_plans()
+    built0 = L.tcc_swtcf_plans_built()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    step()  # first sighting: the kernel
+    step()  # second: builds the plan and runs it
+    torch.cuda.synchronize()
+    first_two_ms = (time.perf_counter() - t0) * 1e3
+    assert L.tcc_swtcf_plans_built() == built0 + 1
+    plan_ms = timed(step, 20, 2)
+    L.tcc_swtcf_release_plans()
+    gf = lambda ms: round(2.0 * nnz * F / (ms * 1e-3) / 1e9, 3)
+    return {"F": F, "S": 16, "kernel_ms": round(kernel_ms, 4), "kernel_gflops": gf(kernel_ms),
+            "plan_ms": round(plan_ms, 4), "plan_gflops": gf(plan_ms),
+            "first_two_calls_ms": round(first_two_ms, 2),
+            "plan": "binary hub tiles on the sparse MFMA + gathered remainder of the matrix's pattern, built on the "
+                    "second call that finds the same arrays (device hash each call)"}
 
 
 def bench_swtcf_ab(args, torch, swtcf):
@@ -772,6 +807,8 @@ def bench_spmm(args, torch, swtcf, cfg):
         del rs32, cs32
         if args.config == 2:
             extra["swtcf"] = swtcf_timings(torch, swtcf, m, X, n, nnz, F)
+        if args.config == 3:
+            extra["swtcf"] = swtcf_plan_timings(torch, swtcf, m, n, nnz)
         del m, ws
         if args.config == 3:
             torch.cuda.empty_cache()
@@ -1033,6 +1070,8 @@ def main():
     if args.swtcf_step:
         if args.config not in (2, 3):
             raise SystemExit("--swtcf-step takes configs 2-3 (config 1's step is the SWTCF SpMM already)")
+        if args.no_swtcf_plans:
+            swtcf._lib.lib().tcc_swtcf_set_plans(0)
         print(json.dumps(bench_swtcf_step(args, torch, swtcf, cfg)), flush=True)
         return 0
     if args.config in (1, 2, 3):

@@ -122,7 +122,16 @@ int tcc_swtcf_convert(const uint32_t* dDst, const uint32_t* dSrc, uint32_t numEd
  * launchSWTCFSpMM: Y[rows x 128] += A * X[cols x 128] (row-major fp32).
  * Requires superWindowSize == 16 like the reference.  Tiles with at least
  * tcThreshold nonzeros use TF32-rounded X (the reference's tensor-core path),
- * sparser tiles use X as given (its fp32 path).  The caller zeroes Y. */
+ * sparser tiles use X as given (its fp32 path).  The caller zeroes Y.
+ * Plans (no reference counterpart, see tcc_swtcf_set_plans): on a matrix of
+ * at least 4M edges of capacity and 64 entries per row on average, with
+ * tcThreshold <= 64 and the stream not capturing a graph, the call hashes
+ * the matrix's arrays on the device and waits for the hash; from the second
+ * call that finds the same matrix on, the product runs through a kept plan
+ * (the matrix's pattern as binary hub tiles plus a gathered remainder,
+ * tcc_coo_to_hybrid_scaled) with TF32(X) for every entry, exact products
+ * and fp32 sums.  The call that builds the plan synchronises the stream
+ * and allocates the plan's device memory. */
 int tcc_swtcf_spmm(const tcc_swtcf_matrix* m, const float* X, float* Y,
                    uint32_t tcThreshold, void* stream);
 
@@ -140,6 +149,19 @@ int tcc_swtcf_spmm_f(const tcc_swtcf_matrix* m, const float* X, float* Y,
  * split (src/swtcf_spmm.cu:188-241) on this GPU. */
 int tcc_swtcf_spmm_mfma(const tcc_swtcf_matrix* m, const float* X, float* Y, uint32_t featureDim,
                         uint32_t tcThreshold, uint32_t mfmaThreshold, void* stream);
+
+/* Plans for repeated products over one matrix (tcc_swtcf_spmm and
+ * tcc_swtcf_spmm_f; no reference counterpart).  At most maxPlans plans are
+ * kept, the least recently used released first; 0 turns plans off.  The
+ * default is 1, or the value of the environment variable TCC_SWTCF_PLANS
+ * read at the first SpMM.  A plan holds the hybrid of its matrix (about
+ * 0.5 GB at 233k rows and 114M edges) and a workspace for the last feature
+ * width. */
+int tcc_swtcf_set_plans(uint32_t maxPlans);
+/* Releases every kept plan. */
+int tcc_swtcf_release_plans(void);
+/* Plans built since the process started. */
+uint32_t tcc_swtcf_plans_built(void);
 
 /* launchSWTCFSpMMQuantized: X[src][f] = q[srcGlobal[src]*128+f] * scales[srcGlobal[src]]
  * (src/swtcf_spmm.cu:317-323), otherwise as tcc_swtcf_spmm. */

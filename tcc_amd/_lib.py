@@ -94,6 +94,9 @@ SIGNATURES = {
     "tcc_swtcf_spmm_f": (ctypes.c_int, [ctypes.POINTER(SWTCFMatrix), vp, vp, u32, u32, vp]),
     "tcc_swtcf_spmm_mfma": (ctypes.c_int, [ctypes.POINTER(SWTCFMatrix), vp, vp, u32, u32, u32, vp]),
     "tcc_swtcf_spmm_quantized": (ctypes.c_int, [ctypes.POINTER(SWTCFMatrix), vp, vp, vp, vp, u32, vp]),
+    "tcc_swtcf_set_plans": (ctypes.c_int, [u32]),
+    "tcc_swtcf_release_plans": (ctypes.c_int, []),
+    "tcc_swtcf_plans_built": (u32, []),
     "tcc_bcsr_spmm": (ctypes.c_int, [ctypes.POINTER(BCSR), vp, vp, u32, ctypes.c_int, vp]),
     "tcc_bcsr_spmm_mixed": (ctypes.c_int, [ctypes.POINTER(BCSR), ctypes.POINTER(FeatureSource), vp, u32,
                                            ctypes.c_int, vp]),

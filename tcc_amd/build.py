@@ -22,8 +22,8 @@ BUILD = os.path.join(ROOT, "_build", "tcc_amd")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("TCC_OFFLOAD_ARCH", "gfx950")
 
-LIB_SOURCES = ["swtcf_convert.hip", "swtcf_spmm.hip", "bcsr_spmm.hip", "bcsr_build.hip", "hub_tiles.hip",
-               "dense_tn.hip",
+LIB_SOURCES = ["swtcf_convert.hip", "swtcf_spmm.hip", "swtcf_plan.hip", "bcsr_spmm.hip", "bcsr_build.hip",
+               "hub_tiles.hip", "dense_tn.hip",
                "errors.cpp"]
 LIB_NAME = "libtcc_swtcf.so"
 

@@ -1,0 +1,383 @@
+// Plans for repeated SWTCF SpMMs over one matrix (no reference counterpart;
+// the product is launchSWTCFSpMM's, src/swtcf_spmm.cu:437-466).
+//
+// The SWTCF SpMM adds every tile row's partial sums into Y with atomics: at
+// 233k rows and 114M edges (F = 128) that is 815.9M 64-byte atomic requests,
+// at 0.86 of the rate a probe reaches, 46.6 ms.  A caller that multiplies
+// by the same matrix again and again (the reference's own timing loop,
+// src/swtcf_spmm_main.cu:203-247; a training loop) can be served by the
+// binary hybrid of the same pattern instead (hub_tiles.hip: degree-ordered
+// binary tiles on the sparse MFMA plus a gather of the rest), which writes
+// each output row once per phase.
+//
+// Every call of tcc_swtcf_spmm / tcc_swtcf_spmm_f on a large, dense enough
+// matrix (at least kPlanMinEdges edges of capacity and 64 entries per row
+// on average) hashes the arrays that define the product (colWindowOffset,
+// superWindowRowOffset, tileLocalBit, tileRowSlot, superWindowRows at their
+// valid extents) on the device and reads the hash back.  The second call
+// that finds the same hash and dimensions decodes the matrix into a COO,
+// builds the hybrid and keeps it; that call and the later ones run the
+// hybrid.  A matrix changed in place hashes differently and is multiplied
+// afresh.  Plans need tcThreshold <= 64: the hybrid multiplies TF32(X)
+// everywhere, where the reference uses X as given for tiles below the
+// threshold (tcThreshold > 64 asks for the fp32 path throughout).
+#include <algorithm>
+#include <cstdlib>
+#include <mutex>
+#include <vector>
+
+#include "../../include/tcc_spmm_cnic.h"
+#include "../../include/tcc_swtcf.h"
+#include "common.hpp"
+#include "primitives.hpp"
+
+namespace tcc {
+namespace {
+
+constexpr unsigned kThreads = 256;
+constexpr std::uint64_t kPlanMinEdges = 4u << 20;
+constexpr std::uint32_t kPlanMinRowDegree = 64;
+constexpr unsigned kHashBlocks = 2048;
+
+// splitmix64's finalizer (Vigna): a bijective mix of 64 bits
+__device__ __forceinline__ std::uint64_t mix64(std::uint64_t x) {
+    x ^= x >> 30;
+    x *= 0xBF58476D1CE4E5B9ull;
+    x ^= x >> 27;
+    x *= 0x94D049BB133111EBull;
+    x ^= x >> 31;
+    return x;
+}
+
+// out[0], out[1]: two sums of mixed (array, index, value) over the arrays
+// that define the product; out[2] = tiles, out[3] = super-window rows.
+// Sums do not depend on the order in which the threads add them.
+__global__ void __launch_bounds__(kThreads) swtcf_hash_kernel(tcc_swtcf_matrix m, std::uint64_t* __restrict__ out) {
+    const std::uint64_t CW1 = m.numColWindows + 1ull, SW1 = m.numSuperWindows + 1ull;
+    const std::uint64_t T = m.colWindowOffset[m.numColWindows], U = m.superWindowRowOffset[m.numSuperWindows];
+    const std::uint64_t b1 = CW1, b2 = b1 + SW1, b3 = b2 + T, b4 = b3 + 8 * T, N = b4 + U;
+    std::uint64_t s0 = 0, s1 = 0;
+    for (std::uint64_t i = static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < N;
+         i += static_cast<std::uint64_t>(gridDim.x) * blockDim.x) {
+        std::uint64_t v, id;
+        if (i < b1) {
+            v = m.colWindowOffset[i];
+            id = 1;
+        } else if (i < b2) {
+            v = m.superWindowRowOffset[i - b1];
+            id = 2;
+        } else if (i < b3) {
+            v = m.tileLocalBit[i - b2];
+            id = 3;
+        } else if (i < b4) {
+            v = m.tileRowSlot[i - b3];
+            id = 4;
+        } else {
+            v = m.superWindowRows[i - b4];
+            id = 5;
+        }
+        s0 += mix64(v ^ mix64(i ^ (id << 58)));
+        s1 += mix64(v + 0x9E3779B97F4A7C15ull * (i + 1) + (id << 40));
+    }
+    __shared__ std::uint64_t r0[kThreads / kWave], r1[kThreads / kWave];
+#pragma unroll
+    for (int d = kWave / 2; d > 0; d >>= 1) {
+        s0 += __shfl_xor(s0, d, kWave);
+        s1 += __shfl_xor(s1, d, kWave);
+    }
+    if (__lane_id() == 0) {
+        r0[threadIdx.x / kWave] = s0;
+        r1[threadIdx.x / kWave] = s1;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (unsigned w = 1; w < kThreads / kWave; ++w) {
+            s0 += r0[w];
+            s1 += r1[w];
+        }
+        atomicAdd(reinterpret_cast<unsigned long long*>(&out[0]), static_cast<unsigned long long>(s0));
+        atomicAdd(reinterpret_cast<unsigned long long*>(&out[1]), static_cast<unsigned long long>(s1));
+        if (blockIdx.x == 0) {
+            out[2] = T;
+            out[3] = U;
+        }
+    }
+}
+
+__global__ void swtcf_tile_counts_kernel(const std::uint64_t* __restrict__ bits, std::uint32_t T,
+                                         std::uint32_t* __restrict__ counts) {
+    const std::uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t < T) counts[t] = static_cast<std::uint32_t>(__popcll(bits[t]));
+}
+
+// The COO of the matrix: tile t of column window w (the last w with
+// colWindowOffset[w] <= t) holds bit 8r + c for the edge (row
+// superWindowRows[superWindowRowOffset[w / S] + tileRowSlot[8t + r]],
+// column 8w + c).  Bits of padding rows or past the matrix (a converted
+// matrix has none) are counted in `dropped`; the matrix then gets no plan.
+__global__ void swtcf_decode_kernel(tcc_swtcf_matrix m, std::uint32_t T, const std::uint32_t* __restrict__ offset,
+                                    std::uint32_t* __restrict__ dst, std::uint32_t* __restrict__ src,
+                                    std::uint32_t* __restrict__ dropped) {
+    const std::uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= T) return;
+    std::uint32_t lo = 0, hi = m.numColWindows;  // colWindowOffset[lo] <= t < colWindowOffset[hi]
+    while (hi - lo > 1) {
+        const std::uint32_t mid = lo + (hi - lo) / 2;
+        if (m.colWindowOffset[mid] <= t) lo = mid;
+        else hi = mid;
+    }
+    const std::uint32_t w = lo, base = m.superWindowRowOffset[w / m.superWindowSize];
+    const std::uint32_t rowsU = m.superWindowRowOffset[m.numSuperWindows];
+    std::uint64_t b = m.tileLocalBit[t];
+    std::uint32_t k = offset[t], bad = 0;
+    while (b) {
+        const unsigned i = static_cast<unsigned>(__builtin_ctzll(b));
+        b &= b - 1;
+        const std::uint32_t slot = m.tileRowSlot[8ull * t + i / 8];
+        const std::uint32_t col = 8 * w + i % 8;
+        const std::uint32_t row = slot < rowsU - base ? m.superWindowRows[base + slot] : 0xFFFFFFFFu;
+        if (row < m.rows && col < m.cols) {
+            dst[k] = row;
+            src[k] = col;
+        } else {
+            dst[k] = 0;
+            src[k] = 0;
+            ++bad;
+        }
+        ++k;
+    }
+    if (bad) atomicAdd(dropped, bad);
+}
+
+struct Plan {
+    int device = -1;
+    std::uint32_t rows = 0, cols = 0, S = 0, CW = 0, SW = 0;
+    std::uint64_t h0 = 0, h1 = 0, T = 0, U = 0;
+    std::uint64_t lastUse = 0;
+    bool built = false;
+    bool unplannable = false;  // bits outside the rows or columns: always the SWTCF kernel
+    tcc_hybrid H{};
+    void* ws = nullptr;
+    std::size_t wsBytes = 0;
+    std::uint32_t wsF = 0;
+
+    void release() {
+        if (built) tcc_hybrid_release(&H);
+        if (ws) (void)hipFree(ws);
+        built = false;
+        ws = nullptr;
+        wsBytes = 0;
+        wsF = 0;
+    }
+};
+
+struct PlanCache {
+    std::mutex mu;
+    bool init = false;
+    std::uint32_t maxPlans = 1;
+    std::uint64_t clock = 0;
+    std::uint32_t builtCount = 0;
+    std::vector<Plan> plans;                 // seen matrices, built or not
+    std::vector<std::pair<int, std::uint64_t*>> hashBuf;  // per device: 4 u64
+
+    void configure() {
+        if (init) return;
+        init = true;
+        if (const char* e = std::getenv("TCC_SWTCF_PLANS")) maxPlans = static_cast<std::uint32_t>(std::strtoul(e, nullptr, 10));
+    }
+    std::uint64_t* buffer(int device) {
+        for (auto& b : hashBuf)
+            if (b.first == device) return b.second;
+        std::uint64_t* p = nullptr;
+        if (hipMalloc(&p, 4 * sizeof(std::uint64_t)) != hipSuccess) return nullptr;
+        hashBuf.emplace_back(device, p);
+        return p;
+    }
+    // keep at most maxPlans built plans and 2 maxPlans + 2 entries, dropping the least recently used
+    void trim() {
+        auto lru = [&](bool builtOnly) {
+            std::size_t best = plans.size();
+            for (std::size_t i = 0; i < plans.size(); ++i)
+                if ((!builtOnly || plans[i].built) && (best == plans.size() || plans[i].lastUse < plans[best].lastUse))
+                    best = i;
+            return best;
+        };
+        for (;;) {
+            std::uint32_t built = 0;
+            for (auto& p : plans) built += p.built ? 1 : 0;
+            if (built <= maxPlans) break;
+            const std::size_t i = lru(true);
+            plans[i].release();
+        }
+        while (plans.size() > 2ull * maxPlans + 2) {
+            const std::size_t i = lru(false);
+            plans[i].release();
+            plans.erase(plans.begin() + static_cast<std::ptrdiff_t>(i));
+        }
+    }
+};
+
+PlanCache& cache() {
+    static PlanCache c;
+    return c;
+}
+
+// The hybrid of the matrix's pattern (binary tiles, no scales).  Two column
+// phases for the remainder: a phased remainder adds only the rows it
+// touches, so Y needs no rows past m.rows.  A matrix with bits outside its
+// rows or columns (the SWTCF kernel skips them) is marked unplannable.
+int build_plan(const tcc_swtcf_matrix* m, Plan& P, hipStream_t st) {
+    const std::uint32_t T = static_cast<std::uint32_t>(P.T);
+    struct Bufs {
+        void* p = nullptr;
+        ~Bufs() {
+            if (p) (void)hipFree(p);
+        }
+    } scratch;
+    const std::uint64_t Tn = std::max<std::uint64_t>(T, 1);
+    const std::size_t a = (4 * (Tn + 1) + 255) / 256 * 256;
+    const std::size_t tempBytes = (4 * scan_temp_elems(Tn + 1) + 255) / 256 * 256;
+    TCC_HIP_CHECK(hipMalloc(&scratch.p, 2 * a + tempBytes + 256));
+    auto* counts = static_cast<std::uint32_t*>(scratch.p);
+    auto* offset = reinterpret_cast<std::uint32_t*>(static_cast<char*>(scratch.p) + a);
+    auto* temp = reinterpret_cast<std::uint32_t*>(static_cast<char*>(scratch.p) + 2 * a);
+    auto* small = reinterpret_cast<std::uint32_t*>(static_cast<char*>(scratch.p) + 2 * a + tempBytes);
+    TCC_HIP_CHECK(fill<std::uint32_t>(small, 4, 0u, st));
+    if (T > 0) {
+        hipLaunchKernelGGL(swtcf_tile_counts_kernel, dim3(grid_for(T, kThreads)), dim3(kThreads), 0, st, m->tileLocalBit,
+                           T, counts);
+        TCC_LAUNCH_CHECK();
+    }
+    TCC_HIP_CHECK(exclusive_scan(counts, offset, T, small, temp, st));
+    std::uint32_t nnz = 0;
+    TCC_HIP_CHECK(hipMemcpyAsync(&nnz, small, 4, hipMemcpyDeviceToHost, st));
+    TCC_HIP_CHECK(hipStreamSynchronize(st));
+    Bufs coo;
+    const std::uint64_t En = std::max<std::uint32_t>(nnz, 1);
+    TCC_HIP_CHECK(hipMalloc(&coo.p, 8 * En));
+    auto* dst = static_cast<std::uint32_t*>(coo.p);
+    auto* src = dst + En;
+    if (T > 0) {
+        hipLaunchKernelGGL(swtcf_decode_kernel, dim3(grid_for(T, kThreads)), dim3(kThreads), 0, st, *m, T, offset, dst,
+                           src, small + 1);
+        TCC_LAUNCH_CHECK();
+    }
+    std::uint32_t dropped = 0;
+    TCC_HIP_CHECK(hipMemcpyAsync(&dropped, small + 1, 4, hipMemcpyDeviceToHost, st));
+    TCC_HIP_CHECK(hipStreamSynchronize(st));
+    if (dropped) {
+        P.unplannable = true;
+        return TCC_OK;
+    }
+    const int rc = tcc_coo_to_hybrid_scaled(dst, src, nnz, m->rows, m->cols, nullptr, nullptr, 0, 0, 0, 2, &P.H, st);
+    if (rc) return rc;
+    P.built = true;
+    return TCC_OK;
+}
+
+}  // namespace
+
+// Runs the SpMM through a plan when one applies; *used = false leaves it to
+// the SWTCF kernel.
+int swtcf_plan_spmm(const tcc_swtcf_matrix* m, const float* X, float* Y, std::uint32_t F, std::uint32_t tc,
+                    void* stream, bool* used) {
+    *used = false;
+    PlanCache& C = cache();
+    std::lock_guard<std::mutex> lock(C.mu);
+    C.configure();
+    if (C.maxPlans == 0 || tc > 64 || m->nnz < kPlanMinEdges || m->rows == 0 ||
+        static_cast<std::uint64_t>(m->nnz) < static_cast<std::uint64_t>(kPlanMinRowDegree) * m->rows)
+        return TCC_OK;
+    const hipStream_t st = as_stream(stream);
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return TCC_OK;
+    int device = 0;
+    TCC_HIP_CHECK(hipGetDevice(&device));
+    std::uint64_t* hb = C.buffer(device);
+    TCC_REQUIRE(hb, TCC_ERR_NO_MEMORY, "out of device memory for the SWTCF plan hash");
+    TCC_HIP_CHECK(fill<std::uint64_t>(hb, 4, 0ull, st));
+    hipLaunchKernelGGL(swtcf_hash_kernel, dim3(kHashBlocks), dim3(kThreads), 0, st, *m, hb);
+    TCC_LAUNCH_CHECK();
+    std::uint64_t h[4] = {};
+    TCC_HIP_CHECK(hipMemcpyAsync(h, hb, sizeof(h), hipMemcpyDeviceToHost, st));
+    TCC_HIP_CHECK(hipStreamSynchronize(st));
+    Plan* P = nullptr;
+    for (auto& p : C.plans)
+        if (p.device == device && p.rows == m->rows && p.cols == m->cols && p.S == m->superWindowSize &&
+            p.CW == m->numColWindows && p.SW == m->numSuperWindows && p.h0 == h[0] && p.h1 == h[1] && p.T == h[2] &&
+            p.U == h[3])
+            P = &p;
+    ++C.clock;
+    if (!P) {
+        // first sighting: remember it, multiply with the SWTCF kernel
+        Plan q;
+        q.device = device;
+        q.rows = m->rows;
+        q.cols = m->cols;
+        q.S = m->superWindowSize;
+        q.CW = m->numColWindows;
+        q.SW = m->numSuperWindows;
+        q.h0 = h[0];
+        q.h1 = h[1];
+        q.T = h[2];
+        q.U = h[3];
+        q.lastUse = C.clock;
+        C.plans.push_back(q);
+        C.trim();
+        return TCC_OK;
+    }
+    P->lastUse = C.clock;
+    if (P->unplannable) return TCC_OK;
+    if (!P->built) {
+        const int rc = build_plan(m, *P, st);
+        if (rc) return rc;
+        if (!P->built) return TCC_OK;
+        ++C.builtCount;
+    }
+    if (P->wsF != F) {
+        if (P->ws) (void)hipFree(P->ws);
+        P->ws = nullptr;
+        P->wsF = 0;
+        P->wsBytes = tcc_hybrid_workspace_bytes(&P->H, F) + 16;
+        TCC_HIP_CHECK(hipMalloc(&P->ws, P->wsBytes));
+        P->wsF = F;
+    }
+    const int rc = tcc_hybrid_spmm(&P->H, X, Y, F, 1, P->ws, P->wsBytes, stream);
+    if (rc) return rc;
+    *used = true;
+    C.trim();  // after the last use of P: trimming may move the entries
+    return TCC_OK;
+}
+
+}  // namespace tcc
+
+using namespace tcc;
+
+extern "C" {
+
+int tcc_swtcf_set_plans(std::uint32_t maxPlans) {
+    clear_last_error();
+    PlanCache& C = cache();
+    std::lock_guard<std::mutex> lock(C.mu);
+    C.init = true;
+    C.maxPlans = maxPlans;
+    C.trim();
+    return TCC_OK;
+}
+
+int tcc_swtcf_release_plans(void) {
+    clear_last_error();
+    PlanCache& C = cache();
+    std::lock_guard<std::mutex> lock(C.mu);
+    for (auto& p : C.plans) p.release();
+    C.plans.clear();
+    return TCC_OK;
+}
+
+uint32_t tcc_swtcf_plans_built(void) {
+    PlanCache& C = cache();
+    std::lock_guard<std::mutex> lock(C.mu);
+    return C.builtCount;
+}
+
+}  // extern "C"

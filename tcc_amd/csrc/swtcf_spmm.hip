@@ -26,6 +26,12 @@
 #include "common.hpp"
 
 namespace tcc {
+
+// swtcf_plan.hip: runs the product through a kept plan (the binary hybrid of
+// the same pattern) when one applies, setting *used.
+int swtcf_plan_spmm(const tcc_swtcf_matrix* m, const float* X, float* Y, std::uint32_t F, std::uint32_t tc,
+                    void* stream, bool* used);
+
 namespace {
 
 constexpr unsigned kThreads = 1024;
@@ -336,6 +342,9 @@ int tcc_swtcf_spmm_f(const tcc_swtcf_matrix* m, const float* X, float* Y, std::u
     TCC_REQUIRE(featureDim >= 1 && m->numSuperWindows >= 1 && m->superWindowSize >= 1 &&
                     m->superWindowSize <= TCC_SWTCF_MAX_SUPER_WINDOW_SIZE,
                 TCC_ERR_INVALID_ARGUMENT, "invalid SWTCF SpMM arguments");
+    bool planned = false;
+    const int rc = swtcf_plan_spmm(m, X, Y, featureDim, tcThreshold, stream, &planned);
+    if (rc || planned) return rc;
     return launch<false>(m, X, nullptr, nullptr, nullptr, Y, featureDim, tcThreshold, stream);
 }
 
@@ -356,6 +365,9 @@ int tcc_swtcf_spmm(const tcc_swtcf_matrix* m, const float* X, float* Y, std::uin
     TCC_REQUIRE(m && X && Y, TCC_ERR_INVALID_ARGUMENT, "null argument");
     // launchSWTCFSpMM (:444-446)
     TCC_REQUIRE(m->superWindowSize == 16, TCC_ERR_UNSUPPORTED, "SWTCF SpMM V1 requires superWindowSize=16");
+    bool planned = false;
+    const int rc = swtcf_plan_spmm(m, X, Y, TCC_SWTCF_FEATURE_DIM, tcThreshold, stream, &planned);
+    if (rc || planned) return rc;
     return launch<false>(m, X, nullptr, nullptr, nullptr, Y, TCC_SWTCF_FEATURE_DIM, tcThreshold, stream);
 }
 

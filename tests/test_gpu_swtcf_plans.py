@@ -1,0 +1,129 @@
+"""Plans for repeated SWTCF SpMMs (tcc_swtcf_set_plans; launchSWTCFSpMM's
+product, src/swtcf_spmm.cu:437-466, through the binary hybrid of the same
+pattern).
+
+Checked through the C-ABI, on an R-MAT matrix above the plan gate (4M edges
+of capacity, 64 entries per row on average):
+- the first call on a matrix runs the SWTCF kernel; the second builds the
+  plan and runs it; the third reuses it (tcc_swtcf_plans_built counts);
+- the planned products against the fp64 CSR oracle over TF32(X) at rel-L2
+  <= 1e-5 (every entry multiplies TF32(X) exactly, sums in fp32), and
+  against the kernel's product (TF32 only for tiles of >= tcThreshold
+  entries) at the north star's 1e-3; Y += AX adds into what Y holds;
+- a matrix converted again in place from another COO hashes differently:
+  its first call is the kernel's again, and correct;
+- tcThreshold 65 (the reference's pure fp32 path) and tcc_swtcf_set_plans(0)
+  never plan;
+- another feature width (tcc_swtcf_spmm_f, F = 72) reuses the plan with a
+  workspace of its own size.
+"""
+import numpy as np
+import pytest
+import torch
+
+from test_gpu_hybrid import oracle_product, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def rmat_coo(n, nnz, seed):
+    from tcc_amd.graphs import rmat_graph
+
+    rows, cols = rmat_graph(n, nnz, seed, device="cuda")
+    return rows.to(torch.int32).contiguous(), cols.to(torch.int32).contiguous()
+
+
+def convert(swtcf, m, ws, r32, c32):
+    swtcf.convertCOOToSWTCF(r32, c32, r32.numel(), m, ws)
+    assert ws.device_error() == 0
+
+
+@pytest.fixture
+def plans():
+    from tcc_amd import _lib
+
+    L = _lib.lib()
+    L.tcc_swtcf_release_plans()
+    L.tcc_swtcf_set_plans(1)
+    yield L
+    L.tcc_swtcf_release_plans()
+    L.tcc_swtcf_set_plans(1)
+
+
+def test_plan_built_on_second_call(gpu, oracle, plans):
+    from tcc_amd import swtcf
+
+    n, E, F = 40000, 4_400_000, 128
+    r32, c32 = rmat_coo(n, E, 11)
+    m = swtcf.DeviceSWTCFMatrix(n, n, E, 16)
+    ws = swtcf.SWTCFConvertWorkspace(E, n, 16)
+    convert(swtcf, m, ws, r32, c32)
+    dst, src = r32.cpu().numpy().view(np.uint32), c32.cpu().numpy().view(np.uint32)
+    X = np.random.default_rng(2).standard_normal((n, F)).astype(np.float32)
+    Xd = torch.from_numpy(X).cuda()
+    want = oracle_product(oracle, dst, src, None, n, X)  # fp64 over TF32(X)
+    b0 = plans.tcc_swtcf_plans_built()
+    Y1 = torch.zeros((n, F), device="cuda")
+    swtcf.launchSWTCFSpMM(m, Xd, Y1)
+    torch.cuda.synchronize()
+    assert plans.tcc_swtcf_plans_built() == b0, "the first call must run the SWTCF kernel"
+    Y2 = torch.zeros((n, F), device="cuda")
+    swtcf.launchSWTCFSpMM(m, Xd, Y2)
+    torch.cuda.synchronize()
+    assert plans.tcc_swtcf_plans_built() == b0 + 1, "the second call must build the plan"
+    Y0 = np.random.default_rng(3).standard_normal((n, F)).astype(np.float32)
+    Y3 = torch.from_numpy(Y0).cuda()
+    swtcf.launchSWTCFSpMM(m, Xd, Y3)  # Y += AX through the kept plan
+    torch.cuda.synchronize()
+    assert plans.tcc_swtcf_plans_built() == b0 + 1
+    y1, y2, y3 = Y1.cpu().numpy(), Y2.cpu().numpy(), Y3.cpu().numpy()
+    e2, e3 = rel_l2(y2, want), rel_l2(y3 - Y0, want)
+    e1 = rel_l2(y1, y2)
+    print(f"plans: kernel vs plan {e1:.2e}, plan vs TF32 oracle {e2:.2e}, accumulate {e3:.2e}", flush=True)
+    assert e2 <= 1e-5 and e3 <= 1e-5 and e1 <= 1e-3
+    # another feature width through tcc_swtcf_spmm_f: the same plan, a workspace of its size
+    F2 = 72
+    X2 = np.ascontiguousarray(X[:, :F2])
+    Y4 = torch.zeros((n, F2), device="cuda")
+    swtcf.swtcf_spmm(m, torch.from_numpy(X2).cuda(), Y4)
+    torch.cuda.synchronize()
+    assert plans.tcc_swtcf_plans_built() == b0 + 1
+    assert rel_l2(Y4.cpu().numpy(), want[:, :F2]) <= 1e-5
+    # the pure fp32 path (tcThreshold > 64) never plans
+    Y5 = torch.zeros((n, F), device="cuda")
+    swtcf.launchSWTCFSpMM(m, Xd, Y5, 65)
+    torch.cuda.synchronize()
+    assert rel_l2(Y5.cpu().numpy(), y1) <= 1e-3 and rel_l2(Y5.cpu().numpy(), want) <= 1e-3
+    # the same arrays converted from another COO: a new hash, the kernel's product first
+    r32b, c32b = rmat_coo(n, E, 12)
+    convert(swtcf, m, ws, r32b, c32b)
+    dstb, srcb = r32b.cpu().numpy().view(np.uint32), c32b.cpu().numpy().view(np.uint32)
+    Y6 = torch.zeros((n, F), device="cuda")
+    swtcf.launchSWTCFSpMM(m, Xd, Y6)
+    torch.cuda.synchronize()
+    assert plans.tcc_swtcf_plans_built() == b0 + 1
+    assert rel_l2(Y6.cpu().numpy(), oracle_product(oracle, dstb, srcb, None, n, X)) <= 1e-3
+    m.free()
+    ws.free()
+
+
+def test_plans_off(gpu, oracle, plans):
+    from tcc_amd import swtcf
+
+    plans.tcc_swtcf_set_plans(0)
+    n, E, F = 30000, 4_300_000, 64
+    r32, c32 = rmat_coo(n, E, 13)
+    m = swtcf.DeviceSWTCFMatrix(n, n, E, 16)
+    ws = swtcf.SWTCFConvertWorkspace(E, n, 16)
+    convert(swtcf, m, ws, r32, c32)
+    X = torch.randn((n, F), device="cuda")
+    b0 = plans.tcc_swtcf_plans_built()
+    for _ in range(3):
+        Y = torch.zeros((n, F), device="cuda")
+        swtcf.swtcf_spmm(m, X, Y)
+    torch.cuda.synchronize()
+    assert plans.tcc_swtcf_plans_built() == b0
+    dst, src = r32.cpu().numpy().view(np.uint32), c32.cpu().numpy().view(np.uint32)
+    assert rel_l2(Y.cpu().numpy(), oracle_product(oracle, dst, src, None, n, X.cpu().numpy())) <= 1e-3
+    m.free()
+    ws.free()
