@@ -14,7 +14,8 @@
 // matrix (at least kPlanMinEdges edges of capacity and 64 entries per row
 // on average) hashes the arrays that define the product (colWindowOffset,
 // superWindowRowOffset, tileLocalBit, tileRowSlot, superWindowRows at their
-// valid extents) on the device and reads the hash back.  The second call
+// valid extents; two order-independent sums of mixed words) on the device
+// and reads the hash back.  The second call
 // that finds the same hash and dimensions decodes the matrix into a COO,
 // builds the hybrid and keeps it; that call and the later ones run the
 // hybrid.  A matrix changed in place hashes differently and is multiplied
@@ -39,46 +40,54 @@ constexpr std::uint64_t kPlanMinEdges = 4u << 20;
 constexpr std::uint32_t kPlanMinRowDegree = 64;
 constexpr unsigned kHashBlocks = 2048;
 
-// splitmix64's finalizer (Vigna): a bijective mix of 64 bits
-__device__ __forceinline__ std::uint64_t mix64(std::uint64_t x) {
-    x ^= x >> 30;
-    x *= 0xBF58476D1CE4E5B9ull;
-    x ^= x >> 27;
-    x *= 0x94D049BB133111EBull;
-    x ^= x >> 31;
-    return x;
+// MurmurHash3's 32-bit finalizer (Appleby): a bijective mix of 32 bits
+__device__ __forceinline__ std::uint32_t fmix32(std::uint32_t h) {
+    h ^= h >> 16;
+    h *= 0x85EBCA6Bu;
+    h ^= h >> 13;
+    h *= 0xC2B2AE35u;
+    h ^= h >> 16;
+    return h;
 }
 
-// out[0], out[1]: two sums of mixed (array, index, value) over the arrays
-// that define the product; out[2] = tiles, out[3] = super-window rows.
-// Sums do not depend on the order in which the threads add them.
-__global__ void __launch_bounds__(kThreads) swtcf_hash_kernel(tcc_swtcf_matrix m, std::uint64_t* __restrict__ out) {
-    const std::uint64_t CW1 = m.numColWindows + 1ull, SW1 = m.numSuperWindows + 1ull;
-    const std::uint64_t T = m.colWindowOffset[m.numColWindows], U = m.superWindowRowOffset[m.numSuperWindows];
-    const std::uint64_t b1 = CW1, b2 = b1 + SW1, b3 = b2 + T, b4 = b3 + 8 * T, N = b4 + U;
-    std::uint64_t s0 = 0, s1 = 0;
-    for (std::uint64_t i = static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < N;
-         i += static_cast<std::uint64_t>(gridDim.x) * blockDim.x) {
-        std::uint64_t v, id;
-        if (i < b1) {
-            v = m.colWindowOffset[i];
-            id = 1;
-        } else if (i < b2) {
-            v = m.superWindowRowOffset[i - b1];
-            id = 2;
-        } else if (i < b3) {
-            v = m.tileLocalBit[i - b2];
-            id = 3;
-        } else if (i < b4) {
-            v = m.tileRowSlot[i - b3];
-            id = 4;
-        } else {
-            v = m.superWindowRows[i - b4];
-            id = 5;
-        }
-        s0 += mix64(v ^ mix64(i ^ (id << 58)));
-        s1 += mix64(v + 0x9E3779B97F4A7C15ull * (i + 1) + (id << 40));
+// Word j of array `salt`, mixed two ways into the two sums.
+__device__ __forceinline__ void hash_word(std::uint32_t w, std::uint64_t j, std::uint32_t salt, std::uint64_t& s0,
+                                          std::uint64_t& s1) {
+    const std::uint32_t k = static_cast<std::uint32_t>(j) ^ (static_cast<std::uint32_t>(j >> 32) * 0x27D4EB2Fu);
+    const std::uint32_t a = fmix32(w + k * 0x9E3779B9u + salt);
+    s0 += a;
+    s1 += fmix32(a ^ (k + 0x5BD1E995u * salt));
+}
+
+// The words of one array, 16 bytes a thread when the array is 16-byte
+// aligned (as tcc_swtcf_alloc_matrix carves them), else one word a thread.
+__device__ __forceinline__ void hash_array(const std::uint32_t* p, std::uint64_t words, std::uint32_t salt,
+                                           std::uint64_t& s0, std::uint64_t& s1) {
+    const std::uint64_t stride = static_cast<std::uint64_t>(gridDim.x) * blockDim.x;
+    const std::uint64_t quads = (reinterpret_cast<std::uintptr_t>(p) & 15u) == 0 ? words / 4 : 0;
+    for (std::uint64_t q = static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; q < quads; q += stride) {
+        const vu4 v = load_global<vu4>(p + 4 * q);
+        hash_word(v.x, 4 * q, salt, s0, s1);
+        hash_word(v.y, 4 * q + 1, salt, s0, s1);
+        hash_word(v.z, 4 * q + 2, salt, s0, s1);
+        hash_word(v.w, 4 * q + 3, salt, s0, s1);
     }
+    for (std::uint64_t j = 4 * quads + static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; j < words;
+         j += stride)
+        hash_word(p[j], j, salt, s0, s1);
+}
+
+// out[0], out[1]: two sums of mixed (array, index, word) over the arrays
+// that define the product; out[2] = tiles, out[3] = super-window rows.
+// The sums do not depend on the order in which the threads add them.
+__global__ void __launch_bounds__(kThreads) swtcf_hash_kernel(tcc_swtcf_matrix m, std::uint64_t* __restrict__ out) {
+    const std::uint64_t T = m.colWindowOffset[m.numColWindows], U = m.superWindowRowOffset[m.numSuperWindows];
+    std::uint64_t s0 = 0, s1 = 0;
+    hash_array(m.colWindowOffset, m.numColWindows + 1ull, 1, s0, s1);
+    hash_array(m.superWindowRowOffset, m.numSuperWindows + 1ull, 2, s0, s1);
+    hash_array(reinterpret_cast<const std::uint32_t*>(m.tileLocalBit), 2 * T, 3, s0, s1);
+    hash_array(m.tileRowSlot, 8 * T, 4, s0, s1);
+    hash_array(m.superWindowRows, U, 5, s0, s1);
     __shared__ std::uint64_t r0[kThreads / kWave], r1[kThreads / kWave];
 #pragma unroll
     for (int d = kWave / 2; d > 0; d >>= 1) {
