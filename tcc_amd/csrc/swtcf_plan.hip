@@ -338,9 +338,15 @@ int swtcf_plan_spmm(const tcc_swtcf_matrix* m, const float* X, float* Y, std::ui
     P->lastUse = C.clock;
     if (P->unplannable) return TCC_OK;
     if (!P->built) {
-        const int rc = build_plan(m, *P, st);
-        if (rc) return rc;
-        if (!P->built) return TCC_OK;
+        // a plan that cannot be built (device memory, an odd matrix) leaves
+        // the product to the SWTCF kernel, now and on later calls
+        if (build_plan(m, *P, st) != TCC_OK || !P->built) {
+            P->release();
+            P->unplannable = true;
+            clear_last_error();
+            (void)hipGetLastError();
+            return TCC_OK;
+        }
         ++C.builtCount;
     }
     if (P->wsF != F) {
@@ -348,7 +354,12 @@ int swtcf_plan_spmm(const tcc_swtcf_matrix* m, const float* X, float* Y, std::ui
         P->ws = nullptr;
         P->wsF = 0;
         P->wsBytes = tcc_hybrid_workspace_bytes(&P->H, F) + 16;
-        TCC_HIP_CHECK(hipMalloc(&P->ws, P->wsBytes));
+        if (hipMalloc(&P->ws, P->wsBytes) != hipSuccess) {  // no room for this F: the kernel
+            P->ws = nullptr;
+            P->wsBytes = 0;
+            (void)hipGetLastError();
+            return TCC_OK;
+        }
         P->wsF = F;
     }
     const int rc = tcc_hybrid_spmm(&P->H, X, Y, F, 1, P->ws, P->wsBytes, stream);
