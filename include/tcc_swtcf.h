@@ -163,6 +163,14 @@ int tcc_swtcf_release_plans(void);
 /* Plans built since the process started. */
 uint32_t tcc_swtcf_plans_built(void);
 
+/* Two order-independent 64-bit sums over the 32-bit words of up to 8 device
+ * arrays (each bytes[k] a multiple of 4), mixed with their array and index,
+ * written to deviceOut[0..1] in stream order (no reference counterpart):
+ * what the plan caches compare to recognise a matrix whose arrays they
+ * have seen. */
+int tcc_hash_arrays(const void* const* arrays, const uint64_t* bytes, uint32_t count, uint64_t* deviceOut,
+                    void* stream);
+
 /* launchSWTCFSpMMQuantized: X[src][f] = q[srcGlobal[src]*128+f] * scales[srcGlobal[src]]
  * (src/swtcf_spmm.cu:317-323), otherwise as tcc_swtcf_spmm. */
 int tcc_swtcf_spmm_quantized(const tcc_swtcf_matrix* m, const int8_t* quantizedX,

@@ -97,6 +97,7 @@ SIGNATURES = {
     "tcc_swtcf_set_plans": (ctypes.c_int, [u32]),
     "tcc_swtcf_release_plans": (ctypes.c_int, []),
     "tcc_swtcf_plans_built": (u32, []),
+    "tcc_hash_arrays": (ctypes.c_int, [vp, vp, u32, vp, vp]),
     "tcc_bcsr_spmm": (ctypes.c_int, [ctypes.POINTER(BCSR), vp, vp, u32, ctypes.c_int, vp]),
     "tcc_bcsr_spmm_mixed": (ctypes.c_int, [ctypes.POINTER(BCSR), ctypes.POINTER(FeatureSource), vp, u32,
                                            ctypes.c_int, vp]),

@@ -18,11 +18,20 @@
 //
 // forward_tensorcore (both forms) packs x into exact TF32 rows first when
 // the BCSR gathers each row at least 16 times (tcc_spmm_cnic_forward_ws,
-// the buffer from torch's caching allocator on the current stream).  With
-// set_graph_plans(n > 0) it also keeps a per-graph plan for up to n graphs
-// (tcc_hybrid_from_bcsr: dense degree-ordered tiles on MFMA plus the gather
-// of the rest), found again by the BCSR arrays' device pointers and sizes;
-// a caller that rewrites a graph's arrays in place calls release_plans().
+// the buffer from torch's caching allocator on the current stream).  It also
+// keeps per-graph plans (tcc_hybrid_from_bcsr: dense degree-ordered tiles on
+// MFMA plus the gather of the rest), found again by a device hash of the
+// BCSR arrays (tcc_hash_arrays) and their sizes, so that a graph rewritten
+// in place is recognised as new:
+//  * by default (automatic), for a graph of at least kAutoMinBlocks blocks
+//    and 64 blocks per row window on average (the skewed graphs where the
+//    plan pays): one plan, built by the second call that finds the same
+//    arrays, so a single call on a graph pays only the hash;
+//  * after set_graph_plans(n > 0): up to n plans for any graph, built by the
+//    first call; set_graph_plans(0) turns plans off, set_graph_plans(-1)
+//    restores the automatic default.
+// The environment variable TCC_SPMM_CNIC_PLANS=0 turns the automatic plans
+// off from the first call.
 #include <torch/extension.h>
 
 #include <c10/hip/HIPStream.h>
@@ -30,6 +39,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdlib>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -46,19 +56,23 @@ std::vector<void*> g_spaces;           // space_malloc buffers, released by fina
 bool g_use_values = false;
 std::uint32_t g_unit_blocks = 0;       // blocks per unit of work (0 = automatic)
 
-// Per-graph plans, most recently used last (set_graph_plans).
+// Per-graph plans, most recently used last (set_graph_plans); entries not
+// yet built are graphs seen once in the automatic mode.
 struct Plan {
     int device;
-    const void* rwo;
-    const void* a2b;
-    const void* bits;
-    const void* data;
     std::uint32_t rows, cols, blocks, windows;
     bool values;
+    std::uint64_t h0, h1;
+    bool built;
     tcc_hybrid H;
 };
 std::vector<Plan> g_plans;
-std::size_t g_max_plans = 0;
+enum class PlanMode { Auto, Explicit, Off };
+PlanMode g_plan_mode = PlanMode::Auto;
+bool g_plan_env_read = false;
+std::size_t g_max_plans = 1;
+constexpr std::uint32_t kAutoMinBlocks = 1u << 16;
+constexpr std::uint32_t kAutoMinBlocksPerWindow = 64;
 
 void check(int rc) {
     if (rc != 0) {
@@ -204,7 +218,9 @@ void* aligned16(const torch::Tensor& t) {
 
 void drop_plan(Plan& p) {
     // hipFree waits for the work in flight that may still read the arrays
-    if (tcc_hybrid_release(&p.H) != 0) throw std::runtime_error(std::string("spmm_cnic: ") + tcc_last_error());
+    if (p.built && tcc_hybrid_release(&p.H) != 0)
+        throw std::runtime_error(std::string("spmm_cnic: ") + tcc_last_error());
+    p.built = false;
 }
 
 void release_plans() {
@@ -212,39 +228,105 @@ void release_plans() {
     g_plans.clear();
 }
 
-void set_graph_plans(std::int64_t n) {
-    TORCH_CHECK(n >= 0, "set_graph_plans: a count of plans (0 = none)");
-    g_max_plans = static_cast<std::size_t>(n);
-    while (g_plans.size() > g_max_plans) {
+// At most g_max_plans built plans and 2 g_max_plans + 2 entries, the least
+// recently used (front) dropped first.
+void trim_plans() {
+    for (;;) {
+        std::size_t built = 0;
+        for (const Plan& p : g_plans) built += p.built ? 1 : 0;
+        if (built <= g_max_plans) break;
+        for (Plan& p : g_plans)
+            if (p.built) {
+                drop_plan(p);
+                break;
+            }
+    }
+    while (g_plans.size() > 2 * g_max_plans + 2) {
         drop_plan(g_plans.front());
         g_plans.erase(g_plans.begin());
     }
 }
 
-std::int64_t graph_plans() { return static_cast<std::int64_t>(g_plans.size()); }
+void set_graph_plans(std::int64_t n) {
+    TORCH_CHECK(n >= -1, "set_graph_plans: a count of plans (0 = none, -1 = automatic)");
+    g_plan_env_read = true;
+    if (n < 0) {
+        g_plan_mode = PlanMode::Auto;
+        g_max_plans = 1;
+    } else {
+        g_plan_mode = n == 0 ? PlanMode::Off : PlanMode::Explicit;
+        g_max_plans = static_cast<std::size_t>(n);
+    }
+    if (g_max_plans == 0) {
+        release_plans();
+        return;
+    }
+    trim_plans();
+}
 
-// The plan of A's graph on `device`: found by its arrays and sizes, or built.
-const tcc_hybrid& plan_for(const tcc_bcsr& A, int device, void* st) {
+std::int64_t graph_plans() {
+    std::int64_t n = 0;
+    for (const Plan& p : g_plans) n += p.built ? 1 : 0;
+    return n;
+}
+
+// The plan of A's graph on `device`, or nullptr when the default path
+// should run: found by the hash of its arrays and its sizes; built by the
+// first call in the explicit mode, by the second in the automatic one.
+const tcc_hybrid* plan_for(const tcc_bcsr& A, int device, void* st) {
+    if (!g_plan_env_read) {
+        g_plan_env_read = true;
+        if (const char* e = std::getenv("TCC_SPMM_CNIC_PLANS"))
+            if (std::string(e) == "0") g_plan_mode = PlanMode::Off;
+    }
+    if (g_plan_mode == PlanMode::Off || g_max_plans == 0 || A.num_TCBlocks == 0 || A.phases > 1) return nullptr;
+    if (g_plan_mode == PlanMode::Auto &&
+        (A.num_TCBlocks < kAutoMinBlocks ||
+         A.num_TCBlocks < static_cast<std::uint64_t>(kAutoMinBlocksPerWindow) * A.num_rowWindows))
+        return nullptr;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(reinterpret_cast<hipStream_t>(st), &cap) != hipSuccess ||
+        cap != hipStreamCaptureStatusNone)
+        return nullptr;  // the hash is read back: not under graph capture
     const bool values = A.data != nullptr;
+    const void* arrays[4] = {A.rowWindowOffset, A.sparseA2B, A.tcLocalBit, A.data};
+    const std::uint64_t bytes[4] = {4ull * (A.num_rowWindows + 1ull), 32ull * A.num_TCBlocks, 8ull * A.num_TCBlocks,
+                                    4ull * A.nnz};
+    torch::Tensor h = torch::empty({2}, torch::TensorOptions().dtype(torch::kInt64).device(torch::kCUDA, device));
+    check(tcc_hash_arrays(arrays, bytes, values ? 4 : 3, reinterpret_cast<std::uint64_t*>(h.data_ptr()), st));
+    const torch::Tensor hh = h.cpu();  // waits for the hash on the current stream
+    const std::uint64_t h0 = static_cast<std::uint64_t>(hh[0].item<std::int64_t>());
+    const std::uint64_t h1 = static_cast<std::uint64_t>(hh[1].item<std::int64_t>());
     for (std::size_t i = 0; i < g_plans.size(); ++i) {
-        const Plan& p = g_plans[i];
-        if (p.device == device && p.rwo == A.rowWindowOffset && p.a2b == A.sparseA2B && p.bits == A.tcLocalBit &&
-            p.data == A.data && p.rows == A.num_rows && p.cols == A.num_cols && p.blocks == A.num_TCBlocks &&
-            p.windows == A.num_rowWindows && p.values == values) {
+        Plan& p = g_plans[i];
+        if (p.device == device && p.rows == A.num_rows && p.cols == A.num_cols && p.blocks == A.num_TCBlocks &&
+            p.windows == A.num_rowWindows && p.values == values && p.h0 == h0 && p.h1 == h1) {
             std::rotate(g_plans.begin() + static_cast<std::ptrdiff_t>(i), g_plans.begin() + static_cast<std::ptrdiff_t>(i) + 1,
                         g_plans.end());
-            return g_plans.back().H;
+            Plan& q = g_plans.back();
+            if (!q.built) {
+                // the automatic plan is an optimisation: if it cannot be
+                // built (device memory), the default path runs
+                if (tcc_hybrid_from_bcsr(&A, values ? 1 : 0, 0, 0, &q.H, st) != 0) {
+                    if (g_plan_mode == PlanMode::Explicit) check(1);
+                    g_plans.pop_back();
+                    (void)hipGetLastError();
+                    return nullptr;
+                }
+                q.built = true;
+                trim_plans();
+            }
+            return &g_plans.back().H;
         }
     }
-    if (g_plans.size() >= g_max_plans) {
-        drop_plan(g_plans.front());
-        g_plans.erase(g_plans.begin());
+    Plan p{device, A.num_rows, A.num_cols, A.num_TCBlocks, A.num_rowWindows, values, h0, h1, false, tcc_hybrid{}};
+    if (g_plan_mode == PlanMode::Explicit) {
+        check(tcc_hybrid_from_bcsr(&A, values ? 1 : 0, 0, 0, &p.H, st));
+        p.built = true;
     }
-    Plan p{device, A.rowWindowOffset, A.sparseA2B, A.tcLocalBit, A.data, A.num_rows, A.num_cols, A.num_TCBlocks,
-           A.num_rowWindows, values, tcc_hybrid{}};
-    check(tcc_hybrid_from_bcsr(&A, values ? 1 : 0, 0, 0, &p.H, st));
     g_plans.push_back(p);
-    return g_plans.back().H;
+    trim_plans();
+    return g_plans.back().built ? &g_plans.back().H : nullptr;
 }
 
 // denseC[(r_win+1)*8*F] = A x + B x (launch_spmm_kernel, spmm_launcher.cu:203-271)
@@ -252,8 +334,8 @@ void forward(const tcc_bcsr& A, const tcc_bcsc& B, const torch::Tensor& x, float
     TORCH_CHECK(x.is_cuda() && x.is_contiguous() && x.scalar_type() == torch::kFloat32, "x must be fp32 on device");
     void* st = stream_of(device);
     const float* X = x.data_ptr<float>();
-    if (g_max_plans > 0 && A.num_TCBlocks > 0 && A.phases <= 1) {
-        const tcc_hybrid& H = plan_for(A, device, st);
+    if (const tcc_hybrid* plan = plan_for(A, device, st)) {
+        const tcc_hybrid& H = *plan;
         const std::size_t need = tcc_hybrid_workspace_bytes(&H, static_cast<std::uint32_t>(F));
         torch::Tensor ws = device_bytes(need + 16, device);
         check(tcc_hybrid_spmm(&H, X, C, static_cast<std::uint32_t>(F), 0, aligned16(ws), need, st));
@@ -458,8 +540,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("set_unit_blocks", &set_unit_blocks,
           "blocks each wave of work walks (default 0 = chosen from the block count)");
     m.def("set_graph_plans", &set_graph_plans,
-          "keep per-graph plans (dense tiles on MFMA + gather) for up to n graphs, found by their BCSR arrays "
-          "(0, the default: none; plans beyond n are released, least recently used first)");
-    m.def("release_plans", &release_plans, "release every per-graph plan (after rewriting a graph's arrays in place)");
+          "per-graph plans (dense tiles on MFMA + gather), found by a hash of the BCSR arrays: n > 0 keeps up to n, "
+          "built by the first call on a graph; 0 turns them off; -1 restores the default (one plan, for large "
+          "skewed graphs, built by the second call that finds the same arrays)");
+    m.def("release_plans", &release_plans, "release every per-graph plan");
     m.def("graph_plans", &graph_plans, "the number of per-graph plans held");
 }

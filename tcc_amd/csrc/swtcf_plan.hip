@@ -113,6 +113,38 @@ __global__ void __launch_bounds__(kThreads) swtcf_hash_kernel(tcc_swtcf_matrix m
     }
 }
 
+// Up to kMaxSpans device arrays of 32-bit words, hashed as hash_array does.
+constexpr unsigned kMaxSpans = 8;
+struct HashSpans {
+    const std::uint32_t* p[kMaxSpans];
+    std::uint64_t words[kMaxSpans];
+    std::uint32_t n;
+};
+
+__global__ void __launch_bounds__(kThreads) hash_spans_kernel(HashSpans s, std::uint64_t* __restrict__ out) {
+    std::uint64_t s0 = 0, s1 = 0;
+    for (std::uint32_t k = 0; k < s.n; ++k) hash_array(s.p[k], s.words[k], k + 1, s0, s1);
+    __shared__ std::uint64_t r0[kThreads / kWave], r1[kThreads / kWave];
+#pragma unroll
+    for (int d = kWave / 2; d > 0; d >>= 1) {
+        s0 += __shfl_xor(s0, d, kWave);
+        s1 += __shfl_xor(s1, d, kWave);
+    }
+    if (__lane_id() == 0) {
+        r0[threadIdx.x / kWave] = s0;
+        r1[threadIdx.x / kWave] = s1;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (unsigned w = 1; w < kThreads / kWave; ++w) {
+            s0 += r0[w];
+            s1 += r1[w];
+        }
+        atomicAdd(reinterpret_cast<unsigned long long*>(&out[0]), static_cast<unsigned long long>(s0));
+        atomicAdd(reinterpret_cast<unsigned long long*>(&out[1]), static_cast<unsigned long long>(s1));
+    }
+}
+
 __global__ void swtcf_tile_counts_kernel(const std::uint64_t* __restrict__ bits, std::uint32_t T,
                                          std::uint32_t* __restrict__ counts) {
     const std::uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
@@ -391,6 +423,26 @@ int tcc_swtcf_release_plans(void) {
     std::lock_guard<std::mutex> lock(C.mu);
     for (auto& p : C.plans) p.release();
     C.plans.clear();
+    return TCC_OK;
+}
+
+int tcc_hash_arrays(const void* const* arrays, const std::uint64_t* bytes, std::uint32_t count,
+                    std::uint64_t* deviceOut, void* stream) {
+    clear_last_error();
+    TCC_REQUIRE(deviceOut && count <= kMaxSpans && (count == 0 || (arrays && bytes)), TCC_ERR_INVALID_ARGUMENT,
+                "tcc_hash_arrays: at most 8 arrays and an output");
+    HashSpans s{};
+    s.n = count;
+    for (std::uint32_t k = 0; k < count; ++k) {
+        TCC_REQUIRE(bytes[k] % 4 == 0 && (bytes[k] == 0 || arrays[k]), TCC_ERR_INVALID_ARGUMENT,
+                    "tcc_hash_arrays: arrays of whole 32-bit words");
+        s.p[k] = static_cast<const std::uint32_t*>(arrays[k]);
+        s.words[k] = bytes[k] / 4;
+    }
+    const hipStream_t st = as_stream(stream);
+    TCC_HIP_CHECK(fill<std::uint64_t>(deviceOut, 2, 0ull, st));
+    hipLaunchKernelGGL(hash_spans_kernel, dim3(kHashBlocks), dim3(kThreads), 0, st, s, deviceOut);
+    TCC_LAUNCH_CHECK();
     return TCC_OK;
 }
 

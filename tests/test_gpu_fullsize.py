@@ -323,7 +323,7 @@ def test_fullsize_config3_extension(gpu, oracle):
                 assert m.graph_plans() == 1
             m.freeMatC()
     finally:
-        m.set_graph_plans(0)
+        m.set_graph_plans(-1)
         m.freeMatC()
 
 

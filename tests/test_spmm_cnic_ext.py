@@ -230,10 +230,11 @@ def test_hybrid_from_bcsr_matches_the_coo_build(gpu, oracle):
 
 @pytest.mark.gpu
 def test_forward_tensorcore_graph_plans(gpu, oracle):
-    """set_graph_plans: the extension keeps a per-graph plan (dense tiles on
-    MFMA + gather), finds it again by the BCSR arrays, keeps at most n, and
-    drops them on release_plans(); with set_use_values the plan holds the
-    values.  Every product against the oracle."""
+    """set_graph_plans(n): the extension keeps a per-graph plan (dense tiles
+    on MFMA + gather) from the first call on any graph, finds it again by a
+    hash of the BCSR arrays, keeps at most n, and drops them on
+    release_plans(); with set_use_values the plan holds the values.  Every
+    product against the oracle."""
     m = import_ext()
     nr, nc, F = 600, 700, 130
     graphs = []
@@ -277,7 +278,61 @@ def test_forward_tensorcore_graph_plans(gpu, oracle):
         assert m.graph_plans() == 0
     finally:
         m.set_use_values(False)
-        m.set_graph_plans(0)
+        m.set_graph_plans(-1)  # the automatic default
         m.freeMatC()
         torch.cuda.synchronize()
         m.finalize(0)
+
+
+@pytest.mark.gpu
+def test_forward_tensorcore_automatic_plans(gpu, oracle):
+    """An unchanged caller: by default a large graph with long row windows
+    (>= 65,536 blocks, >= 64 a window) gets a plan from the second call
+    that finds the same arrays (a device hash of rowWindowOffset, sparseA2B
+    and tcLocalBit); the first call runs the packed gather.  A bitmap
+    rewritten in place hashes differently: that call runs the default path
+    on the new graph, and the next call builds the new graph's plan in
+    place of the old one.  Every product against the oracle."""
+    m = import_ext()
+    nr, nc, F = 512, 60000, 96
+    rng = np.random.default_rng(51)
+    keys = np.unique(rng.integers(0, nr * nc, size=1_300_000, dtype=np.int64))
+    dst, src = (keys // nc).astype(np.uint32), (keys % nc).astype(np.uint32)
+    bcsr, _ = _blocks(dst, src, nr, nc)
+    assert bcsr["num_TCBlocks"] >= 65536 and bcsr["num_TCBlocks"] >= 64 * bcsr["num_rowWindows"]
+    empty = _blocks(np.zeros(0, np.uint32), np.zeros(0, np.uint32), nr, nc)[1]
+    args = _args(bcsr, empty, True)
+    X = np.random.default_rng(52).standard_normal((nc, F)).astype(np.float32)
+    x = torch.from_numpy(X).cuda().flatten()
+    try:
+        m.set_graph_plans(-1)
+        m.release_plans()
+        want = _want(dst, src, nr, X)
+        for call, plans in ((1, 0), (2, 1), (3, 1)):
+            out = m.forward_tensorcore(*args, F, x)
+            assert _rel(out.reshape(nr, F).cpu().numpy(), want) < 1e-5, call
+            assert m.graph_plans() == plans, call
+            m.freeMatC()
+        # one entry of block 0 removed in place
+        b0 = int(np.uint64(bcsr["tcLocalBit"][0]))
+        i = (b0 & -b0).bit_length() - 1
+        w0 = int(np.searchsorted(bcsr["rowWindowOffset"], 0, side="right")) - 1
+        row, col = 8 * w0 + i // 8, int(bcsr["sparseA2B"][i % 8])
+        args[8][0] = int(np.array([b0 & ~(1 << i)], np.uint64).view(np.int64)[0])
+        keep = ~((dst == row) & (src == col))
+        assert keep.sum() == dst.size - 1
+        want2 = _want(dst[keep], src[keep], nr, X)
+        for call, plans in ((4, 1), (5, 1)):
+            out = m.forward_tensorcore(*args, F, x)
+            assert _rel(out.reshape(nr, F).cpu().numpy(), want2) < 1e-5, call
+            assert m.graph_plans() == plans, call
+            m.freeMatC()
+        # turned off: the default path, no plan kept
+        m.set_graph_plans(0)
+        assert m.graph_plans() == 0
+        out = m.forward_tensorcore(*args, F, x)
+        assert _rel(out.reshape(nr, F).cpu().numpy(), want2) < 1e-5
+    finally:
+        m.set_graph_plans(-1)
+        m.freeMatC()
+        torch.cuda.synchronize()
