@@ -377,10 +377,19 @@ def swtcf_plan_timings(torch, swtcf, m, n, nnz):
     first_two_ms = (time.perf_counter() - t0) * 1e3
     assert L.tcc_swtcf_plans_built() == built0 + 1
     plan_ms = timed(step, 20, 2)
+    # int8 X with per-row scales (launchSWTCFSpMMQuantized): the same plan,
+    # X dequantized into its buffer first
+    scale = X.abs().amax(dim=1).clamp_min(1e-30) / 127.0
+    q = torch.round(X / scale[:, None]).clamp(-127, 127).to(torch.int8).contiguous()
+    src_global = torch.arange(n, dtype=torch.int32, device="cuda")
+    qstep = lambda: swtcf.launchSWTCFSpMMQuantized(m, q, scale.contiguous(), src_global, Y, 12)
+    int8_plan_ms = timed(qstep, 20, 2)
+    assert L.tcc_swtcf_plans_built() == built0 + 1
     L.tcc_swtcf_release_plans()
     gf = lambda ms: round(2.0 * nnz * F / (ms * 1e-3) / 1e9, 3)
     return {"F": F, "S": 16, "kernel_ms": round(kernel_ms, 4), "kernel_gflops": gf(kernel_ms),
             "plan_ms": round(plan_ms, 4), "plan_gflops": gf(plan_ms),
+            "int8_plan_ms": round(int8_plan_ms, 4), "int8_plan_gflops": gf(int8_plan_ms),
             "first_two_calls_ms": round(first_two_ms, 2),
             "plan": "binary hub tiles on the sparse MFMA + gathered remainder of the matrix's pattern, built on the "
                     "second call that finds the same arrays (device hash each call)"}

@@ -172,7 +172,9 @@ int tcc_hash_arrays(const void* const* arrays, const uint64_t* bytes, uint32_t c
                     void* stream);
 
 /* launchSWTCFSpMMQuantized: X[src][f] = q[srcGlobal[src]*128+f] * scales[srcGlobal[src]]
- * (src/swtcf_spmm.cu:317-323), otherwise as tcc_swtcf_spmm. */
+ * (src/swtcf_spmm.cu:317-323), otherwise as tcc_swtcf_spmm, plans included
+ * (a plan dequantizes X into a buffer of its own, cols x 128 floats, then
+ * runs as for fp32 X). */
 int tcc_swtcf_spmm_quantized(const tcc_swtcf_matrix* m, const int8_t* quantizedX,
                              const float* scales, const uint32_t* srcGlobal, float* Y,
                              uint32_t tcThreshold, void* stream);

@@ -31,6 +31,7 @@
 #include "../../include/tcc_swtcf.h"
 #include "common.hpp"
 #include "primitives.hpp"
+#include "swtcf_plan.hpp"
 
 namespace tcc {
 namespace {
@@ -190,6 +191,22 @@ __global__ void swtcf_decode_kernel(tcc_swtcf_matrix m, std::uint32_t T, const s
     if (bad) atomicAdd(dropped, bad);
 }
 
+// X[src][f] = q[srcGlobal[src] * F + f] * scales[srcGlobal[src]]
+// (src/swtcf_spmm.cu:317-323), four features a thread.
+__global__ void dequantize_kernel(const std::int8_t* __restrict__ q, const float* __restrict__ scales,
+                                  const std::uint32_t* __restrict__ srcGlobal, std::uint32_t cols, std::uint32_t F,
+                                  float* __restrict__ X) {
+    const std::uint64_t i = static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const std::uint32_t quads = F / 4;
+    if (i >= static_cast<std::uint64_t>(cols) * quads) return;
+    const std::uint32_t src = static_cast<std::uint32_t>(i / quads), f = 4 * static_cast<std::uint32_t>(i % quads);
+    const std::uint32_t g = srcGlobal[src];
+    const float sc = scales[g];
+    const std::int8_t* r = q + static_cast<std::uint64_t>(g) * F + f;
+    *reinterpret_cast<vf4*>(X + static_cast<std::uint64_t>(src) * F + f) =
+        vf4{r[0] * sc, r[1] * sc, r[2] * sc, r[3] * sc};
+}
+
 struct Plan {
     int device = -1;
     std::uint32_t rows = 0, cols = 0, S = 0, CW = 0, SW = 0;
@@ -201,14 +218,17 @@ struct Plan {
     void* ws = nullptr;
     std::size_t wsBytes = 0;
     std::uint32_t wsF = 0;
+    float* xq = nullptr;  // the dequantized X of the int8 entry point ([cols x 128])
 
     void release() {
         if (built) tcc_hybrid_release(&H);
         if (ws) (void)hipFree(ws);
+        if (xq) (void)hipFree(xq);
         built = false;
         ws = nullptr;
         wsBytes = 0;
         wsF = 0;
+        xq = nullptr;
     }
 };
 
@@ -318,10 +338,8 @@ int build_plan(const tcc_swtcf_matrix* m, Plan& P, hipStream_t st) {
 
 }  // namespace
 
-// Runs the SpMM through a plan when one applies; *used = false leaves it to
-// the SWTCF kernel.
 int swtcf_plan_spmm(const tcc_swtcf_matrix* m, const float* X, float* Y, std::uint32_t F, std::uint32_t tc,
-                    void* stream, bool* used) {
+                    void* stream, bool* used, const SwtcfQuantX* quant) {
     *used = false;
     PlanCache& C = cache();
     std::lock_guard<std::mutex> lock(C.mu);
@@ -393,6 +411,18 @@ int swtcf_plan_spmm(const tcc_swtcf_matrix* m, const float* X, float* Y, std::ui
             return TCC_OK;
         }
         P->wsF = F;
+    }
+    if (quant) {
+        if (!P->xq && hipMalloc(&P->xq, 4ull * m->cols * F) != hipSuccess) {
+            P->xq = nullptr;
+            (void)hipGetLastError();
+            return TCC_OK;
+        }
+        const std::uint64_t n = static_cast<std::uint64_t>(m->cols) * (F / 4);
+        hipLaunchKernelGGL(dequantize_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, st, quant->q,
+                           quant->scales, quant->srcGlobal, m->cols, F, P->xq);
+        TCC_LAUNCH_CHECK();
+        X = P->xq;
     }
     const int rc = tcc_hybrid_spmm(&P->H, X, Y, F, 1, P->ws, P->wsBytes, stream);
     if (rc) return rc;

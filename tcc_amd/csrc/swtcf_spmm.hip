@@ -24,14 +24,9 @@
 
 #include "../../include/tcc_swtcf.h"
 #include "common.hpp"
+#include "swtcf_plan.hpp"
 
 namespace tcc {
-
-// swtcf_plan.hip: runs the product through a kept plan (the binary hybrid of
-// the same pattern) when one applies, setting *used.
-int swtcf_plan_spmm(const tcc_swtcf_matrix* m, const float* X, float* Y, std::uint32_t F, std::uint32_t tc,
-                    void* stream, bool* used);
-
 namespace {
 
 constexpr unsigned kThreads = 1024;
@@ -378,6 +373,10 @@ int tcc_swtcf_spmm_quantized(const tcc_swtcf_matrix* m, const std::int8_t* quant
     // launchSWTCFSpMMQuantized (:478-480)
     TCC_REQUIRE(m->superWindowSize == 16, TCC_ERR_UNSUPPORTED,
                 "Quantized SWTCF SpMM requires superWindowSize=16");
+    bool planned = false;
+    const SwtcfQuantX qx{quantizedX, scales, srcGlobal};
+    const int rc = swtcf_plan_spmm(m, nullptr, Y, TCC_SWTCF_FEATURE_DIM, tcThreshold, stream, &planned, &qx);
+    if (rc || planned) return rc;
     return launch<true>(m, nullptr, quantizedX, scales, srcGlobal, Y, TCC_SWTCF_FEATURE_DIM, tcThreshold,
                         stream);
 }

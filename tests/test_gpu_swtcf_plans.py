@@ -15,7 +15,8 @@ of capacity, 64 entries per row on average):
 - tcThreshold 65 (the reference's pure fp32 path) and tcc_swtcf_set_plans(0)
   never plan;
 - another feature width (tcc_swtcf_spmm_f, F = 72) reuses the plan with a
-  workspace of its own size.
+  workspace of its own size;
+- launchSWTCFSpMMQuantized plans too, dequantizing X into the plan's buffer.
 """
 import numpy as np
 import pytest
@@ -125,5 +126,44 @@ def test_plans_off(gpu, oracle, plans):
     assert plans.tcc_swtcf_plans_built() == b0
     dst, src = r32.cpu().numpy().view(np.uint32), c32.cpu().numpy().view(np.uint32)
     assert rel_l2(Y.cpu().numpy(), oracle_product(oracle, dst, src, None, n, X.cpu().numpy())) <= 1e-3
+    m.free()
+    ws.free()
+
+
+def test_quantized_plan(gpu, oracle, plans):
+    """launchSWTCFSpMMQuantized (X[src] = q[srcGlobal[src]] * scales[srcGlobal[src]],
+    src/swtcf_spmm.cu:317-323) through the same plan: the first call runs
+    the SWTCF kernel, the second builds the plan, which dequantizes X into
+    its own buffer and runs the hybrid; against the fp64 oracle over
+    TF32(dequantized X) at 1e-5 (plan) and 1e-3 (kernel)."""
+    from tcc_amd import swtcf
+
+    n, E, F = 36000, 4_250_000, 128
+    r32, c32 = rmat_coo(n, E, 14)
+    m = swtcf.DeviceSWTCFMatrix(n, n, E, 16)
+    ws = swtcf.SWTCFConvertWorkspace(E, n, 16)
+    convert(swtcf, m, ws, r32, c32)
+    rng = np.random.default_rng(15)
+    N = n + 100
+    q = rng.integers(-127, 128, size=(N, F), dtype=np.int8)
+    scales = rng.uniform(0.001, 0.05, N).astype(np.float32)
+    src_global = rng.permutation(N)[:n].astype(np.uint32)
+    Xdq = (q[src_global].astype(np.float32) * scales[src_global][:, None]).astype(np.float32)
+    dst, src = r32.cpu().numpy().view(np.uint32), c32.cpu().numpy().view(np.uint32)
+    want = oracle_product(oracle, dst, src, None, n, Xdq)
+    qd = torch.from_numpy(q).cuda()
+    sd = torch.from_numpy(scales).cuda()
+    gd = torch.from_numpy(src_global.view(np.int32)).cuda()
+    b0 = plans.tcc_swtcf_plans_built()
+    got = []
+    for call in range(3):
+        Y = torch.zeros((n, F), device="cuda")
+        swtcf.launchSWTCFSpMMQuantized(m, qd, sd, gd, Y)
+        torch.cuda.synchronize()
+        assert plans.tcc_swtcf_plans_built() == b0 + (0 if call == 0 else 1), call
+        got.append(Y.cpu().numpy())
+    e = [rel_l2(g, want) for g in got]
+    print(f"quantized: kernel {e[0]:.2e}, plan {e[1]:.2e} {e[2]:.2e}", flush=True)
+    assert e[0] <= 1e-3 and e[1] <= 1e-5 and e[2] <= 1e-5
     m.free()
     ws.free()
