@@ -27,6 +27,7 @@
 // the current window stay in registers and each block row is added into Y
 // with fp32 atomics, as the reference does.
 #include <algorithm>
+#include <mutex>
 
 #include "../../include/tcc_spmm_cnic.h"
 #include "../../include/tcc_swtcf.h"
@@ -1284,18 +1285,28 @@ inline std::uint64_t plan_scatter(ScatterArgs& a, int V, std::uint32_t requested
     return static_cast<std::uint64_t>(a.numUnits) * a.numChunks;
 }
 
-// zeroShared = false: a second launch over other features of the same units
-// (their shared windows were zeroed, over all F features, by the first).
+// Zeroes, over all F features, the windows that several units of a planned
+// gather add into (none when one unit covers each window, or when the gather
+// adds into Y or writes through atomics).
+int zero_shared(const GatherArgs& a, hipStream_t st) {
+    if (a.numWindows == 0 || a.numUnits <= 1 || a.accumulate || a.atomicOut) return TCC_OK;
+    hipLaunchKernelGGL(zero_shared_windows_kernel, dim3(grid_for(a.numWindows, kThreads)), dim3(kThreads), 0, st,
+                       a.winOffset, a.numWindows, a.unitBlocks, a.Y, a.F);
+    TCC_LAUNCH_CHECK();
+    return TCC_OK;
+}
+
+// zeroShared = false: a launch over other features of units whose shared
+// windows were zeroed already.
 template <Src MODE>
 int launch_gather(GatherArgs a, int V, std::uint32_t requestedK, hipStream_t st, bool zeroShared = true) {
     constexpr bool kHostRows = MODE == Src::Mixed || MODE == Src::MixedPacked;
     const std::uint64_t waves = plan_gather(a, V, requestedK, kHostRows ? kHostLinkMaxUnit : kDeviceRowsMaxUnit);
     if (waves == 0) return TCC_OK;
     TCC_REQUIRE(waves <= 0xFFFFFFFFull / kWaves, TCC_ERR_UNSUPPORTED, "SpMM launch too large");
-    if (zeroShared && a.numUnits > 1 && !a.accumulate && !a.atomicOut) {
-        hipLaunchKernelGGL(zero_shared_windows_kernel, dim3(grid_for(a.numWindows, kThreads)), dim3(kThreads), 0, st,
-                           a.winOffset, a.numWindows, a.unitBlocks, a.Y, a.F);
-        TCC_LAUNCH_CHECK();
+    if (zeroShared) {
+        const int rc = zero_shared(a, st);
+        if (rc) return rc;
     }
     const dim3 grid(grid_for(waves, kWaves));
     if (a.data != nullptr) {
@@ -1503,6 +1514,72 @@ int tf32_pack_scaled(const float* X, std::uint32_t rows, std::uint32_t featureDi
     return TCC_OK;
 }
 
+// A second stream per device, for work that runs beside a launch on the
+// caller's stream (default priority, non-blocking).  SideFork orders it
+// after the work queued so far on st (fork) and st after everything queued
+// on it in between (join); when st is being captured, or the side stream
+// cannot be made, the work goes to st itself.  The lock keeps concurrent
+// callers' record/wait pairs on the shared events apart: a wait takes the
+// event's latest record.
+namespace {
+
+struct SideLane {
+    hipStream_t stream = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+};
+std::mutex g_sideMutex;
+SideLane g_sideLanes[64];
+
+class SideFork {
+public:
+    explicit SideFork(hipStream_t st) : st_(st) {
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(st, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return;
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return;
+        lock_ = std::unique_lock<std::mutex>(g_sideMutex);
+        SideLane& l = g_sideLanes[dev];
+        if (!l.stream) {
+            hipStream_t s = nullptr;
+            hipEvent_t f = nullptr, j = nullptr;
+            if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return;
+            if (hipEventCreateWithFlags(&f, hipEventDisableTiming) != hipSuccess ||
+                hipEventCreateWithFlags(&j, hipEventDisableTiming) != hipSuccess) {
+                if (f) (void)hipEventDestroy(f);
+                (void)hipStreamDestroy(s);
+                return;
+            }
+            l.stream = s;
+            l.fork = f;
+            l.join = j;
+        }
+        if (hipEventRecord(l.fork, st) != hipSuccess || hipStreamWaitEvent(l.stream, l.fork, 0) != hipSuccess) return;
+        lane_ = &l;
+    }
+    SideFork(const SideFork&) = delete;
+    SideFork& operator=(const SideFork&) = delete;
+    ~SideFork() { (void)join(); }
+
+    hipStream_t stream() const { return lane_ ? lane_->stream : st_; }
+
+    // Orders st after the side stream's work; idempotent.
+    int join() {
+        if (!lane_) return TCC_OK;
+        SideLane* l = lane_;
+        lane_ = nullptr;
+        TCC_HIP_CHECK(hipEventRecord(l->join, l->stream));
+        TCC_HIP_CHECK(hipStreamWaitEvent(st_, l->join, 0));
+        return TCC_OK;
+    }
+
+private:
+    hipStream_t st_;
+    SideLane* lane_ = nullptr;
+    std::unique_lock<std::mutex> lock_;
+};
+
+}  // namespace
+
 int bcsr_spmm_packed_scaled(const tcc_bcsr* A, const void* packedX, float* Y, std::uint32_t featureDim,
                             int accumulate, const float* rowScale, hipStream_t st) {
     TCC_REQUIRE(bcsr_ok(A) && packedX && Y && feature_dim_ok(featureDim), TCC_ERR_INVALID_ARGUMENT,
@@ -1523,15 +1600,24 @@ int bcsr_spmm_packed_scaled(const tcc_bcsr* A, const void* packedX, float* Y, st
     // features a lane, over the same units, after the full chunks.
     const std::uint32_t tail = featureDim % kPackChunk;
     if (tail == 0 || tail > kPackChunk / 2) return launch_gather<Src::Packed>(a, 4, A->unitBlocks, st);
+    // Both launches take the full chunks' units, whose shared windows are
+    // zeroed (over all F) before either starts.  The last chunk runs on the
+    // device's side stream beside the full chunks, so that its waves fill
+    // the CUs the full launch's last waves leave idle (on a stream being
+    // captured, after them on st).
     GatherArgs full = a;
     full.featureEnd = featureDim - tail;
-    int rc = launch_gather<Src::Packed>(full, 4, A->unitBlocks, st);
-    if (rc) return rc;
     GatherArgs last = a;
     last.featureBase = featureDim - tail;
-    // the same units as the full chunks, so that the windows they share were zeroed
-    plan_gather(full, 4, A->unitBlocks);
-    return launch_gather<Src::Packed>(last, tail > kWave ? 2 : 1, full.unitBlocks, st, false);
+    if (plan_gather(full, 4, A->unitBlocks) == 0) return TCC_OK;
+    int rc = zero_shared(full, st);
+    if (rc) return rc;
+    const int lastV = tail > kWave ? 2 : 1;
+    SideFork side(st);
+    rc = launch_gather<Src::Packed>(last, lastV, full.unitBlocks, side.stream(), false);
+    if (rc == TCC_OK) rc = launch_gather<Src::Packed>(full, 4, A->unitBlocks, st, false);
+    const int joined = side.join();
+    return rc ? rc : joined;
 }
 
 }  // namespace tcc

@@ -1,6 +1,8 @@
 """HIP-graph capture of the library's launches (torch.cuda.CUDAGraph over
 the kernels the C-ABI enqueues on the current stream): the BCSR gather with
-its shared-window zero pass, the packed gather with its separate last chunk,
+its shared-window zero pass, the packed gather with its separate last chunk
+(which runs on the caller's stream while it is captured, and on a second
+stream of the device beside the full chunks otherwise),
 the gathers over a phased BCSR (zero fill of Y, then atomics only),
 the one-launch first-layer forward (fill + mixed kernel), the SWTCF SpMM,
 the narrow and transposed gathers, the split-K dense products and the

@@ -759,6 +759,59 @@ def test_bcsr_spmm_packed(gpu, oracle, unit_blocks, F):
     assert_close(Y2.cpu().numpy()[:nr], 2 * want)
 
 
+def test_bcsr_spmm_packed_concurrent_callers(gpu, oracle):
+    """The last chunk of a packed gather runs on a second stream of the
+    device, forked from and joined back into the caller's stream through
+    events that all callers share under a lock.  Two host threads, each on a
+    stream of its own, call it in turns (F = 602 and 300: last chunks of 90
+    and 44 features, 3-block units with shared windows) into Y filled with
+    NaN, and copy Y on their own stream right after each call: every copy
+    holds the oracle's product, so each caller's stream waited for its own
+    last chunk and the shared windows were zeroed before either launch."""
+    import threading
+
+    from tcc_amd import swtcf
+
+    nr, nc = 640, 900
+    dst, src = skewed_coo(nr, nc, 70)
+    vals = np.random.default_rng(71).uniform(-1, 1, dst.size).astype(np.float32)
+    rowptr, colind, v = csr_of(dst, src, nr, vals)
+    A = swtcf.coo_to_bcsr(dev_u32(dst), dev_u32(src), torch.from_numpy(vals).cuda(), nr, nc)
+    A.set_unit_blocks(3)
+    cases = []
+    for i, F in enumerate((602, 300)):
+        X = np.random.default_rng(72 + i).standard_normal((nc, F)).astype(np.float32)
+        cases.append((F, swtcf.tf32_pack(torch.from_numpy(X).cuda()),
+                      oracle.csr_spmm(rowptr, colind, v, X, use_tf32=True)))
+    torch.cuda.synchronize()
+    results, errors = [[], []], []
+
+    def caller(i):
+        try:
+            F, packed, _ = cases[i]
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                Y = torch.empty((A.view.num_rowWindows * 8, F), device="cuda")
+                for _ in range(12):
+                    Y.fill_(float("nan"))
+                    swtcf.bcsr_spmm_packed(A, packed, F, Y, stream=s)
+                    results[i].append(Y.clone())
+            s.synchronize()
+        except Exception as e:  # surfaced below
+            errors.append(e)
+
+    threads = [threading.Thread(target=caller, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    for i, (F, _, want) in enumerate(cases):
+        assert len(results[i]) == 12
+        for Y in results[i]:
+            assert_close(Y.cpu().numpy()[:nr], want)
+
+
 def test_feature_table_error_is_read_and_cleared(gpu):
     """FeatureTable.error() returns TCC_DEVERR_FEATURE_INDEX after a refused
     lookup (a host row past the table, planted in id_map) and clears it: the
