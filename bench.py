@@ -336,36 +336,32 @@ def line_for(args, value, unit, ms, dtype, config, roof, cpu, extra, higher=True
     }
 
 
-def swtcf_timings(torch, swtcf, m, X, n, nnz, F):
-    """The SWTCF SpMM of the config-2 graph at the reference's F = 128, S = 16
-    contract: fp32 X (launchSWTCFSpMM) and int8 X with per-row scales
-    (launchSWTCFSpMMQuantized, src/swtcf_spmm.cu:469-502).  Y += A X is
-    launched without zeroing Y between launches, as the reference times it
+PLAN_KINDS = {
+    2: "the BCSR gather of the matrix's pattern (a plain BCSR: rows are gathered 7.3 times on average)",
+    3: "binary hub tiles on the sparse MFMA + gathered remainder of the matrix's pattern",
+}
+
+
+def swtcf_plan_timings(torch, swtcf, m, n, nnz, config):
+    """launchSWTCFSpMM (and launchSWTCFSpMMQuantized, int8 X with per-row
+    scales, src/swtcf_spmm.cu:469-502) on the config's graph at the
+    reference's F = 128, S = 16: the SWTCF kernel (plans off) and the kept
+    plan (the second call on the matrix builds it), Y += A X without
+    zeroing Y between launches, as the reference times it
     (swtcf_spmm_main.cu:203-247 sets Y once)."""
-    Y = torch.zeros((n, F), device="cuda")
-    fp32_ms = timed(lambda: swtcf.launchSWTCFSpMM(m, X, Y), 20, 3)
-    scale = X.abs().amax(dim=1).clamp_min(1e-30) / 127.0
-    q = torch.round(X / scale[:, None]).clamp(-127, 127).to(torch.int8).contiguous()
-    src_global = torch.arange(n, dtype=torch.int32, device="cuda")
-    q_ms = timed(lambda: swtcf.launchSWTCFSpMMQuantized(m, q, scale.contiguous(), src_global, Y), 20, 3)
-    gf = lambda ms: round(2.0 * nnz * F / (ms * 1e-3) / 1e9, 3)
-    return {"F": F, "S": 16, "fp32_ms": round(fp32_ms, 4), "fp32_gflops": gf(fp32_ms),
-            "int8_ms": round(q_ms, 4), "int8_gflops": gf(q_ms),
-            "X_bytes_fp32": 4 * n * F, "X_bytes_int8": n * F + 4 * n}
-
-
-def swtcf_plan_timings(torch, swtcf, m, n, nnz):
-    """launchSWTCFSpMM on the config-3 graph at the reference's F = 128,
-    S = 16: the SWTCF kernel (plans off) and the kept plan (the second call
-    on the matrix builds it: the binary hybrid of the same pattern), Y += A X
-    without zeroing Y between launches, as the reference times it."""
     L = swtcf._lib.lib()
     F = 128
     X = torch.randn((n, F), device="cuda", generator=torch.Generator(device="cuda").manual_seed(11))
     Y = torch.zeros((n, F), device="cuda")
     step = lambda: swtcf.launchSWTCFSpMM(m, X, Y, 12)
+    scale = X.abs().amax(dim=1).clamp_min(1e-30) / 127.0
+    q = torch.round(X / scale[:, None]).clamp(-127, 127).to(torch.int8).contiguous()
+    src_global = torch.arange(n, dtype=torch.int32, device="cuda")
+    qstep = lambda: swtcf.launchSWTCFSpMMQuantized(m, q, scale.contiguous(), src_global, Y, 12)
+    reps = (20, 3) if config == 2 else (3, 1)
     L.tcc_swtcf_set_plans(0)
-    kernel_ms = timed(step, 3, 1)
+    kernel_ms = timed(step, *reps)
+    int8_kernel_ms = timed(qstep, *reps)
     L.tcc_swtcf_set_plans(1)
     L.tcc_swtcf_release_plans()
     built0 = L.tcc_swtcf_plans_built()
@@ -377,22 +373,19 @@ def swtcf_plan_timings(torch, swtcf, m, n, nnz):
     first_two_ms = (time.perf_counter() - t0) * 1e3
     assert L.tcc_swtcf_plans_built() == built0 + 1
     plan_ms = timed(step, 20, 2)
-    # int8 X with per-row scales (launchSWTCFSpMMQuantized): the same plan,
-    # X dequantized into its buffer first
-    scale = X.abs().amax(dim=1).clamp_min(1e-30) / 127.0
-    q = torch.round(X / scale[:, None]).clamp(-127, 127).to(torch.int8).contiguous()
-    src_global = torch.arange(n, dtype=torch.int32, device="cuda")
-    qstep = lambda: swtcf.launchSWTCFSpMMQuantized(m, q, scale.contiguous(), src_global, Y, 12)
+    # int8 X: the same plan, X dequantized into its buffer first
     int8_plan_ms = timed(qstep, 20, 2)
     assert L.tcc_swtcf_plans_built() == built0 + 1
     L.tcc_swtcf_release_plans()
     gf = lambda ms: round(2.0 * nnz * F / (ms * 1e-3) / 1e9, 3)
     return {"F": F, "S": 16, "kernel_ms": round(kernel_ms, 4), "kernel_gflops": gf(kernel_ms),
+            "int8_kernel_ms": round(int8_kernel_ms, 4), "int8_kernel_gflops": gf(int8_kernel_ms),
             "plan_ms": round(plan_ms, 4), "plan_gflops": gf(plan_ms),
             "int8_plan_ms": round(int8_plan_ms, 4), "int8_plan_gflops": gf(int8_plan_ms),
             "first_two_calls_ms": round(first_two_ms, 2),
-            "plan": "binary hub tiles on the sparse MFMA + gathered remainder of the matrix's pattern, built on the "
-                    "second call that finds the same arrays (device hash each call)"}
+            "plan": PLAN_KINDS[config] + ", built on the second call that finds the same arrays (device hash "
+                                         "each call)",
+            "X_bytes_fp32": 4 * n * F, "X_bytes_int8": n * F + 4 * n}
 
 
 def bench_swtcf_ab(args, torch, swtcf):
@@ -627,15 +620,17 @@ def bench_swtcf_step(args, torch, swtcf, cfg):
     del ws
     X = torch.randn((n, F), device="cuda", generator=torch.Generator(device="cuda").manual_seed(11))
     Y = torch.zeros((n, F), device="cuda")
+    through = ("swtcf_spmm_kernel" if args.no_swtcf_plans else
+               "its plan from the second call on: " + PLAN_KINDS[args.config])
     if args.swtcf_step == "fp32":
         step = lambda: swtcf.launchSWTCFSpMM(m, X, Y, 12)
-        kernel = "swtcf_spmm_kernel (launchSWTCFSpMM, fp32 X)"
+        kernel = f"launchSWTCFSpMM, fp32 X: {through}"
     else:
         scales = X.abs().amax(dim=1).clamp_min(1e-30) / 127.0
         q = torch.round(X / scales[:, None]).clamp(-127, 127).to(torch.int8).contiguous()
         src_global = torch.arange(n, dtype=torch.int32, device="cuda")
         step = lambda: swtcf.launchSWTCFSpMMQuantized(m, q, scales.contiguous(), src_global, Y, 12)
-        kernel = "swtcf_spmm_kernel (launchSWTCFSpMMQuantized, int8 X, per-row scales)"
+        kernel = f"launchSWTCFSpMMQuantized, int8 X, per-row scales: {through}"
     if args.copy_calibration_mib:
         copy_calibration(args.copy_calibration_mib)
     ms, median = timed_stats(step, args.steps, args.warmup)
@@ -825,10 +820,8 @@ def bench_spmm(args, torch, swtcf, cfg):
         extra["convert_shuffled_ms"] = round(conv_s, 4)
         extra["convert_shuffled_gedges_per_s"] = round(nnz / conv_s / 1e6, 3)
         del rs32, cs32
-        if args.config == 2:
-            extra["swtcf"] = swtcf_timings(torch, swtcf, m, X, n, nnz, F)
-        if args.config == 3:
-            extra["swtcf"] = swtcf_plan_timings(torch, swtcf, m, n, nnz)
+        if args.config in (2, 3):
+            extra["swtcf"] = swtcf_plan_timings(torch, swtcf, m, n, nnz, args.config)
         del m, ws
         if args.config == 3:
             torch.cuda.empty_cache()

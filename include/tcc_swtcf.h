@@ -124,14 +124,17 @@ int tcc_swtcf_convert(const uint32_t* dDst, const uint32_t* dSrc, uint32_t numEd
  * tcThreshold nonzeros use TF32-rounded X (the reference's tensor-core path),
  * sparser tiles use X as given (its fp32 path).  The caller zeroes Y.
  * Plans (no reference counterpart, see tcc_swtcf_set_plans): on a matrix of
- * at least 4M edges of capacity and 64 entries per row on average, with
- * tcThreshold <= 64 and the stream not capturing a graph, the call hashes
- * the matrix's arrays on the device and waits for the hash; from the second
- * call that finds the same matrix on, the product runs through a kept plan
- * (the matrix's pattern as binary hub tiles plus a gathered remainder,
- * tcc_coo_to_hybrid_scaled) with TF32(X) for every entry, exact products
- * and fp32 sums.  The call that builds the plan synchronises the stream
- * and allocates the plan's device memory. */
+ * at least 2^18 edges of capacity, with tcThreshold <= 64 and the stream not
+ * capturing a graph, the call hashes the matrix's arrays on the device and
+ * waits for the hash; from the second call that finds the same matrix on,
+ * the product runs through a kept plan with TF32(X) for every entry, exact
+ * products and fp32 sums: at 4M edges or more and 64 entries per row on
+ * average, the matrix's pattern as binary hub tiles plus a gathered
+ * remainder (tcc_coo_to_hybrid_scaled), else the BCSR gather of the pattern
+ * (tcc_coo_to_bcsr; over X packed to TF32 rows, tcc_tf32_pack, where rows
+ * are gathered 16 times or more on average).  Y keeps exactly rows rows
+ * either way.  The call that builds the plan synchronises the stream and
+ * allocates the plan's device memory. */
 int tcc_swtcf_spmm(const tcc_swtcf_matrix* m, const float* X, float* Y,
                    uint32_t tcThreshold, void* stream);
 
@@ -155,8 +158,8 @@ int tcc_swtcf_spmm_mfma(const tcc_swtcf_matrix* m, const float* X, float* Y, uin
  * kept, the least recently used released first; 0 turns plans off.  The
  * default is 1, or the value of the environment variable TCC_SWTCF_PLANS
  * read at the first SpMM.  A plan holds the hybrid of its matrix (about
- * 0.5 GB at 233k rows and 114M edges) and a workspace for the last feature
- * width. */
+ * 0.5 GB at 233k rows and 114M edges) or its BCSR, and a workspace (or
+ * packed X) for the last feature width. */
 int tcc_swtcf_set_plans(uint32_t maxPlans);
 /* Releases every kept plan. */
 int tcc_swtcf_release_plans(void);

@@ -92,6 +92,10 @@ struct GatherArgs {
     // rowScale[8*ow + r] * (its sum), so that A = diag(rowScale) * B for a
     // pattern (or valued) B; 8 entries per output window.
     const float* rowScale;
+    // Rows of Y when it ends inside the last output window (0: 8 rows per
+    // window), for adding into a Y of exactly the matrix's rows: rows at or
+    // past it are neither read nor written (no window adds to them).
+    std::uint32_t rowLimit;
 };
 
 // Feature row of column `in` for the first-layer (mixed) form
@@ -561,11 +565,15 @@ __device__ __forceinline__ void gather_body(const GatherArgs& a, std::uint32_t g
             }
         } else if (active) {
             float* out = a.Y + static_cast<std::uint64_t>(ow) * 8 * a.F + f0;
+            // rows of the window inside Y (wave-uniform; 8 but in a last
+            // window cut by rowLimit, whose rows past it read row 0)
+            const std::uint32_t live = a.rowLimit ? min(8u, a.rowLimit - ow * 8) : 8u;
             if (!shared && vecStore && a.accumulate) {
                 // Y += : all 8 rows loaded before any is added
                 Vec<V> prev[8];
 #pragma unroll
-                for (int r = 0; r < 8; ++r) prev[r] = load_vec<V>(out + static_cast<std::uint64_t>(r) * a.F);
+                for (int r = 0; r < 8; ++r)
+                    prev[r] = load_vec<V>(out + static_cast<std::uint64_t>(r < static_cast<int>(live) ? r : 0) * a.F);
 #pragma unroll
                 for (int r = 0; r < 8; ++r)
 #pragma unroll
@@ -579,6 +587,8 @@ __device__ __forceinline__ void gather_body(const GatherArgs& a, std::uint32_t g
 #pragma unroll
                     for (int v = 0; v < V; ++v)
                         if (kWhole || f0 + v < a.F) atomic_add_f32(o + v, acc[r][v]);
+                } else if (r >= static_cast<int>(live)) {
+                    continue;
                 } else if (vecStore) {
                     store_vec<V>(o, acc[r]);
                 } else {
@@ -1476,14 +1486,20 @@ bool bcsc_ok(const tcc_bcsc* A) {
 // ---------------------------------------------------------------- scaled forms (gather_ops.hpp)
 
 int bcsr_spmm_scaled(const tcc_bcsr* A, const float* X, float* Y, std::uint32_t featureDim, int accumulate,
-                     const float* rowScale, hipStream_t st) {
+                     const float* rowScale, hipStream_t st, std::uint32_t rowLimit) {
     TCC_REQUIRE(bcsr_ok(A) && X && Y && feature_dim_ok(featureDim), TCC_ERR_INVALID_ARGUMENT,
                 "invalid BCSR SpMM arguments");
-    // the narrow gather has no row scales: scaled products take the wide one
-    if (featureDim <= kNarrowMaxF && rowScale == nullptr)
+    TCC_REQUIRE(rowLimit == 0 || (accumulate && A->phases <= 1 && rowLimit <= 8ull * A->num_rowWindows &&
+                                  rowLimit > 8ull * A->num_rowWindows - 8),
+                TCC_ERR_INVALID_ARGUMENT,
+                "a row limit needs accumulate and an unphased BCSR, and must fall in the last window");
+    // the narrow gather has neither row scales nor a row limit: such
+    // products take the wide one
+    if (featureDim <= kNarrowMaxF && rowScale == nullptr && rowLimit == 0)
         return launch_narrow<Src::Plain>(bcsr_args(A, X, Y, featureDim, accumulate), A->unitBlocks, st);
     GatherArgs a = bcsr_args(A, X, Y, featureDim, accumulate);
     a.rowScale = rowScale;
+    a.rowLimit = rowLimit;
     TCC_HIP_CHECK(zero_phased_output(a, st));
     return launch_gather<Src::Plain>(a, pick_vec(featureDim, {X, Y}), A->unitBlocks, st);
 }
@@ -1581,13 +1597,18 @@ private:
 }  // namespace
 
 int bcsr_spmm_packed_scaled(const tcc_bcsr* A, const void* packedX, float* Y, std::uint32_t featureDim,
-                            int accumulate, const float* rowScale, hipStream_t st) {
+                            int accumulate, const float* rowScale, hipStream_t st, std::uint32_t rowLimit) {
     TCC_REQUIRE(bcsr_ok(A) && packedX && Y && feature_dim_ok(featureDim), TCC_ERR_INVALID_ARGUMENT,
                 "invalid packed BCSR SpMM arguments");
+    TCC_REQUIRE(rowLimit == 0 || (accumulate && A->phases <= 1 && rowLimit <= 8ull * A->num_rowWindows &&
+                                  rowLimit > 8ull * A->num_rowWindows - 8),
+                TCC_ERR_INVALID_ARGUMENT,
+                "a row limit needs accumulate and an unphased BCSR, and must fall in the last window");
     TCC_REQUIRE(reinterpret_cast<std::uintptr_t>(packedX) % 16 == 0, TCC_ERR_INVALID_ARGUMENT,
                 "packed buffer must be 16-byte aligned");
     GatherArgs a = bcsr_args(A, nullptr, Y, featureDim, accumulate);
     a.rowScale = rowScale;
+    a.rowLimit = rowLimit;
     TCC_HIP_CHECK(zero_phased_output(a, st));
     a.packed = static_cast<const unsigned char*>(packedX);
     a.packedStride = static_cast<std::uint32_t>(packed_stride(featureDim));

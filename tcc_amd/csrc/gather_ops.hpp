@@ -20,8 +20,12 @@ constexpr std::uint32_t kPackSliceMaxRows = 64;
 constexpr std::uint32_t kPackMaxSlices = 16384;
 
 // tcc_bcsr_spmm; rowScale (nullptr: none) has 8 entries per output window.
+// rowLimit (0: none) is the number of rows of a Y that ends inside the last
+// window (8 * num_rowWindows - 8 < rowLimit <= 8 * num_rowWindows), for
+// adding (accumulate != 0) into a Y of exactly the matrix's rows; an
+// ordinary (unphased) BCSR then neither reads nor writes rows past it.
 int bcsr_spmm_scaled(const tcc_bcsr* A, const float* X, float* Y, std::uint32_t featureDim, int accumulate,
-                     const float* rowScale, hipStream_t st);
+                     const float* rowScale, hipStream_t st, std::uint32_t rowLimit = 0);
 
 // tcc_tf32_pack of colScale[r] * X[r] (colScale nullptr: X itself).  With
 // sliceMax, the largest finite magnitude's bits of each slice of
@@ -33,8 +37,8 @@ int tf32_pack_scaled(const float* X, std::uint32_t rows, std::uint32_t featureDi
                      void* packed, hipStream_t st, std::uint32_t* sliceMax = nullptr, std::uint32_t sliceWidth = 0,
                      std::uint32_t slices = 0);
 
-// tcc_bcsr_spmm_packed; rowScale as bcsr_spmm_scaled.
+// tcc_bcsr_spmm_packed; rowScale and rowLimit as bcsr_spmm_scaled.
 int bcsr_spmm_packed_scaled(const tcc_bcsr* A, const void* packedX, float* Y, std::uint32_t featureDim,
-                            int accumulate, const float* rowScale, hipStream_t st);
+                            int accumulate, const float* rowScale, hipStream_t st, std::uint32_t rowLimit = 0);
 
 }  // namespace tcc

@@ -10,18 +10,23 @@
 // binary tiles on the sparse MFMA plus a gather of the rest), which writes
 // each output row once per phase.
 //
-// Every call of tcc_swtcf_spmm / tcc_swtcf_spmm_f on a large, dense enough
-// matrix (at least kPlanMinEdges edges of capacity and 64 entries per row
-// on average) hashes the arrays that define the product (colWindowOffset,
-// superWindowRowOffset, tileLocalBit, tileRowSlot, superWindowRows at their
-// valid extents; two order-independent sums of mixed words) on the device
-// and reads the hash back.  The second call
+// A sparser or smaller matrix is served by the BCSR gather of its pattern
+// (bcsr_spmm.hip), which also writes each output row once: 0.63 ms against
+// about 0.08 ms on a 169k-row, 1.17M-edge R-MAT graph at F = 128.
+//
+// Every call of tcc_swtcf_spmm / tcc_swtcf_spmm_f on a matrix of at least
+// kGatherPlanMinEdges edges of capacity hashes the arrays that define the
+// product (colWindowOffset, superWindowRowOffset, tileLocalBit, tileRowSlot,
+// superWindowRows at their valid extents; two order-independent sums of
+// mixed words) on the device and reads the hash back.  The second call
 // that finds the same hash and dimensions decodes the matrix into a COO,
-// builds the hybrid and keeps it; that call and the later ones run the
-// hybrid.  A matrix changed in place hashes differently and is multiplied
-// afresh.  Plans need tcThreshold <= 64: the hybrid multiplies TF32(X)
-// everywhere, where the reference uses X as given for tiles below the
-// threshold (tcThreshold > 64 asks for the fp32 path throughout).
+// builds the plan and keeps it; that call and the later ones run the plan:
+// the hybrid for at least kPlanMinEdges edges and 64 entries per row on
+// average, else the gather (over X packed to TF32 rows where rows are
+// gathered 16 times or more).  A matrix changed in place hashes differently
+// and is multiplied afresh.  Plans need tcThreshold <= 64: they multiply
+// TF32(X) everywhere, where the reference uses X as given for tiles below
+// the threshold (tcThreshold > 64 asks for the fp32 path throughout).
 #include <algorithm>
 #include <cstdlib>
 #include <mutex>
@@ -30,6 +35,7 @@
 #include "../../include/tcc_spmm_cnic.h"
 #include "../../include/tcc_swtcf.h"
 #include "common.hpp"
+#include "gather_ops.hpp"
 #include "primitives.hpp"
 #include "swtcf_plan.hpp"
 
@@ -37,9 +43,17 @@ namespace tcc {
 namespace {
 
 constexpr unsigned kThreads = 256;
-constexpr std::uint64_t kPlanMinEdges = 4u << 20;
+constexpr std::uint64_t kGatherPlanMinEdges = 1u << 18;  // any plan
+constexpr std::uint64_t kPlanMinEdges = 4u << 20;         // the hybrid (with the degree)
 constexpr std::uint32_t kPlanMinRowDegree = 64;
+// Gathers per source row (8 per block column) from which X is packed.
+constexpr std::uint64_t kPlanPackMinGathers = 16;
 constexpr unsigned kHashBlocks = 2048;
+// The blocks add their sums into kHashSlots pairs of words (block b into
+// pair b % kHashSlots), which the host adds up: 2048 atomics on one address
+// are performed one after another past the L2 (about 45 us).
+constexpr unsigned kHashSlots = 32;
+constexpr unsigned kHashWords = 2 * kHashSlots + 2;
 
 // MurmurHash3's 32-bit finalizer (Appleby): a bijective mix of 32 bits
 __device__ __forceinline__ std::uint32_t fmix32(std::uint32_t h) {
@@ -78,9 +92,11 @@ __device__ __forceinline__ void hash_array(const std::uint32_t* p, std::uint64_t
         hash_word(p[j], j, salt, s0, s1);
 }
 
-// out[0], out[1]: two sums of mixed (array, index, word) over the arrays
-// that define the product; out[2] = tiles, out[3] = super-window rows.
-// The sums do not depend on the order in which the threads add them.
+// out[2k], out[2k + 1] (k < kHashSlots): two sums of mixed (array, index,
+// word) over the arrays that define the product, slot k's share of them;
+// out[2 kHashSlots] = tiles, out[2 kHashSlots + 1] = super-window rows.
+// The sums over the slots do not depend on the order in which the threads
+// add them.
 __global__ void __launch_bounds__(kThreads) swtcf_hash_kernel(tcc_swtcf_matrix m, std::uint64_t* __restrict__ out) {
     const std::uint64_t T = m.colWindowOffset[m.numColWindows], U = m.superWindowRowOffset[m.numSuperWindows];
     std::uint64_t s0 = 0, s1 = 0;
@@ -105,11 +121,12 @@ __global__ void __launch_bounds__(kThreads) swtcf_hash_kernel(tcc_swtcf_matrix m
             s0 += r0[w];
             s1 += r1[w];
         }
-        atomicAdd(reinterpret_cast<unsigned long long*>(&out[0]), static_cast<unsigned long long>(s0));
-        atomicAdd(reinterpret_cast<unsigned long long*>(&out[1]), static_cast<unsigned long long>(s1));
+        std::uint64_t* slot = out + 2 * (blockIdx.x % kHashSlots);
+        atomicAdd(reinterpret_cast<unsigned long long*>(&slot[0]), static_cast<unsigned long long>(s0));
+        atomicAdd(reinterpret_cast<unsigned long long*>(&slot[1]), static_cast<unsigned long long>(s1));
         if (blockIdx.x == 0) {
-            out[2] = T;
-            out[3] = U;
+            out[2 * kHashSlots] = T;
+            out[2 * kHashSlots + 1] = U;
         }
     }
 }
@@ -214,17 +231,23 @@ struct Plan {
     std::uint64_t lastUse = 0;
     bool built = false;
     bool unplannable = false;  // bits outside the rows or columns: always the SWTCF kernel
+    bool hybrid = false;       // the binary hybrid, else the BCSR gather
     tcc_hybrid H{};
-    void* ws = nullptr;
+    tcc_bcsr B{};
+    void* bAlloc = nullptr;    // B's arrays (tcc_block_release)
+    bool packs = false;        // the gather reads X packed to TF32 rows (in ws)
+    void* ws = nullptr;        // the hybrid's workspace or the packed X
     std::size_t wsBytes = 0;
     std::uint32_t wsF = 0;
     float* xq = nullptr;  // the dequantized X of the int8 entry point ([cols x 128])
 
     void release() {
-        if (built) tcc_hybrid_release(&H);
+        if (built && hybrid) tcc_hybrid_release(&H);
+        if (bAlloc) (void)tcc_block_release(bAlloc);
         if (ws) (void)hipFree(ws);
         if (xq) (void)hipFree(xq);
         built = false;
+        bAlloc = nullptr;
         ws = nullptr;
         wsBytes = 0;
         wsF = 0;
@@ -239,20 +262,29 @@ struct PlanCache {
     std::uint64_t clock = 0;
     std::uint32_t builtCount = 0;
     std::vector<Plan> plans;                 // seen matrices, built or not
-    std::vector<std::pair<int, std::uint64_t*>> hashBuf;  // per device: 4 u64
+    struct HashBuf {
+        int device;
+        std::uint64_t* dev;   // kHashWords u64 on the device
+        std::uint64_t* host;  // their pinned host copy
+    };
+    std::vector<HashBuf> hashBuf;
 
     void configure() {
         if (init) return;
         init = true;
         if (const char* e = std::getenv("TCC_SWTCF_PLANS")) maxPlans = static_cast<std::uint32_t>(std::strtoul(e, nullptr, 10));
     }
-    std::uint64_t* buffer(int device) {
+    const HashBuf* buffer(int device) {
         for (auto& b : hashBuf)
-            if (b.first == device) return b.second;
-        std::uint64_t* p = nullptr;
-        if (hipMalloc(&p, 4 * sizeof(std::uint64_t)) != hipSuccess) return nullptr;
-        hashBuf.emplace_back(device, p);
-        return p;
+            if (b.device == device) return &b;
+        HashBuf b{device, nullptr, nullptr};
+        if (hipMalloc(&b.dev, kHashWords * sizeof(std::uint64_t)) != hipSuccess) return nullptr;
+        if (hipHostMalloc(&b.host, kHashWords * sizeof(std::uint64_t), hipHostMallocDefault) != hipSuccess) {
+            (void)hipFree(b.dev);
+            return nullptr;
+        }
+        hashBuf.push_back(b);
+        return &hashBuf.back();
     }
     // keep at most maxPlans built plans and 2 maxPlans + 2 entries, dropping the least recently used
     void trim() {
@@ -283,9 +315,10 @@ PlanCache& cache() {
     return c;
 }
 
-// The hybrid of the matrix's pattern (binary tiles, no scales).  Two column
-// phases for the remainder: a phased remainder adds only the rows it
-// touches, so Y needs no rows past m.rows.  A matrix with bits outside its
+// The hybrid of the matrix's pattern (binary tiles, no scales), or the BCSR
+// of its pattern.  Two column phases for the hybrid's remainder: a phased
+// remainder adds only the rows it touches, so Y needs no rows past m.rows
+// (the gather takes a row limit instead).  A matrix with bits outside its
 // rows or columns (the SWTCF kernel skips them) is marked unplannable.
 int build_plan(const tcc_swtcf_matrix* m, Plan& P, hipStream_t st) {
     const std::uint32_t T = static_cast<std::uint32_t>(P.T);
@@ -330,8 +363,15 @@ int build_plan(const tcc_swtcf_matrix* m, Plan& P, hipStream_t st) {
         P.unplannable = true;
         return TCC_OK;
     }
-    const int rc = tcc_coo_to_hybrid_scaled(dst, src, nnz, m->rows, m->cols, nullptr, nullptr, 0, 0, 0, 2, &P.H, st);
-    if (rc) return rc;
+    if (P.hybrid) {
+        const int rc =
+            tcc_coo_to_hybrid_scaled(dst, src, nnz, m->rows, m->cols, nullptr, nullptr, 0, 0, 0, 2, &P.H, st);
+        if (rc) return rc;
+    } else {
+        const int rc = tcc_coo_to_bcsr(dst, src, nullptr, nnz, m->rows, m->cols, &P.B, &P.bAlloc, st);
+        if (rc) return rc;
+        P.packs = 8ull * P.B.num_TCBlocks >= kPlanPackMinGathers * m->cols;
+    }
     P.built = true;
     return TCC_OK;
 }
@@ -344,22 +384,26 @@ int swtcf_plan_spmm(const tcc_swtcf_matrix* m, const float* X, float* Y, std::ui
     PlanCache& C = cache();
     std::lock_guard<std::mutex> lock(C.mu);
     C.configure();
-    if (C.maxPlans == 0 || tc > 64 || m->nnz < kPlanMinEdges || m->rows == 0 ||
-        static_cast<std::uint64_t>(m->nnz) < static_cast<std::uint64_t>(kPlanMinRowDegree) * m->rows)
-        return TCC_OK;
+    if (C.maxPlans == 0 || tc > 64 || m->nnz < kGatherPlanMinEdges || m->rows == 0) return TCC_OK;
+    const bool hybrid = m->nnz >= kPlanMinEdges &&
+                        static_cast<std::uint64_t>(m->nnz) >= static_cast<std::uint64_t>(kPlanMinRowDegree) * m->rows;
     const hipStream_t st = as_stream(stream);
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(st, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return TCC_OK;
     int device = 0;
     TCC_HIP_CHECK(hipGetDevice(&device));
-    std::uint64_t* hb = C.buffer(device);
-    TCC_REQUIRE(hb, TCC_ERR_NO_MEMORY, "out of device memory for the SWTCF plan hash");
-    TCC_HIP_CHECK(fill<std::uint64_t>(hb, 4, 0ull, st));
-    hipLaunchKernelGGL(swtcf_hash_kernel, dim3(kHashBlocks), dim3(kThreads), 0, st, *m, hb);
+    const PlanCache::HashBuf* hb = C.buffer(device);
+    TCC_REQUIRE(hb, TCC_ERR_NO_MEMORY, "out of memory for the SWTCF plan hash");
+    TCC_HIP_CHECK(fill<std::uint64_t>(hb->dev, kHashWords, 0ull, st));
+    hipLaunchKernelGGL(swtcf_hash_kernel, dim3(kHashBlocks), dim3(kThreads), 0, st, *m, hb->dev);
     TCC_LAUNCH_CHECK();
-    std::uint64_t h[4] = {};
-    TCC_HIP_CHECK(hipMemcpyAsync(h, hb, sizeof(h), hipMemcpyDeviceToHost, st));
+    TCC_HIP_CHECK(hipMemcpyAsync(hb->host, hb->dev, kHashWords * sizeof(std::uint64_t), hipMemcpyDeviceToHost, st));
     TCC_HIP_CHECK(hipStreamSynchronize(st));
+    std::uint64_t h[4] = {0, 0, hb->host[2 * kHashSlots], hb->host[2 * kHashSlots + 1]};
+    for (unsigned k = 0; k < kHashSlots; ++k) {
+        h[0] += hb->host[2 * k];
+        h[1] += hb->host[2 * k + 1];
+    }
     Plan* P = nullptr;
     for (auto& p : C.plans)
         if (p.device == device && p.rows == m->rows && p.cols == m->cols && p.S == m->superWindowSize &&
@@ -380,6 +424,7 @@ int swtcf_plan_spmm(const tcc_swtcf_matrix* m, const float* X, float* Y, std::ui
         q.h1 = h[1];
         q.T = h[2];
         q.U = h[3];
+        q.hybrid = hybrid;
         q.lastUse = C.clock;
         C.plans.push_back(q);
         C.trim();
@@ -403,8 +448,9 @@ int swtcf_plan_spmm(const tcc_swtcf_matrix* m, const float* X, float* Y, std::ui
         if (P->ws) (void)hipFree(P->ws);
         P->ws = nullptr;
         P->wsF = 0;
-        P->wsBytes = tcc_hybrid_workspace_bytes(&P->H, F) + 16;
-        if (hipMalloc(&P->ws, P->wsBytes) != hipSuccess) {  // no room for this F: the kernel
+        P->wsBytes = P->hybrid ? tcc_hybrid_workspace_bytes(&P->H, F) + 16
+                               : (P->packs ? tcc_tf32_packed_bytes(m->cols, F) + 16 : 0);
+        if (P->wsBytes && hipMalloc(&P->ws, P->wsBytes) != hipSuccess) {  // no room for this F: the kernel
             P->ws = nullptr;
             P->wsBytes = 0;
             (void)hipGetLastError();
@@ -424,7 +470,19 @@ int swtcf_plan_spmm(const tcc_swtcf_matrix* m, const float* X, float* Y, std::ui
         TCC_LAUNCH_CHECK();
         X = P->xq;
     }
-    const int rc = tcc_hybrid_spmm(&P->H, X, Y, F, 1, P->ws, P->wsBytes, stream);
+    int rc;
+    if (P->hybrid) {
+        rc = tcc_hybrid_spmm(&P->H, X, Y, F, 1, P->ws, P->wsBytes, stream);
+    } else {
+        // Y holds m.rows rows: a last window cut short takes the row limit
+        const std::uint32_t limit = m->rows % 8 ? m->rows : 0;
+        if (P->packs) {
+            rc = tf32_pack_scaled(X, m->cols, F, nullptr, P->ws, st);
+            if (rc == TCC_OK) rc = bcsr_spmm_packed_scaled(&P->B, P->ws, Y, F, 1, nullptr, st, limit);
+        } else {
+            rc = bcsr_spmm_scaled(&P->B, X, Y, F, 1, nullptr, st, limit);
+        }
+    }
     if (rc) return rc;
     *used = true;
     C.trim();  // after the last use of P: trimming may move the entries

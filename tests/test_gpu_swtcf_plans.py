@@ -16,7 +16,11 @@ of capacity, 64 entries per row on average):
   never plan;
 - another feature width (tcc_swtcf_spmm_f, F = 72) reuses the plan with a
   workspace of its own size;
-- launchSWTCFSpMMQuantized plans too, dequantizing X into the plan's buffer.
+- launchSWTCFSpMMQuantized plans too, dequantizing X into the plan's buffer;
+- matrices below the hybrid's gate (at least 2^18 edges) plan the BCSR
+  gather of their pattern, over X or (rows gathered 16 times or more) over
+  X packed to TF32 rows; with rows not a multiple of 8 the last window is
+  cut at Y's end: sentinel rows right after Y stay untouched.
 """
 import numpy as np
 import pytest
@@ -130,15 +134,57 @@ def test_plans_off(gpu, oracle, plans):
     ws.free()
 
 
-def test_quantized_plan(gpu, oracle, plans):
-    """launchSWTCFSpMMQuantized (X[src] = q[srcGlobal[src]] * scales[srcGlobal[src]],
-    src/swtcf_spmm.cu:317-323) through the same plan: the first call runs
-    the SWTCF kernel, the second builds the plan, which dequantizes X into
-    its own buffer and runs the hybrid; against the fp64 oracle over
-    TF32(dequantized X) at 1e-5 (plan) and 1e-3 (kernel)."""
+@pytest.mark.parametrize("n,E,F", [(40003, 420_000, 128), (40005, 1_300_000, 72), (40001, 500_000, 13)])
+def test_gather_plan(gpu, oracle, plans, n, E, F):
+    """Below the hybrid's gate the plan is the BCSR gather of the pattern:
+    over X at 10 entries a row (F = 128; F = 13, which the wide gather takes
+    because of the row limit), over packed TF32 rows at 32 (F = 72).  Each
+    call adds into Y = buf[:n], where buf holds 8 sentinel rows after Y."""
     from tcc_amd import swtcf
 
-    n, E, F = 36000, 4_250_000, 128
+    r32, c32 = rmat_coo(n, E, 21)
+    m = swtcf.DeviceSWTCFMatrix(n, n, E, 16)
+    ws = swtcf.SWTCFConvertWorkspace(E, n, 16)
+    convert(swtcf, m, ws, r32, c32)
+    # the case takes the path it is meant for: packed rows where the BCSR
+    # gathers each row 16 times or more on average
+    A = swtcf.coo_to_bcsr(r32, c32, None, n, n)
+    assert (8 * A.view.num_TCBlocks >= 16 * n) == (F == 72), A.view.num_TCBlocks
+    A.release()
+    dst, src = r32.cpu().numpy().view(np.uint32), c32.cpu().numpy().view(np.uint32)
+    X = np.random.default_rng(22).standard_normal((n, F)).astype(np.float32)
+    Xd = torch.from_numpy(X).cuda()
+    want = oracle_product(oracle, dst, src, None, n, X)
+    Y0 = np.random.default_rng(23).standard_normal((n, F)).astype(np.float32)
+    b0 = plans.tcc_swtcf_plans_built()
+    got = []
+    for call in range(3):
+        buf = torch.full((n + 8, F), 12345.0, device="cuda")
+        buf[:n] = torch.from_numpy(Y0).cuda()
+        swtcf.swtcf_spmm(m, Xd, buf[:n])
+        torch.cuda.synchronize()
+        assert plans.tcc_swtcf_plans_built() == b0 + (0 if call == 0 else 1), call
+        b = buf.cpu().numpy()
+        assert (b[n:] == 12345.0).all(), f"call {call} wrote past Y"
+        got.append(b[:n] - Y0)
+    e = [rel_l2(g, want) for g in got]
+    print(f"gather plan n={n} E={E} F={F}: kernel {e[0]:.2e}, plan {e[1]:.2e} {e[2]:.2e}", flush=True)
+    assert e[0] <= 1e-3 and e[1] <= 1e-5 and e[2] <= 1e-5
+    m.free()
+    ws.free()
+
+
+@pytest.mark.parametrize("n,E", [(36000, 4_250_000), (30001, 500_000)])
+def test_quantized_plan(gpu, oracle, plans, n, E):
+    """launchSWTCFSpMMQuantized (X[src] = q[srcGlobal[src]] * scales[srcGlobal[src]],
+    src/swtcf_spmm.cu:317-323) through the same plans: the first call runs
+    the SWTCF kernel, the second builds the plan, which dequantizes X into
+    its own buffer and runs the hybrid (or, below its gate, the gather);
+    against the fp64 oracle over TF32(dequantized X) at 1e-5 (plan) and
+    1e-3 (kernel)."""
+    from tcc_amd import swtcf
+
+    F = 128
     r32, c32 = rmat_coo(n, E, 14)
     m = swtcf.DeviceSWTCFMatrix(n, n, E, 16)
     ws = swtcf.SWTCFConvertWorkspace(E, n, 16)
