@@ -167,10 +167,14 @@ int tcc_swtcf_release_plans(void);
 uint32_t tcc_swtcf_plans_built(void);
 
 /* Two order-independent 64-bit sums over the 32-bit words of up to 8 device
- * arrays (each bytes[k] a multiple of 4), mixed with their array and index,
- * written to deviceOut[0..1] in stream order (no reference counterpart):
- * what the plan caches compare to recognise a matrix whose arrays they
- * have seen. */
+ * arrays (each bytes[k] a multiple of 4), mixed with their array and index
+ * (no reference counterpart): what the plan caches compare to recognise a
+ * matrix whose arrays they have seen.  Written in stream order to
+ * deviceOut[0 .. TCC_HASH_WORDS-1] as TCC_HASH_WORDS/2 pairs of partial
+ * sums (the threads' sums spread over pairs, so that their atomics do not
+ * queue on one address): the sums are those of the even and of the odd
+ * words, modulo 2^64. */
+#define TCC_HASH_WORDS 64u
 int tcc_hash_arrays(const void* const* arrays, const uint64_t* bytes, uint32_t count, uint64_t* deviceOut,
                     void* stream);
 

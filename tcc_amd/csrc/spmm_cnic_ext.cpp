@@ -292,11 +292,19 @@ const tcc_hybrid* plan_for(const tcc_bcsr& A, int device, void* st) {
     const void* arrays[4] = {A.rowWindowOffset, A.sparseA2B, A.tcLocalBit, A.data};
     const std::uint64_t bytes[4] = {4ull * (A.num_rowWindows + 1ull), 32ull * A.num_TCBlocks, 8ull * A.num_TCBlocks,
                                     4ull * A.nnz};
-    torch::Tensor h = torch::empty({2}, torch::TensorOptions().dtype(torch::kInt64).device(torch::kCUDA, device));
+    torch::Tensor h =
+        torch::empty({TCC_HASH_WORDS}, torch::TensorOptions().dtype(torch::kInt64).device(torch::kCUDA, device));
     check(tcc_hash_arrays(arrays, bytes, values ? 4 : 3, reinterpret_cast<std::uint64_t*>(h.data_ptr()), st));
-    const torch::Tensor hh = h.cpu();  // waits for the hash on the current stream
-    const std::uint64_t h0 = static_cast<std::uint64_t>(hh[0].item<std::int64_t>());
-    const std::uint64_t h1 = static_cast<std::uint64_t>(hh[1].item<std::int64_t>());
+    torch::Tensor hh = torch::empty({TCC_HASH_WORDS}, torch::TensorOptions().dtype(torch::kInt64).pinned_memory(true));
+    hh.copy_(h, /*non_blocking=*/true);
+    if (hipStreamSynchronize(reinterpret_cast<hipStream_t>(st)) != hipSuccess)  // waits for the hash
+        throw std::runtime_error("spmm_cnic: hipStreamSynchronize failed while reading the graph hash");
+    const std::uint64_t* hw = reinterpret_cast<const std::uint64_t*>(hh.data_ptr());
+    std::uint64_t h0 = 0, h1 = 0;
+    for (unsigned k = 0; k < TCC_HASH_WORDS / 2; ++k) {
+        h0 += hw[2 * k];
+        h1 += hw[2 * k + 1];
+    }
     for (std::size_t i = 0; i < g_plans.size(); ++i) {
         Plan& p = g_plans[i];
         if (p.device == device && p.rows == A.num_rows && p.cols == A.num_cols && p.blocks == A.num_TCBlocks &&

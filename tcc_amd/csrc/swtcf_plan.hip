@@ -11,8 +11,9 @@
 // each output row once per phase.
 //
 // A sparser or smaller matrix is served by the BCSR gather of its pattern
-// (bcsr_spmm.hip), which also writes each output row once: 0.63 ms against
-// about 0.08 ms on a 169k-row, 1.17M-edge R-MAT graph at F = 128.
+// (bcsr_spmm.hip), which also writes each output row once: on a 169k-row,
+// 1.17M-edge R-MAT graph at F = 128 the kernel takes 0.61 ms, the plan
+// 0.12 ms (the gather 0.09 ms, the rest the hash and the wait for it).
 //
 // Every call of tcc_swtcf_spmm / tcc_swtcf_spmm_f on a matrix of at least
 // kGatherPlanMinEdges edges of capacity hashes the arrays that define the
@@ -52,7 +53,7 @@ constexpr unsigned kHashBlocks = 2048;
 // The blocks add their sums into kHashSlots pairs of words (block b into
 // pair b % kHashSlots), which the host adds up: 2048 atomics on one address
 // are performed one after another past the L2 (about 45 us).
-constexpr unsigned kHashSlots = 32;
+constexpr unsigned kHashSlots = TCC_HASH_WORDS / 2;
 constexpr unsigned kHashWords = 2 * kHashSlots + 2;
 
 // MurmurHash3's 32-bit finalizer (Appleby): a bijective mix of 32 bits
@@ -139,6 +140,7 @@ struct HashSpans {
     std::uint32_t n;
 };
 
+// out[2k], out[2k + 1] (k < kHashSlots): slot k's share of the two sums.
 __global__ void __launch_bounds__(kThreads) hash_spans_kernel(HashSpans s, std::uint64_t* __restrict__ out) {
     std::uint64_t s0 = 0, s1 = 0;
     for (std::uint32_t k = 0; k < s.n; ++k) hash_array(s.p[k], s.words[k], k + 1, s0, s1);
@@ -158,8 +160,9 @@ __global__ void __launch_bounds__(kThreads) hash_spans_kernel(HashSpans s, std::
             s0 += r0[w];
             s1 += r1[w];
         }
-        atomicAdd(reinterpret_cast<unsigned long long*>(&out[0]), static_cast<unsigned long long>(s0));
-        atomicAdd(reinterpret_cast<unsigned long long*>(&out[1]), static_cast<unsigned long long>(s1));
+        std::uint64_t* slot = out + 2 * (blockIdx.x % kHashSlots);
+        atomicAdd(reinterpret_cast<unsigned long long*>(&slot[0]), static_cast<unsigned long long>(s0));
+        atomicAdd(reinterpret_cast<unsigned long long*>(&slot[1]), static_cast<unsigned long long>(s1));
     }
 }
 
@@ -528,7 +531,7 @@ int tcc_hash_arrays(const void* const* arrays, const std::uint64_t* bytes, std::
         s.words[k] = bytes[k] / 4;
     }
     const hipStream_t st = as_stream(stream);
-    TCC_HIP_CHECK(fill<std::uint64_t>(deviceOut, 2, 0ull, st));
+    TCC_HIP_CHECK(fill<std::uint64_t>(deviceOut, 2 * kHashSlots, 0ull, st));
     hipLaunchKernelGGL(hash_spans_kernel, dim3(kHashBlocks), dim3(kThreads), 0, st, s, deviceOut);
     TCC_LAUNCH_CHECK();
     return TCC_OK;

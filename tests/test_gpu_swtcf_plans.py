@@ -213,3 +213,60 @@ def test_quantized_plan(gpu, oracle, plans, n, E):
     assert e[0] <= 1e-3 and e[1] <= 1e-5 and e[2] <= 1e-5
     m.free()
     ws.free()
+
+
+def _fmix32(h):
+    h = h ^ (h >> np.uint32(16))
+    h = h * np.uint32(0x85EBCA6B)
+    h = h ^ (h >> np.uint32(13))
+    h = h * np.uint32(0xC2B2AE35)
+    return h ^ (h >> np.uint32(16))
+
+
+def hash_sums(arrays):
+    """The two sums tcc_hash_arrays forms, restated in numpy: word j of
+    array k (salt k + 1) with index key k32 = j ^ (j >> 32) * 0x27D4EB2F
+    gives a = fmix32(w + k32 * 0x9E3779B9 + salt) into the first sum and
+    fmix32(a ^ (k32 + 0x5BD1E995 * salt)) into the second (MurmurHash3's
+    32-bit finalizer; 32-bit wrap-around, sums modulo 2^64)."""
+    s0 = s1 = 0
+    with np.errstate(over="ignore"):
+        for k, w in enumerate(arrays):
+            salt = np.uint32(k + 1)
+            j = np.arange(w.size, dtype=np.uint64)
+            k32 = (j & np.uint64(0xFFFFFFFF)).astype(np.uint32) ^ ((j >> np.uint64(32)).astype(np.uint32) * np.uint32(0x27D4EB2F))
+            a = _fmix32(w + k32 * np.uint32(0x9E3779B9) + salt)
+            b = _fmix32(a ^ (k32 + np.uint32(0x5BD1E995) * salt))
+            s0 += int(a.astype(np.uint64).sum())
+            s1 += int(b.astype(np.uint64).sum())
+    return s0 % 2**64, s1 % 2**64
+
+
+def test_hash_arrays_slots(gpu, plans):
+    """tcc_hash_arrays writes TCC_HASH_WORDS / 2 pairs of partial sums, whose
+    even and odd words add up (modulo 2^64) to the two sums of its mixing,
+    restated above: checked on three arrays, one not 16-byte aligned (one
+    word a thread) and one empty; changing one word changes both sums."""
+    import ctypes
+
+    rng = np.random.default_rng(31)
+    host = [rng.integers(0, 2**32, size=n, dtype=np.uint64).astype(np.uint32) for n in (1_000_003, 77_777, 0)]
+    dev = [torch.from_numpy(h.view(np.int32)).cuda() for h in host]
+    base = torch.zeros(77_777 + 1, dtype=torch.int32, device="cuda")
+    base[1:] = dev[1]
+    views = [dev[0], base[1:], dev[2]]  # the second one 4 bytes past a 256-byte boundary
+    out = torch.empty(64, dtype=torch.int64, device="cuda")
+
+    def run(vs):
+        ptrs = (ctypes.c_void_p * 3)(*[v.data_ptr() if v.numel() else None for v in vs])
+        nbytes = (ctypes.c_uint64 * 3)(*[4 * v.numel() for v in vs])
+        assert plans.tcc_hash_arrays(ptrs, nbytes, 3, ctypes.c_void_p(out.data_ptr()), None) == 0
+        w = out.cpu().numpy().view(np.uint64)
+        return int(w[0::2].astype(object).sum()) % 2**64, int(w[1::2].astype(object).sum()) % 2**64
+
+    got = run(views)
+    assert got == hash_sums(host)
+    dev[0][500_000] ^= 1
+    torch.cuda.synchronize()
+    changed = run(views)
+    assert changed[0] != got[0] and changed[1] != got[1]
