@@ -1533,8 +1533,9 @@ int tf32_pack_scaled(const float* X, std::uint32_t rows, std::uint32_t featureDi
 // A second stream per device, for work that runs beside a launch on the
 // caller's stream (default priority, non-blocking).  SideFork orders it
 // after the work queued so far on st (fork) and st after everything queued
-// on it in between (join); when st is being captured, or the side stream
-// cannot be made, the work goes to st itself.  The lock keeps concurrent
+// on it in between (join); when st is being captured, belongs to another
+// device than the current one, or the side stream cannot be made, the work
+// goes to st itself.  The lock keeps concurrent
 // callers' record/wait pairs on the shared events apart: a wait takes the
 // event's latest record.
 namespace {
@@ -1551,8 +1552,12 @@ public:
     explicit SideFork(hipStream_t st) : st_(st) {
         hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
         if (hipStreamIsCapturing(st, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return;
+        // the side stream is made on the current device: st must be one of its streams
         int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return;
+        hipDevice_t stDev = -1;
+        if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || hipStreamGetDevice(st, &stDev) != hipSuccess ||
+            stDev != dev)
+            return;
         lock_ = std::unique_lock<std::mutex>(g_sideMutex);
         SideLane& l = g_sideLanes[dev];
         if (!l.stream) {
