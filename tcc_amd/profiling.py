@@ -3,7 +3,7 @@ profiles/ (kernel-time tables and the counter-measured HBM traffic that
 bench.py's roofline reports).
 
     python -m tcc_amd.profiling stats --csv <kernel_stats.csv> --title T --command C [--kernels REGEX]
-        --out profiles/<name>.md
+        [--trace <kernel_trace.csv> --anchor REGEX] --out profiles/<name>.md
     python -m tcc_amd.profiling counters --csv <counter csv> --kernels REGEX --title T --command C
         --out profiles/<name>.md
     python -m tcc_amd.profiling traffic --config N --fetch <FETCH_SIZE counter csv> --write <WRITE_SIZE csv>
@@ -110,6 +110,21 @@ def sources_sha(kernels=None) -> dict:
     return out
 
 
+def step_periods(trace_csv: str, anchor: str) -> list[float]:
+    """Milliseconds from each dispatch of the step's anchor kernel (a kernel
+    that runs once per step; regex over kernel keys) to the next one's, from
+    a rocprofv3 kernel-trace csv: the step's wall time on the GPU, gaps and
+    kernels that overlap on other streams included."""
+    pat = re.compile(anchor)
+    starts = []
+    with open(trace_csv) as f:
+        for r in csv.DictReader(f):
+            if pat.search(kernel_key(r["Kernel_Name"])):
+                starts.append(int(r["Start_Timestamp"]))
+    starts.sort()
+    return [(b - a) / 1e6 for a, b in zip(starts, starts[1:])]
+
+
 def _short(name: str, width: int = 72) -> str:
     return name if len(name) <= width else name[: width - 3] + "..."
 
@@ -119,6 +134,18 @@ def stats_md(args) -> str:
     total = sum(r["total_ms"] for r in rows)
     lines = [f"# {args.title}", "", "Command (from the repository root on the GPU box, TMPDIR=/tmp):", "", "```",
              args.command, "```", ""]
+    d = re.search(r"rocprofv3 --kernel-trace --stats\b.*? -d (\S+) -o run\b", args.command)
+    if d:
+        # the tables' own command, over the files the profiling run wrote
+        t = [f"python -m tcc_amd.profiling stats --csv {d.group(1)}/run_kernel_stats.csv"]
+        if args.launches:
+            t.append(f"--launches {args.launches}")
+        if args.kernels:
+            t.append(f"--kernels '{args.kernels}'")
+        if args.trace:
+            t.append(f"--trace {d.group(1)}/run_kernel_trace.csv --anchor '{args.anchor}'")
+        t.append(f"--out {os.path.relpath(args.out, ROOT) if os.path.isabs(args.out) else args.out}")
+        lines += [f"Tables: `{' '.join(t)}` (plus `--title` / `--command`).", ""]
     if args.kernels:
         pat = re.compile(args.kernels)
         step = [r for r in rows if pat.search(r["kernel"])]
@@ -132,6 +159,12 @@ def stats_md(args) -> str:
             lines += [f"Step kernels (`{args.kernels}`):", "", "| kernel | calls | avg ms |", "|---|---:|---:|"]
             lines += [f"| `{r['kernel']}` | {r['calls']} | {r['avg_ms']:.4f} |" for r in step]
             lines += [f"| **sum of averages** | | **{sum(r['avg_ms'] for r in step):.4f}** |", ""]
+    if args.trace:
+        per = sorted(step_periods(args.trace, args.anchor))
+        if per:
+            med = per[len(per) // 2] if len(per) % 2 else 0.5 * (per[len(per) // 2 - 1] + per[len(per) // 2])
+            lines += [f"Step period from the kernel trace (one dispatch of `{args.anchor}` to the next, "
+                      f"{len(per)} periods): median **{med:.4f} ms**, min {per[0]:.4f}, max {per[-1]:.4f}.", ""]
     lines += ["All kernels, by total time:", "",
               "| kernel | calls | avg ms | total ms | % of GPU time |", "|---|---:|---:|---:|---:|"]
     for r in rows[: args.top]:
@@ -234,6 +267,8 @@ def main(argv=None) -> int:
     s.add_argument("--kernels", default="", help="regex over kernel names: the step's kernels, listed first")
     s.add_argument("--launches", type=int, default=0, help="steps in the run: report each kernel's time per step")
     s.add_argument("--top", type=int, default=15)
+    s.add_argument("--trace", help="kernel-trace csv of the same run: report the step period")
+    s.add_argument("--anchor", default="", help="regex of a kernel that runs once per step (with --trace)")
     s.add_argument("--out", required=True)
     c = sub.add_parser("counters")
     c.add_argument("--csv", required=True)
