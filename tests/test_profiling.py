@@ -95,3 +95,37 @@ def test_kernel_sources_follow_definitions_and_includes():
     sha = profiling.sources_sha(["tile_emit_kernel<unsigned int>"])
     assert list(sha) == profiling.kernel_sources(["tile_emit_kernel"])
     assert "tcc_amd/csrc/swtcf_convert.hip" in sha and "tcc_amd/csrc/hub_tiles.hip" not in sha
+
+
+def _trace(path, rows):
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Kind", "Kernel_Name", "Start_Timestamp", "End_Timestamp"])
+        w.writeheader()
+        for name, start, end in rows:
+            w.writerow({"Kind": "KERNEL_DISPATCH", "Kernel_Name": name, "Start_Timestamp": start,
+                        "End_Timestamp": end})
+
+
+def test_step_period_from_the_anchor_kernel(tmp_path):
+    """Steps whose kernels overlap on two streams: the period is anchor start
+    to anchor start (the steps' wall time), not the sum of the durations; the
+    rows come in any order."""
+    pack = "void tcc::(anonymous namespace)::tf32_pack_kernel(float const*, unsigned int)"
+    full = "void tcc::(anonymous namespace)::gather_kernel<4, (tcc::(anonymous namespace)::Src)4, false>(int)"
+    last = "void tcc::(anonymous namespace)::gather_kernel<2, (tcc::(anonymous namespace)::Src)4, false>(int)"
+    rows = []
+    for i, t0 in enumerate((1_000_000, 5_000_000, 9_500_000)):
+        rows += [(pack, t0, t0 + 200_000), (full, t0 + 300_000, t0 + 3_800_000), (last, t0 + 300_000, t0 + 2_300_000)]
+    rows.reverse()
+    _trace(tmp_path / "k.csv", rows)
+    assert profiling.step_periods(str(tmp_path / "k.csv"), "^tf32_pack_kernel$") == [4.0, 4.5]
+    _stats(tmp_path / "s.csv", [(pack, 3, 200_000), (full, 3, 3_500_000), (last, 3, 2_000_000)])
+    out = tmp_path / "p.md"
+    profiling.main(["stats", "--csv", str(tmp_path / "s.csv"), "--title", "t",
+                    "--command", "rocprofv3 --kernel-trace --stats --output-format csv -d /tmp/s -o run -- python x.py",
+                    "--kernels", "gather_kernel|tf32_pack", "--launches", "3", "--trace", str(tmp_path / "k.csv"),
+                    "--anchor", "^tf32_pack_kernel$", "--out", str(out)])
+    text = out.read_text()
+    assert "median **4.2500 ms**, min 4.0000, max 4.5000" in text
+    assert "--csv /tmp/s/run_kernel_stats.csv" in text and "--trace /tmp/s/run_kernel_trace.csv" in text
+    assert "| **per step** | | | **5.7000** |" in text  # overlapping durations add up past the period
