@@ -69,7 +69,8 @@ BINARY_REST_PHASES = 2
 # binary tiles on dense MFMA with bf16 halves only 6.56 at 64 entries a
 # 16-column step; with fp16 records, the tiles before the remainder, 5.52
 # at 36 entries; on the 2:4 sparse MFMA over 32-column steps, 4.99 at 40
-# entries and 768-step units (the builder's defaults).  The valued hybrid
+# entries and 768-step units, 4.55 with 1024-step units (the builder's
+# defaults) after the launch-order and second-stream changes.  The valued hybrid
 # is timed beside it under `extra`.
 HUB_MIN_TILE_NNZ = 16
 HUB_GROUP_BLOCKS = 8

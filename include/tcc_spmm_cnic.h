@@ -344,7 +344,7 @@ int tcc_coo_to_hybrid(const uint32_t* dRow, const uint32_t* dCol, const float* d
  * dRowScale [numRows] and dColScale [numCols] device arrays, either NULL
  * for ones), with binary tiles (TCC_TILES_BINARY): steps of at least
  * minStepNnz entries (0 = 40), groupBlocks 8 or 16 (0 = 16), unitSteps
- * 0 = 768 (any number: the SpMM reads a unit's step list 256 steps at a
+ * 0 = 1024 (any number: the SpMM reads a unit's step list 256 steps at a
  * time), phases as tcc_coo_to_hybrid.  The remainder holds the pattern
  * (data NULL); its gather reads the column-scaled packed rows and scales
  * its row sums.  The scales are copied.  Synchronises `stream`; free with

@@ -67,15 +67,19 @@ constexpr int kColRegs = kMaxUnitSteps / 64;
 constexpr std::uint32_t kDefaultMinTileNnz = 16;
 constexpr std::uint32_t kDefaultGroupBlocks = 8;
 // Binary tiles: steps (16 row blocks by a pair of 16-column blocks) of at
-// least 40 entries, groups of 16 row blocks, units of up to 768 sub-steps
+// least 40 entries, groups of 16 row blocks, units of up to 1024 sub-steps
 // (the kernel reads a unit's step list 256 steps at a time, so units are
 // not bound by kMaxUnitSteps).  Config 3, step ms with G = 16 on the
 // sparse MFMA: 5.33 / 5.14 / 5.01 / 5.04 / 4.99 / 5.03 / 5.06 at 24 / 28 /
-// 32 / 36 / 40 / 48 / 64 entries with 768-step units; 5.00 at 40 with 512,
-// 5.10 with 1024.
+// 32 / 36 / 40 / 48 / 64 entries with 768-step units.  With units launched
+// by size and the remainder's last chunk beside its full chunks: 4.565-4.592
+// with 768-step units, 4.538-4.555 with 1024, 4.59-4.60 with 1536, 4.53-4.54
+// with 2048-3072; at F = 128, 1.162-1.166 / 1.143-1.147 / 1.241 / 1.358 ms
+// with 768 / 1024 / 1536 / 2048 (fewer waves); thresholds 32-40 within
+// 5 us with 1024.
 constexpr std::uint32_t kDefaultMinStepNnz = 40;
 constexpr std::uint32_t kDefaultBinaryGroupBlocks = 16;
-constexpr std::uint32_t kDefaultBinaryUnitSteps = 768;
+constexpr std::uint32_t kDefaultBinaryUnitSteps = 1024;
 constexpr std::uint32_t kNoSlot = 0xFFFFFFFFu;
 constexpr unsigned kThreads = 256;
 constexpr std::uint32_t kXcds = 8;

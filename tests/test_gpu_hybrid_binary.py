@@ -44,7 +44,7 @@ pytestmark = pytest.mark.gpu
 
 REL = 1e-5
 NORTH_STAR = 1e-3
-DEFAULT_MIN_STEP, DEFAULT_G, DEFAULT_UNIT_STEPS = 40, 16, 768
+DEFAULT_MIN_STEP, DEFAULT_G, DEFAULT_UNIT_STEPS = 40, 16, 1024
 
 
 def _nibble_tables():
