@@ -60,7 +60,10 @@ constexpr std::uint32_t kDefaultUnitSteps = 128;
 // The remainder's gather: units of 64 blocks (config 3: 9.40-9.44 ms per
 // step at 48-80 blocks, 9.58 at the 128 that tcc_bcsr's automatic choice
 // gives its 4.95M blocks, 9.52 at 32; the whole phased matrix, 12.9M
-// blocks, keeps 128).
+// blocks, keeps 128).  Binary hybrid, its 1.41M-block remainder with the
+// last chunk beside the full ones: 4.561-4.566 / 4.553-4.555 / 4.568-4.579 /
+// 4.632-4.636 ms at 64 / 128 / 192 / 256 blocks (F = 602), 1.140 / 1.143 /
+// 1.200 ms at 64 / 128 / 256 (F = 128).
 constexpr std::uint32_t kRestUnitBlocks = 64;
 constexpr std::uint32_t kMaxUnitSteps = 256;        // a unit's step columns sit one per lane, in four registers
 constexpr int kColRegs = kMaxUnitSteps / 64;
