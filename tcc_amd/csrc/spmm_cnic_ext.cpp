@@ -57,7 +57,9 @@ bool g_use_values = false;
 std::uint32_t g_unit_blocks = 0;       // blocks per unit of work (0 = automatic)
 
 // Per-graph plans, most recently used last (set_graph_plans); entries not
-// yet built are graphs seen once in the automatic mode.
+// yet built are graphs seen once in the automatic mode.  These globals, like
+// the settings above, are guarded by the GIL: no function of the module
+// releases it.
 struct Plan {
     int device;
     std::uint32_t rows, cols, blocks, windows;
