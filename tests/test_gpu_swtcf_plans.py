@@ -20,7 +20,9 @@ of capacity, 64 entries per row on average):
 - matrices below the hybrid's gate (at least 2^18 edges) plan the BCSR
   gather of their pattern, over X or (rows gathered 16 times or more) over
   X packed to TF32 rows; with rows not a multiple of 8 the last window is
-  cut at Y's end: sentinel rows right after Y stay untouched.
+  cut at Y's end: sentinel rows right after Y stay untouched;
+- two matrices in turn: with one plan kept, each build releases the other
+  matrix's plan and its next call builds it again; with two, both stay.
 """
 import numpy as np
 import pytest
@@ -270,3 +272,40 @@ def test_hash_arrays_slots(gpu, plans):
     torch.cuda.synchronize()
     changed = run(views)
     assert changed[0] != got[0] and changed[1] != got[1]
+
+
+@pytest.mark.parametrize("limit", [1, 2])
+def test_two_matrices_alternate(gpu, oracle, plans, limit):
+    """Two matrices multiplied in turn, each twice in a row: with one plan
+    kept, building the second's plan releases the first's (the least
+    recently used) but remembers the matrix, so the first's next call builds
+    it again at once; with two kept, both plans stay.  Every product,
+    through the kernel or a plan, against its own matrix's oracle."""
+    from tcc_amd import swtcf
+
+    plans.tcc_swtcf_set_plans(limit)
+    n, E, F = 40003, 420_000, 64
+    mats = []
+    for seed in (31, 32):
+        r32, c32 = rmat_coo(n, E, seed)
+        m = swtcf.DeviceSWTCFMatrix(n, n, E, 16)
+        ws = swtcf.SWTCFConvertWorkspace(E, n, 16)
+        convert(swtcf, m, ws, r32, c32)
+        mats.append((m, ws, r32.cpu().numpy().view(np.uint32), c32.cpu().numpy().view(np.uint32)))
+    X = np.random.default_rng(33).standard_normal((n, F)).astype(np.float32)
+    Xd = torch.from_numpy(X).cuda()
+    want = [oracle_product(oracle, d, s, None, n, X) for _, _, d, s in mats]
+    b0 = plans.tcc_swtcf_plans_built()
+    order = [0, 0, 1, 1, 0, 0, 1, 1]
+    # builds after each call: one plan kept rebuilds on every return, two keep both
+    builds = [0, 1, 1, 2, 3, 3, 4, 4] if limit == 1 else [0, 1, 1, 2, 2, 2, 2, 2]
+    for call, (k, nb) in enumerate(zip(order, builds)):
+        Y = torch.zeros((n, F), device="cuda")
+        swtcf.swtcf_spmm(mats[k][0], Xd, Y)
+        torch.cuda.synchronize()
+        assert plans.tcc_swtcf_plans_built() == b0 + nb, (limit, call)
+        e = rel_l2(Y.cpu().numpy(), want[k])
+        assert e <= 1e-3, (limit, call, e)
+    for m, ws, _, _ in mats:
+        m.free()
+        ws.free()
