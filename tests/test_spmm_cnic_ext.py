@@ -292,7 +292,8 @@ def test_forward_tensorcore_automatic_plans(gpu, oracle):
     and tcLocalBit); the first call runs the packed gather.  A bitmap
     rewritten in place hashes differently: that call runs the default path
     on the new graph, and the next call builds the new graph's plan in
-    place of the old one.  Every product against the oracle."""
+    place of the old one; restored, the first graph's plan is built again.
+    Every product against the oracle."""
     m = import_ext()
     nr, nc, F = 512, 60000, 96
     rng = np.random.default_rng(51)
@@ -327,11 +328,19 @@ def test_forward_tensorcore_automatic_plans(gpu, oracle):
             assert _rel(out.reshape(nr, F).cpu().numpy(), want2) < 1e-5, call
             assert m.graph_plans() == plans, call
             m.freeMatC()
+        # the entry restored: the first graph again, whose plan the second's
+        # replaced; its plan is built again and the second's released
+        args[8][0] = int(np.array([b0], np.uint64).view(np.int64)[0])
+        for call in (6, 7):
+            out = m.forward_tensorcore(*args, F, x)
+            assert _rel(out.reshape(nr, F).cpu().numpy(), want) < 1e-5, call
+            assert m.graph_plans() == 1, call
+            m.freeMatC()
         # turned off: the default path, no plan kept
         m.set_graph_plans(0)
         assert m.graph_plans() == 0
         out = m.forward_tensorcore(*args, F, x)
-        assert _rel(out.reshape(nr, F).cpu().numpy(), want2) < 1e-5
+        assert _rel(out.reshape(nr, F).cpu().numpy(), want) < 1e-5
     finally:
         m.set_graph_plans(-1)
         m.freeMatC()
